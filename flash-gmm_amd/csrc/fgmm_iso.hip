@@ -1,0 +1,531 @@
+// Isotropic (spherical-covariance) GMM E-step for gfx950.
+//
+// Math (reference: flash_gmm.py:84-103 pass 1, :141-166 pass 2), in log2 units:
+//   b_k   = 0.5 * exp(-lss_k) * log2(e)
+//   C_k   = (lpi_k - 0.5*D*(log(2pi) + lss_k)) * log2(e) - b_k * ||mu_k||^2
+//   ll2_nk = C_k - b_k * (||x_n||^2 - 2 x_n.mu_k)
+//   logZ2_n = log2 sum_k 2^ll2_nk ;  r_nk = 2^(ll2_nk - logZ2_n)
+//   Nk_k = sum_n r_nk ; mu_acc_k = sum_n r_nk x_n ; sig_acc_k = sum_n r_nk ||x_n - mu_k||^2
+//
+// Kernels, all launched on the caller's stream:
+//   iso_prep    O(K*D): per-component constants (fp64) and mu re-laid out in the
+//               matrix-core operand order ("mu_sw").
+//   iso_lse     pass 1, grid over row tiles. Each wave keeps 32 rows of X resident
+//               in registers and streams mu in blocks of 32 components; the cross
+//               term is a 32x32x2 fp32 MFMA contraction (S^T = mu . X^T, so every
+//               lane owns one row) and the log-sum-exp is an online max/sum in
+//               registers. Writes logZ and per-row (||x||^2, logZ2) in fp64.
+//   iso_accum   pass 2, grid over (row slab x group of 128 components). Each wave
+//               owns 32 components (mu resident in registers) and walks its slab in
+//               32-row tiles staged through LDS: S = X . mu^T on MFMA, r = 2^(ll2 -
+//               logZ2) in registers, then mu_acc += r^T X on MFMA with r used directly
+//               as the A operand (no transpose), Nk and sig_acc on the VALU. Writes one
+//               partial per (slab, component).
+//   iso_reduce  fixed-order fp64 sum of the slab partials (deterministic), or
+//               the atomic variant selected by FGMM_FLAG_ATOMIC_REDUCE.
+//
+// Accuracy: the D-contraction runs on the fp32 matrix cores in chunks of 8
+// dimensions (4 MFMA steps from a zero accumulator), and the chunk results are
+// summed in fp64 together with fp64 ||x||^2 and constants (cross_tile()).  A
+// single fp32 chain over D=128 leaves ~3e-4 absolute error in logZ on clustered
+// data; the chunked form stays below 1e-4.  Both passes use the same routine,
+// so they form bitwise-identical log-joints.
+
+#include "fgmm_common.hpp"
+
+#include <math.h>
+
+namespace fgmm {
+namespace {
+
+constexpr int kWaves = 4;        // waves per workgroup
+constexpr int kThreads = 64 * kWaves;
+constexpr int kCUs = 256;  // MI355X compute units
+
+// Waves per SIMD that pass 2 is compiled for (one workgroup of kWaves waves per
+// CU at 1, two at 2); it sets how many slab workgroups are resident at once.
+__host__ __device__ constexpr int accum_waves_per_eu(int DP) { return DP <= 96 ? 2 : 1; }
+
+struct IsoPlan {
+  int64_t N, K, D;
+  int DP;       // D padded to a multiple of 32
+  int KB;       // 32-component blocks
+  int KP;       // K padded to a multiple of 32
+  int ncg;      // groups of kWaves component blocks (pass 2)
+  int nslab;    // row slabs (pass 2)
+  int64_t rows_per_slab;
+  size_t off_musw, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_nk, off_part_sig, total;
+};
+
+IsoPlan make_plan(int64_t N, int64_t K, int64_t D) {
+  IsoPlan p{};
+  p.N = N; p.K = K; p.D = D;
+  p.DP = (int)round_up(D < 1 ? 1 : D, 32);
+  p.KB = (int)cdiv(K, 32);
+  p.KP = p.KB * 32;
+  p.ncg = (int)cdiv(p.KB, kWaves);
+  if (N > 0 && p.ncg > 0) {
+    int64_t want = (int64_t)kCUs * accum_waves_per_eu(p.DP) / p.ncg;
+    if (want >= 8) want = (want / 8) * 8;  // keeps a slab's workgroups on one XCD
+    if (want < 1) want = 1;
+    int64_t max_slabs = cdiv(N, 32);
+    if (want > max_slabs) want = max_slabs;
+    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.nslab = (int)cdiv(N, p.rows_per_slab);
+  } else {
+    p.rows_per_slab = 32;
+    p.nslab = 0;
+  }
+  size_t off = 0;
+  p.off_musw = off;    off = align256(off + (size_t)p.KP * p.DP * sizeof(float));
+  p.off_kcblk = off;   off = align256(off + (size_t)p.KB * 32 * 2 * sizeof(double));
+  p.off_kclin = off;   off = align256(off + (size_t)p.KP * 4 * sizeof(double));
+  p.off_rowstat = off; off = align256(off + (size_t)(N > 0 ? N : 0) * 2 * sizeof(double));
+  p.off_part_mu = off; off = align256(off + (size_t)p.nslab * p.KP * p.DP * sizeof(float));
+  p.off_part_nk = off; off = align256(off + (size_t)p.nslab * p.KP * sizeof(float));
+  p.off_part_sig = off; off = align256(off + (size_t)p.nslab * p.KP * sizeof(float));
+  p.total = off;
+  return p;
+}
+
+// ---------------------------------------------------------------------------
+// Prologue: one 64-thread block per 32-component block.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int64_t ldmu, int64_t K,
+                                               int D, int DP, const float* __restrict__ lss,
+                                               const float* __restrict__ lpi, f32x4* __restrict__ mu_sw,
+                                               double2* __restrict__ kc_blk, double4* __restrict__ kc_lin) {
+  __shared__ double sC[32], sB[32];
+  const int kb = blockIdx.x;
+  const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  const int64_t comp = (int64_t)kb * 32 + c;
+  const bool valid = comp < K;
+  if (g == 0) {
+    double C = -INFINITY, b = 0.0, musq = 0.0;
+    if (valid) {
+      for (int d = 0; d < D; ++d) {
+        double v = (double)mu[comp * ldmu + d];
+        musq = fma(v, v, musq);
+      }
+      const double l = (double)lss[comp];
+      const double lp = (double)lpi[comp];
+      b = 0.5 * exp(-l) * kLog2e;
+      C = (lp - 0.5 * (double)D * (kLog2Pi + l)) * kLog2e - b * musq;
+    }
+    sC[c] = C;
+    sB[c] = b;
+    kc_lin[comp] = make_double4(C, b, musq, 0.0);
+  }
+  // mu in matrix-core operand order: chunk m of lane (c, g) = mu[comp][8m+4g .. 8m+4g+3].
+  const int NM = DP / 8;
+  for (int m = 0; m < NM; ++m) {
+    f32x4 v = zero4();
+    const int d0 = 8 * m + 4 * g;
+    if (valid) {
+      if (d0 + 0 < D) v.x = mu[comp * ldmu + d0 + 0];
+      if (d0 + 1 < D) v.y = mu[comp * ldmu + d0 + 1];
+      if (d0 + 2 < D) v.z = mu[comp * ldmu + d0 + 2];
+      if (d0 + 3 < D) v.w = mu[comp * ldmu + d0 + 3];
+    }
+    mu_sw[((int64_t)kb * NM + m) * 64 + lane] = v;
+  }
+  __syncthreads();
+  // Constants in accumulator-register order: entry (g, i) is component acc_row(i, g).
+  {
+    const int i = lane & 15, gg = (lane >> 4) & 1;
+    if (lane < 32) {
+      const int cc = acc_row(i, gg);
+      kc_blk[((int64_t)kb * 2 + gg) * 16 + i] = make_double2(sC[cc], sB[cc]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 1: logZ by online log-sum-exp over component blocks.
+// ---------------------------------------------------------------------------
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
+void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+             const f32x4* __restrict__ mu_sw, const double2* __restrict__ kc_blk, int KB,
+             float* __restrict__ logZ, double2* __restrict__ rowstat) {
+  constexpr int NM = DP / 8;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t row = ((int64_t)blockIdx.x * kWaves + wave) * 32 + c;
+  const bool valid = row < N;
+
+  f32x4 xb[NM];
+  double xsq = 0.0;
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    xb[m] = load_row4(X, ldx, row, 8 * m + 4 * g, D, valid);
+    xsq = fma((double)xb[m].x, (double)xb[m].x, xsq);
+    xsq = fma((double)xb[m].y, (double)xb[m].y, xsq);
+    xsq = fma((double)xb[m].z, (double)xb[m].z, xsq);
+    xsq = fma((double)xb[m].w, (double)xb[m].w, xsq);
+  }
+  xsq += __shfl_xor(xsq, 32);
+
+  double mx = -INFINITY;
+  float sm = 0.0f;
+
+  for (int kb = 0; kb < KB; ++kb) {
+    const f32x4* mp = mu_sw + (int64_t)kb * NM * 64 + lane;
+    // S^T[comp][row] = mu . x, lane = row, register i = component acc_row(i, g).
+    double xm[16];
+    cross_tile<NM>(xm, [&](int m) { return mp[m * 64]; }, [&](int m) { return xb[m]; });
+    const double2* kp = kc_blk + ((int64_t)kb * 2 + g) * 16;
+    double ll[16];
+    double bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const double2 cb = kp[i];
+      ll[i] = fma(-cb.y, fma(-2.0, xm[i], xsq), cb.x);
+      bm = fmax(bm, ll[i]);
+    }
+    const double mn = fmax(mx, bm);
+    const double ms = (mn == -INFINITY) ? 0.0 : mn;
+    float acc = sm * fast_exp2((float)(mx - ms));
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc += fast_exp2((float)(ll[i] - ms));
+    sm = acc;
+    mx = mn;
+  }
+
+  // Merge the two half-waves that hold the same row.
+  const double mo = __shfl_xor(mx, 32);
+  const float so = __shfl_xor(sm, 32);
+  const double mn = fmax(mx, mo);
+  const double ms = (mn == -INFINITY) ? 0.0 : mn;
+  const float tot = sm * fast_exp2((float)(mx - ms)) + so * fast_exp2((float)(mo - ms));
+  const double lz2 = mn + (double)log2f(tot);
+  if (valid && g == 0) {
+    rowstat[row] = make_double2(xsq, lz2);
+    if (logZ) logZ[row] = (float)(lz2 * kLn2);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2: responsibilities and sufficient statistics, split over components.
+// ---------------------------------------------------------------------------
+template <int DP>
+constexpr size_t accum_lds_bytes() {
+  return (size_t)2 * 32 * (DP + 4) * sizeof(float) + (size_t)2 * 32 * sizeof(double2);
+}
+
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(accum_waves_per_eu(DP), accum_waves_per_eu(DP))))
+void iso_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+               const f32x4* __restrict__ mu_sw, const double4* __restrict__ kc_lin, int KB, int KP,
+               const double2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
+               float* __restrict__ part_mu, float* __restrict__ part_nk, float* __restrict__ part_sig) {
+  constexpr int NM = DP / 8;
+  constexpr int NJ = DP / 32;      // 32-column blocks of mu_acc
+  constexpr int RS = DP + 4;       // LDS row stride in floats
+  constexpr int V4 = DP / 4;       // float4 per row
+  constexpr int LPT = (32 * V4) / kThreads;  // float4 loads per thread per tile
+  static_assert((32 * V4) % kThreads == 0, "tile load must split evenly");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  float* xs = reinterpret_cast<float*>(lds_raw);                                  // [2][32*RS]
+  double2* rs = reinterpret_cast<double2*>(lds_raw + 2 * 32 * RS * sizeof(float));  // [2][32]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int slab = blockIdx.x % nslab;
+  const int cg = blockIdx.x / nslab;
+  const int kb = cg * kWaves + wave;
+  const bool active = kb < KB;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
+
+  f32x4 mub[NM];
+  double Ck = -INFINITY, bk = 0.0, musq = 0.0;
+  if (active) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m) mub[m] = mu_sw[((int64_t)kb * NM + m) * 64 + lane];
+    const double4 kc = kc_lin[(int64_t)kb * 32 + c];
+    Ck = kc.x; bk = kc.y; musq = kc.z;
+  } else {
+#pragma unroll
+    for (int m = 0; m < NM; ++m) mub[m] = zero4();
+  }
+
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
+  float nk = 0.0f, sig = 0.0f;
+
+  // Cooperative tile load: 32 rows x DP columns -> registers -> LDS.
+  f32x4 stage[LPT];
+  double2 rstage = make_double2(0.0, INFINITY);
+  auto fetch = [&](int t) {
+    const int64_t row0 = r_begin + (int64_t)t * 32;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kThreads + tid;
+      const int rr = idx / V4, c4 = idx % V4;
+      const int64_t row = row0 + rr;
+      stage[q] = load_row4(X, ldx, row, c4 * 4, D, row < r_end);
+    }
+    if (tid < 32) {
+      const int64_t row = row0 + tid;
+      rstage = (row < r_end) ? rowstat[row] : make_double2(0.0, INFINITY);
+    }
+  };
+  auto commit = [&](int buf) {
+    float* dst = xs + buf * 32 * RS;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kThreads + tid;
+      const int rr = idx / V4, c4 = idx % V4;
+      *reinterpret_cast<f32x4*>(dst + rr * RS + c4 * 4) = stage[q];
+    }
+    if (tid < 32) rs[buf * 32 + tid] = rstage;
+  };
+
+  if (ntiles > 0) {
+    fetch(0);
+    commit(0);
+  }
+  __syncthreads();
+
+  // One barrier per tile.  The global loads of tile t+1 are issued after the
+  // responsibilities of tile t are formed (the S partials are dead by then) and
+  // land in registers while the accumulation MFMAs run; they are written to
+  // the other LDS buffer just before the barrier.  That buffer was last read in
+  // iteration t-1, which every wave finished before the previous barrier.
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    const float* xt = xs + buf * 32 * RS;
+    const double2* rt = rs + buf * 32;
+    // S[row][comp] = sum_d X[row][d] mu[comp][d] : lane = component, register i = row acc_row(i, g).
+    double xm[16];
+    if (active)
+      cross_tile<NM>(
+          xm, [&](int m) { return *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * m + 4 * g); },
+          [&](int m) { return mub[m]; });
+    float r[16];
+    if (active) {
+      // Rows of this lane's accumulator registers: acc_row(i, g) = 4g + (8*(i/4) + i%4).
+      const double2* rbase = rt + 4 * g;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ro = 8 * (i >> 2) + (i & 3);
+        const double2 st = rbase[ro];  // (||x||^2, logZ2)
+        const double u = fma(-2.0, xm[i], st.x);
+        const double tt = fma(-bk, u, Ck - st.y);
+        const float rv = fast_exp2((float)tt);
+        nk += rv;
+        sig = fmaf(rv, (float)(u + musq), sig);
+        r[i] = rv;
+      }
+    }
+    if (more) fetch(t + 1);
+    if (active) {
+      const float* xbase = xt + 4 * g * RS + c;
+      // mu_acc[comp][32j + n] += sum_rows r[row][comp] * X[row][32j + n]
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ro = 8 * (i >> 2) + (i & 3);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
+      }
+    }
+    if (more) commit(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (active) {
+    nk += __shfl_xor(nk, 32);
+    sig += __shfl_xor(sig, 32);
+    const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[j][i];
+    }
+    if (g == 0) {
+      part_nk[kbase + c] = nk;
+      part_sig[kbase + c] = sig;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Finish: fixed-order fp64 reduction over slabs (deterministic).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void iso_reduce(const float* __restrict__ part_mu,
+                                                  const float* __restrict__ part_nk,
+                                                  const float* __restrict__ part_sig, int nslab,
+                                                  int KP, int DP, int64_t K, int D,
+                                                  float* __restrict__ Nk, float* __restrict__ mu_acc,
+                                                  float* __restrict__ sig_acc, int accumulate) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int W = D + 2;
+  if (idx >= K * W) return;
+  const int64_t k = idx / W;
+  const int col = (int)(idx % W);
+  double s = 0.0;
+  if (col < D) {
+    for (int sl = 0; sl < nslab; ++sl) s += (double)part_mu[((int64_t)sl * KP + k) * DP + col];
+    float* o = mu_acc + k * D + col;
+    *o = accumulate ? (float)((double)*o + s) : (float)s;
+  } else if (col == D) {
+    for (int sl = 0; sl < nslab; ++sl) s += (double)part_nk[(int64_t)sl * KP + k];
+    Nk[k] = accumulate ? (float)((double)Nk[k] + s) : (float)s;
+  } else {
+    for (int sl = 0; sl < nslab; ++sl) s += (double)part_sig[(int64_t)sl * KP + k];
+    sig_acc[k] = accumulate ? (float)((double)sig_acc[k] + s) : (float)s;
+  }
+}
+
+// Atomic finish: every slab partial is added into the (zeroed or accumulated) outputs.
+__global__ __launch_bounds__(256) void iso_reduce_atomic(const float* __restrict__ part_mu,
+                                                         const float* __restrict__ part_nk,
+                                                         const float* __restrict__ part_sig, int nslab,
+                                                         int KP, int DP, int64_t K, int D,
+                                                         float* __restrict__ Nk, float* __restrict__ mu_acc,
+                                                         float* __restrict__ sig_acc) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int W = D + 2;
+  const int sl = blockIdx.y;
+  if (idx >= K * W || sl >= nslab) return;
+  const int64_t k = idx / W;
+  const int col = (int)(idx % W);
+  if (col < D)
+    atomicAdd(mu_acc + k * D + col, part_mu[((int64_t)sl * KP + k) * DP + col]);
+  else if (col == D)
+    atomicAdd(Nk + k, part_nk[(int64_t)sl * KP + k]);
+  else
+    atomicAdd(sig_acc + k, part_sig[(int64_t)sl * KP + k]);
+}
+
+__global__ __launch_bounds__(256) void fill_f32(float* __restrict__ p, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+template <int DP>
+hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
+                         float* logZ, bool run1, bool run2, hipStream_t stream) {
+  const f32x4* mu_sw = reinterpret_cast<const f32x4*>(ws + pl.off_musw);
+  const double2* kc_blk = reinterpret_cast<const double2*>(ws + pl.off_kcblk);
+  const double4* kc_lin = reinterpret_cast<const double4*>(ws + pl.off_kclin);
+  double2* rowstat = reinterpret_cast<double2*>(ws + pl.off_rowstat);
+  if (run1) {
+    const int64_t nblk1 = cdiv(pl.N, 32 * kWaves);
+    hipLaunchKernelGGL(iso_lse<DP>, dim3((unsigned)nblk1), dim3(kThreads), 0, stream, X, ldx, pl.N,
+                       (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
+  }
+  if (!run2) return hipGetLastError();
+  constexpr size_t lds = accum_lds_bytes<DP>();
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum<DP>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(iso_accum<DP>, dim3((unsigned)(pl.nslab * pl.ncg)), dim3(kThreads), lds, stream,
+                     X, ldx, pl.N, (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab,
+                     pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_mu),
+                     reinterpret_cast<float*>(ws + pl.off_part_nk),
+                     reinterpret_cast<float*>(ws + pl.off_part_sig));
+  return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace fgmm
+
+using namespace fgmm;
+
+extern "C" size_t fgmm_iso_workspace_bytes(int64_t N, int64_t K, int64_t D) {
+  if (N < 0 || K < 0 || D < 1) return 0;
+  return make_plan(N, K, D).total;
+}
+
+extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
+                                  int64_t ldmu, int64_t K, const float* log_sigma_sq,
+                                  const float* log_pi, float* logZ, float* Nk, float* mu_acc,
+                                  float* sig_acc, void* workspace, size_t workspace_bytes,
+                                  unsigned flags, void* stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const bool want_logz = !(flags & FGMM_FLAG_NO_LOGZ);
+  const bool accumulate = (flags & FGMM_FLAG_ACCUMULATE) != 0;
+  const bool atomic = (flags & FGMM_FLAG_ATOMIC_REDUCE) != 0;
+  if (N < 0 || K < 0 || D < 1) return FGMM_ERR_INVALID_ARG;
+  if (N > 0 && (X == nullptr || ldx < round_up(D, 4) || (ldx % 4) != 0 ||
+                (reinterpret_cast<uintptr_t>(X) & 15) != 0))
+    return FGMM_ERR_INVALID_ARG;
+  if (N > 0 && want_logz && logZ == nullptr) return FGMM_ERR_INVALID_ARG;
+  if (K > 0 && (mu == nullptr || ldmu < D || log_sigma_sq == nullptr || log_pi == nullptr ||
+                Nk == nullptr || mu_acc == nullptr || sig_acc == nullptr))
+    return FGMM_ERR_INVALID_ARG;
+  if (D > 256) return FGMM_ERR_UNSUPPORTED;
+  if (N > (int64_t)1 << 40 || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
+  const IsoPlan pl = make_plan(N, K, D);
+  if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
+  if (!want_logz) logZ = nullptr;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  const bool sel1 = (flags & FGMM_FLAG_PHASE1) != 0, sel2 = (flags & FGMM_FLAG_PHASE2) != 0;
+  const bool run1 = sel1 || !sel2, run2 = sel2 || !sel1;
+
+  if (K == 0) {
+    // No components: logsumexp over an empty set is -inf (flash_gmm.py:72-73,102).
+    if (N > 0 && logZ)
+      hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, stream, logZ, N,
+                         -INFINITY);
+    return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+  }
+
+  if (run1)
+    hipLaunchKernelGGL(iso_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, K, (int)D, pl.DP,
+                       log_sigma_sq, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_musw),
+                       reinterpret_cast<double2*>(ws + pl.off_kcblk),
+                       reinterpret_cast<double4*>(ws + pl.off_kclin));
+  if (N > 0) {
+    hipError_t e = hipSuccess;
+    switch (pl.DP) {
+      case 32: e = launch_passes<32>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 96: e = launch_passes<96>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 128: e = launch_passes<128>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 160: e = launch_passes<160>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 192: e = launch_passes<192>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 224: e = launch_passes<224>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 256: e = launch_passes<256>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      default: return FGMM_ERR_UNSUPPORTED;
+    }
+    if (e != hipSuccess) return FGMM_ERR_HIP;
+  }
+  if (!run2) return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+  const float* pmu = reinterpret_cast<const float*>(ws + pl.off_part_mu);
+  const float* pnk = reinterpret_cast<const float*>(ws + pl.off_part_nk);
+  const float* psig = reinterpret_cast<const float*>(ws + pl.off_part_sig);
+  const int64_t nout = K * (D + 2);
+  if (atomic) {
+    if (!accumulate) {
+      hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, stream, Nk, K, 0.0f);
+      hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(K * D, 256)), dim3(256), 0, stream, mu_acc,
+                         K * D, 0.0f);
+      hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, stream, sig_acc, K,
+                         0.0f);
+    }
+    if (pl.nslab > 0)
+      hipLaunchKernelGGL(iso_reduce_atomic, dim3((unsigned)cdiv(nout, 256), (unsigned)pl.nslab),
+                         dim3(256), 0, stream, pmu, pnk, psig, pl.nslab, pl.KP, pl.DP, K, (int)D, Nk,
+                         mu_acc, sig_acc);
+  } else {
+    hipLaunchKernelGGL(iso_reduce, dim3((unsigned)cdiv(nout, 256)), dim3(256), 0, stream, pmu, pnk,
+                       psig, pl.nslab, pl.KP, pl.DP, K, (int)D, Nk, mu_acc, sig_acc,
+                       accumulate ? 1 : 0);
+  }
+  return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+}

@@ -1,0 +1,147 @@
+"""Seeded synthetic GMM workloads.
+
+The reference ships no datasets; its only workload is the smoke benchmark at
+flash_gmm.py:224-234 (X ~ N(0, I), mu ~ N(0, I), lss = 0, uniform log pi).
+The workloads below are the E-step shapes this package is measured on.  In
+"N(0, s I)" the second argument is a variance (N(0, 4I) has std 2).
+
+Every generator takes an explicit ``seed`` and ``device`` and draws from a
+``torch.Generator`` on that device, so the same (seed, device) always yields
+the same tensors.  CPU and GPU generators produce different streams: parity
+tests generate on the CPU and copy to the GPU.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Dict
+
+import torch
+
+
+def _gen(device, seed: int) -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(int(seed))
+    return g
+
+
+def _randn(g, *shape, device, std=1.0):
+    return torch.randn(*shape, generator=g, device=device, dtype=torch.float32) * std
+
+
+def _rand(g, *shape, device, lo=0.0, hi=1.0):
+    return torch.rand(*shape, generator=g, device=device, dtype=torch.float32) * (hi - lo) + lo
+
+
+def iso_plain(N: int, K: int, D: int, seed: int = 0, device="cpu") -> Dict[str, torch.Tensor]:
+    """X ~ N(0, I), mu ~ N(0, 4I), lss = 0, lpi = -log K (the N=10,000, K=64, D=32 golden case)."""
+    g = _gen(device, seed)
+    X = _randn(g, N, D, device=device)
+    mu = _randn(g, K, D, device=device, std=2.0)
+    lss = torch.zeros(K, device=device)
+    lpi = torch.full((K,), -math.log(K), device=device)
+    return dict(X=X, mu=mu, log_sigma_sq=lss, log_pi=lpi)
+
+
+def _assign_rows(g, N, K, device, probs=None):
+    if probs is None:
+        return torch.randint(0, K, (N,), generator=g, device=device)
+    return torch.multinomial(probs.to(device), N, replacement=True, generator=g)
+
+
+def iso_clustered(N: int, K: int, D: int, seed: int = 1, device="cpu",
+                  row_chunk: int = 1 << 20) -> Dict[str, torch.Tensor]:
+    """Clustered isotropic workload (the N=1M, K=1024, D=128 headline shape).
+
+    centres c ~ N(0, 4I); assignment uniform; X = c[a] + N(0, I);
+    mu = c + N(0, 0.25 I); lss ~ U(-0.5, 0.5); lpi = log_softmax(N(0, 1)).
+    """
+    g = _gen(device, seed)
+    c = _randn(g, K, D, device=device, std=2.0)
+    mu = c + _randn(g, K, D, device=device, std=0.5)
+    lss = _rand(g, K, device=device, lo=-0.5, hi=0.5)
+    lpi = torch.log_softmax(_randn(g, K, device=device), dim=0)
+    X = torch.empty(N, D, device=device, dtype=torch.float32)
+    for n0 in range(0, N, row_chunk):
+        n1 = min(N, n0 + row_chunk)
+        a = _assign_rows(g, n1 - n0, K, device)
+        X[n0:n1] = c[a] + _randn(g, n1 - n0, D, device=device)
+    return dict(X=X, mu=mu, log_sigma_sq=lss, log_pi=lpi)
+
+
+def diag_clustered(N: int, K: int, D: int, seed: int = 2, device="cpu",
+                   row_chunk: int = 1 << 20) -> Dict[str, torch.Tensor]:
+    """Axis-aligned clusters (the N=1M, K=1024, D=96 diagonal shape).
+
+    centres ~ N(0, 4I); per-(k, d) log variance ~ U(-1, 1);
+    X = c[a] + exp(0.5 logvar[a]) * N(0, I); mu = c + N(0, 0.25 I);
+    lss = logvar (K x D); lpi uniform.
+    """
+    g = _gen(device, seed)
+    c = _randn(g, K, D, device=device, std=2.0)
+    logvar = _rand(g, K, D, device=device, lo=-1.0, hi=1.0)
+    mu = c + _randn(g, K, D, device=device, std=0.5)
+    lpi = torch.full((K,), -math.log(K), device=device)
+    X = torch.empty(N, D, device=device, dtype=torch.float32)
+    sd = torch.exp(0.5 * logvar)
+    for n0 in range(0, N, row_chunk):
+        n1 = min(N, n0 + row_chunk)
+        a = _assign_rows(g, n1 - n0, K, device)
+        X[n0:n1] = c[a] + sd[a] * _randn(g, n1 - n0, D, device=device)
+    return dict(X=X, mu=mu, log_sigma_sq=logvar, log_pi=lpi)
+
+
+def full_clustered(N: int, K: int, D: int, seed: int = 3, device="cpu") -> Dict[str, torch.Tensor]:
+    """Full-covariance mixture (the N=250K, K=256, D=64 shape).
+
+    A_k ~ N(0, 1) (D x D); Sigma_k = A_k A_k^T / D + 0.1 I;
+    prec_chol_k = cholesky(inv(Sigma_k)) computed in float64 on the host and
+    rounded to float32 (lower-triangular, L L^T = Sigma^-1, the
+    parameterisation of flash_gmm_full_h100.py:238,247-248);
+    centres ~ N(0, 4I), mu = centres; lpi = log_softmax(N(0, 0.5));
+    X sampled from the mixture with assignment ~ pi.
+    """
+    g = _gen(device, seed)
+    A = torch.randn(K, D, D, generator=g, device=device, dtype=torch.float32)
+    A64 = A.double().cpu()
+    sigma = A64 @ A64.transpose(1, 2) / D + 0.1 * torch.eye(D, dtype=torch.float64)
+    prec_chol = torch.linalg.cholesky(torch.linalg.inv(sigma))
+    chol_sigma = torch.linalg.cholesky(sigma)
+    mu = _randn(g, K, D, device=device, std=2.0)
+    lpi = torch.log_softmax(_randn(g, K, device=device, std=math.sqrt(0.5)), dim=0)
+    a = _assign_rows(g, N, K, device, probs=torch.exp(lpi.double()).float())
+    z = _randn(g, N, D, device=device)
+    X = torch.empty(N, D, device=device, dtype=torch.float32)
+    cs = chol_sigma.float().to(device)
+    for k in range(K):
+        idx = (a == k).nonzero(as_tuple=True)[0]
+        if idx.numel():
+            X[idx] = mu[k] + z[idx] @ cs[k].T
+    return dict(X=X, mu=mu, prec_chol=prec_chol.float().to(device), log_pi=lpi)
+
+
+def reference_smoke(N: int = 1_000_000, K: int = 1024, D: int = 128, seed: int = 0,
+                    device="cpu") -> Dict[str, torch.Tensor]:
+    """The reference's own smoke workload shape (flash_gmm.py:228-234)."""
+    g = _gen(device, seed)
+    X = _randn(g, N, D, device=device)
+    mu = _randn(g, K, D, device=device)
+    lss = torch.zeros(K, device=device)
+    lpi = torch.full((K,), -math.log(K), device=device)
+    return dict(X=X, mu=mu, log_sigma_sq=lss, log_pi=lpi)
+
+
+WORKLOADS = {
+    # name: (generator, default sizes, default seed)
+    "iso_n10k_k64_d32": (iso_plain, dict(N=10_000, K=64, D=32), 0),
+    "iso_n1m_k1024_d128": (iso_clustered, dict(N=1_000_000, K=1024, D=128), 1),
+    "diag_n1m_k1024_d96": (diag_clustered, dict(N=1_000_000, K=1024, D=96), 2),
+    "full_n250k_k256_d64": (full_clustered, dict(N=250_000, K=256, D=64), 3),
+}
+
+
+def make(name: str, device="cpu", seed=None, **sizes) -> Dict[str, torch.Tensor]:
+    fn, defaults, dseed = WORKLOADS[name]
+    kw = dict(defaults)
+    kw.update(sizes)
+    return fn(seed=dseed if seed is None else seed, device=device, **kw)

@@ -1,0 +1,144 @@
+"""Drop-in E-step entry points backed by the HIP kernels in libflashgmm.so.
+
+Names, positional order, return tuples and argument checks follow the
+reference:
+
+* ``flash_gmm_estep(X, mu, log_sigma_sq, log_pi, BLOCK_N=64, BLOCK_K=16,
+  BLOCK_D=128)`` -- flash_gmm.py:173-217 (and the 4-argument form of
+  flash_gmm_h100.py:254-328).  The BLOCK_* keywords are accepted for
+  compatibility and ignored: tiles are chosen by the library, and D is not
+  limited by BLOCK_D (the same-named H100 entry sizes BLOCK_D from D,
+  flash_gmm_h100.py:268-270).
+
+Outputs are fresh float32 tensors on X.device (flash_gmm.py:192-195), written
+asynchronously on torch's current stream; nothing synchronises.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import FlashGMMError
+
+__all__ = ["flash_gmm_estep", "iso_estep_into"]
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise FlashGMMError(msg)
+
+
+def _prep_rows(X: torch.Tensor):
+    """Return (X, ldx) when the kernels can read X in place, else a padded copy.
+
+    The kernels read 16-byte row chunks: they need a unit column stride, a row
+    stride that is a multiple of 4 elements and at least round_up(D, 4), and a
+    16-byte aligned base.  In place is used only when D % 4 == 0, so a chunk
+    never reaches past the last element of the tensor.  The reference accepts
+    any strides (flash_gmm.py:202); other layouts are copied.
+    """
+    N, D = X.shape
+    D4 = (D + 3) // 4 * 4
+    if N == 0:
+        return X, D4
+    if D % 4 == 0 and X.data_ptr() % 16 == 0 and X.stride(1) == 1:
+        if N == 1:
+            return X, D4
+        if X.stride(0) % 4 == 0 and X.stride(0) >= D4:
+            return X, X.stride(0)
+    Xp = torch.empty(N, D4, device=X.device, dtype=torch.float32)
+    Xp[:, :D] = X
+    return Xp, D4
+
+
+def _check_common(X, mu, log_pi):
+    _require(X.dim() == 2 and mu.dim() == 2, "X must be (N, D) and mu (K, D)")
+    _require(X.is_cuda and mu.is_cuda, "Inputs must be on GPU.")  # flash_gmm.py:190
+    _require(X.dtype == torch.float32 and mu.dtype == torch.float32,
+             "X and mu must be float32")
+    _require(mu.shape[1] == X.shape[1], f"mu must be (K, D) with D={X.shape[1]}, got {tuple(mu.shape)}")
+    _require(mu.device == X.device, "X and mu must be on the same device")
+    K = mu.shape[0]
+    _require(log_pi.shape == (K,), f"log_pi must be ({K},), got {tuple(log_pi.shape)}")
+
+
+def _vec(t: torch.Tensor, device, shape, name) -> torch.Tensor:
+    _require(tuple(t.shape) == tuple(shape), f"{name} must be {tuple(shape)}, got {tuple(t.shape)}")
+    return t.to(device=device, dtype=torch.float32).contiguous()
+
+
+def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
+                   accumulate: bool = False, atomic_reduce: bool = False,
+                   workspace: torch.Tensor | None = None, phase: int = 0) -> None:
+    """Isotropic E-step writing into caller-provided outputs.
+
+    ``logZ`` may be None (it is then not written).  With ``accumulate`` the
+    statistics are added to the current contents of Nk / mu_acc / sig_acc
+    (streaming over row chunks, README.md:86-96).  ``phase`` 1 runs only the
+    log-normaliser pass, 2 only the accumulation (reusing ``workspace`` from a
+    phase-1 call on the same inputs), 0 both.
+    """
+    _check_common(X, mu, log_pi)
+    N, D = X.shape
+    K = mu.shape[0]
+    dev = X.device
+    lss = _vec(log_sigma_sq, dev, (K,), "log_sigma_sq")
+    lpi = _vec(log_pi, dev, (K,), "log_pi")
+    Xk, ldx = _prep_rows(X)
+    muk = mu if (mu.stride(1) == 1 or D == 1) else mu.contiguous()
+    ldmu = muk.stride(0) if K > 1 else D
+    L = _lib.lib()
+    ws_bytes = int(L.fgmm_iso_workspace_bytes(N, K, D))
+    if workspace is None or workspace.numel() < ws_bytes:
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    flags = 0
+    if accumulate:
+        flags |= _lib.FLAG_ACCUMULATE
+    if logZ is None:
+        flags |= _lib.FLAG_NO_LOGZ
+    if atomic_reduce:
+        flags |= _lib.FLAG_ATOMIC_REDUCE
+    if phase == 1:
+        flags |= _lib.FLAG_PHASE1
+    elif phase == 2:
+        flags |= _lib.FLAG_PHASE2
+    elif phase != 0:
+        raise FlashGMMError(f"phase must be 0, 1 or 2, got {phase}")
+    for name, t, shp in (("Nk", Nk, (K,)), ("mu_acc", mu_acc, (K, D)), ("sig_acc", sig_acc, (K,))):
+        _require(tuple(t.shape) == shp and t.dtype == torch.float32 and t.is_contiguous()
+                 and t.device == dev, f"{name} must be a contiguous float32 {shp} tensor on {dev}")
+    if logZ is not None:
+        _require(tuple(logZ.shape) == (N,) and logZ.dtype == torch.float32 and logZ.is_contiguous(),
+                 f"logZ must be a contiguous float32 ({N},) tensor")
+    with torch.cuda.device(dev):
+        st = L.fgmm_iso_estep_f32(
+            Xk.data_ptr() if N > 0 else None, ldx, N, D,
+            muk.data_ptr() if K > 0 else None, ldmu, K,
+            lss.data_ptr() if K > 0 else None, lpi.data_ptr() if K > 0 else None,
+            logZ.data_ptr() if (logZ is not None and N > 0) else None,
+            Nk.data_ptr() if K > 0 else None, mu_acc.data_ptr() if K > 0 else None,
+            sig_acc.data_ptr() if K > 0 else None,
+            workspace.data_ptr(), workspace.numel(), flags, _lib.stream_handle(dev))
+    _lib.check(st, "fgmm_iso_estep_f32")
+
+
+def flash_gmm_estep(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tensor,
+                    log_pi: torch.Tensor, BLOCK_N: int = 64, BLOCK_K: int = 16,
+                    BLOCK_D: int = 128):
+    """Flash-GMM isotropic E-step: returns (logZ, Nk, mu_acc, sig_acc).
+
+    logZ (N,) per-sample log-normaliser, Nk (K,) = sum_n r_nk,
+    mu_acc (K, D) = sum_n r_nk x_n, sig_acc (K,) = sum_n r_nk ||x_n - mu_k||^2
+    (flash_gmm.py:22-37).  BLOCK_N / BLOCK_K / BLOCK_D are ignored.
+    """
+    _check_common(X, mu, log_pi)
+    N, D = X.shape
+    K = mu.shape[0]
+    dev = X.device
+    logZ = torch.empty(N, device=dev, dtype=torch.float32)
+    Nk = torch.empty(K, device=dev, dtype=torch.float32)
+    mu_acc = torch.empty(K, D, device=dev, dtype=torch.float32)
+    sig_acc = torch.empty(K, device=dev, dtype=torch.float32)
+    iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc)
+    return logZ, Nk, mu_acc, sig_acc

@@ -1,0 +1,251 @@
+"""CPU oracle for the Flash-GMM E-step — TEST INFRASTRUCTURE ONLY.
+
+This module restates the reference's E-step mathematics on the CPU with
+PyTorch so that the HIP kernels can be checked against it.  Only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+it, and only as the checker: the product path in ``flash_gmm`` never calls it
+and fails loudly when its native library is missing.
+
+Every function is chunked over rows so that the N x K responsibility matrix is
+never held whole, and runs in either float64 (the golden) or float32 (the
+reference's own arithmetic, used as the CPU baseline).
+
+Parity pinning (what checks each function, see tests/test_oracle.py):
+
+* ``estep_iso`` -- logZ against scipy.stats.multivariate_normal.logpdf +
+  scipy.special.logsumexp; all four outputs against sklearn's spherical
+  GaussianMixture internals; the expansion form against the direct form;
+  invariants (sum Nk = N, sum_k mu_acc = sum_n x_n, the sig_acc identity);
+  special cases (K = 1, identical components, far-apart clusters); brute force
+  with Python loops on tiny inputs; committed golden vectors.
+* ``estep_diag`` -- scipy logpdf with a diagonal covariance, sklearn 'diag'
+  internals, brute force, invariants, reduction to ``estep_iso`` when every
+  per-dimension variance of a component is equal.
+* ``estep_full`` -- scipy logpdf with the full covariance recovered from the
+  precision Cholesky factor, sklearn 'full' internals, brute force, reduction
+  to ``estep_diag`` for diagonal factors.
+* ``mstep_*`` -- closed forms against the README formulas, checked by the
+  fixed point of an exactly-fitted single component.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Tuple
+
+import torch
+
+LOG_2PI = 1.8378770664093453  # flash_gmm.py:91
+Tensor = torch.Tensor
+
+_DEFAULT_CHUNK = 16384
+
+
+def _as(t: Tensor, dtype: torch.dtype) -> Tensor:
+    return t.detach().to(device="cpu", dtype=dtype)
+
+
+def iso_log_prob(X: Tensor, mu: Tensor, lss: Tensor, lpi: Tensor,
+                 form: str = "expansion") -> Tuple[Tensor, Tensor]:
+    """Per-(n, k) log joint ll_nk and squared distance sq_nk for spherical components.
+
+    Follows flash_gmm.py:84-93:
+        sq = ||x||^2 - 2 x.mu + ||mu||^2             (form="expansion")
+        ll = lpi - 0.5 * sq * exp(-lss) - 0.5 * D * (log2pi + lss)
+    ``form="direct"`` evaluates sq as sum_d (x_d - mu_d)^2 instead (no
+    cancellation; used for the float64 golden on small inputs).
+    """
+    D = X.shape[1]
+    if form == "expansion":
+        x_sq = (X * X).sum(dim=1)                       # flash_gmm.py:85
+        mu_sq = (mu * mu).sum(dim=1)                    # flash_gmm.py:86
+        xmu = X @ mu.T                                  # flash_gmm.py:87
+        sq = x_sq[:, None] - 2.0 * xmu + mu_sq[None, :]  # flash_gmm.py:88
+    elif form == "direct":
+        sq = ((X[:, None, :] - mu[None, :, :]) ** 2).sum(dim=2)
+    else:
+        raise ValueError(form)
+    inv_s = torch.exp(-lss)                             # flash_gmm.py:90
+    ll = lpi[None, :] - 0.5 * sq * inv_s[None, :] - 0.5 * D * (LOG_2PI + lss[None, :])  # :92
+    return ll, sq
+
+
+def estep_iso(X: Tensor, mu: Tensor, log_sigma_sq: Tensor, log_pi: Tensor, *,
+              dtype: torch.dtype = torch.float64, form: str = "expansion",
+              chunk: int = _DEFAULT_CHUNK) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Isotropic E-step: (logZ, Nk, mu_acc, sig_acc).
+
+    Pass 1 (logZ = logsumexp_k ll) follows flash_gmm.py:84-103; pass 2 follows
+    flash_gmm.py:141-166: r = exp(ll - logZ), Nk = sum_n r,
+    sig_acc = sum_n r * sq (sq by the same expansion), mu_acc = r^T X.
+    Shapes and dtypes follow flash_gmm.py:187-195.
+    """
+    X, mu = _as(X, dtype), _as(mu, dtype)
+    lss, lpi = _as(log_sigma_sq, dtype), _as(log_pi, dtype)
+    N, D = X.shape
+    K = mu.shape[0]
+    logZ = torch.empty(N, dtype=dtype)
+    Nk = torch.zeros(K, dtype=dtype)
+    mu_acc = torch.zeros(K, D, dtype=dtype)
+    sig_acc = torch.zeros(K, dtype=dtype)
+    for n0 in range(0, N, chunk):
+        x = X[n0:n0 + chunk]
+        ll, sq = iso_log_prob(x, mu, lss, lpi, form)
+        lz = torch.logsumexp(ll, dim=1)                 # flash_gmm.py:95-102
+        logZ[n0:n0 + chunk] = lz
+        r = torch.exp(ll - lz[:, None])                 # flash_gmm.py:151
+        Nk += r.sum(dim=0)                              # flash_gmm.py:155
+        sig_acc += (r * sq).sum(dim=0)                  # flash_gmm.py:156
+        mu_acc += r.T @ x                               # flash_gmm.py:161
+    return logZ, Nk, mu_acc, sig_acc
+
+
+def diag_log_prob(X: Tensor, mu: Tensor, lss: Tensor, lpi: Tensor,
+                  form: str = "expansion") -> Tensor:
+    """Per-(n, k) log joint for diagonal components (natural-log units).
+
+    The reference works in log2 units with
+        inv_sigma_sq = exp(-lss) * 0.5*log2e,  mu_w = mu * inv_sigma_sq
+        c0 = (lpi - 0.5*(D*log2pi + sum_d lss)) * log2e - sum_d mu^2 e^{-lss} * 0.5*log2e
+        ll2 = c0 - (x^2) . inv_sigma_sq^T + 2 x . mu_w^T
+    (flash_gmm_diag_h100.py:332-340, :116-119).  Dividing by log2e gives the
+    natural-log form evaluated here.
+    """
+    D = X.shape[1]
+    w = torch.exp(-lss)                                  # (K, D)
+    if form == "expansion":
+        quad = (X * X) @ w.T - 2.0 * X @ (mu * w).T + (mu * mu * w).sum(dim=1)[None, :]
+    elif form == "direct":
+        quad = (((X[:, None, :] - mu[None, :, :]) ** 2) * w[None, :, :]).sum(dim=2)
+    else:
+        raise ValueError(form)
+    ll = lpi[None, :] - 0.5 * (D * LOG_2PI + lss.sum(dim=1))[None, :] - 0.5 * quad
+    return ll
+
+
+def estep_diag(X: Tensor, mu: Tensor, log_sigma_sq: Tensor, log_pi: Tensor, *,
+               dtype: torch.dtype = torch.float64, form: str = "expansion",
+               chunk: int = _DEFAULT_CHUNK) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Diagonal-covariance E-step: (logZ, Nk, mu_acc, sig_acc[K, D]).
+
+    sig_acc[k, d] = sum_n r_nk (x_nd - mu_kd)^2, which the reference finalises
+    as rxsq - 2 mu * mu_local + mu^2 * nk (flash_gmm_diag_h100.py:254-260) and
+    returns sliced to (K, D) (:380-384).
+    """
+    X, mu = _as(X, dtype), _as(mu, dtype)
+    lss, lpi = _as(log_sigma_sq, dtype), _as(log_pi, dtype)
+    N, D = X.shape
+    K = mu.shape[0]
+    if lss.shape != (K, D):
+        raise ValueError(f"log_sigma_sq must be (K, D)=({K}, {D}), got {tuple(lss.shape)}")
+    logZ = torch.empty(N, dtype=dtype)
+    Nk = torch.zeros(K, dtype=dtype)
+    mu_acc = torch.zeros(K, D, dtype=dtype)
+    rxsq = torch.zeros(K, D, dtype=dtype)
+    for n0 in range(0, N, chunk):
+        x = X[n0:n0 + chunk]
+        ll = diag_log_prob(x, mu, lss, lpi, form)
+        lz = torch.logsumexp(ll, dim=1)
+        logZ[n0:n0 + chunk] = lz
+        r = torch.exp(ll - lz[:, None])
+        Nk += r.sum(dim=0)
+        mu_acc += r.T @ x
+        rxsq += r.T @ (x * x)
+    sig_acc = rxsq - 2.0 * mu * mu_acc + mu * mu * Nk[:, None]
+    return logZ, Nk, mu_acc, sig_acc
+
+
+def full_log_prob(X: Tensor, mu: Tensor, prec_chol: Tensor, lpi: Tensor) -> Tensor:
+    """Per-(n, k) log joint for full covariance given L_k with L_k L_k^T = Sigma_k^-1.
+
+    Follows flash_gmm_full_h100.py:289-296 and :124-130:
+        v = L^T x - L^T mu,  maha = ||v||^2,
+        ll = lpi + sum_d log(|L_dd| + 1e-30) - 0.5*D*log2pi - 0.5*maha
+    """
+    D = X.shape[1]
+    LT = prec_chol.transpose(-1, -2)                               # :289
+    LT_mu = torch.einsum("kij,kj->ki", LT, mu)                      # :290
+    log_diag_sum = torch.log(prec_chol.diagonal(dim1=-2, dim2=-1).abs() + 1e-30).sum(dim=-1)  # :294
+    v = torch.einsum("kij,nj->nki", LT, X) - LT_mu[None, :, :]      # :124-126
+    maha = (v * v).sum(dim=2)                                       # :127
+    return lpi[None, :] + log_diag_sum[None, :] - 0.5 * D * LOG_2PI - 0.5 * maha
+
+
+def estep_full(X: Tensor, mu: Tensor, prec_chol: Tensor, log_pi: Tensor, *,
+               dtype: torch.dtype = torch.float64,
+               chunk: int = 4096) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Full-covariance E-step: (logZ, Nk, mu_acc, sig_outer[K, D, D]).
+
+    sig_outer[k] = sum_n r_nk x_n x_n^T, uncentred (flash_gmm_full_h100.py:213-228,
+    docstring :251-255).
+    """
+    X, mu = _as(X, dtype), _as(mu, dtype)
+    L, lpi = _as(prec_chol, dtype), _as(log_pi, dtype)
+    N, D = X.shape
+    K = mu.shape[0]
+    if L.shape != (K, D, D):
+        raise ValueError(f"prec_chol must be (K, D, D)=({K}, {D}, {D}), got {tuple(L.shape)}")
+    logZ = torch.empty(N, dtype=dtype)
+    Nk = torch.zeros(K, dtype=dtype)
+    mu_acc = torch.zeros(K, D, dtype=dtype)
+    sig_outer = torch.zeros(K, D, D, dtype=dtype)
+    for n0 in range(0, N, chunk):
+        x = X[n0:n0 + chunk]
+        ll = full_log_prob(x, mu, L, lpi)
+        lz = torch.logsumexp(ll, dim=1)
+        logZ[n0:n0 + chunk] = lz
+        r = torch.exp(ll - lz[:, None])
+        Nk += r.sum(dim=0)
+        mu_acc += r.T @ x
+        sig_outer += torch.einsum("nk,ni,nj->kij", r, x, x)
+    return logZ, Nk, mu_acc, sig_outer
+
+
+# ---------------------------------------------------------------------------
+# M-steps (README.md:59-61, :99-100; flash_gmm_full_h100.py:257-260)
+# ---------------------------------------------------------------------------
+
+def mstep_iso(Nk: Tensor, mu_acc: Tensor, sig_acc: Tensor, N: int, D: int):
+    """pi = Nk/N, mu = mu_acc/Nk, sigma^2 = sig_acc/(D*Nk)  (README.md:59-61)."""
+    pi = Nk / N
+    mu = mu_acc / Nk[:, None]
+    sigma_sq = sig_acc / (D * Nk)
+    return pi, mu, sigma_sq
+
+
+def mstep_full(Nk: Tensor, mu_acc: Tensor, sig_outer: Tensor, N: int):
+    """Sigma_k = sig_outer/Nk - mu mu^T  (flash_gmm_full_h100.py:257-260)."""
+    pi = Nk / N
+    mu = mu_acc / Nk[:, None]
+    cov = sig_outer / Nk[:, None, None] - mu[:, :, None] * mu[:, None, :]
+    return pi, mu, cov
+
+
+# ---------------------------------------------------------------------------
+# Brute force (pure Python loops, tiny inputs only)
+# ---------------------------------------------------------------------------
+
+def brute_estep_iso(X, mu, lss, lpi):
+    """Scalar-loop float64 E-step, for N, K, D <= ~16 (direct distances)."""
+    X = [[float(v) for v in row] for row in X.tolist()]
+    mu = [[float(v) for v in row] for row in mu.tolist()]
+    lss = [float(v) for v in lss.tolist()]
+    lpi = [float(v) for v in lpi.tolist()]
+    N, D, K = len(X), len(X[0]) if X else 0, len(mu)
+    logZ, Nk = [], [0.0] * K
+    mu_acc = [[0.0] * D for _ in range(K)]
+    sig_acc = [0.0] * K
+    for n in range(N):
+        sq = [sum((X[n][d] - mu[k][d]) ** 2 for d in range(D)) for k in range(K)]
+        ll = [lpi[k] - 0.5 * sq[k] * math.exp(-lss[k]) - 0.5 * D * (LOG_2PI + lss[k])
+              for k in range(K)]
+        m = max(ll)
+        lz = m + math.log(sum(math.exp(v - m) for v in ll))
+        logZ.append(lz)
+        for k in range(K):
+            r = math.exp(ll[k] - lz)
+            Nk[k] += r
+            sig_acc[k] += r * sq[k]
+            for d in range(D):
+                mu_acc[k][d] += r * X[n][d]
+    return logZ, Nk, mu_acc, sig_acc

@@ -1,0 +1,99 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+declared in include/flashgmm.h, and rejects bad arguments before any HIP call."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from flash_gmm import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "flashgmm.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fgmm_\w+)\s*\(", text)))
+
+
+def test_library_built_and_loads():
+    assert os.path.exists(_lib.LIB_PATH), "run __graft_entry__.build() first"
+    L = _lib.lib()
+    assert L.fgmm_version() >= 10000
+
+
+def test_exports_every_declared_symbol():
+    names = declared_functions()
+    assert "fgmm_iso_estep_f32" in names
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in names if not hasattr(raw, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_strerror_names_every_status():
+    L = _lib.lib()
+    for st in (0, -1, -2, -3, -4):
+        assert L.fgmm_strerror(st).decode() != "unknown status"
+    assert L.fgmm_strerror(-99).decode() == "unknown status"
+
+
+def test_iso_workspace_bytes_grows_with_size():
+    L = _lib.lib()
+    a = L.fgmm_iso_workspace_bytes(1000, 64, 32)
+    b = L.fgmm_iso_workspace_bytes(1_000_000, 1024, 128)
+    assert 0 < a < b
+    # per-row state (16 B/row) + O(K*D) terms: stays far below the N*K responsibility matrix
+    assert b < 1_000_000 * 1024 * 4 // 20
+    assert L.fgmm_iso_workspace_bytes(-1, 4, 4) == 0
+    assert L.fgmm_iso_workspace_bytes(10, 4, 0) == 0
+
+
+# Fake but aligned, non-null addresses: every call below must be rejected by
+# argument validation, which happens before any pointer is used.  They only
+# run where no GPU is present, so a validation bug cannot turn them into a
+# kernel launch on a real device.
+no_gpu = pytest.mark.skipif(torch.cuda.is_available(), reason="host-only validation checks")
+FAKE = 1 << 20
+
+
+def _call_iso(**kw):
+    a = dict(X=FAKE, ldx=32, N=10, D=32, mu=FAKE, ldmu=32, K=4, lss=FAKE, lpi=FAKE,
+             logZ=FAKE, Nk=FAKE, mu_acc=FAKE, sig=FAKE, ws=FAKE, ws_bytes=1 << 40, flags=0)
+    a.update(kw)
+    L = _lib.lib()
+    return L.fgmm_iso_estep_f32(a["X"], a["ldx"], a["N"], a["D"], a["mu"], a["ldmu"], a["K"],
+                                a["lss"], a["lpi"], a["logZ"], a["Nk"], a["mu_acc"], a["sig"],
+                                a["ws"], a["ws_bytes"], a["flags"], None)
+
+
+@no_gpu
+@pytest.mark.parametrize("kw,status", [
+    (dict(N=-1), _lib.FGMM_ERR_INVALID_ARG),
+    (dict(D=0), _lib.FGMM_ERR_INVALID_ARG),
+    (dict(K=-2), _lib.FGMM_ERR_INVALID_ARG),
+    (dict(X=None), _lib.FGMM_ERR_INVALID_ARG),
+    (dict(ldx=30), _lib.FGMM_ERR_INVALID_ARG),          # not a multiple of 4
+    (dict(ldx=28), _lib.FGMM_ERR_INVALID_ARG),          # shorter than the row
+    (dict(X=FAKE + 4), _lib.FGMM_ERR_INVALID_ARG),      # not 16-byte aligned
+    (dict(logZ=None), _lib.FGMM_ERR_INVALID_ARG),
+    (dict(mu=None), _lib.FGMM_ERR_INVALID_ARG),
+    (dict(ldmu=16), _lib.FGMM_ERR_INVALID_ARG),
+    (dict(Nk=None), _lib.FGMM_ERR_INVALID_ARG),
+    (dict(D=300, ldx=300, ldmu=300), _lib.FGMM_ERR_UNSUPPORTED),
+    (dict(ws_bytes=16), _lib.FGMM_ERR_WORKSPACE),
+    (dict(ws=None), _lib.FGMM_ERR_WORKSPACE),
+])
+def test_iso_rejects_bad_arguments(kw, status):
+    assert _call_iso(**kw) == status
+
+
+def test_python_layer_rejects_cpu_tensors():
+    from flash_gmm import FlashGMMError, flash_gmm_estep
+    X = torch.zeros(4, 3)
+    with pytest.raises(AssertionError):
+        flash_gmm_estep(X, torch.zeros(2, 3), torch.zeros(2), torch.zeros(2))
+    with pytest.raises(FlashGMMError):
+        flash_gmm_estep(X, torch.zeros(2, 3), torch.zeros(2), torch.zeros(2))

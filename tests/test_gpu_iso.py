@@ -1,0 +1,209 @@
+"""GPU parity of the isotropic E-step against the CPU oracle.
+
+Tolerances (float32 kernels against the float64 oracle):
+  logZ     abs <= 1e-4
+  Nk, sig  |d| <= 1e-4 * |ref| + 1e-6 * max|ref|   (floor for near-empty components)
+  mu_acc   max|d| <= 1e-4 * max|ref|                (norm-wise; entries near zero
+                                                     make element-wise rel meaningless)
+"""
+
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from flash_gmm import FlashGMMError, data, flash_gmm_estep, iso_estep_into
+from oracle import gmm_oracle as O
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+import make_golden  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+LOGZ_ATOL = 1e-4
+REL = 1e-4
+
+
+def _np(t):
+    return t.detach().double().cpu().numpy()
+
+
+def assert_close_stats(got, ref, what=""):
+    lz, nk, mu_acc, sig = (_np(t) for t in got)
+    rlz, rnk, rmu, rsig = (np.asarray(t, dtype=np.float64) for t in ref)
+    if rlz.size:
+        err = np.abs(lz - rlz)
+        finite = np.isfinite(rlz)
+        assert np.array_equal(np.isfinite(lz), finite), f"{what} logZ finiteness"
+        assert err[finite].max(initial=0) <= LOGZ_ATOL, f"{what} logZ max abs err {err[finite].max()}"
+    for name, g, r in (("Nk", nk, rnk), ("sig", sig, rsig)):
+        if r.size:
+            tol = REL * np.abs(r) + 1e-6 * np.abs(r).max(initial=0)
+            bad = np.abs(g - r) > tol
+            assert not bad.any(), f"{what} {name} max rel err {(np.abs(g - r) / np.maximum(np.abs(r), 1e-30)).max()}"
+    if rmu.size:
+        scale = np.abs(rmu).max(initial=0)
+        assert np.abs(mu_acc - rmu).max(initial=0) <= REL * scale + 1e-30, \
+            f"{what} mu_acc norm-wise err {np.abs(mu_acc - rmu).max() / max(scale, 1e-30)}"
+
+
+def run_gpu(inp, dev, **kw):
+    args = [inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
+    out = flash_gmm_estep(*args, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+def oracle(inp):
+    return O.estep_iso(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+
+
+@pytest.mark.parametrize("name", ["iso_n10k_k64_d32", "iso_clustered_n4096_k96_d40"])
+def test_golden_vectors(name, gpu_device):
+    inp, kind = make_golden.make_inputs(name)
+    fx = np.load(os.path.join(os.path.dirname(make_golden.__file__), name + ".npz"))
+    assert str(fx["sha256"]) == make_golden.input_digest(inp), "input generator changed"
+    got = run_gpu(inp, gpu_device)
+    assert_close_stats(got, (fx["logZ"], fx["Nk"], fx["mu_acc"], fx["sig"]), name)
+
+
+SHAPES = [
+    # (N, K, D)
+    (1, 1, 1), (31, 3, 5), (33, 17, 3), (129, 33, 32), (1000, 100, 96), (257, 64, 100),
+    (300, 40, 128), (200, 32, 129), (150, 7, 256), (2048, 1, 64), (4097, 70, 64),
+]
+
+
+@pytest.mark.parametrize("N,K,D", SHAPES)
+def test_edge_shapes(N, K, D, gpu_device):
+    inp = data.iso_clustered(N, K, D, seed=N + K + D)
+    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), f"N={N} K={K} D={D}")
+
+
+def test_empty_rows(gpu_device):
+    inp = data.iso_plain(0, 8, 16, seed=3)
+    lz, nk, mu_acc, sig = run_gpu(inp, gpu_device)
+    assert lz.shape == (0,)
+    assert torch.all(nk == 0) and torch.all(mu_acc == 0) and torch.all(sig == 0)
+
+
+def test_no_components(gpu_device):
+    inp = data.iso_plain(40, 1, 8, seed=4)
+    inp["mu"] = inp["mu"][:0]
+    inp["log_sigma_sq"] = inp["log_sigma_sq"][:0]
+    inp["log_pi"] = inp["log_pi"][:0]
+    lz, nk, mu_acc, sig = run_gpu(inp, gpu_device)
+    assert torch.all(torch.isneginf(lz)) and nk.numel() == 0 and mu_acc.shape == (0, 8)
+
+
+def test_zero_weight_components(gpu_device):
+    inp = data.iso_clustered(500, 20, 24, seed=5)
+    inp["log_pi"][[0, 3, 19]] = -math.inf
+    got = run_gpu(inp, gpu_device)
+    assert_close_stats(got, oracle(inp), "lpi=-inf")
+    assert float(got[1][0]) == 0.0 and float(got[1][19]) == 0.0
+
+
+def test_strided_inputs(gpu_device):
+    inp = data.iso_clustered(700, 30, 40, seed=6)
+    ref = oracle(inp)
+    big = torch.zeros(700, 57, device=gpu_device)
+    big[:, 3:43] = inp["X"].to(gpu_device)
+    Xv = big[:, 3:43]                                        # row stride 57, misaligned
+    Xt = inp["X"].to(gpu_device).t().contiguous().t()       # column-major
+    mu_t = inp["mu"].to(gpu_device).t().contiguous().t()
+    for X in (Xv, Xt):
+        got = flash_gmm_estep(X, mu_t, inp["log_sigma_sq"].to(gpu_device), inp["log_pi"].to(gpu_device))
+        torch.cuda.synchronize()
+        assert_close_stats(got, ref, "strided")
+
+
+def test_block_kwargs_are_accepted(gpu_device):
+    inp = data.iso_plain(100, 8, 16, seed=7)
+    a = run_gpu(inp, gpu_device)
+    b = run_gpu(inp, gpu_device, BLOCK_N=128, BLOCK_K=32, BLOCK_D=16)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+def test_deterministic_bitwise(gpu_device):
+    inp = data.iso_clustered(20000, 256, 64, seed=8)
+    a = run_gpu(inp, gpu_device)
+    b = run_gpu(inp, gpu_device)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+def test_atomic_reduce_matches(gpu_device):
+    inp = data.iso_clustered(5000, 200, 48, seed=9)
+    ref = run_gpu(inp, gpu_device)
+    dev = gpu_device
+    K, D = 200, 48
+    out = [torch.empty(5000, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, device=dev)]
+    args = [inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
+    iso_estep_into(*args, *out, atomic_reduce=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out[0], ref[0])
+    for u, v in zip(out[1:], ref[1:]):
+        torch.testing.assert_close(u, v, rtol=1e-5, atol=1e-5 * float(v.abs().max()))
+
+
+def test_accumulate_over_chunks_equals_one_call(gpu_device):
+    inp = data.iso_clustered(9000, 128, 64, seed=10)
+    dev = gpu_device
+    args = [inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
+    ref = flash_gmm_estep(*args)
+    K, D = 128, 64
+    nk = torch.zeros(K, device=dev)
+    mu_acc = torch.zeros(K, D, device=dev)
+    sig = torch.zeros(K, device=dev)
+    for n0 in range(0, 9000, 2500):
+        iso_estep_into(args[0][n0:n0 + 2500], *args[1:], None, nk, mu_acc, sig, accumulate=True)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(nk, ref[1], rtol=1e-5, atol=1e-4)
+    torch.testing.assert_close(mu_acc, ref[2], rtol=1e-5, atol=1e-5 * float(ref[2].abs().max()))
+    torch.testing.assert_close(sig, ref[3], rtol=1e-5, atol=1e-4)
+
+
+def test_headline_shape_mid_size(gpu_device):
+    """K=1024, D=128 clustered data at N=65,536 against the float64 oracle."""
+    inp = data.iso_clustered(65536, 1024, 128, seed=1)
+    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "K1024 D128 N65536")
+
+
+def test_headline_shape_full_size_properties(gpu_device):
+    """N=1M, K=1024, D=128: size-independent properties plus sampled rows."""
+    dev = gpu_device
+    inp = data.iso_clustered(1_000_000, 1024, 128, seed=1, device=dev)
+    logZ, Nk, mu_acc, sig = flash_gmm_estep(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+    torch.cuda.synchronize()
+    N = inp["X"].shape[0]
+    assert abs(Nk.double().sum().item() - N) <= 1e-5 * N
+    xs = inp["X"].double().sum(0)
+    torch.testing.assert_close(mu_acc.double().sum(0), xs, rtol=0, atol=1e-5 * float(mu_acc.abs().sum(0).max()))
+    assert torch.all(sig >= 0)
+    g = torch.Generator().manual_seed(0)
+    rows = torch.randint(0, N, (2048,), generator=g)
+    sub = {k: v.cpu() for k, v in inp.items()}
+    sub["X"] = sub["X"][rows]
+    ref_lz = O.estep_iso(sub["X"], sub["mu"], sub["log_sigma_sq"], sub["log_pi"])[0]
+    err = (logZ.cpu()[rows].double() - ref_lz).abs().max().item()
+    assert err <= LOGZ_ATOL, f"sampled logZ err {err}"
+
+
+def test_rejects_bad_shapes(gpu_device):
+    inp = data.iso_plain(10, 4, 8, seed=11)
+    X, mu, lss, lpi = (inp[k].to(gpu_device) for k in ("X", "mu", "log_sigma_sq", "log_pi"))
+    with pytest.raises(AssertionError):
+        flash_gmm_estep(X, mu[:, :4], lss, lpi)
+    with pytest.raises(FlashGMMError):
+        flash_gmm_estep(X, mu, lss[:2], lpi)
+    with pytest.raises(FlashGMMError):
+        flash_gmm_estep(X.double(), mu, lss, lpi)
+    with pytest.raises(FlashGMMError):  # D beyond the compiled range
+        Xw = torch.zeros(4, 300, device=gpu_device)
+        flash_gmm_estep(Xw, torch.zeros(2, 300, device=gpu_device), lss[:2], lpi[:2])
