@@ -61,23 +61,57 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // Each chunk of 8 dimensions is 4 fp32 MFMA steps from a zero accumulator; the
 // chunk sums are then added in fp64, which bounds the fp32 rounding to one
 // 8-term partial sum per chunk.
+//
+// Software pipeline: iteration m issues the MFMA chain of chunk m, adds chunk
+// m-1 (whose chain has finished) into the fp64 sums, and loads the operands of
+// chunk m+1.  The empty asm statements and the scheduling barrier keep the
+// compiler from deferring the flushes, which would hold every chunk's
+// accumulator live at once.
+__device__ __forceinline__ f32x16 mfma_chunk(const f32x4 a, const f32x4 b) {
+  f32x16 c = mfma32(a[0], b[0], zero16());
+  c = mfma32(a[1], b[1], c);
+  c = mfma32(a[2], b[2], c);
+  return mfma32(a[3], b[3], c);
+}
+
 template <int NM, typename LA, typename LB>
 __device__ __forceinline__ void cross_tile(double (&out)[16], LA loadA, LB loadB) {
+  f32x4 a = loadA(0), b = loadB(0);
+  f32x4 an = a, bn = b;
+  if (NM > 1) {
+    an = loadA(1);
+    bn = loadB(1);
+  }
+  f32x16 prev = mfma_chunk(a, b);
 #pragma unroll
-  for (int m = 0; m < NM; ++m) {
-    const f32x4 a = loadA(m);
-    const f32x4 b = loadB(m);
-    f32x16 c = mfma32(a[0], b[0], zero16());
-    c = mfma32(a[1], b[1], c);
-    c = mfma32(a[2], b[2], c);
-    c = mfma32(a[3], b[3], c);
-    if (m == 0) {
+  for (int m = 1; m < NM; ++m) {
+    a = an;
+    b = bn;
+    if (m + 1 < NM) {
+      an = loadA(m + 1);
+      bn = loadB(m + 1);
+    }
+    const f32x16 cur = mfma_chunk(a, b);
+    if (m == 1) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) out[i] = (double)c[i];
+      for (int i = 0; i < 16; ++i) out[i] = (double)prev[i];
     } else {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) out[i] += (double)c[i];
+      for (int i = 0; i < 16; ++i) out[i] += (double)prev[i];
     }
+    // Materialise the fp64 sums here: without this, IR-level sinking moves every
+    // flush down to the first use of out[] and keeps all chunk results live.
+#pragma unroll
+    for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(out[i]));
+    prev = cur;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (NM == 1) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) out[i] = (double)prev[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) out[i] += (double)prev[i];
   }
 }
 

@@ -41,10 +41,17 @@ namespace {
 constexpr int kWaves = 4;        // waves per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kCUs = 256;  // MI355X compute units
+constexpr int kAccWaves = 8;   // pass-2 LDS variant: waves per workgroup
+constexpr int kAccThreads = 64 * kAccWaves;
+constexpr int kRowGroups = 2;  // pass-2 LDS variant: row groups per workgroup
 
-// Waves per SIMD that pass 2 is compiled for (one workgroup of kWaves waves per
-// CU at 1, two at 2); it sets how many slab workgroups are resident at once.
+// Waves per SIMD of the register-resident pass-2 variant (used for D > 128).
 __host__ __device__ constexpr int accum_waves_per_eu(int DP) { return DP <= 96 ? 2 : 1; }
+
+// Pass 2 runs one workgroup per CU: the LDS-resident variant (D <= 128, eight
+// waves, ~100-135 KB of LDS) or the register-resident variant (D > 128, four
+// waves at one wave per SIMD).
+__host__ __device__ constexpr bool accum_uses_lds(int DP) { return DP <= 128; }
 
 struct IsoPlan {
   int64_t N, K, D;
@@ -53,6 +60,8 @@ struct IsoPlan {
   int KP;       // K padded to a multiple of 32
   int ncg;      // groups of kWaves component blocks (pass 2)
   int nslab;    // row slabs (pass 2)
+  int rgroups;  // row groups per slab (partials per slab)
+  int npart;    // nslab * rgroups
   int64_t rows_per_slab;
   size_t off_musw, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_nk, off_part_sig, total;
 };
@@ -64,26 +73,29 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D) {
   p.KB = (int)cdiv(K, 32);
   p.KP = p.KB * 32;
   p.ncg = (int)cdiv(p.KB, kWaves);
+  p.rgroups = accum_uses_lds(p.DP) ? kRowGroups : 1;
+  const int64_t tile_rows = 32 * p.rgroups;
   if (N > 0 && p.ncg > 0) {
-    int64_t want = (int64_t)kCUs * accum_waves_per_eu(p.DP) / p.ncg;
+    int64_t want = (int64_t)kCUs / p.ncg;
     if (want >= 8) want = (want / 8) * 8;  // keeps a slab's workgroups on one XCD
     if (want < 1) want = 1;
-    int64_t max_slabs = cdiv(N, 32);
+    const int64_t max_slabs = cdiv(N, tile_rows);
     if (want > max_slabs) want = max_slabs;
-    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.rows_per_slab = round_up(cdiv(N, want), tile_rows);
     p.nslab = (int)cdiv(N, p.rows_per_slab);
   } else {
-    p.rows_per_slab = 32;
+    p.rows_per_slab = tile_rows;
     p.nslab = 0;
   }
+  p.npart = p.nslab * p.rgroups;
   size_t off = 0;
   p.off_musw = off;    off = align256(off + (size_t)p.KP * p.DP * sizeof(float));
   p.off_kcblk = off;   off = align256(off + (size_t)p.KB * 32 * 2 * sizeof(double));
   p.off_kclin = off;   off = align256(off + (size_t)p.KP * 4 * sizeof(double));
   p.off_rowstat = off; off = align256(off + (size_t)(N > 0 ? N : 0) * 2 * sizeof(double));
-  p.off_part_mu = off; off = align256(off + (size_t)p.nslab * p.KP * p.DP * sizeof(float));
-  p.off_part_nk = off; off = align256(off + (size_t)p.nslab * p.KP * sizeof(float));
-  p.off_part_sig = off; off = align256(off + (size_t)p.nslab * p.KP * sizeof(float));
+  p.off_part_mu = off; off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
+  p.off_part_nk = off; off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
+  p.off_part_sig = off; off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
   p.total = off;
   return p;
 }
@@ -142,18 +154,50 @@ __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int
 
 // ---------------------------------------------------------------------------
 // Pass 1: logZ by online log-sum-exp over component blocks.
+// Each wave keeps 32 rows of X in registers (matrix-core B operand).  The
+// 32-component blocks of mu and their constants stream through LDS, double
+// buffered: the global loads of block kb+1 are in flight while block kb is
+// contracted, and land in the other buffer before the block's barrier.
 // ---------------------------------------------------------------------------
 template <int DP>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
+constexpr size_t lse_lds_bytes() {
+  return (size_t)2 * DP * 32 * sizeof(float) + (size_t)2 * 32 * sizeof(double2);
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(DP <= 192 ? 2 : 1, DP <= 192 ? 2 : 1)))
 void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
              const f32x4* __restrict__ mu_sw, const double2* __restrict__ kc_blk, int KB,
              float* __restrict__ logZ, double2* __restrict__ rowstat) {
   constexpr int NM = DP / 8;
+  constexpr int BLK = NM * 64;            // float4 per 32-component block
+  constexpr int LPT = BLK / kThreads;     // float4 per thread per block
+  static_assert(BLK % kThreads == 0, "block load must split evenly");
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  f32x4* mu_l = reinterpret_cast<f32x4*>(lds_raw);                                  // [2][BLK]
+  double2* kc_l = reinterpret_cast<double2*>(lds_raw + 2 * BLK * sizeof(f32x4));   // [2][32]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
   const int64_t row = ((int64_t)blockIdx.x * kWaves + wave) * 32 + c;
   const bool valid = row < N;
+
+  f32x4 st[LPT];
+  double2 kst = make_double2(0.0, 0.0);
+  auto fetch = [&](int kb) {
+    const f32x4* src = mu_sw + (int64_t)kb * BLK;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) st[q] = src[q * kThreads + tid];
+    if (tid < 32) kst = kc_blk[(int64_t)kb * 32 + tid];
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) mu_l[buf * BLK + q * kThreads + tid] = st[q];
+    if (tid < 32) kc_l[buf * 32 + tid] = kst;
+  };
+  fetch(0);
 
   f32x4 xb[NM];
   double xsq = 0.0;
@@ -166,16 +210,21 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     xsq = fma((double)xb[m].w, (double)xb[m].w, xsq);
   }
   xsq += __shfl_xor(xsq, 32);
+  commit(0);
+  __syncthreads();
 
   double mx = -INFINITY;
   float sm = 0.0f;
 
   for (int kb = 0; kb < KB; ++kb) {
-    const f32x4* mp = mu_sw + (int64_t)kb * NM * 64 + lane;
+    const int buf = kb & 1;
+    const bool more = kb + 1 < KB;
+    if (more) fetch(kb + 1);
+    const f32x4* mp = mu_l + buf * BLK + lane;
     // S^T[comp][row] = mu . x, lane = row, register i = component acc_row(i, g).
     double xm[16];
     cross_tile<NM>(xm, [&](int m) { return mp[m * 64]; }, [&](int m) { return xb[m]; });
-    const double2* kp = kc_blk + ((int64_t)kb * 2 + g) * 16;
+    const double2* kp = kc_l + buf * 32 + g * 16;
     double ll[16];
     double bm = -INFINITY;
 #pragma unroll
@@ -191,6 +240,8 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     for (int i = 0; i < 16; ++i) acc += fast_exp2((float)(ll[i] - ms));
     sm = acc;
     mx = mn;
+    if (more) commit(buf ^ 1);
+    __syncthreads();
   }
 
   // Merge the two half-waves that hold the same row.
@@ -361,6 +412,163 @@ void iso_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 }
 
 // ---------------------------------------------------------------------------
+// Pass 2, D <= 128: eight waves per workgroup = 2 row groups x 4 component
+// blocks.  mu for the workgroup's 128 components is resident in LDS (matrix-
+// core B operand, shared by both row groups); X streams through LDS in 64-row
+// super-tiles (32 rows per row group), double buffered.  Each wave writes its
+// own partial, indexed (slab, row group).
+// ---------------------------------------------------------------------------
+template <int DP>
+constexpr size_t accum_lds_lds_bytes() {
+  return (size_t)kWaves * DP * 32 * sizeof(float)                      // mu, 4 blocks
+         + (size_t)2 * 32 * kRowGroups * (DP + 4) * sizeof(float)      // X, 2 buffers
+         + (size_t)2 * 32 * kRowGroups * sizeof(double2);              // row stats
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
+void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                   const f32x4* __restrict__ mu_sw, const double4* __restrict__ kc_lin, int KB, int KP,
+                   const double2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
+                   float* __restrict__ part_mu, float* __restrict__ part_nk, float* __restrict__ part_sig) {
+  constexpr int NM = DP / 8;
+  constexpr int NJ = DP / 32;
+  constexpr int RS = DP + 4;
+  constexpr int V4 = DP / 4;
+  constexpr int BLK = NM * 64;                   // float4 per 32-component block
+  constexpr int TR = 32 * kRowGroups;            // rows per super-tile
+  constexpr int LPT = (TR * V4) / kAccThreads;   // float4 loads per thread per super-tile
+  constexpr int MPT = (kWaves * BLK) / kAccThreads;
+  static_assert((TR * V4) % kAccThreads == 0 && (kWaves * BLK) % kAccThreads == 0, "even split");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  f32x4* mu_l = reinterpret_cast<f32x4*>(lds_raw);                                        // [4][BLK]
+  float* xs = reinterpret_cast<float*>(lds_raw + kWaves * BLK * sizeof(f32x4));           // [2][TR*RS]
+  double2* rs = reinterpret_cast<double2*>(lds_raw + kWaves * BLK * sizeof(f32x4) +
+                                           2 * TR * RS * sizeof(float));                  // [2][TR]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int cbw = wave & 3, rg = wave >> 2;
+  const int slab = blockIdx.x % nslab;
+  const int cg = blockIdx.x / nslab;
+  const int kb = cg * kWaves + cbw;
+  const bool active = kb < KB;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
+
+  // mu of the workgroup's four component blocks -> LDS (zeros past KB).
+#pragma unroll
+  for (int q = 0; q < MPT; ++q) {
+    const int idx = q * kAccThreads + tid;
+    const int b = idx / BLK;
+    const int kbq = cg * kWaves + b;
+    mu_l[idx] = (kbq < KB) ? mu_sw[(int64_t)kbq * BLK + (idx % BLK)] : zero4();
+  }
+  double Ck = -INFINITY, bk = 0.0, musq = 0.0;
+  if (active) {
+    const double4 kc = kc_lin[(int64_t)kb * 32 + c];
+    Ck = kc.x; bk = kc.y; musq = kc.z;
+  }
+
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
+  float nk = 0.0f, sig = 0.0f;
+
+  f32x4 stage[LPT];
+  double2 rstage = make_double2(0.0, INFINITY);
+  auto fetch = [&](int t) {
+    const int64_t row0 = r_begin + (int64_t)t * TR;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      const int rr = idx / V4, c4 = idx % V4;
+      const int64_t row = row0 + rr;
+      stage[q] = load_row4(X, ldx, row, c4 * 4, D, row < r_end);
+    }
+    if (tid < TR) {
+      const int64_t row = row0 + tid;
+      rstage = (row < r_end) ? rowstat[row] : make_double2(0.0, INFINITY);
+    }
+  };
+  auto commit = [&](int buf) {
+    float* dst = xs + buf * TR * RS;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      const int rr = idx / V4, c4 = idx % V4;
+      *reinterpret_cast<f32x4*>(dst + rr * RS + c4 * 4) = stage[q];
+    }
+    if (tid < TR) rs[buf * TR + tid] = rstage;
+  };
+
+  if (ntiles > 0) {
+    fetch(0);
+    commit(0);
+  }
+  __syncthreads();
+
+  const f32x4* mb = mu_l + cbw * BLK + lane;
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    const float* xt = xs + buf * TR * RS + rg * 32 * RS;
+    const double2* rt = rs + buf * TR + rg * 32;
+    double xm[16];
+    float r[16];
+    if (active) {
+      cross_tile<NM>(
+          xm, [&](int m) { return *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * m + 4 * g); },
+          [&](int m) { return mb[m * 64]; });
+      const double2* rbase = rt + 4 * g;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ro = 8 * (i >> 2) + (i & 3);
+        const double2 stt = rbase[ro];  // (||x||^2, logZ2)
+        const double u = fma(-2.0, xm[i], stt.x);
+        const double tt = fma(-bk, u, Ck - stt.y);
+        const float rv = fast_exp2((float)tt);
+        nk += rv;
+        sig = fmaf(rv, (float)(u + musq), sig);
+        r[i] = rv;
+      }
+    }
+    if (more) fetch(t + 1);
+    if (active) {
+      const float* xbase = xt + 4 * g * RS + c;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ro = 8 * (i >> 2) + (i & 3);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
+      }
+    }
+    if (more) commit(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (active) {
+    nk += __shfl_xor(nk, 32);
+    sig += __shfl_xor(sig, 32);
+    const int64_t kbase = ((int64_t)slab * kRowGroups + rg) * KP + (int64_t)kb * 32;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[j][i];
+    }
+    if (g == 0) {
+      part_nk[kbase + c] = nk;
+      part_sig[kbase + c] = sig;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Finish: fixed-order fp64 reduction over slabs (deterministic).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void iso_reduce(const float* __restrict__ part_mu,
@@ -421,23 +629,43 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   const double2* kc_blk = reinterpret_cast<const double2*>(ws + pl.off_kcblk);
   const double4* kc_lin = reinterpret_cast<const double4*>(ws + pl.off_kclin);
   double2* rowstat = reinterpret_cast<double2*>(ws + pl.off_rowstat);
+  float* pmu = reinterpret_cast<float*>(ws + pl.off_part_mu);
+  float* pnk = reinterpret_cast<float*>(ws + pl.off_part_nk);
+  float* psig = reinterpret_cast<float*>(ws + pl.off_part_sig);
   if (run1) {
+    constexpr size_t lds1 = lse_lds_bytes<DP>();
+    if (lds1 > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_lse<DP>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+      if (e != hipSuccess) return e;
+    }
     const int64_t nblk1 = cdiv(pl.N, 32 * kWaves);
-    hipLaunchKernelGGL(iso_lse<DP>, dim3((unsigned)nblk1), dim3(kThreads), 0, stream, X, ldx, pl.N,
-                       (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
+    hipLaunchKernelGGL(iso_lse<DP>, dim3((unsigned)nblk1), dim3(kThreads), lds1, stream, X, ldx,
+                       pl.N, (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
   }
   if (!run2) return hipGetLastError();
-  constexpr size_t lds = accum_lds_bytes<DP>();
-  if (lds > 65536) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum<DP>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
+  const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
+  if constexpr (accum_uses_lds(DP)) {
+    constexpr size_t lds = accum_lds_lds_bytes<DP>();
+    if (lds > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_lds<DP>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(iso_accum_lds<DP>, grid2, dim3(kAccThreads), lds, stream, X, ldx, pl.N,
+                       (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
+                       pmu, pnk, psig);
+  } else {
+    constexpr size_t lds = accum_lds_bytes<DP>();
+    if (lds > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum<DP>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(iso_accum<DP>, grid2, dim3(kThreads), lds, stream, X, ldx, pl.N, (int)pl.D,
+                       mu_sw, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab, pmu, pnk,
+                       psig);
   }
-  hipLaunchKernelGGL(iso_accum<DP>, dim3((unsigned)(pl.nslab * pl.ncg)), dim3(kThreads), lds, stream,
-                     X, ldx, pl.N, (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab,
-                     pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_mu),
-                     reinterpret_cast<float*>(ws + pl.off_part_nk),
-                     reinterpret_cast<float*>(ws + pl.off_part_sig));
   return hipGetLastError();
 }
 
@@ -518,13 +746,13 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
       hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, stream, sig_acc, K,
                          0.0f);
     }
-    if (pl.nslab > 0)
-      hipLaunchKernelGGL(iso_reduce_atomic, dim3((unsigned)cdiv(nout, 256), (unsigned)pl.nslab),
-                         dim3(256), 0, stream, pmu, pnk, psig, pl.nslab, pl.KP, pl.DP, K, (int)D, Nk,
+    if (pl.npart > 0)
+      hipLaunchKernelGGL(iso_reduce_atomic, dim3((unsigned)cdiv(nout, 256), (unsigned)pl.npart),
+                         dim3(256), 0, stream, pmu, pnk, psig, pl.npart, pl.KP, pl.DP, K, (int)D, Nk,
                          mu_acc, sig_acc);
   } else {
     hipLaunchKernelGGL(iso_reduce, dim3((unsigned)cdiv(nout, 256)), dim3(256), 0, stream, pmu, pnk,
-                       psig, pl.nslab, pl.KP, pl.DP, K, (int)D, Nk, mu_acc, sig_acc,
+                       psig, pl.npart, pl.KP, pl.DP, K, (int)D, Nk, mu_acc, sig_acc,
                        accumulate ? 1 : 0);
   }
   return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
