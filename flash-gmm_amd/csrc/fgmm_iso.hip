@@ -41,6 +41,13 @@ namespace {
 constexpr int kWaves = 4;        // waves per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kCUs = 256;  // MI355X compute units
+
+// Per-row state of pass 2 in LDS: logZ2 in fp64 and ||x||^2 in fp32.
+struct __align__(16) RowStat {
+  double q;
+  float h;
+  float pad;
+};
 constexpr int kAccWaves = 8;   // pass-2 LDS variant: waves per workgroup
 constexpr int kAccThreads = 64 * kAccWaves;
 constexpr int kRowGroups = 2;  // pass-2 LDS variant: row groups per workgroup
@@ -166,7 +173,7 @@ constexpr size_t lse_lds_bytes() {
 
 template <int DP>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(DP <= 192 ? 2 : 1, DP <= 192 ? 2 : 1)))
+                          amdgpu_waves_per_eu(DP <= 160 ? 2 : 1, DP <= 160 ? 2 : 1)))
 void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
              const f32x4* __restrict__ mu_sw, const double2* __restrict__ kc_blk, int KB,
              float* __restrict__ logZ, double2* __restrict__ rowstat) {
@@ -282,7 +289,7 @@ void iso_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   float* xs = reinterpret_cast<float*>(lds_raw);                                  // [2][32*RS]
-  double2* rs = reinterpret_cast<double2*>(lds_raw + 2 * 32 * RS * sizeof(float));  // [2][32]
+  RowStat* rs = reinterpret_cast<RowStat*>(lds_raw + 2 * 32 * RS * sizeof(float));  // [2][32]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
@@ -297,12 +304,13 @@ void iso_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
 
   f32x4 mub[NM];
-  double Ck = -INFINITY, bk = 0.0, musq = 0.0;
+  double Ck = -INFINITY;
+  float bkf = 0.0f, musqf = 0.0f;
   if (active) {
 #pragma unroll
     for (int m = 0; m < NM; ++m) mub[m] = mu_sw[((int64_t)kb * NM + m) * 64 + lane];
     const double4 kc = kc_lin[(int64_t)kb * 32 + c];
-    Ck = kc.x; bk = kc.y; musq = kc.z;
+    Ck = kc.x; bkf = (float)kc.y; musqf = (float)kc.z;
   } else {
 #pragma unroll
     for (int m = 0; m < NM; ++m) mub[m] = zero4();
@@ -338,7 +346,7 @@ void iso_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       const int rr = idx / V4, c4 = idx % V4;
       *reinterpret_cast<f32x4*>(dst + rr * RS + c4 * 4) = stage[q];
     }
-    if (tid < 32) rs[buf * 32 + tid] = rstage;
+    if (tid < 32) rs[buf * 32 + tid] = RowStat{rstage.y, (float)rstage.x, 0.0f};
   };
 
   if (ntiles > 0) {
@@ -356,26 +364,26 @@ void iso_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const int buf = t & 1;
     const bool more = t + 1 < ntiles;
     const float* xt = xs + buf * 32 * RS;
-    const double2* rt = rs + buf * 32;
+    const RowStat* rt = rs + buf * 32;
     // S[row][comp] = sum_d X[row][d] mu[comp][d] : lane = component, register i = row acc_row(i, g).
-    double xm[16];
+    float xm[16];
     if (active)
-      cross_tile<NM>(
+      cross_tile_fast<NM>(
           xm, [&](int m) { return *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * m + 4 * g); },
           [&](int m) { return mub[m]; });
     float r[16];
     if (active) {
       // Rows of this lane's accumulator registers: acc_row(i, g) = 4g + (8*(i/4) + i%4).
-      const double2* rbase = rt + 4 * g;
+      const RowStat* rbase = rt + 4 * g;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int ro = 8 * (i >> 2) + (i & 3);
-        const double2 st = rbase[ro];  // (||x||^2, logZ2)
-        const double u = fma(-2.0, xm[i], st.x);
-        const double tt = fma(-bk, u, Ck - st.y);
-        const float rv = fast_exp2((float)tt);
+        const RowStat stt = rbase[ro];
+        const float u = fmaf(-2.0f, xm[i], stt.h);            // ||x||^2 - 2 x.mu
+        const float dq = (float)(Ck - stt.q);                  // C_k - logZ2, rounded once
+        const float rv = fast_exp2(fmaf(-bkf, u, dq));
         nk += rv;
-        sig = fmaf(rv, (float)(u + musq), sig);
+        sig = fmaf(rv, u + musqf, sig);
         r[i] = rv;
       }
     }
@@ -444,7 +452,7 @@ void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   extern __shared__ __align__(16) unsigned char lds_raw[];
   f32x4* mu_l = reinterpret_cast<f32x4*>(lds_raw);                                        // [4][BLK]
   float* xs = reinterpret_cast<float*>(lds_raw + kWaves * BLK * sizeof(f32x4));           // [2][TR*RS]
-  double2* rs = reinterpret_cast<double2*>(lds_raw + kWaves * BLK * sizeof(f32x4) +
+  RowStat* rs = reinterpret_cast<RowStat*>(lds_raw + kWaves * BLK * sizeof(f32x4) +
                                            2 * TR * RS * sizeof(float));                  // [2][TR]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -468,10 +476,11 @@ void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const int kbq = cg * kWaves + b;
     mu_l[idx] = (kbq < KB) ? mu_sw[(int64_t)kbq * BLK + (idx % BLK)] : zero4();
   }
-  double Ck = -INFINITY, bk = 0.0, musq = 0.0;
+  double Ck = -INFINITY;
+  float bkf = 0.0f, musqf = 0.0f;
   if (active) {
     const double4 kc = kc_lin[(int64_t)kb * 32 + c];
-    Ck = kc.x; bk = kc.y; musq = kc.z;
+    Ck = kc.x; bkf = (float)kc.y; musqf = (float)kc.z;
   }
 
   f32x16 acc[NJ];
@@ -503,7 +512,7 @@ void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       const int rr = idx / V4, c4 = idx % V4;
       *reinterpret_cast<f32x4*>(dst + rr * RS + c4 * 4) = stage[q];
     }
-    if (tid < TR) rs[buf * TR + tid] = rstage;
+    if (tid < TR) rs[buf * TR + tid] = RowStat{rstage.y, (float)rstage.x, 0.0f};
   };
 
   if (ntiles > 0) {
@@ -517,23 +526,23 @@ void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const int buf = t & 1;
     const bool more = t + 1 < ntiles;
     const float* xt = xs + buf * TR * RS + rg * 32 * RS;
-    const double2* rt = rs + buf * TR + rg * 32;
-    double xm[16];
+    const RowStat* rt = rs + buf * TR + rg * 32;
+    float xm[16];
     float r[16];
     if (active) {
-      cross_tile<NM>(
+      cross_tile_fast<NM>(
           xm, [&](int m) { return *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * m + 4 * g); },
           [&](int m) { return mb[m * 64]; });
-      const double2* rbase = rt + 4 * g;
+      const RowStat* rbase = rt + 4 * g;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int ro = 8 * (i >> 2) + (i & 3);
-        const double2 stt = rbase[ro];  // (||x||^2, logZ2)
-        const double u = fma(-2.0, xm[i], stt.x);
-        const double tt = fma(-bk, u, Ck - stt.y);
-        const float rv = fast_exp2((float)tt);
+        const RowStat stt = rbase[ro];
+        const float u = fmaf(-2.0f, xm[i], stt.h);            // ||x||^2 - 2 x.mu
+        const float dq = (float)(Ck - stt.q);                  // C_k - logZ2, rounded once
+        const float rv = fast_exp2(fmaf(-bkf, u, dq));
         nk += rv;
-        sig = fmaf(rv, (float)(u + musq), sig);
+        sig = fmaf(rv, u + musqf, sig);
         r[i] = rv;
       }
     }
