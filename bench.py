@@ -1,12 +1,14 @@
 """E-step throughput on one MI355X: samples/s and fraction of the fp32 MFMA peak.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
+                    [--workload iso_n1m_k1024_d128|diag_n1m_k1024_d96|full_n250k_k256_d64]
 
-Workload: the isotropic E-step at N=1,000,000, K=1024, D=128, float32, on the
-clustered synthetic data of flash_gmm.data.iso_clustered (seed 1), generated
-on the GPU so X is resident in HBM before timing.  One step = one full E-step
-(constant prologue + log-normaliser pass + accumulation pass + reduction)
-through the C ABI on torch's current stream.  Prints one JSON line.
+Default workload (the headline): the isotropic E-step at N=1,000,000, K=1024,
+D=128, float32, on the clustered synthetic data of flash_gmm.data.iso_clustered
+(seed 1), generated on the GPU so X is resident in HBM before timing.  One step
+= one full E-step (constant prologue + log-normaliser pass + accumulation pass +
+reduction) through the C ABI on torch's current stream.  Prints one JSON line.
+The diagonal and full-covariance workloads are measured the same way.
 """
 
 import argparse
@@ -67,6 +69,29 @@ def cpu_baseline(inp, K, D, min_s=10.0, max_s=30.0, rows=16384):
     }
 
 
+WORKLOADS = {
+    # name: (N, K, D)
+    "iso_n1m_k1024_d128": (1_000_000, 1024, 128),
+    "diag_n1m_k1024_d96": (1_000_000, 1024, 96),
+    "full_n250k_k256_d64": (250_000, 256, 64),
+}
+
+
+def algorithmic_flop(kind, N, K, D):
+    """Per-step algorithmic flops and the (phase 1, phase 2) split.
+
+    iso:  4NKD  = x.mu^T (2NKD, phase 1) + r^T X (2NKD, phase 2)
+    diag: 8NKD  = [x^2, x].[-w, 2v]^T (4NKD, phase 1) + r^T [X, X^2] (4NKD, phase 2)
+    full: 4NKD^2 + 2NKD = X.L_k whitening (2NKD^2, phase 1) + sum r x x^T (2NKD^2)
+          + r^T X (2NKD) in phase 2 (dense-equivalent count)
+    """
+    if kind == "iso":
+        return 4.0 * N * K * D, 2.0 * N * K * D, 2.0 * N * K * D
+    if kind == "diag":
+        return 8.0 * N * K * D, 4.0 * N * K * D, 4.0 * N * K * D
+    return 4.0 * N * K * D * D + 2.0 * N * K * D, 2.0 * N * K * D * D, 2.0 * N * K * D * D + 2.0 * N * K * D
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -74,6 +99,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--atomic-reduce", action="store_true")
+    ap.add_argument("--workload", default="iso_n1m_k1024_d128", choices=sorted(WORKLOADS))
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures a single GPU; --gpus {args.gpus} is not supported "
@@ -82,30 +108,42 @@ def main():
         sys.exit(2)
 
     import torch
-    from flash_gmm import data, iso_estep_into
-    from flash_gmm import _lib
+    from flash_gmm import _lib, data, diag_estep_into, full_estep_into, iso_estep_into
 
     dev = torch.device("cuda:0")
-    N, K, D = 1_000_000, 1024, 128
-    log(f"generating workload iso_n1m_k1024_d128 on {torch.cuda.get_device_name(dev)}")
-    inp = data.iso_clustered(N, K, D, seed=1, device=dev)
-    X, mu, lss, lpi = (inp[k] for k in ("X", "mu", "log_sigma_sq", "log_pi"))
+    N, K, D = WORKLOADS[args.workload]
+    kind = args.workload.split("_")[0]
+    log(f"generating workload {args.workload} on {torch.cuda.get_device_name(dev)}")
+    inp = data.make(args.workload, device=dev)
+    L = _lib.lib()
     logZ = torch.empty(N, device=dev)
     Nk = torch.empty(K, device=dev)
     mu_acc = torch.empty(K, D, device=dev)
-    sig = torch.empty(K, device=dev)
-    ws = torch.empty(int(_lib.lib().fgmm_iso_workspace_bytes(N, K, D)), dtype=torch.uint8, device=dev)
+    if kind == "iso":
+        args4 = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+        sig = torch.empty(K, device=dev)
+        ws = torch.empty(int(L.fgmm_iso_workspace_bytes(N, K, D)), dtype=torch.uint8, device=dev)
+        fn = lambda ph: iso_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws, phase=ph,
+                                       atomic_reduce=args.atomic_reduce)
+    elif kind == "diag":
+        args4 = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+        sig = torch.empty(K, D, device=dev)
+        ws = torch.empty(int(L.fgmm_diag_workspace_bytes(N, K, D)), dtype=torch.uint8, device=dev)
+        fn = lambda ph: diag_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws, phase=ph)
+    else:
+        args4 = (inp["X"], inp["mu"], inp["prec_chol"], inp["log_pi"])
+        sig = torch.empty(K, D, D, device=dev)
+        ws = torch.empty(int(L.fgmm_full_workspace_bytes(N, K, D)), dtype=torch.uint8, device=dev)
+        fn = lambda ph: full_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws, phase=ph)
     stream = torch.cuda.current_stream(dev)
 
     def step(ev=None):
         if ev is not None:
             ev[0].record(stream)
-        iso_estep_into(X, mu, lss, lpi, logZ, Nk, mu_acc, sig, workspace=ws, phase=1,
-                       atomic_reduce=args.atomic_reduce)
+        fn(1)
         if ev is not None:
             ev[1].record(stream)
-        iso_estep_into(X, mu, lss, lpi, logZ, Nk, mu_acc, sig, workspace=ws, phase=2,
-                       atomic_reduce=args.atomic_reduce)
+        fn(2)
         if ev is not None:
             ev[2].record(stream)
 
@@ -128,15 +166,20 @@ def main():
     p2 = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
     log(f"timed {args.steps} steps: {ms:.3f} ms/step (phase1 {p1:.3f} ms, phase2 {p2:.3f} ms)")
 
-    half_flop = 2.0 * N * K * D          # x.mu^T (phase 1) or r^T X (phase 2), algorithmic
-    step_tflops = 2 * half_flop / (ms * 1e-3) / 1e12
-    dom, dom_ms = ("iso_accum (accumulation pass + slab reduction)", p2) if p2 >= p1 else \
-        ("iso_lse (log-normaliser pass + prologue)", p1)
-    dom_tflops = half_flop / (dom_ms * 1e-3) / 1e12
-    executed = (6.0 * N * K * D) / (ms * 1e-3) / 1e12
+    flop, f1, f2 = algorithmic_flop(kind, N, K, D)
+    step_tflops = flop / (ms * 1e-3) / 1e12
+    names = {"iso": ("iso_lse (log-normaliser pass + prologue)", "iso_accum (accumulation pass + slab reduction)"),
+             "diag": ("diag_lse (log-normaliser pass + prologue)", "diag_accum (accumulation pass + slab reduction)"),
+             "full": ("full_lse (log-normaliser pass + prologue)", "full_accum (accumulation pass + slab reduction)")}[kind]
+    if p2 >= p1:
+        dom, dom_ms, dom_flop = names[1], p2, f2
+    else:
+        dom, dom_ms, dom_flop = names[0], p1, f1
+    dom_tflops = dom_flop / (dom_ms * 1e-3) / 1e12
 
     out = {
-        "metric": METRIC,
+        "metric": METRIC if kind == "iso" else
+                  f"E-step samples/sec ({args.workload}) fp32 + % of fp32 MFMA peak (1 GPU)",
         "value": N / (ms * 1e-3),
         "unit": "samples/s",
         "n_gpus": 1,
@@ -145,18 +188,18 @@ def main():
         "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": (N / (ms * 1e-3)) / A100_SAMPLES_PER_S,
+        "vs_baseline": (N / (ms * 1e-3)) / A100_SAMPLES_PER_S if kind == "iso" else None,
         "baseline_note": "reference's published A100 80GB figure for this shape: 152 ms at N=1M "
-                         "(README.md:116), TF32 dot",
+                         "(README.md:116), TF32 dot" if kind == "iso" else
+                         "no published reference number for this workload",
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "iso_n1m_k1024_d128", "N": N, "K": K, "D": D,
-                   "generator": "flash_gmm.data.iso_clustered(seed=1), generated on device",
+        "config": {"workload": args.workload, "N": N, "K": K, "D": D,
+                   "generator": f"flash_gmm.data.make({args.workload!r}), generated on device",
                    "reduce": "atomic" if args.atomic_reduce else "deterministic"},
         "fraction_of_fp32_mfma_peak": step_tflops / PEAK_FP32_MFMA_TFLOPS,
         "step_tflops_algorithmic": step_tflops,
-        "executed_mfma_tflops": executed,
-        "phase_ms": {"phase1_lse": p1, "phase2_accum": p2},
+        "phase_ms": {"phase1": p1, "phase2": p2},
         "roofline": {
             "bound": "mfma",
             "kernel": dom,
@@ -165,11 +208,11 @@ def main():
             "unit": "TFLOP/s",
             "frac": dom_tflops / PEAK_FP32_MFMA_TFLOPS,
             "traffic": None,
-            "algorithmic_flop_per_launch": half_flop,
+            "algorithmic_flop_per_launch": dom_flop,
             "avg_launch_ms": dom_ms,
         },
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and kind == "iso":
         log("timing the CPU baseline (bounded sample)")
         out["cpu_baseline"] = cpu_baseline({k: v for k, v in inp.items()}, K, D)
     print(json.dumps(out), flush=True)

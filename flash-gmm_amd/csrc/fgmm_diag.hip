@@ -1,0 +1,534 @@
+// Diagonal-covariance GMM E-step for gfx950.
+//
+// Math (reference: flash_gmm_diag_h100.py:332-340 constants, :116-119 log-joint,
+// :250-260 accumulation, :380-384 outputs), in log2 units with
+//   w_kd = 0.5 * exp(-lss_kd) * log2(e),   v_kd = mu_kd * w_kd,
+//   C_k  = (lpi_k - 0.5*(D*log(2pi) + sum_d lss_kd)) * log2(e) - sum_d mu_kd^2 w_kd:
+//   ll2_nk = C_k + [x_n^2, x_n] . [-w_k, 2 v_k]          (one contraction over 2D features)
+//   r_nk = 2^(ll2_nk - logZ2_n)
+//   Nk_k = sum_n r_nk;  mu_acc_kd = sum_n r_nk x_nd;  rxsq_kd = sum_n r_nk x_nd^2
+//   sig_acc_kd = rxsq_kd - 2 mu_kd mu_acc_kd + mu_kd^2 Nk_k   (fp64, in the finish)
+//
+// Same structure as the isotropic kernels (fgmm_iso.hip): a prologue that lays the
+// 2D-feature operand [-w, 2v] out in matrix-core order, a log-normaliser pass with
+// X resident in registers (the x^2 half of the feature vector is formed on the fly),
+// an accumulation pass split over component groups x row slabs with r used directly
+// as the A operand of r^T [x | x^2], and a fixed-order fp64 reduction of the slab
+// partials.  Row slabs are disjoint ([s*R, min(N, (s+1)*R))), so no row is counted
+// twice at a slab boundary.
+
+#include "fgmm_common.hpp"
+
+#include <math.h>
+
+namespace fgmm {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kCUs = 256;
+constexpr int kAccWaves = 8;
+constexpr int kAccThreads = 64 * kAccWaves;
+constexpr int kRowGroups = 2;
+
+// LDS-resident pass 2 when mu' of 4 component blocks (4 x 32 x 2*DP floats) and two
+// 64-row X buffers fit in LDS.
+__host__ __device__ constexpr bool diag_accum_uses_lds(int DP) { return DP <= 96; }
+
+struct DiagPlan {
+  int64_t N, K, D;
+  int DP, FP;   // D padded to 32; feature count 2*DP
+  int KB, KP, ncg, nslab, rgroups, npart;
+  int64_t rows_per_slab;
+  size_t off_musw, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_sq, off_part_nk, total;
+};
+
+DiagPlan make_plan(int64_t N, int64_t K, int64_t D) {
+  DiagPlan p{};
+  p.N = N; p.K = K; p.D = D;
+  p.DP = (int)round_up(D < 1 ? 1 : D, 32);
+  p.FP = 2 * p.DP;
+  p.KB = (int)cdiv(K, 32);
+  p.KP = p.KB * 32;
+  p.ncg = (int)cdiv(p.KB, kWaves);
+  p.rgroups = diag_accum_uses_lds(p.DP) ? kRowGroups : 1;
+  const int64_t tile_rows = 32 * p.rgroups;
+  if (N > 0 && p.ncg > 0) {
+    int64_t want = (int64_t)kCUs / p.ncg;
+    if (want >= 8) want = (want / 8) * 8;
+    if (want < 1) want = 1;
+    const int64_t max_slabs = cdiv(N, tile_rows);
+    if (want > max_slabs) want = max_slabs;
+    p.rows_per_slab = round_up(cdiv(N, want), tile_rows);
+    p.nslab = (int)cdiv(N, p.rows_per_slab);
+  } else {
+    p.rows_per_slab = tile_rows;
+    p.nslab = 0;
+  }
+  p.npart = p.nslab * p.rgroups;
+  size_t off = 0;
+  p.off_musw = off;    off = align256(off + (size_t)p.KP * p.FP * sizeof(float));
+  p.off_kcblk = off;   off = align256(off + (size_t)p.KP * sizeof(double));
+  p.off_kclin = off;   off = align256(off + (size_t)p.KP * sizeof(double));
+  p.off_rowstat = off; off = align256(off + (size_t)(N > 0 ? N : 0) * sizeof(double));
+  p.off_part_mu = off; off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
+  p.off_part_sq = off; off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
+  p.off_part_nk = off; off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
+  p.total = off;
+  return p;
+}
+
+__device__ __forceinline__ f32x4 sq4(f32x4 v) { return v * v; }
+
+// ---------------------------------------------------------------------------
+// Prologue: features [-w | 2v] in operand order and the per-component constant.
+// One 64-thread block per 32-component block.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void diag_prep(const float* __restrict__ mu, int64_t ldmu,
+                                                const float* __restrict__ lss, int64_t ldlss, int64_t K,
+                                                int D, int DP, const float* __restrict__ lpi,
+                                                f32x4* __restrict__ mu_sw, double* __restrict__ kc_blk,
+                                                double* __restrict__ kc_lin) {
+  __shared__ double sC[32];
+  const int kb = blockIdx.x;
+  const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  const int64_t comp = (int64_t)kb * 32 + c;
+  const bool valid = comp < K;
+  if (g == 0) {
+    double C = -INFINITY;
+    if (valid) {
+      double lsum = 0.0, q = 0.0;
+      for (int d = 0; d < D; ++d) {
+        const double l = (double)lss[comp * ldlss + d];
+        const double m = (double)mu[comp * ldmu + d];
+        const double w = 0.5 * exp(-l) * kLog2e;
+        lsum += l;
+        q = fma(m * m, w, q);
+      }
+      C = ((double)lpi[comp] - 0.5 * ((double)D * kLog2Pi + lsum)) * kLog2e - q;
+    }
+    sC[c] = C;
+    kc_lin[comp] = C;
+  }
+  const int FP = 2 * DP, NM = FP / 8;
+  for (int m = 0; m < NM; ++m) {
+    f32x4 v = zero4();
+    const int f0 = 8 * m + 4 * g;
+    if (valid) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int f = f0 + e;
+        const int d = f < DP ? f : f - DP;
+        float val = 0.0f;
+        if (d < D) {
+          const double w = 0.5 * exp(-(double)lss[comp * ldlss + d]) * kLog2e;
+          val = (f < DP) ? (float)(-w) : (float)(2.0 * (double)mu[comp * ldmu + d] * w);
+        }
+        v[e] = val;
+      }
+    }
+    mu_sw[((int64_t)kb * NM + m) * 64 + lane] = v;
+  }
+  __syncthreads();
+  if (lane < 32) {
+    const int i = lane & 15, gg = lane >> 4;
+    kc_blk[(int64_t)kb * 32 + gg * 16 + i] = sC[acc_row(i, gg)];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 1: logZ.  Each wave keeps 32 rows of X resident; feature chunks m < DP/8
+// are x^2 (formed on the fly), the rest x.  mu' blocks stream through LDS.
+// ---------------------------------------------------------------------------
+template <int DP>
+constexpr size_t lse_lds_bytes() {
+  return (size_t)2 * (2 * DP) * 32 * sizeof(float) + (size_t)2 * 32 * sizeof(double);
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(DP <= 96 ? 2 : 1, DP <= 96 ? 2 : 1)))
+void diag_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+              const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_blk, int KB,
+              float* __restrict__ logZ, double* __restrict__ rowstat) {
+  constexpr int NMX = DP / 8;
+  constexpr int NM = 2 * NMX;
+  constexpr int BLK = NM * 64;
+  constexpr int LPT = BLK / kThreads;
+  static_assert(BLK % kThreads == 0, "block load must split evenly");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  f32x4* mu_l = reinterpret_cast<f32x4*>(lds_raw);                              // [2][BLK]
+  double* kc_l = reinterpret_cast<double*>(lds_raw + 2 * BLK * sizeof(f32x4));  // [2][32]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t row = ((int64_t)blockIdx.x * kWaves + wave) * 32 + c;
+  const bool valid = row < N;
+
+  f32x4 st[LPT];
+  double kst = 0.0;
+  auto fetch = [&](int kb) {
+    const f32x4* src = mu_sw + (int64_t)kb * BLK;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) st[q] = src[q * kThreads + tid];
+    if (tid < 32) kst = kc_blk[(int64_t)kb * 32 + tid];
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) mu_l[buf * BLK + q * kThreads + tid] = st[q];
+    if (tid < 32) kc_l[buf * 32 + tid] = kst;
+  };
+  fetch(0);
+  f32x4 xb[NMX];
+#pragma unroll
+  for (int m = 0; m < NMX; ++m) xb[m] = load_row4(X, ldx, row, 8 * m + 4 * g, D, valid);
+  commit(0);
+  __syncthreads();
+
+  double mx = -INFINITY;
+  float sm = 0.0f;
+  for (int kb = 0; kb < KB; ++kb) {
+    const int buf = kb & 1;
+    const bool more = kb + 1 < KB;
+    if (more) fetch(kb + 1);
+    const f32x4* mp = mu_l + buf * BLK + lane;
+    double xm[16];
+    cross_tile<NM>(xm, [&](int m) { return mp[m * 64]; },
+                   [&](int m) { return m < NMX ? sq4(xb[m]) : xb[m - NMX]; });
+    const double* kp = kc_l + buf * 32 + g * 16;
+    double ll[16];
+    double bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      ll[i] = kp[i] + xm[i];
+      bm = fmax(bm, ll[i]);
+    }
+    const double mn = fmax(mx, bm);
+    const double ms = (mn == -INFINITY) ? 0.0 : mn;
+    float acc = sm * fast_exp2((float)(mx - ms));
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc += fast_exp2((float)(ll[i] - ms));
+    sm = acc;
+    mx = mn;
+    if (more) commit(buf ^ 1);
+    __syncthreads();
+  }
+  const double mo = __shfl_xor(mx, 32);
+  const float so = __shfl_xor(sm, 32);
+  const double mn = fmax(mx, mo);
+  const double ms = (mn == -INFINITY) ? 0.0 : mn;
+  const float tot = sm * fast_exp2((float)(mx - ms)) + so * fast_exp2((float)(mo - ms));
+  const double lz2 = mn + (double)log2f(tot);
+  if (valid && g == 0) {
+    rowstat[row] = lz2;
+    if (logZ) logZ[row] = (float)(lz2 * kLn2);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2.  One template for both residency variants:
+//   LDS = true : 8 waves (2 row groups x 4 component blocks), mu' in LDS.
+//   LDS = false: 4 waves (1 row group), mu' resident in registers.
+// r^T [x | x^2] accumulates into 2*DP/32 32x32 tiles per wave.
+// ---------------------------------------------------------------------------
+template <int DP, bool LDS>
+constexpr size_t accum_lds_bytes() {
+  constexpr int RG = LDS ? kRowGroups : 1;
+  return (LDS ? (size_t)kWaves * (2 * DP) * 32 * sizeof(float) : 0) +
+         (size_t)2 * 32 * RG * (DP + 4) * sizeof(float) + (size_t)2 * 32 * RG * sizeof(double);
+}
+
+template <int DP, bool LDS>
+__global__ __attribute__((amdgpu_flat_work_group_size(LDS ? kAccThreads : kThreads,
+                                                      LDS ? kAccThreads : kThreads),
+                          amdgpu_waves_per_eu(LDS ? 2 : 1, LDS ? 2 : 1)))
+void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_lin, int KB, int KP,
+                const double* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
+                float* __restrict__ part_mu, float* __restrict__ part_sq, float* __restrict__ part_nk) {
+  constexpr int NMX = DP / 8;
+  constexpr int NM = 2 * NMX;
+  constexpr int NJ = DP / 32;
+  constexpr int RS = DP + 4;
+  constexpr int V4 = DP / 4;
+  constexpr int BLK = NM * 64;
+  constexpr int RG = LDS ? kRowGroups : 1;
+  constexpr int NT = LDS ? kAccThreads : kThreads;
+  constexpr int TR = 32 * RG;
+  constexpr int LPT = (TR * V4) / NT;
+  static_assert((TR * V4) % NT == 0, "even split");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const size_t mu_bytes = LDS ? (size_t)kWaves * BLK * sizeof(f32x4) : 0;
+  f32x4* mu_l = reinterpret_cast<f32x4*>(lds_raw);
+  float* xs = reinterpret_cast<float*>(lds_raw + mu_bytes);                               // [2][TR*RS]
+  double* rs = reinterpret_cast<double*>(lds_raw + mu_bytes + 2 * TR * RS * sizeof(float));  // [2][TR]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int cbw = wave & 3, rg = LDS ? (wave >> 2) : 0;
+  const int slab = blockIdx.x % nslab;
+  const int cg = blockIdx.x / nslab;
+  const int kb = cg * kWaves + cbw;
+  const bool active = kb < KB;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
+
+  f32x4 mub[LDS ? 1 : NM];
+  if constexpr (LDS) {
+    constexpr int MPT = (kWaves * BLK) / kAccThreads;
+#pragma unroll
+    for (int q = 0; q < MPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      const int b = idx / BLK;
+      const int kbq = cg * kWaves + b;
+      mu_l[idx] = (kbq < KB) ? mu_sw[(int64_t)kbq * BLK + (idx % BLK)] : zero4();
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < NM; ++m) mub[m] = active ? mu_sw[((int64_t)kb * NM + m) * 64 + lane] : zero4();
+  }
+  const double Ck = active ? kc_lin[(int64_t)kb * 32 + c] : -INFINITY;
+
+  f32x16 accx[NJ], accq[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    accx[j] = zero16();
+    accq[j] = zero16();
+  }
+  float nk = 0.0f;
+
+  f32x4 stage[LPT];
+  double rstage = INFINITY;
+  auto fetch = [&](int t) {
+    const int64_t row0 = r_begin + (int64_t)t * TR;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * NT + tid;
+      const int rr = idx / V4, c4 = idx % V4;
+      const int64_t row = row0 + rr;
+      stage[q] = load_row4(X, ldx, row, c4 * 4, D, row < r_end);
+    }
+    if (tid < TR) {
+      const int64_t row = row0 + tid;
+      rstage = (row < r_end) ? rowstat[row] : INFINITY;
+    }
+  };
+  auto commit = [&](int buf) {
+    float* dst = xs + buf * TR * RS;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * NT + tid;
+      const int rr = idx / V4, c4 = idx % V4;
+      *reinterpret_cast<f32x4*>(dst + rr * RS + c4 * 4) = stage[q];
+    }
+    if (tid < TR) rs[buf * TR + tid] = rstage;
+  };
+
+  if (ntiles > 0) {
+    fetch(0);
+    commit(0);
+  }
+  __syncthreads();
+
+  const f32x4* mb = mu_l + cbw * BLK + lane;
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    const float* xt = xs + buf * TR * RS + rg * 32 * RS;
+    const double* rt = rs + buf * TR + rg * 32;
+    double xm[16];
+    float r[16];
+    if (active) {
+      // The 2D-feature contraction is twice as long as the isotropic one, so the
+      // responsibilities use the chunked fp64 form as well (fp32 chains over 2D
+      // features leave ~1e-4 relative error in r).
+      auto la = [&](int m) {
+        const f32x4 v =
+            *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * (m < NMX ? m : m - NMX) + 4 * g);
+        return m < NMX ? sq4(v) : v;
+      };
+      if constexpr (LDS)
+        cross_tile<NM>(xm, la, [&](int m) { return mb[m * 64]; });
+      else
+        cross_tile<NM>(xm, la, [&](int m) { return mub[m]; });
+      const double* rbase = rt + 4 * g;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ro = 8 * (i >> 2) + (i & 3);
+        const float rv = fast_exp2((float)((Ck - rbase[ro]) + xm[i]));
+        nk += rv;
+        r[i] = rv;
+      }
+    }
+    if (more) fetch(t + 1);
+    if (active) {
+      const float* xbase = xt + 4 * g * RS + c;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ro = 8 * (i >> 2) + (i & 3);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const float xv = xbase[ro * RS + 32 * j];
+          accx[j] = mfma32(r[i], xv, accx[j]);
+          accq[j] = mfma32(r[i], xv * xv, accq[j]);
+        }
+      }
+    }
+    if (more) commit(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (active) {
+    nk += __shfl_xor(nk, 32);
+    const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t o = (kbase + acc_row(i, g)) * DP + 32 * j + c;
+        part_mu[o] = accx[j][i];
+        part_sq[o] = accq[j][i];
+      }
+    }
+    if (g == 0) part_nk[kbase + c] = nk;
+  }
+}
+
+// Finish: one thread per (k, d); fixed-order fp64 sums over partials, then the
+// sig identity in fp64.  Thread d == 0 also writes Nk.
+__global__ __launch_bounds__(256) void diag_reduce(const float* __restrict__ part_mu,
+                                                   const float* __restrict__ part_sq,
+                                                   const float* __restrict__ part_nk, int npart, int KP,
+                                                   int DP, int64_t K, int D, const float* __restrict__ mu,
+                                                   int64_t ldmu, float* __restrict__ Nk,
+                                                   float* __restrict__ mu_acc, float* __restrict__ sig_acc,
+                                                   int accumulate) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= K * D) return;
+  const int64_t k = idx / D;
+  const int d = (int)(idx % D);
+  double sm = 0.0, sq = 0.0, nk = 0.0;
+  for (int p = 0; p < npart; ++p) {
+    const int64_t o = ((int64_t)p * KP + k) * DP + d;
+    sm += (double)part_mu[o];
+    sq += (double)part_sq[o];
+    nk += (double)part_nk[(int64_t)p * KP + k];
+  }
+  const double m = (double)mu[k * ldmu + d];
+  const double sg = sq - 2.0 * m * sm + m * m * nk;
+  float* om = mu_acc + k * D + d;
+  float* os = sig_acc + k * D + d;
+  *om = accumulate ? (float)((double)*om + sm) : (float)sm;
+  *os = accumulate ? (float)((double)*os + sg) : (float)sg;
+  if (d == 0) Nk[k] = accumulate ? (float)((double)Nk[k] + nk) : (float)nk;
+}
+
+__global__ __launch_bounds__(256) void diag_fill(float* __restrict__ p, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+template <int DP>
+hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
+                         float* logZ, bool run1, bool run2, hipStream_t stream) {
+  const f32x4* mu_sw = reinterpret_cast<const f32x4*>(ws + pl.off_musw);
+  const double* kc_blk = reinterpret_cast<const double*>(ws + pl.off_kcblk);
+  const double* kc_lin = reinterpret_cast<const double*>(ws + pl.off_kclin);
+  double* rowstat = reinterpret_cast<double*>(ws + pl.off_rowstat);
+  if (run1) {
+    constexpr size_t lds1 = lse_lds_bytes<DP>();
+    if (lds1 > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_lse<DP>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(diag_lse<DP>, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
+                       stream, X, ldx, pl.N, (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
+  }
+  if (!run2) return hipGetLastError();
+  constexpr bool L = diag_accum_uses_lds(DP);
+  constexpr size_t lds2 = accum_lds_bytes<DP, L>();
+  if (lds2 > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum<DP, L>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((diag_accum<DP, L>), dim3((unsigned)(pl.nslab * pl.ncg)),
+                     dim3(L ? kAccThreads : kThreads), lds2, stream, X, ldx, pl.N, (int)pl.D, mu_sw,
+                     kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
+                     reinterpret_cast<float*>(ws + pl.off_part_mu),
+                     reinterpret_cast<float*>(ws + pl.off_part_sq),
+                     reinterpret_cast<float*>(ws + pl.off_part_nk));
+  return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace fgmm
+
+using namespace fgmm;
+
+extern "C" size_t fgmm_diag_workspace_bytes(int64_t N, int64_t K, int64_t D) {
+  if (N < 0 || K < 0 || D < 1) return 0;
+  return make_plan(N, K, D).total;
+}
+
+extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
+                                   int64_t ldmu, int64_t K, const float* log_sigma_sq, int64_t ldlss,
+                                   const float* log_pi, float* logZ, float* Nk, float* mu_acc,
+                                   float* sig_acc, void* workspace, size_t workspace_bytes,
+                                   unsigned flags, void* stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const bool want_logz = !(flags & FGMM_FLAG_NO_LOGZ);
+  const bool accumulate = (flags & FGMM_FLAG_ACCUMULATE) != 0;
+  if (N < 0 || K < 0 || D < 1) return FGMM_ERR_INVALID_ARG;
+  if (N > 0 && (X == nullptr || ldx < round_up(D, 4) || (ldx % 4) != 0 ||
+                (reinterpret_cast<uintptr_t>(X) & 15) != 0))
+    return FGMM_ERR_INVALID_ARG;
+  if (N > 0 && want_logz && logZ == nullptr) return FGMM_ERR_INVALID_ARG;
+  if (K > 0 && (mu == nullptr || ldmu < D || log_sigma_sq == nullptr || ldlss < D ||
+                log_pi == nullptr || Nk == nullptr || mu_acc == nullptr || sig_acc == nullptr))
+    return FGMM_ERR_INVALID_ARG;
+  if (D > 128) return FGMM_ERR_UNSUPPORTED;
+  if (N > (int64_t)1 << 40 || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
+  const DiagPlan pl = make_plan(N, K, D);
+  if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
+  if (!want_logz) logZ = nullptr;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  const bool sel1 = (flags & FGMM_FLAG_PHASE1) != 0, sel2 = (flags & FGMM_FLAG_PHASE2) != 0;
+  const bool run1 = sel1 || !sel2, run2 = sel2 || !sel1;
+
+  if (K == 0) {
+    if (N > 0 && logZ)
+      hipLaunchKernelGGL(diag_fill, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, stream, logZ, N,
+                         -INFINITY);
+    return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+  }
+  if (run1)
+    hipLaunchKernelGGL(diag_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
+                       (int)D, pl.DP, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_musw),
+                       reinterpret_cast<double*>(ws + pl.off_kcblk),
+                       reinterpret_cast<double*>(ws + pl.off_kclin));
+  if (N > 0) {
+    hipError_t e = hipSuccess;
+    switch (pl.DP) {
+      case 32: e = launch_passes<32>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 96: e = launch_passes<96>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 128: e = launch_passes<128>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      default: return FGMM_ERR_UNSUPPORTED;
+    }
+    if (e != hipSuccess) return FGMM_ERR_HIP;
+  }
+  if (!run2) return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+  hipLaunchKernelGGL(diag_reduce, dim3((unsigned)cdiv(K * D, 256)), dim3(256), 0, stream,
+                     reinterpret_cast<const float*>(ws + pl.off_part_mu),
+                     reinterpret_cast<const float*>(ws + pl.off_part_sq),
+                     reinterpret_cast<const float*>(ws + pl.off_part_nk), pl.npart, pl.KP, pl.DP, K,
+                     (int)D, mu, ldmu, Nk, mu_acc, sig_acc, accumulate ? 1 : 0);
+  return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+}

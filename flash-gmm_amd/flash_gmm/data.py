@@ -8,7 +8,11 @@ The workloads below are the E-step shapes this package is measured on.  In
 Every generator takes an explicit ``seed`` and ``device`` and draws from a
 ``torch.Generator`` on that device, so the same (seed, device) always yields
 the same tensors.  CPU and GPU generators produce different streams: parity
-tests generate on the CPU and copy to the GPU.
+tests generate on the CPU and copy to the GPU.  Values that pass through a
+transcendental function (variances, log-softmax weights) are computed in
+float64 and rounded to float32 once, because float32 vectorised exp/log differ
+in the last bit between host CPUs and the golden fixtures identify inputs by
+their bytes.
 """
 
 from __future__ import annotations
@@ -31,6 +35,10 @@ def _randn(g, *shape, device, std=1.0):
 
 def _rand(g, *shape, device, lo=0.0, hi=1.0):
     return torch.rand(*shape, generator=g, device=device, dtype=torch.float32) * (hi - lo) + lo
+
+
+def _log_softmax(v: torch.Tensor) -> torch.Tensor:
+    return torch.log_softmax(v.double(), dim=0).float()
 
 
 def iso_plain(N: int, K: int, D: int, seed: int = 0, device="cpu") -> Dict[str, torch.Tensor]:
@@ -60,7 +68,7 @@ def iso_clustered(N: int, K: int, D: int, seed: int = 1, device="cpu",
     c = _randn(g, K, D, device=device, std=2.0)
     mu = c + _randn(g, K, D, device=device, std=0.5)
     lss = _rand(g, K, device=device, lo=-0.5, hi=0.5)
-    lpi = torch.log_softmax(_randn(g, K, device=device), dim=0)
+    lpi = _log_softmax(_randn(g, K, device=device))
     X = torch.empty(N, D, device=device, dtype=torch.float32)
     for n0 in range(0, N, row_chunk):
         n1 = min(N, n0 + row_chunk)
@@ -83,7 +91,7 @@ def diag_clustered(N: int, K: int, D: int, seed: int = 2, device="cpu",
     mu = c + _randn(g, K, D, device=device, std=0.5)
     lpi = torch.full((K,), -math.log(K), device=device)
     X = torch.empty(N, D, device=device, dtype=torch.float32)
-    sd = torch.exp(0.5 * logvar)
+    sd = torch.exp(0.5 * logvar.double()).float()
     for n0 in range(0, N, row_chunk):
         n1 = min(N, n0 + row_chunk)
         a = _assign_rows(g, n1 - n0, K, device)
@@ -108,15 +116,16 @@ def full_clustered(N: int, K: int, D: int, seed: int = 3, device="cpu") -> Dict[
     prec_chol = torch.linalg.cholesky(torch.linalg.inv(sigma))
     chol_sigma = torch.linalg.cholesky(sigma)
     mu = _randn(g, K, D, device=device, std=2.0)
-    lpi = torch.log_softmax(_randn(g, K, device=device, std=math.sqrt(0.5)), dim=0)
+    lpi = _log_softmax(_randn(g, K, device=device, std=math.sqrt(0.5)))
     a = _assign_rows(g, N, K, device, probs=torch.exp(lpi.double()).float())
     z = _randn(g, N, D, device=device)
     X = torch.empty(N, D, device=device, dtype=torch.float32)
-    cs = chol_sigma.float().to(device)
+    cs = chol_sigma.float().double().to(device)
+    mu64 = mu.double()
     for k in range(K):
         idx = (a == k).nonzero(as_tuple=True)[0]
         if idx.numel():
-            X[idx] = mu[k] + z[idx] @ cs[k].T
+            X[idx] = (mu64[k] + z[idx].double() @ cs[k].T).float()
     return dict(X=X, mu=mu, prec_chol=prec_chol.float().to(device), log_pi=lpi)
 
 

@@ -9,6 +9,11 @@ reference:
   compatibility and ignored: tiles are chosen by the library, and D is not
   limited by BLOCK_D (the same-named H100 entry sizes BLOCK_D from D,
   flash_gmm_h100.py:268-270).
+* ``flash_gmm_estep_diag(X, mu, log_sigma_sq, log_pi)`` with log_sigma_sq of
+  shape (K, D) -- flash_gmm_diag_h100.py:305-384; sig_acc is (K, D).
+* ``flash_gmm_estep_full(X, mu, prec_chol, log_pi)`` with prec_chol (K, D, D)
+  lower-triangular, L L^T = Sigma^-1 -- flash_gmm_full_h100.py:235-336; the
+  fourth output is sig_outer (K, D, D) = sum_n r_nk x_n x_n^T.
 
 Outputs are fresh float32 tensors on X.device (flash_gmm.py:192-195), written
 asynchronously on torch's current stream; nothing synchronises.
@@ -21,7 +26,8 @@ import torch
 from . import _lib
 from ._lib import FlashGMMError
 
-__all__ = ["flash_gmm_estep", "iso_estep_into"]
+__all__ = ["flash_gmm_estep", "iso_estep_into", "flash_gmm_estep_diag", "diag_estep_into",
+           "flash_gmm_estep_full", "full_estep_into"]
 
 
 def _require(cond: bool, msg: str) -> None:
@@ -68,6 +74,45 @@ def _vec(t: torch.Tensor, device, shape, name) -> torch.Tensor:
     return t.to(device=device, dtype=torch.float32).contiguous()
 
 
+def _flags(accumulate, logZ, atomic_reduce, phase):
+    flags = 0
+    if accumulate:
+        flags |= _lib.FLAG_ACCUMULATE
+    if logZ is None:
+        flags |= _lib.FLAG_NO_LOGZ
+    if atomic_reduce:
+        flags |= _lib.FLAG_ATOMIC_REDUCE
+    if phase == 1:
+        flags |= _lib.FLAG_PHASE1
+    elif phase == 2:
+        flags |= _lib.FLAG_PHASE2
+    elif phase != 0:
+        raise FlashGMMError(f"phase must be 0, 1 or 2, got {phase}")
+    return flags
+
+
+def _check_out(name, t, shape, dev):
+    _require(t is not None and tuple(t.shape) == tuple(shape) and t.dtype == torch.float32
+             and t.is_contiguous() and t.device == dev,
+             f"{name} must be a contiguous float32 {tuple(shape)} tensor on {dev}")
+
+
+def _workspace(ws_fn, N, K, D, dev, workspace):
+    ws_bytes = int(ws_fn(N, K, D))
+    if workspace is None or workspace.numel() < ws_bytes:
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    return workspace
+
+
+def _ptr(t, cond=True):
+    return t.data_ptr() if (t is not None and cond) else None
+
+
+def _rowmajor(t: torch.Tensor) -> torch.Tensor:
+    """Unit stride along the last dimension (any row stride)."""
+    return t if (t.dim() == 0 or t.stride(-1) == 1 or t.shape[-1] == 1) else t.contiguous()
+
+
 def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
                    accumulate: bool = False, atomic_reduce: bool = False,
                    workspace: torch.Tensor | None = None, phase: int = 0) -> None:
@@ -86,39 +131,21 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     lss = _vec(log_sigma_sq, dev, (K,), "log_sigma_sq")
     lpi = _vec(log_pi, dev, (K,), "log_pi")
     Xk, ldx = _prep_rows(X)
-    muk = mu if (mu.stride(1) == 1 or D == 1) else mu.contiguous()
+    muk = _rowmajor(mu)
     ldmu = muk.stride(0) if K > 1 else D
     L = _lib.lib()
-    ws_bytes = int(L.fgmm_iso_workspace_bytes(N, K, D))
-    if workspace is None or workspace.numel() < ws_bytes:
-        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    flags = 0
-    if accumulate:
-        flags |= _lib.FLAG_ACCUMULATE
-    if logZ is None:
-        flags |= _lib.FLAG_NO_LOGZ
-    if atomic_reduce:
-        flags |= _lib.FLAG_ATOMIC_REDUCE
-    if phase == 1:
-        flags |= _lib.FLAG_PHASE1
-    elif phase == 2:
-        flags |= _lib.FLAG_PHASE2
-    elif phase != 0:
-        raise FlashGMMError(f"phase must be 0, 1 or 2, got {phase}")
-    for name, t, shp in (("Nk", Nk, (K,)), ("mu_acc", mu_acc, (K, D)), ("sig_acc", sig_acc, (K,))):
-        _require(tuple(t.shape) == shp and t.dtype == torch.float32 and t.is_contiguous()
-                 and t.device == dev, f"{name} must be a contiguous float32 {shp} tensor on {dev}")
+    workspace = _workspace(L.fgmm_iso_workspace_bytes, N, K, D, dev, workspace)
+    flags = _flags(accumulate, logZ, atomic_reduce, phase)
+    _check_out("Nk", Nk, (K,), dev)
+    _check_out("mu_acc", mu_acc, (K, D), dev)
+    _check_out("sig_acc", sig_acc, (K,), dev)
     if logZ is not None:
-        _require(tuple(logZ.shape) == (N,) and logZ.dtype == torch.float32 and logZ.is_contiguous(),
-                 f"logZ must be a contiguous float32 ({N},) tensor")
+        _check_out("logZ", logZ, (N,), dev)
     with torch.cuda.device(dev):
         st = L.fgmm_iso_estep_f32(
-            Xk.data_ptr() if N > 0 else None, ldx, N, D,
-            muk.data_ptr() if K > 0 else None, ldmu, K,
-            lss.data_ptr() if K > 0 else None, lpi.data_ptr() if K > 0 else None,
-            logZ.data_ptr() if (logZ is not None and N > 0) else None,
-            Nk.data_ptr() if K > 0 else None, mu_acc.data_ptr() if K > 0 else None,
-            sig_acc.data_ptr() if K > 0 else None,
+            _ptr(Xk, N > 0), ldx, N, D, _ptr(muk, K > 0), ldmu, K,
+            _ptr(lss, K > 0), _ptr(lpi, K > 0), _ptr(logZ, N > 0),
+            _ptr(Nk, K > 0), _ptr(mu_acc, K > 0), _ptr(sig_acc, K > 0),
             workspace.data_ptr(), workspace.numel(), flags, _lib.stream_handle(dev))
     _lib.check(st, "fgmm_iso_estep_f32")
 
@@ -142,3 +169,111 @@ def flash_gmm_estep(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tenso
     sig_acc = torch.empty(K, device=dev, dtype=torch.float32)
     iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc)
     return logZ, Nk, mu_acc, sig_acc
+
+
+def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
+                    accumulate: bool = False, workspace: torch.Tensor | None = None,
+                    phase: int = 0) -> None:
+    """Diagonal-covariance E-step into caller-provided outputs (sig_acc is (K, D))."""
+    _check_common(X, mu, log_pi)
+    N, D = X.shape
+    K = mu.shape[0]
+    dev = X.device
+    _require(tuple(log_sigma_sq.shape) == (K, D),
+             f"log_sigma_sq must be (K, D)=({K}, {D}), got {tuple(log_sigma_sq.shape)}")
+    lss = _rowmajor(log_sigma_sq.to(device=dev, dtype=torch.float32))
+    ldlss = lss.stride(0) if K > 1 else D
+    lpi = _vec(log_pi, dev, (K,), "log_pi")
+    Xk, ldx = _prep_rows(X)
+    muk = _rowmajor(mu)
+    ldmu = muk.stride(0) if K > 1 else D
+    L = _lib.lib()
+    _require(hasattr(L, "fgmm_diag_estep_f32"), "library built without the diagonal E-step")
+    workspace = _workspace(L.fgmm_diag_workspace_bytes, N, K, D, dev, workspace)
+    flags = _flags(accumulate, logZ, False, phase)
+    _check_out("Nk", Nk, (K,), dev)
+    _check_out("mu_acc", mu_acc, (K, D), dev)
+    _check_out("sig_acc", sig_acc, (K, D), dev)
+    if logZ is not None:
+        _check_out("logZ", logZ, (N,), dev)
+    with torch.cuda.device(dev):
+        st = L.fgmm_diag_estep_f32(
+            _ptr(Xk, N > 0), ldx, N, D, _ptr(muk, K > 0), ldmu, K, _ptr(lss, K > 0), ldlss,
+            _ptr(lpi, K > 0), _ptr(logZ, N > 0), _ptr(Nk, K > 0), _ptr(mu_acc, K > 0),
+            _ptr(sig_acc, K > 0), workspace.data_ptr(), workspace.numel(), flags,
+            _lib.stream_handle(dev))
+    _lib.check(st, "fgmm_diag_estep_f32")
+
+
+def flash_gmm_estep_diag(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tensor,
+                         log_pi: torch.Tensor):
+    """Diagonal-covariance E-step: returns (logZ, Nk, mu_acc, sig_acc[K, D]).
+
+    sig_acc[k, d] = sum_n r_nk (x_nd - mu_kd)^2 (flash_gmm_diag_h100.py:258-260).
+    """
+    _check_common(X, mu, log_pi)
+    N, D = X.shape
+    K = mu.shape[0]
+    _require(tuple(log_sigma_sq.shape) == (K, D),
+             f"log_sigma_sq must be (K, D)=({K}, {D}), got {tuple(log_sigma_sq.shape)}")
+    dev = X.device
+    logZ = torch.empty(N, device=dev, dtype=torch.float32)
+    Nk = torch.empty(K, device=dev, dtype=torch.float32)
+    mu_acc = torch.empty(K, D, device=dev, dtype=torch.float32)
+    sig_acc = torch.empty(K, D, device=dev, dtype=torch.float32)
+    diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc)
+    return logZ, Nk, mu_acc, sig_acc
+
+
+def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
+                    accumulate: bool = False, workspace: torch.Tensor | None = None,
+                    phase: int = 0) -> None:
+    """Full-covariance E-step into caller-provided outputs (sig_outer is (K, D, D))."""
+    _check_common(X, mu, log_pi)
+    N, D = X.shape
+    K = mu.shape[0]
+    dev = X.device
+    _require(tuple(prec_chol.shape) == (K, D, D),
+             f"prec_chol must be (K, D, D)=({K}, {D}, {D}), got {tuple(prec_chol.shape)}")
+    Lc = prec_chol.to(device=dev, dtype=torch.float32).contiguous()
+    lpi = _vec(log_pi, dev, (K,), "log_pi")
+    Xk, ldx = _prep_rows(X)
+    muk = _rowmajor(mu)
+    ldmu = muk.stride(0) if K > 1 else D
+    L = _lib.lib()
+    _require(hasattr(L, "fgmm_full_estep_f32"), "library built without the full-covariance E-step")
+    workspace = _workspace(L.fgmm_full_workspace_bytes, N, K, D, dev, workspace)
+    flags = _flags(accumulate, logZ, False, phase)
+    _check_out("Nk", Nk, (K,), dev)
+    _check_out("mu_acc", mu_acc, (K, D), dev)
+    _check_out("sig_outer", sig_outer, (K, D, D), dev)
+    if logZ is not None:
+        _check_out("logZ", logZ, (N,), dev)
+    with torch.cuda.device(dev):
+        st = L.fgmm_full_estep_f32(
+            _ptr(Xk, N > 0), ldx, N, D, _ptr(muk, K > 0), ldmu, K, _ptr(Lc, K > 0),
+            _ptr(lpi, K > 0), _ptr(logZ, N > 0), _ptr(Nk, K > 0), _ptr(mu_acc, K > 0),
+            _ptr(sig_outer, K > 0), workspace.data_ptr(), workspace.numel(), flags,
+            _lib.stream_handle(dev))
+    _lib.check(st, "fgmm_full_estep_f32")
+
+
+def flash_gmm_estep_full(X: torch.Tensor, mu: torch.Tensor, prec_chol: torch.Tensor,
+                         log_pi: torch.Tensor):
+    """Full-covariance E-step: returns (logZ, Nk, mu_acc, sig_outer[K, D, D]).
+
+    prec_chol[k] is lower-triangular with prec_chol[k] @ prec_chol[k].T = Sigma_k^-1;
+    sig_outer[k] = sum_n r_nk x_n x_n^T (flash_gmm_full_h100.py:245-260).
+    """
+    _check_common(X, mu, log_pi)
+    N, D = X.shape
+    K = mu.shape[0]
+    _require(tuple(prec_chol.shape) == (K, D, D),
+             f"prec_chol must be (K, D, D)=({K}, {D}, {D}), got {tuple(prec_chol.shape)}")
+    dev = X.device
+    logZ = torch.empty(N, device=dev, dtype=torch.float32)
+    Nk = torch.empty(K, device=dev, dtype=torch.float32)
+    mu_acc = torch.empty(K, D, device=dev, dtype=torch.float32)
+    sig_outer = torch.empty(K, D, D, device=dev, dtype=torch.float32)
+    full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer)
+    return logZ, Nk, mu_acc, sig_outer

@@ -85,6 +85,25 @@ int fgmm_iso_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
                        void *workspace, size_t workspace_bytes,
                        unsigned flags, void *stream);
 
+/* ------------------------------------------------------------------------ */
+/* Diagonal-covariance E-step.                                               */
+/* Replaces flash_gmm_estep_diag(X, mu, log_sigma_sq, log_pi) at             */
+/* flash_gmm_diag_h100.py:305-384.  log_sigma_sq is K x D with row stride     */
+/* ldlss; sig_acc is K x D:                                                   */
+/*   ll_nk      = log_pi_k - 0.5*(D log(2 pi) + sum_d lss_kd)                 */
+/*                - 0.5 * sum_d (x_nd - mu_kd)^2 exp(-lss_kd)                 */
+/*   sig_acc_kd = sum_n r_nk (x_nd - mu_kd)^2                                 */
+/* Supports 1 <= D <= 128.                                                    */
+/* ------------------------------------------------------------------------ */
+size_t fgmm_diag_workspace_bytes(int64_t N, int64_t K, int64_t D);
+
+int fgmm_diag_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
+                        const float *mu, int64_t ldmu, int64_t K,
+                        const float *log_sigma_sq, int64_t ldlss, const float *log_pi,
+                        float *logZ, float *Nk, float *mu_acc, float *sig_acc,
+                        void *workspace, size_t workspace_bytes,
+                        unsigned flags, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,38 @@
+"""Shared tolerance checks for the GPU parity tests.
+
+Float32 kernels against the float64 oracle:
+  logZ        abs <= 1e-4
+  Nk, sig     |d| <= 1e-4 * |ref| + 1e-6 * max|ref|   (floor for near-empty components)
+  mu_acc      max|d| <= 1e-4 * max|ref|                (norm-wise; entries near zero make
+                                                        element-wise relative error meaningless)
+"""
+
+import numpy as np
+
+LOGZ_ATOL = 1e-4
+REL = 1e-4
+
+
+def _np(t):
+    return t.detach().double().cpu().numpy()
+
+
+def assert_close_stats(got, ref, what=""):
+    lz, nk, mu_acc, sig = (_np(t) for t in got)
+    rlz, rnk, rmu, rsig = (np.asarray(t, dtype=np.float64) for t in ref)
+    if rlz.size:
+        err = np.abs(lz - rlz)
+        finite = np.isfinite(rlz)
+        assert np.array_equal(np.isfinite(lz), finite), f"{what} logZ finiteness"
+        assert err[finite].max(initial=0) <= LOGZ_ATOL, f"{what} logZ max abs err {err[finite].max()}"
+    for name, g, r in (("Nk", nk, rnk), ("sig", sig, rsig)):
+        if r.size:
+            tol = REL * np.abs(r) + 1e-6 * np.abs(r).max(initial=0)
+            bad = np.abs(g - r) > tol
+            assert not bad.any(), f"{what} {name} max rel err {(np.abs(g - r) / np.maximum(np.abs(r), 1e-30)).max()}"
+    if rmu.size:
+        scale = np.abs(rmu).max(initial=0)
+        assert np.abs(mu_acc - rmu).max(initial=0) <= REL * scale + 1e-30, \
+            f"{what} mu_acc norm-wise err {np.abs(mu_acc - rmu).max() / max(scale, 1e-30)}"
+
+

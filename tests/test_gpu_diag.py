@@ -1,0 +1,102 @@
+"""GPU parity of the diagonal-covariance E-step against the CPU oracle (tolerances in parity.py)."""
+
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from flash_gmm import data, diag_estep_into, flash_gmm_estep, flash_gmm_estep_diag
+from oracle import gmm_oracle as O
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+import make_golden  # noqa: E402
+from parity import LOGZ_ATOL, assert_close_stats  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gpu(inp, dev):
+    out = flash_gmm_estep_diag(*[inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")])
+    torch.cuda.synchronize()
+    return out
+
+
+def oracle(inp):
+    return O.estep_diag(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+
+
+def test_golden_vectors(gpu_device):
+    name = "diag_n3000_k40_d24"
+    inp, kind = make_golden.make_inputs(name)
+    fx = np.load(os.path.join(os.path.dirname(make_golden.__file__), name + ".npz"))
+    assert str(fx["sha256"]) == make_golden.input_digest(inp)
+    assert_close_stats(run_gpu(inp, gpu_device), (fx["logZ"], fx["Nk"], fx["mu_acc"], fx["sig"]), name)
+
+
+@pytest.mark.parametrize("N,K,D", [(1, 1, 1), (33, 5, 3), (500, 40, 24), (1000, 70, 96),
+                                   (300, 33, 128), (129, 3, 64), (2000, 130, 50)])
+def test_edge_shapes(N, K, D, gpu_device):
+    inp = data.diag_clustered(N, K, D, seed=N + K + D)
+    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), f"diag N={N} K={K} D={D}")
+
+
+def test_equal_variances_match_isotropic(gpu_device):
+    inp = data.iso_clustered(3000, 50, 40, seed=12)
+    dev = gpu_device
+    X, mu, lss, lpi = (inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi"))
+    a = flash_gmm_estep(X, mu, lss, lpi)
+    b = flash_gmm_estep_diag(X, mu, lss[:, None].expand(50, 40).contiguous(), lpi)
+    torch.cuda.synchronize()
+    assert (a[0] - b[0]).abs().max().item() <= 2 * LOGZ_ATOL
+    torch.testing.assert_close(b[1], a[1], rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(b[2], a[2], rtol=1e-4, atol=1e-4 * float(a[2].abs().max()))
+    torch.testing.assert_close(b[3].sum(1), a[3], rtol=1e-4, atol=1e-3)
+
+
+def test_accumulate_over_chunks(gpu_device):
+    inp = data.diag_clustered(7000, 100, 48, seed=13)
+    dev = gpu_device
+    args = [inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
+    ref = flash_gmm_estep_diag(*args)
+    nk = torch.zeros(100, device=dev)
+    ma = torch.zeros(100, 48, device=dev)
+    sg = torch.zeros(100, 48, device=dev)
+    for n0 in range(0, 7000, 3000):
+        diag_estep_into(args[0][n0:n0 + 3000], *args[1:], None, nk, ma, sg, accumulate=True)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(nk, ref[1], rtol=1e-5, atol=1e-4)
+    torch.testing.assert_close(ma, ref[2], rtol=1e-5, atol=1e-5 * float(ref[2].abs().max()))
+    torch.testing.assert_close(sg, ref[3], rtol=1e-5, atol=1e-5 * float(ref[3].abs().max()))
+
+
+def test_diag_shape_mid_size(gpu_device):
+    """K=1024, D=96 axis-aligned clusters at N=32,768 against the float64 oracle."""
+    inp = data.diag_clustered(32768, 1024, 96, seed=2)
+    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "diag K1024 D96 N32768")
+
+
+def test_diag_full_size_properties(gpu_device):
+    """N=1M, K=1024, D=96: every row counted once, sampled rows' logZ exact."""
+    dev = gpu_device
+    inp = data.diag_clustered(1_000_000, 1024, 96, seed=2, device=dev)
+    logZ, Nk, mu_acc, sig = flash_gmm_estep_diag(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+    torch.cuda.synchronize()
+    N = 1_000_000
+    assert abs(Nk.double().sum().item() - N) <= 1e-5 * N
+    torch.testing.assert_close(mu_acc.double().sum(0), inp["X"].double().sum(0), rtol=0,
+                               atol=1e-5 * float(mu_acc.abs().sum(0).max()))
+    assert torch.all(sig >= -1e-3)
+    rows = torch.randint(0, N, (2048,), generator=torch.Generator().manual_seed(1))
+    sub = {k: v.cpu() for k, v in inp.items()}
+    ref = O.estep_diag(sub["X"][rows], sub["mu"], sub["log_sigma_sq"], sub["log_pi"])[0]
+    assert (logZ.cpu()[rows].double() - ref).abs().max().item() <= LOGZ_ATOL
+
+
+def test_rejects_bad_variance_shape(gpu_device):
+    inp = data.diag_clustered(10, 4, 8, seed=14)
+    X, mu, lss, lpi = (inp[k].to(gpu_device) for k in ("X", "mu", "log_sigma_sq", "log_pi"))
+    with pytest.raises(AssertionError):
+        flash_gmm_estep_diag(X, mu, lss[:, :4], lpi)
