@@ -1,0 +1,546 @@
+// Full-covariance GMM E-step for gfx950 (1 <= D <= 64).
+//
+// Math (reference: flash_gmm_full_h100.py:289-296 constants, :103-130 pass 1,
+// :171-228 pass 2), with L_k lower-triangular, L_k L_k^T = Sigma_k^-1, in log2 units:
+//   b_k   = L_k^T mu_k
+//   c_k   = (lpi_k + sum_d log(|L_k,dd| + 1e-30) - 0.5*D*log(2pi)) * log2(e)
+//   v     = L_k^T x_n - b_k,   maha_nk = ||v||^2,   ll2_nk = c_k - 0.5*log2(e)*maha_nk
+//   r_nk  = 2^(ll2_nk - logZ2_n)
+//   Nk_k = sum_n r_nk;  mu_acc_k = sum_n r_nk x_n;  sig_outer_k = sum_n r_nk x_n x_n^T
+//
+// The whitening V^T = L_k^T X^T is a 32x32x2 fp32 MFMA contraction (A = L_k^T laid
+// out in operand order by the prologue, B = X), evaluated with the chunked fp64
+// form of cross_tile() so maha keeps ~1e-5 accuracy; each lane owns one row and 16
+// whitened coordinates per 32-row block of V^T, so maha is an in-lane fp64 sum plus
+// one cross-half exchange.
+//
+// Pass 2 runs 8 waves per workgroup (4 components x 2 row groups).  After r is
+// formed for a 32-row tile it is exchanged through LDS, and sig_outer accumulates as
+// sum_rows (r x)(x^T) on MFMA with the r-scaled rows as the A operand.  Only the
+// upper 32x32 blocks (d1 block <= d2 block) are accumulated; the finish mirrors
+// them.  mu_acc is the running sum of the same r-scaled operands.
+
+#include "fgmm_common.hpp"
+
+#include <math.h>
+
+namespace fgmm {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kCUs = 256;
+constexpr int kAccWaves = 8;
+constexpr int kAccThreads = 64 * kAccWaves;
+constexpr int kCompsPerWG = 4;
+constexpr int kRowGroups = 2;
+
+struct FullPlan {
+  int64_t N, K, D;
+  int DP;       // D padded to 32
+  int NMB;      // 32-row blocks of V^T (DP / 32)
+  int NSB;      // upper 32x32 blocks of sig_outer: NMB*(NMB+1)/2
+  int KP;       // K padded to kCompsPerWG
+  int ncg, nslab, npart;
+  int64_t rows_per_slab;
+  size_t off_lsw, off_bsw, off_ck, off_rowstat, off_part_sig, off_part_mu, off_part_nk, total;
+};
+
+FullPlan make_plan(int64_t N, int64_t K, int64_t D) {
+  FullPlan p{};
+  p.N = N; p.K = K; p.D = D;
+  p.DP = (int)round_up(D < 1 ? 1 : D, 32);
+  p.NMB = p.DP / 32;
+  p.NSB = p.NMB * (p.NMB + 1) / 2;
+  p.KP = (int)round_up(K, kCompsPerWG);
+  p.ncg = p.KP / kCompsPerWG;
+  const int64_t tile_rows = 32 * kRowGroups;
+  if (N > 0 && p.ncg > 0) {
+    int64_t want = (int64_t)kCUs / p.ncg;
+    if (want >= 8) want = (want / 8) * 8;
+    if (want < 1) want = 1;
+    const int64_t max_slabs = cdiv(N, tile_rows);
+    if (want > max_slabs) want = max_slabs;
+    p.rows_per_slab = round_up(cdiv(N, want), tile_rows);
+    p.nslab = (int)cdiv(N, p.rows_per_slab);
+  } else {
+    p.rows_per_slab = tile_rows;
+    p.nslab = 0;
+  }
+  p.npart = p.nslab * kRowGroups;
+  size_t off = 0;
+  p.off_lsw = off;      off = align256(off + (size_t)p.KP * p.DP * p.DP * sizeof(float));
+  p.off_bsw = off;      off = align256(off + (size_t)p.KP * p.DP * sizeof(double));
+  p.off_ck = off;       off = align256(off + (size_t)p.KP * sizeof(double));
+  p.off_rowstat = off;  off = align256(off + (size_t)(N > 0 ? N : 0) * sizeof(double));
+  p.off_part_sig = off; off = align256(off + (size_t)p.npart * p.KP * p.NSB * 1024 * sizeof(float));
+  p.off_part_mu = off;  off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
+  p.off_part_nk = off;  off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
+  p.total = off;
+  return p;
+}
+
+// ---------------------------------------------------------------------------
+// Prologue, one 64-thread block per component:
+//   lsw[k][mb][m][lane] (f32x4) = L[k][8m + 4g + e][32 mb + c], e = 0..3
+//   bsw[k][mb][g][i]    (f64)   = b[k][32 mb + acc_row(i, g)]
+//   ck[k]               (f64)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void full_prep(const float* __restrict__ mu, int64_t ldmu,
+                                                const float* __restrict__ L, int64_t K, int D, int DP,
+                                                const float* __restrict__ lpi, f32x4* __restrict__ lsw,
+                                                double* __restrict__ bsw, double* __restrict__ ck) {
+  __shared__ double sb[64];
+  const int64_t k = blockIdx.x;
+  const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  const bool valid = k < K;
+  const float* Lk = L + k * (int64_t)D * D;
+  // b_j = sum_i L[i][j] mu_i  (one j per lane)
+  if (lane < DP) {
+    double b = 0.0;
+    if (valid && lane < D)
+      for (int i = 0; i < D; ++i) b = fma((double)Lk[(int64_t)i * D + lane], (double)mu[k * ldmu + i], b);
+    sb[lane] = b;
+  }
+  if (lane == 0) {
+    double c0 = -INFINITY;
+    if (valid) {
+      double ld = 0.0;
+      for (int d = 0; d < D; ++d) ld += log(fabs((double)Lk[(int64_t)d * D + d]) + 1e-30);
+      c0 = ((double)lpi[k] + ld - 0.5 * (double)D * kLog2Pi) * kLog2e;
+    }
+    ck[k] = c0;
+  }
+  const int NMB = DP / 32, NM = DP / 8;
+  for (int mb = 0; mb < NMB; ++mb) {
+    const int j = 32 * mb + c;
+    for (int m = 0; m < NM; ++m) {
+      f32x4 v = zero4();
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 8 * m + 4 * g + e;
+        v[e] = (valid && i < D && j < D) ? Lk[(int64_t)i * D + j] : 0.0f;
+      }
+      lsw[((k * NMB + mb) * NM + m) * 64 + lane] = v;
+    }
+  }
+  __syncthreads();
+  for (int mb = 0; mb < NMB; ++mb) {
+    if (lane < 32) {
+      const int gg = lane >> 4, i = lane & 15;
+      bsw[(k * NMB + mb) * 32 + gg * 16 + i] = sb[32 * mb + acc_row(i, gg)];
+    }
+  }
+}
+
+// maha for this lane's row against one component whose operand / centre blocks are
+// at Lc (LDS, [mb][m][lane] f32x4) and bc ([mb][g][i] f64), with B operand loadB.
+template <int NMB, int NM, typename LB>
+__device__ __forceinline__ double maha_one(const f32x4* Lc, const double* bc, int lane, int g, LB loadB) {
+  double q = 0.0;
+#pragma unroll
+  for (int mb = 0; mb < NMB; ++mb) {
+    double v[16];
+    const f32x4* la = Lc + mb * NM * 64 + lane;
+    cross_tile<NM>(v, [&](int m) { return la[m * 64]; }, loadB);
+    const double* bb = bc + mb * 32 + g * 16;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const double t = v[i] - bb[i];
+      q = fma(t, t, q);
+    }
+  }
+  return q + __shfl_xor(q, 32);
+}
+
+// ---------------------------------------------------------------------------
+// Pass 1: online log-sum-exp over components, one component's L^T per LDS stage.
+// ---------------------------------------------------------------------------
+template <int DP>
+constexpr size_t lse_lds_bytes() {
+  return (size_t)2 * DP * DP * sizeof(float) + (size_t)2 * (DP + 8) * sizeof(double);
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
+void full_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+              const f32x4* __restrict__ lsw, const double* __restrict__ bsw,
+              const double* __restrict__ ck, int K, float* __restrict__ logZ,
+              double* __restrict__ rowstat) {
+  constexpr int NMB = DP / 32, NM = DP / 8;
+  constexpr int BLK = NMB * NM * 64;              // float4 per component
+  constexpr int LPT = BLK / kThreads;
+  constexpr int BW = DP + 8;                      // doubles per component stage (b + c)
+  static_assert(BLK % kThreads == 0, "even split");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  f32x4* l_l = reinterpret_cast<f32x4*>(lds_raw);                                // [2][BLK]
+  double* b_l = reinterpret_cast<double*>(lds_raw + 2 * BLK * sizeof(f32x4));    // [2][BW]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t row = ((int64_t)blockIdx.x * kWaves + wave) * 32 + c;
+  const bool valid = row < N;
+
+  f32x4 st[LPT];
+  double bst = 0.0;
+  auto fetch = [&](int k) {
+    const f32x4* src = lsw + (int64_t)k * BLK;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) st[q] = src[q * kThreads + tid];
+    if (tid < DP) bst = bsw[(int64_t)k * DP + tid];
+    else if (tid == DP) bst = ck[k];
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) l_l[buf * BLK + q * kThreads + tid] = st[q];
+    if (tid <= DP) b_l[buf * BW + tid] = bst;
+  };
+  fetch(0);
+  f32x4 xb[NM];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) xb[m] = load_row4(X, ldx, row, 8 * m + 4 * g, D, valid);
+  commit(0);
+  __syncthreads();
+
+  const double hl = 0.5 * kLog2e;
+  double mx = -INFINITY;
+  float sm = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const int buf = k & 1;
+    const bool more = k + 1 < K;
+    if (more) fetch(k + 1);
+    const double maha = maha_one<NMB, NM>(l_l + buf * BLK, b_l + buf * BW, lane, g,
+                                          [&](int m) { return xb[m]; });
+    const double ll = b_l[buf * BW + DP] - hl * maha;
+    const double mn = fmax(mx, ll);
+    const double ms = (mn == -INFINITY) ? 0.0 : mn;
+    sm = sm * fast_exp2((float)(mx - ms)) + fast_exp2((float)(ll - ms));
+    mx = mn;
+    if (more) commit(buf ^ 1);
+    __syncthreads();
+  }
+  const double lz2 = mx + (double)log2f(sm);
+  if (valid && g == 0) {
+    rowstat[row] = lz2;
+    if (logZ) logZ[row] = (float)(lz2 * kLn2);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2.
+// ---------------------------------------------------------------------------
+template <int DP>
+constexpr size_t accum_lds_bytes() {
+  constexpr int TR = 32 * kRowGroups;
+  return (size_t)kCompsPerWG * DP * DP * sizeof(float)          // L^T operands
+         + (size_t)kCompsPerWG * (DP + 8) * sizeof(double)      // b, c
+         + (size_t)2 * TR * (DP + 4) * sizeof(float)            // X tiles
+         + (size_t)2 * TR * sizeof(double)                      // logZ2
+         + (size_t)kAccWaves * 32 * sizeof(float);              // r exchange
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
+void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                const f32x4* __restrict__ lsw, const double* __restrict__ bsw,
+                const double* __restrict__ ck, int K, int KP, const double* __restrict__ rowstat,
+                int nslab, int64_t rows_per_slab, float* __restrict__ part_sig,
+                float* __restrict__ part_mu, float* __restrict__ part_nk) {
+  constexpr int NMB = DP / 32, NM = DP / 8, NSB = NMB * (NMB + 1) / 2;
+  constexpr int RS = DP + 4, V4 = DP / 4;
+  constexpr int BLK = NMB * NM * 64;
+  constexpr int BW = DP + 8;
+  constexpr int TR = 32 * kRowGroups;
+  constexpr int LPT = (TR * V4) / kAccThreads;
+  constexpr int MPT = (kCompsPerWG * BLK) / kAccThreads;
+  static_assert((TR * V4) % kAccThreads == 0 && (kCompsPerWG * BLK) % kAccThreads == 0, "even split");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  unsigned char* p = lds_raw;
+  f32x4* l_l = reinterpret_cast<f32x4*>(p);   p += kCompsPerWG * BLK * sizeof(f32x4);
+  double* b_l = reinterpret_cast<double*>(p); p += kCompsPerWG * BW * sizeof(double);
+  float* xs = reinterpret_cast<float*>(p);    p += 2 * TR * RS * sizeof(float);
+  double* rs = reinterpret_cast<double*>(p);  p += 2 * TR * sizeof(double);
+  float* r_l = reinterpret_cast<float*>(p);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int cw = wave & 3, rg = wave >> 2;
+  const int slab = blockIdx.x % nslab;
+  const int cg = blockIdx.x / nslab;
+  const int k = cg * kCompsPerWG + cw;
+  const bool active = k < K;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
+
+  // Operands of the workgroup's components -> LDS (lsw/bsw/ck are padded to KP).
+#pragma unroll
+  for (int q = 0; q < MPT; ++q) {
+    const int idx = q * kAccThreads + tid;
+    l_l[idx] = lsw[(int64_t)cg * kCompsPerWG * BLK + idx];
+  }
+  for (int idx = tid; idx < kCompsPerWG * BW; idx += kAccThreads) {
+    const int cc = idx / BW, e = idx % BW;
+    const int64_t kk = (int64_t)cg * kCompsPerWG + cc;
+    b_l[idx] = e < DP ? bsw[kk * DP + e] : (e == DP ? ck[kk] : 0.0);
+  }
+
+  f32x16 acc[NSB];
+#pragma unroll
+  for (int s = 0; s < NSB; ++s) acc[s] = zero16();
+  float mua[NMB];
+#pragma unroll
+  for (int mb = 0; mb < NMB; ++mb) mua[mb] = 0.0f;
+  float nk = 0.0f;
+
+  f32x4 stage[LPT];
+  double rstage = INFINITY;
+  auto fetch = [&](int t) {
+    const int64_t row0 = r_begin + (int64_t)t * TR;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      const int rr = idx / V4, c4 = idx % V4;
+      const int64_t row = row0 + rr;
+      stage[q] = load_row4(X, ldx, row, c4 * 4, D, row < r_end);
+    }
+    if (tid < TR) {
+      const int64_t row = row0 + tid;
+      rstage = (row < r_end) ? rowstat[row] : INFINITY;
+    }
+  };
+  auto commit = [&](int buf) {
+    float* dst = xs + buf * TR * RS;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      const int rr = idx / V4, c4 = idx % V4;
+      *reinterpret_cast<f32x4*>(dst + rr * RS + c4 * 4) = stage[q];
+    }
+    if (tid < TR) rs[buf * TR + tid] = rstage;
+  };
+
+  if (ntiles > 0) {
+    fetch(0);
+    commit(0);
+  }
+  __syncthreads();
+
+  const double hl = 0.5 * kLog2e;
+  const f32x4* Lc = l_l + cw * BLK;
+  const double* bc = b_l + cw * BW;
+  float* rx = r_l + wave * 32;
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    const float* xt = xs + buf * TR * RS + rg * 32 * RS;
+    const double* rt = rs + buf * TR + rg * 32;
+    if (active) {
+      // r for this lane's row c (both half-waves hold it after the exchange in maha_one).
+      const double maha = maha_one<NMB, NM>(
+          Lc, bc, lane, g, [&](int m) { return *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * m + 4 * g); });
+      const float rv = fast_exp2((float)((bc[DP] - rt[c]) - hl * maha));
+      if (g == 0) {
+        nk += rv;
+        rx[c] = rv;
+      }
+    }
+    if (more) fetch(t + 1);
+    __builtin_amdgcn_wave_barrier();
+    if (active) {
+      // sig_outer[d1][d2] += sum_rows (r x_d1) x_d2 over the tile's 32 rows; row of step s
+      // for half g is acc_row(s, g), matching the A-operand k index of each half-wave.
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const int row = acc_row(s, g);
+        const float rr = rx[row];
+        float xv[NMB], av[NMB];
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb) {
+          xv[mb] = xt[row * RS + 32 * mb + c];
+          av[mb] = rr * xv[mb];
+          mua[mb] += av[mb];
+        }
+        int sb = 0;
+#pragma unroll
+        for (int m1 = 0; m1 < NMB; ++m1) {
+#pragma unroll
+          for (int m2 = m1; m2 < NMB; ++m2) {
+            acc[sb] = mfma32(av[m1], xv[m2], acc[sb]);
+            ++sb;
+          }
+        }
+      }
+    }
+    if (more) commit(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (active) {
+    const int64_t pbase = ((int64_t)slab * kRowGroups + rg) * KP + k;
+    float* ps = part_sig + pbase * NSB * 1024;
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) ps[sb * 1024 + acc_row(i, g) * 32 + c] = acc[sb][i];
+    }
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+      const float v = mua[mb] + __shfl_xor(mua[mb], 32);
+      if (g == 0) part_mu[pbase * DP + 32 * mb + c] = v;
+    }
+    float nks = nk;
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) nks += __shfl_xor(nks, o);
+    if (lane == 0) part_nk[pbase] = nks;
+  }
+}
+
+// Finish: one thread per (k, d1, d2) of sig_outer plus (k, d) of mu_acc and k of Nk.
+__global__ __launch_bounds__(256) void full_reduce(const float* __restrict__ part_sig,
+                                                   const float* __restrict__ part_mu,
+                                                   const float* __restrict__ part_nk, int npart, int KP,
+                                                   int DP, int NMB, int64_t K, int D,
+                                                   float* __restrict__ Nk, float* __restrict__ mu_acc,
+                                                   float* __restrict__ sig_outer, int accumulate) {
+  const int NSB = NMB * (NMB + 1) / 2;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nsig = K * D * D;
+  if (idx < nsig) {
+    const int64_t k = idx / ((int64_t)D * D);
+    const int rem = (int)(idx % ((int64_t)D * D));
+    int d1 = rem / D, d2 = rem % D;
+    if (d1 > d2) { const int t = d1; d1 = d2; d2 = t; }    // upper blocks only; mirror
+    int b1 = d1 / 32, b2 = d2 / 32;
+    if (b1 > b2) { const int t = b1; b1 = b2; b2 = t; }
+    // upper-block index sb for (b1 <= b2): sum_{m<b1}(NMB-m) + (b2-b1)
+    const int sb = b1 * NMB - b1 * (b1 - 1) / 2 + (b2 - b1);
+    // within the block, element (d1 mod 32, d2 mod 32) with d1 in block b1 ... when b1 == b2
+    // the block is symmetric only in sum, so read (d1%32, d2%32) directly.
+    const int e1 = (d1 / 32 == b1) ? d1 % 32 : d2 % 32;
+    const int e2 = (d1 / 32 == b1) ? d2 % 32 : d1 % 32;
+    double s = 0.0;
+    for (int p = 0; p < npart; ++p)
+      s += (double)part_sig[(((int64_t)p * KP + k) * NSB + sb) * 1024 + e1 * 32 + e2];
+    float* o = sig_outer + idx;
+    *o = accumulate ? (float)((double)*o + s) : (float)s;
+    return;
+  }
+  const int64_t j = idx - nsig;
+  if (j < K * D) {
+    const int64_t k = j / D;
+    const int d = (int)(j % D);
+    double s = 0.0;
+    for (int p = 0; p < npart; ++p) s += (double)part_mu[((int64_t)p * KP + k) * DP + d];
+    float* o = mu_acc + j;
+    *o = accumulate ? (float)((double)*o + s) : (float)s;
+    return;
+  }
+  const int64_t kk = j - K * D;
+  if (kk < K) {
+    double s = 0.0;
+    for (int p = 0; p < npart; ++p) s += (double)part_nk[(int64_t)p * KP + kk];
+    Nk[kk] = accumulate ? (float)((double)Nk[kk] + s) : (float)s;
+  }
+}
+
+__global__ __launch_bounds__(256) void full_fill(float* __restrict__ p, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+template <int DP>
+hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
+                         float* logZ, bool run1, bool run2, hipStream_t stream) {
+  const f32x4* lsw = reinterpret_cast<const f32x4*>(ws + pl.off_lsw);
+  const double* bsw = reinterpret_cast<const double*>(ws + pl.off_bsw);
+  const double* ck = reinterpret_cast<const double*>(ws + pl.off_ck);
+  double* rowstat = reinterpret_cast<double*>(ws + pl.off_rowstat);
+  if (run1) {
+    constexpr size_t lds1 = lse_lds_bytes<DP>();
+    hipLaunchKernelGGL(full_lse<DP>, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
+                       stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, logZ, rowstat);
+  }
+  if (!run2) return hipGetLastError();
+  constexpr size_t lds2 = accum_lds_bytes<DP>();
+  if (lds2 > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&full_accum<DP>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(full_accum<DP>, dim3((unsigned)(pl.nslab * pl.ncg)), dim3(kAccThreads), lds2,
+                     stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, rowstat, pl.nslab,
+                     pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_sig),
+                     reinterpret_cast<float*>(ws + pl.off_part_mu),
+                     reinterpret_cast<float*>(ws + pl.off_part_nk));
+  return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace fgmm
+
+using namespace fgmm;
+
+extern "C" size_t fgmm_full_workspace_bytes(int64_t N, int64_t K, int64_t D) {
+  if (N < 0 || K < 0 || D < 1) return 0;
+  return make_plan(N, K, D).total;
+}
+
+extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
+                                   int64_t ldmu, int64_t K, const float* prec_chol, const float* log_pi,
+                                   float* logZ, float* Nk, float* mu_acc, float* sig_outer,
+                                   void* workspace, size_t workspace_bytes, unsigned flags,
+                                   void* stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const bool want_logz = !(flags & FGMM_FLAG_NO_LOGZ);
+  const bool accumulate = (flags & FGMM_FLAG_ACCUMULATE) != 0;
+  if (N < 0 || K < 0 || D < 1) return FGMM_ERR_INVALID_ARG;
+  if (N > 0 && (X == nullptr || ldx < round_up(D, 4) || (ldx % 4) != 0 ||
+                (reinterpret_cast<uintptr_t>(X) & 15) != 0))
+    return FGMM_ERR_INVALID_ARG;
+  if (N > 0 && want_logz && logZ == nullptr) return FGMM_ERR_INVALID_ARG;
+  if (K > 0 && (mu == nullptr || ldmu < D || prec_chol == nullptr || log_pi == nullptr ||
+                Nk == nullptr || mu_acc == nullptr || sig_outer == nullptr))
+    return FGMM_ERR_INVALID_ARG;
+  if (D > 64) return FGMM_ERR_UNSUPPORTED;
+  if (N > (int64_t)1 << 40 || K > (int64_t)1 << 20) return FGMM_ERR_UNSUPPORTED;
+  const FullPlan pl = make_plan(N, K, D);
+  if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
+  if (!want_logz) logZ = nullptr;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  const bool sel1 = (flags & FGMM_FLAG_PHASE1) != 0, sel2 = (flags & FGMM_FLAG_PHASE2) != 0;
+  const bool run1 = sel1 || !sel2, run2 = sel2 || !sel1;
+
+  if (K == 0) {
+    if (N > 0 && logZ)
+      hipLaunchKernelGGL(full_fill, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, stream, logZ, N,
+                         -INFINITY);
+    return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+  }
+  if (run1)
+    hipLaunchKernelGGL(full_prep, dim3((unsigned)pl.KP), dim3(64), 0, stream, mu, ldmu, prec_chol, K,
+                       (int)D, pl.DP, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_lsw),
+                       reinterpret_cast<double*>(ws + pl.off_bsw),
+                       reinterpret_cast<double*>(ws + pl.off_ck));
+  if (N > 0) {
+    hipError_t e = hipSuccess;
+    switch (pl.DP) {
+      case 32: e = launch_passes<32>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      default: return FGMM_ERR_UNSUPPORTED;
+    }
+    if (e != hipSuccess) return FGMM_ERR_HIP;
+  }
+  if (!run2) return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+  const int64_t nthreads = K * D * D + K * D + K;
+  hipLaunchKernelGGL(full_reduce, dim3((unsigned)cdiv(nthreads, 256)), dim3(256), 0, stream,
+                     reinterpret_cast<const float*>(ws + pl.off_part_sig),
+                     reinterpret_cast<const float*>(ws + pl.off_part_mu),
+                     reinterpret_cast<const float*>(ws + pl.off_part_nk), pl.npart, pl.KP, pl.DP,
+                     pl.NMB, K, (int)D, Nk, mu_acc, sig_outer, accumulate ? 1 : 0);
+  return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+}

@@ -104,6 +104,25 @@ int fgmm_diag_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
                         void *workspace, size_t workspace_bytes,
                         unsigned flags, void *stream);
 
+/* ------------------------------------------------------------------------ */
+/* Full-covariance E-step.                                                   */
+/* Replaces flash_gmm_estep_full(X, mu, prec_chol, log_pi) at                */
+/* flash_gmm_full_h100.py:235-336.  prec_chol is K x D x D contiguous, each   */
+/* L_k lower-triangular with L_k L_k^T = Sigma_k^-1; sig_outer is K x D x D:  */
+/*   ll_nk = log_pi_k + sum_d log(|L_k,dd| + 1e-30) - 0.5 D log(2 pi)         */
+/*           - 0.5 ||L_k^T (x_n - mu_k)||^2                                   */
+/*   sig_outer_k = sum_n r_nk x_n x_n^T   (uncentred second moment)           */
+/* Supports 1 <= D <= 64.                                                     */
+/* ------------------------------------------------------------------------ */
+size_t fgmm_full_workspace_bytes(int64_t N, int64_t K, int64_t D);
+
+int fgmm_full_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
+                        const float *mu, int64_t ldmu, int64_t K,
+                        const float *prec_chol, const float *log_pi,
+                        float *logZ, float *Nk, float *mu_acc, float *sig_outer,
+                        void *workspace, size_t workspace_bytes,
+                        unsigned flags, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,111 @@
+"""GPU parity of the full-covariance E-step against the CPU oracle (tolerances in parity.py;
+sig_outer is checked like sig_acc, element-wise with the 1e-6*max floor)."""
+
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from flash_gmm import data, flash_gmm_estep_diag, flash_gmm_estep_full, full_estep_into
+from oracle import gmm_oracle as O
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+import make_golden  # noqa: E402
+from parity import LOGZ_ATOL, assert_close_stats  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+KEYS = ("X", "mu", "prec_chol", "log_pi")
+
+
+def run_gpu(inp, dev):
+    out = flash_gmm_estep_full(*[inp[k].to(dev) for k in KEYS])
+    torch.cuda.synchronize()
+    return out
+
+
+def oracle(inp):
+    return O.estep_full(*[inp[k] for k in KEYS])
+
+
+def test_golden_vectors(gpu_device):
+    name = "full_n2000_k12_d16"
+    inp, kind = make_golden.make_inputs(name)
+    fx = np.load(os.path.join(os.path.dirname(make_golden.__file__), name + ".npz"))
+    assert str(fx["sha256"]) == make_golden.input_digest(inp)
+    assert_close_stats(run_gpu(inp, gpu_device), (fx["logZ"], fx["Nk"], fx["mu_acc"], fx["sig"]), name)
+
+
+@pytest.mark.parametrize("N,K,D", [(1, 1, 1), (33, 5, 3), (500, 12, 16), (300, 7, 64),
+                                   (1000, 33, 40), (129, 4, 32), (2000, 9, 63)])
+def test_edge_shapes(N, K, D, gpu_device):
+    inp = data.full_clustered(N, K, D, seed=N + K + D)
+    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), f"full N={N} K={K} D={D}")
+
+
+def test_diagonal_factor_matches_diag_entry(gpu_device):
+    inp = data.diag_clustered(3000, 20, 24, seed=15)
+    dev = gpu_device
+    X, mu, lss, lpi = (inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi"))
+    L = torch.diag_embed(torch.exp(-0.5 * lss.double()).float())
+    a = flash_gmm_estep_diag(X, mu, lss, lpi)
+    b = flash_gmm_estep_full(X, mu, L, lpi)
+    torch.cuda.synchronize()
+    assert (a[0] - b[0]).abs().max().item() <= 2 * LOGZ_ATOL
+    torch.testing.assert_close(b[1], a[1], rtol=2e-4, atol=1e-4)
+    torch.testing.assert_close(b[2], a[2], rtol=2e-4, atol=2e-4 * float(a[2].abs().max()))
+    # diag sig_acc from sig_outer: diag(S) - 2 mu mu_acc + mu^2 Nk
+    s = b[3].diagonal(dim1=1, dim2=2) - 2 * mu * b[2] + mu * mu * b[1][:, None]
+    torch.testing.assert_close(s, a[3], rtol=1e-3, atol=1e-3 * float(a[3].abs().max()))
+
+
+def test_accumulate_over_chunks(gpu_device):
+    inp = data.full_clustered(5000, 16, 32, seed=16)
+    dev = gpu_device
+    args = [inp[k].to(dev) for k in KEYS]
+    ref = flash_gmm_estep_full(*args)
+    nk = torch.zeros(16, device=dev)
+    ma = torch.zeros(16, 32, device=dev)
+    so = torch.zeros(16, 32, 32, device=dev)
+    for n0 in range(0, 5000, 1700):
+        full_estep_into(args[0][n0:n0 + 1700], *args[1:], None, nk, ma, so, accumulate=True)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(nk, ref[1], rtol=1e-5, atol=1e-4)
+    torch.testing.assert_close(ma, ref[2], rtol=1e-5, atol=1e-5 * float(ref[2].abs().max()))
+    torch.testing.assert_close(so, ref[3], rtol=1e-5, atol=1e-5 * float(ref[3].abs().max()))
+
+
+def test_full_shape_mid_size(gpu_device):
+    """K=256, D=64 at N=8,192 against the float64 oracle."""
+    inp = data.full_clustered(8192, 256, 64, seed=3)
+    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "full K256 D64 N8192")
+
+
+def test_full_size_properties(gpu_device):
+    """N=250K, K=256, D=64: sum_k Nk = N, sum_k mu_acc = sum x, sum_k sig_outer = X^T X."""
+    dev = gpu_device
+    inp = data.full_clustered(250_000, 256, 64, seed=3, device=dev)
+    logZ, Nk, mu_acc, so = flash_gmm_estep_full(*[inp[k] for k in KEYS])
+    torch.cuda.synchronize()
+    N = 250_000
+    X = inp["X"].double()
+    assert abs(Nk.double().sum().item() - N) <= 1e-5 * N
+    torch.testing.assert_close(mu_acc.double().sum(0), X.sum(0), rtol=0,
+                               atol=1e-5 * float(mu_acc.abs().sum(0).max()))
+    xtx = X.T @ X
+    torch.testing.assert_close(so.double().sum(0), xtx, rtol=0, atol=1e-5 * float(xtx.abs().max()))
+    assert torch.all(so.diagonal(dim1=1, dim2=2) >= 0)
+    rows = torch.randint(0, N, (1024,), generator=torch.Generator().manual_seed(2))
+    sub = {k: v.cpu() for k, v in inp.items()}
+    ref = O.estep_full(sub["X"][rows], sub["mu"], sub["prec_chol"], sub["log_pi"])[0]
+    assert (logZ.cpu()[rows].double() - ref).abs().max().item() <= LOGZ_ATOL
+
+
+def test_rejects_bad_factor_shape(gpu_device):
+    inp = data.full_clustered(10, 3, 8, seed=17)
+    X, mu, L, lpi = (inp[k].to(gpu_device) for k in KEYS)
+    with pytest.raises(AssertionError):
+        flash_gmm_estep_full(X, mu, L[:, :4, :4], lpi)
