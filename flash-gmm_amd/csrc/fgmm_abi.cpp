@@ -10,6 +10,7 @@ extern "C" const char* fgmm_strerror(int status) {
     case FGMM_ERR_UNSUPPORTED: return "unsupported shape (outside the compiled range)";
     case FGMM_ERR_WORKSPACE: return "workspace smaller than the *_workspace_bytes() query";
     case FGMM_ERR_HIP: return "HIP runtime error or kernel launch failure";
+    case FGMM_ERR_SOURCE: return "the host row source returned an error";
     default: return "unknown status";
   }
 }

@@ -1,0 +1,274 @@
+// EM driver pieces for the isotropic model: the GPU M-step, a deterministic
+// sum of logZ, and the streaming E-step driver for data sets larger than HBM.
+//
+// M-step (README.md:59-61, :99-100):  pi = Nk / N,  mu = mu_acc / Nk,
+// sigma^2 = sig_acc / (D Nk).  sig_acc is accumulated about the previous means, so
+// that estimate exceeds the sample variance by ||mu_new - mu_old||^2 / D; the
+// FGMM_MSTEP_EXACT_VARIANCE flag removes that term.  Components with Nk = 0 keep
+// their mean and variance and get log pi = -inf.
+//
+// Streaming (README.md:81-103, where each chunk is a synchronous pageable
+// chunk.cuda()): rows come from a host row source into two pinned buffers; while
+// the host fills one, the other is copied to the device on a copy stream and the
+// previous chunk's E-step runs on a compute stream, with events ordering buffer
+// reuse.  The E-step accumulates Nk / mu_acc / sig_acc across chunks and the
+// M-step runs on the device after the last chunk of each iteration.
+
+#include "fgmm_common.hpp"
+
+#include <math.h>
+
+#include <chrono>
+#include <vector>
+
+namespace fgmm {
+namespace {
+
+__global__ __launch_bounds__(256) void iso_mstep_kernel(const float* __restrict__ Nk,
+                                                        const float* __restrict__ mu_acc,
+                                                        const float* __restrict__ sig_acc, double N,
+                                                        int D, double var_floor, int exact,
+                                                        float* __restrict__ mu, int64_t ldmu,
+                                                        float* __restrict__ lss, float* __restrict__ lpi) {
+  __shared__ double red[256];
+  const int64_t k = blockIdx.x;
+  const int t = threadIdx.x;
+  const double nk = (double)Nk[k];
+  if (!(nk > 0.0)) {
+    if (t == 0) lpi[k] = -INFINITY;
+    return;
+  }
+  // Shift of the mean, summed over dimensions (old means read before any write).
+  double sh = 0.0;
+  for (int d = t; d < D; d += blockDim.x) {
+    const double mn = (double)mu_acc[k * D + d] / nk;
+    const double dm = mn - (double)mu[k * ldmu + d];
+    sh = fma(dm, dm, sh);
+  }
+  red[t] = sh;
+  __syncthreads();
+  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+    if (t < s) red[t] += red[t + s];
+    __syncthreads();
+  }
+  for (int d = t; d < D; d += blockDim.x) mu[k * ldmu + d] = (float)((double)mu_acc[k * D + d] / nk);
+  if (t == 0) {
+    double s2 = (double)sig_acc[k] / ((double)D * nk);
+    if (exact) s2 -= red[0] / (double)D;
+    if (s2 < var_floor) s2 = var_floor;
+    lss[k] = (float)log(s2);
+    lpi[k] = (float)log(nk / N);
+  }
+}
+
+// Deterministic sum of n floats into *acc (fp64): fixed 1024-element blocks, then
+// the block sums in order by one thread.
+__global__ __launch_bounds__(256) void sum_blocks(const float* __restrict__ x, int64_t n,
+                                                  double* __restrict__ part) {
+  __shared__ double red[256];
+  const int64_t base = (int64_t)blockIdx.x * 1024;
+  double s = 0.0;
+  for (int i = threadIdx.x; i < 1024; i += 256) {
+    const int64_t j = base + i;
+    if (j < n) s += (double)x[j];
+  }
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (threadIdx.x < st) red[threadIdx.x] += red[threadIdx.x + st];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[blockIdx.x] = red[0];
+}
+
+__global__ void sum_parts(const double* __restrict__ part, int64_t nparts, double* __restrict__ acc) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  double s = 0.0;
+  for (int64_t i = 0; i < nparts; ++i) s += part[i];
+  *acc += s;
+}
+
+__global__ __launch_bounds__(256) void fill_f32(float* __restrict__ p, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+__global__ void fill_f64_one(double* p, double v) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) *p = v;
+}
+
+double ms_since(std::chrono::steady_clock::time_point t0) {
+  return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
+// Owner of every resource the streaming driver creates; releases them in any exit path.
+struct StreamRes {
+  float* pinned[2] = {nullptr, nullptr};
+  float* dev[2] = {nullptr, nullptr};
+  void* ws = nullptr;
+  float *Nk = nullptr, *mu_acc = nullptr, *sig_acc = nullptr, *logZ = nullptr;
+  double *part = nullptr, *ll = nullptr;
+  hipStream_t copy = nullptr, comp = nullptr;
+  hipEvent_t h2d0[2] = {nullptr, nullptr}, h2d1[2] = {nullptr, nullptr};
+  hipEvent_t e0[2] = {nullptr, nullptr}, e1[2] = {nullptr, nullptr};
+  hipEvent_t m0 = nullptr, m1 = nullptr;
+  ~StreamRes() {
+    if (comp) (void)hipStreamSynchronize(comp);
+    if (copy) (void)hipStreamSynchronize(copy);
+    for (int b = 0; b < 2; ++b) {
+      if (pinned[b]) (void)hipHostFree(pinned[b]);
+      if (dev[b]) (void)hipFree(dev[b]);
+      for (hipEvent_t e : {h2d0[b], h2d1[b], e0[b], e1[b]})
+        if (e) (void)hipEventDestroy(e);
+    }
+    for (void* p : {(void*)ws, (void*)Nk, (void*)mu_acc, (void*)sig_acc, (void*)logZ, (void*)part, (void*)ll})
+      if (p) (void)hipFree(p);
+    if (m0) (void)hipEventDestroy(m0);
+    if (m1) (void)hipEventDestroy(m1);
+    if (copy) (void)hipStreamDestroy(copy);
+    if (comp) (void)hipStreamDestroy(comp);
+  }
+};
+
+}  // namespace
+}  // namespace fgmm
+
+using namespace fgmm;
+
+extern "C" int fgmm_iso_mstep_f32(const float* Nk, const float* mu_acc, const float* sig_acc, int64_t N,
+                                  int64_t K, int64_t D, double var_floor, float* mu, int64_t ldmu,
+                                  float* log_sigma_sq, float* log_pi, unsigned flags, void* stream) {
+  if (N < 0 || K < 0 || D < 1 || ldmu < D || !(var_floor >= 0.0)) return FGMM_ERR_INVALID_ARG;
+  if (K == 0) return FGMM_OK;
+  if (!Nk || !mu_acc || !sig_acc || !mu || !log_sigma_sq || !log_pi) return FGMM_ERR_INVALID_ARG;
+  hipLaunchKernelGGL(iso_mstep_kernel, dim3((unsigned)K), dim3(256), 0, (hipStream_t)stream, Nk,
+                     mu_acc, sig_acc, (double)N, (int)D, var_floor,
+                     (flags & FGMM_MSTEP_EXACT_VARIANCE) ? 1 : 0, mu, ldmu, log_sigma_sq, log_pi);
+  return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+}
+
+extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn src, void* user,
+                                  float* mu, float* log_sigma_sq, float* log_pi,
+                                  fgmm_em_report* report) {
+  const auto t_start = std::chrono::steady_clock::now();
+  if (!cfg || !src || !mu || !log_sigma_sq || !log_pi) return FGMM_ERR_INVALID_ARG;
+  const int64_t N = cfg->N, K = cfg->K, D = cfg->D, R = cfg->chunk_rows;
+  if (N < 0 || K < 1 || D < 1 || D > 256 || R < 1 || cfg->iterations < 0 || !(cfg->var_floor >= 0.0))
+    return FGMM_ERR_INVALID_ARG;
+  fgmm_em_report rep{};
+  const int64_t ld = round_up(D, 4);
+  const int64_t rows = R < N ? R : (N > 0 ? N : 1);
+  const size_t chunk_bytes = (size_t)rows * ld * sizeof(float);
+  const size_t ws_bytes = fgmm_iso_workspace_bytes(rows, K, D);
+  const int64_t nparts = cdiv(rows, 1024);
+
+  StreamRes res;
+  auto ok = [](hipError_t e) { return e == hipSuccess; };
+  if (!ok(hipStreamCreateWithFlags(&res.copy, hipStreamNonBlocking)) ||
+      !ok(hipStreamCreateWithFlags(&res.comp, hipStreamNonBlocking)))
+    return FGMM_ERR_HIP;
+  for (int b = 0; b < 2; ++b) {
+    if (!ok(hipHostMalloc((void**)&res.pinned[b], chunk_bytes, hipHostMallocDefault)) ||
+        !ok(hipMalloc((void**)&res.dev[b], chunk_bytes)) || !ok(hipEventCreate(&res.h2d0[b])) ||
+        !ok(hipEventCreate(&res.h2d1[b])) || !ok(hipEventCreate(&res.e0[b])) ||
+        !ok(hipEventCreate(&res.e1[b])))
+      return FGMM_ERR_HIP;
+  }
+  if (!ok(hipMalloc(&res.ws, ws_bytes > 0 ? ws_bytes : 256)) ||
+      !ok(hipMalloc((void**)&res.Nk, K * sizeof(float))) ||
+      !ok(hipMalloc((void**)&res.mu_acc, K * D * sizeof(float))) ||
+      !ok(hipMalloc((void**)&res.sig_acc, K * sizeof(float))) ||
+      !ok(hipMalloc((void**)&res.logZ, rows * sizeof(float))) ||
+      !ok(hipMalloc((void**)&res.part, nparts * sizeof(double))) ||
+      !ok(hipMalloc((void**)&res.ll, sizeof(double))) || !ok(hipEventCreate(&res.m0)) ||
+      !ok(hipEventCreate(&res.m1)))
+    return FGMM_ERR_HIP;
+  rep.device_bytes = 2 * chunk_bytes + ws_bytes + (size_t)K * (D + 2) * sizeof(float) +
+                     (size_t)rows * sizeof(float) + (size_t)nparts * sizeof(double) + sizeof(double);
+  rep.pinned_bytes = 2 * chunk_bytes;
+
+  const int64_t nchunks = N > 0 ? cdiv(N, R) : 0;
+  std::vector<int64_t> chunk_rows_of(2, 0);
+  std::vector<bool> pending(2, false);
+  auto drain = [&](int b) -> int {
+    if (!pending[b]) return FGMM_OK;
+    if (!ok(hipEventSynchronize(res.e1[b]))) return FGMM_ERR_HIP;
+    float a = 0.0f, e = 0.0f;
+    if (!ok(hipEventElapsedTime(&a, res.h2d0[b], res.h2d1[b])) ||
+        !ok(hipEventElapsedTime(&e, res.e0[b], res.e1[b])))
+      return FGMM_ERR_HIP;
+    rep.h2d_ms += a;
+    rep.estep_ms += e;
+    pending[b] = false;
+    return FGMM_OK;
+  };
+
+  for (int it = 0; it < cfg->iterations; ++it) {
+    hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, res.comp, res.Nk, K, 0.0f);
+    hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(K * D, 256)), dim3(256), 0, res.comp, res.mu_acc,
+                       K * D, 0.0f);
+    hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, res.comp, res.sig_acc, K,
+                       0.0f);
+    hipLaunchKernelGGL(fill_f64_one, dim3(1), dim3(64), 0, res.comp, res.ll, 0.0);
+    for (int64_t c = 0; c < nchunks; ++c) {
+      const int b = (int)(c & 1);
+      const int64_t row0 = c * R;
+      const int64_t n = (row0 + R <= N) ? R : N - row0;
+      // Buffer b is free once the E-step of chunk c-2 (and hence its copy) finished.
+      int st = drain(b);
+      if (st != FGMM_OK) return st;
+      const auto tg = std::chrono::steady_clock::now();
+      float* host = res.pinned[b];
+      if (ld == D) {
+        st = src(user, row0, n, D, host);
+      } else {
+        // Sources write rows of stride D; the kernels read stride round_up(D, 4).
+        st = src(user, row0, n, D, host);
+        if (st == 0)
+          for (int64_t r = n - 1; r >= 0; --r)
+            for (int64_t d = D - 1; d >= 0; --d) host[r * ld + d] = host[r * D + d];
+      }
+      rep.source_ms += ms_since(tg);
+      if (st != 0) return FGMM_ERR_SOURCE;
+      if (!ok(hipEventRecord(res.h2d0[b], res.copy)) ||
+          !ok(hipMemcpyAsync(res.dev[b], host, (size_t)n * ld * sizeof(float), hipMemcpyHostToDevice,
+                             res.copy)) ||
+          !ok(hipEventRecord(res.h2d1[b], res.copy)) || !ok(hipStreamWaitEvent(res.comp, res.h2d1[b], 0)) ||
+          !ok(hipEventRecord(res.e0[b], res.comp)))
+        return FGMM_ERR_HIP;
+      st = fgmm_iso_estep_f32(res.dev[b], ld, n, D, mu, D, K, log_sigma_sq, log_pi, res.logZ, res.Nk,
+                              res.mu_acc, res.sig_acc, res.ws, ws_bytes, FGMM_FLAG_ACCUMULATE, res.comp);
+      if (st != FGMM_OK) return st;
+      hipLaunchKernelGGL(sum_blocks, dim3((unsigned)cdiv(n, 1024)), dim3(256), 0, res.comp, res.logZ, n,
+                         res.part);
+      hipLaunchKernelGGL(sum_parts, dim3(1), dim3(64), 0, res.comp, res.part, cdiv(n, 1024), res.ll);
+      if (!ok(hipEventRecord(res.e1[b], res.comp))) return FGMM_ERR_HIP;
+      // The next copy into dev[b] (chunk c+2) must wait for this E-step.
+      if (!ok(hipStreamWaitEvent(res.copy, res.e1[b], 0))) return FGMM_ERR_HIP;
+      pending[b] = true;
+      chunk_rows_of[b] = n;
+    }
+    for (int b = 0; b < 2; ++b) {
+      const int st = drain(b);
+      if (st != FGMM_OK) return st;
+    }
+    if (!ok(hipEventRecord(res.m0, res.comp))) return FGMM_ERR_HIP;
+    int st = fgmm_iso_mstep_f32(res.Nk, res.mu_acc, res.sig_acc, N, K, D, cfg->var_floor, mu, D,
+                                log_sigma_sq, log_pi, cfg->mstep_flags, res.comp);
+    if (st != FGMM_OK) return st;
+    double ll = 0.0;
+    if (!ok(hipEventRecord(res.m1, res.comp)) ||
+        !ok(hipMemcpyAsync(&ll, res.ll, sizeof(double), hipMemcpyDeviceToHost, res.comp)) ||
+        !ok(hipStreamSynchronize(res.comp)))
+      return FGMM_ERR_HIP;
+    float mm = 0.0f;
+    if (!ok(hipEventElapsedTime(&mm, res.m0, res.m1))) return FGMM_ERR_HIP;
+    rep.mstep_ms += mm;
+    if (it < FGMM_EM_MAX_REPORTED_ITERS) rep.loglik[it] = ll;
+  }
+  if (!ok(hipGetLastError())) return FGMM_ERR_HIP;
+  rep.total_ms = ms_since(t_start);
+  rep.iterations = cfg->iterations;
+  if (report) *report = rep;
+  return FGMM_OK;
+}

@@ -1,0 +1,183 @@
+"""EM on the device: the isotropic M-step, an in-memory EM loop and the streaming
+EM driver for data sets larger than device memory.
+
+The reference has no EM code; its README gives the M-step formulas
+(README.md:59-61) and a chunked streaming recipe (README.md:81-103).  Here the
+M-step is a HIP kernel and streaming is the native driver fgmm_stream_em_iso
+(pinned double buffers, a copy stream and a compute stream), fed by a host row
+source: the built-in counter-based generator (SynthIsoSource) or any Python
+callable returning rows.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Callable, Union
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import FlashGMMError
+from .estep import iso_estep_into
+
+MSTEP_EXACT_VARIANCE = 1 << 8
+MAX_REPORTED_ITERS = 16
+
+ROW_SOURCE = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                              ctypes.c_int64, ctypes.POINTER(ctypes.c_float))
+
+
+class _SynthIso(ctypes.Structure):
+    _fields_ = [("centres", ctypes.c_void_p), ("K", ctypes.c_int64), ("D", ctypes.c_int64),
+                ("seed", ctypes.c_uint64), ("threads", ctypes.c_int)]
+
+
+class _EmConfig(ctypes.Structure):
+    _fields_ = [("N", ctypes.c_int64), ("K", ctypes.c_int64), ("D", ctypes.c_int64),
+                ("chunk_rows", ctypes.c_int64), ("iterations", ctypes.c_int),
+                ("var_floor", ctypes.c_double), ("mstep_flags", ctypes.c_uint)]
+
+
+class _EmReport(ctypes.Structure):
+    _fields_ = [("iterations", ctypes.c_int), ("total_ms", ctypes.c_double),
+                ("source_ms", ctypes.c_double), ("h2d_ms", ctypes.c_double),
+                ("estep_ms", ctypes.c_double), ("mstep_ms", ctypes.c_double),
+                ("device_bytes", ctypes.c_size_t), ("pinned_bytes", ctypes.c_size_t),
+                ("loglik", ctypes.c_double * MAX_REPORTED_ITERS)]
+
+
+def _declare(L):
+    if getattr(L, "_em_declared", False):
+        return L
+    L.fgmm_synth_iso_source.restype = ctypes.c_int
+    L.fgmm_synth_iso_source.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                        ctypes.c_int64, ctypes.c_void_p]
+    L.fgmm_iso_mstep_f32.restype = ctypes.c_int
+    L.fgmm_iso_mstep_f32.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3 + [
+        ctypes.c_double, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_uint, ctypes.c_void_p]
+    L.fgmm_stream_em_iso.restype = ctypes.c_int
+    L.fgmm_stream_em_iso.argtypes = [ctypes.POINTER(_EmConfig), ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.POINTER(_EmReport)]
+    L._em_declared = True
+    return L
+
+
+class SynthIsoSource:
+    """Clustered rows x_n = centres[a_n] + N(0, I), a_n uniform (native generator).
+
+    Row n depends only on (seed, n): Philox4x32-10 keyed by the seed with the row
+    index in the counter, so chunking and threading do not change the data.
+    """
+
+    def __init__(self, centres, seed: int = 4, threads: int = 0):
+        c = np.ascontiguousarray(np.asarray(centres, dtype=np.float32))
+        if c.ndim != 2:
+            raise FlashGMMError("centres must be (K, D)")
+        self.centres = c
+        self.K, self.D = c.shape
+        self._s = _SynthIso(c.ctypes.data, self.K, self.D, int(seed) & (2**64 - 1), int(threads))
+
+    @property
+    def fn(self):
+        L = _declare(_lib.lib())
+        return ctypes.cast(L.fgmm_synth_iso_source, ctypes.c_void_p).value
+
+    @property
+    def user(self):
+        return ctypes.addressof(self._s)
+
+    def rows(self, row0: int, nrows: int) -> np.ndarray:
+        L = _declare(_lib.lib())
+        out = np.empty((nrows, self.D), dtype=np.float32)
+        st = L.fgmm_synth_iso_source(ctypes.addressof(self._s), row0, nrows, self.D, out.ctypes.data)
+        _lib.check(st, "fgmm_synth_iso_source")
+        return out
+
+
+def mstep_iso(Nk, mu_acc, sig_acc, N: int, mu, log_sigma_sq, log_pi, *, var_floor: float = 0.0,
+              exact_variance: bool = False) -> None:
+    """Device M-step: updates mu, log_sigma_sq, log_pi in place (README.md:59-61)."""
+    K, D = mu.shape
+    for t in (Nk, mu_acc, sig_acc, mu, log_sigma_sq, log_pi):
+        if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
+            raise FlashGMMError("M-step tensors must be contiguous float32 on the GPU")
+    L = _declare(_lib.lib())
+    with torch.cuda.device(mu.device):
+        st = L.fgmm_iso_mstep_f32(Nk.data_ptr(), mu_acc.data_ptr(), sig_acc.data_ptr(), int(N), K, D,
+                                  float(var_floor), mu.data_ptr(), D, log_sigma_sq.data_ptr(),
+                                  log_pi.data_ptr(), MSTEP_EXACT_VARIANCE if exact_variance else 0,
+                                  _lib.stream_handle(mu.device))
+    _lib.check(st, "fgmm_iso_mstep_f32")
+
+
+def em_iso(X, mu, log_sigma_sq, log_pi, iterations: int, *, var_floor: float = 0.0,
+           exact_variance: bool = False):
+    """In-memory EM: ``iterations`` rounds of E-step + device M-step.
+
+    Updates mu / log_sigma_sq / log_pi in place and returns the per-iteration
+    log-likelihoods sum_n logZ_n (each evaluated before that iteration's M-step).
+    """
+    N, D = X.shape
+    K = mu.shape[0]
+    dev = X.device
+    logZ = torch.empty(N, device=dev)
+    Nk = torch.empty(K, device=dev)
+    mu_acc = torch.empty(K, D, device=dev)
+    sig = torch.empty(K, device=dev)
+    out = []
+    for _ in range(iterations):
+        iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig)
+        out.append(float(logZ.double().sum()))
+        mstep_iso(Nk, mu_acc, sig, N, mu, log_sigma_sq, log_pi, var_floor=var_floor,
+                  exact_variance=exact_variance)
+    return out
+
+
+def stream_em_iso(source: Union[SynthIsoSource, Callable[[int, int], np.ndarray]], N: int, mu,
+                  log_sigma_sq, log_pi, *, iterations: int = 3, chunk_rows: int = 16 << 20,
+                  var_floor: float = 0.0, exact_variance: bool = False) -> dict:
+    """Streaming EM over N host rows; updates mu / log_sigma_sq / log_pi in place.
+
+    ``source`` is a SynthIsoSource or a callable ``f(row0, nrows) -> (nrows, D)``
+    float32 array.  Returns the driver's timing / memory report.
+    """
+    K, D = mu.shape
+    for t in (mu, log_sigma_sq, log_pi):
+        if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
+            raise FlashGMMError("parameters must be contiguous float32 on the GPU")
+    L = _declare(_lib.lib())
+    cfg = _EmConfig(int(N), K, D, int(chunk_rows), int(iterations), float(var_floor),
+                    MSTEP_EXACT_VARIANCE if exact_variance else 0)
+    rep = _EmReport()
+    keep = None
+    if isinstance(source, SynthIsoSource):
+        if source.D != D:
+            raise FlashGMMError("source dimension does not match mu")
+        fn, user = source.fn, source.user
+    else:
+        def _cb(user, row0, nrows, d, dst):
+            try:
+                rows = np.ascontiguousarray(source(int(row0), int(nrows)), dtype=np.float32).reshape(-1)
+                if rows.size != nrows * d:
+                    return 1
+                ctypes.memmove(dst, rows.ctypes.data, rows.nbytes)
+                return 0
+            except Exception:  # any failure aborts the stream with FGMM_ERR_SOURCE
+                return 1
+        keep = ROW_SOURCE(_cb)
+        fn, user = ctypes.cast(keep, ctypes.c_void_p).value, None
+    torch.cuda.synchronize(mu.device)
+    with torch.cuda.device(mu.device):
+        st = L.fgmm_stream_em_iso(ctypes.byref(cfg), fn, user, mu.data_ptr(), log_sigma_sq.data_ptr(),
+                                  log_pi.data_ptr(), ctypes.byref(rep))
+    del keep
+    _lib.check(st, "fgmm_stream_em_iso")
+    return {
+        "iterations": rep.iterations, "total_ms": rep.total_ms, "source_ms": rep.source_ms,
+        "h2d_ms": rep.h2d_ms, "estep_ms": rep.estep_ms, "mstep_ms": rep.mstep_ms,
+        "device_bytes": rep.device_bytes, "pinned_bytes": rep.pinned_bytes,
+        "loglik": [rep.loglik[i] for i in range(min(rep.iterations, MAX_REPORTED_ITERS))],
+    }

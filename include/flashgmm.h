@@ -34,6 +34,7 @@ enum fgmm_status {
     FGMM_ERR_UNSUPPORTED = -2, /* shape outside the compiled range (e.g. D > 256) */
     FGMM_ERR_WORKSPACE = -3,   /* workspace smaller than *_workspace_bytes() */
     FGMM_ERR_HIP = -4,         /* a HIP runtime call or kernel launch failed */
+    FGMM_ERR_SOURCE = -5,      /* a host row source returned an error */
 };
 
 /* Flags (bitwise OR). */
@@ -122,6 +123,81 @@ int fgmm_full_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
                         float *logZ, float *Nk, float *mu_acc, float *sig_outer,
                         void *workspace, size_t workspace_bytes,
                         unsigned flags, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Host row sources for the streaming driver.                                */
+/* A row source fills dst (host memory, nrows x D floats, row stride D) with  */
+/* rows [row0, row0 + nrows) of the data set and returns 0, or a nonzero     */
+/* status that aborts the stream.  It replaces the README's `for chunk in     */
+/* dataloader: chunk.cuda()` recipe (README.md:86-96).                        */
+/* ------------------------------------------------------------------------ */
+typedef int (*fgmm_row_source_fn)(void *user, int64_t row0, int64_t nrows, int64_t D, float *dst);
+
+/* Built-in synthetic source: x_n = centres[a_n] + z_n with a_n uniform over K
+ * and z_n ~ N(0, I), counter-based (Philox4x32-10 keyed by seed, counter = row
+ * index), so a row's value does not depend on how the rows are chunked.  No
+ * counterpart in the reference (its benchmark draws torch.randn on the GPU,
+ * flash_gmm.py:231). */
+typedef struct fgmm_synth_iso {
+    const float *centres; /* host, K x D, row-major */
+    int64_t K, D;
+    uint64_t seed;
+    int threads;          /* host threads; 0 = all hardware threads */
+} fgmm_synth_iso;
+
+int fgmm_synth_iso_source(void *user, int64_t row0, int64_t nrows, int64_t D, float *dst);
+
+/* ------------------------------------------------------------------------ */
+/* Isotropic M-step on the device (README.md:59-61):                          */
+/*   log_pi = log(Nk / N),  mu = mu_acc / Nk,                                 */
+/*   sigma^2 = max(var_floor, sig_acc / (D Nk) [- ||mu_new - mu_old||^2 / D]) */
+/* The bracketed term is applied with FGMM_MSTEP_EXACT_VARIANCE (sig_acc is    */
+/* accumulated about the old means).  Components with Nk = 0 keep mu and      */
+/* log_sigma_sq and get log_pi = -inf.  mu (K x D, row stride ldmu),           */
+/* log_sigma_sq and log_pi (K) are updated in place.                          */
+/* ------------------------------------------------------------------------ */
+enum { FGMM_MSTEP_EXACT_VARIANCE = 1u << 8 };
+
+int fgmm_iso_mstep_f32(const float *Nk, const float *mu_acc, const float *sig_acc,
+                       int64_t N, int64_t K, int64_t D, double var_floor,
+                       float *mu, int64_t ldmu, float *log_sigma_sq, float *log_pi,
+                       unsigned flags, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Streaming isotropic EM for data sets larger than device memory.           */
+/* Replaces the README recipe at README.md:81-103 (pageable chunk.cuda() per  */
+/* chunk, accumulators summed in Python, M-step in PyTorch).  Rows come from   */
+/* `src` into two pinned host buffers of chunk_rows rows; host filling, the   */
+/* host-to-device copy (copy stream) and the E-step (compute stream) of       */
+/* consecutive chunks overlap.  After every pass over the N rows the M-step   */
+/* updates mu (K x D contiguous), log_sigma_sq and log_pi in place (device    */
+/* pointers).  The call allocates its buffers and frees them before it        */
+/* returns; it blocks until the last iteration is done.                       */
+/* ------------------------------------------------------------------------ */
+#define FGMM_EM_MAX_REPORTED_ITERS 16
+
+typedef struct fgmm_em_config {
+    int64_t N, K, D;         /* rows, components, dimensions (D <= 256) */
+    int64_t chunk_rows;      /* rows per host chunk */
+    int iterations;          /* EM iterations */
+    double var_floor;        /* lower bound on sigma^2 in the M-step */
+    unsigned mstep_flags;    /* FGMM_MSTEP_* */
+} fgmm_em_config;
+
+typedef struct fgmm_em_report {
+    int iterations;
+    double total_ms;         /* wall time of the call */
+    double source_ms;        /* host time spent in the row source */
+    double h2d_ms;           /* device time of the host-to-device copies */
+    double estep_ms;         /* device time of the E-steps (incl. logZ sums) */
+    double mstep_ms;         /* device time of the M-steps */
+    size_t device_bytes;     /* device memory allocated by the call (peak) */
+    size_t pinned_bytes;     /* pinned host memory allocated by the call */
+    double loglik[FGMM_EM_MAX_REPORTED_ITERS]; /* sum_n logZ_n per iteration, before its M-step */
+} fgmm_em_report;
+
+int fgmm_stream_em_iso(const fgmm_em_config *cfg, fgmm_row_source_fn src, void *user,
+                       float *mu, float *log_sigma_sq, float *log_pi, fgmm_em_report *report);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,107 @@
+"""GPU M-step, in-memory EM and the streaming EM driver."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from flash_gmm import (FlashGMMError, SynthIsoSource, data, em_iso, flash_gmm_estep, mstep_iso,
+                       stream_em_iso)
+from oracle import gmm_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(K, D, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    centres = torch.randn(K, D, generator=g) * 2
+    mu = (centres + 0.5 * torch.randn(K, D, generator=g)).to(dev)
+    lss = torch.zeros(K, device=dev)
+    lpi = torch.full((K,), -math.log(K), device=dev)
+    return centres, mu, lss, lpi
+
+
+@pytest.mark.parametrize("exact", [False, True])
+def test_mstep_matches_readme_formulas(exact, gpu_device):
+    inp = data.iso_clustered(4000, 40, 24, seed=21)
+    dev = gpu_device
+    X, mu, lss, lpi = (inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi"))
+    _, Nk, mu_acc, sig = flash_gmm_estep(X, mu, lss, lpi)
+    mu_old = mu.clone()
+    mstep_iso(Nk, mu_acc, sig, 4000, mu, lss, lpi, exact_variance=exact)
+    torch.cuda.synchronize()
+    pi, m, s2 = O.mstep_iso(Nk.double().cpu(), mu_acc.double().cpu(), sig.double().cpu(), 4000, 24)
+    if exact:
+        s2 = s2 - ((m - mu_old.double().cpu()) ** 2).sum(1) / 24
+    torch.testing.assert_close(mu.double().cpu(), m, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(lss.double().cpu(), torch.log(s2), rtol=0, atol=1e-6)
+    torch.testing.assert_close(lpi.double().cpu(), torch.log(pi), rtol=0, atol=1e-6)
+
+
+def test_mstep_empty_component_keeps_parameters(gpu_device):
+    dev = gpu_device
+    K, D = 4, 8
+    Nk = torch.tensor([10.0, 0.0, 5.0, 0.0], device=dev)
+    mu_acc = torch.randn(K, D, device=dev)
+    sig = torch.rand(K, device=dev) * 100
+    mu = torch.randn(K, D, device=dev)
+    lss = torch.full((K,), 0.3, device=dev)
+    lpi = torch.zeros(K, device=dev)
+    mu0 = mu.clone()
+    mstep_iso(Nk, mu_acc, sig, 15, mu, lss, lpi, var_floor=1e-3)
+    torch.cuda.synchronize()
+    assert torch.equal(mu[1], mu0[1]) and torch.equal(mu[3], mu0[3])
+    assert float(lss[1]) == pytest.approx(0.3) and math.isinf(float(lpi[1]))
+    assert float(lpi[0]) == pytest.approx(math.log(10 / 15), abs=1e-6)
+
+
+def test_em_loglik_is_non_decreasing(gpu_device):
+    inp = data.iso_clustered(20000, 32, 16, seed=22)
+    dev = gpu_device
+    X, mu, lss, lpi = (inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi"))
+    ll = em_iso(X, mu, lss, lpi, 6, exact_variance=True)
+    assert all(b >= a - 1e-6 * abs(a) for a, b in zip(ll, ll[1:])), ll
+
+
+def _stream_vs_memory(dev, N, K, D, chunk, iters, source_kind):
+    centres, mu, lss, lpi = _params(K, D, 23, dev)
+    src = SynthIsoSource(centres.numpy(), seed=4)
+    X = torch.from_numpy(src.rows(0, N)).to(dev)
+    mu_m, lss_m, lpi_m = mu.clone(), lss.clone(), lpi.clone()
+    ll_m = em_iso(X, mu_m, lss_m, lpi_m, iters)
+    source = src if source_kind == "native" else (lambda r0, n: src.rows(r0, n))
+    rep = stream_em_iso(source, N, mu, lss, lpi, iterations=iters, chunk_rows=chunk)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(mu, mu_m, rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(lss, lss_m, rtol=0, atol=1e-4)
+    torch.testing.assert_close(lpi, lpi_m, rtol=0, atol=1e-4)
+    np.testing.assert_allclose(rep["loglik"], ll_m, rtol=1e-6)
+    assert rep["iterations"] == iters and rep["device_bytes"] > 0
+    return rep
+
+
+def test_stream_em_matches_in_memory_native_source(gpu_device):
+    rep = _stream_vs_memory(gpu_device, 200_000, 64, 32, 48_000, 2, "native")
+    assert rep["total_ms"] >= rep["source_ms"]
+
+
+def test_stream_em_python_source_and_odd_dimension(gpu_device):
+    _stream_vs_memory(gpu_device, 30_000, 20, 30, 7_000, 2, "python")
+
+
+def test_stream_em_source_error_is_reported(gpu_device):
+    dev = gpu_device
+    centres, mu, lss, lpi = _params(8, 16, 24, dev)
+    src = SynthIsoSource(centres.numpy(), seed=4)
+
+    def failing(row0, n):
+        if row0 >= 20_000:
+            raise RuntimeError("disk went away")
+        return src.rows(row0, n)
+
+    with pytest.raises(FlashGMMError, match="row source"):
+        stream_em_iso(failing, 50_000, mu, lss, lpi, iterations=1, chunk_rows=10_000)
+    # the driver released its resources: a following call works
+    rep = stream_em_iso(src, 50_000, mu, lss, lpi, iterations=1, chunk_rows=10_000)
+    assert rep["iterations"] == 1
