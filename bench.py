@@ -114,8 +114,26 @@ def stream_main(args):
     src = SynthIsoSource(centres.numpy(), seed=4, threads=threads)
     log(f"streaming EM: N={N} rows, K={K}, D={D}, chunks of {chunk} rows, {iters} iterations, "
         f"{threads} host threads")
-    torch.cuda.reset_peak_memory_stats(dev)
-    rep = stream_em_iso(src, N, mu, lss, lpi, iterations=iters, chunk_rows=chunk, exact_variance=True)
+    # Device-wide used memory, sampled while the driver runs (the ctypes call
+    # releases the GIL); the driver's own allocation total is reported beside it.
+    import threading
+    free0, total_mem = torch.cuda.mem_get_info(dev)
+    peak_used = [total_mem - free0]
+    done = threading.Event()
+
+    def sample():
+        while not done.wait(0.25):
+            f, t = torch.cuda.mem_get_info(dev)
+            peak_used[0] = max(peak_used[0], t - f)
+
+    th = threading.Thread(target=sample, daemon=True)
+    th.start()
+    try:
+        rep = stream_em_iso(src, N, mu, lss, lpi, iterations=iters, chunk_rows=chunk,
+                            exact_variance=True)
+    finally:
+        done.set()
+        th.join()
     total_s = rep["total_ms"] / 1e3
     out = {
         "metric": f"streaming EM end-to-end rows/s (N={N}, K={K}, D={D}, {iters} iterations, fp32)",
@@ -140,6 +158,8 @@ def stream_main(args):
         "mstep_device_s": rep["mstep_ms"] / 1e3,
         "h2d_GBps": (N * iters * D * 4) / max(rep["h2d_ms"], 1e-9) / 1e6,
         "peak_device_bytes_driver": rep["device_bytes"],
+        "device_used_bytes_before": total_mem - free0,
+        "device_used_bytes_peak": peak_used[0],
         "pinned_host_bytes": rep["pinned_bytes"],
         "loglik_per_iteration": rep["loglik"],
     }

@@ -111,7 +111,7 @@ struct StreamRes {
   hipStream_t copy = nullptr, comp = nullptr;
   hipEvent_t h2d0[2] = {nullptr, nullptr}, h2d1[2] = {nullptr, nullptr};
   hipEvent_t e0[2] = {nullptr, nullptr}, e1[2] = {nullptr, nullptr};
-  hipEvent_t m0 = nullptr, m1 = nullptr;
+  std::vector<hipEvent_t> m0, m1;  // per iteration, around the M-step
   ~StreamRes() {
     if (comp) (void)hipStreamSynchronize(comp);
     if (copy) (void)hipStreamSynchronize(copy);
@@ -123,8 +123,10 @@ struct StreamRes {
     }
     for (void* p : {(void*)ws, (void*)Nk, (void*)mu_acc, (void*)sig_acc, (void*)logZ, (void*)part, (void*)ll})
       if (p) (void)hipFree(p);
-    if (m0) (void)hipEventDestroy(m0);
-    if (m1) (void)hipEventDestroy(m1);
+    for (hipEvent_t e : m0)
+      if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : m1)
+      if (e) (void)hipEventDestroy(e);
     if (copy) (void)hipStreamDestroy(copy);
     if (comp) (void)hipStreamDestroy(comp);
   }
@@ -153,11 +155,12 @@ extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn 
   const auto t_start = std::chrono::steady_clock::now();
   if (!cfg || !src || !mu || !log_sigma_sq || !log_pi) return FGMM_ERR_INVALID_ARG;
   const int64_t N = cfg->N, K = cfg->K, D = cfg->D, R = cfg->chunk_rows;
-  if (N < 0 || K < 1 || D < 1 || D > 256 || R < 1 || cfg->iterations < 0 || !(cfg->var_floor >= 0.0))
+  const int iters = cfg->iterations;
+  if (N < 1 || K < 1 || D < 1 || D > 256 || R < 1 || iters < 0 || !(cfg->var_floor >= 0.0))
     return FGMM_ERR_INVALID_ARG;
   fgmm_em_report rep{};
   const int64_t ld = round_up(D, 4);
-  const int64_t rows = R < N ? R : (N > 0 ? N : 1);
+  const int64_t rows = R < N ? R : N;
   const size_t chunk_bytes = (size_t)rows * ld * sizeof(float);
   const size_t ws_bytes = fgmm_iso_workspace_bytes(rows, K, D);
   const int64_t nparts = cdiv(rows, 1024);
@@ -174,22 +177,26 @@ extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn 
         !ok(hipEventCreate(&res.e1[b])))
       return FGMM_ERR_HIP;
   }
+  const int nll = iters > 0 ? iters : 1;
   if (!ok(hipMalloc(&res.ws, ws_bytes > 0 ? ws_bytes : 256)) ||
       !ok(hipMalloc((void**)&res.Nk, K * sizeof(float))) ||
       !ok(hipMalloc((void**)&res.mu_acc, K * D * sizeof(float))) ||
       !ok(hipMalloc((void**)&res.sig_acc, K * sizeof(float))) ||
       !ok(hipMalloc((void**)&res.logZ, rows * sizeof(float))) ||
       !ok(hipMalloc((void**)&res.part, nparts * sizeof(double))) ||
-      !ok(hipMalloc((void**)&res.ll, sizeof(double))) || !ok(hipEventCreate(&res.m0)) ||
-      !ok(hipEventCreate(&res.m1)))
+      !ok(hipMalloc((void**)&res.ll, nll * sizeof(double))))
     return FGMM_ERR_HIP;
+  res.m0.assign(iters, nullptr);
+  res.m1.assign(iters, nullptr);
+  for (int it = 0; it < iters; ++it)
+    if (!ok(hipEventCreate(&res.m0[it])) || !ok(hipEventCreate(&res.m1[it]))) return FGMM_ERR_HIP;
   rep.device_bytes = 2 * chunk_bytes + ws_bytes + (size_t)K * (D + 2) * sizeof(float) +
-                     (size_t)rows * sizeof(float) + (size_t)nparts * sizeof(double) + sizeof(double);
+                     (size_t)rows * sizeof(float) + (size_t)nparts * sizeof(double) +
+                     (size_t)nll * sizeof(double);
   rep.pinned_bytes = 2 * chunk_bytes;
 
-  const int64_t nchunks = N > 0 ? cdiv(N, R) : 0;
-  std::vector<int64_t> chunk_rows_of(2, 0);
-  std::vector<bool> pending(2, false);
+  const int64_t nchunks = cdiv(N, R);
+  bool pending[2] = {false, false};
   auto drain = [&](int b) -> int {
     if (!pending[b]) return FGMM_OK;
     if (!ok(hipEventSynchronize(res.e1[b]))) return FGMM_ERR_HIP;
@@ -203,72 +210,79 @@ extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn 
     return FGMM_OK;
   };
 
-  for (int it = 0; it < cfg->iterations; ++it) {
-    hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, res.comp, res.Nk, K, 0.0f);
-    hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(K * D, 256)), dim3(256), 0, res.comp, res.mu_acc,
-                       K * D, 0.0f);
-    hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, res.comp, res.sig_acc, K,
-                       0.0f);
-    hipLaunchKernelGGL(fill_f64_one, dim3(1), dim3(64), 0, res.comp, res.ll, 0.0);
-    for (int64_t c = 0; c < nchunks; ++c) {
-      const int b = (int)(c & 1);
-      const int64_t row0 = c * R;
-      const int64_t n = (row0 + R <= N) ? R : N - row0;
-      // Buffer b is free once the E-step of chunk c-2 (and hence its copy) finished.
-      int st = drain(b);
-      if (st != FGMM_OK) return st;
-      const auto tg = std::chrono::steady_clock::now();
-      float* host = res.pinned[b];
-      if (ld == D) {
-        st = src(user, row0, n, D, host);
-      } else {
-        // Sources write rows of stride D; the kernels read stride round_up(D, 4).
-        st = src(user, row0, n, D, host);
-        if (st == 0)
-          for (int64_t r = n - 1; r >= 0; --r)
-            for (int64_t d = D - 1; d >= 0; --d) host[r * ld + d] = host[r * D + d];
-      }
-      rep.source_ms += ms_since(tg);
-      if (st != 0) return FGMM_ERR_SOURCE;
-      if (!ok(hipEventRecord(res.h2d0[b], res.copy)) ||
-          !ok(hipMemcpyAsync(res.dev[b], host, (size_t)n * ld * sizeof(float), hipMemcpyHostToDevice,
-                             res.copy)) ||
-          !ok(hipEventRecord(res.h2d1[b], res.copy)) || !ok(hipStreamWaitEvent(res.comp, res.h2d1[b], 0)) ||
-          !ok(hipEventRecord(res.e0[b], res.comp)))
-        return FGMM_ERR_HIP;
-      st = fgmm_iso_estep_f32(res.dev[b], ld, n, D, mu, D, K, log_sigma_sq, log_pi, res.logZ, res.Nk,
-                              res.mu_acc, res.sig_acc, res.ws, ws_bytes, FGMM_FLAG_ACCUMULATE, res.comp);
-      if (st != FGMM_OK) return st;
-      hipLaunchKernelGGL(sum_blocks, dim3((unsigned)cdiv(n, 1024)), dim3(256), 0, res.comp, res.logZ, n,
-                         res.part);
-      hipLaunchKernelGGL(sum_parts, dim3(1), dim3(64), 0, res.comp, res.part, cdiv(n, 1024), res.ll);
-      if (!ok(hipEventRecord(res.e1[b], res.comp))) return FGMM_ERR_HIP;
-      // The next copy into dev[b] (chunk c+2) must wait for this E-step.
-      if (!ok(hipStreamWaitEvent(res.copy, res.e1[b], 0))) return FGMM_ERR_HIP;
-      pending[b] = true;
-      chunk_rows_of[b] = n;
-    }
-    for (int b = 0; b < 2; ++b) {
-      const int st = drain(b);
-      if (st != FGMM_OK) return st;
-    }
-    if (!ok(hipEventRecord(res.m0, res.comp))) return FGMM_ERR_HIP;
-    int st = fgmm_iso_mstep_f32(res.Nk, res.mu_acc, res.sig_acc, N, K, D, cfg->var_floor, mu, D,
-                                log_sigma_sq, log_pi, cfg->mstep_flags, res.comp);
+  // One flat pipeline over (iteration, chunk).  The rows do not depend on the
+  // parameters, so the host fills and copies the next iteration's first chunks
+  // while the device finishes the last E-steps and the M-step; stream order on
+  // the compute stream puts each M-step before the next iteration's E-steps.
+  const int64_t total = nchunks * iters;
+  for (int64_t g = 0; g < total; ++g) {
+    const int it = (int)(g / nchunks);
+    const int64_t c = g % nchunks;
+    const int b = (int)(g & 1);
+    const int64_t row0 = c * R;
+    const int64_t n = (row0 + R <= N) ? R : N - row0;
+    // Buffer b is free once the E-step two chunks back (and hence its copy) finished.
+    int st = drain(b);
     if (st != FGMM_OK) return st;
-    double ll = 0.0;
-    if (!ok(hipEventRecord(res.m1, res.comp)) ||
-        !ok(hipMemcpyAsync(&ll, res.ll, sizeof(double), hipMemcpyDeviceToHost, res.comp)) ||
-        !ok(hipStreamSynchronize(res.comp)))
+    const auto tg = std::chrono::steady_clock::now();
+    float* host = res.pinned[b];
+    st = src(user, row0, n, D, host);
+    if (st == 0 && ld != D) {
+      // Sources write rows of stride D; the kernels read stride round_up(D, 4).
+      for (int64_t r = n - 1; r >= 0; --r)
+        for (int64_t d = D - 1; d >= 0; --d) host[r * ld + d] = host[r * D + d];
+    }
+    rep.source_ms += ms_since(tg);
+    if (st != 0) return FGMM_ERR_SOURCE;
+    if (!ok(hipEventRecord(res.h2d0[b], res.copy)) ||
+        !ok(hipMemcpyAsync(res.dev[b], host, (size_t)n * ld * sizeof(float), hipMemcpyHostToDevice,
+                           res.copy)) ||
+        !ok(hipEventRecord(res.h2d1[b], res.copy)))
       return FGMM_ERR_HIP;
+    if (c == 0) {
+      hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, res.comp, res.Nk, K, 0.0f);
+      hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(K * D, 256)), dim3(256), 0, res.comp, res.mu_acc,
+                         K * D, 0.0f);
+      hipLaunchKernelGGL(fill_f32, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, res.comp, res.sig_acc, K,
+                         0.0f);
+      hipLaunchKernelGGL(fill_f64_one, dim3(1), dim3(64), 0, res.comp, res.ll + it, 0.0);
+    }
+    if (!ok(hipStreamWaitEvent(res.comp, res.h2d1[b], 0)) || !ok(hipEventRecord(res.e0[b], res.comp)))
+      return FGMM_ERR_HIP;
+    st = fgmm_iso_estep_f32(res.dev[b], ld, n, D, mu, D, K, log_sigma_sq, log_pi, res.logZ, res.Nk,
+                            res.mu_acc, res.sig_acc, res.ws, ws_bytes, FGMM_FLAG_ACCUMULATE, res.comp);
+    if (st != FGMM_OK) return st;
+    hipLaunchKernelGGL(sum_blocks, dim3((unsigned)cdiv(n, 1024)), dim3(256), 0, res.comp, res.logZ, n,
+                       res.part);
+    hipLaunchKernelGGL(sum_parts, dim3(1), dim3(64), 0, res.comp, res.part, cdiv(n, 1024), res.ll + it);
+    if (!ok(hipEventRecord(res.e1[b], res.comp))) return FGMM_ERR_HIP;
+    // The next copy into dev[b] must wait for this E-step.
+    if (!ok(hipStreamWaitEvent(res.copy, res.e1[b], 0))) return FGMM_ERR_HIP;
+    pending[b] = true;
+    if (c == nchunks - 1) {
+      if (!ok(hipEventRecord(res.m0[it], res.comp))) return FGMM_ERR_HIP;
+      st = fgmm_iso_mstep_f32(res.Nk, res.mu_acc, res.sig_acc, N, K, D, cfg->var_floor, mu, D,
+                              log_sigma_sq, log_pi, cfg->mstep_flags, res.comp);
+      if (st != FGMM_OK) return st;
+      if (!ok(hipEventRecord(res.m1[it], res.comp))) return FGMM_ERR_HIP;
+    }
+  }
+  for (int b = 0; b < 2; ++b) {
+    const int st = drain(b);
+    if (st != FGMM_OK) return st;
+  }
+  std::vector<double> ll(nll, 0.0);
+  if (iters > 0 && !ok(hipMemcpy(ll.data(), res.ll, iters * sizeof(double), hipMemcpyDeviceToHost)))
+    return FGMM_ERR_HIP;
+  for (int it = 0; it < iters; ++it) {
     float mm = 0.0f;
-    if (!ok(hipEventElapsedTime(&mm, res.m0, res.m1))) return FGMM_ERR_HIP;
+    if (!ok(hipEventElapsedTime(&mm, res.m0[it], res.m1[it]))) return FGMM_ERR_HIP;
     rep.mstep_ms += mm;
-    if (it < FGMM_EM_MAX_REPORTED_ITERS) rep.loglik[it] = ll;
+    if (it < FGMM_EM_MAX_REPORTED_ITERS) rep.loglik[it] = ll[it];
   }
   if (!ok(hipGetLastError())) return FGMM_ERR_HIP;
   rep.total_ms = ms_since(t_start);
-  rep.iterations = cfg->iterations;
+  rep.iterations = iters;
   if (report) *report = rep;
   return FGMM_OK;
 }

@@ -169,10 +169,11 @@ int fgmm_iso_mstep_f32(const float *Nk, const float *mu_acc, const float *sig_ac
 /* chunk, accumulators summed in Python, M-step in PyTorch).  Rows come from   */
 /* `src` into two pinned host buffers of chunk_rows rows; host filling, the   */
 /* host-to-device copy (copy stream) and the E-step (compute stream) of       */
-/* consecutive chunks overlap.  After every pass over the N rows the M-step   */
-/* updates mu (K x D contiguous), log_sigma_sq and log_pi in place (device    */
-/* pointers).  The call allocates its buffers and frees them before it        */
-/* returns; it blocks until the last iteration is done.                       */
+/* consecutive chunks overlap, also across iterations (the rows do not       */
+/* depend on the parameters).  After every pass over the N rows (N >= 1) the  */
+/* M-step updates mu (K x D contiguous), log_sigma_sq and log_pi in place     */
+/* (device pointers).  The call allocates its buffers and frees them before   */
+/* it returns; it blocks until the last iteration is done.                    */
 /* ------------------------------------------------------------------------ */
 #define FGMM_EM_MAX_REPORTED_ITERS 16
 
