@@ -173,6 +173,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--atomic-reduce", action="store_true")
+    ap.add_argument("--dense", action="store_true",
+                    help="iso: also run accumulation steps whose responsibilities are all zero")
     ap.add_argument("--workload", default="iso_n1m_k1024_d128",
                     choices=sorted(WORKLOADS) + ["stream_em_n1b_k1024_d128"])
     ap.add_argument("--rows", type=int, default=0, help="override N of the streaming workload")
@@ -203,8 +205,9 @@ def main():
         args4 = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
         sig = torch.empty(K, device=dev)
         ws = torch.empty(int(L.fgmm_iso_workspace_bytes(N, K, D)), dtype=torch.uint8, device=dev)
-        fn = lambda ph: iso_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws, phase=ph,
-                                       atomic_reduce=args.atomic_reduce)
+        fn = lambda ph, dense=args.dense: iso_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
+                                                         phase=ph, atomic_reduce=args.atomic_reduce,
+                                                         dense=dense)
     elif kind == "diag":
         args4 = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
         sig = torch.empty(K, D, device=dev)
@@ -227,6 +230,10 @@ def main():
         if ev is not None:
             ev[2].record(stream)
 
+    def dense_step():
+        fn(1, True)
+        fn(2, True)
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -245,6 +252,21 @@ def main():
     p1 = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
     p2 = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
     log(f"timed {args.steps} steps: {ms:.3f} ms/step (phase1 {p1:.3f} ms, phase2 {p2:.3f} ms)")
+
+    dense_ms = None
+    if kind == "iso" and not args.dense:
+        # The same steps with every accumulation step executed (identical outputs):
+        # the dense cost, reported beside the default.
+        for _ in range(2):
+            dense_step()
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(args.steps):
+            dense_step()
+        end.record(stream)
+        torch.cuda.synchronize()
+        dense_ms = start.elapsed_time(end) / args.steps
+        log(f"dense accumulation: {dense_ms:.3f} ms/step")
 
     flop, f1, f2 = algorithmic_flop(kind, N, K, D)
     step_tflops = flop / (ms * 1e-3) / 1e12
@@ -280,6 +302,11 @@ def main():
         "fraction_of_fp32_mfma_peak": step_tflops / PEAK_FP32_MFMA_TFLOPS,
         "step_tflops_algorithmic": step_tflops,
         "phase_ms": {"phase1": p1, "phase2": p2},
+        "accumulation": "dense" if (args.dense or kind != "iso") else
+                        "skips steps whose responsibilities are all exactly zero (bitwise-identical outputs)",
+        "dense_ms_per_step": dense_ms if dense_ms is not None else (ms if args.dense else None),
+        "dense_fraction_of_fp32_mfma_peak": (flop / (dense_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS)
+                                            if dense_ms is not None else None,
         "roofline": {
             "bound": "mfma",
             "kernel": dom,

@@ -378,9 +378,11 @@ void iso_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int ro = 8 * (i >> 2) + (i & 3);
-        const RowStat stt = rbase[ro];
-        const float u = fmaf(-2.0f, xm[i], stt.h);            // ||x||^2 - 2 x.mu
-        const float dq = (float)(Ck - stt.q);                  // C_k - logZ2, rounded once
+        // One 16-byte LDS read per row: {logZ2 (fp64), ||x||^2 (fp32), pad}.
+        const uint4 w = *reinterpret_cast<const uint4*>(rbase + ro);
+        const double q = __hiloint2double((int)w.y, (int)w.x);
+        const float u = fmaf(-2.0f, xm[i], __uint_as_float(w.z));  // ||x||^2 - 2 x.mu
+        const float dq = (float)(Ck - q);                          // C_k - logZ2, rounded once
         const float rv = fast_exp2(fmaf(-bkf, u, dq));
         nk += rv;
         sig = fmaf(rv, u + musqf, sig);
@@ -438,7 +440,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads),
 void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                    const f32x4* __restrict__ mu_sw, const double4* __restrict__ kc_lin, int KB, int KP,
                    const double2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
-                   float* __restrict__ part_mu, float* __restrict__ part_nk, float* __restrict__ part_sig) {
+                   float* __restrict__ part_mu, float* __restrict__ part_nk, float* __restrict__ part_sig,
+                   int dense) {
   constexpr int NM = DP / 8;
   constexpr int NJ = DP / 32;
   constexpr int RS = DP + 4;
@@ -490,14 +493,25 @@ void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   f32x4 stage[LPT];
   double2 rstage = make_double2(0.0, INFINITY);
+  const bool full_d = (D == DP);
   auto fetch = [&](int t) {
     const int64_t row0 = r_begin + (int64_t)t * TR;
+    if (full_d && row0 + TR <= r_end) {
+      // Interior tile: no row or column masking.
+      const float* src = X + row0 * ldx;
 #pragma unroll
-    for (int q = 0; q < LPT; ++q) {
-      const int idx = q * kAccThreads + tid;
-      const int rr = idx / V4, c4 = idx % V4;
-      const int64_t row = row0 + rr;
-      stage[q] = load_row4(X, ldx, row, c4 * 4, D, row < r_end);
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        const int rr = idx / V4, c4 = idx % V4;
+        const int64_t row = row0 + rr;
+        stage[q] = load_row4(X, ldx, row, c4 * 4, D, row < r_end);
+      }
     }
     if (tid < TR) {
       const int64_t row = row0 + tid;
@@ -537,9 +551,11 @@ void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int ro = 8 * (i >> 2) + (i & 3);
-        const RowStat stt = rbase[ro];
-        const float u = fmaf(-2.0f, xm[i], stt.h);            // ||x||^2 - 2 x.mu
-        const float dq = (float)(Ck - stt.q);                  // C_k - logZ2, rounded once
+        // One 16-byte LDS read per row: {logZ2 (fp64), ||x||^2 (fp32), pad}.
+        const uint4 w = *reinterpret_cast<const uint4*>(rbase + ro);
+        const double q = __hiloint2double((int)w.y, (int)w.x);
+        const float u = fmaf(-2.0f, xm[i], __uint_as_float(w.z));  // ||x||^2 - 2 x.mu
+        const float dq = (float)(Ck - q);                          // C_k - logZ2, rounded once
         const float rv = fast_exp2(fmaf(-bkf, u, dq));
         nk += rv;
         sig = fmaf(rv, u + musqf, sig);
@@ -552,8 +568,12 @@ void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int ro = 8 * (i >> 2) + (i & 3);
+        // A step whose 64 responsibilities are all exactly zero adds nothing:
+        // skip it (wave-uniform branch; identical results).
+        if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
+          for (int j = 0; j < NJ; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
+        }
       }
     }
     if (more) commit(buf ^ 1);
@@ -633,7 +653,7 @@ __global__ __launch_bounds__(256) void fill_f32(float* __restrict__ p, int64_t n
 
 template <int DP>
 hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
-                         float* logZ, bool run1, bool run2, hipStream_t stream) {
+                         float* logZ, bool run1, bool run2, bool dense, hipStream_t stream) {
   const f32x4* mu_sw = reinterpret_cast<const f32x4*>(ws + pl.off_musw);
   const double2* kc_blk = reinterpret_cast<const double2*>(ws + pl.off_kcblk);
   const double4* kc_lin = reinterpret_cast<const double4*>(ws + pl.off_kclin);
@@ -663,7 +683,7 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
     }
     hipLaunchKernelGGL(iso_accum_lds<DP>, grid2, dim3(kAccThreads), lds, stream, X, ldx, pl.N,
                        (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
-                       pmu, pnk, psig);
+                       pmu, pnk, psig, dense ? 1 : 0);
   } else {
     constexpr size_t lds = accum_lds_bytes<DP>();
     if (lds > 65536) {
@@ -697,6 +717,7 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
   const bool want_logz = !(flags & FGMM_FLAG_NO_LOGZ);
   const bool accumulate = (flags & FGMM_FLAG_ACCUMULATE) != 0;
   const bool atomic = (flags & FGMM_FLAG_ATOMIC_REDUCE) != 0;
+  const bool dense = (flags & FGMM_FLAG_DENSE) != 0;
   if (N < 0 || K < 0 || D < 1) return FGMM_ERR_INVALID_ARG;
   if (N > 0 && (X == nullptr || ldx < round_up(D, 4) || (ldx % 4) != 0 ||
                 (reinterpret_cast<uintptr_t>(X) & 15) != 0))
@@ -730,14 +751,14 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
   if (N > 0) {
     hipError_t e = hipSuccess;
     switch (pl.DP) {
-      case 32: e = launch_passes<32>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
-      case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
-      case 96: e = launch_passes<96>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
-      case 128: e = launch_passes<128>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
-      case 160: e = launch_passes<160>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
-      case 192: e = launch_passes<192>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
-      case 224: e = launch_passes<224>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
-      case 256: e = launch_passes<256>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 32: e = launch_passes<32>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 96: e = launch_passes<96>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 128: e = launch_passes<128>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 160: e = launch_passes<160>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 192: e = launch_passes<192>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 224: e = launch_passes<224>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 256: e = launch_passes<256>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       default: return FGMM_ERR_UNSUPPORTED;
     }
     if (e != hipSuccess) return FGMM_ERR_HIP;

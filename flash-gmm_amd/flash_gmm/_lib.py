@@ -26,6 +26,7 @@ FLAG_NO_LOGZ = 1 << 1
 FLAG_ATOMIC_REDUCE = 1 << 2
 FLAG_PHASE1 = 1 << 3
 FLAG_PHASE2 = 1 << 4
+FLAG_DENSE = 1 << 5
 
 
 class FlashGMMError(AssertionError, ValueError):

@@ -115,14 +115,17 @@ def _rowmajor(t: torch.Tensor) -> torch.Tensor:
 
 def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
                    accumulate: bool = False, atomic_reduce: bool = False,
-                   workspace: torch.Tensor | None = None, phase: int = 0) -> None:
+                   workspace: torch.Tensor | None = None, phase: int = 0,
+                   dense: bool = False) -> None:
     """Isotropic E-step writing into caller-provided outputs.
 
     ``logZ`` may be None (it is then not written).  With ``accumulate`` the
     statistics are added to the current contents of Nk / mu_acc / sig_acc
     (streaming over row chunks, README.md:86-96).  ``phase`` 1 runs only the
     log-normaliser pass, 2 only the accumulation (reusing ``workspace`` from a
-    phase-1 call on the same inputs), 0 both.
+    phase-1 call on the same inputs), 0 both.  ``dense`` runs the accumulation
+    steps whose responsibilities are all exactly zero instead of skipping them
+    (same results; for timing).
     """
     _check_common(X, mu, log_pi)
     N, D = X.shape
@@ -136,6 +139,8 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     L = _lib.lib()
     workspace = _workspace(L.fgmm_iso_workspace_bytes, N, K, D, dev, workspace)
     flags = _flags(accumulate, logZ, atomic_reduce, phase)
+    if dense:
+        flags |= _lib.FLAG_DENSE
     _check_out("Nk", Nk, (K,), dev)
     _check_out("mu_acc", mu_acc, (K, D), dev)
     _check_out("sig_acc", sig_acc, (K,), dev)

@@ -57,6 +57,11 @@ enum fgmm_flags {
      * call with the same inputs on the same stream. */
     FGMM_FLAG_PHASE1 = 1u << 3,
     FGMM_FLAG_PHASE2 = 1u << 4,
+    /* The accumulation pass skips every matrix-core step whose responsibilities
+     * (two rows x 32 components) are all exactly zero, since such a step adds
+     * nothing; the results are bitwise the same either way.  DENSE runs every
+     * step (for timing the dense contraction). */
+    FGMM_FLAG_DENSE = 1u << 5,
 };
 
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */

@@ -105,6 +105,32 @@ def test_deterministic_bitwise(gpu_device):
         assert torch.equal(u, v)
 
 
+def _into(inp, dev, **kw):
+    N, D = inp["X"].shape
+    K = inp["mu"].shape[0]
+    out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, device=dev)]
+    iso_estep_into(*[inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")], *out, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("case", ["clustered_d128", "clustered_d64_ragged", "plain_d32"])
+def test_zero_step_skip_is_bitwise_dense(case, gpu_device):
+    """Skipping all-zero responsibility steps changes no bit of any output."""
+    if case == "clustered_d128":
+        inp = data.iso_clustered(12000, 1024, 128, seed=1)   # mostly zero steps
+    elif case == "clustered_d64_ragged":
+        inp = data.iso_clustered(7777, 300, 61, seed=5)
+    else:
+        inp = data.iso_plain(10000, 64, 32, seed=0)          # no zero steps
+    a = _into(inp, gpu_device)
+    b = _into(inp, gpu_device, dense=True)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+    assert_close_stats(a, oracle(inp), case)
+
+
 def test_atomic_reduce_matches(gpu_device):
     inp = data.iso_clustered(5000, 200, 48, seed=9)
     ref = run_gpu(inp, gpu_device)
