@@ -43,20 +43,24 @@ def cpu_model():
     return platform.processor()
 
 
-def cpu_baseline(inp, K, D, min_s=10.0, max_s=30.0, rows=16384):
+def cpu_baseline(inp, kind, K, D, min_s=10.0, max_s=30.0, rows=16384):
     """The oracle's float32 restatement on the host cores, on a bounded sample."""
     import torch
     from oracle import gmm_oracle as O
 
     threads = min(len(os.sched_getaffinity(0)), 16)
     torch.set_num_threads(threads)
+    if kind == "full":
+        rows = 4096
     X = inp["X"][:rows].cpu()
-    mu, lss, lpi = (inp[k].cpu() for k in ("mu", "log_sigma_sq", "log_pi"))
-    O.estep_iso(X[:1024], mu, lss, lpi, dtype=torch.float32)  # warm
+    third = "prec_chol" if kind == "full" else "log_sigma_sq"
+    mu, p3, lpi = (inp[k].cpu() for k in ("mu", third, "log_pi"))
+    fn = {"iso": O.estep_iso, "diag": O.estep_diag, "full": O.estep_full}[kind]
+    fn(X[:512], mu, p3, lpi, dtype=torch.float32)  # warm
     done, t0 = 0, time.perf_counter()
     reps = 0
     while True:
-        O.estep_iso(X, mu, lss, lpi, dtype=torch.float32, chunk=rows)
+        fn(X, mu, p3, lpi, dtype=torch.float32, chunk=rows)
         done += rows
         reps += 1
         el = time.perf_counter() - t0
@@ -174,7 +178,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--atomic-reduce", action="store_true")
     ap.add_argument("--dense", action="store_true",
-                    help="iso: also run accumulation steps whose responsibilities are all zero")
+                    help="also run accumulation steps whose responsibilities are all zero")
     ap.add_argument("--workload", default="iso_n1m_k1024_d128",
                     choices=sorted(WORKLOADS) + ["stream_em_n1b_k1024_d128"])
     ap.add_argument("--rows", type=int, default=0, help="override N of the streaming workload")
@@ -212,12 +216,14 @@ def main():
         args4 = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
         sig = torch.empty(K, D, device=dev)
         ws = torch.empty(int(L.fgmm_diag_workspace_bytes(N, K, D)), dtype=torch.uint8, device=dev)
-        fn = lambda ph: diag_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws, phase=ph)
+        fn = lambda ph, dense=args.dense: diag_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
+                                                          phase=ph, dense=dense)
     else:
         args4 = (inp["X"], inp["mu"], inp["prec_chol"], inp["log_pi"])
         sig = torch.empty(K, D, D, device=dev)
         ws = torch.empty(int(L.fgmm_full_workspace_bytes(N, K, D)), dtype=torch.uint8, device=dev)
-        fn = lambda ph: full_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws, phase=ph)
+        fn = lambda ph, dense=args.dense: full_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
+                                                          phase=ph, dense=dense)
     stream = torch.cuda.current_stream(dev)
 
     def step(ev=None):
@@ -254,7 +260,7 @@ def main():
     log(f"timed {args.steps} steps: {ms:.3f} ms/step (phase1 {p1:.3f} ms, phase2 {p2:.3f} ms)")
 
     dense_ms = None
-    if kind == "iso" and not args.dense:
+    if not args.dense:
         # The same steps with every accumulation step executed (identical outputs):
         # the dense cost, reported beside the default.
         for _ in range(2):
@@ -302,7 +308,7 @@ def main():
         "fraction_of_fp32_mfma_peak": step_tflops / PEAK_FP32_MFMA_TFLOPS,
         "step_tflops_algorithmic": step_tflops,
         "phase_ms": {"phase1": p1, "phase2": p2},
-        "accumulation": "dense" if (args.dense or kind != "iso") else
+        "accumulation": "dense" if args.dense else
                         "skips steps whose responsibilities are all exactly zero (bitwise-identical outputs)",
         "dense_ms_per_step": dense_ms if dense_ms is not None else (ms if args.dense else None),
         "dense_fraction_of_fp32_mfma_peak": (flop / (dense_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS)
@@ -319,9 +325,9 @@ def main():
             "avg_launch_ms": dom_ms,
         },
     }
-    if not args.no_cpu_baseline and kind == "iso":
+    if not args.no_cpu_baseline:
         log("timing the CPU baseline (bounded sample)")
-        out["cpu_baseline"] = cpu_baseline({k: v for k, v in inp.items()}, K, D)
+        out["cpu_baseline"] = cpu_baseline({k: v for k, v in inp.items()}, kind, K, D)
     print(json.dumps(out), flush=True)
 
 

@@ -246,7 +246,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(LDS ? kAccThreads : kThrea
 void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                 const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_lin, int KB, int KP,
                 const double* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
-                float* __restrict__ part_mu, float* __restrict__ part_sq, float* __restrict__ part_nk) {
+                float* __restrict__ part_mu, float* __restrict__ part_sq, float* __restrict__ part_nk,
+                int dense) {
   constexpr int NMX = DP / 8;
   constexpr int NM = 2 * NMX;
   constexpr int NJ = DP / 32;
@@ -304,14 +305,25 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   f32x4 stage[LPT];
   double rstage = INFINITY;
+  const bool full_d = (D == DP);
   auto fetch = [&](int t) {
     const int64_t row0 = r_begin + (int64_t)t * TR;
+    if (full_d && row0 + TR <= r_end) {
+      // Interior tile: no row or column masking.
+      const float* src = X + row0 * ldx;
 #pragma unroll
-    for (int q = 0; q < LPT; ++q) {
-      const int idx = q * NT + tid;
-      const int rr = idx / V4, c4 = idx % V4;
-      const int64_t row = row0 + rr;
-      stage[q] = load_row4(X, ldx, row, c4 * 4, D, row < r_end);
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * NT + tid;
+        stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * NT + tid;
+        const int rr = idx / V4, c4 = idx % V4;
+        const int64_t row = row0 + rr;
+        stage[q] = load_row4(X, ldx, row, c4 * 4, D, row < r_end);
+      }
     }
     if (tid < TR) {
       const int64_t row = row0 + tid;
@@ -371,11 +383,14 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int ro = 8 * (i >> 2) + (i & 3);
+        // Steps whose 64 responsibilities are all exactly zero add nothing.
+        if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const float xv = xbase[ro * RS + 32 * j];
-          accx[j] = mfma32(r[i], xv, accx[j]);
-          accq[j] = mfma32(r[i], xv * xv, accq[j]);
+          for (int j = 0; j < NJ; ++j) {
+            const float xv = xbase[ro * RS + 32 * j];
+            accx[j] = mfma32(r[i], xv, accx[j]);
+            accq[j] = mfma32(r[i], xv * xv, accq[j]);
+          }
         }
       }
     }
@@ -435,7 +450,7 @@ __global__ __launch_bounds__(256) void diag_fill(float* __restrict__ p, int64_t 
 
 template <int DP>
 hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
-                         float* logZ, bool run1, bool run2, hipStream_t stream) {
+                         float* logZ, bool run1, bool run2, bool dense, hipStream_t stream) {
   const f32x4* mu_sw = reinterpret_cast<const f32x4*>(ws + pl.off_musw);
   const double* kc_blk = reinterpret_cast<const double*>(ws + pl.off_kcblk);
   const double* kc_lin = reinterpret_cast<const double*>(ws + pl.off_kclin);
@@ -463,7 +478,7 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
                      kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
                      reinterpret_cast<float*>(ws + pl.off_part_mu),
                      reinterpret_cast<float*>(ws + pl.off_part_sq),
-                     reinterpret_cast<float*>(ws + pl.off_part_nk));
+                     reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -485,6 +500,7 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   const bool want_logz = !(flags & FGMM_FLAG_NO_LOGZ);
   const bool accumulate = (flags & FGMM_FLAG_ACCUMULATE) != 0;
+  const bool dense = (flags & FGMM_FLAG_DENSE) != 0;
   if (N < 0 || K < 0 || D < 1) return FGMM_ERR_INVALID_ARG;
   if (N > 0 && (X == nullptr || ldx < round_up(D, 4) || (ldx % 4) != 0 ||
                 (reinterpret_cast<uintptr_t>(X) & 15) != 0))
@@ -516,10 +532,10 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   if (N > 0) {
     hipError_t e = hipSuccess;
     switch (pl.DP) {
-      case 32: e = launch_passes<32>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
-      case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
-      case 96: e = launch_passes<96>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
-      case 128: e = launch_passes<128>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 32: e = launch_passes<32>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 96: e = launch_passes<96>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 128: e = launch_passes<128>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       default: return FGMM_ERR_UNSUPPORTED;
     }
     if (e != hipSuccess) return FGMM_ERR_HIP;

@@ -246,7 +246,7 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                 const f32x4* __restrict__ lsw, const double* __restrict__ bsw,
                 const double* __restrict__ ck, int K, int KP, const double* __restrict__ rowstat,
                 int nslab, int64_t rows_per_slab, float* __restrict__ part_sig,
-                float* __restrict__ part_mu, float* __restrict__ part_nk) {
+                float* __restrict__ part_mu, float* __restrict__ part_nk, int dense) {
   constexpr int NMB = DP / 32, NM = DP / 8, NSB = NMB * (NMB + 1) / 2;
   constexpr int RS = DP + 4, V4 = DP / 4;
   constexpr int BLK = NMB * NM * 64;
@@ -299,14 +299,25 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   f32x4 stage[LPT];
   double rstage = INFINITY;
+  const bool full_d = (D == DP);
   auto fetch = [&](int t) {
     const int64_t row0 = r_begin + (int64_t)t * TR;
+    if (full_d && row0 + TR <= r_end) {
+      // Interior tile: no row or column masking.
+      const float* src = X + row0 * ldx;
 #pragma unroll
-    for (int q = 0; q < LPT; ++q) {
-      const int idx = q * kAccThreads + tid;
-      const int rr = idx / V4, c4 = idx % V4;
-      const int64_t row = row0 + rr;
-      stage[q] = load_row4(X, ldx, row, c4 * 4, D, row < r_end);
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        const int rr = idx / V4, c4 = idx % V4;
+        const int64_t row = row0 + rr;
+        stage[q] = load_row4(X, ldx, row, c4 * 4, D, row < r_end);
+      }
     }
     if (tid < TR) {
       const int64_t row = row0 + tid;
@@ -358,6 +369,8 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       for (int s = 0; s < 16; ++s) {
         const int row = acc_row(s, g);
         const float rr = rx[row];
+        // A step whose two rows have zero responsibility adds nothing.
+        if (!dense && __builtin_amdgcn_ballot_w64(rr != 0.0f) == 0) continue;
         float xv[NMB], av[NMB];
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb) {
@@ -455,7 +468,7 @@ __global__ __launch_bounds__(256) void full_fill(float* __restrict__ p, int64_t 
 
 template <int DP>
 hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
-                         float* logZ, bool run1, bool run2, hipStream_t stream) {
+                         float* logZ, bool run1, bool run2, bool dense, hipStream_t stream) {
   const f32x4* lsw = reinterpret_cast<const f32x4*>(ws + pl.off_lsw);
   const double* bsw = reinterpret_cast<const double*>(ws + pl.off_bsw);
   const double* ck = reinterpret_cast<const double*>(ws + pl.off_ck);
@@ -476,7 +489,7 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
                      stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, rowstat, pl.nslab,
                      pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_sig),
                      reinterpret_cast<float*>(ws + pl.off_part_mu),
-                     reinterpret_cast<float*>(ws + pl.off_part_nk));
+                     reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -498,6 +511,7 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   const bool want_logz = !(flags & FGMM_FLAG_NO_LOGZ);
   const bool accumulate = (flags & FGMM_FLAG_ACCUMULATE) != 0;
+  const bool dense = (flags & FGMM_FLAG_DENSE) != 0;
   if (N < 0 || K < 0 || D < 1) return FGMM_ERR_INVALID_ARG;
   if (N > 0 && (X == nullptr || ldx < round_up(D, 4) || (ldx % 4) != 0 ||
                 (reinterpret_cast<uintptr_t>(X) & 15) != 0))
@@ -529,8 +543,8 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   if (N > 0) {
     hipError_t e = hipSuccess;
     switch (pl.DP) {
-      case 32: e = launch_passes<32>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
-      case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, stream); break;
+      case 32: e = launch_passes<32>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       default: return FGMM_ERR_UNSUPPORTED;
     }
     if (e != hipSuccess) return FGMM_ERR_HIP;

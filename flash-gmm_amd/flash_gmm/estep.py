@@ -178,7 +178,7 @@ def flash_gmm_estep(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tenso
 
 def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
                     accumulate: bool = False, workspace: torch.Tensor | None = None,
-                    phase: int = 0) -> None:
+                    phase: int = 0, dense: bool = False) -> None:
     """Diagonal-covariance E-step into caller-provided outputs (sig_acc is (K, D))."""
     _check_common(X, mu, log_pi)
     N, D = X.shape
@@ -196,6 +196,8 @@ def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     _require(hasattr(L, "fgmm_diag_estep_f32"), "library built without the diagonal E-step")
     workspace = _workspace(L.fgmm_diag_workspace_bytes, N, K, D, dev, workspace)
     flags = _flags(accumulate, logZ, False, phase)
+    if dense:
+        flags |= _lib.FLAG_DENSE
     _check_out("Nk", Nk, (K,), dev)
     _check_out("mu_acc", mu_acc, (K, D), dev)
     _check_out("sig_acc", sig_acc, (K, D), dev)
@@ -232,7 +234,7 @@ def flash_gmm_estep_diag(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.
 
 def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
                     accumulate: bool = False, workspace: torch.Tensor | None = None,
-                    phase: int = 0) -> None:
+                    phase: int = 0, dense: bool = False) -> None:
     """Full-covariance E-step into caller-provided outputs (sig_outer is (K, D, D))."""
     _check_common(X, mu, log_pi)
     N, D = X.shape
@@ -249,6 +251,8 @@ def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
     _require(hasattr(L, "fgmm_full_estep_f32"), "library built without the full-covariance E-step")
     workspace = _workspace(L.fgmm_full_workspace_bytes, N, K, D, dev, workspace)
     flags = _flags(accumulate, logZ, False, phase)
+    if dense:
+        flags |= _lib.FLAG_DENSE
     _check_out("Nk", Nk, (K,), dev)
     _check_out("mu_acc", mu_acc, (K, D), dev)
     _check_out("sig_outer", sig_outer, (K, D, D), dev)

@@ -43,6 +43,24 @@ def test_edge_shapes(N, K, D, gpu_device):
     assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), f"diag N={N} K={K} D={D}")
 
 
+@pytest.mark.parametrize("N,K,D,seed", [(9000, 512, 96, 2), (3001, 77, 45, 3)])
+def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, gpu_device):
+    """Skipping all-zero responsibility steps changes no bit of any output."""
+    inp = data.diag_clustered(N, K, D, seed=seed)
+    dev = gpu_device
+    args = [inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
+    outs = []
+    for dense in (False, True):
+        o = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+             torch.empty(K, D, device=dev)]
+        diag_estep_into(*args, *o, dense=dense)
+        outs.append(o)
+    torch.cuda.synchronize()
+    for u, v in zip(*outs):
+        assert torch.equal(u, v)
+    assert_close_stats(outs[0], oracle(inp), "diag skip")
+
+
 def test_equal_variances_match_isotropic(gpu_device):
     inp = data.iso_clustered(3000, 50, 40, seed=12)
     dev = gpu_device

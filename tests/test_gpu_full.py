@@ -62,6 +62,24 @@ def test_diagonal_factor_matches_diag_entry(gpu_device):
     torch.testing.assert_close(s, a[3], rtol=1e-3, atol=1e-3 * float(a[3].abs().max()))
 
 
+@pytest.mark.parametrize("N,K,D,seed", [(6000, 128, 64, 3), (2501, 19, 29, 4)])
+def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, gpu_device):
+    """Skipping all-zero responsibility steps changes no bit of any output."""
+    inp = data.full_clustered(N, K, D, seed=seed)
+    dev = gpu_device
+    args = [inp[k].to(dev) for k in KEYS]
+    outs = []
+    for dense in (False, True):
+        o = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+             torch.empty(K, D, D, device=dev)]
+        full_estep_into(*args, *o, dense=dense)
+        outs.append(o)
+    torch.cuda.synchronize()
+    for u, v in zip(*outs):
+        assert torch.equal(u, v)
+    assert_close_stats(outs[0], oracle(inp), "full skip")
+
+
 def test_accumulate_over_chunks(gpu_device):
     inp = data.full_clustered(5000, 16, 32, seed=16)
     dev = gpu_device
