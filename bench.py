@@ -73,6 +73,14 @@ def cpu_baseline(inp, kind, K, D, min_s=10.0, max_s=30.0, rows=16384):
     }
 
 
+# HBM bytes per launch of each pass's main kernel: rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE (separate runs) on this bench command, scaled by what the counters
+# read for a 512 MiB device copy (x2.0 for FETCH_SIZE, x1.0 for WRITE_SIZE); the
+# counter values and commands are in profiles/<kind>_estep_<shape>.md.
+TRAFFIC_BYTES = {
+    "iso_n1m_k1024_d128": {"phase1": 589_618_790, "phase2": 566_709_248},
+}
+
 WORKLOADS = {
     # name: (N, K, D)
     "iso_n1m_k1024_d128": (1_000_000, 1024, 128),
@@ -182,6 +190,9 @@ def main():
     ap.add_argument("--workload", default="iso_n1m_k1024_d128",
                     choices=sorted(WORKLOADS) + ["stream_em_n1b_k1024_d128"])
     ap.add_argument("--rows", type=int, default=0, help="override N of the streaming workload")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a device-to-device copy of MIB MiB five times (scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures a single GPU; --gpus {args.gpus} is not supported "
@@ -191,6 +202,16 @@ def main():
 
     if args.workload.startswith("stream_em"):
         stream_main(args)
+        return
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration * (1 << 20) // 4
+        a = torch.ones(n, device="cuda:0")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n * 4, "launches": 5}), flush=True)
         return
 
     import torch
@@ -280,9 +301,10 @@ def main():
              "diag": ("diag_lse (log-normaliser pass + prologue)", "diag_accum (accumulation pass + slab reduction)"),
              "full": ("full_lse (log-normaliser pass + prologue)", "full_accum (accumulation pass + slab reduction)")}[kind]
     if p2 >= p1:
-        dom, dom_ms, dom_flop = names[1], p2, f2
+        dom, dom_ms, dom_flop, dom_phase = names[1], p2, f2, "phase2"
     else:
-        dom, dom_ms, dom_flop = names[0], p1, f1
+        dom, dom_ms, dom_flop, dom_phase = names[0], p1, f1, "phase1"
+    traffic = TRAFFIC_BYTES.get(args.workload, {}).get(dom_phase)
     dom_tflops = dom_flop / (dom_ms * 1e-3) / 1e12
 
     out = {
@@ -320,7 +342,8 @@ def main():
             "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s",
             "frac": dom_tflops / PEAK_FP32_MFMA_TFLOPS,
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_unit": "bytes per launch (HBM read + write, rocprofv3 counters)",
             "algorithmic_flop_per_launch": dom_flop,
             "avg_launch_ms": dom_ms,
         },

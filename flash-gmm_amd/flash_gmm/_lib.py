@@ -20,6 +20,7 @@ FGMM_ERR_INVALID_ARG = -1
 FGMM_ERR_UNSUPPORTED = -2
 FGMM_ERR_WORKSPACE = -3
 FGMM_ERR_HIP = -4
+FGMM_ERR_SOURCE = -5
 
 FLAG_ACCUMULATE = 1 << 0
 FLAG_NO_LOGZ = 1 << 1
@@ -62,7 +63,7 @@ def _declare(lib):
         _p, _p, _p, _p,                # logZ, Nk, mu_acc, sig_acc
         _p, _sz, _u32, _p,             # workspace, bytes, flags, stream
     ]
-    optional = {
+    decls = {
         "fgmm_diag_workspace_bytes": (_sz, [_i64, _i64, _i64]),
         "fgmm_diag_estep_f32": (ctypes.c_int, [
             _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p,
@@ -71,14 +72,13 @@ def _declare(lib):
         "fgmm_full_estep_f32": (ctypes.c_int, [
             _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p,
             _p, _p, _p, _p, _p, _sz, _u32, _p]),
-        "fgmm_iso_mstep_f32": (ctypes.c_int, [
-            _p, _p, _p, _i64, _i64, _i64, ctypes.c_double, _p, _p, _p, _u32, _p]),
+        # The EM entry points (fgmm_iso_mstep_f32, fgmm_stream_em_iso,
+        # fgmm_synth_iso_source) are declared in em.py next to their structs.
     }
-    for name, (res, args) in optional.items():
-        if hasattr(lib, name):
-            fn = getattr(lib, name)
-            fn.restype = res
-            fn.argtypes = args
+    for name, (res, args) in decls.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
     return lib
 
 
