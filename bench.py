@@ -86,6 +86,8 @@ WORKLOADS = {
     "iso_n1m_k1024_d128": (1_000_000, 1024, 128),
     "diag_n1m_k1024_d96": (1_000_000, 1024, 96),
     "full_n250k_k256_d64": (250_000, 256, 64),
+    "diag_n1m_k256_d256": (1_000_000, 256, 256),
+    "full_n100k_k64_d128": (100_000, 64, 128),
 }
 
 

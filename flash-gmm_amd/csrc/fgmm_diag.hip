@@ -35,10 +35,19 @@ constexpr int kRowGroups = 2;
 // 64-row X buffers fit in LDS.
 __host__ __device__ constexpr bool diag_accum_uses_lds(int DP) { return DP <= 96; }
 
+// Above D = 128 the dimensions are split over two waves per component block in
+// pass 2 (diag_accum_split), so D is padded to a multiple of 64 there.
+__host__ __device__ constexpr bool diag_accum_split_d(int DP) { return DP > 128; }
+__host__ inline int diag_padded_dim(int64_t D) {
+  return D <= 128 ? (int)round_up(D < 1 ? 1 : D, 32) : (int)round_up(D, 64);
+}
+
 struct DiagPlan {
   int64_t N, K, D;
-  int DP, FP;   // D padded to 32; feature count 2*DP
-  int KB, KP, ncg, nslab, rgroups, npart;
+  int DP, FP;   // D padded (32 up to 128, then 64); feature count 2*DP
+  int KB, KP;
+  int cpg;      // component blocks per pass-2 workgroup
+  int ncg, nslab, rgroups, npart;
   int64_t rows_per_slab;
   size_t off_musw, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_sq, off_part_nk, total;
 };
@@ -46,11 +55,12 @@ struct DiagPlan {
 DiagPlan make_plan(int64_t N, int64_t K, int64_t D) {
   DiagPlan p{};
   p.N = N; p.K = K; p.D = D;
-  p.DP = (int)round_up(D < 1 ? 1 : D, 32);
+  p.DP = diag_padded_dim(D);
   p.FP = 2 * p.DP;
   p.KB = (int)cdiv(K, 32);
   p.KP = p.KB * 32;
-  p.ncg = (int)cdiv(p.KB, kWaves);
+  p.cpg = diag_accum_split_d(p.DP) ? kWaves / 2 : kWaves;
+  p.ncg = (int)cdiv(p.KB, p.cpg);
   p.rgroups = diag_accum_uses_lds(p.DP) ? kRowGroups : 1;
   const int64_t tile_rows = 32 * p.rgroups;
   if (N > 0 && p.ncg > 0) {
@@ -414,6 +424,183 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Pass 2 for D > 128: four waves = 2 component blocks x 2 halves of the
+// dimensions.  Each wave keeps the features [-w | 2v] of its half resident in
+// registers and forms the partial contraction over that half (accurate fp64
+// form); the two halves are exchanged through LDS and summed in a fixed order,
+// so both waves of a component block hold the same log-joint and r.  Each wave
+// then accumulates r^T [x | x^2] for the columns of its own half.
+// ---------------------------------------------------------------------------
+template <int DP>
+constexpr size_t accum_split_lds_bytes() {
+  return (size_t)2 * 32 * (DP + 4) * sizeof(float)      // X, 2 buffers of 32 rows
+         + (size_t)2 * 32 * sizeof(double)               // row logZ2, 2 buffers
+         + (size_t)kWaves * 16 * 64 * sizeof(double);    // partial contractions
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(1, 1)))
+void diag_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                      const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_lin, int KB,
+                      int KP, const double* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
+                      float* __restrict__ part_mu, float* __restrict__ part_sq,
+                      float* __restrict__ part_nk, int dense) {
+  constexpr int HD = DP / 2;           // dimensions per wave
+  constexpr int NMX = DP / 8;          // x^2 chunks of the full feature vector
+  constexpr int NMH = HD / 8;          // chunks per half, per feature kind
+  constexpr int NMW = 2 * NMH;         // chunks per wave
+  constexpr int NJH = HD / 32;         // 32-column accumulator tiles per wave
+  constexpr int RS = DP + 4;
+  constexpr int V4 = DP / 4;
+  constexpr int LPT = (32 * V4) / kThreads;
+  static_assert(HD % 32 == 0 && (32 * V4) % kThreads == 0, "split shape");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  float* xs = reinterpret_cast<float*>(lds_raw);                                           // [2][32*RS]
+  double* rs = reinterpret_cast<double*>(lds_raw + 2 * 32 * RS * sizeof(float));          // [2][32]
+  double* ex = reinterpret_cast<double*>(lds_raw + 2 * 32 * RS * sizeof(float) +
+                                         2 * 32 * sizeof(double));                        // [4][16][64]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int cb = wave >> 1, h = wave & 1;
+  const int slab = blockIdx.x % nslab;
+  const int cg = blockIdx.x / nslab;
+  const int kb = cg * 2 + cb;
+  const bool active = kb < KB;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
+
+  // This wave's features: x^2 chunks then x chunks of dimensions [h*HD, (h+1)*HD).
+  f32x4 mub[NMW];
+#pragma unroll
+  for (int m = 0; m < NMW; ++m) {
+    const int mg = m < NMH ? h * NMH + m : NMX + h * NMH + (m - NMH);
+    mub[m] = active ? mu_sw[((int64_t)kb * 2 * NMX + mg) * 64 + lane] : zero4();
+  }
+  const double Ck = active ? kc_lin[(int64_t)kb * 32 + c] : -INFINITY;
+
+  f32x16 accx[NJH], accq[NJH];
+#pragma unroll
+  for (int j = 0; j < NJH; ++j) {
+    accx[j] = zero16();
+    accq[j] = zero16();
+  }
+  float nk = 0.0f;
+
+  f32x4 stage[LPT];
+  double rstage = INFINITY;
+  const bool full_d = (D == DP);
+  auto fetch = [&](int t) {
+    const int64_t row0 = r_begin + (int64_t)t * 32;
+    if (full_d && row0 + 32 <= r_end) {
+      const float* src = X + row0 * ldx;
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kThreads + tid;
+        stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kThreads + tid;
+        const int64_t row = row0 + idx / V4;
+        stage[q] = load_row4(X, ldx, row, (idx % V4) * 4, D, row < r_end);
+      }
+    }
+    if (tid < 32) {
+      const int64_t row = row0 + tid;
+      rstage = (row < r_end) ? rowstat[row] : INFINITY;
+    }
+  };
+  auto commit = [&](int buf) {
+    float* dst = xs + buf * 32 * RS;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kThreads + tid;
+      *reinterpret_cast<f32x4*>(dst + (idx / V4) * RS + (idx % V4) * 4) = stage[q];
+    }
+    if (tid < 32) rs[buf * 32 + tid] = rstage;
+  };
+
+  if (ntiles > 0) {
+    fetch(0);
+    commit(0);
+  }
+  __syncthreads();
+
+  double* my_ex = ex + (size_t)wave * 16 * 64 + lane;
+  const double* ex0 = ex + (size_t)(cb * 2) * 16 * 64 + lane;
+  const double* ex1 = ex + (size_t)(cb * 2 + 1) * 16 * 64 + lane;
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    const float* xt = xs + buf * 32 * RS;
+    const double* rt = rs + buf * 32;
+    if (active) {
+      double xm[16];
+      const float* xrow = xt + c * RS + h * HD + 4 * g;
+      cross_tile<NMW>(
+          xm,
+          [&](int m) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(xrow + 8 * (m < NMH ? m : m - NMH));
+            return m < NMH ? sq4(v) : v;
+          },
+          [&](int m) { return mub[m]; });
+#pragma unroll
+      for (int i = 0; i < 16; ++i) my_ex[i * 64] = xm[i];
+    }
+    __syncthreads();
+    if (more) fetch(t + 1);
+    if (active) {
+      float r[16];
+      const double* rbase = rt + 4 * g;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ro = 8 * (i >> 2) + (i & 3);
+        const double xm = ex0[i * 64] + ex1[i * 64];   // same order in both halves
+        const float rv = fast_exp2((float)((Ck - rbase[ro]) + xm));
+        nk += rv;
+        r[i] = rv;
+      }
+      const float* xbase = xt + 4 * g * RS + h * HD + c;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ro = 8 * (i >> 2) + (i & 3);
+        if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
+#pragma unroll
+          for (int j = 0; j < NJH; ++j) {
+            const float xv = xbase[ro * RS + 32 * j];
+            accx[j] = mfma32(r[i], xv, accx[j]);
+            accq[j] = mfma32(r[i], xv * xv, accq[j]);
+          }
+        }
+      }
+    }
+    if (more) commit(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (active) {
+    nk += __shfl_xor(nk, 32);
+    const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+#pragma unroll
+    for (int j = 0; j < NJH; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t o = (kbase + acc_row(i, g)) * DP + h * HD + 32 * j + c;
+        part_mu[o] = accx[j][i];
+        part_sq[o] = accq[j][i];
+      }
+    }
+    if (g == 0 && h == 0) part_nk[kbase + c] = nk;
+  }
+}
+
 // Finish: one thread per (k, d); fixed-order fp64 sums over partials, then the
 // sig identity in fp64.  Thread d == 0 also writes Nk.
 __global__ __launch_bounds__(256) void diag_reduce(const float* __restrict__ part_mu,
@@ -466,20 +653,35 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
                        stream, X, ldx, pl.N, (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
   }
   if (!run2) return hipGetLastError();
-  constexpr bool L = diag_accum_uses_lds(DP);
-  constexpr size_t lds2 = accum_lds_bytes<DP, L>();
-  if (lds2 > 65536) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum<DP, L>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
-    if (e != hipSuccess) return e;
+  if constexpr (diag_accum_split_d(DP)) {
+    constexpr size_t lds2 = accum_split_lds_bytes<DP>();
+    if (lds2 > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum_split<DP>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(diag_accum_split<DP>, dim3((unsigned)(pl.nslab * pl.ncg)), dim3(kThreads),
+                       lds2, stream, X, ldx, pl.N, (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat,
+                       pl.nslab, pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_mu),
+                       reinterpret_cast<float*>(ws + pl.off_part_sq),
+                       reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
+    return hipGetLastError();
+  } else {
+    constexpr bool L = diag_accum_uses_lds(DP);
+    constexpr size_t lds2 = accum_lds_bytes<DP, L>();
+    if (lds2 > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum<DP, L>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((diag_accum<DP, L>), dim3((unsigned)(pl.nslab * pl.ncg)),
+                       dim3(L ? kAccThreads : kThreads), lds2, stream, X, ldx, pl.N, (int)pl.D, mu_sw,
+                       kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
+                       reinterpret_cast<float*>(ws + pl.off_part_mu),
+                       reinterpret_cast<float*>(ws + pl.off_part_sq),
+                       reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
+    return hipGetLastError();
   }
-  hipLaunchKernelGGL((diag_accum<DP, L>), dim3((unsigned)(pl.nslab * pl.ncg)),
-                     dim3(L ? kAccThreads : kThreads), lds2, stream, X, ldx, pl.N, (int)pl.D, mu_sw,
-                     kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
-                     reinterpret_cast<float*>(ws + pl.off_part_mu),
-                     reinterpret_cast<float*>(ws + pl.off_part_sq),
-                     reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
-  return hipGetLastError();
 }
 
 }  // namespace
@@ -509,7 +711,7 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   if (K > 0 && (mu == nullptr || ldmu < D || log_sigma_sq == nullptr || ldlss < D ||
                 log_pi == nullptr || Nk == nullptr || mu_acc == nullptr || sig_acc == nullptr))
     return FGMM_ERR_INVALID_ARG;
-  if (D > 128) return FGMM_ERR_UNSUPPORTED;
+  if (D > 256) return FGMM_ERR_UNSUPPORTED;
   if (N > (int64_t)1 << 40 || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
   const DiagPlan pl = make_plan(N, K, D);
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
@@ -536,6 +738,8 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
       case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       case 96: e = launch_passes<96>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       case 128: e = launch_passes<128>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 192: e = launch_passes<192>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 256: e = launch_passes<256>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       default: return FGMM_ERR_UNSUPPORTED;
     }
     if (e != hipSuccess) return FGMM_ERR_HIP;

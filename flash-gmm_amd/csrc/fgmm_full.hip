@@ -1,4 +1,4 @@
-// Full-covariance GMM E-step for gfx950 (1 <= D <= 64).
+// Full-covariance GMM E-step for gfx950 (1 <= D <= 128).
 //
 // Math (reference: flash_gmm_full_h100.py:289-296 constants, :103-130 pass 1,
 // :171-228 pass 2), with L_k lower-triangular, L_k L_k^T = Sigma_k^-1, in log2 units:
@@ -19,6 +19,12 @@
 // sum_rows (r x)(x^T) on MFMA with the r-scaled rows as the A operand.  Only the
 // upper 32x32 blocks (d1 block <= d2 block) are accumulated; the finish mirrors
 // them.  mu_acc is the running sum of the same r-scaled operands.
+//
+// Above D = 64 one component's L^T no longer fits LDS four times over, so pass 2
+// (full_accum_split) runs one component per 4-wave workgroup: wave w whitens the
+// w-th 32-row block of V^T, the partial ||v - b||^2 of the blocks are summed in a
+// fixed order through LDS, and the upper sig_outer blocks are dealt out over the
+// four waves.
 
 #include "fgmm_common.hpp"
 
@@ -35,13 +41,16 @@ constexpr int kAccThreads = 64 * kAccWaves;
 constexpr int kCompsPerWG = 4;
 constexpr int kRowGroups = 2;
 
+// Pass 2 splits one component over the waves of a workgroup above D = 64.
+__host__ __device__ constexpr bool full_accum_split_d(int DP) { return DP > 64; }
+
 struct FullPlan {
   int64_t N, K, D;
   int DP;       // D padded to 32
   int NMB;      // 32-row blocks of V^T (DP / 32)
   int NSB;      // upper 32x32 blocks of sig_outer: NMB*(NMB+1)/2
   int KP;       // K padded to kCompsPerWG
-  int ncg, nslab, npart;
+  int ncg, nslab, rgroups, npart;
   int64_t rows_per_slab;
   size_t off_lsw, off_bsw, off_ck, off_rowstat, off_part_sig, off_part_mu, off_part_nk, total;
 };
@@ -53,8 +62,10 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D) {
   p.NMB = p.DP / 32;
   p.NSB = p.NMB * (p.NMB + 1) / 2;
   p.KP = (int)round_up(K, kCompsPerWG);
-  p.ncg = p.KP / kCompsPerWG;
-  const int64_t tile_rows = 32 * kRowGroups;
+  const bool split = full_accum_split_d(p.DP);
+  p.ncg = split ? (int)K : p.KP / kCompsPerWG;
+  p.rgroups = split ? 1 : kRowGroups;
+  const int64_t tile_rows = 32 * p.rgroups;
   if (N > 0 && p.ncg > 0) {
     int64_t want = (int64_t)kCUs / p.ncg;
     if (want >= 8) want = (want / 8) * 8;
@@ -67,7 +78,7 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D) {
     p.rows_per_slab = tile_rows;
     p.nslab = 0;
   }
-  p.npart = p.nslab * kRowGroups;
+  p.npart = p.nslab * p.rgroups;
   size_t off = 0;
   p.off_lsw = off;      off = align256(off + (size_t)p.KP * p.DP * p.DP * sizeof(float));
   p.off_bsw = off;      off = align256(off + (size_t)p.KP * p.DP * sizeof(double));
@@ -90,17 +101,17 @@ __global__ __launch_bounds__(64) void full_prep(const float* __restrict__ mu, in
                                                 const float* __restrict__ L, int64_t K, int D, int DP,
                                                 const float* __restrict__ lpi, f32x4* __restrict__ lsw,
                                                 double* __restrict__ bsw, double* __restrict__ ck) {
-  __shared__ double sb[64];
+  __shared__ double sb[128];   // DP <= 128
   const int64_t k = blockIdx.x;
   const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
   const bool valid = k < K;
   const float* Lk = L + k * (int64_t)D * D;
-  // b_j = sum_i L[i][j] mu_i  (one j per lane)
-  if (lane < DP) {
+  // b_j = sum_i L[i][j] mu_i  (j = lane, lane + 64)
+  for (int j = lane; j < DP; j += 64) {
     double b = 0.0;
-    if (valid && lane < D)
-      for (int i = 0; i < D; ++i) b = fma((double)Lk[(int64_t)i * D + lane], (double)mu[k * ldmu + i], b);
-    sb[lane] = b;
+    if (valid && j < D)
+      for (int i = 0; i < D; ++i) b = fma((double)Lk[(int64_t)i * D + j], (double)mu[k * ldmu + i], b);
+    sb[j] = b;
   }
   if (lane == 0) {
     double c0 = -INFINITY;
@@ -162,7 +173,8 @@ constexpr size_t lse_lds_bytes() {
 }
 
 template <int DP>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(DP <= 64 ? 2 : 1, DP <= 64 ? 2 : 1)))
 void full_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
               const f32x4* __restrict__ lsw, const double* __restrict__ bsw,
               const double* __restrict__ ck, int K, float* __restrict__ logZ,
@@ -413,6 +425,189 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Pass 2 for D > 64: one component per workgroup of 4 waves.
+// ---------------------------------------------------------------------------
+template <int DP>
+constexpr size_t accum_split_lds_bytes() {
+  return (size_t)DP * DP * sizeof(float)               // L^T operands of the component
+         + (size_t)(DP + 8) * sizeof(double)           // b, c
+         + (size_t)2 * 32 * (DP + 4) * sizeof(float)   // X tiles
+         + (size_t)2 * 32 * sizeof(double)             // logZ2
+         + (size_t)kWaves * 32 * sizeof(double)        // per-block ||v - b||^2
+         + (size_t)kWaves * 32 * sizeof(float);        // r, one copy per wave
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(1, 1)))
+void full_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                      const f32x4* __restrict__ lsw, const double* __restrict__ bsw,
+                      const double* __restrict__ ck, int K, int KP, const double* __restrict__ rowstat,
+                      int nslab, int64_t rows_per_slab, float* __restrict__ part_sig,
+                      float* __restrict__ part_mu, float* __restrict__ part_nk, int dense) {
+  constexpr int NMB = DP / 32, NM = DP / 8, NSB = NMB * (NMB + 1) / 2;
+  constexpr int RS = DP + 4, V4 = DP / 4;
+  constexpr int BLK = NMB * NM * 64;
+  constexpr int BW = DP + 8;
+  constexpr int LPT = (32 * V4) / kThreads;
+  constexpr int MPT = BLK / kThreads;
+  constexpr int SPW = (NSB + kWaves - 1) / kWaves;   // sig blocks per wave
+  static_assert(NMB <= kWaves && (32 * V4) % kThreads == 0 && BLK % kThreads == 0, "split shape");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  unsigned char* p = lds_raw;
+  f32x4* l_l = reinterpret_cast<f32x4*>(p);   p += BLK * sizeof(f32x4);
+  double* b_l = reinterpret_cast<double*>(p); p += BW * sizeof(double);
+  float* xs = reinterpret_cast<float*>(p);    p += 2 * 32 * RS * sizeof(float);
+  double* rs = reinterpret_cast<double*>(p);  p += 2 * 32 * sizeof(double);
+  double* qx = reinterpret_cast<double*>(p);  p += kWaves * 32 * sizeof(double);
+  float* r_l = reinterpret_cast<float*>(p);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int slab = blockIdx.x % nslab;
+  const int k = blockIdx.x / nslab;
+  if (k >= K) return;   // whole workgroup: no barrier is left waiting
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
+
+#pragma unroll
+  for (int q = 0; q < MPT; ++q) l_l[q * kThreads + tid] = lsw[(int64_t)k * BLK + q * kThreads + tid];
+  for (int idx = tid; idx < BW; idx += kThreads)
+    b_l[idx] = idx < DP ? bsw[(int64_t)k * DP + idx] : (idx == DP ? ck[k] : 0.0);
+
+  // Upper block sb of sig_outer <-> (m1 <= m2); wave w owns sb = w, w + 4, ...
+  f32x16 acc[SPW];
+  int bm1[SPW], bm2[SPW];
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    acc[j] = zero16();
+    int sb = wave + kWaves * j, m1 = 0;
+    while (sb >= NMB - m1 && m1 < NMB) { sb -= NMB - m1; ++m1; }
+    bm1[j] = m1;
+    bm2[j] = m1 + sb;   // m1 == NMB marks "no block" (sb index past NSB)
+  }
+  float mua = 0.0f, nk = 0.0f;
+
+  f32x4 stage[LPT];
+  double rstage = INFINITY;
+  const bool full_d = (D == DP);
+  auto fetch = [&](int t) {
+    const int64_t row0 = r_begin + (int64_t)t * 32;
+    if (full_d && row0 + 32 <= r_end) {
+      const float* src = X + row0 * ldx;
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kThreads + tid;
+        stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kThreads + tid;
+        const int64_t row = row0 + idx / V4;
+        stage[q] = load_row4(X, ldx, row, (idx % V4) * 4, D, row < r_end);
+      }
+    }
+    if (tid < 32) {
+      const int64_t row = row0 + tid;
+      rstage = (row < r_end) ? rowstat[row] : INFINITY;
+    }
+  };
+  auto commit = [&](int buf) {
+    float* dst = xs + buf * 32 * RS;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kThreads + tid;
+      *reinterpret_cast<f32x4*>(dst + (idx / V4) * RS + (idx % V4) * 4) = stage[q];
+    }
+    if (tid < 32) rs[buf * 32 + tid] = rstage;
+  };
+
+  if (ntiles > 0) {
+    fetch(0);
+    commit(0);
+  }
+  __syncthreads();
+
+  const double hl = 0.5 * kLog2e;
+  float* rx = r_l + wave * 32;
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    const float* xt = xs + buf * 32 * RS;
+    const double* rt = rs + buf * 32;
+    if (wave < NMB) {
+      // Block `wave` of V^T = L^T X^T for the tile; this lane's row is c.
+      double v[16];
+      const f32x4* la = l_l + wave * NM * 64 + lane;
+      const float* xrow = xt + c * RS + 4 * g;
+      cross_tile<NM>(v, [&](int m) { return la[m * 64]; },
+                     [&](int m) { return *reinterpret_cast<const f32x4*>(xrow + 8 * m); });
+      const double* bb = b_l + wave * 32 + g * 16;
+      double q = 0.0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const double d = v[i] - bb[i];
+        q = fma(d, d, q);
+      }
+      q += __shfl_xor(q, 32);
+      if (g == 0) qx[wave * 32 + c] = q;
+    }
+    __syncthreads();
+    {
+      double maha = 0.0;
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) maha += qx[mb * 32 + c];   // same order in every wave
+      const float rv = fast_exp2((float)((b_l[DP] - rt[c]) - hl * maha));
+      if (g == 0) {
+        rx[c] = rv;
+        if (wave == 0) nk += rv;
+      }
+    }
+    if (more) fetch(t + 1);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int row = acc_row(s, g);
+      const float rr = rx[row];
+      if (!dense && __builtin_amdgcn_ballot_w64(rr != 0.0f) == 0) continue;
+      const float* xr = xt + row * RS + c;
+      if (wave < NMB) mua += rr * xr[32 * wave];
+#pragma unroll
+      for (int j = 0; j < SPW; ++j) {
+        if (bm1[j] < NMB) acc[j] = mfma32(rr * xr[32 * bm1[j]], xr[32 * bm2[j]], acc[j]);
+      }
+    }
+    if (more) commit(buf ^ 1);
+    __syncthreads();
+  }
+
+  const int64_t pbase = (int64_t)slab * KP + k;
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    if (bm1[j] < NMB) {
+      const int sb = wave + kWaves * j;
+      float* ps = part_sig + (pbase * NSB + sb) * 1024;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) ps[acc_row(i, g) * 32 + c] = acc[j][i];
+    }
+  }
+  if (wave < NMB) {
+    const float v = mua + __shfl_xor(mua, 32);
+    if (g == 0) part_mu[pbase * DP + 32 * wave + c] = v;
+  }
+  if (wave == 0) {
+    float nks = nk;
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) nks += __shfl_xor(nks, o);
+    if (lane == 0) part_nk[pbase] = nks;
+  }
+}
+
 // Finish: one thread per (k, d1, d2) of sig_outer plus (k, d) of mu_acc and k of Nk.
 __global__ __launch_bounds__(256) void full_reduce(const float* __restrict__ part_sig,
                                                    const float* __restrict__ part_mu,
@@ -475,21 +670,40 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
   double* rowstat = reinterpret_cast<double*>(ws + pl.off_rowstat);
   if (run1) {
     constexpr size_t lds1 = lse_lds_bytes<DP>();
+    if (lds1 > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&full_lse<DP>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+      if (e != hipSuccess) return e;
+    }
     hipLaunchKernelGGL(full_lse<DP>, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
                        stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, logZ, rowstat);
   }
   if (!run2) return hipGetLastError();
-  constexpr size_t lds2 = accum_lds_bytes<DP>();
-  if (lds2 > 65536) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&full_accum<DP>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
-    if (e != hipSuccess) return e;
+  if constexpr (full_accum_split_d(DP)) {
+    constexpr size_t lds2 = accum_split_lds_bytes<DP>();
+    if (lds2 > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&full_accum_split<DP>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(full_accum_split<DP>, dim3((unsigned)(pl.nslab * pl.ncg)), dim3(kThreads), lds2,
+                       stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, rowstat,
+                       pl.nslab, pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_sig),
+                       reinterpret_cast<float*>(ws + pl.off_part_mu),
+                       reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
+  } else {
+    constexpr size_t lds2 = accum_lds_bytes<DP>();
+    if (lds2 > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&full_accum<DP>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(full_accum<DP>, dim3((unsigned)(pl.nslab * pl.ncg)), dim3(kAccThreads), lds2,
+                       stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, rowstat, pl.nslab,
+                       pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_sig),
+                       reinterpret_cast<float*>(ws + pl.off_part_mu),
+                       reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
   }
-  hipLaunchKernelGGL(full_accum<DP>, dim3((unsigned)(pl.nslab * pl.ncg)), dim3(kAccThreads), lds2,
-                     stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, rowstat, pl.nslab,
-                     pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_sig),
-                     reinterpret_cast<float*>(ws + pl.off_part_mu),
-                     reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -520,7 +734,7 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   if (K > 0 && (mu == nullptr || ldmu < D || prec_chol == nullptr || log_pi == nullptr ||
                 Nk == nullptr || mu_acc == nullptr || sig_outer == nullptr))
     return FGMM_ERR_INVALID_ARG;
-  if (D > 64) return FGMM_ERR_UNSUPPORTED;
+  if (D > 128) return FGMM_ERR_UNSUPPORTED;
   if (N > (int64_t)1 << 40 || K > (int64_t)1 << 20) return FGMM_ERR_UNSUPPORTED;
   const FullPlan pl = make_plan(N, K, D);
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
@@ -545,6 +759,8 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     switch (pl.DP) {
       case 32: e = launch_passes<32>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 96: e = launch_passes<96>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 128: e = launch_passes<128>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       default: return FGMM_ERR_UNSUPPORTED;
     }
     if (e != hipSuccess) return FGMM_ERR_HIP;

@@ -99,7 +99,7 @@ int fgmm_iso_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
 /*   ll_nk      = log_pi_k - 0.5*(D log(2 pi) + sum_d lss_kd)                 */
 /*                - 0.5 * sum_d (x_nd - mu_kd)^2 exp(-lss_kd)                 */
 /*   sig_acc_kd = sum_n r_nk (x_nd - mu_kd)^2                                 */
-/* Supports 1 <= D <= 128.                                                    */
+/* Supports 1 <= D <= 256.                                                    */
 /* ------------------------------------------------------------------------ */
 size_t fgmm_diag_workspace_bytes(int64_t N, int64_t K, int64_t D);
 

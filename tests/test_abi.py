@@ -90,6 +90,32 @@ def test_iso_rejects_bad_arguments(kw, status):
     assert _call_iso(**kw) == status
 
 
+def _call_diag(D):
+    L = _lib.lib()
+    ld = (D + 3) // 4 * 4
+    return L.fgmm_diag_estep_f32(FAKE, ld, 10, D, FAKE, D, 4, FAKE, D, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                 FAKE, 1 << 40, 0, None)
+
+
+def _call_full(D):
+    L = _lib.lib()
+    ld = (D + 3) // 4 * 4
+    return L.fgmm_full_estep_f32(FAKE, ld, 10, D, FAKE, D, 4, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                 FAKE, 1 << 40, 0, None)
+
+
+@no_gpu
+def test_dimension_limits():
+    """Largest supported D per covariance model; one past it is UNSUPPORTED."""
+    assert _call_iso(D=257, ldx=260, ldmu=257) == _lib.FGMM_ERR_UNSUPPORTED
+    assert _call_diag(257) == _lib.FGMM_ERR_UNSUPPORTED
+    assert _call_full(129) == _lib.FGMM_ERR_UNSUPPORTED
+    # workspace queries accept the supported range
+    L = _lib.lib()
+    assert L.fgmm_diag_workspace_bytes(100, 10, 256) > L.fgmm_diag_workspace_bytes(100, 10, 128) > 0
+    assert L.fgmm_full_workspace_bytes(100, 10, 128) > L.fgmm_full_workspace_bytes(100, 10, 64) > 0
+
+
 def test_python_layer_rejects_cpu_tensors():
     from flash_gmm import FlashGMMError, flash_gmm_estep
     X = torch.zeros(4, 3)

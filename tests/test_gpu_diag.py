@@ -37,13 +37,15 @@ def test_golden_vectors(gpu_device):
 
 
 @pytest.mark.parametrize("N,K,D", [(1, 1, 1), (33, 5, 3), (500, 40, 24), (1000, 70, 96),
-                                   (300, 33, 128), (129, 3, 64), (2000, 130, 50)])
+                                   (300, 33, 128), (129, 3, 64), (2000, 130, 50),
+                                   (700, 37, 129), (1500, 70, 192), (900, 65, 200), (800, 97, 256),
+                                   (5, 2, 255)])
 def test_edge_shapes(N, K, D, gpu_device):
     inp = data.diag_clustered(N, K, D, seed=N + K + D)
     assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), f"diag N={N} K={K} D={D}")
 
 
-@pytest.mark.parametrize("N,K,D,seed", [(9000, 512, 96, 2), (3001, 77, 45, 3)])
+@pytest.mark.parametrize("N,K,D,seed", [(9000, 512, 96, 2), (3001, 77, 45, 3), (4000, 130, 256, 4)])
 def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, gpu_device):
     """Skipping all-zero responsibility steps changes no bit of any output."""
     inp = data.diag_clustered(N, K, D, seed=seed)
@@ -94,6 +96,12 @@ def test_diag_shape_mid_size(gpu_device):
     """K=1024, D=96 axis-aligned clusters at N=32,768 against the float64 oracle."""
     inp = data.diag_clustered(32768, 1024, 96, seed=2)
     assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "diag K1024 D96 N32768")
+
+
+def test_diag_wide_mid_size(gpu_device):
+    """D=256 (split-dimension accumulation) at N=8192, K=256 against the float64 oracle."""
+    inp = data.diag_clustered(8192, 256, 256, seed=5)
+    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "diag K256 D256 N8192")
 
 
 def test_diag_full_size_properties(gpu_device):

@@ -40,7 +40,9 @@ def test_golden_vectors(gpu_device):
 
 
 @pytest.mark.parametrize("N,K,D", [(1, 1, 1), (33, 5, 3), (500, 12, 16), (300, 7, 64),
-                                   (1000, 33, 40), (129, 4, 32), (2000, 9, 63)])
+                                   (1000, 33, 40), (129, 4, 32), (2000, 9, 63),
+                                   (400, 9, 65), (600, 11, 96), (300, 5, 100), (500, 7, 128),
+                                   (3, 2, 127)])
 def test_edge_shapes(N, K, D, gpu_device):
     inp = data.full_clustered(N, K, D, seed=N + K + D)
     assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), f"full N={N} K={K} D={D}")
@@ -62,7 +64,7 @@ def test_diagonal_factor_matches_diag_entry(gpu_device):
     torch.testing.assert_close(s, a[3], rtol=1e-3, atol=1e-3 * float(a[3].abs().max()))
 
 
-@pytest.mark.parametrize("N,K,D,seed", [(6000, 128, 64, 3), (2501, 19, 29, 4)])
+@pytest.mark.parametrize("N,K,D,seed", [(6000, 128, 64, 3), (2501, 19, 29, 4), (3000, 24, 128, 5)])
 def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, gpu_device):
     """Skipping all-zero responsibility steps changes no bit of any output."""
     inp = data.full_clustered(N, K, D, seed=seed)
@@ -100,6 +102,12 @@ def test_full_shape_mid_size(gpu_device):
     """K=256, D=64 at N=8,192 against the float64 oracle."""
     inp = data.full_clustered(8192, 256, 64, seed=3)
     assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "full K256 D64 N8192")
+
+
+def test_full_wide_mid_size(gpu_device):
+    """D=128 (one component per workgroup in pass 2) at N=4,096, K=48 against the float64 oracle."""
+    inp = data.full_clustered(4096, 48, 128, seed=6)
+    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "full K48 D128 N4096")
 
 
 def test_full_size_properties(gpu_device):
