@@ -166,6 +166,7 @@ def stream_main(args):
         "config": {"workload": "stream_em_n1b_k1024_d128", "N": N, "K": K, "D": D, "chunk_rows": chunk,
                    "iterations": iters, "host_threads": threads},
         "end_to_end_s": total_s,
+        "setup_s": rep["setup_ms"] / 1e3,
         "host_generation_s": rep["source_ms"] / 1e3,
         "h2d_device_s": rep["h2d_ms"] / 1e3,
         "estep_device_s": rep["estep_ms"] / 1e3,

@@ -194,19 +194,28 @@ extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn 
                      (size_t)rows * sizeof(float) + (size_t)nparts * sizeof(double) +
                      (size_t)nll * sizeof(double);
   rep.pinned_bytes = 2 * chunk_bytes;
+  rep.setup_ms = ms_since(t_start);
 
   const int64_t nchunks = cdiv(N, R);
-  bool pending[2] = {false, false};
-  auto drain = [&](int b) -> int {
-    if (!pending[b]) return FGMM_OK;
-    if (!ok(hipEventSynchronize(res.e1[b]))) return FGMM_ERR_HIP;
-    float a = 0.0f, e = 0.0f;
-    if (!ok(hipEventElapsedTime(&a, res.h2d0[b], res.h2d1[b])) ||
-        !ok(hipEventElapsedTime(&e, res.e0[b], res.e1[b])))
+  // pinned[b] may be refilled once its copy has finished; dev[b] once the E-step
+  // that read it has finished (the copy stream waits for that on the device).
+  bool copy_pending[2] = {false, false}, estep_pending[2] = {false, false};
+  auto drain_copy = [&](int b) -> int {
+    if (!copy_pending[b]) return FGMM_OK;
+    float a = 0.0f;
+    if (!ok(hipEventSynchronize(res.h2d1[b])) || !ok(hipEventElapsedTime(&a, res.h2d0[b], res.h2d1[b])))
       return FGMM_ERR_HIP;
     rep.h2d_ms += a;
+    copy_pending[b] = false;
+    return FGMM_OK;
+  };
+  auto drain_estep = [&](int b) -> int {
+    if (!estep_pending[b]) return FGMM_OK;
+    float e = 0.0f;
+    if (!ok(hipEventSynchronize(res.e1[b])) || !ok(hipEventElapsedTime(&e, res.e0[b], res.e1[b])))
+      return FGMM_ERR_HIP;
     rep.estep_ms += e;
-    pending[b] = false;
+    estep_pending[b] = false;
     return FGMM_OK;
   };
 
@@ -221,8 +230,8 @@ extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn 
     const int b = (int)(g & 1);
     const int64_t row0 = c * R;
     const int64_t n = (row0 + R <= N) ? R : N - row0;
-    // Buffer b is free once the E-step two chunks back (and hence its copy) finished.
-    int st = drain(b);
+    // The host buffer is free once the copy of the chunk two back has finished.
+    int st = drain_copy(b);
     if (st != FGMM_OK) return st;
     const auto tg = std::chrono::steady_clock::now();
     float* host = res.pinned[b];
@@ -234,6 +243,10 @@ extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn 
     }
     rep.source_ms += ms_since(tg);
     if (st != 0) return FGMM_ERR_SOURCE;
+    // dev[b] is reused: the copy waits (on the device) for the E-step that read it
+    // two chunks back.  Waiting here, and not right after that E-step was queued,
+    // keeps the copy of the chunk in between free to overlap that E-step.
+    if (estep_pending[b] && !ok(hipStreamWaitEvent(res.copy, res.e1[b], 0))) return FGMM_ERR_HIP;
     if (!ok(hipEventRecord(res.h2d0[b], res.copy)) ||
         !ok(hipMemcpyAsync(res.dev[b], host, (size_t)n * ld * sizeof(float), hipMemcpyHostToDevice,
                            res.copy)) ||
@@ -247,6 +260,10 @@ extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn 
                          0.0f);
       hipLaunchKernelGGL(fill_f64_one, dim3(1), dim3(64), 0, res.comp, res.ll + it, 0.0);
     }
+    // Read the timing of the E-step two chunks back before its events are reused
+    // (long finished by now: the host has generated a whole chunk since).
+    st = drain_estep(b);
+    if (st != FGMM_OK) return st;
     if (!ok(hipStreamWaitEvent(res.comp, res.h2d1[b], 0)) || !ok(hipEventRecord(res.e0[b], res.comp)))
       return FGMM_ERR_HIP;
     st = fgmm_iso_estep_f32(res.dev[b], ld, n, D, mu, D, K, log_sigma_sq, log_pi, res.logZ, res.Nk,
@@ -256,9 +273,8 @@ extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn 
                        res.part);
     hipLaunchKernelGGL(sum_parts, dim3(1), dim3(64), 0, res.comp, res.part, cdiv(n, 1024), res.ll + it);
     if (!ok(hipEventRecord(res.e1[b], res.comp))) return FGMM_ERR_HIP;
-    // The next copy into dev[b] must wait for this E-step.
-    if (!ok(hipStreamWaitEvent(res.copy, res.e1[b], 0))) return FGMM_ERR_HIP;
-    pending[b] = true;
+    copy_pending[b] = true;
+    estep_pending[b] = true;
     if (c == nchunks - 1) {
       if (!ok(hipEventRecord(res.m0[it], res.comp))) return FGMM_ERR_HIP;
       st = fgmm_iso_mstep_f32(res.Nk, res.mu_acc, res.sig_acc, N, K, D, cfg->var_floor, mu, D,
@@ -268,7 +284,8 @@ extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn 
     }
   }
   for (int b = 0; b < 2; ++b) {
-    const int st = drain(b);
+    int st = drain_copy(b);
+    if (st == FGMM_OK) st = drain_estep(b);
     if (st != FGMM_OK) return st;
   }
   std::vector<double> ll(nll, 0.0);

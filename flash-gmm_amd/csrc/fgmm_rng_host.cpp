@@ -8,10 +8,13 @@
 // transform of two 24-bit uniforms in (0, 1); the four normals of counter block j
 // of a row are its coordinates j, J+j, 2J+j and 3J+j (J = D/4, rounded up; the
 // ones at or beyond D are dropped).
+#include <immintrin.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include <algorithm>
 #include <math.h>
+#include <memory>
 #include <thread>
 #include <vector>
 
@@ -52,24 +55,110 @@ constexpr uint32_t kTagAssign = 0x61737367u;  // counter word 3 for the assignme
 // counter blocks: Philox for every (row, block), the Box-Muller radius and angle,
 // cos, sin, then the centre.  Per-block state lives in structure-of-arrays buffers
 // so the compiler maps the 32x32->64 multiplies and the log / sqrt / sin / cos
-// calls to SIMD code (glibc's vector math library).
-constexpr int64_t kBatch = 8;
+// calls to SIMD code (glibc's vector math library).  Every sweep covers a whole
+// number of 16-lane vectors over 64-byte aligned buffers, so no element takes a
+// scalar prologue or epilogue and a row's value does not depend on where in a
+// batch it falls.  The body is compiled twice, for AVX-512 and for AVX2
+// (x86-64-v3), and fill_rows picks the one the host supports; values are
+// reproducible for a given host instruction set.
+constexpr int64_t kBatch = 16;
 
-void fill_rows(const fgmm_synth_iso* s, int64_t row0, int64_t nrows, float* dst) {
+struct FreeDeleter {
+  void operator()(void* p) const { free(p); }
+};
+template <typename T>
+std::unique_ptr<T[], FreeDeleter> aligned_buffer(int64_t n) {
+  const size_t bytes = ((size_t)n * sizeof(T) + 63) & ~size_t(63);
+  return std::unique_ptr<T[], FreeDeleter>(static_cast<T*>(aligned_alloc(64, bytes)));
+}
+
+// Ten Philox rounds over m counter blocks held as four word arrays (m a multiple
+// of 16, 64-byte aligned), 16 (AVX-512) or 8 (AVX2) blocks per vector.  The high
+// half of each 32x32 product comes from two 32x32->64 multiplies (even and odd
+// lanes) and a lane blend, the low half from a 32-bit multiply; results equal the
+// scalar philox10() word for word.
+__attribute__((target("avx512f,avx512bw,avx512dq,avx512vl")))
+void philox_sweep_avx512(uint32_t* c0, uint32_t* c1, uint32_t* c2, uint32_t* c3, int64_t m,
+                         uint32_t k0, uint32_t k1) {
+  const __m512i M0 = _mm512_set1_epi32((int)0xD2511F53u), M1 = _mm512_set1_epi32((int)0xCD9E8D57u);
+  for (int64_t i = 0; i < m; i += 16) {
+    __m512i x0 = _mm512_load_si512(c0 + i), x1 = _mm512_load_si512(c1 + i);
+    __m512i x2 = _mm512_load_si512(c2 + i), x3 = _mm512_load_si512(c3 + i);
+    uint32_t a = k0, b = k1;
+    for (int r = 0; r < 10; ++r) {
+      const __m512i lo0 = _mm512_mullo_epi32(x0, M0), lo1 = _mm512_mullo_epi32(x2, M1);
+      const __m512i hi0 = _mm512_mask_blend_epi32(
+          0xAAAA, _mm512_srli_epi64(_mm512_mul_epu32(x0, M0), 32),
+          _mm512_mul_epu32(_mm512_srli_epi64(x0, 32), M0));
+      const __m512i hi1 = _mm512_mask_blend_epi32(
+          0xAAAA, _mm512_srli_epi64(_mm512_mul_epu32(x2, M1), 32),
+          _mm512_mul_epu32(_mm512_srli_epi64(x2, 32), M1));
+      const __m512i n0 = _mm512_ternarylogic_epi32(hi1, x1, _mm512_set1_epi32((int)a), 0x96);
+      const __m512i n2 = _mm512_ternarylogic_epi32(hi0, x3, _mm512_set1_epi32((int)b), 0x96);
+      x1 = lo1;
+      x3 = lo0;
+      x0 = n0;
+      x2 = n2;
+      a += 0x9E3779B9u;
+      b += 0xBB67AE85u;
+    }
+    _mm512_store_si512(c0 + i, x0);
+    _mm512_store_si512(c1 + i, x1);
+    _mm512_store_si512(c2 + i, x2);
+    _mm512_store_si512(c3 + i, x3);
+  }
+}
+
+void philox_sweep_avx2(uint32_t* c0, uint32_t* c1, uint32_t* c2, uint32_t* c3, int64_t m,
+                       uint32_t k0, uint32_t k1) {
+  const __m256i M0 = _mm256_set1_epi32((int)0xD2511F53u), M1 = _mm256_set1_epi32((int)0xCD9E8D57u);
+  for (int64_t i = 0; i < m; i += 8) {
+    __m256i x0 = _mm256_load_si256(reinterpret_cast<const __m256i*>(c0 + i));
+    __m256i x1 = _mm256_load_si256(reinterpret_cast<const __m256i*>(c1 + i));
+    __m256i x2 = _mm256_load_si256(reinterpret_cast<const __m256i*>(c2 + i));
+    __m256i x3 = _mm256_load_si256(reinterpret_cast<const __m256i*>(c3 + i));
+    uint32_t a = k0, b = k1;
+    for (int r = 0; r < 10; ++r) {
+      const __m256i lo0 = _mm256_mullo_epi32(x0, M0), lo1 = _mm256_mullo_epi32(x2, M1);
+      const __m256i hi0 = _mm256_blend_epi32(_mm256_srli_epi64(_mm256_mul_epu32(x0, M0), 32),
+                                             _mm256_mul_epu32(_mm256_srli_epi64(x0, 32), M0), 0xAA);
+      const __m256i hi1 = _mm256_blend_epi32(_mm256_srli_epi64(_mm256_mul_epu32(x2, M1), 32),
+                                             _mm256_mul_epu32(_mm256_srli_epi64(x2, 32), M1), 0xAA);
+      const __m256i n0 = _mm256_xor_si256(_mm256_xor_si256(hi1, x1), _mm256_set1_epi32((int)a));
+      const __m256i n2 = _mm256_xor_si256(_mm256_xor_si256(hi0, x3), _mm256_set1_epi32((int)b));
+      x1 = lo1;
+      x3 = lo0;
+      x0 = n0;
+      x2 = n2;
+      a += 0x9E3779B9u;
+      b += 0xBB67AE85u;
+    }
+    _mm256_store_si256(reinterpret_cast<__m256i*>(c0 + i), x0);
+    _mm256_store_si256(reinterpret_cast<__m256i*>(c1 + i), x1);
+    _mm256_store_si256(reinterpret_cast<__m256i*>(c2 + i), x2);
+    _mm256_store_si256(reinterpret_cast<__m256i*>(c3 + i), x3);
+  }
+}
+
+template <int ISA>
+__attribute__((always_inline)) inline void fill_rows_body(const fgmm_synth_iso* s, int64_t row0,
+                                                          int64_t nrows, float* dst) {
   const int64_t D = s->D;
   const int64_t J = (D + 3) / 4;
   const int64_t M = kBatch * J;
   const uint32_t k0 = (uint32_t)s->seed, k1 = (uint32_t)(s->seed >> 32);
-  std::vector<uint32_t> w0(M), w1(M), w2(M), w3(M);
-  std::vector<float> rad(2 * M), ang(2 * M), z(4 * M);
+  auto w0 = aligned_buffer<uint32_t>(M), w1 = aligned_buffer<uint32_t>(M);
+  auto w2 = aligned_buffer<uint32_t>(M), w3 = aligned_buffer<uint32_t>(M);
+  auto rad = aligned_buffer<float>(2 * M), ang = aligned_buffer<float>(2 * M);
+  auto z = aligned_buffer<float>(4 * M);
   int64_t comp[kBatch];
-  static_assert(kBatch % 8 == 0, "sweeps are multiples of the SIMD width");
+  static_assert(kBatch % 16 == 0, "sweeps are multiples of the SIMD width");
   for (int64_t b0 = 0; b0 < nrows; b0 += kBatch) {
     const int64_t nb = std::min(kBatch, nrows - b0);
-    uint32_t* c0 = w0.data();
-    uint32_t* c1 = w1.data();
-    uint32_t* c2 = w2.data();
-    uint32_t* c3 = w3.data();
+    uint32_t* c0 = w0.get();
+    uint32_t* c1 = w1.get();
+    uint32_t* c2 = w2.get();
+    uint32_t* c3 = w3.get();
     // Full batches always: rows past nb get dummy counters and are discarded, so
     // every element takes the same (vector) code path and a row's value does not
     // depend on its position in a batch.
@@ -86,30 +175,19 @@ void fill_rows(const fgmm_synth_iso* s, int64_t row0, int64_t nrows, float* dst)
       }
     }
     const int64_t m = M;
-    uint32_t key0 = k0, key1 = k1;
-    for (int r = 0; r < 10; ++r) {
-      for (int64_t i = 0; i < m; ++i) {
-        const uint64_t p0 = (uint64_t)0xD2511F53u * c0[i];
-        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c2[i];
-        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1[i] ^ key0;
-        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3[i] ^ key1;
-        c1[i] = (uint32_t)p1;
-        c3[i] = (uint32_t)p0;
-        c0[i] = n0;
-        c2[i] = n2;
-      }
-      key0 += 0x9E3779B9u;
-      key1 += 0xBB67AE85u;
-    }
+    if constexpr (ISA == 512)
+      philox_sweep_avx512(c0, c1, c2, c3, m, k0, k1);
+    else
+      philox_sweep_avx2(c0, c1, c2, c3, m, k0, k1);
     // Box-Muller.  The radius/angle sweep comes first and sin and cos run in
     // separate sweeps: a fused sin/cos pair becomes a complex-exponential call
     // with no SIMD form.  Outputs: zA = r0 cos t0, zB = r0 sin t0, zC = r1 cos t1,
     // zD = r1 sin t1, each indexed by (row, block).
-    float* ma = rad.data();
+    float* ma = rad.get();
     float* mb = ma + M;
-    float* ta = ang.data();
+    float* ta = ang.get();
     float* tb = ta + M;
-    float* zA = z.data();
+    float* zA = z.get();
     float* zB = zA + M;
     float* zC = zA + 2 * M;
     float* zD = zA + 3 * M;
@@ -139,6 +217,24 @@ void fill_rows(const fgmm_synth_iso* s, int64_t row0, int64_t nrows, float* dst)
       }
     }
   }
+}
+
+__attribute__((target("avx512f,avx512bw,avx512dq,avx512vl")))
+void fill_rows_avx512(const fgmm_synth_iso* s, int64_t row0, int64_t nrows, float* dst) {
+  fill_rows_body<512>(s, row0, nrows, dst);
+}
+
+void fill_rows_avx2(const fgmm_synth_iso* s, int64_t row0, int64_t nrows, float* dst) {
+  fill_rows_body<256>(s, row0, nrows, dst);
+}
+
+void fill_rows(const fgmm_synth_iso* s, int64_t row0, int64_t nrows, float* dst) {
+  static const bool avx512 = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+                             __builtin_cpu_supports("avx512dq") && __builtin_cpu_supports("avx512vl");
+  if (avx512)
+    fill_rows_avx512(s, row0, nrows, dst);
+  else
+    fill_rows_avx2(s, row0, nrows, dst);
 }
 
 }  // namespace

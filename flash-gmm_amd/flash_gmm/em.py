@@ -44,7 +44,7 @@ class _EmReport(ctypes.Structure):
                 ("source_ms", ctypes.c_double), ("h2d_ms", ctypes.c_double),
                 ("estep_ms", ctypes.c_double), ("mstep_ms", ctypes.c_double),
                 ("device_bytes", ctypes.c_size_t), ("pinned_bytes", ctypes.c_size_t),
-                ("loglik", ctypes.c_double * MAX_REPORTED_ITERS)]
+                ("loglik", ctypes.c_double * MAX_REPORTED_ITERS), ("setup_ms", ctypes.c_double)]
 
 
 def _declare(L):
@@ -176,7 +176,8 @@ def stream_em_iso(source: Union[SynthIsoSource, Callable[[int, int], np.ndarray]
     del keep
     _lib.check(st, "fgmm_stream_em_iso")
     return {
-        "iterations": rep.iterations, "total_ms": rep.total_ms, "source_ms": rep.source_ms,
+        "iterations": rep.iterations, "total_ms": rep.total_ms, "setup_ms": rep.setup_ms,
+        "source_ms": rep.source_ms,
         "h2d_ms": rep.h2d_ms, "estep_ms": rep.estep_ms, "mstep_ms": rep.mstep_ms,
         "device_bytes": rep.device_bytes, "pinned_bytes": rep.pinned_bytes,
         "loglik": [rep.loglik[i] for i in range(min(rep.iterations, MAX_REPORTED_ITERS))],

@@ -200,6 +200,7 @@ typedef struct fgmm_em_report {
     size_t device_bytes;     /* device memory allocated by the call (peak) */
     size_t pinned_bytes;     /* pinned host memory allocated by the call */
     double loglik[FGMM_EM_MAX_REPORTED_ITERS]; /* sum_n logZ_n per iteration, before its M-step */
+    double setup_ms;         /* wall time spent allocating streams, events and buffers */
 } fgmm_em_report;
 
 int fgmm_stream_em_iso(const fgmm_em_config *cfg, fgmm_row_source_fn src, void *user,

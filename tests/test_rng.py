@@ -1,6 +1,8 @@
 """The native synthetic row source (host code, no GPU): counter-based
 reproducibility and the distribution of its rows."""
 
+import os
+
 import numpy as np
 import pytest
 from scipy import stats
@@ -55,3 +57,21 @@ def test_bad_arguments():
     s = SynthIsoSource(np.zeros((2, 4), np.float32))
     with pytest.raises(FlashGMMError):
         s.rows(-1, 10)
+
+
+def test_simd_philox_matches_scalar(tmp_path):
+    """AVX2 and AVX-512 Philox sweeps equal the scalar generator word for word."""
+    import shutil
+    import subprocess
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    exe = str(tmp_path / "rng_simd_check")
+    subprocess.run(["g++", "-O2", "-march=x86-64-v3", "-std=c++17",
+                    "-I" + os.path.join(root, "include"),
+                    "-I" + os.path.join(root, "flash-gmm_amd", "csrc"),
+                    os.path.join(here, "rng_simd_check.cpp"), "-o", exe, "-pthread", "-lmvec", "-lm"],
+                   check=True)
+    out = subprocess.run([exe], capture_output=True, text=True)
+    assert out.returncode == 0, out.stdout + out.stderr
