@@ -79,6 +79,8 @@ def cpu_baseline(inp, kind, K, D, min_s=10.0, max_s=30.0, rows=16384):
 # counter values and commands are in profiles/<kind>_estep_<shape>.md.
 TRAFFIC_BYTES = {
     "iso_n1m_k1024_d128": {"phase1": 589_618_790, "phase2": 566_709_248},
+    "diag_n1m_k1024_d96": {"phase1": 402_644_582, "phase2": 452_352_614},
+    "full_n250k_k256_d64": {"phase1": 298_443_879, "phase2": 175_187_251},
 }
 
 WORKLOADS = {

@@ -118,7 +118,7 @@ int fgmm_diag_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
 /*   ll_nk = log_pi_k + sum_d log(|L_k,dd| + 1e-30) - 0.5 D log(2 pi)         */
 /*           - 0.5 ||L_k^T (x_n - mu_k)||^2                                   */
 /*   sig_outer_k = sum_n r_nk x_n x_n^T   (uncentred second moment)           */
-/* Supports 1 <= D <= 64.                                                     */
+/* Supports 1 <= D <= 128.                                                    */
 /* ------------------------------------------------------------------------ */
 size_t fgmm_full_workspace_bytes(int64_t N, int64_t K, int64_t D);
 
