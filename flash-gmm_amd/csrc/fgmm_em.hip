@@ -1,5 +1,6 @@
-// EM driver pieces for the isotropic model: the GPU M-step, a deterministic
-// sum of logZ, and the streaming E-step driver for data sets larger than HBM.
+// EM driver pieces: the GPU M-steps (isotropic, diagonal, full covariance), a
+// deterministic sum of logZ, and the streaming isotropic EM driver for data sets
+// larger than HBM.
 //
 // M-step (README.md:59-61, :99-100):  pi = Nk / N,  mu = mu_acc / Nk,
 // sigma^2 = sig_acc / (D Nk).  sig_acc is accumulated about the previous means, so
@@ -59,6 +60,111 @@ __global__ __launch_bounds__(256) void iso_mstep_kernel(const float* __restrict_
     lss[k] = (float)log(s2);
     lpi[k] = (float)log(nk / N);
   }
+}
+
+// Diagonal M-step, one block per component: pi, mu and per-dimension variances
+// sigma^2_kd = sig_acc_kd / Nk_k (accumulated about the old means; the exact form
+// subtracts (mu_new - mu_old)^2).
+__global__ __launch_bounds__(256) void diag_mstep_kernel(const float* __restrict__ Nk,
+                                                         const float* __restrict__ mu_acc,
+                                                         const float* __restrict__ sig_acc, double N,
+                                                         int D, double var_floor, int exact,
+                                                         float* __restrict__ mu, int64_t ldmu,
+                                                         float* __restrict__ lss, int64_t ldlss,
+                                                         float* __restrict__ lpi) {
+  const int64_t k = blockIdx.x;
+  const double nk = (double)Nk[k];
+  if (!(nk > 0.0)) {
+    if (threadIdx.x == 0) lpi[k] = -INFINITY;
+    return;
+  }
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    const double mn = (double)mu_acc[k * D + d] / nk;
+    double s2 = (double)sig_acc[k * D + d] / nk;
+    if (exact) {
+      const double dm = mn - (double)mu[k * ldmu + d];
+      s2 -= dm * dm;
+    }
+    if (s2 < var_floor) s2 = var_floor;
+    mu[k * ldmu + d] = (float)mn;
+    lss[k * ldlss + d] = (float)log(s2);
+  }
+  if (threadIdx.x == 0) lpi[k] = (float)log(nk / N);
+}
+
+// Full-covariance M-step, one block per component, fp64 in LDS:
+//   Sigma = sig_outer / Nk - mu mu^T + reg I,  Sigma = U U^T with U upper-triangular
+//   (Cholesky taken from the last column), W = U^-1, and prec_chol = L = W^T, the
+//   lower-triangular factor with L L^T = Sigma^-1 and a positive diagonal.
+// A pivot that is not positive (Sigma not positive definite) is replaced by the
+// ridge (or 1e-30) and counted in *info.
+__global__ __launch_bounds__(256) void full_mstep_kernel(const float* __restrict__ Nk,
+                                                         const float* __restrict__ mu_acc,
+                                                         const float* __restrict__ sig_outer, double N,
+                                                         int D, double reg, float* __restrict__ mu,
+                                                         int64_t ldmu, float* __restrict__ prec_chol,
+                                                         float* __restrict__ lpi, int* __restrict__ info) {
+  extern __shared__ double lds_d[];
+  double* S = lds_d;            // D x D: U in the upper triangle, W^T below it
+  double* m = S + D * D;        // new mean
+  double* wd = m + D;           // diagonal of W
+  __shared__ double piv;
+  const int64_t k = blockIdx.x;
+  const int t = threadIdx.x, nt = blockDim.x;
+  const double nk = (double)Nk[k];
+  if (!(nk > 0.0)) {
+    if (t == 0) lpi[k] = -INFINITY;
+    return;
+  }
+  for (int i = t; i < D; i += nt) m[i] = (double)mu_acc[k * D + i] / nk;
+  __syncthreads();
+  const float* so = sig_outer + k * (int64_t)D * D;
+  for (int e = t; e < D * D; e += nt) {
+    const int i = e / D, j = e % D;
+    double v = 0.5 * ((double)so[i * D + j] + (double)so[j * D + i]) / nk - m[i] * m[j];
+    if (i == j) v += reg;
+    S[e] = v;
+  }
+  __syncthreads();
+  bool indefinite = false;   // thread 0 only
+  for (int j = D - 1; j >= 0; --j) {
+    if (t == 0) {
+      double d = S[j * D + j];
+      if (!(d > 0.0)) {
+        d = reg > 0.0 ? reg : 1e-30;
+        indefinite = true;
+      }
+      piv = sqrt(d);
+      S[j * D + j] = piv;
+    }
+    __syncthreads();
+    const double p = piv;
+    for (int i = t; i < j; i += nt) S[i * D + j] /= p;
+    __syncthreads();
+    for (int e = t; e < j * j; e += nt) {
+      const int a = e / j, b = e % j;
+      if (a <= b) S[a * D + b] -= S[a * D + j] * S[b * D + j];
+    }
+    __syncthreads();
+  }
+  if (t == 0 && indefinite && info) atomicAdd(info, 1);
+  // Column c of W = U^-1 by back substitution, stored transposed in row c below the diagonal.
+  for (int c = t; c < D; c += nt) {
+    wd[c] = 1.0 / S[c * D + c];
+    for (int i = c - 1; i >= 0; --i) {
+      double acc = S[i * D + c] * wd[c];
+      for (int l = i + 1; l < c; ++l) acc += S[i * D + l] * S[c * D + l];
+      S[c * D + i] = -acc / S[i * D + i];
+    }
+  }
+  __syncthreads();
+  float* L = prec_chol + k * (int64_t)D * D;
+  for (int e = t; e < D * D; e += nt) {
+    const int i = e / D, j = e % D;
+    L[e] = (float)(j < i ? S[i * D + j] : (j == i ? wd[i] : 0.0));
+  }
+  for (int i = t; i < D; i += nt) mu[k * ldmu + i] = (float)m[i];
+  if (t == 0) lpi[k] = (float)log(nk / N);
 }
 
 // Deterministic sum of n floats into *acc (fp64): fixed 1024-element blocks, then
@@ -146,6 +252,37 @@ extern "C" int fgmm_iso_mstep_f32(const float* Nk, const float* mu_acc, const fl
   hipLaunchKernelGGL(iso_mstep_kernel, dim3((unsigned)K), dim3(256), 0, (hipStream_t)stream, Nk,
                      mu_acc, sig_acc, (double)N, (int)D, var_floor,
                      (flags & FGMM_MSTEP_EXACT_VARIANCE) ? 1 : 0, mu, ldmu, log_sigma_sq, log_pi);
+  return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+}
+
+extern "C" int fgmm_diag_mstep_f32(const float* Nk, const float* mu_acc, const float* sig_acc, int64_t N,
+                                   int64_t K, int64_t D, double var_floor, float* mu, int64_t ldmu,
+                                   float* log_sigma_sq, int64_t ldlss, float* log_pi, unsigned flags,
+                                   void* stream) {
+  if (N < 0 || K < 0 || D < 1 || ldmu < D || ldlss < D || !(var_floor >= 0.0)) return FGMM_ERR_INVALID_ARG;
+  if (K == 0) return FGMM_OK;
+  if (!Nk || !mu_acc || !sig_acc || !mu || !log_sigma_sq || !log_pi) return FGMM_ERR_INVALID_ARG;
+  hipLaunchKernelGGL(diag_mstep_kernel, dim3((unsigned)K), dim3(256), 0, (hipStream_t)stream, Nk,
+                     mu_acc, sig_acc, (double)N, (int)D, var_floor,
+                     (flags & FGMM_MSTEP_EXACT_VARIANCE) ? 1 : 0, mu, ldmu, log_sigma_sq, ldlss, log_pi);
+  return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+}
+
+extern "C" int fgmm_full_mstep_f32(const float* Nk, const float* mu_acc, const float* sig_outer, int64_t N,
+                                   int64_t K, int64_t D, double reg_covar, float* mu, int64_t ldmu,
+                                   float* prec_chol, float* log_pi, int* info, void* stream) {
+  if (N < 0 || K < 0 || D < 1 || ldmu < D || !(reg_covar >= 0.0)) return FGMM_ERR_INVALID_ARG;
+  if (D > 128) return FGMM_ERR_UNSUPPORTED;
+  if (K == 0) return FGMM_OK;
+  if (!Nk || !mu_acc || !sig_outer || !mu || !prec_chol || !log_pi) return FGMM_ERR_INVALID_ARG;
+  const size_t lds = ((size_t)D * D + 2 * (size_t)D) * sizeof(double);
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&full_mstep_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return FGMM_ERR_HIP;
+  }
+  hipLaunchKernelGGL(full_mstep_kernel, dim3((unsigned)K), dim3(256), lds, (hipStream_t)stream, Nk,
+                     mu_acc, sig_outer, (double)N, (int)D, reg_covar, mu, ldmu, prec_chol, log_pi, info);
   return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
 }
 

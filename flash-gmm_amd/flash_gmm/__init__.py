@@ -8,10 +8,12 @@ HIP kernels in ``libflashgmm.so`` (C ABI: include/flashgmm.h):
 """
 
 from ._lib import FlashGMMError  # noqa: F401
-from .em import SynthIsoSource, em_iso, mstep_iso, stream_em_iso  # noqa: F401
+from .em import (SynthIsoSource, em_diag, em_full, em_iso, mstep_diag, mstep_full,  # noqa: F401
+                 mstep_iso, stream_em_iso)
 from .estep import (diag_estep_into, flash_gmm_estep, flash_gmm_estep_diag,  # noqa: F401
                     flash_gmm_estep_full, full_estep_into, iso_estep_into)
 
 __all__ = ["flash_gmm_estep", "flash_gmm_estep_diag", "flash_gmm_estep_full",
            "iso_estep_into", "diag_estep_into", "full_estep_into",
-           "mstep_iso", "em_iso", "stream_em_iso", "SynthIsoSource", "FlashGMMError"]
+           "mstep_iso", "mstep_diag", "mstep_full", "em_iso", "em_diag", "em_full",
+           "stream_em_iso", "SynthIsoSource", "FlashGMMError"]

@@ -126,7 +126,7 @@ def full_clustered(N: int, K: int, D: int, seed: int = 3, device="cpu") -> Dict[
         idx = (a == k).nonzero(as_tuple=True)[0]
         if idx.numel():
             X[idx] = (mu64[k] + z[idx].double() @ cs[k].T).float()
-    return dict(X=X, mu=mu, prec_chol=prec_chol.float().to(device), log_pi=lpi)
+    return dict(X=X, mu=mu, prec_chol=prec_chol.float().contiguous().to(device), log_pi=lpi)
 
 
 def reference_smoke(N: int = 1_000_000, K: int = 1024, D: int = 128, seed: int = 0,

@@ -1,5 +1,5 @@
-"""EM on the device: the isotropic M-step, an in-memory EM loop and the streaming
-EM driver for data sets larger than device memory.
+"""EM on the device: M-steps for the three covariance models, in-memory EM loops
+and the streaming isotropic EM driver for data sets larger than device memory.
 
 The reference has no EM code; its README gives the M-step formulas
 (README.md:59-61) and a chunked streaming recipe (README.md:81-103).  Here the
@@ -19,7 +19,7 @@ import torch
 
 from . import _lib
 from ._lib import FlashGMMError
-from .estep import iso_estep_into
+from .estep import diag_estep_into, full_estep_into, iso_estep_into
 
 MSTEP_EXACT_VARIANCE = 1 << 8
 MAX_REPORTED_ITERS = 16
@@ -57,6 +57,14 @@ def _declare(L):
     L.fgmm_iso_mstep_f32.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3 + [
         ctypes.c_double, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
         ctypes.c_uint, ctypes.c_void_p]
+    L.fgmm_diag_mstep_f32.restype = ctypes.c_int
+    L.fgmm_diag_mstep_f32.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3 + [
+        ctypes.c_double, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+        ctypes.c_void_p, ctypes.c_uint, ctypes.c_void_p]
+    L.fgmm_full_mstep_f32.restype = ctypes.c_int
+    L.fgmm_full_mstep_f32.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3 + [
+        ctypes.c_double, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_void_p, ctypes.c_void_p]
     L.fgmm_stream_em_iso.restype = ctypes.c_int
     L.fgmm_stream_em_iso.argtypes = [ctypes.POINTER(_EmConfig), ctypes.c_void_p, ctypes.c_void_p,
                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -111,6 +119,77 @@ def mstep_iso(Nk, mu_acc, sig_acc, N: int, mu, log_sigma_sq, log_pi, *, var_floo
                                   log_pi.data_ptr(), MSTEP_EXACT_VARIANCE if exact_variance else 0,
                                   _lib.stream_handle(mu.device))
     _lib.check(st, "fgmm_iso_mstep_f32")
+
+
+def _check_dev_f32(*ts):
+    for t in ts:
+        if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
+            raise FlashGMMError("M-step tensors must be contiguous float32 on the GPU")
+
+
+def mstep_diag(Nk, mu_acc, sig_acc, N: int, mu, log_sigma_sq, log_pi, *, var_floor: float = 0.0,
+               exact_variance: bool = False) -> None:
+    """Device diagonal M-step: mu, log_sigma_sq (K x D) and log_pi updated in place."""
+    K, D = mu.shape
+    _check_dev_f32(Nk, mu_acc, sig_acc, mu, log_sigma_sq, log_pi)
+    L = _declare(_lib.lib())
+    with torch.cuda.device(mu.device):
+        st = L.fgmm_diag_mstep_f32(Nk.data_ptr(), mu_acc.data_ptr(), sig_acc.data_ptr(), int(N), K, D,
+                                   float(var_floor), mu.data_ptr(), D, log_sigma_sq.data_ptr(), D,
+                                   log_pi.data_ptr(), MSTEP_EXACT_VARIANCE if exact_variance else 0,
+                                   _lib.stream_handle(mu.device))
+    _lib.check(st, "fgmm_diag_mstep_f32")
+
+
+def mstep_full(Nk, mu_acc, sig_outer, N: int, mu, prec_chol, log_pi, *, reg_covar: float = 1e-6,
+               info=None) -> None:
+    """Device full-covariance M-step: mu, prec_chol (K x D x D, lower-triangular with
+    L L^T = Sigma^-1) and log_pi updated in place.  ``info`` (an int32 device tensor of
+    one element, zeroed by the caller) counts components whose covariance was not
+    positive definite."""
+    K, D = mu.shape
+    _check_dev_f32(Nk, mu_acc, sig_outer, mu, prec_chol, log_pi)
+    if info is not None and not (info.is_cuda and info.dtype == torch.int32 and info.numel() >= 1):
+        raise FlashGMMError("info must be an int32 tensor on the GPU")
+    L = _declare(_lib.lib())
+    with torch.cuda.device(mu.device):
+        st = L.fgmm_full_mstep_f32(Nk.data_ptr(), mu_acc.data_ptr(), sig_outer.data_ptr(), int(N), K, D,
+                                   float(reg_covar), mu.data_ptr(), D, prec_chol.data_ptr(),
+                                   log_pi.data_ptr(), info.data_ptr() if info is not None else None,
+                                   _lib.stream_handle(mu.device))
+    _lib.check(st, "fgmm_full_mstep_f32")
+
+
+def em_diag(X, mu, log_sigma_sq, log_pi, iterations: int, *, var_floor: float = 0.0,
+            exact_variance: bool = False):
+    """In-memory diagonal-covariance EM; returns per-iteration log-likelihoods."""
+    N, D = X.shape
+    K = mu.shape[0]
+    dev = X.device
+    logZ, Nk = torch.empty(N, device=dev), torch.empty(K, device=dev)
+    mu_acc, sig = torch.empty(K, D, device=dev), torch.empty(K, D, device=dev)
+    out = []
+    for _ in range(iterations):
+        diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig)
+        out.append(float(logZ.double().sum()))
+        mstep_diag(Nk, mu_acc, sig, N, mu, log_sigma_sq, log_pi, var_floor=var_floor,
+                   exact_variance=exact_variance)
+    return out
+
+
+def em_full(X, mu, prec_chol, log_pi, iterations: int, *, reg_covar: float = 1e-6):
+    """In-memory full-covariance EM; returns per-iteration log-likelihoods."""
+    N, D = X.shape
+    K = mu.shape[0]
+    dev = X.device
+    logZ, Nk = torch.empty(N, device=dev), torch.empty(K, device=dev)
+    mu_acc, so = torch.empty(K, D, device=dev), torch.empty(K, D, D, device=dev)
+    out = []
+    for _ in range(iterations):
+        full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, so)
+        out.append(float(logZ.double().sum()))
+        mstep_full(Nk, mu_acc, so, N, mu, prec_chol, log_pi, reg_covar=reg_covar)
+    return out
 
 
 def em_iso(X, mu, log_sigma_sq, log_pi, iterations: int, *, var_floor: float = 0.0,

@@ -169,6 +169,36 @@ int fgmm_iso_mstep_f32(const float *Nk, const float *mu_acc, const float *sig_ac
                        unsigned flags, void *stream);
 
 /* ------------------------------------------------------------------------ */
+/* Diagonal-covariance M-step on the device (the per-dimension analogue of    */
+/* README.md:59-61): log_pi = log(Nk/N), mu = mu_acc/Nk,                       */
+/* sigma^2_kd = max(var_floor, sig_acc_kd/Nk [- (mu_new - mu_old)_d^2]), the   */
+/* bracket applied with FGMM_MSTEP_EXACT_VARIANCE.  mu (K x D, stride ldmu),    */
+/* log_sigma_sq (K x D, stride ldlss) and log_pi are updated in place;        */
+/* components with Nk = 0 keep mu and log_sigma_sq and get log_pi = -inf.     */
+/* ------------------------------------------------------------------------ */
+int fgmm_diag_mstep_f32(const float *Nk, const float *mu_acc, const float *sig_acc,
+                        int64_t N, int64_t K, int64_t D, double var_floor,
+                        float *mu, int64_t ldmu, float *log_sigma_sq, int64_t ldlss,
+                        float *log_pi, unsigned flags, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Full-covariance M-step on the device, producing the E-step's own input     */
+/* parameterisation (flash_gmm_full_h100.py:238,257-260):                      */
+/*   Sigma_k = sig_outer_k / Nk_k - mu_k mu_k^T + reg_covar I                 */
+/*   prec_chol_k = L_k lower-triangular, L_k L_k^T = Sigma_k^-1, positive diag */
+/* computed in fp64 per component.  mu (K x D, stride ldmu), prec_chol         */
+/* (K x D x D contiguous) and log_pi are written; components with Nk = 0 keep  */
+/* mu and prec_chol and get log_pi = -inf.  info (device int, may be NULL,     */
+/* zeroed by the caller) is incremented for every component whose Sigma was  */
+/* not positive definite (its failing pivots are replaced by reg_covar).      */
+/* Supports 1 <= D <= 128.                                                    */
+/* ------------------------------------------------------------------------ */
+int fgmm_full_mstep_f32(const float *Nk, const float *mu_acc, const float *sig_outer,
+                        int64_t N, int64_t K, int64_t D, double reg_covar,
+                        float *mu, int64_t ldmu, float *prec_chol, float *log_pi,
+                        int *info, void *stream);
+
+/* ------------------------------------------------------------------------ */
 /* Streaming isotropic EM for data sets larger than device memory.           */
 /* Replaces the README recipe at README.md:81-103 (pageable chunk.cuda() per  */
 /* chunk, accumulators summed in Python, M-step in PyTorch).  Rows come from   */

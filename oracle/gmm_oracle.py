@@ -25,7 +25,9 @@ Parity pinning (what checks each function, see tests/test_oracle.py):
   precision Cholesky factor, sklearn 'full' internals, brute force, reduction
   to ``estep_diag`` for diagonal factors.
 * ``mstep_*`` -- closed forms against the README formulas, checked by the
-  fixed point of an exactly-fitted single component.
+  fixed point of an exactly-fitted single component (sample mean, variance and
+  covariance); ``prec_chol_from_cov`` by L L^T cov = I, lower-triangularity with a
+  positive diagonal, and L = diag(sigma^-1/2) for a diagonal cov.
 """
 
 from __future__ import annotations
@@ -211,6 +213,22 @@ def mstep_iso(Nk: Tensor, mu_acc: Tensor, sig_acc: Tensor, N: int, D: int):
     mu = mu_acc / Nk[:, None]
     sigma_sq = sig_acc / (D * Nk)
     return pi, mu, sigma_sq
+
+
+def mstep_diag(Nk: Tensor, mu_acc: Tensor, sig_acc: Tensor, N: int):
+    """pi = Nk/N, mu = mu_acc/Nk, sigma^2_kd = sig_acc_kd/Nk (the diagonal analogue of
+    README.md:59-61; sig_acc is accumulated about the previous means)."""
+    pi = Nk / N
+    mu = mu_acc / Nk[:, None]
+    var = sig_acc / Nk[:, None]
+    return pi, mu, var
+
+
+def prec_chol_from_cov(cov: Tensor) -> Tensor:
+    """Lower-triangular L with L L^T = cov^-1 (the prec_chol parameterisation of
+    flash_gmm_full_h100.py:238,247-248), in float64."""
+    c = cov.double()
+    return torch.linalg.cholesky(torch.linalg.inv(c))
 
 
 def mstep_full(Nk: Tensor, mu_acc: Tensor, sig_outer: Tensor, N: int):

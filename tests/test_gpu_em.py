@@ -6,7 +6,8 @@ import numpy as np
 import pytest
 import torch
 
-from flash_gmm import (FlashGMMError, SynthIsoSource, data, em_iso, flash_gmm_estep, mstep_iso,
+from flash_gmm import (FlashGMMError, SynthIsoSource, data, em_diag, em_full, em_iso, flash_gmm_estep,
+                       flash_gmm_estep_diag, flash_gmm_estep_full, mstep_diag, mstep_full, mstep_iso,
                        stream_em_iso)
 from oracle import gmm_oracle as O
 
@@ -105,3 +106,73 @@ def test_stream_em_source_error_is_reported(gpu_device):
     # the driver released its resources: a following call works
     rep = stream_em_iso(src, 50_000, mu, lss, lpi, iterations=1, chunk_rows=10_000)
     assert rep["iterations"] == 1
+
+
+@pytest.mark.parametrize("exact", [False, True])
+def test_diag_mstep_matches_oracle(exact, gpu_device):
+    inp = data.diag_clustered(5000, 30, 20, seed=31)
+    dev = gpu_device
+    X, mu, lss, lpi = (inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi"))
+    _, Nk, mu_acc, sig = flash_gmm_estep_diag(X, mu, lss, lpi)
+    mu_old = mu.clone()
+    mstep_diag(Nk, mu_acc, sig, 5000, mu, lss, lpi, exact_variance=exact)
+    torch.cuda.synchronize()
+    pi, m, var = O.mstep_diag(Nk.double().cpu(), mu_acc.double().cpu(), sig.double().cpu(), 5000)
+    if exact:
+        var = var - (m - mu_old.double().cpu()) ** 2
+    torch.testing.assert_close(mu.double().cpu(), m, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(lss.double().cpu(), torch.log(var), rtol=0, atol=1e-6)
+    torch.testing.assert_close(lpi.double().cpu(), torch.log(pi), rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("D", [16, 64, 100, 128])
+def test_full_mstep_matches_oracle(D, gpu_device):
+    # every component holds well over D rows, so each Sigma_k is positive definite
+    N = 24000
+    inp = data.full_clustered(N, 12, D, seed=32)
+    dev = gpu_device
+    X, mu, L, lpi = (inp[k].to(dev) for k in ("X", "mu", "prec_chol", "log_pi"))
+    _, Nk, mu_acc, so = flash_gmm_estep_full(X, mu, L, lpi)
+    assert float(Nk.min()) > 2 * D
+    info = torch.zeros(1, dtype=torch.int32, device=dev)
+    mstep_full(Nk, mu_acc, so, N, mu, L, lpi, reg_covar=1e-6, info=info)
+    torch.cuda.synchronize()
+    assert int(info.item()) == 0
+    pi, m, cov = O.mstep_full(Nk.double().cpu(), mu_acc.double().cpu(), so.double().cpu(), N)
+    cov = 0.5 * (cov + cov.transpose(1, 2)) + 1e-6 * torch.eye(D, dtype=torch.float64)
+    ref_L = O.prec_chol_from_cov(cov)
+    torch.testing.assert_close(mu.double().cpu(), m, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(lpi.double().cpu(), torch.log(pi), rtol=0, atol=1e-6)
+    got = L.double().cpu()
+    assert torch.all(torch.triu(got, 1) == 0)
+    torch.testing.assert_close(got, ref_L, rtol=1e-5, atol=1e-5 * float(ref_L.abs().max()))
+
+
+def test_full_mstep_counts_indefinite_covariance(gpu_device):
+    dev = gpu_device
+    K, D = 2, 8
+    Nk = torch.tensor([10.0, 10.0], device=dev)
+    mu_acc = torch.zeros(K, D, device=dev)
+    so = torch.zeros(K, D, D, device=dev)
+    so[0] = 10 * torch.eye(D, device=dev)          # Sigma = I
+    so[1, 0, 0] = -10.0                              # Sigma with a negative variance
+    mu = torch.zeros(K, D, device=dev)
+    L = torch.empty(K, D, D, device=dev)
+    lpi = torch.zeros(K, device=dev)
+    info = torch.zeros(1, dtype=torch.int32, device=dev)
+    mstep_full(Nk, mu_acc, so, 20, mu, L, lpi, reg_covar=1e-3, info=info)
+    torch.cuda.synchronize()
+    assert int(info.item()) == 1          # one component, counted once
+    torch.testing.assert_close(L[0], torch.eye(D, device=dev) / (1 + 1e-3) ** 0.5)
+
+
+def test_em_diag_and_full_loglik_non_decreasing(gpu_device):
+    dev = gpu_device
+    inp = data.diag_clustered(20000, 24, 16, seed=33)
+    X, mu, lss, lpi = (inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi"))
+    ll = em_diag(X, mu, lss, lpi, 6, exact_variance=True)
+    assert all(b >= a - 1e-6 * abs(a) for a, b in zip(ll, ll[1:])), ll
+    inp = data.full_clustered(20000, 10, 12, seed=34)
+    X, mu, L, lpi = (inp[k].to(dev) for k in ("X", "mu", "prec_chol", "log_pi"))
+    ll = em_full(X, mu, L, lpi, 6, reg_covar=1e-6)
+    assert all(b >= a - 1e-6 * abs(a) for a, b in zip(ll, ll[1:])), ll

@@ -253,3 +253,28 @@ def test_mstep_full_recovers_sample_covariance():
     _, m, cov = O.mstep_full(Nk, mu_acc, so, 200)
     np.testing.assert_allclose(m[0].numpy(), X.mean(0).numpy(), atol=1e-12)
     np.testing.assert_allclose(cov[0].numpy(), np.cov(X.numpy().T, bias=True), atol=1e-10)
+
+
+def test_mstep_diag_single_component():
+    g = torch.Generator().manual_seed(48)
+    X = torch.randn(400, 5, generator=g, dtype=torch.float64) * torch.tensor([1.0, 2, 3, 0.5, 1.5]) - 2
+    mu0 = X.mean(0, keepdim=True)
+    _, Nk, mu_acc, sig = O.estep_diag(X, mu0, torch.zeros(1, 5, dtype=torch.float64),
+                                      torch.zeros(1, dtype=torch.float64))
+    pi, mu, var = O.mstep_diag(Nk, mu_acc, sig, 400)
+    assert abs(pi.item() - 1) < 1e-12
+    np.testing.assert_allclose(mu.numpy(), mu0.numpy(), atol=1e-12)
+    np.testing.assert_allclose(var[0].numpy(), X.var(0, unbiased=False).numpy(), rtol=1e-10)
+
+
+def test_prec_chol_from_cov():
+    g = torch.Generator().manual_seed(49)
+    A = torch.randn(3, 6, 6, generator=g, dtype=torch.float64)
+    cov = A @ A.transpose(1, 2) / 6 + 0.1 * torch.eye(6, dtype=torch.float64)
+    L = O.prec_chol_from_cov(cov)
+    eye = torch.eye(6, dtype=torch.float64).expand(3, 6, 6)
+    torch.testing.assert_close(L @ L.transpose(1, 2) @ cov, eye, rtol=0, atol=1e-10)
+    assert torch.all(torch.triu(L, 1) == 0) and torch.all(torch.diagonal(L, dim1=1, dim2=2) > 0)
+    d = torch.tensor([0.5, 2.0, 4.0], dtype=torch.float64)
+    torch.testing.assert_close(O.prec_chol_from_cov(torch.diag(d)), torch.diag(d.rsqrt()),
+                               rtol=0, atol=1e-14)
