@@ -123,3 +123,14 @@ def test_python_layer_rejects_cpu_tensors():
         flash_gmm_estep(X, torch.zeros(2, 3), torch.zeros(2), torch.zeros(2))
     with pytest.raises(FlashGMMError):
         flash_gmm_estep(X, torch.zeros(2, 3), torch.zeros(2), torch.zeros(2))
+
+
+def test_reference_module_names_resolve():
+    """The reference's module names import and expose its entry points."""
+    import importlib
+    import flash_gmm
+    for mod, fn in (("flash_gmm", "flash_gmm_estep"), ("flash_gmm_h100", "flash_gmm_estep"),
+                    ("flash_gmm_diag_h100", "flash_gmm_estep_diag"),
+                    ("flash_gmm_full_h100", "flash_gmm_estep_full")):
+        m = importlib.import_module(mod)
+        assert getattr(m, fn) is getattr(flash_gmm, fn)
