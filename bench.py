@@ -1,6 +1,6 @@
 """E-step throughput on one MI355X: samples/s and fraction of the fp32 MFMA peak.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 20] [--no-cpu-baseline]
                     [--workload iso_n1m_k1024_d128|diag_n1m_k1024_d96|full_n250k_k256_d64]
 
 Default workload (the headline): the isotropic E-step at N=1,000,000, K=1024,
@@ -187,7 +187,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--atomic-reduce", action="store_true")
     ap.add_argument("--dense", action="store_true",

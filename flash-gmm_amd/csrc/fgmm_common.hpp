@@ -147,6 +147,22 @@ __device__ __forceinline__ void cross_tile_fast(float (&out)[16], LA loadA, LB l
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Sum of n floats p[0], p[stride], ... in fp64, left to right (a fixed order, so
+// the result is deterministic); eight loads are issued before their adds.
+__device__ __forceinline__ double strided_sum(const float* __restrict__ p, int n, int64_t stride) {
+  double s = 0.0;
+  int i = 0;
+  for (; i + 8 <= n; i += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[(int64_t)(i + u) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += (double)v[u];
+  }
+  for (; i < n; ++i) s += (double)p[(int64_t)i * stride];
+  return s;
+}
+
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 __host__ __device__ constexpr int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
 

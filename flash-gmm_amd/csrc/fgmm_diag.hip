@@ -614,13 +614,9 @@ __global__ __launch_bounds__(256) void diag_reduce(const float* __restrict__ par
   if (idx >= K * D) return;
   const int64_t k = idx / D;
   const int d = (int)(idx % D);
-  double sm = 0.0, sq = 0.0, nk = 0.0;
-  for (int p = 0; p < npart; ++p) {
-    const int64_t o = ((int64_t)p * KP + k) * DP + d;
-    sm += (double)part_mu[o];
-    sq += (double)part_sq[o];
-    nk += (double)part_nk[(int64_t)p * KP + k];
-  }
+  const double sm = strided_sum(part_mu + k * DP + d, npart, (int64_t)KP * DP);
+  const double sq = strided_sum(part_sq + k * DP + d, npart, (int64_t)KP * DP);
+  const double nk = strided_sum(part_nk + k, npart, KP);
   const double m = (double)mu[k * ldmu + d];
   const double sg = sq - 2.0 * m * sm + m * m * nk;
   float* om = mu_acc + k * D + d;

@@ -631,9 +631,8 @@ __global__ __launch_bounds__(256) void full_reduce(const float* __restrict__ par
     // the block is symmetric only in sum, so read (d1%32, d2%32) directly.
     const int e1 = (d1 / 32 == b1) ? d1 % 32 : d2 % 32;
     const int e2 = (d1 / 32 == b1) ? d2 % 32 : d1 % 32;
-    double s = 0.0;
-    for (int p = 0; p < npart; ++p)
-      s += (double)part_sig[(((int64_t)p * KP + k) * NSB + sb) * 1024 + e1 * 32 + e2];
+    const double s = strided_sum(part_sig + ((int64_t)k * NSB + sb) * 1024 + e1 * 32 + e2, npart,
+                                 (int64_t)KP * NSB * 1024);
     float* o = sig_outer + idx;
     *o = accumulate ? (float)((double)*o + s) : (float)s;
     return;
@@ -642,16 +641,14 @@ __global__ __launch_bounds__(256) void full_reduce(const float* __restrict__ par
   if (j < K * D) {
     const int64_t k = j / D;
     const int d = (int)(j % D);
-    double s = 0.0;
-    for (int p = 0; p < npart; ++p) s += (double)part_mu[((int64_t)p * KP + k) * DP + d];
+    const double s = strided_sum(part_mu + k * DP + d, npart, (int64_t)KP * DP);
     float* o = mu_acc + j;
     *o = accumulate ? (float)((double)*o + s) : (float)s;
     return;
   }
   const int64_t kk = j - K * D;
   if (kk < K) {
-    double s = 0.0;
-    for (int p = 0; p < npart; ++p) s += (double)part_nk[(int64_t)p * KP + kk];
+    const double s = strided_sum(part_nk + kk, npart, KP);
     Nk[kk] = accumulate ? (float)((double)Nk[kk] + s) : (float)s;
   }
 }

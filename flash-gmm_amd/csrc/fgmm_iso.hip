@@ -613,14 +613,14 @@ __global__ __launch_bounds__(256) void iso_reduce(const float* __restrict__ part
   const int col = (int)(idx % W);
   double s = 0.0;
   if (col < D) {
-    for (int sl = 0; sl < nslab; ++sl) s += (double)part_mu[((int64_t)sl * KP + k) * DP + col];
+    s = strided_sum(part_mu + k * DP + col, nslab, (int64_t)KP * DP);
     float* o = mu_acc + k * D + col;
     *o = accumulate ? (float)((double)*o + s) : (float)s;
   } else if (col == D) {
-    for (int sl = 0; sl < nslab; ++sl) s += (double)part_nk[(int64_t)sl * KP + k];
+    s = strided_sum(part_nk + k, nslab, KP);
     Nk[k] = accumulate ? (float)((double)Nk[k] + s) : (float)s;
   } else {
-    for (int sl = 0; sl < nslab; ++sl) s += (double)part_sig[(int64_t)sl * KP + k];
+    s = strided_sum(part_sig + k, nslab, KP);
     sig_acc[k] = accumulate ? (float)((double)sig_acc[k] + s) : (float)s;
   }
 }
