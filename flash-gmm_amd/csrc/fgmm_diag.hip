@@ -393,8 +393,9 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int ro = 8 * (i >> 2) + (i & 3);
-        // Steps whose 64 responsibilities are all exactly zero add nothing.
-        if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
+        // Steps whose 64 responsibilities are all exactly zero add nothing (tested
+        // only where a step holds enough matrix work to pay for the test).
+        if (NJ < 2 || dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
 #pragma unroll
           for (int j = 0; j < NJ; ++j) {
             const float xv = xbase[ro * RS + 32 * j];

@@ -15,12 +15,14 @@
 //               term is a 32x32x2 fp32 MFMA contraction (S^T = mu . X^T, so every
 //               lane owns one row) and the log-sum-exp is an online max/sum in
 //               registers. Writes logZ and per-row (||x||^2, logZ2) in fp64.
-//   iso_accum   pass 2, grid over (row slab x group of 128 components). Each wave
-//               owns 32 components (mu resident in registers) and walks its slab in
-//               32-row tiles staged through LDS: S = X . mu^T on MFMA, r = 2^(ll2 -
-//               logZ2) in registers, then mu_acc += r^T X on MFMA with r used directly
-//               as the A operand (no transpose), Nk and sig_acc on the VALU. Writes one
-//               partial per (slab, component).
+//   iso_accum_lds / iso_accum_split
+//               pass 2, grid over (row slab x group of 128 components). Each wave
+//               owns 32 components and walks its slab in 32-row tiles staged through
+//               LDS: S = X . mu^T on MFMA, r = 2^(ll2 - logZ2) in registers, then
+//               mu_acc += r^T X on MFMA with r used directly as the A operand (no
+//               transpose), Nk and sig_acc on the VALU. Writes one partial per
+//               (slab, row group, component). Up to D = 128 mu sits in LDS; above,
+//               two waves share a component block, one half of D each.
 //   iso_reduce  fixed-order fp64 sum of the slab partials (deterministic), or
 //               the atomic variant selected by FGMM_FLAG_ATOMIC_REDUCE.
 //
@@ -52,17 +54,19 @@ constexpr int kAccWaves = 8;   // pass-2 LDS variant: waves per workgroup
 constexpr int kAccThreads = 64 * kAccWaves;
 constexpr int kRowGroups = 2;  // pass-2 LDS variant: row groups per workgroup
 
-// Waves per SIMD of the register-resident pass-2 variant (used for D > 128).
-__host__ __device__ constexpr int accum_waves_per_eu(int DP) { return DP <= 96 ? 2 : 1; }
 
-// Pass 2 runs one workgroup per CU: the LDS-resident variant (D <= 128, eight
-// waves, ~100-135 KB of LDS) or the register-resident variant (D > 128, four
-// waves at one wave per SIMD).
+// Pass 2 runs one workgroup of eight waves per CU: the LDS-resident variant for
+// D <= 128 (mu of 4 component blocks and 64-row X tiles in LDS), or for D > 128
+// the split variant (4 component blocks x 2 halves of the dimensions, each wave
+// holding its half of mu in registers), for which D is padded to a multiple of 64.
 __host__ __device__ constexpr bool accum_uses_lds(int DP) { return DP <= 128; }
+__host__ inline int iso_padded_dim(int64_t D) {
+  return D <= 128 ? (int)round_up(D < 1 ? 1 : D, 32) : (int)round_up(D, 64);
+}
 
 struct IsoPlan {
   int64_t N, K, D;
-  int DP;       // D padded to a multiple of 32
+  int DP;       // D padded to a multiple of 32 (of 64 above 128)
   int KB;       // 32-component blocks
   int KP;       // K padded to a multiple of 32
   int ncg;      // groups of kWaves component blocks (pass 2)
@@ -76,7 +80,7 @@ struct IsoPlan {
 IsoPlan make_plan(int64_t N, int64_t K, int64_t D) {
   IsoPlan p{};
   p.N = N; p.K = K; p.D = D;
-  p.DP = (int)round_up(D < 1 ? 1 : D, 32);
+  p.DP = iso_padded_dim(D);
   p.KB = (int)cdiv(K, 32);
   p.KP = p.KB * 32;
   p.ncg = (int)cdiv(p.KB, kWaves);
@@ -268,167 +272,6 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 // Pass 2: responsibilities and sufficient statistics, split over components.
 // ---------------------------------------------------------------------------
 template <int DP>
-constexpr size_t accum_lds_bytes() {
-  return (size_t)2 * 32 * (DP + 4) * sizeof(float) + (size_t)2 * 32 * sizeof(double2);
-}
-
-
-template <int DP>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(accum_waves_per_eu(DP), accum_waves_per_eu(DP))))
-void iso_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
-               const f32x4* __restrict__ mu_sw, const double4* __restrict__ kc_lin, int KB, int KP,
-               const double2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
-               float* __restrict__ part_mu, float* __restrict__ part_nk, float* __restrict__ part_sig) {
-  constexpr int NM = DP / 8;
-  constexpr int NJ = DP / 32;      // 32-column blocks of mu_acc
-  constexpr int RS = DP + 4;       // LDS row stride in floats
-  constexpr int V4 = DP / 4;       // float4 per row
-  constexpr int LPT = (32 * V4) / kThreads;  // float4 loads per thread per tile
-  static_assert((32 * V4) % kThreads == 0, "tile load must split evenly");
-
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  float* xs = reinterpret_cast<float*>(lds_raw);                                  // [2][32*RS]
-  RowStat* rs = reinterpret_cast<RowStat*>(lds_raw + 2 * 32 * RS * sizeof(float));  // [2][32]
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = lane & 31, g = lane >> 5;
-  const int slab = blockIdx.x % nslab;
-  const int cg = blockIdx.x / nslab;
-  const int kb = cg * kWaves + wave;
-  const bool active = kb < KB;
-
-  const int64_t r_begin = (int64_t)slab * rows_per_slab;
-  int64_t r_end = r_begin + rows_per_slab;
-  if (r_end > N) r_end = N;
-  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
-
-  f32x4 mub[NM];
-  double Ck = -INFINITY;
-  float bkf = 0.0f, musqf = 0.0f;
-  if (active) {
-#pragma unroll
-    for (int m = 0; m < NM; ++m) mub[m] = mu_sw[((int64_t)kb * NM + m) * 64 + lane];
-    const double4 kc = kc_lin[(int64_t)kb * 32 + c];
-    Ck = kc.x; bkf = (float)kc.y; musqf = (float)kc.z;
-  } else {
-#pragma unroll
-    for (int m = 0; m < NM; ++m) mub[m] = zero4();
-  }
-
-  f32x16 acc[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
-  float nk = 0.0f, sig = 0.0f;
-
-  // Cooperative tile load: 32 rows x DP columns -> registers -> LDS.
-  f32x4 stage[LPT];
-  double2 rstage = make_double2(0.0, INFINITY);
-  auto fetch = [&](int t) {
-    const int64_t row0 = r_begin + (int64_t)t * 32;
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) {
-      const int idx = q * kThreads + tid;
-      const int rr = idx / V4, c4 = idx % V4;
-      const int64_t row = row0 + rr;
-      stage[q] = load_row4(X, ldx, row, c4 * 4, D, row < r_end);
-    }
-    if (tid < 32) {
-      const int64_t row = row0 + tid;
-      rstage = (row < r_end) ? rowstat[row] : make_double2(0.0, INFINITY);
-    }
-  };
-  auto commit = [&](int buf) {
-    float* dst = xs + buf * 32 * RS;
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) {
-      const int idx = q * kThreads + tid;
-      const int rr = idx / V4, c4 = idx % V4;
-      *reinterpret_cast<f32x4*>(dst + rr * RS + c4 * 4) = stage[q];
-    }
-    if (tid < 32) rs[buf * 32 + tid] = RowStat{rstage.y, (float)rstage.x, 0.0f};
-  };
-
-  if (ntiles > 0) {
-    fetch(0);
-    commit(0);
-  }
-  __syncthreads();
-
-  // One barrier per tile.  The global loads of tile t+1 are issued after the
-  // responsibilities of tile t are formed (the S partials are dead by then) and
-  // land in registers while the accumulation MFMAs run; they are written to
-  // the other LDS buffer just before the barrier.  That buffer was last read in
-  // iteration t-1, which every wave finished before the previous barrier.
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    const bool more = t + 1 < ntiles;
-    const float* xt = xs + buf * 32 * RS;
-    const RowStat* rt = rs + buf * 32;
-    // S[row][comp] = sum_d X[row][d] mu[comp][d] : lane = component, register i = row acc_row(i, g).
-    float xm[16];
-    if (active)
-      cross_tile_fast<NM>(
-          xm, [&](int m) { return *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * m + 4 * g); },
-          [&](int m) { return mub[m]; });
-    float r[16];
-    if (active) {
-      // Rows of this lane's accumulator registers: acc_row(i, g) = 4g + (8*(i/4) + i%4).
-      const RowStat* rbase = rt + 4 * g;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ro = 8 * (i >> 2) + (i & 3);
-        // One 16-byte LDS read per row: {logZ2 (fp64), ||x||^2 (fp32), pad}.
-        const uint4 w = *reinterpret_cast<const uint4*>(rbase + ro);
-        const double q = __hiloint2double((int)w.y, (int)w.x);
-        const float u = fmaf(-2.0f, xm[i], __uint_as_float(w.z));  // ||x||^2 - 2 x.mu
-        const float dq = (float)(Ck - q);                          // C_k - logZ2, rounded once
-        const float rv = fast_exp2(fmaf(-bkf, u, dq));
-        nk += rv;
-        sig = fmaf(rv, u + musqf, sig);
-        r[i] = rv;
-      }
-    }
-    if (more) fetch(t + 1);
-    if (active) {
-      const float* xbase = xt + 4 * g * RS + c;
-      // mu_acc[comp][32j + n] += sum_rows r[row][comp] * X[row][32j + n]
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ro = 8 * (i >> 2) + (i & 3);
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
-      }
-    }
-    if (more) commit(buf ^ 1);
-    __syncthreads();
-  }
-
-  if (active) {
-    nk += __shfl_xor(nk, 32);
-    sig += __shfl_xor(sig, 32);
-    const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[j][i];
-    }
-    if (g == 0) {
-      part_nk[kbase + c] = nk;
-      part_sig[kbase + c] = sig;
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Pass 2, D <= 128: eight waves per workgroup = 2 row groups x 4 component
-// blocks.  mu for the workgroup's 128 components is resident in LDS (matrix-
-// core B operand, shared by both row groups); X streams through LDS in 64-row
-// super-tiles (32 rows per row group), double buffered.  Each wave writes its
-// own partial, indexed (slab, row group).
-// ---------------------------------------------------------------------------
-template <int DP>
 constexpr size_t accum_lds_lds_bytes() {
   return (size_t)kWaves * DP * 32 * sizeof(float)                      // mu, 4 blocks
          + (size_t)2 * 32 * kRowGroups * (DP + 4) * sizeof(float)      // X, 2 buffers
@@ -569,8 +412,9 @@ void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       for (int i = 0; i < 16; ++i) {
         const int ro = 8 * (i >> 2) + (i & 3);
         // A step whose 64 responsibilities are all exactly zero adds nothing:
-        // skip it (wave-uniform branch; identical results).
-        if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
+        // skip it (wave-uniform branch; identical results).  With a single MFMA
+        // per step the test costs more than it saves.
+        if (NJ < 2 || dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
 #pragma unroll
           for (int j = 0; j < NJ; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
         }
@@ -593,6 +437,180 @@ void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     if (g == 0) {
       part_nk[kbase + c] = nk;
       part_sig[kbase + c] = sig;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2 for D > 128: eight waves = 4 component blocks x 2 halves of the
+// dimensions.  Each wave keeps mu of its block and half in registers and forms
+// the fp32 partial cross term of the tile over its half; the halves meet in LDS
+// and are added in a fixed order, so both waves of a block form the same r.
+// Each wave then accumulates r^T X for the columns of its half.
+// ---------------------------------------------------------------------------
+template <int DP>
+constexpr size_t accum_split_lds_bytes() {
+  return (size_t)2 * 32 * (DP + 4) * sizeof(float)       // X, 2 buffers of 32 rows
+         + (size_t)2 * 32 * sizeof(RowStat)               // row state, 2 buffers
+         + (size_t)kAccWaves * 16 * 64 * sizeof(float);   // partial cross terms
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
+void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                     const f32x4* __restrict__ mu_sw, const double4* __restrict__ kc_lin, int KB, int KP,
+                     const double2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
+                     float* __restrict__ part_mu, float* __restrict__ part_nk,
+                     float* __restrict__ part_sig, int dense) {
+  constexpr int HD = DP / 2;       // dimensions per wave
+  constexpr int NM = DP / 8;       // operand chunks of a full row
+  constexpr int NMH = HD / 8;      // chunks per half
+  constexpr int NJH = HD / 32;     // accumulator tiles per wave
+  constexpr int RS = DP + 4;
+  constexpr int V4 = DP / 4;
+  constexpr int LPT = (32 * V4) / kAccThreads;
+  static_assert(HD % 32 == 0 && NMH % 4 == 0 && (32 * V4) % kAccThreads == 0, "split shape");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  float* xs = reinterpret_cast<float*>(lds_raw);                                         // [2][32*RS]
+  RowStat* rs = reinterpret_cast<RowStat*>(lds_raw + 2 * 32 * RS * sizeof(float));       // [2][32]
+  float* ex = reinterpret_cast<float*>(lds_raw + 2 * 32 * RS * sizeof(float) +
+                                       2 * 32 * sizeof(RowStat));                         // [8][16][64]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int cb = wave & 3, h = wave >> 2;
+  const int slab = blockIdx.x % nslab;
+  const int cg = blockIdx.x / nslab;
+  const int kb = cg * kWaves + cb;
+  const bool active = kb < KB;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
+
+  f32x4 mub[NMH];
+#pragma unroll
+  for (int m = 0; m < NMH; ++m)
+    mub[m] = active ? mu_sw[((int64_t)kb * NM + h * NMH + m) * 64 + lane] : zero4();
+  double Ck = -INFINITY;
+  float bkf = 0.0f, musqf = 0.0f;
+  if (active) {
+    const double4 kc = kc_lin[(int64_t)kb * 32 + c];
+    Ck = kc.x; bkf = (float)kc.y; musqf = (float)kc.z;
+  }
+
+  f32x16 acc[NJH];
+#pragma unroll
+  for (int j = 0; j < NJH; ++j) acc[j] = zero16();
+  float nk = 0.0f, sig = 0.0f;
+
+  f32x4 stage[LPT];
+  double2 rstage = make_double2(0.0, INFINITY);
+  const bool full_d = (D == DP);
+  auto fetch = [&](int t) {
+    const int64_t row0 = r_begin + (int64_t)t * 32;
+    if (full_d && row0 + 32 <= r_end) {
+      const float* src = X + row0 * ldx;
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        const int64_t row = row0 + idx / V4;
+        stage[q] = load_row4(X, ldx, row, (idx % V4) * 4, D, row < r_end);
+      }
+    }
+    if (tid < 32) {
+      const int64_t row = row0 + tid;
+      rstage = (row < r_end) ? rowstat[row] : make_double2(0.0, INFINITY);
+    }
+  };
+  auto commit = [&](int buf) {
+    float* dst = xs + buf * 32 * RS;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      *reinterpret_cast<f32x4*>(dst + (idx / V4) * RS + (idx % V4) * 4) = stage[q];
+    }
+    if (tid < 32) rs[buf * 32 + tid] = RowStat{rstage.y, (float)rstage.x, 0.0f};
+  };
+
+  if (ntiles > 0) {
+    fetch(0);
+    commit(0);
+  }
+  __syncthreads();
+
+  float* my_ex = ex + wave * 16 * 64 + lane;
+  const float* ex0 = ex + cb * 16 * 64 + lane;          // half 0 of this block
+  const float* ex1 = ex + (kWaves + cb) * 16 * 64 + lane;  // half 1
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    const float* xt = xs + buf * 32 * RS;
+    const RowStat* rt = rs + buf * 32;
+    if (active) {
+      float xm[16];
+      const float* xrow = xt + c * RS + h * HD + 4 * g;
+      cross_tile_fast<NMH>(
+          xm, [&](int m) { return *reinterpret_cast<const f32x4*>(xrow + 8 * m); },
+          [&](int m) { return mub[m]; });
+#pragma unroll
+      for (int i = 0; i < 16; ++i) my_ex[i * 64] = xm[i];
+    }
+    __syncthreads();
+    if (more) fetch(t + 1);
+    if (active) {
+      float r[16];
+      const RowStat* rbase = rt + 4 * g;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ro = 8 * (i >> 2) + (i & 3);
+        const float xm = ex0[i * 64] + ex1[i * 64];
+        const uint4 w = *reinterpret_cast<const uint4*>(rbase + ro);
+        const double q = __hiloint2double((int)w.y, (int)w.x);
+        const float u = fmaf(-2.0f, xm, __uint_as_float(w.z));
+        const float dq = (float)(Ck - q);
+        const float rv = fast_exp2(fmaf(-bkf, u, dq));
+        nk += rv;
+        sig = fmaf(rv, u + musqf, sig);
+        r[i] = rv;
+      }
+      const float* xbase = xt + 4 * g * RS + h * HD + c;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ro = 8 * (i >> 2) + (i & 3);
+        if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
+#pragma unroll
+          for (int j = 0; j < NJH; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
+        }
+      }
+    }
+    if (more) commit(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (active) {
+    const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+#pragma unroll
+    for (int j = 0; j < NJH; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        part_mu[(kbase + acc_row(i, g)) * DP + h * HD + 32 * j + c] = acc[j][i];
+    }
+    if (h == 0) {
+      nk += __shfl_xor(nk, 32);
+      sig += __shfl_xor(sig, 32);
+      if (g == 0) {
+        part_nk[kbase + c] = nk;
+        part_sig[kbase + c] = sig;
+      }
     }
   }
 }
@@ -685,15 +703,15 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
                        (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
                        pmu, pnk, psig, dense ? 1 : 0);
   } else {
-    constexpr size_t lds = accum_lds_bytes<DP>();
+    constexpr size_t lds = accum_split_lds_bytes<DP>();
     if (lds > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum<DP>),
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_split<DP>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(iso_accum<DP>, grid2, dim3(kThreads), lds, stream, X, ldx, pl.N, (int)pl.D,
-                       mu_sw, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab, pmu, pnk,
-                       psig);
+    hipLaunchKernelGGL(iso_accum_split<DP>, grid2, dim3(kAccThreads), lds, stream, X, ldx, pl.N,
+                       (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
+                       pmu, pnk, psig, dense ? 1 : 0);
   }
   return hipGetLastError();
 }
@@ -755,9 +773,7 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
       case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       case 96: e = launch_passes<96>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       case 128: e = launch_passes<128>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 160: e = launch_passes<160>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       case 192: e = launch_passes<192>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 224: e = launch_passes<224>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       case 256: e = launch_passes<256>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       default: return FGMM_ERR_UNSUPPORTED;
     }

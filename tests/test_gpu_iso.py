@@ -42,6 +42,7 @@ SHAPES = [
     # (N, K, D)
     (1, 1, 1), (31, 3, 5), (33, 17, 3), (129, 33, 32), (1000, 100, 96), (257, 64, 100),
     (300, 40, 128), (200, 32, 129), (150, 7, 256), (2048, 1, 64), (4097, 70, 64),
+    (3000, 150, 160), (2500, 260, 192), (1800, 130, 250),
 ]
 
 
@@ -115,13 +116,15 @@ def _into(inp, dev, **kw):
     return out
 
 
-@pytest.mark.parametrize("case", ["clustered_d128", "clustered_d64_ragged", "plain_d32"])
+@pytest.mark.parametrize("case", ["clustered_d128", "clustered_d64_ragged", "plain_d32", "clustered_d256"])
 def test_zero_step_skip_is_bitwise_dense(case, gpu_device):
     """Skipping all-zero responsibility steps changes no bit of any output."""
     if case == "clustered_d128":
         inp = data.iso_clustered(12000, 1024, 128, seed=1)   # mostly zero steps
     elif case == "clustered_d64_ragged":
         inp = data.iso_clustered(7777, 300, 61, seed=5)
+    elif case == "clustered_d256":
+        inp = data.iso_clustered(6000, 512, 256, seed=6)   # split-dimension pass 2
     else:
         inp = data.iso_plain(10000, 64, 32, seed=0)          # no zero steps
     a = _into(inp, gpu_device)
@@ -167,6 +170,12 @@ def test_headline_shape_mid_size(gpu_device):
     """K=1024, D=128 clustered data at N=65,536 against the float64 oracle."""
     inp = data.iso_clustered(65536, 1024, 128, seed=1)
     assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "K1024 D128 N65536")
+
+
+def test_wide_shape_mid_size(gpu_device):
+    """D=256 (split-dimension accumulation) at N=16,384, K=512 against the float64 oracle."""
+    inp = data.iso_clustered(16384, 512, 256, seed=7)
+    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "K512 D256 N16384")
 
 
 def test_headline_shape_full_size_properties(gpu_device):
