@@ -13,7 +13,8 @@
 // 2D-feature operand [-w, 2v] out in matrix-core order, a log-normaliser pass with
 // X resident in registers (the x^2 half of the feature vector is formed on the fly),
 // an accumulation pass split over component groups x row slabs with r used directly
-// as the A operand of r^T [x | x^2], and a fixed-order fp64 reduction of the slab
+// as the A operand of r^T [x | x^2] (above D = 96 with the dimensions split over
+// two waves per component block), and a fixed-order fp64 reduction of the slab
 // partials.  Row slabs are disjoint ([s*R, min(N, (s+1)*R))), so no row is counted
 // twice at a slab boundary.
 
@@ -35,9 +36,12 @@ constexpr int kRowGroups = 2;
 // 64-row X buffers fit in LDS.
 __host__ __device__ constexpr bool diag_accum_uses_lds(int DP) { return DP <= 96; }
 
-// Above D = 128 the dimensions are split over two waves per component block in
-// pass 2 (diag_accum_split), so D is padded to a multiple of 64 there.
-__host__ __device__ constexpr bool diag_accum_split_d(int DP) { return DP > 128; }
+// From D = 97 on, pass 2 splits the dimensions over two waves per component block
+// (diag_accum_split); above 128, D is padded to a multiple of 64.  At D = 128 the
+// features of a half fit registers with two waves per SIMD (4 component blocks
+// per workgroup); wider halves run one wave per SIMD (2 blocks per workgroup).
+__host__ __device__ constexpr bool diag_accum_split_d(int DP) { return DP > 96; }
+__host__ __device__ constexpr int split_blocks(int DP) { return DP <= 128 ? 4 : 2; }
 __host__ inline int diag_padded_dim(int64_t D) {
   return D <= 128 ? (int)round_up(D < 1 ? 1 : D, 32) : (int)round_up(D, 64);
 }
@@ -59,7 +63,7 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D) {
   p.FP = 2 * p.DP;
   p.KB = (int)cdiv(K, 32);
   p.KP = p.KB * 32;
-  p.cpg = diag_accum_split_d(p.DP) ? kWaves / 2 : kWaves;
+  p.cpg = diag_accum_split_d(p.DP) ? split_blocks(p.DP) : kWaves;
   p.ncg = (int)cdiv(p.KB, p.cpg);
   p.rgroups = diag_accum_uses_lds(p.DP) ? kRowGroups : 1;
   const int64_t tile_rows = 32 * p.rgroups;
@@ -237,22 +241,19 @@ void diag_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2.  One template for both residency variants:
-//   LDS = true : 8 waves (2 row groups x 4 component blocks), mu' in LDS.
-//   LDS = false: 4 waves (1 row group), mu' resident in registers.
-// r^T [x | x^2] accumulates into 2*DP/32 32x32 tiles per wave.
+// Pass 2 up to D = 96: 8 waves (2 row groups x 4 component blocks), the features
+// of the 4 blocks in LDS.  r^T [x | x^2] accumulates into 2*DP/32 32x32 tiles per
+// wave.
 // ---------------------------------------------------------------------------
-template <int DP, bool LDS>
+template <int DP>
 constexpr size_t accum_lds_bytes() {
-  constexpr int RG = LDS ? kRowGroups : 1;
-  return (LDS ? (size_t)kWaves * (2 * DP) * 32 * sizeof(float) : 0) +
-         (size_t)2 * 32 * RG * (DP + 4) * sizeof(float) + (size_t)2 * 32 * RG * sizeof(double);
+  return (size_t)kWaves * (2 * DP) * 32 * sizeof(float) +
+         (size_t)2 * 32 * kRowGroups * (DP + 4) * sizeof(float) +
+         (size_t)2 * 32 * kRowGroups * sizeof(double);
 }
 
-template <int DP, bool LDS>
-__global__ __attribute__((amdgpu_flat_work_group_size(LDS ? kAccThreads : kThreads,
-                                                      LDS ? kAccThreads : kThreads),
-                          amdgpu_waves_per_eu(LDS ? 2 : 1, LDS ? 2 : 1)))
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                 const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_lin, int KB, int KP,
                 const double* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
@@ -264,21 +265,21 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   constexpr int RS = DP + 4;
   constexpr int V4 = DP / 4;
   constexpr int BLK = NM * 64;
-  constexpr int RG = LDS ? kRowGroups : 1;
-  constexpr int NT = LDS ? kAccThreads : kThreads;
+  constexpr int RG = kRowGroups;
+  constexpr int NT = kAccThreads;
   constexpr int TR = 32 * RG;
   constexpr int LPT = (TR * V4) / NT;
   static_assert((TR * V4) % NT == 0, "even split");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  const size_t mu_bytes = LDS ? (size_t)kWaves * BLK * sizeof(f32x4) : 0;
+  const size_t mu_bytes = (size_t)kWaves * BLK * sizeof(f32x4);
   f32x4* mu_l = reinterpret_cast<f32x4*>(lds_raw);
   float* xs = reinterpret_cast<float*>(lds_raw + mu_bytes);                               // [2][TR*RS]
   double* rs = reinterpret_cast<double*>(lds_raw + mu_bytes + 2 * TR * RS * sizeof(float));  // [2][TR]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
-  const int cbw = wave & 3, rg = LDS ? (wave >> 2) : 0;
+  const int cbw = wave & 3, rg = wave >> 2;
   const int slab = blockIdx.x % nslab;
   const int cg = blockIdx.x / nslab;
   const int kb = cg * kWaves + cbw;
@@ -289,8 +290,7 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   if (r_end > N) r_end = N;
   const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
 
-  f32x4 mub[LDS ? 1 : NM];
-  if constexpr (LDS) {
+  {
     constexpr int MPT = (kWaves * BLK) / kAccThreads;
 #pragma unroll
     for (int q = 0; q < MPT; ++q) {
@@ -299,9 +299,6 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       const int kbq = cg * kWaves + b;
       mu_l[idx] = (kbq < KB) ? mu_sw[(int64_t)kbq * BLK + (idx % BLK)] : zero4();
     }
-  } else {
-#pragma unroll
-    for (int m = 0; m < NM; ++m) mub[m] = active ? mu_sw[((int64_t)kb * NM + m) * 64 + lane] : zero4();
   }
   const double Ck = active ? kc_lin[(int64_t)kb * 32 + c] : -INFINITY;
 
@@ -374,10 +371,7 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
             *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * (m < NMX ? m : m - NMX) + 4 * g);
         return m < NMX ? sq4(v) : v;
       };
-      if constexpr (LDS)
-        cross_tile<NM>(xm, la, [&](int m) { return mb[m * 64]; });
-      else
-        cross_tile<NM>(xm, la, [&](int m) { return mub[m]; });
+      cross_tile<NM>(xm, la, [&](int m) { return mb[m * 64]; });
       const double* rbase = rt + 4 * g;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -426,8 +420,9 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2 for D > 128: four waves = 2 component blocks x 2 halves of the
-// dimensions.  Each wave keeps the features [-w | 2v] of its half resident in
+// Pass 2 above D = 96: two waves per component block (2 or 4 blocks per
+// workgroup), one per half of the dimensions.  Each wave keeps the features
+// [-w | 2v] of its half resident in
 // registers and forms the partial contraction over that half (accurate fp64
 // form); the two halves are exchanged through LDS and summed in a fixed order,
 // so both waves of a component block hold the same log-joint and r.  Each wave
@@ -435,13 +430,14 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 // ---------------------------------------------------------------------------
 template <int DP>
 constexpr size_t accum_split_lds_bytes() {
-  return (size_t)2 * 32 * (DP + 4) * sizeof(float)      // X, 2 buffers of 32 rows
-         + (size_t)2 * 32 * sizeof(double)               // row logZ2, 2 buffers
-         + (size_t)kWaves * 16 * 64 * sizeof(double);    // partial contractions
+  return (size_t)2 * 32 * (DP + 4) * sizeof(float)                     // X, 2 buffers of 32 rows
+         + (size_t)2 * 32 * sizeof(double)                              // row logZ2, 2 buffers
+         + (size_t)2 * split_blocks(DP) * 16 * 64 * sizeof(double);    // partial contractions
 }
 
 template <int DP>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(1, 1)))
+__global__ __attribute__((amdgpu_flat_work_group_size(128 * split_blocks(DP), 128 * split_blocks(DP)),
+                          amdgpu_waves_per_eu(split_blocks(DP) / 2, split_blocks(DP) / 2)))
 void diag_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                       const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_lin, int KB,
                       int KP, const double* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
@@ -454,8 +450,10 @@ void diag_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D
   constexpr int NJH = HD / 32;         // 32-column accumulator tiles per wave
   constexpr int RS = DP + 4;
   constexpr int V4 = DP / 4;
-  constexpr int LPT = (32 * V4) / kThreads;
-  static_assert(HD % 32 == 0 && (32 * V4) % kThreads == 0, "split shape");
+  constexpr int CB = split_blocks(DP);  // component blocks per workgroup
+  constexpr int NT = 128 * CB;          // two waves per block
+  constexpr int LPT = (32 * V4) / NT;
+  static_assert(HD % 32 == 0 && (32 * V4) % NT == 0, "split shape");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   float* xs = reinterpret_cast<float*>(lds_raw);                                           // [2][32*RS]
@@ -468,7 +466,7 @@ void diag_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D
   const int cb = wave >> 1, h = wave & 1;
   const int slab = blockIdx.x % nslab;
   const int cg = blockIdx.x / nslab;
-  const int kb = cg * 2 + cb;
+  const int kb = cg * CB + cb;
   const bool active = kb < KB;
 
   const int64_t r_begin = (int64_t)slab * rows_per_slab;
@@ -502,13 +500,13 @@ void diag_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D
       const float* src = X + row0 * ldx;
 #pragma unroll
       for (int q = 0; q < LPT; ++q) {
-        const int idx = q * kThreads + tid;
+        const int idx = q * NT + tid;
         stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
       }
     } else {
 #pragma unroll
       for (int q = 0; q < LPT; ++q) {
-        const int idx = q * kThreads + tid;
+        const int idx = q * NT + tid;
         const int64_t row = row0 + idx / V4;
         stage[q] = load_row4(X, ldx, row, (idx % V4) * 4, D, row < r_end);
       }
@@ -522,7 +520,7 @@ void diag_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D
     float* dst = xs + buf * 32 * RS;
 #pragma unroll
     for (int q = 0; q < LPT; ++q) {
-      const int idx = q * kThreads + tid;
+      const int idx = q * NT + tid;
       *reinterpret_cast<f32x4*>(dst + (idx / V4) * RS + (idx % V4) * 4) = stage[q];
     }
     if (tid < 32) rs[buf * 32 + tid] = rstage;
@@ -657,22 +655,21 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
       if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(diag_accum_split<DP>, dim3((unsigned)(pl.nslab * pl.ncg)), dim3(kThreads),
+    hipLaunchKernelGGL(diag_accum_split<DP>, dim3((unsigned)(pl.nslab * pl.ncg)), dim3(128 * split_blocks(DP)),
                        lds2, stream, X, ldx, pl.N, (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat,
                        pl.nslab, pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_mu),
                        reinterpret_cast<float*>(ws + pl.off_part_sq),
                        reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
     return hipGetLastError();
   } else {
-    constexpr bool L = diag_accum_uses_lds(DP);
-    constexpr size_t lds2 = accum_lds_bytes<DP, L>();
+    constexpr size_t lds2 = accum_lds_bytes<DP>();
     if (lds2 > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum<DP, L>),
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum<DP>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
       if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((diag_accum<DP, L>), dim3((unsigned)(pl.nslab * pl.ncg)),
-                       dim3(L ? kAccThreads : kThreads), lds2, stream, X, ldx, pl.N, (int)pl.D, mu_sw,
+    hipLaunchKernelGGL(diag_accum<DP>, dim3((unsigned)(pl.nslab * pl.ncg)),
+                       dim3(kAccThreads), lds2, stream, X, ldx, pl.N, (int)pl.D, mu_sw,
                        kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
                        reinterpret_cast<float*>(ws + pl.off_part_mu),
                        reinterpret_cast<float*>(ws + pl.off_part_sq),
