@@ -2,6 +2,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 #include <stdint.h>
 
 #include "flashgmm.h"
@@ -167,5 +169,30 @@ __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b
 __host__ __device__ constexpr int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
 
 __host__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Compute units of the current device, cached per device (256 on an MI355X; fewer
+// in a partitioned mode).  Work splits and workspace sizes derive from it, so a
+// workspace query and the call it sizes must run with the same device current.
+// Falls back to 256 where no device is visible (host-only size queries).
+__host__ inline int current_device_cus() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v <= 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+      (void)hipGetLastError();
+      cus = 256;
+    }
+    cache[dev].store(cus, std::memory_order_relaxed);
+    v = cus;
+  }
+  return v;
+}
 
 }  // namespace fgmm

@@ -27,7 +27,6 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kCUs = 256;
 constexpr int kAccWaves = 8;
 constexpr int kAccThreads = 64 * kAccWaves;
 constexpr int kRowGroups = 2;
@@ -68,7 +67,7 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D) {
   p.rgroups = diag_accum_uses_lds(p.DP) ? kRowGroups : 1;
   const int64_t tile_rows = 32 * p.rgroups;
   if (N > 0 && p.ncg > 0) {
-    int64_t want = (int64_t)kCUs / p.ncg;
+    int64_t want = (int64_t)current_device_cus() / p.ncg;
     if (want >= 8) want = (want / 8) * 8;
     if (want < 1) want = 1;
     const int64_t max_slabs = cdiv(N, tile_rows);

@@ -42,7 +42,6 @@ namespace {
 
 constexpr int kWaves = 4;        // waves per workgroup
 constexpr int kThreads = 64 * kWaves;
-constexpr int kCUs = 256;  // MI355X compute units
 
 // Per-row state of pass 2 in LDS: logZ2 in fp64 and ||x||^2 in fp32.
 struct __align__(16) RowStat {
@@ -87,7 +86,7 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D) {
   p.rgroups = accum_uses_lds(p.DP) ? kRowGroups : 1;
   const int64_t tile_rows = 32 * p.rgroups;
   if (N > 0 && p.ncg > 0) {
-    int64_t want = (int64_t)kCUs / p.ncg;
+    int64_t want = (int64_t)current_device_cus() / p.ncg;
     if (want >= 8) want = (want / 8) * 8;  // keeps a slab's workgroups on one XCD
     if (want < 1) want = 1;
     const int64_t max_slabs = cdiv(N, tile_rows);

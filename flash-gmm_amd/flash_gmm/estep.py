@@ -98,7 +98,9 @@ def _check_out(name, t, shape, dev):
 
 
 def _workspace(ws_fn, N, K, D, dev, workspace):
-    ws_bytes = int(ws_fn(N, K, D))
+    # The size depends on the device's compute-unit count: query it with dev current.
+    with torch.cuda.device(dev):
+        ws_bytes = int(ws_fn(N, K, D))
     if workspace is None or workspace.numel() < ws_bytes:
         workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     return workspace

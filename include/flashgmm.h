@@ -8,7 +8,9 @@
  * a negative status; fgmm_strerror() names it.  Nothing aborts or exits.
  *
  * All device memory is owned by the caller: outputs, and a workspace sized by
- * the matching *_workspace_bytes() query.  The library keeps no allocations
+ * the matching *_workspace_bytes() query.  The work split (and so the workspace
+ * size) follows the compute-unit count of the current device: query with the
+ * device current that the call will run on.  The library keeps no allocations
  * between calls.  Calls are re-entrant given distinct outputs and workspaces.
  *
  * Layout conventions (row-major, float32):
