@@ -165,6 +165,21 @@ __device__ __forceinline__ double strided_sum(const float* __restrict__ p, int n
   return s;
 }
 
+// The same sum spread over the 64 lanes of a wave (for large n): lane l adds
+// p[l], p[l + 64], ... in order, then a fixed xor butterfly combines the lanes.
+// Deterministic; every lane returns the total.
+__device__ __forceinline__ double wave_strided_sum(const float* __restrict__ p, int n, int64_t stride,
+                                                   int lane) {
+  double s = 0.0;
+  for (int i = lane; i < n; i += 64) s += (double)p[(int64_t)i * stride];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+  return s;
+}
+
+// Partial counts from which the reductions use one wave per output element.
+constexpr int kWideReduce = 128;
+
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 __host__ __device__ constexpr int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
 

@@ -22,6 +22,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace fgmm {
 namespace {
 
@@ -29,11 +31,26 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kAccWaves = 8;
 constexpr int kAccThreads = 64 * kAccWaves;
-constexpr int kRowGroups = 2;
 
 // LDS-resident pass 2 when mu' of 4 component blocks (4 x 32 x 2*DP floats) and two
 // 64-row X buffers fit in LDS.
 __host__ __device__ constexpr bool diag_accum_uses_lds(int DP) { return DP <= 96; }
+
+// LDS of that pass with CB component blocks per workgroup (8 / CB row groups of
+// 32 rows): features of the blocks, two X buffers, row logZ2.
+constexpr size_t kMaxLds = 160 * 1024;
+__host__ __device__ constexpr size_t accum_lds_bytes_for(int DP, int CB) {
+  return (size_t)CB * (2 * DP) * 32 * sizeof(float) +
+         (size_t)2 * 32 * (8 / CB) * (DP + 4) * sizeof(float) +
+         (size_t)2 * 32 * (8 / CB) * sizeof(double);
+}
+// 4 blocks per workgroup, or 2 / 1 when K has that few blocks (so no wave idles)
+// and the taller X tiles fit.
+__host__ inline int accum_blocks_per_group(int DP, int KB) {
+  if (KB <= 1 && accum_lds_bytes_for(DP, 1) <= kMaxLds) return 1;
+  if (KB <= 2 && accum_lds_bytes_for(DP, 2) <= kMaxLds) return 2;
+  return kWaves;
+}
 
 // From D = 97 on, pass 2 splits the dimensions over two waves per component block
 // (diag_accum_split); above 128, D is padded to a multiple of 64.  At D = 128 the
@@ -62,9 +79,9 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D) {
   p.FP = 2 * p.DP;
   p.KB = (int)cdiv(K, 32);
   p.KP = p.KB * 32;
-  p.cpg = diag_accum_split_d(p.DP) ? split_blocks(p.DP) : kWaves;
+  p.cpg = diag_accum_split_d(p.DP) ? split_blocks(p.DP) : accum_blocks_per_group(p.DP, p.KB);
   p.ncg = (int)cdiv(p.KB, p.cpg);
-  p.rgroups = diag_accum_uses_lds(p.DP) ? kRowGroups : 1;
+  p.rgroups = diag_accum_uses_lds(p.DP) ? kAccWaves / p.cpg : 1;
   const int64_t tile_rows = 32 * p.rgroups;
   if (N > 0 && p.ncg > 0) {
     int64_t want = (int64_t)current_device_cus() / p.ncg;
@@ -240,18 +257,16 @@ void diag_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2 up to D = 96: 8 waves (2 row groups x 4 component blocks), the features
-// of the 4 blocks in LDS.  r^T [x | x^2] accumulates into 2*DP/32 32x32 tiles per
-// wave.
+// Pass 2 up to D = 96: 8 waves (8 / CB row groups x CB component blocks, CB = 4,
+// or 2 / 1 for small K), the features of the blocks in LDS.  r^T [x | x^2]
+// accumulates into 2*DP/32 32x32 tiles per wave.
 // ---------------------------------------------------------------------------
-template <int DP>
+template <int DP, int CB>
 constexpr size_t accum_lds_bytes() {
-  return (size_t)kWaves * (2 * DP) * 32 * sizeof(float) +
-         (size_t)2 * 32 * kRowGroups * (DP + 4) * sizeof(float) +
-         (size_t)2 * 32 * kRowGroups * sizeof(double);
+  return accum_lds_bytes_for(DP, CB);
 }
 
-template <int DP>
+template <int DP, int CB>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                 const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_lin, int KB, int KP,
@@ -264,24 +279,24 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   constexpr int RS = DP + 4;
   constexpr int V4 = DP / 4;
   constexpr int BLK = NM * 64;
-  constexpr int RG = kRowGroups;
+  constexpr int RG = kAccWaves / CB;     // row groups of 32 rows
   constexpr int NT = kAccThreads;
   constexpr int TR = 32 * RG;
   constexpr int LPT = (TR * V4) / NT;
   static_assert((TR * V4) % NT == 0, "even split");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  const size_t mu_bytes = (size_t)kWaves * BLK * sizeof(f32x4);
+  const size_t mu_bytes = (size_t)CB * BLK * sizeof(f32x4);
   f32x4* mu_l = reinterpret_cast<f32x4*>(lds_raw);
   float* xs = reinterpret_cast<float*>(lds_raw + mu_bytes);                               // [2][TR*RS]
   double* rs = reinterpret_cast<double*>(lds_raw + mu_bytes + 2 * TR * RS * sizeof(float));  // [2][TR]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
-  const int cbw = wave & 3, rg = wave >> 2;
+  const int cbw = wave % CB, rg = wave / CB;
   const int slab = blockIdx.x % nslab;
   const int cg = blockIdx.x / nslab;
-  const int kb = cg * kWaves + cbw;
+  const int kb = cg * CB + cbw;
   const bool active = kb < KB;
 
   const int64_t r_begin = (int64_t)slab * rows_per_slab;
@@ -289,15 +304,9 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   if (r_end > N) r_end = N;
   const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
 
-  {
-    constexpr int MPT = (kWaves * BLK) / kAccThreads;
-#pragma unroll
-    for (int q = 0; q < MPT; ++q) {
-      const int idx = q * kAccThreads + tid;
-      const int b = idx / BLK;
-      const int kbq = cg * kWaves + b;
-      mu_l[idx] = (kbq < KB) ? mu_sw[(int64_t)kbq * BLK + (idx % BLK)] : zero4();
-    }
+  for (int idx = tid; idx < CB * BLK; idx += kAccThreads) {
+    const int kbq = cg * CB + idx / BLK;
+    mu_l[idx] = (kbq < KB) ? mu_sw[(int64_t)kbq * BLK + (idx % BLK)] : zero4();
   }
   const double Ck = active ? kc_lin[(int64_t)kb * 32 + c] : -INFINITY;
 
@@ -601,6 +610,7 @@ void diag_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D
 
 // Finish: one thread per (k, d); fixed-order fp64 sums over partials, then the
 // sig identity in fp64.  Thread d == 0 also writes Nk.
+template <bool WIDE>
 __global__ __launch_bounds__(256) void diag_reduce(const float* __restrict__ part_mu,
                                                    const float* __restrict__ part_sq,
                                                    const float* __restrict__ part_nk, int npart, int KP,
@@ -608,13 +618,20 @@ __global__ __launch_bounds__(256) void diag_reduce(const float* __restrict__ par
                                                    int64_t ldmu, float* __restrict__ Nk,
                                                    float* __restrict__ mu_acc, float* __restrict__ sig_acc,
                                                    int accumulate) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  // WIDE: one wave per (k, d) with the partials spread over its lanes (many partials).
+  const int64_t idx = WIDE ? (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)
+                           : (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int lane = threadIdx.x & 63;
   if (idx >= K * D) return;
   const int64_t k = idx / D;
   const int d = (int)(idx % D);
-  const double sm = strided_sum(part_mu + k * DP + d, npart, (int64_t)KP * DP);
-  const double sq = strided_sum(part_sq + k * DP + d, npart, (int64_t)KP * DP);
-  const double nk = strided_sum(part_nk + k, npart, KP);
+  auto sum = [&](const float* p, int64_t stride) {
+    return WIDE ? wave_strided_sum(p, npart, stride, lane) : strided_sum(p, npart, stride);
+  };
+  const double sm = sum(part_mu + k * DP + d, (int64_t)KP * DP);
+  const double sq = sum(part_sq + k * DP + d, (int64_t)KP * DP);
+  const double nk = sum(part_nk + k, KP);
+  if (WIDE && lane != 0) return;
   const double m = (double)mu[k * ldmu + d];
   const double sg = sq - 2.0 * m * sm + m * m * nk;
   float* om = mu_acc + k * D + d;
@@ -661,19 +678,29 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
                        reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
     return hipGetLastError();
   } else {
-    constexpr size_t lds2 = accum_lds_bytes<DP>();
-    if (lds2 > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum<DP>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
-      if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(diag_accum<DP>, dim3((unsigned)(pl.nslab * pl.ncg)),
-                       dim3(kAccThreads), lds2, stream, X, ldx, pl.N, (int)pl.D, mu_sw,
-                       kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
-                       reinterpret_cast<float*>(ws + pl.off_part_mu),
-                       reinterpret_cast<float*>(ws + pl.off_part_sq),
-                       reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
-    return hipGetLastError();
+    auto launch = [&](auto cb_tag) -> hipError_t {
+      constexpr int CB = decltype(cb_tag)::value;
+      constexpr size_t lds2 = accum_lds_bytes<DP, CB>();
+      if constexpr (lds2 > kMaxLds) {
+        return hipErrorInvalidValue;   // never chosen by the plan
+      } else {
+        if (lds2 > 65536) {
+          hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum<DP, CB>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+          if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL((diag_accum<DP, CB>), dim3((unsigned)(pl.nslab * pl.ncg)),
+                           dim3(kAccThreads), lds2, stream, X, ldx, pl.N, (int)pl.D, mu_sw,
+                           kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
+                           reinterpret_cast<float*>(ws + pl.off_part_mu),
+                           reinterpret_cast<float*>(ws + pl.off_part_sq),
+                           reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
+        return hipGetLastError();
+      }
+    };
+    return pl.cpg == 1   ? launch(std::integral_constant<int, 1>{})
+           : pl.cpg == 2 ? launch(std::integral_constant<int, 2>{})
+                         : launch(std::integral_constant<int, kWaves>{});
   }
 }
 
@@ -738,7 +765,9 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     if (e != hipSuccess) return FGMM_ERR_HIP;
   }
   if (!run2) return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
-  hipLaunchKernelGGL(diag_reduce, dim3((unsigned)cdiv(K * D, 256)), dim3(256), 0, stream,
+  const bool wide = pl.npart >= kWideReduce;
+  hipLaunchKernelGGL(wide ? diag_reduce<true> : diag_reduce<false>,
+                     dim3((unsigned)(wide ? cdiv(K * D, 4) : cdiv(K * D, 256))), dim3(256), 0, stream,
                      reinterpret_cast<const float*>(ws + pl.off_part_mu),
                      reinterpret_cast<const float*>(ws + pl.off_part_sq),
                      reinterpret_cast<const float*>(ws + pl.off_part_nk), pl.npart, pl.KP, pl.DP, K,

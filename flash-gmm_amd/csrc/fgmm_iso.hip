@@ -37,6 +37,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace fgmm {
 namespace {
 
@@ -51,7 +53,6 @@ struct __align__(16) RowStat {
 };
 constexpr int kAccWaves = 8;   // pass-2 LDS variant: waves per workgroup
 constexpr int kAccThreads = 64 * kAccWaves;
-constexpr int kRowGroups = 2;  // pass-2 LDS variant: row groups per workgroup
 
 
 // Pass 2 runs one workgroup of eight waves per CU: the LDS-resident variant for
@@ -59,6 +60,23 @@ constexpr int kRowGroups = 2;  // pass-2 LDS variant: row groups per workgroup
 // the split variant (4 component blocks x 2 halves of the dimensions, each wave
 // holding its half of mu in registers), for which D is padded to a multiple of 64.
 __host__ __device__ constexpr bool accum_uses_lds(int DP) { return DP <= 128; }
+
+// LDS of the LDS-resident pass 2 with CB component blocks per workgroup (and
+// 8 / CB row groups of 32 rows): mu of the blocks, two X buffers, row state.
+constexpr size_t kMaxLds = 160 * 1024;
+__host__ __device__ constexpr size_t accum_lds_bytes_for(int DP, int CB) {
+  return (size_t)CB * DP * 32 * sizeof(float) +
+         (size_t)2 * 32 * (8 / CB) * (DP + 4) * sizeof(float) +
+         (size_t)2 * 32 * (8 / CB) * sizeof(double2);
+}
+// Component blocks per pass-2 workgroup: 4, or 2 / 1 when there are that few
+// blocks (K <= 64 / K <= 32) so that no wave idles, where the taller X tiles fit.
+__host__ inline int accum_blocks_per_group(int DP, int KB) {
+  if (!accum_uses_lds(DP)) return kWaves;
+  if (KB <= 1 && accum_lds_bytes_for(DP, 1) <= kMaxLds) return 1;
+  if (KB <= 2 && accum_lds_bytes_for(DP, 2) <= kMaxLds) return 2;
+  return kWaves;
+}
 __host__ inline int iso_padded_dim(int64_t D) {
   return D <= 128 ? (int)round_up(D < 1 ? 1 : D, 32) : (int)round_up(D, 64);
 }
@@ -68,7 +86,8 @@ struct IsoPlan {
   int DP;       // D padded to a multiple of 32 (of 64 above 128)
   int KB;       // 32-component blocks
   int KP;       // K padded to a multiple of 32
-  int ncg;      // groups of kWaves component blocks (pass 2)
+  int cpg;      // component blocks per pass-2 workgroup
+  int ncg;      // groups of cpg component blocks (pass 2)
   int nslab;    // row slabs (pass 2)
   int rgroups;  // row groups per slab (partials per slab)
   int npart;    // nslab * rgroups
@@ -82,8 +101,9 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D) {
   p.DP = iso_padded_dim(D);
   p.KB = (int)cdiv(K, 32);
   p.KP = p.KB * 32;
-  p.ncg = (int)cdiv(p.KB, kWaves);
-  p.rgroups = accum_uses_lds(p.DP) ? kRowGroups : 1;
+  p.cpg = accum_blocks_per_group(p.DP, p.KB);
+  p.ncg = (int)cdiv(p.KB, p.cpg);
+  p.rgroups = accum_uses_lds(p.DP) ? kAccWaves / p.cpg : 1;
   const int64_t tile_rows = 32 * p.rgroups;
   if (N > 0 && p.ncg > 0) {
     int64_t want = (int64_t)current_device_cus() / p.ncg;
@@ -270,14 +290,12 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 // ---------------------------------------------------------------------------
 // Pass 2: responsibilities and sufficient statistics, split over components.
 // ---------------------------------------------------------------------------
-template <int DP>
+template <int DP, int CB>
 constexpr size_t accum_lds_lds_bytes() {
-  return (size_t)kWaves * DP * 32 * sizeof(float)                      // mu, 4 blocks
-         + (size_t)2 * 32 * kRowGroups * (DP + 4) * sizeof(float)      // X, 2 buffers
-         + (size_t)2 * 32 * kRowGroups * sizeof(double2);              // row stats
+  return accum_lds_bytes_for(DP, CB);
 }
 
-template <int DP>
+template <int DP, int CB>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                    const f32x4* __restrict__ mu_sw, const double4* __restrict__ kc_lin, int KB, int KP,
@@ -289,23 +307,23 @@ void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   constexpr int RS = DP + 4;
   constexpr int V4 = DP / 4;
   constexpr int BLK = NM * 64;                   // float4 per 32-component block
-  constexpr int TR = 32 * kRowGroups;            // rows per super-tile
+  constexpr int RG = kAccWaves / CB;             // row groups (32 rows each)
+  constexpr int TR = 32 * RG;                    // rows per super-tile
   constexpr int LPT = (TR * V4) / kAccThreads;   // float4 loads per thread per super-tile
-  constexpr int MPT = (kWaves * BLK) / kAccThreads;
-  static_assert((TR * V4) % kAccThreads == 0 && (kWaves * BLK) % kAccThreads == 0, "even split");
+  static_assert((TR * V4) % kAccThreads == 0 && kAccWaves % CB == 0, "even split");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  f32x4* mu_l = reinterpret_cast<f32x4*>(lds_raw);                                        // [4][BLK]
-  float* xs = reinterpret_cast<float*>(lds_raw + kWaves * BLK * sizeof(f32x4));           // [2][TR*RS]
-  RowStat* rs = reinterpret_cast<RowStat*>(lds_raw + kWaves * BLK * sizeof(f32x4) +
+  f32x4* mu_l = reinterpret_cast<f32x4*>(lds_raw);                                        // [CB][BLK]
+  float* xs = reinterpret_cast<float*>(lds_raw + CB * BLK * sizeof(f32x4));               // [2][TR*RS]
+  RowStat* rs = reinterpret_cast<RowStat*>(lds_raw + CB * BLK * sizeof(f32x4) +
                                            2 * TR * RS * sizeof(float));                  // [2][TR]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
-  const int cbw = wave & 3, rg = wave >> 2;
+  const int cbw = wave % CB, rg = wave / CB;
   const int slab = blockIdx.x % nslab;
   const int cg = blockIdx.x / nslab;
-  const int kb = cg * kWaves + cbw;
+  const int kb = cg * CB + cbw;
   const bool active = kb < KB;
 
   const int64_t r_begin = (int64_t)slab * rows_per_slab;
@@ -313,12 +331,9 @@ void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   if (r_end > N) r_end = N;
   const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
 
-  // mu of the workgroup's four component blocks -> LDS (zeros past KB).
-#pragma unroll
-  for (int q = 0; q < MPT; ++q) {
-    const int idx = q * kAccThreads + tid;
-    const int b = idx / BLK;
-    const int kbq = cg * kWaves + b;
+  // mu of the workgroup's CB component blocks -> LDS (zeros past KB).
+  for (int idx = tid; idx < CB * BLK; idx += kAccThreads) {
+    const int kbq = cg * CB + idx / BLK;
     mu_l[idx] = (kbq < KB) ? mu_sw[(int64_t)kbq * BLK + (idx % BLK)] : zero4();
   }
   double Ck = -INFINITY;
@@ -426,7 +441,7 @@ void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   if (active) {
     nk += __shfl_xor(nk, 32);
     sig += __shfl_xor(sig, 32);
-    const int64_t kbase = ((int64_t)slab * kRowGroups + rg) * KP + (int64_t)kb * 32;
+    const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
 #pragma unroll
@@ -642,6 +657,33 @@ __global__ __launch_bounds__(256) void iso_reduce(const float* __restrict__ part
   }
 }
 
+// The same finish with one wave per output element, for many partials (few
+// components over many row slabs).
+__global__ __launch_bounds__(256) void iso_reduce_wide(const float* __restrict__ part_mu,
+                                                       const float* __restrict__ part_nk,
+                                                       const float* __restrict__ part_sig, int nslab,
+                                                       int KP, int DP, int64_t K, int D,
+                                                       float* __restrict__ Nk, float* __restrict__ mu_acc,
+                                                       float* __restrict__ sig_acc, int accumulate) {
+  const int64_t idx = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int W = D + 2;
+  if (idx >= K * W) return;
+  const int64_t k = idx / W;
+  const int col = (int)(idx % W);
+  if (col < D) {
+    const double s = wave_strided_sum(part_mu + k * DP + col, nslab, (int64_t)KP * DP, lane);
+    float* o = mu_acc + k * D + col;
+    if (lane == 0) *o = accumulate ? (float)((double)*o + s) : (float)s;
+  } else if (col == D) {
+    const double s = wave_strided_sum(part_nk + k, nslab, KP, lane);
+    if (lane == 0) Nk[k] = accumulate ? (float)((double)Nk[k] + s) : (float)s;
+  } else {
+    const double s = wave_strided_sum(part_sig + k, nslab, KP, lane);
+    if (lane == 0) sig_acc[k] = accumulate ? (float)((double)sig_acc[k] + s) : (float)s;
+  }
+}
+
 // Atomic finish: every slab partial is added into the (zeroed or accumulated) outputs.
 __global__ __launch_bounds__(256) void iso_reduce_atomic(const float* __restrict__ part_mu,
                                                          const float* __restrict__ part_nk,
@@ -692,15 +734,27 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   if (!run2) return hipGetLastError();
   const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
   if constexpr (accum_uses_lds(DP)) {
-    constexpr size_t lds = accum_lds_lds_bytes<DP>();
-    if (lds > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_lds<DP>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(iso_accum_lds<DP>, grid2, dim3(kAccThreads), lds, stream, X, ldx, pl.N,
-                       (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
-                       pmu, pnk, psig, dense ? 1 : 0);
+    auto launch = [&](auto cb_tag) -> hipError_t {
+      constexpr int CB = decltype(cb_tag)::value;
+      constexpr size_t lds = accum_lds_lds_bytes<DP, CB>();
+      if constexpr (lds > kMaxLds) {
+        return hipErrorInvalidValue;   // never chosen by the plan
+      } else {
+        if (lds > 65536) {
+          hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_lds<DP, CB>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+          if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL((iso_accum_lds<DP, CB>), grid2, dim3(kAccThreads), lds, stream, X, ldx,
+                           pl.N, (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab,
+                           pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
+        return hipSuccess;
+      }
+    };
+    hipError_t e = pl.cpg == 1   ? launch(std::integral_constant<int, 1>{})
+                   : pl.cpg == 2 ? launch(std::integral_constant<int, 2>{})
+                                 : launch(std::integral_constant<int, kWaves>{});
+    if (e != hipSuccess) return e;
   } else {
     constexpr size_t lds = accum_split_lds_bytes<DP>();
     if (lds > 65536) {
@@ -795,6 +849,10 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
       hipLaunchKernelGGL(iso_reduce_atomic, dim3((unsigned)cdiv(nout, 256), (unsigned)pl.npart),
                          dim3(256), 0, stream, pmu, pnk, psig, pl.npart, pl.KP, pl.DP, K, (int)D, Nk,
                          mu_acc, sig_acc);
+  } else if (pl.npart >= kWideReduce) {
+    hipLaunchKernelGGL(iso_reduce_wide, dim3((unsigned)cdiv(nout, 4)), dim3(256), 0, stream, pmu, pnk,
+                       psig, pl.npart, pl.KP, pl.DP, K, (int)D, Nk, mu_acc, sig_acc,
+                       accumulate ? 1 : 0);
   } else {
     hipLaunchKernelGGL(iso_reduce, dim3((unsigned)cdiv(nout, 256)), dim3(256), 0, stream, pmu, pnk,
                        psig, pl.npart, pl.KP, pl.DP, K, (int)D, Nk, mu_acc, sig_acc,

@@ -63,6 +63,13 @@ def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, gpu_device):
     assert_close_stats(outs[0], oracle(inp), "diag skip")
 
 
+@pytest.mark.parametrize("N,K,D", [(40_000, 30, 16), (30_000, 60, 40), (20_000, 50, 96)])
+def test_small_k_mid_size(N, K, D, gpu_device):
+    """Few component blocks: pass 2 runs 1 or 2 blocks per workgroup with more row groups."""
+    inp = data.diag_clustered(N, K, D, seed=N % 89)
+    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), f"diag small K N={N} K={K} D={D}")
+
+
 def test_equal_variances_match_isotropic(gpu_device):
     inp = data.iso_clustered(3000, 50, 40, seed=12)
     dev = gpu_device

@@ -172,6 +172,18 @@ def test_headline_shape_mid_size(gpu_device):
     assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "K1024 D128 N65536")
 
 
+@pytest.mark.parametrize("N,K,D", [(50_000, 48, 64), (30_000, 20, 30), (40_000, 64, 96)])
+def test_small_k_mid_size(N, K, D, gpu_device):
+    """Few component blocks: pass 2 runs 1 or 2 blocks per workgroup with more row groups."""
+    inp = data.iso_clustered(N, K, D, seed=N % 97)
+    got = run_gpu(inp, gpu_device)
+    assert_close_stats(got, oracle(inp), f"small K N={N} K={K} D={D}")
+    dev = gpu_device
+    dense = _into(inp, dev, dense=True)
+    for u, v in zip(got, dense):
+        assert torch.equal(u, v)
+
+
 def test_wide_shape_mid_size(gpu_device):
     """D=256 (split-dimension accumulation) at N=16,384, K=512 against the float64 oracle."""
     inp = data.iso_clustered(16384, 512, 256, seed=7)
