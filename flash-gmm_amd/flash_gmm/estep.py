@@ -35,6 +35,13 @@ def _require(cond: bool, msg: str) -> None:
         raise FlashGMMError(msg)
 
 
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    """float32 view of a floating tensor (a converted copy for other dtypes): the
+    kernels compute in float32, as the reference does (its wrappers assume float32
+    inputs, flash_gmm.py:187-195)."""
+    return t if t.dtype == torch.float32 else t.float()
+
+
 def _prep_rows(X: torch.Tensor):
     """Return (X, ldx) when the kernels can read X in place, else a padded copy.
 
@@ -61,8 +68,8 @@ def _prep_rows(X: torch.Tensor):
 def _check_common(X, mu, log_pi):
     _require(X.dim() == 2 and mu.dim() == 2, "X must be (N, D) and mu (K, D)")
     _require(X.is_cuda and mu.is_cuda, "Inputs must be on GPU.")  # flash_gmm.py:190
-    _require(X.dtype == torch.float32 and mu.dtype == torch.float32,
-             "X and mu must be float32")
+    _require(X.is_floating_point() and mu.is_floating_point(),
+             "X and mu must be floating point (they are computed on in float32)")
     _require(mu.shape[1] == X.shape[1], f"mu must be (K, D) with D={X.shape[1]}, got {tuple(mu.shape)}")
     _require(mu.device == X.device, "X and mu must be on the same device")
     K = mu.shape[0]
@@ -135,8 +142,8 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     dev = X.device
     lss = _vec(log_sigma_sq, dev, (K,), "log_sigma_sq")
     lpi = _vec(log_pi, dev, (K,), "log_pi")
-    Xk, ldx = _prep_rows(X)
-    muk = _rowmajor(mu)
+    Xk, ldx = _prep_rows(_f32(X))
+    muk = _rowmajor(_f32(mu))
     ldmu = muk.stride(0) if K > 1 else D
     L = _lib.lib()
     workspace = _workspace(L.fgmm_iso_workspace_bytes, N, K, D, dev, workspace)
@@ -191,8 +198,8 @@ def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     lss = _rowmajor(log_sigma_sq.to(device=dev, dtype=torch.float32))
     ldlss = lss.stride(0) if K > 1 else D
     lpi = _vec(log_pi, dev, (K,), "log_pi")
-    Xk, ldx = _prep_rows(X)
-    muk = _rowmajor(mu)
+    Xk, ldx = _prep_rows(_f32(X))
+    muk = _rowmajor(_f32(mu))
     ldmu = muk.stride(0) if K > 1 else D
     L = _lib.lib()
     _require(hasattr(L, "fgmm_diag_estep_f32"), "library built without the diagonal E-step")
@@ -246,8 +253,8 @@ def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
              f"prec_chol must be (K, D, D)=({K}, {D}, {D}), got {tuple(prec_chol.shape)}")
     Lc = prec_chol.to(device=dev, dtype=torch.float32).contiguous()
     lpi = _vec(log_pi, dev, (K,), "log_pi")
-    Xk, ldx = _prep_rows(X)
-    muk = _rowmajor(mu)
+    Xk, ldx = _prep_rows(_f32(X))
+    muk = _rowmajor(_f32(mu))
     ldmu = muk.stride(0) if K > 1 else D
     L = _lib.lib()
     _require(hasattr(L, "fgmm_full_estep_f32"), "library built without the full-covariance E-step")

@@ -90,6 +90,20 @@ def test_strided_inputs(gpu_device):
         assert_close_stats(got, ref, "strided")
 
 
+@pytest.mark.parametrize("dtype", [torch.float64, torch.bfloat16, torch.float16])
+def test_other_float_dtypes_compute_in_float32(dtype, gpu_device):
+    """Non-float32 X / mu are converted (the reference assumes float32 inputs)."""
+    inp = data.iso_clustered(3000, 40, 24, seed=13)
+    dev = gpu_device
+    X, mu, lss, lpi = (inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi"))
+    Xd, mud = X.to(dtype), mu.to(dtype)
+    got = flash_gmm_estep(Xd, mud, lss, lpi)
+    ref = flash_gmm_estep(Xd.float(), mud.float(), lss, lpi)
+    torch.cuda.synchronize()
+    for u, v in zip(got, ref):
+        assert u.dtype == torch.float32 and torch.equal(u, v)
+
+
 def test_block_kwargs_are_accepted(gpu_device):
     inp = data.iso_plain(100, 8, 16, seed=7)
     a = run_gpu(inp, gpu_device)
@@ -217,8 +231,8 @@ def test_rejects_bad_shapes(gpu_device):
         flash_gmm_estep(X, mu[:, :4], lss, lpi)
     with pytest.raises(FlashGMMError):
         flash_gmm_estep(X, mu, lss[:2], lpi)
-    with pytest.raises(FlashGMMError):
-        flash_gmm_estep(X.double(), mu, lss, lpi)
+    with pytest.raises(FlashGMMError):   # not floating point
+        flash_gmm_estep(X.int(), mu, lss, lpi)
     with pytest.raises(FlashGMMError):  # D beyond the compiled range
         Xw = torch.zeros(4, 300, device=gpu_device)
         flash_gmm_estep(Xw, torch.zeros(2, 300, device=gpu_device), lss[:2], lpi[:2])
