@@ -177,6 +177,10 @@ __device__ __forceinline__ double wave_strided_sum(const float* __restrict__ p, 
   return s;
 }
 
+// Largest N one E-step call takes: pass-1 grids hold N / 128 workgroups, which
+// must stay within the 2^31 - 1 grid limit.  Larger data sets stream in chunks.
+constexpr int64_t kMaxRows = (int64_t)1 << 37;
+
 // Partial counts from which the reductions use one wave per output element.
 constexpr int kWideReduce = 128;
 

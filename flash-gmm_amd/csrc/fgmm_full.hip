@@ -731,7 +731,7 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
                 Nk == nullptr || mu_acc == nullptr || sig_outer == nullptr))
     return FGMM_ERR_INVALID_ARG;
   if (D > 128) return FGMM_ERR_UNSUPPORTED;
-  if (N > (int64_t)1 << 40 || K > (int64_t)1 << 20) return FGMM_ERR_UNSUPPORTED;
+  if (N > kMaxRows || K > (int64_t)1 << 20) return FGMM_ERR_UNSUPPORTED;
   const FullPlan pl = make_plan(N, K, D);
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;

@@ -798,7 +798,7 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
                 Nk == nullptr || mu_acc == nullptr || sig_acc == nullptr))
     return FGMM_ERR_INVALID_ARG;
   if (D > 256) return FGMM_ERR_UNSUPPORTED;
-  if (N > (int64_t)1 << 40 || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
+  if (N > kMaxRows || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
   const IsoPlan pl = make_plan(N, K, D);
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;

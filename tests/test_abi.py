@@ -83,6 +83,7 @@ def _call_iso(**kw):
     (dict(ldmu=16), _lib.FGMM_ERR_INVALID_ARG),
     (dict(Nk=None), _lib.FGMM_ERR_INVALID_ARG),
     (dict(D=300, ldx=300, ldmu=300), _lib.FGMM_ERR_UNSUPPORTED),
+    (dict(N=(1 << 37) + 1), _lib.FGMM_ERR_UNSUPPORTED),  # pass-1 grid limit
     (dict(ws_bytes=16), _lib.FGMM_ERR_WORKSPACE),
     (dict(ws=None), _lib.FGMM_ERR_WORKSPACE),
 ])
