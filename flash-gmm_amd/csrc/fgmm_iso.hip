@@ -288,6 +288,129 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 }
 
 // ---------------------------------------------------------------------------
+// Pass 1 above D = 128: eight waves = 4 row groups x 2 halves of the dimensions,
+// so each wave holds half of its 32 rows in registers (two waves per SIMD).  Per
+// component block both halves form their fp64 partial cross terms; the second
+// half's go through LDS (two slots, by block parity) and the first-half wave adds
+// them in a fixed order and runs the online log-sum-exp.  One barrier per block.
+// ---------------------------------------------------------------------------
+template <int DP>
+constexpr size_t lse_split_lds_bytes() {
+  return (size_t)2 * DP * 32 * sizeof(float)                  // mu blocks, 2 buffers
+         + (size_t)3 * 32 * sizeof(double2)                    // constants, 3 buffers
+         + (size_t)2 * kWaves * 16 * 64 * sizeof(double)       // second-half partials
+         + (size_t)kWaves * 64 * sizeof(double);               // second-half ||x||^2
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
+void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                   const f32x4* __restrict__ mu_sw, const double2* __restrict__ kc_blk, int KB,
+                   float* __restrict__ logZ, double2* __restrict__ rowstat) {
+  constexpr int NM = DP / 8;
+  constexpr int NMH = NM / 2;             // chunks per half
+  constexpr int HD = DP / 2;
+  constexpr int BLK = NM * 64;            // float4 per 32-component block
+  constexpr int LPT = BLK / kAccThreads;
+  static_assert(BLK % kAccThreads == 0 && NMH % 2 == 0, "split shape");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  unsigned char* p = lds_raw;
+  f32x4* mu_l = reinterpret_cast<f32x4*>(p);     p += 2 * BLK * sizeof(f32x4);
+  double2* kc_l = reinterpret_cast<double2*>(p); p += 3 * 32 * sizeof(double2);
+  double* ex = reinterpret_cast<double*>(p);     p += 2 * kWaves * 16 * 64 * sizeof(double);
+  double* xq = reinterpret_cast<double*>(p);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int rg = wave & 3, h = wave >> 2;
+  const int64_t row = ((int64_t)blockIdx.x * kWaves + rg) * 32 + c;
+  const bool valid = row < N;
+
+  f32x4 st[LPT];
+  double2 kst = make_double2(0.0, 0.0);
+  auto fetch = [&](int kb) {
+    const f32x4* src = mu_sw + (int64_t)kb * BLK;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) st[q] = src[q * kAccThreads + tid];
+    if (tid < 32) kst = kc_blk[(int64_t)kb * 32 + tid];
+  };
+  // mu of block kb -> buffer kb & 1; its constants -> buffer kb % 3 (the first-half
+  // waves read them after the block's barrier, while others may commit ahead).
+  auto commit = [&](int kb) {
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) mu_l[(kb & 1) * BLK + q * kAccThreads + tid] = st[q];
+    if (tid < 32) kc_l[(kb % 3) * 32 + tid] = kst;
+  };
+  fetch(0);
+
+  f32x4 xb[NMH];
+  double xsq = 0.0;
+#pragma unroll
+  for (int m = 0; m < NMH; ++m) {
+    xb[m] = load_row4(X, ldx, row, h * HD + 8 * m + 4 * g, D, valid);
+    xsq = fma((double)xb[m].x, (double)xb[m].x, xsq);
+    xsq = fma((double)xb[m].y, (double)xb[m].y, xsq);
+    xsq = fma((double)xb[m].z, (double)xb[m].z, xsq);
+    xsq = fma((double)xb[m].w, (double)xb[m].w, xsq);
+  }
+  xsq += __shfl_xor(xsq, 32);
+  if (h == 1) xq[rg * 64 + lane] = xsq;
+  commit(0);
+  __syncthreads();
+  if (h == 0) xsq += xq[rg * 64 + lane];
+
+  double mx = -INFINITY;
+  float sm = 0.0f;
+  for (int kb = 0; kb < KB; ++kb) {
+    const int buf = kb & 1;
+    const bool more = kb + 1 < KB;
+    if (more) fetch(kb + 1);
+    const f32x4* mp = mu_l + buf * BLK + h * NMH * 64 + lane;
+    double xm[16];
+    cross_tile<NMH>(xm, [&](int m) { return mp[m * 64]; }, [&](int m) { return xb[m]; });
+    double* exb = ex + (size_t)(buf * kWaves + rg) * 16 * 64 + lane;
+    if (h == 1) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) exb[i * 64] = xm[i];
+    }
+    if (more) commit(kb + 1);
+    __syncthreads();
+    if (h == 0) {
+      const double2* kp = kc_l + (kb % 3) * 32 + g * 16;
+      double ll[16];
+      double bm = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const double2 cb = kp[i];
+        ll[i] = fma(-cb.y, fma(-2.0, xm[i] + exb[i * 64], xsq), cb.x);
+        bm = fmax(bm, ll[i]);
+      }
+      const double mn = fmax(mx, bm);
+      const double ms = (mn == -INFINITY) ? 0.0 : mn;
+      float acc = sm * fast_exp2((float)(mx - ms));
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc += fast_exp2((float)(ll[i] - ms));
+      sm = acc;
+      mx = mn;
+    }
+  }
+
+  if (h == 0) {
+    const double mo = __shfl_xor(mx, 32);
+    const float so = __shfl_xor(sm, 32);
+    const double mn = fmax(mx, mo);
+    const double ms = (mn == -INFINITY) ? 0.0 : mn;
+    const float tot = sm * fast_exp2((float)(mx - ms)) + so * fast_exp2((float)(mo - ms));
+    const double lz2 = mn + (double)log2f(tot);
+    if (valid && g == 0) {
+      rowstat[row] = make_double2(xsq, lz2);
+      if (logZ) logZ[row] = (float)(lz2 * kLn2);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Pass 2: responsibilities and sufficient statistics, split over components.
 // ---------------------------------------------------------------------------
 template <int DP, int CB>
@@ -721,15 +844,27 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   float* pnk = reinterpret_cast<float*>(ws + pl.off_part_nk);
   float* psig = reinterpret_cast<float*>(ws + pl.off_part_sig);
   if (run1) {
-    constexpr size_t lds1 = lse_lds_bytes<DP>();
-    if (lds1 > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_lse<DP>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
-      if (e != hipSuccess) return e;
-    }
     const int64_t nblk1 = cdiv(pl.N, 32 * kWaves);
-    hipLaunchKernelGGL(iso_lse<DP>, dim3((unsigned)nblk1), dim3(kThreads), lds1, stream, X, ldx,
-                       pl.N, (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
+    if constexpr (accum_uses_lds(DP)) {
+      constexpr size_t lds1 = lse_lds_bytes<DP>();
+      if (lds1 > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_lse<DP>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+        if (e != hipSuccess) return e;
+      }
+      hipLaunchKernelGGL(iso_lse<DP>, dim3((unsigned)nblk1), dim3(kThreads), lds1, stream, X, ldx,
+                         pl.N, (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
+    } else {
+      // Above D = 128 the rows' dimensions are split over two waves.
+      constexpr size_t lds1 = lse_split_lds_bytes<DP>();
+      if (lds1 > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_lse_split<DP>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+        if (e != hipSuccess) return e;
+      }
+      hipLaunchKernelGGL(iso_lse_split<DP>, dim3((unsigned)nblk1), dim3(kAccThreads), lds1, stream,
+                         X, ldx, pl.N, (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
+    }
   }
   if (!run2) return hipGetLastError();
   const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
