@@ -257,6 +257,131 @@ void diag_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 }
 
 // ---------------------------------------------------------------------------
+// Pass 1 from D = 128: eight waves = 4 row groups x 2 halves of the dimensions, so
+// each wave holds half of its 32 rows in registers (two waves per SIMD).  Half h
+// multiplies its x^2 and x chunks by the matching chunks of the mu' block; the
+// second half's fp64 partials go through LDS and the first-half wave adds them in
+// a fixed order and runs the online log-sum-exp.  When two mu' blocks fit in LDS
+// next to two exchange slots, the loop has one barrier per block; otherwise one
+// mu' buffer and one slot, with a second barrier before the buffer is refilled.
+// ---------------------------------------------------------------------------
+template <int DP>
+constexpr int lse_split_mu_buffers() {
+  constexpr size_t blk = (size_t)2 * DP * 32 * sizeof(float);
+  constexpr size_t ex = (size_t)kWaves * 16 * 64 * sizeof(double);
+  return 2 * blk + 2 * ex + 3 * 32 * sizeof(double) <= kMaxLds ? 2 : 1;
+}
+
+template <int DP>
+constexpr size_t lse_split_lds_bytes() {
+  constexpr int MB = lse_split_mu_buffers<DP>();
+  return (size_t)MB * 2 * DP * 32 * sizeof(float)               // mu' blocks
+         + (size_t)MB * kWaves * 16 * 64 * sizeof(double)         // second-half partials
+         + (size_t)(MB + 1) * 32 * sizeof(double);                // constants
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
+void diag_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                    const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_blk, int KB,
+                    float* __restrict__ logZ, double* __restrict__ rowstat) {
+  constexpr int NMX = DP / 8;
+  constexpr int NM = 2 * NMX;
+  constexpr int NMH = NMX / 2;            // x chunks per half
+  constexpr int HD = DP / 2;
+  constexpr int BLK = NM * 64;
+  constexpr int LPT = BLK / kAccThreads;
+  constexpr int MB = lse_split_mu_buffers<DP>();
+  constexpr int NKC = MB + 1;             // constant buffers
+  static_assert(BLK % kAccThreads == 0 && NMH % 2 == 0, "split shape");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  unsigned char* p = lds_raw;
+  f32x4* mu_l = reinterpret_cast<f32x4*>(p);   p += (size_t)MB * BLK * sizeof(f32x4);
+  double* ex = reinterpret_cast<double*>(p);   p += (size_t)MB * kWaves * 16 * 64 * sizeof(double);
+  double* kc_l = reinterpret_cast<double*>(p);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int rg = wave & 3, h = wave >> 2;
+  const int64_t row = ((int64_t)blockIdx.x * kWaves + rg) * 32 + c;
+  const bool valid = row < N;
+
+  f32x4 st[LPT];
+  double kst = 0.0;
+  auto fetch = [&](int kb) {
+    const f32x4* src = mu_sw + (int64_t)kb * BLK;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) st[q] = src[q * kAccThreads + tid];
+    if (tid < 32) kst = kc_blk[(int64_t)kb * 32 + tid];
+  };
+  auto commit = [&](int kb) {
+    f32x4* dst = mu_l + (MB == 2 ? (kb & 1) : 0) * BLK;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) dst[q * kAccThreads + tid] = st[q];
+    if (tid < 32) kc_l[(kb % NKC) * 32 + tid] = kst;
+  };
+  fetch(0);
+  f32x4 xb[NMH];
+#pragma unroll
+  for (int m = 0; m < NMH; ++m) xb[m] = load_row4(X, ldx, row, h * HD + 8 * m + 4 * g, D, valid);
+  commit(0);
+  __syncthreads();
+
+  double mx = -INFINITY;
+  float sm = 0.0f;
+  for (int kb = 0; kb < KB; ++kb) {
+    const int buf = MB == 2 ? (kb & 1) : 0;
+    const bool more = kb + 1 < KB;
+    if (more) fetch(kb + 1);
+    // Chunks 0..NMH-1 pair x^2 with mu' chunks h*NMH.., the rest x with NMX + h*NMH..
+    const f32x4* mp = mu_l + buf * BLK + h * NMH * 64 + lane;
+    double xm[16];
+    cross_tile<2 * NMH>(xm, [&](int m) { return m < NMH ? mp[m * 64] : mp[(NMX - NMH + m) * 64]; },
+                        [&](int m) { return m < NMH ? sq4(xb[m]) : xb[m - NMH]; });
+    double* exb = ex + (size_t)(buf * kWaves + rg) * 16 * 64 + lane;
+    if (h == 1) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) exb[i * 64] = xm[i];
+    }
+    if (MB == 2 && more) commit(kb + 1);
+    __syncthreads();
+    if (MB == 1 && more) commit(kb + 1);
+    if (h == 0) {
+      const double* kp = kc_l + (kb % NKC) * 32 + g * 16;
+      double ll[16];
+      double bm = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        ll[i] = kp[i] + (xm[i] + exb[i * 64]);
+        bm = fmax(bm, ll[i]);
+      }
+      const double mn = fmax(mx, bm);
+      const double ms = (mn == -INFINITY) ? 0.0 : mn;
+      float acc = sm * fast_exp2((float)(mx - ms));
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc += fast_exp2((float)(ll[i] - ms));
+      sm = acc;
+      mx = mn;
+    }
+    if (MB == 1) __syncthreads();
+  }
+
+  if (h == 0) {
+    const double mo = __shfl_xor(mx, 32);
+    const float so = __shfl_xor(sm, 32);
+    const double mn = fmax(mx, mo);
+    const double ms = (mn == -INFINITY) ? 0.0 : mn;
+    const float tot = sm * fast_exp2((float)(mx - ms)) + so * fast_exp2((float)(mo - ms));
+    const double lz2 = mn + (double)log2f(tot);
+    if (valid && g == 0) {
+      rowstat[row] = lz2;
+      if (logZ) logZ[row] = (float)(lz2 * kLn2);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Pass 2 up to D = 96: 8 waves (8 / CB row groups x CB component blocks, CB = 4,
 // or 2 / 1 for small K), the features of the blocks in LDS.  r^T [x | x^2]
 // accumulates into 2*DP/32 32x32 tiles per wave.
@@ -654,14 +779,27 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
   const double* kc_lin = reinterpret_cast<const double*>(ws + pl.off_kclin);
   double* rowstat = reinterpret_cast<double*>(ws + pl.off_rowstat);
   if (run1) {
-    constexpr size_t lds1 = lse_lds_bytes<DP>();
-    if (lds1 > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_lse<DP>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
-      if (e != hipSuccess) return e;
+    const unsigned nblk1 = (unsigned)cdiv(pl.N, 32 * kWaves);
+    if constexpr (!diag_accum_split_d(DP)) {
+      constexpr size_t lds1 = lse_lds_bytes<DP>();
+      if (lds1 > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_lse<DP>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+        if (e != hipSuccess) return e;
+      }
+      hipLaunchKernelGGL(diag_lse<DP>, dim3(nblk1), dim3(kThreads), lds1, stream, X, ldx, pl.N,
+                         (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
+    } else {
+      // From D = 128 the rows' dimensions are split over two waves.
+      constexpr size_t lds1 = lse_split_lds_bytes<DP>();
+      if (lds1 > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_lse_split<DP>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+        if (e != hipSuccess) return e;
+      }
+      hipLaunchKernelGGL(diag_lse_split<DP>, dim3(nblk1), dim3(kAccThreads), lds1, stream, X, ldx,
+                         pl.N, (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
     }
-    hipLaunchKernelGGL(diag_lse<DP>, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
-                       stream, X, ldx, pl.N, (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
   }
   if (!run2) return hipGetLastError();
   if constexpr (diag_accum_split_d(DP)) {
