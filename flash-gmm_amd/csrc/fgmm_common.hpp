@@ -177,6 +177,45 @@ __device__ __forceinline__ double wave_strided_sum(const float* __restrict__ p, 
   return s;
 }
 
+// ---------------------------------------------------------------------------
+// Stored log-joint.  Pass 1 can keep the fp32 log-joint (log2 units) of every
+// (32-row tile, 32-component block) pair in the workspace, so that pass 2 reads
+// it instead of recomputing the contraction.  Tiles are ordered (row tile,
+// component block), 1024 floats each, in pass 1's register order: the pass-1
+// lane l (row l % 32; component acc_row(i, l / 32) in register i) writes
+// register i at i * 64 + l, so each store instruction fills 256 contiguous
+// bytes.  Component k of row r therefore sits at
+//     (4 * (k >> 3) + (k & 3)) * 64 + 32 * ((k >> 2) & 1) + r,
+// and the pass-2 lane (component k = lane % 32, g = lane / 32), whose register
+// i = 4q + j holds row 8q + 4g + j, reads four float4 at that offset for
+// r = 8q + 4g.  The 4 loads of a wave cover each 128-byte line of the tile.
+// ---------------------------------------------------------------------------
+constexpr int kLjTile = 1024;   // floats per (row tile, component block)
+
+// Workgroup barrier for LDS hand-offs.  __syncthreads() also drains every
+// outstanding global access of the wave (vmcnt(0) on gfx9), which would stall on
+// the log-joint stores and on loads prefetched for the next iteration; this one
+// waits for the wave's LDS accesses only.  The memory clobber keeps the compiler
+// from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ void lj_store(float* __restrict__ tile, int lane, const double (&ll)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) __builtin_nontemporal_store((float)ll[i], tile + i * 64 + lane);
+}
+
+__device__ __forceinline__ void lj_load(const float* __restrict__ tile, int lane, f32x4 (&v)[4]) {
+  const int k = lane & 31, g = lane >> 5;
+  const float* p = tile + (4 * (k >> 3) + (k & 3)) * 64 + 32 * ((k >> 2) & 1) + 4 * g;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const f32x4*>(p + 8 * q);
+}
+
+// Workspace cap for the stored log-joint of one call (N/32 x K/32 tiles of 4 KiB).
+constexpr size_t kMaxLjBytes = (size_t)16 << 30;
+
 // Largest N one E-step call takes: pass-1 grids hold N / 128 workgroups, which
 // must stay within the 2^31 - 1 grid limit.  Larger data sets stream in chunks.
 constexpr int64_t kMaxRows = (int64_t)1 << 37;

@@ -299,7 +299,9 @@ extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn 
   const int64_t ld = round_up(D, 4);
   const int64_t rows = R < N ? R : N;
   const size_t chunk_bytes = (size_t)rows * ld * sizeof(float);
-  const size_t ws_bytes = fgmm_iso_workspace_bytes(rows, K, D);
+  // The E-steps hide behind host generation and copies: keep the lean workspace.
+  constexpr unsigned estep_flags = FGMM_FLAG_ACCUMULATE | FGMM_FLAG_RECOMPUTE;
+  const size_t ws_bytes = fgmm_iso_workspace_bytes_ex(rows, K, D, estep_flags);
   const int64_t nparts = cdiv(rows, 1024);
 
   StreamRes res;
@@ -404,7 +406,7 @@ extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn 
     if (!ok(hipStreamWaitEvent(res.comp, res.h2d1[b], 0)) || !ok(hipEventRecord(res.e0[b], res.comp)))
       return FGMM_ERR_HIP;
     st = fgmm_iso_estep_f32(res.dev[b], ld, n, D, mu, D, K, log_sigma_sq, log_pi, res.logZ, res.Nk,
-                            res.mu_acc, res.sig_acc, res.ws, ws_bytes, FGMM_FLAG_ACCUMULATE, res.comp);
+                            res.mu_acc, res.sig_acc, res.ws, ws_bytes, estep_flags, res.comp);
     if (st != FGMM_OK) return st;
     hipLaunchKernelGGL(sum_blocks, dim3((unsigned)cdiv(n, 1024)), dim3(256), 0, res.comp, res.logZ, n,
                        res.part);

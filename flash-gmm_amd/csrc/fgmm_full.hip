@@ -713,6 +713,12 @@ extern "C" size_t fgmm_full_workspace_bytes(int64_t N, int64_t K, int64_t D) {
   return make_plan(N, K, D).total;
 }
 
+extern "C" size_t fgmm_full_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
+  (void)flags;
+  if (N < 0 || K < 0 || D < 1) return 0;
+  return make_plan(N, K, D).total;
+}
+
 extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
                                    int64_t ldmu, int64_t K, const float* prec_chol, const float* log_pi,
                                    float* logZ, float* Nk, float* mu_acc, float* sig_outer,

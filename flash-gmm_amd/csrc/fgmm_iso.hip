@@ -35,6 +35,7 @@
 
 #include "fgmm_common.hpp"
 
+#include <float.h>
 #include <math.h>
 
 #include <type_traits>
@@ -92,18 +93,35 @@ struct IsoPlan {
   int rgroups;  // row groups per slab (partials per slab)
   int npart;    // nslab * rgroups
   int64_t rows_per_slab;
-  size_t off_musw, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_nk, off_part_sig, total;
+  bool lj;      // pass 1 stores the log-joint; pass 2 reads it
+  size_t off_musw, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_nk, off_part_sig, off_lj,
+      total;
 };
 
-IsoPlan make_plan(int64_t N, int64_t K, int64_t D) {
+// Pass 2 reads the stored log-joint when recomputation is not requested, D is at
+// least 33 (below, the recomputed contraction costs less than the extra traffic),
+// there are at least 4 component blocks (8 above D = 128, where the pass-2 tile
+// of 4 blocks would not fit in registers), and the tiles fit under kMaxLjBytes.
+__host__ inline bool use_stored_lj(int64_t N, int DP, int KB, bool allow) {
+  return allow && DP >= 64 && KB >= (DP <= 128 ? 4 : 8) &&
+         (size_t)round_up(cdiv(N, 32), 4) * (size_t)KB * kLjTile * sizeof(float) <= kMaxLjBytes;
+}
+
+IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true) {
   IsoPlan p{};
   p.N = N; p.K = K; p.D = D;
   p.DP = iso_padded_dim(D);
   p.KB = (int)cdiv(K, 32);
   p.KP = p.KB * 32;
-  p.cpg = accum_blocks_per_group(p.DP, p.KB);
+  p.lj = use_stored_lj(N, p.DP, p.KB, allow_lj);
+  if (p.lj) {
+    p.cpg = p.KB >= 8 ? 8 : 4;
+    p.rgroups = kAccWaves / p.cpg;
+  } else {
+    p.cpg = accum_blocks_per_group(p.DP, p.KB);
+    p.rgroups = accum_uses_lds(p.DP) ? kAccWaves / p.cpg : 1;
+  }
   p.ncg = (int)cdiv(p.KB, p.cpg);
-  p.rgroups = accum_uses_lds(p.DP) ? kAccWaves / p.cpg : 1;
   const int64_t tile_rows = 32 * p.rgroups;
   if (N > 0 && p.ncg > 0) {
     int64_t want = (int64_t)current_device_cus() / p.ncg;
@@ -126,6 +144,8 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D) {
   p.off_part_mu = off; off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
   p.off_part_nk = off; off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
   p.off_part_sig = off; off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
+  p.off_lj = off;   // one tile per pass-1 wave: the grid's 32-row tiles, rounded up to 4
+  if (p.lj) off = align256(off + (size_t)round_up(cdiv(N, 32), 4) * p.KB * kLjTile * sizeof(float));
   p.total = off;
   return p;
 }
@@ -194,12 +214,12 @@ constexpr size_t lse_lds_bytes() {
   return (size_t)2 * DP * 32 * sizeof(float) + (size_t)2 * 32 * sizeof(double2);
 }
 
-template <int DP>
+template <int DP, bool LJ>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(DP <= 160 ? 2 : 1, DP <= 160 ? 2 : 1)))
 void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
              const f32x4* __restrict__ mu_sw, const double2* __restrict__ kc_blk, int KB,
-             float* __restrict__ logZ, double2* __restrict__ rowstat) {
+             float* __restrict__ logZ, double2* __restrict__ rowstat, float* __restrict__ lj) {
   constexpr int NM = DP / 8;
   constexpr int BLK = NM * 64;            // float4 per 32-component block
   constexpr int LPT = BLK / kThreads;     // float4 per thread per block
@@ -211,7 +231,8 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
-  const int64_t row = ((int64_t)blockIdx.x * kWaves + wave) * 32 + c;
+  const int64_t tile = (int64_t)blockIdx.x * kWaves + wave;   // 32-row tile
+  const int64_t row = tile * 32 + c;
   const bool valid = row < N;
 
   f32x4 st[LPT];
@@ -241,7 +262,7 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   }
   xsq += __shfl_xor(xsq, 32);
   commit(0);
-  __syncthreads();
+  lds_barrier();
 
   double mx = -INFINITY;
   float sm = 0.0f;
@@ -263,6 +284,11 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       ll[i] = fma(-cb.y, fma(-2.0, xm[i], xsq), cb.x);
       bm = fmax(bm, ll[i]);
     }
+    // Keep the max here: sunk past the conditional commit below, its operands
+    // would cross a block boundary and each cost a canonicalising max.
+    asm volatile("" : "+v"(bm));
+    // Unconditional: tiles are allocated for the whole grid.
+    if constexpr (LJ) lj_store(lj + (tile * KB + kb) * kLjTile, lane, ll);
     const double mn = fmax(mx, bm);
     const double ms = (mn == -INFINITY) ? 0.0 : mn;
     float acc = sm * fast_exp2((float)(mx - ms));
@@ -271,7 +297,7 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     sm = acc;
     mx = mn;
     if (more) commit(buf ^ 1);
-    __syncthreads();
+    lds_barrier();
   }
 
   // Merge the two half-waves that hold the same row.
@@ -302,11 +328,11 @@ constexpr size_t lse_split_lds_bytes() {
          + (size_t)kWaves * 64 * sizeof(double);               // second-half ||x||^2
 }
 
-template <int DP>
+template <int DP, bool LJ>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                    const f32x4* __restrict__ mu_sw, const double2* __restrict__ kc_blk, int KB,
-                   float* __restrict__ logZ, double2* __restrict__ rowstat) {
+                   float* __restrict__ logZ, double2* __restrict__ rowstat, float* __restrict__ lj) {
   constexpr int NM = DP / 8;
   constexpr int NMH = NM / 2;             // chunks per half
   constexpr int HD = DP / 2;
@@ -324,7 +350,8 @@ void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
   const int rg = wave & 3, h = wave >> 2;
-  const int64_t row = ((int64_t)blockIdx.x * kWaves + rg) * 32 + c;
+  const int64_t tile = (int64_t)blockIdx.x * kWaves + rg;   // 32-row tile
+  const int64_t row = tile * 32 + c;
   const bool valid = row < N;
 
   f32x4 st[LPT];
@@ -357,7 +384,7 @@ void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   xsq += __shfl_xor(xsq, 32);
   if (h == 1) xq[rg * 64 + lane] = xsq;
   commit(0);
-  __syncthreads();
+  lds_barrier();
   if (h == 0) xsq += xq[rg * 64 + lane];
 
   double mx = -INFINITY;
@@ -375,7 +402,7 @@ void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       for (int i = 0; i < 16; ++i) exb[i * 64] = xm[i];
     }
     if (more) commit(kb + 1);
-    __syncthreads();
+    lds_barrier();
     if (h == 0) {
       const double2* kp = kc_l + (kb % 3) * 32 + g * 16;
       double ll[16];
@@ -386,6 +413,7 @@ void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
         ll[i] = fma(-cb.y, fma(-2.0, xm[i] + exb[i * 64], xsq), cb.x);
         bm = fmax(bm, ll[i]);
       }
+      if constexpr (LJ) lj_store(lj + (tile * KB + kb) * kLjTile, lane, ll);
       const double mn = fmax(mx, bm);
       const double ms = (mn == -INFINITY) ? 0.0 : mn;
       float acc = sm * fast_exp2((float)(mx - ms));
@@ -753,6 +781,184 @@ void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 }
 
 // ---------------------------------------------------------------------------
+// Pass 2 from the stored log-joint: grid over (row slab x group of CB component
+// blocks); eight waves = CB component blocks x 8 / CB row groups of 32 rows.
+// Each wave reads the log-joint tile of its block and rows (4 KiB, prefetched one
+// tile ahead), forms r = 2^(ll2 - logZ2) and accumulates r^T X on the matrix
+// cores from the X tile that the workgroup's blocks share in LDS.  ||x - mu_k||^2
+// for sig_acc comes back from the log-joint as (C0_k - ll2) / b_k, where
+// C0_k = C_k + b_k ||mu_k||^2.  logZ2 sits in LDS as a hi + lo pair of floats,
+// so ll2 - logZ2 keeps the accuracy of the fp32 log-joint.
+// ---------------------------------------------------------------------------
+template <int DP, int CB>
+constexpr size_t accum_lj_lds_bytes() {
+  return (size_t)2 * 32 * (kAccWaves / CB) * ((DP + 4) * sizeof(float) + sizeof(float2));
+}
+
+template <int DP, int CB>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
+void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                  const float* __restrict__ lj, const double4* __restrict__ kc_lin, int KB, int KP,
+                  const double2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
+                  float* __restrict__ part_mu, float* __restrict__ part_nk, float* __restrict__ part_sig,
+                  int dense) {
+  constexpr int NJ = DP / 32;
+  constexpr int RS = DP + 4;
+  constexpr int V4 = DP / 4;
+  constexpr int RG = kAccWaves / CB;             // row groups (32 rows each)
+  constexpr int TR = 32 * RG;                    // rows per super-tile
+  constexpr int NV = TR * V4;                    // float4 per super-tile
+  constexpr int LPT = (NV + kAccThreads - 1) / kAccThreads;
+  static_assert(kAccWaves % CB == 0, "even split");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  float* xs = reinterpret_cast<float*>(lds_raw);                                  // [2][TR*RS]
+  float2* rz = reinterpret_cast<float2*>(lds_raw + 2 * TR * RS * sizeof(float));  // [2][TR]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int cbw = wave % CB, rg = wave / CB;
+  const int slab = blockIdx.x % nslab;
+  const int cg = blockIdx.x / nslab;
+  const int kb = cg * CB + cbw;
+  const bool active = kb < KB;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
+
+  // C0_k and 1 / b_k; zero for padding and for components with log_pi = -inf
+  // (their r is 0, and the clamp below keeps 0 * inf out of sig).
+  float c0 = 0.0f, ibk = 0.0f;
+  if (active) {
+    const double4 kc = kc_lin[(int64_t)kb * 32 + c];
+    const double c0d = fma(kc.y, kc.z, kc.x);
+    if (c0d > -INFINITY && c0d < INFINITY) {
+      c0 = (float)c0d;
+      ibk = (float)(1.0 / kc.y);
+    }
+  }
+
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
+  float nk = 0.0f, sig = 0.0f;
+
+  f32x4 stage[LPT];
+  double rq = INFINITY;
+  const bool full_d = (D == DP);
+  auto fetch = [&](int t) {
+    const int64_t row0 = r_begin + (int64_t)t * TR;
+    if (full_d && row0 + TR <= r_end) {
+      const float* src = X + row0 * ldx;
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        if (NV % kAccThreads == 0 || idx < NV)
+          stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        const int64_t row = row0 + idx / V4;
+        stage[q] = load_row4(X, ldx, row, (idx % V4) * 4, D, idx < NV && row < r_end);
+      }
+    }
+    if (tid < TR) {
+      const int64_t row = row0 + tid;
+      rq = (row < r_end) ? rowstat[row].y : INFINITY;
+    }
+  };
+  auto commit = [&](int buf) {
+    float* dst = xs + buf * TR * RS;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      if (NV % kAccThreads == 0 || idx < NV)
+        *reinterpret_cast<f32x4*>(dst + (idx / V4) * RS + (idx % V4) * 4) = stage[q];
+    }
+    if (tid < TR) {
+      // Rows past the slab get logZ2 = +inf, hence r = 0.
+      const float hi = (float)rq;
+      const float lo = (rq > -INFINITY && rq < INFINITY) ? (float)(rq - (double)hi) : 0.0f;
+      rz[buf * TR + tid] = make_float2(hi, lo);
+    }
+  };
+  auto lj_fetch = [&](int t, f32x4 (&v)[4]) {
+    const int64_t row0 = r_begin + (int64_t)t * TR + rg * 32;
+    if (active && row0 < r_end) {
+      lj_load(lj + ((row0 >> 5) * KB + kb) * kLjTile, lane, v);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = zero4();
+    }
+  };
+
+  f32x4 ljc[4], ljn[4];
+  if (ntiles > 0) {
+    fetch(0);
+    lj_fetch(0, ljc);
+    commit(0);
+  }
+  lds_barrier();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    if (more) {
+      fetch(t + 1);
+      lj_fetch(t + 1, ljn);
+    }
+    const float* xt = xs + buf * TR * RS + rg * 32 * RS;
+    const float2* rt = rz + buf * TR + rg * 32 + 4 * g;
+    if (active) {
+      float r[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ro = 8 * (i >> 2) + (i & 3);
+        const float2 z = rt[ro];
+        const float l = ljc[i >> 2][i & 3];
+        const float rv = fast_exp2((l - z.x) - z.y);
+        nk += rv;
+        sig = fmaf(rv, fminf((c0 - l) * ibk, FLT_MAX), sig);
+        r[i] = rv;
+      }
+      const float* xbase = xt + 4 * g * RS + c;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ro = 8 * (i >> 2) + (i & 3);
+        if (NJ < 2 || dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
+        }
+      }
+    }
+    if (more) commit(buf ^ 1);
+    lds_barrier();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ljc[q] = ljn[q];
+  }
+
+  if (active) {
+    nk += __shfl_xor(nk, 32);
+    sig += __shfl_xor(sig, 32);
+    const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[j][i];
+    }
+    if (g == 0) {
+      part_nk[kbase + c] = nk;
+      part_sig[kbase + c] = sig;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Finish: fixed-order fp64 reduction over slabs (deterministic).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void iso_reduce(const float* __restrict__ part_mu,
@@ -843,31 +1049,60 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   float* pmu = reinterpret_cast<float*>(ws + pl.off_part_mu);
   float* pnk = reinterpret_cast<float*>(ws + pl.off_part_nk);
   float* psig = reinterpret_cast<float*>(ws + pl.off_part_sig);
+  float* lj = pl.lj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
   if (run1) {
     const int64_t nblk1 = cdiv(pl.N, 32 * kWaves);
     if constexpr (accum_uses_lds(DP)) {
       constexpr size_t lds1 = lse_lds_bytes<DP>();
       if (lds1 > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_lse<DP>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
-        if (e != hipSuccess) return e;
+        for (const void* f : {reinterpret_cast<const void*>(&iso_lse<DP, false>),
+                              reinterpret_cast<const void*>(&iso_lse<DP, true>)}) {
+          hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+          if (e != hipSuccess) return e;
+        }
       }
-      hipLaunchKernelGGL(iso_lse<DP>, dim3((unsigned)nblk1), dim3(kThreads), lds1, stream, X, ldx,
-                         pl.N, (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
+      auto kern = pl.lj ? &iso_lse<DP, true> : &iso_lse<DP, false>;
+      hipLaunchKernelGGL(kern, dim3((unsigned)nblk1), dim3(kThreads), lds1, stream, X, ldx, pl.N,
+                         (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat, lj);
     } else {
       // Above D = 128 the rows' dimensions are split over two waves.
       constexpr size_t lds1 = lse_split_lds_bytes<DP>();
       if (lds1 > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_lse_split<DP>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
-        if (e != hipSuccess) return e;
+        for (const void* f : {reinterpret_cast<const void*>(&iso_lse_split<DP, false>),
+                              reinterpret_cast<const void*>(&iso_lse_split<DP, true>)}) {
+          hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+          if (e != hipSuccess) return e;
+        }
       }
-      hipLaunchKernelGGL(iso_lse_split<DP>, dim3((unsigned)nblk1), dim3(kAccThreads), lds1, stream,
-                         X, ldx, pl.N, (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
+      auto kern = pl.lj ? &iso_lse_split<DP, true> : &iso_lse_split<DP, false>;
+      hipLaunchKernelGGL(kern, dim3((unsigned)nblk1), dim3(kAccThreads), lds1, stream, X, ldx, pl.N,
+                         (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat, lj);
     }
   }
   if (!run2) return hipGetLastError();
   const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
+  if constexpr (DP >= 64) {
+    if (pl.lj) {
+      auto launch = [&](auto cb_tag) -> hipError_t {
+        constexpr int CB = decltype(cb_tag)::value;
+        constexpr size_t lds = accum_lj_lds_bytes<DP, CB>();
+        static_assert(lds <= kMaxLds, "pass-2 tiles exceed LDS");
+        if (lds > 65536) {
+          hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_lj<DP, CB>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+          if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL((iso_accum_lj<DP, CB>), grid2, dim3(kAccThreads), lds, stream, X, ldx,
+                           pl.N, (int)pl.D, lj, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab,
+                           pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
+        return hipSuccess;
+      };
+      hipError_t e = pl.cpg == 8 ? launch(std::integral_constant<int, 8>{})
+                                 : launch(std::integral_constant<int, 4>{});
+      if (e != hipSuccess) return e;
+      return hipGetLastError();
+    }
+  }
   if constexpr (accum_uses_lds(DP)) {
     auto launch = [&](auto cb_tag) -> hipError_t {
       constexpr int CB = decltype(cb_tag)::value;
@@ -914,6 +1149,11 @@ extern "C" size_t fgmm_iso_workspace_bytes(int64_t N, int64_t K, int64_t D) {
   return make_plan(N, K, D).total;
 }
 
+extern "C" size_t fgmm_iso_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
+  if (N < 0 || K < 0 || D < 1) return 0;
+  return make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE)).total;
+}
+
 extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
                                   int64_t ldmu, int64_t K, const float* log_sigma_sq,
                                   const float* log_pi, float* logZ, float* Nk, float* mu_acc,
@@ -934,7 +1174,7 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
     return FGMM_ERR_INVALID_ARG;
   if (D > 256) return FGMM_ERR_UNSUPPORTED;
   if (N > kMaxRows || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
-  const IsoPlan pl = make_plan(N, K, D);
+  const IsoPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE));
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;
   unsigned char* ws = static_cast<unsigned char*>(workspace);

@@ -28,6 +28,7 @@ FLAG_ATOMIC_REDUCE = 1 << 2
 FLAG_PHASE1 = 1 << 3
 FLAG_PHASE2 = 1 << 4
 FLAG_DENSE = 1 << 5
+FLAG_RECOMPUTE = 1 << 6
 
 
 class FlashGMMError(AssertionError, ValueError):
@@ -55,6 +56,8 @@ def _declare(lib):
 
     lib.fgmm_iso_workspace_bytes.restype = _sz
     lib.fgmm_iso_workspace_bytes.argtypes = [_i64, _i64, _i64]
+    lib.fgmm_iso_workspace_bytes_ex.restype = _sz
+    lib.fgmm_iso_workspace_bytes_ex.argtypes = [_i64, _i64, _i64, _u32]
     lib.fgmm_iso_estep_f32.restype = ctypes.c_int
     lib.fgmm_iso_estep_f32.argtypes = [
         _p, _i64, _i64, _i64,          # X, ldx, N, D
@@ -65,10 +68,12 @@ def _declare(lib):
     ]
     decls = {
         "fgmm_diag_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+        "fgmm_diag_workspace_bytes_ex": (_sz, [_i64, _i64, _i64, _u32]),
         "fgmm_diag_estep_f32": (ctypes.c_int, [
             _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p,
             _p, _p, _p, _p, _p, _sz, _u32, _p]),
         "fgmm_full_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+        "fgmm_full_workspace_bytes_ex": (_sz, [_i64, _i64, _i64, _u32]),
         "fgmm_full_estep_f32": (ctypes.c_int, [
             _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p,
             _p, _p, _p, _p, _p, _sz, _u32, _p]),

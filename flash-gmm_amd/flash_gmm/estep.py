@@ -104,10 +104,10 @@ def _check_out(name, t, shape, dev):
              f"{name} must be a contiguous float32 {tuple(shape)} tensor on {dev}")
 
 
-def _workspace(ws_fn, N, K, D, dev, workspace):
+def _workspace(ws_fn, N, K, D, flags, dev, workspace):
     # The size depends on the device's compute-unit count: query it with dev current.
     with torch.cuda.device(dev):
-        ws_bytes = int(ws_fn(N, K, D))
+        ws_bytes = int(ws_fn(N, K, D, flags))
     if workspace is None or workspace.numel() < ws_bytes:
         workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     return workspace
@@ -125,7 +125,7 @@ def _rowmajor(t: torch.Tensor) -> torch.Tensor:
 def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
                    accumulate: bool = False, atomic_reduce: bool = False,
                    workspace: torch.Tensor | None = None, phase: int = 0,
-                   dense: bool = False) -> None:
+                   dense: bool = False, recompute: bool = False) -> None:
     """Isotropic E-step writing into caller-provided outputs.
 
     ``logZ`` may be None (it is then not written).  With ``accumulate`` the
@@ -134,7 +134,9 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     log-normaliser pass, 2 only the accumulation (reusing ``workspace`` from a
     phase-1 call on the same inputs), 0 both.  ``dense`` runs the accumulation
     steps whose responsibilities are all exactly zero instead of skipping them
-    (same results; for timing).
+    (same results; for timing).  ``recompute`` makes the accumulation pass
+    recompute the log-joint instead of reading the copy that the first pass
+    stores in the workspace (smaller workspace; phase-split calls must agree).
     """
     _check_common(X, mu, log_pi)
     N, D = X.shape
@@ -146,10 +148,12 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     muk = _rowmajor(_f32(mu))
     ldmu = muk.stride(0) if K > 1 else D
     L = _lib.lib()
-    workspace = _workspace(L.fgmm_iso_workspace_bytes, N, K, D, dev, workspace)
     flags = _flags(accumulate, logZ, atomic_reduce, phase)
     if dense:
         flags |= _lib.FLAG_DENSE
+    if recompute:
+        flags |= _lib.FLAG_RECOMPUTE
+    workspace = _workspace(L.fgmm_iso_workspace_bytes_ex, N, K, D, flags, dev, workspace)
     _check_out("Nk", Nk, (K,), dev)
     _check_out("mu_acc", mu_acc, (K, D), dev)
     _check_out("sig_acc", sig_acc, (K,), dev)
@@ -187,7 +191,8 @@ def flash_gmm_estep(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tenso
 
 def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
                     accumulate: bool = False, workspace: torch.Tensor | None = None,
-                    phase: int = 0, dense: bool = False) -> None:
+                    phase: int = 0, dense: bool = False,
+                    recompute: bool = False) -> None:
     """Diagonal-covariance E-step into caller-provided outputs (sig_acc is (K, D))."""
     _check_common(X, mu, log_pi)
     N, D = X.shape
@@ -203,10 +208,12 @@ def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     ldmu = muk.stride(0) if K > 1 else D
     L = _lib.lib()
     _require(hasattr(L, "fgmm_diag_estep_f32"), "library built without the diagonal E-step")
-    workspace = _workspace(L.fgmm_diag_workspace_bytes, N, K, D, dev, workspace)
     flags = _flags(accumulate, logZ, False, phase)
     if dense:
         flags |= _lib.FLAG_DENSE
+    if recompute:
+        flags |= _lib.FLAG_RECOMPUTE
+    workspace = _workspace(L.fgmm_diag_workspace_bytes_ex, N, K, D, flags, dev, workspace)
     _check_out("Nk", Nk, (K,), dev)
     _check_out("mu_acc", mu_acc, (K, D), dev)
     _check_out("sig_acc", sig_acc, (K, D), dev)
@@ -243,7 +250,8 @@ def flash_gmm_estep_diag(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.
 
 def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
                     accumulate: bool = False, workspace: torch.Tensor | None = None,
-                    phase: int = 0, dense: bool = False) -> None:
+                    phase: int = 0, dense: bool = False,
+                    recompute: bool = False) -> None:
     """Full-covariance E-step into caller-provided outputs (sig_outer is (K, D, D))."""
     _check_common(X, mu, log_pi)
     N, D = X.shape
@@ -258,10 +266,12 @@ def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
     ldmu = muk.stride(0) if K > 1 else D
     L = _lib.lib()
     _require(hasattr(L, "fgmm_full_estep_f32"), "library built without the full-covariance E-step")
-    workspace = _workspace(L.fgmm_full_workspace_bytes, N, K, D, dev, workspace)
     flags = _flags(accumulate, logZ, False, phase)
     if dense:
         flags |= _lib.FLAG_DENSE
+    if recompute:
+        flags |= _lib.FLAG_RECOMPUTE
+    workspace = _workspace(L.fgmm_full_workspace_bytes_ex, N, K, D, flags, dev, workspace)
     _check_out("Nk", Nk, (K,), dev)
     _check_out("mu_acc", mu_acc, (K, D), dev)
     _check_out("sig_outer", sig_outer, (K, D, D), dev)

@@ -64,6 +64,12 @@ enum fgmm_flags {
      * nothing; the results are bitwise the same either way.  DENSE runs every
      * step (for timing the dense contraction). */
     FGMM_FLAG_DENSE = 1u << 5,
+    /* By default pass 1 also stores the fp32 log-joint (N/32 x K/32 tiles of
+     * 4 KiB, when that is at most 16 GiB, D > 32 and K > 96) in the workspace,
+     * and pass 2 reads it back instead of recomputing the D-contraction.
+     * RECOMPUTE keeps the workspace O(N + K*D) and recomputes.  Calls that
+     * split the phases must agree on this flag. */
+    FGMM_FLAG_RECOMPUTE = 1u << 6,
 };
 
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
@@ -85,6 +91,9 @@ const char *fgmm_strerror(int status);
 /* log_sigma_sq and log_pi are contiguous (K).                                */
 /* ------------------------------------------------------------------------ */
 size_t fgmm_iso_workspace_bytes(int64_t N, int64_t K, int64_t D);
+/* Workspace for a call made with `flags` (only FGMM_FLAG_RECOMPUTE matters);
+ * with flags = 0 it equals fgmm_iso_workspace_bytes(). */
+size_t fgmm_iso_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags);
 
 int fgmm_iso_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
                        const float *mu, int64_t ldmu, int64_t K,
@@ -104,6 +113,7 @@ int fgmm_iso_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
 /* Supports 1 <= D <= 256.                                                    */
 /* ------------------------------------------------------------------------ */
 size_t fgmm_diag_workspace_bytes(int64_t N, int64_t K, int64_t D);
+size_t fgmm_diag_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags);
 
 int fgmm_diag_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
                         const float *mu, int64_t ldmu, int64_t K,
@@ -123,6 +133,7 @@ int fgmm_diag_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
 /* Supports 1 <= D <= 128.                                                    */
 /* ------------------------------------------------------------------------ */
 size_t fgmm_full_workspace_bytes(int64_t N, int64_t K, int64_t D);
+size_t fgmm_full_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags);
 
 int fgmm_full_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
                         const float *mu, int64_t ldmu, int64_t K,

@@ -42,13 +42,33 @@ def test_strerror_names_every_status():
 
 def test_iso_workspace_bytes_grows_with_size():
     L = _lib.lib()
+    R = _lib.FLAG_RECOMPUTE
     a = L.fgmm_iso_workspace_bytes(1000, 64, 32)
-    b = L.fgmm_iso_workspace_bytes(1_000_000, 1024, 128)
+    b = L.fgmm_iso_workspace_bytes_ex(1_000_000, 1024, 128, R)
     assert 0 < a < b
-    # per-row state (16 B/row) + O(K*D) terms: stays far below the N*K responsibility matrix
+    # Recomputing: per-row state (16 B/row) + O(K*D) terms, far below the N*K log-joint.
     assert b < 1_000_000 * 1024 * 4 // 20
     assert L.fgmm_iso_workspace_bytes(-1, 4, 4) == 0
     assert L.fgmm_iso_workspace_bytes(10, 4, 0) == 0
+    assert L.fgmm_iso_workspace_bytes_ex(10, 4, 0, 0) == 0
+
+
+def test_iso_workspace_holds_stored_log_joint():
+    """Default sizing adds the fp32 log-joint tiles (N/32 x K/32 x 4 KiB) where pass 2 reads them."""
+    L = _lib.lib()
+    R = _lib.FLAG_RECOMPUTE
+    N, K, D = 1_000_000, 1024, 128
+    full = L.fgmm_iso_workspace_bytes(N, K, D)
+    assert full == L.fgmm_iso_workspace_bytes_ex(N, K, D, 0)
+    lean = L.fgmm_iso_workspace_bytes_ex(N, K, D, R)
+    tiles = -(-N // 128) * 4 * (K // 32) * 4096
+    assert tiles <= full - lean <= tiles + 256
+    # Not stored: D <= 32, K <= 96, K <= 224 above D = 128, or more than 16 GiB of tiles.
+    for n, k, d in [(N, K, 32), (N, 96, 128), (N, 224, 192), (20_000_000, 1024, 128)]:
+        assert L.fgmm_iso_workspace_bytes(n, k, d) == L.fgmm_iso_workspace_bytes_ex(n, k, d, R)
+    for fam in ("diag", "full"):
+        q, qx = getattr(L, f"fgmm_{fam}_workspace_bytes"), getattr(L, f"fgmm_{fam}_workspace_bytes_ex")
+        assert q(5000, 64, 64) == qx(5000, 64, 64, 0) > 0
 
 
 # Fake but aligned, non-null addresses: every call below must be rejected by

@@ -130,8 +130,9 @@ def _into(inp, dev, **kw):
     return out
 
 
+@pytest.mark.parametrize("recompute", [False, True])
 @pytest.mark.parametrize("case", ["clustered_d128", "clustered_d64_ragged", "plain_d32", "clustered_d256"])
-def test_zero_step_skip_is_bitwise_dense(case, gpu_device):
+def test_zero_step_skip_is_bitwise_dense(case, recompute, gpu_device):
     """Skipping all-zero responsibility steps changes no bit of any output."""
     if case == "clustered_d128":
         inp = data.iso_clustered(12000, 1024, 128, seed=1)   # mostly zero steps
@@ -141,11 +142,65 @@ def test_zero_step_skip_is_bitwise_dense(case, gpu_device):
         inp = data.iso_clustered(6000, 512, 256, seed=6)   # split-dimension pass 2
     else:
         inp = data.iso_plain(10000, 64, 32, seed=0)          # no zero steps
-    a = _into(inp, gpu_device)
-    b = _into(inp, gpu_device, dense=True)
+    a = _into(inp, gpu_device, recompute=recompute)
+    b = _into(inp, gpu_device, dense=True, recompute=recompute)
     for u, v in zip(a, b):
         assert torch.equal(u, v)
     assert_close_stats(a, oracle(inp), case)
+
+
+# Shapes on the stored log-joint path (D > 32 and K > 96; K > 224 above D = 128),
+# including row counts that leave partial 32-row tiles and slabs.
+LJ_SHAPES = [(33, 128, 128), (65, 257, 96), (1000, 130, 64), (777, 300, 61), (4097, 129, 100),
+             (2500, 260, 192), (1800, 300, 250), (9001, 512, 128)]
+
+
+@pytest.mark.parametrize("N,K,D", LJ_SHAPES)
+def test_stored_and_recomputed_log_joint(N, K, D, gpu_device):
+    """Pass 2 from the log-joint stored by pass 1, and recomputed, both against the oracle."""
+    from flash_gmm import _lib
+    L = _lib.lib()
+    # The two plans differ (stored tiles, pass-2 work split), so these shapes take the stored path.
+    assert L.fgmm_iso_workspace_bytes(N, K, D) != L.fgmm_iso_workspace_bytes_ex(N, K, D, _lib.FLAG_RECOMPUTE)
+    inp = data.iso_clustered(N, K, D, seed=N + 3 * K + D)
+    ref = oracle(inp)
+    stored = _into(inp, gpu_device)
+    recomputed = _into(inp, gpu_device, recompute=True)
+    assert torch.equal(stored[0], recomputed[0])          # pass 1 is the same kernel math
+    assert_close_stats(stored, ref, f"stored N={N} K={K} D={D}")
+    assert_close_stats(recomputed, ref, f"recomputed N={N} K={K} D={D}")
+
+
+def test_stored_log_joint_zero_weight_components(gpu_device):
+    """log_pi = -inf components on the stored path: r = 0 and finite sig_acc."""
+    inp = data.iso_clustered(3000, 200, 48, seed=15)
+    inp["log_pi"][[0, 7, 199]] = -math.inf
+    got = _into(inp, gpu_device)
+    assert_close_stats(got, oracle(inp), "stored lpi=-inf")
+    assert float(got[1][0]) == 0.0 and float(got[3][199]) == 0.0
+    assert torch.isfinite(got[3]).all()
+
+
+@pytest.mark.parametrize("recompute", [False, True])
+def test_phase_split_equals_one_call(recompute, gpu_device):
+    """PHASE1 then PHASE2 on one workspace gives the single call's outputs bitwise."""
+    inp = data.iso_clustered(5000, 256, 96, seed=16)
+    dev = gpu_device
+    ref = _into(inp, dev, recompute=recompute)
+    N, D = inp["X"].shape
+    K = inp["mu"].shape[0]
+    from flash_gmm import _lib
+    L = _lib.lib()
+    flags = _lib.FLAG_RECOMPUTE if recompute else 0
+    ws = torch.empty(L.fgmm_iso_workspace_bytes_ex(N, K, D, flags), dtype=torch.uint8, device=dev)
+    out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, device=dev)]
+    args = [inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
+    iso_estep_into(*args, *out, workspace=ws, phase=1, recompute=recompute)
+    iso_estep_into(*args, None, *out[1:], workspace=ws, phase=2, recompute=recompute)
+    torch.cuda.synchronize()
+    for u, v in zip(out, ref):
+        assert torch.equal(u, v)
 
 
 def test_atomic_reduce_matches(gpu_device):
