@@ -56,10 +56,10 @@ constexpr int kAccWaves = 8;   // pass-2 LDS variant: waves per workgroup
 constexpr int kAccThreads = 64 * kAccWaves;
 
 
-// Pass 2 runs one workgroup of eight waves per CU: the LDS-resident variant for
-// D <= 128 (mu of 4 component blocks and 64-row X tiles in LDS), or for D > 128
-// the split variant (4 component blocks x 2 halves of the dimensions, each wave
-// holding its half of mu in registers), for which D is padded to a multiple of 64.
+// The recomputing pass 2 runs the LDS-resident variant for D <= 128 (mu of 4
+// component blocks and 64-row X tiles in LDS), or for D > 128 the split variant
+// (two waves per component block, each holding half of mu in registers), for
+// which D is padded to a multiple of 64.
 __host__ __device__ constexpr bool accum_uses_lds(int DP) { return DP <= 128; }
 
 // LDS of the LDS-resident pass 2 with CB component blocks per workgroup (and
@@ -72,8 +72,13 @@ __host__ __device__ constexpr size_t accum_lds_bytes_for(int DP, int CB) {
 }
 // Component blocks per pass-2 workgroup: 4, or 2 / 1 when there are that few
 // blocks (K <= 64 / K <= 32) so that no wave idles, where the taller X tiles fit.
+// Recomputing pass 2 above D = 128: two waves per component block (one half of
+// the dimensions each), two blocks per 4-wave workgroup, one wave per SIMD.
+__host__ __device__ constexpr int split_parts(int DP) { return DP > 128 ? 2 : 1; }
+__host__ __device__ constexpr int split_blocks(int DP) { return 2; }
+
 __host__ inline int accum_blocks_per_group(int DP, int KB) {
-  if (!accum_uses_lds(DP)) return kWaves;
+  if (!accum_uses_lds(DP)) return split_blocks(DP);
   if (KB <= 1 && accum_lds_bytes_for(DP, 1) <= kMaxLds) return 1;
   if (KB <= 2 && accum_lds_bytes_for(DP, 2) <= kMaxLds) return 2;
   return kWaves;
@@ -94,16 +99,16 @@ struct IsoPlan {
   int npart;    // nslab * rgroups
   int64_t rows_per_slab;
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
+  int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
   size_t off_musw, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_nk, off_part_sig, off_lj,
       total;
 };
 
 // Pass 2 reads the stored log-joint when recomputation is not requested, D is at
 // least 33 (below, the recomputed contraction costs less than the extra traffic),
-// there are at least 4 component blocks (8 above D = 128, where the pass-2 tile
-// of 4 blocks would not fit in registers), and the tiles fit under kMaxLjBytes.
+// there are at least 4 component blocks, and the tiles fit under kMaxLjBytes.
 __host__ inline bool use_stored_lj(int64_t N, int DP, int KB, bool allow) {
-  return allow && DP >= 64 && KB >= (DP <= 128 ? 4 : 8) &&
+  return allow && DP >= 64 && KB >= 4 &&
          (size_t)round_up(cdiv(N, 32), 4) * (size_t)KB * kLjTile * sizeof(float) <= kMaxLjBytes;
 }
 
@@ -115,8 +120,12 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true) {
   p.KP = p.KB * 32;
   p.lj = use_stored_lj(N, p.DP, p.KB, allow_lj);
   if (p.lj) {
+    // 8 component blocks per workgroup, or 4 for K <= 224; then above D = 128 two
+    // waves share a block (one half of the columns each): one wave's accumulators
+    // for 4 row groups would not fit.
     p.cpg = p.KB >= 8 ? 8 : 4;
-    p.rgroups = kAccWaves / p.cpg;
+    p.lj_nh = (p.DP > 128 && p.cpg == 4) ? 2 : 1;
+    p.rgroups = kAccWaves / (p.cpg * p.lj_nh);
   } else {
     p.cpg = accum_blocks_per_group(p.DP, p.KB);
     p.rgroups = accum_uses_lds(p.DP) ? kAccWaves / p.cpg : 1;
@@ -607,47 +616,55 @@ void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2 for D > 128: eight waves = 4 component blocks x 2 halves of the
-// dimensions.  Each wave keeps mu of its block and half in registers and forms
-// the fp32 partial cross term of the tile over its half; the halves meet in LDS
-// and are added in a fixed order, so both waves of a block form the same r.
-// Each wave then accumulates r^T X for the columns of its half.
+// Pass 2 (recomputing) for D > 128: the dimensions are split into NQ = 2 halves,
+// one wave per (component block, half), SB = 2 component blocks per workgroup.
+// Each wave keeps mu of its block and half in registers and forms the accurate
+// fp64 partial contraction of the tile over its half; the partials meet in LDS
+// and are added in a fixed order, so both waves of a block form the same r.  Each
+// wave then accumulates r^T X for the columns of its half.  The fp64 contraction,
+// half of mu and the accumulators need more than the 256 registers of two waves
+// per SIMD, so this kernel runs one wave per SIMD.
 // ---------------------------------------------------------------------------
 template <int DP>
 constexpr size_t accum_split_lds_bytes() {
-  return (size_t)2 * 32 * (DP + 4) * sizeof(float)       // X, 2 buffers of 32 rows
-         + (size_t)2 * 32 * sizeof(RowStat)               // row state, 2 buffers
-         + (size_t)kAccWaves * 16 * 64 * sizeof(float);   // partial cross terms
+  return (size_t)2 * 32 * (DP + 4) * sizeof(float)        // X, 2 buffers of 32 rows
+         + (size_t)2 * 32 * sizeof(double2)                // row state, 2 buffers
+         + (size_t)split_parts(DP) * split_blocks(DP) * 16 * 64 * sizeof(double);  // partials
 }
 
 template <int DP>
-__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * split_parts(DP) * split_blocks(DP),
+                                                      64 * split_parts(DP) * split_blocks(DP)),
+                          amdgpu_waves_per_eu(1, 1)))
 void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                      const f32x4* __restrict__ mu_sw, const double4* __restrict__ kc_lin, int KB, int KP,
                      const double2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
                      float* __restrict__ part_mu, float* __restrict__ part_nk,
                      float* __restrict__ part_sig, int dense) {
-  constexpr int HD = DP / 2;       // dimensions per wave
-  constexpr int NM = DP / 8;       // operand chunks of a full row
-  constexpr int NMH = HD / 8;      // chunks per half
-  constexpr int NJH = HD / 32;     // accumulator tiles per wave
+  constexpr int NQ = split_parts(DP);
+  constexpr int SB = split_blocks(DP);
+  constexpr int NT = 64 * NQ * SB;   // threads
+  constexpr int NM = DP / 8;         // operand chunks of a full row
+  constexpr int PW = DP / NQ;        // dimensions per part
+  constexpr int NMQ = PW / 8;        // chunks per part
+  constexpr int NJQ = PW / 32;       // accumulator tiles per part
   constexpr int RS = DP + 4;
   constexpr int V4 = DP / 4;
-  constexpr int LPT = (32 * V4) / kAccThreads;
-  static_assert(HD % 32 == 0 && NMH % 4 == 0 && (32 * V4) % kAccThreads == 0, "split shape");
+  constexpr int LPT = (32 * V4) / NT;
+  static_assert((32 * V4) % NT == 0 && PW % 32 == 0 && NMQ % 2 == 0, "split shape");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   float* xs = reinterpret_cast<float*>(lds_raw);                                         // [2][32*RS]
-  RowStat* rs = reinterpret_cast<RowStat*>(lds_raw + 2 * 32 * RS * sizeof(float));       // [2][32]
-  float* ex = reinterpret_cast<float*>(lds_raw + 2 * 32 * RS * sizeof(float) +
-                                       2 * 32 * sizeof(RowStat));                         // [8][16][64]
+  double2* rs = reinterpret_cast<double2*>(lds_raw + 2 * 32 * RS * sizeof(float));      // [2][32]
+  double* ex = reinterpret_cast<double*>(lds_raw + 2 * 32 * RS * sizeof(float) +
+                                         2 * 32 * sizeof(double2));                      // [NQ*SB][16][64]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
-  const int cb = wave & 3, h = wave >> 2;
+  const int cb = wave % SB, qp = wave / SB;   // component block, dimension part
   const int slab = blockIdx.x % nslab;
   const int cg = blockIdx.x / nslab;
-  const int kb = cg * kWaves + cb;
+  const int kb = cg * SB + cb;
   const bool active = kb < KB;
 
   const int64_t r_begin = (int64_t)slab * rows_per_slab;
@@ -655,20 +672,19 @@ void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   if (r_end > N) r_end = N;
   const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
 
-  f32x4 mub[NMH];
+  f32x4 mub[NMQ];
 #pragma unroll
-  for (int m = 0; m < NMH; ++m)
-    mub[m] = active ? mu_sw[((int64_t)kb * NM + h * NMH + m) * 64 + lane] : zero4();
-  double Ck = -INFINITY;
-  float bkf = 0.0f, musqf = 0.0f;
+  for (int m = 0; m < NMQ; ++m)
+    mub[m] = active ? mu_sw[((int64_t)kb * NM + qp * NMQ + m) * 64 + lane] : zero4();
+  double Ck = -INFINITY, bk = 0.0, musq = 0.0;
   if (active) {
     const double4 kc = kc_lin[(int64_t)kb * 32 + c];
-    Ck = kc.x; bkf = (float)kc.y; musqf = (float)kc.z;
+    Ck = kc.x; bk = kc.y; musq = kc.z;
   }
 
-  f32x16 acc[NJH];
+  f32x16 acc[NJQ];
 #pragma unroll
-  for (int j = 0; j < NJH; ++j) acc[j] = zero16();
+  for (int j = 0; j < NJQ; ++j) acc[j] = zero16();
   float nk = 0.0f, sig = 0.0f;
 
   f32x4 stage[LPT];
@@ -680,13 +696,13 @@ void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       const float* src = X + row0 * ldx;
 #pragma unroll
       for (int q = 0; q < LPT; ++q) {
-        const int idx = q * kAccThreads + tid;
+        const int idx = q * NT + tid;
         stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
       }
     } else {
 #pragma unroll
       for (int q = 0; q < LPT; ++q) {
-        const int idx = q * kAccThreads + tid;
+        const int idx = q * NT + tid;
         const int64_t row = row0 + idx / V4;
         stage[q] = load_row4(X, ldx, row, (idx % V4) * 4, D, row < r_end);
       }
@@ -700,10 +716,10 @@ void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     float* dst = xs + buf * 32 * RS;
 #pragma unroll
     for (int q = 0; q < LPT; ++q) {
-      const int idx = q * kAccThreads + tid;
+      const int idx = q * NT + tid;
       *reinterpret_cast<f32x4*>(dst + (idx / V4) * RS + (idx % V4) * 4) = stage[q];
     }
-    if (tid < 32) rs[buf * 32 + tid] = RowStat{rstage.y, (float)rstage.x, 0.0f};
+    if (tid < 32) rs[buf * 32 + tid] = rstage;
   };
 
   if (ntiles > 0) {
@@ -712,18 +728,19 @@ void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   }
   __syncthreads();
 
-  float* my_ex = ex + wave * 16 * 64 + lane;
-  const float* ex0 = ex + cb * 16 * 64 + lane;          // half 0 of this block
-  const float* ex1 = ex + (kWaves + cb) * 16 * 64 + lane;  // half 1
+  double* my_ex = ex + wave * 16 * 64 + lane;
+  const double* ex_blk = ex + cb * 16 * 64 + lane;   // part p of this block at + p * SB * 1024
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     const bool more = t + 1 < ntiles;
     const float* xt = xs + buf * 32 * RS;
-    const RowStat* rt = rs + buf * 32;
+    const double2* rt = rs + buf * 32;
     if (active) {
-      float xm[16];
-      const float* xrow = xt + c * RS + h * HD + 4 * g;
-      cross_tile_fast<NMH>(
+      // Accurate partial contraction (fp64 chunk sums), as in pass 1: at these
+      // widths fp32 chains lose too much in ||x - mu||^2.
+      double xm[16];
+      const float* xrow = xt + c * RS + qp * PW + 4 * g;
+      cross_tile<NMQ>(
           xm, [&](int m) { return *reinterpret_cast<const f32x4*>(xrow + 8 * m); },
           [&](int m) { return mub[m]; });
 #pragma unroll
@@ -733,27 +750,32 @@ void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     if (more) fetch(t + 1);
     if (active) {
       float r[16];
-      const RowStat* rbase = rt + 4 * g;
+      const double2* rbase = rt + 4 * g;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int ro = 8 * (i >> 2) + (i & 3);
-        const float xm = ex0[i * 64] + ex1[i * 64];
-        const uint4 w = *reinterpret_cast<const uint4*>(rbase + ro);
-        const double q = __hiloint2double((int)w.y, (int)w.x);
-        const float u = fmaf(-2.0f, xm, __uint_as_float(w.z));
-        const float dq = (float)(Ck - q);
-        const float rv = fast_exp2(fmaf(-bkf, u, dq));
-        nk += rv;
-        sig = fmaf(rv, u + musqf, sig);
+        double xm = ex_blk[i * 64];                  // parts added in a fixed order
+#pragma unroll
+        for (int p = 1; p < NQ; ++p) xm += ex_blk[(p * SB * 16 + i) * 64];
+        const double2 w = rbase[ro];                 // (||x||^2, logZ2)
+        const double u = fma(-2.0, xm, w.x);        // ||x||^2 - 2 x.mu
+        const float rv = fast_exp2((float)(fma(-bk, u, Ck) - w.y));
+        if (qp == 0) {
+          nk += rv;
+          sig = fmaf(rv, (float)(u + musq), sig);
+        }
         r[i] = rv;
+        // Groups of 4 rows: keeps the scheduler from hoisting all 16 * NQ LDS
+        // reads (2 registers each) ahead of their use.
+        if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
-      const float* xbase = xt + 4 * g * RS + h * HD + c;
+      const float* xbase = xt + 4 * g * RS + qp * PW + c;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int ro = 8 * (i >> 2) + (i & 3);
         if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
 #pragma unroll
-          for (int j = 0; j < NJH; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
+          for (int j = 0; j < NJQ; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
         }
       }
     }
@@ -764,12 +786,12 @@ void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   if (active) {
     const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
 #pragma unroll
-    for (int j = 0; j < NJH; ++j) {
+    for (int j = 0; j < NJQ; ++j) {
 #pragma unroll
       for (int i = 0; i < 16; ++i)
-        part_mu[(kbase + acc_row(i, g)) * DP + h * HD + 32 * j + c] = acc[j][i];
+        part_mu[(kbase + acc_row(i, g)) * DP + qp * PW + 32 * j + c] = acc[j][i];
     }
-    if (h == 0) {
+    if (qp == 0) {
       nk += __shfl_xor(nk, 32);
       sig += __shfl_xor(sig, 32);
       if (g == 0) {
@@ -782,34 +804,35 @@ void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
 // ---------------------------------------------------------------------------
 // Pass 2 from the stored log-joint: grid over (row slab x group of CB component
-// blocks); eight waves = CB component blocks x 8 / CB row groups of 32 rows.
-// Each wave reads the log-joint tile of its block and rows (4 KiB, prefetched one
-// tile ahead), forms r = 2^(ll2 - logZ2) and accumulates r^T X on the matrix
-// cores from the X tile that the workgroup's blocks share in LDS.  ||x - mu_k||^2
-// for sig_acc comes back from the log-joint as (C0_k - ll2) / b_k, where
-// C0_k = C_k + b_k ||mu_k||^2.  logZ2 sits in LDS as a hi + lo pair of floats,
-// so ll2 - logZ2 keeps the accuracy of the fp32 log-joint.
+// blocks); eight waves = CB component blocks x NH column parts x 8 / (CB NH) row
+// groups of 32 rows (NH = 2 above D = 128, where one wave's accumulators for all
+// of D would not fit in registers).  Each wave reads the log-joint tile of its
+// block and rows (4 KiB), forms r = 2^(ll2 - logZ2) and accumulates r^T X for its
+// columns on the matrix cores from the X tile that the workgroup's blocks share
+// in LDS.  ||x - mu_k||^2 for sig_acc comes back from the log-joint as
+// (C0_k - ll2) / b_k, where C0_k = C_k + b_k ||mu_k||^2.  logZ2 sits in LDS as a
+// hi + lo pair of floats, so ll2 - logZ2 keeps the accuracy of the fp32 log-joint.
 // ---------------------------------------------------------------------------
-template <int DP, int CB>
+template <int DP, int CB, int NH>
 constexpr size_t accum_lj_lds_bytes() {
-  return (size_t)2 * 32 * (kAccWaves / CB) * ((DP + 4) * sizeof(float) + sizeof(float2));
+  return (size_t)2 * 32 * (kAccWaves / (CB * NH)) * ((DP + 4) * sizeof(float) + sizeof(float2));
 }
 
-template <int DP, int CB>
+template <int DP, int CB, int NH>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                   const float* __restrict__ lj, const double4* __restrict__ kc_lin, int KB, int KP,
                   const double2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
                   float* __restrict__ part_mu, float* __restrict__ part_nk, float* __restrict__ part_sig,
                   int dense) {
-  constexpr int NJ = DP / 32;
+  constexpr int NJ = DP / 32 / NH;               // 32-column accumulator tiles per wave
   constexpr int RS = DP + 4;
   constexpr int V4 = DP / 4;
-  constexpr int RG = kAccWaves / CB;             // row groups (32 rows each)
+  constexpr int RG = kAccWaves / (CB * NH);      // row groups (32 rows each)
   constexpr int TR = 32 * RG;                    // rows per super-tile
   constexpr int NV = TR * V4;                    // float4 per super-tile
   constexpr int LPT = (NV + kAccThreads - 1) / kAccThreads;
-  static_assert(kAccWaves % CB == 0, "even split");
+  static_assert(kAccWaves % (CB * NH) == 0 && (DP / 32) % NH == 0, "even split");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   float* xs = reinterpret_cast<float*>(lds_raw);                                  // [2][TR*RS]
@@ -817,11 +840,12 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
-  const int cbw = wave % CB, rg = wave / CB;
+  const int cbw = wave % CB, h = (wave / CB) % NH, rg = wave / (CB * NH);
   const int slab = blockIdx.x % nslab;
   const int cg = blockIdx.x / nslab;
   const int kb = cg * CB + cbw;
   const bool active = kb < KB;
+  const int col0 = h * (DP / NH);                 // first column of this wave's part
 
   const int64_t r_begin = (int64_t)slab * rows_per_slab;
   int64_t r_end = r_begin + rows_per_slab;
@@ -845,10 +869,14 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   for (int j = 0; j < NJ; ++j) acc[j] = zero16();
   float nk = 0.0f, sig = 0.0f;
 
-  f32x4 stage[LPT];
-  double rq = INFINITY;
+  // X tiles and row logZ2 go global -> registers -> LDS.  Two register stages:
+  // tile t + 2 is loaded while tile t is processed and lands in LDS at the end of
+  // iteration t + 1, so every load has about two iterations to arrive (the LDS-only
+  // barrier leaves them in flight).
+  f32x4 stage[LPT], stage2[LPT];
+  double rq = INFINITY, rq2 = INFINITY;
   const bool full_d = (D == DP);
-  auto fetch = [&](int t) {
+  auto fetch = [&](int t, f32x4 (&stage)[LPT], double& rq) {
     const int64_t row0 = r_begin + (int64_t)t * TR;
     if (full_d && row0 + TR <= r_end) {
       const float* src = X + row0 * ldx;
@@ -871,7 +899,7 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       rq = (row < r_end) ? rowstat[row].y : INFINITY;
     }
   };
-  auto commit = [&](int buf) {
+  auto commit = [&](int buf, const f32x4 (&stage)[LPT], double rq) {
     float* dst = xs + buf * TR * RS;
 #pragma unroll
     for (int q = 0; q < LPT; ++q) {
@@ -896,24 +924,37 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     }
   };
 
-  f32x4 ljc[4], ljn[4];
+  // Log-joint tiles are loaded two super-tiles ahead as well, or one ahead with
+  // 8 accumulator tiles per wave (registers).
+  constexpr bool kLj2 = NJ <= 4;
+  f32x4 ljc[4], ljn[4], ljm[4];
   if (ntiles > 0) {
-    fetch(0);
+    fetch(0, stage, rq);
     lj_fetch(0, ljc);
-    commit(0);
+    commit(0, stage, rq);
+  }
+  if (ntiles > 1) {
+    fetch(1, stage, rq);
+    if (kLj2) lj_fetch(1, ljn);
   }
   lds_barrier();
 
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     const bool more = t + 1 < ntiles;
-    if (more) {
-      fetch(t + 1);
-      lj_fetch(t + 1, ljn);
+    if (t + 2 < ntiles) {
+      fetch(t + 2, stage2, rq2);
+      if (kLj2) lj_fetch(t + 2, ljm);
     }
+    if (!kLj2 && more) lj_fetch(t + 1, ljn);
     const float* xt = xs + buf * TR * RS + rg * 32 * RS;
     const float2* rt = rz + buf * TR + rg * 32 + 4 * g;
     if (active) {
+      const float* xbase = xt + 4 * g * RS + col0 + c;
+      // r of the 16 rows, then the matrix-core steps.  Forming each r just before
+      // its step saves 16 registers (needed with 8 accumulator tiles) but puts the
+      // exp -> ballot latency in front of every step.
+      constexpr bool kInterleave = NJ > 4;
       float r[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -921,24 +962,37 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
         const float2 z = rt[ro];
         const float l = ljc[i >> 2][i & 3];
         const float rv = fast_exp2((l - z.x) - z.y);
-        nk += rv;
-        sig = fmaf(rv, fminf((c0 - l) * ibk, FLT_MAX), sig);
+        if (NH == 1 || h == 0) {
+          nk += rv;
+          sig = fmaf(rv, fminf((c0 - l) * ibk, FLT_MAX), sig);
+        }
         r[i] = rv;
+        if (kInterleave && (NJ < 2 || dense || __builtin_amdgcn_ballot_w64(rv != 0.0f) != 0)) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) acc[j] = mfma32(rv, xbase[ro * RS + 32 * j], acc[j]);
+        }
       }
-      const float* xbase = xt + 4 * g * RS + c;
+      if constexpr (!kInterleave) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ro = 8 * (i >> 2) + (i & 3);
-        if (NJ < 2 || dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
+        for (int i = 0; i < 16; ++i) {
+          const int ro = 8 * (i >> 2) + (i & 3);
+          if (NJ < 2 || dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
+            for (int j = 0; j < NJ; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
+          }
         }
       }
     }
-    if (more) commit(buf ^ 1);
+    if (more) commit(buf ^ 1, stage, rq);
     lds_barrier();
 #pragma unroll
-    for (int q = 0; q < 4; ++q) ljc[q] = ljn[q];
+    for (int q = 0; q < LPT; ++q) stage[q] = stage2[q];
+    rq = rq2;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ljc[q] = ljn[q];
+      if (kLj2) ljn[q] = ljm[q];
+    }
   }
 
   if (active) {
@@ -949,9 +1003,9 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     for (int j = 0; j < NJ; ++j) {
 #pragma unroll
       for (int i = 0; i < 16; ++i)
-        part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[j][i];
+        part_mu[(kbase + acc_row(i, g)) * DP + col0 + 32 * j + c] = acc[j][i];
     }
-    if (g == 0) {
+    if (g == 0 && h == 0) {
       part_nk[kbase + c] = nk;
       part_sig[kbase + c] = sig;
     }
@@ -1083,22 +1137,31 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
   if constexpr (DP >= 64) {
     if (pl.lj) {
-      auto launch = [&](auto cb_tag) -> hipError_t {
+      auto launch = [&](auto cb_tag, auto nh_tag) -> hipError_t {
         constexpr int CB = decltype(cb_tag)::value;
-        constexpr size_t lds = accum_lj_lds_bytes<DP, CB>();
+        constexpr int NH = decltype(nh_tag)::value;
+        constexpr size_t lds = accum_lj_lds_bytes<DP, CB, NH>();
         static_assert(lds <= kMaxLds, "pass-2 tiles exceed LDS");
         if (lds > 65536) {
-          hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_lj<DP, CB>),
+          hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_lj<DP, CB, NH>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
           if (e != hipSuccess) return e;
         }
-        hipLaunchKernelGGL((iso_accum_lj<DP, CB>), grid2, dim3(kAccThreads), lds, stream, X, ldx,
+        hipLaunchKernelGGL((iso_accum_lj<DP, CB, NH>), grid2, dim3(kAccThreads), lds, stream, X, ldx,
                            pl.N, (int)pl.D, lj, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab,
                            pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
         return hipSuccess;
       };
-      hipError_t e = pl.cpg == 8 ? launch(std::integral_constant<int, 8>{})
-                                 : launch(std::integral_constant<int, 4>{});
+      using I1 = std::integral_constant<int, 1>;
+      using I4 = std::integral_constant<int, 4>;
+      hipError_t e;
+      if (pl.cpg == 8) {
+        e = launch(std::integral_constant<int, 8>{}, I1{});
+      } else if constexpr (DP > 128) {
+        e = launch(I4{}, std::integral_constant<int, 2>{});
+      } else {
+        e = launch(I4{}, I1{});
+      }
       if (e != hipSuccess) return e;
       return hipGetLastError();
     }
@@ -1132,7 +1195,8 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(iso_accum_split<DP>, grid2, dim3(kAccThreads), lds, stream, X, ldx, pl.N,
+    hipLaunchKernelGGL(iso_accum_split<DP>, grid2, dim3(64 * split_parts(DP) * split_blocks(DP)), lds,
+                       stream, X, ldx, pl.N,
                        (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
                        pmu, pnk, psig, dense ? 1 : 0);
   }

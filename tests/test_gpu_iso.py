@@ -149,10 +149,10 @@ def test_zero_step_skip_is_bitwise_dense(case, recompute, gpu_device):
     assert_close_stats(a, oracle(inp), case)
 
 
-# Shapes on the stored log-joint path (D > 32 and K > 96; K > 224 above D = 128),
-# including row counts that leave partial 32-row tiles and slabs.
+# Shapes on the stored log-joint path (D > 32 and K > 96), including row counts
+# that leave partial 32-row tiles and slabs, and both column splits of pass 2.
 LJ_SHAPES = [(33, 128, 128), (65, 257, 96), (1000, 130, 64), (777, 300, 61), (4097, 129, 100),
-             (2500, 260, 192), (1800, 300, 250), (9001, 512, 128)]
+             (2500, 260, 192), (1800, 300, 250), (9001, 512, 128), (3000, 150, 160), (700, 200, 256)]
 
 
 @pytest.mark.parametrize("N,K,D", LJ_SHAPES)
