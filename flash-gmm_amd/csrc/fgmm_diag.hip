@@ -69,19 +69,41 @@ struct DiagPlan {
   int cpg;      // component blocks per pass-2 workgroup
   int ncg, nslab, rgroups, npart;
   int64_t rows_per_slab;
-  size_t off_musw, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_sq, off_part_nk, total;
+  bool lj;      // pass 1 stores the log-joint; pass 2 reads it
+  int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
+  size_t off_musw, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_sq, off_part_nk, off_lj,
+      total;
 };
 
-DiagPlan make_plan(int64_t N, int64_t K, int64_t D) {
+// Pass 2 reads the stored log-joint when recomputation is not requested, there are
+// at least 4 component blocks, and the tiles (one per pass-1 wave) fit under
+// kMaxLjBytes.  With 2D features per row the recomputed contraction costs more
+// than the log-joint traffic at every D.
+__host__ inline bool use_stored_lj(int64_t N, int KB, bool allow) {
+  return allow && KB >= 4 &&
+         (size_t)round_up(cdiv(N, 32), 4) * (size_t)KB * kLjTile * sizeof(float) <= kMaxLjBytes;
+}
+
+DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true) {
   DiagPlan p{};
   p.N = N; p.K = K; p.D = D;
   p.DP = diag_padded_dim(D);
   p.FP = 2 * p.DP;
   p.KB = (int)cdiv(K, 32);
   p.KP = p.KB * 32;
-  p.cpg = diag_accum_split_d(p.DP) ? split_blocks(p.DP) : accum_blocks_per_group(p.DP, p.KB);
+  p.lj = use_stored_lj(N, p.KB, allow_lj);
+  if (p.lj) {
+    // 8 component blocks per workgroup, or 4 for K <= 224.  Two waves share a
+    // block (one half of the columns each) where one wave's x and x^2
+    // accumulators would not fit: above D = 128, or at D = 128 with 4 blocks.
+    p.cpg = (p.KB >= 8 && p.DP <= 128) ? 8 : 4;
+    p.lj_nh = (p.DP > 128 || (p.DP == 128 && p.cpg == 4)) ? 2 : 1;
+    p.rgroups = kAccWaves / (p.cpg * p.lj_nh);
+  } else {
+    p.cpg = diag_accum_split_d(p.DP) ? split_blocks(p.DP) : accum_blocks_per_group(p.DP, p.KB);
+    p.rgroups = diag_accum_uses_lds(p.DP) ? kAccWaves / p.cpg : 1;
+  }
   p.ncg = (int)cdiv(p.KB, p.cpg);
-  p.rgroups = diag_accum_uses_lds(p.DP) ? kAccWaves / p.cpg : 1;
   const int64_t tile_rows = 32 * p.rgroups;
   if (N > 0 && p.ncg > 0) {
     int64_t want = (int64_t)current_device_cus() / p.ncg;
@@ -104,6 +126,8 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D) {
   p.off_part_mu = off; off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
   p.off_part_sq = off; off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
   p.off_part_nk = off; off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
+  p.off_lj = off;   // one tile per pass-1 wave: the grid's 32-row tiles, rounded up to 4
+  if (p.lj) off = align256(off + (size_t)round_up(cdiv(N, 32), 4) * p.KB * kLjTile * sizeof(float));
   p.total = off;
   return p;
 }
@@ -175,12 +199,12 @@ constexpr size_t lse_lds_bytes() {
   return (size_t)2 * (2 * DP) * 32 * sizeof(float) + (size_t)2 * 32 * sizeof(double);
 }
 
-template <int DP>
+template <int DP, bool LJ>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(DP <= 96 ? 2 : 1, DP <= 96 ? 2 : 1)))
 void diag_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
               const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_blk, int KB,
-              float* __restrict__ logZ, double* __restrict__ rowstat) {
+              float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj) {
   constexpr int NMX = DP / 8;
   constexpr int NM = 2 * NMX;
   constexpr int BLK = NM * 64;
@@ -193,7 +217,8 @@ void diag_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
-  const int64_t row = ((int64_t)blockIdx.x * kWaves + wave) * 32 + c;
+  const int64_t tile = (int64_t)blockIdx.x * kWaves + wave;   // 32-row tile
+  const int64_t row = tile * 32 + c;
   const bool valid = row < N;
 
   f32x4 st[LPT];
@@ -234,6 +259,11 @@ void diag_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       ll[i] = kp[i] + xm[i];
       bm = fmax(bm, ll[i]);
     }
+    // Keep the max here: sunk past the conditional commit below, its operands
+    // would cross a block boundary and each cost a canonicalising max.
+    asm volatile("" : "+v"(bm));
+    // Unconditional: tiles are allocated for the whole grid.
+    if constexpr (LJ) lj_store(lj + (tile * KB + kb) * kLjTile, lane, ll);
     const double mn = fmax(mx, bm);
     const double ms = (mn == -INFINITY) ? 0.0 : mn;
     float acc = sm * fast_exp2((float)(mx - ms));
@@ -242,7 +272,7 @@ void diag_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     sm = acc;
     mx = mn;
     if (more) commit(buf ^ 1);
-    __syncthreads();
+    lds_barrier();
   }
   const double mo = __shfl_xor(mx, 32);
   const float so = __shfl_xor(sm, 32);
@@ -280,11 +310,11 @@ constexpr size_t lse_split_lds_bytes() {
          + (size_t)(MB + 1) * 32 * sizeof(double);                // constants
 }
 
-template <int DP>
+template <int DP, bool LJ>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void diag_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                     const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_blk, int KB,
-                    float* __restrict__ logZ, double* __restrict__ rowstat) {
+                    float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj) {
   constexpr int NMX = DP / 8;
   constexpr int NM = 2 * NMX;
   constexpr int NMH = NMX / 2;            // x chunks per half
@@ -304,7 +334,8 @@ void diag_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
   const int rg = wave & 3, h = wave >> 2;
-  const int64_t row = ((int64_t)blockIdx.x * kWaves + rg) * 32 + c;
+  const int64_t tile = (int64_t)blockIdx.x * kWaves + rg;   // 32-row tile
+  const int64_t row = tile * 32 + c;
   const bool valid = row < N;
 
   f32x4 st[LPT];
@@ -326,7 +357,7 @@ void diag_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 #pragma unroll
   for (int m = 0; m < NMH; ++m) xb[m] = load_row4(X, ldx, row, h * HD + 8 * m + 4 * g, D, valid);
   commit(0);
-  __syncthreads();
+  lds_barrier();
 
   double mx = -INFINITY;
   float sm = 0.0f;
@@ -345,7 +376,7 @@ void diag_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       for (int i = 0; i < 16; ++i) exb[i * 64] = xm[i];
     }
     if (MB == 2 && more) commit(kb + 1);
-    __syncthreads();
+    lds_barrier();
     if (MB == 1 && more) commit(kb + 1);
     if (h == 0) {
       const double* kp = kc_l + (kb % NKC) * 32 + g * 16;
@@ -356,6 +387,7 @@ void diag_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
         ll[i] = kp[i] + (xm[i] + exb[i * 64]);
         bm = fmax(bm, ll[i]);
       }
+      if constexpr (LJ) lj_store(lj + (tile * KB + kb) * kLjTile, lane, ll);
       const double mn = fmax(mx, bm);
       const double ms = (mn == -INFINITY) ? 0.0 : mn;
       float acc = sm * fast_exp2((float)(mx - ms));
@@ -364,7 +396,7 @@ void diag_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       sm = acc;
       mx = mn;
     }
-    if (MB == 1) __syncthreads();
+    if (MB == 1) lds_barrier();
   }
 
   if (h == 0) {
@@ -549,6 +581,207 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       }
     }
     if (g == 0) part_nk[kbase + c] = nk;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2 from the stored log-joint: grid over (row slab x group of CB component
+// blocks); eight waves = CB component blocks x NH column parts x 8 / (CB NH) row
+// groups of 32 rows (NH = 2 above D = 128, or at D = 128 with 4 blocks: one wave's
+// accumulators for x and x^2 over all of D would not fit in registers).  Each wave
+// reads the log-joint tile of its block and rows (4 KiB), forms
+// r = 2^(ll2 - logZ2) and accumulates r^T [x | x^2] for its columns on the matrix
+// cores from the X tile that the workgroup's blocks share in LDS.  logZ2 sits in
+// LDS as a hi + lo pair of floats, so ll2 - logZ2 keeps the accuracy of the fp32
+// log-joint.
+// ---------------------------------------------------------------------------
+template <int DP, int CB, int NH>
+constexpr size_t accum_lj_lds_bytes() {
+  return (size_t)2 * 32 * (kAccWaves / (CB * NH)) * ((DP + 4) * sizeof(float) + sizeof(float2));
+}
+
+template <int DP, int CB, int NH>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
+void diag_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                   const float* __restrict__ lj, int KB, int KP, const double* __restrict__ rowstat,
+                   int nslab, int64_t rows_per_slab, float* __restrict__ part_mu,
+                   float* __restrict__ part_sq, float* __restrict__ part_nk, int dense) {
+  constexpr int NJ = DP / 32 / NH;               // 32-column tiles per wave (each for x and x^2)
+  constexpr int RS = DP + 4;
+  constexpr int V4 = DP / 4;
+  constexpr int RG = kAccWaves / (CB * NH);      // row groups (32 rows each)
+  constexpr int TR = 32 * RG;                    // rows per super-tile
+  constexpr int NV = TR * V4;                    // float4 per super-tile
+  constexpr int LPT = (NV + kAccThreads - 1) / kAccThreads;
+  static_assert(kAccWaves % (CB * NH) == 0 && (DP / 32) % NH == 0, "even split");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  float* xs = reinterpret_cast<float*>(lds_raw);                                  // [2][TR*RS]
+  float2* rz = reinterpret_cast<float2*>(lds_raw + 2 * TR * RS * sizeof(float));  // [2][TR]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int cbw = wave % CB, h = (wave / CB) % NH, rg = wave / (CB * NH);
+  const int slab = blockIdx.x % nslab;
+  const int cg = blockIdx.x / nslab;
+  const int kb = cg * CB + cbw;
+  const bool active = kb < KB;
+  const int col0 = h * (DP / NH);
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
+
+  f32x16 accx[NJ], accq[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    accx[j] = zero16();
+    accq[j] = zero16();
+  }
+  float nk = 0.0f;
+
+  // X tiles and row logZ2 go global -> registers -> LDS through two register
+  // stages (tile t + 2 is loaded while tile t is processed; the LDS-only barrier
+  // leaves the loads in flight).
+  f32x4 stage[LPT], stage2[LPT];
+  double rq = INFINITY, rq2 = INFINITY;
+  const bool full_d = (D == DP);
+  auto fetch = [&](int t, f32x4 (&stage)[LPT], double& rq) {
+    const int64_t row0 = r_begin + (int64_t)t * TR;
+    if (full_d && row0 + TR <= r_end) {
+      const float* src = X + row0 * ldx;
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        if (NV % kAccThreads == 0 || idx < NV)
+          stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        const int64_t row = row0 + idx / V4;
+        stage[q] = load_row4(X, ldx, row, (idx % V4) * 4, D, idx < NV && row < r_end);
+      }
+    }
+    if (tid < TR) {
+      const int64_t row = row0 + tid;
+      rq = (row < r_end) ? rowstat[row] : INFINITY;
+    }
+  };
+  auto commit = [&](int buf, const f32x4 (&stage)[LPT], double rq) {
+    float* dst = xs + buf * TR * RS;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      if (NV % kAccThreads == 0 || idx < NV)
+        *reinterpret_cast<f32x4*>(dst + (idx / V4) * RS + (idx % V4) * 4) = stage[q];
+    }
+    if (tid < TR) {
+      // Rows past the slab get logZ2 = +inf, hence r = 0.
+      const float hi = (float)rq;
+      const float lo = (rq > -INFINITY && rq < INFINITY) ? (float)(rq - (double)hi) : 0.0f;
+      rz[buf * TR + tid] = make_float2(hi, lo);
+    }
+  };
+  auto lj_fetch = [&](int t, f32x4 (&v)[4]) {
+    const int64_t row0 = r_begin + (int64_t)t * TR + rg * 32;
+    if (active && row0 < r_end) {
+      lj_load(lj + ((row0 >> 5) * KB + kb) * kLjTile, lane, v);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = zero4();
+    }
+  };
+
+  // Log-joint tiles two super-tiles ahead, or one with more than 4 accumulator
+  // tiles per wave; above 6 the r of each row is formed just before its steps
+  // (registers).
+  constexpr int kTiles = 2 * NJ;
+  constexpr bool kLj2 = kTiles <= 4;
+  constexpr bool kInterleave = kTiles > 6;
+  f32x4 ljc[4], ljn[4], ljm[4];
+  if (ntiles > 0) {
+    fetch(0, stage, rq);
+    lj_fetch(0, ljc);
+    commit(0, stage, rq);
+  }
+  if (ntiles > 1) {
+    fetch(1, stage, rq);
+    if (kLj2) lj_fetch(1, ljn);
+  }
+  lds_barrier();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    if (t + 2 < ntiles) {
+      fetch(t + 2, stage2, rq2);
+      if (kLj2) lj_fetch(t + 2, ljm);
+    }
+    if (!kLj2 && more) lj_fetch(t + 1, ljn);
+    const float* xt = xs + buf * TR * RS + rg * 32 * RS;
+    const float2* rt = rz + buf * TR + rg * 32 + 4 * g;
+    if (active) {
+      const float* xbase = xt + 4 * g * RS + col0 + c;
+      float r[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ro = 8 * (i >> 2) + (i & 3);
+        const float2 z = rt[ro];
+        const float rv = fast_exp2((ljc[i >> 2][i & 3] - z.x) - z.y);
+        if (NH == 1 || h == 0) nk += rv;
+        r[i] = rv;
+        if (kInterleave && (dense || __builtin_amdgcn_ballot_w64(rv != 0.0f) != 0)) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const float xv = xbase[ro * RS + 32 * j];
+            accx[j] = mfma32(rv, xv, accx[j]);
+            accq[j] = mfma32(rv, xv * xv, accq[j]);
+          }
+        }
+      }
+      if constexpr (!kInterleave) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int ro = 8 * (i >> 2) + (i & 3);
+          if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+              const float xv = xbase[ro * RS + 32 * j];
+              accx[j] = mfma32(r[i], xv, accx[j]);
+              accq[j] = mfma32(r[i], xv * xv, accq[j]);
+            }
+          }
+        }
+      }
+    }
+    if (more) commit(buf ^ 1, stage, rq);
+    lds_barrier();
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) stage[q] = stage2[q];
+    rq = rq2;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ljc[q] = ljn[q];
+      if (kLj2) ljn[q] = ljm[q];
+    }
+  }
+
+  if (active) {
+    nk += __shfl_xor(nk, 32);
+    const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t o = (kbase + acc_row(i, g)) * DP + col0 + 32 * j + c;
+        part_mu[o] = accx[j][i];
+        part_sq[o] = accq[j][i];
+      }
+    }
+    if (g == 0 && h == 0) part_nk[kbase + c] = nk;
   }
 }
 
@@ -778,30 +1011,68 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
   const double* kc_blk = reinterpret_cast<const double*>(ws + pl.off_kcblk);
   const double* kc_lin = reinterpret_cast<const double*>(ws + pl.off_kclin);
   double* rowstat = reinterpret_cast<double*>(ws + pl.off_rowstat);
+  float* lj = pl.lj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
+  float* pmu = reinterpret_cast<float*>(ws + pl.off_part_mu);
+  float* psq = reinterpret_cast<float*>(ws + pl.off_part_sq);
+  float* pnk = reinterpret_cast<float*>(ws + pl.off_part_nk);
   if (run1) {
     const unsigned nblk1 = (unsigned)cdiv(pl.N, 32 * kWaves);
     if constexpr (!diag_accum_split_d(DP)) {
       constexpr size_t lds1 = lse_lds_bytes<DP>();
       if (lds1 > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_lse<DP>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
-        if (e != hipSuccess) return e;
+        for (const void* f : {reinterpret_cast<const void*>(&diag_lse<DP, false>),
+                              reinterpret_cast<const void*>(&diag_lse<DP, true>)}) {
+          hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+          if (e != hipSuccess) return e;
+        }
       }
-      hipLaunchKernelGGL(diag_lse<DP>, dim3(nblk1), dim3(kThreads), lds1, stream, X, ldx, pl.N,
-                         (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
+      auto kern = pl.lj ? &diag_lse<DP, true> : &diag_lse<DP, false>;
+      hipLaunchKernelGGL(kern, dim3(nblk1), dim3(kThreads), lds1, stream, X, ldx, pl.N, (int)pl.D,
+                         mu_sw, kc_blk, pl.KB, logZ, rowstat, lj);
     } else {
       // From D = 128 the rows' dimensions are split over two waves.
       constexpr size_t lds1 = lse_split_lds_bytes<DP>();
       if (lds1 > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_lse_split<DP>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
-        if (e != hipSuccess) return e;
+        for (const void* f : {reinterpret_cast<const void*>(&diag_lse_split<DP, false>),
+                              reinterpret_cast<const void*>(&diag_lse_split<DP, true>)}) {
+          hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+          if (e != hipSuccess) return e;
+        }
       }
-      hipLaunchKernelGGL(diag_lse_split<DP>, dim3(nblk1), dim3(kAccThreads), lds1, stream, X, ldx,
-                         pl.N, (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat);
+      auto kern = pl.lj ? &diag_lse_split<DP, true> : &diag_lse_split<DP, false>;
+      hipLaunchKernelGGL(kern, dim3(nblk1), dim3(kAccThreads), lds1, stream, X, ldx, pl.N,
+                         (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat, lj);
     }
   }
   if (!run2) return hipGetLastError();
+  const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
+  if (pl.lj) {
+    auto launch = [&](auto cb_tag, auto nh_tag) -> hipError_t {
+      constexpr int CB = decltype(cb_tag)::value;
+      constexpr int NH = decltype(nh_tag)::value;
+      constexpr size_t lds = accum_lj_lds_bytes<DP, CB, NH>();
+      static_assert(lds <= kMaxLds, "pass-2 tiles exceed LDS");
+      if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum_lj<DP, CB, NH>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+      }
+      hipLaunchKernelGGL((diag_accum_lj<DP, CB, NH>), grid2, dim3(kAccThreads), lds, stream, X, ldx,
+                         pl.N, (int)pl.D, lj, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
+                         pmu, psq, pnk, dense ? 1 : 0);
+      return hipGetLastError();
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
+    if constexpr (DP > 128) {
+      return launch(I4{}, I2{});
+    } else if constexpr (DP == 128) {
+      return pl.cpg == 8 ? launch(std::integral_constant<int, 8>{}, I1{}) : launch(I4{}, I2{});
+    } else {
+      return pl.cpg == 8 ? launch(std::integral_constant<int, 8>{}, I1{}) : launch(I4{}, I1{});
+    }
+  }
   if constexpr (diag_accum_split_d(DP)) {
     constexpr size_t lds2 = accum_split_lds_bytes<DP>();
     if (lds2 > 65536) {
@@ -853,9 +1124,8 @@ extern "C" size_t fgmm_diag_workspace_bytes(int64_t N, int64_t K, int64_t D) {
 }
 
 extern "C" size_t fgmm_diag_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
-  (void)flags;
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D).total;
+  return make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE)).total;
 }
 
 extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -877,7 +1147,7 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     return FGMM_ERR_INVALID_ARG;
   if (D > 256) return FGMM_ERR_UNSUPPORTED;
   if (N > kMaxRows || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
-  const DiagPlan pl = make_plan(N, K, D);
+  const DiagPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE));
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;
   unsigned char* ws = static_cast<unsigned char*>(workspace);

@@ -66,9 +66,13 @@ def test_iso_workspace_holds_stored_log_joint():
     # Not stored: D <= 32, K <= 96, or more than 16 GiB of tiles.
     for n, k, d in [(N, K, 32), (N, 96, 128), (N, 96, 192), (20_000_000, 1024, 128)]:
         assert L.fgmm_iso_workspace_bytes(n, k, d) == L.fgmm_iso_workspace_bytes_ex(n, k, d, R)
-    for fam in ("diag", "full"):
-        q, qx = getattr(L, f"fgmm_{fam}_workspace_bytes"), getattr(L, f"fgmm_{fam}_workspace_bytes_ex")
-        assert q(5000, 64, 64) == qx(5000, 64, 64, 0) > 0
+    # Diagonal: stored for K > 96 at every D.
+    d_full = L.fgmm_diag_workspace_bytes(N, K, 96)
+    d_lean = L.fgmm_diag_workspace_bytes_ex(N, K, 96, R)
+    assert d_full == L.fgmm_diag_workspace_bytes_ex(N, K, 96, 0) and d_full - d_lean >= tiles
+    assert L.fgmm_diag_workspace_bytes(N, 96, 96) == L.fgmm_diag_workspace_bytes_ex(N, 96, 96, R)
+    q, qx = L.fgmm_full_workspace_bytes, L.fgmm_full_workspace_bytes_ex
+    assert q(5000, 64, 64) == qx(5000, 64, 64, 0) > 0
 
 
 # Fake but aligned, non-null addresses: every call below must be rejected by

@@ -45,8 +45,10 @@ def test_edge_shapes(N, K, D, gpu_device):
     assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), f"diag N={N} K={K} D={D}")
 
 
-@pytest.mark.parametrize("N,K,D,seed", [(9000, 512, 96, 2), (3001, 77, 45, 3), (4000, 130, 256, 4)])
-def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, gpu_device):
+@pytest.mark.parametrize("recompute", [False, True])
+@pytest.mark.parametrize("N,K,D,seed", [(9000, 512, 96, 2), (3001, 77, 45, 3), (4000, 130, 256, 4),
+                                        (5000, 300, 128, 6)])
+def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, recompute, gpu_device):
     """Skipping all-zero responsibility steps changes no bit of any output."""
     inp = data.diag_clustered(N, K, D, seed=seed)
     dev = gpu_device
@@ -55,7 +57,7 @@ def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, gpu_device):
     for dense in (False, True):
         o = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
              torch.empty(K, D, device=dev)]
-        diag_estep_into(*args, *o, dense=dense)
+        diag_estep_into(*args, *o, dense=dense, recompute=recompute)
         outs.append(o)
     torch.cuda.synchronize()
     for u, v in zip(*outs):
@@ -68,6 +70,60 @@ def test_small_k_mid_size(N, K, D, gpu_device):
     """Few component blocks: pass 2 runs 1 or 2 blocks per workgroup with more row groups."""
     inp = data.diag_clustered(N, K, D, seed=N % 89)
     assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), f"diag small K N={N} K={K} D={D}")
+
+
+def _into(inp, dev, **kw):
+    N, D = inp["X"].shape
+    K = inp["mu"].shape[0]
+    out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, D, device=dev)]
+    diag_estep_into(*[inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")], *out, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+# Shapes on the stored log-joint path (K > 96), with partial tiles and slabs, every
+# padded width and both column splits of pass 2 (8 or 4 blocks per workgroup).
+LJ_SHAPES = [(33, 128, 20), (65, 257, 96), (1000, 130, 64), (777, 300, 61), (4097, 129, 100),
+             (2500, 260, 192), (1800, 300, 250), (9001, 512, 128), (3000, 150, 128), (700, 200, 256)]
+
+
+@pytest.mark.parametrize("N,K,D", LJ_SHAPES)
+def test_stored_and_recomputed_log_joint(N, K, D, gpu_device):
+    """Pass 2 from the log-joint stored by pass 1, and recomputed, both against the oracle."""
+    from flash_gmm import _lib
+    L = _lib.lib()
+    # The two plans differ (stored tiles, pass-2 work split), so these shapes take the stored path.
+    assert L.fgmm_diag_workspace_bytes(N, K, D) != L.fgmm_diag_workspace_bytes_ex(N, K, D, _lib.FLAG_RECOMPUTE)
+    inp = data.diag_clustered(N, K, D, seed=N + 3 * K + D)
+    ref = oracle(inp)
+    stored = _into(inp, gpu_device)
+    recomputed = _into(inp, gpu_device, recompute=True)
+    assert torch.equal(stored[0], recomputed[0])
+    assert_close_stats(stored, ref, f"stored N={N} K={K} D={D}")
+    assert_close_stats(recomputed, ref, f"recomputed N={N} K={K} D={D}")
+
+
+@pytest.mark.parametrize("recompute", [False, True])
+def test_phase_split_equals_one_call(recompute, gpu_device):
+    """PHASE1 then PHASE2 on one workspace gives the single call's outputs bitwise."""
+    from flash_gmm import _lib
+    inp = data.diag_clustered(5000, 256, 80, seed=16)
+    dev = gpu_device
+    ref = _into(inp, dev, recompute=recompute)
+    N, D = inp["X"].shape
+    K = inp["mu"].shape[0]
+    L = _lib.lib()
+    flags = _lib.FLAG_RECOMPUTE if recompute else 0
+    ws = torch.empty(L.fgmm_diag_workspace_bytes_ex(N, K, D, flags), dtype=torch.uint8, device=dev)
+    out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, D, device=dev)]
+    args = [inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
+    diag_estep_into(*args, *out, workspace=ws, phase=1, recompute=recompute)
+    diag_estep_into(*args, None, *out[1:], workspace=ws, phase=2, recompute=recompute)
+    torch.cuda.synchronize()
+    for u, v in zip(out, ref):
+        assert torch.equal(u, v)
 
 
 def test_equal_variances_match_isotropic(gpu_device):
