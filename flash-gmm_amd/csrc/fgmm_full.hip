@@ -30,6 +30,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace fgmm {
 namespace {
 
@@ -51,17 +53,29 @@ struct FullPlan {
   int KP;       // K padded to kCompsPerWG
   int ncg, nslab, rgroups, npart;
   int64_t rows_per_slab;
-  size_t off_lsw, off_bsw, off_ck, off_rowstat, off_part_sig, off_part_mu, off_part_nk, total;
+  bool lj;      // pass 1 stores the log-joint; pass 2 reads it
+  size_t off_lsw, off_bsw, off_ck, off_rowstat, off_part_sig, off_part_mu, off_part_nk, off_lj, total;
 };
 
-FullPlan make_plan(int64_t N, int64_t K, int64_t D) {
+// Stored log-joint of the full model: per (32-row tile, component) 32 floats, rows
+// contiguous, [tile][KP][32]; one tile per pass-1 wave (the grid's tiles, rounded
+// up to 4).  Pass 2 reads it unless recomputation is requested or it would exceed
+// kMaxLjBytes: recomputing costs a D x D whitening per (row, component).
+__host__ inline size_t full_lj_bytes(int64_t N, int KP) {
+  return (size_t)round_up(cdiv(N, 32), 4) * (size_t)KP * 32 * sizeof(float);
+}
+
+FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true) {
   FullPlan p{};
   p.N = N; p.K = K; p.D = D;
   p.DP = (int)round_up(D < 1 ? 1 : D, 32);
   p.NMB = p.DP / 32;
   p.NSB = p.NMB * (p.NMB + 1) / 2;
   p.KP = (int)round_up(K, kCompsPerWG);
-  const bool split = full_accum_split_d(p.DP);
+  p.lj = allow_lj && K > 0 && full_lj_bytes(N, p.KP) <= kMaxLjBytes;
+  // Reading the log-joint, pass 2 needs no whitening operands in LDS, and the
+  // 4-component kernel serves every D.
+  const bool split = full_accum_split_d(p.DP) && !p.lj;
   p.ncg = split ? (int)K : p.KP / kCompsPerWG;
   p.rgroups = split ? 1 : kRowGroups;
   const int64_t tile_rows = 32 * p.rgroups;
@@ -86,6 +100,8 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D) {
   p.off_part_sig = off; off = align256(off + (size_t)p.npart * p.KP * p.NSB * 1024 * sizeof(float));
   p.off_part_mu = off;  off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
   p.off_part_nk = off;  off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
+  p.off_lj = off;
+  if (p.lj) off = align256(off + full_lj_bytes(N, p.KP));
   p.total = off;
   return p;
 }
@@ -171,13 +187,13 @@ constexpr size_t lse_lds_bytes() {
   return (size_t)2 * DP * DP * sizeof(float) + (size_t)2 * (DP + 8) * sizeof(double);
 }
 
-template <int DP>
+template <int DP, bool LJ>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(DP <= 64 ? 2 : 1, DP <= 64 ? 2 : 1)))
 void full_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
               const f32x4* __restrict__ lsw, const double* __restrict__ bsw,
-              const double* __restrict__ ck, int K, float* __restrict__ logZ,
-              double* __restrict__ rowstat) {
+              const double* __restrict__ ck, int K, int KP, float* __restrict__ logZ,
+              double* __restrict__ rowstat, float* __restrict__ lj) {
   constexpr int NMB = DP / 32, NM = DP / 8;
   constexpr int BLK = NMB * NM * 64;              // float4 per component
   constexpr int LPT = BLK / kThreads;
@@ -190,8 +206,11 @@ void full_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
-  const int64_t row = ((int64_t)blockIdx.x * kWaves + wave) * 32 + c;
+  const int64_t tile = (int64_t)blockIdx.x * kWaves + wave;   // 32-row tile
+  const int64_t row = tile * 32 + c;
   const bool valid = row < N;
+  // Both half-waves hold row c's log-joint; both store it (same value, same address).
+  float* ljt = LJ ? lj + tile * KP * 32 + c : nullptr;
 
   f32x4 st[LPT];
   double bst = 0.0;
@@ -224,12 +243,13 @@ void full_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const double maha = maha_one<NMB, NM>(l_l + buf * BLK, b_l + buf * BW, lane, g,
                                           [&](int m) { return xb[m]; });
     const double ll = b_l[buf * BW + DP] - hl * maha;
+    if constexpr (LJ) ljt[k * 32] = (float)ll;
     const double mn = fmax(mx, ll);
     const double ms = (mn == -INFINITY) ? 0.0 : mn;
     sm = sm * fast_exp2((float)(mx - ms)) + fast_exp2((float)(ll - ms));
     mx = mn;
     if (more) commit(buf ^ 1);
-    __syncthreads();
+    lds_barrier();
   }
   const double lz2 = mx + (double)log2f(sm);
   if (valid && g == 0) {
@@ -241,23 +261,24 @@ void full_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 // ---------------------------------------------------------------------------
 // Pass 2.
 // ---------------------------------------------------------------------------
-template <int DP>
+template <int DP, bool LJ>
 constexpr size_t accum_lds_bytes() {
   constexpr int TR = 32 * kRowGroups;
-  return (size_t)kCompsPerWG * DP * DP * sizeof(float)          // L^T operands
+  return (LJ ? 0 : (size_t)kCompsPerWG * DP * DP * sizeof(float))   // L^T operands
          + (size_t)kCompsPerWG * (DP + 8) * sizeof(double)      // b, c
          + (size_t)2 * TR * (DP + 4) * sizeof(float)            // X tiles
          + (size_t)2 * TR * sizeof(double)                      // logZ2
          + (size_t)kAccWaves * 32 * sizeof(float);              // r exchange
 }
 
-template <int DP>
+template <int DP, bool LJ>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                 const f32x4* __restrict__ lsw, const double* __restrict__ bsw,
                 const double* __restrict__ ck, int K, int KP, const double* __restrict__ rowstat,
                 int nslab, int64_t rows_per_slab, float* __restrict__ part_sig,
-                float* __restrict__ part_mu, float* __restrict__ part_nk, int dense) {
+                float* __restrict__ part_mu, float* __restrict__ part_nk, int dense,
+                const float* __restrict__ lj) {
   constexpr int NMB = DP / 32, NM = DP / 8, NSB = NMB * (NMB + 1) / 2;
   constexpr int RS = DP + 4, V4 = DP / 4;
   constexpr int BLK = NMB * NM * 64;
@@ -269,7 +290,7 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   unsigned char* p = lds_raw;
-  f32x4* l_l = reinterpret_cast<f32x4*>(p);   p += kCompsPerWG * BLK * sizeof(f32x4);
+  f32x4* l_l = reinterpret_cast<f32x4*>(p);   p += LJ ? 0 : kCompsPerWG * BLK * sizeof(f32x4);
   double* b_l = reinterpret_cast<double*>(p); p += kCompsPerWG * BW * sizeof(double);
   float* xs = reinterpret_cast<float*>(p);    p += 2 * TR * RS * sizeof(float);
   double* rs = reinterpret_cast<double*>(p);  p += 2 * TR * sizeof(double);
@@ -289,10 +310,12 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
 
   // Operands of the workgroup's components -> LDS (lsw/bsw/ck are padded to KP).
+  if constexpr (!LJ) {
 #pragma unroll
-  for (int q = 0; q < MPT; ++q) {
-    const int idx = q * kAccThreads + tid;
-    l_l[idx] = lsw[(int64_t)cg * kCompsPerWG * BLK + idx];
+    for (int q = 0; q < MPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      l_l[idx] = lsw[(int64_t)cg * kCompsPerWG * BLK + idx];
+    }
   }
   for (int idx = tid; idx < kCompsPerWG * BW; idx += kAccThreads) {
     const int cc = idx / BW, e = idx % BW;
@@ -362,10 +385,17 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const float* xt = xs + buf * TR * RS + rg * 32 * RS;
     const double* rt = rs + buf * TR + rg * 32;
     if (active) {
-      // r for this lane's row c (both half-waves hold it after the exchange in maha_one).
-      const double maha = maha_one<NMB, NM>(
-          Lc, bc, lane, g, [&](int m) { return *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * m + 4 * g); });
-      const float rv = fast_exp2((float)((bc[DP] - rt[c]) - hl * maha));
+      // r for this lane's row c (both half-waves hold it).
+      float rv;
+      if constexpr (LJ) {
+        const int64_t row0 = r_begin + (int64_t)t * TR + rg * 32;
+        const float l = row0 < r_end ? lj[((row0 >> 5) * KP + k) * 32 + c] : 0.0f;
+        rv = fast_exp2((float)((double)l - rt[c]));
+      } else {
+        const double maha = maha_one<NMB, NM>(
+            Lc, bc, lane, g, [&](int m) { return *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * m + 4 * g); });
+        rv = fast_exp2((float)((bc[DP] - rt[c]) - hl * maha));
+      }
       if (g == 0) {
         nk += rv;
         rx[c] = rv;
@@ -664,43 +694,47 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
   const double* bsw = reinterpret_cast<const double*>(ws + pl.off_bsw);
   const double* ck = reinterpret_cast<const double*>(ws + pl.off_ck);
   double* rowstat = reinterpret_cast<double*>(ws + pl.off_rowstat);
+  float* lj = pl.lj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
+  auto set_lds = [](const void* f, size_t bytes) -> hipError_t {
+    return bytes > 65536 ? hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes)
+                         : hipSuccess;
+  };
   if (run1) {
     constexpr size_t lds1 = lse_lds_bytes<DP>();
-    if (lds1 > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&full_lse<DP>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+    for (const void* f : {reinterpret_cast<const void*>(&full_lse<DP, false>),
+                          reinterpret_cast<const void*>(&full_lse<DP, true>)}) {
+      hipError_t e = set_lds(f, lds1);
       if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(full_lse<DP>, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
-                       stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, logZ, rowstat);
+    auto kern = pl.lj ? &full_lse<DP, true> : &full_lse<DP, false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1, stream, X,
+                       ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, logZ, rowstat, lj);
   }
   if (!run2) return hipGetLastError();
-  if constexpr (full_accum_split_d(DP)) {
-    constexpr size_t lds2 = accum_split_lds_bytes<DP>();
-    if (lds2 > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&full_accum_split<DP>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+  float* psig = reinterpret_cast<float*>(ws + pl.off_part_sig);
+  float* pmu = reinterpret_cast<float*>(ws + pl.off_part_mu);
+  float* pnk = reinterpret_cast<float*>(ws + pl.off_part_nk);
+  const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
+  auto launch2 = [&](auto lj_tag) -> hipError_t {
+    constexpr bool LJ = decltype(lj_tag)::value;
+    if constexpr (!LJ && full_accum_split_d(DP)) {
+      constexpr size_t lds2 = accum_split_lds_bytes<DP>();
+      hipError_t e = set_lds(reinterpret_cast<const void*>(&full_accum_split<DP>), lds2);
       if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(full_accum_split<DP>, dim3((unsigned)(pl.nslab * pl.ncg)), dim3(kThreads), lds2,
-                       stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, rowstat,
-                       pl.nslab, pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_sig),
-                       reinterpret_cast<float*>(ws + pl.off_part_mu),
-                       reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
-  } else {
-    constexpr size_t lds2 = accum_lds_bytes<DP>();
-    if (lds2 > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&full_accum<DP>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+      hipLaunchKernelGGL((full_accum_split<DP>), grid2, dim3(kThreads), lds2, stream, X, ldx, pl.N,
+                         (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, rowstat, pl.nslab,
+                         pl.rows_per_slab, psig, pmu, pnk, dense ? 1 : 0);
+    } else {
+      constexpr size_t lds2 = accum_lds_bytes<DP, LJ>();
+      hipError_t e = set_lds(reinterpret_cast<const void*>(&full_accum<DP, LJ>), lds2);
       if (e != hipSuccess) return e;
+      hipLaunchKernelGGL((full_accum<DP, LJ>), grid2, dim3(kAccThreads), lds2, stream, X, ldx, pl.N,
+                         (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, rowstat, pl.nslab,
+                         pl.rows_per_slab, psig, pmu, pnk, dense ? 1 : 0, lj);
     }
-    hipLaunchKernelGGL(full_accum<DP>, dim3((unsigned)(pl.nslab * pl.ncg)), dim3(kAccThreads), lds2,
-                       stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, rowstat, pl.nslab,
-                       pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_sig),
-                       reinterpret_cast<float*>(ws + pl.off_part_mu),
-                       reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
-  }
-  return hipGetLastError();
+    return hipGetLastError();
+  };
+  return pl.lj ? launch2(std::true_type{}) : launch2(std::false_type{});
 }
 
 }  // namespace
@@ -714,9 +748,8 @@ extern "C" size_t fgmm_full_workspace_bytes(int64_t N, int64_t K, int64_t D) {
 }
 
 extern "C" size_t fgmm_full_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
-  (void)flags;
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D).total;
+  return make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE)).total;
 }
 
 extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -738,7 +771,7 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     return FGMM_ERR_INVALID_ARG;
   if (D > 128) return FGMM_ERR_UNSUPPORTED;
   if (N > kMaxRows || K > (int64_t)1 << 20) return FGMM_ERR_UNSUPPORTED;
-  const FullPlan pl = make_plan(N, K, D);
+  const FullPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE));
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;
   unsigned char* ws = static_cast<unsigned char*>(workspace);

@@ -71,8 +71,11 @@ def test_iso_workspace_holds_stored_log_joint():
     d_lean = L.fgmm_diag_workspace_bytes_ex(N, K, 96, R)
     assert d_full == L.fgmm_diag_workspace_bytes_ex(N, K, 96, 0) and d_full - d_lean >= tiles
     assert L.fgmm_diag_workspace_bytes(N, 96, 96) == L.fgmm_diag_workspace_bytes_ex(N, 96, 96, R)
+    # Full: stored whenever it fits, 32 floats per (32-row tile, component).
     q, qx = L.fgmm_full_workspace_bytes, L.fgmm_full_workspace_bytes_ex
     assert q(5000, 64, 64) == qx(5000, 64, 64, 0) > 0
+    n = 250_000
+    assert q(n, 256, 64) - qx(n, 256, 64, R) >= -(-n // 128) * 4 * 256 * 128
 
 
 # Fake but aligned, non-null addresses: every call below must be rejected by
