@@ -73,14 +73,15 @@ def cpu_baseline(inp, kind, K, D, min_s=10.0, max_s=30.0, rows=16384):
     }
 
 
-# HBM bytes per launch of each pass's main kernel: rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE (separate runs) on this bench command, scaled by what the counters
-# read for a 512 MiB device copy (x2.0 for FETCH_SIZE, x1.0 for WRITE_SIZE); the
-# counter values and commands are in profiles/<kind>_estep_<shape>.md.
+# HBM bytes per launch of each pass's main kernel with the stored log-joint (the
+# default): rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (separate runs) on this
+# bench command, scaled by what the counters read for a 512 MiB device copy (x2.0
+# for FETCH_SIZE, x1.0 for WRITE_SIZE); the counter values and commands are in
+# profiles/<kind>_estep_<shape>.md.  Not reported with --recompute.
 TRAFFIC_BYTES = {
-    "iso_n1m_k1024_d128": {"phase1": 589_618_790, "phase2": 566_709_248},
-    "diag_n1m_k1024_d96": {"phase1": 402_644_582, "phase2": 452_352_614},
-    "full_n250k_k256_d64": {"phase1": 298_443_879, "phase2": 175_187_251},
+    "iso_n1m_k1024_d128": {"phase1": 4_684_565_705, "phase2": 4_658_482_852},
+    "diag_n1m_k1024_d96": {"phase1": 4_499_631_140, "phase2": 4_542_595_401},
+    "full_n250k_k256_d64": {"phase1": 589_263_972, "phase2": 414_389_462},
 }
 
 WORKLOADS = {
@@ -106,6 +107,25 @@ def algorithmic_flop(kind, N, K, D):
     if kind == "diag":
         return 8.0 * N * K * D, 4.0 * N * K * D, 4.0 * N * K * D
     return 4.0 * N * K * D * D + 2.0 * N * K * D, 2.0 * N * K * D * D, 2.0 * N * K * D * D + 2.0 * N * K * D
+
+
+def algorithmic_bytes(kind, N, K, D, lj):
+    """Per-step HBM bytes each phase must move (phase 1, phase 2).
+
+    Phase 1 reads X and writes logZ, the per-row state (iso: ||x||^2 and logZ2 in
+    fp64; diag, full: logZ2) and, when pass 2 reads it, the fp32 log-joint.
+    Phase 2 reads X, the per-row state and the log-joint.  O(K*D) operands and the
+    slab partials are left out (under 1% here).
+    """
+    KB = -(-K // 32)
+    if kind == "full":
+        lj_bytes = (-(-N // 128) * 4) * (-(-K // 4) * 4) * 32 * 4
+    else:
+        lj_bytes = (-(-N // 128) * 4) * KB * 4096
+    lj_bytes = lj_bytes if lj else 0
+    row = 16 if kind == "iso" else 8
+    x = 4.0 * N * D
+    return x + 4.0 * N + row * N + lj_bytes, x + row * N + lj_bytes
 
 
 def stream_main(args):
@@ -195,6 +215,9 @@ def main():
     ap.add_argument("--workload", default="iso_n1m_k1024_d128",
                     choices=sorted(WORKLOADS) + ["stream_em_n1b_k1024_d128"])
     ap.add_argument("--rows", type=int, default=0, help="override N of the streaming workload")
+    ap.add_argument("--recompute", action="store_true",
+                    help="pass 2 recomputes the log-joint (FGMM_FLAG_RECOMPUTE) instead of reading "
+                         "the copy pass 1 stores")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB five times (scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -234,22 +257,24 @@ def main():
     if kind == "iso":
         args4 = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
         sig = torch.empty(K, device=dev)
-        ws = torch.empty(int(L.fgmm_iso_workspace_bytes(N, K, D)), dtype=torch.uint8, device=dev)
         fn = lambda ph, dense=args.dense: iso_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
                                                          phase=ph, atomic_reduce=args.atomic_reduce,
-                                                         dense=dense)
+                                                         dense=dense, recompute=args.recompute)
     elif kind == "diag":
         args4 = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
         sig = torch.empty(K, D, device=dev)
-        ws = torch.empty(int(L.fgmm_diag_workspace_bytes(N, K, D)), dtype=torch.uint8, device=dev)
         fn = lambda ph, dense=args.dense: diag_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
-                                                          phase=ph, dense=dense)
+                                                          phase=ph, dense=dense, recompute=args.recompute)
     else:
         args4 = (inp["X"], inp["mu"], inp["prec_chol"], inp["log_pi"])
         sig = torch.empty(K, D, D, device=dev)
-        ws = torch.empty(int(L.fgmm_full_workspace_bytes(N, K, D)), dtype=torch.uint8, device=dev)
         fn = lambda ph, dense=args.dense: full_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
-                                                          phase=ph, dense=dense)
+                                                          phase=ph, dense=dense, recompute=args.recompute)
+    ws_fn = getattr(L, f"fgmm_{kind}_workspace_bytes_ex")
+    flags = _lib.FLAG_RECOMPUTE if args.recompute else 0
+    ws = torch.empty(int(ws_fn(N, K, D, flags)), dtype=torch.uint8, device=dev)
+    # Pass 2 reads the log-joint that pass 1 stores whenever the plan sizes it in.
+    stored_lj = int(ws_fn(N, K, D, 0)) != int(ws_fn(N, K, D, _lib.FLAG_RECOMPUTE)) and not args.recompute
     stream = torch.cuda.current_stream(dev)
 
     def step(ev=None):
@@ -301,16 +326,36 @@ def main():
         log(f"dense accumulation: {dense_ms:.3f} ms/step")
 
     flop, f1, f2 = algorithmic_flop(kind, N, K, D)
+    b1, b2 = algorithmic_bytes(kind, N, K, D, stored_lj)
     step_tflops = flop / (ms * 1e-3) / 1e12
-    names = {"iso": ("iso_lse (log-normaliser pass + prologue)", "iso_accum (accumulation pass + slab reduction)"),
-             "diag": ("diag_lse (log-normaliser pass + prologue)", "diag_accum (accumulation pass + slab reduction)"),
-             "full": ("full_lse (log-normaliser pass + prologue)", "full_accum (accumulation pass + slab reduction)")}[kind]
-    if p2 >= p1:
-        dom, dom_ms, dom_flop, dom_phase = names[1], p2, f2, "phase2"
+    p2_kernel = {"iso": "iso_accum", "diag": "diag_accum", "full": "full_accum"}[kind] + (
+        "_lj" if stored_lj and kind != "full" else "")
+    names = (f"{kind}_lse (log-normaliser pass + prologue"
+             + (", stores the log-joint)" if stored_lj else ")"),
+             f"{p2_kernel} (accumulation pass + slab reduction"
+             + (", reads the stored log-joint)" if stored_lj else ", recomputes the log-joint)"))
+    traffic_tab = {} if args.recompute else TRAFFIC_BYTES.get(args.workload, {})
+    phases = {}
+    for ph, name, t, f, b in (("phase1", names[0], p1, f1, b1), ("phase2", names[1], p2, f2, b2)):
+        phases[ph] = {"kernel": name, "ms": t, "algorithmic_flop": f,
+                      "tflops": f / (t * 1e-3) / 1e12, "algorithmic_bytes": b,
+                      "gbs": b / (t * 1e-3) / 1e9, "traffic": traffic_tab.get(ph)}
+    dom_phase = "phase2" if p2 >= p1 else "phase1"
+    dom = phases[dom_phase]
+    # Phase 1 and the recomputing phase 2 are matrix-core bound.  Reading the stored
+    # log-joint, phase 2 moves ~8 bytes per (row, component) and skips the steps whose
+    # responsibilities are all zero: it is HBM bound.
+    hbm_bound = dom_phase == "phase2" and stored_lj and not args.dense
+    if hbm_bound:
+        roof = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": dom["gbs"] / PEAK_HBM_GBS, "algorithmic_bytes_per_launch": dom["algorithmic_bytes"]}
     else:
-        dom, dom_ms, dom_flop, dom_phase = names[0], p1, f1, "phase1"
-    traffic = TRAFFIC_BYTES.get(args.workload, {}).get(dom_phase)
-    dom_tflops = dom_flop / (dom_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": dom["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": dom["tflops"] / PEAK_FP32_MFMA_TFLOPS,
+                "algorithmic_flop_per_launch": dom["algorithmic_flop"]}
+    roof.update({"kernel": dom["kernel"], "traffic": dom["traffic"],
+                 "traffic_unit": "bytes per launch (HBM read + write, rocprofv3 counters)",
+                 "avg_launch_ms": dom["ms"]})
 
     out = {
         "metric": METRIC if kind == "iso" else
@@ -331,27 +376,23 @@ def main():
         "data": "synthetic",
         "config": {"workload": args.workload, "N": N, "K": K, "D": D,
                    "generator": f"flash_gmm.data.make({args.workload!r}), generated on device",
-                   "reduce": "atomic" if args.atomic_reduce else "deterministic"},
+                   "reduce": "atomic" if args.atomic_reduce else "deterministic",
+                   "log_joint": "stored by phase 1, read by phase 2" if stored_lj else "recomputed by phase 2"},
         "fraction_of_fp32_mfma_peak": step_tflops / PEAK_FP32_MFMA_TFLOPS,
+        "fraction_basis": "dense-equivalent algorithmic flops per step / step time; phase 2 executes "
+                          "only the accumulation steps whose responsibilities are not all zero"
+                          + (" and reads the log-joint instead of recomputing it" if stored_lj else "")
+                          + ", so the matrix work executed is lower: the dense run and the per-phase "
+                            "rates below are the executed figures",
         "step_tflops_algorithmic": step_tflops,
         "phase_ms": {"phase1": p1, "phase2": p2},
+        "phases": phases,
         "accumulation": "dense" if args.dense else
                         "skips steps whose responsibilities are all exactly zero (bitwise-identical outputs)",
         "dense_ms_per_step": dense_ms if dense_ms is not None else (ms if args.dense else None),
         "dense_fraction_of_fp32_mfma_peak": (flop / (dense_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS)
                                             if dense_ms is not None else None,
-        "roofline": {
-            "bound": "mfma",
-            "kernel": dom,
-            "achieved": dom_tflops,
-            "peak": PEAK_FP32_MFMA_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": dom_tflops / PEAK_FP32_MFMA_TFLOPS,
-            "traffic": traffic,
-            "traffic_unit": "bytes per launch (HBM read + write, rocprofv3 counters)",
-            "algorithmic_flop_per_launch": dom_flop,
-            "avg_launch_ms": dom_ms,
-        },
+        "roofline": roof,
     }
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (bounded sample)")
