@@ -1138,6 +1138,7 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   const bool accumulate = (flags & FGMM_FLAG_ACCUMULATE) != 0;
   const bool dense = (flags & FGMM_FLAG_DENSE) != 0;
   if (N < 0 || K < 0 || D < 1) return FGMM_ERR_INVALID_ARG;
+  if (flags & FGMM_FLAG_BF16) return FGMM_ERR_UNSUPPORTED;
   if (N > 0 && (X == nullptr || ldx < round_up(D, 4) || (ldx % 4) != 0 ||
                 (reinterpret_cast<uintptr_t>(X) & 15) != 0))
     return FGMM_ERR_INVALID_ARG;

@@ -98,6 +98,7 @@ struct IsoPlan {
   int rgroups;  // row groups per slab (partials per slab)
   int npart;    // nslab * rgroups
   int64_t rows_per_slab;
+  bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16)
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
   int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
   size_t off_musw, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_nk, off_part_sig, off_lj,
@@ -112,14 +113,24 @@ __host__ inline bool use_stored_lj(int64_t N, int DP, int KB, bool allow) {
          (size_t)round_up(cdiv(N, 32), 4) * (size_t)KB * kLjTile * sizeof(float) <= kMaxLjBytes;
 }
 
-IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true) {
+// bf16 pass 2: 4 component blocks per workgroup, or 2 / 1 for K <= 64 / 32 where
+// the taller X tiles fit in LDS (row-major and transposed bf16, double-buffered).
+__host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB);
+__host__ __device__ constexpr int bf16_halves(int DP);
+__host__ inline int bf16_blocks_per_group(int DP, int KB);
+
+IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf16 = false) {
   IsoPlan p{};
   p.N = N; p.K = K; p.D = D;
   p.DP = iso_padded_dim(D);
   p.KB = (int)cdiv(K, 32);
   p.KP = p.KB * 32;
-  p.lj = use_stored_lj(N, p.DP, p.KB, allow_lj);
-  if (p.lj) {
+  p.bf16 = bf16;
+  p.lj = !bf16 && use_stored_lj(N, p.DP, p.KB, allow_lj);
+  if (bf16) {
+    p.cpg = bf16_blocks_per_group(p.DP, p.KB);
+    p.rgroups = kAccWaves / (p.cpg * bf16_halves(p.DP));
+  } else if (p.lj) {
     // 8 component blocks per workgroup, or 4 for K <= 224; then above D = 128 two
     // waves share a block (one half of the columns each): one wave's accumulators
     // for 4 row groups would not fit.
@@ -1203,6 +1214,452 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   return hipGetLastError();
 }
 
+// ===========================================================================
+// bf16 operand contract (FGMM_FLAG_BF16), the arithmetic of the reference's H100
+// kernels (flash_gmm_h100.py:247-328): X and mu rounded to bfloat16 for x.mu and for
+// r^T X (r rounded to bfloat16 there), fp32 accumulation, constants from the fp32
+// mu, everything else in fp32 log2 units:
+//   ish_k = 0.5 exp(-lss_k) log2 e,  c0_k = (lpi_k - 0.5 D (log 2pi + lss_k)) log2 e - ish_k ||mu_k||^2
+//   ll2 = c0_k - ish_k ||x_b||^2 + 2 ish_k (x_b . mu_b)
+// The matrix step is v_mfma_f32_32x32x16_bf16: 16 dimensions (or rows) per step;
+// the hardware pairs element e of lane-half g of A with the same (g, e) of B, so
+// both operands take dimensions 16q + 8g + e.  Pass 2 recomputes the contraction
+// (at bf16 rates that costs less than storing the log-joint).
+// ===========================================================================
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Above D = 128 pass 2 splits a component block over two waves, one half of the
+// dimensions each (and pass 1 sums its contraction in the same two halves).
+__host__ __device__ constexpr int bf16_halves(int DP) { return DP > 128 ? 2 : 1; }
+
+// Round-to-nearest-even fp32 -> bf16 of 8 values.
+__device__ __forceinline__ bf16x8 to_bf16x8(f32x4 lo, f32x4 hi) {
+  bf16x8 v;
+  v[0] = (__bf16)lo.x; v[1] = (__bf16)lo.y; v[2] = (__bf16)lo.z; v[3] = (__bf16)lo.w;
+  v[4] = (__bf16)hi.x; v[5] = (__bf16)hi.y; v[6] = (__bf16)hi.z; v[7] = (__bf16)hi.w;
+  return v;
+}
+
+// Prologue: mu in operand order mu_op[kb][q][lane] = mu[kb*32 + lane%32][16q + 8(lane/32) + e]
+// (bf16x8), and per component {c0, ish, 2 ish, ||mu||^2} in fp32 (formed in fp64).
+__global__ __launch_bounds__(64) void iso_bf16_prep(const float* __restrict__ mu, int64_t ldmu,
+                                                    int64_t K, int D, int DP,
+                                                    const float* __restrict__ lss,
+                                                    const float* __restrict__ lpi,
+                                                    bf16x8* __restrict__ mu_op, f32x4* __restrict__ kc) {
+  const int kb = blockIdx.x, lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  const int64_t k = (int64_t)kb * 32 + c;
+  const bool valid = k < K;
+  const int NC = DP / 16;
+  for (int q = 0; q < NC; ++q) {
+    bf16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = 16 * q + 8 * g + e;
+      v[e] = (__bf16)((valid && d < D) ? mu[k * ldmu + d] : 0.0f);
+    }
+    mu_op[((int64_t)kb * NC + q) * 64 + lane] = v;
+  }
+  if (g == 0) {
+    f32x4 w = {-INFINITY, 0.0f, 0.0f, 0.0f};
+    if (valid) {
+      double msq = 0.0;
+      for (int d = 0; d < D; ++d) {
+        const double m = (double)mu[k * ldmu + d];
+        msq = fma(m, m, msq);
+      }
+      const double l = (double)lss[k];
+      const double ish = 0.5 * exp(-l) * kLog2e;
+      const double c0 = ((double)lpi[k] - 0.5 * (double)D * (kLog2Pi + l)) * kLog2e - ish * msq;
+      w = f32x4{(float)c0, (float)ish, (float)(2.0 * ish), (float)msq};
+    }
+    kc[k] = w;
+  }
+}
+
+// Pass 1: grid over 128-row tiles, 4 waves of 32 rows.  X is rounded to bf16 in
+// registers as it is loaded; mu blocks (bf16 operands + constants) stream through an
+// LDS double buffer.  Writes logZ and per-row {logZ2, ||x_b||^2} (fp32).
+template <int DP>
+constexpr size_t bf16_lse_lds_bytes() {
+  return (size_t)2 * (DP / 16) * 64 * sizeof(bf16x8) + (size_t)2 * 32 * sizeof(f32x4);
+}
+
+template <int DP>
+__global__ __launch_bounds__(kThreads) void iso_bf16_lse(const float* __restrict__ X, int64_t ldx,
+                                                         int64_t N, int D,
+                                                         const bf16x8* __restrict__ mu_op,
+                                                         const f32x4* __restrict__ kc, int KB,
+                                                         float* __restrict__ logZ,
+                                                         float2* __restrict__ rowstat) {
+  constexpr int NC = DP / 16;
+  constexpr int BLK = NC * 64;                 // bf16x8 per 32-component block
+  constexpr int LPT = (BLK + kThreads - 1) / kThreads;
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                                // [2][BLK]
+  f32x4* kc_l = reinterpret_cast<f32x4*>(lds_raw + 2 * BLK * sizeof(bf16x8));      // [2][32]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t row = ((int64_t)blockIdx.x * kWaves + wave) * 32 + c;
+  const bool valid = row < N;
+
+  bf16x8 st[LPT];
+  f32x4 kst = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto fetch = [&](int kb) {
+    const bf16x8* src = mu_op + (int64_t)kb * BLK;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q)
+      if (BLK % kThreads == 0 || q * kThreads + tid < BLK) st[q] = src[q * kThreads + tid];
+    if (tid < 32) kst = kc[(int64_t)kb * 32 + tid];
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < LPT; ++q)
+      if (BLK % kThreads == 0 || q * kThreads + tid < BLK) mu_l[buf * BLK + q * kThreads + tid] = st[q];
+    if (tid < 32) kc_l[buf * 32 + tid] = kst;
+  };
+  fetch(0);
+
+  // This lane's operand chunks: row `row`, dimensions 16q + 8g .. +7, rounded to bf16.
+  bf16x8 xb[NC];
+  float xsq = 0.0f;
+#pragma unroll
+  for (int q = 0; q < NC; ++q) {
+    const int d0 = 16 * q + 8 * g;
+    xb[q] = to_bf16x8(load_row4(X, ldx, row, d0, D, valid), load_row4(X, ldx, row, d0 + 4, D, valid));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = (float)xb[q][e];
+      xsq = fmaf(v, v, xsq);
+    }
+  }
+  xsq += __shfl_xor(xsq, 32);
+  commit(0);
+  lds_barrier();
+
+  float mx = -INFINITY, sm = 0.0f;
+  for (int kb = 0; kb < KB; ++kb) {
+    const int buf = kb & 1;
+    const bool more = kb + 1 < KB;
+    if (more) fetch(kb + 1);
+    const bf16x8* mp = mu_l + buf * BLK + lane;
+    // S^T = mu . X^T: lane = row, register i = component acc_row(i, g).  Above D = 128
+    // the two halves of D run as separate chains added at the end, the order pass 2
+    // uses, so both passes form bitwise the same log-joint.
+    f32x16 acc = zero16();
+    if constexpr (bf16_halves(DP) == 2) {
+      f32x16 acc1 = zero16();
+#pragma unroll
+      for (int q = 0; q < NC / 2; ++q) {
+        acc = mfma_bf16(mp[q * 64], xb[q], acc);
+        acc1 = mfma_bf16(mp[(q + NC / 2) * 64], xb[q + NC / 2], acc1);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] += acc1[i];
+    } else {
+#pragma unroll
+      for (int q = 0; q < NC; ++q) acc = mfma_bf16(mp[q * 64], xb[q], acc);
+    }
+    const f32x4* kp = kc_l + buf * 32;
+    float ll[16];
+    float bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const f32x4 w = kp[acc_row(i, g)];
+      ll[i] = fmaf(w.z, acc[i], fmaf(-w.y, xsq, w.x));
+      bm = fmaxf(bm, ll[i]);
+    }
+    const float mn = fmaxf(mx, bm);
+    const float ms = (mn == -INFINITY) ? 0.0f : mn;
+    float a = sm * fast_exp2(mx - ms);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) a += fast_exp2(ll[i] - ms);
+    sm = a;
+    mx = mn;
+    if (more) commit(buf ^ 1);
+    lds_barrier();
+  }
+  const float mo = __shfl_xor(mx, 32);
+  const float so = __shfl_xor(sm, 32);
+  const float mn = fmaxf(mx, mo);
+  const float ms = (mn == -INFINITY) ? 0.0f : mn;
+  const float lz2 = mn + log2f(sm * fast_exp2(mx - ms) + so * fast_exp2(mo - ms));
+  if (valid && g == 0) {
+    rowstat[row] = make_float2(lz2, xsq);
+    if (logZ) logZ[row] = lz2 * (float)kLn2;
+  }
+}
+
+// Pass 2: grid over (row slab x group of CB component blocks); 8 waves = CB blocks x
+// NH halves of the dimensions x 8/(CB NH) row groups.  With NH = 2 each wave forms the
+// partial S over its half, the halves meet in LDS and are added in a fixed order (both
+// waves then hold the same r), and each accumulates r^T X for its half of the columns.  X super-tiles are rounded to bf16 once per workgroup and held in
+// LDS in two layouts: row-major (the A operand of the recomputed S = X mu^T) and
+// row-octet interleaved, element (r, d) at ((r / 8) DP + d) 8 + r % 8 (the B operand
+// of r^T X: 8 consecutive rows of one column are 16 contiguous bytes).  r leaves S in
+// the accumulator layout (lane = component, register = row 8q + 4g + j); one
+// v_permlane32_swap per register pair gives each half-wave 8 consecutive rows, the
+// A-operand layout of r^T X, with no trip through LDS.
+__host__ __device__ constexpr int bf16_xr_stride(int DP) { return DP + 8; }   // bf16 per X row
+__host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB) {
+  return (size_t)2 * ((size_t)(256 / (CB * bf16_halves(DP))) * (bf16_xr_stride(DP) + DP)) * 2 +
+         (size_t)2 * (256 / (CB * bf16_halves(DP))) * sizeof(float2) +
+         (bf16_halves(DP) > 1 ? (size_t)kAccWaves * 16 * 64 * sizeof(float) : 0);
+}
+__host__ inline int bf16_blocks_per_group(int DP, int KB) {
+  if (KB <= 1 && bf16_accum_lds_bytes(DP, 1) <= kMaxLds) return 1;
+  if (KB <= 2 && bf16_accum_lds_bytes(DP, 2) <= kMaxLds) return 2;
+  return 4;
+}
+
+template <int DP, int CB, int NH = bf16_halves(DP)>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
+void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                    const bf16x8* __restrict__ mu_op, const f32x4* __restrict__ kc, int KB, int KP,
+                    const float2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
+                    float* __restrict__ part_mu, float* __restrict__ part_nk,
+                    float* __restrict__ part_sig, int dense) {
+  constexpr int NC = DP / 16 / NH;             // 16-dimension chunks of the contraction per wave
+  constexpr int NJ = DP / 32 / NH;             // 32-column tiles of r^T X per wave
+  constexpr int RG = kAccWaves / (CB * NH);    // row groups (32 rows each)
+  constexpr int TR = 32 * RG;                  // rows per super-tile
+  constexpr int XR = bf16_xr_stride(DP);
+  constexpr int V4 = DP / 4;
+  constexpr int NV = TR * V4;                  // float4 per super-tile
+  constexpr int LPT = (NV + kAccThreads - 1) / kAccThreads;
+  static_assert(kAccWaves % (CB * NH) == 0 && NV % kAccThreads == 0 && (DP / 32) % NH == 0,
+                "even split");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  __bf16* xr = reinterpret_cast<__bf16*>(lds_raw);                        // [2][TR][XR]
+  __bf16* xi = xr + 2 * TR * XR;                                           // [2][TR/8][DP][8]
+  float2* rs = reinterpret_cast<float2*>(xi + 2 * TR * DP);                // [2][TR]
+  float* ex = reinterpret_cast<float*>(rs + 2 * TR);                       // [8][16][64] (NH = 2)
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int cbw = wave % CB, h = (wave / CB) % NH, rg = wave / (CB * NH);
+  const int d0 = h * (DP / NH);                // first dimension of this wave's half
+  const int slab = blockIdx.x % nslab;
+  const int cg = blockIdx.x / nslab;
+  const int kb = cg * CB + cbw;
+  const bool active = kb < KB;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
+
+  // B operand of the recompute (lane = component, dimensions 16q + 8g + e) and the
+  // component's constants.
+  bf16x8 mub[NC];
+  f32x4 w = {-INFINITY, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int q = 0; q < NC; ++q) {
+    if (active) {
+      mub[q] = mu_op[((int64_t)kb * (NC * NH) + h * NC + q) * 64 + lane];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mub[q][e] = (__bf16)0.0f;
+    }
+  }
+  if (active) w = kc[(int64_t)kb * 32 + c];
+  const float ish = w.y, ish2 = w.z, musq = w.w, c0 = w.x;
+
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
+  float nk = 0.0f, sig = 0.0f;
+
+  // X super-tiles go global -> registers -> LDS through two register stages: tile t + 2
+  // is loaded while tile t is processed and lands in LDS at the end of iteration t + 1
+  // (the LDS-only barrier leaves the loads in flight).
+  f32x4 stage[LPT], stage2[LPT];
+  float2 rstage = make_float2(INFINITY, 0.0f), rstage2 = rstage;
+  const bool full_d = (D == DP);
+  // float4 idx of a super-tile <-> (row, 4 dimensions) with the row's low 3 bits
+  // fastest: 8 lanes cover one 16-byte column piece of 8 rows, so the interleaved
+  // layout is written in contiguous 16-byte runs.
+  auto tile_row = [](int idx) { return ((idx >> 3) / V4) * 8 + (idx & 7); };
+  auto tile_col = [](int idx) { return ((idx >> 3) % V4) * 4; };
+  auto fetch = [&](int t, f32x4 (&stage)[LPT], float2& rstage) {
+    const int64_t row0 = r_begin + (int64_t)t * TR;
+    if (full_d && row0 + TR <= r_end) {
+      const float* src = X + row0 * ldx;
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)tile_row(idx) * ldx + tile_col(idx));
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        const int64_t row = row0 + tile_row(idx);
+        stage[q] = load_row4(X, ldx, row, tile_col(idx), D, row < r_end);
+      }
+    }
+    if (tid < TR) {
+      const int64_t row = row0 + tid;
+      // Rows past the slab get logZ2 = +inf, hence r = 0.
+      rstage = (row < r_end) ? rowstat[row] : make_float2(INFINITY, 0.0f);
+    }
+  };
+  auto commit = [&](int buf, const f32x4 (&stage)[LPT], float2 rstage) {
+    __bf16* dr = xr + buf * TR * XR;
+    __bf16* di = xi + buf * TR * DP;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      const int r = tile_row(idx), d = tile_col(idx);
+      const f32x4 v = stage[q];
+      typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+      const bf16x4 b = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+      *reinterpret_cast<bf16x4*>(dr + r * XR + d) = b;
+      __bf16* o = di + ((r >> 3) * DP + d) * 8 + (r & 7);
+      o[0] = b[0]; o[8] = b[1]; o[16] = b[2]; o[24] = b[3];
+    }
+    if (tid < TR) rs[buf * TR + tid] = rstage;
+  };
+
+  if (ntiles > 0) {
+    fetch(0, stage, rstage);
+    commit(0, stage, rstage);
+  }
+  if (ntiles > 1) fetch(1, stage, rstage);
+  lds_barrier();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    if (t + 2 < ntiles) fetch(t + 2, stage2, rstage2);
+    f32x16 s = zero16();
+    if (active) {
+      const __bf16* xrow = xr + buf * TR * XR + (rg * 32 + c) * XR + d0 + 8 * g;
+      // S = X mu^T for the wave's 32 rows: lane = component, register i = row acc_row(i, g).
+#pragma unroll
+      for (int q = 0; q < NC; ++q)
+        s = mfma_bf16(*reinterpret_cast<const bf16x8*>(xrow + 16 * q), mub[q], s);
+    }
+    if constexpr (NH == 2) {
+      // Add the two halves' partial S in a fixed order (half 0 + half 1).
+      float* mine = ex + wave * 16 * 64 + lane;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mine[i * 64] = s[i];
+      lds_barrier();
+      const float* s0 = ex + (rg * CB * NH + cbw) * 16 * 64 + lane;
+      const float* s1 = s0 + CB * 16 * 64;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i] = s0[i * 64] + s1[i * 64];
+    }
+    if (active) {
+      const float2* rt = rs + buf * TR + rg * 32;
+      float r[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float2 z = rt[acc_row(i, g)];                 // {logZ2, ||x_b||^2}
+        const float ll = fmaf(ish2, s[i], fmaf(-ish, z.y, c0));
+        const float rv = fast_exp2(ll - z.x);
+        if (h == 0) {
+          nk += rv;
+          sig = fmaf(rv, fmaf(-2.0f, s[i], z.y + musq), sig);
+        }
+        r[i] = rv;
+      }
+      // Registers 4p'+j hold rows 8p' + 4g + j.  Swap across the half-waves so that
+      // lane-half g holds rows 16p + 8g + e (e = j from the first register of the
+      // pair, e = 4 + j from the second) for p = 0, 1.
+      bf16x8 a[2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(r[8 * p + j]),
+                                                           __float_as_uint(r[8 * p + 4 + j]), false, false);
+          a[p][j] = (__bf16)__uint_as_float(sw[0]);
+          a[p][4 + j] = (__bf16)__uint_as_float(sw[1]);
+        }
+      }
+      // B operand: rows rg*32 + 16p + 8g + e of column d0 + 32j + c.
+      const __bf16* xcol = xi + buf * TR * DP + ((rg * 4 + g) * DP + d0 + c) * 8;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const uint4 bits = *reinterpret_cast<const uint4*>(&a[p]);
+        const bool nz = (bits.x | bits.y | bits.z | bits.w) != 0u;
+        // A step whose 16 rows x 32 components of bf16(r) are all zero adds nothing.
+        if (dense || __builtin_amdgcn_ballot_w64(nz) != 0) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+            acc[j] = mfma_bf16(a[p], *reinterpret_cast<const bf16x8*>(xcol + (2 * p * DP + 32 * j) * 8), acc[j]);
+        }
+      }
+    }
+    if (more) commit(buf ^ 1, stage, rstage);
+    lds_barrier();
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) stage[q] = stage2[q];
+    rstage = rstage2;
+  }
+
+  if (active) {
+    nk += __shfl_xor(nk, 32);
+    sig += __shfl_xor(sig, 32);
+    const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        part_mu[(kbase + acc_row(i, g)) * DP + d0 + 32 * j + c] = acc[j][i];
+    }
+    if (g == 0 && h == 0) {
+      part_nk[kbase + c] = nk;
+      part_sig[kbase + c] = sig;
+    }
+  }
+}
+
+template <int DP>
+hipError_t launch_bf16(const IsoPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
+                       float* logZ, bool run1, bool run2, bool dense, hipStream_t stream) {
+  const bf16x8* mu_op = reinterpret_cast<const bf16x8*>(ws + pl.off_musw);
+  const f32x4* kc = reinterpret_cast<const f32x4*>(ws + pl.off_kcblk);
+  float2* rowstat = reinterpret_cast<float2*>(ws + pl.off_rowstat);
+  if (run1) {
+    constexpr size_t lds1 = bf16_lse_lds_bytes<DP>();
+    hipLaunchKernelGGL(iso_bf16_lse<DP>, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
+                       stream, X, ldx, pl.N, (int)pl.D, mu_op, kc, pl.KB, logZ, rowstat);
+  }
+  if (!run2) return hipGetLastError();
+  auto launch = [&](auto cb_tag) -> hipError_t {
+    constexpr int CB = decltype(cb_tag)::value;
+    constexpr size_t lds = bf16_accum_lds_bytes(DP, CB);
+    if constexpr (lds > kMaxLds) {
+      return hipErrorInvalidValue;   // never chosen by the plan
+    } else {
+      if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_bf16_accum<DP, CB>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+      }
+      hipLaunchKernelGGL((iso_bf16_accum<DP, CB>), dim3((unsigned)(pl.nslab * pl.ncg)), dim3(kAccThreads),
+                         lds, stream, X, ldx, pl.N, (int)pl.D, mu_op, kc, pl.KB, pl.KP, rowstat,
+                         pl.nslab, pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_mu),
+                         reinterpret_cast<float*>(ws + pl.off_part_nk),
+                         reinterpret_cast<float*>(ws + pl.off_part_sig), dense ? 1 : 0);
+      return hipGetLastError();
+    }
+  };
+  return pl.cpg == 1   ? launch(std::integral_constant<int, 1>{})
+         : pl.cpg == 2 ? launch(std::integral_constant<int, 2>{})
+                       : launch(std::integral_constant<int, 4>{});
+}
+
 }  // namespace
 }  // namespace fgmm
 
@@ -1215,7 +1672,7 @@ extern "C" size_t fgmm_iso_workspace_bytes(int64_t N, int64_t K, int64_t D) {
 
 extern "C" size_t fgmm_iso_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE)).total;
+  return make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE), (flags & FGMM_FLAG_BF16) != 0).total;
 }
 
 extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -1238,7 +1695,8 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
     return FGMM_ERR_INVALID_ARG;
   if (D > 256) return FGMM_ERR_UNSUPPORTED;
   if (N > kMaxRows || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
-  const IsoPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE));
+  const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
+  const IsoPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE), bf16);
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;
   unsigned char* ws = static_cast<unsigned char*>(workspace);
@@ -1253,20 +1711,29 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
     return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
   }
 
-  if (run1)
+  if (run1 && bf16)
+    hipLaunchKernelGGL(iso_bf16_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, K, (int)D, pl.DP,
+                       log_sigma_sq, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_musw),
+                       reinterpret_cast<f32x4*>(ws + pl.off_kcblk));
+  else if (run1)
     hipLaunchKernelGGL(iso_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, K, (int)D, pl.DP,
                        log_sigma_sq, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_musw),
                        reinterpret_cast<double2*>(ws + pl.off_kcblk),
                        reinterpret_cast<double4*>(ws + pl.off_kclin));
   if (N > 0) {
+    auto run = [&](auto dp_tag) -> hipError_t {
+      constexpr int DP = decltype(dp_tag)::value;
+      return bf16 ? launch_bf16<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream)
+                  : launch_passes<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
+    };
     hipError_t e = hipSuccess;
     switch (pl.DP) {
-      case 32: e = launch_passes<32>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 96: e = launch_passes<96>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 128: e = launch_passes<128>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 192: e = launch_passes<192>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 256: e = launch_passes<256>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 32: e = run(std::integral_constant<int, 32>{}); break;
+      case 64: e = run(std::integral_constant<int, 64>{}); break;
+      case 96: e = run(std::integral_constant<int, 96>{}); break;
+      case 128: e = run(std::integral_constant<int, 128>{}); break;
+      case 192: e = run(std::integral_constant<int, 192>{}); break;
+      case 256: e = run(std::integral_constant<int, 256>{}); break;
       default: return FGMM_ERR_UNSUPPORTED;
     }
     if (e != hipSuccess) return FGMM_ERR_HIP;

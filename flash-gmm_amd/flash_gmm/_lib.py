@@ -29,6 +29,7 @@ FLAG_PHASE1 = 1 << 3
 FLAG_PHASE2 = 1 << 4
 FLAG_DENSE = 1 << 5
 FLAG_RECOMPUTE = 1 << 6
+FLAG_BF16 = 1 << 7
 
 
 class FlashGMMError(AssertionError, ValueError):

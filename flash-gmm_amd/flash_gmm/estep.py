@@ -125,7 +125,8 @@ def _rowmajor(t: torch.Tensor) -> torch.Tensor:
 def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
                    accumulate: bool = False, atomic_reduce: bool = False,
                    workspace: torch.Tensor | None = None, phase: int = 0,
-                   dense: bool = False, recompute: bool = False) -> None:
+                   dense: bool = False, recompute: bool = False,
+                   precision: str = "fp32") -> None:
     """Isotropic E-step writing into caller-provided outputs.
 
     ``logZ`` may be None (it is then not written).  With ``accumulate`` the
@@ -137,8 +138,12 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     (same results; for timing).  ``recompute`` makes the accumulation pass
     recompute the log-joint instead of reading the copy that the first pass
     stores in the workspace (smaller workspace; phase-split calls must agree).
+    ``precision="bf16"`` selects the bf16 operand contract of the reference's H100
+    kernels (flash_gmm_h100.py:247-328): X and mu rounded to bfloat16 for the
+    contractions, fp32 accumulation and log-sum-exp.
     """
     _check_common(X, mu, log_pi)
+    _require(precision in ("fp32", "bf16"), f"precision must be 'fp32' or 'bf16', got {precision!r}")
     N, D = X.shape
     K = mu.shape[0]
     dev = X.device
@@ -153,6 +158,8 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
         flags |= _lib.FLAG_DENSE
     if recompute:
         flags |= _lib.FLAG_RECOMPUTE
+    if precision == "bf16":
+        flags |= _lib.FLAG_BF16
     workspace = _workspace(L.fgmm_iso_workspace_bytes_ex, N, K, D, flags, dev, workspace)
     _check_out("Nk", Nk, (K,), dev)
     _check_out("mu_acc", mu_acc, (K, D), dev)
@@ -170,12 +177,14 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
 
 def flash_gmm_estep(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tensor,
                     log_pi: torch.Tensor, BLOCK_N: int = 64, BLOCK_K: int = 16,
-                    BLOCK_D: int = 128):
+                    BLOCK_D: int = 128, *, precision: str = "fp32"):
     """Flash-GMM isotropic E-step: returns (logZ, Nk, mu_acc, sig_acc).
 
     logZ (N,) per-sample log-normaliser, Nk (K,) = sum_n r_nk,
     mu_acc (K, D) = sum_n r_nk x_n, sig_acc (K,) = sum_n r_nk ||x_n - mu_k||^2
     (flash_gmm.py:22-37).  BLOCK_N / BLOCK_K / BLOCK_D are ignored.
+    ``precision="bf16"`` follows the bf16 operand contract of the H100 variant
+    (flash_gmm_h100.py:247-328) instead of fp32 arithmetic.
     """
     _check_common(X, mu, log_pi)
     N, D = X.shape
@@ -185,7 +194,7 @@ def flash_gmm_estep(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tenso
     Nk = torch.empty(K, device=dev, dtype=torch.float32)
     mu_acc = torch.empty(K, D, device=dev, dtype=torch.float32)
     sig_acc = torch.empty(K, device=dev, dtype=torch.float32)
-    iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc)
+    iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, precision=precision)
     return logZ, Nk, mu_acc, sig_acc
 
 

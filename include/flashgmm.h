@@ -70,6 +70,13 @@ enum fgmm_flags {
      * RECOMPUTE keeps the workspace O(N + K*D) and recomputes.  Calls that
      * split the phases must agree on this flag. */
     FGMM_FLAG_RECOMPUTE = 1u << 6,
+    /* Isotropic E-step only: the bf16 operand contract of the reference's H100
+     * kernels (flash_gmm_h100.py:247-328).  X and mu are rounded to bfloat16 for
+     * x.mu and r^T X (r rounded to bfloat16 there) with fp32 accumulation; the
+     * constants come from the fp32 mu and the log-sum-exp is fp32.  The reference
+     * states a 5e-3 tolerance against fp32 for this contract.  The diagonal and
+     * full entry points return FGMM_ERR_UNSUPPORTED for it. */
+    FGMM_FLAG_BF16 = 1u << 7,
 };
 
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */

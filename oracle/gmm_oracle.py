@@ -21,6 +21,10 @@ Parity pinning (what checks each function, see tests/test_oracle.py):
 * ``estep_diag`` -- scipy logpdf with a diagonal covariance, sklearn 'diag'
   internals, brute force, invariants, reduction to ``estep_iso`` when every
   per-dimension variance of a component is equal.
+* ``estep_iso_bf16`` -- the bf16 operand contract of the reference's H100 kernels:
+  equal to ``estep_iso`` (logZ, Nk, sig_acc) on inputs that are exact in bfloat16
+  and within the bf16 rounding of r for mu_acc; an independent scalar-loop
+  version with bit-level rounding on tiny inputs.
 * ``estep_full`` -- scipy logpdf with the full covariance recovered from the
   precision Cholesky factor, sklearn 'full' internals, brute force, reduction
   to ``estep_diag`` for diagonal factors.
@@ -99,6 +103,53 @@ def estep_iso(X: Tensor, mu: Tensor, log_sigma_sq: Tensor, log_pi: Tensor, *,
         Nk += r.sum(dim=0)                              # flash_gmm.py:155
         sig_acc += (r * sq).sum(dim=0)                  # flash_gmm.py:156
         mu_acc += r.T @ x                               # flash_gmm.py:161
+    return logZ, Nk, mu_acc, sig_acc
+
+
+LOG2_E = 1.4426950408889634  # flash_gmm_h100.py:247
+
+
+def bf16_round(t: Tensor) -> Tensor:
+    """Round float32 values to bfloat16 (nearest, ties to even), returned as float64."""
+    return t.to(torch.float32).to(torch.bfloat16).to(torch.float64)
+
+
+def estep_iso_bf16(X: Tensor, mu: Tensor, log_sigma_sq: Tensor, log_pi: Tensor, *,
+                   chunk: int = _DEFAULT_CHUNK) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Isotropic E-step with the bf16 operand contract of flash_gmm_h100.py:247-328.
+
+    X and mu are rounded to bfloat16 for both contractions (:277-284); x_sq is the
+    sum of squares of the rounded x (:105-107); mu_sq, ish and c0 come from the
+    float32 mu (:286-292); ll2 = c0 - ish x_sq + 2 ish x.mu in log2 units
+    (:137-138); r = 2^(ll2 - logZ2); Nk = sum r, sig_acc = sum r (x_sq - 2 x.mu +
+    mu_sq) (:210-224); mu_acc = bf16(r)^T x (:230-231); logZ = logZ2 ln 2 (:326).
+    Everything except those roundings is float64 here (the reference accumulates
+    in float32).
+    """
+    X32, mu32 = _as(X, torch.float32), _as(mu, torch.float32)
+    Xb, mub = bf16_round(X32), bf16_round(mu32)
+    lss, lpi = _as(log_sigma_sq, torch.float64), _as(log_pi, torch.float64)
+    N, D = X32.shape
+    K = mu32.shape[0]
+    mu_sq = (mu32.double() ** 2).sum(dim=1)
+    ish = 0.5 * torch.exp(-lss) * LOG2_E
+    c0 = (lpi - 0.5 * D * (LOG_2PI + lss)) * LOG2_E - ish * mu_sq
+    logZ = torch.empty(N, dtype=torch.float64)
+    Nk = torch.zeros(K, dtype=torch.float64)
+    mu_acc = torch.zeros(K, D, dtype=torch.float64)
+    sig_acc = torch.zeros(K, dtype=torch.float64)
+    ln2 = math.log(2.0)
+    for n0 in range(0, N, chunk):
+        xb = Xb[n0:n0 + chunk]
+        x_sq = (xb * xb).sum(dim=1)
+        xmu = xb @ mub.T
+        ll2 = c0[None, :] - ish[None, :] * x_sq[:, None] + (2.0 * ish[None, :]) * xmu
+        lz2 = torch.logsumexp(ll2 * ln2, dim=1) / ln2
+        logZ[n0:n0 + chunk] = lz2 * ln2
+        r = torch.exp2(ll2 - lz2[:, None])
+        Nk += r.sum(dim=0)
+        sig_acc += (r * (x_sq[:, None] - 2.0 * xmu + mu_sq[None, :])).sum(dim=0)
+        mu_acc += bf16_round(r).T @ xb
     return logZ, Nk, mu_acc, sig_acc
 
 
@@ -242,6 +293,50 @@ def mstep_full(Nk: Tensor, mu_acc: Tensor, sig_outer: Tensor, N: int):
 # ---------------------------------------------------------------------------
 # Brute force (pure Python loops, tiny inputs only)
 # ---------------------------------------------------------------------------
+
+def _bf16_scalar(v: float) -> float:
+    """Round one float to bfloat16 by bit manipulation: nearest, ties to even."""
+    import struct
+    b = struct.unpack("<I", struct.pack("<f", v))[0]
+    lsb = (b >> 16) & 1
+    b = (b + 0x7FFF + lsb) & 0xFFFF0000
+    return struct.unpack("<f", struct.pack("<I", b))[0]
+
+
+def brute_estep_iso_bf16(X, mu, lss, lpi):
+    """Scalar-loop version of estep_iso_bf16 for tiny inputs (bit-level bf16 rounding)."""
+    X = [[float(v) for v in row] for row in X.tolist()]
+    mu = [[float(v) for v in row] for row in mu.tolist()]
+    lss = [float(v) for v in lss.tolist()]
+    lpi = [float(v) for v in lpi.tolist()]
+    N, D, K = len(X), len(X[0]) if X else 0, len(mu)
+    xb = [[_bf16_scalar(v) for v in row] for row in X]
+    mb = [[_bf16_scalar(v) for v in row] for row in mu]
+    logZ, Nk = [], [0.0] * K
+    mu_acc = [[0.0] * D for _ in range(K)]
+    sig_acc = [0.0] * K
+    for n in range(N):
+        x_sq = sum(v * v for v in xb[n])
+        ll2, sq = [], []
+        for k in range(K):
+            ish = 0.5 * math.exp(-lss[k]) / math.log(2.0)
+            mu_sq = sum(v * v for v in mu[k])
+            xmu = sum(xb[n][d] * mb[k][d] for d in range(D))
+            c0 = (lpi[k] - 0.5 * D * (LOG_2PI + lss[k])) / math.log(2.0) - ish * mu_sq
+            ll2.append(c0 - ish * x_sq + 2.0 * ish * xmu)
+            sq.append(x_sq - 2.0 * xmu + mu_sq)
+        m = max(ll2)
+        lz2 = m + math.log2(sum(2.0 ** (v - m) for v in ll2))
+        logZ.append(lz2 * math.log(2.0))
+        for k in range(K):
+            r = 2.0 ** (ll2[k] - lz2)
+            Nk[k] += r
+            sig_acc[k] += r * sq[k]
+            rb = _bf16_scalar(r)
+            for d in range(D):
+                mu_acc[k][d] += rb * xb[n][d]
+    return logZ, Nk, mu_acc, sig_acc
+
 
 def brute_estep_iso(X, mu, lss, lpi):
     """Scalar-loop float64 E-step, for N, K, D <= ~16 (direct distances)."""

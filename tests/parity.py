@@ -11,20 +11,26 @@ import numpy as np
 
 LOGZ_ATOL = 1e-4
 REL = 1e-4
+# The bf16 operand contract (precision="bf16") against its own oracle
+# (gmm_oracle.estep_iso_bf16): the roundings to bf16 are replayed exactly, so only
+# fp32 arithmetic on the log-joint's large terms (c0, ish ||x||^2, 2 ish x.mu, each
+# ~ ||x||^2) remains; logZ is checked at 2e-3 (the contract itself is ~1 away from
+# the fp64 result on clustered data), the statistics at REL.
+LOGZ_ATOL_BF16 = 2e-3
 
 
 def _np(t):
     return t.detach().double().cpu().numpy()
 
 
-def assert_close_stats(got, ref, what=""):
+def assert_close_stats(got, ref, what="", logz_atol=LOGZ_ATOL):
     lz, nk, mu_acc, sig = (_np(t) for t in got)
     rlz, rnk, rmu, rsig = (np.asarray(t, dtype=np.float64) for t in ref)
     if rlz.size:
         err = np.abs(lz - rlz)
         finite = np.isfinite(rlz)
         assert np.array_equal(np.isfinite(lz), finite), f"{what} logZ finiteness"
-        assert err[finite].max(initial=0) <= LOGZ_ATOL, f"{what} logZ max abs err {err[finite].max()}"
+        assert err[finite].max(initial=0) <= logz_atol, f"{what} logZ max abs err {err[finite].max()}"
     for name, g, r in (("Nk", nk, rnk), ("sig", sig, rsig)):
         if r.size:
             tol = REL * np.abs(r) + 1e-6 * np.abs(r).max(initial=0)

@@ -163,6 +163,44 @@ def test_iso_fp32_restatement_close_to_fp64():
     np.testing.assert_allclose(b[1].double().numpy(), a[1].numpy(), rtol=1e-4)
 
 
+# --------------------------------------------------------------------------- iso, bf16 contract
+
+def test_iso_bf16_equals_fp64_on_bf16_exact_inputs():
+    """With X and mu already exact in bfloat16, the bf16 contract changes only mu_acc
+    (r is rounded to bf16 for r^T x): logZ, Nk and sig_acc equal the float64 E-step."""
+    X, mu, lss, lpi = _iso_inputs(N=300, K=6, D=10, seed=21)
+    X = O.bf16_round(X.float())
+    mu = O.bf16_round(mu.float())
+    ref = O.estep_iso(X, mu, lss, lpi)
+    got = O.estep_iso_bf16(X, mu, lss, lpi)
+    np.testing.assert_allclose(got[0].numpy(), ref[0].numpy(), atol=1e-11)
+    np.testing.assert_allclose(got[1].numpy(), ref[1].numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(got[3].numpy(), ref[3].numpy(), rtol=1e-9, atol=1e-10)
+    err = (got[2] - ref[2]).abs().max() / ref[2].abs().max()
+    assert 1e-6 < err < 2.0 ** -8          # bf16(r) rounding is visible, and bounded
+
+
+def test_iso_bf16_brute_force_tiny():
+    """Against a scalar loop that rounds to bfloat16 by bit manipulation."""
+    X, mu, lss, lpi = _iso_inputs(N=9, K=3, D=5, seed=22)
+    X, mu = X.float(), mu.float()
+    lz_b, nk_b, mu_b, sig_b = O.brute_estep_iso_bf16(X, mu, lss, lpi)
+    logZ, Nk, mu_acc, sig_acc = O.estep_iso_bf16(X, mu, lss, lpi)
+    np.testing.assert_allclose(logZ.numpy(), lz_b, atol=1e-11)
+    np.testing.assert_allclose(Nk.numpy(), nk_b, rtol=1e-11)
+    np.testing.assert_allclose(mu_acc.numpy(), np.array(mu_b), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(sig_acc.numpy(), sig_b, rtol=1e-10)
+
+
+def test_bf16_scalar_rounding_ties_to_even():
+    """The brute-force rounding itself: ties go to the even bfloat16 neighbour."""
+    one_ulp = 2.0 ** -7                      # bf16 spacing at 1.0
+    assert O._bf16_scalar(1.0 + one_ulp / 2) == 1.0                    # tie, even below
+    assert O._bf16_scalar(1.0 + 1.5 * one_ulp) == 1.0 + 2 * one_ulp   # tie, even above
+    assert O._bf16_scalar(1.0 + 0.6 * one_ulp) == 1.0 + one_ulp
+    assert O._bf16_scalar(-3.0) == -3.0
+
+
 # --------------------------------------------------------------------------- diag
 
 def test_diag_logz_matches_scipy_and_sklearn():
