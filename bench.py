@@ -25,6 +25,7 @@ for _p in (os.path.join(ROOT, "flash-gmm_amd"), ROOT):
 
 METRIC = "E-step samples/sec @K=1024,D=128 fp32 + % of fp32 MFMA peak (1 GPU)"
 PEAK_FP32_MFMA_TFLOPS = 157.3       # MI355X dense fp32 matrix, published
+PEAK_BF16_MFMA_TFLOPS = 2500.0      # MI355X dense bf16 matrix, published
 PEAK_HBM_GBS = 8000.0
 A100_SAMPLES_PER_S = 1_000_000 / 0.152   # README.md:116 (A100 80GB, N=1M, 152 ms)
 
@@ -215,6 +216,9 @@ def main():
     ap.add_argument("--workload", default="iso_n1m_k1024_d128",
                     choices=sorted(WORKLOADS) + ["stream_em_n1b_k1024_d128"])
     ap.add_argument("--rows", type=int, default=0, help="override N of the streaming workload")
+    ap.add_argument("--precision", choices=["fp32", "bf16"], default="fp32",
+                    help="isotropic workload only: bf16 runs the H100 variant's bf16 operand "
+                         "contract (FGMM_FLAG_BF16) and is rated against the bf16 matrix peak")
     ap.add_argument("--recompute", action="store_true",
                     help="pass 2 recomputes the log-joint (FGMM_FLAG_RECOMPUTE) instead of reading "
                          "the copy pass 1 stores")
@@ -248,6 +252,11 @@ def main():
     dev = torch.device("cuda:0")
     N, K, D = WORKLOADS[args.workload]
     kind = args.workload.split("_")[0]
+    bf16 = args.precision == "bf16"
+    if bf16 and kind != "iso":
+        print("--precision bf16 applies to the isotropic workloads only", file=sys.stderr)
+        sys.exit(2)
+    peak = PEAK_BF16_MFMA_TFLOPS if bf16 else PEAK_FP32_MFMA_TFLOPS
     log(f"generating workload {args.workload} on {torch.cuda.get_device_name(dev)}")
     inp = data.make(args.workload, device=dev)
     L = _lib.lib()
@@ -259,7 +268,8 @@ def main():
         sig = torch.empty(K, device=dev)
         fn = lambda ph, dense=args.dense: iso_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
                                                          phase=ph, atomic_reduce=args.atomic_reduce,
-                                                         dense=dense, recompute=args.recompute)
+                                                         dense=dense, recompute=args.recompute,
+                                                         precision=args.precision)
     elif kind == "diag":
         args4 = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
         sig = torch.empty(K, D, device=dev)
@@ -271,10 +281,12 @@ def main():
         fn = lambda ph, dense=args.dense: full_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
                                                           phase=ph, dense=dense, recompute=args.recompute)
     ws_fn = getattr(L, f"fgmm_{kind}_workspace_bytes_ex")
-    flags = _lib.FLAG_RECOMPUTE if args.recompute else 0
+    pflag = _lib.FLAG_BF16 if bf16 else 0
+    flags = (_lib.FLAG_RECOMPUTE if args.recompute else 0) | pflag
     ws = torch.empty(int(ws_fn(N, K, D, flags)), dtype=torch.uint8, device=dev)
     # Pass 2 reads the log-joint that pass 1 stores whenever the plan sizes it in.
-    stored_lj = int(ws_fn(N, K, D, 0)) != int(ws_fn(N, K, D, _lib.FLAG_RECOMPUTE)) and not args.recompute
+    stored_lj = (int(ws_fn(N, K, D, pflag)) != int(ws_fn(N, K, D, pflag | _lib.FLAG_RECOMPUTE))
+                 and not args.recompute)
     stream = torch.cuda.current_stream(dev)
 
     def step(ev=None):
@@ -334,7 +346,10 @@ def main():
              + (", stores the log-joint)" if stored_lj else ")"),
              f"{p2_kernel} (accumulation pass + slab reduction"
              + (", reads the stored log-joint)" if stored_lj else ", recomputes the log-joint)"))
-    traffic_tab = {} if args.recompute else TRAFFIC_BYTES.get(args.workload, {})
+    if bf16:
+        names = ("iso_bf16_lse (log-normaliser pass + prologue, bf16 operands)",
+                 "iso_bf16_accum (accumulation pass + slab reduction, recomputes in bf16)")
+    traffic_tab = {} if (args.recompute or bf16) else TRAFFIC_BYTES.get(args.workload, {})
     phases = {}
     for ph, name, t, f, b in (("phase1", names[0], p1, f1, b1), ("phase2", names[1], p2, f2, b2)):
         phases[ph] = {"kernel": name, "ms": t, "algorithmic_flop": f,
@@ -350,16 +365,18 @@ def main():
         roof = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": dom["gbs"] / PEAK_HBM_GBS, "algorithmic_bytes_per_launch": dom["algorithmic_bytes"]}
     else:
-        roof = {"bound": "mfma", "achieved": dom["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
-                "unit": "TFLOP/s", "frac": dom["tflops"] / PEAK_FP32_MFMA_TFLOPS,
+        roof = {"bound": "mfma", "achieved": dom["tflops"], "peak": peak,
+                "unit": "TFLOP/s", "frac": dom["tflops"] / peak,
                 "algorithmic_flop_per_launch": dom["algorithmic_flop"]}
     roof.update({"kernel": dom["kernel"], "traffic": dom["traffic"],
                  "traffic_unit": "bytes per launch (HBM read + write, rocprofv3 counters)",
                  "avg_launch_ms": dom["ms"]})
 
     out = {
-        "metric": METRIC if kind == "iso" else
-                  f"E-step samples/sec ({args.workload}) fp32 + % of fp32 MFMA peak (1 GPU)",
+        "metric": (METRIC if kind == "iso" and not bf16 else
+                   "E-step samples/sec @K=1024,D=128 bf16 operands, fp32 accumulation "
+                   "+ % of bf16 MFMA peak (1 GPU)" if bf16 else
+                   f"E-step samples/sec ({args.workload}) fp32 + % of fp32 MFMA peak (1 GPU)"),
         "value": N / (ms * 1e-3),
         "unit": "samples/s",
         "n_gpus": 1,
@@ -368,17 +385,18 @@ def main():
         "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": (N / (ms * 1e-3)) / A100_SAMPLES_PER_S if kind == "iso" else None,
+        "vs_baseline": (N / (ms * 1e-3)) / A100_SAMPLES_PER_S if kind == "iso" and not bf16 else None,
         "baseline_note": "reference's published A100 80GB figure for this shape: 152 ms at N=1M "
                          "(README.md:116), TF32 dot" if kind == "iso" else
                          "no published reference number for this workload",
-        "dtype": "f32",
+        "dtype": "bf16 operands, f32 accumulation" if bf16 else "f32",
         "data": "synthetic",
         "config": {"workload": args.workload, "N": N, "K": K, "D": D,
                    "generator": f"flash_gmm.data.make({args.workload!r}), generated on device",
                    "reduce": "atomic" if args.atomic_reduce else "deterministic",
                    "log_joint": "stored by phase 1, read by phase 2" if stored_lj else "recomputed by phase 2"},
         "fraction_of_fp32_mfma_peak": step_tflops / PEAK_FP32_MFMA_TFLOPS,
+        "fraction_of_matrix_peak": step_tflops / peak,
         "fraction_basis": "dense-equivalent algorithmic flops per step / step time; phase 2 executes "
                           "only the accumulation steps whose responsibilities are not all zero"
                           + (" and reads the log-joint instead of recomputing it" if stored_lj else "")
@@ -392,9 +410,11 @@ def main():
         "dense_ms_per_step": dense_ms if dense_ms is not None else (ms if args.dense else None),
         "dense_fraction_of_fp32_mfma_peak": (flop / (dense_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS)
                                             if dense_ms is not None else None,
+        "dense_fraction_of_matrix_peak": (flop / (dense_ms * 1e-3) / 1e12 / peak)
+                                         if dense_ms is not None else None,
         "roofline": roof,
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not bf16:
         log("timing the CPU baseline (bounded sample)")
         out["cpu_baseline"] = cpu_baseline({k: v for k, v in inp.items()}, kind, K, D)
     print(json.dumps(out), flush=True)

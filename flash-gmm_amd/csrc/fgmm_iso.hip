@@ -1475,13 +1475,13 @@ void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   f32x16 acc[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) acc[j] = zero16();
-  float nk = 0.0f, sig = 0.0f;
+  // sig = sum r (||x||^2 - 2 x.mu + ||mu||^2) = srx - 2 srs + ||mu||^2 nk, from two running sums.
+  float nk = 0.0f, srx = 0.0f, srs = 0.0f;
 
-  // X super-tiles go global -> registers -> LDS through two register stages: tile t + 2
-  // is loaded while tile t is processed and lands in LDS at the end of iteration t + 1
-  // (the LDS-only barrier leaves the loads in flight).
-  f32x4 stage[LPT], stage2[LPT];
-  float2 rstage = make_float2(INFINITY, 0.0f), rstage2 = rstage;
+  // X super-tiles go global -> registers -> LDS (double-buffered): tile t + 1 is
+  // loaded while tile t is processed.
+  f32x4 stage[LPT];
+  float2 rstage = make_float2(INFINITY, 0.0f);
   const bool full_d = (D == DP);
   // float4 idx of a super-tile <-> (row, 4 dimensions) with the row's low 3 bits
   // fastest: 8 lanes cover one 16-byte column piece of 8 rows, so the interleaved
@@ -1532,13 +1532,12 @@ void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     fetch(0, stage, rstage);
     commit(0, stage, rstage);
   }
-  if (ntiles > 1) fetch(1, stage, rstage);
   lds_barrier();
 
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     const bool more = t + 1 < ntiles;
-    if (t + 2 < ntiles) fetch(t + 2, stage2, rstage2);
+    if (more) fetch(t + 1, stage, rstage);
     f32x16 s = zero16();
     if (active) {
       const __bf16* xrow = xr + buf * TR * XR + (rg * 32 + c) * XR + d0 + 8 * g;
@@ -1568,23 +1567,31 @@ void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
         const float rv = fast_exp2(ll - z.x);
         if (h == 0) {
           nk += rv;
-          sig = fmaf(rv, fmaf(-2.0f, s[i], z.y + musq), sig);
+          srx = fmaf(rv, z.y, srx);
+          srs = fmaf(rv, s[i], srs);
         }
         r[i] = rv;
       }
-      // Registers 4p'+j hold rows 8p' + 4g + j.  Swap across the half-waves so that
-      // lane-half g holds rows 16p + 8g + e (e = j from the first register of the
-      // pair, e = 4 + j from the second) for p = 0, 1.
+      // Registers 4p'+j hold rows 8p' + 4g + j.  Packed to bf16 pairs, one swap across
+      // the half-waves per pair of dwords leaves lane-half g with rows 16p + 8g + e
+      // (e = 0..3 from the first pair, 4..7 from the second) for p = 0, 1.
+      typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+      auto pack = [](float u, float v) {
+        const bf16x2 t = {(__bf16)u, (__bf16)v};
+        return *reinterpret_cast<const unsigned*>(&t);
+      };
       bf16x8 a[2];
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
+        uint4 wv;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(r[8 * p + j]),
-                                                           __float_as_uint(r[8 * p + 4 + j]), false, false);
-          a[p][j] = (__bf16)__uint_as_float(sw[0]);
-          a[p][4 + j] = (__bf16)__uint_as_float(sw[1]);
+        for (int hh = 0; hh < 2; ++hh) {
+          const auto sw = __builtin_amdgcn_permlane32_swap(pack(r[8 * p + 2 * hh], r[8 * p + 2 * hh + 1]),
+                                                           pack(r[8 * p + 4 + 2 * hh], r[8 * p + 5 + 2 * hh]),
+                                                           false, false);
+          if (hh == 0) { wv.x = sw[0]; wv.z = sw[1]; } else { wv.y = sw[0]; wv.w = sw[1]; }
         }
+        a[p] = *reinterpret_cast<const bf16x8*>(&wv);
       }
       // B operand: rows rg*32 + 16p + 8g + e of column d0 + 32j + c.
       const __bf16* xcol = xi + buf * TR * DP + ((rg * 4 + g) * DP + d0 + c) * 8;
@@ -1602,14 +1609,13 @@ void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     }
     if (more) commit(buf ^ 1, stage, rstage);
     lds_barrier();
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) stage[q] = stage2[q];
-    rstage = rstage2;
   }
 
   if (active) {
     nk += __shfl_xor(nk, 32);
-    sig += __shfl_xor(sig, 32);
+    srx += __shfl_xor(srx, 32);
+    srs += __shfl_xor(srs, 32);
+    const float sig = fmaf(musq, nk, fmaf(-2.0f, srs, srx));
     const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
