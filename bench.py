@@ -217,8 +217,8 @@ def main():
                     choices=sorted(WORKLOADS) + ["stream_em_n1b_k1024_d128"])
     ap.add_argument("--rows", type=int, default=0, help="override N of the streaming workload")
     ap.add_argument("--precision", choices=["fp32", "bf16"], default="fp32",
-                    help="isotropic workload only: bf16 runs the H100 variant's bf16 operand "
-                         "contract (FGMM_FLAG_BF16) and is rated against the bf16 matrix peak")
+                    help="isotropic and diagonal workloads: bf16 runs the H100 variants' bf16 "
+                         "operand contract (FGMM_FLAG_BF16) and is rated against the bf16 matrix peak")
     ap.add_argument("--recompute", action="store_true",
                     help="pass 2 recomputes the log-joint (FGMM_FLAG_RECOMPUTE) instead of reading "
                          "the copy pass 1 stores")
@@ -253,8 +253,8 @@ def main():
     N, K, D = WORKLOADS[args.workload]
     kind = args.workload.split("_")[0]
     bf16 = args.precision == "bf16"
-    if bf16 and kind != "iso":
-        print("--precision bf16 applies to the isotropic workloads only", file=sys.stderr)
+    if bf16 and kind not in ("iso", "diag"):
+        print("--precision bf16 applies to the isotropic and diagonal workloads only", file=sys.stderr)
         sys.exit(2)
     peak = PEAK_BF16_MFMA_TFLOPS if bf16 else PEAK_FP32_MFMA_TFLOPS
     log(f"generating workload {args.workload} on {torch.cuda.get_device_name(dev)}")
@@ -274,7 +274,8 @@ def main():
         args4 = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
         sig = torch.empty(K, D, device=dev)
         fn = lambda ph, dense=args.dense: diag_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
-                                                          phase=ph, dense=dense, recompute=args.recompute)
+                                                          phase=ph, dense=dense, recompute=args.recompute,
+                                                          precision=args.precision)
     else:
         args4 = (inp["X"], inp["mu"], inp["prec_chol"], inp["log_pi"])
         sig = torch.empty(K, D, D, device=dev)
@@ -347,8 +348,8 @@ def main():
              f"{p2_kernel} (accumulation pass + slab reduction"
              + (", reads the stored log-joint)" if stored_lj else ", recomputes the log-joint)"))
     if bf16:
-        names = ("iso_bf16_lse (log-normaliser pass + prologue, bf16 operands)",
-                 "iso_bf16_accum (accumulation pass + slab reduction, recomputes in bf16)")
+        names = (f"{kind}_bf16_lse (log-normaliser pass + prologue, bf16 operands)",
+                 f"{kind}_bf16_accum (accumulation pass + slab reduction, recomputes in bf16)")
     traffic_tab = {} if (args.recompute or bf16) else TRAFFIC_BYTES.get(args.workload, {})
     phases = {}
     for ph, name, t, f, b in (("phase1", names[0], p1, f1, b1), ("phase2", names[1], p2, f2, b2)):
@@ -374,7 +375,7 @@ def main():
 
     out = {
         "metric": (METRIC if kind == "iso" and not bf16 else
-                   "E-step samples/sec @K=1024,D=128 bf16 operands, fp32 accumulation "
+                   f"E-step samples/sec ({args.workload}) bf16 operands, fp32 accumulation "
                    "+ % of bf16 MFMA peak (1 GPU)" if bf16 else
                    f"E-step samples/sec ({args.workload}) fp32 + % of fp32 MFMA peak (1 GPU)"),
         "value": N / (ms * 1e-3),

@@ -149,6 +149,58 @@ __device__ __forceinline__ void cross_tile_fast(float (&out)[16], LA loadA, LB l
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// ---------------------------------------------------------------------------
+// bf16 matrix steps (the bf16 operand contracts of the reference's H100 kernels).
+// v_mfma_f32_32x32x16_bf16: C(32x32) += A(32x16) * B(16x32), fp32 accumulation.
+// Lane l holds A[m = l % 32][k = 8 (l / 32) + e] and B[k = 8 (l / 32) + e][n = l % 32]
+// for e = 0..7; C is laid out as for the fp32 step (acc_row).
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Round-to-nearest-even fp32 -> bf16 of 8 values.
+__device__ __forceinline__ bf16x8 to_bf16x8(f32x4 lo, f32x4 hi) {
+  bf16x8 v;
+  v[0] = (__bf16)lo.x; v[1] = (__bf16)lo.y; v[2] = (__bf16)lo.z; v[3] = (__bf16)lo.w;
+  v[4] = (__bf16)hi.x; v[5] = (__bf16)hi.y; v[6] = (__bf16)hi.z; v[7] = (__bf16)hi.w;
+  return v;
+}
+
+// A tile in the accumulator layout (lane = column c, register i = row acc_row(i, g))
+// rounded to bf16 and re-laid as the A operands of two 16-row steps: lane-half g of
+// operand p gets rows 16p + 8g + e, e = 0..7.  Registers 4p'+j hold rows 8p' + 4g + j;
+// packed to bf16 pairs, one swap across the half-waves per pair of dwords moves rows
+// 8p' + 4(1-g) + j to the other half (e = 0..3 from the first pair, 4..7 from the
+// second), with no trip through LDS.
+__device__ __forceinline__ void acc_to_row_operands(const float (&r)[16], bf16x8 (&a)[2]) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  auto pack = [](float u, float v) {
+    const bf16x2 t = {(__bf16)u, (__bf16)v};
+    return *reinterpret_cast<const unsigned*>(&t);
+  };
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    uint4 wv;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(pack(r[8 * p + 2 * hh], r[8 * p + 2 * hh + 1]),
+                                                       pack(r[8 * p + 4 + 2 * hh], r[8 * p + 5 + 2 * hh]),
+                                                       false, false);
+      if (hh == 0) { wv.x = sw[0]; wv.z = sw[1]; } else { wv.y = sw[0]; wv.w = sw[1]; }
+    }
+    a[p] = *reinterpret_cast<const bf16x8*>(&wv);
+  }
+}
+
+// True when any lane's operand holds a nonzero bf16 (wave-uniform).
+__device__ __forceinline__ bool any_nonzero(const bf16x8& a) {
+  const uint4 bits = *reinterpret_cast<const uint4*>(&a);
+  return __builtin_amdgcn_ballot_w64((bits.x | bits.y | bits.z | bits.w) != 0u) != 0;
+}
+
 // Sum of n floats p[0], p[stride], ... in fp64, left to right (a fixed order, so
 // the result is deterministic); eight loads are issued before their adds.
 __device__ __forceinline__ double strided_sum(const float* __restrict__ p, int n, int64_t stride) {

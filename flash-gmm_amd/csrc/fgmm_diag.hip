@@ -62,6 +62,11 @@ __host__ inline int diag_padded_dim(int64_t D) {
   return D <= 128 ? (int)round_up(D < 1 ? 1 : D, 32) : (int)round_up(D, 64);
 }
 
+// bf16 operand contract (defined with its kernels below).
+__host__ __device__ constexpr int bf16_parts(int DP);
+__host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB);
+__host__ inline int bf16_blocks_per_group(int DP, int KB);
+
 struct DiagPlan {
   int64_t N, K, D;
   int DP, FP;   // D padded (32 up to 128, then 64); feature count 2*DP
@@ -69,6 +74,7 @@ struct DiagPlan {
   int cpg;      // component blocks per pass-2 workgroup
   int ncg, nslab, rgroups, npart;
   int64_t rows_per_slab;
+  bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16)
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
   int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
   size_t off_musw, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_sq, off_part_nk, off_lj,
@@ -84,15 +90,19 @@ __host__ inline bool use_stored_lj(int64_t N, int KB, bool allow) {
          (size_t)round_up(cdiv(N, 32), 4) * (size_t)KB * kLjTile * sizeof(float) <= kMaxLjBytes;
 }
 
-DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true) {
+DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf16 = false) {
   DiagPlan p{};
   p.N = N; p.K = K; p.D = D;
   p.DP = diag_padded_dim(D);
   p.FP = 2 * p.DP;
   p.KB = (int)cdiv(K, 32);
   p.KP = p.KB * 32;
-  p.lj = use_stored_lj(N, p.KB, allow_lj);
-  if (p.lj) {
+  p.bf16 = bf16;
+  p.lj = !bf16 && use_stored_lj(N, p.KB, allow_lj);
+  if (bf16) {
+    p.cpg = bf16_blocks_per_group(p.DP, p.KB);
+    p.rgroups = kAccWaves / (p.cpg * bf16_parts(p.DP));
+  } else if (p.lj) {
     // 8 component blocks per workgroup, or 4 for K <= 224.  Two waves share a
     // block (one half of the columns each) where one wave's x and x^2
     // accumulators would not fit: above D = 128, or at D = 128 with 4 blocks.
@@ -1113,6 +1123,470 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
   }
 }
 
+// ===========================================================================
+// bf16 operand contract (FGMM_FLAG_BF16), the arithmetic of the reference's
+// diagonal H100 kernels (flash_gmm_diag_h100.py:63-130 pass 1, :159-282 pass 2,
+// :317-343 constants), in log2 units:
+//   W1_kd = fp32(exp(-lss_kd)) * fp32(0.5 log2 e),   W2_kd = mu_kd * W1_kd      (fp32)
+//   c0_k  = (lpi_k - 0.5 (D log 2pi + sum_d lss_kd)) log2 e - 0.5 log2 e sum_d mu_kd^2 e^-lss_kd
+//   ll2   = c0_k - bf16(x^2) . bf16(W1_k) + 2 bf16(x) . bf16(W2_k)     (fp32 accumulation)
+//   r = 2^(ll2 - logZ2);  Nk = sum r;  mu_acc = bf16(r)^T bf16(x);  rxsq = bf16(r)^T bf16(x^2)
+//   sig_acc = rxsq - 2 mu mu_acc + mu^2 Nk   (fp64, in diag_reduce)
+// One contraction over F = 2 DP features [x^2 | x] against [-bf16(W1) | 2 bf16(W2)]
+// (negation and doubling are exact in bf16) on v_mfma_f32_32x32x16_bf16, 16 features
+// per step.  The features form NCH chains (x^2 and x; each split in two above
+// D = 128) that are added as (c0 + s_x2) + s_x, so that every kernel configuration
+// forms bitwise the same log-joint.  Pass 2 recomputes the contraction (at bf16
+// rates that costs less than storing the log-joint).
+// ===========================================================================
+__host__ __device__ constexpr int bf16_chains(int DP) { return DP > 128 ? 4 : 2; }
+// Waves per component block in pass 2 (each owns NCH / NH chains and the matching
+// feature columns of r^T [x^2 | x]).
+__host__ __device__ constexpr int bf16_parts(int DP) { return DP <= 64 ? 1 : bf16_chains(DP); }
+// X super-tile buffers in pass 2's LDS: two, or one where two do not fit (D = 256).
+__host__ __device__ constexpr int bf16_xbufs(int DP) { return DP > 192 ? 1 : 2; }
+__host__ __device__ constexpr int bf16_xr_stride(int DP) { return 2 * DP + 8; }   // bf16 per row
+
+__host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB) {
+  return (size_t)bf16_xbufs(DP) * (size_t)(256 / (CB * bf16_parts(DP))) *
+             ((size_t)bf16_xr_stride(DP) + 2 * DP) * 2 +
+         (size_t)bf16_xbufs(DP) * (256 / (CB * bf16_parts(DP))) * sizeof(float) +
+         (bf16_parts(DP) > 1 ? (size_t)kAccWaves * 16 * 64 * sizeof(float) : 0);
+}
+// Component blocks per pass-2 workgroup: as many as 8 waves hold (4, or 2 with four
+// parts), fewer when K has fewer blocks so that no wave idles.
+__host__ inline int bf16_blocks_per_group(int DP, int KB) {
+  int cb = bf16_parts(DP) == 4 ? 2 : 4;
+  while (cb > 1 && KB <= cb / 2 && bf16_accum_lds_bytes(DP, cb / 2) <= kMaxLds) cb /= 2;
+  return cb;
+}
+
+// Prologue: the feature operand in matrix-core order, mu_op[kb][q][lane] = features
+// 16q + 8(lane/32) + e of component kb*32 + lane%32 (bf16x8), and c0 per component.
+__global__ __launch_bounds__(64) void diag_bf16_prep(const float* __restrict__ mu, int64_t ldmu,
+                                                     const float* __restrict__ lss, int64_t ldlss,
+                                                     int64_t K, int D, int DP,
+                                                     const float* __restrict__ lpi,
+                                                     bf16x8* __restrict__ mu_op, float* __restrict__ kc) {
+  const int kb = blockIdx.x, lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  const int64_t k = (int64_t)kb * 32 + c;
+  const bool valid = k < K;
+  const int NCF = DP / 8;
+  const float half_log2e = (float)(0.5 * kLog2e);
+  for (int q = 0; q < NCF; ++q) {
+    bf16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int f = 16 * q + 8 * g + e;
+      const int d = f < DP ? f : f - DP;
+      float val = 0.0f;
+      if (valid && d < D) {
+        const float w1 = (float)exp(-(double)lss[k * ldlss + d]) * half_log2e;
+        val = f < DP ? -(float)(__bf16)w1 : 2.0f * (float)(__bf16)(mu[k * ldmu + d] * w1);
+      }
+      v[e] = (__bf16)val;   // exact: val is a bf16 value, negated or doubled
+    }
+    mu_op[((int64_t)kb * NCF + q) * 64 + lane] = v;
+  }
+  if (g == 0) {
+    double C = -INFINITY;
+    if (valid) {
+      double lsum = 0.0, qs = 0.0;
+      for (int d = 0; d < D; ++d) {
+        const double l = (double)lss[k * ldlss + d];
+        const double m = (double)mu[k * ldmu + d];
+        lsum += l;
+        qs = fma(m * m, exp(-l), qs);
+      }
+      C = ((double)lpi[k] - 0.5 * ((double)D * kLog2Pi + lsum)) * kLog2e - 0.5 * kLog2e * qs;
+    }
+    kc[k] = (float)C;
+  }
+}
+
+// The log-joint of a 32 x 32 tile from its NCH chain partials (accumulator layout),
+// in the fixed order shared by both passes.
+template <int NCH>
+__device__ __forceinline__ float bf16_diag_ll(float c0, const float (&s)[NCH]) {
+  if constexpr (NCH == 2) {
+    return (c0 + s[0]) + s[1];
+  } else {
+    return (c0 + (s[0] + s[1])) + (s[2] + s[3]);
+  }
+}
+
+// Pass 1: grid over 128-row tiles, 4 waves of 32 rows.  Each lane rounds its row's
+// x and x^2 to bf16 as it loads them; feature blocks of 32 components (and c0)
+// stream through an LDS double buffer.  Writes logZ and logZ2 per row.
+template <int DP>
+constexpr size_t bf16_lse_lds_bytes() {
+  return (size_t)2 * (DP / 8) * 64 * sizeof(bf16x8) + (size_t)2 * 32 * sizeof(float);
+}
+
+template <int DP>
+__global__ __launch_bounds__(kThreads) void diag_bf16_lse(const float* __restrict__ X, int64_t ldx,
+                                                          int64_t N, int D,
+                                                          const bf16x8* __restrict__ mu_op,
+                                                          const float* __restrict__ kc, int KB,
+                                                          float* __restrict__ logZ,
+                                                          float* __restrict__ rowstat) {
+  constexpr int NCF = DP / 8;                  // 16-feature chunks
+  constexpr int NCH = bf16_chains(DP);
+  constexpr int CPC = NCF / NCH;               // chunks per chain
+  constexpr int BLK = NCF * 64;                // bf16x8 per 32-component block
+  constexpr int LPT = (BLK + kThreads - 1) / kThreads;
+  static_assert(NCF % NCH == 0, "chains split the features evenly");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                               // [2][BLK]
+  float* kc_l = reinterpret_cast<float*>(lds_raw + 2 * BLK * sizeof(bf16x8));      // [2][32]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t row = ((int64_t)blockIdx.x * kWaves + wave) * 32 + c;
+  const bool valid = row < N;
+
+  bf16x8 st[LPT];
+  float kst = 0.0f;
+  auto fetch = [&](int kb) {
+    const bf16x8* src = mu_op + (int64_t)kb * BLK;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q)
+      if (BLK % kThreads == 0 || q * kThreads + tid < BLK) st[q] = src[q * kThreads + tid];
+    if (tid < 32) kst = kc[(int64_t)kb * 32 + tid];
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < LPT; ++q)
+      if (BLK % kThreads == 0 || q * kThreads + tid < BLK) mu_l[buf * BLK + q * kThreads + tid] = st[q];
+    if (tid < 32) kc_l[buf * 32 + tid] = kst;
+  };
+  fetch(0);
+
+  // This lane's feature chunks: chunk q < NCF/2 is bf16(x^2) of dimensions 16q + 8g ..
+  // +7, chunk NCF/2 + q is bf16(x) of the same dimensions.
+  bf16x8 xf[NCF];
+#pragma unroll
+  for (int q = 0; q < NCF / 2; ++q) {
+    const int d0 = 16 * q + 8 * g;
+    const f32x4 lo = load_row4(X, ldx, row, d0, D, valid), hi = load_row4(X, ldx, row, d0 + 4, D, valid);
+    xf[q] = to_bf16x8(lo * lo, hi * hi);
+    xf[NCF / 2 + q] = to_bf16x8(lo, hi);
+  }
+  commit(0);
+  lds_barrier();
+
+  float mx = -INFINITY, sm = 0.0f;
+  for (int kb = 0; kb < KB; ++kb) {
+    const int buf = kb & 1;
+    const bool more = kb + 1 < KB;
+    if (more) fetch(kb + 1);
+    const bf16x8* mp = mu_l + buf * BLK + lane;
+    // S^T = W . F^T per chain: lane = row, register i = component acc_row(i, g).
+    f32x16 ch[NCH];
+#pragma unroll
+    for (int h = 0; h < NCH; ++h) ch[h] = zero16();
+#pragma unroll
+    for (int qq = 0; qq < CPC; ++qq) {
+#pragma unroll
+      for (int h = 0; h < NCH; ++h) ch[h] = mfma_bf16(mp[(h * CPC + qq) * 64], xf[h * CPC + qq], ch[h]);
+    }
+    const float* kp = kc_l + buf * 32;
+    float ll[16];
+    float bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float s[NCH];
+#pragma unroll
+      for (int h = 0; h < NCH; ++h) s[h] = ch[h][i];
+      ll[i] = bf16_diag_ll<NCH>(kp[acc_row(i, g)], s);
+      bm = fmaxf(bm, ll[i]);
+    }
+    const float mn = fmaxf(mx, bm);
+    const float ms = (mn == -INFINITY) ? 0.0f : mn;
+    float a = sm * fast_exp2(mx - ms);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) a += fast_exp2(ll[i] - ms);
+    sm = a;
+    mx = mn;
+    if (more) commit(buf ^ 1);
+    lds_barrier();
+  }
+  const float mo = __shfl_xor(mx, 32);
+  const float so = __shfl_xor(sm, 32);
+  const float mn = fmaxf(mx, mo);
+  const float ms = (mn == -INFINITY) ? 0.0f : mn;
+  const float lz2 = mn + log2f(sm * fast_exp2(mx - ms) + so * fast_exp2(mo - ms));
+  if (valid && g == 0) {
+    rowstat[row] = lz2;
+    if (logZ) logZ[row] = lz2 * (float)kLn2;
+  }
+}
+
+// Pass 2: grid over (row slab x group of CB component blocks); 8 waves = CB blocks x
+// NH parts x 8/(CB NH) row groups.  Part h of a block holds the feature operand of
+// chains [h NCH/NH, (h+1) NCH/NH), recomputes their partial S = F W^T for its 32
+// rows, and with NH > 1 the parts meet in LDS and every part forms the same log-joint
+// in the shared order.  Each part then accumulates r^T F over its own feature columns
+// (x^2 columns into part_sq, x columns into part_mu).  X super-tiles are rounded once
+// per workgroup into LDS in two layouts: features row-major (the A operand of S;
+// x^2 then x) and row-octet interleaved, feature (r, f) at ((r/8) F + f) 8 + r%8 (the
+// B operand of r^T F: 8 consecutive rows of one feature are 16 contiguous bytes).
+template <int DP, int CB, int NH = bf16_parts(DP)>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
+void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                     const bf16x8* __restrict__ mu_op, const float* __restrict__ kc, int KB, int KP,
+                     const float* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
+                     float* __restrict__ part_mu, float* __restrict__ part_sq,
+                     float* __restrict__ part_nk, int dense) {
+  constexpr int F = 2 * DP;                    // features per row
+  constexpr int NCF = F / 16;                  // 16-feature chunks
+  constexpr int NCH = bf16_chains(DP);
+  constexpr int CPC = NCF / NCH;               // chunks per chain
+  constexpr int CPW = NCH / NH;                // chains per wave
+  constexpr int FW = F / NH;                   // feature columns per wave
+  constexpr int NJ = FW / 32;                  // 32-column tiles of r^T F per wave
+  constexpr int RG = kAccWaves / (CB * NH);    // row groups (32 rows each)
+  constexpr int TR = 32 * RG;                  // rows per super-tile
+  constexpr int XR = bf16_xr_stride(DP);
+  constexpr int NB = bf16_xbufs(DP);
+  constexpr int V4 = DP / 4;
+  constexpr int NV = TR * V4;                  // float4 per super-tile
+  constexpr int LPT = (NV + kAccThreads - 1) / kAccThreads;
+  static_assert(kAccWaves % (CB * NH) == 0 && NCH % NH == 0 &&
+                    (NH == 1 || CPW == 1) && FW % 32 == 0 && DP % 32 == 0,
+                "even split");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  __bf16* xr = reinterpret_cast<__bf16*>(lds_raw);                        // [NB][TR][XR]
+  __bf16* xi = xr + NB * TR * XR;                                          // [NB][TR/8][F][8]
+  float* rs = reinterpret_cast<float*>(xi + NB * TR * F);                  // [NB][TR]
+  float* ex = rs + NB * TR;                                                // [8][16][64] (NH > 1)
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int cbw = wave % CB, h = (wave / CB) % NH, rg = wave / (CB * NH);
+  const int f0 = h * FW;                       // first feature of this wave's part
+  const int slab = blockIdx.x % nslab;
+  const int cg = blockIdx.x / nslab;
+  const int kb = cg * CB + cbw;
+  const bool active = kb < KB;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
+
+  // B operand of the recompute (lane = component, features 16q + 8g + e of this
+  // wave's chains) and the component's constant.
+  bf16x8 mub[CPW * CPC];
+#pragma unroll
+  for (int q = 0; q < CPW * CPC; ++q) {
+    if (active) {
+      mub[q] = mu_op[((int64_t)kb * NCF + h * CPW * CPC + q) * 64 + lane];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mub[q][e] = (__bf16)0.0f;
+    }
+  }
+  const float c0 = active ? kc[(int64_t)kb * 32 + c] : -INFINITY;
+
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
+  float nk = 0.0f;
+
+  // X super-tiles go global -> registers -> LDS: tile t + 1 is loaded while tile t
+  // is processed.
+  f32x4 stage[LPT];
+  float rstage = INFINITY;
+  const bool full_d = (D == DP);
+  // float4 idx of a super-tile <-> (row, 4 dimensions) with the row's low 3 bits
+  // fastest: 8 lanes cover one 16-byte column piece of 8 rows.
+  auto tile_row = [](int idx) { return ((idx >> 3) / V4) * 8 + (idx & 7); };
+  auto tile_col = [](int idx) { return ((idx >> 3) % V4) * 4; };
+  auto fetch = [&](int t) {
+    const int64_t row0 = r_begin + (int64_t)t * TR;
+    if (full_d && row0 + TR <= r_end) {
+      const float* src = X + row0 * ldx;
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        if (NV % kAccThreads == 0 || idx < NV)
+          stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)tile_row(idx) * ldx + tile_col(idx));
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        const int64_t row = row0 + tile_row(idx);
+        if (NV % kAccThreads == 0 || idx < NV)
+          stage[q] = load_row4(X, ldx, row, tile_col(idx), D, row < r_end);
+      }
+    }
+    if (tid < TR) {
+      const int64_t row = row0 + tid;
+      // Rows past the slab get logZ2 = +inf, hence r = 0.
+      rstage = (row < r_end) ? rowstat[row] : INFINITY;
+    }
+  };
+  auto commit = [&](int buf) {
+    __bf16* dr = xr + buf * TR * XR;
+    __bf16* di = xi + buf * TR * F;
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      if (NV % kAccThreads != 0 && idx >= NV) continue;
+      const int r = tile_row(idx), d = tile_col(idx);
+      const f32x4 v = stage[q];
+      const f32x4 v2 = v * v;
+      const bf16x4 b = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+      const bf16x4 b2 = {(__bf16)v2.x, (__bf16)v2.y, (__bf16)v2.z, (__bf16)v2.w};
+      *reinterpret_cast<bf16x4*>(dr + r * XR + d) = b2;
+      *reinterpret_cast<bf16x4*>(dr + r * XR + DP + d) = b;
+      __bf16* o = di + ((r >> 3) * F + d) * 8 + (r & 7);
+      o[0] = b2[0]; o[8] = b2[1]; o[16] = b2[2]; o[24] = b2[3];
+      o += DP * 8;
+      o[0] = b[0]; o[8] = b[1]; o[16] = b[2]; o[24] = b[3];
+    }
+    if (tid < TR) rs[buf * TR + tid] = rstage;
+  };
+
+  if (ntiles > 0) {
+    fetch(0);
+    commit(0);
+  }
+  lds_barrier();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = NB == 2 ? (t & 1) : 0;
+    const bool more = t + 1 < ntiles;
+    if (more) fetch(t + 1);
+    // This wave's chain partials of S = F W^T for its 32 rows: lane = component,
+    // register i = row acc_row(i, g).
+    f32x16 ch[CPW];
+#pragma unroll
+    for (int u = 0; u < CPW; ++u) ch[u] = zero16();
+    if (active) {
+      const __bf16* xrow = xr + buf * TR * XR + (rg * 32 + c) * XR + f0 + 8 * g;
+#pragma unroll
+      for (int qq = 0; qq < CPC; ++qq) {
+#pragma unroll
+        for (int u = 0; u < CPW; ++u)
+          ch[u] = mfma_bf16(*reinterpret_cast<const bf16x8*>(xrow + 16 * (u * CPC + qq)), mub[u * CPC + qq],
+                            ch[u]);
+      }
+    }
+    // Chain u of register i: this wave's own, or (NH > 1) the one part u of the block
+    // wrote to LDS, the parts of a block being waves rg*CB*NH + u*CB + cbw.
+    const float* s0 = ex + (rg * CB * NH + cbw) * 16 * 64 + lane;
+    if constexpr (NH > 1) {
+      float* mine = ex + wave * 16 * 64 + lane;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mine[i * 64] = ch[0][i];
+      lds_barrier();
+    }
+    if (active) {
+      const float* rt = rs + buf * TR + rg * 32;
+      float r[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float sv[NCH];
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+          if constexpr (NH == 1) {
+            sv[u] = ch[u][i];
+          } else {
+            sv[u] = s0[u * CB * 16 * 64 + i * 64];
+          }
+        }
+        const float ll = bf16_diag_ll<NCH>(c0, sv);
+        const float rv = fast_exp2(ll - rt[acc_row(i, g)]);
+        if (h == 0) nk += rv;
+        r[i] = rv;
+      }
+      bf16x8 a[2];
+      acc_to_row_operands(r, a);
+      // B operand: rows rg*32 + 16p + 8g + e of feature f0 + 32j + c.
+      const __bf16* xcol = xi + buf * TR * F + ((rg * 4 + g) * F + f0 + c) * 8;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        // A step whose 16 rows x 32 components of bf16(r) are all zero adds nothing.
+        if (dense || any_nonzero(a[p])) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+            acc[j] = mfma_bf16(a[p], *reinterpret_cast<const bf16x8*>(xcol + (2 * p * F + 32 * j) * 8), acc[j]);
+        }
+      }
+    }
+    if (more) {
+      if constexpr (NB == 1) lds_barrier();   // every wave is done with the buffer
+      commit(NB == 2 ? (buf ^ 1) : 0);
+    }
+    lds_barrier();
+  }
+
+  if (active) {
+    nk += __shfl_xor(nk, 32);
+    const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int f = f0 + 32 * j;               // a tile lies wholly in x^2 or in x
+      float* dst = f < DP ? part_sq + f : part_mu + (f - DP);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dst[(kbase + acc_row(i, g)) * DP + c] = acc[j][i];
+    }
+    if (g == 0 && h == 0) part_nk[kbase + c] = nk;
+  }
+}
+
+template <int DP>
+hipError_t launch_bf16(const DiagPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
+                       float* logZ, bool run1, bool run2, bool dense, hipStream_t stream) {
+  const bf16x8* mu_op = reinterpret_cast<const bf16x8*>(ws + pl.off_musw);
+  const float* kc = reinterpret_cast<const float*>(ws + pl.off_kclin);
+  float* rowstat = reinterpret_cast<float*>(ws + pl.off_rowstat);
+  if (run1) {
+    constexpr size_t lds1 = bf16_lse_lds_bytes<DP>();
+    if (lds1 > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_bf16_lse<DP>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(diag_bf16_lse<DP>, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
+                       stream, X, ldx, pl.N, (int)pl.D, mu_op, kc, pl.KB, logZ, rowstat);
+  }
+  if (!run2) return hipGetLastError();
+  auto launch = [&](auto cb_tag) -> hipError_t {
+    constexpr int CB = decltype(cb_tag)::value;
+    if constexpr (CB * bf16_parts(DP) > kAccWaves) {
+      return hipErrorInvalidValue;   // never chosen by the plan
+    } else {
+      constexpr size_t lds = bf16_accum_lds_bytes(DP, CB);
+      if constexpr (lds > kMaxLds) {
+        return hipErrorInvalidValue;   // never chosen by the plan
+      } else {
+        if (lds > 65536) {
+          hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_bf16_accum<DP, CB>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+          if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL((diag_bf16_accum<DP, CB>), dim3((unsigned)(pl.nslab * pl.ncg)),
+                           dim3(kAccThreads), lds, stream, X, ldx, pl.N, (int)pl.D, mu_op, kc, pl.KB,
+                           pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
+                           reinterpret_cast<float*>(ws + pl.off_part_mu),
+                           reinterpret_cast<float*>(ws + pl.off_part_sq),
+                           reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
+        return hipGetLastError();
+      }
+    }
+  };
+  return pl.cpg == 1   ? launch(std::integral_constant<int, 1>{})
+         : pl.cpg == 2 ? launch(std::integral_constant<int, 2>{})
+                       : launch(std::integral_constant<int, 4>{});
+}
+
 }  // namespace
 }  // namespace fgmm
 
@@ -1125,7 +1599,7 @@ extern "C" size_t fgmm_diag_workspace_bytes(int64_t N, int64_t K, int64_t D) {
 
 extern "C" size_t fgmm_diag_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE)).total;
+  return make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE), (flags & FGMM_FLAG_BF16) != 0).total;
 }
 
 extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -1138,7 +1612,6 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   const bool accumulate = (flags & FGMM_FLAG_ACCUMULATE) != 0;
   const bool dense = (flags & FGMM_FLAG_DENSE) != 0;
   if (N < 0 || K < 0 || D < 1) return FGMM_ERR_INVALID_ARG;
-  if (flags & FGMM_FLAG_BF16) return FGMM_ERR_UNSUPPORTED;
   if (N > 0 && (X == nullptr || ldx < round_up(D, 4) || (ldx % 4) != 0 ||
                 (reinterpret_cast<uintptr_t>(X) & 15) != 0))
     return FGMM_ERR_INVALID_ARG;
@@ -1148,7 +1621,8 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     return FGMM_ERR_INVALID_ARG;
   if (D > 256) return FGMM_ERR_UNSUPPORTED;
   if (N > kMaxRows || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
-  const DiagPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE));
+  const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
+  const DiagPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE), bf16);
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;
   unsigned char* ws = static_cast<unsigned char*>(workspace);
@@ -1161,20 +1635,29 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
                          -INFINITY);
     return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
   }
-  if (run1)
+  if (run1 && bf16)
+    hipLaunchKernelGGL(diag_bf16_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
+                       (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_musw),
+                       reinterpret_cast<float*>(ws + pl.off_kclin));
+  else if (run1)
     hipLaunchKernelGGL(diag_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
                        (int)D, pl.DP, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_musw),
                        reinterpret_cast<double*>(ws + pl.off_kcblk),
                        reinterpret_cast<double*>(ws + pl.off_kclin));
   if (N > 0) {
+    auto run = [&](auto dp_tag) -> hipError_t {
+      constexpr int DP = decltype(dp_tag)::value;
+      return bf16 ? launch_bf16<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream)
+                  : launch_passes<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
+    };
     hipError_t e = hipSuccess;
     switch (pl.DP) {
-      case 32: e = launch_passes<32>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 96: e = launch_passes<96>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 128: e = launch_passes<128>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 192: e = launch_passes<192>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 256: e = launch_passes<256>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 32: e = run(std::integral_constant<int, 32>{}); break;
+      case 64: e = run(std::integral_constant<int, 64>{}); break;
+      case 96: e = run(std::integral_constant<int, 96>{}); break;
+      case 128: e = run(std::integral_constant<int, 128>{}); break;
+      case 192: e = run(std::integral_constant<int, 192>{}); break;
+      case 256: e = run(std::integral_constant<int, 256>{}); break;
       default: return FGMM_ERR_UNSUPPORTED;
     }
     if (e != hipSuccess) return FGMM_ERR_HIP;

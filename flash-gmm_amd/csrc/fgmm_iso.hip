@@ -1226,23 +1226,9 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
 // both operands take dimensions 16q + 8g + e.  Pass 2 recomputes the contraction
 // (at bf16 rates that costs less than storing the log-joint).
 // ===========================================================================
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
 // Above D = 128 pass 2 splits a component block over two waves, one half of the
 // dimensions each (and pass 1 sums its contraction in the same two halves).
 __host__ __device__ constexpr int bf16_halves(int DP) { return DP > 128 ? 2 : 1; }
-
-// Round-to-nearest-even fp32 -> bf16 of 8 values.
-__device__ __forceinline__ bf16x8 to_bf16x8(f32x4 lo, f32x4 hi) {
-  bf16x8 v;
-  v[0] = (__bf16)lo.x; v[1] = (__bf16)lo.y; v[2] = (__bf16)lo.z; v[3] = (__bf16)lo.w;
-  v[4] = (__bf16)hi.x; v[5] = (__bf16)hi.y; v[6] = (__bf16)hi.z; v[7] = (__bf16)hi.w;
-  return v;
-}
 
 // Prologue: mu in operand order mu_op[kb][q][lane] = mu[kb*32 + lane%32][16q + 8(lane/32) + e]
 // (bf16x8), and per component {c0, ish, 2 ish, ||mu||^2} in fp32 (formed in fp64).
@@ -1572,35 +1558,14 @@ void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
         }
         r[i] = rv;
       }
-      // Registers 4p'+j hold rows 8p' + 4g + j.  Packed to bf16 pairs, one swap across
-      // the half-waves per pair of dwords leaves lane-half g with rows 16p + 8g + e
-      // (e = 0..3 from the first pair, 4..7 from the second) for p = 0, 1.
-      typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-      auto pack = [](float u, float v) {
-        const bf16x2 t = {(__bf16)u, (__bf16)v};
-        return *reinterpret_cast<const unsigned*>(&t);
-      };
       bf16x8 a[2];
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        uint4 wv;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const auto sw = __builtin_amdgcn_permlane32_swap(pack(r[8 * p + 2 * hh], r[8 * p + 2 * hh + 1]),
-                                                           pack(r[8 * p + 4 + 2 * hh], r[8 * p + 5 + 2 * hh]),
-                                                           false, false);
-          if (hh == 0) { wv.x = sw[0]; wv.z = sw[1]; } else { wv.y = sw[0]; wv.w = sw[1]; }
-        }
-        a[p] = *reinterpret_cast<const bf16x8*>(&wv);
-      }
+      acc_to_row_operands(r, a);
       // B operand: rows rg*32 + 16p + 8g + e of column d0 + 32j + c.
       const __bf16* xcol = xi + buf * TR * DP + ((rg * 4 + g) * DP + d0 + c) * 8;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        const uint4 bits = *reinterpret_cast<const uint4*>(&a[p]);
-        const bool nz = (bits.x | bits.y | bits.z | bits.w) != 0u;
         // A step whose 16 rows x 32 components of bf16(r) are all zero adds nothing.
-        if (dense || __builtin_amdgcn_ballot_w64(nz) != 0) {
+        if (dense || any_nonzero(a[p])) {
 #pragma unroll
           for (int j = 0; j < NJ; ++j)
             acc[j] = mfma_bf16(a[p], *reinterpret_cast<const bf16x8*>(xcol + (2 * p * DP + 32 * j) * 8), acc[j]);

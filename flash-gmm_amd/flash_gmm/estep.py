@@ -201,9 +201,18 @@ def flash_gmm_estep(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tenso
 def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
                     accumulate: bool = False, workspace: torch.Tensor | None = None,
                     phase: int = 0, dense: bool = False,
-                    recompute: bool = False) -> None:
-    """Diagonal-covariance E-step into caller-provided outputs (sig_acc is (K, D))."""
+                    recompute: bool = False, precision: str = "fp32") -> None:
+    """Diagonal-covariance E-step into caller-provided outputs (sig_acc is (K, D)).
+
+    ``precision="bf16"`` selects the bf16 operand contract of the reference's
+    diagonal H100 kernels (flash_gmm_diag_h100.py:63-130, :159-282): x, x^2 and the
+    weights exp(-lss)/2 log2 e and mu exp(-lss)/2 log2 e rounded to bfloat16, r
+    rounded to bfloat16 for r^T x and r^T x^2, fp32 accumulation and log-sum-exp.
+    The accumulation then always recomputes the contraction (``recompute`` has no
+    effect).
+    """
     _check_common(X, mu, log_pi)
+    _require(precision in ("fp32", "bf16"), f"precision must be 'fp32' or 'bf16', got {precision!r}")
     N, D = X.shape
     K = mu.shape[0]
     dev = X.device
@@ -222,6 +231,8 @@ def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
         flags |= _lib.FLAG_DENSE
     if recompute:
         flags |= _lib.FLAG_RECOMPUTE
+    if precision == "bf16":
+        flags |= _lib.FLAG_BF16
     workspace = _workspace(L.fgmm_diag_workspace_bytes_ex, N, K, D, flags, dev, workspace)
     _check_out("Nk", Nk, (K,), dev)
     _check_out("mu_acc", mu_acc, (K, D), dev)
@@ -238,10 +249,12 @@ def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
 
 
 def flash_gmm_estep_diag(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tensor,
-                         log_pi: torch.Tensor):
+                         log_pi: torch.Tensor, *, precision: str = "fp32"):
     """Diagonal-covariance E-step: returns (logZ, Nk, mu_acc, sig_acc[K, D]).
 
     sig_acc[k, d] = sum_n r_nk (x_nd - mu_kd)^2 (flash_gmm_diag_h100.py:258-260).
+    ``precision="bf16"`` follows the reference kernels' bf16 operand contract
+    instead of fp32 arithmetic.
     """
     _check_common(X, mu, log_pi)
     N, D = X.shape
@@ -253,7 +266,7 @@ def flash_gmm_estep_diag(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.
     Nk = torch.empty(K, device=dev, dtype=torch.float32)
     mu_acc = torch.empty(K, D, device=dev, dtype=torch.float32)
     sig_acc = torch.empty(K, D, device=dev, dtype=torch.float32)
-    diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc)
+    diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, precision=precision)
     return logZ, Nk, mu_acc, sig_acc
 
 

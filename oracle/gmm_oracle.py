@@ -25,6 +25,11 @@ Parity pinning (what checks each function, see tests/test_oracle.py):
   equal to ``estep_iso`` (logZ, Nk, sig_acc) on inputs that are exact in bfloat16
   and within the bf16 rounding of r for mu_acc; an independent scalar-loop
   version with bit-level rounding on tiny inputs.
+* ``estep_diag_bf16`` -- the bf16 operand contract of the reference's diagonal
+  H100 kernels: equal to ``estep_diag`` (logZ, Nk) when every rounded operand is
+  already exact in bfloat16 (weights that are powers of two, x with few
+  significant bits) and within the bf16 rounding of r for mu_acc and sig_acc; an
+  independent scalar-loop version with bit-level rounding on tiny inputs.
 * ``estep_full`` -- scipy logpdf with the full covariance recovered from the
   precision Cholesky factor, sklearn 'full' internals, brute force, reduction
   to ``estep_diag`` for diagonal factors.
@@ -208,6 +213,63 @@ def estep_diag(X: Tensor, mu: Tensor, log_sigma_sq: Tensor, log_pi: Tensor, *,
     return logZ, Nk, mu_acc, sig_acc
 
 
+def diag_bf16_weights(mu: Tensor, log_sigma_sq: Tensor) -> Tuple[Tensor, Tensor]:
+    """float32 W1 = exp(-lss) * 0.5 log2e and W2 = mu * W1 of flash_gmm_diag_h100.py:332-333.
+
+    exp is rounded once from float64 (the reference's float32 exp may differ from
+    that by an ulp, which moves a bfloat16 rounding only at a tie).
+    """
+    lss32 = _as(log_sigma_sq, torch.float32)
+    e32 = torch.exp(-lss32.double()).float()
+    w1 = e32 * torch.tensor(0.5 * LOG2_E, dtype=torch.float32)
+    w2 = _as(mu, torch.float32) * w1
+    return w1, w2
+
+
+def estep_diag_bf16(X: Tensor, mu: Tensor, log_sigma_sq: Tensor, log_pi: Tensor, *,
+                    chunk: int = _DEFAULT_CHUNK) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Diagonal E-step with the bf16 operand contract of flash_gmm_diag_h100.py.
+
+    x and x^2 (squared in float32) are rounded to bfloat16 (:86-88, :238-239), and so
+    are W1 and W2 (:332-333, :342-343); c0 comes from the float32 parameters
+    (:335-339); ll2 = c0 - bf16(x^2) . bf16(W1) + 2 bf16(x) . bf16(W2) (:116-119,
+    :242-244); r = 2^(ll2 - logZ2) (:250); Nk = sum r (:254); mu_acc = bf16(r)^T
+    bf16(x) and rxsq = bf16(r)^T bf16(x^2) (:251, :255-256); sig_acc = rxsq -
+    2 mu mu_acc + mu^2 Nk (:260); logZ = logZ2 ln 2 (:382).  Rows are partitioned (no slab
+    overlap, unlike :220-231).  Everything except the roundings is float64 here
+    (the reference accumulates in float32).
+    """
+    X32 = _as(X, torch.float32)
+    mu64 = _as(mu, torch.float64)
+    lss, lpi = _as(log_sigma_sq, torch.float64), _as(log_pi, torch.float64)
+    N, D = X32.shape
+    K = mu64.shape[0]
+    if lss.shape != (K, D):
+        raise ValueError(f"log_sigma_sq must be (K, D)=({K}, {D}), got {tuple(lss.shape)}")
+    w1, w2 = diag_bf16_weights(mu, log_sigma_sq)
+    w1b, w2b = bf16_round(w1), bf16_round(w2)
+    c0 = ((lpi - 0.5 * (D * LOG_2PI + lss.sum(dim=1))) * LOG2_E
+          - 0.5 * LOG2_E * (mu64 * mu64 * torch.exp(-lss)).sum(dim=1))
+    logZ = torch.empty(N, dtype=torch.float64)
+    Nk = torch.zeros(K, dtype=torch.float64)
+    mu_acc = torch.zeros(K, D, dtype=torch.float64)
+    rxsq = torch.zeros(K, D, dtype=torch.float64)
+    ln2 = math.log(2.0)
+    for n0 in range(0, N, chunk):
+        x = X32[n0:n0 + chunk]
+        xb, xsqb = bf16_round(x), bf16_round(x * x)
+        ll2 = c0[None, :] - xsqb @ w1b.T + 2.0 * (xb @ w2b.T)
+        lz2 = torch.logsumexp(ll2 * ln2, dim=1) / ln2
+        logZ[n0:n0 + chunk] = lz2 * ln2
+        r = torch.exp2(ll2 - lz2[:, None])
+        rb = bf16_round(r)
+        Nk += r.sum(dim=0)
+        mu_acc += rb.T @ xb
+        rxsq += rb.T @ xsqb
+    sig_acc = rxsq - 2.0 * mu64 * mu_acc + mu64 * mu64 * Nk[:, None]
+    return logZ, Nk, mu_acc, sig_acc
+
+
 def full_log_prob(X: Tensor, mu: Tensor, prec_chol: Tensor, lpi: Tensor) -> Tensor:
     """Per-(n, k) log joint for full covariance given L_k with L_k L_k^T = Sigma_k^-1.
 
@@ -335,6 +397,51 @@ def brute_estep_iso_bf16(X, mu, lss, lpi):
             rb = _bf16_scalar(r)
             for d in range(D):
                 mu_acc[k][d] += rb * xb[n][d]
+    return logZ, Nk, mu_acc, sig_acc
+
+
+def brute_estep_diag_bf16(X, mu, lss, lpi):
+    """Scalar-loop version of estep_diag_bf16 for tiny inputs (bit-level bf16 rounding)."""
+    import struct
+
+    def f32(v):
+        return struct.unpack("<f", struct.pack("<f", v))[0]
+
+    X = [[float(v) for v in row] for row in X.tolist()]
+    mu = [[float(v) for v in row] for row in mu.tolist()]
+    lss = [[float(v) for v in row] for row in lss.tolist()]
+    lpi = [float(v) for v in lpi.tolist()]
+    N, D, K = len(X), len(X[0]) if X else 0, len(mu)
+    half_log2e = f32(0.5 / math.log(2.0))
+    w1 = [[f32(f32(math.exp(-lss[k][d])) * half_log2e) for d in range(D)] for k in range(K)]
+    w2 = [[f32(mu[k][d] * w1[k][d]) for d in range(D)] for k in range(K)]
+    w1b = [[_bf16_scalar(v) for v in row] for row in w1]
+    w2b = [[_bf16_scalar(v) for v in row] for row in w2]
+    c0 = []
+    for k in range(K):
+        quad = sum(mu[k][d] ** 2 * math.exp(-lss[k][d]) for d in range(D))
+        c0.append((lpi[k] - 0.5 * (D * LOG_2PI + sum(lss[k]))) / math.log(2.0)
+                  - 0.5 / math.log(2.0) * quad)
+    logZ, Nk = [], [0.0] * K
+    mu_acc = [[0.0] * D for _ in range(K)]
+    rxsq = [[0.0] * D for _ in range(K)]
+    for n in range(N):
+        xb = [_bf16_scalar(v) for v in X[n]]
+        x2b = [_bf16_scalar(f32(v * v)) for v in X[n]]
+        ll2 = [c0[k] - sum(x2b[d] * w1b[k][d] for d in range(D))
+               + 2.0 * sum(xb[d] * w2b[k][d] for d in range(D)) for k in range(K)]
+        m = max(ll2)
+        lz2 = m + math.log2(sum(2.0 ** (v - m) for v in ll2))
+        logZ.append(lz2 * math.log(2.0))
+        for k in range(K):
+            r = 2.0 ** (ll2[k] - lz2)
+            Nk[k] += r
+            rb = _bf16_scalar(r)
+            for d in range(D):
+                mu_acc[k][d] += rb * xb[d]
+                rxsq[k][d] += rb * x2b[d]
+    sig_acc = [[rxsq[k][d] - 2.0 * mu[k][d] * mu_acc[k][d] + mu[k][d] ** 2 * Nk[k] for d in range(D)]
+               for k in range(K)]
     return logZ, Nk, mu_acc, sig_acc
 
 

@@ -1,0 +1,109 @@
+"""GPU parity of the diagonal-covariance E-step under the bf16 operand contract
+(precision="bf16", FGMM_FLAG_BF16) against the oracle restatement of that contract,
+gmm_oracle.estep_diag_bf16 (flash_gmm_diag_h100.py:63-130, :159-282, :317-343)."""
+
+import pytest
+import torch
+
+from flash_gmm import FlashGMMError, data, diag_estep_into, flash_gmm_estep_diag
+from oracle import gmm_oracle as O
+from parity import LOGZ_ATOL_BF16, assert_close_stats
+
+pytestmark = pytest.mark.gpu
+
+KEYS = ("X", "mu", "log_sigma_sq", "log_pi")
+
+
+def oracle(inp):
+    return O.estep_diag_bf16(*[inp[k] for k in KEYS])
+
+
+def _into(inp, dev, **kw):
+    N, D = inp["X"].shape
+    K = inp["mu"].shape[0]
+    out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, D, device=dev)]
+    diag_estep_into(*[inp[k].to(dev) for k in KEYS], *out, precision="bf16", **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+# Every padded width (32 .. 256), one / two / many component blocks per workgroup,
+# partial row tiles and slabs, ragged K and D.
+SHAPES = [(1, 1, 1), (33, 1, 1), (31, 3, 5), (200, 5, 7), (129, 33, 32), (1000, 64, 32),
+          (2000, 130, 61), (3000, 100, 96), (1500, 40, 96), (5000, 300, 128), (700, 40, 129),
+          (4000, 260, 192), (3000, 200, 256), (900, 20, 256), (2048, 1, 64), (4097, 70, 100)]
+
+
+@pytest.mark.parametrize("N,K,D", SHAPES)
+def test_edge_shapes(N, K, D, gpu_device):
+    inp = data.diag_clustered(N, K, D, seed=N + K + D)
+    print(f"diag bf16 N={N} K={K} D={D}", flush=True)
+    got = _into(inp, gpu_device)
+    assert_close_stats(got, oracle(inp), f"diag bf16 N={N} K={K} D={D}", logz_atol=LOGZ_ATOL_BF16)
+
+
+def test_entry_point(gpu_device):
+    inp = data.diag_clustered(3000, 64, 48, seed=12)
+    got = flash_gmm_estep_diag(*[inp[k].to(gpu_device) for k in KEYS], precision="bf16")
+    torch.cuda.synchronize()
+    assert_close_stats(got, oracle(inp), "diag bf16 entry", logz_atol=LOGZ_ATOL_BF16)
+
+
+def test_headline_shape_mid_size(gpu_device):
+    inp = data.diag_clustered(32768, 1024, 96, seed=2)
+    assert_close_stats(_into(inp, gpu_device), oracle(inp), "diag bf16 K1024 D96",
+                       logz_atol=LOGZ_ATOL_BF16)
+
+
+@pytest.mark.parametrize("N,K,D", [(12000, 1024, 96), (7777, 300, 61), (5000, 64, 32), (3000, 100, 200)])
+def test_zero_step_skip_is_bitwise_dense(N, K, D, gpu_device):
+    inp = data.diag_clustered(N, K, D, seed=4)
+    a = _into(inp, gpu_device)
+    b = _into(inp, gpu_device, dense=True)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+def test_phase_split_and_accumulate(gpu_device):
+    """PHASE1 then PHASE2 equals one call bitwise; ACCUMULATE over chunks equals one call."""
+    from flash_gmm import _lib
+    inp = data.diag_clustered(9000, 128, 64, seed=10)
+    dev = gpu_device
+    ref = _into(inp, dev)
+    N, D = inp["X"].shape
+    K = inp["mu"].shape[0]
+    L = _lib.lib()
+    ws = torch.empty(L.fgmm_diag_workspace_bytes_ex(N, K, D, _lib.FLAG_BF16), dtype=torch.uint8, device=dev)
+    args = [inp[k].to(dev) for k in KEYS]
+    out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, D, device=dev)]
+    diag_estep_into(*args, *out, workspace=ws, phase=1, precision="bf16")
+    diag_estep_into(*args, None, *out[1:], workspace=ws, phase=2, precision="bf16")
+    torch.cuda.synchronize()
+    for u, v in zip(out, ref):
+        assert torch.equal(u, v)
+    nk = torch.zeros(K, device=dev)
+    ma = torch.zeros(K, D, device=dev)
+    sg = torch.zeros(K, D, device=dev)
+    for n0 in range(0, N, 2500):
+        diag_estep_into(args[0][n0:n0 + 2500], *args[1:], None, nk, ma, sg, accumulate=True,
+                        precision="bf16")
+    torch.cuda.synchronize()
+    torch.testing.assert_close(nk, ref[1], rtol=1e-5, atol=1e-4)
+    torch.testing.assert_close(ma, ref[2], rtol=1e-5, atol=1e-5 * float(ref[2].abs().max()))
+    torch.testing.assert_close(sg, ref[3], rtol=1e-5, atol=1e-4 * float(ref[3].abs().max()))
+
+
+def test_deterministic(gpu_device):
+    inp = data.diag_clustered(20000, 512, 96, seed=6)
+    a = _into(inp, gpu_device)
+    b = _into(inp, gpu_device)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+def test_bad_precision_string(gpu_device):
+    inp = data.diag_clustered(10, 4, 8, seed=11)
+    with pytest.raises(FlashGMMError):
+        flash_gmm_estep_diag(*[inp[k].to(gpu_device) for k in KEYS], precision="fp16")

@@ -6,7 +6,7 @@ import math
 import pytest
 import torch
 
-from flash_gmm import FlashGMMError, data, diag_estep_into, flash_gmm_estep, iso_estep_into
+from flash_gmm import FlashGMMError, data, flash_gmm_estep, iso_estep_into
 from oracle import gmm_oracle as O
 from parity import LOGZ_ATOL_BF16, assert_close_stats
 
@@ -91,17 +91,6 @@ def test_phase_split_and_accumulate(gpu_device):
     torch.testing.assert_close(nk, ref[1], rtol=1e-5, atol=1e-4)
     torch.testing.assert_close(ma, ref[2], rtol=1e-5, atol=1e-5 * float(ref[2].abs().max()))
     torch.testing.assert_close(sg, ref[3], rtol=1e-5, atol=1e-4 * float(ref[3].abs().max()))
-
-
-def test_bf16_is_rejected_by_diag(gpu_device):
-    from flash_gmm import _lib
-    L = _lib.lib()
-    dev = gpu_device
-    x = torch.zeros(8, 4, device=dev)
-    st = L.fgmm_diag_estep_f32(x.data_ptr(), 4, 8, 4, x.data_ptr(), 4, 2, x.data_ptr(), 4, x.data_ptr(),
-                               x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(), 1 << 20,
-                               _lib.FLAG_BF16, None)
-    assert st == _lib.FGMM_ERR_UNSUPPORTED
 
 
 def test_bad_precision_string(gpu_device):

@@ -239,6 +239,71 @@ def test_diag_direct_form():
         np.testing.assert_allclose(u.numpy(), v.numpy(), rtol=1e-10, atol=1e-9)
 
 
+# --------------------------------------------------------------------------- diag, bf16 contract
+
+def _pow2_weight_lss(j: int) -> float:
+    """A float32 log-variance for which the contract's weight W1 = fp32(exp(-lss)) *
+    fp32(0.5 log2 e) is exactly 2**j (so rounding W1 to bfloat16 changes nothing)."""
+    start = np.float32(-math.log(2.0 ** j / (0.5 * O.LOG2_E)))
+    bits = start.view(np.int32)
+    for m in range(4096):
+        for s in (m, -m):
+            cand = np.array(bits + s, dtype=np.int32).view(np.float32)
+            w1, _ = O.diag_bf16_weights(torch.zeros(1, 1), torch.tensor([[float(cand)]]))
+            if float(w1) == 2.0 ** j:
+                return float(cand)
+    raise AssertionError(f"no float32 lss gives W1 = 2^{j}")
+
+
+def test_diag_bf16_equals_fp64_on_bf16_exact_operands():
+    """When x, x^2, W1 and W2 are all exact in bfloat16 (x = k/4 with |k| <= 15, W1 a
+    power of two, mu exact in bfloat16), the contract only rounds r for mu_acc and
+    rxsq: logZ and Nk equal the float64 E-step up to the float32 rounding of W1 that
+    the reference's own c0 (exact exp) does not share (~1e-7 relative)."""
+    g = torch.Generator().manual_seed(31)
+    N, K, D = 400, 5, 7
+    X = torch.randint(-15, 16, (N, D), generator=g).double() / 4
+    mu = O.bf16_round((torch.randn(K, D, generator=g) * 1.5).float())
+    js = torch.randint(-3, 2, (K, D), generator=g)
+    lss = torch.tensor([[_pow2_weight_lss(int(j)) for j in row] for row in js], dtype=torch.float64)
+    lpi = torch.log_softmax(torch.randn(K, generator=g, dtype=torch.float64), 0)
+    w1, w2 = O.diag_bf16_weights(mu, lss)
+    assert torch.equal(O.bf16_round(w1), w1.double()) and torch.equal(O.bf16_round(w2), w2.double())
+    assert torch.equal(O.bf16_round((X * X).float()), X * X)
+    ref = O.estep_diag(X, mu, lss, lpi)
+    got = O.estep_diag_bf16(X, mu, lss, lpi)
+    np.testing.assert_allclose(got[0].numpy(), ref[0].numpy(), atol=2e-5)
+    np.testing.assert_allclose(got[1].numpy(), ref[1].numpy(), rtol=2e-5, atol=1e-9)
+    # r is rounded to bfloat16 for mu_acc and rxsq: visible, and bounded by 2^-8.
+    err_mu = ((got[2] - ref[2]).abs().max() / ref[2].abs().max()).item()
+    err_sig = ((got[3] - ref[3]).abs().max() / ref[3].abs().max()).item()
+    assert 1e-7 < err_mu < 2.0 ** -8 and err_sig < 2.0 ** -7
+
+
+def test_diag_bf16_brute_force_tiny():
+    """Against a scalar loop that rounds to bfloat16 by bit manipulation."""
+    X, mu, lss, lpi = _diag_inputs(N=9, K=3, D=5, seed=23)
+    X, mu, lss = X.float(), mu.float(), lss.float()
+    lz_b, nk_b, mu_b, sig_b = O.brute_estep_diag_bf16(X, mu, lss, lpi)
+    logZ, Nk, mu_acc, sig_acc = O.estep_diag_bf16(X, mu, lss, lpi)
+    np.testing.assert_allclose(logZ.numpy(), lz_b, atol=1e-10)
+    np.testing.assert_allclose(Nk.numpy(), nk_b, rtol=1e-10)
+    np.testing.assert_allclose(mu_acc.numpy(), np.array(mu_b), rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(sig_acc.numpy(), np.array(sig_b), rtol=1e-9, atol=1e-10)
+
+
+def test_diag_bf16_invariants():
+    """Responsibilities sum to one per row; mu_acc sums to the rows' bf16 values up to
+    the bf16 rounding of r."""
+    X, mu, lss, lpi = _diag_inputs(N=500, K=8, D=6, seed=24)
+    logZ, Nk, mu_acc, sig_acc = O.estep_diag_bf16(X.float(), mu.float(), lss.float(), lpi)
+    assert abs(Nk.sum().item() - 500) < 1e-9
+    xb = O.bf16_round(X.float())
+    err = (mu_acc.sum(dim=0) - xb.sum(dim=0)).abs().max() / xb.abs().sum(dim=0).max()
+    assert err < 2.0 ** -8
+    assert (sig_acc > -1e-9).all()
+
+
 # --------------------------------------------------------------------------- full
 
 def test_full_matches_scipy_and_sklearn():
