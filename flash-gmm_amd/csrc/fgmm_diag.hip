@@ -1479,32 +1479,40 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       }
     }
     // Chain u of register i: this wave's own, or (NH > 1) the one part u of the block
-    // wrote to LDS, the parts of a block being waves rg*CB*NH + u*CB + cbw.
-    const float* s0 = ex + (rg * CB * NH + cbw) * 16 * 64 + lane;
+    // wrote to LDS, the parts of a block being waves rg*CB*NH + u*CB + cbw.  The slots
+    // hold registers 4q..4q+3 of a lane as one float4, [wave][q][lane].
+    const f32x4* s0 = reinterpret_cast<const f32x4*>(ex) + (rg * CB * NH + cbw) * 4 * 64 + lane;
     if constexpr (NH > 1) {
-      float* mine = ex + wave * 16 * 64 + lane;
+      f32x4* mine = reinterpret_cast<f32x4*>(ex) + wave * 4 * 64 + lane;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mine[i * 64] = ch[0][i];
+      for (int q = 0; q < 4; ++q) mine[q * 64] = f32x4{ch[0][4 * q], ch[0][4 * q + 1], ch[0][4 * q + 2], ch[0][4 * q + 3]};
       lds_barrier();
     }
     if (active) {
-      const float* rt = rs + buf * TR + rg * 32;
+      const f32x4* rt = reinterpret_cast<const f32x4*>(rs + buf * TR + rg * 32 + 4 * g);
       float r[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float sv[NCH];
+      for (int q = 0; q < 4; ++q) {
+        f32x4 sq[NCH];
 #pragma unroll
         for (int u = 0; u < NCH; ++u) {
           if constexpr (NH == 1) {
-            sv[u] = ch[u][i];
+            sq[u] = f32x4{ch[u][4 * q], ch[u][4 * q + 1], ch[u][4 * q + 2], ch[u][4 * q + 3]};
           } else {
-            sv[u] = s0[u * CB * 16 * 64 + i * 64];
+            sq[u] = s0[(u * CB * 4 + q) * 64];
           }
         }
-        const float ll = bf16_diag_ll<NCH>(c0, sv);
-        const float rv = fast_exp2(ll - rt[acc_row(i, g)]);
-        if (h == 0) nk += rv;
-        r[i] = rv;
+        // Rows acc_row(4q + j, g) = 8q + 4g + j: one float4 of the row state.
+        const f32x4 lz = rt[2 * q];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float sv[NCH];
+#pragma unroll
+          for (int u = 0; u < NCH; ++u) sv[u] = sq[u][j];
+          const float rv = fast_exp2(bf16_diag_ll<NCH>(c0, sv) - lz[j]);
+          if (h == 0) nk += rv;
+          r[4 * q + j] = rv;
+        }
       }
       bf16x8 a[2];
       acc_to_row_operands(r, a);
