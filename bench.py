@@ -217,8 +217,8 @@ def main():
                     choices=sorted(WORKLOADS) + ["stream_em_n1b_k1024_d128"])
     ap.add_argument("--rows", type=int, default=0, help="override N of the streaming workload")
     ap.add_argument("--precision", choices=["fp32", "bf16"], default="fp32",
-                    help="isotropic and diagonal workloads: bf16 runs the H100 variants' bf16 "
-                         "operand contract (FGMM_FLAG_BF16) and is rated against the bf16 matrix peak")
+                    help="bf16 runs the H100 variants' bf16 operand contract (FGMM_FLAG_BF16) "
+                         "and is rated against the bf16 matrix peak")
     ap.add_argument("--recompute", action="store_true",
                     help="pass 2 recomputes the log-joint (FGMM_FLAG_RECOMPUTE) instead of reading "
                          "the copy pass 1 stores")
@@ -253,9 +253,6 @@ def main():
     N, K, D = WORKLOADS[args.workload]
     kind = args.workload.split("_")[0]
     bf16 = args.precision == "bf16"
-    if bf16 and kind not in ("iso", "diag"):
-        print("--precision bf16 applies to the isotropic and diagonal workloads only", file=sys.stderr)
-        sys.exit(2)
     peak = PEAK_BF16_MFMA_TFLOPS if bf16 else PEAK_FP32_MFMA_TFLOPS
     log(f"generating workload {args.workload} on {torch.cuda.get_device_name(dev)}")
     inp = data.make(args.workload, device=dev)
@@ -280,7 +277,8 @@ def main():
         args4 = (inp["X"], inp["mu"], inp["prec_chol"], inp["log_pi"])
         sig = torch.empty(K, D, D, device=dev)
         fn = lambda ph, dense=args.dense: full_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
-                                                          phase=ph, dense=dense, recompute=args.recompute)
+                                                          phase=ph, dense=dense, recompute=args.recompute,
+                                                          precision=args.precision)
     ws_fn = getattr(L, f"fgmm_{kind}_workspace_bytes_ex")
     pflag = _lib.FLAG_BF16 if bf16 else 0
     flags = (_lib.FLAG_RECOMPUTE if args.recompute else 0) | pflag
@@ -348,8 +346,10 @@ def main():
              f"{p2_kernel} (accumulation pass + slab reduction"
              + (", reads the stored log-joint)" if stored_lj else ", recomputes the log-joint)"))
     if bf16:
-        names = (f"{kind}_bf16_lse (log-normaliser pass + prologue, bf16 operands)",
-                 f"{kind}_bf16_accum (accumulation pass + slab reduction, recomputes in bf16)")
+        names = (f"{kind}_bf16_lse (log-normaliser pass + prologue, bf16 operands"
+                 + (", stores the log-joint)" if kind == "full" else ")"),
+                 f"{kind}_bf16_accum (accumulation pass + slab reduction, "
+                 + ("reads the stored log-joint)" if kind == "full" else "recomputes in bf16)"))
     traffic_tab = {} if (args.recompute or bf16) else TRAFFIC_BYTES.get(args.workload, {})
     phases = {}
     for ph, name, t, f, b in (("phase1", names[0], p1, f1, b1), ("phase2", names[1], p2, f2, b2)):

@@ -54,6 +54,7 @@ struct FullPlan {
   int ncg, nslab, rgroups, npart;
   int64_t rows_per_slab;
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
+  bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16); always stores the log-joint
   size_t off_lsw, off_bsw, off_ck, off_rowstat, off_part_sig, off_part_mu, off_part_nk, off_lj, total;
 };
 
@@ -65,19 +66,29 @@ __host__ inline size_t full_lj_bytes(int64_t N, int KP) {
   return (size_t)round_up(cdiv(N, 32), 4) * (size_t)KP * 32 * sizeof(float);
 }
 
-FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true) {
+// Pass-2 layout of the bf16 contract (defined with its kernels below).
+__host__ __device__ constexpr int bf16_comps_per_wg(int NMB);
+__host__ __device__ constexpr int bf16_row_groups(int NMB);
+
+FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf16 = false) {
   FullPlan p{};
   p.N = N; p.K = K; p.D = D;
   p.DP = (int)round_up(D < 1 ? 1 : D, 32);
   p.NMB = p.DP / 32;
   p.NSB = p.NMB * (p.NMB + 1) / 2;
   p.KP = (int)round_up(K, kCompsPerWG);
-  p.lj = allow_lj && K > 0 && full_lj_bytes(N, p.KP) <= kMaxLjBytes;
+  p.bf16 = bf16;
+  p.lj = (allow_lj || bf16) && K > 0 && full_lj_bytes(N, p.KP) <= kMaxLjBytes;
   // Reading the log-joint, pass 2 needs no whitening operands in LDS, and the
   // 4-component kernel serves every D.
-  const bool split = full_accum_split_d(p.DP) && !p.lj;
-  p.ncg = split ? (int)K : p.KP / kCompsPerWG;
-  p.rgroups = split ? 1 : kRowGroups;
+  const bool split = full_accum_split_d(p.DP) && !p.lj && !bf16;
+  if (bf16) {
+    p.ncg = p.KP / bf16_comps_per_wg(p.NMB);
+    p.rgroups = bf16_row_groups(p.NMB);
+  } else {
+    p.ncg = split ? (int)K : p.KP / kCompsPerWG;
+    p.rgroups = split ? 1 : kRowGroups;
+  }
   const int64_t tile_rows = 32 * p.rgroups;
   if (N > 0 && p.ncg > 0) {
     int64_t want = (int64_t)current_device_cus() / p.ncg;
@@ -97,7 +108,8 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true) {
   p.off_bsw = off;      off = align256(off + (size_t)p.KP * p.DP * sizeof(double));
   p.off_ck = off;       off = align256(off + (size_t)p.KP * sizeof(double));
   p.off_rowstat = off;  off = align256(off + (size_t)(N > 0 ? N : 0) * sizeof(double));
-  p.off_part_sig = off; off = align256(off + (size_t)p.npart * p.KP * p.NSB * 1024 * sizeof(float));
+  p.off_part_sig = off;
+  off = align256(off + (size_t)p.npart * p.KP * (bf16 ? p.NMB * p.NMB : p.NSB) * 1024 * sizeof(float));
   p.off_part_mu = off;  off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
   p.off_part_nk = off;  off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
   p.off_lj = off;
@@ -369,8 +381,18 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     if (tid < TR) rs[buf * TR + tid] = rstage;
   };
 
+  // With LJ: the stored log-joint of this wave's component for row c of tile t (0
+  // past the slab, where logZ2 = +inf makes r = 0), loaded one tile ahead where the
+  // register fits (at D = 128 the accumulators leave none).
+  constexpr bool PF = LJ && DP <= 96;
+  auto lj_of = [&](int t) -> float {
+    const int64_t row0 = r_begin + (int64_t)t * TR + rg * 32;
+    return (LJ && active && row0 < r_end) ? lj[((row0 >> 5) * KP + k) * 32 + c] : 0.0f;
+  };
+  float lnext = 0.0f;
   if (ntiles > 0) {
     fetch(0);
+    if (PF) lnext = lj_of(0);
     commit(0);
   }
   __syncthreads();
@@ -384,12 +406,12 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const bool more = t + 1 < ntiles;
     const float* xt = xs + buf * TR * RS + rg * 32 * RS;
     const double* rt = rs + buf * TR + rg * 32;
+    const float l = PF ? lnext : lj_of(t);
+    if (PF && more) lnext = lj_of(t + 1);
     if (active) {
       // r for this lane's row c (both half-waves hold it).
       float rv;
       if constexpr (LJ) {
-        const int64_t row0 = r_begin + (int64_t)t * TR + rg * 32;
-        const float l = row0 < r_end ? lj[((row0 >> 5) * KP + k) * 32 + c] : 0.0f;
         rv = fast_exp2((float)((double)l - rt[c]));
       } else {
         const double maha = maha_one<NMB, NM>(
@@ -737,6 +759,437 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
   return pl.lj ? launch2(std::true_type{}) : launch2(std::false_type{});
 }
 
+// ===========================================================================
+// bf16 operand contract (FGMM_FLAG_BF16), the arithmetic of the reference's full
+// H100 kernels (flash_gmm_full_h100.py:71-139 pass 1, :146-228 pass 2, :289-298
+// constants), in log2 units:
+//   b_k = L_k^T mu_k (fp32),  c_k = (lpi_k + sum_d log(|L_k,dd| + 1e-30) - 0.5 D log 2pi) log2 e
+//   v = bf16(x) . bf16(L_k) - b_k,  maha = ||v||^2,  ll2 = c_k - 0.5 log2 e maha   (fp32)
+//   r = 2^(ll2 - logZ2);  Nk = sum r;  mu_acc = bf16(r)^T bf16(x)
+//   sig_outer_k[d2][d1] = sum_n bf16(r_nk x_n,d2) bf16(x_n,d1)   (not symmetric)
+// Pass 1 whitens on v_mfma_f32_32x32x16_bf16 (V^T = bf16(L)^T bf16(X)^T: lane = row,
+// 16 whitened coordinates per register block) and stores the fp32 log-joint; pass 2
+// reads it back.  Pass 2 forms the A operand bf16(r x_d2) in registers from fp32 X
+// tiles and accumulates every 32x32 block of sig_outer; mu_acc is one more matrix
+// step per row step whose A operand holds bf16(r) of the workgroup's components.
+// ===========================================================================
+
+// Prologue, one 64-thread block per component (k < KP):
+//   lop[k][mb][q][lane] (bf16x8) = bf16(L[k][16q + 8g + e][32 mb + c]), the A operand
+//   bsw[k][mb][g][i]    (fp32)   = b[k][32 mb + acc_row(i, g)]
+//   ck[k]               (fp32)
+__global__ __launch_bounds__(64) void full_bf16_prep(const float* __restrict__ mu, int64_t ldmu,
+                                                     const float* __restrict__ L, int64_t K, int D,
+                                                     int DP, const float* __restrict__ lpi,
+                                                     bf16x8* __restrict__ lop, float* __restrict__ bsw,
+                                                     float* __restrict__ ck) {
+  __shared__ double sb[128];   // DP <= 128
+  const int64_t k = blockIdx.x;
+  const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  const bool valid = k < K;
+  const float* Lk = L + k * (int64_t)D * D;
+  for (int j = lane; j < DP; j += 64) {
+    double b = 0.0;
+    if (valid && j < D)
+      for (int i = 0; i < D; ++i) b = fma((double)Lk[(int64_t)i * D + j], (double)mu[k * ldmu + i], b);
+    sb[j] = b;
+  }
+  if (lane == 0) {
+    double c0 = -INFINITY;
+    if (valid) {
+      double ld = 0.0;
+      for (int d = 0; d < D; ++d) ld += log(fabs((double)Lk[(int64_t)d * D + d]) + 1e-30);
+      c0 = ((double)lpi[k] + ld - 0.5 * (double)D * kLog2Pi) * kLog2e;
+    }
+    ck[k] = (float)c0;
+  }
+  const int NMB = DP / 32, NQ = DP / 16;
+  for (int mb = 0; mb < NMB; ++mb) {
+    const int j = 32 * mb + c;
+    for (int q = 0; q < NQ; ++q) {
+      bf16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = 16 * q + 8 * g + e;
+        v[e] = (__bf16)((valid && i < D && j < D) ? Lk[(int64_t)i * D + j] : 0.0f);
+      }
+      lop[((k * NMB + mb) * NQ + q) * 64 + lane] = v;
+    }
+  }
+  __syncthreads();
+  for (int mb = 0; mb < NMB; ++mb) {
+    if (lane < 32) {
+      const int gg = lane >> 4, i = lane & 15;
+      bsw[(k * NMB + mb) * 32 + gg * 16 + i] = (float)sb[32 * mb + acc_row(i, gg)];
+    }
+  }
+}
+
+// Pass 1: grid over 128-row tiles, 4 waves of 32 rows; one component's bf16 L^T, b
+// and c stream through an LDS double buffer.  Writes logZ, logZ2 and the log-joint.
+template <int DP>
+constexpr size_t bf16_lse_lds_bytes() {
+  return (size_t)2 * DP * DP * 2 + (size_t)2 * (DP + 4) * sizeof(float);
+}
+
+template <int DP>
+__global__ __launch_bounds__(kThreads) void full_bf16_lse(const float* __restrict__ X, int64_t ldx,
+                                                          int64_t N, int D,
+                                                          const bf16x8* __restrict__ lop,
+                                                          const float* __restrict__ bsw,
+                                                          const float* __restrict__ ck, int K, int KP,
+                                                          float* __restrict__ logZ,
+                                                          float* __restrict__ rowstat,
+                                                          float* __restrict__ lj) {
+  constexpr int NMB = DP / 32, NQ = DP / 16;
+  constexpr int BLK = NMB * NQ * 64;              // bf16x8 per component
+  constexpr int LPT = (BLK + kThreads - 1) / kThreads;
+  constexpr int BW = DP + 4;                      // floats per component stage (b, then c)
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  bf16x8* l_l = reinterpret_cast<bf16x8*>(lds_raw);                                // [2][BLK]
+  float* b_l = reinterpret_cast<float*>(lds_raw + 2 * BLK * sizeof(bf16x8));       // [2][BW]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t tile = (int64_t)blockIdx.x * kWaves + wave;   // 32-row tile
+  const int64_t row = tile * 32 + c;
+  const bool valid = row < N;
+  float* ljt = lj + tile * KP * 32 + c;
+
+  bf16x8 st[LPT];
+  float bst = 0.0f;
+  auto fetch = [&](int k) {
+    const bf16x8* src = lop + (int64_t)k * BLK;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q)
+      if (BLK % kThreads == 0 || q * kThreads + tid < BLK) st[q] = src[q * kThreads + tid];
+    if (tid < DP) bst = bsw[(int64_t)k * DP + tid];
+    else if (tid == DP) bst = ck[k];
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < LPT; ++q)
+      if (BLK % kThreads == 0 || q * kThreads + tid < BLK) l_l[buf * BLK + q * kThreads + tid] = st[q];
+    if (tid <= DP) b_l[buf * BW + tid] = bst;
+  };
+  fetch(0);
+  // B operand: this lane's row, dimensions 16q + 8g + e, rounded to bf16.
+  bf16x8 xb[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int d0 = 16 * q + 8 * g;
+    xb[q] = to_bf16x8(load_row4(X, ldx, row, d0, D, valid), load_row4(X, ldx, row, d0 + 4, D, valid));
+  }
+  commit(0);
+  lds_barrier();
+
+  const float hl = (float)(0.5 * kLog2e);
+  float mx = -INFINITY, sm = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const int buf = k & 1;
+    const bool more = k + 1 < K;
+    if (more) fetch(k + 1);
+    const bf16x8* la = l_l + buf * BLK + lane;
+    const float* bb = b_l + buf * BW + g * 16;
+    float maha = 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+      // V^T block mb: lane = row, register i = coordinate 32 mb + acc_row(i, g).
+      f32x16 v = zero16();
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) v = mfma_bf16(la[(mb * NQ + q) * 64], xb[q], v);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float t = v[i] - bb[mb * 32 + i];
+        maha = fmaf(t, t, maha);
+      }
+    }
+    maha += __shfl_xor(maha, 32);
+    const float ll = b_l[buf * BW + DP] - hl * maha;
+    if (g == 0) ljt[k * 32] = ll;
+    const float mn = fmaxf(mx, ll);
+    const float ms = (mn == -INFINITY) ? 0.0f : mn;
+    sm = sm * fast_exp2(mx - ms) + fast_exp2(ll - ms);
+    mx = mn;
+    if (more) commit(buf ^ 1);
+    lds_barrier();
+  }
+  const float lz2 = mx + log2f(sm);
+  if (valid && g == 0) {
+    rowstat[row] = lz2;
+    if (logZ) logZ[row] = lz2 * (float)kLn2;
+  }
+}
+
+// Pass 2 layout: waves per component = NMB (wave owns the 32 rows d2 of block mb2 of
+// sig_outer and all NMB column blocks), components per workgroup and row groups so
+// that the 8 waves are used (D = 96: 6 of them).
+__host__ __device__ constexpr int bf16_comps_per_wg(int NMB) { return NMB <= 2 ? 4 : 2; }
+__host__ __device__ constexpr int bf16_row_groups(int NMB) { return NMB == 1 ? 2 : 1; }
+
+template <int DP>
+constexpr size_t bf16_accum_lds_bytes() {
+  constexpr int NMB = DP / 32;
+  constexpr int TR = 32 * bf16_row_groups(NMB);
+  return (size_t)2 * TR * DP * sizeof(float)      // X tiles, fp32, row-octet interleaved
+         + (size_t)2 * TR * DP * 2                // X tiles, bf16, row-octet interleaved
+         + (size_t)2 * TR * sizeof(float)         // logZ2
+         + (size_t)kAccWaves * 32 * sizeof(float); // r per wave
+}
+
+// X tile element (r, d) of the interleaved layouts sits at ((r / 8) DP + d) 8 + r % 8:
+// the 8 consecutive rows of one column that an operand lane-half needs are contiguous.
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
+void full_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int K, int KP,
+                     const float* __restrict__ rowstat, const float* __restrict__ lj, int nslab,
+                     int64_t rows_per_slab, float* __restrict__ part_sig, float* __restrict__ part_mu,
+                     float* __restrict__ part_nk, int dense) {
+  constexpr int NMB = DP / 32;
+  constexpr int CPWG = bf16_comps_per_wg(NMB);
+  constexpr int RG = bf16_row_groups(NMB);
+  constexpr int TR = 32 * RG;
+  constexpr int V4 = DP / 4;
+  constexpr int NV = TR * V4;                     // float4 per tile
+  constexpr int LPT = (NV + kAccThreads - 1) / kAccThreads;
+  static_assert(CPWG * NMB * RG <= kAccWaves, "waves cover the work");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  float* xf = reinterpret_cast<float*>(lds_raw);                           // [2][TR/8][DP][8]
+  __bf16* xh = reinterpret_cast<__bf16*>(xf + 2 * TR * DP);                // [2][TR/8][DP][8]
+  float* rs = reinterpret_cast<float*>(xh + 2 * TR * DP);                  // [2][TR]
+  float* r_l = rs + 2 * TR;                                                // [8][32]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  // wave = (rg * NMB + mb2) * CPWG + cw
+  const bool in_use = wave < CPWG * NMB * RG;     // D = 96 leaves two waves idle
+  const int cw = wave % CPWG, mb2 = (wave / CPWG) % NMB, rg = in_use ? wave / (CPWG * NMB) : 0;
+  const int slab = blockIdx.x % nslab;
+  const int cg = blockIdx.x / nslab;
+  const int k = cg * CPWG + cw;
+  const bool active = in_use && k < K;
+  const bool mu_wave = in_use && cw == 0;         // also accumulates mu_acc block mb2
+  auto r_wave = [&](int comp) { return (rg * NMB) * CPWG + comp; };   // mb2 = 0 wave of comp
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
+
+  f32x16 acc[NMB];
+#pragma unroll
+  for (int mb = 0; mb < NMB; ++mb) acc[mb] = zero16();
+  f32x16 macc = zero16();
+  float nk = 0.0f;
+
+  f32x4 stage[LPT];
+  float rstage = INFINITY;
+  const bool full_d = (D == DP);
+  auto tile_row = [](int idx) { return ((idx >> 3) / V4) * 8 + (idx & 7); };
+  auto tile_col = [](int idx) { return ((idx >> 3) % V4) * 4; };
+  auto fetch = [&](int t) {
+    const int64_t row0 = r_begin + (int64_t)t * TR;
+    if (full_d && row0 + TR <= r_end) {
+      const float* src = X + row0 * ldx;
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        if (NV % kAccThreads == 0 || idx < NV)
+          stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)tile_row(idx) * ldx + tile_col(idx));
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < LPT; ++q) {
+        const int idx = q * kAccThreads + tid;
+        const int64_t row = row0 + tile_row(idx);
+        if (NV % kAccThreads == 0 || idx < NV)
+          stage[q] = load_row4(X, ldx, row, tile_col(idx), D, row < r_end);
+      }
+    }
+    if (tid < TR) {
+      const int64_t row = row0 + tid;
+      rstage = (row < r_end) ? rowstat[row] : INFINITY;   // r = 0 past the slab
+    }
+  };
+  auto commit = [&](int buf) {
+    float* df = xf + buf * TR * DP;
+    __bf16* dh = xh + buf * TR * DP;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      if (NV % kAccThreads != 0 && idx >= NV) continue;
+      const int r = tile_row(idx), d = tile_col(idx);
+      const f32x4 v = stage[q];
+      const int o = ((r >> 3) * DP + d) * 8 + (r & 7);
+      df[o] = v.x; df[o + 8] = v.y; df[o + 16] = v.z; df[o + 24] = v.w;
+      dh[o] = (__bf16)v.x; dh[o + 8] = (__bf16)v.y; dh[o + 16] = (__bf16)v.z; dh[o + 24] = (__bf16)v.w;
+    }
+    if (tid < TR) rs[buf * TR + tid] = rstage;
+  };
+
+  // This wave's component's stored log-joint for row c of tile t (0 past the slab,
+  // where logZ2 = +inf makes r = 0); loaded one tile ahead.
+  auto lj_of = [&](int t) -> float {
+    const int64_t row0 = r_begin + (int64_t)t * TR + rg * 32;
+    return (active && row0 < r_end) ? lj[((row0 >> 5) * KP + k) * 32 + c] : 0.0f;
+  };
+  float lnext = 0.0f;
+  if (ntiles > 0) {
+    fetch(0);
+    lnext = lj_of(0);
+    commit(0);
+  }
+  lds_barrier();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    const float l = lnext;
+    if (more) lnext = lj_of(t + 1);
+    // r of this wave's component for row c.
+    if (active) {
+      const float rv = fast_exp2(l - rs[buf * TR + rg * 32 + c]);
+      if (g == 0) {
+        r_l[wave * 32 + c] = rv;
+        if (mb2 == 0) nk += rv;
+      }
+    }
+    if (more) fetch(t + 1);
+    lds_barrier();
+    const float* xa = xf + buf * TR * DP;
+    const __bf16* xb = xh + buf * TR * DP;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      // Rows rg*32 + 16p + 8g + e of this step: row octet rg*4 + 2p + g.
+      const int oct = rg * 4 + 2 * p + g;
+      bf16x8 bop[NMB];
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb)
+        bop[mb] = in_use ? *reinterpret_cast<const bf16x8*>(xb + (oct * DP + 32 * mb + c) * 8) : bf16x8{};
+      if (active) {
+        // A = bf16(r x_d2): lane = d2 = 32 mb2 + c, elements = the 8 rows.
+        const f32x4* rr = reinterpret_cast<const f32x4*>(r_l + wave * 32 + 16 * p + 8 * g);
+        const f32x4* xx = reinterpret_cast<const f32x4*>(xa + (oct * DP + 32 * mb2 + c) * 8);
+        const bf16x8 a = to_bf16x8(rr[0] * xx[0], rr[1] * xx[1]);
+        // A step whose 16 rows x 32 coordinates of bf16(r x) are all zero adds nothing.
+        if (dense || any_nonzero(a)) {
+#pragma unroll
+          for (int mb = 0; mb < NMB; ++mb) acc[mb] = mfma_bf16(a, bop[mb], acc[mb]);
+        }
+      }
+      if (mu_wave) {
+        // A = bf16(r) of the workgroup's components (rows m = component), B = block mb2.
+        bf16x8 a = {};
+        if (c < CPWG && cg * CPWG + c < K) {
+          const f32x4* rr = reinterpret_cast<const f32x4*>(r_l + r_wave(c) * 32 + 16 * p + 8 * g);
+          a = to_bf16x8(rr[0], rr[1]);
+        }
+        // B = column block mb2 (mb2 is not a compile-time index: read it again).
+        const bf16x8 bm = *reinterpret_cast<const bf16x8*>(xb + (oct * DP + 32 * mb2 + c) * 8);
+        if (dense || any_nonzero(a)) macc = mfma_bf16(a, bm, macc);
+      }
+    }
+    if (more) commit(buf ^ 1);
+    lds_barrier();
+  }
+
+  const int64_t pbase0 = ((int64_t)slab * RG + rg) * KP + (int64_t)cg * CPWG;
+  if (active) {
+    float* ps = part_sig + ((pbase0 + cw) * NMB * NMB + mb2 * NMB) * 1024;
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) ps[mb * 1024 + acc_row(i, g) * 32 + c] = acc[mb][i];
+    }
+    if (mb2 == 0) {
+      float s = nk;
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+      if (lane == 0) part_nk[pbase0 + cw] = s;
+    }
+  }
+  if (mu_wave && g == 0) {
+    // Register i of half 0 holds component acc_row(i, 0) = i.
+#pragma unroll
+    for (int i = 0; i < CPWG; ++i)
+      if (cg * CPWG + i < K) part_mu[(pbase0 + i) * DP + 32 * mb2 + c] = macc[i];
+  }
+}
+
+// Finish of the bf16 contract: every element of sig_outer from its own block (no
+// mirroring), fixed-order fp64 sums over the partials.
+__global__ __launch_bounds__(256) void full_bf16_reduce(const float* __restrict__ part_sig,
+                                                        const float* __restrict__ part_mu,
+                                                        const float* __restrict__ part_nk, int npart,
+                                                        int KP, int DP, int NMB, int64_t K, int D,
+                                                        float* __restrict__ Nk, float* __restrict__ mu_acc,
+                                                        float* __restrict__ sig_outer, int accumulate) {
+  const int NB2 = NMB * NMB;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nsig = K * D * D;
+  if (idx < nsig) {
+    const int64_t k = idx / ((int64_t)D * D);
+    const int rem = (int)(idx % ((int64_t)D * D));
+    const int d2 = rem / D, d1 = rem % D;
+    const int blk = (d2 / 32) * NMB + d1 / 32;
+    const double s = strided_sum(part_sig + ((int64_t)k * NB2 + blk) * 1024 + (d2 % 32) * 32 + d1 % 32,
+                                 npart, (int64_t)KP * NB2 * 1024);
+    float* o = sig_outer + idx;
+    *o = accumulate ? (float)((double)*o + s) : (float)s;
+    return;
+  }
+  const int64_t j = idx - nsig;
+  if (j < K * D) {
+    const int64_t k = j / D;
+    const int d = (int)(j % D);
+    const double s = strided_sum(part_mu + k * DP + d, npart, (int64_t)KP * DP);
+    float* o = mu_acc + j;
+    *o = accumulate ? (float)((double)*o + s) : (float)s;
+    return;
+  }
+  const int64_t kk = j - K * D;
+  if (kk < K) {
+    const double s = strided_sum(part_nk + kk, npart, KP);
+    Nk[kk] = accumulate ? (float)((double)Nk[kk] + s) : (float)s;
+  }
+}
+
+template <int DP>
+hipError_t launch_bf16(const FullPlan& pl, const float* X, int64_t ldx, unsigned char* ws, float* logZ,
+                       bool run1, bool run2, bool dense, hipStream_t stream) {
+  const bf16x8* lop = reinterpret_cast<const bf16x8*>(ws + pl.off_lsw);
+  const float* bsw = reinterpret_cast<const float*>(ws + pl.off_bsw);
+  const float* ck = reinterpret_cast<const float*>(ws + pl.off_ck);
+  float* rowstat = reinterpret_cast<float*>(ws + pl.off_rowstat);
+  float* lj = reinterpret_cast<float*>(ws + pl.off_lj);
+  if (run1) {
+    constexpr size_t lds1 = bf16_lse_lds_bytes<DP>();
+    if (lds1 > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&full_bf16_lse<DP>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(full_bf16_lse<DP>, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
+                       stream, X, ldx, pl.N, (int)pl.D, lop, bsw, ck, (int)pl.K, pl.KP, logZ, rowstat, lj);
+  }
+  if (!run2) return hipGetLastError();
+  constexpr size_t lds2 = bf16_accum_lds_bytes<DP>();
+  static_assert(lds2 <= (size_t)160 * 1024, "pass-2 tiles fit LDS");
+  if (lds2 > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&full_bf16_accum<DP>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(full_bf16_accum<DP>, dim3((unsigned)(pl.nslab * pl.ncg)), dim3(kAccThreads), lds2,
+                     stream, X, ldx, pl.N, (int)pl.D, (int)pl.K, pl.KP, rowstat, lj, pl.nslab,
+                     pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_sig),
+                     reinterpret_cast<float*>(ws + pl.off_part_mu),
+                     reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
+  return hipGetLastError();
+}
+
 }  // namespace
 }  // namespace fgmm
 
@@ -749,7 +1202,7 @@ extern "C" size_t fgmm_full_workspace_bytes(int64_t N, int64_t K, int64_t D) {
 
 extern "C" size_t fgmm_full_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE)).total;
+  return make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE), (flags & FGMM_FLAG_BF16) != 0).total;
 }
 
 extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -762,7 +1215,6 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   const bool accumulate = (flags & FGMM_FLAG_ACCUMULATE) != 0;
   const bool dense = (flags & FGMM_FLAG_DENSE) != 0;
   if (N < 0 || K < 0 || D < 1) return FGMM_ERR_INVALID_ARG;
-  if (flags & FGMM_FLAG_BF16) return FGMM_ERR_UNSUPPORTED;
   if (N > 0 && (X == nullptr || ldx < round_up(D, 4) || (ldx % 4) != 0 ||
                 (reinterpret_cast<uintptr_t>(X) & 15) != 0))
     return FGMM_ERR_INVALID_ARG;
@@ -772,7 +1224,10 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     return FGMM_ERR_INVALID_ARG;
   if (D > 128) return FGMM_ERR_UNSUPPORTED;
   if (N > kMaxRows || K > (int64_t)1 << 20) return FGMM_ERR_UNSUPPORTED;
-  const FullPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE));
+  const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
+  const FullPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE), bf16);
+  // The bf16 contract always stores the log-joint: N x K floats within kMaxLjBytes.
+  if (bf16 && K > 0 && !pl.lj) return FGMM_ERR_UNSUPPORTED;
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;
   unsigned char* ws = static_cast<unsigned char*>(workspace);
@@ -785,24 +1240,41 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
                          -INFINITY);
     return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
   }
-  if (run1)
+  if (run1 && bf16)
+    hipLaunchKernelGGL(full_bf16_prep, dim3((unsigned)pl.KP), dim3(64), 0, stream, mu, ldmu, prec_chol, K,
+                       (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_lsw),
+                       reinterpret_cast<float*>(ws + pl.off_bsw), reinterpret_cast<float*>(ws + pl.off_ck));
+  else if (run1)
     hipLaunchKernelGGL(full_prep, dim3((unsigned)pl.KP), dim3(64), 0, stream, mu, ldmu, prec_chol, K,
                        (int)D, pl.DP, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_lsw),
                        reinterpret_cast<double*>(ws + pl.off_bsw),
                        reinterpret_cast<double*>(ws + pl.off_ck));
   if (N > 0) {
+    auto run = [&](auto dp_tag) -> hipError_t {
+      constexpr int DP = decltype(dp_tag)::value;
+      return bf16 ? launch_bf16<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream)
+                  : launch_passes<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
+    };
     hipError_t e = hipSuccess;
     switch (pl.DP) {
-      case 32: e = launch_passes<32>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 64: e = launch_passes<64>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 96: e = launch_passes<96>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
-      case 128: e = launch_passes<128>(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
+      case 32: e = run(std::integral_constant<int, 32>{}); break;
+      case 64: e = run(std::integral_constant<int, 64>{}); break;
+      case 96: e = run(std::integral_constant<int, 96>{}); break;
+      case 128: e = run(std::integral_constant<int, 128>{}); break;
       default: return FGMM_ERR_UNSUPPORTED;
     }
     if (e != hipSuccess) return FGMM_ERR_HIP;
   }
   if (!run2) return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
   const int64_t nthreads = K * D * D + K * D + K;
+  if (bf16) {
+    hipLaunchKernelGGL(full_bf16_reduce, dim3((unsigned)cdiv(nthreads, 256)), dim3(256), 0, stream,
+                       reinterpret_cast<const float*>(ws + pl.off_part_sig),
+                       reinterpret_cast<const float*>(ws + pl.off_part_mu),
+                       reinterpret_cast<const float*>(ws + pl.off_part_nk), pl.npart, pl.KP, pl.DP,
+                       pl.NMB, K, (int)D, Nk, mu_acc, sig_outer, accumulate ? 1 : 0);
+    return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+  }
   hipLaunchKernelGGL(full_reduce, dim3((unsigned)cdiv(nthreads, 256)), dim3(256), 0, stream,
                      reinterpret_cast<const float*>(ws + pl.off_part_sig),
                      reinterpret_cast<const float*>(ws + pl.off_part_mu),

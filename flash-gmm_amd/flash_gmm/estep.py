@@ -273,9 +273,19 @@ def flash_gmm_estep_diag(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.
 def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
                     accumulate: bool = False, workspace: torch.Tensor | None = None,
                     phase: int = 0, dense: bool = False,
-                    recompute: bool = False) -> None:
-    """Full-covariance E-step into caller-provided outputs (sig_outer is (K, D, D))."""
+                    recompute: bool = False, precision: str = "fp32") -> None:
+    """Full-covariance E-step into caller-provided outputs (sig_outer is (K, D, D)).
+
+    ``precision="bf16"`` selects the bf16 operand contract of the reference's full
+    H100 kernels (flash_gmm_full_h100.py:71-228): x and L rounded to bfloat16 for the
+    whitening, L^T mu in float32, r rounded to bfloat16 for mu_acc and r x_d2 for
+    sig_outer[k, d2, :] (which is then not exactly symmetric), fp32 accumulation and
+    log-sum-exp.  That path always stores the log-joint (``recompute`` has no
+    effect) and takes at most 16 GiB / (4 K) rows per call; larger inputs go in row
+    chunks with ``accumulate``.
+    """
     _check_common(X, mu, log_pi)
+    _require(precision in ("fp32", "bf16"), f"precision must be 'fp32' or 'bf16', got {precision!r}")
     N, D = X.shape
     K = mu.shape[0]
     dev = X.device
@@ -293,6 +303,8 @@ def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
         flags |= _lib.FLAG_DENSE
     if recompute:
         flags |= _lib.FLAG_RECOMPUTE
+    if precision == "bf16":
+        flags |= _lib.FLAG_BF16
     workspace = _workspace(L.fgmm_full_workspace_bytes_ex, N, K, D, flags, dev, workspace)
     _check_out("Nk", Nk, (K,), dev)
     _check_out("mu_acc", mu_acc, (K, D), dev)
@@ -309,11 +321,13 @@ def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
 
 
 def flash_gmm_estep_full(X: torch.Tensor, mu: torch.Tensor, prec_chol: torch.Tensor,
-                         log_pi: torch.Tensor):
+                         log_pi: torch.Tensor, *, precision: str = "fp32"):
     """Full-covariance E-step: returns (logZ, Nk, mu_acc, sig_outer[K, D, D]).
 
     prec_chol[k] is lower-triangular with prec_chol[k] @ prec_chol[k].T = Sigma_k^-1;
     sig_outer[k] = sum_n r_nk x_n x_n^T (flash_gmm_full_h100.py:245-260).
+    ``precision="bf16"`` follows the reference kernels' bf16 operand contract
+    instead of fp32 arithmetic.
     """
     _check_common(X, mu, log_pi)
     N, D = X.shape
@@ -325,5 +339,5 @@ def flash_gmm_estep_full(X: torch.Tensor, mu: torch.Tensor, prec_chol: torch.Ten
     Nk = torch.empty(K, device=dev, dtype=torch.float32)
     mu_acc = torch.empty(K, D, device=dev, dtype=torch.float32)
     sig_outer = torch.empty(K, D, D, device=dev, dtype=torch.float32)
-    full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer)
+    full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, precision=precision)
     return logZ, Nk, mu_acc, sig_outer

@@ -30,6 +30,10 @@ Parity pinning (what checks each function, see tests/test_oracle.py):
   already exact in bfloat16 (weights that are powers of two, x with few
   significant bits) and within the bf16 rounding of r for mu_acc and sig_acc; an
   independent scalar-loop version with bit-level rounding on tiny inputs.
+* ``estep_full_bf16`` -- the bf16 operand contract of the reference's full H100
+  kernels: equal to ``estep_full`` (logZ, Nk) when x and L are already exact in
+  bfloat16, within the bf16 rounding of r (and of r x for sig_outer) for the
+  statistics; an independent scalar-loop version on tiny inputs.
 * ``estep_full`` -- scipy logpdf with the full covariance recovered from the
   precision Cholesky factor, sklearn 'full' internals, brute force, reduction
   to ``estep_diag`` for diagonal factors.
@@ -316,6 +320,49 @@ def estep_full(X: Tensor, mu: Tensor, prec_chol: Tensor, log_pi: Tensor, *,
     return logZ, Nk, mu_acc, sig_outer
 
 
+def estep_full_bf16(X: Tensor, mu: Tensor, prec_chol: Tensor, log_pi: Tensor, *,
+                    chunk: int = 1024) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Full-covariance E-step with the bf16 operand contract of flash_gmm_full_h100.py.
+
+    x and L^T are rounded to bfloat16 (:98, :176, :298); b = L^T mu stays float32
+    (:290); v = bf16(x) . bf16(L^T)^T - b and maha = sum v^2 (:125-127, :192-194);
+    ll2 = c0 - 0.5 log2e maha with c0 = (lpi + sum_d log(|L_dd| + 1e-30) - 0.5 D
+    log 2pi) log2e (:294-296, :196); r = 2^(ll2 - logZ2) (:198); Nk = sum r (:203);
+    mu_acc = bf16(r)^T bf16(x) (:200, :207); sig_outer[k, d2, :] = sum_n
+    bf16(r_nk x_nd2) bf16(x_n) with x_nd2 the float32 value (:216-222), which is not
+    symmetric; logZ = logZ2 ln 2 (:335).  Everything except the roundings is float64
+    here (the reference accumulates in float32).
+    """
+    X32, mu32 = _as(X, torch.float32), _as(mu, torch.float32)
+    L32, lpi = _as(prec_chol, torch.float32), _as(log_pi, torch.float64)
+    N, D = X32.shape
+    K = mu32.shape[0]
+    if L32.shape != (K, D, D):
+        raise ValueError(f"prec_chol must be (K, D, D)=({K}, {D}, {D}), got {tuple(L32.shape)}")
+    Lb = bf16_round(L32)                                            # L_bf[k, d1, d2]
+    b = torch.einsum("kij,ki->kj", L32.double(), mu32.double())     # (L^T mu)[k, d2]
+    log_diag_sum = torch.log(L32.double().diagonal(dim1=-2, dim2=-1).abs() + 1e-30).sum(dim=-1)
+    c0 = (lpi + log_diag_sum - 0.5 * D * LOG_2PI) * LOG2_E
+    logZ = torch.empty(N, dtype=torch.float64)
+    Nk = torch.zeros(K, dtype=torch.float64)
+    mu_acc = torch.zeros(K, D, dtype=torch.float64)
+    sig_outer = torch.zeros(K, D, D, dtype=torch.float64)
+    ln2 = math.log(2.0)
+    for n0 in range(0, N, chunk):
+        x32 = X32[n0:n0 + chunk]
+        xb = bf16_round(x32)
+        v = torch.einsum("kij,ni->nkj", Lb, xb) - b[None, :, :]
+        ll2 = c0[None, :] - 0.5 * LOG2_E * (v * v).sum(dim=2)
+        lz2 = torch.logsumexp(ll2 * ln2, dim=1) / ln2
+        logZ[n0:n0 + chunk] = lz2 * ln2
+        r = torch.exp2(ll2 - lz2[:, None])
+        Nk += r.sum(dim=0)
+        mu_acc += bf16_round(r).T @ xb
+        rx = bf16_round(r[:, :, None] * x32.double()[:, None, :])   # (n, k, d2)
+        sig_outer += torch.einsum("nki,nj->kij", rx, xb)
+    return logZ, Nk, mu_acc, sig_outer
+
+
 # ---------------------------------------------------------------------------
 # M-steps (README.md:59-61, :99-100; flash_gmm_full_h100.py:257-260)
 # ---------------------------------------------------------------------------
@@ -443,6 +490,52 @@ def brute_estep_diag_bf16(X, mu, lss, lpi):
     sig_acc = [[rxsq[k][d] - 2.0 * mu[k][d] * mu_acc[k][d] + mu[k][d] ** 2 * Nk[k] for d in range(D)]
                for k in range(K)]
     return logZ, Nk, mu_acc, sig_acc
+
+
+def brute_estep_full_bf16(X, mu, L, lpi):
+    """Scalar-loop version of estep_full_bf16 for tiny inputs (bit-level bf16 rounding)."""
+    import struct
+
+    def f32(v):
+        return struct.unpack("<f", struct.pack("<f", v))[0]
+
+    X = [[float(v) for v in row] for row in X.tolist()]
+    mu = [[float(v) for v in row] for row in mu.tolist()]
+    L = [[[float(v) for v in row] for row in Lk] for Lk in L.tolist()]
+    lpi = [float(v) for v in lpi.tolist()]
+    N, D, K = len(X), len(X[0]) if X else 0, len(mu)
+    ln2 = math.log(2.0)
+    c0, bvec = [], []
+    for k in range(K):
+        ld = sum(math.log(abs(L[k][d][d]) + 1e-30) for d in range(D))
+        c0.append((lpi[k] + ld - 0.5 * D * LOG_2PI) / ln2)
+        bvec.append([sum(L[k][i][j] * mu[k][i] for i in range(D)) for j in range(D)])
+    logZ, Nk = [], [0.0] * K
+    mu_acc = [[0.0] * D for _ in range(K)]
+    sig = [[[0.0] * D for _ in range(D)] for _ in range(K)]
+    for n in range(N):
+        xb = [_bf16_scalar(v) for v in X[n]]
+        ll2 = []
+        for k in range(K):
+            maha = 0.0
+            for j in range(D):
+                vj = sum(xb[i] * _bf16_scalar(L[k][i][j]) for i in range(D)) - bvec[k][j]
+                maha += vj * vj
+            ll2.append(c0[k] - 0.5 / ln2 * maha)
+        m = max(ll2)
+        lz2 = m + math.log2(sum(2.0 ** (v - m) for v in ll2))
+        logZ.append(lz2 * ln2)
+        for k in range(K):
+            r = 2.0 ** (ll2[k] - lz2)
+            Nk[k] += r
+            rb = _bf16_scalar(r)
+            for d in range(D):
+                mu_acc[k][d] += rb * xb[d]
+            for d2 in range(D):
+                a = _bf16_scalar(f32(r * X[n][d2]))
+                for d1 in range(D):
+                    sig[k][d2][d1] += a * xb[d1]
+    return logZ, Nk, mu_acc, sig
 
 
 def brute_estep_iso(X, mu, lss, lpi):

@@ -17,13 +17,32 @@ REL = 1e-4
 # ~ ||x||^2) remains; logZ is checked at 2e-3 (the contract itself is ~1 away from
 # the fp64 result on clustered data), the statistics at REL.
 LOGZ_ATOL_BF16 = 2e-3
+# Under the bf16 contract, mu_acc and the diagonal / full second moments sum products
+# whose factor r (or r x) is rounded to bf16.  The kernel's fp32 r differs from the
+# oracle's float64 r in the last bits, and that moves a product's bf16 rounding by one
+# unit (2^-8 relative) now and then: with r perturbed by 1e-6 relative, the oracle's
+# own sig_outer moves by 1.2e-4 of a component's largest entry, and single entries
+# near zero by 10% (overlapping components, N=4000, K=16, D=32).  These statistics are
+# therefore checked norm-wise per component, at 1e-3 (the reference states 5e-3 for
+# this contract, flash_gmm_h100.py:276); Nk and the isotropic sig_acc, formed from
+# the fp32 r, keep the float32 bounds.
+REL_BF16_STATS = 1e-3
 
 
 def _np(t):
     return t.detach().double().cpu().numpy()
 
 
-def assert_close_stats(got, ref, what="", logz_atol=LOGZ_ATOL):
+def _per_component_normwise(g, r, rel, what):
+    if not r.size:
+        return
+    gk, rk = g.reshape(r.shape[0], -1), r.reshape(r.shape[0], -1)
+    scale = np.abs(rk).max(axis=1) + 1e-6 * np.abs(rk).max()
+    err = np.abs(gk - rk).max(axis=1)
+    assert (err <= rel * scale).all(), f"{what} per-component norm-wise err {(err / scale).max()}"
+
+
+def assert_close_stats(got, ref, what="", logz_atol=LOGZ_ATOL, bf16_stats=False):
     lz, nk, mu_acc, sig = (_np(t) for t in got)
     rlz, rnk, rmu, rsig = (np.asarray(t, dtype=np.float64) for t in ref)
     if rlz.size:
@@ -31,6 +50,12 @@ def assert_close_stats(got, ref, what="", logz_atol=LOGZ_ATOL):
         finite = np.isfinite(rlz)
         assert np.array_equal(np.isfinite(lz), finite), f"{what} logZ finiteness"
         assert err[finite].max(initial=0) <= logz_atol, f"{what} logZ max abs err {err[finite].max()}"
+    if bf16_stats:
+        _per_component_normwise(mu_acc, rmu, REL_BF16_STATS, f"{what} mu_acc")
+        if rsig.ndim > 1:
+            _per_component_normwise(sig, rsig, REL_BF16_STATS, f"{what} sig")
+            rsig = rsig[:0]
+        rmu = rmu[:0]
     for name, g, r in (("Nk", nk, rnk), ("sig", sig, rsig)):
         if r.size:
             tol = REL * np.abs(r) + 1e-6 * np.abs(r).max(initial=0)

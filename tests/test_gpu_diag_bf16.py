@@ -40,20 +40,31 @@ def test_edge_shapes(N, K, D, gpu_device):
     inp = data.diag_clustered(N, K, D, seed=N + K + D)
     print(f"diag bf16 N={N} K={K} D={D}", flush=True)
     got = _into(inp, gpu_device)
-    assert_close_stats(got, oracle(inp), f"diag bf16 N={N} K={K} D={D}", logz_atol=LOGZ_ATOL_BF16)
+    assert_close_stats(got, oracle(inp), f"diag bf16 N={N} K={K} D={D}", logz_atol=LOGZ_ATOL_BF16, bf16_stats=True)
 
 
 def test_entry_point(gpu_device):
     inp = data.diag_clustered(3000, 64, 48, seed=12)
     got = flash_gmm_estep_diag(*[inp[k].to(gpu_device) for k in KEYS], precision="bf16")
     torch.cuda.synchronize()
-    assert_close_stats(got, oracle(inp), "diag bf16 entry", logz_atol=LOGZ_ATOL_BF16)
+    assert_close_stats(got, oracle(inp), "diag bf16 entry", logz_atol=LOGZ_ATOL_BF16, bf16_stats=True)
+
+
+def test_overlapping_components(gpu_device):
+    """Fractional responsibilities: every product's bf16 rounding matters."""
+    g = torch.Generator().manual_seed(13)
+    N, K, D = 6000, 24, 40
+    inp = {"X": torch.randn(N, D, generator=g) * 1.5, "mu": torch.randn(K, D, generator=g) * 0.5,
+           "log_sigma_sq": torch.rand(K, D, generator=g) - 0.5,
+           "log_pi": torch.log_softmax(torch.randn(K, generator=g), 0)}
+    assert_close_stats(_into(inp, gpu_device), oracle(inp), "diag bf16 overlapping",
+                       logz_atol=LOGZ_ATOL_BF16, bf16_stats=True)
 
 
 def test_headline_shape_mid_size(gpu_device):
     inp = data.diag_clustered(32768, 1024, 96, seed=2)
     assert_close_stats(_into(inp, gpu_device), oracle(inp), "diag bf16 K1024 D96",
-                       logz_atol=LOGZ_ATOL_BF16)
+                       logz_atol=LOGZ_ATOL_BF16, bf16_stats=True)
 
 
 @pytest.mark.parametrize("N,K,D", [(12000, 1024, 96), (7777, 300, 61), (5000, 64, 32), (3000, 100, 200)])

@@ -336,6 +336,51 @@ def test_full_equals_diag_for_diagonal_factor():
     np.testing.assert_allclose(c.numpy(), d[3].numpy(), rtol=1e-9, atol=1e-9)
 
 
+# --------------------------------------------------------------------------- full, bf16 contract
+
+def test_full_bf16_equals_fp64_on_bf16_exact_operands():
+    """With x and L already exact in bfloat16, the contract rounds only r (mu_acc) and
+    r x_d2 (sig_outer): logZ and Nk equal the float64 E-step, the statistics stay
+    within the bf16 rounding, and sig_outer loses its symmetry by about that much."""
+    X, mu, L, lpi, _ = _full_inputs(N=300, K=4, D=6, seed=51)
+    X = O.bf16_round(X.float())
+    L = O.bf16_round(L.float())
+    mu = mu.float().double()
+    ref = O.estep_full(X, mu, L, lpi)
+    got = O.estep_full_bf16(X, mu, L, lpi)
+    np.testing.assert_allclose(got[0].numpy(), ref[0].numpy(), atol=1e-9)
+    np.testing.assert_allclose(got[1].numpy(), ref[1].numpy(), rtol=1e-9, atol=1e-12)
+    for i in (2, 3):
+        err = ((got[i] - ref[i]).abs().max() / ref[i].abs().max()).item()
+        assert 1e-7 < err < 2.0 ** -8, (i, err)
+    asym = ((got[3] - got[3].transpose(1, 2)).abs().max() / got[3].abs().max()).item()
+    assert 0 < asym < 2.0 ** -7
+
+
+def test_full_bf16_brute_force_tiny():
+    """Against a scalar loop that rounds to bfloat16 by bit manipulation."""
+    X, mu, L, lpi, _ = _full_inputs(N=8, K=3, D=4, seed=52)
+    X, mu, L = X.float(), mu.float(), L.float()
+    lz_b, nk_b, mu_b, sig_b = O.brute_estep_full_bf16(X, mu, L, lpi)
+    logZ, Nk, mu_acc, sig = O.estep_full_bf16(X, mu, L, lpi)
+    np.testing.assert_allclose(logZ.numpy(), lz_b, atol=1e-10)
+    np.testing.assert_allclose(Nk.numpy(), nk_b, rtol=1e-10)
+    np.testing.assert_allclose(mu_acc.numpy(), np.array(mu_b), rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(sig.numpy(), np.array(sig_b), rtol=1e-9, atol=1e-11)
+
+
+def test_full_bf16_invariants():
+    X, mu, L, lpi, _ = _full_inputs(N=400, K=5, D=5, seed=53)
+    logZ, Nk, mu_acc, sig = O.estep_full_bf16(X.float(), mu.float(), L.float(), lpi)
+    assert abs(Nk.sum().item() - 400) < 1e-9
+    xb = O.bf16_round(X.float())
+    err = (mu_acc.sum(dim=0) - xb.sum(dim=0)).abs().max() / xb.abs().sum(dim=0).max()
+    assert err < 2.0 ** -8
+    # the trace of sum_k sig_outer_k is sum_n ||x_n||^2 up to the roundings
+    tr = sig.diagonal(dim1=1, dim2=2).sum().item()
+    assert abs(tr - (X.float().double() ** 2).sum().item()) / tr < 2.0 ** -7
+
+
 # --------------------------------------------------------------------------- M-step
 
 def test_mstep_iso_single_component():
