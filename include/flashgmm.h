@@ -70,12 +70,20 @@ enum fgmm_flags {
      * RECOMPUTE keeps the workspace O(N + K*D) and recomputes.  Calls that
      * split the phases must agree on this flag. */
     FGMM_FLAG_RECOMPUTE = 1u << 6,
-    /* Isotropic E-step only: the bf16 operand contract of the reference's H100
-     * kernels (flash_gmm_h100.py:247-328).  X and mu are rounded to bfloat16 for
-     * x.mu and r^T X (r rounded to bfloat16 there) with fp32 accumulation; the
-     * constants come from the fp32 mu and the log-sum-exp is fp32.  The reference
-     * states a 5e-3 tolerance against fp32 for this contract.  The diagonal and
-     * full entry points return FGMM_ERR_UNSUPPORTED for it. */
+    /* The bf16 operand contract of the reference's H100 kernels, fp32 accumulation
+     * and log-sum-exp throughout (the reference states a 5e-3 tolerance against
+     * fp32 for it, flash_gmm_h100.py:276):
+     *   isotropic (flash_gmm_h100.py:247-328): X and mu rounded to bfloat16 for x.mu
+     *     and r^T X (r rounded there); constants from the fp32 mu.
+     *   diagonal (flash_gmm_diag_h100.py:63-130, :159-282, :317-343): x, x^2,
+     *     exp(-lss)/2 log2 e and mu exp(-lss)/2 log2 e rounded to bfloat16; r rounded
+     *     for r^T x and r^T x^2.
+     *   full (flash_gmm_full_h100.py:71-228, :289-298): x and L rounded to bfloat16
+     *     for the whitening, L^T mu fp32; r rounded for mu_acc and r x_d2 for
+     *     sig_outer[k][d2][:], which is then not exactly symmetric.  This path
+     *     always stores the log-joint and returns FGMM_ERR_UNSUPPORTED when its
+     *     N x K floats exceed 16 GiB (call in row chunks with ACCUMULATE).
+     * FGMM_FLAG_RECOMPUTE has no effect with it. */
     FGMM_FLAG_BF16 = 1u << 7,
 };
 
