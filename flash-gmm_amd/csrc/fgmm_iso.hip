@@ -101,8 +101,8 @@ struct IsoPlan {
   bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16)
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
   int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
-  size_t off_musw, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_nk, off_part_sig, off_lj,
-      total;
+  size_t off_musw, off_mu3, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_nk, off_part_sig,
+      off_lj, total;
 };
 
 // Pass 2 reads the stored log-joint when recomputation is not requested, D is at
@@ -158,6 +158,7 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf
   p.npart = p.nslab * p.rgroups;
   size_t off = 0;
   p.off_musw = off;    off = align256(off + (size_t)p.KP * p.DP * sizeof(float));
+  p.off_mu3 = off;     off = align256(off + (size_t)p.KP * p.DP * 4 * 2);   // bf16 splits of mu
   p.off_kcblk = off;   off = align256(off + (size_t)p.KB * 32 * 2 * sizeof(double));
   p.off_kclin = off;   off = align256(off + (size_t)p.KP * 4 * sizeof(double));
   p.off_rowstat = off; off = align256(off + (size_t)(N > 0 ? N : 0) * 2 * sizeof(double));
@@ -176,25 +177,38 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf
 __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int64_t ldmu, int64_t K,
                                                int D, int DP, const float* __restrict__ lss,
                                                const float* __restrict__ lpi, f32x4* __restrict__ mu_sw,
-                                               double2* __restrict__ kc_blk, double4* __restrict__ kc_lin) {
+                                               double2* __restrict__ kc_blk, double4* __restrict__ kc_lin,
+                                               bf16x8* __restrict__ mu3) {
   __shared__ double sC[32], sB[32];
   const int kb = blockIdx.x;
   const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
   const int64_t comp = (int64_t)kb * 32 + c;
   const bool valid = comp < K;
+  const int NQ = DP / 16;
   if (g == 0) {
-    double C = -INFINITY, b = 0.0, musq = 0.0;
+    double C = -INFINITY, b = 0.0, musq = 0.0, osum = 0.0;
     if (valid) {
       for (int d = 0; d < D; ++d) {
         double v = (double)mu[comp * ldmu + d];
         musq = fma(v, v, musq);
+      }
+      // The centring offsets of the bf16x6 pass 1: o_q = fp32(||mu chunk q||^2).
+      for (int q = 0; q < NQ; ++q) {
+        double o = 0.0;
+        for (int d = 16 * q; d < 16 * q + 16 && d < D; ++d) {
+          const double v = (double)mu[comp * ldmu + d];
+          o = fma(v, v, o);
+        }
+        osum += (double)(float)o;
       }
       const double l = (double)lss[comp];
       const double lp = (double)lpi[comp];
       b = 0.5 * exp(-l) * kLog2e;
       C = (lp - 0.5 * (double)D * (kLog2Pi + l)) * kLog2e - b * musq;
     }
-    sC[c] = C;
+    // Pass 1 at D <= 128 contracts the centred cross term x.mu - sum_q o_q, so its
+    // constant carries + 2 b sum_q o_q; above, pass 1 takes C itself.
+    sC[c] = (DP <= 128 && valid) ? C + 2.0 * b * osum : C;
     sB[c] = b;
     kc_lin[comp] = make_double4(C, b, musq, 0.0);
   }
@@ -211,6 +225,42 @@ __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int
     }
     mu_sw[((int64_t)kb * NM + m) * 64 + lane] = v;
   }
+  // The same chunks as three-way bf16 splits for the bf16x6 pass 1,
+  // mu3[kb][q][s][lane] = split s of mu[comp][16q + 8g .. 16q + 8g + 7] (s < 3), and
+  // slot 3 = the splits of -o_q in k slots 0..2 (lane-half 0, elements 0..2).
+  for (int q = 0; q < NQ; ++q) {
+    f32x4 lo = zero4(), hi = zero4();
+    const int d0 = 16 * q + 8 * g;
+    if (valid) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (d0 + e < D) lo[e] = mu[comp * ldmu + d0 + e];
+        if (d0 + 4 + e < D) hi[e] = mu[comp * ldmu + d0 + 4 + e];
+      }
+    }
+    bf16x8 sp[3];
+    split3_bf16(lo, hi, sp);
+#pragma unroll
+    for (int t = 0; t < 3; ++t) mu3[(((int64_t)kb * NQ + q) * 4 + t) * 64 + lane] = sp[t];
+    f32x4 olo = zero4();
+    if (valid && g == 0) {
+      double o = 0.0;
+      for (int d = 16 * q; d < 16 * q + 16 && d < D; ++d) {
+        const double v = (double)mu[comp * ldmu + d];
+        o = fma(v, v, o);
+      }
+      olo.x = -(float)o;
+    }
+    bf16x8 so[3];
+    split3_bf16(olo, zero4(), so);
+    bf16x8 ov;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ov[e] = (__bf16)0.0f;
+    ov[0] = so[0][0];
+    ov[1] = so[1][0];
+    ov[2] = so[2][0];
+    mu3[(((int64_t)kb * NQ + q) * 4 + 3) * 64 + lane] = ov;
+  }
   __syncthreads();
   // Constants in accumulator-register order: entry (g, i) is component acc_row(i, g).
   {
@@ -224,30 +274,30 @@ __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int
 
 // ---------------------------------------------------------------------------
 // Pass 1: logZ by online log-sum-exp over component blocks.
-// Each wave keeps 32 rows of X in registers (matrix-core B operand).  The
-// 32-component blocks of mu and their constants stream through LDS, double
-// buffered: the global loads of block kb+1 are in flight while block kb is
-// contracted, and land in the other buffer before the block's barrier.
+// Each wave keeps 32 rows of X in registers as three-way bf16 splits (the
+// matrix-core B operand of the centred bf16x6 contraction, x6c_tile).  The
+// 32-component blocks of mu (bf16 splits and centring offsets) and their
+// constants stream through LDS, double buffered: the global loads of block kb+1
+// are in flight while block kb is contracted, and land in the other buffer before
+// the block's barrier.
 // ---------------------------------------------------------------------------
 template <int DP>
 constexpr size_t lse_lds_bytes() {
-  return (size_t)2 * DP * 32 * sizeof(float) + (size_t)2 * 32 * sizeof(double2);
+  return (size_t)2 * (DP / 16) * 4 * 64 * sizeof(bf16x8) + (size_t)2 * 32 * sizeof(double2);
 }
 
 template <int DP, bool LJ>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(DP <= 160 ? 2 : 1, DP <= 160 ? 2 : 1)))
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
 void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
-             const f32x4* __restrict__ mu_sw, const double2* __restrict__ kc_blk, int KB,
+             const bf16x8* __restrict__ mu3, const double2* __restrict__ kc_blk, int KB,
              float* __restrict__ logZ, double2* __restrict__ rowstat, float* __restrict__ lj) {
-  constexpr int NM = DP / 8;
-  constexpr int BLK = NM * 64;            // float4 per 32-component block
-  constexpr int LPT = BLK / kThreads;     // float4 per thread per block
-  static_assert(BLK % kThreads == 0, "block load must split evenly");
+  constexpr int NQ = DP / 16;
+  constexpr int BLK = NQ * 4 * 64;        // bf16x8 per 32-component block
+  constexpr int LPT = (BLK + kThreads - 1) / kThreads;
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  f32x4* mu_l = reinterpret_cast<f32x4*>(lds_raw);                                  // [2][BLK]
-  double2* kc_l = reinterpret_cast<double2*>(lds_raw + 2 * BLK * sizeof(f32x4));   // [2][32]
+  bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                                 // [2][BLK]
+  double2* kc_l = reinterpret_cast<double2*>(lds_raw + 2 * BLK * sizeof(bf16x8));   // [2][32]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
@@ -255,32 +305,39 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   const int64_t row = tile * 32 + c;
   const bool valid = row < N;
 
-  f32x4 st[LPT];
+  bf16x8 st[LPT];
   double2 kst = make_double2(0.0, 0.0);
   auto fetch = [&](int kb) {
-    const f32x4* src = mu_sw + (int64_t)kb * BLK;
+    const bf16x8* src = mu3 + (int64_t)kb * BLK;
 #pragma unroll
-    for (int q = 0; q < LPT; ++q) st[q] = src[q * kThreads + tid];
+    for (int q = 0; q < LPT; ++q)
+      if (BLK % kThreads == 0 || q * kThreads + tid < BLK) st[q] = src[q * kThreads + tid];
     if (tid < 32) kst = kc_blk[(int64_t)kb * 32 + tid];
   };
   auto commit = [&](int buf) {
 #pragma unroll
-    for (int q = 0; q < LPT; ++q) mu_l[buf * BLK + q * kThreads + tid] = st[q];
+    for (int q = 0; q < LPT; ++q)
+      if (BLK % kThreads == 0 || q * kThreads + tid < BLK) mu_l[buf * BLK + q * kThreads + tid] = st[q];
     if (tid < 32) kc_l[buf * 32 + tid] = kst;
   };
   fetch(0);
 
-  f32x4 xb[NM];
+  // This lane's row, dimensions 16q + 8g .. +7, split three ways; ||x||^2 in fp64.
+  bf16x8 xb[NQ][3];
   double xsq = 0.0;
 #pragma unroll
-  for (int m = 0; m < NM; ++m) {
-    xb[m] = load_row4(X, ldx, row, 8 * m + 4 * g, D, valid);
-    xsq = fma((double)xb[m].x, (double)xb[m].x, xsq);
-    xsq = fma((double)xb[m].y, (double)xb[m].y, xsq);
-    xsq = fma((double)xb[m].z, (double)xb[m].z, xsq);
-    xsq = fma((double)xb[m].w, (double)xb[m].w, xsq);
+  for (int q = 0; q < NQ; ++q) {
+    const int d0 = 16 * q + 8 * g;
+    const f32x4 lo = load_row4(X, ldx, row, d0, D, valid), hi = load_row4(X, ldx, row, d0 + 4, D, valid);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xsq = fma((double)lo[e], (double)lo[e], xsq);
+      xsq = fma((double)hi[e], (double)hi[e], xsq);
+    }
+    split3_bf16(lo, hi, xb[q]);
   }
   xsq += __shfl_xor(xsq, 32);
+  const bf16x8 ones = x6c_ones(lane);
   commit(0);
   lds_barrier();
 
@@ -291,17 +348,17 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const int buf = kb & 1;
     const bool more = kb + 1 < KB;
     if (more) fetch(kb + 1);
-    const f32x4* mp = mu_l + buf * BLK + lane;
-    // S^T[comp][row] = mu . x, lane = row, register i = component acc_row(i, g).
-    double xm[16];
-    cross_tile<NM>(xm, [&](int m) { return mp[m * 64]; }, [&](int m) { return xb[m]; });
+    const bf16x8* mp = mu_l + buf * BLK + lane;
+    // Centred S^T[comp][row] = mu . x - sum_q o_q, lane = row, register i = component
+    // acc_row(i, g); the block's constants carry + 2 b sum_q o_q.
+    const f32x16 xm = x6c_tile<NQ>([&](int q, int t) { return mp[(q * 4 + t) * 64]; }, xb, ones);
     const double2* kp = kc_l + buf * 32 + g * 16;
     double ll[16];
     double bm = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const double2 cb = kp[i];
-      ll[i] = fma(-cb.y, fma(-2.0, xm[i], xsq), cb.x);
+      ll[i] = fma(-cb.y, fma(-2.0, (double)xm[i], xsq), cb.x);
       bm = fmax(bm, ll[i]);
     }
     // Keep the max here: sunk past the conditional commit below, its operands
@@ -1128,7 +1185,8 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
       }
       auto kern = pl.lj ? &iso_lse<DP, true> : &iso_lse<DP, false>;
       hipLaunchKernelGGL(kern, dim3((unsigned)nblk1), dim3(kThreads), lds1, stream, X, ldx, pl.N,
-                         (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat, lj);
+                         (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3), kc_blk, pl.KB,
+                         logZ, rowstat, lj);
     } else {
       // Above D = 128 the rows' dimensions are split over two waves.
       constexpr size_t lds1 = lse_split_lds_bytes<DP>();
@@ -1690,7 +1748,8 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
     hipLaunchKernelGGL(iso_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, K, (int)D, pl.DP,
                        log_sigma_sq, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_musw),
                        reinterpret_cast<double2*>(ws + pl.off_kcblk),
-                       reinterpret_cast<double4*>(ws + pl.off_kclin));
+                       reinterpret_cast<double4*>(ws + pl.off_kclin),
+                       reinterpret_cast<bf16x8*>(ws + pl.off_mu3));
   if (N > 0) {
     auto run = [&](auto dp_tag) -> hipError_t {
       constexpr int DP = decltype(dp_tag)::value;
