@@ -372,6 +372,17 @@ def main():
     roof.update({"kernel": dom["kernel"], "traffic": dom["traffic"],
                  "traffic_unit": "bytes per launch (HBM read + write, rocprofv3 counters)",
                  "avg_launch_ms": dom["ms"]})
+    if kind == "iso" and not bf16 and D <= 128 and dom_phase == "phase1":
+        # Phase 1 forms the fp32 cross term from split-bf16 products on the bf16 matrix
+        # cores: 7 steps of 16 dimensions (6 products + 1 centring offset) per 32x32 tile,
+        # 14 D bf16 flop per (row, component) against the 2 D algorithmic fp32 flop.
+        ex = 14.0 * N * K * (D + (-D) % 16)
+        roof["executed"] = {"arithmetic": "split-bf16 (bf16x6) products, fp32 accumulation, fp64 "
+                                          "combination; fp32 inputs and outputs",
+                            "bf16_flop_per_launch": ex,
+                            "bf16_tflops": ex / (dom["ms"] * 1e-3) / 1e12,
+                            "bf16_peak": PEAK_BF16_MFMA_TFLOPS,
+                            "bf16_frac": ex / (dom["ms"] * 1e-3) / 1e12 / PEAK_BF16_MFMA_TFLOPS}
 
     out = {
         "metric": (METRIC if kind == "iso" and not bf16 else

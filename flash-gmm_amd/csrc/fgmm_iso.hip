@@ -1031,8 +1031,11 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
         const float l = ljc[i >> 2][i & 3];
         const float rv = fast_exp2((l - z.x) - z.y);
         if (NH == 1 || h == 0) {
+          // sig gathers r (C0_k - ll2) = r b_k ||x - mu_k||^2; 1 / b_k is applied once
+          // at the end (a component of weight 0 has ll2 = -inf there, so its lane's
+          // sum turns NaN and is dropped below).
           nk += rv;
-          sig = fmaf(rv, fminf((c0 - l) * ibk, FLT_MAX), sig);
+          sig = fmaf(rv, c0 - l, sig);
         }
         r[i] = rv;
         if (kInterleave && (NJ < 2 || dense || __builtin_amdgcn_ballot_w64(rv != 0.0f) != 0)) {
@@ -1066,6 +1069,7 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   if (active) {
     nk += __shfl_xor(nk, 32);
     sig += __shfl_xor(sig, 32);
+    sig = ibk != 0.0f ? sig * ibk : 0.0f;
     const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
