@@ -80,7 +80,7 @@ def cpu_baseline(inp, kind, K, D, min_s=10.0, max_s=30.0, rows=16384):
 # for FETCH_SIZE, x1.0 for WRITE_SIZE); the counter values and commands are in
 # profiles/<kind>_estep_<shape>.md.  Not reported with --recompute.
 TRAFFIC_BYTES = {
-    "iso_n1m_k1024_d128": {"phase1": 4_684_565_705, "phase2": 4_658_482_852},
+    "iso_n1m_k1024_d128": {"phase1": 4_733_227_008, "phase2": 4_658_505_728},
     "diag_n1m_k1024_d96": {"phase1": 4_499_631_140, "phase2": 4_542_595_401},
     "full_n250k_k256_d64": {"phase1": 589_263_972, "phase2": 414_389_462},
 }
@@ -213,6 +213,8 @@ def main():
     ap.add_argument("--atomic-reduce", action="store_true")
     ap.add_argument("--dense", action="store_true",
                     help="also run accumulation steps whose responsibilities are all zero")
+    ap.add_argument("--no-dense-run", action="store_true",
+                    help="skip the dense comparison run (profiling the default launches alone)")
     ap.add_argument("--workload", default="iso_n1m_k1024_d128",
                     choices=sorted(WORKLOADS) + ["stream_em_n1b_k1024_d128"])
     ap.add_argument("--rows", type=int, default=0, help="override N of the streaming workload")
@@ -322,7 +324,7 @@ def main():
     log(f"timed {args.steps} steps: {ms:.3f} ms/step (phase1 {p1:.3f} ms, phase2 {p2:.3f} ms)")
 
     dense_ms = None
-    if not args.dense:
+    if not args.dense and not args.no_dense_run:
         # The same steps with every accumulation step executed (identical outputs):
         # the dense cost, reported beside the default.
         for _ in range(2):

@@ -321,7 +321,8 @@ __device__ __forceinline__ double wave_strided_sum(const float* __restrict__ p, 
 // Stored log-joint.  Pass 1 can keep the fp32 log-joint (log2 units) of every
 // (32-row tile, 32-component block) pair in the workspace, so that pass 2 reads
 // it instead of recomputing the contraction.  Tiles are ordered (row tile,
-// component block), 1024 floats each, in pass 1's register order: the pass-1
+// component block), 1024 floats each.  In the dense form below (diagonal
+// covariances) they are in pass 1's register order: the pass-1
 // lane l (row l % 32; component acc_row(i, l / 32) in register i) writes
 // register i at i * 64 + l, so each store instruction fills 256 contiguous
 // bytes.  Component k of row r therefore sits at
@@ -353,8 +354,128 @@ __device__ __forceinline__ void lj_load(const float* __restrict__ tile, int lane
   for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const f32x4*>(p + 8 * q);
 }
 
+// ---------------------------------------------------------------------------
+// Sparse stored log-joint (row-major tiles with need masks).
+//
+// On clustered data nearly every (row, component block) pair has a log-joint
+// thousands of log2 units below the row's logZ2, so its responsibilities are
+// exactly zero in fp32.  In this form a tile is stored row-major, tile[row * 32 +
+// comp], so that one row of one block is one 128-byte line, and pass 1 leaves
+// beside the tiles:
+//   bmax[(tile, block)][row]  fp32 max of the row's 32 stored values;
+//   mask[(tile, block)]       bit r set when row r may have a nonzero
+//                             responsibility in the block.
+// Pass 1 computes the masks after the row's logZ2 is final: with z = (hi, lo) the
+// float pair pass 2 forms from logZ2, bit r is clear when
+//     fl(fl(bmax - z.hi) - z.lo) < -kLjNeedGap.
+// Rounding is monotone, so every value l <= bmax of the row then gives
+// fl(fl(l - z.hi) - z.lo) < -kLjNeedGap as well, and 2^x is zero in fp32 for
+// x < -149: the responsibilities pass 2 would form are exactly zero.  Pass 2 reads
+// only the rows whose bit is set, so skipping the others changes no output bit.
+//
+// Pass 1 also leaves out the store of a row's block when the running max M of the
+// row's stored values already proves the mask bit will be clear:
+// fl(bmax - M) < -kLjSkipGap with |M| < 2^24.  logZ2 >= max log-joint >= M - 1
+// (M is a float rounding of a log-joint), so bmax - logZ2 < 1 - kLjSkipGap, and the
+// float evaluation above cannot reach -kLjNeedGap.  A half-wave whose block sum is
+// NaN always stores (the row's logZ2 is NaN, so its mask bit is set).
+// ---------------------------------------------------------------------------
+constexpr float kLjNeedGap = 200.0f;
+constexpr float kLjSkipGap = 232.0f;
+
+// Max over both half-waves of the row's block maximum (lane = row in pass 1).
+__device__ __forceinline__ float lj_row_max(double bm) {
+  const unsigned u = __float_as_uint((float)bm);
+  const auto s = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+
+// Pass-1 store of one (row tile, block) pair.  Lane (row c, half g) holds
+// components acc_row(i, g), i.e. 8j + 4g + 0..3 in registers 4j..4j+3: four float4
+// per lane, the two halves together filling each row's line.  Each instruction
+// writes 32 bytes of every row, so these are ordinary (write-back) stores that the
+// L2 merges into whole lines; non-temporal ones reach HBM piecewise, at about
+// twice the bytes.  `lse_sum` is the
+// half-wave's running log-sum-exp sum after the block (NaN if any value was NaN),
+// `run_max` the row's running max of stored values (updated here).
+__device__ __forceinline__ void lj_put_rows(float* __restrict__ tile, float* __restrict__ bmax, int c,
+                                            int g, const double (&ll)[16], double bm, float lse_sum,
+                                            float& run_max, bool dense) {
+  const float R = lj_row_max(bm);
+  run_max = fmaxf(run_max, R);
+  const bool skip = !dense && lse_sum == lse_sum && fabsf(run_max) < 0x1p24f && (R - run_max) < -kLjSkipGap;
+  if (!skip) {
+    float* p = tile + c * 32 + 4 * g;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 v = {(float)ll[4 * j], (float)ll[4 * j + 1], (float)ll[4 * j + 2], (float)ll[4 * j + 3]};
+      *reinterpret_cast<f32x4*>(p + 8 * j) = v;
+    }
+  }
+  if (g == 0) bmax[c] = R;
+}
+
+// Pass-1 epilogue: need masks of the wave's row tile for all KB blocks.  Run by
+// the half-wave g = 0 only (lane c = row c); each lane reads back the maxima it
+// stored itself.  lz2 is the row's final logZ2; rows past N get no bit.  With
+// `dense` (FGMM_FLAG_DENSE: every row stored) every row of the tile is marked, so a
+// dense pass 2 reads and exponentiates all of them; pass 2 itself always follows
+// the masks, whichever flags its own call carries.
+__device__ __forceinline__ void lj_put_masks(const float* __restrict__ bmax, unsigned* __restrict__ mask,
+                                             int KB, int c, double lz2, bool valid, bool dense) {
+  const float zx = (float)lz2;
+  const float zy = (lz2 > -INFINITY && lz2 < INFINITY) ? (float)(lz2 - (double)zx) : 0.0f;
+  for (int kb0 = 0; kb0 < KB; kb0 += 8) {
+    float R[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) R[j] = kb0 + j < KB ? bmax[(kb0 + j) * 32 + c] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (kb0 + j < KB) {
+        const bool need = valid && (dense || !(((R[j] - zx) - zy) < -kLjNeedGap));
+        const unsigned long long b = __builtin_amdgcn_ballot_w64(need);
+        if (c == 0) mask[kb0 + j] = (unsigned)b;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Range-checked buffer loads.  A raw buffer resource covers `bytes` bytes from
+// `base`; a lane whose byte offset is at or beyond that reads zero and makes no
+// memory access.  Streaming loops use them to issue the same number of load
+// instructions in every iteration whatever the data (a row past the slab, a
+// log-joint row not needed): the compiler can then count the outstanding loads
+// exactly and wait only for the ones an instruction consumes, so prefetches stay
+// in flight across iterations.
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t buf_rsrc;
+constexpr int kBufOob = (int)0x80000000u;   // an offset beyond every resource here
+constexpr int kBufNt = 2;                   // cache policy: non-temporal (read once)
+
+__device__ __forceinline__ buf_rsrc make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+template <int AUX = 0>
+__device__ __forceinline__ float buf_load_f32(buf_rsrc r, int off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX));
+}
+__device__ __forceinline__ unsigned buf_load_u32(buf_rsrc r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ double buf_load_f64(buf_rsrc r, int off) {
+  return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+__device__ __forceinline__ f32x4 buf_load_f32x4(buf_rsrc r, int off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
 // Workspace cap for the stored log-joint of one call (N/32 x K/32 tiles of 4 KiB).
 constexpr size_t kMaxLjBytes = (size_t)16 << 30;
+
+// Largest row stride (floats) of X for the buffer-loaded streaming passes: a
+// tile's byte offsets (256 rows x stride x 4) must stay below 2^31.
+constexpr int64_t kMaxBufLdx = (int64_t)1 << 20;
 
 // Largest N one E-step call takes: pass-1 grids hold N / 128 workgroups, which
 // must stay within the 2^31 - 1 grid limit.  Larger data sets stream in chunks.

@@ -102,7 +102,7 @@ struct IsoPlan {
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
   int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
   size_t off_musw, off_mu3, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_nk, off_part_sig,
-      off_lj, total;
+      off_lj, off_ljmax, off_ljmask, total;
 };
 
 // Pass 2 reads the stored log-joint when recomputation is not requested, D is at
@@ -131,10 +131,10 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf
     p.cpg = bf16_blocks_per_group(p.DP, p.KB);
     p.rgroups = kAccWaves / (p.cpg * bf16_halves(p.DP));
   } else if (p.lj) {
-    // 8 component blocks per workgroup, or 4 for K <= 224; then above D = 128 two
-    // waves share a block (one half of the columns each): one wave's accumulators
-    // for 4 row groups would not fit.
-    p.cpg = p.KB >= 8 ? 8 : 4;
+    // 8 component blocks per workgroup, or 4 for K <= 224 and for D > 192; with 4
+    // blocks above D = 128 two waves share a block (one half of the columns each):
+    // one wave's accumulators for all of D would not fit with the other state.
+    p.cpg = (p.KB >= 8 && p.DP <= 192) ? 8 : 4;
     p.lj_nh = (p.DP > 128 && p.cpg == 4) ? 2 : 1;
     p.rgroups = kAccWaves / (p.cpg * p.lj_nh);
   } else {
@@ -165,8 +165,12 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf
   p.off_part_mu = off; off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
   p.off_part_nk = off; off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
   p.off_part_sig = off; off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
-  p.off_lj = off;   // one tile per pass-1 wave: the grid's 32-row tiles, rounded up to 4
-  if (p.lj) off = align256(off + (size_t)round_up(cdiv(N, 32), 4) * p.KB * kLjTile * sizeof(float));
+  // One log-joint tile per pass-1 wave (the grid's 32-row tiles, rounded up to 4),
+  // with its per-row block maxima and need mask.
+  const size_t ntile = p.lj ? (size_t)round_up(cdiv(N, 32), 4) * p.KB : 0;
+  p.off_lj = off;     off = align256(off + ntile * kLjTile * sizeof(float));
+  p.off_ljmax = off;  off = align256(off + ntile * 32 * sizeof(float));
+  p.off_ljmask = off; off = align256(off + ntile * sizeof(unsigned));
   p.total = off;
   return p;
 }
@@ -290,7 +294,8 @@ template <int DP, bool LJ>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
 void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
              const bf16x8* __restrict__ mu3, const double2* __restrict__ kc_blk, int KB,
-             float* __restrict__ logZ, double2* __restrict__ rowstat, float* __restrict__ lj) {
+             float* __restrict__ logZ, double2* __restrict__ rowstat, float* __restrict__ lj,
+             float* __restrict__ ljmax, unsigned* __restrict__ ljmask, int dense) {
   constexpr int NQ = DP / 16;
   constexpr int BLK = NQ * 4 * 64;        // bf16x8 per 32-component block
   constexpr int LPT = (BLK + kThreads - 1) / kThreads;
@@ -343,6 +348,7 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   double mx = -INFINITY;
   float sm = 0.0f;
+  float run_max = -INFINITY;   // running max of the row's stored log-joint
 
   for (int kb = 0; kb < KB; ++kb) {
     const int buf = kb & 1;
@@ -364,8 +370,6 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     // Keep the max here: sunk past the conditional commit below, its operands
     // would cross a block boundary and each cost a canonicalising max.
     asm volatile("" : "+v"(bm));
-    // Unconditional: tiles are allocated for the whole grid.
-    if constexpr (LJ) lj_store(lj + (tile * KB + kb) * kLjTile, lane, ll);
     const double mn = fmax(mx, bm);
     const double ms = (mn == -INFINITY) ? 0.0 : mn;
     float acc = sm * fast_exp2((float)(mx - ms));
@@ -373,6 +377,10 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     for (int i = 0; i < 16; ++i) acc += fast_exp2((float)(ll[i] - ms));
     sm = acc;
     mx = mn;
+    // Tiles are allocated for the whole grid, rows past N included.
+    if constexpr (LJ)
+      lj_put_rows(lj + (tile * KB + kb) * kLjTile, ljmax + (tile * KB + kb) * 32, c, g, ll, bm, acc,
+                  run_max, dense != 0);
     if (more) commit(buf ^ 1);
     lds_barrier();
   }
@@ -387,6 +395,9 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   if (valid && g == 0) {
     rowstat[row] = make_double2(xsq, lz2);
     if (logZ) logZ[row] = (float)(lz2 * kLn2);
+  }
+  if constexpr (LJ) {
+    if (g == 0) lj_put_masks(ljmax + tile * KB * 32, ljmask + tile * KB, KB, c, lz2, valid, dense != 0);
   }
 }
 
@@ -409,7 +420,8 @@ template <int DP, bool LJ>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                    const f32x4* __restrict__ mu_sw, const double2* __restrict__ kc_blk, int KB,
-                   float* __restrict__ logZ, double2* __restrict__ rowstat, float* __restrict__ lj) {
+                   float* __restrict__ logZ, double2* __restrict__ rowstat, float* __restrict__ lj,
+                   float* __restrict__ ljmax, unsigned* __restrict__ ljmask, int dense) {
   constexpr int NM = DP / 8;
   constexpr int NMH = NM / 2;             // chunks per half
   constexpr int HD = DP / 2;
@@ -466,6 +478,7 @@ void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   double mx = -INFINITY;
   float sm = 0.0f;
+  float run_max = -INFINITY;   // running max of the row's stored log-joint
   for (int kb = 0; kb < KB; ++kb) {
     const int buf = kb & 1;
     const bool more = kb + 1 < KB;
@@ -490,7 +503,6 @@ void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
         ll[i] = fma(-cb.y, fma(-2.0, xm[i] + exb[i * 64], xsq), cb.x);
         bm = fmax(bm, ll[i]);
       }
-      if constexpr (LJ) lj_store(lj + (tile * KB + kb) * kLjTile, lane, ll);
       const double mn = fmax(mx, bm);
       const double ms = (mn == -INFINITY) ? 0.0 : mn;
       float acc = sm * fast_exp2((float)(mx - ms));
@@ -498,6 +510,9 @@ void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       for (int i = 0; i < 16; ++i) acc += fast_exp2((float)(ll[i] - ms));
       sm = acc;
       mx = mn;
+      if constexpr (LJ)
+        lj_put_rows(lj + (tile * KB + kb) * kLjTile, ljmax + (tile * KB + kb) * 32, c, g, ll, bm, acc,
+                    run_max, dense != 0);
     }
   }
 
@@ -511,6 +526,9 @@ void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     if (valid && g == 0) {
       rowstat[row] = make_double2(xsq, lz2);
       if (logZ) logZ[row] = (float)(lz2 * kLn2);
+    }
+    if constexpr (LJ) {
+      if (g == 0) lj_put_masks(ljmax + tile * KB * 32, ljmask + tile * KB, KB, c, lz2, valid, dense != 0);
     }
   }
 }
@@ -874,22 +892,36 @@ void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 // Pass 2 from the stored log-joint: grid over (row slab x group of CB component
 // blocks); eight waves = CB component blocks x NH column parts x 8 / (CB NH) row
 // groups of 32 rows (NH = 2 above D = 128, where one wave's accumulators for all
-// of D would not fit in registers).  Each wave reads the log-joint tile of its
-// block and rows (4 KiB), forms r = 2^(ll2 - logZ2) and accumulates r^T X for its
-// columns on the matrix cores from the X tile that the workgroup's blocks share
-// in LDS.  ||x - mu_k||^2 for sig_acc comes back from the log-joint as
-// (C0_k - ll2) / b_k, where C0_k = C_k + b_k ||mu_k||^2.  logZ2 sits in LDS as a
-// hi + lo pair of floats, so ll2 - logZ2 keeps the accuracy of the fp32 log-joint.
+// of D would not fit in registers).  Each wave reads the log-joint rows of its
+// block that pass 1 marked as needed (a 128-byte line per row), forms
+// r = 2^(ll2 - logZ2) and accumulates r^T X for its columns on the matrix cores
+// from the X tile that the workgroup's blocks share in LDS.  ||x - mu_k||^2 for
+// sig_acc comes back from the log-joint as (C0_k - ll2) / b_k, where
+// C0_k = C_k + b_k ||mu_k||^2.  logZ2 sits in LDS as a hi + lo pair of floats, so
+// ll2 - logZ2 keeps the accuracy of the fp32 log-joint.
+//
+// Streaming, with NB register buffers (3 up to D = 128, else 2 for registers):
+// while tile t is processed, X super-tile t + NB and the log-joint rows of tile
+// t + NB - 1 are loaded, so each has NB - 1 iterations or more to arrive.  The need
+// masks that select those rows travel with X: super-tile u carries the masks of
+// tile u + NB - 1.  The loop is unrolled by NB so that every register buffer has a fixed
+// index (no copies between iterations), and every load is a range-checked buffer
+// load issued unconditionally, so the compiler waits only for the loads each
+// instruction consumes.
 // ---------------------------------------------------------------------------
+__host__ __device__ constexpr int accum_lj_buffers(int DP) { return DP <= 128 ? 3 : 2; }
+
 template <int DP, int CB, int NH>
 constexpr size_t accum_lj_lds_bytes() {
-  return (size_t)2 * 32 * (kAccWaves / (CB * NH)) * ((DP + 4) * sizeof(float) + sizeof(float2));
+  return (size_t)2 * 32 * (kAccWaves / (CB * NH)) * ((DP + 4) * sizeof(float) + sizeof(float2)) +
+         (size_t)2 * kAccWaves * sizeof(unsigned);
 }
 
 template <int DP, int CB, int NH>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
-                  const float* __restrict__ lj, const double4* __restrict__ kc_lin, int KB, int KP,
+                  const float* __restrict__ lj, const unsigned* __restrict__ ljmask,
+                  const double4* __restrict__ kc_lin, int KB, int KP,
                   const double2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
                   float* __restrict__ part_mu, float* __restrict__ part_nk, float* __restrict__ part_sig,
                   int dense) {
@@ -901,12 +933,15 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   constexpr int NV = TR * V4;                    // float4 per super-tile
   constexpr int LPT = (NV + kAccThreads - 1) / kAccThreads;
   static_assert(kAccWaves % (CB * NH) == 0 && (DP / 32) % NH == 0, "even split");
+  static_assert(TR + kAccWaves <= kAccThreads, "row-state and mask threads");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   float* xs = reinterpret_cast<float*>(lds_raw);                                  // [2][TR*RS]
   float2* rz = reinterpret_cast<float2*>(lds_raw + 2 * TR * RS * sizeof(float));  // [2][TR]
+  unsigned* mk = reinterpret_cast<unsigned*>(rz + 2 * TR);                        // [2][kAccWaves]
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, g = lane >> 5;
   const int cbw = wave % CB, h = (wave / CB) % NH, rg = wave / (CB * NH);
   const int slab = blockIdx.x % nslab;
@@ -937,132 +972,174 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   for (int j = 0; j < NJ; ++j) acc[j] = zero16();
   float nk = 0.0f, sig = 0.0f;
 
-  // X tiles and row logZ2 go global -> registers -> LDS.  Two register stages:
-  // tile t + 2 is loaded while tile t is processed and lands in LDS at the end of
-  // iteration t + 1, so every load has about two iterations to arrive (the LDS-only
-  // barrier leaves them in flight).
-  f32x4 stage[LPT], stage2[LPT];
-  double rq = INFINITY, rq2 = INFINITY;
-  const bool full_d = (D == DP);
-  auto fetch = [&](int t, f32x4 (&stage)[LPT], double& rq) {
-    const int64_t row0 = r_begin + (int64_t)t * TR;
-    if (full_d && row0 + TR <= r_end) {
-      const float* src = X + row0 * ldx;
-#pragma unroll
-      for (int q = 0; q < LPT; ++q) {
-        const int idx = q * kAccThreads + tid;
-        if (NV % kAccThreads == 0 || idx < NV)
-          stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < LPT; ++q) {
-        const int idx = q * kAccThreads + tid;
-        const int64_t row = row0 + idx / V4;
-        stage[q] = load_row4(X, ldx, row, (idx % V4) * 4, D, idx < NV && row < r_end);
-      }
-    }
-    if (tid < TR) {
-      const int64_t row = row0 + tid;
-      rq = (row < r_end) ? rowstat[row].y : INFINITY;
-    }
+  // Need mask of (row tile, block): bit r set when row r of the 32-row tile may
+  // have a nonzero responsibility in the block; 0 past the slab or the blocks.
+  const buf_rsrc mask_r = make_rsrc(ljmask, (uint32_t)(cdiv(N, 32) * KB * sizeof(unsigned)));
+  auto mask_off = [&](int t, int rgw, int kbw) -> int {
+    const int64_t row0 = r_begin + (int64_t)t * TR + rgw * 32;
+    return (t < ntiles && row0 < r_end && kbw < KB) ? (int)(((row0 >> 5) * KB + kbw) * 4) : kBufOob;
   };
-  auto commit = [&](int buf, const f32x4 (&stage)[LPT], double rq) {
+
+  constexpr int NB = accum_lj_buffers(DP);
+
+  // Super-tile t: X rows, their logZ2 (threads < TR) and the need masks of tile
+  // t + NB - 1 (thread TR + w for wave w), which the waves read once tile t is in
+  // LDS.  Rows past the slab, columns past D and tiles past the end read as zero.
+  const bool ragged = (D & 3) != 0;
+  auto fetch = [&](int t, f32x4 (&st)[LPT], double& rqv, unsigned& mqv) {
+    const int64_t row0 = r_begin + (int64_t)t * TR;
+    int nrow = 0;
+    if (t < ntiles) nrow = (int)(r_end - row0 < TR ? r_end - row0 : TR);
+    const buf_rsrc xr = make_rsrc(nrow ? X + row0 * ldx : X, (uint32_t)(nrow * ldx * 4));
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      const int r = idx / V4, col = (idx % V4) * 4;
+      const bool ok = (NV % kAccThreads == 0 || idx < NV) && r < nrow && col < D;
+      st[q] = buf_load_f32x4(xr, ok ? (int)((r * ldx + col) * 4) : kBufOob);
+    }
+    const buf_rsrc rr = make_rsrc(nrow ? rowstat + row0 : rowstat, (uint32_t)(nrow * sizeof(double2)));
+    const double q2 = buf_load_f64(rr, tid < nrow ? tid * (int)sizeof(double2) + 8 : kBufOob);
+    rqv = tid < nrow ? q2 : INFINITY;   // rows past the slab: logZ2 = +inf, hence r = 0
+    const int w = tid - TR;
+    mqv = buf_load_u32(mask_r, (w >= 0 && w < kAccWaves)
+                                   ? mask_off(t + NB - 1, w / (CB * NH), cg * CB + w % CB)
+                                   : kBufOob);
+  };
+  // Columns past D within the last float4 of a row are zeroed here, where the
+  // loaded values are consumed anyway.
+  auto commit = [&](int buf, const f32x4 (&st)[LPT], double rqv, unsigned mqv) {
     float* dst = xs + buf * TR * RS;
 #pragma unroll
     for (int q = 0; q < LPT; ++q) {
       const int idx = q * kAccThreads + tid;
-      if (NV % kAccThreads == 0 || idx < NV)
-        *reinterpret_cast<f32x4*>(dst + (idx / V4) * RS + (idx % V4) * 4) = stage[q];
+      if (NV % kAccThreads == 0 || idx < NV) {
+        const int col = (idx % V4) * 4;
+        f32x4 v = st[q];
+        if (ragged) {
+          if (col + 1 >= D) v.y = 0.0f;
+          if (col + 2 >= D) v.z = 0.0f;
+          if (col + 3 >= D) v.w = 0.0f;
+        }
+        *reinterpret_cast<f32x4*>(dst + (idx / V4) * RS + col) = v;
+      }
     }
     if (tid < TR) {
-      // Rows past the slab get logZ2 = +inf, hence r = 0.
-      const float hi = (float)rq;
-      const float lo = (rq > -INFINITY && rq < INFINITY) ? (float)(rq - (double)hi) : 0.0f;
+      const float hi = (float)rqv;
+      const float lo = (rqv > -INFINITY && rqv < INFINITY) ? (float)(rqv - (double)hi) : 0.0f;
       rz[buf * TR + tid] = make_float2(hi, lo);
     }
+    if (tid >= TR && tid < TR + kAccWaves) mk[buf * kAccWaves + tid - TR] = mqv;
   };
-  auto lj_fetch = [&](int t, f32x4 (&v)[4]) {
+  // Log-joint rows of tile t (register i: rows 8 (i >> 2) + (i & 3) + 4g), those
+  // whose need bit is set; the others read as 0.
+  auto lj_fetch = [&](int t, unsigned m, f32x16& v) {
     const int64_t row0 = r_begin + (int64_t)t * TR + rg * 32;
-    if (active && row0 < r_end) {
-      lj_load(lj + ((row0 >> 5) * KB + kb) * kLjTile, lane, v);
-    } else {
+    const buf_rsrc lr = make_rsrc(m ? lj + ((row0 >> 5) * KB + kb) * kLjTile : lj, m ? kLjTile * 4 : 0);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) v[q] = zero4();
+    for (int i = 0; i < 16; ++i) {
+      const int row = 8 * (i >> 2) + (i & 3) + 4 * g;
+      v[i] = buf_load_f32<kBufNt>(lr, ((m >> row) & 1u) ? (row * 32 + c) * 4 : kBufOob);
     }
   };
 
-  // Log-joint tiles are loaded two super-tiles ahead as well, or one ahead with
-  // 8 accumulator tiles per wave (registers).
-  constexpr bool kLj2 = NJ <= 4;
-  f32x4 ljc[4], ljn[4], ljm[4];
-  if (ntiles > 0) {
-    fetch(0, stage, rq);
-    lj_fetch(0, ljc);
-    commit(0, stage, rq);
-  }
-  if (ntiles > 1) {
-    fetch(1, stage, rq);
-    if (kLj2) lj_fetch(1, ljn);
-  }
-  lds_barrier();
+  f32x4 stg[NB][LPT];
+  double rqs[NB];
+  unsigned mqs[NB];
+  f32x16 ljb[NB];
+  // Need masks of tiles t .. t + NB - 2 (msk[0] is the current tile's).
+  unsigned msk[NB - 1];
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    const bool more = t + 1 < ntiles;
-    if (t + 2 < ntiles) {
-      fetch(t + 2, stage2, rq2);
-      if (kLj2) lj_fetch(t + 2, ljm);
-    }
-    if (!kLj2 && more) lj_fetch(t + 1, ljn);
-    const float* xt = xs + buf * TR * RS + rg * 32 * RS;
-    const float2* rt = rz + buf * TR + rg * 32 + 4 * g;
-    if (active) {
+  // One tile; P = t mod NB.  Registers P receive X super-tile t + NB (free since
+  // tile t went to LDS), log-joint buffer (P + NB - 1) mod NB tile t + NB - 1 (free
+  // since tile t - 1 was processed); X tile t + 1 goes from registers (P + 1) mod NB
+  // to the other LDS buffer at the end.
+  auto step = [&](int t, auto par) {
+    constexpr int P = decltype(par)::value;
+    const int lb = t & 1;   // LDS buffer of tile t
+    const unsigned ma = __builtin_amdgcn_readfirstlane(mk[lb * kAccWaves + wave]);   // tile t + NB - 1
+    lj_fetch(t + NB - 1, ma, ljb[(P + NB - 1) % NB]);
+    fetch(t + NB, stg[P], rqs[P], mqs[P]);
+    const unsigned mc = msk[0];
+    const float* xt = xs + lb * TR * RS + rg * 32 * RS;
+    const float2* rt = rz + lb * TR + rg * 32 + 4 * g;
+    if (active && mc != 0u) {
       const float* xbase = xt + 4 * g * RS + col0 + c;
-      // r of the 16 rows, then the matrix-core steps.  Forming each r just before
-      // its step saves 16 registers (needed with 8 accumulator tiles) but puts the
-      // exp -> ballot latency in front of every step.
-      constexpr bool kInterleave = NJ > 4;
-      float r[16];
+      // Register rows i whose need bits (rows 8q + j and 8q + j + 4 for i = 4q + j)
+      // are not both clear, in ascending order: r = 2^(ll2 - logZ2) for the lanes
+      // whose row is needed, 0 for the others (their log-joint was not read), then
+      // one matrix-core step per 32 columns unless every r is zero.  The skipped rows
+      // have r = 0 on every lane, so the sums are those of the dense order.
+      unsigned pm = (mc | (mc >> 4)) & 0x0f0f0f0fu;
+      const unsigned mg = mc >> (4 * g);
+      // Two register rows per round (the second optional), their LDS reads issued
+      // together so that the two latency chains overlap.
+      while (pm != 0u) {
+        const int ro0 = __builtin_ctz(pm);   // 8q + j
+        pm &= pm - 1u;
+        const bool two = pm != 0u;
+        const int ro1 = two ? __builtin_ctz(pm) : ro0;
+        if (two) pm &= pm - 1u;
+        const float2 z0 = rt[ro0], z1 = rt[ro1];
+        float xo0[NJ], xo1[NJ];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ro = 8 * (i >> 2) + (i & 3);
-        const float2 z = rt[ro];
-        const float l = ljc[i >> 2][i & 3];
-        const float rv = fast_exp2((l - z.x) - z.y);
+        for (int jj = 0; jj < NJ; ++jj) {
+          xo0[jj] = xbase[ro0 * RS + 32 * jj];
+          xo1[jj] = xbase[ro1 * RS + 32 * jj];
+        }
+        const float l0 = ljb[P][4 * (ro0 >> 3) + (ro0 & 3)];
+        const float l1 = ljb[P][4 * (ro1 >> 3) + (ro1 & 3)];
+        const float rv0 = ((mg >> ro0) & 1u) ? fast_exp2((l0 - z0.x) - z0.y) : 0.0f;
+        const float rv1 = (two && ((mg >> ro1) & 1u)) ? fast_exp2((l1 - z1.x) - z1.y) : 0.0f;
         if (NH == 1 || h == 0) {
           // sig gathers r (C0_k - ll2) = r b_k ||x - mu_k||^2; 1 / b_k is applied once
           // at the end (a component of weight 0 has ll2 = -inf there, so its lane's
-          // sum turns NaN and is dropped below).
-          nk += rv;
-          sig = fmaf(rv, c0 - l, sig);
-        }
-        r[i] = rv;
-        if (kInterleave && (NJ < 2 || dense || __builtin_amdgcn_ballot_w64(rv != 0.0f) != 0)) {
-#pragma unroll
-          for (int j = 0; j < NJ; ++j) acc[j] = mfma32(rv, xbase[ro * RS + 32 * j], acc[j]);
-        }
-      }
-      if constexpr (!kInterleave) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int ro = 8 * (i >> 2) + (i & 3);
-          if (NJ < 2 || dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
+          // sum turns NaN and is dropped below).  Rows not read have l = 0, r = 0.
+          nk += rv0;
+          sig = fmaf(rv0, c0 - l0, sig);
+          if (two) {
+            nk += rv1;
+            sig = fmaf(rv1, c0 - l1, sig);
           }
+        }
+        if (dense || __builtin_amdgcn_ballot_w64(rv0 != 0.0f) != 0) {
+#pragma unroll
+          for (int jj = 0; jj < NJ; ++jj) acc[jj] = mfma32(rv0, xo0[jj], acc[jj]);
+        }
+        if (two && (dense || __builtin_amdgcn_ballot_w64(rv1 != 0.0f) != 0)) {
+#pragma unroll
+          for (int jj = 0; jj < NJ; ++jj) acc[jj] = mfma32(rv1, xo1[jj], acc[jj]);
         }
       }
     }
-    if (more) commit(buf ^ 1, stage, rq);
+    if (t + 1 < ntiles) commit(lb ^ 1, stg[(P + 1) % NB], rqs[(P + 1) % NB], mqs[(P + 1) % NB]);
     lds_barrier();
 #pragma unroll
-    for (int q = 0; q < LPT; ++q) stage[q] = stage2[q];
-    rq = rq2;
+    for (int u = 0; u + 1 < NB - 1; ++u) msk[u] = msk[u + 1];
+    msk[NB - 2] = ma;
+  };
+
+  if (ntiles > 0) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      ljc[q] = ljn[q];
-      if (kLj2) ljn[q] = ljm[q];
+    for (int u = 0; u < NB; ++u) fetch(u, stg[u], rqs[u], mqs[u]);
+#pragma unroll
+    for (int u = 0; u < NB - 1; ++u) {
+      msk[u] = __builtin_amdgcn_readfirstlane(buf_load_u32(mask_r, mask_off(u, rg, kb)));
+      lj_fetch(u, msk[u], ljb[u]);
+    }
+    commit(0, stg[0], rqs[0], mqs[0]);
+    lds_barrier();
+  }
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  using P2 = std::integral_constant<int, 2>;
+  for (int t = 0; t < ntiles; t += NB) {
+    step(t, P0{});
+    if (t + 1 >= ntiles) break;
+    step(t + 1, P1{});
+    if constexpr (NB == 3) {
+      if (t + 2 >= ntiles) break;
+      step(t + 2, P2{});
     }
   }
 
@@ -1176,6 +1253,8 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   float* pnk = reinterpret_cast<float*>(ws + pl.off_part_nk);
   float* psig = reinterpret_cast<float*>(ws + pl.off_part_sig);
   float* lj = pl.lj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
+  float* ljmax = pl.lj ? reinterpret_cast<float*>(ws + pl.off_ljmax) : nullptr;
+  unsigned* ljmask = pl.lj ? reinterpret_cast<unsigned*>(ws + pl.off_ljmask) : nullptr;
   if (run1) {
     const int64_t nblk1 = cdiv(pl.N, 32 * kWaves);
     if constexpr (accum_uses_lds(DP)) {
@@ -1190,7 +1269,7 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
       auto kern = pl.lj ? &iso_lse<DP, true> : &iso_lse<DP, false>;
       hipLaunchKernelGGL(kern, dim3((unsigned)nblk1), dim3(kThreads), lds1, stream, X, ldx, pl.N,
                          (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3), kc_blk, pl.KB,
-                         logZ, rowstat, lj);
+                         logZ, rowstat, lj, ljmax, ljmask, dense ? 1 : 0);
     } else {
       // Above D = 128 the rows' dimensions are split over two waves.
       constexpr size_t lds1 = lse_split_lds_bytes<DP>();
@@ -1203,7 +1282,8 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
       }
       auto kern = pl.lj ? &iso_lse_split<DP, true> : &iso_lse_split<DP, false>;
       hipLaunchKernelGGL(kern, dim3((unsigned)nblk1), dim3(kAccThreads), lds1, stream, X, ldx, pl.N,
-                         (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat, lj);
+                         (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat, lj, ljmax, ljmask,
+                         dense ? 1 : 0);
     }
   }
   if (!run2) return hipGetLastError();
@@ -1221,15 +1301,15 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
           if (e != hipSuccess) return e;
         }
         hipLaunchKernelGGL((iso_accum_lj<DP, CB, NH>), grid2, dim3(kAccThreads), lds, stream, X, ldx,
-                           pl.N, (int)pl.D, lj, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab,
+                           pl.N, (int)pl.D, lj, ljmask, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab,
                            pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
         return hipSuccess;
       };
       using I1 = std::integral_constant<int, 1>;
       using I4 = std::integral_constant<int, 4>;
       hipError_t e;
-      if (pl.cpg == 8) {
-        e = launch(std::integral_constant<int, 8>{}, I1{});
+      if (DP <= 192 && pl.cpg == 8) {
+        if constexpr (DP <= 192) e = launch(std::integral_constant<int, 8>{}, I1{});
       } else if constexpr (DP > 128) {
         e = launch(I4{}, std::integral_constant<int, 2>{});
       } else {
@@ -1729,7 +1809,9 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
   if (D > 256) return FGMM_ERR_UNSUPPORTED;
   if (N > kMaxRows || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
   const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
-  const IsoPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE), bf16);
+  // The stored log-joint path streams X with 32-bit buffer offsets (row stride at
+  // most kMaxBufLdx floats); wider strides recompute, which needs less workspace.
+  const IsoPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE) && ldx <= kMaxBufLdx, bf16);
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;
   unsigned char* ws = static_cast<unsigned char*>(workspace);

@@ -54,22 +54,24 @@ def test_iso_workspace_bytes_grows_with_size():
 
 
 def test_iso_workspace_holds_stored_log_joint():
-    """Default sizing adds the fp32 log-joint tiles (N/32 x K/32 x 4 KiB) where pass 2 reads them."""
+    """Default sizing adds the fp32 log-joint tiles (N/32 x K/32 x 4 KiB) where pass 2 reads them,
+    with a per-row block maximum (128 bytes) and a need mask (4 bytes) per tile."""
     L = _lib.lib()
     R = _lib.FLAG_RECOMPUTE
     N, K, D = 1_000_000, 1024, 128
     full = L.fgmm_iso_workspace_bytes(N, K, D)
     assert full == L.fgmm_iso_workspace_bytes_ex(N, K, D, 0)
     lean = L.fgmm_iso_workspace_bytes_ex(N, K, D, R)
-    tiles = -(-N // 128) * 4 * (K // 32) * 4096
-    assert tiles <= full - lean <= tiles + 256
+    pairs = -(-N // 128) * 4 * (K // 32)
+    tiles = pairs * (4096 + 128 + 4)
+    assert tiles <= full - lean <= tiles + 3 * 256
     # Not stored: D <= 32, K <= 96, or more than 16 GiB of tiles.
     for n, k, d in [(N, K, 32), (N, 96, 128), (N, 96, 192), (20_000_000, 1024, 128)]:
         assert L.fgmm_iso_workspace_bytes(n, k, d) == L.fgmm_iso_workspace_bytes_ex(n, k, d, R)
     # Diagonal: stored for K > 96 at every D.
     d_full = L.fgmm_diag_workspace_bytes(N, K, 96)
     d_lean = L.fgmm_diag_workspace_bytes_ex(N, K, 96, R)
-    assert d_full == L.fgmm_diag_workspace_bytes_ex(N, K, 96, 0) and d_full - d_lean >= tiles
+    assert d_full == L.fgmm_diag_workspace_bytes_ex(N, K, 96, 0) and d_full - d_lean >= pairs * 4096
     assert L.fgmm_diag_workspace_bytes(N, 96, 96) == L.fgmm_diag_workspace_bytes_ex(N, 96, 96, R)
     # Full: stored whenever it fits, 32 floats per (32-row tile, component).
     q, qx = L.fgmm_full_workspace_bytes, L.fgmm_full_workspace_bytes_ex
