@@ -421,10 +421,19 @@ __device__ __forceinline__ void lj_put_rows(float* __restrict__ tile, float* __r
 // `dense` (FGMM_FLAG_DENSE: every row stored) every row of the tile is marked, so a
 // dense pass 2 reads and exponentiates all of them; pass 2 itself always follows
 // the masks, whichever flags its own call carries.
+//
+// `count` gathers the number of register-row pairs (rows r and r + 4, r & 4 == 0:
+// the two rows of one accumulation step) with a bit set, over the tile's blocks; the
+// accumulation pass picks its sparse or dense form from the total.  The caller
+// spreads tiles over 64 counters (one atomic per wave) that the prologue zeroes.
+__device__ __forceinline__ unsigned lj_pair_mask(unsigned m) { return (m | (m >> 4)) & 0x0f0f0f0fu; }
+
 __device__ __forceinline__ void lj_put_masks(const float* __restrict__ bmax, unsigned* __restrict__ mask,
-                                             int KB, int c, double lz2, bool valid, bool dense) {
+                                             unsigned* __restrict__ count, int KB, int c, double lz2,
+                                             bool valid, bool dense) {
   const float zx = (float)lz2;
   const float zy = (lz2 > -INFINITY && lz2 < INFINITY) ? (float)(lz2 - (double)zx) : 0.0f;
+  unsigned pairs = 0;
   for (int kb0 = 0; kb0 < KB; kb0 += 8) {
     float R[8];
 #pragma unroll
@@ -433,11 +442,13 @@ __device__ __forceinline__ void lj_put_masks(const float* __restrict__ bmax, uns
     for (int j = 0; j < 8; ++j) {
       if (kb0 + j < KB) {
         const bool need = valid && (dense || !(((R[j] - zx) - zy) < -kLjNeedGap));
-        const unsigned long long b = __builtin_amdgcn_ballot_w64(need);
-        if (c == 0) mask[kb0 + j] = (unsigned)b;
+        const unsigned b = (unsigned)__builtin_amdgcn_ballot_w64(need);
+        pairs += __builtin_popcount(lj_pair_mask(b));
+        if (c == 0) mask[kb0 + j] = b;
       }
     }
   }
+  if (c == 0 && pairs != 0) atomicAdd(count, pairs);
 }
 
 // ---------------------------------------------------------------------------
@@ -452,6 +463,14 @@ __device__ __forceinline__ void lj_put_masks(const float* __restrict__ bmax, uns
 typedef __amdgpu_buffer_rsrc_t buf_rsrc;
 constexpr int kBufOob = (int)0x80000000u;   // an offset beyond every resource here
 constexpr int kBufNt = 2;                   // cache policy: non-temporal (read once)
+
+// A lane's offset, kept in a register as computed: without this the compiler may
+// turn `cond ? offset : kBufOob` into a branch around the load, which makes the
+// number of loads depend on the path again.
+__device__ __forceinline__ int buf_off(int off) {
+  asm volatile("" : "+v"(off));
+  return off;
+}
 
 __device__ __forceinline__ buf_rsrc make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);

@@ -102,7 +102,7 @@ struct IsoPlan {
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
   int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
   size_t off_musw, off_mu3, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_nk, off_part_sig,
-      off_lj, off_ljmax, off_ljmask, total;
+      off_lj, off_ljmax, off_ljmask, off_ljcount, total;
 };
 
 // Pass 2 reads the stored log-joint when recomputation is not requested, D is at
@@ -171,6 +171,7 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf
   p.off_lj = off;     off = align256(off + ntile * kLjTile * sizeof(float));
   p.off_ljmax = off;  off = align256(off + ntile * 32 * sizeof(float));
   p.off_ljmask = off; off = align256(off + ntile * sizeof(unsigned));
+  p.off_ljcount = off; off = align256(off + (p.lj ? 64 * sizeof(unsigned) : 0));
   p.total = off;
   return p;
 }
@@ -182,10 +183,12 @@ __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int
                                                int D, int DP, const float* __restrict__ lss,
                                                const float* __restrict__ lpi, f32x4* __restrict__ mu_sw,
                                                double2* __restrict__ kc_blk, double4* __restrict__ kc_lin,
-                                               bf16x8* __restrict__ mu3) {
+                                               bf16x8* __restrict__ mu3, unsigned* __restrict__ ljcount) {
   __shared__ double sC[32], sB[32];
   const int kb = blockIdx.x;
   const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  // Pass 1 counts the needed row pairs of the stored log-joint into these.
+  if (ljcount && kb == 0) ljcount[lane] = 0u;
   const int64_t comp = (int64_t)kb * 32 + c;
   const bool valid = comp < K;
   const int NQ = DP / 16;
@@ -295,7 +298,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgp
 void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
              const bf16x8* __restrict__ mu3, const double2* __restrict__ kc_blk, int KB,
              float* __restrict__ logZ, double2* __restrict__ rowstat, float* __restrict__ lj,
-             float* __restrict__ ljmax, unsigned* __restrict__ ljmask, int dense) {
+             float* __restrict__ ljmax, unsigned* __restrict__ ljmask, unsigned* __restrict__ ljcount,
+             int dense) {
   constexpr int NQ = DP / 16;
   constexpr int BLK = NQ * 4 * 64;        // bf16x8 per 32-component block
   constexpr int LPT = (BLK + kThreads - 1) / kThreads;
@@ -397,7 +401,8 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     if (logZ) logZ[row] = (float)(lz2 * kLn2);
   }
   if constexpr (LJ) {
-    if (g == 0) lj_put_masks(ljmax + tile * KB * 32, ljmask + tile * KB, KB, c, lz2, valid, dense != 0);
+    if (g == 0) lj_put_masks(ljmax + tile * KB * 32, ljmask + tile * KB, ljcount + (tile & 63), KB, c, lz2,
+                   valid, dense != 0);
   }
 }
 
@@ -421,7 +426,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads),
 void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                    const f32x4* __restrict__ mu_sw, const double2* __restrict__ kc_blk, int KB,
                    float* __restrict__ logZ, double2* __restrict__ rowstat, float* __restrict__ lj,
-                   float* __restrict__ ljmax, unsigned* __restrict__ ljmask, int dense) {
+                   float* __restrict__ ljmax, unsigned* __restrict__ ljmask, unsigned* __restrict__ ljcount,
+                   int dense) {
   constexpr int NM = DP / 8;
   constexpr int NMH = NM / 2;             // chunks per half
   constexpr int HD = DP / 2;
@@ -528,7 +534,8 @@ void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       if (logZ) logZ[row] = (float)(lz2 * kLn2);
     }
     if constexpr (LJ) {
-      if (g == 0) lj_put_masks(ljmax + tile * KB * 32, ljmask + tile * KB, KB, c, lz2, valid, dense != 0);
+      if (g == 0) lj_put_masks(ljmax + tile * KB * 32, ljmask + tile * KB, ljcount + (tile & 63), KB, c, lz2,
+                   valid, dense != 0);
     }
   }
 }
@@ -888,6 +895,14 @@ void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   }
 }
 
+// Total of the 64 needed-pair counters (one wave, uniform result).
+__device__ __forceinline__ unsigned lj_pair_total(const unsigned* __restrict__ count) {
+  unsigned v = count[threadIdx.x & 63];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
 // ---------------------------------------------------------------------------
 // Pass 2 from the stored log-joint: grid over (row slab x group of CB component
 // blocks); eight waves = CB component blocks x NH column parts x 8 / (CB NH) row
@@ -921,6 +936,7 @@ template <int DP, int CB, int NH>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                   const float* __restrict__ lj, const unsigned* __restrict__ ljmask,
+                  const unsigned* __restrict__ ljcount, int64_t sparse_max,
                   const double4* __restrict__ kc_lin, int KB, int KP,
                   const double2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
                   float* __restrict__ part_mu, float* __restrict__ part_nk, float* __restrict__ part_sig,
@@ -934,6 +950,9 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   constexpr int LPT = (NV + kAccThreads - 1) / kAccThreads;
   static_assert(kAccWaves % (CB * NH) == 0 && (DP / 32) % NH == 0, "even split");
   static_assert(TR + kAccWaves <= kAccThreads, "row-state and mask threads");
+
+  // iso_accum_sparse takes the call when pass 1 found the masks sparse.
+  if (sparse_max >= 0 && (int64_t)lj_pair_total(ljcount) <= sparse_max) return;
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   float* xs = reinterpret_cast<float*>(lds_raw);                                  // [2][TR*RS]
@@ -1162,6 +1181,199 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 }
 
 // ---------------------------------------------------------------------------
+// Pass 2 from the sparse stored log-joint, for data whose need masks are sparse
+// (clustered data: most (row, block) pairs have no nonzero responsibility).  No
+// workgroup-wide staging: each wave owns one (row slab, row group, component
+// block), the same split as iso_accum_lj, and walks its 32-row tiles in the same
+// order, so it writes the same partials bit for bit.  Per tile it fetches only the
+// register-row pairs (rows r and r + 4) with a need bit: their log-joint, logZ2 and
+// X rows, straight from memory into registers.
+//
+// The first kSparseSlots pairs of a tile have fixed register slots and are loaded
+// kSparseDepth tiles ahead; every slot load is issued whether or not the slot is
+// used (range-checked buffer loads, out of range when unused), so the compiler
+// waits only for the slots each tile consumes.  Further pairs of a tile are loaded
+// when the tile is processed.  The masks of 256 tiles at a time are staged in LDS.
+//
+// The accumulator tile jj holds columns NJ * c + jj (lane c), so that each lane
+// reads its NJ columns of an X row with one load; every sum is formed in the same
+// order as in iso_accum_lj (pairs in ascending row order, unread rows r = 0), and
+// both kernels run on every call: each returns at once unless the needed-pair
+// count of pass 1 selects it.
+// ---------------------------------------------------------------------------
+constexpr int kSparseSlots = 3;
+constexpr int kSparseDepth = 4;
+constexpr int kSparseBatch = 256;
+constexpr int kSparseWaves = 4;
+
+template <int DP>
+__global__ __launch_bounds__(64 * kSparseWaves)
+void iso_accum_sparse(const float* __restrict__ X, int64_t ldx, int64_t N, const float* __restrict__ lj,
+                      const unsigned* __restrict__ ljmask, const unsigned* __restrict__ ljcount,
+                      int64_t sparse_max, const double4* __restrict__ kc_lin, int KB, int KP,
+                      const double2* __restrict__ rowstat, int nslab, int RG, int64_t rows_per_slab,
+                      float* __restrict__ part_mu, float* __restrict__ part_nk,
+                      float* __restrict__ part_sig, int dense) {
+  constexpr int NJ = DP / 32;
+  constexpr int S = kSparseSlots;
+  constexpr int PD = kSparseDepth;
+  constexpr int BT = kSparseBatch;
+  typedef float fNJ __attribute__((ext_vector_type(NJ)));
+  __shared__ unsigned mks[kSparseWaves][BT];
+
+  if ((int64_t)lj_pair_total(ljcount) > sparse_max) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t w = (int64_t)blockIdx.x * kSparseWaves + wave;
+  if (w >= (int64_t)nslab * RG * KB) return;
+  const int kb = (int)(w % KB);
+  const int rg = (int)((w / KB) % RG);
+  const int slab = (int)(w / ((int64_t)KB * RG));
+  const int TR = 32 * RG;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
+
+  float c0 = 0.0f, ibk = 0.0f;
+  {
+    const double4 kc = kc_lin[(int64_t)kb * 32 + c];
+    const double c0d = fma(kc.y, kc.z, kc.x);
+    if (c0d > -INFINITY && c0d < INFINITY) {
+      c0 = (float)c0d;
+      ibk = (float)(1.0 / kc.y);
+    }
+  }
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
+  float nk = 0.0f, sig = 0.0f;
+
+  // Slot registers of the PD tiles in flight.
+  float sl[PD][S];
+  double sz[PD][S];
+  fNJ sx[PD][S];
+  unsigned smk[PD];
+
+  auto tile_row0 = [&](int t) { return r_begin + (int64_t)t * TR + rg * 32; };
+  auto rsrcs = [&](int64_t row0, bool any, buf_rsrc& lr, buf_rsrc& rr, buf_rsrc& xr) {
+    const int nrow = any ? (int)(r_end - row0 < 32 ? r_end - row0 : 32) : 0;
+    lr = make_rsrc(any ? lj + ((row0 >> 5) * KB + kb) * kLjTile : lj, any ? kLjTile * 4 : 0);
+    rr = make_rsrc(any ? rowstat + row0 : rowstat, (uint32_t)(nrow * sizeof(double2)));
+    xr = make_rsrc(any ? X + row0 * ldx : X, (uint32_t)(nrow * ldx * 4));
+  };
+  // Loads of one register-row pair (rows ro and ro + 4; this lane's is ro + 4g).
+  auto load_pair = [&](const buf_rsrc& lr, const buf_rsrc& rr, const buf_rsrc& xr, unsigned m, int ro,
+                       bool used, float& l, double& z, fNJ& x) {
+    const int row = ro + 4 * g;
+    const bool need = used && ((m >> row) & 1u);
+    l = buf_load_f32<kBufNt>(lr, buf_off(need ? (row * 32 + c) * 4 : kBufOob));
+    z = buf_load_f64(rr, buf_off(need ? row * (int)sizeof(double2) + 8 : kBufOob));
+    const int xo = buf_off(need ? (int)((row * ldx + NJ * c) * 4) : kBufOob);
+    if constexpr (NJ == 4) {
+      x = buf_load_f32x4(xr, xo);
+    } else if constexpr (NJ == 2) {
+      x = __builtin_bit_cast(fNJ, __builtin_amdgcn_raw_buffer_load_b64(xr, xo, 0, 0));
+    } else if constexpr (NJ == 3) {
+      x = __builtin_bit_cast(fNJ, __builtin_amdgcn_raw_buffer_load_b96(xr, xo, 0, 0));
+    } else {
+      x = __builtin_bit_cast(fNJ, __builtin_amdgcn_raw_buffer_load_b32(xr, xo, 0, 0));
+    }
+  };
+  // One pair's contribution, in the arithmetic of iso_accum_lj.
+  auto accumulate = [&](unsigned m, int ro, float l, double q, const fNJ& x) {
+    const bool need = (m >> (ro + 4 * g)) & 1u;
+    const float zh = (float)q;
+    const float zl = (q > -INFINITY && q < INFINITY) ? (float)(q - (double)zh) : 0.0f;
+    const float rv = need ? fast_exp2((l - zh) - zl) : 0.0f;
+    nk += rv;
+    sig = fmaf(rv, c0 - l, sig);
+    if (dense || __builtin_amdgcn_ballot_w64(rv != 0.0f) != 0) {
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj) acc[jj] = mfma32(rv, x[jj], acc[jj]);
+    }
+  };
+  // Issue tile t's slot loads into stage u (mask 0: all out of range).
+  auto issue = [&](int t, int b0, int u) {
+    unsigned m = 0u;
+    if (t < ntiles && t - b0 < BT) m = __builtin_amdgcn_readfirstlane(mks[wave][t - b0]);
+    smk[u] = m;
+    buf_rsrc lr, rr, xr;
+    rsrcs(tile_row0(t), m != 0u, lr, rr, xr);
+    unsigned pm = lj_pair_mask(m);
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+      const bool used = pm != 0u;
+      const int ro = used ? __builtin_ctz(pm) : 0;
+      pm &= pm - 1u;
+      load_pair(lr, rr, xr, m, ro, used, sl[u][k], sz[u][k], sx[u][k]);
+    }
+  };
+  auto process = [&](int t, int u) {
+    const unsigned m = smk[u];
+    if (m == 0u) return;
+    unsigned pm = lj_pair_mask(m);
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+      if (pm == 0u) return;
+      const int ro = __builtin_ctz(pm);
+      pm &= pm - 1u;
+      accumulate(m, ro, sl[u][k], sz[u][k], sx[u][k]);
+    }
+    if (pm != 0u) {   // more pairs than slots: load them now
+      buf_rsrc lr, rr, xr;
+      rsrcs(tile_row0(t), true, lr, rr, xr);
+      while (pm != 0u) {
+        const int ro = __builtin_ctz(pm);
+        pm &= pm - 1u;
+        float l;
+        double q;
+        fNJ x;
+        load_pair(lr, rr, xr, m, ro, true, l, q, x);
+        accumulate(m, ro, l, q, x);
+      }
+    }
+  };
+
+  for (int b0 = 0; b0 < ntiles; b0 += BT) {
+    // Masks of tiles b0 .. b0 + BT - 1.
+#pragma unroll
+    for (int q = 0; q < BT / 64; ++q) {
+      const int t = b0 + 64 * q + lane;
+      const int64_t row0 = tile_row0(t);
+      mks[wave][64 * q + lane] = (t < ntiles && row0 < r_end) ? ljmask[(row0 >> 5) * KB + kb] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < PD; ++u) issue(b0 + u, b0, u);
+    for (int tt = 0; tt < BT; tt += PD) {
+      if (b0 + tt >= ntiles) break;
+#pragma unroll
+      for (int u = 0; u < PD; ++u) {
+        process(b0 + tt + u, u);
+        issue(b0 + tt + u + PD, b0, u);
+      }
+    }
+  }
+
+  nk += __shfl_xor(nk, 32);
+  sig += __shfl_xor(sig, 32);
+  sig = ibk != 0.0f ? sig * ibk : 0.0f;
+  const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float* dst = part_mu + (kbase + acc_row(i, g)) * DP + NJ * c;
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) dst[jj] = acc[jj][i];
+  }
+  if (g == 0) {
+    part_nk[kbase + c] = nk;
+    part_sig[kbase + c] = sig;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Finish: fixed-order fp64 reduction over slabs (deterministic).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void iso_reduce(const float* __restrict__ part_mu,
@@ -1255,6 +1467,7 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   float* lj = pl.lj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
   float* ljmax = pl.lj ? reinterpret_cast<float*>(ws + pl.off_ljmax) : nullptr;
   unsigned* ljmask = pl.lj ? reinterpret_cast<unsigned*>(ws + pl.off_ljmask) : nullptr;
+  unsigned* ljcount = pl.lj ? reinterpret_cast<unsigned*>(ws + pl.off_ljcount) : nullptr;
   if (run1) {
     const int64_t nblk1 = cdiv(pl.N, 32 * kWaves);
     if constexpr (accum_uses_lds(DP)) {
@@ -1269,7 +1482,7 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
       auto kern = pl.lj ? &iso_lse<DP, true> : &iso_lse<DP, false>;
       hipLaunchKernelGGL(kern, dim3((unsigned)nblk1), dim3(kThreads), lds1, stream, X, ldx, pl.N,
                          (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3), kc_blk, pl.KB,
-                         logZ, rowstat, lj, ljmax, ljmask, dense ? 1 : 0);
+                         logZ, rowstat, lj, ljmax, ljmask, ljcount, dense ? 1 : 0);
     } else {
       // Above D = 128 the rows' dimensions are split over two waves.
       constexpr size_t lds1 = lse_split_lds_bytes<DP>();
@@ -1282,7 +1495,7 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
       }
       auto kern = pl.lj ? &iso_lse_split<DP, true> : &iso_lse_split<DP, false>;
       hipLaunchKernelGGL(kern, dim3((unsigned)nblk1), dim3(kAccThreads), lds1, stream, X, ldx, pl.N,
-                         (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat, lj, ljmax, ljmask,
+                         (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat, lj, ljmax, ljmask, ljcount,
                          dense ? 1 : 0);
     }
   }
@@ -1290,6 +1503,20 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
   if constexpr (DP >= 64) {
     if (pl.lj) {
+      // Sparse masks (on average at most 2 needed row pairs per tile and block) go to
+      // iso_accum_sparse where it applies (D a multiple of 32 up to 128); both
+      // kernels are launched and each returns unless the count selects it.
+      int64_t sparse_max = -1;
+      if constexpr (DP <= 128) {
+        if (pl.D == DP) {
+          sparse_max = 2 * cdiv(pl.N, 32) * pl.KB;
+          const int64_t nw = (int64_t)pl.nslab * pl.rgroups * pl.KB;
+          hipLaunchKernelGGL((iso_accum_sparse<DP>), dim3((unsigned)cdiv(nw, kSparseWaves)),
+                             dim3(64 * kSparseWaves), 0, stream, X, ldx, pl.N, lj, ljmask, ljcount,
+                             sparse_max, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rgroups,
+                             pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
+        }
+      }
       auto launch = [&](auto cb_tag, auto nh_tag) -> hipError_t {
         constexpr int CB = decltype(cb_tag)::value;
         constexpr int NH = decltype(nh_tag)::value;
@@ -1301,7 +1528,8 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
           if (e != hipSuccess) return e;
         }
         hipLaunchKernelGGL((iso_accum_lj<DP, CB, NH>), grid2, dim3(kAccThreads), lds, stream, X, ldx,
-                           pl.N, (int)pl.D, lj, ljmask, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab,
+                           pl.N, (int)pl.D, lj, ljmask, ljcount, sparse_max, kc_lin, pl.KB, pl.KP,
+                           rowstat, pl.nslab,
                            pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
         return hipSuccess;
       };
@@ -1835,7 +2063,8 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
                        log_sigma_sq, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_musw),
                        reinterpret_cast<double2*>(ws + pl.off_kcblk),
                        reinterpret_cast<double4*>(ws + pl.off_kclin),
-                       reinterpret_cast<bf16x8*>(ws + pl.off_mu3));
+                       reinterpret_cast<bf16x8*>(ws + pl.off_mu3),
+                       pl.lj ? reinterpret_cast<unsigned*>(ws + pl.off_ljcount) : nullptr);
   if (N > 0) {
     auto run = [&](auto dp_tag) -> hipError_t {
       constexpr int DP = decltype(dp_tag)::value;

@@ -149,6 +149,23 @@ def test_zero_step_skip_is_bitwise_dense(case, recompute, gpu_device):
     assert_close_stats(a, oracle(inp), case)
 
 
+# Clustered shapes whose need masks are sparse (K >= 512): the accumulation pass
+# takes its sparse form (register-row pairs fetched per tile, with the overflow path
+# for tiles of more than three pairs at K=512), which must give the dense pass's bits.
+SPARSE_SHAPES = [(20000, 1024, 64), (20000, 512, 96), (40000, 512, 128), (30001, 1024, 128)]
+
+
+@pytest.mark.parametrize("N,K,D", SPARSE_SHAPES)
+def test_sparse_accumulation_is_bitwise_dense(N, K, D, gpu_device):
+    """Sparse accumulation (default) against the dense one (FGMM_FLAG_DENSE) and the oracle."""
+    inp = data.iso_clustered(N, K, D, seed=N % 101)
+    a = _into(inp, gpu_device)
+    b = _into(inp, gpu_device, dense=True)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+    assert_close_stats(a, oracle(inp), f"sparse N={N} K={K} D={D}")
+
+
 # Shapes on the stored log-joint path (D > 32 and K > 96), including row counts
 # that leave partial 32-row tiles and slabs, and both column splits of pass 2.
 LJ_SHAPES = [(33, 128, 128), (65, 257, 96), (1000, 130, 64), (777, 300, 61), (4097, 129, 100),
