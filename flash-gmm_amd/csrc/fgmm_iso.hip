@@ -1219,7 +1219,8 @@ void iso_accum_sparse(const float* __restrict__ X, int64_t ldx, int64_t N, const
   constexpr int PD = kSparseDepth;
   constexpr int BT = kSparseBatch;
   typedef float fNJ __attribute__((ext_vector_type(NJ)));
-  __shared__ unsigned mks[kSparseWaves][BT];
+  // The batch's tiles with a nonzero mask, in order: (mask, tile offset in the batch).
+  __shared__ uint2 work[kSparseWaves][BT];
 
   if ((int64_t)lj_pair_total(ljcount) > sparse_max) return;
   const int lane = threadIdx.x & 63;
@@ -1251,20 +1252,29 @@ void iso_accum_sparse(const float* __restrict__ X, int64_t ldx, int64_t N, const
   for (int j = 0; j < NJ; ++j) acc[j] = zero16();
   float nk = 0.0f, sig = 0.0f;
 
+  // One window per tile for each operand: the tile's log-joint (4 KiB), its rows'
+  // state and its X rows (32 rows; rows past N are never in range, their need bits
+  // being clear).
+  const int64_t row00 = r_begin + rg * 32;
+  const float* lj0 = lj + ((row00 >> 5) * KB + kb) * kLjTile;
+  const double2* rs0 = rowstat + row00;
+  const float* x0 = X + row00 * ldx;
+  const int64_t lj_step = (int64_t)RG * KB * kLjTile, x_step = TR * ldx;
+  auto windows = [&](int t, buf_rsrc& lr, buf_rsrc& rr, buf_rsrc& xr) {
+    lr = make_rsrc(lj0 + t * lj_step, kLjTile * 4);
+    rr = make_rsrc(rs0 + (int64_t)t * TR, 32 * sizeof(double2));
+    xr = make_rsrc(x0 + t * x_step, (uint32_t)(32 * ldx * 4));
+  };
+
   // Slot registers of the PD tiles in flight.
   float sl[PD][S];
   double sz[PD][S];
   fNJ sx[PD][S];
   unsigned smk[PD];
+  int stl[PD];
 
-  auto tile_row0 = [&](int t) { return r_begin + (int64_t)t * TR + rg * 32; };
-  auto rsrcs = [&](int64_t row0, bool any, buf_rsrc& lr, buf_rsrc& rr, buf_rsrc& xr) {
-    const int nrow = any ? (int)(r_end - row0 < 32 ? r_end - row0 : 32) : 0;
-    lr = make_rsrc(any ? lj + ((row0 >> 5) * KB + kb) * kLjTile : lj, any ? kLjTile * 4 : 0);
-    rr = make_rsrc(any ? rowstat + row0 : rowstat, (uint32_t)(nrow * sizeof(double2)));
-    xr = make_rsrc(any ? X + row0 * ldx : X, (uint32_t)(nrow * ldx * 4));
-  };
-  // Loads of one register-row pair (rows ro and ro + 4; this lane's is ro + 4g).
+  // Loads of one register-row pair (rows ro and ro + 4; this lane's is ro + 4g) of
+  // tile t; nothing when `used` is false or this lane's row is not needed.
   auto load_pair = [&](const buf_rsrc& lr, const buf_rsrc& rr, const buf_rsrc& xr, unsigned m, int ro,
                        bool used, float& l, double& z, fNJ& x) {
     const int row = ro + 4 * g;
@@ -1274,12 +1284,10 @@ void iso_accum_sparse(const float* __restrict__ X, int64_t ldx, int64_t N, const
     const int xo = buf_off(need ? (int)((row * ldx + NJ * c) * 4) : kBufOob);
     if constexpr (NJ == 4) {
       x = buf_load_f32x4(xr, xo);
-    } else if constexpr (NJ == 2) {
-      x = __builtin_bit_cast(fNJ, __builtin_amdgcn_raw_buffer_load_b64(xr, xo, 0, 0));
     } else if constexpr (NJ == 3) {
       x = __builtin_bit_cast(fNJ, __builtin_amdgcn_raw_buffer_load_b96(xr, xo, 0, 0));
     } else {
-      x = __builtin_bit_cast(fNJ, __builtin_amdgcn_raw_buffer_load_b32(xr, xo, 0, 0));
+      x = __builtin_bit_cast(fNJ, __builtin_amdgcn_raw_buffer_load_b64(xr, xo, 0, 0));
     }
   };
   // One pair's contribution, in the arithmetic of iso_accum_lj.
@@ -1295,64 +1303,75 @@ void iso_accum_sparse(const float* __restrict__ X, int64_t ldx, int64_t N, const
       for (int jj = 0; jj < NJ; ++jj) acc[jj] = mfma32(rv, x[jj], acc[jj]);
     }
   };
-  // Issue tile t's slot loads into stage u (mask 0: all out of range).
-  auto issue = [&](int t, int b0, int u) {
+  // Issue work item k of the batch (tile b0 + offset) into stage u; past the count,
+  // mask 0 makes every load out of range.
+  auto issue = [&](int k, int cnt, int b0, int u) {
     unsigned m = 0u;
-    if (t < ntiles && t - b0 < BT) m = __builtin_amdgcn_readfirstlane(mks[wave][t - b0]);
+    int t = 0;
+    if (k < cnt) {
+      const uint2 e = work[wave][k];
+      m = __builtin_amdgcn_readfirstlane(e.x);
+      t = b0 + __builtin_amdgcn_readfirstlane(e.y);
+    }
     smk[u] = m;
+    stl[u] = t;
     buf_rsrc lr, rr, xr;
-    rsrcs(tile_row0(t), m != 0u, lr, rr, xr);
+    windows(t, lr, rr, xr);
     unsigned pm = lj_pair_mask(m);
 #pragma unroll
-    for (int k = 0; k < S; ++k) {
+    for (int j = 0; j < S; ++j) {
       const bool used = pm != 0u;
       const int ro = used ? __builtin_ctz(pm) : 0;
       pm &= pm - 1u;
-      load_pair(lr, rr, xr, m, ro, used, sl[u][k], sz[u][k], sx[u][k]);
+      load_pair(lr, rr, xr, m, ro, used, sl[u][j], sz[u][j], sx[u][j]);
     }
   };
-  auto process = [&](int t, int u) {
+  auto process = [&](int u) {
     const unsigned m = smk[u];
     if (m == 0u) return;
     unsigned pm = lj_pair_mask(m);
 #pragma unroll
-    for (int k = 0; k < S; ++k) {
+    for (int j = 0; j < S; ++j) {
       if (pm == 0u) return;
       const int ro = __builtin_ctz(pm);
       pm &= pm - 1u;
-      accumulate(m, ro, sl[u][k], sz[u][k], sx[u][k]);
+      accumulate(m, ro, sl[u][j], sz[u][j], sx[u][j]);
     }
-    if (pm != 0u) {   // more pairs than slots: load them now
-      buf_rsrc lr, rr, xr;
-      rsrcs(tile_row0(t), true, lr, rr, xr);
-      while (pm != 0u) {
-        const int ro = __builtin_ctz(pm);
-        pm &= pm - 1u;
-        float l;
-        double q;
-        fNJ x;
-        load_pair(lr, rr, xr, m, ro, true, l, q, x);
-        accumulate(m, ro, l, q, x);
-      }
+    if (pm == 0u) return;
+    buf_rsrc lr, rr, xr;   // more pairs than slots: load them now
+    windows(stl[u], lr, rr, xr);
+    while (pm != 0u) {
+      const int ro = __builtin_ctz(pm);
+      pm &= pm - 1u;
+      float l;
+      double q;
+      fNJ x;
+      load_pair(lr, rr, xr, m, ro, true, l, q, x);
+      accumulate(m, ro, l, q, x);
     }
   };
 
   for (int b0 = 0; b0 < ntiles; b0 += BT) {
-    // Masks of tiles b0 .. b0 + BT - 1.
+    // Compact the batch's nonzero masks (this wave only; LDS is in order per wave).
+    int cnt = 0;
 #pragma unroll
     for (int q = 0; q < BT / 64; ++q) {
       const int t = b0 + 64 * q + lane;
-      const int64_t row0 = tile_row0(t);
-      mks[wave][64 * q + lane] = (t < ntiles && row0 < r_end) ? ljmask[(row0 >> 5) * KB + kb] : 0u;
+      const int64_t row0 = r_begin + (int64_t)t * TR + rg * 32;
+      const unsigned m = (t < ntiles && row0 < r_end) ? ljmask[(row0 >> 5) * KB + kb] : 0u;
+      const unsigned long long bal = __builtin_amdgcn_ballot_w64(m != 0u);
+      const int pos = cnt + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bal >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((unsigned)bal, 0u));
+      if (m != 0u) work[wave][pos] = make_uint2(m, (unsigned)(64 * q + lane));
+      cnt += __builtin_popcountll(bal);
     }
 #pragma unroll
-    for (int u = 0; u < PD; ++u) issue(b0 + u, b0, u);
-    for (int tt = 0; tt < BT; tt += PD) {
-      if (b0 + tt >= ntiles) break;
+    for (int u = 0; u < PD; ++u) issue(u, cnt, b0, u);
+    for (int kk = 0; kk < cnt; kk += PD) {
 #pragma unroll
       for (int u = 0; u < PD; ++u) {
-        process(b0 + tt + u, u);
-        issue(b0 + tt + u + PD, b0, u);
+        process(u);
+        issue(kk + u + PD, cnt, b0, u);
       }
     }
   }
