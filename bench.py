@@ -80,7 +80,7 @@ def cpu_baseline(inp, kind, K, D, min_s=10.0, max_s=30.0, rows=16384):
 # for FETCH_SIZE, x1.0 for WRITE_SIZE); the counter values and commands are in
 # profiles/<kind>_estep_<shape>.md.  Not reported with --recompute.
 TRAFFIC_BYTES = {
-    "iso_n1m_k1024_d128": {"phase1": 4_733_227_008, "phase2": 4_658_505_728},
+    "iso_n1m_k1024_d128": {"phase1": 3_145_381_888, "phase2": 799_930_368},
     "diag_n1m_k1024_d96": {"phase1": 4_499_631_140, "phase2": 4_542_595_401},
     "full_n250k_k256_d64": {"phase1": 589_263_972, "phase2": 414_389_462},
 }
@@ -117,6 +117,12 @@ def algorithmic_bytes(kind, N, K, D, lj):
     fp64; diag, full: logZ2) and, when pass 2 reads it, the fp32 log-joint.
     Phase 2 reads X, the per-row state and the log-joint.  O(K*D) operands and the
     slab partials are left out (under 1% here).
+
+    The isotropic log-joint is sparse: phase 1 writes it whole at most (rows the
+    running max already rules out are left unwritten) with a per-row block maximum
+    and a need mask per tile, and phase 2 reads X, the row state and the masks, plus
+    only the log-joint rows whose need bit is set, a data-dependent share that is
+    not counted here (the measured traffic includes it).
     """
     KB = -(-K // 32)
     if kind == "full":
@@ -126,6 +132,9 @@ def algorithmic_bytes(kind, N, K, D, lj):
     lj_bytes = lj_bytes if lj else 0
     row = 16 if kind == "iso" else 8
     x = 4.0 * N * D
+    if kind == "iso" and lj:
+        masks = lj_bytes / 4096 * (128 + 4)
+        return x + 4.0 * N + row * N + lj_bytes + masks, x + row * N + lj_bytes / 4096 * 4
     return x + 4.0 * N + row * N + lj_bytes, x + row * N + lj_bytes
 
 
@@ -343,6 +352,8 @@ def main():
     step_tflops = flop / (ms * 1e-3) / 1e12
     p2_kernel = {"iso": "iso_accum", "diag": "diag_accum", "full": "full_accum"}[kind] + (
         "_lj" if stored_lj and kind != "full" else "")
+    if kind == "iso" and stored_lj and D % 32 == 0 and D <= 128:
+        p2_kernel = "iso_accum_sparse or iso_accum_lj, picked on device by mask density"
     names = (f"{kind}_lse (log-normaliser pass + prologue"
              + (", stores the log-joint)" if stored_lj else ")"),
              f"{p2_kernel} (accumulation pass + slab reduction"

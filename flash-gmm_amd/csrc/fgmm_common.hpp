@@ -369,9 +369,10 @@ __device__ __forceinline__ void lj_load(const float* __restrict__ tile, int lane
 // float pair pass 2 forms from logZ2, bit r is clear when
 //     fl(fl(bmax - z.hi) - z.lo) < -kLjNeedGap.
 // Rounding is monotone, so every value l <= bmax of the row then gives
-// fl(fl(l - z.hi) - z.lo) < -kLjNeedGap as well, and 2^x is zero in fp32 for
-// x < -149: the responsibilities pass 2 would form are exactly zero.  Pass 2 reads
-// only the rows whose bit is set, so skipping the others changes no output bit.
+// fl(fl(l - z.hi) - z.lo) < -kLjNeedGap as well.  Below -150, 2^x is under half
+// the smallest fp32 denormal and v_exp_f32 returns 0, so the responsibilities pass
+// 2 would form are exactly zero.  Pass 2 reads only the rows whose bit is set, so
+// skipping the others changes no output bit.
 //
 // Pass 1 also leaves out the store of a row's block when the running max M of the
 // row's stored values already proves the mask bit will be clear:
@@ -380,8 +381,8 @@ __device__ __forceinline__ void lj_load(const float* __restrict__ tile, int lane
 // float evaluation above cannot reach -kLjNeedGap.  A half-wave whose block sum is
 // NaN always stores (the row's logZ2 is NaN, so its mask bit is set).
 // ---------------------------------------------------------------------------
-constexpr float kLjNeedGap = 200.0f;
-constexpr float kLjSkipGap = 232.0f;
+constexpr float kLjNeedGap = 160.0f;
+constexpr float kLjSkipGap = 192.0f;
 
 // Max over both half-waves of the row's block maximum (lane = row in pass 1).
 __device__ __forceinline__ float lj_row_max(double bm) {

@@ -1091,6 +1091,32 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       // have r = 0 on every lane, so the sums are those of the dense order.
       unsigned pm = (mc | (mc >> 4)) & 0x0f0f0f0fu;
       const unsigned mg = mc >> (4 * g);
+      if (__builtin_popcount(pm) >= 8) {
+        // A dense tile: all 16 register rows unrolled, in the same order.
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 z01 = *reinterpret_cast<const f32x4*>(rt + 8 * q);
+          const f32x4 z23 = *reinterpret_cast<const f32x4*>(rt + 8 * q + 2);
+          const float zh[4] = {z01.x, z01.z, z23.x, z23.z}, zl[4] = {z01.y, z01.w, z23.y, z23.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int ro = 8 * q + j;
+            if ((pm >> ro) & 1u) {
+              const float l = ljb[P][4 * q + j];
+              const float rv = ((mg >> ro) & 1u) ? fast_exp2((l - zh[j]) - zl[j]) : 0.0f;
+              if (NH == 1 || h == 0) {
+                nk += rv;
+                sig = fmaf(rv, c0 - l, sig);
+              }
+              if (dense || __builtin_amdgcn_ballot_w64(rv != 0.0f) != 0) {
+#pragma unroll
+                for (int jj = 0; jj < NJ; ++jj) acc[jj] = mfma32(rv, xbase[ro * RS + 32 * jj], acc[jj]);
+              }
+            }
+          }
+        }
+        pm = 0u;
+      }
       // Two register rows per round (the second optional), their LDS reads issued
       // together so that the two latency chains overlap.
       while (pm != 0u) {
