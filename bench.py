@@ -80,7 +80,7 @@ def cpu_baseline(inp, kind, K, D, min_s=10.0, max_s=30.0, rows=16384):
 # for FETCH_SIZE, x1.0 for WRITE_SIZE); the counter values and commands are in
 # profiles/<kind>_estep_<shape>.md.  Not reported with --recompute.
 TRAFFIC_BYTES = {
-    "iso_n1m_k1024_d128": {"phase1": 3_145_381_888, "phase2": 799_930_368},
+    "iso_n1m_k1024_d128": {"phase1": 3_140_715_520, "phase2": 799_602_688},
     "diag_n1m_k1024_d96": {"phase1": 4_499_631_140, "phase2": 4_542_595_401},
     "full_n250k_k256_d64": {"phase1": 589_263_972, "phase2": 414_389_462},
 }

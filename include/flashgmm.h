@@ -61,8 +61,10 @@ enum fgmm_flags {
     FGMM_FLAG_PHASE2 = 1u << 4,
     /* The accumulation pass skips every matrix-core step whose responsibilities
      * (two rows x 32 components) are all exactly zero, since such a step adds
-     * nothing; the results are bitwise the same either way.  DENSE runs every
-     * step (for timing the dense contraction). */
+     * nothing; on the isotropic stored log-joint it does not even read the rows
+     * whose responsibilities pass 1 proved zero.  The results are bitwise the same
+     * either way.  DENSE runs every step and, in pass 1, stores every row (for
+     * timing the dense contraction). */
     FGMM_FLAG_DENSE = 1u << 5,
     /* By default pass 1 also stores the fp32 log-joint (N/32 x K/32 tiles of
      * 4 KiB, when that is at most 16 GiB, D > 32 and K > 96) in the workspace,
