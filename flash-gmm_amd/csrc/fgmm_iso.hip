@@ -8,30 +8,42 @@
 //   Nk_k = sum_n r_nk ; mu_acc_k = sum_n r_nk x_n ; sig_acc_k = sum_n r_nk ||x_n - mu_k||^2
 //
 // Kernels, all launched on the caller's stream:
-//   iso_prep    O(K*D): per-component constants (fp64) and mu re-laid out in the
-//               matrix-core operand order ("mu_sw").
-//   iso_lse     pass 1, grid over row tiles. Each wave keeps 32 rows of X resident
-//               in registers and streams mu in blocks of 32 components; the cross
-//               term is a 32x32x2 fp32 MFMA contraction (S^T = mu . X^T, so every
-//               lane owns one row) and the log-sum-exp is an online max/sum in
-//               registers. Writes logZ and per-row (||x||^2, logZ2) in fp64.
+//   iso_prep    O(K*D): per-component constants (fp64), mu re-laid out in the
+//               matrix-core operand orders (fp32 and three-way bf16 splits with
+//               the centring offsets), and the needed-pair counters zeroed.
+//   iso_lse     pass 1 up to D = 128, grid over row tiles.  Each wave keeps 32 rows
+//               of X resident in registers as bf16 splits and streams mu in blocks
+//               of 32 components through LDS; the cross term is the centred
+//               split-bf16 contraction (x6c_tile, lane = row, register = component)
+//               and the log-sum-exp is an online max/sum in registers.  Writes logZ
+//               and per-row (||x||^2, logZ2) in fp64; with the stored log-joint also
+//               its rows (row-major tiles), each row's block maximum, and after the
+//               last block the need masks and the needed-pair count.
+//   iso_lse_split
+//               pass 1 above D = 128: two waves per row tile, one half of D each,
+//               with the accurate fp32-step contraction (cross_tile).
+//   iso_accum_sparse / iso_accum_lj
+//               pass 2 from the stored log-joint.  Both are launched; the count of
+//               needed register-row pairs left by pass 1 selects one on the device.
+//               The sparse kernel fetches each needed row pair into registers
+//               without any workgroup staging; the other stages X tiles in LDS for
+//               8 component blocks and reads the needed log-joint rows.  Either way
+//               r = 2^(ll2 - logZ2) and mu_acc += r^T X on the matrix cores with r as
+//               the A operand, Nk and sig_acc on the VALU, one partial per (slab,
+//               row group, component).
 //   iso_accum_lds / iso_accum_split
-//               pass 2, grid over (row slab x group of 128 components). Each wave
-//               owns 32 components and walks its slab in 32-row tiles staged through
-//               LDS: S = X . mu^T on MFMA, r = 2^(ll2 - logZ2) in registers, then
-//               mu_acc += r^T X on MFMA with r used directly as the A operand (no
-//               transpose), Nk and sig_acc on the VALU. Writes one partial per
-//               (slab, row group, component). Up to D = 128 mu sits in LDS; above,
-//               two waves share a component block, one half of D each.
+//               pass 2 recomputing the log-joint (FGMM_FLAG_RECOMPUTE, small K or
+//               past the workspace cap): X tiles through LDS, S = X . mu^T on the
+//               matrix cores, then as above.
 //   iso_reduce  fixed-order fp64 sum of the slab partials (deterministic), or
 //               the atomic variant selected by FGMM_FLAG_ATOMIC_REDUCE.
+//   iso_bf16_*  the bf16 operand contract (FGMM_FLAG_BF16).
 //
-// Accuracy: the D-contraction runs on the fp32 matrix cores in chunks of 8
-// dimensions (4 MFMA steps from a zero accumulator), and the chunk results are
-// summed in fp64 together with fp64 ||x||^2 and constants (cross_tile()).  A
-// single fp32 chain over D=128 leaves ~3e-4 absolute error in logZ on clustered
-// data; the chunked form stays below 1e-4.  Both passes use the same routine,
-// so they form bitwise-identical log-joints.
+// Accuracy: pass 1 sums the split-bf16 chunk results in fp32 and combines them with
+// the fp64 ||x||^2 and constants; the fp32-step contraction keeps every 8 dimensions
+// in a fresh accumulator and sums chunk pairs in fp64 (cross_tile()).  A single fp32
+// chain over D=128 would leave ~3e-4 absolute error in logZ on clustered data; both
+// forms stay below 1e-4.
 
 #include "fgmm_common.hpp"
 
