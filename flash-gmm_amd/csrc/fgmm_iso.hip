@@ -320,7 +320,8 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                                 // [2][BLK]
   double2* kc_l = reinterpret_cast<double2*>(lds_raw + 2 * BLK * sizeof(bf16x8));   // [2][32]
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: tile bases in scalars
   const int c = lane & 31, g = lane >> 5;
   const int64_t tile = (int64_t)blockIdx.x * kWaves + wave;   // 32-row tile
   const int64_t row = tile * 32 + c;
@@ -454,7 +455,8 @@ void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   double* ex = reinterpret_cast<double*>(p);     p += 2 * kWaves * 16 * 64 * sizeof(double);
   double* xq = reinterpret_cast<double*>(p);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: tile bases in scalars
   const int c = lane & 31, g = lane >> 5;
   const int rg = wave & 3, h = wave >> 2;
   const int64_t tile = (int64_t)blockIdx.x * kWaves + rg;   // 32-row tile
