@@ -228,15 +228,17 @@ __device__ __forceinline__ void split3_bf16(const f32x4 lo, const f32x4 hi, bf16
 // adds sum_q o_q back in fp64).  Per chunk: the five small terms, then -o_q (three
 // bf16 values in k slots 0..2 of split 3 of the A operand, times the ones operand),
 // then x1 mu1: for the components near a row the accumulator then stays small,
-// and chunk q accumulates in chain q % 4 (four independent chains cover the matrix
-// latency), the chains being added in fp32 at the end.  loadA(q, s) returns split s
+// and chunk q accumulates in chain q % MAXCH (independent chains cover the matrix
+// latency; four by default), the chains being added in fp32 at the end.  The same
+// form serves other feature layouts whose o_q centres the chunk (the diagonal
+// model's [x^2, x] chunks).  loadA(q, s) returns split s
 // of A-operand chunk q (lane: row m = lane % 32, dimensions 16q + 8(lane/32) + e),
 // xb[q][s] the B operand.  CPU emulation of the hardware rules on the N=1M, K=1024,
 // D=128 clustered data: max logZ error 4.5e-5 over 65,536 rows (4.2e-5 with the
 // chunks summed in fp64, 5.5e-5 for fp32 steps on 8-dimension chunks).
-template <int NQ, typename LA>
+template <int NQ, int MAXCH = 4, typename LA>
 __device__ __forceinline__ f32x16 x6c_tile(LA loadA, const bf16x8 (&xb)[NQ][3], const bf16x8 ones) {
-  constexpr int NCH = NQ < 4 ? NQ : 4;
+  constexpr int NCH = NQ < MAXCH ? NQ : MAXCH;
   f32x16 acc[NCH];
 #pragma unroll
   for (int h = 0; h < NCH; ++h) acc[h] = zero16();

@@ -77,8 +77,8 @@ struct DiagPlan {
   bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16)
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
   int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
-  size_t off_musw, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_sq, off_part_nk, off_lj,
-      total;
+  size_t off_musw, off_mu3, off_kcx6, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_sq,
+      off_part_nk, off_lj, total;
 };
 
 // Pass 2 reads the stored log-joint when recomputation is not requested, there are
@@ -130,6 +130,8 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool b
   p.npart = p.nslab * p.rgroups;
   size_t off = 0;
   p.off_musw = off;    off = align256(off + (size_t)p.KP * p.FP * sizeof(float));
+  p.off_mu3 = off;     off = align256(off + (bf16 ? 0 : (size_t)p.KP * (p.DP / 8) * 4 * 2 * sizeof(bf16x8)));
+  p.off_kcx6 = off;    off = align256(off + (bf16 ? 0 : (size_t)p.KP * sizeof(double)));
   p.off_kcblk = off;   off = align256(off + (size_t)p.KP * sizeof(double));
   p.off_kclin = off;   off = align256(off + (size_t)p.KP * sizeof(double));
   p.off_rowstat = off; off = align256(off + (size_t)(N > 0 ? N : 0) * sizeof(double));
@@ -415,6 +417,266 @@ void diag_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const double mn = fmax(mx, mo);
     const double ms = (mn == -INFINITY) ? 0.0 : mn;
     const float tot = sm * fast_exp2((float)(mx - ms)) + so * fast_exp2((float)(mo - ms));
+    const double lz2 = mn + (double)log2f(tot);
+    if (valid && g == 0) {
+      rowstat[row] = lz2;
+      if (logZ) logZ[row] = (float)(lz2 * kLn2);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 1 on the bf16 matrix cores, up to D = 128: the centred split-bf16 cross term
+// of the isotropic pass 1 (x6c_tile) over chunks of 8 dimensions.  Chunk q is 16
+// features: lane-half g holds dimensions 8q + 4g .. +3 as [x^2 (4), x (4)] against
+// [-w (4), 2v (4)], each fp32 value split exactly into three bf16.  The chunk's
+// centring offset is o_q = fp32(sum over its 8 dimensions of mu_d^2 w_d), so for
+// the components near a row the chunk sum -sum (x_d - mu_d)^2 w_d stays small; the
+// offsets return through C'_k = C_k + sum_q o_q in fp64.  CPU emulation of the
+// matrix-step rounding on the N=1M, K=1024, D=96 clustered data: max logZ error
+// 2.4e-5 over 16,384 rows, against 5.2e-5 for the fp32-step form.
+//
+// Eight waves = 4 row groups x 2 halves of the chunks, so each wave holds the bf16
+// splits of half of its 32 rows' features (72 registers at D = 96).  The two waves
+// of a row group then share the rest evenly: each sends the other the fp32 chunk
+// sums of the 8 accumulator registers the other owns (through LDS), adds the pair
+// for its own 8 (fp32 addition commutes, so the sum does not depend on which wave
+// forms it) and runs the online log-sum-exp and the log-joint stores for them; the
+// two partial (max, sum) pairs of a row are merged once at the end.
+// ---------------------------------------------------------------------------
+template <int DP>
+constexpr size_t x6_block_bytes() { return (size_t)(DP / 8) * 4 * 64 * sizeof(bf16x8); }
+template <int DP>
+constexpr int x6_mu_buffers() {
+  constexpr size_t ex = (size_t)kWaves * 16 * 64 * sizeof(float);
+  return 2 * x6_block_bytes<DP>() + 2 * ex + 3 * 32 * sizeof(double) <= kMaxLds ? 2 : 1;
+}
+template <int DP>
+constexpr size_t x6_lds_bytes() {
+  constexpr int MB = x6_mu_buffers<DP>();
+  return (size_t)MB * x6_block_bytes<DP>() + (size_t)MB * kWaves * 16 * 64 * sizeof(float) +
+         (size_t)(MB + 1) * 32 * sizeof(double);
+}
+__host__ __device__ constexpr bool diag_uses_x6(int DP) { return DP <= 128; }
+
+// Prologue of that pass: the split operands [kb][chunk][split 0..2, offset][lane] and
+// C'_k in the accumulator's row order.  One 64-thread block per 32 components.
+__global__ __launch_bounds__(64) void diag_x6_prep(const float* __restrict__ mu, int64_t ldmu,
+                                                   const float* __restrict__ lss, int64_t ldlss, int64_t K,
+                                                   int D, int DP, const float* __restrict__ lpi,
+                                                   bf16x8* __restrict__ mu3, double* __restrict__ kc_x6) {
+  __shared__ double sC[32];
+  const int kb = blockIdx.x;
+  const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  const int64_t comp = (int64_t)kb * 32 + c;
+  const bool valid = comp < K;
+  const int NQ = DP / 8;
+  double osum = 0.0;
+  for (int q = 0; q < NQ; ++q) {
+    f32x4 fw = zero4(), fv = zero4();
+    double o = 0.0;
+    if (valid) {
+      for (int d = 8 * q; d < 8 * q + 8 && d < D; ++d) {
+        const double m = (double)mu[comp * ldmu + d];
+        const double w = 0.5 * exp(-(double)lss[comp * ldlss + d]) * kLog2e;
+        o = fma(m * m, w, o);
+        const int e = d - 8 * q - 4 * g;
+        if (e >= 0 && e < 4) {
+          fw[e] = (float)(-w);
+          fv[e] = (float)(2.0 * m * w);
+        }
+      }
+    }
+    bf16x8 s[3];
+    split3_bf16(fw, fv, s);
+    bf16x8* dst = mu3 + ((int64_t)kb * NQ + q) * 4 * 64 + lane;
+#pragma unroll
+    for (int t = 0; t < 3; ++t) dst[t * 64] = s[t];
+    const float of = (float)o;
+    osum += (double)of;
+    f32x4 ov = zero4();
+    if (g == 0) ov.x = -of;
+    bf16x8 so[3];
+    split3_bf16(ov, zero4(), so);
+    bf16x8 off;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) off[e] = (__bf16)0.0f;
+    if (g == 0) {
+      off[0] = so[0][0];
+      off[1] = so[1][0];
+      off[2] = so[2][0];
+    }
+    dst[3 * 64] = off;
+  }
+  if (g == 0) {
+    double C = -INFINITY;
+    if (valid) {
+      double lsum = 0.0, qs = 0.0;
+      for (int d = 0; d < D; ++d) {
+        const double l = (double)lss[comp * ldlss + d];
+        const double m = (double)mu[comp * ldmu + d];
+        lsum += l;
+        qs = fma(m * m, 0.5 * exp(-l) * kLog2e, qs);
+      }
+      C = ((double)lpi[comp] - 0.5 * ((double)D * kLog2Pi + lsum)) * kLog2e - qs + osum;
+    }
+    sC[c] = C;
+  }
+  __syncthreads();
+  if (lane < 32) {
+    const int i = lane & 15, gg = lane >> 4;
+    kc_x6[(int64_t)kb * 32 + gg * 16 + i] = sC[acc_row(i, gg)];
+  }
+}
+
+template <int DP, bool LJ>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
+void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                 const bf16x8* __restrict__ mu3, const double* __restrict__ kc_x6, int KB,
+                 float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj) {
+  constexpr int NQ = DP / 8;              // chunks of 8 dimensions (16 features)
+  constexpr int NQH = NQ / 2;             // per half
+  constexpr int BLK = NQ * 4 * 64;        // bf16x8 per 32-component block
+  constexpr int LPT = BLK / kAccThreads;
+  constexpr int MB = x6_mu_buffers<DP>();
+  constexpr int NKC = MB + 1;             // constant buffers
+  static_assert(BLK % kAccThreads == 0 && NQ % 2 == 0, "split shape");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  unsigned char* p = lds_raw;
+  bf16x8* mu_l = reinterpret_cast<bf16x8*>(p); p += (size_t)MB * BLK * sizeof(bf16x8);
+  float* ex = reinterpret_cast<float*>(p);     p += (size_t)MB * kWaves * 16 * 64 * sizeof(float);
+  double* kc_l = reinterpret_cast<double*>(p);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int rg = wave & 3, h = wave >> 2;
+  const int64_t tile = (int64_t)blockIdx.x * kWaves + rg;   // 32-row tile
+  const int64_t row = tile * 32 + c;
+  const bool valid = row < N;
+
+  // Blocks go global -> registers -> LDS.  Up to D = 96 through two register
+  // stages: block kb + 2 is fetched while block kb is contracted and lands in LDS at
+  // the end of iteration kb + 1, so each fetch has a whole iteration to arrive.  At
+  // D = 128 (registers) one stage: block kb + 1 is fetched and committed in
+  // iteration kb.
+  constexpr int NST = DP <= 96 ? 2 : 1;
+  bf16x8 st[NST][LPT];
+  double kst[NST];
+#pragma unroll
+  for (int u = 0; u < NST; ++u) kst[u] = 0.0;
+  auto fetch = [&](int kb, bf16x8 (&s)[LPT], double& k) {
+    if (kb >= KB) return;
+    const bf16x8* src = mu3 + (int64_t)kb * BLK;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) s[q] = src[q * kAccThreads + tid];
+    if (tid < 32) k = kc_x6[(int64_t)kb * 32 + tid];
+  };
+  auto commit = [&](int kb, const bf16x8 (&s)[LPT], double k) {
+    bf16x8* dst = mu_l + (MB == 2 ? (kb & 1) : 0) * BLK;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) dst[q * kAccThreads + tid] = s[q];
+    if (tid < 32) kc_l[(kb % NKC) * 32 + tid] = k;
+  };
+  fetch(0, st[0], kst[0]);
+  // This half's chunks: dimensions 8q + 4g .. +3 as [x^2, x], split three ways.
+  bf16x8 xb[NQH][3];
+#pragma unroll
+  for (int qq = 0; qq < NQH; ++qq) {
+    const f32x4 x = load_row4(X, ldx, row, 8 * (h * NQH + qq) + 4 * g, D, valid);
+    split3_bf16(x * x, x, xb[qq]);
+  }
+  const bf16x8 ones = x6c_ones(lane);
+  commit(0, st[0], kst[0]);
+  if constexpr (NST == 2) fetch(1, st[NST - 1], kst[NST - 1]);
+  lds_barrier();
+
+  double mx = -INFINITY;
+  float sm = 0.0f;
+  // The loop is compiled once per half so that register indices stay constant, and
+  // unrolled by two so that the staging registers have fixed parity.
+  auto run = [&](auto half) {
+    constexpr int H = decltype(half)::value;
+    constexpr int ib = 8 * H;   // this wave's accumulator registers ib .. ib + 7
+    auto step = [&](int kb, auto par) {
+      constexpr int P = decltype(par)::value;   // kb & 1
+      const int buf = MB == 2 ? P : 0;
+      const bool more = kb + 1 < KB;
+      constexpr int SN = NST == 2 ? 1 - P : 0;   // stage holding block kb + 1
+      if constexpr (NST == 2) {
+        fetch(kb + 2, st[P], kst[P]);
+      } else {
+        fetch(kb + 1, st[0], kst[0]);
+      }
+      const bf16x8* mp = mu_l + buf * BLK + H * NQH * 4 * 64 + lane;
+      // Two accumulator chains (CPU emulation: as accurate as four here, 32 fewer adds).
+      const f32x16 xm = x6c_tile<NQH, 2>([&](int q, int t) { return mp[(q * 4 + t) * 64]; }, xb, ones);
+      // Slot (buf, rg, H) carries this wave's sums for the other wave's registers.
+      float* exw = ex + ((size_t)(buf * kWaves + rg) * 2 + H) * 8 * 64 + lane;
+      const float* exr = ex + ((size_t)(buf * kWaves + rg) * 2 + (1 - H)) * 8 * 64 + lane;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) exw[j * 64] = xm[8 * (1 - H) + j];
+      if (MB == 2 && more) commit(kb + 1, st[SN], kst[SN]);
+      lds_barrier();
+      if (MB == 1 && more) commit(kb + 1, st[SN], kst[SN]);
+      const double* kp = kc_l + (kb % NKC) * 32 + g * 16 + ib;
+      double ll[8];
+      double bm = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        ll[j] = kp[j] + (double)(xm[ib + j] + exr[j * 64]);
+        bm = fmax(bm, ll[j]);
+      }
+      if constexpr (LJ) {
+        float* t = lj + (tile * KB + kb) * kLjTile + ib * 64 + lane;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) __builtin_nontemporal_store((float)ll[j], t + j * 64);
+      }
+      const double mn = fmax(mx, bm);
+      const double ms = (mn == -INFINITY) ? 0.0 : mn;
+      float acc = sm * fast_exp2((float)(mx - ms));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc += fast_exp2((float)(ll[j] - ms));
+      sm = acc;
+      mx = mn;
+      if (MB == 1) lds_barrier();
+    };
+    for (int kb = 0; kb < KB; kb += 2) {
+      step(kb, std::integral_constant<int, 0>{});
+      if (kb + 1 >= KB) break;
+      step(kb + 1, std::integral_constant<int, 1>{});
+    }
+  };
+  if (h == 0) {
+    run(std::integral_constant<int, 0>{});
+  } else {
+    run(std::integral_constant<int, 1>{});
+  }
+
+  // Merge the four partial (max, sum) pairs of a row: the lane-halves first, then
+  // the second wave's pair through LDS, in a fixed order.
+  double m1 = fmax(mx, __shfl_xor(mx, 32));
+  {
+    const double mo = __shfl_xor(mx, 32);
+    const float so = __shfl_xor(sm, 32);
+    const double ms = (m1 == -INFINITY) ? 0.0 : m1;
+    sm = sm * fast_exp2((float)(mx - ms)) + so * fast_exp2((float)(mo - ms));
+  }
+  double* px = reinterpret_cast<double*>(ex);                 // [kWaves][64] max, then sum
+  float* ps = reinterpret_cast<float*>(px + kWaves * 64);
+  lds_barrier();   // every wave has read its last exchange slot
+  if (h == 1) {
+    px[rg * 64 + lane] = m1;
+    ps[rg * 64 + lane] = sm;
+  }
+  lds_barrier();
+  if (h == 0) {
+    const double mo = px[rg * 64 + lane];
+    const float so = ps[rg * 64 + lane];
+    const double mn = fmax(m1, mo);
+    const double ms = (mn == -INFINITY) ? 0.0 : mn;
+    const float tot = sm * fast_exp2((float)(m1 - ms)) + so * fast_exp2((float)(mo - ms));
     const double lz2 = mn + (double)log2f(tot);
     if (valid && g == 0) {
       rowstat[row] = lz2;
@@ -1027,20 +1289,21 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
   float* pnk = reinterpret_cast<float*>(ws + pl.off_part_nk);
   if (run1) {
     const unsigned nblk1 = (unsigned)cdiv(pl.N, 32 * kWaves);
-    if constexpr (!diag_accum_split_d(DP)) {
-      constexpr size_t lds1 = lse_lds_bytes<DP>();
+    if constexpr (diag_uses_x6(DP)) {
+      constexpr size_t lds1 = x6_lds_bytes<DP>();
       if (lds1 > 65536) {
-        for (const void* f : {reinterpret_cast<const void*>(&diag_lse<DP, false>),
-                              reinterpret_cast<const void*>(&diag_lse<DP, true>)}) {
+        for (const void* f : {reinterpret_cast<const void*>(&diag_lse_x6<DP, false>),
+                              reinterpret_cast<const void*>(&diag_lse_x6<DP, true>)}) {
           hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
           if (e != hipSuccess) return e;
         }
       }
-      auto kern = pl.lj ? &diag_lse<DP, true> : &diag_lse<DP, false>;
-      hipLaunchKernelGGL(kern, dim3(nblk1), dim3(kThreads), lds1, stream, X, ldx, pl.N, (int)pl.D,
-                         mu_sw, kc_blk, pl.KB, logZ, rowstat, lj);
+      auto kern = pl.lj ? &diag_lse_x6<DP, true> : &diag_lse_x6<DP, false>;
+      hipLaunchKernelGGL(kern, dim3(nblk1), dim3(kAccThreads), lds1, stream, X, ldx, pl.N, (int)pl.D,
+                         reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
+                         reinterpret_cast<const double*>(ws + pl.off_kcx6), pl.KB, logZ, rowstat, lj);
     } else {
-      // From D = 128 the rows' dimensions are split over two waves.
+      // Above D = 128 the rows' dimensions are split over two waves.
       constexpr size_t lds1 = lse_split_lds_bytes<DP>();
       if (lds1 > 65536) {
         for (const void* f : {reinterpret_cast<const void*>(&diag_lse_split<DP, false>),
@@ -1647,11 +1910,16 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     hipLaunchKernelGGL(diag_bf16_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
                        (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_musw),
                        reinterpret_cast<float*>(ws + pl.off_kclin));
-  else if (run1)
+  else if (run1) {
     hipLaunchKernelGGL(diag_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
                        (int)D, pl.DP, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_musw),
                        reinterpret_cast<double*>(ws + pl.off_kcblk),
                        reinterpret_cast<double*>(ws + pl.off_kclin));
+    if (diag_uses_x6(pl.DP))
+      hipLaunchKernelGGL(diag_x6_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
+                         (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_mu3),
+                         reinterpret_cast<double*>(ws + pl.off_kcx6));
+  }
   if (N > 0) {
     auto run = [&](auto dp_tag) -> hipError_t {
       constexpr int DP = decltype(dp_tag)::value;
