@@ -11,7 +11,9 @@
 //
 // Same structure as the isotropic kernels (fgmm_iso.hip): a prologue that lays the
 // 2D-feature operand [-w, 2v] out in matrix-core order, a log-normaliser pass with
-// X resident in registers (the x^2 half of the feature vector is formed on the fly),
+// X resident in registers (the x^2 half of the feature vector is formed on the fly;
+// up to D = 128 on the bf16 matrix cores in the centred split-bf16 form,
+// diag_lse_x6, above with fp32 steps, diag_lse_split),
 // an accumulation pass split over component groups x row slabs with r used directly
 // as the A operand of r^T [x | x^2] (above D = 96 with the dimensions split over
 // two waves per component block), and a fixed-order fp64 reduction of the slab
@@ -203,103 +205,7 @@ __global__ __launch_bounds__(64) void diag_prep(const float* __restrict__ mu, in
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1: logZ.  Each wave keeps 32 rows of X resident; feature chunks m < DP/8
-// are x^2 (formed on the fly), the rest x.  mu' blocks stream through LDS.
-// ---------------------------------------------------------------------------
-template <int DP>
-constexpr size_t lse_lds_bytes() {
-  return (size_t)2 * (2 * DP) * 32 * sizeof(float) + (size_t)2 * 32 * sizeof(double);
-}
-
-template <int DP, bool LJ>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(DP <= 96 ? 2 : 1, DP <= 96 ? 2 : 1)))
-void diag_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
-              const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_blk, int KB,
-              float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj) {
-  constexpr int NMX = DP / 8;
-  constexpr int NM = 2 * NMX;
-  constexpr int BLK = NM * 64;
-  constexpr int LPT = BLK / kThreads;
-  static_assert(BLK % kThreads == 0, "block load must split evenly");
-
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  f32x4* mu_l = reinterpret_cast<f32x4*>(lds_raw);                              // [2][BLK]
-  double* kc_l = reinterpret_cast<double*>(lds_raw + 2 * BLK * sizeof(f32x4));  // [2][32]
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = lane & 31, g = lane >> 5;
-  const int64_t tile = (int64_t)blockIdx.x * kWaves + wave;   // 32-row tile
-  const int64_t row = tile * 32 + c;
-  const bool valid = row < N;
-
-  f32x4 st[LPT];
-  double kst = 0.0;
-  auto fetch = [&](int kb) {
-    const f32x4* src = mu_sw + (int64_t)kb * BLK;
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) st[q] = src[q * kThreads + tid];
-    if (tid < 32) kst = kc_blk[(int64_t)kb * 32 + tid];
-  };
-  auto commit = [&](int buf) {
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) mu_l[buf * BLK + q * kThreads + tid] = st[q];
-    if (tid < 32) kc_l[buf * 32 + tid] = kst;
-  };
-  fetch(0);
-  f32x4 xb[NMX];
-#pragma unroll
-  for (int m = 0; m < NMX; ++m) xb[m] = load_row4(X, ldx, row, 8 * m + 4 * g, D, valid);
-  commit(0);
-  __syncthreads();
-
-  double mx = -INFINITY;
-  float sm = 0.0f;
-  for (int kb = 0; kb < KB; ++kb) {
-    const int buf = kb & 1;
-    const bool more = kb + 1 < KB;
-    if (more) fetch(kb + 1);
-    const f32x4* mp = mu_l + buf * BLK + lane;
-    double xm[16];
-    cross_tile<NM>(xm, [&](int m) { return mp[m * 64]; },
-                   [&](int m) { return m < NMX ? sq4(xb[m]) : xb[m - NMX]; });
-    const double* kp = kc_l + buf * 32 + g * 16;
-    double ll[16];
-    double bm = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      ll[i] = kp[i] + xm[i];
-      bm = fmax(bm, ll[i]);
-    }
-    // Keep the max here: sunk past the conditional commit below, its operands
-    // would cross a block boundary and each cost a canonicalising max.
-    asm volatile("" : "+v"(bm));
-    // Unconditional: tiles are allocated for the whole grid.
-    if constexpr (LJ) lj_store(lj + (tile * KB + kb) * kLjTile, lane, ll);
-    const double mn = fmax(mx, bm);
-    const double ms = (mn == -INFINITY) ? 0.0 : mn;
-    float acc = sm * fast_exp2((float)(mx - ms));
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc += fast_exp2((float)(ll[i] - ms));
-    sm = acc;
-    mx = mn;
-    if (more) commit(buf ^ 1);
-    lds_barrier();
-  }
-  const double mo = __shfl_xor(mx, 32);
-  const float so = __shfl_xor(sm, 32);
-  const double mn = fmax(mx, mo);
-  const double ms = (mn == -INFINITY) ? 0.0 : mn;
-  const float tot = sm * fast_exp2((float)(mx - ms)) + so * fast_exp2((float)(mo - ms));
-  const double lz2 = mn + (double)log2f(tot);
-  if (valid && g == 0) {
-    rowstat[row] = lz2;
-    if (logZ) logZ[row] = (float)(lz2 * kLn2);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Pass 1 from D = 128: eight waves = 4 row groups x 2 halves of the dimensions, so
+// Pass 1 above D = 128: eight waves = 4 row groups x 2 halves of the dimensions, so
 // each wave holds half of its 32 rows in registers (two waves per SIMD).  Half h
 // multiplies its x^2 and x chunks by the matching chunks of the mu' block; the
 // second half's fp64 partials go through LDS and the first-half wave adds them in
