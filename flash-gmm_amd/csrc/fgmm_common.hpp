@@ -393,29 +393,38 @@ __device__ __forceinline__ float lj_row_max(double bm) {
   return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
 }
 
-// Pass-1 store of one (row tile, block) pair.  Lane (row c, half g) holds
-// components acc_row(i, g), i.e. 8j + 4g + 0..3 in registers 4j..4j+3: four float4
-// per lane, the two halves together filling each row's line.  Each instruction
-// writes 32 bytes of every row, so these are ordinary (write-back) stores that the
-// L2 merges into whole lines; non-temporal ones reach HBM piecewise, at about
-// twice the bytes.  `lse_sum` is the
-// half-wave's running log-sum-exp sum after the block (NaN if any value was NaN),
-// `run_max` the row's running max of stored values (updated here).
-__device__ __forceinline__ void lj_put_rows(float* __restrict__ tile, float* __restrict__ bmax, int c,
-                                            int g, const double (&ll)[16], double bm, float lse_sum,
-                                            float& run_max, bool dense) {
+// Pass-1 store of one (row tile, block) pair, or of the part of it one wave holds.
+// Lane (row c, half g) holds components acc_row(i, g), i.e. 8j + 4g + 0..3 in
+// registers 4j..4j+3: NG float4 per lane for the register groups j0 .. j0 + NG - 1,
+// the two halves together filling each row's line.  Each instruction writes 32 bytes
+// of every row, so these are ordinary (write-back) stores that the L2 merges into
+// whole lines; non-temporal ones reach HBM piecewise, at about twice the bytes.
+// `bm` is the lane's max over its values, `lse_sum` the half-wave's running
+// log-sum-exp sum after the block (NaN if any value was NaN), `run_max` the row's
+// running max of the stored values it covers (updated here); `bmax` receives the max
+// over both lane-halves.
+template <int NG>
+__device__ __forceinline__ void lj_put_rows_g(float* __restrict__ tile, float* __restrict__ bmax, int c,
+                                              int g, int j0, const double (&ll)[4 * NG], double bm,
+                                              float lse_sum, float& run_max, bool dense) {
   const float R = lj_row_max(bm);
   run_max = fmaxf(run_max, R);
   const bool skip = !dense && lse_sum == lse_sum && fabsf(run_max) < 0x1p24f && (R - run_max) < -kLjSkipGap;
   if (!skip) {
     float* p = tile + c * 32 + 4 * g;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NG; ++j) {
       const f32x4 v = {(float)ll[4 * j], (float)ll[4 * j + 1], (float)ll[4 * j + 2], (float)ll[4 * j + 3]};
-      *reinterpret_cast<f32x4*>(p + 8 * j) = v;
+      *reinterpret_cast<f32x4*>(p + 8 * (j0 + j)) = v;
     }
   }
   if (g == 0) bmax[c] = R;
+}
+
+__device__ __forceinline__ void lj_put_rows(float* __restrict__ tile, float* __restrict__ bmax, int c,
+                                            int g, const double (&ll)[16], double bm, float lse_sum,
+                                            float& run_max, bool dense) {
+  lj_put_rows_g<4>(tile, bmax, c, g, 0, ll, bm, lse_sum, run_max, dense);
 }
 
 // Pass-1 epilogue: need masks of the wave's row tile for all KB blocks.  Run by
@@ -431,23 +440,25 @@ __device__ __forceinline__ void lj_put_rows(float* __restrict__ tile, float* __r
 // spreads tiles over 64 counters (one atomic per wave) that the prologue zeroes.
 __device__ __forceinline__ unsigned lj_pair_mask(unsigned m) { return (m | (m >> 4)) & 0x0f0f0f0fu; }
 
+// Block kb's maxima are at bmax[kb * bstride + c] and its mask at mask[kb * mstride]
+// (strides 32 and 1 when one wave covers the whole block).
 __device__ __forceinline__ void lj_put_masks(const float* __restrict__ bmax, unsigned* __restrict__ mask,
                                              unsigned* __restrict__ count, int KB, int c, double lz2,
-                                             bool valid, bool dense) {
+                                             bool valid, bool dense, int bstride = 32, int mstride = 1) {
   const float zx = (float)lz2;
   const float zy = (lz2 > -INFINITY && lz2 < INFINITY) ? (float)(lz2 - (double)zx) : 0.0f;
   unsigned pairs = 0;
   for (int kb0 = 0; kb0 < KB; kb0 += 8) {
     float R[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) R[j] = kb0 + j < KB ? bmax[(kb0 + j) * 32 + c] : 0.0f;
+    for (int j = 0; j < 8; ++j) R[j] = kb0 + j < KB ? bmax[(kb0 + j) * bstride + c] : 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if (kb0 + j < KB) {
         const bool need = valid && (dense || !(((R[j] - zx) - zy) < -kLjNeedGap));
         const unsigned b = (unsigned)__builtin_amdgcn_ballot_w64(need);
         pairs += __builtin_popcount(lj_pair_mask(b));
-        if (c == 0) mask[kb0 + j] = b;
+        if (c == 0) mask[(kb0 + j) * mstride] = b;
       }
     }
   }

@@ -69,6 +69,9 @@ __host__ __device__ constexpr int bf16_parts(int DP);
 __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB);
 __host__ inline int bf16_blocks_per_group(int DP, int KB);
 
+// Pass 1 runs on the bf16 matrix cores (split-bf16 cross term) up to D = 128.
+__host__ __device__ constexpr bool diag_uses_x6(int DP) { return DP <= 128; }
+
 struct DiagPlan {
   int64_t N, K, D;
   int DP, FP;   // D padded (32 up to 128, then 64); feature count 2*DP
@@ -79,8 +82,9 @@ struct DiagPlan {
   bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16)
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
   int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
+  bool lj_sparse;   // the stored log-joint in the sparse form (pass 1 on the bf16 cores, D <= 128)
   size_t off_musw, off_mu3, off_kcx6, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_sq,
-      off_part_nk, off_lj, total;
+      off_part_nk, off_lj, off_ljmax, off_ljmask, off_ljcount, total;
 };
 
 // Pass 2 reads the stored log-joint when recomputation is not requested, there are
@@ -140,8 +144,16 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool b
   p.off_part_mu = off; off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
   p.off_part_sq = off; off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
   p.off_part_nk = off; off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
-  p.off_lj = off;   // one tile per pass-1 wave: the grid's 32-row tiles, rounded up to 4
-  if (p.lj) off = align256(off + (size_t)round_up(cdiv(N, 32), 4) * p.KB * kLjTile * sizeof(float));
+  // One log-joint tile per pass-1 wave (the grid's 32-row tiles, rounded up to 4);
+  // in the sparse form with each row's block maxima and the need masks, one half
+  // (16 components) per pass-1 wave.
+  p.lj_sparse = p.lj && diag_uses_x6(p.DP);
+  const size_t ntile = p.lj ? (size_t)round_up(cdiv(N, 32), 4) * p.KB : 0;
+  const size_t nsp = p.lj_sparse ? ntile : 0;
+  p.off_lj = off;      off = align256(off + ntile * kLjTile * sizeof(float));
+  p.off_ljmax = off;   off = align256(off + nsp * 64 * sizeof(float));
+  p.off_ljmask = off;  off = align256(off + nsp * sizeof(uint2));
+  p.off_ljcount = off; off = align256(off + (p.lj_sparse ? 64 * sizeof(unsigned) : 0));
   p.total = off;
   return p;
 }
@@ -363,17 +375,19 @@ constexpr size_t x6_lds_bytes() {
   return (size_t)MB * x6_block_bytes<DP>() + (size_t)MB * kWaves * 16 * 64 * sizeof(float) +
          (size_t)(MB + 1) * 32 * sizeof(double);
 }
-__host__ __device__ constexpr bool diag_uses_x6(int DP) { return DP <= 128; }
 
 // Prologue of that pass: the split operands [kb][chunk][split 0..2, offset][lane] and
 // C'_k in the accumulator's row order.  One 64-thread block per 32 components.
 __global__ __launch_bounds__(64) void diag_x6_prep(const float* __restrict__ mu, int64_t ldmu,
                                                    const float* __restrict__ lss, int64_t ldlss, int64_t K,
                                                    int D, int DP, const float* __restrict__ lpi,
-                                                   bf16x8* __restrict__ mu3, double* __restrict__ kc_x6) {
+                                                   bf16x8* __restrict__ mu3, double* __restrict__ kc_x6,
+                                                   unsigned* __restrict__ ljcount) {
   __shared__ double sC[32];
   const int kb = blockIdx.x;
   const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  // Pass 1 counts the needed row pairs of the sparse log-joint into these.
+  if (ljcount && kb == 0) ljcount[lane] = 0u;
   const int64_t comp = (int64_t)kb * 32 + c;
   const bool valid = comp < K;
   const int NQ = DP / 8;
@@ -439,7 +453,9 @@ template <int DP, bool LJ>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                  const bf16x8* __restrict__ mu3, const double* __restrict__ kc_x6, int KB,
-                 float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj) {
+                 float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj,
+                 float* __restrict__ ljmax, unsigned* __restrict__ ljmask, unsigned* __restrict__ ljcount,
+                 int dense) {
   constexpr int NQ = DP / 8;              // chunks of 8 dimensions (16 features)
   constexpr int NQH = NQ / 2;             // per half
   constexpr int BLK = NQ * 4 * 64;        // bf16x8 per 32-component block
@@ -500,6 +516,7 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   double mx = -INFINITY;
   float sm = 0.0f;
+  float run_max = -INFINITY;   // running max of the stored log-joint this wave covers
   // The loop is compiled once per half so that register indices stay constant, and
   // unrolled by two so that the staging registers have fixed parity.
   auto run = [&](auto half) {
@@ -534,11 +551,6 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
         ll[j] = kp[j] + (double)(xm[ib + j] + exr[j * 64]);
         bm = fmax(bm, ll[j]);
       }
-      if constexpr (LJ) {
-        float* t = lj + (tile * KB + kb) * kLjTile + ib * 64 + lane;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) __builtin_nontemporal_store((float)ll[j], t + j * 64);
-      }
       const double mn = fmax(mx, bm);
       const double ms = (mn == -INFINITY) ? 0.0 : mn;
       float acc = sm * fast_exp2((float)(mx - ms));
@@ -546,6 +558,11 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       for (int j = 0; j < 8; ++j) acc += fast_exp2((float)(ll[j] - ms));
       sm = acc;
       mx = mn;
+      // Sparse stored log-joint (fgmm_common.hpp): this wave's 16 components of each
+      // row (register groups 2H, 2H + 1), with their max in its half of the maxima.
+      if constexpr (LJ)
+        lj_put_rows_g<2>(lj + (tile * KB + kb) * kLjTile, ljmax + ((tile * KB + kb) * 2 + H) * 32, c, g,
+                         2 * H, ll, bm, acc, run_max, dense != 0);
       if (MB == 1) lds_barrier();
     };
     for (int kb = 0; kb < KB; kb += 2) {
@@ -569,25 +586,29 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const double ms = (m1 == -INFINITY) ? 0.0 : m1;
     sm = sm * fast_exp2((float)(mx - ms)) + so * fast_exp2((float)(mo - ms));
   }
-  double* px = reinterpret_cast<double*>(ex);                 // [kWaves][64] max, then sum
-  float* ps = reinterpret_cast<float*>(px + kWaves * 64);
+  double* px = reinterpret_cast<double*>(ex);                 // [2][kWaves][64] max, then sum
+  float* ps = reinterpret_cast<float*>(px + 2 * kWaves * 64);
   lds_barrier();   // every wave has read its last exchange slot
-  if (h == 1) {
-    px[rg * 64 + lane] = m1;
-    ps[rg * 64 + lane] = sm;
-  }
+  px[(h * kWaves + rg) * 64 + lane] = m1;
+  ps[(h * kWaves + rg) * 64 + lane] = sm;
   lds_barrier();
-  if (h == 0) {
-    const double mo = px[rg * 64 + lane];
-    const float so = ps[rg * 64 + lane];
-    const double mn = fmax(m1, mo);
-    const double ms = (mn == -INFINITY) ? 0.0 : mn;
-    const float tot = sm * fast_exp2((float)(m1 - ms)) + so * fast_exp2((float)(mo - ms));
-    const double lz2 = mn + (double)log2f(tot);
-    if (valid && g == 0) {
-      rowstat[row] = lz2;
-      if (logZ) logZ[row] = (float)(lz2 * kLn2);
-    }
+  // Both waves form logZ2 from the same two pairs (max and sum commute, so the
+  // result is the same bits in each).
+  const double mo = px[((1 - h) * kWaves + rg) * 64 + lane];
+  const float so = ps[((1 - h) * kWaves + rg) * 64 + lane];
+  const double mn = fmax(m1, mo);
+  const double ms = (mn == -INFINITY) ? 0.0 : mn;
+  const float tot = sm * fast_exp2((float)(m1 - ms)) + so * fast_exp2((float)(mo - ms));
+  const double lz2 = mn + (double)log2f(tot);
+  if (h == 0 && valid && g == 0) {
+    rowstat[row] = lz2;
+    if (logZ) logZ[row] = (float)(lz2 * kLn2);
+  }
+  // Each wave's need masks from its own maxima; pass 2 ORs the two words.
+  if constexpr (LJ) {
+    if (g == 0)
+      lj_put_masks(ljmax + tile * KB * 64 + h * 32, ljmask + tile * KB * 2 + h, ljcount + (tile & 63), KB, c,
+                   lz2, valid, dense != 0, 64, 2);
   }
 }
 
@@ -759,6 +780,435 @@ void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       }
     }
     if (g == 0) part_nk[kbase + c] = nk;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2 from the sparse stored log-joint (up to D = 128, D a multiple of 32), for
+// sparse need masks: as iso_accum_sparse (fgmm_iso.hip), one wave per (row slab, row
+// group, component block) fetching only the needed register-row pairs of each tile,
+// here accumulating r^T x and r^T x^2.  The same split and order as diag_accum_lj2,
+// so the two write the same partials; the needed-pair count of pass 1 picks one.
+// ---------------------------------------------------------------------------
+constexpr int kSparseSlots = 3;
+constexpr int kSparseDepth = 4;
+constexpr int kSparseBatch = 256;
+constexpr int kSparseWaves = 4;
+
+// Total of the 64 needed-pair counters (one wave, uniform result).
+__device__ __forceinline__ unsigned lj_pair_total(const unsigned* __restrict__ count) {
+  unsigned v = count[threadIdx.x & 63];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+template <int DP>
+__global__ __launch_bounds__(64 * kSparseWaves)
+void diag_accum_sparse(const float* __restrict__ X, int64_t ldx, int64_t N, const float* __restrict__ lj,
+                       const uint2* __restrict__ ljmask, const unsigned* __restrict__ ljcount,
+                       int64_t sparse_max, int KB, int KP, const double* __restrict__ rowstat, int nslab,
+                       int RG, int64_t rows_per_slab, float* __restrict__ part_mu,
+                       float* __restrict__ part_sq, float* __restrict__ part_nk, int dense) {
+  constexpr int NJ = DP / 32;
+  constexpr int S = kSparseSlots;
+  constexpr int PD = kSparseDepth;
+  constexpr int BT = kSparseBatch;
+  typedef float fNJ __attribute__((ext_vector_type(NJ)));
+  __shared__ uint2 work[kSparseWaves][BT];      // the tile's two mask words
+  __shared__ unsigned wtile[kSparseWaves][BT];  // and its index in the batch
+
+  if ((int64_t)lj_pair_total(ljcount) > sparse_max) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t w = (int64_t)blockIdx.x * kSparseWaves + wave;
+  if (w >= (int64_t)nslab * RG * KB) return;
+  const int kb = (int)(w % KB);
+  const int rg = (int)((w / KB) % RG);
+  const int slab = (int)(w / ((int64_t)KB * RG));
+  const int TR = 32 * RG;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
+
+  f32x16 accx[NJ], accq[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    accx[j] = zero16();
+    accq[j] = zero16();
+  }
+  float nk = 0.0f;
+
+  const int64_t row00 = r_begin + rg * 32;
+  const float* lj0 = lj + ((row00 >> 5) * KB + kb) * kLjTile;
+  const double* rs0 = rowstat + row00;
+  const float* x0 = X + row00 * ldx;
+  const int64_t lj_step = (int64_t)RG * KB * kLjTile, x_step = TR * ldx;
+  auto windows = [&](int t, buf_rsrc& lr, buf_rsrc& rr, buf_rsrc& xr) {
+    lr = make_rsrc(lj0 + t * lj_step, kLjTile * 4);
+    rr = make_rsrc(rs0 + (int64_t)t * TR, 32 * sizeof(double));
+    xr = make_rsrc(x0 + t * x_step, (uint32_t)(32 * ldx * 4));
+  };
+
+  float sl[PD][S];
+  double sz[PD][S];
+  fNJ sx[PD][S];
+  unsigned smk[PD];   // rows needed by either half of the block (uniform)
+  unsigned smh[PD];   // rows needed by this lane's half (components 16 (c >> 4) ..)
+  int stl[PD];
+
+  // Each half of a row's line is stored by its own pass-1 wave, which may leave it
+  // out (it is then negligible and its mask bit clear), so a lane reads its
+  // component's value (and the row's logZ2) under its half's mask word mh.  Its X
+  // columns feed every component of the block: they follow the row mask m.
+  auto load_pair = [&](const buf_rsrc& lr, const buf_rsrc& rr, const buf_rsrc& xr, unsigned m, unsigned mh,
+                       int ro, bool used, float& l, double& z, fNJ& x) {
+    const int row = ro + 4 * g;
+    const bool need = used && ((mh >> row) & 1u);
+    const bool row_need = used && ((m >> row) & 1u);
+    l = buf_load_f32<kBufNt>(lr, buf_off(need ? (row * 32 + c) * 4 : kBufOob));
+    z = buf_load_f64(rr, buf_off(need ? row * (int)sizeof(double) : kBufOob));
+    const int xo = buf_off(row_need ? (int)((row * ldx + NJ * c) * 4) : kBufOob);
+    if constexpr (NJ == 4) {
+      x = buf_load_f32x4(xr, xo);
+    } else if constexpr (NJ == 3) {
+      x = __builtin_bit_cast(fNJ, __builtin_amdgcn_raw_buffer_load_b96(xr, xo, 0, 0));
+    } else if constexpr (NJ == 2) {
+      x = __builtin_bit_cast(fNJ, __builtin_amdgcn_raw_buffer_load_b64(xr, xo, 0, 0));
+    } else {
+      x = __builtin_bit_cast(fNJ, __builtin_amdgcn_raw_buffer_load_b32(xr, xo, 0, 0));
+    }
+  };
+  // One pair's contribution, in the arithmetic of diag_accum_lj2.
+  auto accumulate = [&](unsigned mh, int ro, float l, double q, const fNJ& x) {
+    const bool need = (mh >> (ro + 4 * g)) & 1u;
+    const float zh = (float)q;
+    const float zl = (q > -INFINITY && q < INFINITY) ? (float)(q - (double)zh) : 0.0f;
+    const float rv = need ? fast_exp2((l - zh) - zl) : 0.0f;
+    nk += rv;
+    if (dense || __builtin_amdgcn_ballot_w64(rv != 0.0f) != 0) {
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj) {
+        accx[jj] = mfma32(rv, x[jj], accx[jj]);
+        accq[jj] = mfma32(rv, x[jj] * x[jj], accq[jj]);
+      }
+    }
+  };
+  auto issue = [&](int k, int cnt, int b0, int u) {
+    unsigned m = 0u, mh = 0u;
+    int t = 0;
+    if (k < cnt) {
+      const uint2 e = work[wave][k];
+      const unsigned mx = __builtin_amdgcn_readfirstlane(e.x), my = __builtin_amdgcn_readfirstlane(e.y);
+      m = mx | my;
+      mh = c < 16 ? mx : my;
+      t = b0 + __builtin_amdgcn_readfirstlane(wtile[wave][k]);
+    }
+    smk[u] = m;
+    smh[u] = mh;
+    stl[u] = t;
+    buf_rsrc lr, rr, xr;
+    windows(t, lr, rr, xr);
+    unsigned pm = lj_pair_mask(m);
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      const bool used = pm != 0u;
+      const int ro = used ? __builtin_ctz(pm) : 0;
+      pm &= pm - 1u;
+      load_pair(lr, rr, xr, m, mh, ro, used, sl[u][j], sz[u][j], sx[u][j]);
+    }
+  };
+  auto process = [&](int u) {
+    const unsigned m = smk[u], mh = smh[u];
+    if (m == 0u) return;
+    unsigned pm = lj_pair_mask(m);
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      if (pm == 0u) return;
+      const int ro = __builtin_ctz(pm);
+      pm &= pm - 1u;
+      accumulate(mh, ro, sl[u][j], sz[u][j], sx[u][j]);
+    }
+    if (pm == 0u) return;
+    buf_rsrc lr, rr, xr;   // more pairs than slots: load them now
+    windows(stl[u], lr, rr, xr);
+    while (pm != 0u) {
+      const int ro = __builtin_ctz(pm);
+      pm &= pm - 1u;
+      float l;
+      double q;
+      fNJ x;
+      load_pair(lr, rr, xr, m, mh, ro, true, l, q, x);
+      accumulate(mh, ro, l, q, x);
+    }
+  };
+
+  for (int b0 = 0; b0 < ntiles; b0 += BT) {
+    int cnt = 0;
+#pragma unroll
+    for (int q = 0; q < BT / 64; ++q) {
+      const int t = b0 + 64 * q + lane;
+      const int64_t row0 = r_begin + (int64_t)t * TR + rg * 32;
+      uint2 mm = make_uint2(0u, 0u);
+      if (t < ntiles && row0 < r_end) mm = ljmask[(row0 >> 5) * KB + kb];
+      const bool any = (mm.x | mm.y) != 0u;
+      const unsigned long long bal = __builtin_amdgcn_ballot_w64(any);
+      const int pos = cnt + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bal >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((unsigned)bal, 0u));
+      if (any) {
+        work[wave][pos] = mm;
+        wtile[wave][pos] = (unsigned)(64 * q + lane);
+      }
+      cnt += __builtin_popcountll(bal);
+    }
+#pragma unroll
+    for (int u = 0; u < PD; ++u) issue(u, cnt, b0, u);
+    for (int kk = 0; kk < cnt; kk += PD) {
+#pragma unroll
+      for (int u = 0; u < PD; ++u) {
+        process(u);
+        issue(kk + u + PD, cnt, b0, u);
+      }
+    }
+  }
+
+  nk += __shfl_xor(nk, 32);
+  const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t o = (kbase + acc_row(i, g)) * DP + NJ * c;
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+      part_mu[o + jj] = accx[jj][i];
+      part_sq[o + jj] = accq[jj][i];
+    }
+  }
+  if (g == 0) part_nk[kbase + c] = nk;
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2 from the sparse stored log-joint (up to D = 128), for dense need masks (and
+// every FGMM_FLAG_DENSE run): the structure of iso_accum_lj (fgmm_iso.hip).  X
+// super-tiles, with their rows' logZ2 and the masks of the next tile, are staged in
+// LDS for 8 component blocks through two register stages (loop unrolled by two);
+// each wave reads the needed log-joint rows of its block one tile ahead with
+// range-checked buffer loads and accumulates r^T x and r^T x^2 for the needed
+// register-row pairs, in ascending order (unrolled for tiles with 8 or more pairs).
+// ---------------------------------------------------------------------------
+template <int DP, int CB, int NH>
+constexpr size_t accum_lj2_lds_bytes() {
+  return (size_t)2 * 32 * (kAccWaves / (CB * NH)) * ((DP + 4) * sizeof(float) + sizeof(float2)) +
+         (size_t)2 * kAccWaves * sizeof(uint2);
+}
+
+template <int DP, int CB, int NH>
+__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
+void diag_accum_lj2(const float* __restrict__ X, int64_t ldx, int64_t N, int D, const float* __restrict__ lj,
+                    const uint2* __restrict__ ljmask, const unsigned* __restrict__ ljcount,
+                    int64_t sparse_max, int KB, int KP, const double* __restrict__ rowstat, int nslab,
+                    int64_t rows_per_slab, float* __restrict__ part_mu, float* __restrict__ part_sq,
+                    float* __restrict__ part_nk, int dense) {
+  constexpr int NJ = DP / 32 / NH;               // 32-column tiles per wave (each for x and x^2)
+  constexpr int RS = DP + 4;
+  constexpr int V4 = DP / 4;
+  constexpr int RG = kAccWaves / (CB * NH);      // row groups (32 rows each)
+  constexpr int TR = 32 * RG;                    // rows per super-tile
+  constexpr int NV = TR * V4;                    // float4 per super-tile
+  constexpr int LPT = (NV + kAccThreads - 1) / kAccThreads;
+  constexpr int NB = 2;                          // register stages
+  static_assert(kAccWaves % (CB * NH) == 0 && (DP / 32) % NH == 0, "even split");
+  static_assert(TR + kAccWaves <= kAccThreads, "row-state and mask threads");
+
+  // diag_accum_sparse takes the call when pass 1 found the masks sparse.
+  if (sparse_max >= 0 && (int64_t)lj_pair_total(ljcount) <= sparse_max) return;
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  float* xs = reinterpret_cast<float*>(lds_raw);                                  // [2][TR*RS]
+  float2* rz = reinterpret_cast<float2*>(lds_raw + 2 * TR * RS * sizeof(float));  // [2][TR]
+  uint2* mk = reinterpret_cast<uint2*>(rz + 2 * TR);                              // [2][kAccWaves]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int cbw = wave % CB, h = (wave / CB) % NH, rg = wave / (CB * NH);
+  const int slab = blockIdx.x % nslab;
+  const int cg = blockIdx.x / nslab;
+  const int kb = cg * CB + cbw;
+  const bool active = kb < KB;
+  const int col0 = h * (DP / NH);
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
+
+  f32x16 accx[NJ], accq[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    accx[j] = zero16();
+    accq[j] = zero16();
+  }
+  float nk = 0.0f;
+
+  // Need masks of (row tile, block): one word per half of the block's components,
+  // each from the pass-1 wave that stored that half of the rows' lines (and may
+  // have left it out; it is then negligible and its bit clear).  A register-row
+  // pair is visited when either half needs a row; a lane reads its value only
+  // under its own half's word.
+  const buf_rsrc mask_r = make_rsrc(ljmask, (uint32_t)(cdiv(N, 32) * KB * sizeof(uint2)));
+  auto mask_off = [&](int t, int rgw, int kbw) -> int {
+    const int64_t row0 = r_begin + (int64_t)t * TR + rgw * 32;
+    return (t < ntiles && row0 < r_end && kbw < KB) ? (int)(((row0 >> 5) * KB + kbw) * sizeof(uint2)) : kBufOob;
+  };
+  auto mask_load = [&](int off) -> uint2 {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(mask_r, buf_off(off), 0, 0);
+    return make_uint2(v[0], v[1]);
+  };
+
+  const bool ragged = (D & 3) != 0;
+  auto fetch = [&](int t, f32x4 (&st)[LPT], double& rqv, uint2& mqv) {
+    const int64_t row0 = r_begin + (int64_t)t * TR;
+    int nrow = 0;
+    if (t < ntiles) nrow = (int)(r_end - row0 < TR ? r_end - row0 : TR);
+    const buf_rsrc xr = make_rsrc(nrow ? X + row0 * ldx : X, (uint32_t)(nrow * ldx * 4));
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      const int r = idx / V4, col = (idx % V4) * 4;
+      const bool ok = (NV % kAccThreads == 0 || idx < NV) && r < nrow && col < D;
+      st[q] = buf_load_f32x4(xr, buf_off(ok ? (int)((r * ldx + col) * 4) : kBufOob));
+    }
+    const buf_rsrc rr = make_rsrc(nrow ? rowstat + row0 : rowstat, (uint32_t)(nrow * sizeof(double)));
+    const double q2 = buf_load_f64(rr, buf_off(tid < nrow ? tid * (int)sizeof(double) : kBufOob));
+    rqv = tid < nrow ? q2 : INFINITY;   // rows past the slab: logZ2 = +inf, hence r = 0
+    const int w = tid - TR;
+    mqv = mask_load((w >= 0 && w < kAccWaves) ? mask_off(t + NB - 1, w / (CB * NH), cg * CB + w % CB)
+                                              : kBufOob);
+  };
+  auto commit = [&](int buf, const f32x4 (&st)[LPT], double rqv, uint2 mqv) {
+    float* dst = xs + buf * TR * RS;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * kAccThreads + tid;
+      if (NV % kAccThreads == 0 || idx < NV) {
+        const int col = (idx % V4) * 4;
+        f32x4 v = st[q];
+        if (ragged) {
+          if (col + 1 >= D) v.y = 0.0f;
+          if (col + 2 >= D) v.z = 0.0f;
+          if (col + 3 >= D) v.w = 0.0f;
+        }
+        *reinterpret_cast<f32x4*>(dst + (idx / V4) * RS + col) = v;
+      }
+    }
+    if (tid < TR) {
+      const float hi = (float)rqv;
+      const float lo = (rqv > -INFINITY && rqv < INFINITY) ? (float)(rqv - (double)hi) : 0.0f;
+      rz[buf * TR + tid] = make_float2(hi, lo);
+    }
+    if (tid >= TR && tid < TR + kAccWaves) mk[buf * kAccWaves + tid - TR] = mqv;
+  };
+  auto lj_fetch = [&](int t, uint2 m, f32x16& v) {
+    const int64_t row0 = r_begin + (int64_t)t * TR + rg * 32;
+    const bool any = (m.x | m.y) != 0u;
+    const unsigned mh = c < 16 ? m.x : m.y;
+    const buf_rsrc lr = make_rsrc(any ? lj + ((row0 >> 5) * KB + kb) * kLjTile : lj, any ? kLjTile * 4 : 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = 8 * (i >> 2) + (i & 3) + 4 * g;
+      v[i] = buf_load_f32<kBufNt>(lr, buf_off(((mh >> row) & 1u) ? (row * 32 + c) * 4 : kBufOob));
+    }
+  };
+  auto uniform = [](uint2 m) {
+    return make_uint2(__builtin_amdgcn_readfirstlane(m.x), __builtin_amdgcn_readfirstlane(m.y));
+  };
+
+  f32x4 stg[NB][LPT];
+  double rqs[NB];
+  uint2 mqs[NB];
+  f32x16 ljb[NB];
+  uint2 mcur = make_uint2(0u, 0u);   // need masks of the current tile
+
+  // One register-row pair: r for the needed lanes, then the steps of r^T x and r^T x^2.
+  auto pair = [&](unsigned mg, int ro, float l, float2 z, const float* xb) {
+    const float rv = ((mg >> ro) & 1u) ? fast_exp2((l - z.x) - z.y) : 0.0f;
+    if (NH == 1 || h == 0) nk += rv;
+    if (dense || __builtin_amdgcn_ballot_w64(rv != 0.0f) != 0) {
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj) {
+        const float xv = xb[ro * RS + 32 * jj];
+        accx[jj] = mfma32(rv, xv, accx[jj]);
+        accq[jj] = mfma32(rv, xv * xv, accq[jj]);
+      }
+    }
+  };
+
+  auto step = [&](int t, auto par) {
+    constexpr int P = decltype(par)::value;
+    const int lb = t & 1;
+    const uint2 ma = uniform(mk[lb * kAccWaves + wave]);   // tile t + 1
+    lj_fetch(t + 1, ma, ljb[1 - P]);
+    fetch(t + 2, stg[P], rqs[P], mqs[P]);
+    const unsigned mc = mcur.x | mcur.y;
+    const float* xt = xs + lb * TR * RS + rg * 32 * RS;
+    const float2* rt = rz + lb * TR + rg * 32 + 4 * g;
+    if (active && mc != 0u) {
+      const float* xbase = xt + 4 * g * RS + col0 + c;
+      unsigned pm = lj_pair_mask(mc);
+      const unsigned mg = (c < 16 ? mcur.x : mcur.y) >> (4 * g);
+      // Unrolled for dense tiles where the accumulators leave registers for it.
+      if (NJ <= 2 && __builtin_popcount(pm) >= 8) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int ro = 8 * q + j;
+            if ((pm >> ro) & 1u) pair(mg, ro, ljb[P][4 * q + j], rt[ro], xbase);
+          }
+        }
+      } else {
+        while (pm != 0u) {
+          const int ro = __builtin_ctz(pm);
+          pm &= pm - 1u;
+          pair(mg, ro, ljb[P][4 * (ro >> 3) + (ro & 3)], rt[ro], xbase);
+        }
+      }
+    }
+    if (t + 1 < ntiles) commit(lb ^ 1, stg[1 - P], rqs[1 - P], mqs[1 - P]);
+    lds_barrier();
+    mcur = ma;
+  };
+
+  if (ntiles > 0) {
+    fetch(0, stg[0], rqs[0], mqs[0]);
+    fetch(1, stg[1], rqs[1], mqs[1]);
+    mcur = uniform(mask_load(mask_off(0, rg, kb)));
+    lj_fetch(0, mcur, ljb[0]);
+    commit(0, stg[0], rqs[0], mqs[0]);
+    lds_barrier();
+  }
+  for (int t = 0; t < ntiles; t += 2) {
+    step(t, std::integral_constant<int, 0>{});
+    if (t + 1 >= ntiles) break;
+    step(t + 1, std::integral_constant<int, 1>{});
+  }
+
+  if (active) {
+    nk += __shfl_xor(nk, 32);
+    const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t o = (kbase + acc_row(i, g)) * DP + col0 + 32 * j + c;
+        part_mu[o] = accx[j][i];
+        part_sq[o] = accq[j][i];
+      }
+    }
+    if (g == 0 && h == 0) part_nk[kbase + c] = nk;
   }
 }
 
@@ -1190,6 +1640,9 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
   const double* kc_lin = reinterpret_cast<const double*>(ws + pl.off_kclin);
   double* rowstat = reinterpret_cast<double*>(ws + pl.off_rowstat);
   float* lj = pl.lj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
+  float* ljmax = pl.lj_sparse ? reinterpret_cast<float*>(ws + pl.off_ljmax) : nullptr;
+  uint2* ljmask = pl.lj_sparse ? reinterpret_cast<uint2*>(ws + pl.off_ljmask) : nullptr;
+  unsigned* ljcount = pl.lj_sparse ? reinterpret_cast<unsigned*>(ws + pl.off_ljcount) : nullptr;
   float* pmu = reinterpret_cast<float*>(ws + pl.off_part_mu);
   float* psq = reinterpret_cast<float*>(ws + pl.off_part_sq);
   float* pnk = reinterpret_cast<float*>(ws + pl.off_part_nk);
@@ -1207,7 +1660,8 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
       auto kern = pl.lj ? &diag_lse_x6<DP, true> : &diag_lse_x6<DP, false>;
       hipLaunchKernelGGL(kern, dim3(nblk1), dim3(kAccThreads), lds1, stream, X, ldx, pl.N, (int)pl.D,
                          reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
-                         reinterpret_cast<const double*>(ws + pl.off_kcx6), pl.KB, logZ, rowstat, lj);
+                         reinterpret_cast<const double*>(ws + pl.off_kcx6), pl.KB, logZ, rowstat, lj,
+                         ljmax, reinterpret_cast<unsigned*>(ljmask), ljcount, dense ? 1 : 0);
     } else {
       // Above D = 128 the rows' dimensions are split over two waves.
       constexpr size_t lds1 = lse_split_lds_bytes<DP>();
@@ -1225,6 +1679,45 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
   }
   if (!run2) return hipGetLastError();
   const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
+  if constexpr (diag_uses_x6(DP)) {
+    if (pl.lj_sparse) {
+      // Sparse masks (on average at most 2 needed register-row pairs per tile and
+      // block) go to diag_accum_sparse where D is a multiple of 32; both kernels are
+      // launched and each returns unless the count selects it.
+      int64_t sparse_max = -1;
+      if (pl.D == DP) {
+        sparse_max = 2 * cdiv(pl.N, 32) * pl.KB;
+        const int64_t nw = (int64_t)pl.nslab * pl.rgroups * pl.KB;
+        hipLaunchKernelGGL((diag_accum_sparse<DP>), dim3((unsigned)cdiv(nw, kSparseWaves)),
+                           dim3(64 * kSparseWaves), 0, stream, X, ldx, pl.N, lj, ljmask, ljcount,
+                           sparse_max, pl.KB, pl.KP, rowstat, pl.nslab, pl.rgroups, pl.rows_per_slab,
+                           pmu, psq, pnk, dense ? 1 : 0);
+      }
+      auto launch2 = [&](auto cb_tag, auto nh_tag) -> hipError_t {
+        constexpr int CB = decltype(cb_tag)::value;
+        constexpr int NH = decltype(nh_tag)::value;
+        constexpr size_t lds = accum_lj2_lds_bytes<DP, CB, NH>();
+        static_assert(lds <= kMaxLds, "pass-2 tiles exceed LDS");
+        if (lds > 65536) {
+          hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum_lj2<DP, CB, NH>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+          if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL((diag_accum_lj2<DP, CB, NH>), grid2, dim3(kAccThreads), lds, stream, X, ldx,
+                           pl.N, (int)pl.D, lj, ljmask, ljcount, sparse_max, pl.KB, pl.KP, rowstat,
+                           pl.nslab, pl.rows_per_slab, pmu, psq, pnk, dense ? 1 : 0);
+        return hipGetLastError();
+      };
+      using J1 = std::integral_constant<int, 1>;
+      using J4 = std::integral_constant<int, 4>;
+      using J8 = std::integral_constant<int, 8>;
+      if constexpr (DP == 128) {
+        return pl.cpg == 8 ? launch2(J8{}, J1{}) : launch2(J4{}, std::integral_constant<int, 2>{});
+      } else {
+        return pl.cpg == 8 ? launch2(J8{}, J1{}) : launch2(J4{}, J1{});
+      }
+    }
+  }
   if (pl.lj) {
     auto launch = [&](auto cb_tag, auto nh_tag) -> hipError_t {
       constexpr int CB = decltype(cb_tag)::value;
@@ -1824,7 +2317,8 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     if (diag_uses_x6(pl.DP))
       hipLaunchKernelGGL(diag_x6_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
                          (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_mu3),
-                         reinterpret_cast<double*>(ws + pl.off_kcx6));
+                         reinterpret_cast<double*>(ws + pl.off_kcx6),
+                         pl.lj_sparse ? reinterpret_cast<unsigned*>(ws + pl.off_ljcount) : nullptr);
   }
   if (N > 0) {
     auto run = [&](auto dp_tag) -> hipError_t {

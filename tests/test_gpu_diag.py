@@ -104,6 +104,25 @@ def test_stored_and_recomputed_log_joint(N, K, D, gpu_device):
     assert_close_stats(recomputed, ref, f"recomputed N={N} K={K} D={D}")
 
 
+# Shapes of the sparse stored log-joint (D <= 128): sparse masks (D = 64 .. 128), the
+# dense-mask kernel at D = 32, and a width that is not a multiple of 32 (dense-mask
+# kernel only).  Each half block of a row is stored by its own pass-1 wave, so a row
+# may hold one stored and one left-out half.
+SPARSE_SHAPES = [(20000, 1024, 64), (20000, 512, 96), (40000, 512, 128), (30001, 1024, 96),
+                 (20000, 600, 32), (20000, 512, 90)]
+
+
+@pytest.mark.parametrize("N,K,D", SPARSE_SHAPES)
+def test_sparse_accumulation_is_bitwise_dense(N, K, D, gpu_device):
+    """Default accumulation from the sparse log-joint against FGMM_FLAG_DENSE and the oracle."""
+    inp = data.diag_clustered(N, K, D, seed=N % 97 + D)
+    a = _into(inp, gpu_device)
+    b = _into(inp, gpu_device, dense=True)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+    assert_close_stats(a, oracle(inp), f"sparse N={N} K={K} D={D}")
+
+
 @pytest.mark.parametrize("recompute", [False, True])
 def test_phase_split_equals_one_call(recompute, gpu_device):
     """PHASE1 then PHASE2 on one workspace gives the single call's outputs bitwise."""
