@@ -81,7 +81,7 @@ def cpu_baseline(inp, kind, K, D, min_s=10.0, max_s=30.0, rows=16384):
 # profiles/<kind>_estep_<shape>.md.  Not reported with --recompute.
 TRAFFIC_BYTES = {
     "iso_n1m_k1024_d128": {"phase1": 3_140_715_520, "phase2": 799_602_688},
-    "diag_n1m_k1024_d96": {"phase1": 4_499_631_140, "phase2": 4_542_595_401},
+    "diag_n1m_k1024_d96": {"phase1": 4_374_549_504, "phase2": 656_783_360},
     "full_n250k_k256_d64": {"phase1": 589_263_972, "phase2": 414_389_462},
 }
 
@@ -118,11 +118,13 @@ def algorithmic_bytes(kind, N, K, D, lj):
     Phase 2 reads X, the per-row state and the log-joint.  O(K*D) operands and the
     slab partials are left out (under 1% here).
 
-    The isotropic log-joint is sparse: phase 1 writes it whole at most (rows the
-    running max already rules out are left unwritten) with a per-row block maximum
-    and a need mask per tile, and phase 2 reads X, the row state and the masks, plus
-    only the log-joint rows whose need bit is set, a data-dependent share that is
-    not counted here (the measured traffic includes it).
+    The isotropic log-joint, and the diagonal one up to D = 128, are sparse: phase 1
+    writes it whole at most (rows the running max already rules out are left
+    unwritten) with per-row block maxima and need masks per tile (iso: one maximum
+    per row and one mask word; diag: one per half block, 64 maxima and two words),
+    and phase 2 reads X, the row state and the masks, plus only the log-joint rows
+    whose need bit is set, a data-dependent share that is not counted here (the
+    measured traffic includes it).
     """
     KB = -(-K // 32)
     if kind == "full":
@@ -132,9 +134,11 @@ def algorithmic_bytes(kind, N, K, D, lj):
     lj_bytes = lj_bytes if lj else 0
     row = 16 if kind == "iso" else 8
     x = 4.0 * N * D
-    if kind == "iso" and lj:
-        masks = lj_bytes / 4096 * (128 + 4)
-        return x + 4.0 * N + row * N + lj_bytes + masks, x + row * N + lj_bytes / 4096 * 4
+    if lj and (kind == "iso" or (kind == "diag" and D <= 128)):
+        per_tile = (128, 4) if kind == "iso" else (256, 8)   # maxima, mask words
+        tiles = lj_bytes / 4096
+        return (x + 4.0 * N + row * N + lj_bytes + tiles * sum(per_tile),
+                x + row * N + tiles * per_tile[1])
     return x + 4.0 * N + row * N + lj_bytes, x + row * N + lj_bytes
 
 
@@ -354,6 +358,9 @@ def main():
         "_lj" if stored_lj and kind != "full" else "")
     if kind == "iso" and stored_lj and D % 32 == 0 and D <= 128:
         p2_kernel = "iso_accum_sparse or iso_accum_lj, picked on device by mask density"
+    if kind == "diag" and stored_lj and D <= 128:
+        p2_kernel = ("diag_accum_sparse or diag_accum_lj2, picked on device by mask density"
+                     if D % 32 == 0 else "diag_accum_lj2")
     names = (f"{kind}_lse (log-normaliser pass + prologue"
              + (", stores the log-joint)" if stored_lj else ")"),
              f"{p2_kernel} (accumulation pass + slab reduction"

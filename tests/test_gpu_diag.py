@@ -84,7 +84,7 @@ def _into(inp, dev, **kw):
 
 # Shapes on the stored log-joint path (K > 96), with partial tiles and slabs, every
 # padded width and both column splits of pass 2 (8 or 4 blocks per workgroup).
-LJ_SHAPES = [(33, 128, 20), (65, 257, 96), (1000, 130, 64), (777, 300, 61), (4097, 129, 100),
+LJ_SHAPES = [(33, 128, 40), (65, 257, 96), (1000, 130, 64), (777, 300, 61), (4097, 129, 100),
              (2500, 260, 192), (1800, 300, 250), (9001, 512, 128), (3000, 150, 128), (700, 200, 256)]
 
 
@@ -104,12 +104,12 @@ def test_stored_and_recomputed_log_joint(N, K, D, gpu_device):
     assert_close_stats(recomputed, ref, f"recomputed N={N} K={K} D={D}")
 
 
-# Shapes of the sparse stored log-joint (D <= 128): sparse masks (D = 64 .. 128), the
-# dense-mask kernel at D = 32, and a width that is not a multiple of 32 (dense-mask
-# kernel only).  Each half block of a row is stored by its own pass-1 wave, so a row
-# may hold one stored and one left-out half.
+# Shapes of the sparse stored log-joint (32 < D <= 128): sparse masks (D = 64 .. 128)
+# and widths that are not a multiple of 32 (mask-driven dense kernel only).  Each
+# half block of a row is stored by its own pass-1 wave, so a row may hold one
+# stored and one left-out half.
 SPARSE_SHAPES = [(20000, 1024, 64), (20000, 512, 96), (40000, 512, 128), (30001, 1024, 96),
-                 (20000, 600, 32), (20000, 512, 90)]
+                 (20000, 300, 40), (20000, 512, 90)]
 
 
 @pytest.mark.parametrize("N,K,D", SPARSE_SHAPES)
