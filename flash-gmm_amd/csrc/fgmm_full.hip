@@ -55,8 +55,12 @@ struct FullPlan {
   int64_t rows_per_slab;
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
   bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16); always stores the log-joint
-  size_t off_lsw, off_bsw, off_ck, off_rowstat, off_part_sig, off_part_mu, off_part_nk, off_lj, total;
+  size_t off_lsw, off_bsw, off_ck, off_l3, off_esw, off_rowstat, off_part_sig, off_part_mu, off_part_nk,
+      off_lj, total;
 };
+
+// Pass 1 runs on the bf16 matrix cores (centred split-bf16 whitening) up to D = 64.
+__host__ __device__ constexpr bool full_pass1_x6(int DP) { return DP <= 64; }
 
 // Stored log-joint of the full model: per (32-row tile, component) 32 floats, rows
 // contiguous, [tile][KP][32]; one tile per pass-1 wave (the grid's tiles, rounded
@@ -107,6 +111,12 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool b
   p.off_lsw = off;      off = align256(off + (size_t)p.KP * p.DP * p.DP * sizeof(float));
   p.off_bsw = off;      off = align256(off + (size_t)p.KP * p.DP * sizeof(double));
   p.off_ck = off;       off = align256(off + (size_t)p.KP * sizeof(double));
+  // Split-bf16 operands of pass 1: 4 bf16x8 per (16 dimensions, 32 coordinates, lane).
+  const bool x6 = !bf16 && full_pass1_x6(p.DP);
+  p.off_l3 = off;
+  if (x6) off = align256(off + (size_t)p.KP * (p.DP / 32) * (p.DP / 16) * 4 * 64 * sizeof(bf16x8));
+  p.off_esw = off;
+  if (x6) off = align256(off + (size_t)p.KP * p.DP * sizeof(double));
   p.off_rowstat = off;  off = align256(off + (size_t)(N > 0 ? N : 0) * sizeof(double));
   p.off_part_sig = off;
   off = align256(off + (size_t)p.npart * p.KP * (bf16 ? p.NMB * p.NMB : p.NSB) * 1024 * sizeof(float));
@@ -255,6 +265,179 @@ void full_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const double maha = maha_one<NMB, NM>(l_l + buf * BLK, b_l + buf * BW, lane, g,
                                           [&](int m) { return xb[m]; });
     const double ll = b_l[buf * BW + DP] - hl * maha;
+    if constexpr (LJ) ljt[k * 32] = (float)ll;
+    const double mn = fmax(mx, ll);
+    const double ms = (mn == -INFINITY) ? 0.0 : mn;
+    sm = sm * fast_exp2((float)(mx - ms)) + fast_exp2((float)(ll - ms));
+    mx = mn;
+    if (more) commit(buf ^ 1);
+    lds_barrier();
+  }
+  const double lz2 = mx + (double)log2f(sm);
+  if (valid && g == 0) {
+    rowstat[row] = lz2;
+    if (logZ) logZ[row] = (float)(lz2 * kLn2);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 1 on the bf16 matrix cores up to D = 64: the whitening in the centred
+// split-bf16 form of the isotropic pass 1 (x6c_tile, fgmm_common.hpp).  V^T =
+// L_k^T X^T over chunks of 16 dimensions; the A operand is L_k^T split exactly into
+// three bf16 plus, in a fourth slot, the chunk's centring offsets
+// -o_qj = -fp32(sum over d in chunk q of L_k,dj mu_k,d) against a ones operand, so
+// each chunk adds L_k[q]^T (x - mu_k)[q] - a small number for the rows near the
+// component - to the fp32 accumulator.  The offsets come back in fp64:
+// v_j = t_j + e_j with e_j = sum_q o_qj - b_j.  Six of the nine split products are
+// kept (the dropped ones are below 2^-24 of the largest), so v carries the error of
+// an fp32 contraction of the centred row, not of L^T x against b.
+//
+//   l3[k][mb][q][s][lane] (bf16x8): s < 3: split s of L_k[16q + 8g + e][32 mb + c];
+//                                   s = 3: splits of -o_q,32mb+c in elements 0..2 (g = 0)
+//   esw[k][mb][g][i]     (f64):    e_j, j = 32 mb + acc_row(i, g)
+// ---------------------------------------------------------------------------
+template <int DP>
+constexpr int full_x6_block() { return (DP / 32) * (DP / 16) * 4 * 64; }   // bf16x8 per component
+
+__global__ __launch_bounds__(64) void full_x6_prep(const float* __restrict__ mu, int64_t ldmu,
+                                                   const float* __restrict__ L, int64_t K, int D, int DP,
+                                                   bf16x8* __restrict__ l3, double* __restrict__ esw) {
+  __shared__ float so[4][64];   // o_qj, DP <= 64
+  __shared__ double se[64];     // e_j
+  const int64_t k = blockIdx.x;
+  const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  const bool valid = k < K;
+  const float* Lk = L + k * (int64_t)D * D;
+  const int NQ = DP / 16, NMB = DP / 32;
+  if (lane < DP) {
+    const int j = lane;
+    double b = 0.0, osum = 0.0;
+    for (int q = 0; q < NQ; ++q) {
+      double o = 0.0;
+      if (valid && j < D)
+        for (int d = 16 * q; d < 16 * q + 16 && d < D; ++d)
+          o = fma((double)Lk[(int64_t)d * D + j], (double)mu[k * ldmu + d], o);
+      const float of = (float)o;
+      so[q][j] = of;
+      osum += (double)of;
+      b += o;
+    }
+    se[j] = osum - b;
+  }
+  __syncthreads();
+  for (int mb = 0; mb < NMB; ++mb) {
+    const int j = 32 * mb + c;
+    for (int q = 0; q < NQ; ++q) {
+      f32x4 lo = zero4(), hi = zero4();
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d0 = 16 * q + 8 * g + e, d1 = d0 + 4;
+        lo[e] = (valid && d0 < D && j < D) ? Lk[(int64_t)d0 * D + j] : 0.0f;
+        hi[e] = (valid && d1 < D && j < D) ? Lk[(int64_t)d1 * D + j] : 0.0f;
+      }
+      bf16x8 sp[3];
+      split3_bf16(lo, hi, sp);
+      bf16x8* dst = l3 + (((k * NMB + mb) * NQ + q) * 4) * 64 + lane;
+#pragma unroll
+      for (int t = 0; t < 3; ++t) dst[t * 64] = sp[t];
+      // Offset slot: -o_qj in k slots 0..2 (lane-half 0), against x6c_ones.
+      const float mo = -so[q][j];
+      const f32x4 olo = {g == 0 ? mo : 0.0f, 0.0f, 0.0f, 0.0f};
+      bf16x8 os[3];
+      split3_bf16(olo, zero4(), os);
+      bf16x8 ov;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ov[e] = (__bf16)0.0f;
+      ov[0] = os[0][0];
+      ov[1] = os[1][0];
+      ov[2] = os[2][0];
+      dst[3 * 64] = ov;
+    }
+    if (lane < 32) {
+      const int gg = lane >> 4, i = lane & 15;
+      esw[(k * NMB + mb) * 32 + gg * 16 + i] = se[32 * mb + acc_row(i, gg)];
+    }
+  }
+}
+
+template <int DP>
+constexpr size_t full_x6_lds_bytes() {
+  return (size_t)2 * full_x6_block<DP>() * sizeof(bf16x8) + (size_t)2 * (DP + 8) * sizeof(double);
+}
+
+template <int DP, bool LJ>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
+void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, const bf16x8* __restrict__ l3,
+                 const double* __restrict__ esw, const double* __restrict__ ck, int K, int KP,
+                 float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj) {
+  constexpr int NMB = DP / 32, NQ = DP / 16;
+  constexpr int BLK = full_x6_block<DP>();
+  constexpr int LPT = BLK / kThreads;
+  constexpr int BW = DP + 8;                      // doubles per component stage (e + c)
+  static_assert(BLK % kThreads == 0, "even split");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  bf16x8* l_l = reinterpret_cast<bf16x8*>(lds_raw);                                // [2][BLK]
+  double* e_l = reinterpret_cast<double*>(lds_raw + 2 * BLK * sizeof(bf16x8));     // [2][BW]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t tile = (int64_t)blockIdx.x * kWaves + wave;   // 32-row tile
+  const int64_t row = tile * 32 + c;
+  const bool valid = row < N;
+  // Both half-waves hold row c's log-joint; both store it (same value, same address).
+  float* ljt = LJ ? lj + tile * KP * 32 + c : nullptr;
+
+  bf16x8 st[LPT];
+  double est = 0.0;
+  auto fetch = [&](int k) {
+    const bf16x8* src = l3 + (int64_t)k * BLK;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) st[q] = src[q * kThreads + tid];
+    if (tid < DP) est = esw[(int64_t)k * DP + tid];
+    else if (tid == DP) est = ck[k];
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) l_l[buf * BLK + q * kThreads + tid] = st[q];
+    if (tid <= DP) e_l[buf * BW + tid] = est;
+  };
+  fetch(0);
+  // This lane's row, dimensions 16q + 8g .. +7, split three ways.
+  bf16x8 xb[NQ][3];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int d0 = 16 * q + 8 * g;
+    split3_bf16(load_row4(X, ldx, row, d0, D, valid), load_row4(X, ldx, row, d0 + 4, D, valid), xb[q]);
+  }
+  const bf16x8 ones = x6c_ones(lane);
+  commit(0);
+  __syncthreads();
+
+  const double hl = 0.5 * kLog2e;
+  double mx = -INFINITY;
+  float sm = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    const int buf = k & 1;
+    const bool more = k + 1 < K;
+    if (more) fetch(k + 1);
+    const bf16x8* lc = l_l + buf * BLK + lane;
+    const double* ec = e_l + buf * BW;
+    double maha = 0.0;
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+      // lane = row, register i = whitened coordinate 32 mb + acc_row(i, g)
+      const f32x16 t = x6c_tile<NQ>([&](int q, int s) { return lc[((mb * NQ + q) * 4 + s) * 64]; }, xb, ones);
+      const double* eb = ec + mb * 32 + g * 16;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const double v = (double)t[i] + eb[i];
+        maha = fma(v, v, maha);
+      }
+    }
+    maha += __shfl_xor(maha, 32);
+    const double ll = ec[DP] - hl * maha;
     if constexpr (LJ) ljt[k * 32] = (float)ll;
     const double mn = fmax(mx, ll);
     const double ms = (mn == -INFINITY) ? 0.0 : mn;
@@ -721,7 +904,21 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
     return bytes > 65536 ? hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes)
                          : hipSuccess;
   };
-  if (run1) {
+  if constexpr (full_pass1_x6(DP)) {
+    if (run1) {
+      constexpr size_t lds1 = full_x6_lds_bytes<DP>();
+      for (const void* f : {reinterpret_cast<const void*>(&full_lse_x6<DP, false>),
+                            reinterpret_cast<const void*>(&full_lse_x6<DP, true>)}) {
+        hipError_t e = set_lds(f, lds1);
+        if (e != hipSuccess) return e;
+      }
+      auto kern = pl.lj ? &full_lse_x6<DP, true> : &full_lse_x6<DP, false>;
+      hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1, stream, X,
+                         ldx, pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
+                         reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, logZ,
+                         rowstat, lj);
+    }
+  } else if (run1) {
     constexpr size_t lds1 = lse_lds_bytes<DP>();
     for (const void* f : {reinterpret_cast<const void*>(&full_lse<DP, false>),
                           reinterpret_cast<const void*>(&full_lse<DP, true>)}) {
@@ -1249,6 +1446,10 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
                        (int)D, pl.DP, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_lsw),
                        reinterpret_cast<double*>(ws + pl.off_bsw),
                        reinterpret_cast<double*>(ws + pl.off_ck));
+  if (run1 && !bf16 && full_pass1_x6(pl.DP))
+    hipLaunchKernelGGL(full_x6_prep, dim3((unsigned)pl.KP), dim3(64), 0, stream, mu, ldmu, prec_chol, K,
+                       (int)D, pl.DP, reinterpret_cast<bf16x8*>(ws + pl.off_l3),
+                       reinterpret_cast<double*>(ws + pl.off_esw));
   if (N > 0) {
     auto run = [&](auto dp_tag) -> hipError_t {
       constexpr int DP = decltype(dp_tag)::value;
