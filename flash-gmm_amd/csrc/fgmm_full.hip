@@ -8,11 +8,15 @@
 //   r_nk  = 2^(ll2_nk - logZ2_n)
 //   Nk_k = sum_n r_nk;  mu_acc_k = sum_n r_nk x_n;  sig_outer_k = sum_n r_nk x_n x_n^T
 //
-// The whitening V^T = L_k^T X^T is a 32x32x2 fp32 MFMA contraction (A = L_k^T laid
-// out in operand order by the prologue, B = X), evaluated with the chunked fp64
-// form of cross_tile() so maha keeps ~1e-5 accuracy; each lane owns one row and 16
-// whitened coordinates per 32-row block of V^T, so maha is an in-lane fp64 sum plus
-// one cross-half exchange.
+// Pass 1 (full_lse_x6) whitens on the bf16 matrix cores in a centred split-bf16
+// form: V^T = L_k^T X^T - b_k with each 16-dimension chunk contributing
+// L_k[q]^T (x - mu_k)[q] to an fp32 accumulator, the offsets returned in fp64; each
+// lane owns one row and 16 whitened coordinates per 32-row block of V^T, so maha is
+// an in-lane fp64 sum plus one cross-half exchange.  With FGMM_FLAG_RECOMPUTE both
+// passes (full_lse, then the recomputing pass 2) whiten with 32x32x2 fp32 MFMA steps
+// in the chunked fp64 form of cross_tile() (A = L_k^T laid out in operand order by
+// full_prep, B = X), so that logZ and the recomputed responsibilities come from the
+// same log-joint.
 //
 // Pass 2 runs 8 waves per workgroup (4 components x 2 row groups).  After r is
 // formed for a 32-row tile it is exchanged through LDS, and sig_outer accumulates as
@@ -59,8 +63,7 @@ struct FullPlan {
       off_lj, total;
 };
 
-// Pass 1 runs on the bf16 matrix cores (centred split-bf16 whitening) up to D = 64.
-__host__ __device__ constexpr bool full_pass1_x6(int DP) { return DP <= 64; }
+
 
 // Stored log-joint of the full model: per (32-row tile, component) 32 floats, rows
 // contiguous, [tile][KP][32]; one tile per pass-1 wave (the grid's tiles, rounded
@@ -112,7 +115,7 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool b
   p.off_bsw = off;      off = align256(off + (size_t)p.KP * p.DP * sizeof(double));
   p.off_ck = off;       off = align256(off + (size_t)p.KP * sizeof(double));
   // Split-bf16 operands of pass 1: 4 bf16x8 per (16 dimensions, 32 coordinates, lane).
-  const bool x6 = !bf16 && full_pass1_x6(p.DP);
+  const bool x6 = !bf16 && p.lj;
   p.off_l3 = off;
   if (x6) off = align256(off + (size_t)p.KP * (p.DP / 32) * (p.DP / 16) * 4 * 64 * sizeof(bf16x8));
   p.off_esw = off;
@@ -202,7 +205,9 @@ __device__ __forceinline__ double maha_one(const f32x4* Lc, const double* bc, in
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1: online log-sum-exp over components, one component's L^T per LDS stage.
+// Pass 1 with FGMM_FLAG_RECOMPUTE: online log-sum-exp over components, one
+// component's L^T per LDS stage, whitening in the fp32 form the recomputing pass 2
+// uses, so that logZ and the recomputed responsibilities come from one log-joint.
 // ---------------------------------------------------------------------------
 template <int DP>
 constexpr size_t lse_lds_bytes() {
@@ -281,7 +286,7 @@ void full_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1 on the bf16 matrix cores up to D = 64: the whitening in the centred
+// Pass 1 on the bf16 matrix cores: the whitening in the centred
 // split-bf16 form of the isotropic pass 1 (x6c_tile, fgmm_common.hpp).  V^T =
 // L_k^T X^T over chunks of 16 dimensions; the A operand is L_k^T split exactly into
 // three bf16 plus, in a fourth slot, the chunk's centring offsets
@@ -296,21 +301,18 @@ void full_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 //                                   s = 3: splits of -o_q,32mb+c in elements 0..2 (g = 0)
 //   esw[k][mb][g][i]     (f64):    e_j, j = 32 mb + acc_row(i, g)
 // ---------------------------------------------------------------------------
-template <int DP>
-constexpr int full_x6_block() { return (DP / 32) * (DP / 16) * 4 * 64; }   // bf16x8 per component
 
 __global__ __launch_bounds__(64) void full_x6_prep(const float* __restrict__ mu, int64_t ldmu,
                                                    const float* __restrict__ L, int64_t K, int D, int DP,
                                                    bf16x8* __restrict__ l3, double* __restrict__ esw) {
-  __shared__ float so[4][64];   // o_qj, DP <= 64
-  __shared__ double se[64];     // e_j
+  __shared__ float so[8][128];  // o_qj, DP <= 128
+  __shared__ double se[128];    // e_j
   const int64_t k = blockIdx.x;
   const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
   const bool valid = k < K;
   const float* Lk = L + k * (int64_t)D * D;
   const int NQ = DP / 16, NMB = DP / 32;
-  if (lane < DP) {
-    const int j = lane;
+  for (int j = lane; j < DP; j += 64) {
     double b = 0.0, osum = 0.0;
     for (int q = 0; q < NQ; ++q) {
       double o = 0.0;
@@ -360,9 +362,15 @@ __global__ __launch_bounds__(64) void full_x6_prep(const float* __restrict__ mu,
   }
 }
 
+// One LDS stage holds SMB 32-coordinate blocks of one component: all of them up to
+// D = 64, one above (a whole component's operands, 72 or 128 KiB, would not fit twice).
+template <int DP>
+constexpr int full_x6_smb() { return DP <= 64 ? DP / 32 : 1; }
+template <int DP>
+constexpr int full_x6_stage() { return full_x6_smb<DP>() * (DP / 16) * 4 * 64; }   // bf16x8
 template <int DP>
 constexpr size_t full_x6_lds_bytes() {
-  return (size_t)2 * full_x6_block<DP>() * sizeof(bf16x8) + (size_t)2 * (DP + 8) * sizeof(double);
+  return (size_t)2 * full_x6_stage<DP>() * sizeof(bf16x8) + (size_t)2 * (32 * full_x6_smb<DP>() + 8) * sizeof(double);
 }
 
 template <int DP, bool LJ>
@@ -371,10 +379,13 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
                  const double* __restrict__ esw, const double* __restrict__ ck, int K, int KP,
                  float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj) {
   constexpr int NMB = DP / 32, NQ = DP / 16;
-  constexpr int BLK = full_x6_block<DP>();
+  constexpr int SMB = full_x6_smb<DP>();          // coordinate blocks per stage
+  constexpr int NST = NMB / SMB;                  // stages per component
+  constexpr int BLK = full_x6_stage<DP>();        // bf16x8 per stage
   constexpr int LPT = BLK / kThreads;
-  constexpr int BW = DP + 8;                      // doubles per component stage (e + c)
-  static_assert(BLK % kThreads == 0, "even split");
+  constexpr int NE = 32 * SMB;                    // e values per stage
+  constexpr int BW = NE + 8;                      // doubles per stage (e, then c)
+  static_assert(BLK % kThreads == 0 && kThreads > NE, "even split");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   bf16x8* l_l = reinterpret_cast<bf16x8*>(lds_raw);                                // [2][BLK]
@@ -389,19 +400,21 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
   // Both half-waves hold row c's log-joint; both store it (same value, same address).
   float* ljt = LJ ? lj + tile * KP * 32 + c : nullptr;
 
+  // Stage s = k NST + sub holds blocks SMB sub .. of component k: contiguous in
+  // l3 and esw.
   bf16x8 st[LPT];
   double est = 0.0;
-  auto fetch = [&](int k) {
-    const bf16x8* src = l3 + (int64_t)k * BLK;
+  auto fetch = [&](int64_t s) {
+    const bf16x8* src = l3 + s * BLK;
 #pragma unroll
     for (int q = 0; q < LPT; ++q) st[q] = src[q * kThreads + tid];
-    if (tid < DP) est = esw[(int64_t)k * DP + tid];
-    else if (tid == DP) est = ck[k];
+    if (tid < NE) est = esw[s * NE + tid];
+    else if (tid == NE) est = ck[s / NST];
   };
   auto commit = [&](int buf) {
 #pragma unroll
     for (int q = 0; q < LPT; ++q) l_l[buf * BLK + q * kThreads + tid] = st[q];
-    if (tid <= DP) e_l[buf * BW + tid] = est;
+    if (tid <= NE) e_l[buf * BW + tid] = est;
   };
   fetch(0);
   // This lane's row, dimensions 16q + 8g .. +7, split three ways.
@@ -418,17 +431,20 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
   const double hl = 0.5 * kLog2e;
   double mx = -INFINITY;
   float sm = 0.0f;
-  for (int k = 0; k < K; ++k) {
-    const int buf = k & 1;
-    const bool more = k + 1 < K;
-    if (more) fetch(k + 1);
+  const int64_t nstage = (int64_t)K * NST;
+  double maha = 0.0;
+  for (int64_t s = 0; s < nstage; ++s) {
+    const int buf = (int)(s & 1);
+    const bool more = s + 1 < nstage;
+    if (more) fetch(s + 1);
     const bf16x8* lc = l_l + buf * BLK + lane;
     const double* ec = e_l + buf * BW;
-    double maha = 0.0;
 #pragma unroll
-    for (int mb = 0; mb < NMB; ++mb) {
-      // lane = row, register i = whitened coordinate 32 mb + acc_row(i, g)
-      const f32x16 t = x6c_tile<NQ>([&](int q, int s) { return lc[((mb * NQ + q) * 4 + s) * 64]; }, xb, ones);
+    for (int mb = 0; mb < SMB; ++mb) {
+      // lane = row, register i = whitened coordinate 32 mb + acc_row(i, g).  One
+      // accumulation chain: no chain sums, and 3.12 ms against 3.56 ms with four at
+      // N=250K, K=256, D=64.
+      const f32x16 t = x6c_tile<NQ, 1>([&](int q, int u) { return lc[((mb * NQ + q) * 4 + u) * 64]; }, xb, ones);
       const double* eb = ec + mb * 32 + g * 16;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -436,13 +452,16 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
         maha = fma(v, v, maha);
       }
     }
-    maha += __shfl_xor(maha, 32);
-    const double ll = ec[DP] - hl * maha;
-    if constexpr (LJ) ljt[k * 32] = (float)ll;
-    const double mn = fmax(mx, ll);
-    const double ms = (mn == -INFINITY) ? 0.0 : mn;
-    sm = sm * fast_exp2((float)(mx - ms)) + fast_exp2((float)(ll - ms));
-    mx = mn;
+    if (NST == 1 || (int)(s % NST) == NST - 1) {   // component s / NST complete
+      maha += __shfl_xor(maha, 32);
+      const double ll = ec[NE] - hl * maha;
+      if constexpr (LJ) ljt[(s / NST) * 32] = (float)ll;
+      const double mn = fmax(mx, ll);
+      const double ms = (mn == -INFINITY) ? 0.0 : mn;
+      sm = sm * fast_exp2((float)(mx - ms)) + fast_exp2((float)(ll - ms));
+      mx = mn;
+      maha = 0.0;
+    }
     if (more) commit(buf ^ 1);
     lds_barrier();
   }
@@ -904,30 +923,24 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
     return bytes > 65536 ? hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes)
                          : hipSuccess;
   };
-  if constexpr (full_pass1_x6(DP)) {
-    if (run1) {
-      constexpr size_t lds1 = full_x6_lds_bytes<DP>();
-      for (const void* f : {reinterpret_cast<const void*>(&full_lse_x6<DP, false>),
-                            reinterpret_cast<const void*>(&full_lse_x6<DP, true>)}) {
-        hipError_t e = set_lds(f, lds1);
-        if (e != hipSuccess) return e;
-      }
-      auto kern = pl.lj ? &full_lse_x6<DP, true> : &full_lse_x6<DP, false>;
-      hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1, stream, X,
-                         ldx, pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
-                         reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, logZ,
-                         rowstat, lj);
-    }
-  } else if (run1) {
+  if (run1 && !pl.lj) {
     constexpr size_t lds1 = lse_lds_bytes<DP>();
-    for (const void* f : {reinterpret_cast<const void*>(&full_lse<DP, false>),
-                          reinterpret_cast<const void*>(&full_lse<DP, true>)}) {
+    hipError_t e = set_lds(reinterpret_cast<const void*>(&full_lse<DP, false>), lds1);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((full_lse<DP, false>), dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
+                       stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, logZ, rowstat, lj);
+  } else if (run1) {
+    constexpr size_t lds1 = full_x6_lds_bytes<DP>();
+    for (const void* f : {reinterpret_cast<const void*>(&full_lse_x6<DP, false>),
+                          reinterpret_cast<const void*>(&full_lse_x6<DP, true>)}) {
       hipError_t e = set_lds(f, lds1);
       if (e != hipSuccess) return e;
     }
-    auto kern = pl.lj ? &full_lse<DP, true> : &full_lse<DP, false>;
-    hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1, stream, X,
-                       ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, logZ, rowstat, lj);
+    auto kern = pl.lj ? &full_lse_x6<DP, true> : &full_lse_x6<DP, false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1, stream, X, ldx,
+                       pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
+                       reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, logZ,
+                       rowstat, lj);
   }
   if (!run2) return hipGetLastError();
   float* psig = reinterpret_cast<float*>(ws + pl.off_part_sig);
@@ -1446,7 +1459,7 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
                        (int)D, pl.DP, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_lsw),
                        reinterpret_cast<double*>(ws + pl.off_bsw),
                        reinterpret_cast<double*>(ws + pl.off_ck));
-  if (run1 && !bf16 && full_pass1_x6(pl.DP))
+  if (run1 && !bf16 && pl.lj)
     hipLaunchKernelGGL(full_x6_prep, dim3((unsigned)pl.KP), dim3(64), 0, stream, mu, ldmu, prec_chol, K,
                        (int)D, pl.DP, reinterpret_cast<bf16x8*>(ws + pl.off_l3),
                        reinterpret_cast<double*>(ws + pl.off_esw));
