@@ -82,7 +82,7 @@ def cpu_baseline(inp, kind, K, D, min_s=10.0, max_s=30.0, rows=16384):
 TRAFFIC_BYTES = {
     "iso_n1m_k1024_d128": {"phase1": 3_140_715_520, "phase2": 799_602_688},
     "diag_n1m_k1024_d96": {"phase1": 4_374_549_504, "phase2": 656_783_360},
-    "full_n250k_k256_d64": {"phase1": 589_263_972, "phase2": 414_389_462},
+    "full_n250k_k256_d64": {"phase1": 836_218_880, "phase2": 414_390_272},
 }
 
 WORKLOADS = {
@@ -361,7 +361,10 @@ def main():
     if kind == "diag" and stored_lj and D <= 128:
         p2_kernel = ("diag_accum_sparse or diag_accum_lj2, picked on device by mask density"
                      if D % 32 == 0 else "diag_accum_lj2")
-    names = (f"{kind}_lse (log-normaliser pass + prologue"
+    split_p1 = (kind in ("iso", "diag") and D <= 128) or (kind == "full" and stored_lj)
+    p1_kernel = f"{kind}_lse" + ("_x6" if split_p1 and kind != "iso" else "")
+    names = (f"{p1_kernel} (log-normaliser pass + prologue"
+             + (", split-bf16 products" if split_p1 else "")
              + (", stores the log-joint)" if stored_lj else ")"),
              f"{p2_kernel} (accumulation pass + slab reduction"
              + (", reads the stored log-joint)" if stored_lj else ", recomputes the log-joint)"))
@@ -392,11 +395,22 @@ def main():
     roof.update({"kernel": dom["kernel"], "traffic": dom["traffic"],
                  "traffic_unit": "bytes per launch (HBM read + write, rocprofv3 counters)",
                  "avg_launch_ms": dom["ms"]})
-    if kind == "iso" and not bf16 and D <= 128 and dom_phase == "phase1":
-        # Phase 1 forms the fp32 cross term from split-bf16 products on the bf16 matrix
-        # cores: 7 steps of 16 dimensions (6 products + 1 centring offset) per 32x32 tile,
-        # 14 D bf16 flop per (row, component) against the 2 D algorithmic fp32 flop.
-        ex = 14.0 * N * K * (D + (-D) % 16)
+    # Phase 1 forms its fp32 contraction from split-bf16 products on the bf16 matrix
+    # cores: 7 steps (6 products + 1 centring offset) per chunk and 32x32 tile, each
+    # step 32 bf16 flop per (row, output).  Per (row, component):
+    #   iso:  16-dimension chunks, 1 output:          14 D bf16 flop (2 D algorithmic)
+    #   diag: 8-dimension chunks of [x^2, x]:         28 D               (4 D)
+    #   full: 16-dimension chunks, D outputs:         14 D^2             (2 D^2)
+    # (D padded: iso to 16, diag and full to 32.)  Full recomputation keeps fp32 steps.
+    ex = None
+    if not bf16 and dom_phase == "phase1":
+        if kind == "iso" and D <= 128:
+            ex = 14.0 * N * K * (D + (-D) % 16)
+        elif kind == "diag" and D <= 128:
+            ex = 28.0 * N * K * (D + (-D) % 32)
+        elif kind == "full" and stored_lj:
+            ex = 14.0 * N * K * (D + (-D) % 32) ** 2
+    if ex is not None:
         roof["executed"] = {"arithmetic": "split-bf16 (bf16x6) products, fp32 accumulation, fp64 "
                                           "combination; fp32 inputs and outputs",
                             "bf16_flop_per_launch": ex,
