@@ -610,9 +610,9 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const double* rt = rs + buf * TR + rg * 32;
     const float l = PF ? lnext : lj_of(t);
     if (PF && more) lnext = lj_of(t + 1);
+    float rv = 0.0f;
     if (active) {
       // r for this lane's row c (both half-waves hold it).
-      float rv;
       if constexpr (LJ) {
         rv = fast_exp2((float)((double)l - rt[c]));
       } else {
@@ -628,14 +628,18 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     if (more) fetch(t + 1);
     __builtin_amdgcn_wave_barrier();
     if (active) {
-      // sig_outer[d1][d2] += sum_rows (r x_d1) x_d2 over the tile's 32 rows; row of step s
-      // for half g is acc_row(s, g), matching the A-operand k index of each half-wave.
-#pragma unroll
-      for (int s = 0; s < 16; ++s) {
-        const int row = acc_row(s, g);
+      // sig_outer[d1][d2] += sum_rows (r x_d1) x_d2 over the tile's 32 rows.  Step s
+      // takes rows r0 + 4g (r0 = 8 (s >> 2) + (s & 3)) for half g, matching the
+      // A-operand k index of each half-wave; a step whose two rows have zero
+      // responsibility adds nothing, so the loop visits the steps with a nonzero row
+      // (bit r0 of the pair mask), in ascending order.
+      const unsigned nz = (unsigned)__builtin_amdgcn_ballot_w64(rv != 0.0f);   // lanes 0..31: rows
+      unsigned pm = dense ? 0x0f0f0f0fu : lj_pair_mask(nz);
+      while (pm != 0u) {
+        const int r0 = __builtin_ctz(pm);
+        pm &= pm - 1u;
+        const int row = r0 + 4 * g;
         const float rr = rx[row];
-        // A step whose two rows have zero responsibility adds nothing.
-        if (!dense && __builtin_amdgcn_ballot_w64(rr != 0.0f) == 0) continue;
         float xv[NMB], av[NMB];
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb) {
