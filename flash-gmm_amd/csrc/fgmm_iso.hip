@@ -207,17 +207,19 @@ __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int
   if (g == 0) {
     double C = -INFINITY, b = 0.0, musq = 0.0, osum = 0.0;
     if (valid) {
-      for (int d = 0; d < D; ++d) {
-        double v = (double)mu[comp * ldmu + d];
-        musq = fma(v, v, musq);
-      }
-      // The centring offsets of the bf16x6 pass 1: o_q = fp32(||mu chunk q||^2).
+      // ||mu||^2 as the sum of the chunks' squared norms, and the centring offsets
+      // of the bf16x6 pass 1, o_q = fp32(||mu chunk q||^2).  Each chunk's 16 loads
+      // are unrolled so they are in flight together (this kernel runs K / 32 blocks
+      // and is latency bound).
       for (int q = 0; q < NQ; ++q) {
         double o = 0.0;
-        for (int d = 16 * q; d < 16 * q + 16 && d < D; ++d) {
-          const double v = (double)mu[comp * ldmu + d];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int d = 16 * q + e;
+          const double v = d < D ? (double)mu[comp * ldmu + d] : 0.0;
           o = fma(v, v, o);
         }
+        musq += o;
         osum += (double)(float)o;
       }
       const double l = (double)lss[comp];
@@ -264,8 +266,10 @@ __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int
     f32x4 olo = zero4();
     if (valid && g == 0) {
       double o = 0.0;
-      for (int d = 16 * q; d < 16 * q + 16 && d < D; ++d) {
-        const double v = (double)mu[comp * ldmu + d];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int d = 16 * q + e;
+        const double v = d < D ? (double)mu[comp * ldmu + d] : 0.0;
         o = fma(v, v, o);
       }
       olo.x = -(float)o;
