@@ -197,6 +197,10 @@ def test_diag_full_size_properties(gpu_device):
     torch.testing.assert_close(mu_acc.double().sum(0), inp["X"].double().sum(0), rtol=0,
                                atol=1e-5 * float(mu_acc.abs().sum(0).max()))
     assert torch.all(sig >= -1e-3)
+    # The sparse accumulation this data takes writes what the dense one writes.
+    dense = _into(inp, dev, dense=True)
+    for u, v in zip((logZ, Nk, mu_acc, sig), dense):
+        assert torch.equal(u, v)
     rows = torch.randint(0, N, (2048,), generator=torch.Generator().manual_seed(1))
     sub = {k: v.cpu() for k, v in inp.items()}
     ref = O.estep_diag(sub["X"][rows], sub["mu"], sub["log_sigma_sq"], sub["log_pi"])[0]

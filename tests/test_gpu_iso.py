@@ -289,6 +289,10 @@ def test_headline_shape_full_size_against_oracle(gpu_device):
     xs = inp["X"].double().sum(0)
     torch.testing.assert_close(mu_acc.double().sum(0), xs, rtol=0, atol=1e-5 * float(mu_acc.abs().sum(0).max()))
     assert torch.all(sig >= 0)
+    # The sparse accumulation this data takes writes what the dense one writes.
+    dense = _into(inp, dev, dense=True)
+    for u, v in zip(got, dense):
+        assert torch.equal(u, v)
     print("full-size oracle (float64, CPU)", flush=True)
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     ref = O.estep_iso(*[inp[k].cpu() for k in ("X", "mu", "log_sigma_sq", "log_pi")])
