@@ -2293,7 +2293,10 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   if (D > 256) return FGMM_ERR_UNSUPPORTED;
   if (N > kMaxRows || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
   const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
-  const DiagPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE), bf16);
+  // The stored-log-joint pass 2 addresses X tiles with 32-bit buffer offsets (row
+  // stride at most kMaxBufLdx floats); wider strides recompute, which needs less
+  // workspace.
+  const DiagPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE) && ldx <= kMaxBufLdx, bf16);
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;
   unsigned char* ws = static_cast<unsigned char*>(workspace);

@@ -207,6 +207,17 @@ def test_diag_full_size_properties(gpu_device):
     assert (logZ.cpu()[rows].double() - ref).abs().max().item() <= LOGZ_ATOL
 
 
+def test_wide_row_stride(gpu_device):
+    """A row stride of X above 2^20 floats, past the stored path's 32-bit buffer offsets:
+    the call recomputes instead, with results to the same bar."""
+    inp = data.diag_clustered(200, 128, 64, seed=21)
+    big = torch.zeros(200, (1 << 20) + 64, device=gpu_device)
+    big[:, :64] = inp["X"].to(gpu_device)
+    got = flash_gmm_estep_diag(big[:, :64], *[inp[k].to(gpu_device) for k in ("mu", "log_sigma_sq", "log_pi")])
+    torch.cuda.synchronize()
+    assert_close_stats(got, oracle(inp), "diag wide row stride")
+
+
 def test_rejects_bad_variance_shape(gpu_device):
     inp = data.diag_clustered(10, 4, 8, seed=14)
     X, mu, lss, lpi = (inp[k].to(gpu_device) for k in ("X", "mu", "log_sigma_sq", "log_pi"))

@@ -300,6 +300,17 @@ def test_headline_shape_full_size_against_oracle(gpu_device):
     assert_close_stats(got, ref, "K1024 D128 N=1M")
 
 
+def test_wide_row_stride(gpu_device):
+    """A row stride of X above 2^20 floats, past the stored path's 32-bit buffer offsets:
+    the call recomputes instead, with results to the same bar."""
+    inp = data.iso_clustered(200, 128, 64, seed=21)
+    big = torch.zeros(200, (1 << 20) + 64, device=gpu_device)
+    big[:, :64] = inp["X"].to(gpu_device)
+    got = flash_gmm_estep(big[:, :64], *[inp[k].to(gpu_device) for k in ("mu", "log_sigma_sq", "log_pi")])
+    torch.cuda.synchronize()
+    assert_close_stats(got, oracle(inp), "iso wide row stride")
+
+
 def test_rejects_bad_shapes(gpu_device):
     inp = data.iso_plain(10, 4, 8, seed=11)
     X, mu, lss, lpi = (inp[k].to(gpu_device) for k in ("X", "mu", "log_sigma_sq", "log_pi"))
