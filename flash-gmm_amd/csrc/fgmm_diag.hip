@@ -179,6 +179,7 @@ __global__ __launch_bounds__(64) void diag_prep(const float* __restrict__ mu, in
     double C = -INFINITY;
     if (valid) {
       double lsum = 0.0, q = 0.0;
+#pragma unroll 8
       for (int d = 0; d < D; ++d) {
         const double l = (double)lss[comp * ldlss + d];
         const double m = (double)mu[comp * ldmu + d];
@@ -397,6 +398,7 @@ __global__ __launch_bounds__(64) void diag_x6_prep(const float* __restrict__ mu,
     f32x4 fw = zero4(), fv = zero4();
     double o = 0.0;
     if (valid) {
+#pragma unroll 8
       for (int d = 8 * q; d < 8 * q + 8 && d < D; ++d) {
         const double m = (double)mu[comp * ldmu + d];
         const double w = 0.5 * exp(-(double)lss[comp * ldlss + d]) * kLog2e;
@@ -433,6 +435,7 @@ __global__ __launch_bounds__(64) void diag_x6_prep(const float* __restrict__ mu,
     double C = -INFINITY;
     if (valid) {
       double lsum = 0.0, qs = 0.0;
+#pragma unroll 8
       for (int d = 0; d < D; ++d) {
         const double l = (double)lss[comp * ldlss + d];
         const double m = (double)mu[comp * ldmu + d];
@@ -1855,6 +1858,7 @@ __global__ __launch_bounds__(64) void diag_bf16_prep(const float* __restrict__ m
     double C = -INFINITY;
     if (valid) {
       double lsum = 0.0, qs = 0.0;
+#pragma unroll 8
       for (int d = 0; d < D; ++d) {
         const double l = (double)lss[k * ldlss + d];
         const double m = (double)mu[k * ldmu + d];

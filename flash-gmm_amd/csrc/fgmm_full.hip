@@ -150,6 +150,7 @@ __global__ __launch_bounds__(64) void full_prep(const float* __restrict__ mu, in
   for (int j = lane; j < DP; j += 64) {
     double b = 0.0;
     if (valid && j < D)
+#pragma unroll 8
       for (int i = 0; i < D; ++i) b = fma((double)Lk[(int64_t)i * D + j], (double)mu[k * ldmu + i], b);
     sb[j] = b;
   }
@@ -157,6 +158,7 @@ __global__ __launch_bounds__(64) void full_prep(const float* __restrict__ mu, in
     double c0 = -INFINITY;
     if (valid) {
       double ld = 0.0;
+#pragma unroll 8
       for (int d = 0; d < D; ++d) ld += log(fabs((double)Lk[(int64_t)d * D + d]) + 1e-30);
       c0 = ((double)lpi[k] + ld - 0.5 * (double)D * kLog2Pi) * kLog2e;
     }
@@ -317,6 +319,7 @@ __global__ __launch_bounds__(64) void full_x6_prep(const float* __restrict__ mu,
     for (int q = 0; q < NQ; ++q) {
       double o = 0.0;
       if (valid && j < D)
+#pragma unroll 8
         for (int d = 16 * q; d < 16 * q + 16 && d < D; ++d)
           o = fma((double)Lk[(int64_t)d * D + j], (double)mu[k * ldmu + d], o);
       const float of = (float)o;
@@ -1005,6 +1008,7 @@ __global__ __launch_bounds__(64) void full_bf16_prep(const float* __restrict__ m
   for (int j = lane; j < DP; j += 64) {
     double b = 0.0;
     if (valid && j < D)
+#pragma unroll 8
       for (int i = 0; i < D; ++i) b = fma((double)Lk[(int64_t)i * D + j], (double)mu[k * ldmu + i], b);
     sb[j] = b;
   }
@@ -1012,6 +1016,7 @@ __global__ __launch_bounds__(64) void full_bf16_prep(const float* __restrict__ m
     double c0 = -INFINITY;
     if (valid) {
       double ld = 0.0;
+#pragma unroll 8
       for (int d = 0; d < D; ++d) ld += log(fabs((double)Lk[(int64_t)d * D + d]) + 1e-30);
       c0 = ((double)lpi[k] + ld - 0.5 * (double)D * kLog2Pi) * kLog2e;
     }
