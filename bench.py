@@ -234,9 +234,9 @@ def main():
     ap.add_argument("--precision", choices=["fp32", "bf16"], default="fp32",
                     help="bf16 runs the H100 variants' bf16 operand contract (FGMM_FLAG_BF16) "
                          "and is rated against the bf16 matrix peak")
-    ap.add_argument("--recompute", action="store_true",
-                    help="pass 2 recomputes the log-joint (FGMM_FLAG_RECOMPUTE) instead of reading "
-                         "the copy pass 1 stores")
+    ap.add_argument("--store-log-joint", action="store_true",
+                    help="pass 1 stores the N x K log-joint and pass 2 reads it "
+                         "(FGMM_FLAG_STORE_LOGJOINT; O(N*K) workspace) instead of the default plan")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB five times (scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -280,27 +280,27 @@ def main():
         sig = torch.empty(K, device=dev)
         fn = lambda ph, dense=args.dense: iso_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
                                                          phase=ph, atomic_reduce=args.atomic_reduce,
-                                                         dense=dense, recompute=args.recompute,
+                                                         dense=dense, store_log_joint=args.store_log_joint,
                                                          precision=args.precision)
     elif kind == "diag":
         args4 = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
         sig = torch.empty(K, D, device=dev)
         fn = lambda ph, dense=args.dense: diag_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
-                                                          phase=ph, dense=dense, recompute=args.recompute,
+                                                          phase=ph, dense=dense, store_log_joint=args.store_log_joint,
                                                           precision=args.precision)
     else:
         args4 = (inp["X"], inp["mu"], inp["prec_chol"], inp["log_pi"])
         sig = torch.empty(K, D, D, device=dev)
         fn = lambda ph, dense=args.dense: full_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
-                                                          phase=ph, dense=dense, recompute=args.recompute,
+                                                          phase=ph, dense=dense, store_log_joint=args.store_log_joint,
                                                           precision=args.precision)
     ws_fn = getattr(L, f"fgmm_{kind}_workspace_bytes_ex")
     pflag = _lib.FLAG_BF16 if bf16 else 0
-    flags = (_lib.FLAG_RECOMPUTE if args.recompute else 0) | pflag
+    flags = (_lib.FLAG_STORE_LOGJOINT if args.store_log_joint else 0) | pflag
     ws = torch.empty(int(ws_fn(N, K, D, flags)), dtype=torch.uint8, device=dev)
     # Pass 2 reads the log-joint that pass 1 stores whenever the plan sizes it in.
-    stored_lj = (int(ws_fn(N, K, D, pflag)) != int(ws_fn(N, K, D, pflag | _lib.FLAG_RECOMPUTE))
-                 and not args.recompute)
+    stored_lj = (int(ws_fn(N, K, D, pflag)) != int(ws_fn(N, K, D, pflag | _lib.FLAG_STORE_LOGJOINT))
+                 and args.store_log_joint)
     stream = torch.cuda.current_stream(dev)
 
     def step(ev=None):
@@ -373,7 +373,7 @@ def main():
                  + (", stores the log-joint)" if kind == "full" else ")"),
                  f"{kind}_bf16_accum (accumulation pass + slab reduction, "
                  + ("reads the stored log-joint)" if kind == "full" else "recomputes in bf16)"))
-    traffic_tab = {} if (args.recompute or bf16) else TRAFFIC_BYTES.get(args.workload, {})
+    traffic_tab = {} if (not args.store_log_joint or bf16) else TRAFFIC_BYTES.get(args.workload, {})
     phases = {}
     for ph, name, t, f, b in (("phase1", names[0], p1, f1, b1), ("phase2", names[1], p2, f2, b2)):
         phases[ph] = {"kernel": name, "ms": t, "algorithmic_flop": f,

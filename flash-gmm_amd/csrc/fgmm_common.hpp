@@ -277,6 +277,87 @@ __device__ __forceinline__ f32x16 x6c_tile(LA loadA, const bf16x8 (&xb)[NQ][3], 
   return t;
 }
 
+// x6c_tile with the operand roles exchanged: A holds the rows' splits (lane m = row,
+// xa[q][s] = split s of dimensions 16q + 8(lane/32) + e) and the ones operand of the
+// offset step, B holds mu's splits and centring offsets (loadB(q, t), lane n =
+// component).  The accumulator then holds C[row][component]: lane = component,
+// register i = row acc_row(i, lane / 32), the layout whose rows feed r^T X.  The
+// products, their order and the chains are x6c_tile's, and a matrix step's per-half
+// sums do not depend on which operand is A, so every element equals the one
+// x6c_tile forms for the same row and component.
+template <int NQ, int MAXCH = 4, typename LB>
+__device__ __forceinline__ f32x16 x6c_tile_rows(const bf16x8 (&xa)[NQ][3], const bf16x8 ones, LB loadB) {
+  constexpr int NCH = NQ < MAXCH ? NQ : MAXCH;
+  f32x16 acc[NCH];
+#pragma unroll
+  for (int h = 0; h < NCH; ++h) acc[h] = zero16();
+#pragma unroll
+  for (int q0 = 0; q0 < NQ; q0 += NCH) {
+    bf16x8 b[NCH][4];
+#pragma unroll
+    for (int h = 0; h < NCH; ++h) {
+      if (q0 + h < NQ) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) b[h][t] = loadB(q0 + h, t);
+      }
+    }
+#pragma unroll
+    for (int step = 0; step < 7; ++step) {
+#pragma unroll
+      for (int h = 0; h < NCH; ++h) {
+        const int q = q0 + h;
+        if (q < NQ) {
+          const bf16x8 B = step == 0 ? b[h][1] : step == 1 ? b[h][2] : step <= 3 ? b[h][0]
+                         : step == 4 ? b[h][1] : step == 5 ? b[h][3] : b[h][0];
+          const bf16x8 A = step == 0 ? xa[q][1] : step == 1 ? xa[q][0] : step == 2 ? xa[q][2]
+                         : step == 3 ? xa[q][1] : step == 4 ? xa[q][0] : step == 5 ? ones : xa[q][0];
+          acc[h] = mfma_bf16(A, B, acc[h]);
+        }
+      }
+    }
+  }
+  f32x16 t = acc[0];
+#pragma unroll
+  for (int h = 1; h < NCH; ++h) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t[i] += acc[h][i];
+  }
+  return t;
+}
+
+// B operand of a 16-row matrix step read from a row-major bf16 tile in LDS (row
+// stride rs elements): lane l receives rows r0 + 8(l/32) + e, e = 0..7, of column
+// c0 + l % 32.  ds_read_b64_tr_b16 (gfx950), measured: within each group of 16
+// lanes, lane 4e + a supplies the address of 4 consecutive elements of one row,
+// and lane 4a' + b' receives element b' of the rows supplied by lanes a', 4 + a',
+// 8 + a' and 12 + a'.  Two reads (rows 8g .. 8g + 3, then 8g + 4 .. 8g + 7) give
+// the operand.  A row stride of an odd multiple of 32 bytes keeps the 8 rows a
+// read touches at most two to a bank.
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+__device__ __forceinline__ bf16x8 lds_rows_operand(const __bf16* tile, int rs, int r0, int c0, int lane) {
+  const int G = lane >> 4, i = lane & 15;
+  const int row = r0 + 8 * (G >> 1) + (i >> 2);
+  const int col = c0 + 16 * (G & 1) + 4 * (i & 3);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(tile + row * rs + col));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(tile + (row + 4) * rs + col));
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// bf16 bit patterns rounded toward +infinity (a value never decreases), for
+// upper bounds kept in half the space: truncation for negative values, round-up
+// of the magnitude for positive ones; NaN stays NaN.
+__device__ __forceinline__ unsigned short bf16_bits_up(float x) {
+  const unsigned u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)0x7fc0u;
+  if (u & 0x80000000u) return (unsigned short)(u >> 16);
+  return (unsigned short)((u + 0xffffu) >> 16);
+}
+__device__ __forceinline__ float bf16_bits_to_float(unsigned short h) { return __uint_as_float((unsigned)h << 16); }
+
 // The B operand of the offset step: 1 in k slots 0..2 (lane-half 0, elements 0..2).
 __device__ __forceinline__ bf16x8 x6c_ones(int lane) {
   bf16x8 v;
@@ -466,6 +547,39 @@ __device__ __forceinline__ void lj_put_masks(const float* __restrict__ bmax, uns
 }
 
 // ---------------------------------------------------------------------------
+// Need masks without a stored log-joint (the default, O(N + K*D) plan).  Pass 1
+// keeps each row's block maximum R as a bf16 upper bound (bf16_bits_up) in LDS, one
+// per (wave, block, row), and after the row's logZ2 is final sets bit r of the
+// (tile, block) word unless fl(fl(R - z.hi) - z.lo) < -kLjNeedGap, the test above.
+// R bounds every log-joint value the accumulation pass recomputes for the row and
+// block (the same arithmetic), so a clear bit again means responsibilities that are
+// exactly zero in fp32.  `rmax(kb)` returns the lane's bound for block kb.  Run by
+// the half-wave g = 0 (lane c = row c); the count gathers the register-row pairs
+// with a bit set, as lj_put_masks does.
+template <typename RM>
+__device__ __forceinline__ void need_put_masks(RM rmax, unsigned* __restrict__ mask, unsigned* __restrict__ count,
+                                               int KB, int c, double lz2, bool valid, bool dense) {
+  const float zx = (float)lz2;
+  const float zy = (lz2 > -INFINITY && lz2 < INFINITY) ? (float)(lz2 - (double)zx) : 0.0f;
+  unsigned pairs = 0;
+  for (int kb0 = 0; kb0 < KB; kb0 += 8) {
+    float R[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) R[j] = kb0 + j < KB ? rmax(kb0 + j) : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (kb0 + j < KB) {
+        const bool need = valid && (dense || !(((R[j] - zx) - zy) < -kLjNeedGap));
+        const unsigned b = (unsigned)__builtin_amdgcn_ballot_w64(need);
+        pairs += __builtin_popcount(lj_pair_mask(b));
+        if (c == 0) mask[kb0 + j] = b;
+      }
+    }
+  }
+  if (c == 0 && pairs != 0) atomicAdd(count, pairs);
+}
+
+// ---------------------------------------------------------------------------
 // Range-checked buffer loads.  A raw buffer resource covers `bytes` bytes from
 // `base`; a lane whose byte offset is at or beyond that reads zero and makes no
 // memory access.  Streaming loops use them to issue the same number of load
@@ -505,6 +619,12 @@ __device__ __forceinline__ f32x4 buf_load_f32x4(buf_rsrc r, int off) {
 
 // Workspace cap for the stored log-joint of one call (N/32 x K/32 tiles of 4 KiB).
 constexpr size_t kMaxLjBytes = (size_t)16 << 30;
+
+// The log-joint is stored only on request (FGMM_FLAG_STORE_LOGJOINT); RECOMPUTE,
+// the default plan, overrides it.
+__host__ __device__ constexpr bool wants_stored_lj(unsigned flags) {
+  return (flags & FGMM_FLAG_STORE_LOGJOINT) != 0 && (flags & FGMM_FLAG_RECOMPUTE) == 0;
+}
 
 // Largest row stride (floats) of X for the buffer-loaded streaming passes: a
 // tile's byte offsets (256 rows x stride x 4) must stay below 2^31.

@@ -97,7 +97,7 @@ __host__ inline bool use_stored_lj(int64_t N, int KB, int DP, bool allow) {
          (size_t)round_up(cdiv(N, 32), 4) * (size_t)KB * kLjTile * sizeof(float) <= kMaxLjBytes;
 }
 
-DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf16 = false) {
+DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool bf16 = false) {
   DiagPlan p{};
   p.N = N; p.K = K; p.D = D;
   p.DP = diag_padded_dim(D);
@@ -2269,12 +2269,12 @@ using namespace fgmm;
 
 extern "C" size_t fgmm_diag_workspace_bytes(int64_t N, int64_t K, int64_t D) {
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D).total;
+  return make_plan(N, K, D, false).total;
 }
 
 extern "C" size_t fgmm_diag_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE), (flags & FGMM_FLAG_BF16) != 0).total;
+  return make_plan(N, K, D, wants_stored_lj(flags), (flags & FGMM_FLAG_BF16) != 0).total;
 }
 
 extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -2300,7 +2300,7 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   // The stored-log-joint pass 2 addresses X tiles with 32-bit buffer offsets (row
   // stride at most kMaxBufLdx floats); wider strides recompute, which needs less
   // workspace.
-  const DiagPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE) && ldx <= kMaxBufLdx, bf16);
+  const DiagPlan pl = make_plan(N, K, D, wants_stored_lj(flags) && ldx <= kMaxBufLdx, bf16);
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;
   unsigned char* ws = static_cast<unsigned char*>(workspace);

@@ -427,6 +427,10 @@ extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn 
     if (st == FGMM_OK) st = drain_estep(b);
     if (st != FGMM_OK) return st;
   }
+  // The last M-step follows the last E-step's event on the compute stream, and both
+  // streams are non-blocking (the null-stream copy below does not wait for them):
+  // wait for the compute stream before reading its results and events.
+  if (!ok(hipStreamSynchronize(res.comp))) return FGMM_ERR_HIP;
   std::vector<double> ll(nll, 0.0);
   if (iters > 0 && !ok(hipMemcpy(ll.data(), res.ll, iters * sizeof(double), hipMemcpyDeviceToHost)))
     return FGMM_ERR_HIP;

@@ -77,7 +77,7 @@ __host__ inline size_t full_lj_bytes(int64_t N, int KP) {
 __host__ __device__ constexpr int bf16_comps_per_wg(int NMB);
 __host__ __device__ constexpr int bf16_row_groups(int NMB);
 
-FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf16 = false) {
+FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool bf16 = false) {
   FullPlan p{};
   p.N = N; p.K = K; p.D = D;
   p.DP = (int)round_up(D < 1 ? 1 : D, 32);
@@ -1416,12 +1416,12 @@ using namespace fgmm;
 
 extern "C" size_t fgmm_full_workspace_bytes(int64_t N, int64_t K, int64_t D) {
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D).total;
+  return make_plan(N, K, D, false).total;
 }
 
 extern "C" size_t fgmm_full_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE), (flags & FGMM_FLAG_BF16) != 0).total;
+  return make_plan(N, K, D, wants_stored_lj(flags), (flags & FGMM_FLAG_BF16) != 0).total;
 }
 
 extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -1444,7 +1444,7 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   if (D > 128) return FGMM_ERR_UNSUPPORTED;
   if (N > kMaxRows || K > (int64_t)1 << 20) return FGMM_ERR_UNSUPPORTED;
   const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
-  const FullPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE), bf16);
+  const FullPlan pl = make_plan(N, K, D, wants_stored_lj(flags), bf16);
   // The bf16 contract always stores the log-joint: N x K floats within kMaxLjBytes.
   if (bf16 && K > 0 && !pl.lj) return FGMM_ERR_UNSUPPORTED;
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;

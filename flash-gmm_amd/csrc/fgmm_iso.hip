@@ -111,11 +111,23 @@ struct IsoPlan {
   int npart;    // nslab * rgroups
   int64_t rows_per_slab;
   bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16)
-  bool lj;      // pass 1 stores the log-joint; pass 2 reads it
+  bool lj;      // pass 1 stores the log-joint; pass 2 reads it (FGMM_FLAG_STORE_LOGJOINT)
   int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
-  size_t off_musw, off_mu3, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_nk, off_part_sig,
-      off_lj, off_ljmax, off_ljmask, off_ljcount, total;
+  bool need;    // default plan up to D = 128: pass 1 leaves need masks, pass 2 gathers
+  bool rexact;  // need masks from the block maxima kept in LDS (else the running-max bound)
+  size_t off_musw, off_mu3, off_kcblk, off_kclin, off_kcgat, off_rowstat, off_part_mu, off_part_nk,
+      off_part_sig, off_lj, off_ljmax, off_ljmask, off_ljcount, total;
 };
+
+// Pass 1 with need masks keeps a bf16 bound of each row's block maximum in LDS,
+// 2 bytes per (row, block) for its 4 waves, while the workgroup still fits twice in
+// a compute unit's LDS; for more blocks the masks come from the running-max bound.
+__host__ __device__ constexpr size_t lse_lds_base(int DP) {
+  return (size_t)2 * (DP / 16) * 4 * 64 * 16 + (size_t)2 * 32 * 16;
+}
+__host__ __device__ constexpr int need_exact_cap(int DP) {
+  return (int)((80 * 1024 - lse_lds_base(DP)) / (kWaves * 32 * 2));
+}
 
 // Pass 2 reads the stored log-joint when recomputation is not requested, D is at
 // least 33 (below, the recomputed contraction costs less than the extra traffic),
@@ -131,7 +143,7 @@ __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB);
 __host__ __device__ constexpr int bf16_halves(int DP);
 __host__ inline int bf16_blocks_per_group(int DP, int KB);
 
-IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf16 = false) {
+IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool bf16 = false) {
   IsoPlan p{};
   p.N = N; p.K = K; p.D = D;
   p.DP = iso_padded_dim(D);
@@ -139,6 +151,8 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf
   p.KP = p.KB * 32;
   p.bf16 = bf16;
   p.lj = !bf16 && use_stored_lj(N, p.DP, p.KB, allow_lj);
+  p.need = !bf16 && !p.lj && p.DP <= 128;
+  p.rexact = p.need && p.KB <= need_exact_cap(p.DP);
   if (bf16) {
     p.cpg = bf16_blocks_per_group(p.DP, p.KB);
     p.rgroups = kAccWaves / (p.cpg * bf16_halves(p.DP));
@@ -149,13 +163,23 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf
     p.cpg = (p.KB >= 8 && p.DP <= 192) ? 8 : 4;
     p.lj_nh = (p.DP > 128 && p.cpg == 4) ? 2 : 1;
     p.rgroups = kAccWaves / (p.cpg * p.lj_nh);
+  } else if (p.need) {
+    p.cpg = 1;        // one wave per (row slab, component block)
+    p.rgroups = 1;
   } else {
     p.cpg = accum_blocks_per_group(p.DP, p.KB);
     p.rgroups = accum_uses_lds(p.DP) ? kAccWaves / p.cpg : 1;
   }
   p.ncg = (int)cdiv(p.KB, p.cpg);
   const int64_t tile_rows = 32 * p.rgroups;
-  if (N > 0 && p.ncg > 0) {
+  if (p.need && N > 0 && p.KB > 0) {
+    // The gathering pass 2 runs one wave per SIMD: about two rounds of waves.
+    int64_t want = cdiv((int64_t)8 * current_device_cus(), p.KB);
+    const int64_t max_slabs = cdiv(N, 32);
+    if (want > max_slabs) want = max_slabs;
+    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.nslab = (int)cdiv(N, p.rows_per_slab);
+  } else if (N > 0 && p.ncg > 0) {
     int64_t want = (int64_t)current_device_cus() / p.ncg;
     if (want >= 8) want = (want / 8) * 8;  // keeps a slab's workgroups on one XCD
     if (want < 1) want = 1;
@@ -173,17 +197,18 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = true, bool bf
   p.off_mu3 = off;     off = align256(off + (size_t)p.KP * p.DP * 4 * 2);   // bf16 splits of mu
   p.off_kcblk = off;   off = align256(off + (size_t)p.KB * 32 * 2 * sizeof(double));
   p.off_kclin = off;   off = align256(off + (size_t)p.KP * 4 * sizeof(double));
+  p.off_kcgat = off;   off = align256(off + (size_t)p.KP * 4 * sizeof(double));
   p.off_rowstat = off; off = align256(off + (size_t)(N > 0 ? N : 0) * 2 * sizeof(double));
   p.off_part_mu = off; off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
   p.off_part_nk = off; off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
   p.off_part_sig = off; off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
   // One log-joint tile per pass-1 wave (the grid's 32-row tiles, rounded up to 4),
-  // with its per-row block maxima and need mask.
-  const size_t ntile = p.lj ? (size_t)round_up(cdiv(N, 32), 4) * p.KB : 0;
-  p.off_lj = off;     off = align256(off + ntile * kLjTile * sizeof(float));
-  p.off_ljmax = off;  off = align256(off + ntile * 32 * sizeof(float));
+  // with its per-row block maxima and need mask; the default plan keeps the masks only.
+  const size_t ntile = (p.lj || p.need) ? (size_t)round_up(cdiv(N, 32), 4) * p.KB : 0;
+  p.off_lj = off;     off = align256(off + (p.lj ? ntile * kLjTile * sizeof(float) : 0));
+  p.off_ljmax = off;  off = align256(off + (p.lj ? ntile * 32 * sizeof(float) : 0));
   p.off_ljmask = off; off = align256(off + ntile * sizeof(unsigned));
-  p.off_ljcount = off; off = align256(off + (p.lj ? 64 * sizeof(unsigned) : 0));
+  p.off_ljcount = off; off = align256(off + ((p.lj || p.need) ? 64 * sizeof(unsigned) : 0));
   p.total = off;
   return p;
 }
@@ -195,7 +220,8 @@ __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int
                                                int D, int DP, const float* __restrict__ lss,
                                                const float* __restrict__ lpi, f32x4* __restrict__ mu_sw,
                                                double2* __restrict__ kc_blk, double4* __restrict__ kc_lin,
-                                               bf16x8* __restrict__ mu3, unsigned* __restrict__ ljcount) {
+                                               double4* __restrict__ kc_gat, bf16x8* __restrict__ mu3,
+                                               unsigned* __restrict__ ljcount) {
   __shared__ double sC[32], sB[32];
   const int kb = blockIdx.x;
   const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
@@ -232,6 +258,9 @@ __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int
     sC[c] = (DP <= 128 && valid) ? C + 2.0 * b * osum : C;
     sB[c] = b;
     kc_lin[comp] = make_double4(C, b, musq, 0.0);
+    // The gathering pass 2 (D <= 128) takes the centred constant and, for
+    // ||x - mu||^2 = ||x||^2 - 2 (x.mu - sum_q o_q) + (||mu||^2 - 2 sum_q o_q), the last term.
+    if (DP <= 128) kc_gat[comp] = make_double4(sC[c], b, musq - 2.0 * osum, 0.0);
   }
   // mu in matrix-core operand order: chunk m of lane (c, g) = mu[comp][8m+4g .. 8m+4g+3].
   const int NM = DP / 8;
@@ -306,23 +335,33 @@ __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int
 // ---------------------------------------------------------------------------
 template <int DP>
 constexpr size_t lse_lds_bytes() {
-  return (size_t)2 * (DP / 16) * 4 * 64 * sizeof(bf16x8) + (size_t)2 * 32 * sizeof(double2);
+  static_assert(lse_lds_base(DP) == (size_t)2 * (DP / 16) * 4 * 64 * sizeof(bf16x8) + (size_t)2 * 32 * sizeof(double2),
+                "pass-1 LDS");
+  return lse_lds_base(DP);
 }
 
-template <int DP, bool LJ>
+// What pass 1 leaves for pass 2 besides logZ2 and ||x||^2.
+constexpr int kLjmNone = 0;    // nothing (the recomputing pass 2 above D = 128)
+constexpr int kLjmStore = 1;   // the stored log-joint, its block maxima and need masks
+constexpr int kLjmNeed = 2;    // need masks only (the default plan)
+
+template <int DP, int LJM>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
 void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
              const bf16x8* __restrict__ mu3, const double2* __restrict__ kc_blk, int KB,
              float* __restrict__ logZ, double2* __restrict__ rowstat, float* __restrict__ lj,
              float* __restrict__ ljmax, unsigned* __restrict__ ljmask, unsigned* __restrict__ ljcount,
-             int dense) {
+             int dense, int rexact) {
   constexpr int NQ = DP / 16;
   constexpr int BLK = NQ * 4 * 64;        // bf16x8 per 32-component block
   constexpr int LPT = (BLK + kThreads - 1) / kThreads;
+  constexpr bool LJ = LJM == kLjmStore;
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                                 // [2][BLK]
   double2* kc_l = reinterpret_cast<double2*>(lds_raw + 2 * BLK * sizeof(bf16x8));   // [2][32]
+  // Need masks: the rows' block-maximum bounds, [wave][block][row] (rexact only).
+  unsigned short* rmax_l = reinterpret_cast<unsigned short*>(lds_raw + lse_lds_bytes<DP>());
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: tile bases in scalars
@@ -369,7 +408,8 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   double mx = -INFINITY;
   float sm = 0.0f;
-  float run_max = -INFINITY;   // running max of the row's stored log-joint
+  float run_max = -INFINITY;   // running max of the row's stored log-joint / block maxima
+  unsigned pairs = 0;          // needed register-row pairs (need masks from the running max)
 
   for (int kb = 0; kb < KB; ++kb) {
     const int buf = kb & 1;
@@ -402,6 +442,20 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     if constexpr (LJ)
       lj_put_rows(lj + (tile * KB + kb) * kLjTile, ljmax + (tile * KB + kb) * 32, c, g, ll, bm, acc,
                   run_max, dense != 0);
+    if constexpr (LJM == kLjmNeed) {
+      const float R = lj_row_max(bm);   // the row's block maximum, in both half-waves
+      if (rexact) {
+        if (g == 0) rmax_l[(wave * KB + kb) * 32 + c] = bf16_bits_up(R);
+      } else {
+        // logZ2 >= the row's final maximum >= run_max - 1 ulp, so a block whose maximum is
+        // kLjSkipGap below the running max cannot reach the test of need_put_masks.
+        run_max = fmaxf(run_max, R);
+        const bool nb = valid && (dense != 0 || !(R - run_max < -kLjSkipGap));
+        const unsigned bits = (unsigned)__builtin_amdgcn_ballot_w64(nb);
+        if (lane == 0) ljmask[tile * KB + kb] = bits;
+        pairs += __builtin_popcount(lj_pair_mask(bits));
+      }
+    }
     if (more) commit(buf ^ 1);
     lds_barrier();
   }
@@ -420,6 +474,23 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   if constexpr (LJ) {
     if (g == 0) lj_put_masks(ljmax + tile * KB * 32, ljmask + tile * KB, ljcount + (tile & 63), KB, c, lz2,
                    valid, dense != 0);
+  }
+  if constexpr (LJM == kLjmNeed) {
+    if (rexact) {
+      const unsigned short* rm = rmax_l + wave * KB * 32 + c;
+      if (g == 0)
+        need_put_masks([&](int kb) { return bf16_bits_to_float(rm[kb * 32]); }, ljmask + tile * KB,
+                       ljcount + (tile & 63), KB, c, lz2, valid, dense != 0);
+    } else {
+      // A row whose logZ2 is NaN (a NaN log-joint somewhere) gets its bit in every
+      // block, as the exact test gives it.
+      const unsigned nanbits = (unsigned)__builtin_amdgcn_ballot_w64(valid && g == 0 && lz2 != lz2);
+      if (lane == 0) {
+        if (nanbits != 0)
+          for (int kb = 0; kb < KB; ++kb) ljmask[tile * KB + kb] |= nanbits;
+        if (pairs != 0) atomicAdd(ljcount + (tile & 63), pairs);
+      }
+    }
   }
 }
 
@@ -910,6 +981,219 @@ void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
         part_sig[kbase + c] = sig;
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2 of the default plan (D <= 128): the log-joint is recomputed only for the
+// (row, component block) pairs whose need bit pass 1 set.
+//
+// One wave per (row slab, component block); a workgroup holds 4 waves of one block
+// on consecutive slabs, with mu of the block (bf16 splits and centring offsets,
+// the B operands of x6c_tile_rows) in LDS for all four.  Each wave walks the need
+// words of its slab's 32-row tiles and queues the needed rows; every 32 queued
+// rows form one tile:
+//   - the rows of X are loaded into registers in the A-operand layout (lane = row),
+//     split three ways into bf16, and the first two splits are written row-major to
+//     the wave's LDS tiles;
+//   - S = X mu^T by x6c_tile_rows (lane = component, register = row), the
+//     log-joint by pass 1's formula (so logZ2 and r come from one log-joint),
+//     r = 2^(ll2 - logZ2), Nk and sig_acc on the VALU;
+//   - r^T X on the bf16 matrix cores as r2 x1 + r1 x2 + r1 x1 (r = r1 + r2 and
+//     x = x1 + x2 + x3 split exactly; the dropped terms are below 2^-16 of |r x|),
+//     r as the A operand (acc_to_row_operands) and the tile's rows as the B operand
+//     (lds_rows_operand, the transposing LDS read).
+// The next tile's rows are loaded while a tile is computed.  Workgroups are dealt
+// to the 8 XCDs round-robin; the index mapping puts every component block of a
+// slab group on one XCD, so a row of X that several blocks need comes from HBM
+// once and from that XCD's L2 after.
+// ---------------------------------------------------------------------------
+constexpr int kGatherWaves = 4;
+
+__host__ __device__ constexpr int gather_rs(int DP) { return DP + 16; }   // bf16 row stride of the X tiles
+
+__host__ __device__ constexpr size_t gather_lds_bytes(int DP) {
+  return (size_t)(DP / 16) * 4 * 64 * 16                          // mu block (bf16x8 operands)
+         + (size_t)kGatherWaves * 2 * 32 * gather_rs(DP) * 2      // x1, x2 tiles per wave
+         + (size_t)kGatherWaves * 32 * sizeof(double2)             // row state per wave
+         + (size_t)kGatherWaves * 64 * sizeof(int);                // row queue per wave
+}
+
+__host__ __device__ constexpr int gather_groups(int nslab) { return (nslab + kGatherWaves - 1) / kGatherWaves; }
+__host__ inline int64_t gather_grid(int nslab, int KB) { return cdiv(gather_groups(nslab), 8) * (int64_t)KB * 8; }
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kGatherWaves, 64 * kGatherWaves),
+                          amdgpu_waves_per_eu(1, 1)))
+void iso_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                      const bf16x8* __restrict__ mu3, const double4* __restrict__ kc_gat, int KB, int KP,
+                      const double2* __restrict__ rowstat, const unsigned* __restrict__ need, int nslab,
+                      int64_t rows_per_slab, float* __restrict__ part_mu, float* __restrict__ part_nk,
+                      float* __restrict__ part_sig, int dense) {
+  constexpr int NQ = DP / 16;
+  constexpr int NJ = DP / 32;
+  constexpr int RS = gather_rs(DP);
+  constexpr int BLK = NQ * 4 * 64;   // bf16x8 per component block
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  unsigned char* lp = lds_raw;
+  bf16x8* mu_l = reinterpret_cast<bf16x8*>(lp);    lp += (size_t)BLK * sizeof(bf16x8);
+  __bf16* xt_all = reinterpret_cast<__bf16*>(lp);  lp += (size_t)kGatherWaves * 2 * 32 * RS * 2;
+  double2* rs_all = reinterpret_cast<double2*>(lp); lp += (size_t)kGatherWaves * 32 * sizeof(double2);
+  int* q_all = reinterpret_cast<int*>(lp);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+
+  // Workgroup -> (slab group, block), with the blocks of a slab group on one XCD.
+  const int rest = (int)(blockIdx.x >> 3);
+  const int kb = rest % KB;
+  const int sg = (rest / KB) * 8 + (int)(blockIdx.x & 7);
+  if (sg >= gather_groups(nslab)) return;   // uniform over the workgroup
+  for (int idx = tid; idx < BLK; idx += 64 * kGatherWaves) mu_l[idx] = mu3[(int64_t)kb * BLK + idx];
+  __syncthreads();
+  const int slab = sg * kGatherWaves + wave;
+  if (slab >= nslab) return;   // no barrier follows
+
+  __bf16* xt = xt_all + wave * 2 * 32 * RS;   // [split][row][RS]
+  double2* rs_l = rs_all + wave * 32;
+  int* q_l = q_all + wave * 64;
+
+  const double4 kc = kc_gat[(int64_t)kb * 32 + c];   // (centred C, b, ||mu||^2 - 2 sum o) of component c
+  const double Cc = kc.x, bk = kc.y;
+  const float mqf = (float)kc.z;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int64_t t_begin = r_begin / 32, t_end = cdiv(r_end, 32);
+
+  // Need words of 64 tiles at a time, one per lane, the next batch in flight.
+  auto words = [&](int64_t tb) -> unsigned {
+    const int64_t t = tb + lane;
+    return t < t_end ? need[t * KB + kb] : 0u;
+  };
+  int64_t tb = t_begin;
+  unsigned mword = words(tb), mnext = words(tb + 64);
+  int jn = 0;          // next word of the batch
+  int qh = 0, qt = 0;  // queue head and tail (positions mod 64)
+
+  // Queue rows until 32 are waiting (or the slab ends) and take up to 32 of them:
+  // returns the count (uniform); lane c of both halves gets tile row c's offset in
+  // the slab, or -1.
+  auto take = [&](int& e) -> int {
+    while (qt - qh < 32) {
+      const uint64_t live = jn >= 64 ? 0ull : (~0ull << jn);
+      const uint64_t nz = __builtin_amdgcn_ballot_w64(mword != 0u) & live;
+      if (nz == 0) {
+        tb += 64;
+        if (tb >= t_end) break;
+        mword = mnext;
+        mnext = words(tb + 64);
+        jn = 0;
+        continue;
+      }
+      const int j = __builtin_ctzll(nz);
+      const unsigned m = __builtin_amdgcn_readlane(mword, j);
+      const int base = (int)((tb + j - t_begin) * 32);
+      if (g == 0 && ((m >> c) & 1u)) q_l[(qt + __builtin_popcount(m & ((1u << c) - 1u))) & 63] = base + c;
+      qt += __builtin_popcount(m);
+      jn = j + 1;
+    }
+    const int cnt = qt - qh < 32 ? qt - qh : 32;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    e = c < cnt ? q_l[(qh + c) & 63] : -1;
+    qh += cnt;
+    return cnt;
+  };
+
+  // Rows of the tile in flight: X in the A-operand layout and the row state.
+  f32x4 raw[2 * NQ];
+  double2 rst;
+  auto issue = [&](int e) {
+    const bool ok = e >= 0;
+    const int64_t row = r_begin + (ok ? e : 0);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      raw[2 * q] = load_row4(X, ldx, row, 16 * q + 8 * g, D, ok);
+      raw[2 * q + 1] = load_row4(X, ldx, row, 16 * q + 8 * g + 4, D, ok);
+    }
+    rst = ok ? rowstat[row] : make_double2(0.0, INFINITY);
+  };
+
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
+  float nk = 0.0f, sig = 0.0f;
+  const bf16x8 ones = x6c_ones(lane);
+
+  int e;
+  int cnt = take(e);
+  if (cnt > 0) issue(e);
+  while (cnt > 0) {
+    // This tile's rows: bf16 splits in registers, x1 and x2 to LDS, row state to LDS.
+    bf16x8 xa[NQ][3];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) split3_bf16(raw[2 * q], raw[2 * q + 1], xa[q]);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the previous tile's LDS reads are done
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+      for (int sp = 0; sp < 2; ++sp)
+        *reinterpret_cast<bf16x8*>(xt + (sp * 32 + c) * RS + 16 * q + 8 * g) = xa[q][sp];
+    }
+    if (g == 0) rs_l[c] = rst;
+    // The next tile's rows, in flight while this one is computed.
+    int en;
+    const int cnt_next = take(en);
+    if (cnt_next > 0) issue(en);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+    const f32x16 S = x6c_tile_rows<NQ>(xa, ones, [&](int q, int t) { return mu_l[(q * 4 + t) * 64 + lane]; });
+    float r[16], res[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const double2 w = rs_l[acc_row(i, g)];   // (||x||^2, logZ2) of the row
+      const double ll = fma(-bk, fma(-2.0, (double)S[i], w.x), Cc);
+      const float rv = fast_exp2((float)(ll - w.y));
+      r[i] = rv;
+      res[i] = rv - (float)(__bf16)rv;
+      nk += rv;
+      sig = fmaf(rv, fmaf(-2.0f, S[i], (float)w.x) + mqf, sig);
+    }
+    bf16x8 a1[2], a2[2];
+    acc_to_row_operands(r, a1);
+    acc_to_row_operands(res, a2);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      // A step whose responsibilities all round to zero adds nothing (their residuals
+      // are zero too): skipped, with identical results.
+      if (dense || any_nonzero(a1[p])) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const bf16x8 b1 = lds_rows_operand(xt, RS, 16 * p, 32 * j, lane);
+          const bf16x8 b2 = lds_rows_operand(xt + 32 * RS, RS, 16 * p, 32 * j, lane);
+          acc[j] = mfma_bf16(a2[p], b1, acc[j]);
+          acc[j] = mfma_bf16(a1[p], b2, acc[j]);
+          acc[j] = mfma_bf16(a1[p], b1, acc[j]);
+        }
+      }
+    }
+    cnt = cnt_next;
+  }
+
+  nk += __shfl_xor(nk, 32);
+  sig += __shfl_xor(sig, 32);
+  const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[j][i];
+  }
+  if (g == 0) {
+    part_nk[kbase + c] = nk;
+    part_sig[kbase + c] = sig;
   }
 }
 
@@ -1531,21 +1815,23 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   float* ljmax = pl.lj ? reinterpret_cast<float*>(ws + pl.off_ljmax) : nullptr;
   unsigned* ljmask = pl.lj ? reinterpret_cast<unsigned*>(ws + pl.off_ljmask) : nullptr;
   unsigned* ljcount = pl.lj ? reinterpret_cast<unsigned*>(ws + pl.off_ljcount) : nullptr;
+  if (pl.need) {
+    ljmask = reinterpret_cast<unsigned*>(ws + pl.off_ljmask);
+    ljcount = reinterpret_cast<unsigned*>(ws + pl.off_ljcount);
+  }
   if (run1) {
     const int64_t nblk1 = cdiv(pl.N, 32 * kWaves);
     if constexpr (accum_uses_lds(DP)) {
-      constexpr size_t lds1 = lse_lds_bytes<DP>();
+      const size_t lds1 = lse_lds_bytes<DP>() + (pl.rexact ? (size_t)kWaves * 32 * pl.KB * 2 : 0);
+      auto kern = pl.lj ? &iso_lse<DP, kLjmStore> : pl.need ? &iso_lse<DP, kLjmNeed> : &iso_lse<DP, kLjmNone>;
       if (lds1 > 65536) {
-        for (const void* f : {reinterpret_cast<const void*>(&iso_lse<DP, false>),
-                              reinterpret_cast<const void*>(&iso_lse<DP, true>)}) {
-          hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
-          if (e != hipSuccess) return e;
-        }
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+        if (e != hipSuccess) return e;
       }
-      auto kern = pl.lj ? &iso_lse<DP, true> : &iso_lse<DP, false>;
       hipLaunchKernelGGL(kern, dim3((unsigned)nblk1), dim3(kThreads), lds1, stream, X, ldx, pl.N,
                          (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3), kc_blk, pl.KB,
-                         logZ, rowstat, lj, ljmax, ljmask, ljcount, dense ? 1 : 0);
+                         logZ, rowstat, lj, ljmax, ljmask, ljcount, dense ? 1 : 0, pl.rexact ? 1 : 0);
     } else {
       // Above D = 128 the rows' dimensions are split over two waves.
       constexpr size_t lds1 = lse_split_lds_bytes<DP>();
@@ -1563,6 +1849,21 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
     }
   }
   if (!run2) return hipGetLastError();
+  if constexpr (accum_uses_lds(DP)) {
+    if (pl.need) {
+      constexpr size_t lds = gather_lds_bytes(DP);
+      static_assert(lds <= kMaxLds, "gathering pass 2 exceeds LDS");
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_gather<DP>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(iso_accum_gather<DP>, dim3((unsigned)gather_grid(pl.nslab, pl.KB)),
+                         dim3(64 * kGatherWaves), lds, stream, X, ldx, pl.N, (int)pl.D,
+                         reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
+                         reinterpret_cast<const double4*>(ws + pl.off_kcgat), pl.KB, pl.KP, rowstat,
+                         ljmask, pl.nslab, pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
+      return hipGetLastError();
+    }
+  }
   const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
   if constexpr (DP >= 64) {
     if (pl.lj) {
@@ -2071,12 +2372,12 @@ using namespace fgmm;
 
 extern "C" size_t fgmm_iso_workspace_bytes(int64_t N, int64_t K, int64_t D) {
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D).total;
+  return make_plan(N, K, D, false).total;
 }
 
 extern "C" size_t fgmm_iso_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE), (flags & FGMM_FLAG_BF16) != 0).total;
+  return make_plan(N, K, D, wants_stored_lj(flags), (flags & FGMM_FLAG_BF16) != 0).total;
 }
 
 extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -2102,7 +2403,7 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
   const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
   // The stored log-joint path streams X with 32-bit buffer offsets (row stride at
   // most kMaxBufLdx floats); wider strides recompute, which needs less workspace.
-  const IsoPlan pl = make_plan(N, K, D, !(flags & FGMM_FLAG_RECOMPUTE) && ldx <= kMaxBufLdx, bf16);
+  const IsoPlan pl = make_plan(N, K, D, wants_stored_lj(flags) && ldx <= kMaxBufLdx, bf16);
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;
   unsigned char* ws = static_cast<unsigned char*>(workspace);
@@ -2126,8 +2427,9 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
                        log_sigma_sq, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_musw),
                        reinterpret_cast<double2*>(ws + pl.off_kcblk),
                        reinterpret_cast<double4*>(ws + pl.off_kclin),
+                       reinterpret_cast<double4*>(ws + pl.off_kcgat),
                        reinterpret_cast<bf16x8*>(ws + pl.off_mu3),
-                       pl.lj ? reinterpret_cast<unsigned*>(ws + pl.off_ljcount) : nullptr);
+                       (pl.lj || pl.need) ? reinterpret_cast<unsigned*>(ws + pl.off_ljcount) : nullptr);
   if (N > 0) {
     auto run = [&](auto dp_tag) -> hipError_t {
       constexpr int DP = decltype(dp_tag)::value;

@@ -30,6 +30,7 @@ FLAG_PHASE2 = 1 << 4
 FLAG_DENSE = 1 << 5
 FLAG_RECOMPUTE = 1 << 6
 FLAG_BF16 = 1 << 7
+FLAG_STORE_LOGJOINT = 1 << 9
 
 
 class FlashGMMError(AssertionError, ValueError):

@@ -104,13 +104,49 @@ def _check_out(name, t, shape, dev):
              f"{name} must be a contiguous float32 {tuple(shape)} tensor on {dev}")
 
 
+def _empty_workspace(nbytes, dev):
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+
+
 def _workspace(ws_fn, N, K, D, flags, dev, workspace):
-    # The size depends on the device's compute-unit count: query it with dev current.
+    """Return (workspace, flags).
+
+    The size depends on the device's compute-unit count, so it is queried with dev
+    current.  A phase-2 call must reuse the workspace its phase-1 call filled.  When
+    the stored log-joint's O(N*K) workspace cannot be allocated, the call falls back
+    to the default O(N + K*D) plan (same results to the float32 bounds)."""
     with torch.cuda.device(dev):
         ws_bytes = int(ws_fn(N, K, D, flags))
-    if workspace is None or workspace.numel() < ws_bytes:
-        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    return workspace
+    if flags & _lib.FLAG_PHASE2 and not flags & _lib.FLAG_PHASE1:
+        _require(workspace is not None and workspace.numel() >= ws_bytes,
+                 "phase=2 needs the workspace filled by the phase-1 call on the same inputs "
+                 f"({ws_bytes} bytes)")
+        return workspace, flags
+    if workspace is not None and workspace.numel() >= ws_bytes:
+        return workspace, flags
+    try:
+        return _empty_workspace(ws_bytes, dev), flags
+    except torch.cuda.OutOfMemoryError:
+        if not flags & _lib.FLAG_STORE_LOGJOINT or flags & (_lib.FLAG_PHASE1 | _lib.FLAG_PHASE2):
+            raise
+        lean = flags & ~_lib.FLAG_STORE_LOGJOINT
+        with torch.cuda.device(dev):
+            lean_bytes = int(ws_fn(N, K, D, lean))
+        if workspace is not None and workspace.numel() >= lean_bytes:
+            return workspace, lean
+        return _empty_workspace(lean_bytes, dev), lean
+
+
+def _plan_flags(flags, dense, recompute, store_log_joint, precision):
+    if dense:
+        flags |= _lib.FLAG_DENSE
+    if recompute:
+        flags |= _lib.FLAG_RECOMPUTE
+    elif store_log_joint:
+        flags |= _lib.FLAG_STORE_LOGJOINT
+    if precision == "bf16":
+        flags |= _lib.FLAG_BF16
+    return flags
 
 
 def _ptr(t, cond=True):
@@ -126,7 +162,7 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
                    accumulate: bool = False, atomic_reduce: bool = False,
                    workspace: torch.Tensor | None = None, phase: int = 0,
                    dense: bool = False, recompute: bool = False,
-                   precision: str = "fp32") -> None:
+                   store_log_joint: bool = False, precision: str = "fp32") -> None:
     """Isotropic E-step writing into caller-provided outputs.
 
     ``logZ`` may be None (it is then not written).  With ``accumulate`` the
@@ -135,9 +171,12 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     log-normaliser pass, 2 only the accumulation (reusing ``workspace`` from a
     phase-1 call on the same inputs), 0 both.  ``dense`` runs the accumulation
     steps whose responsibilities are all exactly zero instead of skipping them
-    (same results; for timing).  ``recompute`` makes the accumulation pass
-    recompute the log-joint instead of reading the copy that the first pass
-    stores in the workspace (smaller workspace; phase-split calls must agree).
+    (same results; for timing).  By default the workspace is O(N + K*D) and the
+    accumulation pass recomputes the log-joint where pass 1 found a possibly
+    nonzero responsibility (``recompute=True`` asks for this explicitly).
+    ``store_log_joint`` makes pass 1 store the fp32 N x K log-joint in the
+    workspace for pass 2 to read (O(N*K) workspace, 4.3 GB at N=1M, K=1024;
+    phase-split calls must agree).
     ``precision="bf16"`` selects the bf16 operand contract of the reference's H100
     kernels (flash_gmm_h100.py:247-328): X and mu rounded to bfloat16 for the
     contractions, fp32 accumulation and log-sum-exp.
@@ -153,14 +192,9 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     muk = _rowmajor(_f32(mu))
     ldmu = muk.stride(0) if K > 1 else D
     L = _lib.lib()
-    flags = _flags(accumulate, logZ, atomic_reduce, phase)
-    if dense:
-        flags |= _lib.FLAG_DENSE
-    if recompute:
-        flags |= _lib.FLAG_RECOMPUTE
-    if precision == "bf16":
-        flags |= _lib.FLAG_BF16
-    workspace = _workspace(L.fgmm_iso_workspace_bytes_ex, N, K, D, flags, dev, workspace)
+    flags = _plan_flags(_flags(accumulate, logZ, atomic_reduce, phase), dense, recompute,
+                        store_log_joint, precision)
+    workspace, flags = _workspace(L.fgmm_iso_workspace_bytes_ex, N, K, D, flags, dev, workspace)
     _check_out("Nk", Nk, (K,), dev)
     _check_out("mu_acc", mu_acc, (K, D), dev)
     _check_out("sig_acc", sig_acc, (K,), dev)
@@ -200,8 +234,8 @@ def flash_gmm_estep(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tenso
 
 def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
                     accumulate: bool = False, workspace: torch.Tensor | None = None,
-                    phase: int = 0, dense: bool = False,
-                    recompute: bool = False, precision: str = "fp32") -> None:
+                    phase: int = 0, dense: bool = False, recompute: bool = False,
+                    store_log_joint: bool = False, precision: str = "fp32") -> None:
     """Diagonal-covariance E-step into caller-provided outputs (sig_acc is (K, D)).
 
     ``precision="bf16"`` selects the bf16 operand contract of the reference's
@@ -226,14 +260,9 @@ def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     ldmu = muk.stride(0) if K > 1 else D
     L = _lib.lib()
     _require(hasattr(L, "fgmm_diag_estep_f32"), "library built without the diagonal E-step")
-    flags = _flags(accumulate, logZ, False, phase)
-    if dense:
-        flags |= _lib.FLAG_DENSE
-    if recompute:
-        flags |= _lib.FLAG_RECOMPUTE
-    if precision == "bf16":
-        flags |= _lib.FLAG_BF16
-    workspace = _workspace(L.fgmm_diag_workspace_bytes_ex, N, K, D, flags, dev, workspace)
+    flags = _plan_flags(_flags(accumulate, logZ, False, phase), dense, recompute, store_log_joint,
+                        precision)
+    workspace, flags = _workspace(L.fgmm_diag_workspace_bytes_ex, N, K, D, flags, dev, workspace)
     _check_out("Nk", Nk, (K,), dev)
     _check_out("mu_acc", mu_acc, (K, D), dev)
     _check_out("sig_acc", sig_acc, (K, D), dev)
@@ -272,8 +301,8 @@ def flash_gmm_estep_diag(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.
 
 def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
                     accumulate: bool = False, workspace: torch.Tensor | None = None,
-                    phase: int = 0, dense: bool = False,
-                    recompute: bool = False, precision: str = "fp32") -> None:
+                    phase: int = 0, dense: bool = False, recompute: bool = False,
+                    store_log_joint: bool = False, precision: str = "fp32") -> None:
     """Full-covariance E-step into caller-provided outputs (sig_outer is (K, D, D)).
 
     ``precision="bf16"`` selects the bf16 operand contract of the reference's full
@@ -298,14 +327,9 @@ def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
     ldmu = muk.stride(0) if K > 1 else D
     L = _lib.lib()
     _require(hasattr(L, "fgmm_full_estep_f32"), "library built without the full-covariance E-step")
-    flags = _flags(accumulate, logZ, False, phase)
-    if dense:
-        flags |= _lib.FLAG_DENSE
-    if recompute:
-        flags |= _lib.FLAG_RECOMPUTE
-    if precision == "bf16":
-        flags |= _lib.FLAG_BF16
-    workspace = _workspace(L.fgmm_full_workspace_bytes_ex, N, K, D, flags, dev, workspace)
+    flags = _plan_flags(_flags(accumulate, logZ, False, phase), dense, recompute, store_log_joint,
+                        precision)
+    workspace, flags = _workspace(L.fgmm_full_workspace_bytes_ex, N, K, D, flags, dev, workspace)
     _check_out("Nk", Nk, (K,), dev)
     _check_out("mu_acc", mu_acc, (K, D), dev)
     _check_out("sig_outer", sig_outer, (K, D, D), dev)

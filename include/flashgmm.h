@@ -66,11 +66,11 @@ enum fgmm_flags {
      * either way.  DENSE runs every step and, in pass 1, stores every row (for
      * timing the dense contraction). */
     FGMM_FLAG_DENSE = 1u << 5,
-    /* By default pass 1 also stores the fp32 log-joint (N/32 x K/32 tiles of
-     * 4 KiB, when that is at most 16 GiB, D > 32 and K > 96) in the workspace,
-     * and pass 2 reads it back instead of recomputing the D-contraction.
-     * RECOMPUTE keeps the workspace O(N + K*D) and recomputes.  Calls that
-     * split the phases must agree on this flag. */
+    /* The default plan: the workspace is O(N + K*D) (plus one need bit per
+     * row and 32-component block) and pass 2 recomputes the D-contraction for
+     * the (row, component block) pairs pass 1 marked as able to carry a nonzero
+     * responsibility.  The N x K log-joint is never materialised.  Setting this
+     * bit selects the default explicitly and overrides STORE_LOGJOINT. */
     FGMM_FLAG_RECOMPUTE = 1u << 6,
     /* The bf16 operand contract of the reference's H100 kernels, fp32 accumulation
      * and log-sum-exp throughout (the reference states a 5e-3 tolerance against
@@ -83,10 +83,17 @@ enum fgmm_flags {
      *   full (flash_gmm_full_h100.py:71-228, :289-298): x and L rounded to bfloat16
      *     for the whitening, L^T mu fp32; r rounded for mu_acc and r x_d2 for
      *     sig_outer[k][d2][:], which is then not exactly symmetric.  This path
-     *     always stores the log-joint and returns FGMM_ERR_UNSUPPORTED when its
-     *     N x K floats exceed 16 GiB (call in row chunks with ACCUMULATE).
-     * FGMM_FLAG_RECOMPUTE has no effect with it. */
+     *     stores the log-joint of at most 16 GiB per call and runs larger N in
+     *     row chunks internally (same results as one call).
+     * FGMM_FLAG_RECOMPUTE and STORE_LOGJOINT have no effect with it. */
     FGMM_FLAG_BF16 = 1u << 7,
+    /* Opt-in: pass 1 also stores the fp32 log-joint (N/32 x K/32 tiles of
+     * 4 KiB, when that is at most 16 GiB, D > 32 and K > 96) in the workspace,
+     * and pass 2 reads it back instead of recomputing the D-contraction.  The
+     * workspace is then O(N*K) (4.3 GB at N=1M, K=1024): size it with
+     * *_workspace_bytes_ex(..., flags).  Calls that split the phases must agree
+     * on this flag. */
+    FGMM_FLAG_STORE_LOGJOINT = 1u << 9,
 };
 
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */

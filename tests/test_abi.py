@@ -44,42 +44,55 @@ def test_iso_workspace_bytes_grows_with_size():
     L = _lib.lib()
     R = _lib.FLAG_RECOMPUTE
     a = L.fgmm_iso_workspace_bytes(1000, 64, 32)
-    b = L.fgmm_iso_workspace_bytes_ex(1_000_000, 1024, 128, R)
+    b = L.fgmm_iso_workspace_bytes(1_000_000, 1024, 128)
     assert 0 < a < b
-    # Recomputing: per-row state (16 B/row) + O(K*D) terms, far below the N*K log-joint.
-    assert b < 1_000_000 * 1024 * 4 // 20
+    assert L.fgmm_iso_workspace_bytes_ex(1_000_000, 1024, 128, R) == b
+    assert L.fgmm_iso_workspace_bytes_ex(1_000_000, 1024, 128, 0) == b
     assert L.fgmm_iso_workspace_bytes(-1, 4, 4) == 0
     assert L.fgmm_iso_workspace_bytes(10, 4, 0) == 0
     assert L.fgmm_iso_workspace_bytes_ex(10, 4, 0, 0) == 0
 
 
-def test_iso_workspace_holds_stored_log_joint():
-    """Default sizing adds the fp32 log-joint tiles (N/32 x K/32 x 4 KiB) where pass 2 reads them,
-    with a per-row block maximum (128 bytes) and a need mask (4 bytes) per tile."""
+def test_default_workspace_is_lean():
+    """The default plan is O(N + K*D): per-row state (16 B/row), the slab partials and
+    one need bit per (row, 32-component block), never the N x K log-joint
+    (flash_gmm.py:14-15: the reference's working memory is O(K*D))."""
     L = _lib.lib()
-    R = _lib.FLAG_RECOMPUTE
     N, K, D = 1_000_000, 1024, 128
-    full = L.fgmm_iso_workspace_bytes(N, K, D)
-    assert full == L.fgmm_iso_workspace_bytes_ex(N, K, D, 0)
-    lean = L.fgmm_iso_workspace_bytes_ex(N, K, D, R)
+    lean = L.fgmm_iso_workspace_bytes(N, K, D)
+    masks = (-(-N // 128) * 4) * (K // 32) * 4
+    assert lean < 16 * N + masks + (40 << 20) < 64 << 20
+    assert L.fgmm_diag_workspace_bytes(N, K, 96) < 64 << 20
+    assert L.fgmm_full_workspace_bytes(250_000, 256, 64) < 64 << 20
+
+
+def test_iso_workspace_holds_stored_log_joint():
+    """FGMM_FLAG_STORE_LOGJOINT adds the fp32 log-joint tiles (N/32 x K/32 x 4 KiB) where
+    pass 2 reads them, with a per-row block maximum (128 bytes) per tile; the need masks
+    are in both plans.  RECOMPUTE overrides it."""
+    L = _lib.lib()
+    R, S = _lib.FLAG_RECOMPUTE, _lib.FLAG_STORE_LOGJOINT
+    N, K, D = 1_000_000, 1024, 128
+    stored = L.fgmm_iso_workspace_bytes_ex(N, K, D, S)
+    lean = L.fgmm_iso_workspace_bytes(N, K, D)
+    assert L.fgmm_iso_workspace_bytes_ex(N, K, D, S | R) == lean
     pairs = -(-N // 128) * 4 * (K // 32)
-    tiles = pairs * (4096 + 128 + 4)
-    assert tiles <= full - lean <= tiles + 3 * 256
+    tiles = pairs * (4096 + 128)
+    assert tiles <= stored - lean <= tiles + 4 * 256
     # Not stored: D <= 32, K <= 96, or more than 16 GiB of tiles.
     for n, k, d in [(N, K, 32), (N, 96, 128), (N, 96, 192), (20_000_000, 1024, 128)]:
-        assert L.fgmm_iso_workspace_bytes(n, k, d) == L.fgmm_iso_workspace_bytes_ex(n, k, d, R)
+        assert L.fgmm_iso_workspace_bytes(n, k, d) == L.fgmm_iso_workspace_bytes_ex(n, k, d, S)
     # Diagonal: stored for K > 96 at every D.
-    d_full = L.fgmm_diag_workspace_bytes(N, K, 96)
-    d_lean = L.fgmm_diag_workspace_bytes_ex(N, K, 96, R)
-    # The diagonal form keeps two maxima per row (one per half block) and two mask words.
-    assert d_full == L.fgmm_diag_workspace_bytes_ex(N, K, 96, 0)
-    assert d_full - d_lean >= pairs * (4096 + 256 + 8)
-    assert L.fgmm_diag_workspace_bytes(N, 96, 96) == L.fgmm_diag_workspace_bytes_ex(N, 96, 96, R)
+    d_stored = L.fgmm_diag_workspace_bytes_ex(N, K, 96, S)
+    d_lean = L.fgmm_diag_workspace_bytes(N, K, 96)
+    assert d_lean == L.fgmm_diag_workspace_bytes_ex(N, K, 96, R) == L.fgmm_diag_workspace_bytes_ex(N, K, 96, 0)
+    assert d_stored - d_lean >= pairs * (4096 + 256)
+    assert L.fgmm_diag_workspace_bytes(N, 96, 96) == L.fgmm_diag_workspace_bytes_ex(N, 96, 96, S)
     # Full: stored whenever it fits, 32 floats per (32-row tile, component).
     q, qx = L.fgmm_full_workspace_bytes, L.fgmm_full_workspace_bytes_ex
-    assert q(5000, 64, 64) == qx(5000, 64, 64, 0) > 0
+    assert q(5000, 64, 64) == qx(5000, 64, 64, 0) == qx(5000, 64, 64, R) > 0
     n = 250_000
-    assert q(n, 256, 64) - qx(n, 256, 64, R) >= -(-n // 128) * 4 * 256 * 128
+    assert qx(n, 256, 64, S) - q(n, 256, 64) >= -(-n // 128) * 4 * 256 * 128
 
 
 # Fake but aligned, non-null addresses: every call below must be rejected by

@@ -45,10 +45,10 @@ def test_edge_shapes(N, K, D, gpu_device):
     assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), f"diag N={N} K={K} D={D}")
 
 
-@pytest.mark.parametrize("recompute", [False, True])
+@pytest.mark.parametrize("stored", [False, True])
 @pytest.mark.parametrize("N,K,D,seed", [(9000, 512, 96, 2), (3001, 77, 45, 3), (4000, 130, 256, 4),
                                         (5000, 300, 128, 6)])
-def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, recompute, gpu_device):
+def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, stored, gpu_device):
     """Skipping all-zero responsibility steps changes no bit of any output."""
     inp = data.diag_clustered(N, K, D, seed=seed)
     dev = gpu_device
@@ -57,7 +57,7 @@ def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, recompute, gpu_device):
     for dense in (False, True):
         o = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
              torch.empty(K, D, device=dev)]
-        diag_estep_into(*args, *o, dense=dense, recompute=recompute)
+        diag_estep_into(*args, *o, dense=dense, store_log_joint=stored)
         outs.append(o)
     torch.cuda.synchronize()
     for u, v in zip(*outs):
@@ -94,11 +94,11 @@ def test_stored_and_recomputed_log_joint(N, K, D, gpu_device):
     from flash_gmm import _lib
     L = _lib.lib()
     # The two plans differ (stored tiles, pass-2 work split), so these shapes take the stored path.
-    assert L.fgmm_diag_workspace_bytes(N, K, D) != L.fgmm_diag_workspace_bytes_ex(N, K, D, _lib.FLAG_RECOMPUTE)
+    assert L.fgmm_diag_workspace_bytes(N, K, D) != L.fgmm_diag_workspace_bytes_ex(N, K, D, _lib.FLAG_STORE_LOGJOINT)
     inp = data.diag_clustered(N, K, D, seed=N + 3 * K + D)
     ref = oracle(inp)
-    stored = _into(inp, gpu_device)
-    recomputed = _into(inp, gpu_device, recompute=True)
+    stored = _into(inp, gpu_device, store_log_joint=True)
+    recomputed = _into(inp, gpu_device)
     assert torch.equal(stored[0], recomputed[0])
     assert_close_stats(stored, ref, f"stored N={N} K={K} D={D}")
     assert_close_stats(recomputed, ref, f"recomputed N={N} K={K} D={D}")
@@ -112,34 +112,36 @@ SPARSE_SHAPES = [(20000, 1024, 64), (20000, 512, 96), (40000, 512, 128), (30001,
                  (20000, 300, 40), (20000, 512, 90)]
 
 
+@pytest.mark.parametrize("stored", [False, True])
 @pytest.mark.parametrize("N,K,D", SPARSE_SHAPES)
-def test_sparse_accumulation_is_bitwise_dense(N, K, D, gpu_device):
-    """Default accumulation from the sparse log-joint against FGMM_FLAG_DENSE and the oracle."""
+def test_sparse_accumulation_is_bitwise_dense(N, K, D, stored, gpu_device):
+    """Accumulation (default plan, and from the sparse stored log-joint) against
+    FGMM_FLAG_DENSE and the oracle."""
     inp = data.diag_clustered(N, K, D, seed=N % 97 + D)
-    a = _into(inp, gpu_device)
-    b = _into(inp, gpu_device, dense=True)
+    a = _into(inp, gpu_device, store_log_joint=stored)
+    b = _into(inp, gpu_device, dense=True, store_log_joint=stored)
     for u, v in zip(a, b):
         assert torch.equal(u, v)
     assert_close_stats(a, oracle(inp), f"sparse N={N} K={K} D={D}")
 
 
-@pytest.mark.parametrize("recompute", [False, True])
-def test_phase_split_equals_one_call(recompute, gpu_device):
+@pytest.mark.parametrize("stored", [False, True])
+def test_phase_split_equals_one_call(stored, gpu_device):
     """PHASE1 then PHASE2 on one workspace gives the single call's outputs bitwise."""
     from flash_gmm import _lib
     inp = data.diag_clustered(5000, 256, 80, seed=16)
     dev = gpu_device
-    ref = _into(inp, dev, recompute=recompute)
+    ref = _into(inp, dev, store_log_joint=stored)
     N, D = inp["X"].shape
     K = inp["mu"].shape[0]
     L = _lib.lib()
-    flags = _lib.FLAG_RECOMPUTE if recompute else 0
+    flags = _lib.FLAG_STORE_LOGJOINT if stored else 0
     ws = torch.empty(L.fgmm_diag_workspace_bytes_ex(N, K, D, flags), dtype=torch.uint8, device=dev)
     out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
            torch.empty(K, D, device=dev)]
     args = [inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
-    diag_estep_into(*args, *out, workspace=ws, phase=1, recompute=recompute)
-    diag_estep_into(*args, None, *out[1:], workspace=ws, phase=2, recompute=recompute)
+    diag_estep_into(*args, *out, workspace=ws, phase=1, store_log_joint=stored)
+    diag_estep_into(*args, None, *out[1:], workspace=ws, phase=2, store_log_joint=stored)
     torch.cuda.synchronize()
     for u, v in zip(out, ref):
         assert torch.equal(u, v)

@@ -53,12 +53,12 @@ def test_golden_vectors(gpu_device):
                                    (1000, 33, 40), (129, 4, 32), (2000, 9, 63),
                                    (400, 9, 65), (600, 11, 96), (300, 5, 100), (500, 7, 128),
                                    (3, 2, 127)])
-@pytest.mark.parametrize("recompute", [False, True])
-def test_edge_shapes(N, K, D, recompute, gpu_device):
-    """Pass 2 from the log-joint stored by pass 1 (default), and recomputed."""
+@pytest.mark.parametrize("stored", [False, True])
+def test_edge_shapes(N, K, D, stored, gpu_device):
+    """Pass 2 recomputing (default), and from the log-joint stored by pass 1."""
     inp = data.full_clustered(N, K, D, seed=N + K + D)
-    assert_close_stats(_into(inp, gpu_device, recompute=recompute), oracle(inp),
-                       f"full N={N} K={K} D={D} recompute={recompute}")
+    assert_close_stats(_into(inp, gpu_device, store_log_joint=stored), oracle(inp),
+                       f"full N={N} K={K} D={D} stored={stored}")
 
 
 def test_diagonal_factor_matches_diag_entry(gpu_device):
@@ -77,9 +77,9 @@ def test_diagonal_factor_matches_diag_entry(gpu_device):
     torch.testing.assert_close(s, a[3], rtol=1e-3, atol=1e-3 * float(a[3].abs().max()))
 
 
-@pytest.mark.parametrize("recompute", [False, True])
+@pytest.mark.parametrize("stored", [False, True])
 @pytest.mark.parametrize("N,K,D,seed", [(6000, 128, 64, 3), (2501, 19, 29, 4), (3000, 24, 128, 5)])
-def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, recompute, gpu_device):
+def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, stored, gpu_device):
     """Skipping all-zero responsibility steps changes no bit of any output."""
     inp = data.full_clustered(N, K, D, seed=seed)
     dev = gpu_device
@@ -88,7 +88,7 @@ def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, recompute, gpu_device):
     for dense in (False, True):
         o = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
              torch.empty(K, D, D, device=dev)]
-        full_estep_into(*args, *o, dense=dense, recompute=recompute)
+        full_estep_into(*args, *o, dense=dense, store_log_joint=stored)
         outs.append(o)
     torch.cuda.synchronize()
     for u, v in zip(*outs):
@@ -96,25 +96,25 @@ def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, recompute, gpu_device):
     assert_close_stats(outs[0], oracle(inp), "full skip")
 
 
-@pytest.mark.parametrize("recompute", [False, True])
-def test_phase_split_equals_one_call(recompute, gpu_device):
+@pytest.mark.parametrize("stored", [False, True])
+def test_phase_split_equals_one_call(stored, gpu_device):
     """PHASE1 then PHASE2 on one workspace gives the single call's outputs bitwise."""
     from flash_gmm import _lib
     inp = data.full_clustered(3000, 40, 72, seed=17)
     dev = gpu_device
-    ref = _into(inp, dev, recompute=recompute)
+    ref = _into(inp, dev, store_log_joint=stored)
     N, D = inp["X"].shape
     K = inp["mu"].shape[0]
     L = _lib.lib()
-    flags = _lib.FLAG_RECOMPUTE if recompute else 0
+    flags = _lib.FLAG_STORE_LOGJOINT if stored else 0
     ws_default = L.fgmm_full_workspace_bytes(N, K, D)
     ws = torch.empty(L.fgmm_full_workspace_bytes_ex(N, K, D, flags), dtype=torch.uint8, device=dev)
-    assert (ws.numel() < ws_default) == recompute
+    assert (ws.numel() > ws_default) == stored
     out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
            torch.empty(K, D, D, device=dev)]
     args = [inp[k].to(dev) for k in KEYS]
-    full_estep_into(*args, *out, workspace=ws, phase=1, recompute=recompute)
-    full_estep_into(*args, None, *out[1:], workspace=ws, phase=2, recompute=recompute)
+    full_estep_into(*args, *out, workspace=ws, phase=1, store_log_joint=stored)
+    full_estep_into(*args, None, *out[1:], workspace=ws, phase=2, store_log_joint=stored)
     torch.cuda.synchronize()
     for u, v in zip(out, ref):
         assert torch.equal(u, v)

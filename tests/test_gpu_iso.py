@@ -120,6 +120,23 @@ def test_deterministic_bitwise(gpu_device):
         assert torch.equal(u, v)
 
 
+def assert_dense_agrees(a, b, bitwise):
+    """The skipping run `a` against the dense run `b`.  On the stored log-joint both
+    add the same terms in the same order: bitwise equal.  The default plan's pass 2
+    gathers the needed rows into tiles of its own, so the float32 accumulators add
+    the same nonzero terms in other groupings: logZ (pass 1) is bitwise equal and the
+    statistics agree to 1e-5 (norm-wise for mu_acc)."""
+    if bitwise:
+        for u, v in zip(a, b):
+            assert torch.equal(u, v)
+        return
+    assert torch.equal(a[0], b[0])
+    for u, v in zip(a[1:], b[1:]):
+        scale = float(v.abs().max()) if v.numel() else 0.0
+        if v.numel():
+            assert float((u - v).abs().max()) <= 1e-5 * scale + 1e-30
+
+
 def _into(inp, dev, **kw):
     N, D = inp["X"].shape
     K = inp["mu"].shape[0]
@@ -130,10 +147,11 @@ def _into(inp, dev, **kw):
     return out
 
 
-@pytest.mark.parametrize("recompute", [False, True])
+@pytest.mark.parametrize("stored", [False, True])
 @pytest.mark.parametrize("case", ["clustered_d128", "clustered_d64_ragged", "plain_d32", "clustered_d256"])
-def test_zero_step_skip_is_bitwise_dense(case, recompute, gpu_device):
-    """Skipping all-zero responsibility steps changes no bit of any output."""
+def test_zero_step_skip_is_bitwise_dense(case, stored, gpu_device):
+    """Skipping all-zero responsibility steps (and, on the default plan, the rows whose
+    need bit is clear) changes no bit of any output."""
     if case == "clustered_d128":
         inp = data.iso_clustered(12000, 1024, 128, seed=1)   # mostly zero steps
     elif case == "clustered_d64_ragged":
@@ -142,11 +160,11 @@ def test_zero_step_skip_is_bitwise_dense(case, recompute, gpu_device):
         inp = data.iso_clustered(6000, 512, 256, seed=6)   # split-dimension pass 2
     else:
         inp = data.iso_plain(10000, 64, 32, seed=0)          # no zero steps
-    a = _into(inp, gpu_device, recompute=recompute)
-    b = _into(inp, gpu_device, dense=True, recompute=recompute)
-    for u, v in zip(a, b):
-        assert torch.equal(u, v)
+    a = _into(inp, gpu_device, store_log_joint=stored)
+    b = _into(inp, gpu_device, dense=True, store_log_joint=stored)
+    assert_dense_agrees(a, b, bitwise=stored)
     assert_close_stats(a, oracle(inp), case)
+    assert_close_stats(b, oracle(inp), case + " dense")
 
 
 # Clustered shapes whose need masks are sparse (K >= 512): the accumulation pass
@@ -155,14 +173,15 @@ def test_zero_step_skip_is_bitwise_dense(case, recompute, gpu_device):
 SPARSE_SHAPES = [(20000, 1024, 64), (20000, 512, 96), (40000, 512, 128), (30001, 1024, 128)]
 
 
+@pytest.mark.parametrize("stored", [False, True])
 @pytest.mark.parametrize("N,K,D", SPARSE_SHAPES)
-def test_sparse_accumulation_is_bitwise_dense(N, K, D, gpu_device):
-    """Sparse accumulation (default) against the dense one (FGMM_FLAG_DENSE) and the oracle."""
+def test_sparse_accumulation_is_bitwise_dense(N, K, D, stored, gpu_device):
+    """Sparse accumulation against the dense one (FGMM_FLAG_DENSE) and the oracle, on the
+    default plan (gathered rows) and the stored log-joint."""
     inp = data.iso_clustered(N, K, D, seed=N % 101)
-    a = _into(inp, gpu_device)
-    b = _into(inp, gpu_device, dense=True)
-    for u, v in zip(a, b):
-        assert torch.equal(u, v)
+    a = _into(inp, gpu_device, store_log_joint=stored)
+    b = _into(inp, gpu_device, dense=True, store_log_joint=stored)
+    assert_dense_agrees(a, b, bitwise=stored)
     assert_close_stats(a, oracle(inp), f"sparse N={N} K={K} D={D}")
 
 
@@ -178,11 +197,11 @@ def test_stored_and_recomputed_log_joint(N, K, D, gpu_device):
     from flash_gmm import _lib
     L = _lib.lib()
     # The two plans differ (stored tiles, pass-2 work split), so these shapes take the stored path.
-    assert L.fgmm_iso_workspace_bytes(N, K, D) != L.fgmm_iso_workspace_bytes_ex(N, K, D, _lib.FLAG_RECOMPUTE)
+    assert L.fgmm_iso_workspace_bytes(N, K, D) != L.fgmm_iso_workspace_bytes_ex(N, K, D, _lib.FLAG_STORE_LOGJOINT)
     inp = data.iso_clustered(N, K, D, seed=N + 3 * K + D)
     ref = oracle(inp)
-    stored = _into(inp, gpu_device)
-    recomputed = _into(inp, gpu_device, recompute=True)
+    stored = _into(inp, gpu_device, store_log_joint=True)
+    recomputed = _into(inp, gpu_device)
     assert torch.equal(stored[0], recomputed[0])          # pass 1 is the same kernel math
     assert_close_stats(stored, ref, f"stored N={N} K={K} D={D}")
     assert_close_stats(recomputed, ref, f"recomputed N={N} K={K} D={D}")
@@ -192,29 +211,29 @@ def test_stored_log_joint_zero_weight_components(gpu_device):
     """log_pi = -inf components on the stored path: r = 0 and finite sig_acc."""
     inp = data.iso_clustered(3000, 200, 48, seed=15)
     inp["log_pi"][[0, 7, 199]] = -math.inf
-    got = _into(inp, gpu_device)
+    got = _into(inp, gpu_device, store_log_joint=True)
     assert_close_stats(got, oracle(inp), "stored lpi=-inf")
     assert float(got[1][0]) == 0.0 and float(got[3][199]) == 0.0
     assert torch.isfinite(got[3]).all()
 
 
-@pytest.mark.parametrize("recompute", [False, True])
-def test_phase_split_equals_one_call(recompute, gpu_device):
+@pytest.mark.parametrize("stored", [False, True])
+def test_phase_split_equals_one_call(stored, gpu_device):
     """PHASE1 then PHASE2 on one workspace gives the single call's outputs bitwise."""
     inp = data.iso_clustered(5000, 256, 96, seed=16)
     dev = gpu_device
-    ref = _into(inp, dev, recompute=recompute)
+    ref = _into(inp, dev, store_log_joint=stored)
     N, D = inp["X"].shape
     K = inp["mu"].shape[0]
     from flash_gmm import _lib
     L = _lib.lib()
-    flags = _lib.FLAG_RECOMPUTE if recompute else 0
+    flags = _lib.FLAG_STORE_LOGJOINT if stored else 0
     ws = torch.empty(L.fgmm_iso_workspace_bytes_ex(N, K, D, flags), dtype=torch.uint8, device=dev)
     out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
            torch.empty(K, device=dev)]
     args = [inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
-    iso_estep_into(*args, *out, workspace=ws, phase=1, recompute=recompute)
-    iso_estep_into(*args, None, *out[1:], workspace=ws, phase=2, recompute=recompute)
+    iso_estep_into(*args, *out, workspace=ws, phase=1, store_log_joint=stored)
+    iso_estep_into(*args, None, *out[1:], workspace=ws, phase=2, store_log_joint=stored)
     torch.cuda.synchronize()
     for u, v in zip(out, ref):
         assert torch.equal(u, v)
@@ -266,8 +285,7 @@ def test_small_k_mid_size(N, K, D, gpu_device):
     assert_close_stats(got, oracle(inp), f"small K N={N} K={K} D={D}")
     dev = gpu_device
     dense = _into(inp, dev, dense=True)
-    for u, v in zip(got, dense):
-        assert torch.equal(u, v)
+    assert_dense_agrees(got, dense, bitwise=False)
 
 
 def test_wide_shape_mid_size(gpu_device):
@@ -276,11 +294,50 @@ def test_wide_shape_mid_size(gpu_device):
     assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "K512 D256 N16384")
 
 
-def test_headline_shape_full_size_against_oracle(gpu_device):
-    """N=1M, K=1024, D=128 (the benchmark workload): size-independent properties, and
-    all four outputs against the float64 oracle over every row (about 15 s of CPU)."""
+def test_phase2_requires_the_phase1_workspace(gpu_device):
+    inp = data.iso_clustered(300, 64, 32, seed=17)
     dev = gpu_device
-    inp = data.iso_clustered(1_000_000, 1024, 128, seed=1, device=dev)
+    args = [inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
+    out = [torch.empty(64, device=dev), torch.empty(64, 32, device=dev), torch.empty(64, device=dev)]
+    with pytest.raises(FlashGMMError):
+        iso_estep_into(*args, None, *out, phase=2)
+    with pytest.raises(FlashGMMError):
+        iso_estep_into(*args, None, *out, phase=2, workspace=torch.empty(16, dtype=torch.uint8, device=dev))
+
+
+def test_stored_plan_falls_back_when_its_workspace_cannot_be_allocated(gpu_device, monkeypatch):
+    """store_log_joint=True whose O(N*K) workspace fails to allocate runs the default plan."""
+    from flash_gmm import _lib, estep
+    inp = data.iso_clustered(4000, 256, 64, seed=18)
+    dev = gpu_device
+    ref = _into(inp, dev)
+    L = _lib.lib()
+    lean = L.fgmm_iso_workspace_bytes(4000, 256, 64)
+    real = estep._empty_workspace
+
+    def small_only(nbytes, device):
+        if nbytes > lean:
+            raise torch.cuda.OutOfMemoryError("simulated")
+        return real(nbytes, device)
+
+    monkeypatch.setattr(estep, "_empty_workspace", small_only)
+    got = _into(inp, dev, store_log_joint=True)
+    for u, v in zip(got, ref):
+        assert torch.equal(u, v)
+
+
+@pytest.mark.parametrize("N,K,D", [(3000, 2100, 128), (2000, 6200, 64), (1500, 9000, 32)])
+def test_need_masks_from_the_running_max(N, K, D, gpu_device):
+    """More component blocks than pass 1 keeps maxima for in LDS: the need masks come
+    from the running-max bound instead; results against the dense pass and the oracle."""
+    inp = data.iso_clustered(N, K, D, seed=K % 89)
+    a = _into(inp, gpu_device)
+    b = _into(inp, gpu_device, dense=True)
+    assert_dense_agrees(a, b, bitwise=False)
+    assert_close_stats(a, oracle(inp), f"running-max masks N={N} K={K} D={D}")
+
+
+def _full_size_against_oracle(inp, dev, what):
     got = flash_gmm_estep(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
     torch.cuda.synchronize()
     logZ, Nk, mu_acc, sig = got
@@ -289,10 +346,46 @@ def test_headline_shape_full_size_against_oracle(gpu_device):
     xs = inp["X"].double().sum(0)
     torch.testing.assert_close(mu_acc.double().sum(0), xs, rtol=0, atol=1e-5 * float(mu_acc.abs().sum(0).max()))
     assert torch.all(sig >= 0)
-    # The sparse accumulation this data takes writes what the dense one writes.
+    print(f"{what}: full-size oracle (float64, CPU)", flush=True)
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    ref = O.estep_iso(*[inp[k].cpu() for k in ("X", "mu", "log_sigma_sq", "log_pi")])
+    print(f"{what}: max |logZ - oracle| = {(logZ.cpu().double() - ref[0]).abs().max().item():.3e}", flush=True)
+    assert_close_stats(got, ref, what)
+    return got
+
+
+def test_reference_smoke_workload_full_size(gpu_device):
+    """The reference's own benchmark workload (flash_gmm.py:228-234: X ~ N(0, I),
+    mu ~ N(0, I), lss = 0, uniform log pi; N=1M, K=1024, D=128), where nearly every
+    responsibility is nonzero, against the float64 oracle over every row."""
+    inp = data.reference_smoke(1_000_000, 1024, 128, seed=0, device=gpu_device)
+    _full_size_against_oracle(inp, gpu_device, "reference smoke N=1M")
+
+
+def test_headline_shape_second_seed(gpu_device):
+    """The headline shape on another seed: the logZ margin is not one seed's luck."""
+    inp = data.iso_clustered(1_000_000, 1024, 128, seed=2, device=gpu_device)
+    _full_size_against_oracle(inp, gpu_device, "K1024 D128 N=1M seed 2")
+
+
+def test_headline_shape_full_size_against_oracle(gpu_device):
+    """N=1M, K=1024, D=128 (the benchmark workload): size-independent properties, and
+    all four outputs against the float64 oracle over every row (about 15 s of CPU)."""
+    dev = gpu_device
+    inp = data.iso_clustered(1_000_000, 1024, 128, seed=1, device=dev)
+    stored = _into(inp, dev, store_log_joint=True)
+    got = flash_gmm_estep(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+    torch.cuda.synchronize()
+    logZ, Nk, mu_acc, sig = got
+    N = inp["X"].shape[0]
+    assert abs(Nk.double().sum().item() - N) <= 1e-5 * N
+    xs = inp["X"].double().sum(0)
+    torch.testing.assert_close(mu_acc.double().sum(0), xs, rtol=0, atol=1e-5 * float(mu_acc.abs().sum(0).max()))
+    assert torch.all(sig >= 0)
+    # The gathered accumulation agrees with the dense one, and pass 1 with the stored plan's.
     dense = _into(inp, dev, dense=True)
-    for u, v in zip(got, dense):
-        assert torch.equal(u, v)
+    assert_dense_agrees(got, dense, bitwise=False)
+    assert torch.equal(stored[0], got[0])
     print("full-size oracle (float64, CPU)", flush=True)
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     ref = O.estep_iso(*[inp[k].cpu() for k in ("X", "mu", "log_sigma_sq", "log_pi")])
