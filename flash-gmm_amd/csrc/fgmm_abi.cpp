@@ -11,6 +11,7 @@ extern "C" const char* fgmm_strerror(int status) {
     case FGMM_ERR_WORKSPACE: return "workspace smaller than the *_workspace_bytes() query";
     case FGMM_ERR_HIP: return "HIP runtime error or kernel launch failure";
     case FGMM_ERR_SOURCE: return "the host row source returned an error";
+    case FGMM_ERR_SCRATCH: return "the call needs more workspace than the no-allocation entry point's scratch";
     default: return "unknown status";
   }
 }

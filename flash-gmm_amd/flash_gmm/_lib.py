@@ -21,6 +21,7 @@ FGMM_ERR_UNSUPPORTED = -2
 FGMM_ERR_WORKSPACE = -3
 FGMM_ERR_HIP = -4
 FGMM_ERR_SOURCE = -5
+FGMM_ERR_SCRATCH = -6
 
 FLAG_ACCUMULATE = 1 << 0
 FLAG_NO_LOGZ = 1 << 1
@@ -79,6 +80,9 @@ def _declare(lib):
         "fgmm_full_estep_f32": (ctypes.c_int, [
             _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p,
             _p, _p, _p, _p, _p, _sz, _u32, _p]),
+        "fgmm_iso_estep_f32_noalloc": (ctypes.c_int, [
+            _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p,
+            _p, _p, _p, _p, _u32, _p]),
         # The EM entry points (fgmm_iso_mstep_f32, fgmm_stream_em_iso,
         # fgmm_synth_iso_source) are declared in em.py next to their structs.
     }

@@ -11,7 +11,8 @@
  * the matching *_workspace_bytes() query.  The work split (and so the workspace
  * size) follows the compute-unit count of the current device: query with the
  * device current that the call will run on.  The library keeps no allocations
- * between calls.  Calls are re-entrant given distinct outputs and workspaces.
+ * between calls, except the fixed scratch array of fgmm_iso_estep_f32_noalloc.
+ * Calls are re-entrant given distinct outputs and workspaces.
  *
  * Layout conventions (row-major, float32):
  *   X      N x D, row stride ldx (elements), unit column stride.  Requires
@@ -37,6 +38,7 @@ enum fgmm_status {
     FGMM_ERR_WORKSPACE = -3,   /* workspace smaller than *_workspace_bytes() */
     FGMM_ERR_HIP = -4,         /* a HIP runtime call or kernel launch failed */
     FGMM_ERR_SOURCE = -5,      /* a host row source returned an error */
+    FGMM_ERR_SCRATCH = -6,     /* the call needs more than the no-allocation entry point's scratch */
 };
 
 /* Flags (bitwise OR). */
@@ -60,11 +62,13 @@ enum fgmm_flags {
     FGMM_FLAG_PHASE1 = 1u << 3,
     FGMM_FLAG_PHASE2 = 1u << 4,
     /* The accumulation pass skips every matrix-core step whose responsibilities
-     * (two rows x 32 components) are all exactly zero, since such a step adds
-     * nothing; on the isotropic stored log-joint it does not even read the rows
-     * whose responsibilities pass 1 proved zero.  The results are bitwise the same
-     * either way.  DENSE runs every step and, in pass 1, stores every row (for
-     * timing the dense contraction). */
+     * are all exactly zero, since such a step adds nothing, and the rows whose
+     * responsibilities pass 1 proved zero for a component block.  DENSE runs
+     * every step and every row (for timing the dense contraction).  With the
+     * stored log-joint the results are bitwise the same either way; on the
+     * default plan, whose pass 2 gathers the needed rows into tiles, the
+     * statistics add the same nonzero terms in other groupings (last-bit
+     * differences; logZ is the same). */
     FGMM_FLAG_DENSE = 1u << 5,
     /* The default plan: the workspace is O(N + K*D) (plus one need bit per
      * row and 32-component block) and pass 2 recomputes the D-contraction for
@@ -115,8 +119,8 @@ const char *fgmm_strerror(int status);
 /* log_sigma_sq and log_pi are contiguous (K).                                */
 /* ------------------------------------------------------------------------ */
 size_t fgmm_iso_workspace_bytes(int64_t N, int64_t K, int64_t D);
-/* Workspace for a call made with `flags` (only FGMM_FLAG_RECOMPUTE matters);
- * with flags = 0 it equals fgmm_iso_workspace_bytes(). */
+/* Workspace for a call made with `flags` (FGMM_FLAG_STORE_LOGJOINT, RECOMPUTE
+ * and BF16 matter); with flags = 0 it equals fgmm_iso_workspace_bytes(). */
 size_t fgmm_iso_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags);
 
 int fgmm_iso_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
@@ -125,6 +129,29 @@ int fgmm_iso_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
                        float *logZ, float *Nk, float *mu_acc, float *sig_acc,
                        void *workspace, size_t workspace_bytes,
                        unsigned flags, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Isotropic E-step that allocates nothing.  No counterpart in the reference:  */
+/* for callers that cannot allocate device memory (code under HIP graph        */
+/* capture, tight serving loops, harnesses that forbid hipMalloc).  The same   */
+/* computation and results as fgmm_iso_estep_f32 with the same flags, with its */
+/* workspace in a fixed device-resident scratch array of                       */
+/* FGMM_NOALLOC_SCRATCH_BYTES per GPU, held from the library's first such call */
+/* on that GPU until the process ends.  Calls whose workspace                  */
+/* (fgmm_iso_workspace_bytes_ex with the same flags) exceeds it return         */
+/* FGMM_ERR_SCRATCH: about 1.4M rows at K=1024, D=128 (N=1M fits).             */
+/* FGMM_FLAG_STORE_LOGJOINT is rejected (FGMM_ERR_INVALID_ARG).  Every call on */
+/* a GPU uses that GPU's one array: calls that overlap on one GPU (different   */
+/* streams or host threads without ordering) race, and a PHASE2 call reads     */
+/* what the last PHASE1 call on that GPU left.                                 */
+/* ------------------------------------------------------------------------ */
+#define FGMM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+int fgmm_iso_estep_f32_noalloc(const float *X, int64_t ldx, int64_t N, int64_t D,
+                               const float *mu, int64_t ldmu, int64_t K,
+                               const float *log_sigma_sq, const float *log_pi,
+                               float *logZ, float *Nk, float *mu_acc, float *sig_acc,
+                               unsigned flags, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* Diagonal-covariance E-step.                                               */
