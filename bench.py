@@ -1,18 +1,25 @@
-"""E-step throughput on one MI355X: samples/s and fraction of the fp32 MFMA peak.
+"""E-step throughput on one MI355X: samples/s and the dominant kernel's roofline fraction.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 20] [--no-cpu-baseline]
-                    [--workload iso_n1m_k1024_d128|diag_n1m_k1024_d96|full_n250k_k256_d64]
+                    [--workload iso_n1m_k1024_d128|iso_ref_n1m_k1024_d128|diag_n1m_k1024_d96|
+                                full_n250k_k256_d64|stream_em_n1b_k1024_d128|...]
+                    [--precision fp32|bf16] [--store-log-joint] [--no-extra-runs]
+    python bench.py --sweep iso:1000000:1024:32,64,96,128,192,256   (one JSON line per D)
+    python bench.py --reduce-compare                                (tree vs atomic finish)
 
 Default workload (the headline): the isotropic E-step at N=1,000,000, K=1024,
 D=128, float32, on the clustered synthetic data of flash_gmm.data.iso_clustered
 (seed 1), generated on the GPU so X is resident in HBM before timing.  One step
-= one full E-step (constant prologue + log-normaliser pass + accumulation pass +
-reduction) through the C ABI on torch's current stream.  Prints one JSON line.
-The diagonal and full-covariance workloads are measured the same way.
+= one full E-step on the default O(N + K*D) plan (constant prologue +
+log-normaliser pass + accumulation pass + reduction) through the C ABI on
+torch's current stream.  Prints one JSON line.  The other workloads are measured
+the same way; the stored log-joint plan (FGMM_FLAG_STORE_LOGJOINT) and the dense
+accumulation are timed after the headline and reported as extra keys.
 """
 
 import argparse
 import json
+import math
 import os
 import platform
 import sys
@@ -28,6 +35,25 @@ PEAK_FP32_MFMA_TFLOPS = 157.3       # MI355X dense fp32 matrix, published
 PEAK_BF16_MFMA_TFLOPS = 2500.0      # MI355X dense bf16 matrix, published
 PEAK_HBM_GBS = 8000.0
 A100_SAMPLES_PER_S = 1_000_000 / 0.152   # README.md:116 (A100 80GB, N=1M, 152 ms)
+LJ_NEED_GAP = 160.0                 # log2 units: a (row, block) below this under logZ2 is skipped
+
+WORKLOADS = {
+    # name: (N, K, D)
+    "iso_n1m_k1024_d128": (1_000_000, 1024, 128),
+    "iso_ref_n1m_k1024_d128": (1_000_000, 1024, 128),
+    "diag_n1m_k1024_d96": (1_000_000, 1024, 96),
+    "full_n250k_k256_d64": (250_000, 256, 64),
+    "diag_n1m_k256_d256": (1_000_000, 256, 256),
+    "full_n100k_k64_d128": (100_000, 64, 128),
+}
+
+# HBM bytes per launch of the dominant kernel: rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE (separate runs) on this bench command, scaled by what the counters read
+# for a 512 MiB device copy (bench.py --copy-calibration 512: FETCH_SIZE x2.0,
+# WRITE_SIZE x1.0); the counter values and commands are in profiles/.
+TRAFFIC_BYTES = {
+    # (workload, plan, precision): {kernel: bytes}
+}
 
 
 def log(msg):
@@ -44,12 +70,101 @@ def cpu_model():
     return platform.processor()
 
 
-def cpu_baseline(inp, kind, K, D, min_s=10.0, max_s=30.0, rows=16384):
-    """The oracle's float32 restatement on the host cores, on a bounded sample."""
+def rup(a, b):
+    return -(-a // b) * b
+
+
+def padded_dim(kind, D):
+    """D as the kernels pad it: to 32 up to 128, then to 64 (iso, diag); to 32 (full)."""
+    if kind == "full":
+        return rup(D, 32)
+    return rup(D, 32) if D <= 128 else rup(D, 64)
+
+
+def algorithmic(kind, N, K, D):
+    """Per-step algorithmic flops (total, pass 1, pass 2) and pass-1 bytes.
+
+    iso:  4NKD  = x.mu^T (2NKD, pass 1) + r^T X (2NKD, pass 2)
+    diag: 8NKD  = [x^2, x].[-w, 2v]^T (4NKD, pass 1) + r^T [X, X^2] (4NKD, pass 2)
+    full: 4NKD^2 + 2NKD (dense-equivalent) = whitening (2NKD^2, pass 1)
+          + sum r x x^T (2NKD^2) + r^T X (2NKD), pass 2
+    Bytes: X read once + logZ written + the O(K*D) parameters (the per-row state and
+    need bits the passes exchange are O(N) and O(N K / 32) bits, listed apart).
+    """
+    if kind == "iso":
+        f = (4.0 * N * K * D, 2.0 * N * K * D, 2.0 * N * K * D)
+        par = K * (D + 2) * 4
+    elif kind == "diag":
+        f = (8.0 * N * K * D, 4.0 * N * K * D, 4.0 * N * K * D)
+        par = K * (2 * D + 1) * 4
+    else:
+        f = (4.0 * N * K * D * D + 2.0 * N * K * D, 2.0 * N * K * D * D, 2.0 * N * K * D * D + 2.0 * N * K * D)
+        par = K * (D * D + D + 1) * 4
+    return f, 4.0 * N * D + 4.0 * N + par
+
+
+def pass1_executed(kind, N, K, D, precision, stored):
+    """Matrix-core flops pass 1 executes per launch, and the unit that runs them.
+
+    Split-bf16 ("bf16x6") passes form each fp32 product from 7 bf16 matrix steps
+    (6 products of the three-way splits + 1 centring offset) per chunk, each step
+    32 bf16 flop per (row, output):
+      iso D <= 128:   16-dimension chunks, 1 output:   14 DP bf16 flop per (row, component)
+      diag D <= 128:  8-dimension chunks of [x^2, x]:  28 DP
+      full (stored):  16-dimension chunks, DP outputs: 14 DP^2
+    Wider iso / diag and the recomputing full pass 1 run fp32 32x32x2 steps over the
+    padded width (2 DP, 4 DP, 2 DP^2).  The bf16 contract runs one bf16 step per
+    product (2 DP, 4 DP, 2 DP^2 bf16 flop).
+    """
+    DP = padded_dim(kind, D)
+    if precision == "bf16":
+        per = {"iso": 2 * DP, "diag": 4 * DP, "full": 2 * DP * DP}[kind]
+        return per * float(N) * K, "bf16", PEAK_BF16_MFMA_TFLOPS
+    if kind == "iso" and D <= 128:
+        return 14.0 * DP * N * K, "bf16", PEAK_BF16_MFMA_TFLOPS
+    if kind == "diag" and D <= 128:
+        return 28.0 * DP * N * K, "bf16", PEAK_BF16_MFMA_TFLOPS
+    if kind == "full" and stored:
+        return 14.0 * DP * DP * N * K, "bf16", PEAK_BF16_MFMA_TFLOPS
+    per = {"iso": 2 * DP, "diag": 4 * DP, "full": 2 * DP * DP}[kind]
+    return per * float(N) * K, "fp32", PEAK_FP32_MFMA_TFLOPS
+
+
+def iso_need_pairs(inp, logZ, chunk=65536):
+    """Needed (row, 32-component block) pairs, from the inputs and the kernel's logZ:
+    a pair is needed when its largest log-joint is within LJ_NEED_GAP (log2 units) of
+    logZ2, the kernels' test.  float32 here, so pairs within ~1 unit of the edge may
+    be miscounted: an estimate of the gathering pass's work."""
+    import torch
+    X, mu, lss, lpi = (inp[k] for k in ("X", "mu", "log_sigma_sq", "log_pi"))
+    N, D = X.shape
+    K = mu.shape[0]
+    KB = -(-K // 32)
+    b = 0.5 * torch.exp(-lss.double()) * 1.4426950408889634
+    C = (lpi.double() - 0.5 * D * (1.8378770664093453 + lss.double())) * 1.4426950408889634
+    musq = (mu.double() ** 2).sum(1)
+    C0, b, musq = C.float(), b.float(), musq.float()
+    total = 0
+    for n0 in range(0, N, chunk):
+        x = X[n0:n0 + chunk]
+        ll2 = C0[None, :] - b[None, :] * ((x * x).sum(1)[:, None] - 2.0 * (x @ mu.T) + musq[None, :])
+        pad = KB * 32 - K
+        if pad:
+            ll2 = torch.nn.functional.pad(ll2, (0, pad), value=-math.inf)
+        bm = ll2.view(ll2.shape[0], KB, 32).amax(dim=2)
+        lz2 = logZ[n0:n0 + chunk].float() * 1.4426950408889634
+        total += int((bm - lz2[:, None] >= -LJ_NEED_GAP).sum())
+    return total
+
+
+def cpu_baseline(inp, kind, K, D, gpu_logZ, min_s=10.0, max_s=30.0, rows=16384):
+    """The oracle's float32 restatement on every host core this process may use, on a
+    bounded sample of the workload's rows; beside it, the float64 oracle on the same
+    rows checks the CPU restatement and the GPU's logZ."""
     import torch
     from oracle import gmm_oracle as O
 
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     if kind == "full":
         rows = 4096
@@ -61,90 +176,292 @@ def cpu_baseline(inp, kind, K, D, min_s=10.0, max_s=30.0, rows=16384):
     done, t0 = 0, time.perf_counter()
     reps = 0
     while True:
-        fn(X, mu, p3, lpi, dtype=torch.float32, chunk=rows)
+        out32 = fn(X, mu, p3, lpi, dtype=torch.float32, chunk=rows)
         done += rows
         reps += 1
         el = time.perf_counter() - t0
         if el >= min_s or el >= max_s:
             break
+    ref = fn(X, mu, p3, lpi, dtype=torch.float64)
+    lz64 = ref[0]
     return {
         "value": done / el, "unit": "samples/s", "cores": threads, "kind": "port",
-        "sample": f"{rows} rows of the same workload (K={K}, D={D}) x {reps} repetitions, "
-                  f"{el:.1f} s, float32 oracle (torch CPU) on {cpu_model()}",
+        "sample": f"the first {rows} rows of the same workload (K={K}, D={D}) x {reps} passes, "
+                  f"{el:.1f} s, float32 oracle (torch CPU) on {threads} threads of {cpu_model()}",
+        "max_abs_logZ_err_vs_fp64": {
+            "cpu_fp32": float((out32[0].double() - lz64).abs().max()),
+            "gpu": float((gpu_logZ[:rows].double().cpu() - lz64).abs().max()),
+            "rows": rows,
+        },
     }
 
 
-# HBM bytes per launch of each pass's main kernel with the stored log-joint (the
-# default): rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (separate runs) on this
-# bench command, scaled by what the counters read for a 512 MiB device copy (x2.0
-# for FETCH_SIZE, x1.0 for WRITE_SIZE); the counter values and commands are in
-# profiles/<kind>_estep_<shape>.md.  Not reported with --recompute.
-TRAFFIC_BYTES = {
-    "iso_n1m_k1024_d128": {"phase1": 3_140_715_520, "phase2": 799_602_688},
-    "diag_n1m_k1024_d96": {"phase1": 4_374_549_504, "phase2": 656_783_360},
-    "full_n250k_k256_d64": {"phase1": 836_218_880, "phase2": 414_390_272},
-}
+def make_runner(kind, inp, N, K, D, dev, precision="fp32", store=False, atomic=False):
+    """Return (step(phase, dense), workspace bytes) for one plan."""
+    import torch
+    from flash_gmm import _lib, diag_estep_into, full_estep_into, iso_estep_into
 
-WORKLOADS = {
-    # name: (N, K, D)
-    "iso_n1m_k1024_d128": (1_000_000, 1024, 128),
-    "diag_n1m_k1024_d96": (1_000_000, 1024, 96),
-    "full_n250k_k256_d64": (250_000, 256, 64),
-    "diag_n1m_k256_d256": (1_000_000, 256, 256),
-    "full_n100k_k64_d128": (100_000, 64, 128),
-}
-
-
-def algorithmic_flop(kind, N, K, D):
-    """Per-step algorithmic flops and the (phase 1, phase 2) split.
-
-    iso:  4NKD  = x.mu^T (2NKD, phase 1) + r^T X (2NKD, phase 2)
-    diag: 8NKD  = [x^2, x].[-w, 2v]^T (4NKD, phase 1) + r^T [X, X^2] (4NKD, phase 2)
-    full: 4NKD^2 + 2NKD = X.L_k whitening (2NKD^2, phase 1) + sum r x x^T (2NKD^2)
-          + r^T X (2NKD) in phase 2 (dense-equivalent count)
-    """
+    L = _lib.lib()
+    logZ = torch.empty(N, device=dev)
+    Nk = torch.empty(K, device=dev)
+    mu_acc = torch.empty(K, D, device=dev)
+    flags = (_lib.FLAG_STORE_LOGJOINT if store else 0) | (_lib.FLAG_BF16 if precision == "bf16" else 0)
+    ws = torch.empty(max(1, int(getattr(L, f"fgmm_{kind}_workspace_bytes_ex")(N, K, D, flags))),
+                     dtype=torch.uint8, device=dev)
     if kind == "iso":
-        return 4.0 * N * K * D, 2.0 * N * K * D, 2.0 * N * K * D
-    if kind == "diag":
-        return 8.0 * N * K * D, 4.0 * N * K * D, 4.0 * N * K * D
-    return 4.0 * N * K * D * D + 2.0 * N * K * D, 2.0 * N * K * D * D, 2.0 * N * K * D * D + 2.0 * N * K * D
-
-
-def algorithmic_bytes(kind, N, K, D, lj):
-    """Per-step HBM bytes each phase must move (phase 1, phase 2).
-
-    Phase 1 reads X and writes logZ, the per-row state (iso: ||x||^2 and logZ2 in
-    fp64; diag, full: logZ2) and, when pass 2 reads it, the fp32 log-joint.
-    Phase 2 reads X, the per-row state and the log-joint.  O(K*D) operands and the
-    slab partials are left out (under 1% here).
-
-    The isotropic log-joint, and the diagonal one up to D = 128, are sparse: phase 1
-    writes it whole at most (rows the running max already rules out are left
-    unwritten) with per-row block maxima and need masks per tile (iso: one maximum
-    per row and one mask word; diag: one per half block, 64 maxima and two words),
-    and phase 2 reads X, the row state and the masks, plus only the log-joint rows
-    whose need bit is set, a data-dependent share that is not counted here (the
-    measured traffic includes it).
-    """
-    KB = -(-K // 32)
-    if kind == "full":
-        lj_bytes = (-(-N // 128) * 4) * (-(-K // 4) * 4) * 32 * 4
+        args = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+        sig = torch.empty(K, device=dev)
+        call = lambda ph, dense: iso_estep_into(*args, logZ, Nk, mu_acc, sig, workspace=ws, phase=ph,
+                                                atomic_reduce=atomic, dense=dense, store_log_joint=store,
+                                                precision=precision)
+    elif kind == "diag":
+        args = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+        sig = torch.empty(K, D, device=dev)
+        call = lambda ph, dense: diag_estep_into(*args, logZ, Nk, mu_acc, sig, workspace=ws, phase=ph,
+                                                 atomic_reduce=atomic, dense=dense, store_log_joint=store,
+                                                 precision=precision)
     else:
-        lj_bytes = (-(-N // 128) * 4) * KB * 4096
-    lj_bytes = lj_bytes if lj else 0
-    row = 16 if kind == "iso" else 8
-    x = 4.0 * N * D
-    if lj and (kind == "iso" or (kind == "diag" and D <= 128)):
-        per_tile = (128, 4) if kind == "iso" else (256, 8)   # maxima, mask words
-        tiles = lj_bytes / 4096
-        return (x + 4.0 * N + row * N + lj_bytes + tiles * sum(per_tile),
-                x + row * N + tiles * per_tile[1])
-    return x + 4.0 * N + row * N + lj_bytes, x + row * N + lj_bytes
+        args = (inp["X"], inp["mu"], inp["prec_chol"], inp["log_pi"])
+        sig = torch.empty(K, D, D, device=dev)
+        call = lambda ph, dense: full_estep_into(*args, logZ, Nk, mu_acc, sig, workspace=ws, phase=ph,
+                                                 atomic_reduce=atomic, dense=dense, store_log_joint=store,
+                                                 precision=precision)
+    return call, ws.numel(), (logZ, Nk, mu_acc, sig)
+
+
+def time_steps(call, steps, warmup, stream, dense=False):
+    """W untimed steps, then K timed ones between two synchronisations; each step is
+    PHASE1 then PHASE2 with HIP events on the launch stream around each phase."""
+    import torch
+    for _ in range(warmup):
+        call(1, dense)
+        call(2, dense)
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(steps):
+        evs[i][0].record(stream)
+        call(1, dense)
+        evs[i][1].record(stream)
+        call(2, dense)
+        evs[i][2].record(stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    p1 = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
+    p2 = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
+    return ms, p1, p2
+
+
+KERNELS = {
+    # (kind, plan) -> (pass-1 kernel, pass-2 kernel)
+    ("iso", "default"): ("iso_lse (need masks)", "iso_accum_gather"),
+    ("iso", "default_wide"): ("iso_lse_split", "iso_accum_split"),
+    ("iso", "stored"): ("iso_lse (stores the log-joint)", "iso_accum_sparse / iso_accum_lj"),
+    ("diag", "default"): ("diag_lse_x6 (need masks)", "diag_accum_gather"),
+    ("diag", "default_wide"): ("diag_lse_split", "diag_accum_split"),
+    ("diag", "stored"): ("diag_lse_x6 (stores the log-joint)", "diag_accum_sparse / diag_accum_lj2"),
+    ("full", "default"): ("full_lse", "full_accum"),
+    ("full", "stored"): ("full_lse_x6 (stores the log-joint)", "full_accum"),
+}
+
+
+def kernel_names(kind, D, precision, stored):
+    if precision == "bf16":
+        return f"{kind}_bf16_lse", f"{kind}_bf16_accum"
+    plan = "stored" if stored else ("default" if (kind == "full" or D <= 128) else "default_wide")
+    return KERNELS[(kind, plan)]
+
+
+def measure(args, workload, precision, store, dev, inp=None):
+    """One plan of one workload: the headline-style record (without the CPU leg)."""
+    import torch
+    from flash_gmm import data
+
+    N, K, D = WORKLOADS[workload]
+    kind = workload.split("_")[0]
+    if inp is None:
+        inp = data.make(workload, device=dev)
+    call, ws_bytes, outs = make_runner(kind, inp, N, K, D, dev, precision, store)
+    stream = torch.cuda.current_stream(dev)
+    ms, p1, p2 = time_steps(call, args.steps, args.warmup, stream)
+    return inp, outs, dict(ms=ms, p1=p1, p2=p2, ws=ws_bytes, call=call)
+
+
+def main_workload(args):
+    import torch
+
+    dev = torch.device("cuda:0")
+    workload = args.workload
+    N, K, D = WORKLOADS[workload]
+    kind = workload.split("_")[0]
+    bf16 = args.precision == "bf16"
+    log(f"generating workload {workload} on {torch.cuda.get_device_name(dev)}")
+    inp, outs, r = measure(args, workload, args.precision, args.store_log_joint, dev)
+    ms, p1, p2 = r["ms"], r["p1"], r["p2"]
+    log(f"timed {args.steps} steps: {ms:.3f} ms/step (phase1 {p1:.3f} ms, phase2 {p2:.3f} ms)")
+    logZ = outs[0].clone()
+    stream = torch.cuda.current_stream(dev)
+
+    (flop, f1, f2), alg_bytes = algorithmic(kind, N, K, D)
+    k1, k2 = kernel_names(kind, D, args.precision, args.store_log_joint)
+    ex1, unit1, peak1 = pass1_executed(kind, N, K, D, args.precision, args.store_log_joint)
+    phases = {
+        "phase1": {"kernel": k1 + " + prologue", "ms": p1, "fp32_algorithmic_flop": f1,
+                   "fp32_equivalent_tflops": f1 / (p1 * 1e-3) / 1e12,
+                   "executed_matrix_flop": ex1, "executed_unit": unit1,
+                   "executed_tflops": ex1 / (p1 * 1e-3) / 1e12},
+        "phase2": {"kernel": k2 + " + slab reduction", "ms": p2, "fp32_algorithmic_flop": f2,
+                   "fp32_equivalent_tflops": f2 / (p2 * 1e-3) / 1e12},
+    }
+    need = None
+    if kind == "iso" and not bf16 and not args.store_log_joint and D <= 128:
+        pairs = iso_need_pairs(inp, logZ)
+        KB = -(-K // 32)
+        DP = padded_dim(kind, D)
+        # gathered tiles of 32 rows; per tile the split-bf16 recompute (7 steps per
+        # 16 dimensions) and r^T X (3 products, DP/32 column tiles, 2 row steps)
+        ex2 = pairs / 32.0 * (7 * DP // 16 + 3 * 2 * DP // 32) * 32768.0
+        need = {"needed_row_block_pairs": pairs, "fraction": pairs / (N * KB),
+                "basis": "estimated from the inputs and the kernel's logZ (float32)"}
+        phases["phase2"].update(executed_matrix_flop=ex2, executed_unit="bf16",
+                                executed_tflops=ex2 / (p2 * 1e-3) / 1e12, needed_pairs=need)
+    dom = "phase1" if p1 >= p2 else "phase2"
+    d = phases[dom]
+    if "executed_matrix_flop" in d:
+        unit = d["executed_unit"]
+        peak = PEAK_BF16_MFMA_TFLOPS if unit == "bf16" else PEAK_FP32_MFMA_TFLOPS
+        roof = {"bound": "mfma", "achieved": d["executed_tflops"], "peak": peak, "unit": "TFLOP/s",
+                "frac": d["executed_tflops"] / peak, "kernel": d["kernel"], "avg_launch_ms": d["ms"],
+                "achieved_basis": f"matrix flops executed per launch on the {unit} matrix cores / the "
+                                  "phase's mean duration (HIP events on the launch stream)",
+                "fp32_equivalent_tflops": d["fp32_equivalent_tflops"]}
+    else:
+        roof = {"bound": "mfma", "achieved": d["fp32_equivalent_tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": min(1.0, d["fp32_equivalent_tflops"] / PEAK_FP32_MFMA_TFLOPS),
+                "kernel": d["kernel"], "avg_launch_ms": d["ms"],
+                "achieved_basis": "dense-equivalent fp32 flops / the phase's mean duration"}
+    traffic = TRAFFIC_BYTES.get((workload, "stored" if args.store_log_joint else "default", args.precision),
+                                {}).get(dom)
+    roof.update({"traffic": traffic, "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE)",
+                 "algorithmic_bytes": alg_bytes if dom == "phase1" else None,
+                 "traffic_over_algorithmic": (traffic / alg_bytes) if (traffic and dom == "phase1") else None})
+
+    out = {
+        "metric": (METRIC if workload == "iso_n1m_k1024_d128" and not bf16 else
+                   f"E-step samples/sec ({workload}) bf16 operands, fp32 accumulation (1 GPU)" if bf16 else
+                   f"E-step samples/sec ({workload}) fp32 (1 GPU)"),
+        "value": N / (ms * 1e-3),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": (N / (ms * 1e-3)) / A100_SAMPLES_PER_S
+                       if kind == "iso" and D == 128 and K == 1024 and not bf16 else None,
+        "baseline_note": "reference's published A100 80GB figure for this shape: 152 ms at N=1M "
+                         "(README.md:116), TF32 dot; context, not the same hardware"
+                         if kind == "iso" and K == 1024 and D == 128 else
+                         "no published reference number for this workload",
+        "dtype": "bf16 operands, f32 accumulation" if bf16 else "f32",
+        "data": "synthetic",
+        "config": {"workload": workload, "N": N, "K": K, "D": D,
+                   "generator": f"flash_gmm.data.make({workload!r}), generated on device",
+                   "reduce": "deterministic fixed-order tree",
+                   "log_joint": "stored by phase 1, read by phase 2 (opt-in)" if args.store_log_joint
+                   else "recomputed (default O(N + K*D) plan: need bits from phase 1, gathered rows "
+                        "in phase 2)" if (kind == "iso" and D <= 128 and not bf16)
+                   else "recomputed (default O(N + K*D) plan)",
+                   "workspace_bytes": r["ws"]},
+        "fp32_equivalent_tflops": flop / (ms * 1e-3) / 1e12,
+        "fp32_equivalent_basis": "the metric's algorithmic flops (iso 4NKD) per step / step time. Not a "
+                                 "roofline: pass 1 forms its fp32 products from split-bf16 steps on the "
+                                 "bf16 matrix cores and pass 2 skips the work whose responsibilities are "
+                                 "zero; roofline.frac rates the executed work against the peak of the unit "
+                                 "that runs it",
+        "phases": phases,
+        "roofline": roof,
+    }
+    if not args.no_extra_runs:
+        call = r["call"]
+        dms, d1, d2 = time_steps(call, args.steps, 2, stream, dense=True)
+        out["dense_accumulation"] = {"ms_per_step": dms, "phase1_ms": d1, "phase2_ms": d2,
+                                     "note": "every row and accumulation step executed (FGMM_FLAG_DENSE)"}
+        log(f"dense: {dms:.3f} ms/step")
+        if not bf16 and not args.store_log_joint:
+            del call, r
+            torch.cuda.empty_cache()
+            _, _, rs = measure(args, workload, "fp32", True, dev, inp=inp)
+            out["stored_log_joint_plan"] = {
+                "ms_per_step": rs["ms"], "phase1_ms": rs["p1"], "phase2_ms": rs["p2"],
+                "workspace_bytes": rs["ws"], "note": "opt-in FGMM_FLAG_STORE_LOGJOINT: pass 1 stores the "
+                                                     "N x K fp32 log-joint, pass 2 reads it"}
+            log(f"stored log-joint plan: {rs['ms']:.3f} ms/step")
+            del rs
+            torch.cuda.empty_cache()
+    if not args.no_cpu_baseline and not bf16:
+        log("timing the CPU baseline (bounded sample)")
+        out["cpu_baseline"] = cpu_baseline(inp, kind, K, D, logZ)
+    print(json.dumps(out), flush=True)
+
+
+def sweep_main(args):
+    """One JSON line per D: default plan, stored log-joint and dense, ms per step."""
+    import torch
+    from flash_gmm import data
+
+    kind, N, K, Ds = args.sweep.split(":")
+    N, K = int(N), int(K)
+    dev = torch.device("cuda:0")
+    gen = {"iso": data.iso_clustered, "diag": data.diag_clustered, "full": data.full_clustered}[kind]
+    stream = torch.cuda.current_stream(dev)
+    for D in (int(d) for d in Ds.split(",")):
+        inp = gen(N, K, D, seed=1, device=dev)
+        res = {"sweep": kind, "N": N, "K": K, "D": D}
+        for name, store in (("default", False), ("stored", True)):
+            call, ws, _ = make_runner(kind, inp, N, K, D, dev, "fp32", store)
+            ms, p1, p2 = time_steps(call, args.steps, 3, stream)
+            res[name] = {"ms": round(ms, 3), "phase1_ms": round(p1, 3), "phase2_ms": round(p2, 3),
+                         "workspace_MB": round(ws / 2**20, 1)}
+            if name == "default":
+                dms, _, _ = time_steps(call, args.steps, 2, stream, dense=True)
+                res["default"]["dense_ms"] = round(dms, 3)
+            del call
+            torch.cuda.empty_cache()
+        print(json.dumps(res), flush=True)
+        del inp
+        torch.cuda.empty_cache()
+
+
+def reduce_compare_main(args):
+    """Deterministic fixed-order tree against float atomics for the finish, per workload."""
+    import torch
+    from flash_gmm import data
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    for workload in ("iso_n1m_k1024_d128", "diag_n1m_k1024_d96", "full_n250k_k256_d64"):
+        N, K, D = WORKLOADS[workload]
+        kind = workload.split("_")[0]
+        inp = data.make(workload, device=dev)
+        res = {"reduce_compare": workload}
+        for name, atomic in (("tree", False), ("atomic", True)):
+            call, _, _ = make_runner(kind, inp, N, K, D, dev, "fp32", False, atomic)
+            ms, p1, p2 = time_steps(call, args.steps, 3, stream)
+            res[name] = {"ms": round(ms, 4), "phase2_ms": round(p2, 4)}
+            del call
+            torch.cuda.empty_cache()
+        print(json.dumps(res), flush=True)
+        del inp
+        torch.cuda.empty_cache()
 
 
 def stream_main(args):
     """Streaming EM over host-generated rows (pinned double buffers, copy/compute overlap)."""
-    import numpy as np
     import torch
     from flash_gmm import SynthIsoSource, data, stream_em_iso
 
@@ -160,7 +477,7 @@ def stream_main(args):
     mu = (centres + 0.5 * torch.randn(K, D, generator=g)).to(dev)
     lss = torch.zeros(K, device=dev)
     lpi = model["log_pi"].to(dev)
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    threads = len(os.sched_getaffinity(0))
     src = SynthIsoSource(centres.numpy(), seed=4, threads=threads)
     log(f"streaming EM: N={N} rows, K={K}, D={D}, chunks of {chunk} rows, {iters} iterations, "
         f"{threads} host threads")
@@ -223,20 +540,19 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--atomic-reduce", action="store_true")
-    ap.add_argument("--dense", action="store_true",
-                    help="also run accumulation steps whose responsibilities are all zero")
-    ap.add_argument("--no-dense-run", action="store_true",
-                    help="skip the dense comparison run (profiling the default launches alone)")
+    ap.add_argument("--no-extra-runs", action="store_true",
+                    help="time only the selected plan (no dense and stored-log-joint runs)")
     ap.add_argument("--workload", default="iso_n1m_k1024_d128",
                     choices=sorted(WORKLOADS) + ["stream_em_n1b_k1024_d128"])
     ap.add_argument("--rows", type=int, default=0, help="override N of the streaming workload")
     ap.add_argument("--precision", choices=["fp32", "bf16"], default="fp32",
-                    help="bf16 runs the H100 variants' bf16 operand contract (FGMM_FLAG_BF16) "
-                         "and is rated against the bf16 matrix peak")
+                    help="bf16 runs the H100 variants' bf16 operand contract (FGMM_FLAG_BF16)")
     ap.add_argument("--store-log-joint", action="store_true",
-                    help="pass 1 stores the N x K log-joint and pass 2 reads it "
-                         "(FGMM_FLAG_STORE_LOGJOINT; O(N*K) workspace) instead of the default plan")
+                    help="time the opt-in plan that stores the N x K log-joint (FGMM_FLAG_STORE_LOGJOINT)")
+    ap.add_argument("--sweep", default="", metavar="KIND:N:K:D1,D2,...",
+                    help="time the default, stored and dense plans over several D")
+    ap.add_argument("--reduce-compare", action="store_true",
+                    help="time the fixed-order tree finish against float atomics at the benchmark shapes")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB five times (scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -246,11 +562,9 @@ def main():
               "(the E-step shards by rows with one all-reduce of O(K*D) statistics, "
               "which is not built here).", file=sys.stderr)
         sys.exit(2)
-
     if args.workload.startswith("stream_em"):
         stream_main(args)
-        return
-    if args.copy_calibration:
+    elif args.copy_calibration:
         import torch
         n = args.copy_calibration * (1 << 20) // 4
         a = torch.ones(n, device="cuda:0")
@@ -259,211 +573,12 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": n * 4, "launches": 5}), flush=True)
-        return
-
-    import torch
-    from flash_gmm import _lib, data, diag_estep_into, full_estep_into, iso_estep_into
-
-    dev = torch.device("cuda:0")
-    N, K, D = WORKLOADS[args.workload]
-    kind = args.workload.split("_")[0]
-    bf16 = args.precision == "bf16"
-    peak = PEAK_BF16_MFMA_TFLOPS if bf16 else PEAK_FP32_MFMA_TFLOPS
-    log(f"generating workload {args.workload} on {torch.cuda.get_device_name(dev)}")
-    inp = data.make(args.workload, device=dev)
-    L = _lib.lib()
-    logZ = torch.empty(N, device=dev)
-    Nk = torch.empty(K, device=dev)
-    mu_acc = torch.empty(K, D, device=dev)
-    if kind == "iso":
-        args4 = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
-        sig = torch.empty(K, device=dev)
-        fn = lambda ph, dense=args.dense: iso_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
-                                                         phase=ph, atomic_reduce=args.atomic_reduce,
-                                                         dense=dense, store_log_joint=args.store_log_joint,
-                                                         precision=args.precision)
-    elif kind == "diag":
-        args4 = (inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
-        sig = torch.empty(K, D, device=dev)
-        fn = lambda ph, dense=args.dense: diag_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
-                                                          phase=ph, dense=dense, store_log_joint=args.store_log_joint,
-                                                          precision=args.precision)
+    elif args.sweep:
+        sweep_main(args)
+    elif args.reduce_compare:
+        reduce_compare_main(args)
     else:
-        args4 = (inp["X"], inp["mu"], inp["prec_chol"], inp["log_pi"])
-        sig = torch.empty(K, D, D, device=dev)
-        fn = lambda ph, dense=args.dense: full_estep_into(*args4, logZ, Nk, mu_acc, sig, workspace=ws,
-                                                          phase=ph, dense=dense, store_log_joint=args.store_log_joint,
-                                                          precision=args.precision)
-    ws_fn = getattr(L, f"fgmm_{kind}_workspace_bytes_ex")
-    pflag = _lib.FLAG_BF16 if bf16 else 0
-    flags = (_lib.FLAG_STORE_LOGJOINT if args.store_log_joint else 0) | pflag
-    ws = torch.empty(int(ws_fn(N, K, D, flags)), dtype=torch.uint8, device=dev)
-    # Pass 2 reads the log-joint that pass 1 stores whenever the plan sizes it in.
-    stored_lj = (int(ws_fn(N, K, D, pflag)) != int(ws_fn(N, K, D, pflag | _lib.FLAG_STORE_LOGJOINT))
-                 and args.store_log_joint)
-    stream = torch.cuda.current_stream(dev)
-
-    def step(ev=None):
-        if ev is not None:
-            ev[0].record(stream)
-        fn(1)
-        if ev is not None:
-            ev[1].record(stream)
-        fn(2)
-        if ev is not None:
-            ev[2].record(stream)
-
-    def dense_step():
-        fn(1, True)
-        fn(2, True)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    log(f"warmup done; sum Nk = {Nk.double().sum().item():.3f} (N = {N})")
-
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
-    for i in range(args.steps):
-        step(evs[i])
-    end.record(stream)
-    torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    ms = total_ms / args.steps
-    p1 = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
-    p2 = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
-    log(f"timed {args.steps} steps: {ms:.3f} ms/step (phase1 {p1:.3f} ms, phase2 {p2:.3f} ms)")
-
-    dense_ms = None
-    if not args.dense and not args.no_dense_run:
-        # The same steps with every accumulation step executed (identical outputs):
-        # the dense cost, reported beside the default.
-        for _ in range(2):
-            dense_step()
-        torch.cuda.synchronize()
-        start.record(stream)
-        for _ in range(args.steps):
-            dense_step()
-        end.record(stream)
-        torch.cuda.synchronize()
-        dense_ms = start.elapsed_time(end) / args.steps
-        log(f"dense accumulation: {dense_ms:.3f} ms/step")
-
-    flop, f1, f2 = algorithmic_flop(kind, N, K, D)
-    b1, b2 = algorithmic_bytes(kind, N, K, D, stored_lj)
-    step_tflops = flop / (ms * 1e-3) / 1e12
-    p2_kernel = {"iso": "iso_accum", "diag": "diag_accum", "full": "full_accum"}[kind] + (
-        "_lj" if stored_lj and kind != "full" else "")
-    if kind == "iso" and stored_lj and D % 32 == 0 and D <= 128:
-        p2_kernel = "iso_accum_sparse or iso_accum_lj, picked on device by mask density"
-    if kind == "diag" and stored_lj and D <= 128:
-        p2_kernel = ("diag_accum_sparse or diag_accum_lj2, picked on device by mask density"
-                     if D % 32 == 0 else "diag_accum_lj2")
-    split_p1 = (kind in ("iso", "diag") and D <= 128) or (kind == "full" and stored_lj)
-    p1_kernel = f"{kind}_lse" + ("_x6" if split_p1 and kind != "iso" else "")
-    names = (f"{p1_kernel} (log-normaliser pass + prologue"
-             + (", split-bf16 products" if split_p1 else "")
-             + (", stores the log-joint)" if stored_lj else ")"),
-             f"{p2_kernel} (accumulation pass + slab reduction"
-             + (", reads the stored log-joint)" if stored_lj else ", recomputes the log-joint)"))
-    if bf16:
-        names = (f"{kind}_bf16_lse (log-normaliser pass + prologue, bf16 operands"
-                 + (", stores the log-joint)" if kind == "full" else ")"),
-                 f"{kind}_bf16_accum (accumulation pass + slab reduction, "
-                 + ("reads the stored log-joint)" if kind == "full" else "recomputes in bf16)"))
-    traffic_tab = {} if (not args.store_log_joint or bf16) else TRAFFIC_BYTES.get(args.workload, {})
-    phases = {}
-    for ph, name, t, f, b in (("phase1", names[0], p1, f1, b1), ("phase2", names[1], p2, f2, b2)):
-        phases[ph] = {"kernel": name, "ms": t, "algorithmic_flop": f,
-                      "tflops": f / (t * 1e-3) / 1e12, "algorithmic_bytes": b,
-                      "gbs": b / (t * 1e-3) / 1e9, "traffic": traffic_tab.get(ph)}
-    dom_phase = "phase2" if p2 >= p1 else "phase1"
-    dom = phases[dom_phase]
-    # Phase 1 and the recomputing phase 2 are matrix-core bound.  Reading the stored
-    # log-joint, phase 2 moves ~8 bytes per (row, component) and skips the steps whose
-    # responsibilities are all zero: it is HBM bound.
-    hbm_bound = dom_phase == "phase2" and stored_lj and not args.dense
-    if hbm_bound:
-        roof = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": dom["gbs"] / PEAK_HBM_GBS, "algorithmic_bytes_per_launch": dom["algorithmic_bytes"]}
-    else:
-        roof = {"bound": "mfma", "achieved": dom["tflops"], "peak": peak,
-                "unit": "TFLOP/s", "frac": dom["tflops"] / peak,
-                "algorithmic_flop_per_launch": dom["algorithmic_flop"]}
-    roof.update({"kernel": dom["kernel"], "traffic": dom["traffic"],
-                 "traffic_unit": "bytes per launch (HBM read + write, rocprofv3 counters)",
-                 "avg_launch_ms": dom["ms"]})
-    # Phase 1 forms its fp32 contraction from split-bf16 products on the bf16 matrix
-    # cores: 7 steps (6 products + 1 centring offset) per chunk and 32x32 tile, each
-    # step 32 bf16 flop per (row, output).  Per (row, component):
-    #   iso:  16-dimension chunks, 1 output:          14 D bf16 flop (2 D algorithmic)
-    #   diag: 8-dimension chunks of [x^2, x]:         28 D               (4 D)
-    #   full: 16-dimension chunks, D outputs:         14 D^2             (2 D^2)
-    # (D padded: iso to 16, diag and full to 32.)  Full recomputation keeps fp32 steps.
-    ex = None
-    if not bf16 and dom_phase == "phase1":
-        if kind == "iso" and D <= 128:
-            ex = 14.0 * N * K * (D + (-D) % 16)
-        elif kind == "diag" and D <= 128:
-            ex = 28.0 * N * K * (D + (-D) % 32)
-        elif kind == "full" and stored_lj:
-            ex = 14.0 * N * K * (D + (-D) % 32) ** 2
-    if ex is not None:
-        roof["executed"] = {"arithmetic": "split-bf16 (bf16x6) products, fp32 accumulation, fp64 "
-                                          "combination; fp32 inputs and outputs",
-                            "bf16_flop_per_launch": ex,
-                            "bf16_tflops": ex / (dom["ms"] * 1e-3) / 1e12,
-                            "bf16_peak": PEAK_BF16_MFMA_TFLOPS,
-                            "bf16_frac": ex / (dom["ms"] * 1e-3) / 1e12 / PEAK_BF16_MFMA_TFLOPS}
-
-    out = {
-        "metric": (METRIC if kind == "iso" and not bf16 else
-                   f"E-step samples/sec ({args.workload}) bf16 operands, fp32 accumulation "
-                   "+ % of bf16 MFMA peak (1 GPU)" if bf16 else
-                   f"E-step samples/sec ({args.workload}) fp32 + % of fp32 MFMA peak (1 GPU)"),
-        "value": N / (ms * 1e-3),
-        "unit": "samples/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": (N / (ms * 1e-3)) / A100_SAMPLES_PER_S if kind == "iso" and not bf16 else None,
-        "baseline_note": "reference's published A100 80GB figure for this shape: 152 ms at N=1M "
-                         "(README.md:116), TF32 dot" if kind == "iso" else
-                         "no published reference number for this workload",
-        "dtype": "bf16 operands, f32 accumulation" if bf16 else "f32",
-        "data": "synthetic",
-        "config": {"workload": args.workload, "N": N, "K": K, "D": D,
-                   "generator": f"flash_gmm.data.make({args.workload!r}), generated on device",
-                   "reduce": "atomic" if args.atomic_reduce else "deterministic",
-                   "log_joint": "stored by phase 1, read by phase 2" if stored_lj else "recomputed by phase 2"},
-        "fraction_of_fp32_mfma_peak": step_tflops / PEAK_FP32_MFMA_TFLOPS,
-        "fraction_of_matrix_peak": step_tflops / peak,
-        "fraction_basis": "dense-equivalent algorithmic flops per step / step time; phase 2 executes "
-                          "only the accumulation steps whose responsibilities are not all zero"
-                          + (" and reads the log-joint instead of recomputing it" if stored_lj else "")
-                          + ", so the matrix work executed is lower: the dense run and the per-phase "
-                            "rates below are the executed figures",
-        "step_tflops_algorithmic": step_tflops,
-        "phase_ms": {"phase1": p1, "phase2": p2},
-        "phases": phases,
-        "accumulation": "dense" if args.dense else
-                        "skips steps whose responsibilities are all exactly zero (bitwise-identical outputs)",
-        "dense_ms_per_step": dense_ms if dense_ms is not None else (ms if args.dense else None),
-        "dense_fraction_of_fp32_mfma_peak": (flop / (dense_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS)
-                                            if dense_ms is not None else None,
-        "dense_fraction_of_matrix_peak": (flop / (dense_ms * 1e-3) / 1e12 / peak)
-                                         if dense_ms is not None else None,
-        "roofline": roof,
-    }
-    if not args.no_cpu_baseline and not bf16:
-        log("timing the CPU baseline (bounded sample)")
-        out["cpu_baseline"] = cpu_baseline({k: v for k, v in inp.items()}, kind, K, D)
-    print(json.dumps(out), flush=True)
+        main_workload(args)
 
 
 if __name__ == "__main__":

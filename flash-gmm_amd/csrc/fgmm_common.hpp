@@ -210,17 +210,34 @@ __device__ __forceinline__ void acc_to_row_operands(const float (&r)[16], bf16x8
 // Six bf16 steps (192 matrix cycles) replace 8 fp32 steps (512 cycles) per 16
 // dimensions.
 // ---------------------------------------------------------------------------
+// Two values at a time: one packed round-to-nearest-even conversion per pair
+// (v_cvt_pk_bf16_f32), the bf16 halves widened back by a shift or a mask.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ unsigned bf16_pair(f32x2 v) {
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf16x2));
+}
+__device__ __forceinline__ f32x2 bf16_pair_widen(unsigned w) {
+  const f32x2 r = {__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u)};
+  return r;
+}
+
 __device__ __forceinline__ void split3_bf16(const f32x4 lo, const f32x4 hi, bf16x8 (&s)[3]) {
   const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  uint4 w[3];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const __bf16 h = (__bf16)v[e];
-    const float r = v[e] - (float)h;
-    const __bf16 m = (__bf16)r;
-    s[0][e] = h;
-    s[1][e] = m;
-    s[2][e] = (__bf16)(r - (float)m);
+  for (int j = 0; j < 4; ++j) {
+    const f32x2 a = {v[2 * j], v[2 * j + 1]};
+    const unsigned h = bf16_pair(a);
+    const f32x2 r = a - bf16_pair_widen(h);
+    const unsigned m = bf16_pair(r);
+    const unsigned l = bf16_pair(r - bf16_pair_widen(m));
+    (j == 0 ? w[0].x : j == 1 ? w[0].y : j == 2 ? w[0].z : w[0].w) = h;
+    (j == 0 ? w[1].x : j == 1 ? w[1].y : j == 2 ? w[1].z : w[1].w) = m;
+    (j == 0 ? w[2].x : j == 1 ? w[2].y : j == 2 ? w[2].z : w[2].w) = l;
   }
+#pragma unroll
+  for (int t = 0; t < 3; ++t) s[t] = __builtin_bit_cast(bf16x8, w[t]);
 }
 
 // One 32x32 tile of the centred cross term t = x.mu - sum_q o_q over NQ
@@ -554,8 +571,8 @@ __device__ __forceinline__ void lj_put_masks(const float* __restrict__ bmax, uns
 // R bounds every log-joint value the accumulation pass recomputes for the row and
 // block (the same arithmetic), so a clear bit again means responsibilities that are
 // exactly zero in fp32.  `rmax(kb)` returns the lane's bound for block kb.  Run by
-// the half-wave g = 0 (lane c = row c); the count gathers the register-row pairs
-// with a bit set, as lj_put_masks does.
+// the half-wave g = 0 (lane c = row c); `count` gathers the number of bits set
+// (needed (row, block) pairs), from which the accumulation pass picks its form.
 template <typename RM>
 __device__ __forceinline__ void need_put_masks(RM rmax, unsigned* __restrict__ mask, unsigned* __restrict__ count,
                                                int KB, int c, double lz2, bool valid, bool dense) {
@@ -571,7 +588,7 @@ __device__ __forceinline__ void need_put_masks(RM rmax, unsigned* __restrict__ m
       if (kb0 + j < KB) {
         const bool need = valid && (dense || !(((R[j] - zx) - zy) < -kLjNeedGap));
         const unsigned b = (unsigned)__builtin_amdgcn_ballot_w64(need);
-        pairs += __builtin_popcount(lj_pair_mask(b));
+        pairs += __builtin_popcount(b);
         if (c == 0) mask[kb0 + j] = b;
       }
     }

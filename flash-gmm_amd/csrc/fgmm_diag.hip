@@ -1631,6 +1631,29 @@ __global__ __launch_bounds__(256) void diag_reduce(const float* __restrict__ par
   if (d == 0) Nk[k] = accumulate ? (float)((double)Nk[k] + nk) : (float)nk;
 }
 
+// Atomic finish (FGMM_FLAG_ATOMIC_REDUCE): partial blockIdx.y of every (k, d) is added
+// into the zeroed (or accumulated) outputs; the sig identity is formed per partial in
+// fp64 and added in fp32.
+__global__ __launch_bounds__(256) void diag_reduce_atomic(const float* __restrict__ part_mu,
+                                                          const float* __restrict__ part_sq,
+                                                          const float* __restrict__ part_nk, int KP, int DP,
+                                                          int64_t K, int D, const float* __restrict__ mu,
+                                                          int64_t ldmu, float* __restrict__ Nk,
+                                                          float* __restrict__ mu_acc, float* __restrict__ sig_acc) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= K * D) return;
+  const int64_t k = idx / D;
+  const int d = (int)(idx % D);
+  const int64_t pk = (int64_t)blockIdx.y * KP + k;
+  const double sm = (double)part_mu[pk * DP + d];
+  const double sq = (double)part_sq[pk * DP + d];
+  const double nk = (double)part_nk[pk];
+  const double m = (double)mu[k * ldmu + d];
+  atomicAdd(mu_acc + k * D + d, (float)sm);
+  atomicAdd(sig_acc + k * D + d, (float)(sq - 2.0 * m * sm + m * m * nk));
+  if (d == 0) atomicAdd(Nk + k, (float)nk);
+}
+
 __global__ __launch_bounds__(256) void diag_fill(float* __restrict__ p, int64_t n, float v) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -2347,6 +2370,20 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     if (e != hipSuccess) return FGMM_ERR_HIP;
   }
   if (!run2) return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+  if ((flags & FGMM_FLAG_ATOMIC_REDUCE) && !bf16) {
+    if (!accumulate) {
+      hipLaunchKernelGGL(diag_fill, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, stream, Nk, K, 0.0f);
+      hipLaunchKernelGGL(diag_fill, dim3((unsigned)cdiv(K * D, 256)), dim3(256), 0, stream, mu_acc, K * D, 0.0f);
+      hipLaunchKernelGGL(diag_fill, dim3((unsigned)cdiv(K * D, 256)), dim3(256), 0, stream, sig_acc, K * D, 0.0f);
+    }
+    if (pl.npart > 0)
+      hipLaunchKernelGGL(diag_reduce_atomic, dim3((unsigned)cdiv(K * D, 256), (unsigned)pl.npart), dim3(256), 0,
+                         stream, reinterpret_cast<const float*>(ws + pl.off_part_mu),
+                         reinterpret_cast<const float*>(ws + pl.off_part_sq),
+                         reinterpret_cast<const float*>(ws + pl.off_part_nk), pl.KP, pl.DP, K, (int)D, mu,
+                         ldmu, Nk, mu_acc, sig_acc);
+    return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+  }
   const bool wide = pl.npart >= kWideReduce;
   hipLaunchKernelGGL(wide ? diag_reduce<true> : diag_reduce<false>,
                      dim3((unsigned)(wide ? cdiv(K * D, 4) : cdiv(K * D, 256))), dim3(256), 0, stream,

@@ -869,12 +869,24 @@ void full_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D
 }
 
 // Finish: one thread per (k, d1, d2) of sig_outer plus (k, d) of mu_acc and k of Nk.
+// ATOMIC (FGMM_FLAG_ATOMIC_REDUCE): partial blockIdx.y is added with float atomics into
+// the zeroed (or accumulated) outputs instead of the fixed-order fp64 sum.
+template <bool ATOMIC>
 __global__ __launch_bounds__(256) void full_reduce(const float* __restrict__ part_sig,
                                                    const float* __restrict__ part_mu,
                                                    const float* __restrict__ part_nk, int npart, int KP,
                                                    int DP, int NMB, int64_t K, int D,
                                                    float* __restrict__ Nk, float* __restrict__ mu_acc,
                                                    float* __restrict__ sig_outer, int accumulate) {
+  // Sum over the partials of p[0], p[stride], ... (or, atomically, the one of this grid row).
+  auto finish = [&](const float* p, int64_t stride, float* o) {
+    if (ATOMIC) {
+      atomicAdd(o, p[(int64_t)blockIdx.y * stride]);
+    } else {
+      const double s = strided_sum(p, npart, stride);
+      *o = accumulate ? (float)((double)*o + s) : (float)s;
+    }
+  };
   const int NSB = NMB * (NMB + 1) / 2;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t nsig = K * D * D;
@@ -891,26 +903,18 @@ __global__ __launch_bounds__(256) void full_reduce(const float* __restrict__ par
     // the block is symmetric only in sum, so read (d1%32, d2%32) directly.
     const int e1 = (d1 / 32 == b1) ? d1 % 32 : d2 % 32;
     const int e2 = (d1 / 32 == b1) ? d2 % 32 : d1 % 32;
-    const double s = strided_sum(part_sig + ((int64_t)k * NSB + sb) * 1024 + e1 * 32 + e2, npart,
-                                 (int64_t)KP * NSB * 1024);
-    float* o = sig_outer + idx;
-    *o = accumulate ? (float)((double)*o + s) : (float)s;
+    finish(part_sig + ((int64_t)k * NSB + sb) * 1024 + e1 * 32 + e2, (int64_t)KP * NSB * 1024, sig_outer + idx);
     return;
   }
   const int64_t j = idx - nsig;
   if (j < K * D) {
     const int64_t k = j / D;
     const int d = (int)(j % D);
-    const double s = strided_sum(part_mu + k * DP + d, npart, (int64_t)KP * DP);
-    float* o = mu_acc + j;
-    *o = accumulate ? (float)((double)*o + s) : (float)s;
+    finish(part_mu + k * DP + d, (int64_t)KP * DP, mu_acc + j);
     return;
   }
   const int64_t kk = j - K * D;
-  if (kk < K) {
-    const double s = strided_sum(part_nk + kk, npart, KP);
-    Nk[kk] = accumulate ? (float)((double)Nk[kk] + s) : (float)s;
-  }
+  if (kk < K) finish(part_nk + kk, KP, Nk + kk);
 }
 
 __global__ __launch_bounds__(256) void full_fill(float* __restrict__ p, int64_t n, float v) {
@@ -1498,7 +1502,22 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
                        pl.NMB, K, (int)D, Nk, mu_acc, sig_outer, accumulate ? 1 : 0);
     return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
   }
-  hipLaunchKernelGGL(full_reduce, dim3((unsigned)cdiv(nthreads, 256)), dim3(256), 0, stream,
+  if (flags & FGMM_FLAG_ATOMIC_REDUCE) {
+    if (!accumulate) {
+      hipLaunchKernelGGL(full_fill, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, stream, Nk, K, 0.0f);
+      hipLaunchKernelGGL(full_fill, dim3((unsigned)cdiv(K * D, 256)), dim3(256), 0, stream, mu_acc, K * D, 0.0f);
+      hipLaunchKernelGGL(full_fill, dim3((unsigned)cdiv(K * D * D, 256)), dim3(256), 0, stream, sig_outer,
+                         K * D * D, 0.0f);
+    }
+    if (pl.npart > 0)
+      hipLaunchKernelGGL(full_reduce<true>, dim3((unsigned)cdiv(nthreads, 256), (unsigned)pl.npart), dim3(256), 0,
+                         stream, reinterpret_cast<const float*>(ws + pl.off_part_sig),
+                         reinterpret_cast<const float*>(ws + pl.off_part_mu),
+                         reinterpret_cast<const float*>(ws + pl.off_part_nk), pl.npart, pl.KP, pl.DP, pl.NMB, K,
+                         (int)D, Nk, mu_acc, sig_outer, 1);
+    return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
+  }
+  hipLaunchKernelGGL(full_reduce<false>, dim3((unsigned)cdiv(nthreads, 256)), dim3(256), 0, stream,
                      reinterpret_cast<const float*>(ws + pl.off_part_sig),
                      reinterpret_cast<const float*>(ws + pl.off_part_mu),
                      reinterpret_cast<const float*>(ws + pl.off_part_nk), pl.npart, pl.KP, pl.DP,

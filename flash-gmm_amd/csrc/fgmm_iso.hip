@@ -410,7 +410,7 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   double mx = -INFINITY;
   float sm = 0.0f;
   float run_max = -INFINITY;   // running max of the row's stored log-joint / block maxima
-  unsigned pairs = 0;          // needed register-row pairs (need masks from the running max)
+  unsigned pairs = 0;          // needed rows over the blocks (need masks from the running max)
 
   for (int kb = 0; kb < KB; ++kb) {
     const int buf = kb & 1;
@@ -454,7 +454,7 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
         const bool nb = valid && (dense != 0 || !(R - run_max < -kLjSkipGap));
         const unsigned bits = (unsigned)__builtin_amdgcn_ballot_w64(nb);
         if (lane == 0) ljmask[tile * KB + kb] = bits;
-        pairs += __builtin_popcount(lj_pair_mask(bits));
+        pairs += __builtin_popcount(bits);
       }
     }
     if (more) commit(buf ^ 1);
@@ -985,6 +985,23 @@ void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   }
 }
 
+// Total of the 64 needed-pair counters (one wave, uniform result).
+__device__ __forceinline__ unsigned lj_pair_total(const unsigned* __restrict__ count) {
+  unsigned v = count[threadIdx.x & 63];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+// The same total in 64 bits (needed rows of the default plan can pass 2^32).
+__device__ __forceinline__ int64_t need_total(const unsigned* __restrict__ count) {
+  uint64_t v = count[threadIdx.x & 63];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return (int64_t)__builtin_amdgcn_readfirstlane((unsigned)(v & 0xffffffffu)) |
+         ((int64_t)__builtin_amdgcn_readfirstlane((unsigned)(v >> 32)) << 32);
+}
+
 // ---------------------------------------------------------------------------
 // Pass 2 of the default plan (D <= 128): the log-joint is recomputed only for the
 // (row, component block) pairs whose need bit pass 1 set.
@@ -1028,13 +1045,16 @@ __global__ __attribute__((amdgpu_flat_work_group_size(64 * kGatherWaves, 64 * kG
                           amdgpu_waves_per_eu(1, 1)))
 void iso_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                       const bf16x8* __restrict__ mu3, const double4* __restrict__ kc_gat, int KB, int KP,
-                      const double2* __restrict__ rowstat, const unsigned* __restrict__ need, int nslab,
+                      const double2* __restrict__ rowstat, const unsigned* __restrict__ need,
+                      const unsigned* __restrict__ needcount, int64_t dense_min, int nslab,
                       int64_t rows_per_slab, float* __restrict__ part_mu, float* __restrict__ part_nk,
                       float* __restrict__ part_sig, int dense) {
   constexpr int NQ = DP / 16;
   constexpr int NJ = DP / 32;
   constexpr int RS = gather_rs(DP);
   constexpr int BLK = NQ * 4 * 64;   // bf16x8 per component block
+  // With at least dense_min needed rows iso_accum_tiles runs instead (uniform exit).
+  if (need_total(needcount) >= dense_min) return;
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   unsigned char* lp = lds_raw;
@@ -1198,12 +1218,196 @@ void iso_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D
   }
 }
 
-// Total of the 64 needed-pair counters (one wave, uniform result).
-__device__ __forceinline__ unsigned lj_pair_total(const unsigned* __restrict__ count) {
-  unsigned v = count[threadIdx.x & 63];
+
+// ---------------------------------------------------------------------------
+// Pass 2 of the default plan (D <= 128) when most pairs are needed (pass 1 counted
+// at least dense_min needed rows; the gathering kernel runs otherwise).  Grid over
+// (row slab x group of 4 component blocks), one wave per SIMD; wave w owns block
+// 4 cg + w, its mu operands in registers, and the slab's partial of that block
+// (the gathering kernel's slab split, so either kernel fills the same partials).
+// The 32-row tiles of X are loaded once per workgroup, split three ways into bf16
+// by all 256 threads and kept row-major in LDS (double-buffered), where the four
+// waves read the A operands of S (x6c_tile_rows) and the transposed B operands of
+// r^T X (lds_rows_operand).  A wave whose need word of the tile is zero skips it;
+// rows whose bit is clear enter with responsibilities that are exactly zero.
+// ---------------------------------------------------------------------------
+constexpr int kTileBlocks = 4;
+
+__host__ __device__ constexpr size_t tiles_lds_bytes(int DP) {
+  return (size_t)2 * 3 * 32 * gather_rs(DP) * 2 + (size_t)2 * 32 * sizeof(double2);
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kTileBlocks, 64 * kTileBlocks),
+                          amdgpu_waves_per_eu(1, 1)))
+void iso_accum_tiles(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                     const bf16x8* __restrict__ mu3, const double4* __restrict__ kc_gat, int KB, int KP,
+                     const double2* __restrict__ rowstat, const unsigned* __restrict__ need,
+                     const unsigned* __restrict__ needcount, int64_t dense_min, int nslab,
+                     int64_t rows_per_slab, float* __restrict__ part_mu, float* __restrict__ part_nk,
+                     float* __restrict__ part_sig, int dense) {
+  constexpr int NQ = DP / 16;
+  constexpr int NJ = DP / 32;
+  constexpr int RS = gather_rs(DP);
+  constexpr int BLK = NQ * 4 * 64;
+  constexpr int NT = 64 * kTileBlocks;
+  constexpr int V4 = DP / 4;              // float4 per row
+  constexpr int LPT = 32 * V4 / NT;       // float4 per thread per tile
+  static_assert((32 * V4) % NT == 0, "tile split");
+  if (need_total(needcount) < dense_min) return;   // the gathering kernel runs (uniform exit)
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  __bf16* xs = reinterpret_cast<__bf16*>(lds_raw);                                   // [2][3][32][RS]
+  double2* rs_l = reinterpret_cast<double2*>(lds_raw + (size_t)2 * 3 * 32 * RS * 2);  // [2][32]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int slab = (int)(blockIdx.x % (unsigned)nslab);
+  const int kb = (int)(blockIdx.x / (unsigned)nslab) * kTileBlocks + wave;
+  const bool active = kb < KB;
+
+  bf16x8 mb[NQ][4];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return __builtin_amdgcn_readfirstlane(v);
+  for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      bf16x8 z;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) z[e] = (__bf16)0.0f;
+      mb[q][t] = active ? mu3[(int64_t)kb * BLK + (q * 4 + t) * 64 + lane] : z;
+    }
+  }
+  double Cc = -INFINITY, bk = 0.0;
+  float mqf = 0.0f;
+  if (active) {
+    const double4 kc = kc_gat[(int64_t)kb * 32 + c];
+    Cc = kc.x; bk = kc.y; mqf = (float)kc.z;
+  }
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int64_t t_begin = r_begin / 32, t_end = r_end > r_begin ? cdiv(r_end, 32) : t_begin;
+
+  f32x4 st[LPT];
+  double2 rst = make_double2(0.0, INFINITY);
+  const bool full_d = (D == DP);
+  auto fetch = [&](int64_t t) {
+    const int64_t row0 = t * 32;
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int idx = u * NT + tid;
+      const int64_t row = row0 + idx / V4;
+      const int d0 = (idx % V4) * 4;
+      if (full_d && row < r_end)
+        st[u] = *reinterpret_cast<const f32x4*>(X + row * ldx + d0);
+      else
+        st[u] = load_row4(X, ldx, row, d0, D, row < r_end);
+    }
+    if (tid < 32) {
+      const int64_t row = row0 + tid;
+      rst = row < r_end ? rowstat[row] : make_double2(0.0, INFINITY);
+    }
+  };
+  // Split the staged tile into bf16 x1, x2, x3 (4 values per float4: two packed pairs).
+  auto commit = [&](int buf) {
+    __bf16* dst = xs + (size_t)buf * 3 * 32 * RS;
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int idx = u * NT + tid;
+      const int rr = idx / V4, d0 = (idx % V4) * 4;
+      uint2 w[3];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f32x2 a = {st[u][2 * j], st[u][2 * j + 1]};
+        const unsigned h = bf16_pair(a);
+        const f32x2 r = a - bf16_pair_widen(h);
+        const unsigned m = bf16_pair(r);
+        const unsigned l = bf16_pair(r - bf16_pair_widen(m));
+        (j == 0 ? w[0].x : w[0].y) = h;
+        (j == 0 ? w[1].x : w[1].y) = m;
+        (j == 0 ? w[2].x : w[2].y) = l;
+      }
+#pragma unroll
+      for (int sp = 0; sp < 3; ++sp) *reinterpret_cast<uint2*>(dst + (sp * 32 + rr) * RS + d0) = w[sp];
+    }
+    if (tid < 32) rs_l[buf * 32 + tid] = rst;
+  };
+
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
+  float nk = 0.0f, sig = 0.0f;
+  const bf16x8 ones = x6c_ones(lane);
+
+  if (t_begin < t_end) {
+    fetch(t_begin);
+    commit(0);
+  }
+  __syncthreads();
+  for (int64_t t = t_begin; t < t_end; ++t) {
+    const int buf = (int)((t - t_begin) & 1);
+    const bool more = t + 1 < t_end;
+    if (more) fetch(t + 1);
+    const unsigned m = active ? (dense ? ~0u : need[t * KB + kb]) : 0u;
+    if (m != 0u) {
+      const __bf16* xt = xs + (size_t)buf * 3 * 32 * RS;
+      bf16x8 xa[NQ][3];
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+        for (int sp = 0; sp < 3; ++sp)
+          xa[q][sp] = *reinterpret_cast<const bf16x8*>(xt + (sp * 32 + c) * RS + 16 * q + 8 * g);
+      }
+      const f32x16 S = x6c_tile_rows<NQ>(xa, ones, [&](int q, int t4) { return mb[q][t4]; });
+      const double2* rw = rs_l + buf * 32;
+      float r[16], res[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const double2 w = rw[acc_row(i, g)];
+        const double ll = fma(-bk, fma(-2.0, (double)S[i], w.x), Cc);
+        const float rv = fast_exp2((float)(ll - w.y));
+        r[i] = rv;
+        res[i] = rv - (float)(__bf16)rv;
+        nk += rv;
+        sig = fmaf(rv, fmaf(-2.0f, S[i], (float)w.x) + mqf, sig);
+      }
+      bf16x8 a1[2], a2[2];
+      acc_to_row_operands(r, a1);
+      acc_to_row_operands(res, a2);
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        if (dense || any_nonzero(a1[p])) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const bf16x8 b1 = lds_rows_operand(xt, RS, 16 * p, 32 * j, lane);
+            const bf16x8 b2 = lds_rows_operand(xt + 32 * RS, RS, 16 * p, 32 * j, lane);
+            acc[j] = mfma_bf16(a2[p], b1, acc[j]);
+            acc[j] = mfma_bf16(a1[p], b2, acc[j]);
+            acc[j] = mfma_bf16(a1[p], b1, acc[j]);
+          }
+        }
+      }
+    }
+    if (more) commit(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (active) {
+    nk += __shfl_xor(nk, 32);
+    sig += __shfl_xor(sig, 32);
+    const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[j][i];
+    }
+    if (g == 0) {
+      part_nk[kbase + c] = nk;
+      part_sig[kbase + c] = sig;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1852,6 +2056,9 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   if (!run2) return hipGetLastError();
   if constexpr (accum_uses_lds(DP)) {
     if (pl.need) {
+      // Both forms are launched; the needed-row count pass 1 left selects one on the
+      // device: the gathering kernel below a quarter of all (row, block) pairs.
+      const int64_t dense_min = cdiv(cdiv(pl.N, 32) * 32 * (int64_t)pl.KB, 4);
       constexpr size_t lds = gather_lds_bytes(DP);
       static_assert(lds <= kMaxLds, "gathering pass 2 exceeds LDS");
       hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_gather<DP>),
@@ -1861,7 +2068,19 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
                          dim3(64 * kGatherWaves), lds, stream, X, ldx, pl.N, (int)pl.D,
                          reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
                          reinterpret_cast<const double4*>(ws + pl.off_kcgat), pl.KB, pl.KP, rowstat,
-                         ljmask, pl.nslab, pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
+                         ljmask, ljcount, dense_min, pl.nslab, pl.rows_per_slab, pmu, pnk, psig,
+                         dense ? 1 : 0);
+      constexpr size_t lds_t = tiles_lds_bytes(DP);
+      static_assert(lds_t <= kMaxLds, "tile pass 2 exceeds LDS");
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_tiles<DP>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_t);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(iso_accum_tiles<DP>, dim3((unsigned)(pl.nslab * cdiv(pl.KB, kTileBlocks))),
+                         dim3(64 * kTileBlocks), lds_t, stream, X, ldx, pl.N, (int)pl.D,
+                         reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
+                         reinterpret_cast<const double4*>(ws + pl.off_kcgat), pl.KB, pl.KP, rowstat,
+                         ljmask, ljcount, dense_min, pl.nslab, pl.rows_per_slab, pmu, pnk, psig,
+                         dense ? 1 : 0);
       return hipGetLastError();
     }
   }

@@ -146,6 +146,9 @@ WORKLOADS = {
     "iso_n1m_k1024_d128": (iso_clustered, dict(N=1_000_000, K=1024, D=128), 1),
     "diag_n1m_k1024_d96": (diag_clustered, dict(N=1_000_000, K=1024, D=96), 2),
     "full_n250k_k256_d64": (full_clustered, dict(N=250_000, K=256, D=64), 3),
+    # the reference's own smoke workload (flash_gmm.py:228-234): nearly every
+    # responsibility is nonzero, so no accumulation work can be skipped
+    "iso_ref_n1m_k1024_d128": (reference_smoke, dict(N=1_000_000, K=1024, D=128), 0),
     # wider shapes (split-dimension accumulation paths)
     "diag_n1m_k256_d256": (diag_clustered, dict(N=1_000_000, K=256, D=256), 5),
     "full_n100k_k64_d128": (full_clustered, dict(N=100_000, K=64, D=128), 6),

@@ -233,9 +233,10 @@ def flash_gmm_estep(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tenso
 
 
 def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
-                    accumulate: bool = False, workspace: torch.Tensor | None = None,
-                    phase: int = 0, dense: bool = False, recompute: bool = False,
-                    store_log_joint: bool = False, precision: str = "fp32") -> None:
+                    accumulate: bool = False, atomic_reduce: bool = False,
+                    workspace: torch.Tensor | None = None, phase: int = 0, dense: bool = False,
+                    recompute: bool = False, store_log_joint: bool = False,
+                    precision: str = "fp32") -> None:
     """Diagonal-covariance E-step into caller-provided outputs (sig_acc is (K, D)).
 
     ``precision="bf16"`` selects the bf16 operand contract of the reference's
@@ -260,7 +261,7 @@ def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     ldmu = muk.stride(0) if K > 1 else D
     L = _lib.lib()
     _require(hasattr(L, "fgmm_diag_estep_f32"), "library built without the diagonal E-step")
-    flags = _plan_flags(_flags(accumulate, logZ, False, phase), dense, recompute, store_log_joint,
+    flags = _plan_flags(_flags(accumulate, logZ, atomic_reduce, phase), dense, recompute, store_log_joint,
                         precision)
     workspace, flags = _workspace(L.fgmm_diag_workspace_bytes_ex, N, K, D, flags, dev, workspace)
     _check_out("Nk", Nk, (K,), dev)
@@ -300,9 +301,10 @@ def flash_gmm_estep_diag(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.
 
 
 def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
-                    accumulate: bool = False, workspace: torch.Tensor | None = None,
-                    phase: int = 0, dense: bool = False, recompute: bool = False,
-                    store_log_joint: bool = False, precision: str = "fp32") -> None:
+                    accumulate: bool = False, atomic_reduce: bool = False,
+                    workspace: torch.Tensor | None = None, phase: int = 0, dense: bool = False,
+                    recompute: bool = False, store_log_joint: bool = False,
+                    precision: str = "fp32") -> None:
     """Full-covariance E-step into caller-provided outputs (sig_outer is (K, D, D)).
 
     ``precision="bf16"`` selects the bf16 operand contract of the reference's full
@@ -327,7 +329,7 @@ def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
     ldmu = muk.stride(0) if K > 1 else D
     L = _lib.lib()
     _require(hasattr(L, "fgmm_full_estep_f32"), "library built without the full-covariance E-step")
-    flags = _plan_flags(_flags(accumulate, logZ, False, phase), dense, recompute, store_log_joint,
+    flags = _plan_flags(_flags(accumulate, logZ, atomic_reduce, phase), dense, recompute, store_log_joint,
                         precision)
     workspace, flags = _workspace(L.fgmm_full_workspace_bytes_ex, N, K, D, flags, dev, workspace)
     _check_out("Nk", Nk, (K,), dev)

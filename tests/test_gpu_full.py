@@ -173,3 +173,21 @@ def test_rejects_bad_factor_shape(gpu_device):
     X, mu, L, lpi = (inp[k].to(gpu_device) for k in KEYS)
     with pytest.raises(AssertionError):
         flash_gmm_estep_full(X, mu, L[:, :4, :4], lpi)
+
+
+def test_atomic_reduce_matches_the_tree(gpu_device):
+    """FGMM_FLAG_ATOMIC_REDUCE: the partials added with float atomics agree with the
+    fixed-order tree to float32 rounding (accumulate included)."""
+    inp = data.full_clustered(5000, 200, 48, seed=9)
+    ref = _into(inp, gpu_device)
+    got = _into(inp, gpu_device, atomic_reduce=True)
+    assert torch.equal(got[0], ref[0])
+    for u, v in zip(got[1:], ref[1:]):
+        torch.testing.assert_close(u, v, rtol=1e-5, atol=1e-5 * float(v.abs().max()))
+    acc = [t.clone() for t in got]
+    acc_out = [None] + [t.clone() for t in got[1:]]
+    full_estep_into(*[inp[k].to(gpu_device) for k in KEYS], None,
+                    *acc_out[1:], accumulate=True, atomic_reduce=True)
+    torch.cuda.synchronize()
+    for u, v in zip(acc_out[1:], acc[1:]):
+        torch.testing.assert_close(u, 2 * v, rtol=1e-5, atol=1e-5 * float(v.abs().max()))
