@@ -575,7 +575,8 @@ __device__ __forceinline__ void lj_put_masks(const float* __restrict__ bmax, uns
 // (needed (row, block) pairs), from which the accumulation pass picks its form.
 template <typename RM>
 __device__ __forceinline__ void need_put_masks(RM rmax, unsigned* __restrict__ mask, unsigned* __restrict__ count,
-                                               int KB, int c, double lz2, bool valid, bool dense) {
+                                               int KB, int c, double lz2, bool valid, bool dense,
+                                               int mstride = 1) {
   const float zx = (float)lz2;
   const float zy = (lz2 > -INFINITY && lz2 < INFINITY) ? (float)(lz2 - (double)zx) : 0.0f;
   unsigned pairs = 0;
@@ -589,11 +590,54 @@ __device__ __forceinline__ void need_put_masks(RM rmax, unsigned* __restrict__ m
         const bool need = valid && (dense || !(((R[j] - zx) - zy) < -kLjNeedGap));
         const unsigned b = (unsigned)__builtin_amdgcn_ballot_w64(need);
         pairs += __builtin_popcount(b);
-        if (c == 0) mask[kb0 + j] = b;
+        if (c == 0) mask[(kb0 + j) * mstride] = b;
       }
     }
   }
-  if (c == 0 && pairs != 0) atomicAdd(count, pairs);
+  if (count && c == 0 && pairs != 0) atomicAdd(count, pairs);
+}
+
+// x6c_tile_rows with the rows' splits produced per chunk by loadX(q, xa[3]) (for
+// operands formed from other data, such as the diagonal model's [x^2, x] features):
+// the same products, order and chains, NCH chunks' splits live at a time.
+template <int NQ, int MAXCH, typename LX, typename LB>
+__device__ __forceinline__ f32x16 x6c_tile_rows_fn(LX loadX, const bf16x8 ones, LB loadB) {
+  constexpr int NCH = NQ < MAXCH ? NQ : MAXCH;
+  f32x16 acc[NCH];
+#pragma unroll
+  for (int h = 0; h < NCH; ++h) acc[h] = zero16();
+#pragma unroll
+  for (int q0 = 0; q0 < NQ; q0 += NCH) {
+    bf16x8 b[NCH][4], xa[NCH][3];
+#pragma unroll
+    for (int h = 0; h < NCH; ++h) {
+      if (q0 + h < NQ) {
+        loadX(q0 + h, xa[h]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) b[h][t] = loadB(q0 + h, t);
+      }
+    }
+#pragma unroll
+    for (int step = 0; step < 7; ++step) {
+#pragma unroll
+      for (int h = 0; h < NCH; ++h) {
+        if (q0 + h < NQ) {
+          const bf16x8 B = step == 0 ? b[h][1] : step == 1 ? b[h][2] : step <= 3 ? b[h][0]
+                         : step == 4 ? b[h][1] : step == 5 ? b[h][3] : b[h][0];
+          const bf16x8 A = step == 0 ? xa[h][1] : step == 1 ? xa[h][0] : step == 2 ? xa[h][2]
+                         : step == 3 ? xa[h][1] : step == 4 ? xa[h][0] : step == 5 ? ones : xa[h][0];
+          acc[h] = mfma_bf16(A, B, acc[h]);
+        }
+      }
+    }
+  }
+  f32x16 t = acc[0];
+#pragma unroll
+  for (int h = 1; h < NCH; ++h) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t[i] += acc[h][i];
+  }
+  return t;
 }
 
 // ---------------------------------------------------------------------------

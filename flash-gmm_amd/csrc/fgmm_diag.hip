@@ -83,9 +83,22 @@ struct DiagPlan {
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
   int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
   bool lj_sparse;   // the stored log-joint in the sparse form (pass 1 on the bf16 cores, D <= 128)
-  size_t off_musw, off_mu3, off_kcx6, off_kcblk, off_kclin, off_rowstat, off_part_mu, off_part_sq,
-      off_part_nk, off_lj, off_ljmax, off_ljmask, off_ljcount, total;
+  bool need;        // default plan up to D = 128: pass 1 leaves need masks, pass 2 gathers
+  bool rexact;      // need masks from block maxima kept in LDS (else the running-max bound)
+  size_t off_musw, off_mu3, off_kcx6, off_kcx6lin, off_kcblk, off_kclin, off_rowstat, off_part_mu,
+      off_part_sq, off_part_nk, off_lj, off_ljmax, off_ljmask, off_ljcount, total;
 };
+
+// Bytes of LDS the split-bf16 pass 1 uses at width DP (x6_lds_bytes, for the host).
+__host__ size_t x6_lds_bytes_rt(int DP);
+
+// Pass 1 with need masks keeps a bf16 bound of each row's half-block maximum in LDS,
+// 2 bytes per (row, block) for each of its 8 waves, up to the LDS left in a compute
+// unit; beyond that many blocks the masks come from the running-max bound.
+__host__ inline int need_exact_cap(int DP) {
+  const size_t base = x6_lds_bytes_rt(DP);
+  return base >= 160 * 1024 ? 0 : (int)((160 * 1024 - base) / (8 * 32 * 2));
+}
 
 // Pass 2 reads the stored log-joint when recomputation is not requested, there are
 // at least 4 component blocks, D > 32, and the tiles (one per pass-1 wave) fit
@@ -106,6 +119,8 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.KP = p.KB * 32;
   p.bf16 = bf16;
   p.lj = !bf16 && use_stored_lj(N, p.KB, p.DP, allow_lj);
+  p.need = !bf16 && !p.lj && diag_uses_x6(p.DP);
+  p.rexact = p.need && p.KB <= need_exact_cap(p.DP);
   if (bf16) {
     p.cpg = bf16_blocks_per_group(p.DP, p.KB);
     p.rgroups = kAccWaves / (p.cpg * bf16_parts(p.DP));
@@ -116,13 +131,23 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
     p.cpg = (p.KB >= 8 && p.DP <= 128) ? 8 : 4;
     p.lj_nh = (p.DP > 128 || (p.DP == 128 && p.cpg == 4)) ? 2 : 1;
     p.rgroups = kAccWaves / (p.cpg * p.lj_nh);
+  } else if (p.need) {
+    p.cpg = 1;        // one wave per (row slab, component block)
+    p.rgroups = 1;
   } else {
     p.cpg = diag_accum_split_d(p.DP) ? split_blocks(p.DP) : accum_blocks_per_group(p.DP, p.KB);
     p.rgroups = diag_accum_uses_lds(p.DP) ? kAccWaves / p.cpg : 1;
   }
   p.ncg = (int)cdiv(p.KB, p.cpg);
   const int64_t tile_rows = 32 * p.rgroups;
-  if (N > 0 && p.ncg > 0) {
+  if (p.need && N > 0 && p.KB > 0) {
+    // The gathering pass 2 runs one wave per SIMD: about two rounds of waves.
+    int64_t want = cdiv((int64_t)8 * current_device_cus(), p.KB);
+    const int64_t max_slabs = cdiv(N, 32);
+    if (want > max_slabs) want = max_slabs;
+    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.nslab = (int)cdiv(N, p.rows_per_slab);
+  } else if (N > 0 && p.ncg > 0) {
     int64_t want = (int64_t)current_device_cus() / p.ncg;
     if (want >= 8) want = (want / 8) * 8;
     if (want < 1) want = 1;
@@ -139,6 +164,7 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.off_musw = off;    off = align256(off + (size_t)p.KP * p.FP * sizeof(float));
   p.off_mu3 = off;     off = align256(off + (bf16 ? 0 : (size_t)p.KP * (p.DP / 8) * 4 * 2 * sizeof(bf16x8)));
   p.off_kcx6 = off;    off = align256(off + (bf16 ? 0 : (size_t)p.KP * sizeof(double)));
+  p.off_kcx6lin = off; off = align256(off + (bf16 ? 0 : (size_t)p.KP * sizeof(double)));
   p.off_kcblk = off;   off = align256(off + (size_t)p.KP * sizeof(double));
   p.off_kclin = off;   off = align256(off + (size_t)p.KP * sizeof(double));
   p.off_rowstat = off; off = align256(off + (size_t)(N > 0 ? N : 0) * sizeof(double));
@@ -148,11 +174,13 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   // One log-joint tile per pass-1 wave (the grid's 32-row tiles, rounded up to 4);
   // in the sparse form with each row's block maxima and the need masks, one half
   // (16 components) per pass-1 wave.
+  // The default plan keeps the need masks only: two words (one per half block) per
+  // (32-row tile, block), ORed by pass 2.
   p.lj_sparse = p.lj && diag_uses_x6(p.DP);
-  const size_t ntile = p.lj ? (size_t)round_up(cdiv(N, 32), 4) * p.KB : 0;
-  const size_t nsp = p.lj_sparse ? ntile : 0;
-  p.off_lj = off;      off = align256(off + ntile * kLjTile * sizeof(float));
-  p.off_ljmax = off;   off = align256(off + nsp * 64 * sizeof(float));
+  const size_t ntile = (p.lj || p.need) ? (size_t)round_up(cdiv(N, 32), 4) * p.KB : 0;
+  const size_t nsp = (p.lj_sparse || p.need) ? ntile : 0;
+  p.off_lj = off;      off = align256(off + (p.lj ? ntile * kLjTile * sizeof(float) : 0));
+  p.off_ljmax = off;   off = align256(off + (p.lj_sparse ? nsp * 64 * sizeof(float) : 0));
   p.off_ljmask = off;  off = align256(off + nsp * sizeof(uint2));
   p.off_ljcount = off; off = align256(off + (p.lj_sparse ? 64 * sizeof(unsigned) : 0));
   p.total = off;
@@ -384,7 +412,7 @@ __global__ __launch_bounds__(64) void diag_x6_prep(const float* __restrict__ mu,
                                                    const float* __restrict__ lss, int64_t ldlss, int64_t K,
                                                    int D, int DP, const float* __restrict__ lpi,
                                                    bf16x8* __restrict__ mu3, double* __restrict__ kc_x6,
-                                                   unsigned* __restrict__ ljcount) {
+                                                   double* __restrict__ kc_x6lin, unsigned* __restrict__ ljcount) {
   __shared__ double sC[32];
   const int kb = blockIdx.x;
   const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
@@ -445,6 +473,7 @@ __global__ __launch_bounds__(64) void diag_x6_prep(const float* __restrict__ mu,
       C = ((double)lpi[comp] - 0.5 * ((double)D * kLog2Pi + lsum)) * kLog2e - qs + osum;
     }
     sC[c] = C;
+    kc_x6lin[comp] = C;   // component order, for the gathering pass 2
   }
   __syncthreads();
   if (lane < 32) {
@@ -453,13 +482,19 @@ __global__ __launch_bounds__(64) void diag_x6_prep(const float* __restrict__ mu,
   }
 }
 
-template <int DP, bool LJ>
+// What pass 1 leaves for pass 2 besides logZ2.
+constexpr int kLjmNone = 0;    // nothing
+constexpr int kLjmStore = 1;   // the stored log-joint, its half-block maxima and need masks
+constexpr int kLjmNeed = 2;    // need masks only (the default plan)
+
+template <int DP, int LJM>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                  const bf16x8* __restrict__ mu3, const double* __restrict__ kc_x6, int KB,
                  float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj,
                  float* __restrict__ ljmax, unsigned* __restrict__ ljmask, unsigned* __restrict__ ljcount,
-                 int dense) {
+                 int dense, int rexact) {
+  constexpr bool LJ = LJM == kLjmStore;
   constexpr int NQ = DP / 8;              // chunks of 8 dimensions (16 features)
   constexpr int NQH = NQ / 2;             // per half
   constexpr int BLK = NQ * 4 * 64;        // bf16x8 per 32-component block
@@ -473,6 +508,8 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   bf16x8* mu_l = reinterpret_cast<bf16x8*>(p); p += (size_t)MB * BLK * sizeof(bf16x8);
   float* ex = reinterpret_cast<float*>(p);     p += (size_t)MB * kWaves * 16 * 64 * sizeof(float);
   double* kc_l = reinterpret_cast<double*>(p);
+  // Need masks: each wave's half-block maximum bounds, [wave][block][row] (rexact).
+  unsigned short* rmax_l = reinterpret_cast<unsigned short*>(lds_raw + x6_lds_bytes<DP>());
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -567,6 +604,19 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       if constexpr (LJ)
         lj_put_rows_g<2>(lj + (tile * KB + kb) * kLjTile, ljmax + ((tile * KB + kb) * 2 + H) * 32, c, g,
                          2 * H, ll, bm, acc, run_max, dense != 0);
+      if constexpr (LJM == kLjmNeed) {
+        const float R = lj_row_max(bm);   // the row's maximum over this wave's 16 components
+        if (rexact) {
+          if (g == 0) rmax_l[(wave * KB + kb) * 32 + c] = bf16_bits_up(R);
+        } else {
+          // As the isotropic pass 1: a half block kLjSkipGap below the half's running
+          // max cannot carry a nonzero responsibility (logZ2 is above both halves' maxima).
+          run_max = fmaxf(run_max, R);
+          const bool nb = valid && (dense != 0 || !(R - run_max < -kLjSkipGap));
+          const unsigned bits = (unsigned)__builtin_amdgcn_ballot_w64(nb);
+          if (lane == 0) ljmask[(tile * KB + kb) * 2 + H] = bits;
+        }
+      }
       if (MB == 1) lds_barrier();
     };
     for (int kb = 0; kb < KB; kb += 2) {
@@ -613,6 +663,19 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     if (g == 0)
       lj_put_masks(ljmax + tile * KB * 64 + h * 32, ljmask + tile * KB * 2 + h, ljcount + (tile & 63), KB, c,
                    lz2, valid, dense != 0, 64, 2);
+  }
+  if constexpr (LJM == kLjmNeed) {
+    if (rexact) {
+      const unsigned short* rm = rmax_l + wave * KB * 32 + c;
+      if (g == 0)
+        need_put_masks([&](int kb) { return bf16_bits_to_float(rm[kb * 32]); }, ljmask + tile * KB * 2 + h,
+                       nullptr, KB, c, lz2, valid, dense != 0, 2);
+    } else {
+      // A row whose logZ2 is NaN gets its bit in every block, as the exact test gives it.
+      const unsigned nanbits = (unsigned)__builtin_amdgcn_ballot_w64(valid && g == 0 && lz2 != lz2);
+      if (lane == 0 && nanbits != 0)
+        for (int kb = 0; kb < KB; ++kb) ljmask[(tile * KB + kb) * 2 + h] |= nanbits;
+    }
   }
 }
 
@@ -1598,6 +1661,200 @@ void diag_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D
   }
 }
 
+__host__ size_t x6_lds_bytes_rt(int DP) {
+  switch (DP) {
+    case 32: return x6_lds_bytes<32>();
+    case 64: return x6_lds_bytes<64>();
+    case 96: return x6_lds_bytes<96>();
+    case 128: return x6_lds_bytes<128>();
+    default: return 160 * 1024;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2 of the default plan (D <= 128): the log-joint is recomputed only for the
+// (row, component block) pairs whose need bit (either half's word) pass 1 set.
+// One wave per (row slab, component block), 4 waves of one block per workgroup on
+// consecutive slabs (the isotropic gathering kernel's structure), mu's split
+// features and centring offsets of the block in LDS for the four.  Per tile of 32
+// queued rows: the rows of X (fp32) go to the wave's LDS tile; S = [x^2, x] . [-w, 2v]^T
+// is formed as pass 1 forms it, the two halves' chains (x6c_tile_rows_fn, two chains
+// each) added in fp32, so the log-joint C'_k + S equals pass 1's; r = 2^(ll2 - logZ2),
+// Nk on the VALU, and r^T [X | X^2] on fp32 32x32x2 steps with r as the A operand
+// (steps whose 64 responsibilities are all zero are skipped).  sig follows in
+// diag_reduce from the moments.
+// ---------------------------------------------------------------------------
+constexpr int kGatherWaves = 4;
+
+__host__ __device__ constexpr int gather_rs(int DP) { return DP + 8; }   // fp32 row stride of the X tiles
+
+__host__ __device__ constexpr size_t gather_lds_bytes(int DP) {
+  return (size_t)(DP / 8) * 4 * 64 * 16                          // mu block (bf16x8 operands)
+         + (size_t)kGatherWaves * 32 * gather_rs(DP) * 4          // X tile per wave
+         + (size_t)kGatherWaves * 32 * sizeof(double)              // logZ2 per wave
+         + (size_t)kGatherWaves * 64 * sizeof(int);                // row queue per wave
+}
+__host__ __device__ constexpr int gather_groups(int nslab) { return (nslab + kGatherWaves - 1) / kGatherWaves; }
+__host__ inline int64_t gather_grid(int nslab, int KB) { return cdiv(gather_groups(nslab), 8) * (int64_t)KB * 8; }
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kGatherWaves, 64 * kGatherWaves),
+                          amdgpu_waves_per_eu(1, 1)))
+void diag_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                       const bf16x8* __restrict__ mu3, const double* __restrict__ kc_x6lin, int KB, int KP,
+                       const double* __restrict__ rowstat, const uint2* __restrict__ need, int nslab,
+                       int64_t rows_per_slab, float* __restrict__ part_mu, float* __restrict__ part_sq,
+                       float* __restrict__ part_nk, int dense) {
+  constexpr int NQ = DP / 8;      // chunks of 8 dimensions (16 features)
+  constexpr int NQH = NQ / 2;
+  constexpr int NJ = DP / 32;
+  constexpr int RS = gather_rs(DP);
+  constexpr int BLK = NQ * 4 * 64;
+  static_assert(NQ % 2 == 0, "two halves of chunks");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  unsigned char* lp = lds_raw;
+  bf16x8* mu_l = reinterpret_cast<bf16x8*>(lp);  lp += (size_t)BLK * sizeof(bf16x8);
+  float* xt_all = reinterpret_cast<float*>(lp);  lp += (size_t)kGatherWaves * 32 * RS * 4;
+  double* rs_all = reinterpret_cast<double*>(lp); lp += (size_t)kGatherWaves * 32 * sizeof(double);
+  int* q_all = reinterpret_cast<int*>(lp);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int rest = (int)(blockIdx.x >> 3);
+  const int kb = rest % KB;
+  const int sg = (rest / KB) * 8 + (int)(blockIdx.x & 7);
+  if (sg >= gather_groups(nslab)) return;   // uniform over the workgroup
+  for (int idx = tid; idx < BLK; idx += 64 * kGatherWaves) mu_l[idx] = mu3[(int64_t)kb * BLK + idx];
+  __syncthreads();
+  const int slab = sg * kGatherWaves + wave;
+  if (slab >= nslab) return;   // no barrier follows
+
+  float* xt = xt_all + wave * 32 * RS;
+  double* rs_l = rs_all + wave * 32;
+  int* q_l = q_all + wave * 64;
+  const double Cc = kc_x6lin[(int64_t)kb * 32 + c];
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int64_t t_begin = r_begin / 32, t_end = cdiv(r_end, 32);
+
+  auto words = [&](int64_t tb) -> unsigned {
+    const int64_t t = tb + lane;
+    if (t >= t_end) return 0u;
+    const uint2 w = need[t * KB + kb];
+    return w.x | w.y;
+  };
+  int64_t tb = t_begin;
+  unsigned mword = words(tb), mnext = words(tb + 64);
+  int jn = 0;
+  int qh = 0, qt = 0;
+  auto take = [&](int& e) -> int {
+    while (qt - qh < 32) {
+      const uint64_t live = jn >= 64 ? 0ull : (~0ull << jn);
+      const uint64_t nz = __builtin_amdgcn_ballot_w64(mword != 0u) & live;
+      if (nz == 0) {
+        tb += 64;
+        if (tb >= t_end) break;
+        mword = mnext;
+        mnext = words(tb + 64);
+        jn = 0;
+        continue;
+      }
+      const int j = __builtin_ctzll(nz);
+      const unsigned m = __builtin_amdgcn_readlane(mword, j);
+      const int base = (int)((tb + j - t_begin) * 32);
+      if (g == 0 && ((m >> c) & 1u)) q_l[(qt + __builtin_popcount(m & ((1u << c) - 1u))) & 63] = base + c;
+      qt += __builtin_popcount(m);
+      jn = j + 1;
+    }
+    const int cnt = qt - qh < 32 ? qt - qh : 32;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    e = c < cnt ? q_l[(qh + c) & 63] : -1;
+    qh += cnt;
+    return cnt;
+  };
+
+  // The tile in flight: lane (c, g) holds row c's dimensions 8q + 4g .. +3.
+  f32x4 raw[NQ];
+  double rst;
+  auto issue = [&](int e) {
+    const bool ok = e >= 0;
+    const int64_t row = r_begin + (ok ? e : 0);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) raw[q] = load_row4(X, ldx, row, 8 * q + 4 * g, D, ok);
+    rst = ok ? rowstat[row] : INFINITY;
+  };
+
+  f32x16 accx[NJ], accq[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    accx[j] = zero16();
+    accq[j] = zero16();
+  }
+  float nk = 0.0f;
+  const bf16x8 ones = x6c_ones(lane);
+
+  int e;
+  int cnt = take(e);
+  if (cnt > 0) issue(e);
+  while (cnt > 0) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the previous tile's LDS reads are done
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) *reinterpret_cast<f32x4*>(xt + c * RS + 8 * q + 4 * g) = raw[q];
+    if (g == 0) rs_l[c] = rst;
+    int en;
+    const int cnt_next = take(en);
+    if (cnt_next > 0) issue(en);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+    // [x^2, x] of chunk q, split three ways (pass 1's B operand, here the A operand).
+    auto loadX = [&](int q, bf16x8 (&xa)[3]) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * q + 4 * g);
+      split3_bf16(x * x, x, xa);
+    };
+    const f32x16 s0 = x6c_tile_rows_fn<NQH, 2>(loadX, ones, [&](int q, int t) { return mu_l[(q * 4 + t) * 64 + lane]; });
+    const f32x16 s1 = x6c_tile_rows_fn<NQH, 2>([&](int q, bf16x8 (&xa)[3]) { loadX(NQH + q, xa); }, ones,
+                                               [&](int q, int t) { return mu_l[((NQH + q) * 4 + t) * 64 + lane]; });
+    float r[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const double ll = Cc + (double)(s0[i] + s1[i]);
+      const float rv = fast_exp2((float)(ll - rs_l[acc_row(i, g)]));
+      r[i] = rv;
+      nk += rv;
+    }
+    const float* xbase = xt + 4 * g * RS + c;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int ro = 8 * (i >> 2) + (i & 3);
+      if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const float xv = xbase[ro * RS + 32 * j];
+          accx[j] = mfma32(r[i], xv, accx[j]);
+          accq[j] = mfma32(r[i], xv * xv, accq[j]);
+        }
+      }
+    }
+    cnt = cnt_next;
+  }
+
+  nk += __shfl_xor(nk, 32);
+  const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = accx[j][i];
+      part_sq[(kbase + acc_row(i, g)) * DP + 32 * j + c] = accq[j][i];
+    }
+  }
+  if (g == 0) part_nk[kbase + c] = nk;
+}
+
 // Finish: one thread per (k, d); fixed-order fp64 sums over partials, then the
 // sig identity in fp64.  Thread d == 0 also writes Nk.
 template <bool WIDE>
@@ -1676,19 +1933,19 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
   if (run1) {
     const unsigned nblk1 = (unsigned)cdiv(pl.N, 32 * kWaves);
     if constexpr (diag_uses_x6(DP)) {
-      constexpr size_t lds1 = x6_lds_bytes<DP>();
+      const size_t lds1 = x6_lds_bytes<DP>() + (pl.rexact ? (size_t)kAccWaves * 32 * pl.KB * 2 : 0);
+      auto kern = pl.lj ? &diag_lse_x6<DP, kLjmStore> : pl.need ? &diag_lse_x6<DP, kLjmNeed>
+                                                                : &diag_lse_x6<DP, kLjmNone>;
       if (lds1 > 65536) {
-        for (const void* f : {reinterpret_cast<const void*>(&diag_lse_x6<DP, false>),
-                              reinterpret_cast<const void*>(&diag_lse_x6<DP, true>)}) {
-          hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
-          if (e != hipSuccess) return e;
-        }
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+        if (e != hipSuccess) return e;
       }
-      auto kern = pl.lj ? &diag_lse_x6<DP, true> : &diag_lse_x6<DP, false>;
+      uint2* masks = pl.need ? reinterpret_cast<uint2*>(ws + pl.off_ljmask) : ljmask;
       hipLaunchKernelGGL(kern, dim3(nblk1), dim3(kAccThreads), lds1, stream, X, ldx, pl.N, (int)pl.D,
                          reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
                          reinterpret_cast<const double*>(ws + pl.off_kcx6), pl.KB, logZ, rowstat, lj,
-                         ljmax, reinterpret_cast<unsigned*>(ljmask), ljcount, dense ? 1 : 0);
+                         ljmax, reinterpret_cast<unsigned*>(masks), ljcount, dense ? 1 : 0, pl.rexact ? 1 : 0);
     } else {
       // Above D = 128 the rows' dimensions are split over two waves.
       constexpr size_t lds1 = lse_split_lds_bytes<DP>();
@@ -1707,6 +1964,20 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
   if (!run2) return hipGetLastError();
   const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
   if constexpr (diag_uses_x6(DP)) {
+    if (pl.need) {
+      constexpr size_t lds = gather_lds_bytes(DP);
+      static_assert(lds <= kMaxLds, "gathering pass 2 exceeds LDS");
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum_gather<DP>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(diag_accum_gather<DP>, dim3((unsigned)gather_grid(pl.nslab, pl.KB)),
+                         dim3(64 * kGatherWaves), lds, stream, X, ldx, pl.N, (int)pl.D,
+                         reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
+                         reinterpret_cast<const double*>(ws + pl.off_kcx6lin), pl.KB, pl.KP, rowstat,
+                         reinterpret_cast<const uint2*>(ws + pl.off_ljmask), pl.nslab, pl.rows_per_slab,
+                         pmu, psq, pnk, dense ? 1 : 0);
+      return hipGetLastError();
+    }
     if (pl.lj_sparse) {
       // Sparse masks (on average at most 2 needed register-row pairs per tile and
       // block) go to diag_accum_sparse where D is a multiple of 32; both kernels are
@@ -2349,6 +2620,7 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
       hipLaunchKernelGGL(diag_x6_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
                          (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_mu3),
                          reinterpret_cast<double*>(ws + pl.off_kcx6),
+                         reinterpret_cast<double*>(ws + pl.off_kcx6lin),
                          pl.lj_sparse ? reinterpret_cast<unsigned*>(ws + pl.off_ljcount) : nullptr);
   }
   if (N > 0) {
