@@ -7,6 +7,7 @@ HIP kernels in ``libflashgmm.so`` (C ABI: include/flashgmm.h):
     logZ, Nk, mu_acc, sig_acc = flash_gmm_estep(X, mu, log_sigma_sq, log_pi)
 """
 
+from . import datasets  # noqa: F401
 from ._lib import FlashGMMError  # noqa: F401
 from .em import (SynthIsoSource, em_diag, em_full, em_iso, mstep_diag, mstep_full,  # noqa: F401
                  mstep_iso, stream_em_iso)
@@ -16,4 +17,4 @@ from .estep import (diag_estep_into, flash_gmm_estep, flash_gmm_estep_diag,  # n
 __all__ = ["flash_gmm_estep", "flash_gmm_estep_diag", "flash_gmm_estep_full",
            "iso_estep_into", "diag_estep_into", "full_estep_into",
            "mstep_iso", "mstep_diag", "mstep_full", "em_iso", "em_diag", "em_full",
-           "stream_em_iso", "SynthIsoSource", "FlashGMMError"]
+           "stream_em_iso", "SynthIsoSource", "FlashGMMError", "datasets"]

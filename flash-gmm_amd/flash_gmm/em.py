@@ -220,8 +220,10 @@ def stream_em_iso(source: Union[SynthIsoSource, Callable[[int, int], np.ndarray]
                   var_floor: float = 0.0, exact_variance: bool = False) -> dict:
     """Streaming EM over N host rows; updates mu / log_sigma_sq / log_pi in place.
 
-    ``source`` is a SynthIsoSource or a callable ``f(row0, nrows) -> (nrows, D)``
-    float32 array.  Returns the driver's timing / memory report.
+    ``source`` is a native source (SynthIsoSource, datasets.VecsFile over a local
+    .fvecs / .bvecs / .fbin / .u8bin file) or a callable ``f(row0, nrows) ->
+    (nrows, D)`` float32 array (datasets.TextEmbeddingFile is one).  Returns the
+    driver's timing / memory report.
     """
     K, D = mu.shape
     for t in (mu, log_sigma_sq, log_pi):
@@ -232,9 +234,13 @@ def stream_em_iso(source: Union[SynthIsoSource, Callable[[int, int], np.ndarray]
                     MSTEP_EXACT_VARIANCE if exact_variance else 0)
     rep = _EmReport()
     keep = None
-    if isinstance(source, SynthIsoSource):
+    if hasattr(source, "fn") and hasattr(source, "user"):
+        # A native source (SynthIsoSource, datasets.VecsFile): the C callback runs
+        # on the driver's thread with no Python in between.
         if source.D != D:
             raise FlashGMMError("source dimension does not match mu")
+        if getattr(source, "N", N) < N:
+            raise FlashGMMError(f"the source holds {source.N} rows, fewer than N={N}")
         fn, user = source.fn, source.user
     else:
         def _cb(user, row0, nrows, d, dst):

@@ -216,6 +216,34 @@ typedef struct fgmm_synth_iso {
 
 int fgmm_synth_iso_source(void *user, int64_t row0, int64_t nrows, int64_t D, float *dst);
 
+/* Row sources over local vector files, the layouts the reference's tuning    */
+/* data sets are distributed in (SIFT1M, GIST1M: .fvecs; SIFT1B: .bvecs;       */
+/* Deep1B / Deep10M: .fbin, .u8bin; flash_gmm_diag_h100.py:17,299-301 names    */
+/* SIFT1M, GloVe and Deep10M, and the reference ships no reader).  The file is */
+/* memory-mapped; N and D come from its headers; byte values become floats.    */
+/* fgmm_vecs_open returns FGMM_ERR_SOURCE when the file cannot be opened or    */
+/* mapped and FGMM_ERR_INVALID_ARG for a malformed header.  Pass the           */
+/* fgmm_vecs_file as the `user` of fgmm_vecs_source.                           */
+/* ------------------------------------------------------------------------ */
+enum fgmm_vecs_format {
+    FGMM_VECS_FVECS = 0,   /* per vector: int32 d, then d float32 */
+    FGMM_VECS_BVECS = 1,   /* per vector: int32 d, then d uint8 */
+    FGMM_VECS_FBIN = 2,    /* uint32 n, uint32 d, then n*d float32 */
+    FGMM_VECS_U8BIN = 3,   /* uint32 n, uint32 d, then n*d uint8 */
+};
+
+typedef struct fgmm_vecs_file {
+    void *base;            /* mapping (owned; release with fgmm_vecs_close) */
+    size_t bytes;
+    int64_t N, D;          /* vectors and dimensions in the file */
+    int format;            /* fgmm_vecs_format */
+    int threads;           /* host threads per chunk; 0 = all hardware threads */
+} fgmm_vecs_file;
+
+int fgmm_vecs_open(const char *path, int format, int threads, fgmm_vecs_file *f);
+int fgmm_vecs_source(void *user, int64_t row0, int64_t nrows, int64_t D, float *dst);
+void fgmm_vecs_close(fgmm_vecs_file *f);
+
 /* ------------------------------------------------------------------------ */
 /* Isotropic M-step on the device (README.md:59-61):                          */
 /*   log_pi = log(Nk / N),  mu = mu_acc / Nk,                                 */

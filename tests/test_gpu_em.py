@@ -176,3 +176,31 @@ def test_em_diag_and_full_loglik_non_decreasing(gpu_device):
     X, mu, L, lpi = (inp[k].to(dev) for k in ("X", "mu", "prec_chol", "log_pi"))
     ll = em_full(X, mu, L, lpi, 6, reg_covar=1e-6)
     assert all(b >= a - 1e-6 * abs(a) for a, b in zip(ll, ll[1:])), ll
+
+
+def test_stream_em_c5_shape_against_the_oracle(gpu_device):
+    """The streaming driver at the shape of the 1e9-row workload (K=1024, D=128), on
+    N=2M rows in four 512K-row chunks, one iteration: the M-step it applies and the
+    log-likelihood it reports against the float64 oracle's E-step over the same host
+    rows followed by the README M-step (README.md:59-61).  The accumulated Nk,
+    mu_acc and sig_acc enter the three parameters: log pi = log(Nk / N) within
+    1e-4 + 1e-4 (Nk relative), mu = mu_acc / Nk, sigma^2 = sig_acc / (D Nk)."""
+    dev = gpu_device
+    K, D, N, chunk = 1024, 128, 2_000_000, 1 << 19
+    centres, mu, lss, lpi = _params(K, D, 25, dev)
+    src = SynthIsoSource(centres.numpy(), seed=4)
+    mu0, lss0, lpi0 = mu.cpu().clone(), lss.cpu().clone(), lpi.cpu().clone()
+    rep = stream_em_iso(src, N, mu, lss, lpi, iterations=1, chunk_rows=chunk)
+    torch.cuda.synchronize()
+    assert rep["iterations"] == 1
+    print("C5-shape oracle over 2M streamed rows (float64, CPU)", flush=True)
+    X = torch.from_numpy(src.rows(0, N))
+    logZ, Nk, mu_acc, sig = O.estep_iso(X, mu0, lss0, lpi0)
+    assert float(Nk.min()) > 100          # every component is populated: no empty-component rule
+    pi, m, s2 = O.mstep_iso(Nk, mu_acc, sig, N, D)
+    scale = float(m.abs().max())
+    assert float((mu.double().cpu() - m).abs().max()) <= 2e-4 * scale
+    assert float((lss.double().cpu() - torch.log(s2)).abs().max()) <= 3e-4
+    assert float((lpi.double().cpu() - torch.log(pi)).abs().max()) <= 2e-4
+    ll = float(logZ.sum())
+    assert abs(rep["loglik"][0] - ll) <= 1e-4 * N
