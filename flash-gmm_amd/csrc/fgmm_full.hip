@@ -34,6 +34,7 @@
 
 #include <math.h>
 
+#include <algorithm>
 #include <type_traits>
 
 namespace fgmm {
@@ -59,9 +60,18 @@ struct FullPlan {
   int64_t rows_per_slab;
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
   bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16); always stores the log-joint
+  bool need;    // default plan up to D = 64: pass 1 leaves need masks, pass 2 gathers
+  bool rexact;  // need masks from the per-(row, component) bounds (else the running max)
+  int grid1;    // pass-1 workgroups with need masks (a persistent grid)
   size_t off_lsw, off_bsw, off_ck, off_l3, off_esw, off_rowstat, off_part_sig, off_part_mu, off_part_nk,
-      off_lj, total;
+      off_lj, off_need, off_bound, total;
 };
+
+// Need masks of the full model are per (32-row tile, component).  Pass 1 then runs a
+// persistent grid of grid1 workgroups, each wave with a slot of 32 x KP bf16 bounds
+// of its rows' log-joint in the workspace, reused tile after tile; beyond this many
+// components the masks come from the running-max bound instead.
+constexpr int kNeedExactMaxK = 1024;
 
 
 
@@ -86,18 +96,31 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.KP = (int)round_up(K, kCompsPerWG);
   p.bf16 = bf16;
   p.lj = (allow_lj || bf16) && K > 0 && full_lj_bytes(N, p.KP) <= kMaxLjBytes;
+  p.need = !bf16 && !p.lj && K > 0 && p.DP <= 64;
+  p.rexact = p.need && K <= kNeedExactMaxK;
   // Reading the log-joint, pass 2 needs no whitening operands in LDS, and the
   // 4-component kernel serves every D.
   const bool split = full_accum_split_d(p.DP) && !p.lj && !bf16;
   if (bf16) {
     p.ncg = p.KP / bf16_comps_per_wg(p.NMB);
     p.rgroups = bf16_row_groups(p.NMB);
+  } else if (p.need) {
+    p.ncg = (int)K;   // one wave per (row slab, component)
+    p.rgroups = 1;
   } else {
     p.ncg = split ? (int)K : p.KP / kCompsPerWG;
     p.rgroups = split ? 1 : kRowGroups;
   }
   const int64_t tile_rows = 32 * p.rgroups;
-  if (N > 0 && p.ncg > 0) {
+  if (p.need && N > 0) {
+    // The gathering pass 2: about two rounds of waves at two waves per SIMD (each
+    // slab holds a partial of D x D per component, so no more slabs than that).
+    int64_t want = cdiv((int64_t)8 * current_device_cus(), K);
+    const int64_t max_slabs = cdiv(N, 32);
+    if (want > max_slabs) want = max_slabs;
+    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.nslab = (int)cdiv(N, p.rows_per_slab);
+  } else if (N > 0 && p.ncg > 0) {
     int64_t want = (int64_t)current_device_cus() / p.ncg;
     if (want >= 8) want = (want / 8) * 8;
     if (want < 1) want = 1;
@@ -115,7 +138,7 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.off_bsw = off;      off = align256(off + (size_t)p.KP * p.DP * sizeof(double));
   p.off_ck = off;       off = align256(off + (size_t)p.KP * sizeof(double));
   // Split-bf16 operands of pass 1: 4 bf16x8 per (16 dimensions, 32 coordinates, lane).
-  const bool x6 = !bf16 && p.lj;
+  const bool x6 = !bf16 && (p.lj || p.need);
   p.off_l3 = off;
   if (x6) off = align256(off + (size_t)p.KP * (p.DP / 32) * (p.DP / 16) * 4 * 64 * sizeof(bf16x8));
   p.off_esw = off;
@@ -127,6 +150,15 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.off_part_nk = off;  off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
   p.off_lj = off;
   if (p.lj) off = align256(off + full_lj_bytes(N, p.KP));
+  // Need masks: one word per (32-row tile of the pass-1 grid, component).
+  p.grid1 = 0;
+  p.off_need = off;
+  if (p.need) off = align256(off + (size_t)round_up(cdiv(N, 32), 4) * p.KP * sizeof(unsigned));
+  p.off_bound = off;
+  if (p.need && N > 0) {
+    p.grid1 = (int)std::min<int64_t>(cdiv(N, 32 * kWaves), (int64_t)2 * current_device_cus());
+    if (p.rexact) off = align256(off + (size_t)p.grid1 * kWaves * 32 * p.KP * sizeof(unsigned short));
+  }
   p.total = off;
   return p;
 }
@@ -376,11 +408,24 @@ constexpr size_t full_x6_lds_bytes() {
   return (size_t)2 * full_x6_stage<DP>() * sizeof(bf16x8) + (size_t)2 * (32 * full_x6_smb<DP>() + 8) * sizeof(double);
 }
 
-template <int DP, bool LJ>
+// What pass 1 leaves for pass 2 besides logZ2.
+constexpr int kLjmNone = 0;    // nothing
+constexpr int kLjmStore = 1;   // the stored log-joint
+constexpr int kLjmNeed = 2;    // need masks only (the default plan)
+
+// With need masks (LJM == kLjmNeed) the grid is persistent: workgroup b takes the
+// 128-row tiles b, b + gridDim.x, ...; wave w of workgroup b keeps the bf16 upper
+// bounds of its rows' log-joint, [component][row], in slot 4 b + w of `bound` (its
+// own writes, read back by the same lanes once logZ2 is final), and writes the need
+// word of each (32-row tile, component): bit r set unless the bound of row r is
+// kLjNeedGap below its logZ2 (need_put_masks).
+template <int DP, int LJM>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
 void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, const bf16x8* __restrict__ l3,
                  const double* __restrict__ esw, const double* __restrict__ ck, int K, int KP,
-                 float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj) {
+                 float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj,
+                 unsigned* __restrict__ need, unsigned short* __restrict__ bound, int rexact, int dense) {
+  constexpr bool LJ = LJM == kLjmStore;
   constexpr int NMB = DP / 32, NQ = DP / 16;
   constexpr int SMB = full_x6_smb<DP>();          // coordinate blocks per stage
   constexpr int NST = NMB / SMB;                  // stages per component
@@ -397,7 +442,13 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, g = lane >> 5;
-  const int64_t tile = (int64_t)blockIdx.x * kWaves + wave;   // 32-row tile
+  const int64_t ntw = cdiv(N, 32 * kWaves);
+  const int64_t tw_step = LJM == kLjmNeed ? (int64_t)gridDim.x : ntw;
+  unsigned short* bnd = LJM == kLjmNeed && rexact
+                            ? bound + ((int64_t)blockIdx.x * kWaves + wave) * 32 * KP : nullptr;
+
+  for (int64_t tw = blockIdx.x; tw < ntw; tw += tw_step) {
+  const int64_t tile = tw * kWaves + wave;   // 32-row tile
   const int64_t row = tile * 32 + c;
   const bool valid = row < N;
   // Both half-waves hold row c's log-joint; both store it (same value, same address).
@@ -434,6 +485,7 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
   const double hl = 0.5 * kLog2e;
   double mx = -INFINITY;
   float sm = 0.0f;
+  float run_max = -INFINITY;   // need masks from the running max (not rexact)
   const int64_t nstage = (int64_t)K * NST;
   double maha = 0.0;
   for (int64_t s = 0; s < nstage; ++s) {
@@ -459,6 +511,19 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
       maha += __shfl_xor(maha, 32);
       const double ll = ec[NE] - hl * maha;
       if constexpr (LJ) ljt[(s / NST) * 32] = (float)ll;
+      if constexpr (LJM == kLjmNeed) {
+        const int64_t k = s / NST;
+        if (rexact) {
+          if (g == 0) bnd[k * 32 + c] = bf16_bits_up((float)ll);
+        } else {
+          // logZ2 >= the row's final maximum >= run_max (less a rounding), so a
+          // component kLjSkipGap below the running max cannot reach need_put_masks' test.
+          run_max = fmaxf(run_max, (float)ll);
+          const bool nb = valid && (dense != 0 || !((float)ll - run_max < -kLjSkipGap));
+          const unsigned bits = (unsigned)__builtin_amdgcn_ballot_w64(nb);
+          if (lane == 0) need[tile * KP + k] = bits;
+        }
+      }
       const double mn = fmax(mx, ll);
       const double ms = (mn == -INFINITY) ? 0.0 : mn;
       sm = sm * fast_exp2((float)(mx - ms)) + fast_exp2((float)(ll - ms));
@@ -472,6 +537,19 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
   if (valid && g == 0) {
     rowstat[row] = lz2;
     if (logZ) logZ[row] = (float)(lz2 * kLn2);
+  }
+  if constexpr (LJM == kLjmNeed) {
+    if (rexact) {
+      if (g == 0)
+        need_put_masks([&](int k) { return bf16_bits_to_float(bnd[(int64_t)k * 32 + c]); }, need + tile * KP,
+                       nullptr, K, c, lz2, valid, dense != 0);
+    } else {
+      // A row whose logZ2 is NaN gets its bit for every component, as the exact test gives it.
+      const unsigned nanbits = (unsigned)__builtin_amdgcn_ballot_w64(valid && g == 0 && lz2 != lz2);
+      if (lane == 0 && nanbits != 0)
+        for (int k = 0; k < K; ++k) need[tile * KP + k] |= nanbits;
+    }
+  }
   }
 }
 
@@ -922,6 +1000,224 @@ __global__ __launch_bounds__(256) void full_fill(float* __restrict__ p, int64_t 
   if (i < n) p[i] = v;
 }
 
+// ---------------------------------------------------------------------------
+// Pass 2 of the default plan (D <= 64): the whitening is recomputed only for the
+// (row, component) pairs whose need bit pass 1 set.  One wave per (row slab,
+// component); a workgroup holds 4 waves of one component on consecutive slabs,
+// with the component's split-bf16 operands (pass 1's l3, esw and c) in LDS.  Each
+// wave walks its slab's need words for the component and queues the needed rows;
+// per tile of 32 queued rows it stages the rows of X in its LDS tile, whitens them
+// as pass 1 does (x6c_tile over the coordinate blocks, the same operands and order,
+// so maha and the log-joint are pass 1's), forms r = 2^(ll2 - logZ2), and then
+// accumulates Nk, mu_acc and the upper 32x32 blocks of sig_outer = sum r x x^T as
+// full_accum does (r-scaled rows as the A operand of fp32 32x32x2 steps, only the
+// steps with a nonzero row).  Workgroups map to the 8 XCDs so that every component
+// of a slab group shares an XCD's L2 for the rows of X.
+// ---------------------------------------------------------------------------
+constexpr int kGatherWaves = 4;
+
+template <int DP>
+constexpr size_t gather_lds_bytes() {
+  return (size_t)(DP / 32) * (DP / 16) * 4 * 64 * sizeof(bf16x8)   // the component's operands
+         + (size_t)(DP + 8) * sizeof(double)                        // e, then c
+         + (size_t)kGatherWaves * 32 * (DP + 4) * sizeof(float)     // X tile per wave
+         + (size_t)kGatherWaves * 32 * sizeof(double)                // logZ2 per wave
+         + (size_t)kGatherWaves * 32 * sizeof(float)                 // r per wave
+         + (size_t)kGatherWaves * 64 * sizeof(int);                  // row queue per wave
+}
+__host__ __device__ constexpr int gather_groups(int nslab) { return (nslab + kGatherWaves - 1) / kGatherWaves; }
+__host__ inline int64_t gather_grid(int nslab, int K) { return cdiv(gather_groups(nslab), 8) * (int64_t)K * 8; }
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kGatherWaves, 64 * kGatherWaves),
+                          amdgpu_waves_per_eu(2, 2)))
+void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                       const bf16x8* __restrict__ l3, const double* __restrict__ esw,
+                       const double* __restrict__ ck, int K, int KP, const double* __restrict__ rowstat,
+                       const unsigned* __restrict__ need, int nslab, int64_t rows_per_slab,
+                       float* __restrict__ part_sig, float* __restrict__ part_mu, float* __restrict__ part_nk,
+                       int dense) {
+  constexpr int NMB = DP / 32, NQ = DP / 16, NSB = NMB * (NMB + 1) / 2;
+  constexpr int RS = DP + 4;
+  constexpr int BLK = NMB * NQ * 4 * 64;   // bf16x8 per component
+  static_assert(DP <= 64, "one component's operands per workgroup");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  unsigned char* lp = lds_raw;
+  bf16x8* l_l = reinterpret_cast<bf16x8*>(lp);   lp += (size_t)BLK * sizeof(bf16x8);
+  double* e_l = reinterpret_cast<double*>(lp);   lp += (size_t)(DP + 8) * sizeof(double);
+  float* xt_all = reinterpret_cast<float*>(lp);  lp += (size_t)kGatherWaves * 32 * RS * sizeof(float);
+  double* rs_all = reinterpret_cast<double*>(lp); lp += (size_t)kGatherWaves * 32 * sizeof(double);
+  float* r_all = reinterpret_cast<float*>(lp);   lp += (size_t)kGatherWaves * 32 * sizeof(float);
+  int* q_all = reinterpret_cast<int*>(lp);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int rest = (int)(blockIdx.x >> 3);
+  const int k = rest % K;
+  const int sg = (rest / K) * 8 + (int)(blockIdx.x & 7);
+  if (sg >= gather_groups(nslab)) return;   // uniform over the workgroup
+  for (int idx = tid; idx < BLK; idx += 64 * kGatherWaves) l_l[idx] = l3[(int64_t)k * BLK + idx];
+  for (int idx = tid; idx <= DP; idx += 64 * kGatherWaves) e_l[idx] = idx < DP ? esw[(int64_t)k * DP + idx] : ck[k];
+  __syncthreads();
+  const int slab = sg * kGatherWaves + wave;
+  if (slab >= nslab) return;   // no barrier follows
+
+  float* xt = xt_all + wave * 32 * RS;
+  double* rs_l = rs_all + wave * 32;
+  float* rx = r_all + wave * 32;
+  int* q_l = q_all + wave * 64;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int64_t t_begin = r_begin / 32, t_end = cdiv(r_end, 32);
+
+  auto words = [&](int64_t tb) -> unsigned {
+    const int64_t t = tb + lane;
+    return t < t_end ? need[t * KP + k] : 0u;
+  };
+  int64_t tb = t_begin;
+  unsigned mword = words(tb), mnext = words(tb + 64);
+  int jn = 0;
+  int qh = 0, qt = 0;
+  auto take = [&](int& e) -> int {
+    while (qt - qh < 32) {
+      const uint64_t live = jn >= 64 ? 0ull : (~0ull << jn);
+      const uint64_t nz = __builtin_amdgcn_ballot_w64(mword != 0u) & live;
+      if (nz == 0) {
+        tb += 64;
+        if (tb >= t_end) break;
+        mword = mnext;
+        mnext = words(tb + 64);
+        jn = 0;
+        continue;
+      }
+      const int j = __builtin_ctzll(nz);
+      const unsigned m = __builtin_amdgcn_readlane(mword, j);
+      const int base = (int)((tb + j - t_begin) * 32);
+      if (g == 0 && ((m >> c) & 1u)) q_l[(qt + __builtin_popcount(m & ((1u << c) - 1u))) & 63] = base + c;
+      qt += __builtin_popcount(m);
+      jn = j + 1;
+    }
+    const int cnt = qt - qh < 32 ? qt - qh : 32;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    e = c < cnt ? q_l[(qh + c) & 63] : -1;
+    qh += cnt;
+    return cnt;
+  };
+
+  // The tile in flight: lane (c, g) holds row c's dimensions 16q + 8g .. +7.
+  f32x4 raw[2 * NQ];
+  double rst;
+  auto issue = [&](int e) {
+    const bool ok = e >= 0;
+    const int64_t row = r_begin + (ok ? e : 0);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      raw[2 * q] = load_row4(X, ldx, row, 16 * q + 8 * g, D, ok);
+      raw[2 * q + 1] = load_row4(X, ldx, row, 16 * q + 8 * g + 4, D, ok);
+    }
+    rst = ok ? rowstat[row] : INFINITY;
+  };
+
+  f32x16 acc[NSB];
+#pragma unroll
+  for (int sb = 0; sb < NSB; ++sb) acc[sb] = zero16();
+  float mua[NMB];
+#pragma unroll
+  for (int mb = 0; mb < NMB; ++mb) mua[mb] = 0.0f;
+  float nk = 0.0f;
+  const bf16x8 ones = x6c_ones(lane);
+  const double hl = 0.5 * kLog2e;
+
+  int e;
+  int cnt = take(e);
+  if (cnt > 0) issue(e);
+  while (cnt > 0) {
+    bf16x8 xb[NQ][3];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) split3_bf16(raw[2 * q], raw[2 * q + 1], xb[q]);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the previous tile's LDS reads are done
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      *reinterpret_cast<f32x4*>(xt + c * RS + 16 * q + 8 * g) = raw[2 * q];
+      *reinterpret_cast<f32x4*>(xt + c * RS + 16 * q + 8 * g + 4) = raw[2 * q + 1];
+    }
+    const double lz2 = rst;
+    int en;
+    const int cnt_next = take(en);
+    if (cnt_next > 0) issue(en);
+
+    // maha of row c as pass 1 forms it (lane = row, register = coordinate).
+    double maha = 0.0;
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+      const f32x16 t = x6c_tile<NQ, 1>([&](int q, int u) { return l_l[((mb * NQ + q) * 4 + u) * 64 + lane]; },
+                                       xb, ones);
+      const double* eb = e_l + mb * 32 + g * 16;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const double v = (double)t[i] + eb[i];
+        maha = fma(v, v, maha);
+      }
+    }
+    maha += __shfl_xor(maha, 32);
+    const double ll = e_l[DP] - hl * maha;
+    const float rv = fast_exp2((float)(ll - lz2));
+    if (g == 0) {
+      nk += rv;
+      rx[c] = rv;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // sig_outer[d1][d2] += sum_rows (r x_d1) x_d2, as full_accum: step s takes rows
+    // r0 + 4g (r0 = 8 (s >> 2) + (s & 3)); only the steps with a nonzero row.
+    const unsigned nz = (unsigned)__builtin_amdgcn_ballot_w64(rv != 0.0f);
+    unsigned pm = dense ? 0x0f0f0f0fu : lj_pair_mask(nz);
+    while (pm != 0u) {
+      const int r0 = __builtin_ctz(pm);
+      pm &= pm - 1u;
+      const int rw = r0 + 4 * g;
+      const float rr = rx[rw];
+      float xv[NMB], av[NMB];
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) {
+        xv[mb] = xt[rw * RS + 32 * mb + c];
+        av[mb] = rr * xv[mb];
+        mua[mb] += av[mb];
+      }
+      int sb = 0;
+#pragma unroll
+      for (int m1 = 0; m1 < NMB; ++m1) {
+#pragma unroll
+        for (int m2 = m1; m2 < NMB; ++m2) {
+          acc[sb] = mfma32(av[m1], xv[m2], acc[sb]);
+          ++sb;
+        }
+      }
+    }
+    cnt = cnt_next;
+  }
+
+  const int64_t pbase = (int64_t)slab * KP + k;
+  float* ps = part_sig + pbase * NSB * 1024;
+#pragma unroll
+  for (int sb = 0; sb < NSB; ++sb) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ps[sb * 1024 + acc_row(i, g) * 32 + c] = acc[sb][i];
+  }
+#pragma unroll
+  for (int mb = 0; mb < NMB; ++mb) {
+    const float v = mua[mb] + __shfl_xor(mua[mb], 32);
+    if (g == 0) part_mu[pbase * DP + 32 * mb + c] = v;
+  }
+  float nks = nk;
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) nks += __shfl_xor(nks, o);
+  if (lane == 0) part_nk[pbase] = nks;
+}
+
 template <int DP>
 hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
                          float* logZ, bool run1, bool run2, bool dense, hipStream_t stream) {
@@ -934,7 +1230,7 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
     return bytes > 65536 ? hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes)
                          : hipSuccess;
   };
-  if (run1 && !pl.lj) {
+  if (run1 && !pl.lj && !pl.need) {
     constexpr size_t lds1 = lse_lds_bytes<DP>();
     hipError_t e = set_lds(reinterpret_cast<const void*>(&full_lse<DP, false>), lds1);
     if (e != hipSuccess) return e;
@@ -942,22 +1238,38 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
                        stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, logZ, rowstat, lj);
   } else if (run1) {
     constexpr size_t lds1 = full_x6_lds_bytes<DP>();
-    for (const void* f : {reinterpret_cast<const void*>(&full_lse_x6<DP, false>),
-                          reinterpret_cast<const void*>(&full_lse_x6<DP, true>)}) {
-      hipError_t e = set_lds(f, lds1);
-      if (e != hipSuccess) return e;
+    auto kern = &full_lse_x6<DP, kLjmStore>;
+    if constexpr (DP <= 64) {
+      if (pl.need) kern = &full_lse_x6<DP, kLjmNeed>;
     }
-    auto kern = pl.lj ? &full_lse_x6<DP, true> : &full_lse_x6<DP, false>;
-    hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1, stream, X, ldx,
+    hipError_t e = set_lds(reinterpret_cast<const void*>(kern), lds1);
+    if (e != hipSuccess) return e;
+    const unsigned grid1 = pl.need ? (unsigned)pl.grid1 : (unsigned)cdiv(pl.N, 32 * kWaves);
+    hipLaunchKernelGGL(kern, dim3(grid1), dim3(kThreads), lds1, stream, X, ldx,
                        pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
                        reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, logZ,
-                       rowstat, lj);
+                       rowstat, lj, reinterpret_cast<unsigned*>(ws + pl.off_need),
+                       reinterpret_cast<unsigned short*>(ws + pl.off_bound), pl.rexact ? 1 : 0, dense ? 1 : 0);
   }
   if (!run2) return hipGetLastError();
   float* psig = reinterpret_cast<float*>(ws + pl.off_part_sig);
   float* pmu = reinterpret_cast<float*>(ws + pl.off_part_mu);
   float* pnk = reinterpret_cast<float*>(ws + pl.off_part_nk);
   const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
+  if constexpr (DP <= 64) {
+    if (pl.need) {
+      constexpr size_t lds2 = gather_lds_bytes<DP>();
+      hipError_t e = set_lds(reinterpret_cast<const void*>(&full_accum_gather<DP>), lds2);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL((full_accum_gather<DP>), dim3((unsigned)gather_grid(pl.nslab, (int)pl.K)),
+                         dim3(64 * kGatherWaves), lds2, stream, X, ldx, pl.N, (int)pl.D,
+                         reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
+                         reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, rowstat,
+                         reinterpret_cast<const unsigned*>(ws + pl.off_need), pl.nslab, pl.rows_per_slab, psig,
+                         pmu, pnk, dense ? 1 : 0);
+      return hipGetLastError();
+    }
+  }
   auto launch2 = [&](auto lj_tag) -> hipError_t {
     constexpr bool LJ = decltype(lj_tag)::value;
     if constexpr (!LJ && full_accum_split_d(DP)) {
@@ -1472,7 +1784,7 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
                        (int)D, pl.DP, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_lsw),
                        reinterpret_cast<double*>(ws + pl.off_bsw),
                        reinterpret_cast<double*>(ws + pl.off_ck));
-  if (run1 && !bf16 && pl.lj)
+  if (run1 && !bf16 && (pl.lj || pl.need))
     hipLaunchKernelGGL(full_x6_prep, dim3((unsigned)pl.KP), dim3(64), 0, stream, mu, ldmu, prec_chol, K,
                        (int)D, pl.DP, reinterpret_cast<bf16x8*>(ws + pl.off_l3),
                        reinterpret_cast<double*>(ws + pl.off_esw));

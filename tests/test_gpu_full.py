@@ -14,7 +14,7 @@ from oracle import gmm_oracle as O
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
 import make_golden  # noqa: E402
-from parity import LOGZ_ATOL, assert_close_stats  # noqa: E402
+from parity import LOGZ_ATOL, assert_close_stats, assert_dense_agrees  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -91,16 +91,18 @@ def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, stored, gpu_device):
         full_estep_into(*args, *o, dense=dense, store_log_joint=stored)
         outs.append(o)
     torch.cuda.synchronize()
-    for u, v in zip(*outs):
-        assert torch.equal(u, v)
+    # The default plan's gathering pass 2 (D <= 64) adds the needed rows in its own tiles.
+    assert_dense_agrees(outs[0], outs[1], bitwise=stored or D > 64)
     assert_close_stats(outs[0], oracle(inp), "full skip")
+    assert_close_stats(outs[1], oracle(inp), "full dense")
 
 
+@pytest.mark.parametrize("D", [72, 48])
 @pytest.mark.parametrize("stored", [False, True])
-def test_phase_split_equals_one_call(stored, gpu_device):
+def test_phase_split_equals_one_call(stored, D, gpu_device):
     """PHASE1 then PHASE2 on one workspace gives the single call's outputs bitwise."""
     from flash_gmm import _lib
-    inp = data.full_clustered(3000, 40, 72, seed=17)
+    inp = data.full_clustered(3000, 40, D, seed=17)
     dev = gpu_device
     ref = _into(inp, dev, store_log_joint=stored)
     N, D = inp["X"].shape
@@ -109,7 +111,7 @@ def test_phase_split_equals_one_call(stored, gpu_device):
     flags = _lib.FLAG_STORE_LOGJOINT if stored else 0
     ws_default = L.fgmm_full_workspace_bytes(N, K, D)
     ws = torch.empty(L.fgmm_full_workspace_bytes_ex(N, K, D, flags), dtype=torch.uint8, device=dev)
-    assert (ws.numel() > ws_default) == stored
+    assert (ws.numel() != ws_default) == stored
     out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
            torch.empty(K, D, D, device=dev)]
     args = [inp[k].to(dev) for k in KEYS]
