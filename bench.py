@@ -111,10 +111,9 @@ def pass1_executed(kind, N, K, D, precision, stored):
     32 bf16 flop per (row, output):
       iso D <= 128:   16-dimension chunks, 1 output:   14 DP bf16 flop per (row, component)
       diag D <= 128:  8-dimension chunks of [x^2, x]:  28 DP
-      full (stored):  16-dimension chunks, DP outputs: 14 DP^2
-    Wider iso / diag and the recomputing full pass 1 run fp32 32x32x2 steps over the
-    padded width (2 DP, 4 DP, 2 DP^2).  The bf16 contract runs one bf16 step per
-    product (2 DP, 4 DP, 2 DP^2 bf16 flop).
+      full D <= 128:  16-dimension chunks, DP outputs: 14 DP^2
+    Wider iso / diag run fp32 32x32x2 steps over the padded width (2 DP, 4 DP).  The
+    bf16 contract runs one bf16 step per product (2 DP, 4 DP, 2 DP^2 bf16 flop).
     """
     DP = padded_dim(kind, D)
     if precision == "bf16":
@@ -124,7 +123,7 @@ def pass1_executed(kind, N, K, D, precision, stored):
         return 14.0 * DP * N * K, "bf16", PEAK_BF16_MFMA_TFLOPS
     if kind == "diag" and D <= 128:
         return 28.0 * DP * N * K, "bf16", PEAK_BF16_MFMA_TFLOPS
-    if kind == "full" and stored:
+    if kind == "full" and D <= 128:
         return 14.0 * DP * DP * N * K, "bf16", PEAK_BF16_MFMA_TFLOPS
     per = {"iso": 2 * DP, "diag": 4 * DP, "full": 2 * DP * DP}[kind]
     return per * float(N) * K, "fp32", PEAK_FP32_MFMA_TFLOPS
@@ -263,7 +262,7 @@ KERNELS = {
     ("diag", "default"): ("diag_lse_x6 (need masks)", "diag_accum_gather"),
     ("diag", "default_wide"): ("diag_lse_split", "diag_accum_split"),
     ("diag", "stored"): ("diag_lse_x6 (stores the log-joint)", "diag_accum_sparse / diag_accum_lj2"),
-    ("full", "default"): ("full_lse", "full_accum"),
+    ("full", "default"): ("full_lse_x6 (need masks)", "full_accum_gather"),
     ("full", "stored"): ("full_lse_x6 (stores the log-joint)", "full_accum"),
 }
 
@@ -374,11 +373,11 @@ def main_workload(args):
                    "reduce": "deterministic fixed-order tree",
                    "log_joint": "stored by phase 1, read by phase 2 (opt-in)" if args.store_log_joint
                    else "recomputed (default O(N + K*D) plan: need bits from phase 1, gathered rows "
-                        "in phase 2)" if (kind == "iso" and D <= 128 and not bf16)
+                        "in phase 2)" if (D <= 128 and not bf16)
                    else "recomputed (default O(N + K*D) plan)",
                    "workspace_bytes": r["ws"]},
         "fp32_equivalent_tflops": flop / (ms * 1e-3) / 1e12,
-        "fp32_equivalent_basis": "the metric's algorithmic flops (iso 4NKD) per step / step time. Not a "
+        "fp32_equivalent_basis": "the workload's algorithmic flops (iso 4NKD, diag 8NKD, full 4NKD^2 + 2NKD) per step / step time. Not a "
                                  "roofline: pass 1 forms its fp32 products from split-bf16 steps on the "
                                  "bf16 matrix cores and pass 2 skips the work whose responsibilities are "
                                  "zero; roofline.frac rates the executed work against the peak of the unit "

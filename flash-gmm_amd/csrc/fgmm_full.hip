@@ -96,7 +96,7 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.KP = (int)round_up(K, kCompsPerWG);
   p.bf16 = bf16;
   p.lj = (allow_lj || bf16) && K > 0 && full_lj_bytes(N, p.KP) <= kMaxLjBytes;
-  p.need = !bf16 && !p.lj && K > 0 && p.DP <= 64;
+  p.need = !bf16 && !p.lj && K > 0;
   p.rexact = p.need && K <= kNeedExactMaxK;
   // Reading the log-joint, pass 2 needs no whitening operands in LDS, and the
   // 4-component kernel serves every D.
@@ -1001,7 +1001,7 @@ __global__ __launch_bounds__(256) void full_fill(float* __restrict__ p, int64_t 
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2 of the default plan (D <= 64): the whitening is recomputed only for the
+// Pass 2 of the default plan: the whitening is recomputed only for the
 // (row, component) pairs whose need bit pass 1 set.  One wave per (row slab,
 // component); a workgroup holds 4 waves of one component on consecutive slabs,
 // with the component's split-bf16 operands (pass 1's l3, esw and c) in LDS.  Each
@@ -1016,9 +1016,15 @@ __global__ __launch_bounds__(256) void full_fill(float* __restrict__ p, int64_t 
 // ---------------------------------------------------------------------------
 constexpr int kGatherWaves = 4;
 
+// Up to D = 96 the component's operands (32 KB at D = 64, 72 KB at 96) sit in LDS;
+// at D = 128 (128 KB) they are read from the workspace (L2) by each wave.  Above
+// D = 64 the kernel runs one wave per SIMD.
+__host__ __device__ constexpr bool gather_ops_in_lds(int DP) { return DP <= 96; }
+__host__ __device__ constexpr int gather_waves_per_eu(int DP) { return DP <= 64 ? 2 : 1; }
+
 template <int DP>
 constexpr size_t gather_lds_bytes() {
-  return (size_t)(DP / 32) * (DP / 16) * 4 * 64 * sizeof(bf16x8)   // the component's operands
+  return (gather_ops_in_lds(DP) ? (size_t)(DP / 32) * (DP / 16) * 4 * 64 * sizeof(bf16x8) : 0)   // operands
          + (size_t)(DP + 8) * sizeof(double)                        // e, then c
          + (size_t)kGatherWaves * 32 * (DP + 4) * sizeof(float)     // X tile per wave
          + (size_t)kGatherWaves * 32 * sizeof(double)                // logZ2 per wave
@@ -1030,7 +1036,7 @@ __host__ inline int64_t gather_grid(int nslab, int K) { return cdiv(gather_group
 
 template <int DP>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * kGatherWaves, 64 * kGatherWaves),
-                          amdgpu_waves_per_eu(2, 2)))
+                          amdgpu_waves_per_eu(gather_waves_per_eu(DP), gather_waves_per_eu(DP))))
 void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                        const bf16x8* __restrict__ l3, const double* __restrict__ esw,
                        const double* __restrict__ ck, int K, int KP, const double* __restrict__ rowstat,
@@ -1040,11 +1046,11 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   constexpr int NMB = DP / 32, NQ = DP / 16, NSB = NMB * (NMB + 1) / 2;
   constexpr int RS = DP + 4;
   constexpr int BLK = NMB * NQ * 4 * 64;   // bf16x8 per component
-  static_assert(DP <= 64, "one component's operands per workgroup");
+  constexpr bool OPS_LDS = gather_ops_in_lds(DP);
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   unsigned char* lp = lds_raw;
-  bf16x8* l_l = reinterpret_cast<bf16x8*>(lp);   lp += (size_t)BLK * sizeof(bf16x8);
+  bf16x8* l_l = reinterpret_cast<bf16x8*>(lp);   lp += OPS_LDS ? (size_t)BLK * sizeof(bf16x8) : 0;
   double* e_l = reinterpret_cast<double*>(lp);   lp += (size_t)(DP + 8) * sizeof(double);
   float* xt_all = reinterpret_cast<float*>(lp);  lp += (size_t)kGatherWaves * 32 * RS * sizeof(float);
   double* rs_all = reinterpret_cast<double*>(lp); lp += (size_t)kGatherWaves * 32 * sizeof(double);
@@ -1058,8 +1064,10 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   const int k = rest % K;
   const int sg = (rest / K) * 8 + (int)(blockIdx.x & 7);
   if (sg >= gather_groups(nslab)) return;   // uniform over the workgroup
-  for (int idx = tid; idx < BLK; idx += 64 * kGatherWaves) l_l[idx] = l3[(int64_t)k * BLK + idx];
+  if constexpr (OPS_LDS)
+    for (int idx = tid; idx < BLK; idx += 64 * kGatherWaves) l_l[idx] = l3[(int64_t)k * BLK + idx];
   for (int idx = tid; idx <= DP; idx += 64 * kGatherWaves) e_l[idx] = idx < DP ? esw[(int64_t)k * DP + idx] : ck[k];
+  const bf16x8* lops = OPS_LDS ? l_l : l3 + (int64_t)k * BLK;
   __syncthreads();
   const int slab = sg * kGatherWaves + wave;
   if (slab >= nslab) return;   // no barrier follows
@@ -1132,10 +1140,14 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   const bf16x8 ones = x6c_ones(lane);
   const double hl = 0.5 * kLog2e;
 
+  // Up to D = 64 the next tile's rows are loaded while a tile is computed; above,
+  // the registers they would take are needed by sig_outer's accumulators.
+  constexpr bool PREFETCH = DP <= 64;
   int e;
   int cnt = take(e);
-  if (cnt > 0) issue(e);
+  if (PREFETCH && cnt > 0) issue(e);
   while (cnt > 0) {
+    if (!PREFETCH) issue(e);
     bf16x8 xb[NQ][3];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) split3_bf16(raw[2 * q], raw[2 * q + 1], xb[q]);
@@ -1146,15 +1158,18 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
       *reinterpret_cast<f32x4*>(xt + c * RS + 16 * q + 8 * g + 4) = raw[2 * q + 1];
     }
     const double lz2 = rst;
-    int en;
-    const int cnt_next = take(en);
-    if (cnt_next > 0) issue(en);
+    int en = -1;
+    int cnt_next = 0;
+    if (PREFETCH) {
+      cnt_next = take(en);
+      if (cnt_next > 0) issue(en);
+    }
 
     // maha of row c as pass 1 forms it (lane = row, register = coordinate).
     double maha = 0.0;
-#pragma unroll
+#pragma unroll DP <= 64 ? NMB : 1
     for (int mb = 0; mb < NMB; ++mb) {
-      const f32x16 t = x6c_tile<NQ, 1>([&](int q, int u) { return l_l[((mb * NQ + q) * 4 + u) * 64 + lane]; },
+      const f32x16 t = x6c_tile<NQ, 1>([&](int q, int u) { return lops[((mb * NQ + q) * 4 + u) * 64 + lane]; },
                                        xb, ones);
       const double* eb = e_l + mb * 32 + g * 16;
 #pragma unroll
@@ -1197,6 +1212,8 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
         }
       }
     }
+    if (!PREFETCH) cnt_next = take(en);
+    e = en;
     cnt = cnt_next;
   }
 
@@ -1238,10 +1255,7 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
                        stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, logZ, rowstat, lj);
   } else if (run1) {
     constexpr size_t lds1 = full_x6_lds_bytes<DP>();
-    auto kern = &full_lse_x6<DP, kLjmStore>;
-    if constexpr (DP <= 64) {
-      if (pl.need) kern = &full_lse_x6<DP, kLjmNeed>;
-    }
+    auto kern = pl.need ? &full_lse_x6<DP, kLjmNeed> : &full_lse_x6<DP, kLjmStore>;
     hipError_t e = set_lds(reinterpret_cast<const void*>(kern), lds1);
     if (e != hipSuccess) return e;
     const unsigned grid1 = pl.need ? (unsigned)pl.grid1 : (unsigned)cdiv(pl.N, 32 * kWaves);
@@ -1256,7 +1270,7 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
   float* pmu = reinterpret_cast<float*>(ws + pl.off_part_mu);
   float* pnk = reinterpret_cast<float*>(ws + pl.off_part_nk);
   const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
-  if constexpr (DP <= 64) {
+  {
     if (pl.need) {
       constexpr size_t lds2 = gather_lds_bytes<DP>();
       hipError_t e = set_lds(reinterpret_cast<const void*>(&full_accum_gather<DP>), lds2);
