@@ -12,23 +12,18 @@
 // form: V^T = L_k^T X^T - b_k with each 16-dimension chunk contributing
 // L_k[q]^T (x - mu_k)[q] to an fp32 accumulator, the offsets returned in fp64; each
 // lane owns one row and 16 whitened coordinates per 32-row block of V^T, so maha is
-// an in-lane fp64 sum plus one cross-half exchange.  With FGMM_FLAG_RECOMPUTE both
-// passes (full_lse, then the recomputing pass 2) whiten with 32x32x2 fp32 MFMA steps
-// in the chunked fp64 form of cross_tile() (A = L_k^T laid out in operand order by
-// full_prep, B = X), so that logZ and the recomputed responsibilities come from the
-// same log-joint.
+// an in-lane fp64 sum plus one cross-half exchange.
 //
-// Pass 2 runs 8 waves per workgroup (4 components x 2 row groups).  After r is
-// formed for a 32-row tile it is exchanged through LDS, and sig_outer accumulates as
-// sum_rows (r x)(x^T) on MFMA with the r-scaled rows as the A operand.  Only the
-// upper 32x32 blocks (d1 block <= d2 block) are accumulated; the finish mirrors
-// them.  mu_acc is the running sum of the same r-scaled operands.
+// Default plan (workspace O(N + K D^2 + N K / 32 bits)): pass 1 leaves logZ2 per row
+// and one need bit per (row, component); pass 2 (full_accum_gather) recomputes the
+// whitening, bit for bit as pass 1 formed it, for the needed pairs only.  With
+// FGMM_FLAG_STORE_LOGJOINT pass 1 stores the fp32 log-joint (N x K) and pass 2
+// (full_accum) reads it.
 //
-// Above D = 64 one component's L^T no longer fits LDS four times over, so pass 2
-// (full_accum_split) runs one component per 4-wave workgroup: wave w whitens the
-// w-th 32-row block of V^T, the partial ||v - b||^2 of the blocks are summed in a
-// fixed order through LDS, and the upper sig_outer blocks are dealt out over the
-// four waves.
+// Pass 2 accumulates sig_outer as sum_rows (r x)(x^T) on fp32 MFMA with the r-scaled
+// rows as the A operand.  Only the upper 32x32 blocks (d1 block <= d2 block) are
+// accumulated; the finish mirrors them.  mu_acc is the running sum of the same
+// r-scaled operands.
 
 #include "fgmm_common.hpp"
 
@@ -47,9 +42,6 @@ constexpr int kAccThreads = 64 * kAccWaves;
 constexpr int kCompsPerWG = 4;
 constexpr int kRowGroups = 2;
 
-// Pass 2 splits one component over the waves of a workgroup above D = 64.
-__host__ __device__ constexpr bool full_accum_split_d(int DP) { return DP > 64; }
-
 struct FullPlan {
   int64_t N, K, D;
   int DP;       // D padded to 32
@@ -60,10 +52,10 @@ struct FullPlan {
   int64_t rows_per_slab;
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
   bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16); always stores the log-joint
-  bool need;    // default plan up to D = 64: pass 1 leaves need masks, pass 2 gathers
+  bool need;    // default plan: pass 1 leaves need masks, pass 2 gathers
   bool rexact;  // need masks from the per-(row, component) bounds (else the running max)
   int grid1;    // pass-1 workgroups with need masks (a persistent grid)
-  size_t off_lsw, off_bsw, off_ck, off_l3, off_esw, off_rowstat, off_part_sig, off_part_mu, off_part_nk,
+  size_t off_lop, off_bsw, off_ck, off_l3, off_esw, off_rowstat, off_part_sig, off_part_mu, off_part_nk,
       off_lj, off_need, off_bound, total;
 };
 
@@ -98,9 +90,6 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.lj = (allow_lj || bf16) && K > 0 && full_lj_bytes(N, p.KP) <= kMaxLjBytes;
   p.need = !bf16 && !p.lj && K > 0;
   p.rexact = p.need && K <= kNeedExactMaxK;
-  // Reading the log-joint, pass 2 needs no whitening operands in LDS, and the
-  // 4-component kernel serves every D.
-  const bool split = full_accum_split_d(p.DP) && !p.lj && !bf16;
   if (bf16) {
     p.ncg = p.KP / bf16_comps_per_wg(p.NMB);
     p.rgroups = bf16_row_groups(p.NMB);
@@ -108,8 +97,8 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
     p.ncg = (int)K;   // one wave per (row slab, component)
     p.rgroups = 1;
   } else {
-    p.ncg = split ? (int)K : p.KP / kCompsPerWG;
-    p.rgroups = split ? 1 : kRowGroups;
+    p.ncg = p.KP / kCompsPerWG;
+    p.rgroups = kRowGroups;
   }
   const int64_t tile_rows = 32 * p.rgroups;
   if (p.need && N > 0) {
@@ -134,11 +123,14 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   }
   p.npart = p.nslab * p.rgroups;
   size_t off = 0;
-  p.off_lsw = off;      off = align256(off + (size_t)p.KP * p.DP * p.DP * sizeof(float));
-  p.off_bsw = off;      off = align256(off + (size_t)p.KP * p.DP * sizeof(double));
+  // The bf16 contract's operands: bf16(L) and b in fp32.
+  p.off_lop = off;
+  if (bf16) off = align256(off + (size_t)p.KP * p.DP * p.DP * sizeof(__bf16));
+  p.off_bsw = off;
+  if (bf16) off = align256(off + (size_t)p.KP * p.DP * sizeof(float));
   p.off_ck = off;       off = align256(off + (size_t)p.KP * sizeof(double));
   // Split-bf16 operands of pass 1: 4 bf16x8 per (16 dimensions, 32 coordinates, lane).
-  const bool x6 = !bf16 && (p.lj || p.need);
+  const bool x6 = !bf16;
   p.off_l3 = off;
   if (x6) off = align256(off + (size_t)p.KP * (p.DP / 32) * (p.DP / 16) * 4 * 64 * sizeof(bf16x8));
   p.off_esw = off;
@@ -164,162 +156,6 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
 }
 
 // ---------------------------------------------------------------------------
-// Prologue, one 64-thread block per component:
-//   lsw[k][mb][m][lane] (f32x4) = L[k][8m + 4g + e][32 mb + c], e = 0..3
-//   bsw[k][mb][g][i]    (f64)   = b[k][32 mb + acc_row(i, g)]
-//   ck[k]               (f64)
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void full_prep(const float* __restrict__ mu, int64_t ldmu,
-                                                const float* __restrict__ L, int64_t K, int D, int DP,
-                                                const float* __restrict__ lpi, f32x4* __restrict__ lsw,
-                                                double* __restrict__ bsw, double* __restrict__ ck) {
-  __shared__ double sb[128];   // DP <= 128
-  const int64_t k = blockIdx.x;
-  const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
-  const bool valid = k < K;
-  const float* Lk = L + k * (int64_t)D * D;
-  // b_j = sum_i L[i][j] mu_i  (j = lane, lane + 64)
-  for (int j = lane; j < DP; j += 64) {
-    double b = 0.0;
-    if (valid && j < D)
-#pragma unroll 8
-      for (int i = 0; i < D; ++i) b = fma((double)Lk[(int64_t)i * D + j], (double)mu[k * ldmu + i], b);
-    sb[j] = b;
-  }
-  if (lane == 0) {
-    double c0 = -INFINITY;
-    if (valid) {
-      double ld = 0.0;
-#pragma unroll 8
-      for (int d = 0; d < D; ++d) ld += log(fabs((double)Lk[(int64_t)d * D + d]) + 1e-30);
-      c0 = ((double)lpi[k] + ld - 0.5 * (double)D * kLog2Pi) * kLog2e;
-    }
-    ck[k] = c0;
-  }
-  const int NMB = DP / 32, NM = DP / 8;
-  for (int mb = 0; mb < NMB; ++mb) {
-    const int j = 32 * mb + c;
-    for (int m = 0; m < NM; ++m) {
-      f32x4 v = zero4();
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 8 * m + 4 * g + e;
-        v[e] = (valid && i < D && j < D) ? Lk[(int64_t)i * D + j] : 0.0f;
-      }
-      lsw[((k * NMB + mb) * NM + m) * 64 + lane] = v;
-    }
-  }
-  __syncthreads();
-  for (int mb = 0; mb < NMB; ++mb) {
-    if (lane < 32) {
-      const int gg = lane >> 4, i = lane & 15;
-      bsw[(k * NMB + mb) * 32 + gg * 16 + i] = sb[32 * mb + acc_row(i, gg)];
-    }
-  }
-}
-
-// maha for this lane's row against one component whose operand / centre blocks are
-// at Lc (LDS, [mb][m][lane] f32x4) and bc ([mb][g][i] f64), with B operand loadB.
-template <int NMB, int NM, typename LB>
-__device__ __forceinline__ double maha_one(const f32x4* Lc, const double* bc, int lane, int g, LB loadB) {
-  double q = 0.0;
-#pragma unroll
-  for (int mb = 0; mb < NMB; ++mb) {
-    double v[16];
-    const f32x4* la = Lc + mb * NM * 64 + lane;
-    cross_tile<NM>(v, [&](int m) { return la[m * 64]; }, loadB);
-    const double* bb = bc + mb * 32 + g * 16;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const double t = v[i] - bb[i];
-      q = fma(t, t, q);
-    }
-  }
-  return q + __shfl_xor(q, 32);
-}
-
-// ---------------------------------------------------------------------------
-// Pass 1 with FGMM_FLAG_RECOMPUTE: online log-sum-exp over components, one
-// component's L^T per LDS stage, whitening in the fp32 form the recomputing pass 2
-// uses, so that logZ and the recomputed responsibilities come from one log-joint.
-// ---------------------------------------------------------------------------
-template <int DP>
-constexpr size_t lse_lds_bytes() {
-  return (size_t)2 * DP * DP * sizeof(float) + (size_t)2 * (DP + 8) * sizeof(double);
-}
-
-template <int DP, bool LJ>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(DP <= 64 ? 2 : 1, DP <= 64 ? 2 : 1)))
-void full_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
-              const f32x4* __restrict__ lsw, const double* __restrict__ bsw,
-              const double* __restrict__ ck, int K, int KP, float* __restrict__ logZ,
-              double* __restrict__ rowstat, float* __restrict__ lj) {
-  constexpr int NMB = DP / 32, NM = DP / 8;
-  constexpr int BLK = NMB * NM * 64;              // float4 per component
-  constexpr int LPT = BLK / kThreads;
-  constexpr int BW = DP + 8;                      // doubles per component stage (b + c)
-  static_assert(BLK % kThreads == 0, "even split");
-
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  f32x4* l_l = reinterpret_cast<f32x4*>(lds_raw);                                // [2][BLK]
-  double* b_l = reinterpret_cast<double*>(lds_raw + 2 * BLK * sizeof(f32x4));    // [2][BW]
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = lane & 31, g = lane >> 5;
-  const int64_t tile = (int64_t)blockIdx.x * kWaves + wave;   // 32-row tile
-  const int64_t row = tile * 32 + c;
-  const bool valid = row < N;
-  // Both half-waves hold row c's log-joint; both store it (same value, same address).
-  float* ljt = LJ ? lj + tile * KP * 32 + c : nullptr;
-
-  f32x4 st[LPT];
-  double bst = 0.0;
-  auto fetch = [&](int k) {
-    const f32x4* src = lsw + (int64_t)k * BLK;
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) st[q] = src[q * kThreads + tid];
-    if (tid < DP) bst = bsw[(int64_t)k * DP + tid];
-    else if (tid == DP) bst = ck[k];
-  };
-  auto commit = [&](int buf) {
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) l_l[buf * BLK + q * kThreads + tid] = st[q];
-    if (tid <= DP) b_l[buf * BW + tid] = bst;
-  };
-  fetch(0);
-  f32x4 xb[NM];
-#pragma unroll
-  for (int m = 0; m < NM; ++m) xb[m] = load_row4(X, ldx, row, 8 * m + 4 * g, D, valid);
-  commit(0);
-  __syncthreads();
-
-  const double hl = 0.5 * kLog2e;
-  double mx = -INFINITY;
-  float sm = 0.0f;
-  for (int k = 0; k < K; ++k) {
-    const int buf = k & 1;
-    const bool more = k + 1 < K;
-    if (more) fetch(k + 1);
-    const double maha = maha_one<NMB, NM>(l_l + buf * BLK, b_l + buf * BW, lane, g,
-                                          [&](int m) { return xb[m]; });
-    const double ll = b_l[buf * BW + DP] - hl * maha;
-    if constexpr (LJ) ljt[k * 32] = (float)ll;
-    const double mn = fmax(mx, ll);
-    const double ms = (mn == -INFINITY) ? 0.0 : mn;
-    sm = sm * fast_exp2((float)(mx - ms)) + fast_exp2((float)(ll - ms));
-    mx = mn;
-    if (more) commit(buf ^ 1);
-    lds_barrier();
-  }
-  const double lz2 = mx + (double)log2f(sm);
-  if (valid && g == 0) {
-    rowstat[row] = lz2;
-    if (logZ) logZ[row] = (float)(lz2 * kLn2);
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Pass 1 on the bf16 matrix cores: the whitening in the centred
 // split-bf16 form of the isotropic pass 1 (x6c_tile, fgmm_common.hpp).  V^T =
 // L_k^T X^T over chunks of 16 dimensions; the A operand is L_k^T split exactly into
@@ -336,64 +172,85 @@ void full_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 //   esw[k][mb][g][i]     (f64):    e_j, j = 32 mb + acc_row(i, g)
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(64) void full_x6_prep(const float* __restrict__ mu, int64_t ldmu,
-                                                   const float* __restrict__ L, int64_t K, int D, int DP,
-                                                   bf16x8* __restrict__ l3, double* __restrict__ esw) {
-  __shared__ float so[8][128];  // o_qj, DP <= 128
-  __shared__ double se[128];    // e_j
+//   ck[k]                (f64):    c_k
+// One 256-thread workgroup per component k < KP.
+__global__ __launch_bounds__(256) void full_x6_prep(const float* __restrict__ mu, int64_t ldmu,
+                                                    const float* __restrict__ L, int64_t K, int D, int DP,
+                                                    const float* __restrict__ lpi, bf16x8* __restrict__ l3,
+                                                    double* __restrict__ esw, double* __restrict__ ck) {
+  __shared__ double so[8][128];   // o_qj, DP <= 128
+  __shared__ double se[128];      // e_j, then log |L_jj|
   const int64_t k = blockIdx.x;
-  const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
   const bool valid = k < K;
   const float* Lk = L + k * (int64_t)D * D;
   const int NQ = DP / 16, NMB = DP / 32;
-  for (int j = lane; j < DP; j += 64) {
-    double b = 0.0, osum = 0.0;
-    for (int q = 0; q < NQ; ++q) {
-      double o = 0.0;
-      if (valid && j < D)
+  // o_qj = sum over d in chunk q of L_dj mu_d (fp64), one (q, j) per thread.
+  for (int idx = tid; idx < NQ * DP; idx += 256) {
+    const int q = idx / DP, j = idx % DP;
+    double o = 0.0;
+    if (valid && j < D)
 #pragma unroll 8
-        for (int d = 16 * q; d < 16 * q + 16 && d < D; ++d)
-          o = fma((double)Lk[(int64_t)d * D + j], (double)mu[k * ldmu + d], o);
-      const float of = (float)o;
-      so[q][j] = of;
-      osum += (double)of;
-      b += o;
-    }
-    se[j] = osum - b;
+      for (int d = 16 * q; d < 16 * q + 16 && d < D; ++d) o = fma((double)Lk[(int64_t)d * D + j], (double)mu[k * ldmu + d], o);
+    so[q][j] = o;
   }
   __syncthreads();
-  for (int mb = 0; mb < NMB; ++mb) {
-    const int j = 32 * mb + c;
+  // e_j = sum_q fp32(o_qj) - b_j with b_j = sum_q o_qj, both summed in q order.
+  if (tid < DP) {
+    double b = 0.0, osum = 0.0;
     for (int q = 0; q < NQ; ++q) {
-      f32x4 lo = zero4(), hi = zero4();
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int d0 = 16 * q + 8 * g + e, d1 = d0 + 4;
-        lo[e] = (valid && d0 < D && j < D) ? Lk[(int64_t)d0 * D + j] : 0.0f;
-        hi[e] = (valid && d1 < D && j < D) ? Lk[(int64_t)d1 * D + j] : 0.0f;
-      }
-      bf16x8 sp[3];
-      split3_bf16(lo, hi, sp);
-      bf16x8* dst = l3 + (((k * NMB + mb) * NQ + q) * 4) * 64 + lane;
-#pragma unroll
-      for (int t = 0; t < 3; ++t) dst[t * 64] = sp[t];
-      // Offset slot: -o_qj in k slots 0..2 (lane-half 0), against x6c_ones.
-      const float mo = -so[q][j];
-      const f32x4 olo = {g == 0 ? mo : 0.0f, 0.0f, 0.0f, 0.0f};
-      bf16x8 os[3];
-      split3_bf16(olo, zero4(), os);
-      bf16x8 ov;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ov[e] = (__bf16)0.0f;
-      ov[0] = os[0][0];
-      ov[1] = os[1][0];
-      ov[2] = os[2][0];
-      dst[3 * 64] = ov;
+      osum += (double)(float)so[q][tid];
+      b += so[q][tid];
     }
-    if (lane < 32) {
-      const int gg = lane >> 4, i = lane & 15;
-      esw[(k * NMB + mb) * 32 + gg * 16 + i] = se[32 * mb + acc_row(i, gg)];
+    se[tid] = osum - b;
+  }
+  __syncthreads();
+  // Operands: (mb, q) pairs dealt over the four waves.
+  for (int pq = wave; pq < NMB * NQ; pq += 4) {
+    const int mb = pq / NQ, q = pq % NQ;
+    const int j = 32 * mb + c;
+    f32x4 lo = zero4(), hi = zero4();
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d0 = 16 * q + 8 * g + e, d1 = d0 + 4;
+      lo[e] = (valid && d0 < D && j < D) ? Lk[(int64_t)d0 * D + j] : 0.0f;
+      hi[e] = (valid && d1 < D && j < D) ? Lk[(int64_t)d1 * D + j] : 0.0f;
     }
+    bf16x8 sp[3];
+    split3_bf16(lo, hi, sp);
+    bf16x8* dst = l3 + (((k * NMB + mb) * NQ + q) * 4) * 64 + lane;
+#pragma unroll
+    for (int t = 0; t < 3; ++t) dst[t * 64] = sp[t];
+    // Offset slot: -o_qj in k slots 0..2 (lane-half 0), against x6c_ones.
+    const float mo = -(float)so[q][j];
+    const f32x4 olo = {g == 0 ? mo : 0.0f, 0.0f, 0.0f, 0.0f};
+    bf16x8 os[3];
+    split3_bf16(olo, zero4(), os);
+    bf16x8 ov;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ov[e] = (__bf16)0.0f;
+    ov[0] = os[0][0];
+    ov[1] = os[1][0];
+    ov[2] = os[2][0];
+    dst[3 * 64] = ov;
+  }
+  if (tid < DP) {
+    const int mb = tid / 32, gg = (tid >> 4) & 1, i = tid & 15;
+    esw[(k * NMB + mb) * 32 + gg * 16 + i] = se[32 * mb + acc_row(i, gg)];
+  }
+  __syncthreads();
+  // c_k, the log-determinant summed in d order.
+  if (tid < D) se[tid] = valid ? log(fabs((double)Lk[(int64_t)tid * D + tid]) + 1e-30) : 0.0;
+  __syncthreads();
+  if (tid == 0) {
+    double c0 = -INFINITY;
+    if (valid) {
+      double ld = 0.0;
+      for (int d = 0; d < D; ++d) ld += se[d];
+      c0 = ((double)lpi[k] + ld - 0.5 * (double)D * kLog2Pi) * kLog2e;
+    }
+    ck[k] = c0;
   }
 }
 
@@ -409,7 +266,6 @@ constexpr size_t full_x6_lds_bytes() {
 }
 
 // What pass 1 leaves for pass 2 besides logZ2.
-constexpr int kLjmNone = 0;    // nothing
 constexpr int kLjmStore = 1;   // the stored log-joint
 constexpr int kLjmNeed = 2;    // need masks only (the default plan)
 
@@ -554,39 +410,31 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2.
+// Pass 2 of the stored plan (FGMM_FLAG_STORE_LOGJOINT): r from the log-joint pass 1
+// stored, no whitening.
 // ---------------------------------------------------------------------------
-template <int DP, bool LJ>
+template <int DP>
 constexpr size_t accum_lds_bytes() {
   constexpr int TR = 32 * kRowGroups;
-  return (LJ ? 0 : (size_t)kCompsPerWG * DP * DP * sizeof(float))   // L^T operands
-         + (size_t)kCompsPerWG * (DP + 8) * sizeof(double)      // b, c
-         + (size_t)2 * TR * (DP + 4) * sizeof(float)            // X tiles
+  return (size_t)2 * TR * (DP + 4) * sizeof(float)              // X tiles
          + (size_t)2 * TR * sizeof(double)                      // logZ2
          + (size_t)kAccWaves * 32 * sizeof(float);              // r exchange
 }
 
-template <int DP, bool LJ>
+template <int DP>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
-void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
-                const f32x4* __restrict__ lsw, const double* __restrict__ bsw,
-                const double* __restrict__ ck, int K, int KP, const double* __restrict__ rowstat,
-                int nslab, int64_t rows_per_slab, float* __restrict__ part_sig,
-                float* __restrict__ part_mu, float* __restrict__ part_nk, int dense,
-                const float* __restrict__ lj) {
-  constexpr int NMB = DP / 32, NM = DP / 8, NSB = NMB * (NMB + 1) / 2;
+void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int K, int KP,
+                const double* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
+                float* __restrict__ part_sig, float* __restrict__ part_mu, float* __restrict__ part_nk,
+                int dense, const float* __restrict__ lj) {
+  constexpr int NMB = DP / 32, NSB = NMB * (NMB + 1) / 2;
   constexpr int RS = DP + 4, V4 = DP / 4;
-  constexpr int BLK = NMB * NM * 64;
-  constexpr int BW = DP + 8;
   constexpr int TR = 32 * kRowGroups;
   constexpr int LPT = (TR * V4) / kAccThreads;
-  constexpr int MPT = (kCompsPerWG * BLK) / kAccThreads;
-  static_assert((TR * V4) % kAccThreads == 0 && (kCompsPerWG * BLK) % kAccThreads == 0, "even split");
+  static_assert((TR * V4) % kAccThreads == 0, "even split");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   unsigned char* p = lds_raw;
-  f32x4* l_l = reinterpret_cast<f32x4*>(p);   p += LJ ? 0 : kCompsPerWG * BLK * sizeof(f32x4);
-  double* b_l = reinterpret_cast<double*>(p); p += kCompsPerWG * BW * sizeof(double);
   float* xs = reinterpret_cast<float*>(p);    p += 2 * TR * RS * sizeof(float);
   double* rs = reinterpret_cast<double*>(p);  p += 2 * TR * sizeof(double);
   float* r_l = reinterpret_cast<float*>(p);
@@ -603,20 +451,6 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   int64_t r_end = r_begin + rows_per_slab;
   if (r_end > N) r_end = N;
   const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
-
-  // Operands of the workgroup's components -> LDS (lsw/bsw/ck are padded to KP).
-  if constexpr (!LJ) {
-#pragma unroll
-    for (int q = 0; q < MPT; ++q) {
-      const int idx = q * kAccThreads + tid;
-      l_l[idx] = lsw[(int64_t)cg * kCompsPerWG * BLK + idx];
-    }
-  }
-  for (int idx = tid; idx < kCompsPerWG * BW; idx += kAccThreads) {
-    const int cc = idx / BW, e = idx % BW;
-    const int64_t kk = (int64_t)cg * kCompsPerWG + cc;
-    b_l[idx] = e < DP ? bsw[kk * DP + e] : (e == DP ? ck[kk] : 0.0);
-  }
 
   f32x16 acc[NSB];
 #pragma unroll
@@ -664,13 +498,13 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     if (tid < TR) rs[buf * TR + tid] = rstage;
   };
 
-  // With LJ: the stored log-joint of this wave's component for row c of tile t (0
-  // past the slab, where logZ2 = +inf makes r = 0), loaded one tile ahead where the
-  // register fits (at D = 128 the accumulators leave none).
-  constexpr bool PF = LJ && DP <= 96;
+  // The stored log-joint of this wave's component for row c of tile t (0 past the
+  // slab, where logZ2 = +inf makes r = 0), loaded one tile ahead where the register
+  // fits (at D = 128 the accumulators leave none).
+  constexpr bool PF = DP <= 96;
   auto lj_of = [&](int t) -> float {
     const int64_t row0 = r_begin + (int64_t)t * TR + rg * 32;
-    return (LJ && active && row0 < r_end) ? lj[((row0 >> 5) * KP + k) * 32 + c] : 0.0f;
+    return (active && row0 < r_end) ? lj[((row0 >> 5) * KP + k) * 32 + c] : 0.0f;
   };
   float lnext = 0.0f;
   if (ntiles > 0) {
@@ -680,9 +514,6 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   }
   __syncthreads();
 
-  const double hl = 0.5 * kLog2e;
-  const f32x4* Lc = l_l + cw * BLK;
-  const double* bc = b_l + cw * BW;
   float* rx = r_l + wave * 32;
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
@@ -694,13 +525,7 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     float rv = 0.0f;
     if (active) {
       // r for this lane's row c (both half-waves hold it).
-      if constexpr (LJ) {
-        rv = fast_exp2((float)((double)l - rt[c]));
-      } else {
-        const double maha = maha_one<NMB, NM>(
-            Lc, bc, lane, g, [&](int m) { return *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * m + 4 * g); });
-        rv = fast_exp2((float)((bc[DP] - rt[c]) - hl * maha));
-      }
+      rv = fast_exp2((float)((double)l - rt[c]));
       if (g == 0) {
         nk += rv;
         rx[c] = rv;
@@ -763,199 +588,15 @@ void full_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   }
 }
 
-// ---------------------------------------------------------------------------
-// Pass 2 for D > 64: one component per workgroup of 4 waves.
-// ---------------------------------------------------------------------------
-template <int DP>
-constexpr size_t accum_split_lds_bytes() {
-  return (size_t)DP * DP * sizeof(float)               // L^T operands of the component
-         + (size_t)(DP + 8) * sizeof(double)           // b, c
-         + (size_t)2 * 32 * (DP + 4) * sizeof(float)   // X tiles
-         + (size_t)2 * 32 * sizeof(double)             // logZ2
-         + (size_t)kWaves * 32 * sizeof(double)        // per-block ||v - b||^2
-         + (size_t)kWaves * 32 * sizeof(float);        // r, one copy per wave
-}
-
-template <int DP>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(1, 1)))
-void full_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
-                      const f32x4* __restrict__ lsw, const double* __restrict__ bsw,
-                      const double* __restrict__ ck, int K, int KP, const double* __restrict__ rowstat,
-                      int nslab, int64_t rows_per_slab, float* __restrict__ part_sig,
-                      float* __restrict__ part_mu, float* __restrict__ part_nk, int dense) {
-  constexpr int NMB = DP / 32, NM = DP / 8, NSB = NMB * (NMB + 1) / 2;
-  constexpr int RS = DP + 4, V4 = DP / 4;
-  constexpr int BLK = NMB * NM * 64;
-  constexpr int BW = DP + 8;
-  constexpr int LPT = (32 * V4) / kThreads;
-  constexpr int MPT = BLK / kThreads;
-  constexpr int SPW = (NSB + kWaves - 1) / kWaves;   // sig blocks per wave
-  static_assert(NMB <= kWaves && (32 * V4) % kThreads == 0 && BLK % kThreads == 0, "split shape");
-
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  unsigned char* p = lds_raw;
-  f32x4* l_l = reinterpret_cast<f32x4*>(p);   p += BLK * sizeof(f32x4);
-  double* b_l = reinterpret_cast<double*>(p); p += BW * sizeof(double);
-  float* xs = reinterpret_cast<float*>(p);    p += 2 * 32 * RS * sizeof(float);
-  double* rs = reinterpret_cast<double*>(p);  p += 2 * 32 * sizeof(double);
-  double* qx = reinterpret_cast<double*>(p);  p += kWaves * 32 * sizeof(double);
-  float* r_l = reinterpret_cast<float*>(p);
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = lane & 31, g = lane >> 5;
-  const int slab = blockIdx.x % nslab;
-  const int k = blockIdx.x / nslab;
-  if (k >= K) return;   // whole workgroup: no barrier is left waiting
-
-  const int64_t r_begin = (int64_t)slab * rows_per_slab;
-  int64_t r_end = r_begin + rows_per_slab;
-  if (r_end > N) r_end = N;
-  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
-
-#pragma unroll
-  for (int q = 0; q < MPT; ++q) l_l[q * kThreads + tid] = lsw[(int64_t)k * BLK + q * kThreads + tid];
-  for (int idx = tid; idx < BW; idx += kThreads)
-    b_l[idx] = idx < DP ? bsw[(int64_t)k * DP + idx] : (idx == DP ? ck[k] : 0.0);
-
-  // Upper block sb of sig_outer <-> (m1 <= m2); wave w owns sb = w, w + 4, ...
-  f32x16 acc[SPW];
-  int bm1[SPW], bm2[SPW];
-#pragma unroll
-  for (int j = 0; j < SPW; ++j) {
-    acc[j] = zero16();
-    int sb = wave + kWaves * j, m1 = 0;
-    while (sb >= NMB - m1 && m1 < NMB) { sb -= NMB - m1; ++m1; }
-    bm1[j] = m1;
-    bm2[j] = m1 + sb;   // m1 == NMB marks "no block" (sb index past NSB)
-  }
-  float mua = 0.0f, nk = 0.0f;
-
-  f32x4 stage[LPT];
-  double rstage = INFINITY;
-  const bool full_d = (D == DP);
-  auto fetch = [&](int t) {
-    const int64_t row0 = r_begin + (int64_t)t * 32;
-    if (full_d && row0 + 32 <= r_end) {
-      const float* src = X + row0 * ldx;
-#pragma unroll
-      for (int q = 0; q < LPT; ++q) {
-        const int idx = q * kThreads + tid;
-        stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < LPT; ++q) {
-        const int idx = q * kThreads + tid;
-        const int64_t row = row0 + idx / V4;
-        stage[q] = load_row4(X, ldx, row, (idx % V4) * 4, D, row < r_end);
-      }
-    }
-    if (tid < 32) {
-      const int64_t row = row0 + tid;
-      rstage = (row < r_end) ? rowstat[row] : INFINITY;
-    }
-  };
-  auto commit = [&](int buf) {
-    float* dst = xs + buf * 32 * RS;
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) {
-      const int idx = q * kThreads + tid;
-      *reinterpret_cast<f32x4*>(dst + (idx / V4) * RS + (idx % V4) * 4) = stage[q];
-    }
-    if (tid < 32) rs[buf * 32 + tid] = rstage;
-  };
-
-  if (ntiles > 0) {
-    fetch(0);
-    commit(0);
-  }
-  __syncthreads();
-
-  const double hl = 0.5 * kLog2e;
-  float* rx = r_l + wave * 32;
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    const bool more = t + 1 < ntiles;
-    const float* xt = xs + buf * 32 * RS;
-    const double* rt = rs + buf * 32;
-    if (wave < NMB) {
-      // Block `wave` of V^T = L^T X^T for the tile; this lane's row is c.
-      double v[16];
-      const f32x4* la = l_l + wave * NM * 64 + lane;
-      const float* xrow = xt + c * RS + 4 * g;
-      cross_tile<NM>(v, [&](int m) { return la[m * 64]; },
-                     [&](int m) { return *reinterpret_cast<const f32x4*>(xrow + 8 * m); });
-      const double* bb = b_l + wave * 32 + g * 16;
-      double q = 0.0;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const double d = v[i] - bb[i];
-        q = fma(d, d, q);
-      }
-      q += __shfl_xor(q, 32);
-      if (g == 0) qx[wave * 32 + c] = q;
-    }
-    __syncthreads();
-    {
-      double maha = 0.0;
-#pragma unroll
-      for (int mb = 0; mb < NMB; ++mb) maha += qx[mb * 32 + c];   // same order in every wave
-      const float rv = fast_exp2((float)((b_l[DP] - rt[c]) - hl * maha));
-      if (g == 0) {
-        rx[c] = rv;
-        if (wave == 0) nk += rv;
-      }
-    }
-    if (more) fetch(t + 1);
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int s = 0; s < 16; ++s) {
-      const int row = acc_row(s, g);
-      const float rr = rx[row];
-      if (!dense && __builtin_amdgcn_ballot_w64(rr != 0.0f) == 0) continue;
-      const float* xr = xt + row * RS + c;
-      if (wave < NMB) mua += rr * xr[32 * wave];
-#pragma unroll
-      for (int j = 0; j < SPW; ++j) {
-        if (bm1[j] < NMB) acc[j] = mfma32(rr * xr[32 * bm1[j]], xr[32 * bm2[j]], acc[j]);
-      }
-    }
-    if (more) commit(buf ^ 1);
-    __syncthreads();
-  }
-
-  const int64_t pbase = (int64_t)slab * KP + k;
-#pragma unroll
-  for (int j = 0; j < SPW; ++j) {
-    if (bm1[j] < NMB) {
-      const int sb = wave + kWaves * j;
-      float* ps = part_sig + (pbase * NSB + sb) * 1024;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) ps[acc_row(i, g) * 32 + c] = acc[j][i];
-    }
-  }
-  if (wave < NMB) {
-    const float v = mua + __shfl_xor(mua, 32);
-    if (g == 0) part_mu[pbase * DP + 32 * wave + c] = v;
-  }
-  if (wave == 0) {
-    float nks = nk;
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) nks += __shfl_xor(nks, o);
-    if (lane == 0) part_nk[pbase] = nks;
-  }
-}
-
-// Finish: one thread per (k, d1, d2) of sig_outer plus (k, d) of mu_acc and k of Nk.
+// Finish of mu_acc and Nk: one thread per (k, d) of mu_acc and per k of Nk.
 // ATOMIC (FGMM_FLAG_ATOMIC_REDUCE): partial blockIdx.y is added with float atomics into
 // the zeroed (or accumulated) outputs instead of the fixed-order fp64 sum.
 template <bool ATOMIC>
-__global__ __launch_bounds__(256) void full_reduce(const float* __restrict__ part_sig,
-                                                   const float* __restrict__ part_mu,
+__global__ __launch_bounds__(256) void full_reduce(const float* __restrict__ part_mu,
                                                    const float* __restrict__ part_nk, int npart, int KP,
-                                                   int DP, int NMB, int64_t K, int D,
+                                                   int DP, int64_t K, int D,
                                                    float* __restrict__ Nk, float* __restrict__ mu_acc,
-                                                   float* __restrict__ sig_outer, int accumulate) {
+                                                   int accumulate) {
   // Sum over the partials of p[0], p[stride], ... (or, atomically, the one of this grid row).
   auto finish = [&](const float* p, int64_t stride, float* o) {
     if (ATOMIC) {
@@ -965,26 +606,7 @@ __global__ __launch_bounds__(256) void full_reduce(const float* __restrict__ par
       *o = accumulate ? (float)((double)*o + s) : (float)s;
     }
   };
-  const int NSB = NMB * (NMB + 1) / 2;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t nsig = K * D * D;
-  if (idx < nsig) {
-    const int64_t k = idx / ((int64_t)D * D);
-    const int rem = (int)(idx % ((int64_t)D * D));
-    int d1 = rem / D, d2 = rem % D;
-    if (d1 > d2) { const int t = d1; d1 = d2; d2 = t; }    // upper blocks only; mirror
-    int b1 = d1 / 32, b2 = d2 / 32;
-    if (b1 > b2) { const int t = b1; b1 = b2; b2 = t; }
-    // upper-block index sb for (b1 <= b2): sum_{m<b1}(NMB-m) + (b2-b1)
-    const int sb = b1 * NMB - b1 * (b1 - 1) / 2 + (b2 - b1);
-    // within the block, element (d1 mod 32, d2 mod 32) with d1 in block b1 ... when b1 == b2
-    // the block is symmetric only in sum, so read (d1%32, d2%32) directly.
-    const int e1 = (d1 / 32 == b1) ? d1 % 32 : d2 % 32;
-    const int e2 = (d1 / 32 == b1) ? d2 % 32 : d1 % 32;
-    finish(part_sig + ((int64_t)k * NSB + sb) * 1024 + e1 * 32 + e2, (int64_t)KP * NSB * 1024, sig_outer + idx);
-    return;
-  }
-  const int64_t j = idx - nsig;
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (j < K * D) {
     const int64_t k = j / D;
     const int d = (int)(j % D);
@@ -993,6 +615,54 @@ __global__ __launch_bounds__(256) void full_reduce(const float* __restrict__ par
   }
   const int64_t kk = j - K * D;
   if (kk < K) finish(part_nk + kk, KP, Nk + kk);
+}
+
+// sig_outer: one workgroup per (component k, upper 32x32 block sb = (b1, b2)).  The
+// block's partials are read coalesced and summed in partial order in fp64 (or, with
+// ATOMIC, partial blockIdx.y alone is taken); the sums go through LDS so that both the
+// (b1, b2) tile and its mirror (b2, b1) are written row-contiguously.  A diagonal
+// block's upper triangle is mirrored onto its lower one, so sig_outer is exactly
+// symmetric.
+template <bool ATOMIC>
+__global__ __launch_bounds__(256) void full_reduce_sig(const float* __restrict__ part_sig, int npart, int KP,
+                                                       int NMB, int D, float* __restrict__ sig_outer,
+                                                       int accumulate) {
+  __shared__ double tile[32][33];
+  const int NSB = NMB * (NMB + 1) / 2;
+  const int k = (int)(blockIdx.x / NSB);
+  const int sb = (int)(blockIdx.x % NSB);
+  int b1 = 0, rem = sb;
+  while (rem >= NMB - b1) {
+    rem -= NMB - b1;
+    ++b1;
+  }
+  const int b2 = b1 + rem;
+  const int tid = threadIdx.x;
+  const int64_t pstride = (int64_t)KP * NSB * 1024;
+  const float* p = part_sig + ((int64_t)k * NSB + sb) * 1024;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = tid + 256 * j;
+    tile[e >> 5][e & 31] = ATOMIC ? (double)p[(int64_t)blockIdx.y * pstride + e] : strided_sum(p + e, npart, pstride);
+  }
+  __syncthreads();
+  float* out = sig_outer + (int64_t)k * D * D;
+  auto put = [&](int d1, int d2, double v) {
+    float* o = out + (int64_t)d1 * D + d2;
+    if (ATOMIC) atomicAdd(o, (float)v);
+    else *o = accumulate ? (float)((double)*o + v) : (float)v;
+  };
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = tid + 256 * j;
+    const int r = e >> 5, c = e & 31;
+    const int d1 = 32 * b1 + r, d2 = 32 * b2 + c;
+    if (d1 < D && d2 < D) put(d1, d2, b1 == b2 && r > c ? tile[c][r] : tile[r][c]);
+    if (b1 != b2) {
+      const int m1 = 32 * b2 + r, m2 = 32 * b1 + c;
+      if (m1 < D && m2 < D) put(m1, m2, tile[c][r]);
+    }
+  }
 }
 
 __global__ __launch_bounds__(256) void full_fill(float* __restrict__ p, int64_t n, float v) {
@@ -1027,7 +697,6 @@ constexpr size_t gather_lds_bytes() {
   return (gather_ops_in_lds(DP) ? (size_t)(DP / 32) * (DP / 16) * 4 * 64 * sizeof(bf16x8) : 0)   // operands
          + (size_t)(DP + 8) * sizeof(double)                        // e, then c
          + (size_t)kGatherWaves * 32 * (DP + 4) * sizeof(float)     // X tile per wave
-         + (size_t)kGatherWaves * 32 * sizeof(double)                // logZ2 per wave
          + (size_t)kGatherWaves * 32 * sizeof(float)                 // r per wave
          + (size_t)kGatherWaves * 64 * sizeof(int);                  // row queue per wave
 }
@@ -1053,7 +722,6 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   bf16x8* l_l = reinterpret_cast<bf16x8*>(lp);   lp += OPS_LDS ? (size_t)BLK * sizeof(bf16x8) : 0;
   double* e_l = reinterpret_cast<double*>(lp);   lp += (size_t)(DP + 8) * sizeof(double);
   float* xt_all = reinterpret_cast<float*>(lp);  lp += (size_t)kGatherWaves * 32 * RS * sizeof(float);
-  double* rs_all = reinterpret_cast<double*>(lp); lp += (size_t)kGatherWaves * 32 * sizeof(double);
   float* r_all = reinterpret_cast<float*>(lp);   lp += (size_t)kGatherWaves * 32 * sizeof(float);
   int* q_all = reinterpret_cast<int*>(lp);
 
@@ -1073,7 +741,6 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   if (slab >= nslab) return;   // no barrier follows
 
   float* xt = xt_all + wave * 32 * RS;
-  double* rs_l = rs_all + wave * 32;
   float* rx = r_all + wave * 32;
   int* q_l = q_all + wave * 64;
 
@@ -1238,8 +905,6 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
 template <int DP>
 hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
                          float* logZ, bool run1, bool run2, bool dense, hipStream_t stream) {
-  const f32x4* lsw = reinterpret_cast<const f32x4*>(ws + pl.off_lsw);
-  const double* bsw = reinterpret_cast<const double*>(ws + pl.off_bsw);
   const double* ck = reinterpret_cast<const double*>(ws + pl.off_ck);
   double* rowstat = reinterpret_cast<double*>(ws + pl.off_rowstat);
   float* lj = pl.lj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
@@ -1247,13 +912,7 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
     return bytes > 65536 ? hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes)
                          : hipSuccess;
   };
-  if (run1 && !pl.lj && !pl.need) {
-    constexpr size_t lds1 = lse_lds_bytes<DP>();
-    hipError_t e = set_lds(reinterpret_cast<const void*>(&full_lse<DP, false>), lds1);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((full_lse<DP, false>), dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
-                       stream, X, ldx, pl.N, (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, logZ, rowstat, lj);
-  } else if (run1) {
+  if (run1) {
     constexpr size_t lds1 = full_x6_lds_bytes<DP>();
     auto kern = pl.need ? &full_lse_x6<DP, kLjmNeed> : &full_lse_x6<DP, kLjmStore>;
     hipError_t e = set_lds(reinterpret_cast<const void*>(kern), lds1);
@@ -1284,26 +943,12 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
       return hipGetLastError();
     }
   }
-  auto launch2 = [&](auto lj_tag) -> hipError_t {
-    constexpr bool LJ = decltype(lj_tag)::value;
-    if constexpr (!LJ && full_accum_split_d(DP)) {
-      constexpr size_t lds2 = accum_split_lds_bytes<DP>();
-      hipError_t e = set_lds(reinterpret_cast<const void*>(&full_accum_split<DP>), lds2);
-      if (e != hipSuccess) return e;
-      hipLaunchKernelGGL((full_accum_split<DP>), grid2, dim3(kThreads), lds2, stream, X, ldx, pl.N,
-                         (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, rowstat, pl.nslab,
-                         pl.rows_per_slab, psig, pmu, pnk, dense ? 1 : 0);
-    } else {
-      constexpr size_t lds2 = accum_lds_bytes<DP, LJ>();
-      hipError_t e = set_lds(reinterpret_cast<const void*>(&full_accum<DP, LJ>), lds2);
-      if (e != hipSuccess) return e;
-      hipLaunchKernelGGL((full_accum<DP, LJ>), grid2, dim3(kAccThreads), lds2, stream, X, ldx, pl.N,
-                         (int)pl.D, lsw, bsw, ck, (int)pl.K, pl.KP, rowstat, pl.nslab,
-                         pl.rows_per_slab, psig, pmu, pnk, dense ? 1 : 0, lj);
-    }
-    return hipGetLastError();
-  };
-  return pl.lj ? launch2(std::true_type{}) : launch2(std::false_type{});
+  constexpr size_t lds2 = accum_lds_bytes<DP>();
+  hipError_t e = set_lds(reinterpret_cast<const void*>(&full_accum<DP>), lds2);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((full_accum<DP>), grid2, dim3(kAccThreads), lds2, stream, X, ldx, pl.N, (int)pl.D,
+                     (int)pl.K, pl.KP, rowstat, pl.nslab, pl.rows_per_slab, psig, pmu, pnk, dense ? 1 : 0, lj);
+  return hipGetLastError();
 }
 
 // ===========================================================================
@@ -1708,7 +1353,7 @@ __global__ __launch_bounds__(256) void full_bf16_reduce(const float* __restrict_
 template <int DP>
 hipError_t launch_bf16(const FullPlan& pl, const float* X, int64_t ldx, unsigned char* ws, float* logZ,
                        bool run1, bool run2, bool dense, hipStream_t stream) {
-  const bf16x8* lop = reinterpret_cast<const bf16x8*>(ws + pl.off_lsw);
+  const bf16x8* lop = reinterpret_cast<const bf16x8*>(ws + pl.off_lop);
   const float* bsw = reinterpret_cast<const float*>(ws + pl.off_bsw);
   const float* ck = reinterpret_cast<const float*>(ws + pl.off_ck);
   float* rowstat = reinterpret_cast<float*>(ws + pl.off_rowstat);
@@ -1791,17 +1436,12 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   }
   if (run1 && bf16)
     hipLaunchKernelGGL(full_bf16_prep, dim3((unsigned)pl.KP), dim3(64), 0, stream, mu, ldmu, prec_chol, K,
-                       (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_lsw),
+                       (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_lop),
                        reinterpret_cast<float*>(ws + pl.off_bsw), reinterpret_cast<float*>(ws + pl.off_ck));
   else if (run1)
-    hipLaunchKernelGGL(full_prep, dim3((unsigned)pl.KP), dim3(64), 0, stream, mu, ldmu, prec_chol, K,
-                       (int)D, pl.DP, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_lsw),
-                       reinterpret_cast<double*>(ws + pl.off_bsw),
-                       reinterpret_cast<double*>(ws + pl.off_ck));
-  if (run1 && !bf16 && (pl.lj || pl.need))
-    hipLaunchKernelGGL(full_x6_prep, dim3((unsigned)pl.KP), dim3(64), 0, stream, mu, ldmu, prec_chol, K,
-                       (int)D, pl.DP, reinterpret_cast<bf16x8*>(ws + pl.off_l3),
-                       reinterpret_cast<double*>(ws + pl.off_esw));
+    hipLaunchKernelGGL(full_x6_prep, dim3((unsigned)pl.KP), dim3(256), 0, stream, mu, ldmu, prec_chol, K,
+                       (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_l3),
+                       reinterpret_cast<double*>(ws + pl.off_esw), reinterpret_cast<double*>(ws + pl.off_ck));
   if (N > 0) {
     auto run = [&](auto dp_tag) -> hipError_t {
       constexpr int DP = decltype(dp_tag)::value;
@@ -1820,6 +1460,8 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   }
   if (!run2) return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
   const int64_t nthreads = K * D * D + K * D + K;
+  const int64_t nvec = K * D + K;
+  const int64_t nsb = (int64_t)pl.NMB * (pl.NMB + 1) / 2;
   if (bf16) {
     hipLaunchKernelGGL(full_bf16_reduce, dim3((unsigned)cdiv(nthreads, 256)), dim3(256), 0, stream,
                        reinterpret_cast<const float*>(ws + pl.off_part_sig),
@@ -1835,18 +1477,23 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
       hipLaunchKernelGGL(full_fill, dim3((unsigned)cdiv(K * D * D, 256)), dim3(256), 0, stream, sig_outer,
                          K * D * D, 0.0f);
     }
-    if (pl.npart > 0)
-      hipLaunchKernelGGL(full_reduce<true>, dim3((unsigned)cdiv(nthreads, 256), (unsigned)pl.npart), dim3(256), 0,
-                         stream, reinterpret_cast<const float*>(ws + pl.off_part_sig),
-                         reinterpret_cast<const float*>(ws + pl.off_part_mu),
-                         reinterpret_cast<const float*>(ws + pl.off_part_nk), pl.npart, pl.KP, pl.DP, pl.NMB, K,
-                         (int)D, Nk, mu_acc, sig_outer, 1);
+    if (pl.npart > 0) {
+      hipLaunchKernelGGL(full_reduce_sig<true>, dim3((unsigned)(K * nsb), (unsigned)pl.npart), dim3(256), 0,
+                         stream, reinterpret_cast<const float*>(ws + pl.off_part_sig), pl.npart, pl.KP, pl.NMB,
+                         (int)D, sig_outer, 1);
+      hipLaunchKernelGGL(full_reduce<true>, dim3((unsigned)cdiv(nvec, 256), (unsigned)pl.npart), dim3(256), 0,
+                         stream, reinterpret_cast<const float*>(ws + pl.off_part_mu),
+                         reinterpret_cast<const float*>(ws + pl.off_part_nk), pl.npart, pl.KP, pl.DP, K,
+                         (int)D, Nk, mu_acc, 1);
+    }
     return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
   }
-  hipLaunchKernelGGL(full_reduce<false>, dim3((unsigned)cdiv(nthreads, 256)), dim3(256), 0, stream,
-                     reinterpret_cast<const float*>(ws + pl.off_part_sig),
+  hipLaunchKernelGGL(full_reduce_sig<false>, dim3((unsigned)(K * nsb)), dim3(256), 0, stream,
+                     reinterpret_cast<const float*>(ws + pl.off_part_sig), pl.npart, pl.KP, pl.NMB, (int)D,
+                     sig_outer, accumulate ? 1 : 0);
+  hipLaunchKernelGGL(full_reduce<false>, dim3((unsigned)cdiv(nvec, 256)), dim3(256), 0, stream,
                      reinterpret_cast<const float*>(ws + pl.off_part_mu),
-                     reinterpret_cast<const float*>(ws + pl.off_part_nk), pl.npart, pl.KP, pl.DP,
-                     pl.NMB, K, (int)D, Nk, mu_acc, sig_outer, accumulate ? 1 : 0);
+                     reinterpret_cast<const float*>(ws + pl.off_part_nk), pl.npart, pl.KP, pl.DP, K,
+                     (int)D, Nk, mu_acc, accumulate ? 1 : 0);
   return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
 }
