@@ -341,6 +341,10 @@ constexpr size_t lse_lds_bytes() {
   return lse_lds_base(DP);
 }
 
+// Accumulation chains of the split-bf16 contraction (x6c_tile, x6c_tile_rows): pass 1
+// and the recomputing pass 2 use the same number, so they form the same sums.
+constexpr int kIsoChains = 2;
+
 // What pass 1 leaves for pass 2 besides logZ2 and ||x||^2.
 constexpr int kLjmNone = 0;    // nothing (the recomputing pass 2 above D = 128)
 constexpr int kLjmStore = 1;   // the stored log-joint, its block maxima and need masks
@@ -373,11 +377,14 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   bf16x8 st[LPT];
   double2 kst = make_double2(0.0, 0.0);
+  // Buffer loads from a resource per block: the lane's offset is loop-invariant and
+  // the per-load part is a scalar, so the fetch costs no vector address arithmetic.
   auto fetch = [&](int kb) {
-    const bf16x8* src = mu3 + (int64_t)kb * BLK;
+    const buf_rsrc r = make_rsrc(mu3 + (int64_t)kb * BLK, (uint32_t)(BLK * sizeof(bf16x8)));
 #pragma unroll
     for (int q = 0; q < LPT; ++q)
-      if (BLK % kThreads == 0 || q * kThreads + tid < BLK) st[q] = src[q * kThreads + tid];
+      st[q] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                             r, tid * (int)sizeof(bf16x8), q * kThreads * (int)sizeof(bf16x8), 0));
     if (tid < 32) kst = kc_blk[(int64_t)kb * 32 + tid];
   };
   auto commit = [&](int buf) {
@@ -419,7 +426,7 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const bf16x8* mp = mu_l + buf * BLK + lane;
     // Centred S^T[comp][row] = mu . x - sum_q o_q, lane = row, register i = component
     // acc_row(i, g); the block's constants carry + 2 b sum_q o_q.
-    const f32x16 xm = x6c_tile<NQ>([&](int q, int t) { return mp[(q * 4 + t) * 64]; }, xb, ones);
+    const f32x16 xm = x6c_tile<NQ, kIsoChains>([&](int q, int t) { return mp[(q * 4 + t) * 64]; }, xb, ones);
     const double2* kp = kc_l + buf * 32 + g * 16;
     double ll[16];
     double bm = -INFINITY;
@@ -1171,7 +1178,7 @@ void iso_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D
     if (cnt_next > 0) issue(en);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
-    const f32x16 S = x6c_tile_rows<NQ>(xa, ones, [&](int q, int t) { return mu_l[(q * 4 + t) * 64 + lane]; });
+    const f32x16 S = x6c_tile_rows<NQ, kIsoChains>(xa, ones, [&](int q, int t) { return mu_l[(q * 4 + t) * 64 + lane]; });
     float r[16], res[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -1360,7 +1367,7 @@ void iso_accum_tiles(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
         for (int sp = 0; sp < 3; ++sp)
           xa[q][sp] = *reinterpret_cast<const bf16x8*>(xt + (sp * 32 + c) * RS + 16 * q + 8 * g);
       }
-      const f32x16 S = x6c_tile_rows<NQ>(xa, ones, [&](int q, int t4) { return mb[q][t4]; });
+      const f32x16 S = x6c_tile_rows<NQ, kIsoChains>(xa, ones, [&](int q, int t4) { return mb[q][t4]; });
       const double2* rw = rs_l + buf * 32;
       float r[16], res[16];
 #pragma unroll
