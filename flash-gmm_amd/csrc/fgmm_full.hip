@@ -1389,6 +1389,17 @@ hipError_t launch_bf16(const FullPlan& pl, const float* X, int64_t ldx, unsigned
 
 using namespace fgmm;
 
+namespace {
+// Rows per call of the bf16 contract, whose log-joint (N/32 tiles of KP x 32 floats)
+// must fit kMaxLjBytes: a multiple of 128 rows.  Larger calls run in chunks of this
+// many rows.
+int64_t full_bf16_chunk_rows(int64_t K) {
+  const int64_t KP = round_up(K < 1 ? 1 : K, kCompsPerWG);
+  const int64_t tiles = (int64_t)(kMaxLjBytes / ((size_t)KP * 32 * sizeof(float))) / 4 * 4;
+  return tiles * 32;
+}
+}  // namespace
+
 extern "C" size_t fgmm_full_workspace_bytes(int64_t N, int64_t K, int64_t D) {
   if (N < 0 || K < 0 || D < 1) return 0;
   return make_plan(N, K, D, false).total;
@@ -1396,7 +1407,9 @@ extern "C" size_t fgmm_full_workspace_bytes(int64_t N, int64_t K, int64_t D) {
 
 extern "C" size_t fgmm_full_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D, wants_stored_lj(flags), (flags & FGMM_FLAG_BF16) != 0).total;
+  const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
+  const int64_t rows = bf16 ? std::min(N, full_bf16_chunk_rows(K)) : N;
+  return make_plan(rows, K, D, wants_stored_lj(flags), bf16).total;
 }
 
 extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -1419,6 +1432,22 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   if (D > 128) return FGMM_ERR_UNSUPPORTED;
   if (N > kMaxRows || K > (int64_t)1 << 20) return FGMM_ERR_UNSUPPORTED;
   const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
+  if (bf16 && K > 0 && N > full_bf16_chunk_rows(K)) {
+    // The bf16 contract stores the log-joint, at most kMaxLjBytes per call: larger N
+    // runs as consecutive row chunks on one workspace, each chunk after the first
+    // adding its statistics to the outputs.  A phase split cannot span the chunks.
+    if (flags & (FGMM_FLAG_PHASE1 | FGMM_FLAG_PHASE2)) return FGMM_ERR_UNSUPPORTED;
+    const int64_t rows = full_bf16_chunk_rows(K);
+    for (int64_t r0 = 0; r0 < N; r0 += rows) {
+      const int64_t n = std::min(rows, N - r0);
+      const unsigned f = r0 == 0 ? flags : (flags | FGMM_FLAG_ACCUMULATE);
+      const int st = fgmm_full_estep_f32(X + r0 * ldx, ldx, n, D, mu, ldmu, K, prec_chol, log_pi,
+                                         logZ ? logZ + r0 : nullptr, Nk, mu_acc, sig_outer, workspace,
+                                         workspace_bytes, f, stream_);
+      if (st != FGMM_OK) return st;
+    }
+    return FGMM_OK;
+  }
   const FullPlan pl = make_plan(N, K, D, wants_stored_lj(flags), bf16);
   // The bf16 contract always stores the log-joint: N x K floats within kMaxLjBytes.
   if (bf16 && K > 0 && !pl.lj) return FGMM_ERR_UNSUPPORTED;

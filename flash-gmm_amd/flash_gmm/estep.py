@@ -312,8 +312,10 @@ def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
     whitening, L^T mu in float32, r rounded to bfloat16 for mu_acc and r x_d2 for
     sig_outer[k, d2, :] (which is then not exactly symmetric), fp32 accumulation and
     log-sum-exp.  That path always stores the log-joint (``recompute`` has no
-    effect) and takes at most 16 GiB / (4 K) rows per call; larger inputs go in row
-    chunks with ``accumulate``.
+    effect), at most 16 GiB of it at a time: the library runs larger N as row chunks
+    of 16 GiB / (4 K) rows on one workspace, each chunk adding its statistics to the
+    outputs, so the sums round once per chunk (a ``phase`` split of such a call is
+    refused).
     """
     _check_common(X, mu, log_pi)
     _require(precision in ("fp32", "bf16"), f"precision must be 'fp32' or 'bf16', got {precision!r}")

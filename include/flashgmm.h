@@ -87,8 +87,12 @@ enum fgmm_flags {
      *   full (flash_gmm_full_h100.py:71-228, :289-298): x and L rounded to bfloat16
      *     for the whitening, L^T mu fp32; r rounded for mu_acc and r x_d2 for
      *     sig_outer[k][d2][:], which is then not exactly symmetric.  This path
-     *     stores the log-joint of at most 16 GiB per call and runs larger N in
-     *     row chunks internally (same results as one call).
+     *     stores the log-joint, at most 16 GiB of it at a time: larger N runs as
+     *     consecutive row chunks of 16 GiB / (4 K_padded) rows on one workspace
+     *     (fgmm_full_workspace_bytes_ex sizes it for one chunk), each chunk adding
+     *     its statistics to the outputs, so the sums round once per chunk.  A
+     *     PHASE1 / PHASE2 call that needs more than one chunk returns
+     *     FGMM_ERR_UNSUPPORTED.
      * FGMM_FLAG_RECOMPUTE and STORE_LOGJOINT have no effect with it. */
     FGMM_FLAG_BF16 = 1u << 7,
     /* Opt-in: pass 1 also stores the fp32 log-joint (N/32 x K/32 tiles of
@@ -139,7 +143,7 @@ int fgmm_iso_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
 /* FGMM_NOALLOC_SCRATCH_BYTES per GPU, held from the library's first such call */
 /* on that GPU until the process ends.  Calls whose workspace                  */
 /* (fgmm_iso_workspace_bytes_ex with the same flags) exceeds it return         */
-/* FGMM_ERR_SCRATCH: about 1.4M rows at K=1024, D=128 (N=1M fits).             */
+/* FGMM_ERR_SCRATCH: about 1.5M rows at K=1024, D=128 (N=1M fits).             */
 /* FGMM_FLAG_STORE_LOGJOINT is rejected (FGMM_ERR_INVALID_ARG).  Every call on */
 /* a GPU uses that GPU's one array: calls that overlap on one GPU (different   */
 /* streams or host threads without ordering) race, and a PHASE2 call reads     */

@@ -123,3 +123,40 @@ def test_bad_precision_string(gpu_device):
     inp = data.full_clustered(10, 4, 8, seed=11)
     with pytest.raises(FlashGMMError):
         flash_gmm_estep_full(*[inp[k].to(gpu_device) for k in KEYS], precision="fp16")
+
+
+def test_log_joint_beyond_16gib_runs_in_row_chunks(gpu_device):
+    """N x K x 4 bytes above 16 GiB: the library splits the call into row chunks of
+    16 GiB / (4 K) rows on one workspace.  The result equals explicit calls on the same
+    boundaries (the first overwriting, the second accumulating) bit for bit, logZ of
+    sampled rows in both chunks matches the oracle, and a phase split is refused."""
+    from flash_gmm import _lib
+    dev = gpu_device
+    K, D = 1024, 8
+    chunk = (16 << 30) // (K * 32 * 4) // 4 * 4 * 32          # rows per 16 GiB of log-joint
+    N = chunk + 3000
+    assert N * K * 4 > 16 << 30
+    print(f"full bf16 chunked N={N} K={K} D={D} chunk={chunk}", flush=True)
+    inp = data.full_clustered(N, K, D, seed=21, device=dev)
+    L = _lib.lib()
+    assert L.fgmm_full_workspace_bytes_ex(N, K, D, _lib.FLAG_BF16) == \
+        L.fgmm_full_workspace_bytes_ex(chunk, K, D, _lib.FLAG_BF16)
+    args = [inp[k] for k in KEYS]
+    got = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, D, D, device=dev)]
+    full_estep_into(*args, *got, precision="bf16")
+    ref = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, D, D, device=dev)]
+    full_estep_into(args[0][:chunk], *args[1:], ref[0][:chunk], *ref[1:], precision="bf16")
+    full_estep_into(args[0][chunk:], *args[1:], ref[0][chunk:], *ref[1:], accumulate=True, precision="bf16")
+    torch.cuda.synchronize()
+    for u, v in zip(got, ref):
+        assert torch.equal(u, v)
+    assert abs(got[1].double().sum().item() - N) <= 1e-4 * N
+    rows = torch.cat([torch.arange(0, 512), torch.arange(chunk - 256, chunk + 256), torch.arange(N - 512, N)])
+    sub = {k: v.cpu() for k, v in inp.items()}
+    sub["X"] = sub["X"][rows]
+    lz = O.estep_full_bf16(*[sub[k] for k in KEYS])[0]
+    assert (got[0].cpu()[rows].double() - lz).abs().max().item() <= LOGZ_ATOL_BF16
+    with pytest.raises(FlashGMMError):
+        full_estep_into(*args, *got, phase=1, precision="bf16")
