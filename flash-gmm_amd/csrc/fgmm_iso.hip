@@ -8,42 +8,47 @@
 //   Nk_k = sum_n r_nk ; mu_acc_k = sum_n r_nk x_n ; sig_acc_k = sum_n r_nk ||x_n - mu_k||^2
 //
 // Kernels, all launched on the caller's stream:
-//   iso_prep    O(K*D): per-component constants (fp64), mu re-laid out in the
-//               matrix-core operand orders (fp32 and three-way bf16 splits with
-//               the centring offsets), and the needed-pair counters zeroed.
+//   iso_prep    O(K*D): per-component constants (fp64), mu as three-way bf16 splits
+//               with per-chunk centring offsets in matrix-core operand order, and
+//               the needed-pair counters zeroed.
 //   iso_lse     pass 1 up to D = 128, grid over row tiles.  Each wave keeps 32 rows
 //               of X resident in registers as bf16 splits and streams mu in blocks
 //               of 32 components through LDS; the cross term is the centred
 //               split-bf16 contraction (x6c_tile, lane = row, register = component)
 //               and the log-sum-exp is an online max/sum in registers.  Writes logZ
-//               and per-row (||x||^2, logZ2) in fp64; with the stored log-joint also
-//               its rows (row-major tiles), each row's block maximum, and after the
-//               last block the need masks and the needed-pair count.
-//   iso_lse_split
-//               pass 1 above D = 128: two waves per row tile, one half of D each,
-//               with the accurate fp32-step contraction (cross_tile).
+//               and per-row (||x||^2, logZ2) in fp64 and, after the last block, the
+//               need masks (one bit per row and 32-component block: set where the
+//               row's responsibility in the block can be nonzero) and their count;
+//               with the stored log-joint also its rows (row-major tiles) and each
+//               row's block maximum.
+//   iso_lse_ctile
+//               pass 1 above D = 128 (any D): the contraction tiled over components
+//               (128 per tile) as well as rows, the rows' chunks re-read and split
+//               per component tile, four accumulation chains.  Same outputs.
+//   iso_accum_gather / iso_accum_tiles
+//               pass 2 of the default plan up to D = 128: the log-joint of the
+//               needed (row, block) pairs recomputed bit for bit as pass 1 forms it,
+//               r = 2^(ll2 - logZ2), r^T X as split-bf16 products on the matrix cores,
+//               Nk and sig_acc on the VALU, one partial per (slab, component).  The
+//               gathering kernel queues the needed rows of each slab; the tile
+//               kernel (most pairs needed) visits every row.  The needed-pair count
+//               selects one of them on the device.
+//   iso_accum_drange
+//               pass 2 of the default plan above D = 128: per (slab, block, range of
+//               up to 1024 dimensions) four waves share the queued rows, each forming
+//               one chain of the contraction and a quarter of r^T X.
 //   iso_accum_sparse / iso_accum_lj
-//               pass 2 from the stored log-joint.  Both are launched; the count of
-//               needed register-row pairs left by pass 1 selects one on the device.
-//               The sparse kernel fetches each needed row pair into registers
-//               without any workgroup staging; the other stages X tiles in LDS for
-//               8 component blocks and reads the needed log-joint rows.  Either way
-//               r = 2^(ll2 - logZ2) and mu_acc += r^T X on the matrix cores with r as
-//               the A operand, Nk and sig_acc on the VALU, one partial per (slab,
-//               row group, component).
-//   iso_accum_lds / iso_accum_split
-//               pass 2 recomputing the log-joint (FGMM_FLAG_RECOMPUTE, small K or
-//               past the workspace cap): X tiles through LDS, S = X . mu^T on the
-//               matrix cores, then as above.
+//               pass 2 of the stored plan (FGMM_FLAG_STORE_LOGJOINT, D <= 256): the
+//               needed rows of the stored log-joint instead of a recomputation.
 //   iso_reduce  fixed-order fp64 sum of the slab partials (deterministic), or
 //               the atomic variant selected by FGMM_FLAG_ATOMIC_REDUCE.
 //   iso_bf16_*  the bf16 operand contract (FGMM_FLAG_BF16).
 //
-// Accuracy: pass 1 sums the split-bf16 chunk results in fp32 and combines them with
-// the fp64 ||x||^2 and constants; the fp32-step contraction keeps every 8 dimensions
-// in a fresh accumulator and sums chunk pairs in fp64 (cross_tile()).  A single fp32
-// chain over D=128 would leave ~3e-4 absolute error in logZ on clustered data; both
-// forms stay below 1e-4.
+// Accuracy: the split-bf16 contraction keeps each 16-dimension chunk's result small
+// (centred on the chunk's ||mu_q||^2) and sums the chunks in fp32 chains (two up to
+// D = 128, four above), then combines them with the fp64 ||x||^2 and constants.
+// A single fp32 chain of fp32 matrix steps over D=128 would leave ~3e-4 absolute
+// error in logZ on clustered data.
 
 #include "fgmm_common.hpp"
 
@@ -69,33 +74,34 @@ constexpr int kAccWaves = 8;   // pass-2 LDS variant: waves per workgroup
 constexpr int kAccThreads = 64 * kAccWaves;
 
 
-// The recomputing pass 2 runs the LDS-resident variant for D <= 128 (mu of 4
-// component blocks and 64-row X tiles in LDS), or for D > 128 the split variant
-// (two waves per component block, each holding half of mu in registers), for
-// which D is padded to a multiple of 64.
-__host__ __device__ constexpr bool accum_uses_lds(int DP) { return DP <= 128; }
-
-// LDS of the LDS-resident pass 2 with CB component blocks per workgroup (and
-// 8 / CB row groups of 32 rows): mu of the blocks, two X buffers, row state.
 constexpr size_t kMaxLds = 160 * 1024;
-__host__ __device__ constexpr size_t accum_lds_bytes_for(int DP, int CB) {
-  return (size_t)CB * DP * 32 * sizeof(float) +
-         (size_t)2 * 32 * (8 / CB) * (DP + 4) * sizeof(float) +
-         (size_t)2 * 32 * (8 / CB) * sizeof(double2);
-}
-// Component blocks per pass-2 workgroup: 4, or 2 / 1 when there are that few
-// blocks (K <= 64 / K <= 32) so that no wave idles, where the taller X tiles fit.
-// Recomputing pass 2 above D = 128: two waves per component block (one half of
-// the dimensions each), two blocks per 4-wave workgroup, one wave per SIMD.
-__host__ __device__ constexpr int split_parts(int DP) { return DP > 128 ? 2 : 1; }
-__host__ __device__ constexpr int split_blocks(int DP) { return 2; }
 
-__host__ inline int accum_blocks_per_group(int DP, int KB) {
-  if (!accum_uses_lds(DP)) return split_blocks(DP);
-  if (KB <= 1 && accum_lds_bytes_for(DP, 1) <= kMaxLds) return 1;
-  if (KB <= 2 && accum_lds_bytes_for(DP, 2) <= kMaxLds) return 2;
-  return kWaves;
+// Above D = 128 the default plan tiles pass 1 over components as well
+// (iso_lse_ctile) and splits pass 2 over dimension ranges (iso_accum_drange); D is
+// padded to a multiple of 64 there, so each of the four accumulation chains gets
+// the same number of 16-dimension chunks.
+constexpr int kCtWaves = 4;                               // waves per workgroup, one per SIMD
+constexpr int kCtBlocks = 4;                              // component blocks per pass-1 tile
+constexpr int kCtChains = 4;                              // accumulation chains (chunk q -> q % 4)
+constexpr int kCtStageOps = kCtBlocks * 2 * 4 * 64;       // bf16x8 per two-chunk operand stage (32 KiB)
+constexpr int kDrange = 1024;                             // dimensions of r^T X per pass-2 workgroup
+constexpr int kDrTiles = kDrange / 32 / kCtWaves;         // 32-column tiles per pass-2 wave
+
+__host__ __device__ constexpr size_t lse_ctile_base() {
+  return (size_t)2 * kCtStageOps * sizeof(bf16x8) + (size_t)2 * kCtBlocks * 32 * sizeof(double2);
 }
+// Component blocks whose need bounds (bf16, 32 rows per wave) fit beside the stages.
+__host__ __device__ constexpr int ctile_need_exact_cap() {
+  return (int)((kMaxLds - lse_ctile_base()) / (kCtWaves * 32 * 2));
+}
+__host__ __device__ constexpr int drange_rs(int DR) { return DR + 16; }   // bf16 row stride of the X tile
+__host__ __device__ constexpr size_t accum_drange_lds_bytes(int DR) {
+  return (size_t)2 * 32 * drange_rs(DR) * 2                 // x1, x2 of 32 rows
+         + (size_t)kCtWaves * 16 * 64 * sizeof(float)        // the four chains of S
+         + (size_t)32 * sizeof(double2)                      // row state
+         + (size_t)kCtWaves * 64 * sizeof(int);              // row queue per wave
+}
+
 __host__ inline int iso_padded_dim(int64_t D) {
   return D <= 128 ? (int)round_up(D < 1 ? 1 : D, 32) : (int)round_up(D, 64);
 }
@@ -114,8 +120,10 @@ struct IsoPlan {
   bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16)
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it (FGMM_FLAG_STORE_LOGJOINT)
   int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
-  bool need;    // default plan up to D = 128: pass 1 leaves need masks, pass 2 gathers
+  bool need;    // default plan: pass 1 leaves need masks, pass 2 gathers the needed rows
+  bool ctile;   // default plan above D = 128: component-tiled pass 1, dimension-range pass 2
   bool rexact;  // need masks from the block maxima kept in LDS (else the running-max bound)
+  int ndr;      // dimension ranges of the component-tiled pass 2
   size_t off_musw, off_mu3, off_kcblk, off_kclin, off_kcgat, off_rowstat, off_part_mu, off_part_nk,
       off_part_sig, off_lj, off_ljmax, off_ljmask, off_ljcount, total;
 };
@@ -130,11 +138,12 @@ __host__ __device__ constexpr int need_exact_cap(int DP) {
   return (int)((80 * 1024 - lse_lds_base(DP)) / (kWaves * 32 * 2));
 }
 
-// Pass 2 reads the stored log-joint when recomputation is not requested, D is at
-// least 33 (below, the recomputed contraction costs less than the extra traffic),
-// there are at least 4 component blocks, and the tiles fit under kMaxLjBytes.
+// Pass 2 reads the stored log-joint when it is requested, D is 33 to 256 (below,
+// the recomputed contraction costs less than the extra traffic; above, only the
+// default plan has kernels), there are at least 4 component blocks, and the tiles
+// fit under kMaxLjBytes.
 __host__ inline bool use_stored_lj(int64_t N, int DP, int KB, bool allow) {
-  return allow && DP >= 64 && KB >= 4 &&
+  return allow && DP >= 64 && DP <= 256 && KB >= 4 &&
          (size_t)round_up(cdiv(N, 32), 4) * (size_t)KB * kLjTile * sizeof(float) <= kMaxLjBytes;
 }
 
@@ -152,8 +161,10 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
   p.KP = p.KB * 32;
   p.bf16 = bf16;
   p.lj = !bf16 && use_stored_lj(N, p.DP, p.KB, allow_lj);
-  p.need = !bf16 && !p.lj && p.DP <= 128;
-  p.rexact = p.need && p.KB <= need_exact_cap(p.DP);
+  p.need = !bf16 && !p.lj;
+  p.ctile = p.need && p.DP > 128;
+  p.rexact = p.need && p.KB <= (p.ctile ? ctile_need_exact_cap() : need_exact_cap(p.DP));
+  p.ndr = p.ctile ? (int)cdiv(p.DP, kDrange) : 1;
   if (bf16) {
     p.cpg = bf16_blocks_per_group(p.DP, p.KB);
     p.rgroups = kAccWaves / (p.cpg * bf16_halves(p.DP));
@@ -164,16 +175,21 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
     p.cpg = (p.KB >= 8 && p.DP <= 192) ? 8 : 4;
     p.lj_nh = (p.DP > 128 && p.cpg == 4) ? 2 : 1;
     p.rgroups = kAccWaves / (p.cpg * p.lj_nh);
-  } else if (p.need) {
-    p.cpg = 1;        // one wave per (row slab, component block)
-    p.rgroups = 1;
   } else {
-    p.cpg = accum_blocks_per_group(p.DP, p.KB);
-    p.rgroups = accum_uses_lds(p.DP) ? kAccWaves / p.cpg : 1;
+    p.cpg = 1;        // one wave (D <= 128) or workgroup per (row slab, component block)
+    p.rgroups = 1;
   }
   p.ncg = (int)cdiv(p.KB, p.cpg);
   const int64_t tile_rows = 32 * p.rgroups;
-  if (p.need && N > 0 && p.KB > 0) {
+  if (p.ctile && N > 0 && p.KB > 0) {
+    // One 4-wave workgroup per (slab, block, dimension range) and compute unit (its
+    // X tile takes most of the LDS): about two rounds of workgroups.
+    int64_t want = cdiv((int64_t)2 * current_device_cus(), (int64_t)p.KB * p.ndr);
+    const int64_t max_slabs = cdiv(N, 32);
+    if (want > max_slabs) want = max_slabs;
+    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.nslab = (int)cdiv(N, p.rows_per_slab);
+  } else if (p.need && N > 0 && p.KB > 0) {
     // The gathering pass 2 runs one wave per SIMD: about two rounds of waves.
     int64_t want = cdiv((int64_t)8 * current_device_cus(), p.KB);
     const int64_t max_slabs = cdiv(N, 32);
@@ -194,7 +210,8 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
   }
   p.npart = p.nslab * p.rgroups;
   size_t off = 0;
-  p.off_musw = off;    off = align256(off + (size_t)p.KP * p.DP * sizeof(float));
+  // The bf16 contract's operands (the fp32 plans read only the split operands below).
+  p.off_musw = off;    off = align256(off + (bf16 ? (size_t)p.KP * p.DP * sizeof(float) : 0));
   p.off_mu3 = off;     off = align256(off + (size_t)p.KP * p.DP * 4 * 2);   // bf16 splits of mu
   p.off_kcblk = off;   off = align256(off + (size_t)p.KB * 32 * 2 * sizeof(double));
   p.off_kclin = off;   off = align256(off + (size_t)p.KP * 4 * sizeof(double));
@@ -219,8 +236,7 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int64_t ldmu, int64_t K,
                                                int D, int DP, const float* __restrict__ lss,
-                                               const float* __restrict__ lpi, f32x4* __restrict__ mu_sw,
-                                               double2* __restrict__ kc_blk, double4* __restrict__ kc_lin,
+                                               const float* __restrict__ lpi, double2* __restrict__ kc_blk, double4* __restrict__ kc_lin,
                                                double4* __restrict__ kc_gat, bf16x8* __restrict__ mu3,
                                                unsigned* __restrict__ ljcount) {
   __shared__ double sC[32], sB[32];
@@ -254,27 +270,14 @@ __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int
       b = 0.5 * exp(-l) * kLog2e;
       C = (lp - 0.5 * (double)D * (kLog2Pi + l)) * kLog2e - b * musq;
     }
-    // Pass 1 at D <= 128 contracts the centred cross term x.mu - sum_q o_q, so its
-    // constant carries + 2 b sum_q o_q; above, pass 1 takes C itself.
-    sC[c] = (DP <= 128 && valid) ? C + 2.0 * b * osum : C;
+    // The split-bf16 passes contract the centred cross term x.mu - sum_q o_q, so
+    // their constant carries + 2 b sum_q o_q.
+    sC[c] = valid ? C + 2.0 * b * osum : C;
     sB[c] = b;
     kc_lin[comp] = make_double4(C, b, musq, 0.0);
-    // The gathering pass 2 (D <= 128) takes the centred constant and, for
+    // The gathering passes 2 take the centred constant and, for
     // ||x - mu||^2 = ||x||^2 - 2 (x.mu - sum_q o_q) + (||mu||^2 - 2 sum_q o_q), the last term.
-    if (DP <= 128) kc_gat[comp] = make_double4(sC[c], b, musq - 2.0 * osum, 0.0);
-  }
-  // mu in matrix-core operand order: chunk m of lane (c, g) = mu[comp][8m+4g .. 8m+4g+3].
-  const int NM = DP / 8;
-  for (int m = 0; m < NM; ++m) {
-    f32x4 v = zero4();
-    const int d0 = 8 * m + 4 * g;
-    if (valid) {
-      if (d0 + 0 < D) v.x = mu[comp * ldmu + d0 + 0];
-      if (d0 + 1 < D) v.y = mu[comp * ldmu + d0 + 1];
-      if (d0 + 2 < D) v.z = mu[comp * ldmu + d0 + 2];
-      if (d0 + 3 < D) v.w = mu[comp * ldmu + d0 + 3];
-    }
-    mu_sw[((int64_t)kb * NM + m) * 64 + lane] = v;
+    kc_gat[comp] = make_double4(sC[c], b, musq - 2.0 * osum, 0.0);
   }
   // The same chunks as three-way bf16 splits for the bf16x6 pass 1,
   // mu3[kb][q][s][lane] = split s of mu[comp][16q + 8g .. 16q + 8g + 7] (s < 3), and
@@ -346,7 +349,6 @@ constexpr size_t lse_lds_bytes() {
 constexpr int kIsoChains = 2;
 
 // What pass 1 leaves for pass 2 besides logZ2 and ||x||^2.
-constexpr int kLjmNone = 0;    // nothing (the recomputing pass 2 above D = 128)
 constexpr int kLjmStore = 1;   // the stored log-joint, its block maxima and need masks
 constexpr int kLjmNeed = 2;    // need masks only (the default plan)
 
@@ -503,491 +505,236 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1 above D = 128: eight waves = 4 row groups x 2 halves of the dimensions,
-// so each wave holds half of its 32 rows in registers (two waves per SIMD).  Per
-// component block both halves form their fp64 partial cross terms; the second
-// half's go through LDS (two slots, by block parity) and the first-half wave adds
-// them in a fixed order and runs the online log-sum-exp.  One barrier per block.
+// Pass 1 of the default plan above D = 128 (any D).  The split operands of a row
+// no longer fit in registers for all of D, so the contraction is tiled over the
+// components as well: each wave owns a 32-row tile, and for each component tile of
+// kCtBlocks blocks (128 components) it streams its rows' chunks of 16 dimensions
+// from global memory (read once per component tile; from L2 or the MALL after the
+// first), splits them three ways into bf16 as they arrive and contracts them with
+// the tile's mu operands (bf16 splits and centring offsets), which the
+// workgroup's four waves share through an LDS double buffer of two-chunk stages.
+// Chunk q accumulates into chain q % 4 of each block with x6c_tile's products and
+// order; after the last chunk the chains are added as ((c0 + c1) + c2) + c3, and
+// the online log-sum-exp and the need bounds proceed as in iso_lse.  Four blocks x
+// four chains fill the 256 accumulator registers: one wave per SIMD.  The stored
+// plan (LJM = kLjmStore, D up to 256) runs the same kernel and also writes the
+// log-joint rows, their block maxima and the need masks, as iso_lse does.
 // ---------------------------------------------------------------------------
-template <int DP>
-constexpr size_t lse_split_lds_bytes() {
-  return (size_t)2 * DP * 32 * sizeof(float)                  // mu blocks, 2 buffers
-         + (size_t)3 * 32 * sizeof(double2)                    // constants, 3 buffers
-         + (size_t)2 * kWaves * 16 * 64 * sizeof(double)       // second-half partials
-         + (size_t)kWaves * 64 * sizeof(double);               // second-half ||x||^2
-}
-
-template <int DP, bool LJ>
-__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
-void iso_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
-                   const f32x4* __restrict__ mu_sw, const double2* __restrict__ kc_blk, int KB,
+template <int LJM>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kCtWaves, 64 * kCtWaves), amdgpu_waves_per_eu(1, 1)))
+void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int NQ,
+                   const bf16x8* __restrict__ mu3, const double2* __restrict__ kc_blk, int KB,
                    float* __restrict__ logZ, double2* __restrict__ rowstat, float* __restrict__ lj,
                    float* __restrict__ ljmax, unsigned* __restrict__ ljmask, unsigned* __restrict__ ljcount,
-                   int dense) {
-  constexpr int NM = DP / 8;
-  constexpr int NMH = NM / 2;             // chunks per half
-  constexpr int HD = DP / 2;
-  constexpr int BLK = NM * 64;            // float4 per 32-component block
-  constexpr int LPT = BLK / kAccThreads;
-  static_assert(BLK % kAccThreads == 0 && NMH % 2 == 0, "split shape");
+                   int dense, int rexact) {
+  constexpr bool LJ = LJM == kLjmStore;
+  constexpr int NT = 64 * kCtWaves;
+  constexpr int LPT = kCtStageOps / NT;   // operand loads per thread per stage
+  static_assert(kCtStageOps % NT == 0 && kCtBlocks * 32 <= NT, "stage split");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  unsigned char* p = lds_raw;
-  f32x4* mu_l = reinterpret_cast<f32x4*>(p);     p += 2 * BLK * sizeof(f32x4);
-  double2* kc_l = reinterpret_cast<double2*>(p); p += 3 * 32 * sizeof(double2);
-  double* ex = reinterpret_cast<double*>(p);     p += 2 * kWaves * 16 * 64 * sizeof(double);
-  double* xq = reinterpret_cast<double*>(p);
+  bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                                        // [2][stage]
+  double2* kc_l = reinterpret_cast<double2*>(lds_raw + 2 * kCtStageOps * sizeof(bf16x8));   // [2][blocks*32]
+  unsigned short* rmax_l = reinterpret_cast<unsigned short*>(lds_raw + lse_ctile_base());  // [wave][KB][32]
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: tile bases in scalars
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, g = lane >> 5;
-  const int rg = wave & 3, h = wave >> 2;
-  const int64_t tile = (int64_t)blockIdx.x * kWaves + rg;   // 32-row tile
+  const int64_t tile = (int64_t)blockIdx.x * kCtWaves + wave;   // 32-row tile
   const int64_t row = tile * 32 + c;
   const bool valid = row < N;
+  const int NS = NQ / 2;                        // stages per component tile (even: NQ % 4 == 0)
+  const int nstage = (int)cdiv(KB, kCtBlocks) * NS;
+  const int nq_full = D / 16;                   // chunks that end at or before D
 
-  f32x4 st[LPT];
-  double2 kst = make_double2(0.0, 0.0);
-  auto fetch = [&](int kb) {
-    const f32x4* src = mu_sw + (int64_t)kb * BLK;
+  // Stage s = (component tile s / NS, chunk pair s % NS).  Thread element u covers
+  // block u / 2 of the tile and entry (u % 2) * NT + tid of its 512 = (chunk in the
+  // pair, split, lane): the same order in LDS, so operand (b, qq, t) of a lane is
+  // at b * 512 + (qq * 4 + t) * 64 + lane.  Blocks at or past KB read zero.
+  const int64_t blk_ops = (int64_t)NQ * 4 * 64;     // bf16x8 per block
+  const int64_t all_ops = (int64_t)KB * blk_ops;
+  bf16x8 st[LPT];
+  double2 kst = make_double2(-INFINITY, 0.0);
+  auto fetch = [&](int s) {
+    const int ct = s / NS, sp = s - ct * NS;
+    const int64_t base = (int64_t)ct * kCtBlocks * blk_ops + (int64_t)sp * 2 * 4 * 64;
+    int64_t avail = (all_ops - base) * (int64_t)sizeof(bf16x8);
+    if (avail > ((int64_t)1 << 31) - 16) avail = ((int64_t)1 << 31) - 16;
+    const buf_rsrc r = make_rsrc(mu3 + base, (uint32_t)avail);
 #pragma unroll
-    for (int q = 0; q < LPT; ++q) st[q] = src[q * kAccThreads + tid];
-    if (tid < 32) kst = kc_blk[(int64_t)kb * 32 + tid];
+    for (int u = 0; u < LPT; ++u) {
+      const int soff = (int)(((int64_t)(u >> 1) * blk_ops + (u & 1) * NT) * (int64_t)sizeof(bf16x8));
+      st[u] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, tid * (int)sizeof(bf16x8), soff, 0));
+    }
+    if (sp == 0 && tid < kCtBlocks * 32) {
+      const int64_t kc = (int64_t)ct * kCtBlocks * 32 + tid;
+      kst = kc < (int64_t)KB * 32 ? kc_blk[kc] : make_double2(-INFINITY, 0.0);
+    }
   };
-  // mu of block kb -> buffer kb & 1; its constants -> buffer kb % 3 (the first-half
-  // waves read them after the block's barrier, while others may commit ahead).
-  auto commit = [&](int kb) {
+  auto commit = [&](int s, int buf) {
+    const int ct = s / NS, sp = s - ct * NS;
 #pragma unroll
-    for (int q = 0; q < LPT; ++q) mu_l[(kb & 1) * BLK + q * kAccThreads + tid] = st[q];
-    if (tid < 32) kc_l[(kb % 3) * 32 + tid] = kst;
+    for (int u = 0; u < LPT; ++u) mu_l[buf * kCtStageOps + u * NT + tid] = st[u];
+    if (sp == 0 && tid < kCtBlocks * 32) kc_l[(ct & 1) * kCtBlocks * 32 + tid] = kst;
   };
+
+  // The wave's rows, dimensions 16q + 8g .. + 7 of chunk q (zero past D and N).
+  const float* xrow = X + (valid ? row : 0) * ldx + 8 * g;
+  auto xload = [&](int q, f32x4& lo, f32x4& hi) {
+    if (q < nq_full) {
+      lo = *reinterpret_cast<const f32x4*>(xrow + 16 * q);
+      hi = *reinterpret_cast<const f32x4*>(xrow + 16 * q + 4);
+      if (!valid) { lo = zero4(); hi = zero4(); }
+    } else {
+      lo = load_row4(X, ldx, row, 16 * q + 8 * g, D, valid);
+      hi = load_row4(X, ldx, row, 16 * q + 8 * g + 4, D, valid);
+    }
+  };
+  f32x4 xr[2][2][2];   // [stage parity][chunk in the pair][lo, hi]
+  auto xstage = [&](int s, f32x4 (&dst)[2][2]) {
+    if (s >= nstage) return;
+    const int sp = s % NS;
+    xload(2 * sp, dst[0][0], dst[0][1]);
+    xload(2 * sp + 1, dst[1][0], dst[1][1]);
+  };
+
   fetch(0);
-
-  f32x4 xb[NMH];
-  double xsq = 0.0;
-#pragma unroll
-  for (int m = 0; m < NMH; ++m) {
-    xb[m] = load_row4(X, ldx, row, h * HD + 8 * m + 4 * g, D, valid);
-    xsq = fma((double)xb[m].x, (double)xb[m].x, xsq);
-    xsq = fma((double)xb[m].y, (double)xb[m].y, xsq);
-    xsq = fma((double)xb[m].z, (double)xb[m].z, xsq);
-    xsq = fma((double)xb[m].w, (double)xb[m].w, xsq);
-  }
-  xsq += __shfl_xor(xsq, 32);
-  if (h == 1) xq[rg * 64 + lane] = xsq;
-  commit(0);
+  xstage(0, xr[0]);
+  commit(0, 0);
   lds_barrier();
-  if (h == 0) xsq += xq[rg * 64 + lane];
 
+  f32x16 acc[kCtBlocks][kCtChains];
+#pragma unroll
+  for (int b = 0; b < kCtBlocks; ++b) {
+#pragma unroll
+    for (int h = 0; h < kCtChains; ++h) acc[b][h] = zero16();
+  }
+  const bf16x8 ones = x6c_ones(lane);
+  double xsq_part = 0.0, xsq = 0.0;
   double mx = -INFINITY;
   float sm = 0.0f;
-  float run_max = -INFINITY;   // running max of the row's stored log-joint
-  for (int kb = 0; kb < KB; ++kb) {
-    const int buf = kb & 1;
-    const bool more = kb + 1 < KB;
-    if (more) fetch(kb + 1);
-    const f32x4* mp = mu_l + buf * BLK + h * NMH * 64 + lane;
-    double xm[16];
-    cross_tile<NMH>(xm, [&](int m) { return mp[m * 64]; }, [&](int m) { return xb[m]; });
-    double* exb = ex + (size_t)(buf * kWaves + rg) * 16 * 64 + lane;
-    if (h == 1) {
+  float run_max = -INFINITY;   // running max of the row's block maxima (running-max need bound)
+  unsigned pairs = 0;
+
+  // Component tile ct is complete: log-joint, log-sum-exp and need bounds per block.
+  auto finish_tile = [&](int ct) {
+    if (ct == 0) xsq = xsq_part + __shfl_xor(xsq_part, 32);
+    const double2* kp0 = kc_l + (ct & 1) * kCtBlocks * 32 + g * 16;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) exb[i * 64] = xm[i];
+    for (int b = 0; b < kCtBlocks; ++b) {
+      const int kb = ct * kCtBlocks + b;
+      if (kb < KB) {
+        double ll[16];
+        double bm = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float S = ((acc[b][0][i] + acc[b][1][i]) + acc[b][2][i]) + acc[b][3][i];
+          const double2 cb = kp0[b * 32 + i];
+          ll[i] = fma(-cb.y, fma(-2.0, (double)S, xsq), cb.x);
+          bm = fmax(bm, ll[i]);
+        }
+        asm volatile("" : "+v"(bm));
+        const double mn = fmax(mx, bm);
+        const double ms = (mn == -INFINITY) ? 0.0 : mn;
+        float a = sm * fast_exp2((float)(mx - ms));
+#pragma unroll
+        for (int i = 0; i < 16; ++i) a += fast_exp2((float)(ll[i] - ms));
+        sm = a;
+        mx = mn;
+        if constexpr (LJ) {
+          lj_put_rows(lj + (tile * KB + kb) * kLjTile, ljmax + (tile * KB + kb) * 32, c, g, ll, bm, a, run_max,
+                      dense != 0);
+        } else {
+          const float R = lj_row_max(bm);
+          if (rexact) {
+            if (g == 0) rmax_l[(wave * KB + kb) * 32 + c] = bf16_bits_up(R);
+          } else {
+            run_max = fmaxf(run_max, R);
+            const bool nb = valid && (dense != 0 || !(R - run_max < -kLjSkipGap));
+            const unsigned bits = (unsigned)__builtin_amdgcn_ballot_w64(nb);
+            if (lane == 0) ljmask[tile * KB + kb] = bits;
+            pairs += __builtin_popcount(bits);
+          }
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < kCtChains; ++h) acc[b][h] = zero16();
     }
-    if (more) commit(kb + 1);
+  };
+
+  // One stage; P = s & 1 is the LDS buffer and the register stage, and the chunks
+  // 2 sp, 2 sp + 1 go to chains 2P, 2P + 1 (NS is even, so sp and s share parity).
+  auto stage = [&](int s, auto par) {
+    constexpr int P = decltype(par)::value;
+    const int ct = s / NS, sp = s - ct * NS;
+    const bool more = s + 1 < nstage;
+    if (more) fetch(s + 1);
+    xstage(s + 1, xr[1 - P]);
+    const bf16x8* mp = mu_l + P * kCtStageOps + lane;
+#pragma unroll
+    for (int qq = 0; qq < 2; ++qq) {
+      bf16x8 xb[3];
+      split3_bf16(xr[P][qq][0], xr[P][qq][1], xb);
+      if (ct == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xsq_part = fma((double)xr[P][qq][0][e], (double)xr[P][qq][0][e], xsq_part);
+          xsq_part = fma((double)xr[P][qq][1][e], (double)xr[P][qq][1][e], xsq_part);
+        }
+      }
+      bf16x8 a[kCtBlocks][4];
+#pragma unroll
+      for (int b = 0; b < kCtBlocks; ++b) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) a[b][t] = mp[b * 512 + (qq * 4 + t) * 64];
+      }
+      // Steps in x6c_tile's order: x2 mu2, x1 mu3, x3 mu1, x2 mu1, x1 mu2, -o, x1 mu1.
+#pragma unroll
+      for (int step = 0; step < 7; ++step) {
+#pragma unroll
+        for (int b = 0; b < kCtBlocks; ++b) {
+          const bf16x8 A = step == 0 ? a[b][1] : step == 1 ? a[b][2] : step <= 3 ? a[b][0]
+                         : step == 4 ? a[b][1] : step == 5 ? a[b][3] : a[b][0];
+          const bf16x8 B = step == 0 ? xb[1] : step == 1 ? xb[0] : step == 2 ? xb[2]
+                         : step == 3 ? xb[1] : step == 4 ? xb[0] : step == 5 ? ones : xb[0];
+          acc[b][2 * P + qq] = mfma_bf16(A, B, acc[b][2 * P + qq]);
+        }
+      }
+    }
+    if (more) commit(s + 1, 1 - P);
     lds_barrier();
-    if (h == 0) {
-      const double2* kp = kc_l + (kb % 3) * 32 + g * 16;
-      double ll[16];
-      double bm = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const double2 cb = kp[i];
-        ll[i] = fma(-cb.y, fma(-2.0, xm[i] + exb[i * 64], xsq), cb.x);
-        bm = fmax(bm, ll[i]);
-      }
-      const double mn = fmax(mx, bm);
-      const double ms = (mn == -INFINITY) ? 0.0 : mn;
-      float acc = sm * fast_exp2((float)(mx - ms));
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc += fast_exp2((float)(ll[i] - ms));
-      sm = acc;
-      mx = mn;
-      if constexpr (LJ)
-        lj_put_rows(lj + (tile * KB + kb) * kLjTile, ljmax + (tile * KB + kb) * 32, c, g, ll, bm, acc,
-                    run_max, dense != 0);
-    }
-  }
-
-  if (h == 0) {
-    const double mo = __shfl_xor(mx, 32);
-    const float so = __shfl_xor(sm, 32);
-    const double mn = fmax(mx, mo);
-    const double ms = (mn == -INFINITY) ? 0.0 : mn;
-    const float tot = sm * fast_exp2((float)(mx - ms)) + so * fast_exp2((float)(mo - ms));
-    const double lz2 = mn + (double)log2f(tot);
-    if (valid && g == 0) {
-      rowstat[row] = make_double2(xsq, lz2);
-      if (logZ) logZ[row] = (float)(lz2 * kLn2);
-    }
-    if constexpr (LJ) {
-      if (g == 0) lj_put_masks(ljmax + tile * KB * 32, ljmask + tile * KB, ljcount + (tile & 63), KB, c, lz2,
-                   valid, dense != 0);
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Pass 2: responsibilities and sufficient statistics, split over components.
-// ---------------------------------------------------------------------------
-template <int DP, int CB>
-constexpr size_t accum_lds_lds_bytes() {
-  return accum_lds_bytes_for(DP, CB);
-}
-
-template <int DP, int CB>
-__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
-void iso_accum_lds(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
-                   const f32x4* __restrict__ mu_sw, const double4* __restrict__ kc_lin, int KB, int KP,
-                   const double2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
-                   float* __restrict__ part_mu, float* __restrict__ part_nk, float* __restrict__ part_sig,
-                   int dense) {
-  constexpr int NM = DP / 8;
-  constexpr int NJ = DP / 32;
-  constexpr int RS = DP + 4;
-  constexpr int V4 = DP / 4;
-  constexpr int BLK = NM * 64;                   // float4 per 32-component block
-  constexpr int RG = kAccWaves / CB;             // row groups (32 rows each)
-  constexpr int TR = 32 * RG;                    // rows per super-tile
-  constexpr int LPT = (TR * V4) / kAccThreads;   // float4 loads per thread per super-tile
-  static_assert((TR * V4) % kAccThreads == 0 && kAccWaves % CB == 0, "even split");
-
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  f32x4* mu_l = reinterpret_cast<f32x4*>(lds_raw);                                        // [CB][BLK]
-  float* xs = reinterpret_cast<float*>(lds_raw + CB * BLK * sizeof(f32x4));               // [2][TR*RS]
-  RowStat* rs = reinterpret_cast<RowStat*>(lds_raw + CB * BLK * sizeof(f32x4) +
-                                           2 * TR * RS * sizeof(float));                  // [2][TR]
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = lane & 31, g = lane >> 5;
-  const int cbw = wave % CB, rg = wave / CB;
-  const int slab = blockIdx.x % nslab;
-  const int cg = blockIdx.x / nslab;
-  const int kb = cg * CB + cbw;
-  const bool active = kb < KB;
-
-  const int64_t r_begin = (int64_t)slab * rows_per_slab;
-  int64_t r_end = r_begin + rows_per_slab;
-  if (r_end > N) r_end = N;
-  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
-
-  // mu of the workgroup's CB component blocks -> LDS (zeros past KB).
-  for (int idx = tid; idx < CB * BLK; idx += kAccThreads) {
-    const int kbq = cg * CB + idx / BLK;
-    mu_l[idx] = (kbq < KB) ? mu_sw[(int64_t)kbq * BLK + (idx % BLK)] : zero4();
-  }
-  double Ck = -INFINITY;
-  float bkf = 0.0f, musqf = 0.0f;
-  if (active) {
-    const double4 kc = kc_lin[(int64_t)kb * 32 + c];
-    Ck = kc.x; bkf = (float)kc.y; musqf = (float)kc.z;
-  }
-
-  f32x16 acc[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
-  float nk = 0.0f, sig = 0.0f;
-
-  f32x4 stage[LPT];
-  double2 rstage = make_double2(0.0, INFINITY);
-  const bool full_d = (D == DP);
-  auto fetch = [&](int t) {
-    const int64_t row0 = r_begin + (int64_t)t * TR;
-    if (full_d && row0 + TR <= r_end) {
-      // Interior tile: no row or column masking.
-      const float* src = X + row0 * ldx;
-#pragma unroll
-      for (int q = 0; q < LPT; ++q) {
-        const int idx = q * kAccThreads + tid;
-        stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < LPT; ++q) {
-        const int idx = q * kAccThreads + tid;
-        const int rr = idx / V4, c4 = idx % V4;
-        const int64_t row = row0 + rr;
-        stage[q] = load_row4(X, ldx, row, c4 * 4, D, row < r_end);
-      }
-    }
-    if (tid < TR) {
-      const int64_t row = row0 + tid;
-      rstage = (row < r_end) ? rowstat[row] : make_double2(0.0, INFINITY);
-    }
+    if (sp == NS - 1) finish_tile(ct);
   };
-  auto commit = [&](int buf) {
-    float* dst = xs + buf * TR * RS;
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) {
-      const int idx = q * kAccThreads + tid;
-      const int rr = idx / V4, c4 = idx % V4;
-      *reinterpret_cast<f32x4*>(dst + rr * RS + c4 * 4) = stage[q];
-    }
-    if (tid < TR) rs[buf * TR + tid] = RowStat{rstage.y, (float)rstage.x, 0.0f};
-  };
-
-  if (ntiles > 0) {
-    fetch(0);
-    commit(0);
-  }
-  __syncthreads();
-
-  const f32x4* mb = mu_l + cbw * BLK + lane;
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    const bool more = t + 1 < ntiles;
-    const float* xt = xs + buf * TR * RS + rg * 32 * RS;
-    const RowStat* rt = rs + buf * TR + rg * 32;
-    float xm[16];
-    float r[16];
-    if (active) {
-      cross_tile_fast<NM>(
-          xm, [&](int m) { return *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * m + 4 * g); },
-          [&](int m) { return mb[m * 64]; });
-      const RowStat* rbase = rt + 4 * g;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ro = 8 * (i >> 2) + (i & 3);
-        // One 16-byte LDS read per row: {logZ2 (fp64), ||x||^2 (fp32), pad}.
-        const uint4 w = *reinterpret_cast<const uint4*>(rbase + ro);
-        const double q = __hiloint2double((int)w.y, (int)w.x);
-        const float u = fmaf(-2.0f, xm[i], __uint_as_float(w.z));  // ||x||^2 - 2 x.mu
-        const float dq = (float)(Ck - q);                          // C_k - logZ2, rounded once
-        const float rv = fast_exp2(fmaf(-bkf, u, dq));
-        nk += rv;
-        sig = fmaf(rv, u + musqf, sig);
-        r[i] = rv;
-      }
-    }
-    if (more) fetch(t + 1);
-    if (active) {
-      const float* xbase = xt + 4 * g * RS + c;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ro = 8 * (i >> 2) + (i & 3);
-        // A step whose 64 responsibilities are all exactly zero adds nothing:
-        // skip it (wave-uniform branch; identical results).  With a single MFMA
-        // per step the test costs more than it saves.
-        if (NJ < 2 || dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
-#pragma unroll
-          for (int j = 0; j < NJ; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
-        }
-      }
-    }
-    if (more) commit(buf ^ 1);
-    __syncthreads();
+  for (int s = 0; s < nstage; s += 2) {
+    stage(s, std::integral_constant<int, 0>{});
+    stage(s + 1, std::integral_constant<int, 1>{});
   }
 
-  if (active) {
-    nk += __shfl_xor(nk, 32);
-    sig += __shfl_xor(sig, 32);
-    const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[j][i];
-    }
-    if (g == 0) {
-      part_nk[kbase + c] = nk;
-      part_sig[kbase + c] = sig;
-    }
+  // Merge the two half-waves that hold the same row.
+  const double mo = __shfl_xor(mx, 32);
+  const float so = __shfl_xor(sm, 32);
+  const double mn = fmax(mx, mo);
+  const double ms = (mn == -INFINITY) ? 0.0 : mn;
+  const float tot = sm * fast_exp2((float)(mx - ms)) + so * fast_exp2((float)(mo - ms));
+  const double lz2 = mn + (double)log2f(tot);
+  if (valid && g == 0) {
+    rowstat[row] = make_double2(xsq, lz2);
+    if (logZ) logZ[row] = (float)(lz2 * kLn2);
   }
-}
-
-// ---------------------------------------------------------------------------
-// Pass 2 (recomputing) for D > 128: the dimensions are split into NQ = 2 halves,
-// one wave per (component block, half), SB = 2 component blocks per workgroup.
-// Each wave keeps mu of its block and half in registers and forms the accurate
-// fp64 partial contraction of the tile over its half; the partials meet in LDS
-// and are added in a fixed order, so both waves of a block form the same r.  Each
-// wave then accumulates r^T X for the columns of its half.  The fp64 contraction,
-// half of mu and the accumulators need more than the 256 registers of two waves
-// per SIMD, so this kernel runs one wave per SIMD.
-// ---------------------------------------------------------------------------
-template <int DP>
-constexpr size_t accum_split_lds_bytes() {
-  return (size_t)2 * 32 * (DP + 4) * sizeof(float)        // X, 2 buffers of 32 rows
-         + (size_t)2 * 32 * sizeof(double2)                // row state, 2 buffers
-         + (size_t)split_parts(DP) * split_blocks(DP) * 16 * 64 * sizeof(double);  // partials
-}
-
-template <int DP>
-__global__ __attribute__((amdgpu_flat_work_group_size(64 * split_parts(DP) * split_blocks(DP),
-                                                      64 * split_parts(DP) * split_blocks(DP)),
-                          amdgpu_waves_per_eu(1, 1)))
-void iso_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
-                     const f32x4* __restrict__ mu_sw, const double4* __restrict__ kc_lin, int KB, int KP,
-                     const double2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
-                     float* __restrict__ part_mu, float* __restrict__ part_nk,
-                     float* __restrict__ part_sig, int dense) {
-  constexpr int NQ = split_parts(DP);
-  constexpr int SB = split_blocks(DP);
-  constexpr int NT = 64 * NQ * SB;   // threads
-  constexpr int NM = DP / 8;         // operand chunks of a full row
-  constexpr int PW = DP / NQ;        // dimensions per part
-  constexpr int NMQ = PW / 8;        // chunks per part
-  constexpr int NJQ = PW / 32;       // accumulator tiles per part
-  constexpr int RS = DP + 4;
-  constexpr int V4 = DP / 4;
-  constexpr int LPT = (32 * V4) / NT;
-  static_assert((32 * V4) % NT == 0 && PW % 32 == 0 && NMQ % 2 == 0, "split shape");
-
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  float* xs = reinterpret_cast<float*>(lds_raw);                                         // [2][32*RS]
-  double2* rs = reinterpret_cast<double2*>(lds_raw + 2 * 32 * RS * sizeof(float));      // [2][32]
-  double* ex = reinterpret_cast<double*>(lds_raw + 2 * 32 * RS * sizeof(float) +
-                                         2 * 32 * sizeof(double2));                      // [NQ*SB][16][64]
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = lane & 31, g = lane >> 5;
-  const int cb = wave % SB, qp = wave / SB;   // component block, dimension part
-  const int slab = blockIdx.x % nslab;
-  const int cg = blockIdx.x / nslab;
-  const int kb = cg * SB + cb;
-  const bool active = kb < KB;
-
-  const int64_t r_begin = (int64_t)slab * rows_per_slab;
-  int64_t r_end = r_begin + rows_per_slab;
-  if (r_end > N) r_end = N;
-  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
-
-  f32x4 mub[NMQ];
-#pragma unroll
-  for (int m = 0; m < NMQ; ++m)
-    mub[m] = active ? mu_sw[((int64_t)kb * NM + qp * NMQ + m) * 64 + lane] : zero4();
-  double Ck = -INFINITY, bk = 0.0, musq = 0.0;
-  if (active) {
-    const double4 kc = kc_lin[(int64_t)kb * 32 + c];
-    Ck = kc.x; bk = kc.y; musq = kc.z;
-  }
-
-  f32x16 acc[NJQ];
-#pragma unroll
-  for (int j = 0; j < NJQ; ++j) acc[j] = zero16();
-  float nk = 0.0f, sig = 0.0f;
-
-  f32x4 stage[LPT];
-  double2 rstage = make_double2(0.0, INFINITY);
-  const bool full_d = (D == DP);
-  auto fetch = [&](int t) {
-    const int64_t row0 = r_begin + (int64_t)t * 32;
-    if (full_d && row0 + 32 <= r_end) {
-      const float* src = X + row0 * ldx;
-#pragma unroll
-      for (int q = 0; q < LPT; ++q) {
-        const int idx = q * NT + tid;
-        stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < LPT; ++q) {
-        const int idx = q * NT + tid;
-        const int64_t row = row0 + idx / V4;
-        stage[q] = load_row4(X, ldx, row, (idx % V4) * 4, D, row < r_end);
-      }
-    }
-    if (tid < 32) {
-      const int64_t row = row0 + tid;
-      rstage = (row < r_end) ? rowstat[row] : make_double2(0.0, INFINITY);
-    }
-  };
-  auto commit = [&](int buf) {
-    float* dst = xs + buf * 32 * RS;
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) {
-      const int idx = q * NT + tid;
-      *reinterpret_cast<f32x4*>(dst + (idx / V4) * RS + (idx % V4) * 4) = stage[q];
-    }
-    if (tid < 32) rs[buf * 32 + tid] = rstage;
-  };
-
-  if (ntiles > 0) {
-    fetch(0);
-    commit(0);
-  }
-  __syncthreads();
-
-  double* my_ex = ex + wave * 16 * 64 + lane;
-  const double* ex_blk = ex + cb * 16 * 64 + lane;   // part p of this block at + p * SB * 1024
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    const bool more = t + 1 < ntiles;
-    const float* xt = xs + buf * 32 * RS;
-    const double2* rt = rs + buf * 32;
-    if (active) {
-      // Accurate partial contraction (fp64 chunk sums), as in pass 1: at these
-      // widths fp32 chains lose too much in ||x - mu||^2.
-      double xm[16];
-      const float* xrow = xt + c * RS + qp * PW + 4 * g;
-      cross_tile<NMQ>(
-          xm, [&](int m) { return *reinterpret_cast<const f32x4*>(xrow + 8 * m); },
-          [&](int m) { return mub[m]; });
-#pragma unroll
-      for (int i = 0; i < 16; ++i) my_ex[i * 64] = xm[i];
-    }
-    __syncthreads();
-    if (more) fetch(t + 1);
-    if (active) {
-      float r[16];
-      const double2* rbase = rt + 4 * g;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ro = 8 * (i >> 2) + (i & 3);
-        double xm = ex_blk[i * 64];                  // parts added in a fixed order
-#pragma unroll
-        for (int p = 1; p < NQ; ++p) xm += ex_blk[(p * SB * 16 + i) * 64];
-        const double2 w = rbase[ro];                 // (||x||^2, logZ2)
-        const double u = fma(-2.0, xm, w.x);        // ||x||^2 - 2 x.mu
-        const float rv = fast_exp2((float)(fma(-bk, u, Ck) - w.y));
-        if (qp == 0) {
-          nk += rv;
-          sig = fmaf(rv, (float)(u + musq), sig);
-        }
-        r[i] = rv;
-        // Groups of 4 rows: keeps the scheduler from hoisting all 16 * NQ LDS
-        // reads (2 registers each) ahead of their use.
-        if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-      }
-      const float* xbase = xt + 4 * g * RS + qp * PW + c;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ro = 8 * (i >> 2) + (i & 3);
-        if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
-#pragma unroll
-          for (int j = 0; j < NJQ; ++j) acc[j] = mfma32(r[i], xbase[ro * RS + 32 * j], acc[j]);
-        }
-      }
-    }
-    if (more) commit(buf ^ 1);
-    __syncthreads();
-  }
-
-  if (active) {
-    const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
-#pragma unroll
-    for (int j = 0; j < NJQ; ++j) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        part_mu[(kbase + acc_row(i, g)) * DP + qp * PW + 32 * j + c] = acc[j][i];
-    }
-    if (qp == 0) {
-      nk += __shfl_xor(nk, 32);
-      sig += __shfl_xor(sig, 32);
-      if (g == 0) {
-        part_nk[kbase + c] = nk;
-        part_sig[kbase + c] = sig;
-      }
+  if constexpr (LJ) {
+    if (g == 0) lj_put_masks(ljmax + tile * KB * 32, ljmask + tile * KB, ljcount + (tile & 63), KB, c, lz2,
+                             valid, dense != 0);
+  } else if (rexact) {
+    const unsigned short* rm = rmax_l + wave * KB * 32 + c;
+    if (g == 0)
+      need_put_masks([&](int kb) { return bf16_bits_to_float(rm[kb * 32]); }, ljmask + tile * KB,
+                     ljcount + (tile & 63), KB, c, lz2, valid, dense != 0);
+  } else {
+    const unsigned nanbits = (unsigned)__builtin_amdgcn_ballot_w64(valid && g == 0 && lz2 != lz2);
+    if (lane == 0) {
+      if (nanbits != 0)
+        for (int kb = 0; kb < KB; ++kb) ljmask[tile * KB + kb] |= nanbits;
+      if (pairs != 0) atomicAdd(ljcount + (tile & 63), pairs);
     }
   }
 }
@@ -1410,6 +1157,234 @@ void iso_accum_tiles(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 #pragma unroll
       for (int i = 0; i < 16; ++i) part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[j][i];
     }
+    if (g == 0) {
+      part_nk[kbase + c] = nk;
+      part_sig[kbase + c] = sig;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2 of the default plan above D = 128.  One workgroup of four waves per (row
+// slab, component block, range of up to kDrange dimensions).  The waves walk the
+// slab's need words alike, so they queue the same rows; for every 32 queued rows:
+//   - wave w forms chain w of S = X mu^T, the chunks q = w, w + 4, ... of all of D
+//     with x6c_tile_rows' products and order (mu's operands read from global
+//     memory), and writes the first two bf16 splits of those of its chunks that lie
+//     in the workgroup's range to the LDS tile of the rows;
+//   - the four chains meet in LDS and every wave adds them as pass 1 does,
+//     ((c0 + c1) + c2) + c3, so S, the log-joint and r equal pass 1's bit for bit;
+//   - r = 2^(ll2 - logZ2), and wave w accumulates r^T X for its quarter of the
+//     range's 32-column tiles (r2 x1 + r1 x2 + r1 x1, the rows read transposed from
+//     LDS); wave 0 of the first range also sums Nk and sig_acc.
+// Wider D runs several ranges, each workgroup recomputing S.  Workgroups are dealt
+// to the XCDs so that each XCD serves a contiguous run of component blocks: at this
+// width mu of a block is the larger operand stream, and it stays in that XCD's L2.
+// ---------------------------------------------------------------------------
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kCtWaves, 64 * kCtWaves), amdgpu_waves_per_eu(1, 1)))
+void iso_accum_drange(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int NQ, int DP,
+                      const bf16x8* __restrict__ mu3, const double4* __restrict__ kc_gat, int KB, int KP,
+                      const double2* __restrict__ rowstat, const unsigned* __restrict__ need, int nslab,
+                      int64_t rows_per_slab, int ndr, float* __restrict__ part_mu, float* __restrict__ part_nk,
+                      float* __restrict__ part_sig, int dense) {
+  // Workgroup -> (block, slab, range), blocks contiguous per XCD.
+  const int64_t total = (int64_t)KB * nslab * ndr;
+  const int64_t per = cdiv(total, 8);
+  const int64_t item = (int64_t)(blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (item >= total) return;   // uniform over the workgroup
+  const int dr = (int)(item % ndr);
+  const int slab = (int)((item / ndr) % nslab);
+  const int kb = (int)(item / ((int64_t)ndr * nslab));
+
+  const int RS = drange_rs(DP < kDrange ? DP : kDrange);
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  unsigned char* lp = lds_raw;
+  __bf16* xt = reinterpret_cast<__bf16*>(lp);     lp += (size_t)2 * 32 * RS * 2;   // [split][row][RS]
+  float* ex = reinterpret_cast<float*>(lp);       lp += (size_t)kCtWaves * 16 * 64 * sizeof(float);
+  double2* rs_l = reinterpret_cast<double2*>(lp); lp += (size_t)32 * sizeof(double2);
+  int* q_all = reinterpret_cast<int*>(lp);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  int* q_l = q_all + wave * 64;
+
+  const int d0 = dr * kDrange;
+  const int DR = DP - d0 < kDrange ? DP - d0 : kDrange;   // a multiple of 64
+  const int q_lo = d0 / 16, q_hi = (d0 + DR) / 16;         // chunks of the range
+  const int njr = DR / 32;
+  const int tj = (njr + kCtWaves - 1) / kCtWaves;
+  const int j0 = wave * tj;
+  const int nj = njr - j0 < tj ? (njr - j0 > 0 ? njr - j0 : 0) : tj;   // this wave's column tiles
+  const int nqw = NQ / kCtWaves;                                       // chunks per wave (NQ % 4 == 0)
+
+  const double4 kc = kc_gat[(int64_t)kb * 32 + c];   // (centred C, b, ||mu||^2 - 2 sum o) of component c
+  const double Cc = kc.x, bk = kc.y;
+  const float mqf = (float)kc.z;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int64_t t_begin = r_begin / 32, t_end = cdiv(r_end, 32);
+
+  // Need words of 64 tiles at a time, one per lane, the next batch in flight.
+  auto words = [&](int64_t tb) -> unsigned {
+    const int64_t t = tb + lane;
+    return t < t_end ? need[t * KB + kb] : 0u;
+  };
+  int64_t tb = t_begin;
+  unsigned mword = words(tb), mnext = words(tb + 64);
+  int jn = 0;          // next word of the batch
+  int qh = 0, qt = 0;  // queue head and tail (positions mod 64)
+  // Queue rows until 32 are waiting (or the slab ends) and take up to 32 of them:
+  // returns the count (the same in every wave); lane c of both halves gets tile row
+  // c's offset in the slab, or -1.
+  auto take = [&](int& e) -> int {
+    while (qt - qh < 32) {
+      const uint64_t live = jn >= 64 ? 0ull : (~0ull << jn);
+      const uint64_t nz = __builtin_amdgcn_ballot_w64(mword != 0u) & live;
+      if (nz == 0) {
+        tb += 64;
+        if (tb >= t_end) break;
+        mword = mnext;
+        mnext = words(tb + 64);
+        jn = 0;
+        continue;
+      }
+      const int j = __builtin_ctzll(nz);
+      const unsigned m = __builtin_amdgcn_readlane(mword, j);
+      const int base = (int)((tb + j - t_begin) * 32);
+      if (g == 0 && ((m >> c) & 1u)) q_l[(qt + __builtin_popcount(m & ((1u << c) - 1u))) & 63] = base + c;
+      qt += __builtin_popcount(m);
+      jn = j + 1;
+    }
+    const int cnt = qt - qh < 32 ? qt - qh : 32;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    e = c < cnt ? q_l[(qh + c) & 63] : -1;
+    qh += cnt;
+    return cnt;
+  };
+
+  // Chunk i of this wave (chunk q = wave + 4 i): the rows' dimensions 16q + 8g .. + 7
+  // and mu's four operands of the chunk.
+  const buf_rsrc mrs = make_rsrc(mu3 + (int64_t)kb * NQ * 4 * 64, (uint32_t)((int64_t)NQ * 4 * 64 * sizeof(bf16x8)));
+  auto issue = [&](int i, int e, f32x4 (&x)[2], bf16x8 (&m)[4]) {
+    const int q = wave + kCtWaves * i;
+    const bool ok = e >= 0;
+    const int64_t row = r_begin + (ok ? e : 0);
+    x[0] = load_row4(X, ldx, row, 16 * q + 8 * g, D, ok);
+    x[1] = load_row4(X, ldx, row, 16 * q + 8 * g + 4, D, ok);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      m[t] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                            mrs, lane * (int)sizeof(bf16x8), (q * 4 + t) * 64 * (int)sizeof(bf16x8), 0));
+  };
+  f32x4 xr[2][2];
+  bf16x8 mr[2][4];
+  double2 rst = make_double2(0.0, INFINITY);
+  auto start = [&](int e) {
+    issue(0, e, xr[0], mr[0]);
+    if (nqw > 1) issue(1, e, xr[1], mr[1]);
+    if (wave == 0) rst = e >= 0 ? rowstat[r_begin + e] : make_double2(0.0, INFINITY);
+  };
+
+  f32x16 acc[kDrTiles];
+#pragma unroll
+  for (int j = 0; j < kDrTiles; ++j) acc[j] = zero16();
+  float nk = 0.0f, sig = 0.0f;
+  const bf16x8 ones = x6c_ones(lane);
+
+  int e;
+  int cnt = take(e);
+  if (cnt > 0) start(e);
+  while (cnt > 0) {
+    // Chain `wave` of S over this wave's chunks (x6c_tile_rows' steps per chunk).
+    f32x16 cs = zero16();
+    auto chunk = [&](int i, const f32x4 (&x)[2], const bf16x8 (&m)[4]) {
+      const int q = wave + kCtWaves * i;
+      bf16x8 xa[3];
+      split3_bf16(x[0], x[1], xa);
+      if (q >= q_lo && q < q_hi) {
+#pragma unroll
+        for (int sp = 0; sp < 2; ++sp)
+          *reinterpret_cast<bf16x8*>(xt + (sp * 32 + c) * RS + 16 * (q - q_lo) + 8 * g) = xa[sp];
+      }
+#pragma unroll
+      for (int step = 0; step < 7; ++step) {
+        const bf16x8 B = step == 0 ? m[1] : step == 1 ? m[2] : step <= 3 ? m[0] : step == 4 ? m[1]
+                       : step == 5 ? m[3] : m[0];
+        const bf16x8 A = step == 0 ? xa[1] : step == 1 ? xa[0] : step == 2 ? xa[2] : step == 3 ? xa[1]
+                       : step == 4 ? xa[0] : step == 5 ? ones : xa[0];
+        cs = mfma_bf16(A, B, cs);
+      }
+    };
+    for (int i = 0; i < nqw; i += 2) {
+      chunk(i, xr[0], mr[0]);
+      if (i + 2 < nqw) issue(i + 2, e, xr[0], mr[0]);
+      if (i + 1 < nqw) {
+        chunk(i + 1, xr[1], mr[1]);
+        if (i + 3 < nqw) issue(i + 3, e, xr[1], mr[1]);
+      }
+    }
+    float* exw = ex + wave * 16 * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) exw[i * 64] = cs[i];
+    if (wave == 0 && g == 0) rs_l[c] = rst;
+    // The next rows: queued now, their first chunks in flight during r^T X.
+    int en;
+    const int cnt_next = take(en);
+    if (cnt_next > 0) start(en);
+    lds_barrier();
+
+    float r[16], res[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float S = ((ex[i * 64 + lane] + ex[(16 + i) * 64 + lane]) + ex[(32 + i) * 64 + lane]) +
+                      ex[(48 + i) * 64 + lane];
+      const double2 w = rs_l[acc_row(i, g)];   // (||x||^2, logZ2) of the row
+      const double ll = fma(-bk, fma(-2.0, (double)S, w.x), Cc);
+      const float rv = fast_exp2((float)(ll - w.y));
+      r[i] = rv;
+      res[i] = rv - (float)(__bf16)rv;
+      nk += rv;
+      sig = fmaf(rv, fmaf(-2.0f, S, (float)w.x) + mqf, sig);
+    }
+    bf16x8 a1[2], a2[2];
+    acc_to_row_operands(r, a1);
+    acc_to_row_operands(res, a2);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if (dense || any_nonzero(a1[p])) {
+#pragma unroll
+        for (int jj = 0; jj < kDrTiles; ++jj) {
+          if (jj < nj) {
+            const int col = 32 * (j0 + jj);
+            const bf16x8 b1 = lds_rows_operand(xt, RS, 16 * p, col, lane);
+            const bf16x8 b2 = lds_rows_operand(xt + 32 * RS, RS, 16 * p, col, lane);
+            acc[jj] = mfma_bf16(a2[p], b1, acc[jj]);
+            acc[jj] = mfma_bf16(a1[p], b2, acc[jj]);
+            acc[jj] = mfma_bf16(a1[p], b1, acc[jj]);
+          }
+        }
+      }
+    }
+    lds_barrier();   // the tile and the chains are free for the next rows
+    e = en;
+    cnt = cnt_next;
+  }
+
+  const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+#pragma unroll
+  for (int jj = 0; jj < kDrTiles; ++jj) {
+    if (jj < nj) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        part_mu[(kbase + acc_row(i, g)) * DP + d0 + 32 * (j0 + jj) + c] = acc[jj][i];
+    }
+  }
+  if (dr == 0 && wave == 0) {
+    nk += __shfl_xor(nk, 32);
+    sig += __shfl_xor(sig, 32);
     if (g == 0) {
       part_nk[kbase + c] = nk;
       part_sig[kbase + c] = sig;
@@ -2013,10 +1988,50 @@ __global__ __launch_bounds__(256) void fill_f32(float* __restrict__ p, int64_t n
   if (i < n) p[i] = v;
 }
 
+// Above D = 128: pass 1 is iso_lse_ctile for both plans; pass 2 of the default plan
+// (any D) is iso_accum_drange, that of the stored plan (D <= 256) launch_passes'.
+hipError_t launch_ctile(const IsoPlan& pl, const float* X, int64_t ldx, unsigned char* ws, float* logZ,
+                        bool run1, bool run2, bool dense, hipStream_t stream) {
+  const bf16x8* mu3 = reinterpret_cast<const bf16x8*>(ws + pl.off_mu3);
+  double2* rowstat = reinterpret_cast<double2*>(ws + pl.off_rowstat);
+  unsigned* ljmask = reinterpret_cast<unsigned*>(ws + pl.off_ljmask);
+  unsigned* ljcount = reinterpret_cast<unsigned*>(ws + pl.off_ljcount);
+  const int NQ = pl.DP / 16;
+  if (run1) {
+    const bool exact = pl.rexact && !pl.lj;
+    const size_t lds1 = lse_ctile_base() + (exact ? (size_t)kCtWaves * 32 * pl.KB * 2 : 0);
+    auto kern = pl.lj ? &iso_lse_ctile<kLjmStore> : &iso_lse_ctile<kLjmNeed>;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(pl.N, 32 * kCtWaves)), dim3(64 * kCtWaves), lds1,
+                       stream, X, ldx, pl.N, (int)pl.D, NQ, mu3,
+                       reinterpret_cast<const double2*>(ws + pl.off_kcblk), pl.KB, logZ, rowstat,
+                       pl.lj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr,
+                       pl.lj ? reinterpret_cast<float*>(ws + pl.off_ljmax) : nullptr, ljmask, ljcount,
+                       dense ? 1 : 0, exact ? 1 : 0);
+  }
+  if (run2 && !pl.lj) {
+    const size_t lds2 = accum_drange_lds_bytes(pl.DP < kDrange ? pl.DP : kDrange);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_drange),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+    if (e != hipSuccess) return e;
+    const int64_t items = (int64_t)pl.KB * pl.nslab * pl.ndr;
+    hipLaunchKernelGGL(iso_accum_drange, dim3((unsigned)(8 * cdiv(items, 8))), dim3(64 * kCtWaves), lds2,
+                       stream, X, ldx, pl.N, (int)pl.D, NQ, pl.DP, mu3,
+                       reinterpret_cast<const double4*>(ws + pl.off_kcgat), pl.KB, pl.KP, rowstat, ljmask,
+                       pl.nslab, pl.rows_per_slab, pl.ndr, reinterpret_cast<float*>(ws + pl.off_part_mu),
+                       reinterpret_cast<float*>(ws + pl.off_part_nk),
+                       reinterpret_cast<float*>(ws + pl.off_part_sig), dense ? 1 : 0);
+  }
+  return hipGetLastError();
+}
+
+// The default plan up to D = 128, the stored plan's passes up to D = 128 and its
+// pass 2 above (pass 1 there is launch_ctile's).
 template <int DP>
 hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
                          float* logZ, bool run1, bool run2, bool dense, hipStream_t stream) {
-  const f32x4* mu_sw = reinterpret_cast<const f32x4*>(ws + pl.off_musw);
   const double2* kc_blk = reinterpret_cast<const double2*>(ws + pl.off_kcblk);
   const double4* kc_lin = reinterpret_cast<const double4*>(ws + pl.off_kclin);
   double2* rowstat = reinterpret_cast<double2*>(ws + pl.off_rowstat);
@@ -2025,17 +2040,13 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   float* psig = reinterpret_cast<float*>(ws + pl.off_part_sig);
   float* lj = pl.lj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
   float* ljmax = pl.lj ? reinterpret_cast<float*>(ws + pl.off_ljmax) : nullptr;
-  unsigned* ljmask = pl.lj ? reinterpret_cast<unsigned*>(ws + pl.off_ljmask) : nullptr;
-  unsigned* ljcount = pl.lj ? reinterpret_cast<unsigned*>(ws + pl.off_ljcount) : nullptr;
-  if (pl.need) {
-    ljmask = reinterpret_cast<unsigned*>(ws + pl.off_ljmask);
-    ljcount = reinterpret_cast<unsigned*>(ws + pl.off_ljcount);
-  }
+  unsigned* ljmask = reinterpret_cast<unsigned*>(ws + pl.off_ljmask);
+  unsigned* ljcount = reinterpret_cast<unsigned*>(ws + pl.off_ljcount);
   if (run1) {
     const int64_t nblk1 = cdiv(pl.N, 32 * kWaves);
-    if constexpr (accum_uses_lds(DP)) {
+    if constexpr (DP <= 128) {
       const size_t lds1 = lse_lds_bytes<DP>() + (pl.rexact ? (size_t)kWaves * 32 * pl.KB * 2 : 0);
-      auto kern = pl.lj ? &iso_lse<DP, kLjmStore> : pl.need ? &iso_lse<DP, kLjmNeed> : &iso_lse<DP, kLjmNone>;
+      auto kern = pl.lj ? &iso_lse<DP, kLjmStore> : &iso_lse<DP, kLjmNeed>;
       if (lds1 > 65536) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
@@ -2045,23 +2056,11 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
                          (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3), kc_blk, pl.KB,
                          logZ, rowstat, lj, ljmax, ljmask, ljcount, dense ? 1 : 0, pl.rexact ? 1 : 0);
     } else {
-      // Above D = 128 the rows' dimensions are split over two waves.
-      constexpr size_t lds1 = lse_split_lds_bytes<DP>();
-      if (lds1 > 65536) {
-        for (const void* f : {reinterpret_cast<const void*>(&iso_lse_split<DP, false>),
-                              reinterpret_cast<const void*>(&iso_lse_split<DP, true>)}) {
-          hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
-          if (e != hipSuccess) return e;
-        }
-      }
-      auto kern = pl.lj ? &iso_lse_split<DP, true> : &iso_lse_split<DP, false>;
-      hipLaunchKernelGGL(kern, dim3((unsigned)nblk1), dim3(kAccThreads), lds1, stream, X, ldx, pl.N,
-                         (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat, lj, ljmax, ljmask, ljcount,
-                         dense ? 1 : 0);
+      return hipErrorInvalidValue;   // launch_ctile runs pass 1 above D = 128
     }
   }
   if (!run2) return hipGetLastError();
-  if constexpr (accum_uses_lds(DP)) {
+  if constexpr (DP <= 128) {
     if (pl.need) {
       // Both forms are launched; the needed-row count pass 1 left selects one on the
       // device: the gathering kernel below a quarter of all (row, block) pairs.
@@ -2091,87 +2090,51 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
       return hipGetLastError();
     }
   }
+  if (!pl.lj) return hipErrorInvalidValue;   // not a plan of this launcher
   const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
-  if constexpr (DP >= 64) {
-    if (pl.lj) {
-      // Sparse masks (on average at most 2 needed row pairs per tile and block) go to
-      // iso_accum_sparse where it applies (D a multiple of 32 up to 128); both
-      // kernels are launched and each returns unless the count selects it.
-      int64_t sparse_max = -1;
-      if constexpr (DP <= 128) {
-        if (pl.D == DP) {
-          sparse_max = 2 * cdiv(pl.N, 32) * pl.KB;
-          const int64_t nw = (int64_t)pl.nslab * pl.rgroups * pl.KB;
-          hipLaunchKernelGGL((iso_accum_sparse<DP>), dim3((unsigned)cdiv(nw, kSparseWaves)),
-                             dim3(64 * kSparseWaves), 0, stream, X, ldx, pl.N, lj, ljmask, ljcount,
-                             sparse_max, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rgroups,
-                             pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
-        }
-      }
-      auto launch = [&](auto cb_tag, auto nh_tag) -> hipError_t {
-        constexpr int CB = decltype(cb_tag)::value;
-        constexpr int NH = decltype(nh_tag)::value;
-        constexpr size_t lds = accum_lj_lds_bytes<DP, CB, NH>();
-        static_assert(lds <= kMaxLds, "pass-2 tiles exceed LDS");
-        if (lds > 65536) {
-          hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_lj<DP, CB, NH>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-          if (e != hipSuccess) return e;
-        }
-        hipLaunchKernelGGL((iso_accum_lj<DP, CB, NH>), grid2, dim3(kAccThreads), lds, stream, X, ldx,
-                           pl.N, (int)pl.D, lj, ljmask, ljcount, sparse_max, kc_lin, pl.KB, pl.KP,
-                           rowstat, pl.nslab,
-                           pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
-        return hipSuccess;
-      };
-      using I1 = std::integral_constant<int, 1>;
-      using I4 = std::integral_constant<int, 4>;
-      hipError_t e;
-      if (DP <= 192 && pl.cpg == 8) {
-        if constexpr (DP <= 192) e = launch(std::integral_constant<int, 8>{}, I1{});
-      } else if constexpr (DP > 128) {
-        e = launch(I4{}, std::integral_constant<int, 2>{});
-      } else {
-        e = launch(I4{}, I1{});
-      }
-      if (e != hipSuccess) return e;
-      return hipGetLastError();
+  // Sparse masks (on average at most 2 needed row pairs per tile and block) go to
+  // iso_accum_sparse where it applies (D a multiple of 32 up to 128); both kernels
+  // are launched and each returns unless the count selects it.
+  int64_t sparse_max = -1;
+  if constexpr (DP >= 64 && DP <= 128) {
+    if (pl.D == DP) {
+      sparse_max = 2 * cdiv(pl.N, 32) * pl.KB;
+      const int64_t nw = (int64_t)pl.nslab * pl.rgroups * pl.KB;
+      hipLaunchKernelGGL((iso_accum_sparse<DP>), dim3((unsigned)cdiv(nw, kSparseWaves)),
+                         dim3(64 * kSparseWaves), 0, stream, X, ldx, pl.N, lj, ljmask, ljcount,
+                         sparse_max, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rgroups,
+                         pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
     }
   }
-  if constexpr (accum_uses_lds(DP)) {
-    auto launch = [&](auto cb_tag) -> hipError_t {
-      constexpr int CB = decltype(cb_tag)::value;
-      constexpr size_t lds = accum_lds_lds_bytes<DP, CB>();
-      if constexpr (lds > kMaxLds) {
-        return hipErrorInvalidValue;   // never chosen by the plan
-      } else {
-        if (lds > 65536) {
-          hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_lds<DP, CB>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-          if (e != hipSuccess) return e;
-        }
-        hipLaunchKernelGGL((iso_accum_lds<DP, CB>), grid2, dim3(kAccThreads), lds, stream, X, ldx,
-                           pl.N, (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab,
-                           pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
-        return hipSuccess;
-      }
-    };
-    hipError_t e = pl.cpg == 1   ? launch(std::integral_constant<int, 1>{})
-                   : pl.cpg == 2 ? launch(std::integral_constant<int, 2>{})
-                                 : launch(std::integral_constant<int, kWaves>{});
-    if (e != hipSuccess) return e;
-  } else {
-    constexpr size_t lds = accum_split_lds_bytes<DP>();
+  auto launch = [&](auto cb_tag, auto nh_tag) -> hipError_t {
+    constexpr int CB = decltype(cb_tag)::value;
+    constexpr int NH = decltype(nh_tag)::value;
+    constexpr size_t lds = accum_lj_lds_bytes<DP, CB, NH>();
+    static_assert(lds <= kMaxLds, "pass-2 tiles exceed LDS");
     if (lds > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_split<DP>),
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_lj<DP, CB, NH>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(iso_accum_split<DP>, grid2, dim3(64 * split_parts(DP) * split_blocks(DP)), lds,
-                       stream, X, ldx, pl.N,
-                       (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
-                       pmu, pnk, psig, dense ? 1 : 0);
+    hipLaunchKernelGGL((iso_accum_lj<DP, CB, NH>), grid2, dim3(kAccThreads), lds, stream, X, ldx,
+                       pl.N, (int)pl.D, lj, ljmask, ljcount, sparse_max, kc_lin, pl.KB, pl.KP,
+                       rowstat, pl.nslab,
+                       pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
+    return hipSuccess;
+  };
+  using I1 = std::integral_constant<int, 1>;
+  using I4 = std::integral_constant<int, 4>;
+  hipError_t e = hipSuccess;
+  if constexpr (DP >= 64) {
+    if (DP <= 192 && pl.cpg == 8) {
+      if constexpr (DP <= 192) e = launch(std::integral_constant<int, 8>{}, I1{});
+    } else if constexpr (DP > 128) {
+      e = launch(I4{}, std::integral_constant<int, 2>{});
+    } else {
+      e = launch(I4{}, I1{});
+    }
   }
+  if (e != hipSuccess) return e;
   return hipGetLastError();
 }
 
@@ -2651,9 +2614,9 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
   if (K > 0 && (mu == nullptr || ldmu < D || log_sigma_sq == nullptr || log_pi == nullptr ||
                 Nk == nullptr || mu_acc == nullptr || sig_acc == nullptr))
     return FGMM_ERR_INVALID_ARG;
-  if (D > 256) return FGMM_ERR_UNSUPPORTED;
   if (N > kMaxRows || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
   const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
+  if (bf16 && D > 256) return FGMM_ERR_UNSUPPORTED;
   // The stored log-joint path streams X with 32-bit buffer offsets (row stride at
   // most kMaxBufLdx floats); wider strides recompute, which needs less workspace.
   const IsoPlan pl = make_plan(N, K, D, wants_stored_lj(flags) && ldx <= kMaxBufLdx, bf16);
@@ -2677,8 +2640,7 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
                        reinterpret_cast<f32x4*>(ws + pl.off_kcblk));
   else if (run1)
     hipLaunchKernelGGL(iso_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, K, (int)D, pl.DP,
-                       log_sigma_sq, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_musw),
-                       reinterpret_cast<double2*>(ws + pl.off_kcblk),
+                       log_sigma_sq, log_pi, reinterpret_cast<double2*>(ws + pl.off_kcblk),
                        reinterpret_cast<double4*>(ws + pl.off_kclin),
                        reinterpret_cast<double4*>(ws + pl.off_kcgat),
                        reinterpret_cast<bf16x8*>(ws + pl.off_mu3),
@@ -2690,7 +2652,14 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
                   : launch_passes<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
     };
     hipError_t e = hipSuccess;
-    switch (pl.DP) {
+    if (!bf16 && pl.DP > 128) {
+      e = launch_ctile(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
+      if (e == hipSuccess && pl.lj && run2) {
+        if (pl.DP == 192) e = launch_passes<192>(pl, X, ldx, ws, logZ, false, true, dense, stream);
+        else if (pl.DP == 256) e = launch_passes<256>(pl, X, ldx, ws, logZ, false, true, dense, stream);
+        else return FGMM_ERR_UNSUPPORTED;
+      }
+    } else switch (pl.DP) {
       case 32: e = run(std::integral_constant<int, 32>{}); break;
       case 64: e = run(std::integral_constant<int, 64>{}); break;
       case 96: e = run(std::integral_constant<int, 96>{}); break;

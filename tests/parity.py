@@ -1,7 +1,7 @@
 """Shared tolerance checks for the GPU parity tests.
 
 Float32 kernels against the float64 oracle:
-  logZ        abs <= 1e-4
+  logZ        abs <= 1e-4 (x D / 128 above D = 128, logz_atol_for)
   Nk, sig     |d| <= 1e-4 * |ref| + 1e-6 * max|ref|   (floor for near-empty components)
   mu_acc      max|d| <= 1e-4 * max|ref|                (norm-wise; entries near zero make
                                                         element-wise relative error meaningless)
@@ -11,6 +11,15 @@ import numpy as np
 
 LOGZ_ATOL = 1e-4
 REL = 1e-4
+
+
+def logz_atol_for(D):
+    """The logZ bound at width D.  The log-joint's terms (||x||^2, x.mu, ||mu||^2) grow
+    in proportion to D, and a float32 evaluation of them has an absolute error that
+    grows with them: above D = 128 the bound scales by D / 128, the relative accuracy
+    the 1e-4 bound sets at the benchmark width D = 128."""
+    return LOGZ_ATOL * max(1.0, D / 128.0)
+
 # The bf16 operand contract (precision="bf16") against its own oracle
 # (gmm_oracle.estep_iso_bf16): the roundings to bf16 are replayed exactly, so only
 # fp32 arithmetic on the log-joint's large terms (c0, ish ||x||^2, 2 ish x.mu, each

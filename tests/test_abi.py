@@ -134,7 +134,7 @@ def _call_iso(**kw):
     (dict(mu=None), _lib.FGMM_ERR_INVALID_ARG),
     (dict(ldmu=16), _lib.FGMM_ERR_INVALID_ARG),
     (dict(Nk=None), _lib.FGMM_ERR_INVALID_ARG),
-    (dict(D=300, ldx=300, ldmu=300), _lib.FGMM_ERR_UNSUPPORTED),
+    (dict(D=300, ldx=300, ldmu=300, flags=_lib.FLAG_BF16), _lib.FGMM_ERR_UNSUPPORTED),
     (dict(N=(1 << 37) + 1), _lib.FGMM_ERR_UNSUPPORTED),  # pass-1 grid limit
     (dict(ws_bytes=16), _lib.FGMM_ERR_WORKSPACE),
     (dict(ws=None), _lib.FGMM_ERR_WORKSPACE),
@@ -159,12 +159,14 @@ def _call_full(D):
 
 @no_gpu
 def test_dimension_limits():
-    """Largest supported D per covariance model; one past it is UNSUPPORTED."""
-    assert _call_iso(D=257, ldx=260, ldmu=257) == _lib.FGMM_ERR_UNSUPPORTED
+    """Largest supported D per covariance model; one past it is UNSUPPORTED.  The
+    isotropic fp32 E-step takes any D; its bf16 contract stops at 256."""
+    assert _call_iso(D=257, ldx=260, ldmu=257, flags=_lib.FLAG_BF16) == _lib.FGMM_ERR_UNSUPPORTED
     assert _call_diag(257) == _lib.FGMM_ERR_UNSUPPORTED
     assert _call_full(129) == _lib.FGMM_ERR_UNSUPPORTED
     # workspace queries accept the supported range
     L = _lib.lib()
+    assert L.fgmm_iso_workspace_bytes(100, 10, 4000) > L.fgmm_iso_workspace_bytes(100, 10, 300) > 0
     assert L.fgmm_diag_workspace_bytes(100, 10, 256) > L.fgmm_diag_workspace_bytes(100, 10, 128) > 0
     assert L.fgmm_full_workspace_bytes(100, 10, 128) > L.fgmm_full_workspace_bytes(100, 10, 64) > 0
 

@@ -1,0 +1,123 @@
+"""GPU parity of the isotropic E-step above D = 128, where pass 1 tiles the
+contraction over components (iso_lse_ctile) and pass 2 splits r^T X over ranges of
+dimensions (iso_accum_drange), against the float64 oracle.  The reference takes any D
+(flash_gmm.py:186-188, flash_gmm_h100.py:268-270: BLOCK_D is the next power of two)."""
+
+import os
+import sys
+
+import pytest
+import torch
+
+from flash_gmm import data, flash_gmm_estep, iso_estep_into
+from oracle import gmm_oracle as O
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+from parity import assert_close_stats, assert_dense_agrees, logz_atol_for  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle(inp):
+    return O.estep_iso(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+
+
+def _into(inp, dev, **kw):
+    N, D = inp["X"].shape
+    K = inp["mu"].shape[0]
+    out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, device=dev)]
+    iso_estep_into(*[inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")], *out, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+# (N, K, D): one past the register-resident width; ragged K and D (the Python layer
+# pads D % 4 != 0); GloVe-300 and GIST-960 widths; two and three dimension ranges of
+# pass 2 (1100, 2100); partial row tiles, partial component tiles and tiny K.
+SHAPES = [(300, 5, 129), (2500, 260, 192), (3000, 200, 300), (4097, 257, 301), (2000, 130, 960),
+          (1500, 70, 1100), (700, 40, 2100), (33, 1, 640)]
+
+
+@pytest.mark.parametrize("N,K,D", SHAPES)
+def test_wide_d_against_oracle(N, K, D, gpu_device):
+    print(f"iso wide N={N} K={K} D={D}", flush=True)
+    inp = data.iso_clustered(N, K, D, seed=N + K + D)
+    got = _into(inp, gpu_device)
+    assert_close_stats(got, oracle(inp), f"iso N={N} K={K} D={D}", logz_atol=logz_atol_for(D))
+
+
+@pytest.mark.parametrize("N,K,D", [(4000, 256, 300), (3000, 128, 960)])
+def test_wide_d_reference_randn_workload(N, K, D, gpu_device):
+    """The reference's smoke data (X, mu ~ N(0, I), lss = 0) at large D: every row needs
+    many component blocks, so pass 2 gathers nearly every (row, block) pair."""
+    inp = data.reference_smoke(N, K, D, seed=3)
+    got = _into(inp, gpu_device)
+    assert_close_stats(got, oracle(inp), f"randn N={N} K={K} D={D}", logz_atol=logz_atol_for(D))
+
+
+@pytest.mark.parametrize("N,K,D", [(6000, 512, 256), (3000, 300, 960)])
+def test_wide_d_skip_agrees_with_dense(N, K, D, gpu_device):
+    """Gathering only the needed rows against FGMM_FLAG_DENSE (every row of every block):
+    logZ bitwise, statistics to 1e-5 (other groupings of the same nonzero terms)."""
+    inp = data.iso_clustered(N, K, D, seed=6)
+    a = _into(inp, gpu_device)
+    b = _into(inp, gpu_device, dense=True)
+    assert_dense_agrees(a, b, bitwise=False)
+    assert_close_stats(b, oracle(inp), f"dense N={N} K={K} D={D}", logz_atol=logz_atol_for(D))
+
+
+@pytest.mark.parametrize("D", [200, 1100])
+def test_wide_d_phase_split_equals_one_call(D, gpu_device):
+    """PHASE1 then PHASE2 on one workspace gives the single call's outputs bitwise."""
+    inp = data.iso_clustered(3000, 160, D, seed=16)
+    dev = gpu_device
+    ref = _into(inp, dev)
+    N, K = 3000, 160
+    from flash_gmm import _lib
+    L = _lib.lib()
+    ws = torch.empty(L.fgmm_iso_workspace_bytes(N, K, D), dtype=torch.uint8, device=dev)
+    out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, device=dev)]
+    args = [inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
+    iso_estep_into(*args, *out, workspace=ws, phase=1)
+    iso_estep_into(*args, None, *out[1:], workspace=ws, phase=2)
+    torch.cuda.synchronize()
+    for u, v in zip(out, ref):
+        assert torch.equal(u, v)
+
+
+def test_wide_d_need_masks_from_the_running_max(gpu_device):
+    """More component blocks than pass 1 keeps bounds for in LDS (K=12,000): the need masks
+    come from the running-max bound; against the dense pass and the oracle."""
+    inp = data.iso_clustered(1200, 12000, 160, seed=23)
+    a = _into(inp, gpu_device)
+    b = _into(inp, gpu_device, dense=True)
+    assert_dense_agrees(a, b, bitwise=False)
+    assert_close_stats(a, oracle(inp), "running-max masks D=160", logz_atol=logz_atol_for(160))
+
+
+def test_wide_d_deterministic_and_strided(gpu_device):
+    """Bitwise repeatable, and a strided (padded-row) X gives the same bits."""
+    inp = data.iso_clustered(5000, 200, 400, seed=9)
+    dev = gpu_device
+    a = _into(inp, dev)
+    b = _into(inp, dev)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+    big = torch.zeros(5000, 437, device=dev)
+    big[:, :400] = inp["X"].to(dev)
+    got = flash_gmm_estep(big[:, :400], *[inp[k].to(dev) for k in ("mu", "log_sigma_sq", "log_pi")])
+    torch.cuda.synchronize()
+    for u, v in zip(got, a):
+        assert torch.equal(u, v)
+
+
+def test_wide_d_mid_size(gpu_device):
+    """GIST-960 width at N=32,768, K=1024 against the float64 oracle."""
+    inp = data.iso_clustered(32768, 1024, 960, seed=4)
+    got = _into(inp, gpu_device)
+    ref = oracle(inp)
+    err = (got[0].cpu().double() - ref[0]).abs().max().item()
+    print(f"iso N=32768 K=1024 D=960: max |logZ - oracle| = {err:.3e}", flush=True)
+    assert_close_stats(got, ref, "iso N=32768 K=1024 D=960", logz_atol=logz_atol_for(960))
