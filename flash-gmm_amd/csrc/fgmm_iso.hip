@@ -555,7 +555,7 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
   const int64_t all_ops = (int64_t)KB * blk_ops;
   bf16x8 st[LPT];
   double2 kst = make_double2(-INFINITY, 0.0);
-  auto fetch = [&](int s) {
+  auto fetch = [&](int s) __attribute__((always_inline)) {
     const int ct = s / NS, sp = s - ct * NS;
     const int64_t base = (int64_t)ct * kCtBlocks * blk_ops + (int64_t)sp * 2 * 4 * 64;
     int64_t avail = (all_ops - base) * (int64_t)sizeof(bf16x8);
@@ -571,7 +571,7 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
       kst = kc < (int64_t)KB * 32 ? kc_blk[kc] : make_double2(-INFINITY, 0.0);
     }
   };
-  auto commit = [&](int s, int buf) {
+  auto commit = [&](int s, int buf) __attribute__((always_inline)) {
     const int ct = s / NS, sp = s - ct * NS;
 #pragma unroll
     for (int u = 0; u < LPT; ++u) mu_l[buf * kCtStageOps + u * NT + tid] = st[u];
@@ -580,7 +580,7 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
 
   // The wave's rows, dimensions 16q + 8g .. + 7 of chunk q (zero past D and N).
   const float* xrow = X + (valid ? row : 0) * ldx + 8 * g;
-  auto xload = [&](int q, f32x4& lo, f32x4& hi) {
+  auto xload = [&](int q, f32x4& lo, f32x4& hi) __attribute__((always_inline)) {
     if (q < nq_full) {
       lo = *reinterpret_cast<const f32x4*>(xrow + 16 * q);
       hi = *reinterpret_cast<const f32x4*>(xrow + 16 * q + 4);
@@ -591,7 +591,7 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
     }
   };
   f32x4 xr[2][2][2];   // [stage parity][chunk in the pair][lo, hi]
-  auto xstage = [&](int s, f32x4 (&dst)[2][2]) {
+  auto xstage = [&](int s, f32x4 (&dst)[2][2]) __attribute__((always_inline)) {
     if (s >= nstage) return;
     const int sp = s % NS;
     xload(2 * sp, dst[0][0], dst[0][1]);
@@ -617,7 +617,7 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
   unsigned pairs = 0;
 
   // Component tile ct is complete: log-joint, log-sum-exp and need bounds per block.
-  auto finish_tile = [&](int ct) {
+  auto finish_tile = [&](int ct) __attribute__((always_inline)) {
     if (ct == 0) xsq = xsq_part + __shfl_xor(xsq_part, 32);
     const double2* kp0 = kc_l + (ct & 1) * kCtBlocks * 32 + g * 16;
 #pragma unroll
@@ -664,17 +664,17 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
 
   // One stage; P = s & 1 is the LDS buffer and the register stage, and the chunks
   // 2 sp, 2 sp + 1 go to chains 2P, 2P + 1 (NS is even, so sp and s share parity).
-  auto stage = [&](int s, auto par) {
+  auto stage = [&](int ct, int sp, auto par) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
-    const int ct = s / NS, sp = s - ct * NS;
+    const int s = ct * NS + sp;
     const bool more = s + 1 < nstage;
     if (more) fetch(s + 1);
     xstage(s + 1, xr[1 - P]);
     const bf16x8* mp = mu_l + P * kCtStageOps + lane;
+    bf16x8 xb[2][3];
 #pragma unroll
     for (int qq = 0; qq < 2; ++qq) {
-      bf16x8 xb[3];
-      split3_bf16(xr[P][qq][0], xr[P][qq][1], xb);
+      split3_bf16(xr[P][qq][0], xr[P][qq][1], xb[qq]);
       if (ct == 0) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -682,32 +682,38 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
           xsq_part = fma((double)xr[P][qq][1][e], (double)xr[P][qq][1][e], xsq_part);
         }
       }
-      bf16x8 a[kCtBlocks][4];
+    }
+    // Block by block (its operands for both chunks), the two chunks' chains interleaved.
+    // Steps in x6c_tile's order: x2 mu2, x1 mu3, x3 mu1, x2 mu1, x1 mu2, -o, x1 mu1.
 #pragma unroll
-      for (int b = 0; b < kCtBlocks; ++b) {
+    for (int b = 0; b < kCtBlocks; ++b) {
+      bf16x8 a[2][4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) a[b][t] = mp[b * 512 + (qq * 4 + t) * 64];
+      for (int qq = 0; qq < 2; ++qq) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) a[qq][t] = mp[b * 512 + (qq * 4 + t) * 64];
       }
-      // Steps in x6c_tile's order: x2 mu2, x1 mu3, x3 mu1, x2 mu1, x1 mu2, -o, x1 mu1.
 #pragma unroll
       for (int step = 0; step < 7; ++step) {
 #pragma unroll
-        for (int b = 0; b < kCtBlocks; ++b) {
-          const bf16x8 A = step == 0 ? a[b][1] : step == 1 ? a[b][2] : step <= 3 ? a[b][0]
-                         : step == 4 ? a[b][1] : step == 5 ? a[b][3] : a[b][0];
-          const bf16x8 B = step == 0 ? xb[1] : step == 1 ? xb[0] : step == 2 ? xb[2]
-                         : step == 3 ? xb[1] : step == 4 ? xb[0] : step == 5 ? ones : xb[0];
+        for (int qq = 0; qq < 2; ++qq) {
+          const bf16x8 A = step == 0 ? a[qq][1] : step == 1 ? a[qq][2] : step <= 3 ? a[qq][0]
+                         : step == 4 ? a[qq][1] : step == 5 ? a[qq][3] : a[qq][0];
+          const bf16x8 B = step == 0 ? xb[qq][1] : step == 1 ? xb[qq][0] : step == 2 ? xb[qq][2]
+                         : step == 3 ? xb[qq][1] : step == 4 ? xb[qq][0] : step == 5 ? ones : xb[qq][0];
           acc[b][2 * P + qq] = mfma_bf16(A, B, acc[b][2 * P + qq]);
         }
       }
     }
     if (more) commit(s + 1, 1 - P);
     lds_barrier();
-    if (sp == NS - 1) finish_tile(ct);
   };
-  for (int s = 0; s < nstage; s += 2) {
-    stage(s, std::integral_constant<int, 0>{});
-    stage(s + 1, std::integral_constant<int, 1>{});
+  for (int ct = 0; ct * NS < nstage; ++ct) {
+    for (int sp = 0; sp < NS; sp += 2) {
+      stage(ct, sp, std::integral_constant<int, 0>{});
+      stage(ct, sp + 1, std::integral_constant<int, 1>{});
+    }
+    finish_tile(ct);
   }
 
   // Merge the two half-waves that hold the same row.
