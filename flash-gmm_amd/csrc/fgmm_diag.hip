@@ -9,16 +9,24 @@
 //   Nk_k = sum_n r_nk;  mu_acc_kd = sum_n r_nk x_nd;  rxsq_kd = sum_n r_nk x_nd^2
 //   sig_acc_kd = rxsq_kd - 2 mu_kd mu_acc_kd + mu_kd^2 Nk_k   (fp64, in the finish)
 //
-// Same structure as the isotropic kernels (fgmm_iso.hip): a prologue that lays the
-// 2D-feature operand [-w, 2v] out in matrix-core order, a log-normaliser pass with
-// X resident in registers (the x^2 half of the feature vector is formed on the fly;
-// up to D = 128 on the bf16 matrix cores in the centred split-bf16 form,
-// diag_lse_x6, above with fp32 steps, diag_lse_split),
-// an accumulation pass split over component groups x row slabs with r used directly
-// as the A operand of r^T [x | x^2] (above D = 96 with the dimensions split over
-// two waves per component block), and a fixed-order fp64 reduction of the slab
-// partials.  Row slabs are disjoint ([s*R, min(N, (s+1)*R))), so no row is counted
-// twice at a slab boundary.
+// Same structure as the isotropic kernels (fgmm_iso.hip):
+//   diag_x6_prep      O(K*D): the feature operand [-w, 2v] as three-way bf16 splits with
+//                     per-chunk centring offsets in matrix-core operand order, and C'_k.
+//   diag_lse_x6       pass 1 up to D = 128 with the rows' split features resident in
+//                     registers (the x^2 half formed on the fly), the centred
+//                     split-bf16 contraction, online log-sum-exp, need masks per half
+//                     block (16 components) or the stored log-joint.
+//   diag_lse_ctile    pass 1 above D = 128 (any D), tiled over components as well.
+//   diag_accum_gather pass 2 of the default plan up to D = 128: the needed rows of each
+//                     slab, the log-joint recomputed bit for bit as pass 1 forms it,
+//                     r^T [X | X^2] on fp32 matrix steps.
+//   diag_accum_drange pass 2 of the default plan above D = 128, per dimension range.
+//   diag_accum_sparse / diag_accum_lj2 / diag_accum_lj
+//                     pass 2 of the stored plan (FGMM_FLAG_STORE_LOGJOINT, D <= 256).
+//   diag_reduce       fixed-order fp64 sum of the slab partials and the sig identity.
+//   diag_bf16_*       the bf16 operand contract (FGMM_FLAG_BF16).
+// Row slabs are disjoint ([s*R, min(N, (s+1)*R))), so no row is counted twice at a
+// slab boundary.
 
 #include "fgmm_common.hpp"
 
@@ -34,34 +42,34 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kAccWaves = 8;
 constexpr int kAccThreads = 64 * kAccWaves;
 
-// LDS-resident pass 2 when mu' of 4 component blocks (4 x 32 x 2*DP floats) and two
-// 64-row X buffers fit in LDS.
-__host__ __device__ constexpr bool diag_accum_uses_lds(int DP) { return DP <= 96; }
-
-// LDS of that pass with CB component blocks per workgroup (8 / CB row groups of
-// 32 rows): features of the blocks, two X buffers, row logZ2.
 constexpr size_t kMaxLds = 160 * 1024;
-__host__ __device__ constexpr size_t accum_lds_bytes_for(int DP, int CB) {
-  return (size_t)CB * (2 * DP) * 32 * sizeof(float) +
-         (size_t)2 * 32 * (8 / CB) * (DP + 4) * sizeof(float) +
-         (size_t)2 * 32 * (8 / CB) * sizeof(double);
-}
-// 4 blocks per workgroup, or 2 / 1 when K has that few blocks (so no wave idles)
-// and the taller X tiles fit.
-__host__ inline int accum_blocks_per_group(int DP, int KB) {
-  if (KB <= 1 && accum_lds_bytes_for(DP, 1) <= kMaxLds) return 1;
-  if (KB <= 2 && accum_lds_bytes_for(DP, 2) <= kMaxLds) return 2;
-  return kWaves;
-}
 
-// From D = 97 on, pass 2 splits the dimensions over two waves per component block
-// (diag_accum_split); above 128, D is padded to a multiple of 64.  At D = 128 the
-// features of a half fit registers with two waves per SIMD (4 component blocks
-// per workgroup); wider halves run one wave per SIMD (2 blocks per workgroup).
-__host__ __device__ constexpr bool diag_accum_split_d(int DP) { return DP > 96; }
-__host__ __device__ constexpr int split_blocks(int DP) { return DP <= 128 ? 4 : 2; }
+// D padded to a multiple of 32 up to 128, of 64 above (where pass 1 tiles the
+// contraction over components and pass 2 splits r^T [X | X^2] over dimension ranges:
+// each of the four accumulation chains then gets the same number of chunks).
 __host__ inline int diag_padded_dim(int64_t D) {
   return D <= 128 ? (int)round_up(D < 1 ? 1 : D, 32) : (int)round_up(D, 64);
+}
+constexpr int kCtWaves = 4;                               // waves per workgroup, one per SIMD
+constexpr int kCtBlocks = 4;                              // component blocks per pass-1 tile
+constexpr int kCtChains = 4;                              // accumulation chains (chunk q -> q % 4)
+constexpr int kCtStageOps = kCtBlocks * 2 * 4 * 64;       // bf16x8 per two-chunk operand stage (32 KiB)
+constexpr int kDrange = 1024;                             // dimensions of r^T [X | X^2] per pass-2 workgroup
+constexpr int kDrTiles = kDrange / 32 / kCtWaves;         // 32-column tiles per pass-2 wave
+__host__ __device__ constexpr size_t lse_ctile_base() {
+  return (size_t)2 * kCtStageOps * sizeof(bf16x8) + (size_t)2 * kCtBlocks * 32 * sizeof(double);
+}
+// Component blocks whose half-block need bounds (bf16, 2 x 32 rows per wave) fit
+// beside the stages.
+__host__ __device__ constexpr int ctile_need_exact_cap() {
+  return (int)((kMaxLds - lse_ctile_base()) / (kCtWaves * 2 * 32 * 2));
+}
+__host__ __device__ constexpr int drange_rs(int DR) { return DR + 8; }   // fp32 row stride of the X tile
+__host__ __device__ constexpr size_t accum_drange_lds_bytes(int DR) {
+  return (size_t)32 * drange_rs(DR) * sizeof(float)         // X of 32 rows
+         + (size_t)kCtWaves * 16 * 64 * sizeof(float)        // the four chains of S
+         + (size_t)32 * sizeof(double)                       // logZ2 of the rows
+         + (size_t)kCtWaves * 64 * sizeof(int);              // row queue per wave
 }
 
 // bf16 operand contract (defined with its kernels below).
@@ -69,7 +77,7 @@ __host__ __device__ constexpr int bf16_parts(int DP);
 __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB);
 __host__ inline int bf16_blocks_per_group(int DP, int KB);
 
-// Pass 1 runs on the bf16 matrix cores (split-bf16 cross term) up to D = 128.
+// Pass 1 keeps the rows' split features in registers (diag_lse_x6) up to D = 128.
 __host__ __device__ constexpr bool diag_uses_x6(int DP) { return DP <= 128; }
 
 struct DiagPlan {
@@ -82,10 +90,12 @@ struct DiagPlan {
   bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16)
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
   int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
-  bool lj_sparse;   // the stored log-joint in the sparse form (pass 1 on the bf16 cores, D <= 128)
-  bool need;        // default plan up to D = 128: pass 1 leaves need masks, pass 2 gathers
+  bool lj_sparse;   // the stored log-joint in the sparse form (D <= 128)
+  bool need;        // default plan: pass 1 leaves need masks, pass 2 gathers the needed rows
+  bool ctile;       // above D = 128: component-tiled pass 1 (both plans), range pass 2 (default)
   bool rexact;      // need masks from block maxima kept in LDS (else the running-max bound)
-  size_t off_musw, off_mu3, off_kcx6, off_kcx6lin, off_kcblk, off_kclin, off_rowstat, off_part_mu,
+  int ndr;          // dimension ranges of the range pass 2
+  size_t off_musw, off_mu3, off_kcx6, off_kcx6lin, off_kclin, off_rowstat, off_part_mu,
       off_part_sq, off_part_nk, off_lj, off_ljmax, off_ljmask, off_ljcount, total;
 };
 
@@ -100,13 +110,13 @@ __host__ inline int need_exact_cap(int DP) {
   return base >= 160 * 1024 ? 0 : (int)((160 * 1024 - base) / (8 * 32 * 2));
 }
 
-// Pass 2 reads the stored log-joint when recomputation is not requested, there are
-// at least 4 component blocks, D > 32, and the tiles (one per pass-1 wave) fit
-// under kMaxLjBytes.  At D <= 32 nearly every row of a tile is needed and
+// Pass 2 reads the stored log-joint when it is requested, there are at least 4
+// component blocks, 32 < D <= 256 (above, only the default plan has kernels), and
+// the tiles (one per pass-1 wave) fit under kMaxLjBytes.  At D <= 32 nearly every row of a tile is needed and
 // recomputing the short contraction costs less than the traffic (N=1M, K=1024:
 // 3.67 ms recomputed, 4.12 ms stored).
 __host__ inline bool use_stored_lj(int64_t N, int KB, int DP, bool allow) {
-  return allow && KB >= 4 && DP > 32 &&
+  return allow && KB >= 4 && DP > 32 && DP <= 256 &&
          (size_t)round_up(cdiv(N, 32), 4) * (size_t)KB * kLjTile * sizeof(float) <= kMaxLjBytes;
 }
 
@@ -119,8 +129,10 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.KP = p.KB * 32;
   p.bf16 = bf16;
   p.lj = !bf16 && use_stored_lj(N, p.KB, p.DP, allow_lj);
-  p.need = !bf16 && !p.lj && diag_uses_x6(p.DP);
-  p.rexact = p.need && p.KB <= need_exact_cap(p.DP);
+  p.need = !bf16 && !p.lj;
+  p.ctile = !bf16 && !diag_uses_x6(p.DP);
+  p.rexact = p.need && p.KB <= (p.ctile ? ctile_need_exact_cap() : need_exact_cap(p.DP));
+  p.ndr = p.ctile ? (int)cdiv(p.DP, kDrange) : 1;
   if (bf16) {
     p.cpg = bf16_blocks_per_group(p.DP, p.KB);
     p.rgroups = kAccWaves / (p.cpg * bf16_parts(p.DP));
@@ -131,16 +143,21 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
     p.cpg = (p.KB >= 8 && p.DP <= 128) ? 8 : 4;
     p.lj_nh = (p.DP > 128 || (p.DP == 128 && p.cpg == 4)) ? 2 : 1;
     p.rgroups = kAccWaves / (p.cpg * p.lj_nh);
-  } else if (p.need) {
-    p.cpg = 1;        // one wave per (row slab, component block)
-    p.rgroups = 1;
   } else {
-    p.cpg = diag_accum_split_d(p.DP) ? split_blocks(p.DP) : accum_blocks_per_group(p.DP, p.KB);
-    p.rgroups = diag_accum_uses_lds(p.DP) ? kAccWaves / p.cpg : 1;
+    p.cpg = 1;        // one wave (D <= 128) or workgroup per (row slab, component block)
+    p.rgroups = 1;
   }
   p.ncg = (int)cdiv(p.KB, p.cpg);
   const int64_t tile_rows = 32 * p.rgroups;
-  if (p.need && N > 0 && p.KB > 0) {
+  if (p.need && p.ctile && N > 0 && p.KB > 0) {
+    // One 4-wave workgroup per (slab, block, dimension range) and compute unit (its
+    // X tile takes most of the LDS): about two rounds of workgroups.
+    int64_t want = cdiv((int64_t)2 * current_device_cus(), (int64_t)p.KB * p.ndr);
+    const int64_t max_slabs = cdiv(N, 32);
+    if (want > max_slabs) want = max_slabs;
+    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.nslab = (int)cdiv(N, p.rows_per_slab);
+  } else if (p.need && N > 0 && p.KB > 0) {
     // The gathering pass 2 runs one wave per SIMD: about two rounds of waves.
     int64_t want = cdiv((int64_t)8 * current_device_cus(), p.KB);
     const int64_t max_slabs = cdiv(N, 32);
@@ -161,12 +178,12 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   }
   p.npart = p.nslab * p.rgroups;
   size_t off = 0;
-  p.off_musw = off;    off = align256(off + (size_t)p.KP * p.FP * sizeof(float));
+  // The bf16 contract's operands and constants; the fp32 plans' split operands.
+  p.off_musw = off;    off = align256(off + (bf16 ? (size_t)p.KP * p.FP * sizeof(float) : 0));
+  p.off_kclin = off;   off = align256(off + (bf16 ? (size_t)p.KP * sizeof(double) : 0));
   p.off_mu3 = off;     off = align256(off + (bf16 ? 0 : (size_t)p.KP * (p.DP / 8) * 4 * 2 * sizeof(bf16x8)));
   p.off_kcx6 = off;    off = align256(off + (bf16 ? 0 : (size_t)p.KP * sizeof(double)));
   p.off_kcx6lin = off; off = align256(off + (bf16 ? 0 : (size_t)p.KP * sizeof(double)));
-  p.off_kcblk = off;   off = align256(off + (size_t)p.KP * sizeof(double));
-  p.off_kclin = off;   off = align256(off + (size_t)p.KP * sizeof(double));
   p.off_rowstat = off; off = align256(off + (size_t)(N > 0 ? N : 0) * sizeof(double));
   p.off_part_mu = off; off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
   p.off_part_sq = off; off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
@@ -188,190 +205,6 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
 }
 
 __device__ __forceinline__ f32x4 sq4(f32x4 v) { return v * v; }
-
-// ---------------------------------------------------------------------------
-// Prologue: features [-w | 2v] in operand order and the per-component constant.
-// One 64-thread block per 32-component block.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void diag_prep(const float* __restrict__ mu, int64_t ldmu,
-                                                const float* __restrict__ lss, int64_t ldlss, int64_t K,
-                                                int D, int DP, const float* __restrict__ lpi,
-                                                f32x4* __restrict__ mu_sw, double* __restrict__ kc_blk,
-                                                double* __restrict__ kc_lin) {
-  __shared__ double sC[32];
-  const int kb = blockIdx.x;
-  const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
-  const int64_t comp = (int64_t)kb * 32 + c;
-  const bool valid = comp < K;
-  if (g == 0) {
-    double C = -INFINITY;
-    if (valid) {
-      double lsum = 0.0, q = 0.0;
-#pragma unroll 8
-      for (int d = 0; d < D; ++d) {
-        const double l = (double)lss[comp * ldlss + d];
-        const double m = (double)mu[comp * ldmu + d];
-        const double w = 0.5 * exp(-l) * kLog2e;
-        lsum += l;
-        q = fma(m * m, w, q);
-      }
-      C = ((double)lpi[comp] - 0.5 * ((double)D * kLog2Pi + lsum)) * kLog2e - q;
-    }
-    sC[c] = C;
-    kc_lin[comp] = C;
-  }
-  const int FP = 2 * DP, NM = FP / 8;
-  for (int m = 0; m < NM; ++m) {
-    f32x4 v = zero4();
-    const int f0 = 8 * m + 4 * g;
-    if (valid) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int f = f0 + e;
-        const int d = f < DP ? f : f - DP;
-        float val = 0.0f;
-        if (d < D) {
-          const double w = 0.5 * exp(-(double)lss[comp * ldlss + d]) * kLog2e;
-          val = (f < DP) ? (float)(-w) : (float)(2.0 * (double)mu[comp * ldmu + d] * w);
-        }
-        v[e] = val;
-      }
-    }
-    mu_sw[((int64_t)kb * NM + m) * 64 + lane] = v;
-  }
-  __syncthreads();
-  if (lane < 32) {
-    const int i = lane & 15, gg = lane >> 4;
-    kc_blk[(int64_t)kb * 32 + gg * 16 + i] = sC[acc_row(i, gg)];
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Pass 1 above D = 128: eight waves = 4 row groups x 2 halves of the dimensions, so
-// each wave holds half of its 32 rows in registers (two waves per SIMD).  Half h
-// multiplies its x^2 and x chunks by the matching chunks of the mu' block; the
-// second half's fp64 partials go through LDS and the first-half wave adds them in
-// a fixed order and runs the online log-sum-exp.  When two mu' blocks fit in LDS
-// next to two exchange slots, the loop has one barrier per block; otherwise one
-// mu' buffer and one slot, with a second barrier before the buffer is refilled.
-// ---------------------------------------------------------------------------
-template <int DP>
-constexpr int lse_split_mu_buffers() {
-  constexpr size_t blk = (size_t)2 * DP * 32 * sizeof(float);
-  constexpr size_t ex = (size_t)kWaves * 16 * 64 * sizeof(double);
-  return 2 * blk + 2 * ex + 3 * 32 * sizeof(double) <= kMaxLds ? 2 : 1;
-}
-
-template <int DP>
-constexpr size_t lse_split_lds_bytes() {
-  constexpr int MB = lse_split_mu_buffers<DP>();
-  return (size_t)MB * 2 * DP * 32 * sizeof(float)               // mu' blocks
-         + (size_t)MB * kWaves * 16 * 64 * sizeof(double)         // second-half partials
-         + (size_t)(MB + 1) * 32 * sizeof(double);                // constants
-}
-
-template <int DP, bool LJ>
-__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
-void diag_lse_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
-                    const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_blk, int KB,
-                    float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj) {
-  constexpr int NMX = DP / 8;
-  constexpr int NM = 2 * NMX;
-  constexpr int NMH = NMX / 2;            // x chunks per half
-  constexpr int HD = DP / 2;
-  constexpr int BLK = NM * 64;
-  constexpr int LPT = BLK / kAccThreads;
-  constexpr int MB = lse_split_mu_buffers<DP>();
-  constexpr int NKC = MB + 1;             // constant buffers
-  static_assert(BLK % kAccThreads == 0 && NMH % 2 == 0, "split shape");
-
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  unsigned char* p = lds_raw;
-  f32x4* mu_l = reinterpret_cast<f32x4*>(p);   p += (size_t)MB * BLK * sizeof(f32x4);
-  double* ex = reinterpret_cast<double*>(p);   p += (size_t)MB * kWaves * 16 * 64 * sizeof(double);
-  double* kc_l = reinterpret_cast<double*>(p);
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = lane & 31, g = lane >> 5;
-  const int rg = wave & 3, h = wave >> 2;
-  const int64_t tile = (int64_t)blockIdx.x * kWaves + rg;   // 32-row tile
-  const int64_t row = tile * 32 + c;
-  const bool valid = row < N;
-
-  f32x4 st[LPT];
-  double kst = 0.0;
-  auto fetch = [&](int kb) {
-    const f32x4* src = mu_sw + (int64_t)kb * BLK;
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) st[q] = src[q * kAccThreads + tid];
-    if (tid < 32) kst = kc_blk[(int64_t)kb * 32 + tid];
-  };
-  auto commit = [&](int kb) {
-    f32x4* dst = mu_l + (MB == 2 ? (kb & 1) : 0) * BLK;
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) dst[q * kAccThreads + tid] = st[q];
-    if (tid < 32) kc_l[(kb % NKC) * 32 + tid] = kst;
-  };
-  fetch(0);
-  f32x4 xb[NMH];
-#pragma unroll
-  for (int m = 0; m < NMH; ++m) xb[m] = load_row4(X, ldx, row, h * HD + 8 * m + 4 * g, D, valid);
-  commit(0);
-  lds_barrier();
-
-  double mx = -INFINITY;
-  float sm = 0.0f;
-  for (int kb = 0; kb < KB; ++kb) {
-    const int buf = MB == 2 ? (kb & 1) : 0;
-    const bool more = kb + 1 < KB;
-    if (more) fetch(kb + 1);
-    // Chunks 0..NMH-1 pair x^2 with mu' chunks h*NMH.., the rest x with NMX + h*NMH..
-    const f32x4* mp = mu_l + buf * BLK + h * NMH * 64 + lane;
-    double xm[16];
-    cross_tile<2 * NMH>(xm, [&](int m) { return m < NMH ? mp[m * 64] : mp[(NMX - NMH + m) * 64]; },
-                        [&](int m) { return m < NMH ? sq4(xb[m]) : xb[m - NMH]; });
-    double* exb = ex + (size_t)(buf * kWaves + rg) * 16 * 64 + lane;
-    if (h == 1) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) exb[i * 64] = xm[i];
-    }
-    if (MB == 2 && more) commit(kb + 1);
-    lds_barrier();
-    if (MB == 1 && more) commit(kb + 1);
-    if (h == 0) {
-      const double* kp = kc_l + (kb % NKC) * 32 + g * 16;
-      double ll[16];
-      double bm = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        ll[i] = kp[i] + (xm[i] + exb[i * 64]);
-        bm = fmax(bm, ll[i]);
-      }
-      if constexpr (LJ) lj_store(lj + (tile * KB + kb) * kLjTile, lane, ll);
-      const double mn = fmax(mx, bm);
-      const double ms = (mn == -INFINITY) ? 0.0 : mn;
-      float acc = sm * fast_exp2((float)(mx - ms));
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc += fast_exp2((float)(ll[i] - ms));
-      sm = acc;
-      mx = mn;
-    }
-    if (MB == 1) lds_barrier();
-  }
-
-  if (h == 0) {
-    const double mo = __shfl_xor(mx, 32);
-    const float so = __shfl_xor(sm, 32);
-    const double mn = fmax(mx, mo);
-    const double ms = (mn == -INFINITY) ? 0.0 : mn;
-    const float tot = sm * fast_exp2((float)(mx - ms)) + so * fast_exp2((float)(mo - ms));
-    const double lz2 = mn + (double)log2f(tot);
-    if (valid && g == 0) {
-      rowstat[row] = lz2;
-      if (logZ) logZ[row] = (float)(lz2 * kLn2);
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Pass 1 on the bf16 matrix cores, up to D = 128: the centred split-bf16 cross term
@@ -483,7 +316,6 @@ __global__ __launch_bounds__(64) void diag_x6_prep(const float* __restrict__ mu,
 }
 
 // What pass 1 leaves for pass 2 besides logZ2.
-constexpr int kLjmNone = 0;    // nothing
 constexpr int kLjmStore = 1;   // the stored log-joint, its half-block maxima and need masks
 constexpr int kLjmNeed = 2;    // need masks only (the default plan)
 
@@ -680,173 +512,226 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2 up to D = 96: 8 waves (8 / CB row groups x CB component blocks, CB = 4,
-// or 2 / 1 for small K), the features of the blocks in LDS.  r^T [x | x^2]
-// accumulates into 2*DP/32 32x32 tiles per wave.
+// Pass 1 above D = 128 (any D): the component-tiled form of the isotropic
+// iso_lse_ctile over the diagonal features.  Each wave owns a 32-row tile; per
+// component tile of kCtBlocks blocks it streams its rows' chunks of 8 dimensions
+// from global memory (lane-half g: dimensions 8q + 4g .. + 3 as [x^2, x], split three
+// ways into bf16) against the tile's [-w, 2v] operands and centring offsets, which
+// the four waves share through an LDS double buffer of two-chunk stages.  Chunk q
+// accumulates into chain q % 4 (x6c_tile's products and order); the chains are
+// added as ((c0 + c1) + c2) + c3 and ll2 = C'_k + S in fp64.  Need bounds per half
+// block (16 components) as diag_lse_x6 leaves them.  With LJM = kLjmStore (the
+// stored plan, D up to 256) the log-joint is written in the register-order tiles
+// that diag_accum_lj reads.
 // ---------------------------------------------------------------------------
-template <int DP, int CB>
-constexpr size_t accum_lds_bytes() {
-  return accum_lds_bytes_for(DP, CB);
-}
-
-template <int DP, int CB>
-__global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
-void diag_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
-                const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_lin, int KB, int KP,
-                const double* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
-                float* __restrict__ part_mu, float* __restrict__ part_sq, float* __restrict__ part_nk,
-                int dense) {
-  constexpr int NMX = DP / 8;
-  constexpr int NM = 2 * NMX;
-  constexpr int NJ = DP / 32;
-  constexpr int RS = DP + 4;
-  constexpr int V4 = DP / 4;
-  constexpr int BLK = NM * 64;
-  constexpr int RG = kAccWaves / CB;     // row groups of 32 rows
-  constexpr int NT = kAccThreads;
-  constexpr int TR = 32 * RG;
-  constexpr int LPT = (TR * V4) / NT;
-  static_assert((TR * V4) % NT == 0, "even split");
+template <int LJM>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kCtWaves, 64 * kCtWaves), amdgpu_waves_per_eu(1, 1)))
+void diag_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int NQ,
+                    const bf16x8* __restrict__ mu3, const double* __restrict__ kc_x6, int KB,
+                    float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj,
+                    uint2* __restrict__ ljmask, int dense, int rexact) {
+  constexpr bool LJ = LJM == kLjmStore;
+  constexpr int NT = 64 * kCtWaves;
+  constexpr int LPT = kCtStageOps / NT;   // operand loads per thread per stage
+  static_assert(kCtStageOps % NT == 0 && kCtBlocks * 32 <= NT, "stage split");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  const size_t mu_bytes = (size_t)CB * BLK * sizeof(f32x4);
-  f32x4* mu_l = reinterpret_cast<f32x4*>(lds_raw);
-  float* xs = reinterpret_cast<float*>(lds_raw + mu_bytes);                               // [2][TR*RS]
-  double* rs = reinterpret_cast<double*>(lds_raw + mu_bytes + 2 * TR * RS * sizeof(float));  // [2][TR]
+  bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                                       // [2][stage]
+  double* kc_l = reinterpret_cast<double*>(lds_raw + 2 * kCtStageOps * sizeof(bf16x8));   // [2][blocks*32]
+  unsigned short* rmax_l = reinterpret_cast<unsigned short*>(lds_raw + lse_ctile_base());  // [wave][KB][2][32]
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, g = lane >> 5;
-  const int cbw = wave % CB, rg = wave / CB;
-  const int slab = blockIdx.x % nslab;
-  const int cg = blockIdx.x / nslab;
-  const int kb = cg * CB + cbw;
-  const bool active = kb < KB;
+  const int64_t tile = (int64_t)blockIdx.x * kCtWaves + wave;   // 32-row tile
+  const int64_t row = tile * 32 + c;
+  const bool valid = row < N;
+  const int NS = NQ / 2;                        // stages per component tile (even: NQ % 4 == 0)
+  const int nstage = (int)cdiv(KB, kCtBlocks) * NS;
+  const int nq_full = D / 8;                    // chunks that end at or before D
 
-  const int64_t r_begin = (int64_t)slab * rows_per_slab;
-  int64_t r_end = r_begin + rows_per_slab;
-  if (r_end > N) r_end = N;
-  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
-
-  for (int idx = tid; idx < CB * BLK; idx += kAccThreads) {
-    const int kbq = cg * CB + idx / BLK;
-    mu_l[idx] = (kbq < KB) ? mu_sw[(int64_t)kbq * BLK + (idx % BLK)] : zero4();
-  }
-  const double Ck = active ? kc_lin[(int64_t)kb * 32 + c] : -INFINITY;
-
-  f32x16 accx[NJ], accq[NJ];
+  // Operand stages exactly as iso_lse_ctile: thread element u covers block u / 2 of
+  // the tile, entry (u % 2) * NT + tid of its 512; blocks past KB read zero.
+  const int64_t blk_ops = (int64_t)NQ * 4 * 64;
+  const int64_t all_ops = (int64_t)KB * blk_ops;
+  bf16x8 st[LPT];
+  double kst = -INFINITY;
+  auto fetch = [&](int s) __attribute__((always_inline)) {
+    const int ct = s / NS, sp = s - ct * NS;
+    const int64_t base = (int64_t)ct * kCtBlocks * blk_ops + (int64_t)sp * 2 * 4 * 64;
+    int64_t avail = (all_ops - base) * (int64_t)sizeof(bf16x8);
+    if (avail > ((int64_t)1 << 31) - 16) avail = ((int64_t)1 << 31) - 16;
+    const buf_rsrc r = make_rsrc(mu3 + base, (uint32_t)avail);
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    accx[j] = zero16();
-    accq[j] = zero16();
-  }
-  float nk = 0.0f;
-
-  f32x4 stage[LPT];
-  double rstage = INFINITY;
-  const bool full_d = (D == DP);
-  auto fetch = [&](int t) {
-    const int64_t row0 = r_begin + (int64_t)t * TR;
-    if (full_d && row0 + TR <= r_end) {
-      // Interior tile: no row or column masking.
-      const float* src = X + row0 * ldx;
-#pragma unroll
-      for (int q = 0; q < LPT; ++q) {
-        const int idx = q * NT + tid;
-        stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < LPT; ++q) {
-        const int idx = q * NT + tid;
-        const int rr = idx / V4, c4 = idx % V4;
-        const int64_t row = row0 + rr;
-        stage[q] = load_row4(X, ldx, row, c4 * 4, D, row < r_end);
-      }
+    for (int u = 0; u < LPT; ++u) {
+      const int soff = (int)(((int64_t)(u >> 1) * blk_ops + (u & 1) * NT) * (int64_t)sizeof(bf16x8));
+      st[u] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, tid * (int)sizeof(bf16x8), soff, 0));
     }
-    if (tid < TR) {
-      const int64_t row = row0 + tid;
-      rstage = (row < r_end) ? rowstat[row] : INFINITY;
+    if (sp == 0 && tid < kCtBlocks * 32) {
+      const int64_t kc = (int64_t)ct * kCtBlocks * 32 + tid;
+      kst = kc < (int64_t)KB * 32 ? kc_x6[kc] : -INFINITY;
     }
   };
-  auto commit = [&](int buf) {
-    float* dst = xs + buf * TR * RS;
+  auto commit = [&](int s, int buf) __attribute__((always_inline)) {
+    const int ct = s / NS, sp = s - ct * NS;
 #pragma unroll
-    for (int q = 0; q < LPT; ++q) {
-      const int idx = q * NT + tid;
-      const int rr = idx / V4, c4 = idx % V4;
-      *reinterpret_cast<f32x4*>(dst + rr * RS + c4 * 4) = stage[q];
-    }
-    if (tid < TR) rs[buf * TR + tid] = rstage;
+    for (int u = 0; u < LPT; ++u) mu_l[buf * kCtStageOps + u * NT + tid] = st[u];
+    if (sp == 0 && tid < kCtBlocks * 32) kc_l[(ct & 1) * kCtBlocks * 32 + tid] = kst;
   };
 
-  if (ntiles > 0) {
-    fetch(0);
-    commit(0);
-  }
-  __syncthreads();
-
-  const f32x4* mb = mu_l + cbw * BLK + lane;
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    const bool more = t + 1 < ntiles;
-    const float* xt = xs + buf * TR * RS + rg * 32 * RS;
-    const double* rt = rs + buf * TR + rg * 32;
-    double xm[16];
-    float r[16];
-    if (active) {
-      // The 2D-feature contraction is twice as long as the isotropic one, so the
-      // responsibilities use the chunked fp64 form as well (fp32 chains over 2D
-      // features leave ~1e-4 relative error in r).
-      auto la = [&](int m) {
-        const f32x4 v =
-            *reinterpret_cast<const f32x4*>(xt + c * RS + 8 * (m < NMX ? m : m - NMX) + 4 * g);
-        return m < NMX ? sq4(v) : v;
-      };
-      cross_tile<NM>(xm, la, [&](int m) { return mb[m * 64]; });
-      const double* rbase = rt + 4 * g;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ro = 8 * (i >> 2) + (i & 3);
-        const float rv = fast_exp2((float)((Ck - rbase[ro]) + xm[i]));
-        nk += rv;
-        r[i] = rv;
-      }
+  // The wave's rows, dimensions 8q + 4g .. + 3 of chunk q (zero past D and N).
+  const float* xrow = X + (valid ? row : 0) * ldx + 4 * g;
+  auto xload = [&](int q) __attribute__((always_inline)) -> f32x4 {
+    if (q < nq_full) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(xrow + 8 * q);
+      return valid ? v : zero4();
     }
-    if (more) fetch(t + 1);
-    if (active) {
-      const float* xbase = xt + 4 * g * RS + c;
+    return load_row4(X, ldx, row, 8 * q + 4 * g, D, valid);
+  };
+  f32x4 xr[2][2];   // [stage parity][chunk in the pair]
+  auto xstage = [&](int s, f32x4 (&dst)[2]) __attribute__((always_inline)) {
+    if (s >= nstage) return;
+    const int sp = s % NS;
+    dst[0] = xload(2 * sp);
+    dst[1] = xload(2 * sp + 1);
+  };
+
+  fetch(0);
+  xstage(0, xr[0]);
+  commit(0, 0);
+  lds_barrier();
+
+  f32x16 acc[kCtBlocks][kCtChains];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ro = 8 * (i >> 2) + (i & 3);
-        // Steps whose 64 responsibilities are all exactly zero add nothing (tested
-        // only where a step holds enough matrix work to pay for the test).
-        if (NJ < 2 || dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
+  for (int b = 0; b < kCtBlocks; ++b) {
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) {
-            const float xv = xbase[ro * RS + 32 * j];
-            accx[j] = mfma32(r[i], xv, accx[j]);
-            accq[j] = mfma32(r[i], xv * xv, accq[j]);
+    for (int h = 0; h < kCtChains; ++h) acc[b][h] = zero16();
+  }
+  const bf16x8 ones = x6c_ones(lane);
+  double mx = -INFINITY;
+  float sm = 0.0f;
+  float run_max = -INFINITY;   // running max of the row's half-block maxima (running-max bound)
+
+  // Component tile ct is complete: log-joint, log-sum-exp and need bounds per block.
+  auto finish_tile = [&](int ct) __attribute__((always_inline)) {
+    const double* kp0 = kc_l + (ct & 1) * kCtBlocks * 32 + g * 16;
+#pragma unroll
+    for (int b = 0; b < kCtBlocks; ++b) {
+      const int kb = ct * kCtBlocks + b;
+      if (kb < KB) {
+        double ll[16];
+        double bh[2] = {-INFINITY, -INFINITY};   // maxima of the half blocks (registers 0-7, 8-15)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float S = ((acc[b][0][i] + acc[b][1][i]) + acc[b][2][i]) + acc[b][3][i];
+          ll[i] = kp0[b * 32 + i] + (double)S;
+          bh[i >> 3] = fmax(bh[i >> 3], ll[i]);
+        }
+        double bm = fmax(bh[0], bh[1]);
+        asm volatile("" : "+v"(bm));
+        const double mn = fmax(mx, bm);
+        const double ms = (mn == -INFINITY) ? 0.0 : mn;
+        float a = sm * fast_exp2((float)(mx - ms));
+#pragma unroll
+        for (int i = 0; i < 16; ++i) a += fast_exp2((float)(ll[i] - ms));
+        sm = a;
+        mx = mn;
+        if constexpr (LJ) {
+          lj_store(lj + (tile * KB + kb) * kLjTile, lane, ll);
+        } else {
+#pragma unroll
+          for (int H = 0; H < 2; ++H) {
+            const float R = lj_row_max(bh[H]);
+            if (rexact) {
+              if (g == 0) rmax_l[((wave * KB + kb) * 2 + H) * 32 + c] = bf16_bits_up(R);
+            } else {
+              run_max = fmaxf(run_max, R);
+              const bool nb = valid && (dense != 0 || !(R - run_max < -kLjSkipGap));
+              const unsigned bits = (unsigned)__builtin_amdgcn_ballot_w64(nb);
+              if (lane == 0) reinterpret_cast<unsigned*>(ljmask)[(tile * KB + kb) * 2 + H] = bits;
+            }
           }
         }
       }
+#pragma unroll
+      for (int h = 0; h < kCtChains; ++h) acc[b][h] = zero16();
     }
-    if (more) commit(buf ^ 1);
-    __syncthreads();
-  }
+  };
 
-  if (active) {
-    nk += __shfl_xor(nk, 32);
-    const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
+  // One stage; P = s & 1 is the LDS buffer and the register stage, the chunks go to
+  // chains 2P and 2P + 1 (NS is even).
+  auto stage = [&](int ct, int sp, auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    const int s = ct * NS + sp;
+    const bool more = s + 1 < nstage;
+    if (more) fetch(s + 1);
+    xstage(s + 1, xr[1 - P]);
+    const bf16x8* mp = mu_l + P * kCtStageOps + lane;
+    bf16x8 xb[2][3];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
+    for (int qq = 0; qq < 2; ++qq) split3_bf16(xr[P][qq] * xr[P][qq], xr[P][qq], xb[qq]);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int64_t o = (kbase + acc_row(i, g)) * DP + 32 * j + c;
-        part_mu[o] = accx[j][i];
-        part_sq[o] = accq[j][i];
+    for (int b = 0; b < kCtBlocks; ++b) {
+      bf16x8 a[2][4];
+#pragma unroll
+      for (int qq = 0; qq < 2; ++qq) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) a[qq][t] = mp[b * 512 + (qq * 4 + t) * 64];
+      }
+      // Steps in x6c_tile's order: x2 mu2, x1 mu3, x3 mu1, x2 mu1, x1 mu2, -o, x1 mu1.
+#pragma unroll
+      for (int step = 0; step < 7; ++step) {
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq) {
+          const bf16x8 A = step == 0 ? a[qq][1] : step == 1 ? a[qq][2] : step <= 3 ? a[qq][0]
+                         : step == 4 ? a[qq][1] : step == 5 ? a[qq][3] : a[qq][0];
+          const bf16x8 B = step == 0 ? xb[qq][1] : step == 1 ? xb[qq][0] : step == 2 ? xb[qq][2]
+                         : step == 3 ? xb[qq][1] : step == 4 ? xb[qq][0] : step == 5 ? ones : xb[qq][0];
+          acc[b][2 * P + qq] = mfma_bf16(A, B, acc[b][2 * P + qq]);
+        }
       }
     }
-    if (g == 0) part_nk[kbase + c] = nk;
+    if (more) commit(s + 1, 1 - P);
+    lds_barrier();
+  };
+  for (int ct = 0; ct * NS < nstage; ++ct) {
+    for (int sp = 0; sp < NS; sp += 2) {
+      stage(ct, sp, std::integral_constant<int, 0>{});
+      stage(ct, sp + 1, std::integral_constant<int, 1>{});
+    }
+    finish_tile(ct);
+  }
+
+  // Merge the two half-waves that hold the same row.
+  const double mo = __shfl_xor(mx, 32);
+  const float so = __shfl_xor(sm, 32);
+  const double mn = fmax(mx, mo);
+  const double ms = (mn == -INFINITY) ? 0.0 : mn;
+  const float tot = sm * fast_exp2((float)(mx - ms)) + so * fast_exp2((float)(mo - ms));
+  const double lz2 = mn + (double)log2f(tot);
+  if (valid && g == 0) {
+    rowstat[row] = lz2;
+    if (logZ) logZ[row] = (float)(lz2 * kLn2);
+  }
+  if constexpr (!LJ) {
+    unsigned* mk = reinterpret_cast<unsigned*>(ljmask);
+    if (rexact) {
+#pragma unroll
+      for (int H = 0; H < 2; ++H) {
+        const unsigned short* rm = rmax_l + (wave * KB * 2 + H) * 32 + c;
+        if (g == 0)
+          need_put_masks([&](int kb) { return bf16_bits_to_float(rm[kb * 64]); }, mk + tile * KB * 2 + H,
+                         nullptr, KB, c, lz2, valid, dense != 0, 2);
+      }
+    } else {
+      // A row whose logZ2 is NaN gets its bit in every half block, as the exact test gives it.
+      const unsigned nanbits = (unsigned)__builtin_amdgcn_ballot_w64(valid && g == 0 && lz2 != lz2);
+      if (lane == 0 && nanbits != 0)
+        for (int kb = 0; kb < KB; ++kb) {
+          mk[(tile * KB + kb) * 2] |= nanbits;
+          mk[(tile * KB + kb) * 2 + 1] |= nanbits;
+        }
+    }
   }
 }
 
@@ -1480,187 +1365,6 @@ void diag_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   }
 }
 
-// ---------------------------------------------------------------------------
-// Pass 2 above D = 96: two waves per component block (2 or 4 blocks per
-// workgroup), one per half of the dimensions.  Each wave keeps the features
-// [-w | 2v] of its half resident in
-// registers and forms the partial contraction over that half (accurate fp64
-// form); the two halves are exchanged through LDS and summed in a fixed order,
-// so both waves of a component block hold the same log-joint and r.  Each wave
-// then accumulates r^T [x | x^2] for the columns of its own half.
-// ---------------------------------------------------------------------------
-template <int DP>
-constexpr size_t accum_split_lds_bytes() {
-  return (size_t)2 * 32 * (DP + 4) * sizeof(float)                     // X, 2 buffers of 32 rows
-         + (size_t)2 * 32 * sizeof(double)                              // row logZ2, 2 buffers
-         + (size_t)2 * split_blocks(DP) * 16 * 64 * sizeof(double);    // partial contractions
-}
-
-template <int DP>
-__global__ __attribute__((amdgpu_flat_work_group_size(128 * split_blocks(DP), 128 * split_blocks(DP)),
-                          amdgpu_waves_per_eu(split_blocks(DP) / 2, split_blocks(DP) / 2)))
-void diag_accum_split(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
-                      const f32x4* __restrict__ mu_sw, const double* __restrict__ kc_lin, int KB,
-                      int KP, const double* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
-                      float* __restrict__ part_mu, float* __restrict__ part_sq,
-                      float* __restrict__ part_nk, int dense) {
-  constexpr int HD = DP / 2;           // dimensions per wave
-  constexpr int NMX = DP / 8;          // x^2 chunks of the full feature vector
-  constexpr int NMH = HD / 8;          // chunks per half, per feature kind
-  constexpr int NMW = 2 * NMH;         // chunks per wave
-  constexpr int NJH = HD / 32;         // 32-column accumulator tiles per wave
-  constexpr int RS = DP + 4;
-  constexpr int V4 = DP / 4;
-  constexpr int CB = split_blocks(DP);  // component blocks per workgroup
-  constexpr int NT = 128 * CB;          // two waves per block
-  constexpr int LPT = (32 * V4) / NT;
-  static_assert(HD % 32 == 0 && (32 * V4) % NT == 0, "split shape");
-
-  extern __shared__ __align__(16) unsigned char lds_raw[];
-  float* xs = reinterpret_cast<float*>(lds_raw);                                           // [2][32*RS]
-  double* rs = reinterpret_cast<double*>(lds_raw + 2 * 32 * RS * sizeof(float));          // [2][32]
-  double* ex = reinterpret_cast<double*>(lds_raw + 2 * 32 * RS * sizeof(float) +
-                                         2 * 32 * sizeof(double));                        // [4][16][64]
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = lane & 31, g = lane >> 5;
-  const int cb = wave >> 1, h = wave & 1;
-  const int slab = blockIdx.x % nslab;
-  const int cg = blockIdx.x / nslab;
-  const int kb = cg * CB + cb;
-  const bool active = kb < KB;
-
-  const int64_t r_begin = (int64_t)slab * rows_per_slab;
-  int64_t r_end = r_begin + rows_per_slab;
-  if (r_end > N) r_end = N;
-  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
-
-  // This wave's features: x^2 chunks then x chunks of dimensions [h*HD, (h+1)*HD).
-  f32x4 mub[NMW];
-#pragma unroll
-  for (int m = 0; m < NMW; ++m) {
-    const int mg = m < NMH ? h * NMH + m : NMX + h * NMH + (m - NMH);
-    mub[m] = active ? mu_sw[((int64_t)kb * 2 * NMX + mg) * 64 + lane] : zero4();
-  }
-  const double Ck = active ? kc_lin[(int64_t)kb * 32 + c] : -INFINITY;
-
-  f32x16 accx[NJH], accq[NJH];
-#pragma unroll
-  for (int j = 0; j < NJH; ++j) {
-    accx[j] = zero16();
-    accq[j] = zero16();
-  }
-  float nk = 0.0f;
-
-  f32x4 stage[LPT];
-  double rstage = INFINITY;
-  const bool full_d = (D == DP);
-  auto fetch = [&](int t) {
-    const int64_t row0 = r_begin + (int64_t)t * 32;
-    if (full_d && row0 + 32 <= r_end) {
-      const float* src = X + row0 * ldx;
-#pragma unroll
-      for (int q = 0; q < LPT; ++q) {
-        const int idx = q * NT + tid;
-        stage[q] = *reinterpret_cast<const f32x4*>(src + (int64_t)(idx / V4) * ldx + (idx % V4) * 4);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < LPT; ++q) {
-        const int idx = q * NT + tid;
-        const int64_t row = row0 + idx / V4;
-        stage[q] = load_row4(X, ldx, row, (idx % V4) * 4, D, row < r_end);
-      }
-    }
-    if (tid < 32) {
-      const int64_t row = row0 + tid;
-      rstage = (row < r_end) ? rowstat[row] : INFINITY;
-    }
-  };
-  auto commit = [&](int buf) {
-    float* dst = xs + buf * 32 * RS;
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) {
-      const int idx = q * NT + tid;
-      *reinterpret_cast<f32x4*>(dst + (idx / V4) * RS + (idx % V4) * 4) = stage[q];
-    }
-    if (tid < 32) rs[buf * 32 + tid] = rstage;
-  };
-
-  if (ntiles > 0) {
-    fetch(0);
-    commit(0);
-  }
-  __syncthreads();
-
-  double* my_ex = ex + (size_t)wave * 16 * 64 + lane;
-  const double* ex0 = ex + (size_t)(cb * 2) * 16 * 64 + lane;
-  const double* ex1 = ex + (size_t)(cb * 2 + 1) * 16 * 64 + lane;
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    const bool more = t + 1 < ntiles;
-    const float* xt = xs + buf * 32 * RS;
-    const double* rt = rs + buf * 32;
-    if (active) {
-      double xm[16];
-      const float* xrow = xt + c * RS + h * HD + 4 * g;
-      cross_tile<NMW>(
-          xm,
-          [&](int m) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(xrow + 8 * (m < NMH ? m : m - NMH));
-            return m < NMH ? sq4(v) : v;
-          },
-          [&](int m) { return mub[m]; });
-#pragma unroll
-      for (int i = 0; i < 16; ++i) my_ex[i * 64] = xm[i];
-    }
-    __syncthreads();
-    if (more) fetch(t + 1);
-    if (active) {
-      float r[16];
-      const double* rbase = rt + 4 * g;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ro = 8 * (i >> 2) + (i & 3);
-        const double xm = ex0[i * 64] + ex1[i * 64];   // same order in both halves
-        const float rv = fast_exp2((float)((Ck - rbase[ro]) + xm));
-        nk += rv;
-        r[i] = rv;
-      }
-      const float* xbase = xt + 4 * g * RS + h * HD + c;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ro = 8 * (i >> 2) + (i & 3);
-        if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
-#pragma unroll
-          for (int j = 0; j < NJH; ++j) {
-            const float xv = xbase[ro * RS + 32 * j];
-            accx[j] = mfma32(r[i], xv, accx[j]);
-            accq[j] = mfma32(r[i], xv * xv, accq[j]);
-          }
-        }
-      }
-    }
-    if (more) commit(buf ^ 1);
-    __syncthreads();
-  }
-
-  if (active) {
-    nk += __shfl_xor(nk, 32);
-    const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
-#pragma unroll
-    for (int j = 0; j < NJH; ++j) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int64_t o = (kbase + acc_row(i, g)) * DP + h * HD + 32 * j + c;
-        part_mu[o] = accx[j][i];
-        part_sq[o] = accq[j][i];
-      }
-    }
-    if (g == 0 && h == 0) part_nk[kbase + c] = nk;
-  }
-}
-
 __host__ size_t x6_lds_bytes_rt(int DP) {
   switch (DP) {
     case 32: return x6_lds_bytes<32>();
@@ -1855,6 +1559,213 @@ void diag_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   if (g == 0) part_nk[kbase + c] = nk;
 }
 
+// ---------------------------------------------------------------------------
+// Pass 2 of the default plan above D = 128: the isotropic iso_accum_drange's
+// structure over the diagonal features.  One workgroup of four waves per (row slab,
+// component block, range of up to kDrange dimensions); the waves queue the same
+// needed rows (either half's word); per 32 queued rows wave w forms chain w of S
+// over the chunks q = w, w + 4, ... of all of D (x6c_tile_rows' products and order
+// on [x^2, x]) and stores the fp32 rows of its chunks in the range to the LDS tile;
+// the chains meet in LDS and every wave adds them as pass 1 does, so the log-joint
+// C'_k + S equals pass 1's bit for bit; r = 2^(ll2 - logZ2), and each wave
+// accumulates r^T X and r^T X^2 for a quarter of the range's 32-column tiles on fp32
+// 32x32x2 steps (the sig identity in diag_reduce cancels, so these moments keep
+// fp32 accuracy).  Wave 0 of the first range also sums Nk.
+// ---------------------------------------------------------------------------
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kCtWaves, 64 * kCtWaves), amdgpu_waves_per_eu(1, 1)))
+void diag_accum_drange(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int NQ, int DP,
+                       const bf16x8* __restrict__ mu3, const double* __restrict__ kc_x6lin, int KB, int KP,
+                       const double* __restrict__ rowstat, const uint2* __restrict__ need, int nslab,
+                       int64_t rows_per_slab, int ndr, float* __restrict__ part_mu, float* __restrict__ part_sq,
+                       float* __restrict__ part_nk, int dense) {
+  // Workgroup -> (block, slab, range), blocks contiguous per XCD.
+  const int64_t total = (int64_t)KB * nslab * ndr;
+  const int64_t per = cdiv(total, 8);
+  const int64_t item = (int64_t)(blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (item >= total) return;   // uniform over the workgroup
+  const int dr = (int)(item % ndr);
+  const int slab = (int)((item / ndr) % nslab);
+  const int kb = (int)(item / ((int64_t)ndr * nslab));
+
+  const int RS = drange_rs(DP < kDrange ? DP : kDrange);
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  unsigned char* lp = lds_raw;
+  float* xt = reinterpret_cast<float*>(lp);       lp += (size_t)32 * RS * sizeof(float);   // [row][RS]
+  float* ex = reinterpret_cast<float*>(lp);       lp += (size_t)kCtWaves * 16 * 64 * sizeof(float);
+  double* rs_l = reinterpret_cast<double*>(lp);   lp += (size_t)32 * sizeof(double);
+  int* q_all = reinterpret_cast<int*>(lp);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  int* q_l = q_all + wave * 64;
+
+  const int d0 = dr * kDrange;
+  const int DR = DP - d0 < kDrange ? DP - d0 : kDrange;   // a multiple of 64
+  const int q_lo = d0 / 8, q_hi = (d0 + DR) / 8;           // chunks of the range
+  const int njr = DR / 32;
+  const int tj = (njr + kCtWaves - 1) / kCtWaves;
+  const int j0 = wave * tj;
+  const int nj = njr - j0 < tj ? (njr - j0 > 0 ? njr - j0 : 0) : tj;   // this wave's column tiles
+  const int nqw = NQ / kCtWaves;                                       // chunks per wave
+
+  const double Cc = kc_x6lin[(int64_t)kb * 32 + c];
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int64_t t_begin = r_begin / 32, t_end = cdiv(r_end, 32);
+
+  auto words = [&](int64_t tb) -> unsigned {
+    const int64_t t = tb + lane;
+    if (t >= t_end) return 0u;
+    const uint2 w = need[t * KB + kb];
+    return w.x | w.y;
+  };
+  int64_t tb = t_begin;
+  unsigned mword = words(tb), mnext = words(tb + 64);
+  int jn = 0;
+  int qh = 0, qt = 0;
+  auto take = [&](int& e) -> int {
+    while (qt - qh < 32) {
+      const uint64_t live = jn >= 64 ? 0ull : (~0ull << jn);
+      const uint64_t nz = __builtin_amdgcn_ballot_w64(mword != 0u) & live;
+      if (nz == 0) {
+        tb += 64;
+        if (tb >= t_end) break;
+        mword = mnext;
+        mnext = words(tb + 64);
+        jn = 0;
+        continue;
+      }
+      const int j = __builtin_ctzll(nz);
+      const unsigned m = __builtin_amdgcn_readlane(mword, j);
+      const int base = (int)((tb + j - t_begin) * 32);
+      if (g == 0 && ((m >> c) & 1u)) q_l[(qt + __builtin_popcount(m & ((1u << c) - 1u))) & 63] = base + c;
+      qt += __builtin_popcount(m);
+      jn = j + 1;
+    }
+    const int cnt = qt - qh < 32 ? qt - qh : 32;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    e = c < cnt ? q_l[(qh + c) & 63] : -1;
+    qh += cnt;
+    return cnt;
+  };
+
+  // Chunk i of this wave (chunk q = wave + 4 i): the rows' dimensions 8q + 4g .. + 3
+  // and mu's four operands of the chunk.
+  const buf_rsrc mrs = make_rsrc(mu3 + (int64_t)kb * NQ * 4 * 64, (uint32_t)((int64_t)NQ * 4 * 64 * sizeof(bf16x8)));
+  auto issue = [&](int i, int e, f32x4& x, bf16x8 (&m)[4]) __attribute__((always_inline)) {
+    const int q = wave + kCtWaves * i;
+    const bool ok = e >= 0;
+    x = load_row4(X, ldx, r_begin + (ok ? e : 0), 8 * q + 4 * g, D, ok);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      m[t] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                            mrs, lane * (int)sizeof(bf16x8), (q * 4 + t) * 64 * (int)sizeof(bf16x8), 0));
+  };
+  f32x4 xr[2];
+  bf16x8 mr[2][4];
+  double rst = INFINITY;
+  auto start = [&](int e) __attribute__((always_inline)) {
+    issue(0, e, xr[0], mr[0]);
+    if (nqw > 1) issue(1, e, xr[1], mr[1]);
+    if (wave == 0) rst = e >= 0 ? rowstat[r_begin + e] : INFINITY;
+  };
+
+  f32x16 accx[kDrTiles], accq[kDrTiles];
+#pragma unroll
+  for (int j = 0; j < kDrTiles; ++j) {
+    accx[j] = zero16();
+    accq[j] = zero16();
+  }
+  float nk = 0.0f;
+  const bf16x8 ones = x6c_ones(lane);
+
+  int e;
+  int cnt = take(e);
+  if (cnt > 0) start(e);
+  while (cnt > 0) {
+    f32x16 cs = zero16();
+    auto chunk = [&](int i, const f32x4& x, const bf16x8 (&m)[4]) __attribute__((always_inline)) {
+      const int q = wave + kCtWaves * i;
+      if (q >= q_lo && q < q_hi) *reinterpret_cast<f32x4*>(xt + c * RS + 8 * (q - q_lo) + 4 * g) = x;
+      bf16x8 xa[3];
+      split3_bf16(x * x, x, xa);
+#pragma unroll
+      for (int step = 0; step < 7; ++step) {
+        const bf16x8 B = step == 0 ? m[1] : step == 1 ? m[2] : step <= 3 ? m[0] : step == 4 ? m[1]
+                       : step == 5 ? m[3] : m[0];
+        const bf16x8 A = step == 0 ? xa[1] : step == 1 ? xa[0] : step == 2 ? xa[2] : step == 3 ? xa[1]
+                       : step == 4 ? xa[0] : step == 5 ? ones : xa[0];
+        cs = mfma_bf16(A, B, cs);
+      }
+    };
+    for (int i = 0; i < nqw; i += 2) {
+      chunk(i, xr[0], mr[0]);
+      if (i + 2 < nqw) issue(i + 2, e, xr[0], mr[0]);
+      if (i + 1 < nqw) {
+        chunk(i + 1, xr[1], mr[1]);
+        if (i + 3 < nqw) issue(i + 3, e, xr[1], mr[1]);
+      }
+    }
+    float* exw = ex + wave * 16 * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) exw[i * 64] = cs[i];
+    if (wave == 0 && g == 0) rs_l[c] = rst;
+    int en;
+    const int cnt_next = take(en);
+    if (cnt_next > 0) start(en);
+    lds_barrier();
+
+    float r[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float S = ((ex[i * 64 + lane] + ex[(16 + i) * 64 + lane]) + ex[(32 + i) * 64 + lane]) +
+                      ex[(48 + i) * 64 + lane];
+      const double ll = Cc + (double)S;
+      const float rv = fast_exp2((float)(ll - rs_l[acc_row(i, g)]));
+      r[i] = rv;
+      nk += rv;
+    }
+    const float* xbase = xt + 4 * g * RS + c;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int ro = 8 * (i >> 2) + (i & 3);
+      if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
+#pragma unroll
+        for (int jj = 0; jj < kDrTiles; ++jj) {
+          if (jj < nj) {
+            const float xv = xbase[ro * RS + 32 * (j0 + jj)];
+            accx[jj] = mfma32(r[i], xv, accx[jj]);
+            accq[jj] = mfma32(r[i], xv * xv, accq[jj]);
+          }
+        }
+      }
+    }
+    lds_barrier();   // the tile and the chains are free for the next rows
+    e = en;
+    cnt = cnt_next;
+  }
+
+  const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+#pragma unroll
+  for (int jj = 0; jj < kDrTiles; ++jj) {
+    if (jj < nj) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t o = (kbase + acc_row(i, g)) * DP + d0 + 32 * (j0 + jj) + c;
+        part_mu[o] = accx[jj][i];
+        part_sq[o] = accq[jj][i];
+      }
+    }
+  }
+  if (dr == 0 && wave == 0) {
+    nk += __shfl_xor(nk, 32);
+    if (g == 0) part_nk[kbase + c] = nk;
+  }
+}
+
 // Finish: one thread per (k, d); fixed-order fp64 sums over partials, then the
 // sig identity in fp64.  Thread d == 0 also writes Nk.
 template <bool WIDE>
@@ -1916,12 +1827,46 @@ __global__ __launch_bounds__(256) void diag_fill(float* __restrict__ p, int64_t 
   if (i < n) p[i] = v;
 }
 
+// Above D = 128: pass 1 is diag_lse_ctile for both plans; pass 2 of the default plan
+// (any D) is diag_accum_drange, that of the stored plan (D <= 256) launch_passes'.
+hipError_t launch_ctile(const DiagPlan& pl, const float* X, int64_t ldx, unsigned char* ws, float* logZ,
+                        bool run1, bool run2, bool dense, hipStream_t stream) {
+  const bf16x8* mu3 = reinterpret_cast<const bf16x8*>(ws + pl.off_mu3);
+  double* rowstat = reinterpret_cast<double*>(ws + pl.off_rowstat);
+  uint2* masks = reinterpret_cast<uint2*>(ws + pl.off_ljmask);
+  const int NQ = pl.DP / 8;
+  if (run1) {
+    const bool exact = pl.rexact && !pl.lj;
+    const size_t lds1 = lse_ctile_base() + (exact ? (size_t)kCtWaves * 2 * 32 * pl.KB * 2 : 0);
+    auto kern = pl.lj ? &diag_lse_ctile<kLjmStore> : &diag_lse_ctile<kLjmNeed>;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(pl.N, 32 * kCtWaves)), dim3(64 * kCtWaves), lds1, stream, X,
+                       ldx, pl.N, (int)pl.D, NQ, mu3, reinterpret_cast<const double*>(ws + pl.off_kcx6), pl.KB,
+                       logZ, rowstat, pl.lj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr, masks,
+                       dense ? 1 : 0, exact ? 1 : 0);
+  }
+  if (run2 && !pl.lj) {
+    const size_t lds2 = accum_drange_lds_bytes(pl.DP < kDrange ? pl.DP : kDrange);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum_drange),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+    if (e != hipSuccess) return e;
+    const int64_t items = (int64_t)pl.KB * pl.nslab * pl.ndr;
+    hipLaunchKernelGGL(diag_accum_drange, dim3((unsigned)(8 * cdiv(items, 8))), dim3(64 * kCtWaves), lds2,
+                       stream, X, ldx, pl.N, (int)pl.D, NQ, pl.DP, mu3,
+                       reinterpret_cast<const double*>(ws + pl.off_kcx6lin), pl.KB, pl.KP, rowstat, masks,
+                       pl.nslab, pl.rows_per_slab, pl.ndr, reinterpret_cast<float*>(ws + pl.off_part_mu),
+                       reinterpret_cast<float*>(ws + pl.off_part_sq), reinterpret_cast<float*>(ws + pl.off_part_nk),
+                       dense ? 1 : 0);
+  }
+  return hipGetLastError();
+}
+
+// Up to D = 128 both plans; above, the stored plan's pass 2 (pass 1 is launch_ctile's).
 template <int DP>
 hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
                          float* logZ, bool run1, bool run2, bool dense, hipStream_t stream) {
-  const f32x4* mu_sw = reinterpret_cast<const f32x4*>(ws + pl.off_musw);
-  const double* kc_blk = reinterpret_cast<const double*>(ws + pl.off_kcblk);
-  const double* kc_lin = reinterpret_cast<const double*>(ws + pl.off_kclin);
   double* rowstat = reinterpret_cast<double*>(ws + pl.off_rowstat);
   float* lj = pl.lj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
   float* ljmax = pl.lj_sparse ? reinterpret_cast<float*>(ws + pl.off_ljmax) : nullptr;
@@ -1934,8 +1879,7 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
     const unsigned nblk1 = (unsigned)cdiv(pl.N, 32 * kWaves);
     if constexpr (diag_uses_x6(DP)) {
       const size_t lds1 = x6_lds_bytes<DP>() + (pl.rexact ? (size_t)kAccWaves * 32 * pl.KB * 2 : 0);
-      auto kern = pl.lj ? &diag_lse_x6<DP, kLjmStore> : pl.need ? &diag_lse_x6<DP, kLjmNeed>
-                                                                : &diag_lse_x6<DP, kLjmNone>;
+      auto kern = pl.lj ? &diag_lse_x6<DP, kLjmStore> : &diag_lse_x6<DP, kLjmNeed>;
       if (lds1 > 65536) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
@@ -1947,18 +1891,7 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
                          reinterpret_cast<const double*>(ws + pl.off_kcx6), pl.KB, logZ, rowstat, lj,
                          ljmax, reinterpret_cast<unsigned*>(masks), ljcount, dense ? 1 : 0, pl.rexact ? 1 : 0);
     } else {
-      // Above D = 128 the rows' dimensions are split over two waves.
-      constexpr size_t lds1 = lse_split_lds_bytes<DP>();
-      if (lds1 > 65536) {
-        for (const void* f : {reinterpret_cast<const void*>(&diag_lse_split<DP, false>),
-                              reinterpret_cast<const void*>(&diag_lse_split<DP, true>)}) {
-          hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
-          if (e != hipSuccess) return e;
-        }
-      }
-      auto kern = pl.lj ? &diag_lse_split<DP, true> : &diag_lse_split<DP, false>;
-      hipLaunchKernelGGL(kern, dim3(nblk1), dim3(kAccThreads), lds1, stream, X, ldx, pl.N,
-                         (int)pl.D, mu_sw, kc_blk, pl.KB, logZ, rowstat, lj);
+      return hipErrorInvalidValue;   // launch_ctile runs pass 1 above D = 128
     }
   }
   if (!run2) return hipGetLastError();
@@ -2016,70 +1949,27 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
       }
     }
   }
-  if (pl.lj) {
-    auto launch = [&](auto cb_tag, auto nh_tag) -> hipError_t {
-      constexpr int CB = decltype(cb_tag)::value;
-      constexpr int NH = decltype(nh_tag)::value;
-      constexpr size_t lds = accum_lj_lds_bytes<DP, CB, NH>();
-      static_assert(lds <= kMaxLds, "pass-2 tiles exceed LDS");
-      if (lds > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum_lj<DP, CB, NH>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-      }
-      hipLaunchKernelGGL((diag_accum_lj<DP, CB, NH>), grid2, dim3(kAccThreads), lds, stream, X, ldx,
-                         pl.N, (int)pl.D, lj, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
-                         pmu, psq, pnk, dense ? 1 : 0);
-      return hipGetLastError();
-    };
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-    using I4 = std::integral_constant<int, 4>;
-    if constexpr (DP > 128) {
-      return launch(I4{}, I2{});
-    } else if constexpr (DP == 128) {
-      return pl.cpg == 8 ? launch(std::integral_constant<int, 8>{}, I1{}) : launch(I4{}, I2{});
-    } else {
-      return pl.cpg == 8 ? launch(std::integral_constant<int, 8>{}, I1{}) : launch(I4{}, I1{});
-    }
-  }
-  if constexpr (diag_accum_split_d(DP)) {
-    constexpr size_t lds2 = accum_split_lds_bytes<DP>();
-    if (lds2 > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum_split<DP>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+  if (!pl.lj) return hipErrorInvalidValue;   // not a plan of this launcher
+  // The stored plan above D = 128: the register-order log-joint tiles of diag_lse_ctile.
+  auto launch = [&](auto cb_tag, auto nh_tag) -> hipError_t {
+    constexpr int CB = decltype(cb_tag)::value;
+    constexpr int NH = decltype(nh_tag)::value;
+    constexpr size_t lds = accum_lj_lds_bytes<DP, CB, NH>();
+    static_assert(lds <= kMaxLds, "pass-2 tiles exceed LDS");
+    if (lds > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum_lj<DP, CB, NH>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(diag_accum_split<DP>, dim3((unsigned)(pl.nslab * pl.ncg)), dim3(128 * split_blocks(DP)),
-                       lds2, stream, X, ldx, pl.N, (int)pl.D, mu_sw, kc_lin, pl.KB, pl.KP, rowstat,
-                       pl.nslab, pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_mu),
-                       reinterpret_cast<float*>(ws + pl.off_part_sq),
-                       reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
+    hipLaunchKernelGGL((diag_accum_lj<DP, CB, NH>), grid2, dim3(kAccThreads), lds, stream, X, ldx,
+                       pl.N, (int)pl.D, lj, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
+                       pmu, psq, pnk, dense ? 1 : 0);
     return hipGetLastError();
+  };
+  if constexpr (DP > 128) {
+    return launch(std::integral_constant<int, 4>{}, std::integral_constant<int, 2>{});
   } else {
-    auto launch = [&](auto cb_tag) -> hipError_t {
-      constexpr int CB = decltype(cb_tag)::value;
-      constexpr size_t lds2 = accum_lds_bytes<DP, CB>();
-      if constexpr (lds2 > kMaxLds) {
-        return hipErrorInvalidValue;   // never chosen by the plan
-      } else {
-        if (lds2 > 65536) {
-          hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum<DP, CB>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
-          if (e != hipSuccess) return e;
-        }
-        hipLaunchKernelGGL((diag_accum<DP, CB>), dim3((unsigned)(pl.nslab * pl.ncg)),
-                           dim3(kAccThreads), lds2, stream, X, ldx, pl.N, (int)pl.D, mu_sw,
-                           kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
-                           reinterpret_cast<float*>(ws + pl.off_part_mu),
-                           reinterpret_cast<float*>(ws + pl.off_part_sq),
-                           reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
-        return hipGetLastError();
-      }
-    };
-    return pl.cpg == 1   ? launch(std::integral_constant<int, 1>{})
-           : pl.cpg == 2 ? launch(std::integral_constant<int, 2>{})
-                         : launch(std::integral_constant<int, kWaves>{});
+    return hipErrorInvalidValue;   // the stored plan up to D = 128 is the sparse form
   }
 }
 
@@ -2588,9 +2478,9 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   if (K > 0 && (mu == nullptr || ldmu < D || log_sigma_sq == nullptr || ldlss < D ||
                 log_pi == nullptr || Nk == nullptr || mu_acc == nullptr || sig_acc == nullptr))
     return FGMM_ERR_INVALID_ARG;
-  if (D > 256) return FGMM_ERR_UNSUPPORTED;
   if (N > kMaxRows || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
   const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
+  if (bf16 && D > 256) return FGMM_ERR_UNSUPPORTED;
   // The stored-log-joint pass 2 addresses X tiles with 32-bit buffer offsets (row
   // stride at most kMaxBufLdx floats); wider strides recompute, which needs less
   // workspace.
@@ -2611,18 +2501,12 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     hipLaunchKernelGGL(diag_bf16_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
                        (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_musw),
                        reinterpret_cast<float*>(ws + pl.off_kclin));
-  else if (run1) {
-    hipLaunchKernelGGL(diag_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
-                       (int)D, pl.DP, log_pi, reinterpret_cast<f32x4*>(ws + pl.off_musw),
-                       reinterpret_cast<double*>(ws + pl.off_kcblk),
-                       reinterpret_cast<double*>(ws + pl.off_kclin));
-    if (diag_uses_x6(pl.DP))
-      hipLaunchKernelGGL(diag_x6_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
-                         (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_mu3),
-                         reinterpret_cast<double*>(ws + pl.off_kcx6),
-                         reinterpret_cast<double*>(ws + pl.off_kcx6lin),
-                         pl.lj_sparse ? reinterpret_cast<unsigned*>(ws + pl.off_ljcount) : nullptr);
-  }
+  else if (run1)
+    hipLaunchKernelGGL(diag_x6_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
+                       (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_mu3),
+                       reinterpret_cast<double*>(ws + pl.off_kcx6),
+                       reinterpret_cast<double*>(ws + pl.off_kcx6lin),
+                       pl.lj_sparse ? reinterpret_cast<unsigned*>(ws + pl.off_ljcount) : nullptr);
   if (N > 0) {
     auto run = [&](auto dp_tag) -> hipError_t {
       constexpr int DP = decltype(dp_tag)::value;
@@ -2630,7 +2514,14 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
                   : launch_passes<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
     };
     hipError_t e = hipSuccess;
-    switch (pl.DP) {
+    if (pl.ctile) {
+      e = launch_ctile(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
+      if (e == hipSuccess && pl.lj && run2) {
+        if (pl.DP == 192) e = launch_passes<192>(pl, X, ldx, ws, logZ, false, true, dense, stream);
+        else if (pl.DP == 256) e = launch_passes<256>(pl, X, ldx, ws, logZ, false, true, dense, stream);
+        else return FGMM_ERR_UNSUPPORTED;
+      }
+    } else switch (pl.DP) {
       case 32: e = run(std::integral_constant<int, 32>{}); break;
       case 64: e = run(std::integral_constant<int, 64>{}); break;
       case 96: e = run(std::integral_constant<int, 96>{}); break;
