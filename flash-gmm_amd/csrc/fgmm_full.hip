@@ -1,4 +1,4 @@
-// Full-covariance GMM E-step for gfx950 (1 <= D <= 128).
+// Full-covariance GMM E-step for gfx950 (1 <= D <= 256).
 //
 // Math (reference: flash_gmm_full_h100.py:289-296 constants, :103-130 pass 1,
 // :171-228 pass 2), with L_k lower-triangular, L_k L_k^T = Sigma_k^-1, in log2 units:
@@ -54,6 +54,7 @@ struct FullPlan {
   bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16); always stores the log-joint
   bool need;    // default plan: pass 1 leaves need masks, pass 2 gathers
   bool rexact;  // need masks from the per-(row, component) bounds (else the running max)
+  int ngrp;     // waves per (slab, component) in the gathering pass 2 (groups of sig blocks)
   int grid1;    // pass-1 workgroups with need masks (a persistent grid)
   size_t off_lop, off_bsw, off_ck, off_l3, off_esw, off_rowstat, off_part_sig, off_part_mu, off_part_nk,
       off_lj, off_need, off_bound, total;
@@ -75,6 +76,16 @@ __host__ inline size_t full_lj_bytes(int64_t N, int KP) {
   return (size_t)round_up(cdiv(N, 32), 4) * (size_t)KP * 32 * sizeof(float);
 }
 
+// The gathering pass 2 holds the accumulators of the upper 32x32 blocks of sig_outer
+// it owns in registers, with the rows' split operands: above D = 128 the blocks are
+// dealt to this many waves per (slab, component), each recomputing the whitening.
+__host__ __device__ constexpr int gather_sig_groups(int DP) {
+  return DP <= 128 ? 1 : DP <= 160 ? 2 : DP <= 224 ? 3 : 4;
+}
+// Pass 1 and the gathering pass 2 run one wave per SIMD above D = 128 (the rows'
+// split operands alone take 12 registers per 16 dimensions).
+__host__ __device__ constexpr int full_waves_per_eu(int DP) { return DP <= 128 ? 2 : 1; }
+
 // Pass-2 layout of the bf16 contract (defined with its kernels below).
 __host__ __device__ constexpr int bf16_comps_per_wg(int NMB);
 __host__ __device__ constexpr int bf16_row_groups(int NMB);
@@ -87,9 +98,11 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.NSB = p.NMB * (p.NMB + 1) / 2;
   p.KP = (int)round_up(K, kCompsPerWG);
   p.bf16 = bf16;
-  p.lj = (allow_lj || bf16) && K > 0 && full_lj_bytes(N, p.KP) <= kMaxLjBytes;
+  // The stored log-joint (and with it the bf16 contract) up to D = 128.
+  p.lj = (allow_lj || bf16) && K > 0 && p.DP <= 128 && full_lj_bytes(N, p.KP) <= kMaxLjBytes;
   p.need = !bf16 && !p.lj && K > 0;
   p.rexact = p.need && K <= kNeedExactMaxK;
+  p.ngrp = gather_sig_groups(p.DP);
   if (bf16) {
     p.ncg = p.KP / bf16_comps_per_wg(p.NMB);
     p.rgroups = bf16_row_groups(p.NMB);
@@ -104,7 +117,7 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   if (p.need && N > 0) {
     // The gathering pass 2: about two rounds of waves at two waves per SIMD (each
     // slab holds a partial of D x D per component, so no more slabs than that).
-    int64_t want = cdiv((int64_t)8 * current_device_cus(), K);
+    int64_t want = cdiv((int64_t)8 * current_device_cus(), K * p.ngrp);
     const int64_t max_slabs = cdiv(N, 32);
     if (want > max_slabs) want = max_slabs;
     p.rows_per_slab = round_up(cdiv(N, want), 32);
@@ -148,7 +161,7 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   if (p.need) off = align256(off + (size_t)round_up(cdiv(N, 32), 4) * p.KP * sizeof(unsigned));
   p.off_bound = off;
   if (p.need && N > 0) {
-    p.grid1 = (int)std::min<int64_t>(cdiv(N, 32 * kWaves), (int64_t)2 * current_device_cus());
+    p.grid1 = (int)std::min<int64_t>(cdiv(N, 32 * kWaves), (int64_t)full_waves_per_eu(p.DP) * current_device_cus());
     if (p.rexact) off = align256(off + (size_t)p.grid1 * kWaves * 32 * p.KP * sizeof(unsigned short));
   }
   p.total = off;
@@ -178,8 +191,8 @@ __global__ __launch_bounds__(256) void full_x6_prep(const float* __restrict__ mu
                                                     const float* __restrict__ L, int64_t K, int D, int DP,
                                                     const float* __restrict__ lpi, bf16x8* __restrict__ l3,
                                                     double* __restrict__ esw, double* __restrict__ ck) {
-  __shared__ double so[8][128];   // o_qj, DP <= 128
-  __shared__ double se[128];      // e_j, then log |L_jj|
+  __shared__ double so[16][256];  // o_qj, DP <= 256
+  __shared__ double se[256];      // e_j, then log |L_jj|
   const int64_t k = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
@@ -276,7 +289,8 @@ constexpr int kLjmNeed = 2;    // need masks only (the default plan)
 // word of each (32-row tile, component): bit r set unless the bound of row r is
 // kLjNeedGap below its logZ2 (need_put_masks).
 template <int DP, int LJM>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(full_waves_per_eu(DP), full_waves_per_eu(DP))))
 void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, const bf16x8* __restrict__ l3,
                  const double* __restrict__ esw, const double* __restrict__ ck, int K, int KP,
                  float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj,
@@ -682,7 +696,10 @@ __global__ __launch_bounds__(256) void full_fill(float* __restrict__ p, int64_t 
 // accumulates Nk, mu_acc and the upper 32x32 blocks of sig_outer = sum r x x^T as
 // full_accum does (r-scaled rows as the A operand of fp32 32x32x2 steps, only the
 // steps with a nonzero row).  Workgroups map to the 8 XCDs so that every component
-// of a slab group shares an XCD's L2 for the rows of X.
+// of a slab group shares an XCD's L2 for the rows of X.  Above D = 128 the upper
+// blocks are dealt to gather_sig_groups(DP) launches, GRP = 0, 1, ..., each
+// accumulating a contiguous run of blocks (GRP 0 also mu_acc and Nk) after the same
+// whitening.
 // ---------------------------------------------------------------------------
 constexpr int kGatherWaves = 4;
 
@@ -703,7 +720,7 @@ constexpr size_t gather_lds_bytes() {
 __host__ __device__ constexpr int gather_groups(int nslab) { return (nslab + kGatherWaves - 1) / kGatherWaves; }
 __host__ inline int64_t gather_grid(int nslab, int K) { return cdiv(gather_groups(nslab), 8) * (int64_t)K * 8; }
 
-template <int DP>
+template <int DP, int GRP>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * kGatherWaves, 64 * kGatherWaves),
                           amdgpu_waves_per_eu(gather_waves_per_eu(DP), gather_waves_per_eu(DP))))
 void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
@@ -713,6 +730,12 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
                        float* __restrict__ part_sig, float* __restrict__ part_mu, float* __restrict__ part_nk,
                        int dense) {
   constexpr int NMB = DP / 32, NQ = DP / 16, NSB = NMB * (NMB + 1) / 2;
+  constexpr int NGRP = gather_sig_groups(DP);
+  constexpr int NSBG = (NSB + NGRP - 1) / NGRP;              // blocks per group
+  constexpr int SB0 = GRP * NSBG;                            // this group's blocks SB0 .. SB1 - 1
+  constexpr int SB1 = SB0 + NSBG < NSB ? SB0 + NSBG : NSB;
+  constexpr bool FIRST = GRP == 0;                           // also mu_acc and Nk
+  static_assert(GRP < NGRP && SB0 < NSB, "group of sig blocks");
   constexpr int RS = DP + 4;
   constexpr int BLK = NMB * NQ * 4 * 64;   // bf16x8 per component
   constexpr bool OPS_LDS = gather_ops_in_lds(DP);
@@ -797,9 +820,9 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
     rst = ok ? rowstat[row] : INFINITY;
   };
 
-  f32x16 acc[NSB];
+  f32x16 acc[SB1 - SB0];
 #pragma unroll
-  for (int sb = 0; sb < NSB; ++sb) acc[sb] = zero16();
+  for (int sb = 0; sb < SB1 - SB0; ++sb) acc[sb] = zero16();
   float mua[NMB];
 #pragma unroll
   for (int mb = 0; mb < NMB; ++mb) mua[mb] = 0.0f;
@@ -815,14 +838,14 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   if (PREFETCH && cnt > 0) issue(e);
   while (cnt > 0) {
     if (!PREFETCH) issue(e);
-    bf16x8 xb[NQ][3];
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) split3_bf16(raw[2 * q], raw[2 * q + 1], xb[q]);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the previous tile's LDS reads are done
+    // Each chunk to the LDS tile, then split three ways (its fp32 registers free after).
+    bf16x8 xb[NQ][3];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       *reinterpret_cast<f32x4*>(xt + c * RS + 16 * q + 8 * g) = raw[2 * q];
       *reinterpret_cast<f32x4*>(xt + c * RS + 16 * q + 8 * g + 4) = raw[2 * q + 1];
+      split3_bf16(raw[2 * q], raw[2 * q + 1], xb[q]);
     }
     const double lz2 = rst;
     int en = -1;
@@ -849,7 +872,7 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
     const double ll = e_l[DP] - hl * maha;
     const float rv = fast_exp2((float)(ll - lz2));
     if (g == 0) {
-      nk += rv;
+      if constexpr (FIRST) nk += rv;
       rx[c] = rv;
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -867,15 +890,14 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
       for (int mb = 0; mb < NMB; ++mb) {
         xv[mb] = xt[rw * RS + 32 * mb + c];
         av[mb] = rr * xv[mb];
-        mua[mb] += av[mb];
+        if constexpr (FIRST) mua[mb] += av[mb];
       }
-      int sb = 0;
 #pragma unroll
       for (int m1 = 0; m1 < NMB; ++m1) {
 #pragma unroll
         for (int m2 = m1; m2 < NMB; ++m2) {
-          acc[sb] = mfma32(av[m1], xv[m2], acc[sb]);
-          ++sb;
+          const int sb = m1 * NMB - m1 * (m1 - 1) / 2 + (m2 - m1);   // upper-block index of (m1, m2)
+          if (sb >= SB0 && sb < SB1) acc[sb - SB0] = mfma32(av[m1], xv[m2], acc[sb - SB0]);
         }
       }
     }
@@ -887,19 +909,21 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   const int64_t pbase = (int64_t)slab * KP + k;
   float* ps = part_sig + pbase * NSB * 1024;
 #pragma unroll
-  for (int sb = 0; sb < NSB; ++sb) {
+  for (int sb = SB0; sb < SB1; ++sb) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) ps[sb * 1024 + acc_row(i, g) * 32 + c] = acc[sb][i];
+    for (int i = 0; i < 16; ++i) ps[sb * 1024 + acc_row(i, g) * 32 + c] = acc[sb - SB0][i];
   }
+  if constexpr (FIRST) {
 #pragma unroll
-  for (int mb = 0; mb < NMB; ++mb) {
-    const float v = mua[mb] + __shfl_xor(mua[mb], 32);
-    if (g == 0) part_mu[pbase * DP + 32 * mb + c] = v;
+    for (int mb = 0; mb < NMB; ++mb) {
+      const float v = mua[mb] + __shfl_xor(mua[mb], 32);
+      if (g == 0) part_mu[pbase * DP + 32 * mb + c] = v;
+    }
+    float nks = nk;
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) nks += __shfl_xor(nks, o);
+    if (lane == 0) part_nk[pbase] = nks;
   }
-  float nks = nk;
-#pragma unroll
-  for (int o = 16; o >= 1; o >>= 1) nks += __shfl_xor(nks, o);
-  if (lane == 0) part_nk[pbase] = nks;
 }
 
 template <int DP>
@@ -914,7 +938,8 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
   };
   if (run1) {
     constexpr size_t lds1 = full_x6_lds_bytes<DP>();
-    auto kern = pl.need ? &full_lse_x6<DP, kLjmNeed> : &full_lse_x6<DP, kLjmStore>;
+    // The stored plan runs up to D = 128 only.
+    auto kern = (DP > 128 || pl.need) ? &full_lse_x6<DP, kLjmNeed> : &full_lse_x6<DP, DP <= 128 ? kLjmStore : kLjmNeed>;
     hipError_t e = set_lds(reinterpret_cast<const void*>(kern), lds1);
     if (e != hipSuccess) return e;
     const unsigned grid1 = pl.need ? (unsigned)pl.grid1 : (unsigned)cdiv(pl.N, 32 * kWaves);
@@ -932,23 +957,39 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
   {
     if (pl.need) {
       constexpr size_t lds2 = gather_lds_bytes<DP>();
-      hipError_t e = set_lds(reinterpret_cast<const void*>(&full_accum_gather<DP>), lds2);
+      static_assert(lds2 <= 160 * 1024, "gathering pass 2 exceeds LDS");
+      auto launch = [&](auto grp_tag) -> hipError_t {
+        constexpr int GRP = decltype(grp_tag)::value;
+        if constexpr (GRP < gather_sig_groups(DP)) {
+          hipError_t e = set_lds(reinterpret_cast<const void*>(&full_accum_gather<DP, GRP>), lds2);
+          if (e != hipSuccess) return e;
+          hipLaunchKernelGGL((full_accum_gather<DP, GRP>), dim3((unsigned)gather_grid(pl.nslab, (int)pl.K)),
+                             dim3(64 * kGatherWaves), lds2, stream, X, ldx, pl.N, (int)pl.D,
+                             reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
+                             reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, rowstat,
+                             reinterpret_cast<const unsigned*>(ws + pl.off_need), pl.nslab, pl.rows_per_slab,
+                             psig, pmu, pnk, dense ? 1 : 0);
+        }
+        return hipSuccess;
+      };
+      hipError_t e = launch(std::integral_constant<int, 0>{});
+      if (e == hipSuccess) e = launch(std::integral_constant<int, 1>{});
+      if (e == hipSuccess) e = launch(std::integral_constant<int, 2>{});
+      if (e == hipSuccess) e = launch(std::integral_constant<int, 3>{});
       if (e != hipSuccess) return e;
-      hipLaunchKernelGGL((full_accum_gather<DP>), dim3((unsigned)gather_grid(pl.nslab, (int)pl.K)),
-                         dim3(64 * kGatherWaves), lds2, stream, X, ldx, pl.N, (int)pl.D,
-                         reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
-                         reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, rowstat,
-                         reinterpret_cast<const unsigned*>(ws + pl.off_need), pl.nslab, pl.rows_per_slab, psig,
-                         pmu, pnk, dense ? 1 : 0);
       return hipGetLastError();
     }
   }
-  constexpr size_t lds2 = accum_lds_bytes<DP>();
-  hipError_t e = set_lds(reinterpret_cast<const void*>(&full_accum<DP>), lds2);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((full_accum<DP>), grid2, dim3(kAccThreads), lds2, stream, X, ldx, pl.N, (int)pl.D,
-                     (int)pl.K, pl.KP, rowstat, pl.nslab, pl.rows_per_slab, psig, pmu, pnk, dense ? 1 : 0, lj);
-  return hipGetLastError();
+  if constexpr (DP > 128) {
+    return hipErrorInvalidValue;   // the stored plan runs up to D = 128 only
+  } else {
+    constexpr size_t lds2 = accum_lds_bytes<DP>();
+    hipError_t e = set_lds(reinterpret_cast<const void*>(&full_accum<DP>), lds2);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((full_accum<DP>), grid2, dim3(kAccThreads), lds2, stream, X, ldx, pl.N, (int)pl.D,
+                       (int)pl.K, pl.KP, rowstat, pl.nslab, pl.rows_per_slab, psig, pmu, pnk, dense ? 1 : 0, lj);
+    return hipGetLastError();
+  }
 }
 
 // ===========================================================================
@@ -1429,9 +1470,9 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   if (K > 0 && (mu == nullptr || ldmu < D || prec_chol == nullptr || log_pi == nullptr ||
                 Nk == nullptr || mu_acc == nullptr || sig_outer == nullptr))
     return FGMM_ERR_INVALID_ARG;
-  if (D > 128) return FGMM_ERR_UNSUPPORTED;
   if (N > kMaxRows || K > (int64_t)1 << 20) return FGMM_ERR_UNSUPPORTED;
   const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
+  if (D > (bf16 ? 128 : 256)) return FGMM_ERR_UNSUPPORTED;
   if (bf16 && K > 0 && N > full_bf16_chunk_rows(K)) {
     // The bf16 contract stores the log-joint, at most kMaxLjBytes per call: larger N
     // runs as consecutive row chunks on one workspace, each chunk after the first
@@ -1474,8 +1515,11 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   if (N > 0) {
     auto run = [&](auto dp_tag) -> hipError_t {
       constexpr int DP = decltype(dp_tag)::value;
-      return bf16 ? launch_bf16<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream)
-                  : launch_passes<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
+      if constexpr (DP <= 128)
+        return bf16 ? launch_bf16<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream)
+                    : launch_passes<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
+      else
+        return launch_passes<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
     };
     hipError_t e = hipSuccess;
     switch (pl.DP) {
@@ -1483,6 +1527,10 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
       case 64: e = run(std::integral_constant<int, 64>{}); break;
       case 96: e = run(std::integral_constant<int, 96>{}); break;
       case 128: e = run(std::integral_constant<int, 128>{}); break;
+      case 160: e = run(std::integral_constant<int, 160>{}); break;
+      case 192: e = run(std::integral_constant<int, 192>{}); break;
+      case 224: e = run(std::integral_constant<int, 224>{}); break;
+      case 256: e = run(std::integral_constant<int, 256>{}); break;
       default: return FGMM_ERR_UNSUPPORTED;
     }
     if (e != hipSuccess) return FGMM_ERR_HIP;

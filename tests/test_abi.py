@@ -150,26 +150,29 @@ def _call_diag(D, flags=0):
                                  FAKE, 1 << 40, flags, None)
 
 
-def _call_full(D):
+def _call_full(D, flags=0):
     L = _lib.lib()
     ld = (D + 3) // 4 * 4
     return L.fgmm_full_estep_f32(FAKE, ld, 10, D, FAKE, D, 4, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
-                                 FAKE, 1 << 40, 0, None)
+                                 FAKE, 1 << 40, flags, None)
 
 
 @no_gpu
 def test_dimension_limits():
     """Largest supported D per covariance model; one past it is UNSUPPORTED.  The
-    isotropic and diagonal fp32 E-steps take any D; their bf16 contracts stop at 256."""
+    isotropic and diagonal fp32 E-steps take any D, their bf16 contracts stop at 256;
+    the full-covariance E-step stops at 256, its bf16 contract at 128."""
     assert _call_iso(D=257, ldx=260, ldmu=257, flags=_lib.FLAG_BF16) == _lib.FGMM_ERR_UNSUPPORTED
     assert _call_diag(257, flags=_lib.FLAG_BF16) == _lib.FGMM_ERR_UNSUPPORTED
-    assert _call_full(129) == _lib.FGMM_ERR_UNSUPPORTED
+    assert _call_full(257) == _lib.FGMM_ERR_UNSUPPORTED
+    assert _call_full(129, flags=_lib.FLAG_BF16) == _lib.FGMM_ERR_UNSUPPORTED
     # workspace queries accept the supported range
     L = _lib.lib()
     assert L.fgmm_iso_workspace_bytes(100, 10, 4000) > L.fgmm_iso_workspace_bytes(100, 10, 300) > 0
     assert L.fgmm_diag_workspace_bytes(100, 10, 1000) > L.fgmm_diag_workspace_bytes(100, 10, 256) > \
         L.fgmm_diag_workspace_bytes(100, 10, 128) > 0
-    assert L.fgmm_full_workspace_bytes(100, 10, 128) > L.fgmm_full_workspace_bytes(100, 10, 64) > 0
+    assert L.fgmm_full_workspace_bytes(100, 10, 256) > L.fgmm_full_workspace_bytes(100, 10, 128) > \
+        L.fgmm_full_workspace_bytes(100, 10, 64) > 0
 
 
 def test_python_layer_rejects_cpu_tensors():
