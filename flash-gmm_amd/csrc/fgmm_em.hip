@@ -293,7 +293,7 @@ extern "C" int fgmm_stream_em_iso(const fgmm_em_config* cfg, fgmm_row_source_fn 
   if (!cfg || !src || !mu || !log_sigma_sq || !log_pi) return FGMM_ERR_INVALID_ARG;
   const int64_t N = cfg->N, K = cfg->K, D = cfg->D, R = cfg->chunk_rows;
   const int iters = cfg->iterations;
-  if (N < 1 || K < 1 || D < 1 || D > 256 || R < 1 || iters < 0 || !(cfg->var_floor >= 0.0))
+  if (N < 1 || K < 1 || D < 1 || R < 1 || iters < 0 || !(cfg->var_floor >= 0.0))
     return FGMM_ERR_INVALID_ARG;
   fgmm_em_report rep{};
   const int64_t ld = round_up(D, 4);

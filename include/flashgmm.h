@@ -34,7 +34,7 @@ extern "C" {
 enum fgmm_status {
     FGMM_OK = 0,
     FGMM_ERR_INVALID_ARG = -1, /* bad shape, stride, alignment or null pointer */
-    FGMM_ERR_UNSUPPORTED = -2, /* shape outside the compiled range (e.g. D > 256) */
+    FGMM_ERR_UNSUPPORTED = -2, /* shape outside the supported range (e.g. full D > 256) */
     FGMM_ERR_WORKSPACE = -3,   /* workspace smaller than *_workspace_bytes() */
     FGMM_ERR_HIP = -4,         /* a HIP runtime call or kernel launch failed */
     FGMM_ERR_SOURCE = -5,      /* a host row source returned an error */
@@ -96,7 +96,8 @@ enum fgmm_flags {
      * FGMM_FLAG_RECOMPUTE and STORE_LOGJOINT have no effect with it. */
     FGMM_FLAG_BF16 = 1u << 7,
     /* Opt-in: pass 1 also stores the fp32 log-joint (N/32 x K/32 tiles of
-     * 4 KiB, when that is at most 16 GiB, D > 32 and K > 96) in the workspace,
+     * 4 KiB, when that is at most 16 GiB, 32 < D <= 256 (full: D <= 128) and
+     * K > 96) in the workspace,
      * and pass 2 reads it back instead of recomputing the D-contraction.  The
      * workspace is then O(N*K) (4.3 GB at N=1M, K=1024): size it with
      * *_workspace_bytes_ex(..., flags).  Calls that split the phases must agree
@@ -120,7 +121,8 @@ const char *fgmm_strerror(int status);
 /*   Nk_k    = sum_n r_nk,  r_nk = exp(ll_nk - logZ_n)                        */
 /*   mu_acc  = sum_n r_nk x_n                                                 */
 /*   sig_acc = sum_n r_nk ||x_n - mu_k||^2                                    */
-/* log_sigma_sq and log_pi are contiguous (K).                                */
+/* log_sigma_sq and log_pi are contiguous (K).  Any D >= 1 (the bf16         */
+/* contract: D <= 256).                                                       */
 /* ------------------------------------------------------------------------ */
 size_t fgmm_iso_workspace_bytes(int64_t N, int64_t K, int64_t D);
 /* Workspace for a call made with `flags` (FGMM_FLAG_STORE_LOGJOINT, RECOMPUTE
@@ -165,7 +167,7 @@ int fgmm_iso_estep_f32_noalloc(const float *X, int64_t ldx, int64_t N, int64_t D
 /*   ll_nk      = log_pi_k - 0.5*(D log(2 pi) + sum_d lss_kd)                 */
 /*                - 0.5 * sum_d (x_nd - mu_kd)^2 exp(-lss_kd)                 */
 /*   sig_acc_kd = sum_n r_nk (x_nd - mu_kd)^2                                 */
-/* Supports 1 <= D <= 256.                                                    */
+/* Any D >= 1 (the bf16 contract: D <= 256).                                  */
 /* ------------------------------------------------------------------------ */
 size_t fgmm_diag_workspace_bytes(int64_t N, int64_t K, int64_t D);
 size_t fgmm_diag_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags);
@@ -185,7 +187,8 @@ int fgmm_diag_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
 /*   ll_nk = log_pi_k + sum_d log(|L_k,dd| + 1e-30) - 0.5 D log(2 pi)         */
 /*           - 0.5 ||L_k^T (x_n - mu_k)||^2                                   */
 /*   sig_outer_k = sum_n r_nk x_n x_n^T   (uncentred second moment)           */
-/* Supports 1 <= D <= 128.                                                    */
+/* Supports 1 <= D <= 256 (the bf16 contract and the stored log-joint:        */
+/* D <= 128).                                                                 */
 /* ------------------------------------------------------------------------ */
 size_t fgmm_full_workspace_bytes(int64_t N, int64_t K, int64_t D);
 size_t fgmm_full_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags);
@@ -309,7 +312,7 @@ int fgmm_full_mstep_f32(const float *Nk, const float *mu_acc, const float *sig_o
 #define FGMM_EM_MAX_REPORTED_ITERS 16
 
 typedef struct fgmm_em_config {
-    int64_t N, K, D;         /* rows, components, dimensions (D <= 256) */
+    int64_t N, K, D;         /* rows, components, dimensions (any D >= 1) */
     int64_t chunk_rows;      /* rows per host chunk */
     int iterations;          /* EM iterations */
     double var_floor;        /* lower bound on sigma^2 in the M-step */

@@ -111,3 +111,38 @@ def test_stream_em_from_an_fvecs_file(tmp_path, gpu_device):
     torch.testing.assert_close(mu, mu_m, rtol=1e-4, atol=1e-4)
     torch.testing.assert_close(lss, lss_m, rtol=0, atol=1e-4)
     np.testing.assert_allclose(rep["loglik"], ll_m, rtol=1e-6)
+
+
+@pytest.mark.gpu
+def test_stream_em_gist_width_file_against_the_oracle(tmp_path, gpu_device):
+    """A GIST-width .fvecs file (D = 960, where pass 1 tiles over components) streamed
+    through the EM driver in three chunks, one iteration: the parameters it applies and
+    the log-likelihood it reports against the float64 oracle's E-step over the file's
+    rows followed by the README M-step (README.md:59-61)."""
+    import sys
+    from flash_gmm import stream_em_iso
+    from oracle import gmm_oracle as O
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from parity import logz_atol_for
+    g = torch.Generator().manual_seed(11)
+    K, D, N = 64, 960, 30000
+    centres = torch.randn(K, D, generator=g) * 0.5
+    X = centres[torch.randint(0, K, (N,), generator=g)] + torch.randn(N, D, generator=g)
+    path = str(tmp_path / "gist_like.fvecs")
+    datasets.write_vecs(path, X.numpy())
+    mu0 = centres + 0.1 * torch.randn(K, D, generator=g)
+    lss0 = torch.zeros(K)
+    lpi0 = torch.full((K,), -float(np.log(K)))
+    dev = gpu_device
+    mu, lss, lpi = mu0.to(dev), lss0.to(dev), lpi0.to(dev)
+    with datasets.VecsFile(path) as f:
+        rep = stream_em_iso(f, N, mu, lss, lpi, iterations=1, chunk_rows=12000)
+    torch.cuda.synchronize()
+    logZ, Nk, mu_acc, sig = O.estep_iso(X, mu0, lss0, lpi0)
+    assert float(Nk.min()) > 100          # every component is populated
+    pi, m, s2 = O.mstep_iso(Nk, mu_acc, sig, N, D)
+    scale = float(m.abs().max())
+    assert float((mu.double().cpu() - m).abs().max()) <= 2e-4 * scale
+    assert float((lss.double().cpu() - torch.log(s2)).abs().max()) <= 3e-4
+    assert float((lpi.double().cpu() - torch.log(pi)).abs().max()) <= 2e-4
+    assert abs(rep["loglik"][0] - float(logZ.sum())) <= logz_atol_for(D) * N
