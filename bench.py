@@ -45,6 +45,11 @@ WORKLOADS = {
     "full_n250k_k256_d64": (250_000, 256, 64),
     "diag_n1m_k256_d256": (1_000_000, 256, 256),
     "full_n100k_k64_d128": (100_000, 64, 128),
+    # widths above 128 (component-tiled pass 1, dimension-range pass 2; full up to 256)
+    "iso_n1m_k1024_d256": (1_000_000, 1024, 256),
+    "iso_n1m_k1024_d960": (1_000_000, 1024, 960),
+    "diag_n1m_k1024_d960": (1_000_000, 1024, 960),
+    "full_n100k_k64_d256": (100_000, 64, 256),
 }
 
 # HBM bytes per launch of the dominant kernel: rocprofv3 --pmc FETCH_SIZE and
@@ -112,25 +117,18 @@ def pass1_executed(kind, N, K, D, precision, stored):
 
     Split-bf16 ("bf16x6") passes form each fp32 product from 7 bf16 matrix steps
     (6 products of the three-way splits + 1 centring offset) per chunk, each step
-    32 bf16 flop per (row, output):
-      iso D <= 128:   16-dimension chunks, 1 output:   14 DP bf16 flop per (row, component)
-      diag D <= 128:  8-dimension chunks of [x^2, x]:  28 DP
-      full D <= 128:  16-dimension chunks, DP outputs: 14 DP^2
-    Wider iso / diag run fp32 32x32x2 steps over the padded width (2 DP, 4 DP).  The
-    bf16 contract runs one bf16 step per product (2 DP, 4 DP, 2 DP^2 bf16 flop).
+    32 bf16 flop per (row, output), at every width:
+      iso:   16-dimension chunks, 1 output:   14 DP bf16 flop per (row, component)
+      diag:  8-dimension chunks of [x^2, x]:  28 DP
+      full:  16-dimension chunks, DP outputs: 14 DP^2
+    The bf16 contract runs one bf16 step per product (2 DP, 4 DP, 2 DP^2 bf16 flop).
     """
     DP = padded_dim(kind, D)
     if precision == "bf16":
         per = {"iso": 2 * DP, "diag": 4 * DP, "full": 2 * DP * DP}[kind]
         return per * float(N) * K, "bf16", PEAK_BF16_MFMA_TFLOPS
-    if kind == "iso" and D <= 128:
-        return 14.0 * DP * N * K, "bf16", PEAK_BF16_MFMA_TFLOPS
-    if kind == "diag" and D <= 128:
-        return 28.0 * DP * N * K, "bf16", PEAK_BF16_MFMA_TFLOPS
-    if kind == "full" and D <= 128:
-        return 14.0 * DP * DP * N * K, "bf16", PEAK_BF16_MFMA_TFLOPS
-    per = {"iso": 2 * DP, "diag": 4 * DP, "full": 2 * DP * DP}[kind]
-    return per * float(N) * K, "fp32", PEAK_FP32_MFMA_TFLOPS
+    per = {"iso": 14 * DP, "diag": 28 * DP, "full": 14 * DP * DP}[kind]
+    return per * float(N) * K, "bf16", PEAK_BF16_MFMA_TFLOPS
 
 
 def iso_need_pairs(inp, logZ, chunk=65536):
@@ -261,11 +259,13 @@ def time_steps(call, steps, warmup, stream, dense=False):
 KERNELS = {
     # (kind, plan) -> (pass-1 kernel, pass-2 kernel)
     ("iso", "default"): ("iso_lse (need masks)", "iso_accum_gather"),
-    ("iso", "default_wide"): ("iso_lse_split", "iso_accum_split"),
+    ("iso", "default_wide"): ("iso_lse_ctile (need masks)", "iso_accum_drange"),
     ("iso", "stored"): ("iso_lse (stores the log-joint)", "iso_accum_sparse / iso_accum_lj"),
+    ("iso", "stored_wide"): ("iso_lse_ctile (stores the log-joint)", "iso_accum_lj"),
     ("diag", "default"): ("diag_lse_x6 (need masks)", "diag_accum_gather"),
-    ("diag", "default_wide"): ("diag_lse_split", "diag_accum_split"),
+    ("diag", "default_wide"): ("diag_lse_ctile (need masks)", "diag_accum_drange"),
     ("diag", "stored"): ("diag_lse_x6 (stores the log-joint)", "diag_accum_sparse / diag_accum_lj2"),
+    ("diag", "stored_wide"): ("diag_lse_ctile (stores the log-joint)", "diag_accum_lj"),
     ("full", "default"): ("full_lse_x6 (need masks)", "full_accum_gather"),
     ("full", "stored"): ("full_lse_x6 (stores the log-joint)", "full_accum"),
 }
@@ -274,7 +274,10 @@ KERNELS = {
 def kernel_names(kind, D, precision, stored):
     if precision == "bf16":
         return f"{kind}_bf16_lse", f"{kind}_bf16_accum"
-    plan = "stored" if stored else ("default" if (kind == "full" or D <= 128) else "default_wide")
+    wide = kind != "full" and D > 128
+    if stored and (D > 256 or (kind == "full" and D > 128)):
+        stored = False          # the stored plan's widths; above them the call runs the default plan
+    plan = ("stored" if stored else "default") + ("_wide" if wide else "")
     return KERNELS[(kind, plan)]
 
 

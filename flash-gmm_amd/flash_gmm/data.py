@@ -152,6 +152,11 @@ WORKLOADS = {
     # wider shapes (split-dimension accumulation paths)
     "diag_n1m_k256_d256": (diag_clustered, dict(N=1_000_000, K=256, D=256), 5),
     "full_n100k_k64_d128": (full_clustered, dict(N=100_000, K=64, D=128), 6),
+    # widths above 128 (GIST-960 and the full model's widest)
+    "iso_n1m_k1024_d256": (iso_clustered, dict(N=1_000_000, K=1024, D=256), 1),
+    "iso_n1m_k1024_d960": (iso_clustered, dict(N=1_000_000, K=1024, D=960), 1),
+    "diag_n1m_k1024_d960": (diag_clustered, dict(N=1_000_000, K=1024, D=960), 2),
+    "full_n100k_k64_d256": (full_clustered, dict(N=100_000, K=64, D=256), 6),
 }
 
 
