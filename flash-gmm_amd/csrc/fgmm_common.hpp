@@ -59,95 +59,10 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 // The fp32 matrix cores add the products of a 32x32x2 (or 16x16x4) step to the
 // accumulator one at a time, rounding after each, so a single chain over D=128
-// carries ~1e-4 absolute error in the cross term of clustered data.  Two forms:
-//
-// cross_tile():      accurate.  Every 8 dimensions (one operand chunk, 4 MFMA
-//                    steps) start from a zero accumulator; two chunk sums are
-//                    added in fp32 and the pair is accumulated in fp64.  Used
-//                    where logZ is formed.
-// cross_tile_fast(): four interleaved fp32 chains over D/4 each, summed in fp32.
-//                    Used for the responsibilities, whose errors average out in
-//                    the accumulated statistics.
-//
-// loadA(m) / loadB(m) return this lane's operand chunk m: four consecutive values
-// of its dimension slice 8m + 4*(lane/32) .. +3.  On gfx950 VALU and MFMA work of a
-// SIMD do not overlap, so every VALU instruction here is paid in matrix time.
-__device__ __forceinline__ f32x16 mfma_chunk(const f32x4 a, const f32x4 b, f32x16 c) {
-  c = mfma32(a[0], b[0], c);
-  c = mfma32(a[1], b[1], c);
-  c = mfma32(a[2], b[2], c);
-  return mfma32(a[3], b[3], c);
-}
-
-template <int NM, typename LA, typename LB>
-__device__ __forceinline__ void cross_tile(double (&out)[16], LA loadA, LB loadB) {
-  static_assert(NM % 2 == 0, "chunks are processed in pairs");
-  constexpr int NP = NM / 2;
-  f32x4 a0 = loadA(0), b0 = loadB(0), a1 = loadA(1), b1 = loadB(1);
-  f32x16 cA = mfma_chunk(a0, b0, zero16());
-  f32x16 cB = mfma_chunk(a1, b1, zero16());
-  f32x16 s;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) s[i] = cA[i] + cB[i];
-  if (NP > 1) {
-    a0 = loadA(2); b0 = loadB(2); a1 = loadA(3); b1 = loadB(3);
-  }
-#pragma unroll
-  for (int p = 1; p < NP; ++p) {
-    cA = mfma_chunk(a0, b0, zero16());
-    cB = mfma_chunk(a1, b1, zero16());
-    if (p + 1 < NP) {
-      a0 = loadA(2 * p + 2); b0 = loadB(2 * p + 2);
-      a1 = loadA(2 * p + 3); b1 = loadB(2 * p + 3);
-    }
-    if (p == 1) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) out[i] = (double)s[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) out[i] += (double)s[i];
-    }
-    // Materialise the fp64 sums here: without this, IR-level sinking moves every
-    // flush down to the first use of out[] and keeps all chunk results live.
-#pragma unroll
-    for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(out[i]));
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = cA[i] + cB[i];
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  if (NP == 1) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) out[i] = (double)s[i];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) out[i] += (double)s[i];
-  }
-}
-
-template <int NM, typename LA, typename LB>
-__device__ __forceinline__ void cross_tile_fast(float (&out)[16], LA loadA, LB loadB) {
-  static_assert(NM % 4 == 0, "four chains over equal D slices");
-  constexpr int Q = NM / 4;
-  f32x16 c0 = zero16(), c1 = zero16(), c2 = zero16(), c3 = zero16();
-#pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    const f32x4 a0 = loadA(q), b0 = loadB(q);
-    const f32x4 a1 = loadA(Q + q), b1 = loadB(Q + q);
-    const f32x4 a2 = loadA(2 * Q + q), b2 = loadB(2 * Q + q);
-    const f32x4 a3 = loadA(3 * Q + q), b3 = loadB(3 * Q + q);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      c0 = mfma32(a0[j], b0[j], c0);
-      c1 = mfma32(a1[j], b1[j], c1);
-      c2 = mfma32(a2[j], b2[j], c2);
-      c3 = mfma32(a3[j], b3[j], c3);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) out[i] = (c0[i] + c1[i]) + (c2[i] + c3[i]);
-  __builtin_amdgcn_sched_barrier(0);
-}
+// carries ~1e-4 absolute error in the cross term of clustered data; the log-joints
+// are formed by the centred split-bf16 contraction below instead.  On gfx950 VALU
+// and MFMA work of a SIMD do not overlap, so every VALU instruction in a
+// contraction is paid in matrix time.
 
 // ---------------------------------------------------------------------------
 // bf16 matrix steps (the bf16 operand contracts of the reference's H100 kernels).
