@@ -1993,14 +1993,13 @@ __host__ __device__ constexpr int bf16_chains(int DP) { return DP > 128 ? 4 : 2;
 // Waves per component block in pass 2 (each owns NCH / NH chains and the matching
 // feature columns of r^T [x^2 | x]).
 __host__ __device__ constexpr int bf16_parts(int DP) { return DP <= 64 ? 1 : bf16_chains(DP); }
-// X super-tile buffers in pass 2's LDS: two, or one where two do not fit (D = 256).
-__host__ __device__ constexpr int bf16_xbufs(int DP) { return DP > 192 ? 1 : 2; }
-__host__ __device__ constexpr int bf16_xr_stride(int DP) { return 2 * DP + 8; }   // bf16 per row
+// bf16 per row of the feature tile: an odd multiple of 32 bytes, the stride the
+// transposing reads (lds_rows_operand) want.
+__host__ __device__ constexpr int bf16_xr_stride(int DP) { return 2 * DP + 16; }
 
 __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB) {
-  return (size_t)bf16_xbufs(DP) * (size_t)(256 / (CB * bf16_parts(DP))) *
-             ((size_t)bf16_xr_stride(DP) + 2 * DP) * 2 +
-         (size_t)bf16_xbufs(DP) * (256 / (CB * bf16_parts(DP))) * sizeof(float) +
+  return (size_t)2 * (size_t)(256 / (CB * bf16_parts(DP))) * (size_t)bf16_xr_stride(DP) * 2 +
+         (size_t)2 * (256 / (CB * bf16_parts(DP))) * sizeof(float) +
          (bf16_parts(DP) > 1 ? (size_t)kAccWaves * 16 * 64 * sizeof(float) : 0);
 }
 // Component blocks per pass-2 workgroup: as many as 8 waves hold (4, or 2 with four
@@ -2179,10 +2178,11 @@ __global__ __launch_bounds__(kThreads) void diag_bf16_lse(const float* __restric
 // chains [h NCH/NH, (h+1) NCH/NH), recomputes their partial S = F W^T for its 32
 // rows, and with NH > 1 the parts meet in LDS and every part forms the same log-joint
 // in the shared order.  Each part then accumulates r^T F over its own feature columns
-// (x^2 columns into part_sq, x columns into part_mu).  X super-tiles are rounded once
-// per workgroup into LDS in two layouts: features row-major (the A operand of S;
-// x^2 then x) and row-octet interleaved, feature (r, f) at ((r/8) F + f) 8 + r%8 (the
-// B operand of r^T F: 8 consecutive rows of one feature are 16 contiguous bytes).
+// (x^2 columns into part_sq, x columns into part_mu).  X super-tiles are loaded
+// coalesced, squared and rounded once per workgroup into a double-buffered row-major
+// feature tile in LDS (x^2 then x): the A operand of S is a 16-byte read per lane, and
+// the B operand of r^T F (8 consecutive rows of one feature per lane-half) comes from
+// two transposing reads (lds_rows_operand).
 template <int DP, int CB, int NH = bf16_parts(DP)>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
@@ -2200,7 +2200,6 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   constexpr int RG = kAccWaves / (CB * NH);    // row groups (32 rows each)
   constexpr int TR = 32 * RG;                  // rows per super-tile
   constexpr int XR = bf16_xr_stride(DP);
-  constexpr int NB = bf16_xbufs(DP);
   constexpr int V4 = DP / 4;
   constexpr int NV = TR * V4;                  // float4 per super-tile
   constexpr int LPT = (NV + kAccThreads - 1) / kAccThreads;
@@ -2209,10 +2208,9 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                 "even split");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  __bf16* xr = reinterpret_cast<__bf16*>(lds_raw);                        // [NB][TR][XR]
-  __bf16* xi = xr + NB * TR * XR;                                          // [NB][TR/8][F][8]
-  float* rs = reinterpret_cast<float*>(xi + NB * TR * F);                  // [NB][TR]
-  float* ex = rs + NB * TR;                                                // [8][16][64] (NH > 1)
+  __bf16* xr = reinterpret_cast<__bf16*>(lds_raw);                        // [2][TR][XR]
+  float* rs = reinterpret_cast<float*>(xr + 2 * TR * XR);                  // [2][TR]
+  float* ex = rs + 2 * TR;                                                 // [8][16][64] (NH > 1)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
@@ -2252,10 +2250,9 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   f32x4 stage[LPT];
   float rstage = INFINITY;
   const bool full_d = (D == DP);
-  // float4 idx of a super-tile <-> (row, 4 dimensions) with the row's low 3 bits
-  // fastest: 8 lanes cover one 16-byte column piece of 8 rows.
-  auto tile_row = [](int idx) { return ((idx >> 3) / V4) * 8 + (idx & 7); };
-  auto tile_col = [](int idx) { return ((idx >> 3) % V4) * 4; };
+  // float4 idx of a super-tile <-> (row, 4 dimensions), row-major.
+  auto tile_row = [](int idx) { return idx / V4; };
+  auto tile_col = [](int idx) { return (idx % V4) * 4; };
   auto fetch = [&](int t) {
     const int64_t row0 = r_begin + (int64_t)t * TR;
     if (full_d && row0 + TR <= r_end) {
@@ -2283,7 +2280,6 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   };
   auto commit = [&](int buf) {
     __bf16* dr = xr + buf * TR * XR;
-    __bf16* di = xi + buf * TR * F;
     typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int q = 0; q < LPT; ++q) {
@@ -2296,10 +2292,6 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       const bf16x4 b2 = {(__bf16)v2.x, (__bf16)v2.y, (__bf16)v2.z, (__bf16)v2.w};
       *reinterpret_cast<bf16x4*>(dr + r * XR + d) = b2;
       *reinterpret_cast<bf16x4*>(dr + r * XR + DP + d) = b;
-      __bf16* o = di + ((r >> 3) * F + d) * 8 + (r & 7);
-      o[0] = b2[0]; o[8] = b2[1]; o[16] = b2[2]; o[24] = b2[3];
-      o += DP * 8;
-      o[0] = b[0]; o[8] = b[1]; o[16] = b[2]; o[24] = b[3];
     }
     if (tid < TR) rs[buf * TR + tid] = rstage;
   };
@@ -2311,7 +2303,7 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   lds_barrier();
 
   for (int t = 0; t < ntiles; ++t) {
-    const int buf = NB == 2 ? (t & 1) : 0;
+    const int buf = t & 1;
     const bool more = t + 1 < ntiles;
     if (more) fetch(t + 1);
     // This wave's chain partials of S = F W^T for its 32 rows: lane = component,
@@ -2368,21 +2360,18 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       bf16x8 a[2];
       acc_to_row_operands(r, a);
       // B operand: rows rg*32 + 16p + 8g + e of feature f0 + 32j + c.
-      const __bf16* xcol = xi + buf * TR * F + ((rg * 4 + g) * F + f0 + c) * 8;
+      const __bf16* xt = xr + buf * TR * XR;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         // A step whose 16 rows x 32 components of bf16(r) are all zero adds nothing.
         if (dense || any_nonzero(a[p])) {
 #pragma unroll
           for (int j = 0; j < NJ; ++j)
-            acc[j] = mfma_bf16(a[p], *reinterpret_cast<const bf16x8*>(xcol + (2 * p * F + 32 * j) * 8), acc[j]);
+            acc[j] = mfma_bf16(a[p], lds_rows_operand(xt, XR, rg * 32 + 16 * p, f0 + 32 * j, lane), acc[j]);
         }
       }
     }
-    if (more) {
-      if constexpr (NB == 1) lds_barrier();   // every wave is done with the buffer
-      commit(NB == 2 ? (buf ^ 1) : 0);
-    }
+    if (more) commit(buf ^ 1);
     lds_barrier();
   }
 

@@ -1163,18 +1163,25 @@ __global__ __launch_bounds__(kThreads) void full_bf16_lse(const float* __restric
 __host__ __device__ constexpr int bf16_comps_per_wg(int NMB) { return NMB <= 2 ? 4 : 2; }
 __host__ __device__ constexpr int bf16_row_groups(int NMB) { return NMB == 1 ? 2 : 1; }
 
+// Row strides of pass 2's X tiles: fp32 DP + 4 words (rows r and r + 8 of one column,
+// which one A-operand read takes for the two half-waves, fall 32 banks apart), bf16
+// DP + 16 (an odd multiple of 32 bytes, for the transposing B-operand reads).
+__host__ __device__ constexpr int bf16_xf_stride(int DP) { return DP + 4; }
+__host__ __device__ constexpr int bf16_xh_stride(int DP) { return DP + 16; }
+
 template <int DP>
 constexpr size_t bf16_accum_lds_bytes() {
   constexpr int NMB = DP / 32;
   constexpr int TR = 32 * bf16_row_groups(NMB);
-  return (size_t)2 * TR * DP * sizeof(float)      // X tiles, fp32, row-octet interleaved
-         + (size_t)2 * TR * DP * 2                // X tiles, bf16, row-octet interleaved
-         + (size_t)2 * TR * sizeof(float)         // logZ2
-         + (size_t)kAccWaves * 32 * sizeof(float); // r per wave
+  return (size_t)2 * TR * bf16_xf_stride(DP) * sizeof(float)   // X tiles, fp32, row-major
+         + (size_t)2 * TR * bf16_xh_stride(DP) * 2             // X tiles, bf16, row-major
+         + (size_t)2 * TR * sizeof(float)                      // logZ2
+         + (size_t)kAccWaves * 32 * sizeof(float);             // r per wave
 }
 
-// X tile element (r, d) of the interleaved layouts sits at ((r / 8) DP + d) 8 + r % 8:
-// the 8 consecutive rows of one column that an operand lane-half needs are contiguous.
+// The X tiles are loaded coalesced and held row-major in LDS, in fp32 (for r x, which
+// the contract forms in fp32 before rounding) and in bf16 (the B operands, two
+// transposing reads each, lds_rows_operand).
 template <int DP>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void full_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int K, int KP,
@@ -1190,10 +1197,11 @@ void full_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   constexpr int LPT = (NV + kAccThreads - 1) / kAccThreads;
   static_assert(CPWG * NMB * RG <= kAccWaves, "waves cover the work");
 
+  constexpr int XF = bf16_xf_stride(DP), XH = bf16_xh_stride(DP);
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  float* xf = reinterpret_cast<float*>(lds_raw);                           // [2][TR/8][DP][8]
-  __bf16* xh = reinterpret_cast<__bf16*>(xf + 2 * TR * DP);                // [2][TR/8][DP][8]
-  float* rs = reinterpret_cast<float*>(xh + 2 * TR * DP);                  // [2][TR]
+  float* xf = reinterpret_cast<float*>(lds_raw);                           // [2][TR][XF]
+  __bf16* xh = reinterpret_cast<__bf16*>(xf + 2 * TR * XF);                // [2][TR][XH]
+  float* rs = reinterpret_cast<float*>(xh + 2 * TR * XH);                  // [2][TR]
   float* r_l = rs + 2 * TR;                                                // [8][32]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1222,8 +1230,8 @@ void full_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   f32x4 stage[LPT];
   float rstage = INFINITY;
   const bool full_d = (D == DP);
-  auto tile_row = [](int idx) { return ((idx >> 3) / V4) * 8 + (idx & 7); };
-  auto tile_col = [](int idx) { return ((idx >> 3) % V4) * 4; };
+  auto tile_row = [](int idx) { return idx / V4; };
+  auto tile_col = [](int idx) { return (idx % V4) * 4; };
   auto fetch = [&](int t) {
     const int64_t row0 = r_begin + (int64_t)t * TR;
     if (full_d && row0 + TR <= r_end) {
@@ -1249,17 +1257,17 @@ void full_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     }
   };
   auto commit = [&](int buf) {
-    float* df = xf + buf * TR * DP;
-    __bf16* dh = xh + buf * TR * DP;
+    float* df = xf + buf * TR * XF;
+    __bf16* dh = xh + buf * TR * XH;
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int q = 0; q < LPT; ++q) {
       const int idx = q * kAccThreads + tid;
       if (NV % kAccThreads != 0 && idx >= NV) continue;
       const int r = tile_row(idx), d = tile_col(idx);
       const f32x4 v = stage[q];
-      const int o = ((r >> 3) * DP + d) * 8 + (r & 7);
-      df[o] = v.x; df[o + 8] = v.y; df[o + 16] = v.z; df[o + 24] = v.w;
-      dh[o] = (__bf16)v.x; dh[o + 8] = (__bf16)v.y; dh[o + 16] = (__bf16)v.z; dh[o + 24] = (__bf16)v.w;
+      *reinterpret_cast<f32x4*>(df + r * XF + d) = v;
+      *reinterpret_cast<bf16x4*>(dh + r * XH + d) = bf16x4{(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
     }
     if (tid < TR) rs[buf * TR + tid] = rstage;
   };
@@ -1293,21 +1301,22 @@ void full_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     }
     if (more) fetch(t + 1);
     lds_barrier();
-    const float* xa = xf + buf * TR * DP;
-    const __bf16* xb = xh + buf * TR * DP;
+    const float* xa = xf + buf * TR * XF;
+    const __bf16* xb = xh + buf * TR * XH;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      // Rows rg*32 + 16p + 8g + e of this step: row octet rg*4 + 2p + g.
-      const int oct = rg * 4 + 2 * p + g;
+      // Rows rg*32 + 16p + 8g + e of this step.
+      const int r0 = rg * 32 + 16 * p;
       bf16x8 bop[NMB];
 #pragma unroll
-      for (int mb = 0; mb < NMB; ++mb)
-        bop[mb] = in_use ? *reinterpret_cast<const bf16x8*>(xb + (oct * DP + 32 * mb + c) * 8) : bf16x8{};
+      for (int mb = 0; mb < NMB; ++mb) bop[mb] = in_use ? lds_rows_operand(xb, XH, r0, 32 * mb, lane) : bf16x8{};
       if (active) {
         // A = bf16(r x_d2): lane = d2 = 32 mb2 + c, elements = the 8 rows.
         const f32x4* rr = reinterpret_cast<const f32x4*>(r_l + wave * 32 + 16 * p + 8 * g);
-        const f32x4* xx = reinterpret_cast<const f32x4*>(xa + (oct * DP + 32 * mb2 + c) * 8);
-        const bf16x8 a = to_bf16x8(rr[0] * xx[0], rr[1] * xx[1]);
+        const float* xx = xa + (r0 + 8 * g) * XF + 32 * mb2 + c;
+        const f32x4 x0 = {xx[0], xx[XF], xx[2 * XF], xx[3 * XF]};
+        const f32x4 x1 = {xx[4 * XF], xx[5 * XF], xx[6 * XF], xx[7 * XF]};
+        const bf16x8 a = to_bf16x8(rr[0] * x0, rr[1] * x1);
         // A step whose 16 rows x 32 coordinates of bf16(r x) are all zero adds nothing.
         if (dense || any_nonzero(a)) {
 #pragma unroll
@@ -1322,7 +1331,7 @@ void full_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
           a = to_bf16x8(rr[0], rr[1]);
         }
         // B = column block mb2 (mb2 is not a compile-time index: read it again).
-        const bf16x8 bm = *reinterpret_cast<const bf16x8*>(xb + (oct * DP + 32 * mb2 + c) * 8);
+        const bf16x8 bm = lds_rows_operand(xb, XH, r0, 32 * mb2, lane);
         if (dense || any_nonzero(a)) macc = mfma_bf16(a, bm, macc);
       }
     }

@@ -2315,17 +2315,26 @@ __global__ __launch_bounds__(kThreads) void iso_bf16_lse(const float* __restrict
 // Pass 2: grid over (row slab x group of CB component blocks); 8 waves = CB blocks x
 // NH halves of the dimensions x 8/(CB NH) row groups.  With NH = 2 each wave forms the
 // partial S over its half, the halves meet in LDS and are added in a fixed order (both
-// waves then hold the same r), and each accumulates r^T X for its half of the columns.  X super-tiles are rounded to bf16 once per workgroup and held in
-// LDS in two layouts: row-major (the A operand of the recomputed S = X mu^T) and
-// row-octet interleaved, element (r, d) at ((r / 8) DP + d) 8 + r % 8 (the B operand
-// of r^T X: 8 consecutive rows of one column are 16 contiguous bytes).  r leaves S in
-// the accumulator layout (lane = component, register = row 8q + 4g + j); one
-// v_permlane32_swap per register pair gives each half-wave 8 consecutive rows, the
-// A-operand layout of r^T X, with no trip through LDS.
-__host__ __device__ constexpr int bf16_xr_stride(int DP) { return DP + 8; }   // bf16 per X row
+// waves then hold the same r), and each accumulates r^T X for its half of the columns.
+// X super-tiles are loaded coalesced (consecutive lanes, consecutive 16 bytes of a
+// row), rounded to bf16 once per workgroup and held row-major in LDS: the A operand of
+// the recomputed S = X mu^T is a 16-byte read per lane, and the B operand of r^T X (8
+// consecutive rows of one column per lane-half) comes from two transposing reads
+// (lds_rows_operand).  r leaves S in the accumulator layout (lane = component,
+// register = row 8q + 4g + j); one v_permlane32_swap per register pair gives each
+// half-wave 8 consecutive rows, the A-operand layout of r^T X, with no trip through LDS.
+// The row stride (DP + 16 bf16) is an odd multiple of 32 bytes, the stride the
+// transposing reads want.
+__host__ __device__ constexpr int bf16_xr_stride(int DP) { return DP + 16; }   // bf16 per X row
+// Row groups each wave takes per super-tile: two where the halves of D need no
+// exchange, so every barrier and every tile load covers twice the work.
+__host__ __device__ constexpr int bf16_rows_per_wave(int DP) { return bf16_halves(DP) == 1 ? 2 : 1; }
+__host__ __device__ constexpr int bf16_tile_rows(int DP, int CB) {
+  return 32 * (kAccWaves / (CB * bf16_halves(DP))) * bf16_rows_per_wave(DP);
+}
 __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB) {
-  return (size_t)2 * ((size_t)(256 / (CB * bf16_halves(DP))) * (bf16_xr_stride(DP) + DP)) * 2 +
-         (size_t)2 * (256 / (CB * bf16_halves(DP))) * sizeof(float2) +
+  return (size_t)2 * ((size_t)bf16_tile_rows(DP, CB) * bf16_xr_stride(DP)) * 2 +
+         (size_t)2 * bf16_tile_rows(DP, CB) * sizeof(float2) +
          (bf16_halves(DP) > 1 ? (size_t)kAccWaves * 16 * 64 * sizeof(float) : 0);
 }
 __host__ inline int bf16_blocks_per_group(int DP, int KB) {
@@ -2343,8 +2352,9 @@ void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                     float* __restrict__ part_sig, int dense) {
   constexpr int NC = DP / 16 / NH;             // 16-dimension chunks of the contraction per wave
   constexpr int NJ = DP / 32 / NH;             // 32-column tiles of r^T X per wave
-  constexpr int RG = kAccWaves / (CB * NH);    // row groups (32 rows each)
-  constexpr int TR = 32 * RG;                  // rows per super-tile
+  constexpr int RG = kAccWaves / (CB * NH);    // row groups of waves (32 rows each)
+  constexpr int RPW = bf16_rows_per_wave(DP);  // row groups per wave per super-tile
+  constexpr int TR = bf16_tile_rows(DP, CB);   // rows per super-tile, 32 RG RPW
   constexpr int XR = bf16_xr_stride(DP);
   constexpr int V4 = DP / 4;
   constexpr int NV = TR * V4;                  // float4 per super-tile
@@ -2354,8 +2364,7 @@ void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   __bf16* xr = reinterpret_cast<__bf16*>(lds_raw);                        // [2][TR][XR]
-  __bf16* xi = xr + 2 * TR * XR;                                           // [2][TR/8][DP][8]
-  float2* rs = reinterpret_cast<float2*>(xi + 2 * TR * DP);                // [2][TR]
+  float2* rs = reinterpret_cast<float2*>(xr + 2 * TR * XR);                // [2][TR]
   float* ex = reinterpret_cast<float*>(rs + 2 * TR);                       // [8][16][64] (NH = 2)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -2399,11 +2408,9 @@ void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   f32x4 stage[LPT];
   float2 rstage = make_float2(INFINITY, 0.0f);
   const bool full_d = (D == DP);
-  // float4 idx of a super-tile <-> (row, 4 dimensions) with the row's low 3 bits
-  // fastest: 8 lanes cover one 16-byte column piece of 8 rows, so the interleaved
-  // layout is written in contiguous 16-byte runs.
-  auto tile_row = [](int idx) { return ((idx >> 3) / V4) * 8 + (idx & 7); };
-  auto tile_col = [](int idx) { return ((idx >> 3) % V4) * 4; };
+  // float4 idx of a super-tile <-> (row, 4 dimensions), row-major.
+  auto tile_row = [](int idx) { return idx / V4; };
+  auto tile_col = [](int idx) { return (idx % V4) * 4; };
   auto fetch = [&](int t, f32x4 (&stage)[LPT], float2& rstage) {
     const int64_t row0 = r_begin + (int64_t)t * TR;
     if (full_d && row0 + TR <= r_end) {
@@ -2429,17 +2436,13 @@ void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   };
   auto commit = [&](int buf, const f32x4 (&stage)[LPT], float2 rstage) {
     __bf16* dr = xr + buf * TR * XR;
-    __bf16* di = xi + buf * TR * DP;
 #pragma unroll
     for (int q = 0; q < LPT; ++q) {
       const int idx = q * kAccThreads + tid;
-      const int r = tile_row(idx), d = tile_col(idx);
       const f32x4 v = stage[q];
       typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
       const bf16x4 b = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
-      *reinterpret_cast<bf16x4*>(dr + r * XR + d) = b;
-      __bf16* o = di + ((r >> 3) * DP + d) * 8 + (r & 7);
-      o[0] = b[0]; o[8] = b[1]; o[16] = b[2]; o[24] = b[3];
+      *reinterpret_cast<bf16x4*>(dr + tile_row(idx) * XR + tile_col(idx)) = b;
     }
     if (tid < TR) rs[buf * TR + tid] = rstage;
   };
@@ -2454,51 +2457,55 @@ void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const int buf = t & 1;
     const bool more = t + 1 < ntiles;
     if (more) fetch(t + 1, stage, rstage);
-    f32x16 s = zero16();
-    if (active) {
-      const __bf16* xrow = xr + buf * TR * XR + (rg * 32 + c) * XR + d0 + 8 * g;
-      // S = X mu^T for the wave's 32 rows: lane = component, register i = row acc_row(i, g).
+#pragma unroll 1
+    for (int u = 0; u < RPW; ++u) {
+      const int rgu = u * RG + rg;                 // the wave's row group in this super-tile
+      f32x16 s = zero16();
+      if (active) {
+        const __bf16* xrow = xr + buf * TR * XR + (rgu * 32 + c) * XR + d0 + 8 * g;
+        // S = X mu^T for the wave's 32 rows: lane = component, register i = row acc_row(i, g).
 #pragma unroll
-      for (int q = 0; q < NC; ++q)
-        s = mfma_bf16(*reinterpret_cast<const bf16x8*>(xrow + 16 * q), mub[q], s);
-    }
-    if constexpr (NH == 2) {
-      // Add the two halves' partial S in a fixed order (half 0 + half 1).
-      float* mine = ex + wave * 16 * 64 + lane;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mine[i * 64] = s[i];
-      lds_barrier();
-      const float* s0 = ex + (rg * CB * NH + cbw) * 16 * 64 + lane;
-      const float* s1 = s0 + CB * 16 * 64;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] = s0[i * 64] + s1[i * 64];
-    }
-    if (active) {
-      const float2* rt = rs + buf * TR + rg * 32;
-      float r[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float2 z = rt[acc_row(i, g)];                 // {logZ2, ||x_b||^2}
-        const float ll = fmaf(ish2, s[i], fmaf(-ish, z.y, c0));
-        const float rv = fast_exp2(ll - z.x);
-        if (h == 0) {
-          nk += rv;
-          srx = fmaf(rv, z.y, srx);
-          srs = fmaf(rv, s[i], srs);
-        }
-        r[i] = rv;
+        for (int q = 0; q < NC; ++q)
+          s = mfma_bf16(*reinterpret_cast<const bf16x8*>(xrow + 16 * q), mub[q], s);
       }
-      bf16x8 a[2];
-      acc_to_row_operands(r, a);
-      // B operand: rows rg*32 + 16p + 8g + e of column d0 + 32j + c.
-      const __bf16* xcol = xi + buf * TR * DP + ((rg * 4 + g) * DP + d0 + c) * 8;
+      if constexpr (NH == 2) {
+        // Add the two halves' partial S in a fixed order (half 0 + half 1).
+        float* mine = ex + wave * 16 * 64 + lane;
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        // A step whose 16 rows x 32 components of bf16(r) are all zero adds nothing.
-        if (dense || any_nonzero(a[p])) {
+        for (int i = 0; i < 16; ++i) mine[i * 64] = s[i];
+        lds_barrier();
+        const float* s0 = ex + (rg * CB * NH + cbw) * 16 * 64 + lane;
+        const float* s1 = s0 + CB * 16 * 64;
 #pragma unroll
-          for (int j = 0; j < NJ; ++j)
-            acc[j] = mfma_bf16(a[p], *reinterpret_cast<const bf16x8*>(xcol + (2 * p * DP + 32 * j) * 8), acc[j]);
+        for (int i = 0; i < 16; ++i) s[i] = s0[i * 64] + s1[i * 64];
+      }
+      if (active) {
+        const float2* rt = rs + buf * TR + rgu * 32;
+        float r[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float2 z = rt[acc_row(i, g)];                 // {logZ2, ||x_b||^2}
+          const float ll = fmaf(ish2, s[i], fmaf(-ish, z.y, c0));
+          const float rv = fast_exp2(ll - z.x);
+          if (h == 0) {
+            nk += rv;
+            srx = fmaf(rv, z.y, srx);
+            srs = fmaf(rv, s[i], srs);
+          }
+          r[i] = rv;
+        }
+        bf16x8 a[2];
+        acc_to_row_operands(r, a);
+        // B operand: rows rgu*32 + 16p + 8g + e of column d0 + 32j + c.
+        const __bf16* xt = xr + buf * TR * XR;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          // A step whose 16 rows x 32 components of bf16(r) are all zero adds nothing.
+          if (dense || any_nonzero(a[p])) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+              acc[j] = mfma_bf16(a[p], lds_rows_operand(xt, XR, rgu * 32 + 16 * p, d0 + 32 * j, lane), acc[j]);
+          }
         }
       }
     }
