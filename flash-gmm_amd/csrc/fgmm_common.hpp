@@ -40,19 +40,24 @@ __device__ __forceinline__ f32x4 zero4() {
   return z;
 }
 
-// 16-byte load of X[row][d0 .. d0+3] with the columns at or beyond D zeroed.
-// The caller guarantees ldx >= round_up(D, 4), so the whole vector lies inside
-// the row whenever d0 < D.
+// 16-byte load of X[row][d0 .. d0+3] with the columns at or beyond D zeroed (all
+// four when !valid).  The caller guarantees ldx >= round_up(D, 4), ldx % 4 == 0 and
+// d0 % 4 == 0, so the whole vector lies inside the row whenever d0 < D, and N >= 1.
+// No branch: an unused lane loads from row 0 or dimension 0 instead (its address is
+// selected, not skipped), so a sequence of these loads is issued back to back and
+// stays in flight together; a branch per load would make each wait for its data
+// before the next.
 __device__ __forceinline__ f32x4 load_row4(const float* __restrict__ X, int64_t ldx, int64_t row,
                                            int d0, int D, bool valid) {
-  f32x4 v = zero4();
-  if (valid && d0 < D) {
-    v = *reinterpret_cast<const f32x4*>(X + row * ldx + d0);
-    if (d0 + 1 >= D) v.y = 0.0f;
-    if (d0 + 2 >= D) v.z = 0.0f;
-    if (d0 + 3 >= D) v.w = 0.0f;
-  }
-  return v;
+  const bool in = valid && d0 < D;
+  const float* p = X + (valid ? row * ldx : (int64_t)0);
+  const f32x4 v = *reinterpret_cast<const f32x4*>(p + (d0 < D ? d0 : 0));
+  f32x4 r;
+  r.x = in ? v.x : 0.0f;
+  r.y = (in && d0 + 1 < D) ? v.y : 0.0f;
+  r.z = (in && d0 + 2 < D) ? v.z : 0.0f;
+  r.w = (in && d0 + 3 < D) ? v.w : 0.0f;
+  return r;
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

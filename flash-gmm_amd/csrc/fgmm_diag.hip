@@ -1489,7 +1489,8 @@ void diag_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
     const int64_t row = r_begin + (ok ? e : 0);
 #pragma unroll
     for (int q = 0; q < NQ; ++q) raw[q] = load_row4(X, ldx, row, 8 * q + 4 * g, D, ok);
-    rst = ok ? rowstat[row] : INFINITY;
+    const double z = rowstat[row];   // row is a row of the slab even without a queued one: no branch
+    rst = ok ? z : INFINITY;
   };
 
   f32x16 accx[NJ], accq[NJ];
@@ -1670,7 +1671,10 @@ void diag_accum_drange(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   auto start = [&](int e) __attribute__((always_inline)) {
     issue(0, e, xr[0], mr[0]);
     if (nqw > 1) issue(1, e, xr[1], mr[1]);
-    if (wave == 0) rst = e >= 0 ? rowstat[r_begin + e] : INFINITY;
+    if (wave == 0) {
+      const double z = rowstat[r_begin + (e >= 0 ? e : 0)];   // a row of the slab: no branch
+      rst = e >= 0 ? z : INFINITY;
+    }
   };
 
   f32x16 accx[kDrTiles], accq[kDrTiles];

@@ -817,7 +817,8 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
       raw[2 * q] = load_row4(X, ldx, row, 16 * q + 8 * g, D, ok);
       raw[2 * q + 1] = load_row4(X, ldx, row, 16 * q + 8 * g + 4, D, ok);
     }
-    rst = ok ? rowstat[row] : INFINITY;
+    const double z = rowstat[row];   // row is a row of the slab even without a queued one: no branch
+    rst = ok ? z : INFINITY;
   };
 
   f32x16 acc[SB1 - SB0];

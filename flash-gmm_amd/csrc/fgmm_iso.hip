@@ -781,7 +781,7 @@ __device__ __forceinline__ int64_t need_total(const unsigned* __restrict__ count
 //     x = x1 + x2 + x3 split exactly; the dropped terms are below 2^-16 of |r x|),
 //     r as the A operand (acc_to_row_operands) and the tile's rows as the B operand
 //     (lds_rows_operand, the transposing LDS read).
-// The next tile's rows are loaded while a tile is computed.  Workgroups are dealt
+// The rows of the two next tiles are in flight while a tile is computed.  Workgroups are dealt
 // to the 8 XCDs round-robin; the index mapping puts every component block of a
 // slab group on one XCD, so a row of X that several blocks need comes from HBM
 // once and from that XCD's L2 after.
@@ -889,18 +889,37 @@ void iso_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D
     return cnt;
   };
 
-  // Rows of the tile in flight: X in the A-operand layout and the row state.
-  f32x4 raw[2 * NQ];
-  double2 rst;
-  auto issue = [&](int e) {
+  // Rows of the tiles in flight, two deep: X in the A-operand layout and the row
+  // state.  Stage P holds the tile after next while tile P is computed.
+  f32x4 raw[2][2 * NQ];
+  double2 rst[2];
+  // The rows come through resources over the slab: a lane without a row reads zeros
+  // and makes no access, and the loads of a tile issue back to back.  X so while D
+  // fills whole chunks and the slab spans under 2 GiB (uniform), else load_row4.
+  const int64_t slab_bytes = (r_end - r_begin) * ldx * (int64_t)sizeof(float);
+  const bool xbuf = D == DP && slab_bytes <= ((int64_t)1 << 31) - 256;
+  const buf_rsrc xres = make_rsrc(X + r_begin * ldx, xbuf ? (uint32_t)slab_bytes : 0u);
+  const buf_rsrc rres = make_rsrc(rowstat + r_begin, (uint32_t)((r_end - r_begin) * sizeof(double2)));
+  auto issue = [&](int e, f32x4 (&rw)[2 * NQ], double2& rs) __attribute__((always_inline)) {
     const bool ok = e >= 0;
-    const int64_t row = r_begin + (ok ? e : 0);
+    if (xbuf) {
+      const int off = buf_off(ok ? (int)((int64_t)e * ldx * (int64_t)sizeof(float)) + 32 * g : kBufOob);
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      raw[2 * q] = load_row4(X, ldx, row, 16 * q + 8 * g, D, ok);
-      raw[2 * q + 1] = load_row4(X, ldx, row, 16 * q + 8 * g + 4, D, ok);
+      for (int q = 0; q < NQ; ++q) {
+        rw[2 * q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 64 * q, 0));
+        rw[2 * q + 1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 64 * q + 16, 0));
+      }
+    } else {
+      const int64_t row = r_begin + (ok ? e : 0);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        rw[2 * q] = load_row4(X, ldx, row, 16 * q + 8 * g, D, ok);
+        rw[2 * q + 1] = load_row4(X, ldx, row, 16 * q + 8 * g + 4, D, ok);
+      }
     }
-    rst = ok ? rowstat[row] : make_double2(0.0, INFINITY);
+    const double2 v = __builtin_bit_cast(
+        double2, __builtin_amdgcn_raw_buffer_load_b128(rres, buf_off(ok ? e * (int)sizeof(double2) : kBufOob), 0, 0));
+    rs = make_double2(v.x, ok ? v.y : INFINITY);   // a row past the queue: logZ2 = +inf, r = 0
   };
 
   f32x16 acc[NJ];
@@ -909,14 +928,14 @@ void iso_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D
   float nk = 0.0f, sig = 0.0f;
   const bf16x8 ones = x6c_ones(lane);
 
-  int e;
-  int cnt = take(e);
-  if (cnt > 0) issue(e);
-  while (cnt > 0) {
+  // One tile from stage P; the tile two ahead is taken from the queue and its loads
+  // issued into the same stage once its registers are free.  Returns that tile's count.
+  auto tile = [&](auto par) __attribute__((always_inline)) -> int {
+    constexpr int P = decltype(par)::value;
     // This tile's rows: bf16 splits in registers, x1 and x2 to LDS, row state to LDS.
     bf16x8 xa[NQ][3];
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) split3_bf16(raw[2 * q], raw[2 * q + 1], xa[q]);
+    for (int q = 0; q < NQ; ++q) split3_bf16(raw[P][2 * q], raw[P][2 * q + 1], xa[q]);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the previous tile's LDS reads are done
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
@@ -924,11 +943,10 @@ void iso_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D
       for (int sp = 0; sp < 2; ++sp)
         *reinterpret_cast<bf16x8*>(xt + (sp * 32 + c) * RS + 16 * q + 8 * g) = xa[q][sp];
     }
-    if (g == 0) rs_l[c] = rst;
-    // The next tile's rows, in flight while this one is computed.
+    if (g == 0) rs_l[c] = rst[P];
     int en;
-    const int cnt_next = take(en);
-    if (cnt_next > 0) issue(en);
+    const int cnt_ahead = take(en);
+    if (cnt_ahead > 0) issue(en, raw[P], rst[P]);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
     const f32x16 S = x6c_tile_rows<NQ, kIsoChains>(xa, ones, [&](int q, int t) { return mu_l[(q * 4 + t) * 64 + lane]; });
@@ -961,7 +979,18 @@ void iso_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D
         }
       }
     }
-    cnt = cnt_next;
+    return cnt_ahead;
+  };
+
+  int e;
+  int cnt0 = take(e);
+  if (cnt0 > 0) issue(e, raw[0], rst[0]);
+  int cnt1 = cnt0 > 0 ? take(e) : 0;
+  if (cnt1 > 0) issue(e, raw[1], rst[1]);
+  while (cnt0 > 0) {
+    cnt0 = tile(std::integral_constant<int, 0>{});
+    if (cnt1 == 0) break;
+    cnt1 = tile(std::integral_constant<int, 1>{});
   }
 
   nk += __shfl_xor(nk, 32);
@@ -1291,7 +1320,10 @@ void iso_accum_drange(const float* __restrict__ X, int64_t ldx, int64_t N, int D
   auto start = [&](int e) {
     issue(0, e, xr[0], mr[0]);
     if (nqw > 1) issue(1, e, xr[1], mr[1]);
-    if (wave == 0) rst = e >= 0 ? rowstat[r_begin + e] : make_double2(0.0, INFINITY);
+    if (wave == 0) {
+      const double2 z = rowstat[r_begin + (e >= 0 ? e : 0)];   // a row of the slab: no branch
+      rst = e >= 0 ? z : make_double2(0.0, INFINITY);
+    }
   };
 
   f32x16 acc[kDrTiles];
