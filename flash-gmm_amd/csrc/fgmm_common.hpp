@@ -501,9 +501,11 @@ __device__ __forceinline__ void need_put_masks(RM rmax, unsigned* __restrict__ m
   const float zy = (lz2 > -INFINITY && lz2 < INFINITY) ? (float)(lz2 - (double)zx) : 0.0f;
   unsigned pairs = 0;
   for (int kb0 = 0; kb0 < KB; kb0 += 8) {
+    // Eight bounds in flight together: the index is clamped rather than the read
+    // skipped, which would put a branch (and a wait) around each one.
     float R[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) R[j] = kb0 + j < KB ? rmax(kb0 + j) : 0.0f;
+    for (int j = 0; j < 8; ++j) R[j] = rmax(kb0 + j < KB ? kb0 + j : KB - 1);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if (kb0 + j < KB) {

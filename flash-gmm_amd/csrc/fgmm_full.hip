@@ -806,18 +806,34 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
     return cnt;
   };
 
-  // The tile in flight: lane (c, g) holds row c's dimensions 16q + 8g .. +7.
+  // The tile in flight: lane (c, g) holds row c's dimensions 16q + 8g .. +7.  The rows
+  // come through resources over the slab (a lane without a row reads zeros and makes
+  // no access, so the loads issue back to back): X so while D fills whole chunks and
+  // the slab spans under 2 GiB (uniform), else load_row4.
   f32x4 raw[2 * NQ];
   double rst;
+  const int64_t slab_bytes = (r_end - r_begin) * ldx * (int64_t)sizeof(float);
+  const bool xbuf = D == DP && slab_bytes <= ((int64_t)1 << 31) - 256;
+  const buf_rsrc xres = make_rsrc(X + r_begin * ldx, xbuf ? (uint32_t)slab_bytes : 0u);
+  const buf_rsrc rres = make_rsrc(rowstat + r_begin, (uint32_t)((r_end - r_begin) * sizeof(double)));
   auto issue = [&](int e) {
     const bool ok = e >= 0;
-    const int64_t row = r_begin + (ok ? e : 0);
+    if (xbuf) {
+      const int off = buf_off(ok ? (int)((int64_t)e * ldx * (int64_t)sizeof(float)) + 32 * g : kBufOob);
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      raw[2 * q] = load_row4(X, ldx, row, 16 * q + 8 * g, D, ok);
-      raw[2 * q + 1] = load_row4(X, ldx, row, 16 * q + 8 * g + 4, D, ok);
+      for (int q = 0; q < NQ; ++q) {
+        raw[2 * q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 64 * q, 0));
+        raw[2 * q + 1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 64 * q + 16, 0));
+      }
+    } else {
+      const int64_t row = r_begin + (ok ? e : 0);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        raw[2 * q] = load_row4(X, ldx, row, 16 * q + 8 * g, D, ok);
+        raw[2 * q + 1] = load_row4(X, ldx, row, 16 * q + 8 * g + 4, D, ok);
+      }
     }
-    const double z = rowstat[row];   // row is a row of the slab even without a queued one: no branch
+    const double z = buf_load_f64(rres, buf_off(ok ? e * (int)sizeof(double) : kBufOob));
     rst = ok ? z : INFINITY;
   };
 
