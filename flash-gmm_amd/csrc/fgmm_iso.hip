@@ -800,9 +800,14 @@ __host__ __device__ constexpr size_t gather_lds_bytes(int DP) {
 __host__ __device__ constexpr int gather_groups(int nslab) { return (nslab + kGatherWaves - 1) / kGatherWaves; }
 __host__ inline int64_t gather_grid(int nslab, int KB) { return cdiv(gather_groups(nslab), 8) * (int64_t)KB * 8; }
 
+// Waves per SIMD of the gathering pass: two where a wave's registers and the
+// workgroup's LDS allow it (D <= 64), so one wave's row loads overlap the other's
+// matrix steps.
+__host__ __device__ constexpr int gather_waves_per_simd(int DP) { return DP <= 64 ? 2 : 1; }
+
 template <int DP>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * kGatherWaves, 64 * kGatherWaves),
-                          amdgpu_waves_per_eu(1, 1)))
+                          amdgpu_waves_per_eu(gather_waves_per_simd(DP), gather_waves_per_simd(DP))))
 void iso_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                       const bf16x8* __restrict__ mu3, const double4* __restrict__ kc_gat, int KB, int KP,
                       const double2* __restrict__ rowstat, const unsigned* __restrict__ need,
@@ -2101,8 +2106,10 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   if constexpr (DP <= 128) {
     if (pl.need) {
       // Both forms are launched; the needed-row count pass 1 left selects one on the
-      // device: the gathering kernel below a quarter of all (row, block) pairs.
-      const int64_t dense_min = cdiv(cdiv(pl.N, 32) * 32 * (int64_t)pl.KB, 4);
+      // device: the gathering kernel below three quarters of all (row, block) pairs
+      // (measured at N=1M K=1024: at a quarter it takes half the tile kernel's time, with
+      // every pair needed 1.1-1.25 times it).
+      const int64_t dense_min = cdiv(cdiv(pl.N, 32) * 32 * (int64_t)pl.KB * 3, 4);
       constexpr size_t lds = gather_lds_bytes(DP);
       static_assert(lds <= kMaxLds, "gathering pass 2 exceeds LDS");
       hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_gather<DP>),
