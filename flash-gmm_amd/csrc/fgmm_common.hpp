@@ -600,6 +600,29 @@ __device__ __forceinline__ f32x4 buf_load_f32x4(buf_rsrc r, int off) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+// Rows of one slab of X through a resource whose byte 0 is the slab's first row
+// (slab_rsrc; the slab spans under 2 GiB, slab_fits).  slab_row4 reads the four floats
+// at column d0 of slab row `rel`: zero when !valid and from column D on.  A lane with
+// nothing to read gets an offset past the resource, so there is no branch and the loads
+// of a sequence stay in flight together; only where D % 4 != 0 (uniform) are the
+// columns past D inside the last vector zeroed by selects.
+__host__ __device__ inline bool slab_fits(int64_t rows, int64_t ldx) {
+  return rows * ldx * (int64_t)sizeof(float) <= ((int64_t)1 << 31) - 256;
+}
+__device__ __forceinline__ buf_rsrc slab_rsrc(const float* X, int64_t ldx, int64_t r_begin, int64_t r_end) {
+  return make_rsrc(X + r_begin * ldx, (uint32_t)((r_end - r_begin) * ldx * (int64_t)sizeof(float)));
+}
+__device__ __forceinline__ f32x4 slab_row4(buf_rsrc r, int64_t ldx, int rel, int d0, int D, bool valid) {
+  const bool in = valid && d0 < D;
+  f32x4 v = buf_load_f32x4(r, buf_off(in ? (int)(((int64_t)rel * ldx + d0) * (int64_t)sizeof(float)) : kBufOob));
+  if (D & 3) {
+    if (d0 + 1 >= D) v.y = 0.0f;
+    if (d0 + 2 >= D) v.z = 0.0f;
+    if (d0 + 3 >= D) v.w = 0.0f;
+  }
+  return v;
+}
+
 // Workspace cap for the stored log-joint of one call (N/32 x K/32 tiles of 4 KiB).
 constexpr size_t kMaxLjBytes = (size_t)16 << 30;
 

@@ -899,20 +899,27 @@ void iso_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D
   f32x4 raw[2][2 * NQ];
   double2 rst[2];
   // The rows come through resources over the slab: a lane without a row reads zeros
-  // and makes no access, and the loads of a tile issue back to back.  X so while D
-  // fills whole chunks and the slab spans under 2 GiB (uniform), else load_row4.
-  const int64_t slab_bytes = (r_end - r_begin) * ldx * (int64_t)sizeof(float);
-  const bool xbuf = D == DP && slab_bytes <= ((int64_t)1 << 31) - 256;
-  const buf_rsrc xres = make_rsrc(X + r_begin * ldx, xbuf ? (uint32_t)slab_bytes : 0u);
+  // and makes no access, and the loads of a tile issue back to back.  X so while the
+  // slab spans under 2 GiB (uniform; with one offset per lane where D fills whole
+  // chunks), else load_row4.
+  const bool xbuf = slab_fits(r_end - r_begin, ldx);
+  const bool xfull = xbuf && D == DP;
+  const buf_rsrc xres = slab_rsrc(X, ldx, r_begin, xbuf ? r_end : r_begin);
   const buf_rsrc rres = make_rsrc(rowstat + r_begin, (uint32_t)((r_end - r_begin) * sizeof(double2)));
   auto issue = [&](int e, f32x4 (&rw)[2 * NQ], double2& rs) __attribute__((always_inline)) {
     const bool ok = e >= 0;
-    if (xbuf) {
+    if (xfull) {
       const int off = buf_off(ok ? (int)((int64_t)e * ldx * (int64_t)sizeof(float)) + 32 * g : kBufOob);
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
         rw[2 * q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 64 * q, 0));
         rw[2 * q + 1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 64 * q + 16, 0));
+      }
+    } else if (xbuf) {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        rw[2 * q] = slab_row4(xres, ldx, e, 16 * q + 8 * g, D, ok);
+        rw[2 * q + 1] = slab_row4(xres, ldx, e, 16 * q + 8 * g + 4, D, ok);
       }
     } else {
       const int64_t row = r_begin + (ok ? e : 0);
@@ -1086,7 +1093,10 @@ void iso_accum_tiles(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   f32x4 st[LPT];
   double2 rst = make_double2(0.0, INFINITY);
-  const bool full_d = (D == DP);
+  // Tile rows through a resource over the slab (no branch per load, rows past the
+  // slab read zeros) while it spans under 2 GiB (uniform), else load_row4.
+  const bool xbuf = slab_fits(r_end - r_begin, ldx);
+  const buf_rsrc xres = slab_rsrc(X, ldx, r_begin, xbuf ? r_end : r_begin);
   auto fetch = [&](int64_t t) {
     const int64_t row0 = t * 32;
 #pragma unroll
@@ -1094,10 +1104,8 @@ void iso_accum_tiles(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       const int idx = u * NT + tid;
       const int64_t row = row0 + idx / V4;
       const int d0 = (idx % V4) * 4;
-      if (full_d && row < r_end)
-        st[u] = *reinterpret_cast<const f32x4*>(X + row * ldx + d0);
-      else
-        st[u] = load_row4(X, ldx, row, d0, D, row < r_end);
+      st[u] = xbuf ? slab_row4(xres, ldx, (int)(row - r_begin), d0, D, row < r_end)
+                   : load_row4(X, ldx, row, d0, D, row < r_end);
     }
     if (tid < 32) {
       const int64_t row = row0 + tid;
