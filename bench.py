@@ -58,7 +58,7 @@ WORKLOADS = {
 # WRITE_SIZE x1.0); the counter values and commands are in profiles/.
 TRAFFIC_BYTES = {
     # (workload, plan, precision): {phase: bytes of its main kernel}
-    ("iso_n1m_k1024_d128", "default", "fp32"): {"phase1": 303_502 * 2048 + 24_414 * 1024},    # iso_lse<128, 2>
+    ("iso_n1m_k1024_d128", "default", "fp32"): {"phase1": 305_014 * 2048 + 24_414 * 1024},    # iso_lse<128, 2>
     ("diag_n1m_k1024_d96", "default", "fp32"): {"phase1": 193_935 * 2048 + 19_532 * 1024},    # diag_lse_x6<96, 2>
     ("full_n250k_k256_d64", "default", "fp32"): {"phase1": 329_068 * 2048 + 135_802 * 1024},  # full_lse_x6<64, 2>
     ("full_n100k_k64_d128", "default", "fp32"): {"phase1": 125_725 * 2048 + 18_587 * 1024},   # full_lse_x6<128, 2>
