@@ -800,9 +800,9 @@ __host__ __device__ constexpr size_t gather_lds_bytes(int DP) {
 __host__ __device__ constexpr int gather_groups(int nslab) { return (nslab + kGatherWaves - 1) / kGatherWaves; }
 __host__ inline int64_t gather_grid(int nslab, int KB) { return cdiv(gather_groups(nslab), 8) * (int64_t)KB * 8; }
 
-// Waves per SIMD of the gathering pass: two where a wave's registers and the
-// workgroup's LDS allow it (D <= 64), so one wave's row loads overlap the other's
-// matrix steps.
+// Waves per SIMD of the gathering and tile passes: two where a wave's registers and
+// the workgroup's LDS allow it (D <= 64), so one wave's loads and waits overlap the
+// other's matrix steps.
 __host__ __device__ constexpr int gather_waves_per_simd(int DP) { return DP <= 64 ? 2 : 1; }
 
 template <int DP>
@@ -1040,7 +1040,7 @@ __host__ __device__ constexpr size_t tiles_lds_bytes(int DP) {
 
 template <int DP>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * kTileBlocks, 64 * kTileBlocks),
-                          amdgpu_waves_per_eu(1, 1)))
+                          amdgpu_waves_per_eu(gather_waves_per_simd(DP), gather_waves_per_simd(DP))))
 void iso_accum_tiles(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                      const bf16x8* __restrict__ mu3, const double4* __restrict__ kc_gat, int KB, int KP,
                      const double2* __restrict__ rowstat, const unsigned* __restrict__ need,
