@@ -95,24 +95,26 @@ __device__ __forceinline__ bf16x8 to_bf16x8(f32x4 lo, f32x4 hi) {
 // packed to bf16 pairs, one swap across the half-waves per pair of dwords moves rows
 // 8p' + 4(1-g) + j to the other half (e = 0..3 from the first pair, 4..7 from the
 // second), with no trip through LDS.
-__device__ __forceinline__ void acc_to_row_operands(const float (&r)[16], bf16x8 (&a)[2]) {
+// One of the two: registers 8p .. 8p + 7 of the tile, passed as r8[0 .. 7], form the
+// operand of the 16-row step p.
+__device__ __forceinline__ bf16x8 acc_to_row_operand(const float* r8) {
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   auto pack = [](float u, float v) {
     const bf16x2 t = {(__bf16)u, (__bf16)v};
     return *reinterpret_cast<const unsigned*>(&t);
   };
+  uint4 wv;
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    uint4 wv;
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const auto sw = __builtin_amdgcn_permlane32_swap(pack(r[8 * p + 2 * hh], r[8 * p + 2 * hh + 1]),
-                                                       pack(r[8 * p + 4 + 2 * hh], r[8 * p + 5 + 2 * hh]),
-                                                       false, false);
-      if (hh == 0) { wv.x = sw[0]; wv.z = sw[1]; } else { wv.y = sw[0]; wv.w = sw[1]; }
-    }
-    a[p] = *reinterpret_cast<const bf16x8*>(&wv);
+  for (int hh = 0; hh < 2; ++hh) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(pack(r8[2 * hh], r8[2 * hh + 1]),
+                                                     pack(r8[4 + 2 * hh], r8[5 + 2 * hh]), false, false);
+    if (hh == 0) { wv.x = sw[0]; wv.z = sw[1]; } else { wv.y = sw[0]; wv.w = sw[1]; }
   }
+  return *reinterpret_cast<const bf16x8*>(&wv);
+}
+__device__ __forceinline__ void acc_to_row_operands(const float (&r)[16], bf16x8 (&a)[2]) {
+  a[0] = acc_to_row_operand(r);
+  a[1] = acc_to_row_operand(r + 8);
 }
 
 // ---------------------------------------------------------------------------

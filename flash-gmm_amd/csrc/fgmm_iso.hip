@@ -25,14 +25,15 @@
 //               pass 1 above D = 128 (any D): the contraction tiled over components
 //               (128 per tile) as well as rows, the rows' chunks re-read and split
 //               per component tile, four accumulation chains.  Same outputs.
-//   iso_accum_gather / iso_accum_tiles
+//   iso_accum_gather / iso_accum_tiles / iso_accum_tiles2
 //               pass 2 of the default plan up to D = 128: the log-joint of the
 //               needed (row, block) pairs recomputed bit for bit as pass 1 forms it,
 //               r = 2^(ll2 - logZ2), r^T X as split-bf16 products on the matrix cores,
 //               Nk and sig_acc on the VALU, one partial per (slab, component).  The
 //               gathering kernel queues the needed rows of each slab; the tile
-//               kernel (most pairs needed) visits every row.  The needed-pair count
-//               selects one of them on the device.
+//               kernels (most pairs needed) visit every row, at D = 96 and 128 with
+//               two waves per block, one accumulation chain each.  The needed-pair
+//               count selects one of them on the device.
 //   iso_accum_drange
 //               pass 2 of the default plan above D = 128: per (slab, block, range of
 //               up to 1024 dimensions) four waves share the queued rows, each forming
@@ -1021,9 +1022,10 @@ void iso_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D
 
 
 // ---------------------------------------------------------------------------
-// Pass 2 of the default plan (D <= 128) when most pairs are needed (pass 1 counted
-// at least dense_min needed rows; the gathering kernel runs otherwise).  Grid over
-// (row slab x group of 4 component blocks), one wave per SIMD; wave w owns block
+// Pass 2 of the default plan (D <= 64; iso_accum_tiles2 at D = 96 and 128) when
+// most pairs are needed (pass 1 counted at least dense_min needed rows; the
+// gathering kernel runs otherwise).  Grid over (row slab x group of 4 component
+// blocks), two waves per SIMD; wave w owns block
 // 4 cg + w, its mu operands in registers, and the slab's partial of that block
 // (the gathering kernel's slab split, so either kernel fills the same partials).
 // The 32-row tiles of X are loaded once per workgroup, split three ways into bf16
@@ -1209,6 +1211,240 @@ void iso_accum_tiles(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       part_nk[kbase + c] = nk;
       part_sig[kbase + c] = sig;
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The tile pass for D = 96 and 128, where a wave holding a block's mu operands for
+// all of D leaves room for one wave per SIMD only: each block is split over two
+// waves by accumulation chain.  Eight waves per workgroup; wave (h, w) owns block
+// 4 cg + w and chain h, that is the chunks q = h, h + 2, ... (the chunks pass 1's
+// chain h adds, in the same order), so it keeps half the operands.  Per 32-row tile:
+//   - each wave forms its chain over the tile's rows (x6c_tile_rows' products and
+//     order) and leaves it in LDS; after a barrier both waves of a block add the two
+//     chains as pass 1 does, c0 + c1, and have S bit for bit;
+//   - wave (h, w) takes the 16 rows of step h (registers 8h .. 8h + 7 of S): their
+//     log-joint, r and residual, Nk and sig_acc, and their r^T X for all of D;
+//   - at the end the two waves' partials of a block are added in a fixed order.
+// Two waves per SIMD, so the waits of one overlap the other's matrix steps.
+// ---------------------------------------------------------------------------
+constexpr int kTileWaves2 = 2 * kTileBlocks;
+
+__host__ __device__ constexpr size_t tiles2_lds_bytes(int DP) {
+  return (size_t)2 * 3 * 32 * gather_rs(DP) * 2 + (size_t)2 * 32 * sizeof(double2) +
+         (size_t)kTileWaves2 * 4 * 64 * sizeof(f32x4);
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kTileWaves2, 64 * kTileWaves2),
+                          amdgpu_waves_per_eu(2, 2)))
+void iso_accum_tiles2(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                      const bf16x8* __restrict__ mu3, const double4* __restrict__ kc_gat, int KB, int KP,
+                      const double2* __restrict__ rowstat, const unsigned* __restrict__ need,
+                      const unsigned* __restrict__ needcount, int64_t dense_min, int nslab,
+                      int64_t rows_per_slab, float* __restrict__ part_mu, float* __restrict__ part_nk,
+                      float* __restrict__ part_sig, int dense) {
+  constexpr int NQ = DP / 16;
+  constexpr int NQH = NQ / 2;              // chunks of this wave's chain
+  constexpr int NJ = DP / 32;
+  constexpr int RS = gather_rs(DP);
+  constexpr int BLK = NQ * 4 * 64;
+  constexpr int NT = 64 * kTileWaves2;
+  constexpr int V4 = DP / 4;               // float4 per row
+  constexpr int NV = 32 * V4;              // float4 per tile
+  constexpr int LPT = (NV + NT - 1) / NT;  // float4 per thread per tile
+  static_assert(NQ % 2 == 0 && kIsoChains == 2, "one chain per wave of a pair");
+  if (need_total(needcount) < dense_min) return;   // the gathering kernel runs (uniform exit)
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  __bf16* xs = reinterpret_cast<__bf16*>(lds_raw);                                   // [2][3][32][RS]
+  double2* rs_l = reinterpret_cast<double2*>(lds_raw + (size_t)2 * 3 * 32 * RS * 2);  // [2][32]
+  f32x4* ex = reinterpret_cast<f32x4*>(rs_l + 2 * 32);                                // [wave][4][64]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w = wave % kTileBlocks, h = wave / kTileBlocks;
+  const int c = lane & 31, g = lane >> 5;
+  const int slab = (int)(blockIdx.x % (unsigned)nslab);
+  const int kb = (int)(blockIdx.x / (unsigned)nslab) * kTileBlocks + w;
+  const bool active = kb < KB;
+
+  // This wave's chain: operands of the chunks q = 2u + h.
+  bf16x8 mb[NQH][4];
+#pragma unroll
+  for (int u = 0; u < NQH; ++u) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      bf16x8 z;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) z[e] = (__bf16)0.0f;
+      mb[u][t] = active ? mu3[(int64_t)kb * BLK + ((2 * u + h) * 4 + t) * 64 + lane] : z;
+    }
+  }
+  double Cc = -INFINITY, bk = 0.0;
+  float mqf = 0.0f;
+  if (active) {
+    const double4 kc = kc_gat[(int64_t)kb * 32 + c];
+    Cc = kc.x; bk = kc.y; mqf = (float)kc.z;
+  }
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int64_t t_begin = r_begin / 32, t_end = r_end > r_begin ? cdiv(r_end, 32) : t_begin;
+
+  f32x4 st[LPT];
+  double2 rst = make_double2(0.0, INFINITY);
+  // Tile rows through a resource over the slab (no branch per load, rows past the
+  // slab read zeros) while it spans under 2 GiB (uniform), else load_row4.
+  const bool xbuf = slab_fits(r_end - r_begin, ldx);
+  const buf_rsrc xres = slab_rsrc(X, ldx, r_begin, xbuf ? r_end : r_begin);
+  auto fetch = [&](int64_t t) {
+    const int64_t row0 = t * 32;
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int idx = u * NT + tid;
+      const int64_t row = row0 + (idx < NV ? idx / V4 : 0);
+      const int d0 = (idx % V4) * 4;
+      const bool ok = idx < NV && row < r_end;
+      st[u] = xbuf ? slab_row4(xres, ldx, (int)(row - r_begin), d0, D, ok) : load_row4(X, ldx, row, d0, D, ok);
+    }
+    if (tid < 32) {
+      const int64_t row = row0 + tid;
+      const double2 z = rowstat[row < r_end ? row : r_begin];   // a row of the slab: no branch
+      rst = row < r_end ? z : make_double2(0.0, INFINITY);
+    }
+  };
+  // Split the staged tile into bf16 x1, x2, x3 (4 values per float4: two packed pairs).
+  auto commit = [&](int buf) {
+    __bf16* dst = xs + (size_t)buf * 3 * 32 * RS;
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int idx = u * NT + tid;
+      if (NV % NT != 0 && idx >= NV) continue;
+      const int rr = idx / V4, d0 = (idx % V4) * 4;
+      uint2 wd[3];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f32x2 a = {st[u][2 * j], st[u][2 * j + 1]};
+        const unsigned hi = bf16_pair(a);
+        const f32x2 r = a - bf16_pair_widen(hi);
+        const unsigned m = bf16_pair(r);
+        const unsigned l = bf16_pair(r - bf16_pair_widen(m));
+        (j == 0 ? wd[0].x : wd[0].y) = hi;
+        (j == 0 ? wd[1].x : wd[1].y) = m;
+        (j == 0 ? wd[2].x : wd[2].y) = l;
+      }
+#pragma unroll
+      for (int sp = 0; sp < 3; ++sp) *reinterpret_cast<uint2*>(dst + (sp * 32 + rr) * RS + d0) = wd[sp];
+    }
+    if (tid < 32) rs_l[buf * 32 + tid] = rst;
+  };
+
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
+  float nk = 0.0f, sig = 0.0f;
+  const bf16x8 ones = x6c_ones(lane);
+  f32x4* mine = ex + wave * 4 * 64 + lane;
+  const f32x4* ch0 = ex + w * 4 * 64 + lane;                       // chain 0 of the block
+  const f32x4* ch1 = ex + (kTileBlocks + w) * 4 * 64 + lane;       // chain 1
+
+  if (t_begin < t_end) {
+    fetch(t_begin);
+    commit(0);
+  }
+  __syncthreads();
+  for (int64_t t = t_begin; t < t_end; ++t) {
+    const int buf = (int)((t - t_begin) & 1);
+    const bool more = t + 1 < t_end;
+    if (more) fetch(t + 1);
+    const unsigned m = active ? (dense ? ~0u : need[t * KB + kb]) : 0u;   // the same for both waves
+    const __bf16* xt = xs + (size_t)buf * 3 * 32 * RS;
+    if (m != 0u) {
+      // Chain h over the tile's rows: x6c_tile_rows' steps for the chunks q = 2u + h.
+      f32x16 cacc = zero16();
+#pragma unroll
+      for (int u = 0; u < NQH; ++u) {
+        const int q = 2 * u + h;
+        bf16x8 xa[3];
+#pragma unroll
+        for (int sp = 0; sp < 3; ++sp) xa[sp] = *reinterpret_cast<const bf16x8*>(xt + (sp * 32 + c) * RS + 16 * q + 8 * g);
+        cacc = mfma_bf16(xa[1], mb[u][1], cacc);
+        cacc = mfma_bf16(xa[0], mb[u][2], cacc);
+        cacc = mfma_bf16(xa[2], mb[u][0], cacc);
+        cacc = mfma_bf16(xa[1], mb[u][0], cacc);
+        cacc = mfma_bf16(xa[0], mb[u][1], cacc);
+        cacc = mfma_bf16(ones, mb[u][3], cacc);
+        cacc = mfma_bf16(xa[0], mb[u][0], cacc);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) mine[k * 64] = f32x4{cacc[4 * k], cacc[4 * k + 1], cacc[4 * k + 2], cacc[4 * k + 3]};
+    }
+    __syncthreads();   // both chains of every block are in LDS
+    if (m != 0u) {
+      // Registers 8h .. 8h + 7 of S = c0 + c1: the rows of step h.
+      float S[8];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const f32x4 a = ch0[(2 * h + k) * 64], b = ch1[(2 * h + k) * 64];
+        S[4 * k] = a.x + b.x; S[4 * k + 1] = a.y + b.y; S[4 * k + 2] = a.z + b.z; S[4 * k + 3] = a.w + b.w;
+      }
+      const double2* rw = rs_l + buf * 32;
+      float r[8], res[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const double2 z = rw[acc_row(8 * h + k, g)];
+        const double ll = fma(-bk, fma(-2.0, (double)S[k], z.x), Cc);
+        const float rv = fast_exp2((float)(ll - z.y));
+        r[k] = rv;
+        res[k] = rv - (float)(__bf16)rv;
+        nk += rv;
+        sig = fmaf(rv, fmaf(-2.0f, S[k], (float)z.x) + mqf, sig);
+      }
+      const bf16x8 a1 = acc_to_row_operand(r), a2 = acc_to_row_operand(res);
+      if (dense || any_nonzero(a1)) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const bf16x8 b1 = lds_rows_operand(xt, RS, 16 * h, 32 * j, lane);
+          const bf16x8 b2 = lds_rows_operand(xt + 32 * RS, RS, 16 * h, 32 * j, lane);
+          acc[j] = mfma_bf16(a2, b1, acc[j]);
+          acc[j] = mfma_bf16(a1, b2, acc[j]);
+          acc[j] = mfma_bf16(a1, b1, acc[j]);
+        }
+      }
+    }
+    if (more) commit(buf ^ 1);
+    __syncthreads();
+  }
+
+  // The two waves' partials of a block, added in a fixed order (h = 0 first) by wave
+  // (0, w) through LDS, one 32-column tile at a time.
+  nk += __shfl_xor(nk, 32);
+  sig += __shfl_xor(sig, 32);
+  const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+  float* exf = reinterpret_cast<float*>(ex);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if (h == 1) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) exf[(w * 16 + i) * 64 + lane] = acc[j][i];
+      if (j == 0) {
+        exf[(kTileBlocks * 16) * 64 + w * 64 + lane] = nk;
+        exf[(kTileBlocks * 16 + kTileBlocks) * 64 + w * 64 + lane] = sig;
+      }
+    }
+    __syncthreads();
+    if (h == 0 && active) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[j][i] + exf[(w * 16 + i) * 64 + lane];
+      if (j == 0 && g == 0) {
+        part_nk[kbase + c] = nk + exf[(kTileBlocks * 16) * 64 + w * 64 + lane];
+        part_sig[kbase + c] = sig + exf[(kTileBlocks * 16 + kTileBlocks) * 64 + w * 64 + lane];
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -2129,18 +2365,25 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
                          reinterpret_cast<const double4*>(ws + pl.off_kcgat), pl.KB, pl.KP, rowstat,
                          ljmask, ljcount, dense_min, pl.nslab, pl.rows_per_slab, pmu, pnk, psig,
                          dense ? 1 : 0);
-      constexpr size_t lds_t = tiles_lds_bytes(DP);
-      static_assert(lds_t <= kMaxLds, "tile pass 2 exceeds LDS");
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_tiles<DP>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_t);
-      if (e != hipSuccess) return e;
-      hipLaunchKernelGGL(iso_accum_tiles<DP>, dim3((unsigned)(pl.nslab * cdiv(pl.KB, kTileBlocks))),
-                         dim3(64 * kTileBlocks), lds_t, stream, X, ldx, pl.N, (int)pl.D,
-                         reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
-                         reinterpret_cast<const double4*>(ws + pl.off_kcgat), pl.KB, pl.KP, rowstat,
-                         ljmask, ljcount, dense_min, pl.nslab, pl.rows_per_slab, pmu, pnk, psig,
-                         dense ? 1 : 0);
-      return hipGetLastError();
+      // The tile pass: one wave per block up to D = 64, a pair of waves (one chain
+      // each) at D = 96 and 128.
+      auto tiles = [&](auto kern, size_t lds_t, int waves) -> hipError_t {
+        hipError_t et = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_t);
+        if (et != hipSuccess) return et;
+        hipLaunchKernelGGL(kern, dim3((unsigned)(pl.nslab * cdiv(pl.KB, kTileBlocks))), dim3(64 * waves), lds_t,
+                           stream, X, ldx, pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
+                           reinterpret_cast<const double4*>(ws + pl.off_kcgat), pl.KB, pl.KP, rowstat, ljmask,
+                           ljcount, dense_min, pl.nslab, pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
+        return hipGetLastError();
+      };
+      if constexpr (DP > 64) {
+        static_assert(tiles2_lds_bytes(DP) <= kMaxLds, "tile pass 2 exceeds LDS");
+        return tiles(&iso_accum_tiles2<DP>, tiles2_lds_bytes(DP), kTileWaves2);
+      } else {
+        static_assert(tiles_lds_bytes(DP) <= kMaxLds, "tile pass 2 exceeds LDS");
+        return tiles(&iso_accum_tiles<DP>, tiles_lds_bytes(DP), kTileBlocks);
+      }
     }
   }
   if (!pl.lj) return hipErrorInvalidValue;   // not a plan of this launcher

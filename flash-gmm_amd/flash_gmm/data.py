@@ -20,6 +20,7 @@ from __future__ import annotations
 import math
 from typing import Dict
 
+import numpy as np
 import torch
 
 
@@ -111,10 +112,18 @@ def full_clustered(N: int, K: int, D: int, seed: int = 3, device="cpu") -> Dict[
     """
     g = _gen(device, seed)
     A = torch.randn(K, D, D, generator=g, device=device, dtype=torch.float32)
-    A64 = A.double().cpu()
-    sigma = A64 @ A64.transpose(1, 2) / D + 0.1 * torch.eye(D, dtype=torch.float64)
-    prec_chol = torch.linalg.cholesky(torch.linalg.inv(sigma))
-    chol_sigma = torch.linalg.cholesky(sigma)
+    # The host-side float64 algebra runs per component in numpy: batched float64
+    # products and factorizations through torch's CPU backend have returned a
+    # non-positive-definite inverse now and then on some hosts.
+    A64 = A.double().cpu().numpy()
+    prec = np.empty((K, D, D))
+    chs = np.empty((K, D, D))
+    for k in range(K):
+        s = A64[k] @ A64[k].T / D + 0.1 * np.eye(D)
+        chs[k] = np.linalg.cholesky(s)
+        prec[k] = np.linalg.cholesky(np.linalg.inv(s))
+    prec_chol = torch.from_numpy(prec)
+    chol_sigma = torch.from_numpy(chs)
     mu = _randn(g, K, D, device=device, std=2.0)
     lpi = _log_softmax(_randn(g, K, device=device, std=math.sqrt(0.5)))
     a = _assign_rows(g, N, K, device, probs=torch.exp(lpi.double()).float())
