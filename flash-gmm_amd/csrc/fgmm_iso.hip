@@ -82,18 +82,22 @@ constexpr size_t kMaxLds = 160 * 1024;
 // padded to a multiple of 64 there, so each of the four accumulation chains gets
 // the same number of 16-dimension chunks.
 constexpr int kCtWaves = 4;                               // waves per workgroup, one per SIMD
-constexpr int kCtBlocks = 4;                              // component blocks per pass-1 tile
 constexpr int kCtChains = 4;                              // accumulation chains (chunk q -> q % 4)
-constexpr int kCtStageOps = kCtBlocks * 2 * 4 * 64;       // bf16x8 per two-chunk operand stage (32 KiB)
 constexpr int kDrange = 1024;                             // dimensions of r^T X per pass-2 workgroup
 constexpr int kDrTiles = kDrange / 32 / kCtWaves;         // 32-column tiles per pass-2 wave
 
-__host__ __device__ constexpr size_t lse_ctile_base() {
-  return (size_t)2 * kCtStageOps * sizeof(bf16x8) + (size_t)2 * kCtBlocks * 32 * sizeof(double2);
+// Component blocks per pass-1 tile: 2 up to D = 512 (two waves per SIMD, which the
+// 128 accumulator registers of 2 blocks x 4 chains allow), 4 above (one wave per SIMD;
+// the rows are re-read once per component tile, and at large D the reads of the
+// narrower tile cost more than the second wave gains).
+__host__ __device__ constexpr int ctile_blocks(int DP) { return DP <= 512 ? 2 : 4; }
+__host__ __device__ constexpr int ctile_stage_ops(int CTB) { return CTB * 2 * 4 * 64; }   // bf16x8 per two-chunk stage
+__host__ __device__ constexpr size_t lse_ctile_base(int CTB) {
+  return (size_t)2 * ctile_stage_ops(CTB) * sizeof(bf16x8) + (size_t)2 * CTB * 32 * sizeof(double2);
 }
 // Component blocks whose need bounds (bf16, 32 rows per wave) fit beside the stages.
-__host__ __device__ constexpr int ctile_need_exact_cap() {
-  return (int)((kMaxLds - lse_ctile_base()) / (kCtWaves * 32 * 2));
+__host__ __device__ constexpr int ctile_need_exact_cap(int CTB) {
+  return (int)((kMaxLds - lse_ctile_base(CTB)) / (kCtWaves * 32 * 2));
 }
 __host__ __device__ constexpr int drange_rs(int DR) { return DR + 16; }   // bf16 row stride of the X tile
 __host__ __device__ constexpr size_t accum_drange_lds_bytes(int DR) {
@@ -164,7 +168,7 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
   p.lj = !bf16 && use_stored_lj(N, p.DP, p.KB, allow_lj);
   p.need = !bf16 && !p.lj;
   p.ctile = p.need && p.DP > 128;
-  p.rexact = p.need && p.KB <= (p.ctile ? ctile_need_exact_cap() : need_exact_cap(p.DP));
+  p.rexact = p.need && p.KB <= (p.ctile ? ctile_need_exact_cap(ctile_blocks(p.DP)) : need_exact_cap(p.DP));
   p.ndr = p.ctile ? (int)cdiv(p.DP, kDrange) : 1;
   if (bf16) {
     p.cpg = bf16_blocks_per_group(p.DP, p.KB);
@@ -509,34 +513,37 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 // Pass 1 of the default plan above D = 128 (any D).  The split operands of a row
 // no longer fit in registers for all of D, so the contraction is tiled over the
 // components as well: each wave owns a 32-row tile, and for each component tile of
-// kCtBlocks blocks (128 components) it streams its rows' chunks of 16 dimensions
+// CTB blocks (ctile_blocks) it streams its rows' chunks of 16 dimensions
 // from global memory (read once per component tile; from L2 or the MALL after the
 // first), splits them three ways into bf16 as they arrive and contracts them with
 // the tile's mu operands (bf16 splits and centring offsets), which the
 // workgroup's four waves share through an LDS double buffer of two-chunk stages.
 // Chunk q accumulates into chain q % 4 of each block with x6c_tile's products and
 // order; after the last chunk the chains are added as ((c0 + c1) + c2) + c3, and
-// the online log-sum-exp and the need bounds proceed as in iso_lse.  Four blocks x
-// four chains fill the 256 accumulator registers: one wave per SIMD.  The stored
+// the online log-sum-exp and the need bounds proceed as in iso_lse.  CTB blocks x
+// four chains take 64 CTB accumulator registers: two waves per SIMD with 2 blocks,
+// one with 4.  The stored
 // plan (LJM = kLjmStore, D up to 256) runs the same kernel and also writes the
 // log-joint rows, their block maxima and the need masks, as iso_lse does.
 // ---------------------------------------------------------------------------
-template <int LJM>
-__global__ __attribute__((amdgpu_flat_work_group_size(64 * kCtWaves, 64 * kCtWaves), amdgpu_waves_per_eu(1, 1)))
+template <int LJM, int CTB>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kCtWaves, 64 * kCtWaves),
+                          amdgpu_waves_per_eu(CTB == 2 ? 2 : 1, CTB == 2 ? 2 : 1)))
 void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int NQ,
                    const bf16x8* __restrict__ mu3, const double2* __restrict__ kc_blk, int KB,
                    float* __restrict__ logZ, double2* __restrict__ rowstat, float* __restrict__ lj,
                    float* __restrict__ ljmax, unsigned* __restrict__ ljmask, unsigned* __restrict__ ljcount,
                    int dense, int rexact) {
   constexpr bool LJ = LJM == kLjmStore;
+  constexpr int SO = ctile_stage_ops(CTB);   // bf16x8 per two-chunk operand stage
   constexpr int NT = 64 * kCtWaves;
-  constexpr int LPT = kCtStageOps / NT;   // operand loads per thread per stage
-  static_assert(kCtStageOps % NT == 0 && kCtBlocks * 32 <= NT, "stage split");
+  constexpr int LPT = SO / NT;   // operand loads per thread per stage
+  static_assert(SO % NT == 0 && CTB * 32 <= NT, "stage split");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                                        // [2][stage]
-  double2* kc_l = reinterpret_cast<double2*>(lds_raw + 2 * kCtStageOps * sizeof(bf16x8));   // [2][blocks*32]
-  unsigned short* rmax_l = reinterpret_cast<unsigned short*>(lds_raw + lse_ctile_base());  // [wave][KB][32]
+  double2* kc_l = reinterpret_cast<double2*>(lds_raw + 2 * SO * sizeof(bf16x8));   // [2][blocks*32]
+  unsigned short* rmax_l = reinterpret_cast<unsigned short*>(lds_raw + lse_ctile_base(CTB));  // [wave][KB][32]
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -545,7 +552,7 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
   const int64_t row = tile * 32 + c;
   const bool valid = row < N;
   const int NS = NQ / 2;                        // stages per component tile (even: NQ % 4 == 0)
-  const int nstage = (int)cdiv(KB, kCtBlocks) * NS;
+  const int nstage = (int)cdiv(KB, CTB) * NS;
   const int nq_full = D / 16;                   // chunks that end at or before D
 
   // Stage s = (component tile s / NS, chunk pair s % NS).  Thread element u covers
@@ -558,7 +565,7 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
   double2 kst = make_double2(-INFINITY, 0.0);
   auto fetch = [&](int s) __attribute__((always_inline)) {
     const int ct = s / NS, sp = s - ct * NS;
-    const int64_t base = (int64_t)ct * kCtBlocks * blk_ops + (int64_t)sp * 2 * 4 * 64;
+    const int64_t base = (int64_t)ct * CTB * blk_ops + (int64_t)sp * 2 * 4 * 64;
     int64_t avail = (all_ops - base) * (int64_t)sizeof(bf16x8);
     if (avail > ((int64_t)1 << 31) - 16) avail = ((int64_t)1 << 31) - 16;
     const buf_rsrc r = make_rsrc(mu3 + base, (uint32_t)avail);
@@ -567,16 +574,16 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
       const int soff = (int)(((int64_t)(u >> 1) * blk_ops + (u & 1) * NT) * (int64_t)sizeof(bf16x8));
       st[u] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, tid * (int)sizeof(bf16x8), soff, 0));
     }
-    if (sp == 0 && tid < kCtBlocks * 32) {
-      const int64_t kc = (int64_t)ct * kCtBlocks * 32 + tid;
+    if (sp == 0 && tid < CTB * 32) {
+      const int64_t kc = (int64_t)ct * CTB * 32 + tid;
       kst = kc < (int64_t)KB * 32 ? kc_blk[kc] : make_double2(-INFINITY, 0.0);
     }
   };
   auto commit = [&](int s, int buf) __attribute__((always_inline)) {
     const int ct = s / NS, sp = s - ct * NS;
 #pragma unroll
-    for (int u = 0; u < LPT; ++u) mu_l[buf * kCtStageOps + u * NT + tid] = st[u];
-    if (sp == 0 && tid < kCtBlocks * 32) kc_l[(ct & 1) * kCtBlocks * 32 + tid] = kst;
+    for (int u = 0; u < LPT; ++u) mu_l[buf * SO + u * NT + tid] = st[u];
+    if (sp == 0 && tid < CTB * 32) kc_l[(ct & 1) * CTB * 32 + tid] = kst;
   };
 
   // The wave's rows, dimensions 16q + 8g .. + 7 of chunk q (zero past D and N).
@@ -604,9 +611,9 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
   commit(0, 0);
   lds_barrier();
 
-  f32x16 acc[kCtBlocks][kCtChains];
+  f32x16 acc[CTB][kCtChains];
 #pragma unroll
-  for (int b = 0; b < kCtBlocks; ++b) {
+  for (int b = 0; b < CTB; ++b) {
 #pragma unroll
     for (int h = 0; h < kCtChains; ++h) acc[b][h] = zero16();
   }
@@ -620,10 +627,10 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
   // Component tile ct is complete: log-joint, log-sum-exp and need bounds per block.
   auto finish_tile = [&](int ct) __attribute__((always_inline)) {
     if (ct == 0) xsq = xsq_part + __shfl_xor(xsq_part, 32);
-    const double2* kp0 = kc_l + (ct & 1) * kCtBlocks * 32 + g * 16;
+    const double2* kp0 = kc_l + (ct & 1) * CTB * 32 + g * 16;
 #pragma unroll
-    for (int b = 0; b < kCtBlocks; ++b) {
-      const int kb = ct * kCtBlocks + b;
+    for (int b = 0; b < CTB; ++b) {
+      const int kb = ct * CTB + b;
       if (kb < KB) {
         double ll[16];
         double bm = -INFINITY;
@@ -671,7 +678,7 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
     const bool more = s + 1 < nstage;
     if (more) fetch(s + 1);
     xstage(s + 1, xr[1 - P]);
-    const bf16x8* mp = mu_l + P * kCtStageOps + lane;
+    const bf16x8* mp = mu_l + P * SO + lane;
     bf16x8 xb[2][3];
 #pragma unroll
     for (int qq = 0; qq < 2; ++qq) {
@@ -687,7 +694,7 @@ void iso_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, i
     // Block by block (its operands for both chunks), the two chunks' chains interleaved.
     // Steps in x6c_tile's order: x2 mu2, x1 mu3, x3 mu1, x2 mu1, x1 mu2, -o, x1 mu1.
 #pragma unroll
-    for (int b = 0; b < kCtBlocks; ++b) {
+    for (int b = 0; b < CTB; ++b) {
       bf16x8 a[2][4];
 #pragma unroll
       for (int qq = 0; qq < 2; ++qq) {
@@ -2286,8 +2293,10 @@ hipError_t launch_ctile(const IsoPlan& pl, const float* X, int64_t ldx, unsigned
   const int NQ = pl.DP / 16;
   if (run1) {
     const bool exact = pl.rexact && !pl.lj;
-    const size_t lds1 = lse_ctile_base() + (exact ? (size_t)kCtWaves * 32 * pl.KB * 2 : 0);
-    auto kern = pl.lj ? &iso_lse_ctile<kLjmStore> : &iso_lse_ctile<kLjmNeed>;
+    const int ctb = ctile_blocks(pl.DP);
+    const size_t lds1 = lse_ctile_base(ctb) + (exact ? (size_t)kCtWaves * 32 * pl.KB * 2 : 0);
+    auto kern = pl.lj ? (ctb == 2 ? &iso_lse_ctile<kLjmStore, 2> : &iso_lse_ctile<kLjmStore, 4>)
+                      : (ctb == 2 ? &iso_lse_ctile<kLjmNeed, 2> : &iso_lse_ctile<kLjmNeed, 4>);
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
     if (e != hipSuccess) return e;
