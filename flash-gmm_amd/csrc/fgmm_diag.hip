@@ -51,18 +51,20 @@ __host__ inline int diag_padded_dim(int64_t D) {
   return D <= 128 ? (int)round_up(D < 1 ? 1 : D, 32) : (int)round_up(D, 64);
 }
 constexpr int kCtWaves = 4;                               // waves per workgroup, one per SIMD
-constexpr int kCtBlocks = 4;                              // component blocks per pass-1 tile
 constexpr int kCtChains = 4;                              // accumulation chains (chunk q -> q % 4)
-constexpr int kCtStageOps = kCtBlocks * 2 * 4 * 64;       // bf16x8 per two-chunk operand stage (32 KiB)
 constexpr int kDrange = 1024;                             // dimensions of r^T [X | X^2] per pass-2 workgroup
 constexpr int kDrTiles = kDrange / 32 / kCtWaves;         // 32-column tiles per pass-2 wave
-__host__ __device__ constexpr size_t lse_ctile_base() {
-  return (size_t)2 * kCtStageOps * sizeof(bf16x8) + (size_t)2 * kCtBlocks * 32 * sizeof(double);
+// Component blocks per pass-1 tile: two (two waves per SIMD) up to D = 1024, four
+// (one wave per SIMD) above.
+__host__ __device__ constexpr int ctile_blocks(int DP) { return DP <= 1024 ? 2 : 4; }
+__host__ __device__ constexpr int ctile_stage_ops(int CTB) { return CTB * 2 * 4 * 64; }   // bf16x8 per two-chunk stage
+__host__ __device__ constexpr size_t lse_ctile_base(int CTB) {
+  return (size_t)2 * ctile_stage_ops(CTB) * sizeof(bf16x8) + (size_t)2 * CTB * 32 * sizeof(double);
 }
 // Component blocks whose half-block need bounds (bf16, 2 x 32 rows per wave) fit
 // beside the stages.
-__host__ __device__ constexpr int ctile_need_exact_cap() {
-  return (int)((kMaxLds - lse_ctile_base()) / (kCtWaves * 2 * 32 * 2));
+__host__ __device__ constexpr int ctile_need_exact_cap(int CTB) {
+  return (int)((kMaxLds - lse_ctile_base(CTB)) / (kCtWaves * 2 * 32 * 2));
 }
 __host__ __device__ constexpr int drange_rs(int DR) { return DR + 8; }   // fp32 row stride of the X tile
 __host__ __device__ constexpr size_t accum_drange_lds_bytes(int DR) {
@@ -131,7 +133,7 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.lj = !bf16 && use_stored_lj(N, p.KB, p.DP, allow_lj);
   p.need = !bf16 && !p.lj;
   p.ctile = !bf16 && !diag_uses_x6(p.DP);
-  p.rexact = p.need && p.KB <= (p.ctile ? ctile_need_exact_cap() : need_exact_cap(p.DP));
+  p.rexact = p.need && p.KB <= (p.ctile ? ctile_need_exact_cap(ctile_blocks(p.DP)) : need_exact_cap(p.DP));
   p.ndr = p.ctile ? (int)cdiv(p.DP, kDrange) : 1;
   if (bf16) {
     p.cpg = bf16_blocks_per_group(p.DP, p.KB);
@@ -514,7 +516,7 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 // ---------------------------------------------------------------------------
 // Pass 1 above D = 128 (any D): the component-tiled form of the isotropic
 // iso_lse_ctile over the diagonal features.  Each wave owns a 32-row tile; per
-// component tile of kCtBlocks blocks it streams its rows' chunks of 8 dimensions
+// component tile of CTB blocks (ctile_blocks) it streams its rows' chunks of 8 dimensions
 // from global memory (lane-half g: dimensions 8q + 4g .. + 3 as [x^2, x], split three
 // ways into bf16) against the tile's [-w, 2v] operands and centring offsets, which
 // the four waves share through an LDS double buffer of two-chunk stages.  Chunk q
@@ -524,21 +526,23 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 // stored plan, D up to 256) the log-joint is written in the register-order tiles
 // that diag_accum_lj reads.
 // ---------------------------------------------------------------------------
-template <int LJM>
-__global__ __attribute__((amdgpu_flat_work_group_size(64 * kCtWaves, 64 * kCtWaves), amdgpu_waves_per_eu(1, 1)))
+template <int LJM, int CTB>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kCtWaves, 64 * kCtWaves),
+                          amdgpu_waves_per_eu(CTB == 2 ? 2 : 1, CTB == 2 ? 2 : 1)))
 void diag_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int NQ,
                     const bf16x8* __restrict__ mu3, const double* __restrict__ kc_x6, int KB,
                     float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj,
                     uint2* __restrict__ ljmask, int dense, int rexact) {
   constexpr bool LJ = LJM == kLjmStore;
   constexpr int NT = 64 * kCtWaves;
-  constexpr int LPT = kCtStageOps / NT;   // operand loads per thread per stage
-  static_assert(kCtStageOps % NT == 0 && kCtBlocks * 32 <= NT, "stage split");
+  constexpr int SO = ctile_stage_ops(CTB);   // bf16x8 per two-chunk operand stage
+  constexpr int LPT = SO / NT;               // operand loads per thread per stage
+  static_assert(SO % NT == 0 && CTB * 32 <= NT, "stage split");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                                       // [2][stage]
-  double* kc_l = reinterpret_cast<double*>(lds_raw + 2 * kCtStageOps * sizeof(bf16x8));   // [2][blocks*32]
-  unsigned short* rmax_l = reinterpret_cast<unsigned short*>(lds_raw + lse_ctile_base());  // [wave][KB][2][32]
+  double* kc_l = reinterpret_cast<double*>(lds_raw + 2 * SO * sizeof(bf16x8));   // [2][blocks*32]
+  unsigned short* rmax_l = reinterpret_cast<unsigned short*>(lds_raw + lse_ctile_base(CTB));  // [wave][KB][2][32]
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -547,7 +551,7 @@ void diag_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, 
   const int64_t row = tile * 32 + c;
   const bool valid = row < N;
   const int NS = NQ / 2;                        // stages per component tile (even: NQ % 4 == 0)
-  const int nstage = (int)cdiv(KB, kCtBlocks) * NS;
+  const int nstage = (int)cdiv(KB, CTB) * NS;
   const int nq_full = D / 8;                    // chunks that end at or before D
 
   // Operand stages exactly as iso_lse_ctile: thread element u covers block u / 2 of
@@ -558,7 +562,7 @@ void diag_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, 
   double kst = -INFINITY;
   auto fetch = [&](int s) __attribute__((always_inline)) {
     const int ct = s / NS, sp = s - ct * NS;
-    const int64_t base = (int64_t)ct * kCtBlocks * blk_ops + (int64_t)sp * 2 * 4 * 64;
+    const int64_t base = (int64_t)ct * CTB * blk_ops + (int64_t)sp * 2 * 4 * 64;
     int64_t avail = (all_ops - base) * (int64_t)sizeof(bf16x8);
     if (avail > ((int64_t)1 << 31) - 16) avail = ((int64_t)1 << 31) - 16;
     const buf_rsrc r = make_rsrc(mu3 + base, (uint32_t)avail);
@@ -567,16 +571,16 @@ void diag_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, 
       const int soff = (int)(((int64_t)(u >> 1) * blk_ops + (u & 1) * NT) * (int64_t)sizeof(bf16x8));
       st[u] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, tid * (int)sizeof(bf16x8), soff, 0));
     }
-    if (sp == 0 && tid < kCtBlocks * 32) {
-      const int64_t kc = (int64_t)ct * kCtBlocks * 32 + tid;
+    if (sp == 0 && tid < CTB * 32) {
+      const int64_t kc = (int64_t)ct * CTB * 32 + tid;
       kst = kc < (int64_t)KB * 32 ? kc_x6[kc] : -INFINITY;
     }
   };
   auto commit = [&](int s, int buf) __attribute__((always_inline)) {
     const int ct = s / NS, sp = s - ct * NS;
 #pragma unroll
-    for (int u = 0; u < LPT; ++u) mu_l[buf * kCtStageOps + u * NT + tid] = st[u];
-    if (sp == 0 && tid < kCtBlocks * 32) kc_l[(ct & 1) * kCtBlocks * 32 + tid] = kst;
+    for (int u = 0; u < LPT; ++u) mu_l[buf * SO + u * NT + tid] = st[u];
+    if (sp == 0 && tid < CTB * 32) kc_l[(ct & 1) * CTB * 32 + tid] = kst;
   };
 
   // The wave's rows, dimensions 8q + 4g .. + 3 of chunk q (zero past D and N).
@@ -601,9 +605,9 @@ void diag_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, 
   commit(0, 0);
   lds_barrier();
 
-  f32x16 acc[kCtBlocks][kCtChains];
+  f32x16 acc[CTB][kCtChains];
 #pragma unroll
-  for (int b = 0; b < kCtBlocks; ++b) {
+  for (int b = 0; b < CTB; ++b) {
 #pragma unroll
     for (int h = 0; h < kCtChains; ++h) acc[b][h] = zero16();
   }
@@ -614,10 +618,10 @@ void diag_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, 
 
   // Component tile ct is complete: log-joint, log-sum-exp and need bounds per block.
   auto finish_tile = [&](int ct) __attribute__((always_inline)) {
-    const double* kp0 = kc_l + (ct & 1) * kCtBlocks * 32 + g * 16;
+    const double* kp0 = kc_l + (ct & 1) * CTB * 32 + g * 16;
 #pragma unroll
-    for (int b = 0; b < kCtBlocks; ++b) {
-      const int kb = ct * kCtBlocks + b;
+    for (int b = 0; b < CTB; ++b) {
+      const int kb = ct * CTB + b;
       if (kb < KB) {
         double ll[16];
         double bh[2] = {-INFINITY, -INFINITY};   // maxima of the half blocks (registers 0-7, 8-15)
@@ -666,12 +670,12 @@ void diag_lse_ctile(const float* __restrict__ X, int64_t ldx, int64_t N, int D, 
     const bool more = s + 1 < nstage;
     if (more) fetch(s + 1);
     xstage(s + 1, xr[1 - P]);
-    const bf16x8* mp = mu_l + P * kCtStageOps + lane;
+    const bf16x8* mp = mu_l + P * SO + lane;
     bf16x8 xb[2][3];
 #pragma unroll
     for (int qq = 0; qq < 2; ++qq) split3_bf16(xr[P][qq] * xr[P][qq], xr[P][qq], xb[qq]);
 #pragma unroll
-    for (int b = 0; b < kCtBlocks; ++b) {
+    for (int b = 0; b < CTB; ++b) {
       bf16x8 a[2][4];
 #pragma unroll
       for (int qq = 0; qq < 2; ++qq) {
@@ -1860,8 +1864,10 @@ hipError_t launch_ctile(const DiagPlan& pl, const float* X, int64_t ldx, unsigne
   const int NQ = pl.DP / 8;
   if (run1) {
     const bool exact = pl.rexact && !pl.lj;
-    const size_t lds1 = lse_ctile_base() + (exact ? (size_t)kCtWaves * 2 * 32 * pl.KB * 2 : 0);
-    auto kern = pl.lj ? &diag_lse_ctile<kLjmStore> : &diag_lse_ctile<kLjmNeed>;
+    const int ctb = ctile_blocks(pl.DP);
+    const size_t lds1 = lse_ctile_base(ctb) + (exact ? (size_t)kCtWaves * 2 * 32 * pl.KB * 2 : 0);
+    auto kern = pl.lj ? (ctb == 2 ? &diag_lse_ctile<kLjmStore, 2> : &diag_lse_ctile<kLjmStore, 4>)
+                      : (ctb == 2 ? &diag_lse_ctile<kLjmNeed, 2> : &diag_lse_ctile<kLjmNeed, 4>);
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
     if (e != hipSuccess) return e;
