@@ -288,7 +288,7 @@ def time_steps(call, steps, warmup, stream, dense=False):
 
 KERNELS = {
     # (kind, plan) -> (pass-1 kernel, pass-2 kernel)
-    ("iso", "default"): ("iso_lse (need masks)", "iso_accum_gather"),
+    ("iso", "default"): ("iso_lse (need masks)", "iso_accum_gather / iso_accum_tiles (by the needed-pair count)"),
     ("iso", "default_wide"): ("iso_lse_ctile (need masks)", "iso_accum_drange"),
     ("iso", "stored"): ("iso_lse (stores the log-joint)", "iso_accum_sparse / iso_accum_lj"),
     ("iso", "stored_wide"): ("iso_lse_ctile (stores the log-joint)", "iso_accum_lj"),
