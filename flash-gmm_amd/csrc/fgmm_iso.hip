@@ -1233,13 +1233,16 @@ void iso_accum_tiles(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 //   - wave (h, w) takes the 16 rows of step h (registers 8h .. 8h + 7 of S): their
 //     log-joint, r and residual, Nk and sig_acc, and their r^T X for all of D;
 //   - at the end the two waves' partials of a block are added in a fixed order.
-// Two waves per SIMD, so the waits of one overlap the other's matrix steps.
+// Two waves per SIMD, so the waits of one overlap the other's matrix steps.  The X
+// tiles are triple-buffered and the chain exchange double-buffered, so one barrier
+// per tile orders everything: tile t + 2 is written after it, into the buffer that
+// tile t - 1 left, which every wave finished before the barrier.
 // ---------------------------------------------------------------------------
 constexpr int kTileWaves2 = 2 * kTileBlocks;
 
 __host__ __device__ constexpr size_t tiles2_lds_bytes(int DP) {
-  return (size_t)2 * 3 * 32 * gather_rs(DP) * 2 + (size_t)2 * 32 * sizeof(double2) +
-         (size_t)kTileWaves2 * 4 * 64 * sizeof(f32x4);
+  return (size_t)3 * 3 * 32 * gather_rs(DP) * 2 + (size_t)3 * 32 * sizeof(double2) +
+         (size_t)2 * kTileWaves2 * 4 * 64 * sizeof(f32x4);
 }
 
 template <int DP>
@@ -1264,9 +1267,9 @@ void iso_accum_tiles2(const float* __restrict__ X, int64_t ldx, int64_t N, int D
   if (need_total(needcount) < dense_min) return;   // the gathering kernel runs (uniform exit)
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  __bf16* xs = reinterpret_cast<__bf16*>(lds_raw);                                   // [2][3][32][RS]
-  double2* rs_l = reinterpret_cast<double2*>(lds_raw + (size_t)2 * 3 * 32 * RS * 2);  // [2][32]
-  f32x4* ex = reinterpret_cast<f32x4*>(rs_l + 2 * 32);                                // [wave][4][64]
+  __bf16* xs = reinterpret_cast<__bf16*>(lds_raw);                                   // [3][3][32][RS]
+  double2* rs_l = reinterpret_cast<double2*>(lds_raw + (size_t)3 * 3 * 32 * RS * 2);  // [3][32]
+  f32x4* ex = reinterpret_cast<f32x4*>(rs_l + 3 * 32);                                // [2][wave][4][64]
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1353,21 +1356,25 @@ void iso_accum_tiles2(const float* __restrict__ X, int64_t ldx, int64_t N, int D
   for (int j = 0; j < NJ; ++j) acc[j] = zero16();
   float nk = 0.0f, sig = 0.0f;
   const bf16x8 ones = x6c_ones(lane);
-  f32x4* mine = ex + wave * 4 * 64 + lane;
-  const f32x4* ch0 = ex + w * 4 * 64 + lane;                       // chain 0 of the block
-  const f32x4* ch1 = ex + (kTileBlocks + w) * 4 * 64 + lane;       // chain 1
+  constexpr int EXB = kTileWaves2 * 4 * 64;                         // f32x4 per exchange buffer
 
-  if (t_begin < t_end) {
-    fetch(t_begin);
-    commit(0);
+  for (int p = 0; p < 2; ++p) {
+    if (t_begin + p < t_end) {
+      fetch(t_begin + p);
+      commit(p);
+    }
   }
   __syncthreads();
   for (int64_t t = t_begin; t < t_end; ++t) {
-    const int buf = (int)((t - t_begin) & 1);
-    const bool more = t + 1 < t_end;
-    if (more) fetch(t + 1);
+    const int it = (int)(t - t_begin);
+    const int buf = it % 3;
+    const bool more = t + 2 < t_end;
+    if (more) fetch(t + 2);
     const unsigned m = active ? (dense ? ~0u : need[t * KB + kb]) : 0u;   // the same for both waves
     const __bf16* xt = xs + (size_t)buf * 3 * 32 * RS;
+    f32x4* mine = ex + (it & 1) * EXB + wave * 4 * 64 + lane;
+    const f32x4* ch0 = ex + (it & 1) * EXB + w * 4 * 64 + lane;                   // chain 0 of the block
+    const f32x4* ch1 = ex + (it & 1) * EXB + (kTileBlocks + w) * 4 * 64 + lane;   // chain 1
     if (m != 0u) {
       // Chain h over the tile's rows: x6c_tile_rows' steps for the chunks q = 2u + h.
       f32x16 cacc = zero16();
@@ -1421,9 +1428,9 @@ void iso_accum_tiles2(const float* __restrict__ X, int64_t ldx, int64_t N, int D
         }
       }
     }
-    if (more) commit(buf ^ 1);
-    __syncthreads();
+    if (more) commit((it + 2) % 3);
   }
+  __syncthreads();   // the last tile's exchange has been read
 
   // The two waves' partials of a block, added in a fixed order (h = 0 first) by wave
   // (0, w) through LDS, one 32-column tile at a time.
