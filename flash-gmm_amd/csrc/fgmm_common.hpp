@@ -675,4 +675,35 @@ __host__ inline int current_device_cus() {
   return v;
 }
 
+// Gathering passes: one workgroup of W waves per (slab group of W row slabs,
+// component or component block), workgroup b running on XCD b % 8.  With 8 or more
+// slab groups each XCD serves whole groups, so all components of a group share that
+// XCD's L2 for the rows of X; with fewer, the XCDs that share a group split its
+// components (x % G serves group x % G, taking every c-th component).  The slab count
+// is rounded so that the group count is 1, 2, 4 or a multiple of 8: every XCD then
+// gets the same work.
+__host__ inline int64_t gather_slab_count(int64_t want, int64_t max_slabs, int W) {
+  const int64_t groups = cdiv(want < 1 ? 1 : want, W);
+  const int64_t g = groups <= 1 ? 1 : groups <= 2 ? 2 : groups <= 4 ? 4 : round_up(groups, 8);
+  const int64_t n = g * W;
+  return n < max_slabs ? n : max_slabs;
+}
+__host__ inline int64_t gather_item_grid(int G, int K) {
+  if (G >= 8) return cdiv(G, 8) * (int64_t)K * 8;
+  return 8 * cdiv(K, 8 / (G < 1 ? 1 : G));
+}
+// (slab group sg, component k) of workgroup b; false for a workgroup with no item.
+__device__ __forceinline__ bool gather_item(unsigned b, int G, int K, int& sg, int& k) {
+  const int x = (int)(b & 7u), i = (int)(b >> 3);
+  if (G >= 8) {
+    k = i % K;
+    sg = (i / K) * 8 + x;
+    return sg < G;
+  }
+  sg = x % G;
+  const int c = (8 - sg + G - 1) / G;   // XCDs serving group sg
+  k = x / G + i * c;
+  return k < K;
+}
+
 }  // namespace fgmm

@@ -51,6 +51,7 @@ __host__ inline int diag_padded_dim(int64_t D) {
   return D <= 128 ? (int)round_up(D < 1 ? 1 : D, 32) : (int)round_up(D, 64);
 }
 constexpr int kCtWaves = 4;                               // waves per workgroup, one per SIMD
+constexpr int kGatherWaves = 4;                           // waves (row slabs) per gathering workgroup
 constexpr int kCtChains = 4;                              // accumulation chains (chunk q -> q % 4)
 constexpr int kDrange = 1024;                             // dimensions of r^T [X | X^2] per pass-2 workgroup
 constexpr int kDrTiles = kDrange / 32 / kCtWaves;         // 32-column tiles per pass-2 wave
@@ -160,10 +161,9 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
     p.rows_per_slab = round_up(cdiv(N, want), 32);
     p.nslab = (int)cdiv(N, p.rows_per_slab);
   } else if (p.need && N > 0 && p.KB > 0) {
-    // The gathering pass 2 runs one wave per SIMD: about two rounds of waves.
-    int64_t want = cdiv((int64_t)8 * current_device_cus(), p.KB);
-    const int64_t max_slabs = cdiv(N, 32);
-    if (want > max_slabs) want = max_slabs;
+    // The gathering pass 2: eight waves per compute unit, two rounds at one wave per
+    // SIMD (one round where two fit).
+    const int64_t want = gather_slab_count(cdiv((int64_t)8 * current_device_cus(), p.KB), cdiv(N, 32), kGatherWaves);
     p.rows_per_slab = round_up(cdiv(N, want), 32);
     p.nslab = (int)cdiv(N, p.rows_per_slab);
   } else if (N > 0 && p.ncg > 0) {
@@ -1392,7 +1392,6 @@ __host__ size_t x6_lds_bytes_rt(int DP) {
 // (steps whose 64 responsibilities are all zero are skipped).  sig follows in
 // diag_reduce from the moments.
 // ---------------------------------------------------------------------------
-constexpr int kGatherWaves = 4;
 
 __host__ __device__ constexpr int gather_rs(int DP) { return DP + 8; }   // fp32 row stride of the X tiles
 
@@ -1403,7 +1402,7 @@ __host__ __device__ constexpr size_t gather_lds_bytes(int DP) {
          + (size_t)kGatherWaves * 64 * sizeof(int);                // row queue per wave
 }
 __host__ __device__ constexpr int gather_groups(int nslab) { return (nslab + kGatherWaves - 1) / kGatherWaves; }
-__host__ inline int64_t gather_grid(int nslab, int KB) { return cdiv(gather_groups(nslab), 8) * (int64_t)KB * 8; }
+__host__ inline int64_t gather_grid(int nslab, int KB) { return gather_item_grid(gather_groups(nslab), KB); }
 
 // Waves per SIMD of the gathering pass: two where a wave's registers and the
 // workgroup's LDS allow it (D <= 32), so one wave's row loads overlap the other's
@@ -1435,10 +1434,8 @@ void diag_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, g = lane >> 5;
-  const int rest = (int)(blockIdx.x >> 3);
-  const int kb = rest % KB;
-  const int sg = (rest / KB) * 8 + (int)(blockIdx.x & 7);
-  if (sg >= gather_groups(nslab)) return;   // uniform over the workgroup
+  int sg, kb;
+  if (!gather_item(blockIdx.x, gather_groups(nslab), KB, sg, kb)) return;   // uniform over the workgroup
   for (int idx = tid; idx < BLK; idx += 64 * kGatherWaves) mu_l[idx] = mu3[(int64_t)kb * BLK + idx];
   __syncthreads();
   const int slab = sg * kGatherWaves + wave;

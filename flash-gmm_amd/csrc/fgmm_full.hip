@@ -36,6 +36,7 @@ namespace fgmm {
 namespace {
 
 constexpr int kWaves = 4;
+constexpr int kGatherWaves = 4;                           // waves (row slabs) per gathering workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kAccWaves = 8;
 constexpr int kAccThreads = 64 * kAccWaves;
@@ -117,9 +118,7 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   if (p.need && N > 0) {
     // The gathering pass 2: about two rounds of waves at two waves per SIMD (each
     // slab holds a partial of D x D per component, so no more slabs than that).
-    int64_t want = cdiv((int64_t)8 * current_device_cus(), K * p.ngrp);
-    const int64_t max_slabs = cdiv(N, 32);
-    if (want > max_slabs) want = max_slabs;
+    const int64_t want = gather_slab_count(cdiv((int64_t)8 * current_device_cus(), K * p.ngrp), cdiv(N, 32), kGatherWaves);
     p.rows_per_slab = round_up(cdiv(N, want), 32);
     p.nslab = (int)cdiv(N, p.rows_per_slab);
   } else if (N > 0 && p.ncg > 0) {
@@ -695,13 +694,14 @@ __global__ __launch_bounds__(256) void full_fill(float* __restrict__ p, int64_t 
 // so maha and the log-joint are pass 1's), forms r = 2^(ll2 - logZ2), and then
 // accumulates Nk, mu_acc and the upper 32x32 blocks of sig_outer = sum r x x^T as
 // full_accum does (r-scaled rows as the A operand of fp32 32x32x2 steps, only the
-// steps with a nonzero row).  Workgroups map to the 8 XCDs so that every component
-// of a slab group shares an XCD's L2 for the rows of X.  Above D = 128 the upper
+// steps with a nonzero row).  Workgroups are dealt to the 8 XCDs by gather_item: the
+// components of a slab group share an XCD's L2 for the rows of X where there are 8
+// or more groups, and split over the XCDs that share a group where there are fewer.
+// Above D = 128 the upper
 // blocks are dealt to gather_sig_groups(DP) launches, GRP = 0, 1, ..., each
 // accumulating a contiguous run of blocks (GRP 0 also mu_acc and Nk) after the same
 // whitening.
 // ---------------------------------------------------------------------------
-constexpr int kGatherWaves = 4;
 
 // Up to D = 96 the component's operands (32 KB at D = 64, 72 KB at 96) sit in LDS;
 // at D = 128 (128 KB) they are read from the workspace (L2) by each wave.  Above
@@ -718,7 +718,7 @@ constexpr size_t gather_lds_bytes() {
          + (size_t)kGatherWaves * 64 * sizeof(int);                  // row queue per wave
 }
 __host__ __device__ constexpr int gather_groups(int nslab) { return (nslab + kGatherWaves - 1) / kGatherWaves; }
-__host__ inline int64_t gather_grid(int nslab, int K) { return cdiv(gather_groups(nslab), 8) * (int64_t)K * 8; }
+__host__ inline int64_t gather_grid(int nslab, int K) { return gather_item_grid(gather_groups(nslab), K); }
 
 template <int DP, int GRP>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * kGatherWaves, 64 * kGatherWaves),
@@ -751,10 +751,8 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, g = lane >> 5;
-  const int rest = (int)(blockIdx.x >> 3);
-  const int k = rest % K;
-  const int sg = (rest / K) * 8 + (int)(blockIdx.x & 7);
-  if (sg >= gather_groups(nslab)) return;   // uniform over the workgroup
+  int sg, k;
+  if (!gather_item(blockIdx.x, gather_groups(nslab), K, sg, k)) return;   // uniform over the workgroup
   if constexpr (OPS_LDS)
     for (int idx = tid; idx < BLK; idx += 64 * kGatherWaves) l_l[idx] = l3[(int64_t)k * BLK + idx];
   for (int idx = tid; idx <= DP; idx += 64 * kGatherWaves) e_l[idx] = idx < DP ? esw[(int64_t)k * DP + idx] : ck[k];
