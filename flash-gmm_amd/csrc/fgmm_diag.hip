@@ -1388,12 +1388,17 @@ __host__ size_t x6_lds_bytes_rt(int DP) {
 // queued rows: the rows of X (fp32) go to the wave's LDS tile; S = [x^2, x] . [-w, 2v]^T
 // is formed as pass 1 forms it, the two halves' chains (x6c_tile_rows_fn, two chains
 // each) added in fp32, so the log-joint C'_k + S equals pass 1's; r = 2^(ll2 - logZ2),
-// Nk on the VALU, and r^T [X | X^2] on fp32 32x32x2 steps with r as the A operand
-// (steps whose 64 responsibilities are all zero are skipped).  sig follows in
+// Nk on the VALU, and r^T [X | X^2] on the bf16 matrix cores with r as the A operand:
+// r, x and x^2 split exactly into three bf16 values each and the six products of
+// significance at least 2^-16 accumulated smallest first (error near an fp32 step's,
+// which the sig identity needs), 16 rows per step (steps whose 16 rows carry no
+// responsibility are skipped).  sig follows in
 // diag_reduce from the moments.
 // ---------------------------------------------------------------------------
 
-__host__ __device__ constexpr int gather_rs(int DP) { return DP + 8; }   // fp32 row stride of the X tiles
+// fp32 row stride of the X tiles: rows 8 apart (the two lane-halves of a B operand)
+// and the 16-byte row accesses of the contraction fall in distinct banks.
+__host__ __device__ constexpr int gather_rs(int DP) { return DP + 4; }
 
 __host__ __device__ constexpr size_t gather_lds_bytes(int DP) {
   return (size_t)(DP / 8) * 4 * 64 * 16                          // mu block (bf16x8 operands)
@@ -1551,17 +1556,48 @@ void diag_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
       r[i] = rv;
       nk += rv;
     }
-    const float* xbase = xt + 4 * g * RS + c;
+    // r = r1 + r2 + r3 (exact), as A operands of the two 16-row steps.
+    bf16x8 a1[2], a2[2], a3[2];
+    {
+      float d1[16], d2[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int ro = 8 * (i >> 2) + (i & 3);
-      if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
+      for (int i = 0; i < 16; ++i) {
+        d1[i] = r[i] - (float)(__bf16)r[i];
+        d2[i] = d1[i] - (float)(__bf16)d1[i];
+      }
+      acc_to_row_operands(r, a1);
+      acc_to_row_operands(d1, a2);
+      acc_to_row_operands(d2, a3);
+    }
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const float xv = xbase[ro * RS + 32 * j];
-          accx[j] = mfma32(r[i], xv, accx[j]);
-          accq[j] = mfma32(r[i], xv * xv, accq[j]);
-        }
+    for (int p = 0; p < 2; ++p) {
+      bool any = false;
+#pragma unroll
+      for (int i = 8 * p; i < 8 * p + 8; ++i) any = any || r[i] != 0.0f;
+      if (!dense && __builtin_amdgcn_ballot_w64(any) == 0) continue;
+      // B operands: rows 16p + 8g + e of column 32j + c, and their squares.
+      const float* xb = xt + (16 * p + 8 * g) * RS + c;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = xb[e * RS + 32 * j];
+        bf16x8 bx[3], bq[3];
+        split3_bf16(f32x4{v[0], v[1], v[2], v[3]}, f32x4{v[4], v[5], v[6], v[7]}, bx);
+        split3_bf16(f32x4{v[0] * v[0], v[1] * v[1], v[2] * v[2], v[3] * v[3]},
+                    f32x4{v[4] * v[4], v[5] * v[5], v[6] * v[6], v[7] * v[7]}, bq);
+        accx[j] = mfma_bf16(a3[p], bx[0], accx[j]);
+        accx[j] = mfma_bf16(a2[p], bx[1], accx[j]);
+        accx[j] = mfma_bf16(a1[p], bx[2], accx[j]);
+        accx[j] = mfma_bf16(a2[p], bx[0], accx[j]);
+        accx[j] = mfma_bf16(a1[p], bx[1], accx[j]);
+        accx[j] = mfma_bf16(a1[p], bx[0], accx[j]);
+        accq[j] = mfma_bf16(a3[p], bq[0], accq[j]);
+        accq[j] = mfma_bf16(a2[p], bq[1], accq[j]);
+        accq[j] = mfma_bf16(a1[p], bq[2], accq[j]);
+        accq[j] = mfma_bf16(a2[p], bq[0], accq[j]);
+        accq[j] = mfma_bf16(a1[p], bq[1], accq[j]);
+        accq[j] = mfma_bf16(a1[p], bq[0], accq[j]);
       }
     }
     cnt = cnt_next;
