@@ -692,9 +692,9 @@ __global__ __launch_bounds__(256) void full_fill(float* __restrict__ p, int64_t 
 // per tile of 32 queued rows it stages the rows of X in its LDS tile, whitens them
 // as pass 1 does (x6c_tile over the coordinate blocks, the same operands and order,
 // so maha and the log-joint are pass 1's), forms r = 2^(ll2 - logZ2), and then
-// accumulates Nk, mu_acc and the upper 32x32 blocks of sig_outer = sum r x x^T as
-// full_accum does (r-scaled rows as the A operand of fp32 32x32x2 steps, only the
-// steps with a nonzero row).  Workgroups are dealt to the 8 XCDs by gather_item: the
+// accumulates Nk, mu_acc and the upper 32x32 blocks of sig_outer = sum r x x^T
+// (r-scaled rows as the A operand of six split-bf16 products per 16 rows, only the
+// 16-row steps with a nonzero row).  Workgroups are dealt to the 8 XCDs by gather_item: the
 // components of a slab group share an XCD's L2 for the rows of X where there are 8
 // or more groups, and split over the XCDs that share a group where there are fewer.
 // Above D = 128 the upper
@@ -891,28 +891,50 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
       rx[c] = rv;
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    // sig_outer[d1][d2] += sum_rows (r x_d1) x_d2, as full_accum: step s takes rows
-    // r0 + 4g (r0 = 8 (s >> 2) + (s & 3)); only the steps with a nonzero row.
+    // sig_outer[d1][d2] += sum_rows (r x_d1) x_d2 on the bf16 matrix cores, 16 rows per
+    // step: a = r x (fp32, as an fp32 step forms it) and x split exactly into three
+    // bf16 values each, the six products of significance at least 2^-16 added smallest
+    // first (error near an fp32 step's).  Lane (c, g) of step p holds rows
+    // 16p + 8g + e of column c of each 32-coordinate block; steps whose 16 rows carry
+    // no responsibility are skipped.
     const unsigned nz = (unsigned)__builtin_amdgcn_ballot_w64(rv != 0.0f);
-    unsigned pm = dense ? 0x0f0f0f0fu : lj_pair_mask(nz);
-    while (pm != 0u) {
-      const int r0 = __builtin_ctz(pm);
-      pm &= pm - 1u;
-      const int rw = r0 + 4 * g;
-      const float rr = rx[rw];
-      float xv[NMB], av[NMB];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if (!dense && ((nz >> (16 * p)) & 0xffffu) == 0u) continue;
+      const int rb = 16 * p + 8 * g;
+      float rr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rr[e] = rx[rb + e];
+      bf16x8 bx[NMB][3], ba[NMB][3];
 #pragma unroll
       for (int mb = 0; mb < NMB; ++mb) {
-        xv[mb] = xt[rw * RS + 32 * mb + c];
-        av[mb] = rr * xv[mb];
-        if constexpr (FIRST) mua[mb] += av[mb];
+        float v[8], a[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          v[e] = xt[(rb + e) * RS + 32 * mb + c];
+          a[e] = rr[e] * v[e];
+        }
+        if constexpr (FIRST) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) mua[mb] += a[e];
+        }
+        split3_bf16(f32x4{v[0], v[1], v[2], v[3]}, f32x4{v[4], v[5], v[6], v[7]}, bx[mb]);
+        split3_bf16(f32x4{a[0], a[1], a[2], a[3]}, f32x4{a[4], a[5], a[6], a[7]}, ba[mb]);
       }
 #pragma unroll
       for (int m1 = 0; m1 < NMB; ++m1) {
 #pragma unroll
         for (int m2 = m1; m2 < NMB; ++m2) {
           const int sb = m1 * NMB - m1 * (m1 - 1) / 2 + (m2 - m1);   // upper-block index of (m1, m2)
-          if (sb >= SB0 && sb < SB1) acc[sb - SB0] = mfma32(av[m1], xv[m2], acc[sb - SB0]);
+          if (sb >= SB0 && sb < SB1) {
+            f32x16& t = acc[sb - SB0];
+            t = mfma_bf16(ba[m1][2], bx[m2][0], t);
+            t = mfma_bf16(ba[m1][1], bx[m2][1], t);
+            t = mfma_bf16(ba[m1][0], bx[m2][2], t);
+            t = mfma_bf16(ba[m1][1], bx[m2][0], t);
+            t = mfma_bf16(ba[m1][0], bx[m2][1], t);
+            t = mfma_bf16(ba[m1][0], bx[m2][0], t);
+          }
         }
       }
     }
