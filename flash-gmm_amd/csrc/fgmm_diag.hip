@@ -67,7 +67,9 @@ __host__ __device__ constexpr size_t lse_ctile_base(int CTB) {
 __host__ __device__ constexpr int ctile_need_exact_cap(int CTB) {
   return (int)((kMaxLds - lse_ctile_base(CTB)) / (kCtWaves * 2 * 32 * 2));
 }
-__host__ __device__ constexpr int drange_rs(int DR) { return DR + 8; }   // fp32 row stride of the X tile
+// fp32 row stride of the X tile: rows 8 apart (the lane-halves of a B operand) and the
+// 16-byte row writes fall in distinct banks.
+__host__ __device__ constexpr int drange_rs(int DR) { return DR + 4; }
 __host__ __device__ constexpr size_t accum_drange_lds_bytes(int DR) {
   return (size_t)32 * drange_rs(DR) * sizeof(float)         // X of 32 rows
          + (size_t)kCtWaves * 16 * 64 * sizeof(float)        // the four chains of S
@@ -1625,9 +1627,9 @@ void diag_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
 // on [x^2, x]) and stores the fp32 rows of its chunks in the range to the LDS tile;
 // the chains meet in LDS and every wave adds them as pass 1 does, so the log-joint
 // C'_k + S equals pass 1's bit for bit; r = 2^(ll2 - logZ2), and each wave
-// accumulates r^T X and r^T X^2 for a quarter of the range's 32-column tiles on fp32
-// 32x32x2 steps (the sig identity in diag_reduce cancels, so these moments keep
-// fp32 accuracy).  Wave 0 of the first range also sums Nk.
+// accumulates r^T X and r^T X^2 for a quarter of the range's 32-column tiles as six
+// split-bf16 products per 16 rows (the sig identity in diag_reduce cancels, so these
+// moments keep an fp32 step's accuracy).  Wave 0 of the first range also sums Nk.
 // ---------------------------------------------------------------------------
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * kCtWaves, 64 * kCtWaves), amdgpu_waves_per_eu(1, 1)))
 void diag_accum_drange(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int NQ, int DP,
@@ -1788,18 +1790,48 @@ void diag_accum_drange(const float* __restrict__ X, int64_t ldx, int64_t N, int 
       r[i] = rv;
       nk += rv;
     }
-    const float* xbase = xt + 4 * g * RS + c;
+    // r^T [X | X^2] as diag_accum_gather forms it: six split-bf16 products per 16 rows.
+    bf16x8 a1[2], a2[2], a3[2];
+    {
+      float d1[16], d2[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int ro = 8 * (i >> 2) + (i & 3);
-      if (dense || __builtin_amdgcn_ballot_w64(r[i] != 0.0f) != 0) {
+      for (int i = 0; i < 16; ++i) {
+        d1[i] = r[i] - (float)(__bf16)r[i];
+        d2[i] = d1[i] - (float)(__bf16)d1[i];
+      }
+      acc_to_row_operands(r, a1);
+      acc_to_row_operands(d1, a2);
+      acc_to_row_operands(d2, a3);
+    }
 #pragma unroll
-        for (int jj = 0; jj < kDrTiles; ++jj) {
-          if (jj < nj) {
-            const float xv = xbase[ro * RS + 32 * (j0 + jj)];
-            accx[jj] = mfma32(r[i], xv, accx[jj]);
-            accq[jj] = mfma32(r[i], xv * xv, accq[jj]);
-          }
+    for (int p = 0; p < 2; ++p) {
+      bool any = false;
+#pragma unroll
+      for (int i = 8 * p; i < 8 * p + 8; ++i) any = any || r[i] != 0.0f;
+      if (!dense && __builtin_amdgcn_ballot_w64(any) == 0) continue;
+      const float* xb = xt + (16 * p + 8 * g) * RS + c;
+#pragma unroll
+      for (int jj = 0; jj < kDrTiles; ++jj) {
+        if (jj < nj) {
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = xb[e * RS + 32 * (j0 + jj)];
+          bf16x8 bx[3], bq[3];
+          split3_bf16(f32x4{v[0], v[1], v[2], v[3]}, f32x4{v[4], v[5], v[6], v[7]}, bx);
+          split3_bf16(f32x4{v[0] * v[0], v[1] * v[1], v[2] * v[2], v[3] * v[3]},
+                      f32x4{v[4] * v[4], v[5] * v[5], v[6] * v[6], v[7] * v[7]}, bq);
+          accx[jj] = mfma_bf16(a3[p], bx[0], accx[jj]);
+          accx[jj] = mfma_bf16(a2[p], bx[1], accx[jj]);
+          accx[jj] = mfma_bf16(a1[p], bx[2], accx[jj]);
+          accx[jj] = mfma_bf16(a2[p], bx[0], accx[jj]);
+          accx[jj] = mfma_bf16(a1[p], bx[1], accx[jj]);
+          accx[jj] = mfma_bf16(a1[p], bx[0], accx[jj]);
+          accq[jj] = mfma_bf16(a3[p], bq[0], accq[jj]);
+          accq[jj] = mfma_bf16(a2[p], bq[1], accq[jj]);
+          accq[jj] = mfma_bf16(a1[p], bq[2], accq[jj]);
+          accq[jj] = mfma_bf16(a2[p], bq[0], accq[jj]);
+          accq[jj] = mfma_bf16(a1[p], bq[1], accq[jj]);
+          accq[jj] = mfma_bf16(a1[p], bq[0], accq[jj]);
         }
       }
     }
