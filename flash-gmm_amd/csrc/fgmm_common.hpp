@@ -675,6 +675,85 @@ __host__ inline int current_device_cus() {
   return v;
 }
 
+// One step of a gathering pass's row queue (a 64-entry ring in LDS, q_l[pos & 63],
+// with qt - qh < 32 rows waiting): w is the need word of tile base / 32 + lane of the
+// current batch (0 for words already taken, lanes below jn), nz the ballot of w != 0.
+// A first word with 8 or more rows is queued by 32 lanes at once, one row each; a run
+// of sparser words is queued in one go, each lane writing the rows of its own word
+// after a prefix sum of the counts, as many words as the ring holds.  Either way the
+// rows go in tile order and, within a word, in bit order, and qt and jn advance past
+// the words taken.
+__device__ __forceinline__ void queue_words(unsigned w, uint64_t nz, int base, int lane, int c, int g,
+                                            int* q_l, int& qt, int& jn) {
+  const int pc = __builtin_popcount(w);
+  const uint64_t big = __builtin_amdgcn_ballot_w64(pc >= 8);
+  const int j = __builtin_ctzll(nz);
+  if ((big >> j) & 1ull) {
+    const unsigned m = __builtin_amdgcn_readlane(w, j);
+    if (g == 0 && ((m >> c) & 1u)) q_l[(qt + __builtin_popcount(m & ((1u << c) - 1u))) & 63] = base + 32 * j + c;
+    qt += __builtin_popcount(m);
+    jn = j + 1;
+    return;
+  }
+  // Words before the next dense one; word j (fewer than 8 rows) always fits, since
+  // the ring has more than 32 free entries.
+  const int lim = big != 0ull ? __builtin_ctzll(big) : 64;
+  int incl = pc;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o);
+    if (lane >= o) incl += v;
+  }
+  const bool take = lane >= jn && lane < lim && incl <= 64 - 32;
+  const uint64_t tm = __builtin_amdgcn_ballot_w64(take);
+  const int jl = 64 - __builtin_clzll(tm);
+  if (take) {
+    unsigned m = w;
+    int pos = qt + incl - pc;
+    while (m != 0u) {
+      q_l[pos & 63] = base + 32 * lane + __builtin_ctz(m);
+      ++pos;
+      m &= m - 1u;
+    }
+  }
+  qt += __builtin_amdgcn_readlane(incl, jl - 1);
+  jn = jl;
+}
+
+// Fill a gathering pass's row queue until 32 rows wait or the slab's tiles run out.
+// words(tb) loads the need word of tile tb + lane (0 past the slab); mword holds the
+// current batch of 64 words, mnext the next, jn the first word not yet taken.  PAR
+// selects queue_words' prefix-sum step; without it one word is queued per step (for
+// kernels whose registers are too tight for the prefix sum).
+template <bool PAR, typename Words>
+__device__ __forceinline__ void queue_fill(Words words, int64_t& tb, int64_t t_begin, int64_t t_end,
+                                           unsigned& mword, unsigned& mnext, int& jn, int& qt, int qh,
+                                           int lane, int c, int g, int* q_l) {
+  while (qt - qh < 32) {
+    const unsigned w = (PAR && lane >= jn) ? mword : 0u;
+    const uint64_t live = jn >= 64 ? 0ull : (~0ull << jn);
+    const uint64_t nz = PAR ? __builtin_amdgcn_ballot_w64(w != 0u) : __builtin_amdgcn_ballot_w64(mword != 0u) & live;
+    if (nz == 0) {
+      tb += 64;
+      if (tb >= t_end) break;
+      mword = mnext;
+      mnext = words(tb + 64);
+      jn = 0;
+      continue;
+    }
+    if constexpr (PAR) {
+      queue_words(w, nz, (int)(tb - t_begin) * 32, lane, c, g, q_l, qt, jn);
+    } else {
+      const int j = __builtin_ctzll(nz);
+      const unsigned m = __builtin_amdgcn_readlane(mword, j);
+      const int base = (int)((tb + j - t_begin) * 32);
+      if (g == 0 && ((m >> c) & 1u)) q_l[(qt + __builtin_popcount(m & ((1u << c) - 1u))) & 63] = base + c;
+      qt += __builtin_popcount(m);
+      jn = j + 1;
+    }
+  }
+}
+
 // Gathering passes: one workgroup of W waves per (slab group of W row slabs,
 // component or component block), workgroup b running on XCD b % 8.  With 8 or more
 // slab groups each XCD serves whole groups, so all components of a group share that

@@ -779,24 +779,7 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   int jn = 0;
   int qh = 0, qt = 0;
   auto take = [&](int& e) -> int {
-    while (qt - qh < 32) {
-      const uint64_t live = jn >= 64 ? 0ull : (~0ull << jn);
-      const uint64_t nz = __builtin_amdgcn_ballot_w64(mword != 0u) & live;
-      if (nz == 0) {
-        tb += 64;
-        if (tb >= t_end) break;
-        mword = mnext;
-        mnext = words(tb + 64);
-        jn = 0;
-        continue;
-      }
-      const int j = __builtin_ctzll(nz);
-      const unsigned m = __builtin_amdgcn_readlane(mword, j);
-      const int base = (int)((tb + j - t_begin) * 32);
-      if (g == 0 && ((m >> c) & 1u)) q_l[(qt + __builtin_popcount(m & ((1u << c) - 1u))) & 63] = base + c;
-      qt += __builtin_popcount(m);
-      jn = j + 1;
-    }
+    queue_fill<(DP > 32)>(words, tb, t_begin, t_end, mword, mnext, jn, qt, qh, lane, c, g, q_l);
     const int cnt = qt - qh < 32 ? qt - qh : 32;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     e = c < cnt ? q_l[(qh + c) & 63] : -1;

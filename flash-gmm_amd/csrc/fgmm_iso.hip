@@ -872,26 +872,9 @@ void iso_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D
 
   // Queue rows until 32 are waiting (or the slab ends) and take up to 32 of them:
   // returns the count (uniform); lane c of both halves gets tile row c's offset in
-  // the slab, or -1.
+  // the slab, or -1.  Rows are queued in tile order, each word's rows in bit order.
   auto take = [&](int& e) -> int {
-    while (qt - qh < 32) {
-      const uint64_t live = jn >= 64 ? 0ull : (~0ull << jn);
-      const uint64_t nz = __builtin_amdgcn_ballot_w64(mword != 0u) & live;
-      if (nz == 0) {
-        tb += 64;
-        if (tb >= t_end) break;
-        mword = mnext;
-        mnext = words(tb + 64);
-        jn = 0;
-        continue;
-      }
-      const int j = __builtin_ctzll(nz);
-      const unsigned m = __builtin_amdgcn_readlane(mword, j);
-      const int base = (int)((tb + j - t_begin) * 32);
-      if (g == 0 && ((m >> c) & 1u)) q_l[(qt + __builtin_popcount(m & ((1u << c) - 1u))) & 63] = base + c;
-      qt += __builtin_popcount(m);
-      jn = j + 1;
-    }
+    queue_fill<(DP > 64)>(words, tb, t_begin, t_end, mword, mnext, jn, qt, qh, lane, c, g, q_l);
     const int cnt = qt - qh < 32 ? qt - qh : 32;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     e = c < cnt ? q_l[(qh + c) & 63] : -1;
@@ -1535,24 +1518,7 @@ void iso_accum_drange(const float* __restrict__ X, int64_t ldx, int64_t N, int D
   // returns the count (the same in every wave); lane c of both halves gets tile row
   // c's offset in the slab, or -1.
   auto take = [&](int& e) -> int {
-    while (qt - qh < 32) {
-      const uint64_t live = jn >= 64 ? 0ull : (~0ull << jn);
-      const uint64_t nz = __builtin_amdgcn_ballot_w64(mword != 0u) & live;
-      if (nz == 0) {
-        tb += 64;
-        if (tb >= t_end) break;
-        mword = mnext;
-        mnext = words(tb + 64);
-        jn = 0;
-        continue;
-      }
-      const int j = __builtin_ctzll(nz);
-      const unsigned m = __builtin_amdgcn_readlane(mword, j);
-      const int base = (int)((tb + j - t_begin) * 32);
-      if (g == 0 && ((m >> c) & 1u)) q_l[(qt + __builtin_popcount(m & ((1u << c) - 1u))) & 63] = base + c;
-      qt += __builtin_popcount(m);
-      jn = j + 1;
-    }
+    queue_fill<true>(words, tb, t_begin, t_end, mword, mnext, jn, qt, qh, lane, c, g, q_l);
     const int cnt = qt - qh < 32 ? qt - qh : 32;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     e = c < cnt ? q_l[(qh + c) & 63] : -1;
