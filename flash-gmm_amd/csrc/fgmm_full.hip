@@ -89,6 +89,7 @@ __host__ __device__ constexpr int full_waves_per_eu(int DP) { return DP <= 128 ?
 
 // Pass-2 layout of the bf16 contract (defined with its kernels below).
 __host__ __device__ constexpr int bf16_comps_per_wg(int NMB);
+__host__ __device__ constexpr int bf16_comp_reps(int NMB);
 __host__ __device__ constexpr int bf16_row_groups(int NMB);
 
 FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool bf16 = false) {
@@ -105,7 +106,7 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.rexact = p.need && K <= kNeedExactMaxK;
   p.ngrp = gather_sig_groups(p.DP);
   if (bf16) {
-    p.ncg = p.KP / bf16_comps_per_wg(p.NMB);
+    p.ncg = (int)cdiv(K, (int64_t)bf16_comps_per_wg(p.NMB) * bf16_comp_reps(p.NMB));
     p.rgroups = bf16_row_groups(p.NMB);
   } else if (p.need) {
     p.ncg = (int)K;   // one wave per (row slab, component)
@@ -1181,6 +1182,9 @@ __global__ __launch_bounds__(kThreads) void full_bf16_lse(const float* __restric
 // sig_outer and all NMB column blocks), components per workgroup and row groups so
 // that the 8 waves are used (D = 96: 6 of them).
 __host__ __device__ constexpr int bf16_comps_per_wg(int NMB) { return NMB <= 2 ? 4 : 2; }
+// Components per wave: each wave accumulates its column block for this many
+// components from one staged X tile (their sig blocks take 64 or 128 registers).
+__host__ __device__ constexpr int bf16_comp_reps(int NMB) { return NMB <= 2 ? 4 : 2; }
 __host__ __device__ constexpr int bf16_row_groups(int NMB) { return NMB == 1 ? 2 : 1; }
 
 // Row strides of pass 2's X tiles: fp32 DP + 4 words (rows r and r + 8 of one column,
@@ -1196,7 +1200,7 @@ constexpr size_t bf16_accum_lds_bytes() {
   return (size_t)2 * TR * bf16_xf_stride(DP) * sizeof(float)   // X tiles, fp32, row-major
          + (size_t)2 * TR * bf16_xh_stride(DP) * 2             // X tiles, bf16, row-major
          + (size_t)2 * TR * sizeof(float)                      // logZ2
-         + (size_t)kAccWaves * 32 * sizeof(float);             // r per wave
+         + (size_t)bf16_row_groups(NMB) * bf16_comps_per_wg(NMB) * bf16_comp_reps(NMB) * 32 * sizeof(float);   // r
 }
 
 // The X tiles are loaded coalesced and held row-major in LDS, in fp32 (for r x, which
@@ -1226,26 +1230,33 @@ void full_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
-  // wave = (rg * NMB + mb2) * CPWG + cw
+  // wave = (rg * NMB + mb2) * CPWG + cw; wave cw serves the Q components cw Q + qi of the
+  // workgroup's CQ = CPWG Q.
+  constexpr int Q = bf16_comp_reps(NMB), CQ = CPWG * Q;
+  static_assert(CQ <= 32, "components of the mu_acc step");
   const bool in_use = wave < CPWG * NMB * RG;     // D = 96 leaves two waves idle
   const int cw = wave % CPWG, mb2 = (wave / CPWG) % NMB, rg = in_use ? wave / (CPWG * NMB) : 0;
   const int slab = blockIdx.x % nslab;
   const int cg = blockIdx.x / nslab;
-  const int k = cg * CPWG + cw;
-  const bool active = in_use && k < K;
+  const int k0 = cg * CQ + cw * Q;                // this wave's first component
+  const bool active = in_use && k0 < K;
   const bool mu_wave = in_use && cw == 0;         // also accumulates mu_acc block mb2
-  auto r_wave = [&](int comp) { return (rg * NMB) * CPWG + comp; };   // mb2 = 0 wave of comp
 
   const int64_t r_begin = (int64_t)slab * rows_per_slab;
   int64_t r_end = r_begin + rows_per_slab;
   if (r_end > N) r_end = N;
   const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, TR) : 0;
 
-  f32x16 acc[NMB];
+  f32x16 acc[Q][NMB];
 #pragma unroll
-  for (int mb = 0; mb < NMB; ++mb) acc[mb] = zero16();
+  for (int qi = 0; qi < Q; ++qi) {
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) acc[qi][mb] = zero16();
+  }
   f32x16 macc = zero16();
-  float nk = 0.0f;
+  float nk[Q];
+#pragma unroll
+  for (int qi = 0; qi < Q; ++qi) nk[qi] = 0.0f;
 
   f32x4 stage[LPT];
   float rstage = INFINITY;
@@ -1292,34 +1303,44 @@ void full_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     if (tid < TR) rs[buf * TR + tid] = rstage;
   };
 
-  // This wave's component's stored log-joint for row c of tile t (0 past the slab,
-  // where logZ2 = +inf makes r = 0); loaded one tile ahead.
-  auto lj_of = [&](int t) -> float {
+  // The stored log-joint of component k0 + qi for row c of tile t (0 past the slab or
+  // past K, where logZ2 = +inf or the skipped store leave r = 0); loaded one tile ahead.
+  // The mb2 = 0 wave of each component set forms r for the workgroup.
+  const bool r_maker = active && mb2 == 0;
+  auto lj_of = [&](int t, int qi) -> float {
     const int64_t row0 = r_begin + (int64_t)t * TR + rg * 32;
-    return (active && row0 < r_end) ? lj[((row0 >> 5) * KP + k) * 32 + c] : 0.0f;
+    return (r_maker && k0 + qi < K && row0 < r_end) ? lj[((row0 >> 5) * KP + k0 + qi) * 32 + c] : 0.0f;
   };
-  float lnext = 0.0f;
+  float lnext[Q];
+#pragma unroll
+  for (int qi = 0; qi < Q; ++qi) lnext[qi] = 0.0f;
   if (ntiles > 0) {
     fetch(0);
-    lnext = lj_of(0);
+#pragma unroll
+    for (int qi = 0; qi < Q; ++qi) lnext[qi] = lj_of(0, qi);
     commit(0);
   }
   lds_barrier();
 
+  float* r_rg = r_l + rg * CQ * 32;   // [row group][CQ][32]
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     const bool more = t + 1 < ntiles;
-    const float l = lnext;
-    if (more) lnext = lj_of(t + 1);
-    // r of this wave's component for row c.
-    if (active) {
-      const float rv = fast_exp2(l - rs[buf * TR + rg * 32 + c]);
-      if (g == 0) {
-        r_l[wave * 32 + c] = rv;
-        if (mb2 == 0) nk += rv;
+    if (r_maker) {
+#pragma unroll
+      for (int qi = 0; qi < Q; ++qi) {
+        const float rv = (k0 + qi < K) ? fast_exp2(lnext[qi] - rs[buf * TR + rg * 32 + c]) : 0.0f;
+        if (g == 0) {
+          r_rg[(cw * Q + qi) * 32 + c] = rv;
+          nk[qi] += rv;
+        }
       }
     }
-    if (more) fetch(t + 1);
+    if (more) {
+#pragma unroll
+      for (int qi = 0; qi < Q; ++qi) lnext[qi] = lj_of(t + 1, qi);
+      fetch(t + 1);
+    }
     lds_barrier();
     const float* xa = xf + buf * TR * XF;
     const __bf16* xb = xh + buf * TR * XH;
@@ -1332,22 +1353,25 @@ void full_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       for (int mb = 0; mb < NMB; ++mb) bop[mb] = in_use ? lds_rows_operand(xb, XH, r0, 32 * mb, lane) : bf16x8{};
       if (active) {
         // A = bf16(r x_d2): lane = d2 = 32 mb2 + c, elements = the 8 rows.
-        const f32x4* rr = reinterpret_cast<const f32x4*>(r_l + wave * 32 + 16 * p + 8 * g);
         const float* xx = xa + (r0 + 8 * g) * XF + 32 * mb2 + c;
         const f32x4 x0 = {xx[0], xx[XF], xx[2 * XF], xx[3 * XF]};
         const f32x4 x1 = {xx[4 * XF], xx[5 * XF], xx[6 * XF], xx[7 * XF]};
-        const bf16x8 a = to_bf16x8(rr[0] * x0, rr[1] * x1);
-        // A step whose 16 rows x 32 coordinates of bf16(r x) are all zero adds nothing.
-        if (dense || any_nonzero(a)) {
 #pragma unroll
-          for (int mb = 0; mb < NMB; ++mb) acc[mb] = mfma_bf16(a, bop[mb], acc[mb]);
+        for (int qi = 0; qi < Q; ++qi) {
+          const f32x4* rr = reinterpret_cast<const f32x4*>(r_rg + (cw * Q + qi) * 32 + 16 * p + 8 * g);
+          const bf16x8 a = to_bf16x8(rr[0] * x0, rr[1] * x1);
+          // A step whose 16 rows x 32 coordinates of bf16(r x) are all zero adds nothing.
+          if (dense || any_nonzero(a)) {
+#pragma unroll
+            for (int mb = 0; mb < NMB; ++mb) acc[qi][mb] = mfma_bf16(a, bop[mb], acc[qi][mb]);
+          }
         }
       }
       if (mu_wave) {
         // A = bf16(r) of the workgroup's components (rows m = component), B = block mb2.
         bf16x8 a = {};
-        if (c < CPWG && cg * CPWG + c < K) {
-          const f32x4* rr = reinterpret_cast<const f32x4*>(r_l + r_wave(c) * 32 + 16 * p + 8 * g);
+        if (c < CQ && cg * CQ + c < K) {
+          const f32x4* rr = reinterpret_cast<const f32x4*>(r_rg + c * 32 + 16 * p + 8 * g);
           a = to_bf16x8(rr[0], rr[1]);
         }
         // B = column block mb2 (mb2 is not a compile-time index: read it again).
@@ -1359,26 +1383,32 @@ void full_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     lds_barrier();
   }
 
-  const int64_t pbase0 = ((int64_t)slab * RG + rg) * KP + (int64_t)cg * CPWG;
+  const int64_t pbase0 = ((int64_t)slab * RG + rg) * KP + (int64_t)cg * CQ;
   if (active) {
-    float* ps = part_sig + ((pbase0 + cw) * NMB * NMB + mb2 * NMB) * 1024;
 #pragma unroll
-    for (int mb = 0; mb < NMB; ++mb) {
+    for (int qi = 0; qi < Q; ++qi) {
+      if (k0 + qi >= K) continue;
+      float* ps = part_sig + ((pbase0 + cw * Q + qi) * NMB * NMB + mb2 * NMB) * 1024;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) ps[mb * 1024 + acc_row(i, g) * 32 + c] = acc[mb][i];
-    }
-    if (mb2 == 0) {
-      float s = nk;
+      for (int mb = 0; mb < NMB; ++mb) {
 #pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) s += __shfl_xor(s, o);
-      if (lane == 0) part_nk[pbase0 + cw] = s;
+        for (int i = 0; i < 16; ++i) ps[mb * 1024 + acc_row(i, g) * 32 + c] = acc[qi][mb][i];
+      }
+      if (mb2 == 0) {
+        float s = nk[qi];
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+        if (lane == 0) part_nk[pbase0 + cw * Q + qi] = s;
+      }
     }
   }
-  if (mu_wave && g == 0) {
-    // Register i of half 0 holds component acc_row(i, 0) = i.
+  if (mu_wave) {
+    // Register i of lane-half g holds component acc_row(i, g) of the workgroup.
 #pragma unroll
-    for (int i = 0; i < CPWG; ++i)
-      if (cg * CPWG + i < K) part_mu[(pbase0 + i) * DP + 32 * mb2 + c] = macc[i];
+    for (int i = 0; i < 16; ++i) {
+      const int ci = acc_row(i, g);
+      if (ci < CQ && cg * CQ + ci < K) part_mu[(pbase0 + ci) * DP + 32 * mb2 + c] = macc[i];
+    }
   }
 }
 
