@@ -81,6 +81,7 @@ __host__ __device__ constexpr size_t accum_drange_lds_bytes(int DR) {
 __host__ __device__ constexpr int bf16_parts(int DP);
 __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB);
 __host__ inline int bf16_blocks_per_group(int DP, int KB);
+__host__ __device__ constexpr int bf16_row_partials(int DP, int CB);
 
 // Pass 1 keeps the rows' split features in registers (diag_lse_x6) up to D = 128.
 __host__ __device__ constexpr bool diag_uses_x6(int DP) { return DP <= 128; }
@@ -140,7 +141,7 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.ndr = p.ctile ? (int)cdiv(p.DP, kDrange) : 1;
   if (bf16) {
     p.cpg = bf16_blocks_per_group(p.DP, p.KB);
-    p.rgroups = kAccWaves / (p.cpg * bf16_parts(p.DP));
+    p.rgroups = bf16_row_partials(p.DP, p.cpg);
   } else if (p.lj) {
     // 8 component blocks per workgroup, or 4 for K <= 224.  Two waves share a
     // block (one half of the columns each) where one wave's x and x^2
@@ -153,7 +154,7 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
     p.rgroups = 1;
   }
   p.ncg = (int)cdiv(p.KB, p.cpg);
-  const int64_t tile_rows = 32 * p.rgroups;
+  const int64_t tile_rows = 32 * (bf16 ? kAccWaves / (p.cpg * bf16_parts(p.DP)) : p.rgroups);
   if (p.need && p.ctile && N > 0 && p.KB > 0) {
     // One 4-wave workgroup per (slab, block, dimension range) and compute unit (its
     // X tile takes most of the LDS): about two rounds of workgroups.
@@ -2057,6 +2058,12 @@ __host__ __device__ constexpr int bf16_parts(int DP) { return DP <= 64 ? 1 : bf1
 // transposing reads (lds_rows_operand) want.
 __host__ __device__ constexpr int bf16_xr_stride(int DP) { return 2 * DP + 16; }
 
+// Partials per row slab and component block in pass 2: one per row group, and with two
+// parts per block (D = 96, 128) one per part, since each part then accumulates all
+// feature columns for its own 16 of the 32 rows.
+__host__ __device__ constexpr int bf16_row_partials(int DP, int CB) {
+  return kAccWaves / (CB * bf16_parts(DP)) * (bf16_parts(DP) == 2 ? 2 : 1);
+}
 __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB) {
   return (size_t)2 * (size_t)(256 / (CB * bf16_parts(DP))) * (size_t)bf16_xr_stride(DP) * 2 +
          (size_t)2 * (256 / (CB * bf16_parts(DP))) * sizeof(float) +
@@ -2255,7 +2262,11 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   constexpr int NCH = bf16_chains(DP);
   constexpr int CPC = NCF / NCH;               // chunks per chain
   constexpr int CPW = NCH / NH;                // chains per wave
-  constexpr int FW = F / NH;                   // feature columns per wave
+  // With two parts, part h forms r for the 16 rows of step h and accumulates r^T F
+  // over all features for them (r is formed once per element); otherwise each part
+  // forms r for all 32 rows and accumulates its own feature columns.
+  constexpr bool SPLIT_ROWS = NH == 2;
+  constexpr int FW = SPLIT_ROWS ? F : F / NH;  // feature columns per wave
   constexpr int NJ = FW / 32;                  // 32-column tiles of r^T F per wave
   constexpr int RG = kAccWaves / (CB * NH);    // row groups (32 rows each)
   constexpr int TR = 32 * RG;                  // rows per super-tile
@@ -2275,7 +2286,8 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
   const int cbw = wave % CB, h = (wave / CB) % NH, rg = wave / (CB * NH);
-  const int f0 = h * FW;                       // first feature of this wave's part
+  const int fc = h * (F / NH);                 // first feature of this wave's chains
+  const int f0 = SPLIT_ROWS ? 0 : fc;          // first feature of this wave's r^T F columns
   const int slab = blockIdx.x % nslab;
   const int cg = blockIdx.x / nslab;
   const int kb = cg * CB + cbw;
@@ -2372,7 +2384,7 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 #pragma unroll
     for (int u = 0; u < CPW; ++u) ch[u] = zero16();
     if (active) {
-      const __bf16* xrow = xr + buf * TR * XR + (rg * 32 + c) * XR + f0 + 8 * g;
+      const __bf16* xrow = xr + buf * TR * XR + (rg * 32 + c) * XR + fc + 8 * g;
 #pragma unroll
       for (int qq = 0; qq < CPC; ++qq) {
 #pragma unroll
@@ -2391,7 +2403,37 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       for (int q = 0; q < 4; ++q) mine[q * 64] = f32x4{ch[0][4 * q], ch[0][4 * q + 1], ch[0][4 * q + 2], ch[0][4 * q + 3]};
       lds_barrier();
     }
-    if (active) {
+    if constexpr (SPLIT_ROWS) {
+      if (active) {
+        // Registers 8h .. 8h + 7: rows rg*32 + 16h + 8(q - 2h) + 4g + j.
+        const f32x4* rt = reinterpret_cast<const f32x4*>(rs + buf * TR + rg * 32 + 4 * g);
+        float r8[8];
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq) {
+          const int q = 2 * h + qq;
+          f32x4 sq[NCH];
+#pragma unroll
+          for (int u = 0; u < NCH; ++u) sq[u] = s0[(u * CB * 4 + q) * 64];
+          const f32x4 lz = rt[2 * q];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float sv[NCH];
+#pragma unroll
+            for (int u = 0; u < NCH; ++u) sv[u] = sq[u][j];
+            const float rv = fast_exp2(bf16_diag_ll<NCH>(c0, sv) - lz[j]);
+            nk += rv;
+            r8[4 * qq + j] = rv;
+          }
+        }
+        const bf16x8 a = acc_to_row_operand(r8);
+        const __bf16* xt = xr + buf * TR * XR;
+        if (dense || any_nonzero(a)) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+            acc[j] = mfma_bf16(a, lds_rows_operand(xt, XR, rg * 32 + 16 * h, 32 * j, lane), acc[j]);
+        }
+      }
+    } else if (active) {
       const f32x4* rt = reinterpret_cast<const f32x4*>(rs + buf * TR + rg * 32 + 4 * g);
       float r[16];
 #pragma unroll
@@ -2437,7 +2479,9 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 
   if (active) {
     nk += __shfl_xor(nk, 32);
-    const int64_t kbase = ((int64_t)slab * RG + rg) * KP + (int64_t)kb * 32;
+    // Partial index: the row group, and with SPLIT_ROWS the part within it.
+    const int rp = SPLIT_ROWS ? rg * NH + h : rg;
+    const int64_t kbase = ((int64_t)slab * bf16_row_partials(DP, CB) + rp) * KP + (int64_t)kb * 32;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int f = f0 + 32 * j;               // a tile lies wholly in x^2 or in x
@@ -2445,7 +2489,7 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 #pragma unroll
       for (int i = 0; i < 16; ++i) dst[(kbase + acc_row(i, g)) * DP + c] = acc[j][i];
     }
-    if (g == 0 && h == 0) part_nk[kbase + c] = nk;
+    if (g == 0 && (SPLIT_ROWS || h == 0)) part_nk[kbase + c] = nk;
   }
 }
 
