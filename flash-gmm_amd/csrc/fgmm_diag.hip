@@ -19,7 +19,7 @@
 //   diag_lse_ctile    pass 1 above D = 128 (any D), tiled over components as well.
 //   diag_accum_gather pass 2 of the default plan up to D = 128: the needed rows of each
 //                     slab, the log-joint recomputed bit for bit as pass 1 forms it,
-//                     r^T [X | X^2] on fp32 matrix steps.
+//                     r^T [X | X^2] as six split-bf16 products per 16 rows.
 //   diag_accum_drange pass 2 of the default plan above D = 128, per dimension range.
 //   diag_accum_sparse / diag_accum_lj2 / diag_accum_lj
 //                     pass 2 of the stored plan (FGMM_FLAG_STORE_LOGJOINT, D <= 256).
