@@ -1137,11 +1137,15 @@ void iso_accum_tiles(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     commit(0);
   }
   __syncthreads();
+  // The tile's need word, loaded one tile ahead (a load used at once would stall every tile).
+  auto need_of = [&](int64_t t) -> unsigned { return active ? (dense ? ~0u : need[t * KB + kb]) : 0u; };
+  unsigned mnext = t_begin < t_end ? need_of(t_begin) : 0u;
   for (int64_t t = t_begin; t < t_end; ++t) {
     const int buf = (int)((t - t_begin) & 1);
     const bool more = t + 1 < t_end;
     if (more) fetch(t + 1);
-    const unsigned m = active ? (dense ? ~0u : need[t * KB + kb]) : 0u;
+    const unsigned m = mnext;
+    if (more) mnext = need_of(t + 1);
     if (m != 0u) {
       const __bf16* xt = xs + (size_t)buf * 3 * 32 * RS;
       bf16x8 xa[NQ][3];
@@ -1345,12 +1349,16 @@ void iso_accum_tiles2(const float* __restrict__ X, int64_t ldx, int64_t N, int D
     }
   }
   __syncthreads();
+  // The tile's need word (the same for both waves of a block), loaded one tile ahead.
+  auto need_of = [&](int64_t t) -> unsigned { return active ? (dense ? ~0u : need[t * KB + kb]) : 0u; };
+  unsigned mnext = t_begin < t_end ? need_of(t_begin) : 0u;
   for (int64_t t = t_begin; t < t_end; ++t) {
     const int it = (int)(t - t_begin);
     const int buf = it % 3;
     const bool more = t + 2 < t_end;
     if (more) fetch(t + 2);
-    const unsigned m = active ? (dense ? ~0u : need[t * KB + kb]) : 0u;   // the same for both waves
+    const unsigned m = mnext;
+    if (t + 1 < t_end) mnext = need_of(t + 1);
     const __bf16* xt = xs + (size_t)buf * 3 * 32 * RS;
     f32x4* mine = ex + (it & 1) * EXB + wave * 4 * 64 + lane;
     const f32x4* ch0 = ex + (it & 1) * EXB + w * 4 * 64 + lane;                   // chain 0 of the block
