@@ -140,8 +140,13 @@ struct IsoPlan {
 __host__ __device__ constexpr size_t lse_lds_base(int DP) {
   return (size_t)2 * (DP / 16) * 4 * 64 * 16 + (size_t)2 * 32 * 16;
 }
+// Pass 1 with the rows' split operands resident in registers (iso_lse) runs up to
+// D = 128 at two waves per SIMD, and at D = 192 and 256 (default plan) at one, with
+// four accumulation chains as the component-tiled pass 1 forms them.
+__host__ __device__ constexpr bool lse_in_regs(int DP) { return DP <= 128 || DP == 192 || DP == 256; }
+__host__ __device__ constexpr int lse_waves_per_simd(int DP) { return DP <= 128 ? 2 : 1; }
 __host__ __device__ constexpr int need_exact_cap(int DP) {
-  return (int)((80 * 1024 - lse_lds_base(DP)) / (kWaves * 32 * 2));
+  return (int)((kMaxLds / (lse_waves_per_simd(DP) == 2 ? 2 : 1) - lse_lds_base(DP)) / (kWaves * 32 * 2));
 }
 
 // Pass 2 reads the stored log-joint when it is requested, D is 33 to 256 (below,
@@ -169,7 +174,8 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
   p.lj = !bf16 && use_stored_lj(N, p.DP, p.KB, allow_lj);
   p.need = !bf16 && !p.lj;
   p.ctile = p.need && p.DP > 128;
-  p.rexact = p.need && p.KB <= (p.ctile ? ctile_need_exact_cap(ctile_blocks(p.DP)) : need_exact_cap(p.DP));
+  p.rexact = p.need && p.KB <= ((p.ctile && !lse_in_regs(p.DP)) ? ctile_need_exact_cap(ctile_blocks(p.DP))
+                                                                 : need_exact_cap(p.DP));
   p.ndr = p.ctile ? (int)cdiv(p.DP, kDrange) : 1;
   if (bf16) {
     p.cpg = bf16_blocks_per_group(p.DP, p.KB);
@@ -358,7 +364,8 @@ constexpr int kLjmStore = 1;   // the stored log-joint, its block maxima and nee
 constexpr int kLjmNeed = 2;    // need masks only (the default plan)
 
 template <int DP, int LJM>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads), amdgpu_waves_per_eu(2, 2)))
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(lse_waves_per_simd(DP), lse_waves_per_simd(DP))))
 void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
              const bf16x8* __restrict__ mu3, const double2* __restrict__ kc_blk, int KB,
              float* __restrict__ logZ, double2* __restrict__ rowstat, float* __restrict__ lj,
@@ -433,7 +440,8 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     const bf16x8* mp = mu_l + buf * BLK + lane;
     // Centred S^T[comp][row] = mu . x - sum_q o_q, lane = row, register i = component
     // acc_row(i, g); the block's constants carry + 2 b sum_q o_q.
-    const f32x16 xm = x6c_tile<NQ, kIsoChains>([&](int q, int t) { return mp[(q * 4 + t) * 64]; }, xb, ones);
+    const f32x16 xm = x6c_tile<NQ, (DP <= 128 ? kIsoChains : 4)>([&](int q, int t) { return mp[(q * 4 + t) * 64]; },
+                                                                   xb, ones);
     const double2* kp = kc_l + buf * 32 + g * 16;
     double ll[16];
     double bm = -INFINITY;
@@ -2269,7 +2277,23 @@ hipError_t launch_ctile(const IsoPlan& pl, const float* X, int64_t ldx, unsigned
   unsigned* ljmask = reinterpret_cast<unsigned*>(ws + pl.off_ljmask);
   unsigned* ljcount = reinterpret_cast<unsigned*>(ws + pl.off_ljcount);
   const int NQ = pl.DP / 16;
-  if (run1) {
+  if (run1 && !pl.lj && lse_in_regs(pl.DP)) {
+    // D = 192, 256: the register-resident pass 1 (same operands, chains and order).
+    auto lse = [&](auto dp_tag) -> hipError_t {
+      constexpr int DP = decltype(dp_tag)::value;
+      const size_t lds1 = lse_lds_base(DP) + (pl.rexact ? (size_t)kWaves * 32 * pl.KB * 2 : 0);
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_lse<DP, kLjmNeed>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL((iso_lse<DP, kLjmNeed>), dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
+                         stream, X, ldx, pl.N, (int)pl.D, mu3, reinterpret_cast<const double2*>(ws + pl.off_kcblk),
+                         pl.KB, logZ, rowstat, nullptr, nullptr, ljmask, ljcount, dense ? 1 : 0,
+                         pl.rexact ? 1 : 0);
+      return hipGetLastError();
+    };
+    hipError_t e = pl.DP == 192 ? lse(std::integral_constant<int, 192>{}) : lse(std::integral_constant<int, 256>{});
+    if (e != hipSuccess) return e;
+  } else if (run1) {
     const bool exact = pl.rexact && !pl.lj;
     const int ctb = ctile_blocks(pl.DP);
     const size_t lds1 = lse_ctile_base(ctb) + (exact ? (size_t)kCtWaves * 32 * pl.KB * 2 : 0);
