@@ -11,7 +11,9 @@
 //   iso_prep    O(K*D): per-component constants (fp64), mu as three-way bf16 splits
 //               with per-chunk centring offsets in matrix-core operand order, and
 //               the needed-pair counters zeroed.
-//   iso_lse     pass 1 up to D = 128, grid over row tiles.  Each wave keeps 32 rows
+//   iso_lse     pass 1 up to D = 128 (two waves per SIMD), and at D = 192 and 256 on
+//               the default plan (one wave per SIMD, four chains in iso_lse_ctile's
+//               order), grid over row tiles.  Each wave keeps 32 rows
 //               of X resident in registers as bf16 splits and streams mu in blocks
 //               of 32 components through LDS; the cross term is the centred
 //               split-bf16 contraction (x6c_tile, lane = row, register = component)
@@ -22,9 +24,10 @@
 //               with the stored log-joint also its rows (row-major tiles) and each
 //               row's block maximum.
 //   iso_lse_ctile
-//               pass 1 above D = 128 (any D): the contraction tiled over components
-//               (128 per tile) as well as rows, the rows' chunks re-read and split
-//               per component tile, four accumulation chains.  Same outputs.
+//               pass 1 above D = 128 (any D; the default plan uses it above 256): the
+//               contraction tiled over components (64 or 128 per tile) as well as
+//               rows, the rows' chunks re-read and split per component tile, four
+//               accumulation chains.  Same outputs.
 //   iso_accum_gather / iso_accum_tiles / iso_accum_tiles2
 //               pass 2 of the default plan up to D = 128: the log-joint of the
 //               needed (row, block) pairs recomputed bit for bit as pass 1 forms it,
