@@ -1413,9 +1413,9 @@ __host__ __device__ constexpr int gather_groups(int nslab) { return (nslab + kGa
 __host__ inline int64_t gather_grid(int nslab, int KB) { return gather_item_grid(gather_groups(nslab), KB); }
 
 // Waves per SIMD of the gathering pass: two where a wave's registers and the
-// workgroup's LDS allow it (D <= 32), so one wave's row loads overlap the other's
+// workgroup's LDS allow it (D <= 64), so one wave's row loads overlap the other's
 // matrix steps.
-__host__ __device__ constexpr int gather_waves_per_simd(int DP) { return DP <= 32 ? 2 : 1; }
+__host__ __device__ constexpr int gather_waves_per_simd(int DP) { return DP <= 64 ? 2 : 1; }
 
 template <int DP>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * kGatherWaves, 64 * kGatherWaves),
