@@ -268,12 +268,16 @@ __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int
       // of the bf16x6 pass 1, o_q = fp32(||mu chunk q||^2).  Each chunk's 16 loads
       // are unrolled so they are in flight together (this kernel runs K / 32 blocks
       // and is latency bound).
+      // Loads from clamped addresses with the value selected after, so no load waits
+      // behind a branch.
+#pragma unroll 2
       for (int q = 0; q < NQ; ++q) {
         double o = 0.0;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int d = 16 * q + e;
-          const double v = d < D ? (double)mu[comp * ldmu + d] : 0.0;
+          const float f = mu[comp * ldmu + (d < D ? d : D - 1)];
+          const double v = d < D ? (double)f : 0.0;
           o = fma(v, v, o);
         }
         musq += o;
@@ -302,8 +306,10 @@ __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int
     if (valid) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        if (d0 + e < D) lo[e] = mu[comp * ldmu + d0 + e];
-        if (d0 + 4 + e < D) hi[e] = mu[comp * ldmu + d0 + 4 + e];
+        const float a = mu[comp * ldmu + (d0 + e < D ? d0 + e : D - 1)];
+        const float b = mu[comp * ldmu + (d0 + 4 + e < D ? d0 + 4 + e : D - 1)];
+        lo[e] = d0 + e < D ? a : 0.0f;
+        hi[e] = d0 + 4 + e < D ? b : 0.0f;
       }
     }
     bf16x8 sp[3];
@@ -316,7 +322,8 @@ __global__ __launch_bounds__(64) void iso_prep(const float* __restrict__ mu, int
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int d = 16 * q + e;
-        const double v = d < D ? (double)mu[comp * ldmu + d] : 0.0;
+        const float f = mu[comp * ldmu + (d < D ? d : D - 1)];
+        const double v = d < D ? (double)f : 0.0;
         o = fma(v, v, o);
       }
       olo.x = -(float)o;
