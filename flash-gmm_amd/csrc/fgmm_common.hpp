@@ -65,9 +65,11 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // The fp32 matrix cores add the products of a 32x32x2 (or 16x16x4) step to the
 // accumulator one at a time, rounding after each, so a single chain over D=128
 // carries ~1e-4 absolute error in the cross term of clustered data; the log-joints
-// are formed by the centred split-bf16 contraction below instead.  On gfx950 VALU
-// and MFMA work of a SIMD do not overlap, so every VALU instruction in a
-// contraction is paid in matrix time.
+// are formed by the centred split-bf16 contraction below instead.  On gfx950 a
+// matrix step leaves the SIMD's issue port free for part of its 32 cycles: VALU
+// instructions of another wave (or later independent ones of the same wave) run
+// there, about half of them hidden when two waves on a SIMD are in the same phase
+// and nearly all when one runs its VALU work while the other runs matrix steps.
 
 // ---------------------------------------------------------------------------
 // bf16 matrix steps (the bf16 operand contracts of the reference's H100 kernels).
@@ -191,13 +193,17 @@ __device__ __forceinline__ f32x16 x6c_tile(LA loadA, const bf16x8 (&xb)[NQ][3], 
         for (int t = 0; t < 4; ++t) a[h][t] = loadA(q0 + h, t);
       }
     }
-    // Steps in order: x2 mu2, x1 mu3, x3 mu1, x2 mu1, x1 mu2, -o, x1 mu1.
+    // Steps in order: x2 mu2, x1 mu3, x3 mu1, x2 mu1, x1 mu2, -o, x1 mu1.  A chunk's
+    // seven steps are issued back to back (chain-major): consecutive matrix steps on
+    // one accumulator use the hardware's accumulator forwarding, while alternating
+    // two accumulators step by step measured 16% slower per step on gfx950.  The
+    // order of the steps within each chain, and so every bit, is the same.
 #pragma unroll
-    for (int step = 0; step < 7; ++step) {
+    for (int h = 0; h < NCH; ++h) {
+      const int q = q0 + h;
+      if (q < NQ) {
 #pragma unroll
-      for (int h = 0; h < NCH; ++h) {
-        const int q = q0 + h;
-        if (q < NQ) {
+        for (int step = 0; step < 7; ++step) {
           const bf16x8 A = step == 0 ? a[h][1] : step == 1 ? a[h][2] : step <= 3 ? a[h][0]
                          : step == 4 ? a[h][1] : step == 5 ? a[h][3] : a[h][0];
           const bf16x8 B = step == 0 ? xb[q][1] : step == 1 ? xb[q][0] : step == 2 ? xb[q][2]
@@ -240,12 +246,13 @@ __device__ __forceinline__ f32x16 x6c_tile_rows(const bf16x8 (&xa)[NQ][3], const
         for (int t = 0; t < 4; ++t) b[h][t] = loadB(q0 + h, t);
       }
     }
+    // Chain-major, as x6c_tile.
 #pragma unroll
-    for (int step = 0; step < 7; ++step) {
+    for (int h = 0; h < NCH; ++h) {
+      const int q = q0 + h;
+      if (q < NQ) {
 #pragma unroll
-      for (int h = 0; h < NCH; ++h) {
-        const int q = q0 + h;
-        if (q < NQ) {
+        for (int step = 0; step < 7; ++step) {
           const bf16x8 B = step == 0 ? b[h][1] : step == 1 ? b[h][2] : step <= 3 ? b[h][0]
                          : step == 4 ? b[h][1] : step == 5 ? b[h][3] : b[h][0];
           const bf16x8 A = step == 0 ? xa[q][1] : step == 1 ? xa[q][0] : step == 2 ? xa[q][2]
@@ -290,10 +297,10 @@ __device__ __forceinline__ bf16x8 lds_rows_operand(const __bf16* tile, int rs, i
 // upper bounds kept in half the space: truncation for negative values, round-up
 // of the magnitude for positive ones; NaN stays NaN.
 __device__ __forceinline__ unsigned short bf16_bits_up(float x) {
+  // Selects, not branches (callers keep their loop bodies one scheduling region).
   const unsigned u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)0x7fc0u;
-  if (u & 0x80000000u) return (unsigned short)(u >> 16);
-  return (unsigned short)((u + 0xffffu) >> 16);
+  const unsigned up = (u & 0x80000000u) ? u : u + 0xffffu;
+  return (unsigned short)(((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc0u : (up >> 16));
 }
 __device__ __forceinline__ float bf16_bits_to_float(unsigned short h) { return __uint_as_float((unsigned)h << 16); }
 
@@ -541,11 +548,12 @@ __device__ __forceinline__ f32x16 x6c_tile_rows_fn(LX loadX, const bf16x8 ones, 
         for (int t = 0; t < 4; ++t) b[h][t] = loadB(q0 + h, t);
       }
     }
+    // Chain-major, as x6c_tile.
 #pragma unroll
-    for (int step = 0; step < 7; ++step) {
+    for (int h = 0; h < NCH; ++h) {
+      if (q0 + h < NQ) {
 #pragma unroll
-      for (int h = 0; h < NCH; ++h) {
-        if (q0 + h < NQ) {
+        for (int step = 0; step < 7; ++step) {
           const bf16x8 B = step == 0 ? b[h][1] : step == 1 ? b[h][2] : step <= 3 ? b[h][0]
                          : step == 4 ? b[h][1] : step == 5 ? b[h][3] : b[h][0];
           const bf16x8 A = step == 0 ? xa[h][1] : step == 1 ? xa[h][0] : step == 2 ? xa[h][2]
@@ -587,6 +595,42 @@ __device__ __forceinline__ int buf_off(int off) {
 
 __device__ __forceinline__ buf_rsrc make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes per lane from a buffer straight into LDS (buffer_load_dwordx4 ... lds):
+// lane l's bytes at byte offset voff + soff of the buffer land at dst + 16 l, where
+// dst is the wave's LDS base (wave-uniform; it goes to M0).  No registers hold the
+// data on the way.  The writes are complete, for the issuing wave, once its
+// vector-memory count drains: dma_barrier waits for that before the workgroup
+// barrier, and nothing may read the destination before that barrier.
+// Issued from inline assembly on purpose: the compiler does not see an LDS store,
+// so it does not make every later LDS read wait for the transfer (it cannot tell
+// the buffers apart).  Its own vector-memory waits stay correct, since these
+// loads only add to the in-order count those waits drain.
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+struct DmaSrc {
+  i32x4_t words;
+};
+__device__ __forceinline__ DmaSrc dma_src(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  DmaSrc d;
+  d.words.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  d.words.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+  d.words.z = __builtin_amdgcn_readfirstlane((int)bytes);
+  d.words.w = 0x00020000;
+  return d;
+}
+// M0 is the compiler's reserved register, so the asm saves and restores it.
+__device__ __forceinline__ void lds_dma16(const DmaSrc& r, void* dst, int voff, int soff) {
+  const int lds = __builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(lds_void_t*)dst);
+  int saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+               "s_mov_b32 m0, %0"
+               : "=&s"(saved) : "s"(lds), "v"(voff), "s"(r.words), "s"(soff) : "memory");
+}
+__device__ __forceinline__ void dma_barrier() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 template <int AUX = 0>
 __device__ __forceinline__ float buf_load_f32(buf_rsrc r, int off) {

@@ -11,9 +11,14 @@
 //   iso_prep    O(K*D): per-component constants (fp64), mu as three-way bf16 splits
 //               with per-chunk centring offsets in matrix-core operand order, and
 //               the needed-pair counters zeroed.
-//   iso_lse     pass 1 up to D = 128 (two waves per SIMD), and at D = 192 and 256 on
-//               the default plan (one wave per SIMD, four chains in iso_lse_ctile's
-//               order), grid over row tiles.  Each wave keeps 32 rows
+//   iso_lse_pipe
+//               pass 1 of the default plan up to D = 128: iso_lse's arithmetic in an
+//               8-wave workgroup whose two waves per SIMD run a block's contraction
+//               and the previous block's epilogue in opposite orders (ping-pong), so
+//               one wave's VALU work runs under the other's matrix steps.
+//   iso_lse     pass 1 of the stored plan up to D = 128 (two waves per SIMD), and at
+//               D = 192 and 256 on the default plan (one wave per SIMD, four chains in
+//               iso_lse_ctile's order), grid over row tiles.  Each wave keeps 32 rows
 //               of X resident in registers as bf16 splits and streams mu in blocks
 //               of 32 components through LDS; the cross term is the centred
 //               split-bf16 contraction (x6c_tile, lane = row, register = component)
@@ -148,8 +153,11 @@ __host__ __device__ constexpr size_t lse_lds_base(int DP) {
 // four accumulation chains as the component-tiled pass 1 forms them.
 __host__ __device__ constexpr bool lse_in_regs(int DP) { return DP <= 128 || DP == 192 || DP == 256; }
 __host__ __device__ constexpr int lse_waves_per_simd(int DP) { return DP <= 128 ? 2 : 1; }
+// The pipelined pass 1 up to D = 128 is one 8-wave workgroup per compute unit
+// (two waves per SIMD) with a third buffer of block constants.
 __host__ __device__ constexpr int need_exact_cap(int DP) {
-  return (int)((kMaxLds / (lse_waves_per_simd(DP) == 2 ? 2 : 1) - lse_lds_base(DP)) / (kWaves * 32 * 2));
+  return DP <= 128 ? (int)((kMaxLds - lse_lds_base(DP) - 32 * 16 - 16) / (8 * 32 * 2))
+                   : (int)((kMaxLds / (lse_waves_per_simd(DP) == 2 ? 2 : 1) - lse_lds_base(DP)) / (kWaves * 32 * 2));
 }
 
 // Pass 2 reads the stored log-joint when it is requested, D is 33 to 256 (below,
@@ -236,7 +244,8 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
   p.off_part_sig = off; off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
   // One log-joint tile per pass-1 wave (the grid's 32-row tiles, rounded up to 4),
   // with its per-row block maxima and need mask; the default plan keeps the masks only.
-  const size_t ntile = (p.lj || p.need) ? (size_t)round_up(cdiv(N, 32), 4) * p.KB : 0;
+  // (The default plan's pass 1 up to D = 128 runs 8 tiles per workgroup.)
+  const size_t ntile = (p.lj || p.need) ? (size_t)round_up(cdiv(N, 32), p.need ? 8 : 4) * p.KB : 0;
   p.off_lj = off;     off = align256(off + (p.lj ? ntile * kLjTile * sizeof(float) : 0));
   p.off_ljmax = off;  off = align256(off + (p.lj ? ntile * 32 * sizeof(float) : 0));
   p.off_ljmask = off; off = align256(off + ntile * sizeof(unsigned));
@@ -523,6 +532,206 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
           for (int kb = 0; kb < KB; ++kb) ljmask[tile * KB + kb] |= nanbits;
         if (pairs != 0) atomicAdd(ljcount + (tile & 63), pairs);
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 1 of the default plan up to D = 128, software-pipelined in ping-pong.  The
+// arithmetic is iso_lse's (same contraction, chains, fp64 log-joint, online
+// log-sum-exp and need bounds), so logZ2 and the need bits are the same bits; only
+// the schedule differs.
+//
+// On gfx950 a matrix step leaves the SIMD's issue free for part of its 32 cycles,
+// and another wave's VALU instructions run there.  iso_lse's two waves per SIMD
+// fall into step (both contracting a block, then both in its epilogue), so little
+// of that overlap happens.  Here one workgroup of 8 waves holds 256 rows, two
+// waves per SIMD, and each iteration does the contraction of block kb and the
+// epilogue (log-joint, max, exp2 sum, need bound) of block kb - 1 in opposite
+// orders on the two waves of a SIMD: one contracts first, the other runs the
+// epilogue first.  The workgroup barrier at the end of each block keeps them in
+// opposite phase, so one wave's VALU work fills the other's matrix steps.  Roles
+// come from the hardware wave id's SIMD field, one of each per SIMD (the first
+// wave of a SIMD to arrive takes the contract-first role), so the pairing does not
+// depend on how the dispatcher places waves.  The mu blocks reach LDS by direct
+// buffer-to-LDS loads (no staging registers), double buffered; the constants are
+// triple buffered, since block kb - 1's are read while block kb + 1's arrive.
+// The eight 32-row tiles share one staging of each mu block.
+// ---------------------------------------------------------------------------
+constexpr int kPipeWaves = 8;
+constexpr int kPipeThreads = 64 * kPipeWaves;
+
+template <int DP>
+constexpr size_t lse_pipe_lds_bytes() {
+  return (size_t)2 * (DP / 16) * 4 * 64 * sizeof(bf16x8) + (size_t)3 * 32 * sizeof(double2) + 16;
+}
+
+template <int DP, int REXACT>
+__global__ __attribute__((amdgpu_flat_work_group_size(kPipeThreads, kPipeThreads), amdgpu_waves_per_eu(2, 2)))
+void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                  const bf16x8* __restrict__ mu3, const double2* __restrict__ kc_blk, int KB,
+                  float* __restrict__ logZ, double2* __restrict__ rowstat, unsigned* __restrict__ ljmask,
+                  unsigned* __restrict__ ljcount, int dense) {
+  static_assert(DP <= 128, "pipelined pass 1 keeps all of a row's splits in registers");
+  constexpr int NQ = DP / 16;
+  constexpr int BLK = NQ * 4 * 64;        // bf16x8 per 32-component block
+  constexpr int LPT = (BLK + kPipeThreads - 1) / kPipeThreads;
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                                 // [2][BLK]
+  double2* kc_l = reinterpret_cast<double2*>(lds_raw + 2 * BLK * sizeof(bf16x8));   // [3][32]
+  unsigned* simd_l = reinterpret_cast<unsigned*>(kc_l + 3 * 32);                     // [4]
+  unsigned short* rmax_l = reinterpret_cast<unsigned short*>(lds_raw + lse_pipe_lds_bytes<DP>());
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t tile = (int64_t)blockIdx.x * kPipeWaves + wave;
+  const int64_t row = tile * 32 + c;
+  const bool valid = row < N;
+
+  // Block kb's operands into mu buffer kb & 1, its constants into kc buffer kb % 3.
+  // A lane whose piece lies past the block (BLK not a multiple of the workgroup's
+  // 512 lanes) is switched off rather than given an out-of-range offset, which
+  // would write zeros into LDS.
+  auto fetch = [&](int kb) {
+    const DmaSrc r = dma_src(mu3 + (int64_t)kb * BLK, (uint32_t)(BLK * sizeof(bf16x8)));
+    bf16x8* dst = mu_l + (kb & 1) * BLK + wave * 64;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      if (BLK % kPipeThreads == 0 || q * kPipeThreads + wave * 64 < BLK)
+        lds_dma16(r, dst + q * kPipeThreads, tid * (int)sizeof(bf16x8), q * kPipeThreads * (int)sizeof(bf16x8));
+    }
+    if (wave == 0) {
+      if (lane < 32) {
+        const DmaSrc rk = dma_src(kc_blk + (int64_t)kb * 32, (uint32_t)(32 * sizeof(double2)));
+        lds_dma16(rk, kc_l + (kb % 3) * 32, lane * (int)sizeof(double2), 0);
+      }
+    }
+  };
+  if (tid < 4) simd_l[tid] = 0u;
+  fetch(0);
+
+  bf16x8 xb[NQ][3];
+  double xsq = 0.0;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int d0 = 16 * q + 8 * g;
+    const f32x4 lo = load_row4(X, ldx, row, d0, D, valid), hi = load_row4(X, ldx, row, d0 + 4, D, valid);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xsq = fma((double)lo[e], (double)lo[e], xsq);
+      xsq = fma((double)hi[e], (double)hi[e], xsq);
+    }
+    split3_bf16(lo, hi, xb[q]);
+  }
+  xsq += __shfl_xor(xsq, 32);
+  const bf16x8 ones = x6c_ones(lane);
+  lds_barrier();   // simd_l cleared
+  // HW_ID bits 5:4 are the wave's SIMD.  The first wave of a SIMD to arrive
+  // contracts first; the second runs the epilogue first.
+  const int simd = (__builtin_amdgcn_s_getreg((4) | (0 << 6) | ((32 - 1) << 11)) >> 4) & 3;
+  unsigned order = 0;
+  if (lane == 0) order = atomicAdd(simd_l + simd, 1u);
+  const bool epi_first = __builtin_amdgcn_readfirstlane(order) != 0;
+  dma_barrier();
+
+  auto contract = [&](int kb) {
+    const bf16x8* mp = mu_l + (kb & 1) * BLK + lane;
+    return x6c_tile<NQ, kIsoChains>([&](int q, int t) { return mp[(q * 4 + t) * 64]; }, xb, ones);
+  };
+
+  double mx = -INFINITY;
+  float sm = 0.0f;
+  float run_max = -INFINITY;
+  unsigned pairs = 0;
+  // Log-joint, block max and exp2 sum of block kb (its contraction in xm), as iso_lse
+  // forms them; returns the row's block maximum over both half-waves.
+  auto epilogue = [&](int kb, const f32x16& xm) {
+    const double2* kp = kc_l + (kb % 3) * 32 + g * 16;
+    // All 16 constant reads in flight before the first is used.
+    double2 cb[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) cb[i] = kp[i];
+    __builtin_amdgcn_sched_barrier(0);
+    double ll[16];
+    double bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      ll[i] = fma(-cb[i].y, fma(-2.0, (double)xm[i], xsq), cb[i].x);
+      bm = fmax(bm, ll[i]);
+    }
+    const double mn = fmax(mx, bm);
+    const double ms = (mn == -INFINITY) ? 0.0 : mn;
+    float acc = sm * fast_exp2((float)(mx - ms));
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc += fast_exp2((float)(ll[i] - ms));
+    sm = acc;
+    mx = mn;
+    return lj_row_max(bm);
+  };
+  // The need bound of block kb: kept in LDS (REXACT) or tested against the running
+  // max.  Both half-waves store the row's bound (the same value); the mask word goes
+  // out through a buffer store whose offset is out of range on every lane but 0.
+  const buf_rsrc mask_r = make_rsrc(ljmask + tile * KB, (uint32_t)(KB * sizeof(unsigned)));
+  const int mask_off = buf_off(lane == 0 ? 0 : kBufOob);
+  auto put_need = [&](int kb, float R) {
+    if constexpr (REXACT) {
+      rmax_l[(wave * KB + kb) * 32 + c] = bf16_bits_up(R);
+    } else {
+      run_max = fmaxf(run_max, R);
+      const bool nb = valid && (dense != 0 || !(R - run_max < -kLjSkipGap));
+      const unsigned bits = (unsigned)__builtin_amdgcn_ballot_w64(nb);
+      __builtin_amdgcn_raw_buffer_store_b32(bits, mask_r, mask_off, kb * (int)sizeof(unsigned), 0);
+      pairs += __builtin_popcount(bits);
+    }
+  };
+
+  if (KB > 1) fetch(1);
+  f32x16 xm = contract(0);
+  dma_barrier();
+  for (int kb = 1; kb < KB; ++kb) {
+    if (kb + 1 < KB) fetch(kb + 1);
+    f32x16 xn;
+    float R;
+    if (epi_first) {
+      R = epilogue(kb - 1, xm);
+      __builtin_amdgcn_sched_barrier(0);
+      xn = contract(kb);
+    } else {
+      xn = contract(kb);
+      __builtin_amdgcn_sched_barrier(0);
+      R = epilogue(kb - 1, xm);
+    }
+    put_need(kb - 1, R);
+    xm = xn;
+    dma_barrier();
+  }
+  put_need(KB - 1, epilogue(KB - 1, xm));
+
+  // Merge the two half-waves that hold the same row.
+  const double mo = __shfl_xor(mx, 32);
+  const float so = __shfl_xor(sm, 32);
+  const double mn = fmax(mx, mo);
+  const double ms = (mn == -INFINITY) ? 0.0 : mn;
+  const float tot = sm * fast_exp2((float)(mx - ms)) + so * fast_exp2((float)(mo - ms));
+  const double lz2 = mn + (double)log2f(tot);
+  if (valid && g == 0) {
+    rowstat[row] = make_double2(xsq, lz2);
+    if (logZ) logZ[row] = (float)(lz2 * kLn2);
+  }
+  if constexpr (REXACT) {
+    // Each lane reads back the bounds it wrote itself.
+    const unsigned short* rm = rmax_l + wave * KB * 32 + c;
+    if (g == 0)
+      need_put_masks([&](int kb) { return bf16_bits_to_float(rm[kb * 32]); }, ljmask + tile * KB,
+                     ljcount + (tile & 63), KB, c, lz2, valid, dense != 0);
+  } else {
+    const unsigned nanbits = (unsigned)__builtin_amdgcn_ballot_w64(valid && g == 0 && lz2 != lz2);
+    if (lane == 0) {
+      if (nanbits != 0)
+        for (int kb = 0; kb < KB; ++kb) ljmask[tile * KB + kb] |= nanbits;
+      if (pairs != 0) atomicAdd(ljcount + (tile & 63), pairs);
     }
   }
 }
@@ -2353,16 +2562,30 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   if (run1) {
     const int64_t nblk1 = cdiv(pl.N, 32 * kWaves);
     if constexpr (DP <= 128) {
-      const size_t lds1 = lse_lds_bytes<DP>() + (pl.rexact ? (size_t)kWaves * 32 * pl.KB * 2 : 0);
-      auto kern = pl.lj ? &iso_lse<DP, kLjmStore> : &iso_lse<DP, kLjmNeed>;
-      if (lds1 > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+      hipError_t e = hipSuccess;
+      if (pl.need) {
+        // The default plan: the software-pipelined pass 1.
+        const size_t lds1 = lse_pipe_lds_bytes<DP>() + (pl.rexact ? (size_t)kPipeWaves * 32 * pl.KB * 2 : 0);
+        auto kern = pl.rexact ? &iso_lse_pipe<DP, 1> : &iso_lse_pipe<DP, 0>;
+        if (lds1 > 65536)
+          e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds1);
         if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(pl.N, 32 * kPipeWaves)), dim3(kPipeThreads), lds1, stream,
+                           X, ldx, pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3), kc_blk,
+                           pl.KB, logZ, rowstat, ljmask, ljcount, dense ? 1 : 0);
+      } else {
+        // The stored plan: iso_lse also writes the log-joint rows.
+        const size_t lds1 = lse_lds_bytes<DP>();
+        auto kern = &iso_lse<DP, kLjmStore>;
+        if (lds1 > 65536)
+          e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds1);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, dim3((unsigned)nblk1), dim3(kThreads), lds1, stream, X, ldx, pl.N,
+                           (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3), kc_blk, pl.KB,
+                           logZ, rowstat, lj, ljmax, ljmask, ljcount, dense ? 1 : 0, 0);
       }
-      hipLaunchKernelGGL(kern, dim3((unsigned)nblk1), dim3(kThreads), lds1, stream, X, ldx, pl.N,
-                         (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3), kc_blk, pl.KB,
-                         logZ, rowstat, lj, ljmax, ljmask, ljcount, dense ? 1 : 0, pl.rexact ? 1 : 0);
     } else {
       return hipErrorInvalidValue;   // launch_ctile runs pass 1 above D = 128
     }
