@@ -1,7 +1,9 @@
 """Shared tolerance checks for the GPU parity tests.
 
 Float32 kernels against the float64 oracle:
-  logZ        abs <= 1e-4 (x D / 128 above D = 128, logz_atol_for)
+  logZ        abs <= 1e-4 up to D = 128; above, abs <= max(1e-4, e32), where e32 is the
+              error of the float32 restatement of the reference's arithmetic on the
+              same rows (logz_atol_fp32)
   Nk, sig     |d| <= 1e-4 * |ref| + 1e-6 * max|ref|   (floor for near-empty components)
   mu_acc      max|d| <= 1e-4 * max|ref|                (norm-wise; entries near zero make
                                                         element-wise relative error meaningless)
@@ -13,12 +15,24 @@ LOGZ_ATOL = 1e-4
 REL = 1e-4
 
 
-def logz_atol_for(D):
-    """The logZ bound at width D.  The log-joint's terms (||x||^2, x.mu, ||mu||^2) grow
-    in proportion to D, and a float32 evaluation of them has an absolute error that
-    grows with them: above D = 128 the bound scales by D / 128, the relative accuracy
-    the 1e-4 bound sets at the benchmark width D = 128."""
-    return LOGZ_ATOL * max(1.0, D / 128.0)
+def logz_err(lz, ref):
+    """max |lz - ref| over the rows where ref is finite (float64 numpy or torch)."""
+    a = np.asarray(lz.detach().double().cpu().numpy() if hasattr(lz, "detach") else lz, dtype=np.float64)
+    b = np.asarray(ref.detach().double().cpu().numpy() if hasattr(ref, "detach") else ref, dtype=np.float64)
+    fin = np.isfinite(b)
+    return float(np.abs(a[fin] - b[fin]).max(initial=0.0))
+
+
+def logz_atol_fp32(ref32_logZ, ref64_logZ, D):
+    """The logZ bound at width D.  Up to D = 128 it is 1e-4.  Above, the log-joint's
+    terms (||x||^2, x.mu, ||mu||^2) grow in proportion to D, and the reference's own
+    float32 arithmetic loses accuracy with them: the bound is max(1e-4, the error of
+    the float32 restatement of that arithmetic on the same rows), so the kernels are
+    held to the reference's accuracy at every width.  The error is measured, not
+    assumed: ref32_logZ comes from the oracle run in float32 on the same inputs."""
+    if D <= 128:
+        return LOGZ_ATOL
+    return max(LOGZ_ATOL, logz_err(ref32_logZ, ref64_logZ))
 
 # The bf16 operand contract (precision="bf16") against its own oracle
 # (gmm_oracle.estep_iso_bf16): the roundings to bf16 are replayed exactly, so only

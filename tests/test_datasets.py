@@ -123,7 +123,7 @@ def test_stream_em_gist_width_file_against_the_oracle(tmp_path, gpu_device):
     from flash_gmm import stream_em_iso
     from oracle import gmm_oracle as O
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from parity import logz_atol_for
+    from parity import logz_atol_fp32
     g = torch.Generator().manual_seed(11)
     K, D, N = 64, 960, 30000
     centres = torch.randn(K, D, generator=g) * 0.5
@@ -145,4 +145,7 @@ def test_stream_em_gist_width_file_against_the_oracle(tmp_path, gpu_device):
     assert float((mu.double().cpu() - m).abs().max()) <= 2e-4 * scale
     assert float((lss.double().cpu() - torch.log(s2)).abs().max()) <= 3e-4
     assert float((lpi.double().cpu() - torch.log(pi)).abs().max()) <= 2e-4
-    assert abs(rep["loglik"][0] - float(logZ.sum())) <= logz_atol_for(D) * N
+    # The log-likelihood is a sum of N logZ values: N times the logZ bound at this
+    # width (the float32 restatement's error on these rows, above D = 128).
+    lz32 = O.estep_iso(X, mu0, lss0, lpi0, dtype=torch.float32)[0]
+    assert abs(rep["loglik"][0] - float(logZ.sum())) <= logz_atol_fp32(lz32, logZ, D) * N

@@ -13,7 +13,7 @@ from oracle import gmm_oracle as O
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
 import make_golden  # noqa: E402
-from parity import LOGZ_ATOL, assert_close_stats, assert_dense_agrees, logz_atol_for  # noqa: E402
+from parity import LOGZ_ATOL, assert_close_stats, assert_dense_agrees, logz_atol_fp32, logz_err  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -24,8 +24,18 @@ def run_gpu(inp, dev):
     return out
 
 
-def oracle(inp):
-    return O.estep_diag(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+def oracle(inp, dtype=torch.float64):
+    return O.estep_diag(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"], dtype=dtype)
+
+
+def check_wide(got, inp, what, D, ref=None):
+    """All four outputs against the float64 oracle.  The logZ bound is 1e-4 up to
+    D = 128; above, max(1e-4, the error of the float32 restatement of the reference's
+    arithmetic on the same rows), measured here."""
+    ref = oracle(inp) if ref is None else ref
+    atol = logz_atol_fp32(oracle(inp, torch.float32)[0] if D > 128 else None, ref[0], D)
+    print(f"{what}: max |logZ - oracle| {logz_err(got[0], ref[0]):.2e}, bound {atol:.2e}", flush=True)
+    assert_close_stats(got, ref, what, logz_atol=atol)
 
 
 def test_golden_vectors(gpu_device):
@@ -42,7 +52,7 @@ def test_golden_vectors(gpu_device):
                                    (5, 2, 255)])
 def test_edge_shapes(N, K, D, gpu_device):
     inp = data.diag_clustered(N, K, D, seed=N + K + D)
-    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), f"diag N={N} K={K} D={D}", logz_atol=logz_atol_for(D))
+    check_wide(run_gpu(inp, gpu_device), inp, f"diag N={N} K={K} D={D}", D)
 
 
 @pytest.mark.parametrize("stored", [False, True])
@@ -61,8 +71,8 @@ def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, stored, gpu_device):
         outs.append(o)
     torch.cuda.synchronize()
     assert_dense_agrees(outs[0], outs[1], bitwise=_stored_applies(N, K, D, stored))
-    assert_close_stats(outs[0], oracle(inp), "diag skip", logz_atol=logz_atol_for(D))
-    assert_close_stats(outs[1], oracle(inp), "diag dense", logz_atol=logz_atol_for(D))
+    check_wide(outs[0], inp, "diag skip", D)
+    check_wide(outs[1], inp, "diag dense", D)
 
 
 @pytest.mark.parametrize("N,K,D", [(40_000, 30, 16), (30_000, 60, 40), (20_000, 50, 96)])
@@ -108,8 +118,8 @@ def test_stored_and_recomputed_log_joint(N, K, D, gpu_device):
     stored = _into(inp, gpu_device, store_log_joint=True)
     recomputed = _into(inp, gpu_device)
     assert torch.equal(stored[0], recomputed[0])
-    assert_close_stats(stored, ref, f"stored N={N} K={K} D={D}", logz_atol=logz_atol_for(D))
-    assert_close_stats(recomputed, ref, f"recomputed N={N} K={K} D={D}", logz_atol=logz_atol_for(D))
+    check_wide(stored, inp, f"stored N={N} K={K} D={D}", D, ref=ref)
+    check_wide(recomputed, inp, f"recomputed N={N} K={K} D={D}", D, ref=ref)
 
 
 # Shapes of the sparse stored log-joint (32 < D <= 128): sparse masks (D = 64 .. 128)
@@ -193,11 +203,13 @@ def test_diag_wide_mid_size(gpu_device):
     """D=256 (component-tiled pass 1, dimension-range pass 2) at N=8192, K=256 against
     the float64 oracle."""
     inp = data.diag_clustered(8192, 256, 256, seed=5)
-    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "diag K256 D256 N8192", logz_atol=logz_atol_for(256))
+    check_wide(run_gpu(inp, gpu_device), inp, "diag K256 D256 N8192", 256)
 
 
 def test_diag_full_size_properties(gpu_device):
-    """N=1M, K=1024, D=96: every row counted once, sampled rows' logZ exact."""
+    """N=1M, K=1024, D=96 (the diagonal benchmark workload): every row counted once,
+    the gathered accumulation against the dense one, and all four outputs against the
+    float64 oracle over every row (about 15 s of CPU)."""
     dev = gpu_device
     inp = data.diag_clustered(1_000_000, 1024, 96, seed=2, device=dev)
     logZ, Nk, mu_acc, sig = flash_gmm_estep_diag(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
@@ -210,10 +222,11 @@ def test_diag_full_size_properties(gpu_device):
     # The gathered accumulation this data takes agrees with the dense one.
     dense = _into(inp, dev, dense=True)
     assert_dense_agrees((logZ, Nk, mu_acc, sig), dense, bitwise=False)
-    rows = torch.randint(0, N, (2048,), generator=torch.Generator().manual_seed(1))
-    sub = {k: v.cpu() for k, v in inp.items()}
-    ref = O.estep_diag(sub["X"][rows], sub["mu"], sub["log_sigma_sq"], sub["log_pi"])[0]
-    assert (logZ.cpu()[rows].double() - ref).abs().max().item() <= LOGZ_ATOL
+    print("diag N=1M: full-size oracle (float64, CPU)", flush=True)
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    ref = O.estep_diag(*[inp[k].cpu() for k in ("X", "mu", "log_sigma_sq", "log_pi")])
+    print(f"diag N=1M max |logZ - oracle| = {(logZ.cpu().double() - ref[0]).abs().max().item():.3e}", flush=True)
+    assert_close_stats((logZ, Nk, mu_acc, sig), ref, "diag K1024 D96 N=1M")
 
 
 def test_wide_row_stride(gpu_device):

@@ -13,13 +13,23 @@ from flash_gmm import data, diag_estep_into
 from oracle import gmm_oracle as O
 
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-from parity import assert_close_stats, assert_dense_agrees, logz_atol_for  # noqa: E402
+from parity import assert_close_stats, assert_dense_agrees, logz_atol_fp32, logz_err  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
 
-def oracle(inp):
-    return O.estep_diag(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+def oracle(inp, dtype=torch.float64):
+    return O.estep_diag(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"], dtype=dtype)
+
+
+def check_wide(got, inp, what, D, ref=None):
+    """All four outputs against the float64 oracle.  The logZ bound is 1e-4 up to
+    D = 128; above, max(1e-4, the error of the float32 restatement of the reference's
+    arithmetic on the same rows), measured here."""
+    ref = oracle(inp) if ref is None else ref
+    atol = logz_atol_fp32(oracle(inp, torch.float32)[0] if D > 128 else None, ref[0], D)
+    print(f"{what}: max |logZ - oracle| {logz_err(got[0], ref[0]):.2e}, bound {atol:.2e}", flush=True)
+    assert_close_stats(got, ref, what, logz_atol=atol)
 
 
 def _into(inp, dev, **kw):
@@ -43,7 +53,7 @@ def test_wide_d_against_oracle(N, K, D, gpu_device):
     print(f"diag wide N={N} K={K} D={D}", flush=True)
     inp = data.diag_clustered(N, K, D, seed=N + K + D)
     got = _into(inp, gpu_device)
-    assert_close_stats(got, oracle(inp), f"diag N={N} K={K} D={D}", logz_atol=logz_atol_for(D))
+    check_wide(got, inp, f"diag N={N} K={K} D={D}", D)
 
 
 @pytest.mark.parametrize("N,K,D", [(6000, 512, 256), (3000, 300, 960)])
@@ -54,7 +64,7 @@ def test_wide_d_skip_agrees_with_dense(N, K, D, gpu_device):
     a = _into(inp, gpu_device)
     b = _into(inp, gpu_device, dense=True)
     assert_dense_agrees(a, b, bitwise=False)
-    assert_close_stats(b, oracle(inp), f"diag dense N={N} K={K} D={D}", logz_atol=logz_atol_for(D))
+    check_wide(b, inp, f"diag dense N={N} K={K} D={D}", D)
 
 
 @pytest.mark.parametrize("stored", [False, True])
@@ -87,7 +97,7 @@ def test_wide_d_need_masks_from_the_running_max(gpu_device):
     a = _into(inp, gpu_device)
     b = _into(inp, gpu_device, dense=True)
     assert_dense_agrees(a, b, bitwise=False)
-    assert_close_stats(a, oracle(inp), "diag running-max masks D=160", logz_atol=logz_atol_for(160))
+    check_wide(a, inp, "diag running-max masks D=160", 160)
 
 
 def test_wide_d_randn_variances(gpu_device):
@@ -99,7 +109,7 @@ def test_wide_d_randn_variances(gpu_device):
                log_sigma_sq=torch.rand(K, D, generator=g) - 0.5,
                log_pi=torch.log_softmax(torch.randn(K, generator=g, dtype=torch.float64), 0).float())
     got = _into(inp, gpu_device)
-    assert_close_stats(got, oracle(inp), "diag randn D=400", logz_atol=logz_atol_for(D))
+    check_wide(got, inp, "diag randn D=400", D)
 
 
 def test_wide_d_mid_size(gpu_device):
@@ -109,4 +119,4 @@ def test_wide_d_mid_size(gpu_device):
     ref = oracle(inp)
     err = (got[0].cpu().double() - ref[0]).abs().max().item()
     print(f"diag N=16384 K=512 D=960: max |logZ - oracle| = {err:.3e}", flush=True)
-    assert_close_stats(got, ref, "diag N=16384 K=512 D=960", logz_atol=logz_atol_for(960))
+    check_wide(got, inp, "diag N=16384 K=512 D=960", 960, ref=ref)

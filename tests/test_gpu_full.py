@@ -151,7 +151,9 @@ def test_full_wide_mid_size(gpu_device):
 
 
 def test_full_size_properties(gpu_device):
-    """N=250K, K=256, D=64: sum_k Nk = N, sum_k mu_acc = sum x, sum_k sig_outer = X^T X."""
+    """N=250K, K=256, D=64 (the full-covariance benchmark workload): sum_k Nk = N,
+    sum_k mu_acc = sum x, sum_k sig_outer = X^T X, and all four outputs (sig_outer
+    included) against the float64 oracle over every row (about 25 s of CPU)."""
     dev = gpu_device
     inp = data.full_clustered(250_000, 256, 64, seed=3, device=dev)
     logZ, Nk, mu_acc, so = flash_gmm_estep_full(*[inp[k] for k in KEYS])
@@ -164,10 +166,11 @@ def test_full_size_properties(gpu_device):
     xtx = X.T @ X
     torch.testing.assert_close(so.double().sum(0), xtx, rtol=0, atol=1e-5 * float(xtx.abs().max()))
     assert torch.all(so.diagonal(dim1=1, dim2=2) >= 0)
-    rows = torch.randint(0, N, (1024,), generator=torch.Generator().manual_seed(2))
-    sub = {k: v.cpu() for k, v in inp.items()}
-    ref = O.estep_full(sub["X"][rows], sub["mu"], sub["prec_chol"], sub["log_pi"])[0]
-    assert (logZ.cpu()[rows].double() - ref).abs().max().item() <= LOGZ_ATOL
+    print("full N=250K: full-size oracle (float64, CPU)", flush=True)
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    ref = O.estep_full(*[inp[k].cpu() for k in KEYS])
+    print(f"full N=250K max |logZ - oracle| = {(logZ.cpu().double() - ref[0]).abs().max().item():.3e}", flush=True)
+    assert_close_stats((logZ, Nk, mu_acc, so), ref, "full K256 D64 N=250K")
 
 
 def test_rejects_bad_factor_shape(gpu_device):

@@ -13,15 +13,25 @@ from flash_gmm import data, full_estep_into
 from oracle import gmm_oracle as O
 
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-from parity import assert_close_stats, assert_dense_agrees, logz_atol_for  # noqa: E402
+from parity import assert_close_stats, assert_dense_agrees, logz_atol_fp32, logz_err  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
 KEYS = ("X", "mu", "prec_chol", "log_pi")
 
 
-def oracle(inp):
-    return O.estep_full(*[inp[k] for k in KEYS])
+def oracle(inp, dtype=torch.float64):
+    return O.estep_full(*[inp[k] for k in KEYS], dtype=dtype)
+
+
+def check_wide(got, inp, what, D, ref=None):
+    """All four outputs against the float64 oracle.  The logZ bound is 1e-4 up to
+    D = 128; above, max(1e-4, the error of the float32 restatement of the reference's
+    arithmetic on the same rows), measured here."""
+    ref = oracle(inp) if ref is None else ref
+    atol = logz_atol_fp32(oracle(inp, torch.float32)[0] if D > 128 else None, ref[0], D)
+    print(f"{what}: max |logZ - oracle| {logz_err(got[0], ref[0]):.2e}, bound {atol:.2e}", flush=True)
+    assert_close_stats(got, ref, what, logz_atol=atol)
 
 
 def _into(inp, dev, **kw):
@@ -45,7 +55,7 @@ def test_wide_d_against_oracle(N, K, D, gpu_device):
     print(f"full wide N={N} K={K} D={D}", flush=True)
     inp = data.full_clustered(N, K, D, seed=N + K + D)
     got = _into(inp, gpu_device)
-    assert_close_stats(got, oracle(inp), f"full N={N} K={K} D={D}", logz_atol=logz_atol_for(D))
+    check_wide(got, inp, f"full N={N} K={K} D={D}", D)
 
 
 @pytest.mark.parametrize("D", [200, 256])
@@ -56,7 +66,7 @@ def test_wide_d_skip_agrees_with_dense(D, gpu_device):
     a = _into(inp, gpu_device)
     b = _into(inp, gpu_device, dense=True)
     assert_dense_agrees(a, b, bitwise=False)
-    assert_close_stats(b, oracle(inp), f"full dense D={D}", logz_atol=logz_atol_for(D))
+    check_wide(b, inp, f"full dense D={D}", D)
 
 
 def test_wide_d_phase_split_equals_one_call(gpu_device):
@@ -99,4 +109,4 @@ def test_wide_d_mid_size(gpu_device):
     ref = oracle(inp)
     err = (got[0].cpu().double() - ref[0]).abs().max().item()
     print(f"full N=16384 K=64 D=200: max |logZ - oracle| = {err:.3e}", flush=True)
-    assert_close_stats(got, ref, "full N=16384 K=64 D=200", logz_atol=logz_atol_for(200))
+    check_wide(got, inp, "full N=16384 K=64 D=200", 200, ref=ref)

@@ -14,7 +14,7 @@ from oracle import gmm_oracle as O
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
 import make_golden  # noqa: E402
-from parity import LOGZ_ATOL, assert_close_stats, assert_dense_agrees, logz_atol_for  # noqa: E402
+from parity import LOGZ_ATOL, assert_close_stats, assert_dense_agrees, logz_atol_fp32, logz_err  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -25,8 +25,18 @@ def run_gpu(inp, dev, **kw):
     return out
 
 
-def oracle(inp):
-    return O.estep_iso(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+def oracle(inp, dtype=torch.float64):
+    return O.estep_iso(inp["X"], inp["mu"], inp["log_sigma_sq"], inp["log_pi"], dtype=dtype)
+
+
+def check_wide(got, inp, what, D, ref=None):
+    """All four outputs against the float64 oracle.  The logZ bound is 1e-4 up to
+    D = 128; above, max(1e-4, the error of the float32 restatement of the reference's
+    arithmetic on the same rows), measured here."""
+    ref = oracle(inp) if ref is None else ref
+    atol = logz_atol_fp32(oracle(inp, torch.float32)[0] if D > 128 else None, ref[0], D)
+    print(f"{what}: max |logZ - oracle| {logz_err(got[0], ref[0]):.2e}, bound {atol:.2e}", flush=True)
+    assert_close_stats(got, ref, what, logz_atol=atol)
 
 
 @pytest.mark.parametrize("name", ["iso_n10k_k64_d32", "iso_clustered_n4096_k96_d40"])
@@ -49,7 +59,7 @@ SHAPES = [
 @pytest.mark.parametrize("N,K,D", SHAPES)
 def test_edge_shapes(N, K, D, gpu_device):
     inp = data.iso_clustered(N, K, D, seed=N + K + D)
-    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), f"N={N} K={K} D={D}", logz_atol=logz_atol_for(D))
+    check_wide(run_gpu(inp, gpu_device), inp, f"N={N} K={K} D={D}", D)
 
 
 def test_empty_rows(gpu_device):
@@ -152,8 +162,8 @@ def test_zero_step_skip_is_bitwise_dense(case, stored, gpu_device):
     applies = stored and L.fgmm_iso_workspace_bytes_ex(N, K, D, _lib.FLAG_STORE_LOGJOINT) != \
         L.fgmm_iso_workspace_bytes(N, K, D)
     assert_dense_agrees(a, b, bitwise=applies)
-    assert_close_stats(a, oracle(inp), case, logz_atol=logz_atol_for(D))
-    assert_close_stats(b, oracle(inp), case + " dense", logz_atol=logz_atol_for(D))
+    check_wide(a, inp, case, D)
+    check_wide(b, inp, case + " dense", D)
 
 
 # Clustered shapes whose need masks are sparse (K >= 512): the accumulation pass
@@ -192,8 +202,8 @@ def test_stored_and_recomputed_log_joint(N, K, D, gpu_device):
     stored = _into(inp, gpu_device, store_log_joint=True)
     recomputed = _into(inp, gpu_device)
     assert torch.equal(stored[0], recomputed[0])          # pass 1 is the same kernel math
-    assert_close_stats(stored, ref, f"stored N={N} K={K} D={D}", logz_atol=logz_atol_for(D))
-    assert_close_stats(recomputed, ref, f"recomputed N={N} K={K} D={D}", logz_atol=logz_atol_for(D))
+    check_wide(stored, inp, f"stored N={N} K={K} D={D}", D, ref=ref)
+    check_wide(recomputed, inp, f"recomputed N={N} K={K} D={D}", D, ref=ref)
 
 
 def test_stored_log_joint_zero_weight_components(gpu_device):
@@ -281,7 +291,7 @@ def test_wide_shape_mid_size(gpu_device):
     """D=256 (component-tiled pass 1, dimension-range pass 2) at N=16,384, K=512 against
     the float64 oracle."""
     inp = data.iso_clustered(16384, 512, 256, seed=7)
-    assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "K512 D256 N16384", logz_atol=logz_atol_for(256))
+    check_wide(run_gpu(inp, gpu_device), inp, "K512 D256 N16384", 256)
 
 
 def test_phase2_requires_the_phase1_workspace(gpu_device):
