@@ -811,6 +811,17 @@ __host__ inline int64_t gather_slab_count(int64_t want, int64_t max_slabs, int W
   const int64_t n = g * W;
   return n < max_slabs ? n : max_slabs;
 }
+// The gathering passes read a slab's row state (logZ2, and ||x||^2 for the isotropic
+// model) through one buffer resource whose byte offsets are 32-bit: a slab holds at
+// most this many rows, so the offsets stay below 2^31 whatever N and K are (beyond
+// it the plan takes more slabs).  Rounded down to whole 32-row tiles.
+__host__ inline int64_t max_slab_rows(size_t state_bytes_per_row) {
+  return ((((int64_t)1 << 31) - 256) / (int64_t)state_bytes_per_row) / 32 * 32;
+}
+__host__ inline int64_t cap_slab_rows(int64_t rows_per_slab, size_t state_bytes_per_row) {
+  const int64_t cap = max_slab_rows(state_bytes_per_row);
+  return rows_per_slab < cap ? rows_per_slab : cap;
+}
 __host__ inline int64_t gather_item_grid(int G, int K) {
   if (G >= 8) return cdiv(G, 8) * (int64_t)K * 8;
   return 8 * cdiv(K, 8 / (G < 1 ? 1 : G));

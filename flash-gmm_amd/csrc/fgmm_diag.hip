@@ -161,13 +161,13 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
     int64_t want = cdiv((int64_t)2 * current_device_cus(), (int64_t)p.KB * p.ndr);
     const int64_t max_slabs = cdiv(N, 32);
     if (want > max_slabs) want = max_slabs;
-    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.rows_per_slab = cap_slab_rows(round_up(cdiv(N, want), 32), sizeof(double));
     p.nslab = (int)cdiv(N, p.rows_per_slab);
   } else if (p.need && N > 0 && p.KB > 0) {
     // The gathering pass 2: eight waves per compute unit, two rounds at one wave per
     // SIMD (one round where two fit).
     const int64_t want = gather_slab_count(cdiv((int64_t)8 * current_device_cus(), p.KB), cdiv(N, 32), kGatherWaves);
-    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.rows_per_slab = cap_slab_rows(round_up(cdiv(N, want), 32), sizeof(double));
     p.nslab = (int)cdiv(N, p.rows_per_slab);
   } else if (N > 0 && p.ncg > 0) {
     int64_t want = (int64_t)current_device_cus() / p.ncg;

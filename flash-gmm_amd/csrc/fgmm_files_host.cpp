@@ -104,7 +104,10 @@ extern "C" int fgmm_vecs_open(const char* path, int format, int threads, fgmm_ve
     memcpy(&hn, b, 4);
     memcpy(&hd, b + 4, 4);
     const size_t w = format == FGMM_VECS_FBIN ? 4 : 1;
-    if (hd < 1 || 8 + (size_t)hn * hd * w > bytes) {
+    // The rows must fit in the file.  Tested by division: the product n * d * w of a
+    // malformed header can pass 2^64 and wrap around.
+    const size_t body = bytes >= 8 ? bytes - 8 : 0;
+    if (bytes < 8 || hd < 1 || (size_t)hd > body / w || (size_t)hn > body / (w * (size_t)hd)) {
       munmap(base, bytes);
       return FGMM_ERR_INVALID_ARG;
     }

@@ -120,7 +120,7 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
     // The gathering pass 2: about two rounds of waves at two waves per SIMD (each
     // slab holds a partial of D x D per component, so no more slabs than that).
     const int64_t want = gather_slab_count(cdiv((int64_t)8 * current_device_cus(), K * p.ngrp), cdiv(N, 32), kGatherWaves);
-    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.rows_per_slab = cap_slab_rows(round_up(cdiv(N, want), 32), sizeof(double));
     p.nslab = (int)cdiv(N, p.rows_per_slab);
   } else if (N > 0 && p.ncg > 0) {
     int64_t want = (int64_t)current_device_cus() / p.ncg;

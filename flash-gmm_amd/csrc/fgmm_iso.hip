@@ -64,7 +64,6 @@
 #include <float.h>
 #include <math.h>
 
-#include <mutex>
 #include <type_traits>
 
 namespace fgmm {
@@ -210,13 +209,13 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
     int64_t want = cdiv((int64_t)2 * current_device_cus(), (int64_t)p.KB * p.ndr);
     const int64_t max_slabs = cdiv(N, 32);
     if (want > max_slabs) want = max_slabs;
-    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.rows_per_slab = cap_slab_rows(round_up(cdiv(N, want), 32), sizeof(double2));
     p.nslab = (int)cdiv(N, p.rows_per_slab);
   } else if (p.need && N > 0 && p.KB > 0) {
     // The gathering pass 2: eight waves per compute unit, two rounds at one wave per
     // SIMD (one round where two fit).
     const int64_t want = gather_slab_count(cdiv((int64_t)8 * current_device_cus(), p.KB), cdiv(N, 32), kGatherWaves);
-    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.rows_per_slab = cap_slab_rows(round_up(cdiv(N, want), 32), sizeof(double2));
     p.nslab = (int)cdiv(N, p.rows_per_slab);
   } else if (N > 0 && p.ncg > 0) {
     int64_t want = (int64_t)current_device_cus() / p.ncg;
@@ -3107,32 +3106,6 @@ hipError_t launch_bf16(const IsoPlan& pl, const float* X, int64_t ldx, unsigned 
 
 using namespace fgmm;
 
-// Workspace of fgmm_iso_estep_f32_noalloc: one array per GPU, in device memory the
-// code object reserves when it is loaded on that GPU.  Host code never passes the
-// name `scratch` itself (on the host it is a stand-in, not a device address): the
-// device address comes from hipGetSymbolAddress, looked up once per device.
-static __device__ __align__(256) unsigned char scratch[FGMM_NOALLOC_SCRATCH_BYTES];
-
-namespace {
-constexpr int kMaxScratchDevices = 64;
-std::mutex scratch_mutex;
-void* scratch_ptr[kMaxScratchDevices];
-
-// Device address of the current device's scratch array (nullptr and a status on error).
-int current_scratch(void** out) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) return FGMM_ERR_HIP;
-  std::lock_guard<std::mutex> lock(scratch_mutex);
-  if (scratch_ptr[dev] == nullptr) {
-    void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return FGMM_ERR_HIP;
-    scratch_ptr[dev] = p;
-  }
-  *out = scratch_ptr[dev];
-  return FGMM_OK;
-}
-}  // namespace
-
 extern "C" size_t fgmm_iso_workspace_bytes(int64_t N, int64_t K, int64_t D) {
   if (N < 0 || K < 0 || D < 1) return 0;
   return make_plan(N, K, D, false).total;
@@ -3244,18 +3217,4 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
                        accumulate ? 1 : 0);
   }
   return hipGetLastError() == hipSuccess ? FGMM_OK : FGMM_ERR_HIP;
-}
-
-extern "C" int fgmm_iso_estep_f32_noalloc(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
-                                          int64_t ldmu, int64_t K, const float* log_sigma_sq,
-                                          const float* log_pi, float* logZ, float* Nk, float* mu_acc,
-                                          float* sig_acc, unsigned flags, void* stream) {
-  if (flags & FGMM_FLAG_STORE_LOGJOINT) return FGMM_ERR_INVALID_ARG;
-  if (N < 0 || K < 0 || D < 1) return FGMM_ERR_INVALID_ARG;
-  if (fgmm_iso_workspace_bytes_ex(N, K, D, flags) > FGMM_NOALLOC_SCRATCH_BYTES) return FGMM_ERR_SCRATCH;
-  void* ws = nullptr;
-  const int st = current_scratch(&ws);
-  if (st != FGMM_OK) return st;
-  return fgmm_iso_estep_f32(X, ldx, N, D, mu, ldmu, K, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, ws,
-                            FGMM_NOALLOC_SCRATCH_BYTES, flags, stream);
 }

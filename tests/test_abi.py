@@ -195,3 +195,41 @@ def test_reference_module_names_resolve():
                     ("flash_gmm_full_h100", "flash_gmm_estep_full")):
         m = importlib.import_module(mod)
         assert getattr(m, fn) is getattr(flash_gmm, fn)
+
+
+def test_gather_slabs_keep_row_state_offsets_in_32_bits():
+    """The gathering pass 2 reads a slab's row state through a buffer resource with
+    32-bit byte offsets, so no slab may hold more than 2^31 bytes of it.  At large N
+    with many components (few slabs wanted) the plan must take more slabs: seen here
+    through the workspace, whose slab partials grow with the slab count while the
+    other sections it adds between the two sizes are the row state and need words."""
+    L = _lib.lib()
+
+    def r8(n):
+        return -(-n // 8) * 8
+
+    def r4(n):
+        return -(-n // 4) * 4
+
+    # Isotropic: 16 bytes of row state per row; cap = 134,217,696 rows per slab.
+    K, D, DP = 16384, 16, 32
+    KB, KP = K // 32, K
+    N1, N2 = 1 << 26, 1 << 30
+    grow = L.fgmm_iso_workspace_bytes(N2, K, D) - L.fgmm_iso_workspace_bytes(N1, K, D)
+    fixed = 16 * (N2 - N1) + 4 * KB * (r8(N2 // 32) - r8(N1 // 32))
+    per_slab = KP * (DP + 2) * 4
+    cap = ((1 << 31) - 256) // 16 // 32 * 32
+    slabs_added = -(-N2 // cap) - 4          # 4 slabs at N1 (one group of four)
+    assert slabs_added == 5
+    assert abs(grow - fixed - slabs_added * per_slab) <= 16 * 256
+    # Diagonal: 8 bytes of row state per row; cap = 268,435,424 rows per slab.
+    K, D, DP = 16384, 32, 32
+    KB, KP = K // 32, K
+    N1, N2 = 1 << 26, 1 << 31
+    grow = L.fgmm_diag_workspace_bytes(N2, K, D) - L.fgmm_diag_workspace_bytes(N1, K, D)
+    fixed = 8 * (N2 - N1) + 8 * KB * (r4(N2 // 32) - r4(N1 // 32))
+    per_slab = KP * (2 * DP + 1) * 4
+    cap = ((1 << 31) - 256) // 8 // 32 * 32
+    slabs_added = -(-N2 // cap) - 4
+    assert slabs_added == 5
+    assert abs(grow - fixed - slabs_added * per_slab) <= 16 * 256

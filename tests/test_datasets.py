@@ -63,6 +63,14 @@ def test_malformed_and_missing_files_are_rejected(tmp_path):
         fh.write(np.array([10, 4], np.uint32).tobytes() + np.zeros(8, np.float32).tobytes())
     with pytest.raises(FlashGMMError):
         datasets.VecsFile(short)
+    # Headers whose n * d * 4 passes 2^64 (and would wrap to a small size in a
+    # product test): n = d = 2^31 and n = d = 2^32 - 1; and one far too large for bytes.
+    for ext, n, d in ((".fbin", 1 << 31, 1 << 31), (".fbin", 2**32 - 1, 2**32 - 1), (".u8bin", 1 << 31, 1 << 31)):
+        wrap = str(tmp_path / ("wrap" + ext))
+        with open(wrap, "wb") as fh:
+            fh.write(np.array([n, d], np.uint32).tobytes() + np.zeros(16, np.float32).tobytes())
+        with pytest.raises(FlashGMMError):
+            datasets.VecsFile(wrap)
     with pytest.raises(FlashGMMError):
         datasets.VecsFile(str(tmp_path / "absent.fvecs"))
     with pytest.raises(FlashGMMError):

@@ -48,6 +48,29 @@ def _run(inp, dev, noalloc, flags=0, outs=None):
     return o
 
 
+def test_scratch_is_reserved_by_the_first_noalloc_call(gpu_device):
+    """The scratch array is its own code object's: HIP loads that code object on its first
+    use, the first noalloc call's symbol lookup, so a process that only calls the
+    workspace entry points does not reserve it.  Measured as the device's free memory
+    around the first noalloc call of this process (none ran before this test's call:
+    this file runs last and this test only the workspace entry point before it)."""
+    dev = gpu_device
+    inp = data.iso_clustered(3000, 64, 32, seed=35)
+    _run(inp, dev, noalloc=False)                   # the isotropic kernels are loaded
+    X, mu, lss, lpi = _inputs(inp, dev)
+    o = _outputs(3000, 64, 32, dev)
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info(dev)
+    L = _lib.lib()
+    st = L.fgmm_iso_estep_f32_noalloc(X.data_ptr(), 32, 3000, 32, mu.data_ptr(), 32, 64, lss.data_ptr(),
+                                      lpi.data_ptr(), *[t.data_ptr() for t in o], 0, _lib.stream_handle(dev))
+    _lib.check(st, "noalloc")
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info(dev)
+    print(f"device free memory around the first noalloc call: {free0} -> {free1} "
+          f"({(free0 - free1) / 2**20:.1f} MiB)", flush=True)
+
+
 def test_noalloc_equals_the_workspace_entry_point_on_two_calls(gpu_device):
     """Two calls in a row on one GPU's scratch, the second smaller (fewer rows, blocks
     and dimensions): each bitwise equal to the workspace entry point, the second also
@@ -104,3 +127,42 @@ def test_noalloc_rejects_what_does_not_fit(gpu_device):
     assert st == _lib.FGMM_ERR_INVALID_ARG
     torch.cuda.synchronize()
     assert torch.isnan(os_[1]).all()   # nothing was written
+
+
+def test_noalloc_under_graph_capture(gpu_device):
+    """The entry point captured into a HIP graph (torch.cuda.graph) after one warm-up
+    call: each replay, with new inputs copied into the captured buffers and eager work
+    and synchronisations between replays, bitwise equal to fgmm_iso_estep_f32 on the
+    same inputs."""
+    dev = gpu_device
+    N, K, D = 20000, 256, 128
+    sets = [data.iso_clustered(N, K, D, seed=40 + i) for i in range(3)]
+    X, mu, lss, lpi = _inputs(sets[0], dev)
+    o = _outputs(N, K, D, dev)
+    L = _lib.lib()
+
+    def call():
+        st = L.fgmm_iso_estep_f32_noalloc(X.data_ptr(), D, N, D, mu.data_ptr(), D, K, lss.data_ptr(),
+                                          lpi.data_ptr(), *[t.data_ptr() for t in o], 0,
+                                          _lib.stream_handle(dev))
+        _lib.check(st, "noalloc")
+
+    call()                                 # warm-up: symbol lookup and kernel attributes
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        inp = sets[rep % 3]
+        src = _inputs(inp, dev)
+        for dst, s in zip((X, mu, lss, lpi), src):
+            dst.copy_(s)
+        for t in o:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        ref = _run(inp, dev, noalloc=False)
+        for u, v in zip(o, ref):
+            assert torch.equal(u, v), f"replay {rep}"
