@@ -52,16 +52,44 @@ WORKLOADS = {
     "full_n100k_k64_d256": (100_000, 64, 256),
 }
 
-# HBM bytes per launch of the dominant kernel: rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE (separate runs) on this bench command, scaled by what the counters read
-# for a 512 MiB device copy (bench.py --copy-calibration 512: FETCH_SIZE x2.0,
-# WRITE_SIZE x1.0); the counter values and commands are in profiles/.
+# HBM traffic per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (separate runs)
+# on this bench command (--steps 2 --warmup 1 --no-cpu-baseline --no-extra-runs), each
+# scaled by what the counter reads for a 512 MiB device copy (bench.py
+# --copy-calibration 512: FETCH_SIZE x2.0, WRITE_SIZE x1.0).  Per kernel of one step:
+# (FETCH_SIZE KiB, WRITE_SIZE KiB); the commands and tables are in profiles/.
+TRAFFIC_KIB = {
+    # (workload, plan, precision): {kernel: (fetch KiB, write KiB)}; "phase1" names pass 1's
+    ("iso_n1m_k1024_d128", "default", "fp32"): {
+        "phase1": "iso_lse_pipe<128, 1>",
+        "iso_prep": (314, 1_104), "iso_lse_pipe<128, 1>": (311_019, 24_415),
+        "iso_accum_gather<128>": (268_553, 33_280), "iso_accum_tiles2<128>": (22, 0),
+        "iso_reduce": (20_873, 662)},
+    ("diag_n1m_k1024_d96", "default", "fp32"): {
+        "phase1": "diag_lse_x6<96, 2>",
+        "diag_x6_prep": (457, 1_552), "diag_lse_x6<96, 2>": (193_991, 19_532),
+        "diag_accum_gather<96>": (207_844, 49_408), "diag_reduce": (25_823, 780)},
+    ("full_n250k_k256_d64", "default", "fp32"): {
+        "phase1": "full_lse_x6<64, 2>",
+        "full_x6_prep": (2_130, 8_328), "full_lse_x6<64, 2>": (332_914, 135_805),
+        "full_accum_gather<64, 0>": (68_315, 25_150), "full_reduce_sig": (12_323, 4_096),
+        "full_reduce": (284, 65)},
+    ("full_n100k_k64_d128", "default", "fp32"): {
+        "phase1": "full_lse_x6<128, 2>",
+        "full_x6_prep": (2_108, 8_258), "full_lse_x6<128, 2>": (138_802, 49_128),
+        "full_accum_gather<128, 0>": (94_638, 82_968), "full_reduce_sig": (40_995, 4_096),
+        "full_reduce": (540, 32)},
+}
+
+
+def _kib_bytes(fw):
+    return fw[0] * 2048 + fw[1] * 1024
+
+
 TRAFFIC_BYTES = {
-    # (workload, plan, precision): {phase: bytes of its main kernel}
-    ("iso_n1m_k1024_d128", "default", "fp32"): {"phase1": 305_014 * 2048 + 24_414 * 1024},    # iso_lse<128, 2>
-    ("diag_n1m_k1024_d96", "default", "fp32"): {"phase1": 193_935 * 2048 + 19_532 * 1024},    # diag_lse_x6<96, 2>
-    ("full_n250k_k256_d64", "default", "fp32"): {"phase1": 329_068 * 2048 + 135_802 * 1024},  # full_lse_x6<64, 2>
-    ("full_n100k_k64_d128", "default", "fp32"): {"phase1": 125_725 * 2048 + 18_587 * 1024},   # full_lse_x6<128, 2>
+    key: {"phase1": _kib_bytes(v[v["phase1"]]),
+          "step": sum(_kib_bytes(fw) for k, fw in v.items() if k != "phase1"),
+          "step_kernels": {k: _kib_bytes(fw) for k, fw in v.items() if k != "phase1"}}
+    for key, v in TRAFFIC_KIB.items()
 }
 
 
@@ -286,9 +314,37 @@ def time_steps(call, steps, warmup, stream, dense=False):
     return ms, p1, p2
 
 
+def time_dropin(kind, inp, steps, warmup, stream):
+    """The reference's own call, timed as a whole: flash_gmm_estep (or its diagonal /
+    full counterpart) on device-resident inputs, with its output allocation, argument
+    checks and workspace (torch's caching allocator) inside the timing.  W untimed calls,
+    then K timed ones between two synchronisations, HIP events on the stream around
+    each call; returns (mean ms per call over the K calls, median per-call ms)."""
+    import torch
+    from flash_gmm import flash_gmm_estep, flash_gmm_estep_diag, flash_gmm_estep_full
+    fn = {"iso": flash_gmm_estep, "diag": flash_gmm_estep_diag, "full": flash_gmm_estep_full}[kind]
+    third = "prec_chol" if kind == "full" else "log_sigma_sq"
+    args = (inp["X"], inp["mu"], inp[third], inp["log_pi"])
+    for _ in range(warmup):
+        fn(*args)
+    torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    evs[0].record(stream)
+    for i in range(steps):
+        fn(*args)
+        evs[i + 1].record(stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(steps))
+    return start.elapsed_time(end) / steps, per[len(per) // 2]
+
+
 KERNELS = {
     # (kind, plan) -> (pass-1 kernel, pass-2 kernel)
-    ("iso", "default"): ("iso_lse (need masks)", "iso_accum_gather / iso_accum_tiles (by the needed-pair count)"),
+    ("iso", "default"): ("iso_lse_pipe (need masks)", "iso_accum_gather / iso_accum_tiles (by the needed-pair count)"),
     ("iso", "default_wide"): ("iso_lse_ctile (need masks)", "iso_accum_drange"),
     ("iso", "stored"): ("iso_lse (stores the log-joint)", "iso_accum_sparse / iso_accum_lj"),
     ("iso", "stored_wide"): ("iso_lse_ctile (stores the log-joint)", "iso_accum_lj"),
@@ -336,10 +392,19 @@ def main_workload(args):
     bf16 = args.precision == "bf16"
     log(f"generating workload {workload} on {torch.cuda.get_device_name(dev)}")
     inp, outs, r = measure(args, workload, args.precision, args.store_log_joint, dev)
-    ms, p1, p2 = r["ms"], r["p1"], r["p2"]
-    log(f"timed {args.steps} steps: {ms:.3f} ms/step (phase1 {p1:.3f} ms, phase2 {p2:.3f} ms)")
+    split_ms, p1, p2 = r["ms"], r["p1"], r["p2"]
+    log(f"timed {args.steps} steps as two phase calls: {split_ms:.3f} ms/step (phase1 {p1:.3f} ms, "
+        f"phase2 {p2:.3f} ms)")
     logZ = outs[0].clone()
     stream = torch.cuda.current_stream(dev)
+    # The step: the whole drop-in call (outputs allocated, arguments checked, one C call)
+    # for the default fp32 plan; the opt-in plans time their preallocated calls.
+    dropin = not bf16 and not args.store_log_joint
+    if dropin:
+        ms, med = time_dropin(kind, inp, args.steps, args.warmup, stream)
+        log(f"timed {args.steps} drop-in calls: {ms:.3f} ms/step (median call {med:.3f} ms)")
+    else:
+        ms, med = split_ms, None
 
     (flop, f1, f2), alg_bytes = algorithmic(kind, N, K, D)
     k1, k2 = kernel_names(kind, D, args.precision, args.store_log_joint)
@@ -435,7 +500,23 @@ def main_workload(args):
                                  "that runs it",
         "phases": phases,
         "roofline": roof,
+        "step_definition": ("one drop-in call (flash_gmm_estep and its diagonal / full counterparts: "
+                            "outputs allocated, arguments checked, both passes and the reduction)"
+                            if dropin else "one preallocated call per phase (opt-in plan)"),
+        "timing_paths": {"dropin_ms_per_call": ms if dropin else None,
+                         "dropin_median_call_ms": med,
+                         "phase_split_ms_per_step": split_ms,
+                         "note": "phase_split: the same work as two preallocated C calls "
+                                 "(FGMM_FLAG_PHASE1, then PHASE2) with HIP events between them; "
+                                 "the phases above come from it"},
     }
+    st = TRAFFIC_BYTES.get((workload, "stored" if args.store_log_joint else "default", args.precision), {})
+    if "step" in st:
+        out["step_traffic"] = {"bytes": st["step"], "algorithmic_bytes": alg_bytes,
+                               "over_algorithmic": st["step"] / alg_bytes,
+                               "kernels": st.get("step_kernels"),
+                               "basis": "HBM bytes of every kernel of one step, rocprofv3 FETCH_SIZE x2.0 "
+                                        "+ WRITE_SIZE x1.0 (calibrated on a device copy), profiles/"}
     if not args.no_extra_runs:
         call = r["call"]
         dms, d1, d2 = time_steps(call, args.steps, 2, stream, dense=True)
@@ -453,6 +534,21 @@ def main_workload(args):
             log(f"stored log-joint plan: {rs['ms']:.3f} ms/step")
             del rs
             torch.cuda.empty_cache()
+    if workload == "iso_n1m_k1024_d128" and not bf16 and not args.store_log_joint and not args.no_extra_runs:
+        # The reference's own benchmark data (flash_gmm.py:228-234: X, mu ~ N(0, I),
+        # lss = 0, uniform log pi), where every responsibility is nonzero.
+        ref_wl = "iso_ref_n1m_k1024_d128"
+        torch.cuda.empty_cache()
+        rinp, _, rr = measure(args, ref_wl, "fp32", False, dev)
+        rms, rmed = time_dropin("iso", rinp, args.steps, args.warmup, stream)
+        out["reference_smoke_workload"] = {
+            "workload": ref_wl, "N": N, "K": K, "D": D, "value": N / (rms * 1e-3), "unit": "samples/s",
+            "ms_per_step": rms, "median_call_ms": rmed, "phase1_ms": rr["p1"], "phase2_ms": rr["p2"],
+            "vs_baseline": (N / (rms * 1e-3)) / A100_SAMPLES_PER_S,
+            "data": "X, mu ~ N(0, I), lss = 0, log pi = -log K (flash_gmm.py:228-234), generated on device"}
+        log(f"reference smoke workload: {rms:.3f} ms/step (phase1 {rr['p1']:.3f}, phase2 {rr['p2']:.3f})")
+        del rinp, rr
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline and not bf16:
         log("timing the CPU baseline (bounded sample)")
         out["cpu_baseline"] = cpu_baseline(inp, kind, K, D, logZ)

@@ -142,8 +142,12 @@ int fgmm_iso_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
 /* capture, tight serving loops, harnesses that forbid hipMalloc).  The same   */
 /* computation and results as fgmm_iso_estep_f32 with the same flags, with its */
 /* workspace in a fixed device-resident scratch array of                       */
-/* FGMM_NOALLOC_SCRATCH_BYTES per GPU, held from the library's first such call */
-/* on that GPU until the process ends.  Calls whose workspace                  */
+/* FGMM_NOALLOC_SCRATCH_BYTES per GPU.  The array is the only content of its   */
+/* own code object, which HIP loads on a GPU at its first use there: the first */
+/* noalloc call on that GPU reserves it (other entry points never do; with     */
+/* deferred loading off, HIP_ENABLE_DEFERRED_LOADING=0, every code object is   */
+/* loaded with the library), and it is held until the process ends.  Calls     */
+/* whose workspace                                                             */
 /* (fgmm_iso_workspace_bytes_ex with the same flags) exceeds it return         */
 /* FGMM_ERR_SCRATCH: about 1.5M rows at K=1024, D=128 (N=1M fits).             */
 /* FGMM_FLAG_STORE_LOGJOINT is rejected (FGMM_ERR_INVALID_ARG).  Every call on */
