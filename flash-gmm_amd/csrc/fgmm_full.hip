@@ -1,4 +1,4 @@
-// Full-covariance GMM E-step for gfx950 (1 <= D <= 256).
+// Full-covariance GMM E-step for gfx950 (1 <= D <= 4096).
 //
 // Math (reference: flash_gmm_full_h100.py:289-296 constants, :103-130 pass 1,
 // :171-228 pass 2), with L_k lower-triangular, L_k L_k^T = Sigma_k^-1, in log2 units:
@@ -55,6 +55,8 @@ struct FullPlan {
   bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16); always stores the log-joint
   bool need;    // default plan: pass 1 leaves need masks, pass 2 gathers
   bool rexact;  // need masks from the per-(row, component) bounds (else the running max)
+  bool wide;    // D > 256: full_lse_wide stores the log-joint, full_accum_wide reads it
+  int nstrip;   // wide pass 2: strips of upper sig_outer blocks (one wave each)
   int ngrp;     // waves per (slab, component) in the gathering pass 2 (groups of sig blocks)
   int grid1;    // pass-1 workgroups with need masks (a persistent grid)
   size_t off_lop, off_bsw, off_ck, off_l3, off_esw, off_rowstat, off_part_sig, off_part_mu, off_part_nk,
@@ -87,6 +89,27 @@ __host__ __device__ constexpr int gather_sig_groups(int DP) {
 // split operands alone take 12 registers per 16 dimensions).
 __host__ __device__ constexpr int full_waves_per_eu(int DP) { return DP <= 128 ? 2 : 1; }
 
+// Above D = 256 (up to kFullMaxD) a row's split operands no longer fit in registers.
+// Pass 1 (full_lse_wide) re-reads and re-splits each row for every group of
+// kWideCG coordinate blocks and stores the log-joint; pass 2 (full_accum_wide)
+// reads r from it, so the whitening is formed once per (row, component), and
+// accumulates sig_outer in strips of up to kWideSW upper 32x32 blocks of one block
+// row, one wave per (slab, component, strip).  Row counts whose log-joint would
+// exceed kMaxLjBytes run as row chunks, as the bf16 contract does.
+constexpr int kFullMaxD = 4096;
+constexpr int kWideCG = 4;       // 32-coordinate blocks per pass-1 group
+constexpr int kWideWaves1 = 8;   // waves (32-row tiles) per pass-1 workgroup
+constexpr int kWideSW = 8;       // upper sig blocks per pass-2 strip
+constexpr int kWideWaves2 = 4;   // strips per pass-2 workgroup
+__host__ __device__ constexpr bool full_is_wide(int DP) { return DP > 256; }
+// Partials of the wide pass 2 (slabs x KP x NSB x 4 KiB) are capped at this size.
+constexpr size_t kWidePartBytes = (size_t)1 << 30;
+__host__ __device__ inline int wide_strips(int NMB) {
+  int s = 0;
+  for (int b1 = 0; b1 < NMB; ++b1) s += (NMB - b1 + kWideSW - 1) / kWideSW;
+  return s;
+}
+
 // Pass-2 layout of the bf16 contract (defined with its kernels below).
 __host__ __device__ constexpr int bf16_comps_per_wg(int NMB);
 __host__ __device__ constexpr int bf16_comp_reps(int NMB);
@@ -100,8 +123,11 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.NSB = p.NMB * (p.NMB + 1) / 2;
   p.KP = (int)round_up(K, kCompsPerWG);
   p.bf16 = bf16;
-  // The stored log-joint (and with it the bf16 contract) up to D = 128.
-  p.lj = (allow_lj || bf16) && K > 0 && p.DP <= 128 && full_lj_bytes(N, p.KP) <= kMaxLjBytes;
+  p.wide = !bf16 && full_is_wide(p.DP);
+  // The stored log-joint (and with it the bf16 contract) up to D = 128; above
+  // D = 256 always (the entry point chunks the rows to keep it within kMaxLjBytes).
+  p.lj = p.wide ? K > 0
+                : (allow_lj || bf16) && K > 0 && p.DP <= 128 && full_lj_bytes(N, p.KP) <= kMaxLjBytes;
   p.need = !bf16 && !p.lj && K > 0;
   p.rexact = p.need && K <= kNeedExactMaxK;
   p.ngrp = gather_sig_groups(p.DP);
@@ -110,6 +136,10 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
     p.rgroups = bf16_row_groups(p.NMB);
   } else if (p.need) {
     p.ncg = (int)K;   // one wave per (row slab, component)
+    p.rgroups = 1;
+  } else if (p.wide) {
+    p.nstrip = wide_strips(p.NMB);
+    p.ncg = (int)K;
     p.rgroups = 1;
   } else {
     p.ncg = p.KP / kCompsPerWG;
@@ -121,6 +151,15 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
     // slab holds a partial of D x D per component, so no more slabs than that).
     const int64_t want = gather_slab_count(cdiv((int64_t)8 * current_device_cus(), K * p.ngrp), cdiv(N, 32), kGatherWaves);
     p.rows_per_slab = cap_slab_rows(round_up(cdiv(N, want), 32), sizeof(double));
+    p.nslab = (int)cdiv(N, p.rows_per_slab);
+  } else if (p.wide && N > 0 && K > 0) {
+    // About two rounds of pass-2 waves at two waves per SIMD, within the partials' cap.
+    int64_t want = cdiv((int64_t)16 * current_device_cus(), K * p.nstrip);
+    const int64_t cap = (int64_t)(kWidePartBytes / ((size_t)p.KP * p.NSB * 1024 * sizeof(float)));
+    if (want > cap) want = cap;
+    if (want > cdiv(N, 32)) want = cdiv(N, 32);
+    if (want < 1) want = 1;
+    p.rows_per_slab = round_up(cdiv(N, want), 32);
     p.nslab = (int)cdiv(N, p.rows_per_slab);
   } else if (N > 0 && p.ncg > 0) {
     int64_t want = (int64_t)current_device_cus() / p.ncg;
@@ -1014,6 +1053,410 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
 }
 
 // ===========================================================================
+// Above D = 256 (any D up to kFullMaxD).  The prologue writes pass 1's operands in
+// full_x6_prep's layout (l3, esw, ck) from one workgroup per (component,
+// 32-coordinate block), without staging the o_qj of every coordinate in LDS.
+// Pass 1 (full_lse_wide) forms the whitening in the same centred split-bf16 form
+// and chain order as full_lse_x6, but the rows' split operands are re-read (L2)
+// and re-split for every group of kWideCG coordinate blocks instead of being held
+// in registers; it stores the log-joint.  Pass 2 (full_accum_wide) reads r from
+// it and accumulates sig_outer strip by strip.
+// ===========================================================================
+__global__ __launch_bounds__(256) void full_x6_prep_wide(const float* __restrict__ mu, int64_t ldmu,
+                                                         const float* __restrict__ L, int64_t K, int D, int DP,
+                                                         const float* __restrict__ lpi, bf16x8* __restrict__ l3,
+                                                         double* __restrict__ esw, double* __restrict__ ck) {
+  __shared__ double se[32];   // e_j of this block's coordinates
+  const int NQ = DP / 16, NMB = DP / 32;
+  const int64_t k = blockIdx.x / NMB;
+  const int mb = (int)(blockIdx.x % NMB);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, g = lane >> 5;
+  const bool valid = k < K;
+  const float* Lk = L + k * (int64_t)D * D;
+  // o_qj = sum over d in chunk q of L_dj mu_d, an fp64 fma chain in d order.
+  auto o_of = [&](int q, int j) -> double {
+    double o = 0.0;
+    if (valid && j < D)
+      for (int d = 16 * q; d < 16 * q + 16 && d < D; ++d) o = fma((double)Lk[(int64_t)d * D + j], (double)mu[k * ldmu + d], o);
+    return o;
+  };
+  // e_j = sum_q fp32(o_qj) - b_j with b_j = sum_q o_qj, both summed in q order.
+  if (tid < 32) {
+    double b = 0.0, osum = 0.0;
+    for (int q = 0; q < NQ; ++q) {
+      const double o = o_of(q, 32 * mb + tid);
+      osum += (double)(float)o;
+      b += o;
+    }
+    se[tid] = osum - b;
+  }
+  // Operands of chunks q = wave, wave + 4, ...: L^T split three ways, then the
+  // offset slot -o_qj in k slots 0..2 against x6c_ones.
+  const int j = 32 * mb + c;
+  for (int q = wave; q < NQ; q += 4) {
+    f32x4 lo = zero4(), hi = zero4();
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d0 = 16 * q + 8 * g + e, d1 = d0 + 4;
+      lo[e] = (valid && d0 < D && j < D) ? Lk[(int64_t)d0 * D + j] : 0.0f;
+      hi[e] = (valid && d1 < D && j < D) ? Lk[(int64_t)d1 * D + j] : 0.0f;
+    }
+    bf16x8 sp[3];
+    split3_bf16(lo, hi, sp);
+    bf16x8* dst = l3 + (((k * NMB + mb) * NQ + q) * 4) * 64 + lane;
+#pragma unroll
+    for (int t = 0; t < 3; ++t) dst[t * 64] = sp[t];
+    const float mo = -(float)o_of(q, j);
+    const f32x4 olo = {g == 0 ? mo : 0.0f, 0.0f, 0.0f, 0.0f};
+    bf16x8 os[3];
+    split3_bf16(olo, zero4(), os);
+    bf16x8 ov;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ov[e] = (__bf16)0.0f;
+    ov[0] = os[0][0];
+    ov[1] = os[1][0];
+    ov[2] = os[2][0];
+    dst[3 * 64] = ov;
+  }
+  __syncthreads();
+  if (tid < 32) {
+    const int gg = tid >> 4, i = tid & 15;
+    esw[(k * NMB + mb) * 32 + gg * 16 + i] = se[acc_row(i, gg)];
+  }
+  // c_k, the log-determinant summed in d order.
+  if (mb == 0 && tid == 0) {
+    double c0 = -INFINITY;
+    if (valid) {
+      double ld = 0.0;
+      for (int d = 0; d < D; ++d) ld += log(fabs((double)Lk[(int64_t)d * D + d]) + 1e-30);
+      c0 = ((double)lpi[k] + ld - 0.5 * (double)D * kLog2Pi) * kLog2e;
+    }
+    ck[k] = c0;
+  }
+}
+
+// Pass-1 stage: the operands of kWideCG coordinate blocks x two chunks (4 splits
+// each) of one component, and the blocks' e values and c_k.
+__host__ __device__ constexpr int wide_stage_ops() { return kWideCG * 2 * 4 * 64; }   // bf16x8
+__host__ __device__ constexpr int wide_stage_e() { return kWideCG * 32 + 8; }          // doubles
+__host__ __device__ constexpr size_t wide_lse_lds_bytes() {
+  return (size_t)2 * (wide_stage_ops() * sizeof(bf16x8) + wide_stage_e() * sizeof(double));
+}
+
+// One workgroup of kWideWaves1 waves per 32 kWideWaves1 rows; wave w owns tile
+// blockIdx.x kWideWaves1 + w (lane = row, both half-waves).  Stage s = (k ngrp +
+// grp) NQ/2 + qp runs chunks 2 qp and 2 qp + 1 of coordinate group grp of
+// component k for every block of the group: seven bf16 steps per (block, chunk) in
+// x6c_tile's order on the block's one accumulation chain, so each block's t equals
+// what full_lse_x6 forms.  After a group's last chunk pair its blocks' (t + e)^2
+// are added to maha in block order; after the component's last group the
+// log-joint is stored and the online log-sum-exp advances.
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kWideWaves1, 64 * kWideWaves1),
+                          amdgpu_waves_per_eu(2, 2)))
+void full_lse_wide(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int DP,
+                   const bf16x8* __restrict__ l3, const double* __restrict__ esw,
+                   const double* __restrict__ ck, int K, int KP, float* __restrict__ logZ,
+                   double* __restrict__ rowstat, float* __restrict__ lj) {
+  constexpr int T = 64 * kWideWaves1;
+  constexpr int SO = wide_stage_ops();
+  constexpr int LPT = SO / T;               // one coordinate block per fetch register
+  constexpr int NE = kWideCG * 32;
+  constexpr int BW = wide_stage_e();
+  static_assert(SO == LPT * T && T == 512 && LPT == kWideCG, "fetch index u is the block of the group");
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  bf16x8* l_l = reinterpret_cast<bf16x8*>(lds_raw);                              // [2][SO]
+  double* e_l = reinterpret_cast<double*>(lds_raw + 2 * SO * sizeof(bf16x8));   // [2][BW]
+
+  const int NMB = DP / 32, NQ = DP / 16, NQH = NQ / 2;
+  const int ngrp = (NMB + kWideCG - 1) / kWideCG;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t tile = (int64_t)blockIdx.x * kWideWaves1 + wave;
+  const int64_t row = tile * 32 + c;
+  const bool valid = row < N;
+  const int64_t nstage = (int64_t)K * ngrp * NQH;
+
+  // Stage s -> component, group, chunk pair.
+  auto decode = [&](int64_t s, int64_t& k, int& grp, int& qp) {
+    qp = (int)(s % NQH);
+    const int64_t kg = s / NQH;
+    grp = (int)(kg % ngrp);
+    k = kg / ngrp;
+  };
+  bf16x8 st[LPT];
+  double est = 0.0;
+  auto fetch = [&](int64_t s) {
+    int64_t k;
+    int grp, qp;
+    decode(s, k, grp, qp);
+    const int mb0 = grp * kWideCG;
+    const int cnt = NMB - mb0 < kWideCG ? NMB - mb0 : kWideCG;
+    // Register u holds block mb0 + u: (chunk 2 qp + (tid >> 8) & 1, split (tid >> 6) & 3, lane).
+    const int qq = (tid >> 8) & 1, sp = (tid >> 6) & 3;
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      if (u < cnt) {
+        st[u] = l3[(((k * NMB + mb0 + u) * NQ + 2 * qp + qq) * 4 + sp) * 64 + lane];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) st[u][e] = (__bf16)0.0f;
+      }
+    }
+    if (tid < NE) est = tid < cnt * 32 ? esw[(k * NMB + mb0) * 32 + tid] : 0.0;
+    else if (tid == NE) est = ck[k];
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) l_l[buf * SO + u * T + tid] = st[u];
+    if (tid <= NE) e_l[buf * BW + tid] = est;
+  };
+  // This lane's row, dimensions 16q + 8g .. +7 of the stage's two chunks.
+  f32x4 raw[4];
+  auto loadx = [&](int64_t s) {
+    const int qp = (int)(s % NQH);
+#pragma unroll
+    for (int qq = 0; qq < 2; ++qq) {
+      const int d0 = 16 * (2 * qp + qq) + 8 * g;
+      raw[2 * qq] = load_row4(X, ldx, row, d0, D, valid);
+      raw[2 * qq + 1] = load_row4(X, ldx, row, d0 + 4, D, valid);
+    }
+  };
+
+  f32x16 acc[kWideCG];
+#pragma unroll
+  for (int u = 0; u < kWideCG; ++u) acc[u] = zero16();
+  const bf16x8 ones = x6c_ones(lane);
+  const double hl = 0.5 * kLog2e;
+  double mx = -INFINITY, maha = 0.0;
+  float sm = 0.0f;
+  float* ljt = lj + tile * KP * 32 + c;
+
+  if (nstage > 0) {
+    fetch(0);
+    loadx(0);
+    commit(0);
+  }
+  __syncthreads();
+  for (int64_t s = 0; s < nstage; ++s) {
+    const int buf = (int)(s & 1);
+    const bool more = s + 1 < nstage;
+    int64_t k;
+    int grp, qp;
+    decode(s, k, grp, qp);
+    const int cnt = NMB - grp * kWideCG < kWideCG ? NMB - grp * kWideCG : kWideCG;
+    bf16x8 xb[2][3];
+    split3_bf16(raw[0], raw[1], xb[0]);
+    split3_bf16(raw[2], raw[3], xb[1]);
+    if (more) {
+      fetch(s + 1);
+      loadx(s + 1);
+    }
+    const bf16x8* lc = l_l + buf * SO + lane;
+#pragma unroll
+    for (int u = 0; u < kWideCG; ++u) {
+      if (u < cnt) {
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq) {
+          bf16x8 a[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) a[t] = lc[((u * 2 + qq) * 4 + t) * 64];
+          // x6c_tile's steps: x2 mu2, x1 mu3, x3 mu1, x2 mu1, x1 mu2, -o, x1 mu1.
+#pragma unroll
+          for (int step = 0; step < 7; ++step) {
+            const bf16x8 A = step == 0 ? a[1] : step == 1 ? a[2] : step <= 3 ? a[0]
+                           : step == 4 ? a[1] : step == 5 ? a[3] : a[0];
+            const bf16x8 B = step == 0 ? xb[qq][1] : step == 1 ? xb[qq][0] : step == 2 ? xb[qq][2]
+                           : step == 3 ? xb[qq][1] : step == 4 ? xb[qq][0] : step == 5 ? ones : xb[qq][0];
+            acc[u] = mfma_bf16(A, B, acc[u]);
+          }
+        }
+      }
+    }
+    if (qp == NQH - 1) {   // the group's blocks are complete
+      const double* ec = e_l + buf * BW;
+#pragma unroll
+      for (int u = 0; u < kWideCG; ++u) {
+        if (u < cnt) {
+          const double* eb = ec + u * 32 + g * 16;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const double v = (double)acc[u][i] + eb[i];
+            maha = fma(v, v, maha);
+          }
+        }
+        acc[u] = zero16();
+      }
+      if (grp == ngrp - 1) {   // component k is complete
+        maha += __shfl_xor(maha, 32);
+        const double ll = ec[NE] - hl * maha;
+        if (valid && g == 0) ljt[k * 32] = (float)ll;
+        const double mn = fmax(mx, ll);
+        const double ms = (mn == -INFINITY) ? 0.0 : mn;
+        sm = sm * fast_exp2((float)(mx - ms)) + fast_exp2((float)(ll - ms));
+        mx = mn;
+        maha = 0.0;
+      }
+    }
+    if (more) commit(buf ^ 1);
+    lds_barrier();
+  }
+  const double lz2 = mx + (double)log2f(sm);
+  if (valid && g == 0) {
+    rowstat[row] = lz2;
+    if (logZ) logZ[row] = (float)(lz2 * kLn2);
+  }
+}
+
+// Pass 2 above D = 256: one wave per (row slab, component, strip), where strip
+// (b1, b2s) holds the upper blocks (b1, b2), b2s <= b2 < b2s + kWideSW, of one
+// block row of sig_outer; the strips of a (slab, component) are dealt in fours to
+// workgroups.  Per 32-row tile the lanes form r = 2^(ll2 - logZ2) from the stored
+// log-joint; tiles and 16-row steps with no nonzero r are skipped.  Each step forms
+// a = r x over block b1 and accumulates a x^T into every block of the strip as six
+// split-bf16 products (the gathering pass 2's order); the strip starting on the
+// diagonal also sums mu_acc of block b1, and strip 0 Nk.  Rows are read from L2
+// (each 32-column slice of a row is one 128-byte line per 32 lanes).
+__global__ __launch_bounds__(64 * kWideWaves2)
+void full_accum_wide(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int DP, int K, int KP,
+                     const double* __restrict__ rowstat, const float* __restrict__ lj, int nslab,
+                     int64_t rows_per_slab, int nstrip, float* __restrict__ part_sig,
+                     float* __restrict__ part_mu, float* __restrict__ part_nk, int dense) {
+  __shared__ float r_all[kWideWaves2][32];
+  const int NMB = DP / 32;
+  const int64_t NSB = (int64_t)NMB * (NMB + 1) / 2;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int nsg = (nstrip + kWideWaves2 - 1) / kWideWaves2;
+  const int sgp = (int)(blockIdx.x % nsg);
+  const int64_t rest = blockIdx.x / nsg;
+  const int k = (int)(rest % K);
+  const int slab = (int)(rest / K);
+  const int strip = sgp * kWideWaves2 + wave;
+  if (strip >= nstrip || slab >= nslab) return;   // no barrier in this kernel
+  int b1 = 0, sr = strip;
+  for (;;) {
+    const int ns = (NMB - b1 + kWideSW - 1) / kWideSW;
+    if (sr < ns) break;
+    sr -= ns;
+    ++b1;
+  }
+  const int b2s = b1 + sr * kWideSW;
+  const int cnt = NMB - b2s < kWideSW ? NMB - b2s : kWideSW;
+  const bool first = b2s == b1;   // forms mu_acc of block b1
+  const bool nkw = strip == 0;    // forms Nk
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+
+  f32x16 acc[kWideSW];
+#pragma unroll
+  for (int j = 0; j < kWideSW; ++j) acc[j] = zero16();
+  float mua = 0.0f, nk = 0.0f;
+  float* rx = r_all[wave];
+  const int cb1 = 32 * b1 + c;
+  auto xval = [&](int64_t rw, int col) -> float {
+    return (rw < r_end && col < D) ? X[rw * ldx + col] : 0.0f;
+  };
+
+  for (int64_t r0 = r_begin; r0 < r_end; r0 += 32) {
+    const int64_t row = r0 + c;
+    float rv = 0.0f;
+    if (row < r_end) {
+      const float l = lj[((row >> 5) * KP + k) * 32 + (row & 31)];
+      rv = fast_exp2((float)((double)l - rowstat[row]));
+    }
+    if (nkw && g == 0) nk += rv;
+    const unsigned nz = (unsigned)__builtin_amdgcn_ballot_w64(rv != 0.0f);   // lanes 0..31: rows
+    if (!dense && nz == 0u) continue;
+    if (g == 0) rx[c] = rv;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if (!dense && ((nz >> (16 * p)) & 0xffffu) == 0u) continue;
+      const int rb = 16 * p + 8 * g;   // this lane's rows rb .. rb + 7 of the tile
+      float a[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        a[e] = rx[rb + e] * xval(r0 + rb + e, cb1);
+        if (first) mua += a[e];
+      }
+      bf16x8 ba[3];
+      split3_bf16(f32x4{a[0], a[1], a[2], a[3]}, f32x4{a[4], a[5], a[6], a[7]}, ba);
+#pragma unroll
+      for (int j = 0; j < kWideSW; ++j) {
+        if (j < cnt) {
+          const int col = 32 * (b2s + j) + c;
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = xval(r0 + rb + e, col);
+          bf16x8 bx[3];
+          split3_bf16(f32x4{v[0], v[1], v[2], v[3]}, f32x4{v[4], v[5], v[6], v[7]}, bx);
+          f32x16& t = acc[j];
+          t = mfma_bf16(ba[2], bx[0], t);
+          t = mfma_bf16(ba[1], bx[1], t);
+          t = mfma_bf16(ba[0], bx[2], t);
+          t = mfma_bf16(ba[1], bx[0], t);
+          t = mfma_bf16(ba[0], bx[1], t);
+          t = mfma_bf16(ba[0], bx[0], t);
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  const int64_t pbase = (int64_t)slab * KP + k;
+  float* ps = part_sig + pbase * NSB * 1024;
+  const int64_t sb0 = (int64_t)b1 * NMB - (int64_t)b1 * (b1 - 1) / 2 + (b2s - b1);
+#pragma unroll
+  for (int j = 0; j < kWideSW; ++j) {
+    if (j < cnt) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) ps[(sb0 + j) * 1024 + acc_row(i, g) * 32 + c] = acc[j][i];
+    }
+  }
+  if (first) {
+    const float v = mua + __shfl_xor(mua, 32);
+    if (g == 0) part_mu[pbase * DP + cb1] = v;
+  }
+  if (nkw) {
+    float nks = nk;
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) nks += __shfl_xor(nks, o);
+    if (lane == 0) part_nk[pbase] = nks;
+  }
+}
+
+hipError_t launch_wide(const FullPlan& pl, const float* X, int64_t ldx, unsigned char* ws, float* logZ,
+                       bool run1, bool run2, bool dense, hipStream_t stream) {
+  const double* ck = reinterpret_cast<const double*>(ws + pl.off_ck);
+  double* rowstat = reinterpret_cast<double*>(ws + pl.off_rowstat);
+  float* lj = reinterpret_cast<float*>(ws + pl.off_lj);
+  if (run1) {
+    constexpr size_t lds1 = wide_lse_lds_bytes();
+    static_assert(lds1 <= (size_t)160 * 1024, "pass-1 stages fit LDS");
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&full_lse_wide),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(full_lse_wide, dim3((unsigned)cdiv(pl.N, 32 * kWideWaves1)), dim3(64 * kWideWaves1), lds1,
+                       stream, X, ldx, pl.N, (int)pl.D, pl.DP, reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
+                       reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, logZ, rowstat, lj);
+  }
+  if (!run2) return hipGetLastError();
+  const int64_t nsg = cdiv(pl.nstrip, kWideWaves2);
+  hipLaunchKernelGGL(full_accum_wide, dim3((unsigned)((int64_t)pl.nslab * pl.K * nsg)), dim3(64 * kWideWaves2), 0,
+                     stream, X, ldx, pl.N, (int)pl.D, pl.DP, (int)pl.K, pl.KP, rowstat, lj, pl.nslab,
+                     pl.rows_per_slab, pl.nstrip, reinterpret_cast<float*>(ws + pl.off_part_sig),
+                     reinterpret_cast<float*>(ws + pl.off_part_mu), reinterpret_cast<float*>(ws + pl.off_part_nk),
+                     dense ? 1 : 0);
+  return hipGetLastError();
+}
+
+// ===========================================================================
 // bf16 operand contract (FGMM_FLAG_BF16), the arithmetic of the reference's full
 // H100 kernels (flash_gmm_full_h100.py:71-139 pass 1, :146-228 pass 2, :289-298
 // constants), in log2 units:
@@ -1490,10 +1933,11 @@ hipError_t launch_bf16(const FullPlan& pl, const float* X, int64_t ldx, unsigned
 using namespace fgmm;
 
 namespace {
-// Rows per call of the bf16 contract, whose log-joint (N/32 tiles of KP x 32 floats)
-// must fit kMaxLjBytes: a multiple of 128 rows.  Larger calls run in chunks of this
-// many rows.
-int64_t full_bf16_chunk_rows(int64_t K) {
+// Rows per call of the plans that always store the log-joint (the bf16 contract and
+// D > 256), whose N/32 tiles of KP x 32 floats must fit kMaxLjBytes: a multiple of
+// 128 rows.  Larger calls run in chunks of this many rows.
+bool full_lj_chunked(int64_t D, bool bf16) { return bf16 || full_is_wide((int)round_up(D, 32)); }
+int64_t full_lj_chunk_rows(int64_t K) {
   const int64_t KP = round_up(K < 1 ? 1 : K, kCompsPerWG);
   const int64_t tiles = (int64_t)(kMaxLjBytes / ((size_t)KP * 32 * sizeof(float))) / 4 * 4;
   return tiles * 32;
@@ -1501,14 +1945,14 @@ int64_t full_bf16_chunk_rows(int64_t K) {
 }  // namespace
 
 extern "C" size_t fgmm_full_workspace_bytes(int64_t N, int64_t K, int64_t D) {
-  if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D, false).total;
+  return fgmm_full_workspace_bytes_ex(N, K, D, 0u);
 }
 
 extern "C" size_t fgmm_full_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
   if (N < 0 || K < 0 || D < 1) return 0;
   const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
-  const int64_t rows = bf16 ? std::min(N, full_bf16_chunk_rows(K)) : N;
+  if (D > (bf16 ? 128 : kFullMaxD)) return 0;
+  const int64_t rows = full_lj_chunked(D, bf16) ? std::min(N, full_lj_chunk_rows(K)) : N;
   return make_plan(rows, K, D, wants_stored_lj(flags), bf16).total;
 }
 
@@ -1531,13 +1975,18 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     return FGMM_ERR_INVALID_ARG;
   if (N > kMaxRows || K > (int64_t)1 << 20) return FGMM_ERR_UNSUPPORTED;
   const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
-  if (D > (bf16 ? 128 : 256)) return FGMM_ERR_UNSUPPORTED;
-  if (bf16 && K > 0 && N > full_bf16_chunk_rows(K)) {
-    // The bf16 contract stores the log-joint, at most kMaxLjBytes per call: larger N
-    // runs as consecutive row chunks on one workspace, each chunk after the first
-    // adding its statistics to the outputs.  A phase split cannot span the chunks.
+  if (D > (bf16 ? 128 : kFullMaxD)) return FGMM_ERR_UNSUPPORTED;
+  {
+    // Launch grids: the sig_outer finish runs one workgroup per (component, upper block).
+    const int64_t nmb = cdiv(D, 32);
+    if (K * (nmb * (nmb + 1) / 2) >= ((int64_t)1 << 24)) return FGMM_ERR_UNSUPPORTED;
+  }
+  if (full_lj_chunked(D, bf16) && K > 0 && N > full_lj_chunk_rows(K)) {
+    // The bf16 contract and D > 256 store the log-joint, at most kMaxLjBytes per call:
+    // larger N runs as consecutive row chunks on one workspace, each chunk after the
+    // first adding its statistics to the outputs.  A phase split cannot span the chunks.
     if (flags & (FGMM_FLAG_PHASE1 | FGMM_FLAG_PHASE2)) return FGMM_ERR_UNSUPPORTED;
-    const int64_t rows = full_bf16_chunk_rows(K);
+    const int64_t rows = full_lj_chunk_rows(K);
     for (int64_t r0 = 0; r0 < N; r0 += rows) {
       const int64_t n = std::min(rows, N - r0);
       const unsigned f = r0 == 0 ? flags : (flags | FGMM_FLAG_ACCUMULATE);
@@ -1567,6 +2016,10 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     hipLaunchKernelGGL(full_bf16_prep, dim3((unsigned)pl.KP), dim3(64), 0, stream, mu, ldmu, prec_chol, K,
                        (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_lop),
                        reinterpret_cast<float*>(ws + pl.off_bsw), reinterpret_cast<float*>(ws + pl.off_ck));
+  else if (run1 && pl.wide)
+    hipLaunchKernelGGL(full_x6_prep_wide, dim3((unsigned)((int64_t)pl.KP * pl.NMB)), dim3(256), 0, stream, mu,
+                       ldmu, prec_chol, K, (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_l3),
+                       reinterpret_cast<double*>(ws + pl.off_esw), reinterpret_cast<double*>(ws + pl.off_ck));
   else if (run1)
     hipLaunchKernelGGL(full_x6_prep, dim3((unsigned)pl.KP), dim3(256), 0, stream, mu, ldmu, prec_chol, K,
                        (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_l3),
@@ -1581,7 +2034,8 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
         return launch_passes<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
     };
     hipError_t e = hipSuccess;
-    switch (pl.DP) {
+    switch (pl.wide ? 0 : pl.DP) {
+      case 0: e = launch_wide(pl, X, ldx, ws, logZ, run1, run2, dense, stream); break;
       case 32: e = run(std::integral_constant<int, 32>{}); break;
       case 64: e = run(std::integral_constant<int, 64>{}); break;
       case 96: e = run(std::integral_constant<int, 96>{}); break;

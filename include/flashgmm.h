@@ -34,7 +34,7 @@ extern "C" {
 enum fgmm_status {
     FGMM_OK = 0,
     FGMM_ERR_INVALID_ARG = -1, /* bad shape, stride, alignment or null pointer */
-    FGMM_ERR_UNSUPPORTED = -2, /* shape outside the supported range (e.g. full D > 256) */
+    FGMM_ERR_UNSUPPORTED = -2, /* shape outside the supported range (e.g. full D > 4096) */
     FGMM_ERR_WORKSPACE = -3,   /* workspace smaller than *_workspace_bytes() */
     FGMM_ERR_HIP = -4,         /* a HIP runtime call or kernel launch failed */
     FGMM_ERR_SOURCE = -5,      /* a host row source returned an error */
@@ -191,8 +191,12 @@ int fgmm_diag_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
 /*   ll_nk = log_pi_k + sum_d log(|L_k,dd| + 1e-30) - 0.5 D log(2 pi)         */
 /*           - 0.5 ||L_k^T (x_n - mu_k)||^2                                   */
 /*   sig_outer_k = sum_n r_nk x_n x_n^T   (uncentred second moment)           */
-/* Supports 1 <= D <= 256 (the bf16 contract and the stored log-joint:        */
-/* D <= 128).                                                                 */
+/* Supports 1 <= D <= 4096 (the bf16 contract and the stored log-joint:       */
+/* D <= 128) and K * u(u+1)/2 < 2^24 with u = ceil(D / 32).  Above D = 256    */
+/* pass 1 always stores the N x K log-joint (pass 2 reads r from it); calls   */
+/* whose log-joint would exceed 16 GiB run as row chunks, as with the bf16    */
+/* contract (a PHASE1 / PHASE2 call that needs more than one chunk returns    */
+/* FGMM_ERR_UNSUPPORTED).                                                     */
 /* ------------------------------------------------------------------------ */
 size_t fgmm_full_workspace_bytes(int64_t N, int64_t K, int64_t D);
 size_t fgmm_full_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags);
@@ -294,7 +298,10 @@ int fgmm_diag_mstep_f32(const float *Nk, const float *mu_acc, const float *sig_a
 /* mu and prec_chol and get log_pi = -inf.  info (device int, may be NULL,     */
 /* zeroed by the caller) is incremented for every component whose Sigma was  */
 /* not positive definite (its failing pivots are replaced by reg_covar).      */
-/* Supports 1 <= D <= 128.                                                    */
+/* Supports 1 <= D <= 4096.  Above D = 128 the fp64 matrices of each component */
+/* live in device scratch the call allocates and frees in stream order         */
+/* (hipMallocAsync / hipFreeAsync, at most 1 GiB; components run in batches);  */
+/* the work is O(D^3) per component.                                          */
 /* ------------------------------------------------------------------------ */
 int fgmm_full_mstep_f32(const float *Nk, const float *mu_acc, const float *sig_outer,
                         int64_t N, int64_t K, int64_t D, double reg_covar,

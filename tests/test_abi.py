@@ -163,18 +163,20 @@ def _call_full(D, flags=0):
 def test_dimension_limits():
     """Largest supported D per covariance model; one past it is UNSUPPORTED.  The
     isotropic and diagonal fp32 E-steps take any D, their bf16 contracts stop at 256;
-    the full-covariance E-step stops at 256, its bf16 contract at 128."""
+    the full-covariance E-step stops at 4096, its bf16 contract at 128."""
     assert _call_iso(D=257, ldx=260, ldmu=257, flags=_lib.FLAG_BF16) == _lib.FGMM_ERR_UNSUPPORTED
     assert _call_diag(257, flags=_lib.FLAG_BF16) == _lib.FGMM_ERR_UNSUPPORTED
-    assert _call_full(257) == _lib.FGMM_ERR_UNSUPPORTED
+    assert _call_full(4097) == _lib.FGMM_ERR_UNSUPPORTED
     assert _call_full(129, flags=_lib.FLAG_BF16) == _lib.FGMM_ERR_UNSUPPORTED
     # workspace queries accept the supported range
     L = _lib.lib()
     assert L.fgmm_iso_workspace_bytes(100, 10, 4000) > L.fgmm_iso_workspace_bytes(100, 10, 300) > 0
     assert L.fgmm_diag_workspace_bytes(100, 10, 1000) > L.fgmm_diag_workspace_bytes(100, 10, 256) > \
         L.fgmm_diag_workspace_bytes(100, 10, 128) > 0
-    assert L.fgmm_full_workspace_bytes(100, 10, 256) > L.fgmm_full_workspace_bytes(100, 10, 128) > \
+    assert L.fgmm_full_workspace_bytes(100, 10, 512) > L.fgmm_full_workspace_bytes(100, 10, 300) > \
+        L.fgmm_full_workspace_bytes(100, 10, 256) > L.fgmm_full_workspace_bytes(100, 10, 128) > \
         L.fgmm_full_workspace_bytes(100, 10, 64) > 0
+    assert L.fgmm_full_workspace_bytes(100, 10, 4096) > 0 == L.fgmm_full_workspace_bytes(100, 10, 4097)
 
 
 def test_python_layer_rejects_cpu_tensors():

@@ -1,7 +1,9 @@
-"""GPU parity of the full-covariance E-step above D = 128 (up to 256: pass 1 at one
-wave per SIMD, the gathering pass 2 with the upper blocks of sig_outer dealt to
-several waves per (slab, component)), against the float64 oracle.  The reference
-pads any D to a power of two (flash_gmm_full_h100.py:268)."""
+"""GPU parity of the full-covariance E-step above D = 128, against the float64 oracle.
+Up to D = 256 pass 1 runs at one wave per SIMD and the gathering pass 2 deals the
+upper blocks of sig_outer to several waves per (slab, component); above 256 pass 1
+(full_lse_wide) re-splits the rows per group of coordinate blocks and stores the
+log-joint, and pass 2 (full_accum_wide) reads r from it.  The reference pads any D
+to a power of two (flash_gmm_full_h100.py:268)."""
 
 import os
 import sys
@@ -110,3 +112,53 @@ def test_wide_d_mid_size(gpu_device):
     err = (got[0].cpu().double() - ref[0]).abs().max().item()
     print(f"full N=16384 K=64 D=200: max |logZ - oracle| = {err:.3e}", flush=True)
     check_wide(got, inp, "full N=16384 K=64 D=200", 200, ref=ref)
+
+
+# Above D = 256: one past the register-resident width, GloVe-300, a power of two,
+# ragged widths over several coordinate groups and sig strips, K = 1 at D = 1000.
+SHAPES_ABOVE_256 = [(257, 3, 257), (600, 5, 300), (400, 4, 512), (300, 2, 520), (65, 1, 1000)]
+
+
+@pytest.mark.parametrize("N,K,D", SHAPES_ABOVE_256)
+def test_above_256_against_oracle(N, K, D, gpu_device):
+    print(f"full wide N={N} K={K} D={D}", flush=True)
+    inp = data.full_clustered(N, K, D, seed=N + K + D)
+    got = _into(inp, gpu_device)
+    check_wide(got, inp, f"full N={N} K={K} D={D}", D)
+
+
+def test_above_256_dense_and_phase_split_are_bitwise(gpu_device):
+    """Above D = 256 pass 2 reads the stored log-joint: skipping the steps whose
+    responsibilities are zero adds nothing, so FGMM_FLAG_DENSE gives the same bits;
+    PHASE1 then PHASE2 on one workspace gives the single call's bits."""
+    N, K, D = 1500, 6, 300
+    inp = data.full_clustered(N, K, D, seed=21)
+    dev = gpu_device
+    ref = _into(inp, dev)
+    dense = _into(inp, dev, dense=True)
+    for u, v in zip(ref, dense):
+        assert torch.equal(u, v)
+    from flash_gmm import _lib
+    L = _lib.lib()
+    ws = torch.empty(L.fgmm_full_workspace_bytes(N, K, D), dtype=torch.uint8, device=dev)
+    out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, D, D, device=dev)]
+    args = [inp[k].to(dev) for k in KEYS]
+    full_estep_into(*args, *out, workspace=ws, phase=1)
+    full_estep_into(*args, None, *out[1:], workspace=ws, phase=2)
+    torch.cuda.synchronize()
+    for u, v in zip(out, ref):
+        assert torch.equal(u, v)
+
+
+def test_above_256_mid_size(gpu_device):
+    """D = 300 at N=8,192, K=16 against the float64 oracle, with the sig_outer
+    invariant sum_k sig_outer_k = X^T X."""
+    N, K, D = 8192, 16, 300
+    inp = data.full_clustered(N, K, D, seed=5)
+    got = _into(inp, gpu_device)
+    check_wide(got, inp, f"full N={N} K={K} D={D}", D)
+    X = inp["X"].double()
+    xtx = X.T @ X
+    tot = got[3].double().cpu().sum(0)
+    assert float((tot - xtx).abs().max()) <= 1e-4 * float(xtx.abs().max())
