@@ -32,6 +32,7 @@
 
 #include <math.h>
 
+#include <algorithm>
 #include <type_traits>
 
 namespace fgmm {
@@ -77,7 +78,14 @@ __host__ __device__ constexpr size_t accum_drange_lds_bytes(int DR) {
          + (size_t)kCtWaves * 64 * sizeof(int);              // row queue per wave
 }
 
-// bf16 operand contract (defined with its kernels below).
+// bf16 operand contract (defined with its kernels below).  Above D = 256 it stores
+// the log-joint ([32-row tile][KP][32 rows], fp32).
+constexpr int kBwCB = 8;     // component blocks per wide bf16 pass-2 workgroup (one per wave)
+constexpr int kBwDR = 128;   // dimensions per wide bf16 pass-2 workgroup
+__host__ __device__ constexpr bool diag_bf16_wide(int DP) { return DP > 256; }
+__host__ inline size_t bw_lj_bytes(int64_t N, int KP) {
+  return (size_t)round_up(cdiv(N, 32), 4) * (size_t)KP * 32 * sizeof(float);
+}
 __host__ __device__ constexpr int bf16_parts(int DP);
 __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB);
 __host__ inline int bf16_blocks_per_group(int DP, int KB);
@@ -100,7 +108,8 @@ struct DiagPlan {
   bool need;        // default plan: pass 1 leaves need masks, pass 2 gathers the needed rows
   bool ctile;       // above D = 128: component-tiled pass 1 (both plans), range pass 2 (default)
   bool rexact;      // need masks from block maxima kept in LDS (else the running-max bound)
-  int ndr;          // dimension ranges of the range pass 2
+  int ndr;          // dimension ranges of the range pass 2 (and of the wide bf16 pass 2)
+  bool bfw;         // bf16 contract above D = 256: stored log-joint, diag_bf16_*_wide
   size_t off_musw, off_mu3, off_kcx6, off_kcx6lin, off_kclin, off_rowstat, off_part_mu,
       off_part_sq, off_part_nk, off_lj, off_ljmax, off_ljmask, off_ljcount, total;
 };
@@ -139,7 +148,12 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.ctile = !bf16 && !diag_uses_x6(p.DP);
   p.rexact = p.need && p.KB <= (p.ctile ? ctile_need_exact_cap(ctile_blocks(p.DP)) : need_exact_cap(p.DP));
   p.ndr = p.ctile ? (int)cdiv(p.DP, kDrange) : 1;
-  if (bf16) {
+  p.bfw = bf16 && diag_bf16_wide(p.DP);
+  if (p.bfw) {
+    p.cpg = kBwCB;
+    p.rgroups = 1;
+    p.ndr = (int)cdiv(p.DP, kBwDR);
+  } else if (bf16) {
     p.cpg = bf16_blocks_per_group(p.DP, p.KB);
     p.rgroups = bf16_row_partials(p.DP, p.cpg);
   } else if (p.lj) {
@@ -154,8 +168,14 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
     p.rgroups = 1;
   }
   p.ncg = (int)cdiv(p.KB, p.cpg);
-  const int64_t tile_rows = 32 * (bf16 ? kAccWaves / (p.cpg * bf16_parts(p.DP)) : p.rgroups);
-  if (p.need && p.ctile && N > 0 && p.KB > 0) {
+  const int64_t tile_rows = 32 * (bf16 && !p.bfw ? kAccWaves / (p.cpg * bf16_parts(p.DP)) : p.rgroups);
+  if (p.bfw && N > 0 && p.KB > 0) {
+    // About two workgroups per compute unit.
+    int64_t want = cdiv((int64_t)2 * current_device_cus(), (int64_t)p.ncg * p.ndr);
+    if (want > cdiv(N, 32)) want = cdiv(N, 32);
+    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.nslab = (int)cdiv(N, p.rows_per_slab);
+  } else if (p.need && p.ctile && N > 0 && p.KB > 0) {
     // One 4-wave workgroup per (slab, block, dimension range) and compute unit (its
     // X tile takes most of the LDS): about two rounds of workgroups.
     int64_t want = cdiv((int64_t)2 * current_device_cus(), (int64_t)p.KB * p.ndr);
@@ -201,7 +221,8 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.lj_sparse = p.lj && diag_uses_x6(p.DP);
   const size_t ntile = (p.lj || p.need) ? (size_t)round_up(cdiv(N, 32), 4) * p.KB : 0;
   const size_t nsp = (p.lj_sparse || p.need) ? ntile : 0;
-  p.off_lj = off;      off = align256(off + (p.lj ? ntile * kLjTile * sizeof(float) : 0));
+  p.off_lj = off;
+  off = align256(off + (p.bfw ? bw_lj_bytes(N, p.KP) : p.lj ? ntile * kLjTile * sizeof(float) : 0));
   p.off_ljmax = off;   off = align256(off + (p.lj_sparse ? nsp * 64 * sizeof(float) : 0));
   p.off_ljmask = off;  off = align256(off + nsp * sizeof(uint2));
   p.off_ljcount = off; off = align256(off + (p.lj_sparse ? 64 * sizeof(unsigned) : 0));
@@ -2539,10 +2560,364 @@ hipError_t launch_bf16(const DiagPlan& pl, const float* X, int64_t ldx, unsigned
                        : launch(std::integral_constant<int, 4>{});
 }
 
+// ---------------------------------------------------------------------------
+// bf16 operand contract above D = 256 (any D), as for the isotropic model: pass 1
+// (diag_bf16_lse_wide) tiles the contraction over components, re-reading each
+// wave's 32 rows per tile of kBwCTB component blocks, and accumulates fp32 chains of
+// x^2 and x over 256 dimensions at a time into an fp64 sum, to which c0 is added
+// in fp64; it stores the fp32 log-joint,
+// [32-row tile][KP][32 rows].  Pass 2 (diag_bf16_accum_wide) reads r from it and
+// accumulates bf16(r)^T bf16(x) and bf16(r)^T bf16(x^2) per range of kBwDR
+// dimensions from bf16 tiles of x and x^2 in LDS.  Calls whose log-joint exceeds
+// kMaxLjBytes run as row chunks.
+// ---------------------------------------------------------------------------
+constexpr int kBwCTB = 2;    // component blocks per pass-1 tile
+constexpr int kBwQS = 4;     // 16-dimension chunks per pass-1 stage
+constexpr int kBwFlush = 4;  // stages per fp32 chain: its sum then joins an fp64 one
+__host__ __device__ constexpr int bw_stage_ops() { return kBwCTB * 2 * kBwQS * 64; }   // bf16x8
+__host__ __device__ constexpr size_t bw_lse_lds_bytes() {
+  return (size_t)2 * (bw_stage_ops() * sizeof(bf16x8) + kBwCTB * 32 * sizeof(float));
+}
+
+__global__ __launch_bounds__(kThreads) void diag_bf16_lse_wide(const float* __restrict__ X, int64_t ldx,
+                                                               int64_t N, int D, int DP,
+                                                               const bf16x8* __restrict__ mu_op,
+                                                               const float* __restrict__ kc, int KB, int KP,
+                                                               float* __restrict__ logZ,
+                                                               float* __restrict__ rowstat,
+                                                               float* __restrict__ lj) {
+  constexpr int SO = bw_stage_ops();
+  constexpr int LPT = SO / kThreads;
+  static_assert(LPT == 2 * kBwCTB && kThreads == kBwQS * 64, "fetch register u = 2 block + feature");
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                               // [2][SO]
+  float* kc_l = reinterpret_cast<float*>(lds_raw + 2 * SO * sizeof(bf16x8));       // [2][CTB * 32]
+
+  const int NQ = DP / 16, NCF = DP / 8, nst = NQ / kBwQS;
+  const int ntile = (KB + kBwCTB - 1) / kBwCTB;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t tile = (int64_t)blockIdx.x * kWaves + wave;
+  const int64_t row = tile * 32 + c;
+  const bool valid = row < N;
+  const int64_t nstage = (int64_t)ntile * nst;
+
+  bf16x8 st[LPT];
+  float kst = -INFINITY;
+  auto fetch = [&](int64_t s) {
+    const int t = (int)(s / nst), qs = (int)(s % nst);
+    const int kb0 = t * kBwCTB;
+    const int cnt = KB - kb0 < kBwCTB ? KB - kb0 : kBwCTB;
+    const int qq = tid >> 6;
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int b = u >> 1, f = u & 1;   // block of the tile; feature (0: x^2, 1: x)
+      if (b < cnt) {
+        st[u] = mu_op[((int64_t)(kb0 + b) * NCF + f * NQ + kBwQS * qs + qq) * 64 + lane];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) st[u][e] = (__bf16)0.0f;
+      }
+    }
+    if (tid < kBwCTB * 32) kst = tid < cnt * 32 ? kc[(int64_t)kb0 * 32 + tid] : -INFINITY;
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) mu_l[buf * SO + u * kThreads + tid] = st[u];
+    if (tid < kBwCTB * 32) kc_l[buf * kBwCTB * 32 + tid] = kst;
+  };
+  f32x4 raw[2 * kBwQS];
+  auto loadx = [&](int64_t s) {
+    const int qs = (int)(s % nst);
+#pragma unroll
+    for (int qq = 0; qq < kBwQS; ++qq) {
+      const int d0 = 16 * (kBwQS * qs + qq) + 8 * g;
+      raw[2 * qq] = load_row4(X, ldx, row, d0, D, valid);
+      raw[2 * qq + 1] = load_row4(X, ldx, row, d0 + 4, D, valid);
+    }
+  };
+
+  // Per block two fp32 chains (x^2, x) over kBwFlush stages (256 dimensions), then
+  // added to an fp64 sum, so no fp32 chain grows past ~1/4 of its term at D ~ 1000.
+  f32x16 acc[kBwCTB][2];
+  double sacc[kBwCTB][16];
+#pragma unroll
+  for (int b = 0; b < kBwCTB; ++b) {
+    acc[b][0] = acc[b][1] = zero16();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sacc[b][i] = 0.0;
+  }
+  float mx = -INFINITY, sm = 0.0f;
+  float* ljr = lj + tile * (int64_t)KP * 32 + c;
+
+  if (nstage > 0) {
+    fetch(0);
+    loadx(0);
+    commit(0);
+  }
+  __syncthreads();
+  for (int64_t s = 0; s < nstage; ++s) {
+    const int buf = (int)(s & 1);
+    const bool more = s + 1 < nstage;
+    const int t = (int)(s / nst), qs = (int)(s % nst);
+    const int kb0 = t * kBwCTB;
+    const int cnt = KB - kb0 < kBwCTB ? KB - kb0 : kBwCTB;
+    bf16x8 x2[kBwQS], x1[kBwQS];
+#pragma unroll
+    for (int qq = 0; qq < kBwQS; ++qq) {
+      x2[qq] = to_bf16x8(raw[2 * qq] * raw[2 * qq], raw[2 * qq + 1] * raw[2 * qq + 1]);
+      x1[qq] = to_bf16x8(raw[2 * qq], raw[2 * qq + 1]);
+    }
+    if (more) {
+      fetch(s + 1);
+      loadx(s + 1);
+    }
+    const bf16x8* mp = mu_l + buf * SO + lane;
+#pragma unroll
+    for (int b = 0; b < kBwCTB; ++b) {
+      if (b < cnt) {
+#pragma unroll
+        for (int qq = 0; qq < kBwQS; ++qq) {
+          const bf16x8 w2 = mp[((2 * b) * kBwQS + qq) * 64];
+          const bf16x8 w1 = mp[((2 * b + 1) * kBwQS + qq) * 64];
+          acc[b][0] = mfma_bf16(w2, x2[qq], acc[b][0]);
+          acc[b][1] = mfma_bf16(w1, x1[qq], acc[b][1]);
+        }
+      }
+    }
+    if ((qs + 1) % kBwFlush == 0 || qs == nst - 1) {
+#pragma unroll
+      for (int b = 0; b < kBwCTB; ++b) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sacc[b][i] += (double)acc[b][0][i] + (double)acc[b][1][i];
+        acc[b][0] = acc[b][1] = zero16();
+      }
+    }
+    if (qs == nst - 1) {   // the tile's blocks are complete: lane = row, register i = component
+      const float* kp = kc_l + buf * kBwCTB * 32;
+      float bm = -INFINITY;
+      float ll[kBwCTB][16];
+#pragma unroll
+      for (int b = 0; b < kBwCTB; ++b) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          // c0 + the fp64 sum of the chains (each term ~4 D log2 units on clustered
+          // data), rounded once.
+          ll[b][i] = (float)((double)kp[b * 32 + acc_row(i, g)] + sacc[b][i]);
+          sacc[b][i] = 0.0;
+          if (b < cnt) {
+            if (valid) ljr[((int64_t)(kb0 + b) * 32 + acc_row(i, g)) * 32] = ll[b][i];
+            bm = fmaxf(bm, ll[b][i]);
+          }
+        }
+      }
+      const float mn = fmaxf(mx, bm);
+      const float ms = (mn == -INFINITY) ? 0.0f : mn;
+      float a = sm * fast_exp2(mx - ms);
+#pragma unroll
+      for (int b = 0; b < kBwCTB; ++b) {
+        if (b < cnt) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) a += fast_exp2(ll[b][i] - ms);
+        }
+      }
+      sm = a;
+      mx = mn;
+    }
+    if (more) commit(buf ^ 1);
+    lds_barrier();
+  }
+  const float mo = __shfl_xor(mx, 32);
+  const float so = __shfl_xor(sm, 32);
+  const float mn = fmaxf(mx, mo);
+  const float ms = (mn == -INFINITY) ? 0.0f : mn;
+  const float lz2 = mn + log2f(sm * fast_exp2(mx - ms) + so * fast_exp2(mo - ms));
+  if (valid && g == 0) {
+    rowstat[row] = lz2;
+    if (logZ) logZ[row] = lz2 * (float)kLn2;
+  }
+}
+
+// Pass 2: one workgroup per (row slab, group of kBwCB component blocks, range of
+// kBwDR dimensions); wave u owns block cg kBwCB + u and every column of the range in
+// both features.  Per 32-row tile the workgroup stages bf16(x) and bf16(x^2) of the
+// rows' range (row-major, stride kBwDR + 16) and their logZ2; each lane forms r for
+// its component and the 8 rows of each 16-row step its half-wave supplies (the A
+// layout of bf16(r)^T F).  The waves of range 0 also sum Nk.
+__host__ __device__ constexpr int bw_xr() { return kBwDR + 16; }
+__host__ __device__ constexpr size_t bw_accum_lds_bytes() {
+  return (size_t)2 * 2 * 32 * bw_xr() * sizeof(__bf16) + (size_t)2 * 32 * sizeof(float);
+}
+
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kBwCB, 64 * kBwCB), amdgpu_waves_per_eu(2, 2)))
+void diag_bf16_accum_wide(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int DP, int KB, int KP,
+                          const float* __restrict__ rowstat, const float* __restrict__ lj, int nslab,
+                          int64_t rows_per_slab, int ncg, int ndr, float* __restrict__ part_mu,
+                          float* __restrict__ part_sq, float* __restrict__ part_nk, int dense) {
+  constexpr int T = 64 * kBwCB;
+  constexpr int XR = bw_xr();
+  constexpr int NJ = kBwDR / 32;
+  constexpr int LPT = 32 * (kBwDR / 4) / T;   // float4 of the X tile per thread
+  static_assert(LPT * T == 32 * kBwDR / 4, "even split");
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  __bf16* xr = reinterpret_cast<__bf16*>(lds_raw);                      // [2][2][32][XR]: x^2, then x
+  float* rs = reinterpret_cast<float*>(xr + 2 * 2 * 32 * XR);            // [2][32]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int dr = (int)(blockIdx.x % ndr);
+  const int64_t rest = blockIdx.x / ndr;
+  const int cg = (int)(rest % ncg);
+  const int slab = (int)(rest / ncg);
+  const int kb = cg * kBwCB + wave;
+  const bool active = kb < KB;
+  const bool stats = active && dr == 0;
+  const int col0 = dr * kBwDR;
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
+  const int64_t comp = (int64_t)kb * 32 + c;
+
+  f32x4 stage[LPT];
+  float rstage = INFINITY;
+  auto fetch = [&](int t) {
+    const int64_t row0 = r_begin + (int64_t)t * 32;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * T + tid;
+      const int64_t rw = row0 + idx / (kBwDR / 4);
+      stage[q] = load_row4(X, ldx, rw, col0 + (idx % (kBwDR / 4)) * 4, D, rw < r_end);
+    }
+    if (tid < 32) rstage = row0 + tid < r_end ? rowstat[row0 + tid] : INFINITY;
+  };
+  auto commit = [&](int buf) {
+    __bf16* dst = xr + buf * 2 * 32 * XR;
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * T + tid;
+      const f32x4 v = stage[q];
+      const int o = (idx / (kBwDR / 4)) * XR + (idx % (kBwDR / 4)) * 4;
+      *reinterpret_cast<bf16x4*>(dst + o) = bf16x4{(__bf16)(v.x * v.x), (__bf16)(v.y * v.y), (__bf16)(v.z * v.z),
+                                                   (__bf16)(v.w * v.w)};
+      *reinterpret_cast<bf16x4*>(dst + 32 * XR + o) = bf16x4{(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+    }
+    if (tid < 32) rs[buf * 32 + tid] = rstage;
+  };
+
+  f32x16 acc[2][NJ];
+#pragma unroll
+  for (int f = 0; f < 2; ++f)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[f][j] = zero16();
+  float nk = 0.0f;
+  if (ntiles > 0) {
+    fetch(0);
+    commit(0);
+  }
+  lds_barrier();
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    if (more) fetch(t + 1);
+    if (active) {
+      const int64_t row0 = r_begin + (int64_t)t * 32;
+      const float* lrow = lj + (((row0 >> 5) * KP) + comp) * 32;
+      const float* rt = rs + buf * 32;
+      bf16x8 a[2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const f32x4 l0 = *reinterpret_cast<const f32x4*>(lrow + 16 * p + 8 * g);
+        const f32x4 l1 = *reinterpret_cast<const f32x4*>(lrow + 16 * p + 8 * g + 4);
+        const float lv[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+        float r8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int rr = 16 * p + 8 * g + e;
+          // rows past N hold no log-joint
+          const float rv = row0 + rr < r_end ? fast_exp2(lv[e] - rt[rr]) : 0.0f;
+          r8[e] = rv;
+          if (stats) nk += rv;
+        }
+        a[p] = to_bf16x8(f32x4{r8[0], r8[1], r8[2], r8[3]}, f32x4{r8[4], r8[5], r8[6], r8[7]});
+      }
+      const __bf16* xt = xr + buf * 2 * 32 * XR;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        // A step whose 16 rows x 32 components of bf16(r) are all zero adds nothing.
+        if (dense || any_nonzero(a[p])) {
+#pragma unroll
+          for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+              acc[f][j] = mfma_bf16(a[p], lds_rows_operand(xt + f * 32 * XR, XR, 16 * p, 32 * j, lane), acc[f][j]);
+        }
+      }
+    }
+    if (more) commit(buf ^ 1);
+    lds_barrier();
+  }
+  if (!active) return;
+  const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int col = col0 + 32 * j + c;
+    if (col < DP) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        part_sq[(kbase + acc_row(i, g)) * DP + col] = acc[0][j][i];
+        part_mu[(kbase + acc_row(i, g)) * DP + col] = acc[1][j][i];
+      }
+    }
+  }
+  if (dr == 0) {
+    nk += __shfl_xor(nk, 32);
+    if (g == 0) part_nk[kbase + c] = nk;
+  }
+}
+
+hipError_t launch_bf16_wide(const DiagPlan& pl, const float* X, int64_t ldx, unsigned char* ws, float* logZ,
+                            bool run1, bool run2, bool dense, hipStream_t stream) {
+  const bf16x8* mu_op = reinterpret_cast<const bf16x8*>(ws + pl.off_musw);
+  const float* kc = reinterpret_cast<const float*>(ws + pl.off_kclin);
+  float* rowstat = reinterpret_cast<float*>(ws + pl.off_rowstat);
+  float* lj = reinterpret_cast<float*>(ws + pl.off_lj);
+  if (run1) {
+    constexpr size_t lds1 = bw_lse_lds_bytes();
+    static_assert(lds1 <= 65536, "pass-1 stages fit the default LDS allocation");
+    hipLaunchKernelGGL(diag_bf16_lse_wide, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1, stream,
+                       X, ldx, pl.N, (int)pl.D, pl.DP, mu_op, kc, pl.KB, pl.KP, logZ, rowstat, lj);
+  }
+  if (!run2) return hipGetLastError();
+  constexpr size_t lds2 = bw_accum_lds_bytes();
+  static_assert(lds2 <= 65536, "pass-2 tiles fit the default LDS allocation");
+  hipLaunchKernelGGL(diag_bf16_accum_wide, dim3((unsigned)((int64_t)pl.nslab * pl.ncg * pl.ndr)), dim3(64 * kBwCB),
+                     lds2, stream, X, ldx, pl.N, (int)pl.D, pl.DP, pl.KB, pl.KP, rowstat, lj, pl.nslab,
+                     pl.rows_per_slab, pl.ncg, pl.ndr, reinterpret_cast<float*>(ws + pl.off_part_mu),
+                     reinterpret_cast<float*>(ws + pl.off_part_sq), reinterpret_cast<float*>(ws + pl.off_part_nk),
+                     dense ? 1 : 0);
+  return hipGetLastError();
+}
+
 }  // namespace
 }  // namespace fgmm
 
 using namespace fgmm;
+
+namespace {
+// Rows per call of the bf16 contract above D = 256, whose log-joint must fit
+// kMaxLjBytes: a multiple of 128 rows.  Larger calls run in chunks of this many rows.
+int64_t diag_bw_chunk_rows(int64_t K) {
+  const int64_t KP = round_up(K < 1 ? 1 : K, 32);
+  return (int64_t)(kMaxLjBytes / ((size_t)KP * 32 * sizeof(float))) / 4 * 4 * 32;
+}
+bool diag_bw_call(int64_t D, unsigned flags) {
+  return (flags & FGMM_FLAG_BF16) != 0 && diag_bf16_wide(diag_padded_dim(D));
+}
+}  // namespace
 
 extern "C" size_t fgmm_diag_workspace_bytes(int64_t N, int64_t K, int64_t D) {
   if (N < 0 || K < 0 || D < 1) return 0;
@@ -2551,7 +2926,8 @@ extern "C" size_t fgmm_diag_workspace_bytes(int64_t N, int64_t K, int64_t D) {
 
 extern "C" size_t fgmm_diag_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D, wants_stored_lj(flags), (flags & FGMM_FLAG_BF16) != 0).total;
+  const int64_t rows = diag_bw_call(D, flags) ? std::min(N, diag_bw_chunk_rows(K)) : N;
+  return make_plan(rows, K, D, wants_stored_lj(flags), (flags & FGMM_FLAG_BF16) != 0).total;
 }
 
 extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -2573,7 +2949,22 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     return FGMM_ERR_INVALID_ARG;
   if (N > kMaxRows || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
   const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
-  if (bf16 && D > 256) return FGMM_ERR_UNSUPPORTED;
+  if (diag_bw_call(D, flags) && K > 0 && N > diag_bw_chunk_rows(K)) {
+    // The bf16 contract above D = 256 stores the log-joint, at most kMaxLjBytes per
+    // call: larger N runs as consecutive row chunks on one workspace, each chunk after
+    // the first adding its statistics to the outputs.  A phase split cannot span them.
+    if (flags & (FGMM_FLAG_PHASE1 | FGMM_FLAG_PHASE2)) return FGMM_ERR_UNSUPPORTED;
+    const int64_t rows = diag_bw_chunk_rows(K);
+    for (int64_t r0 = 0; r0 < N; r0 += rows) {
+      const int64_t n = std::min(rows, N - r0);
+      const unsigned f = r0 == 0 ? flags : (flags | FGMM_FLAG_ACCUMULATE);
+      const int st = fgmm_diag_estep_f32(X + r0 * ldx, ldx, n, D, mu, ldmu, K, log_sigma_sq, ldlss, log_pi,
+                                         logZ ? logZ + r0 : nullptr, Nk, mu_acc, sig_acc, workspace,
+                                         workspace_bytes, f, stream_);
+      if (st != FGMM_OK) return st;
+    }
+    return FGMM_OK;
+  }
   // The stored-log-joint pass 2 addresses X tiles with 32-bit buffer offsets (row
   // stride at most kMaxBufLdx floats); wider strides recompute, which needs less
   // workspace.
@@ -2607,7 +2998,9 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
                   : launch_passes<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
     };
     hipError_t e = hipSuccess;
-    if (pl.ctile) {
+    if (pl.bfw) {
+      e = launch_bf16_wide(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
+    } else if (pl.ctile) {
       e = launch_ctile(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
       if (e == hipSuccess && pl.lj && run2) {
         if (pl.DP == 192) e = launch_passes<192>(pl, X, ldx, ws, logZ, false, true, dense, stream);

@@ -64,6 +64,7 @@
 #include <float.h>
 #include <math.h>
 
+#include <algorithm>
 #include <type_traits>
 
 namespace fgmm {
@@ -136,7 +137,8 @@ struct IsoPlan {
   bool need;    // default plan: pass 1 leaves need masks, pass 2 gathers the needed rows
   bool ctile;   // default plan above D = 128: component-tiled pass 1, dimension-range pass 2
   bool rexact;  // need masks from the block maxima kept in LDS (else the running-max bound)
-  int ndr;      // dimension ranges of the component-tiled pass 2
+  int ndr;      // dimension ranges of the component-tiled pass 2 (and of the wide bf16 pass 2)
+  bool bfw;     // bf16 contract above D = 256: stored log-joint, iso_bf16_*_wide
   size_t off_musw, off_mu3, off_kcblk, off_kclin, off_kcgat, off_rowstat, off_part_mu, off_part_nk,
       off_part_sig, off_lj, off_ljmax, off_ljmask, off_ljcount, total;
 };
@@ -171,6 +173,13 @@ __host__ inline bool use_stored_lj(int64_t N, int DP, int KB, bool allow) {
 // bf16 pass 2: 4 component blocks per workgroup, or 2 / 1 for K <= 64 / 32 where
 // the taller X tiles fit in LDS (row-major and transposed bf16, double-buffered).
 __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB);
+// Above D = 256 the bf16 contract stores the log-joint (defined with its kernels).
+constexpr int kBwCB = 8;     // component blocks per wide bf16 pass-2 workgroup (one per wave)
+constexpr int kBwDR = 256;   // dimensions per wide bf16 pass-2 workgroup
+__host__ __device__ constexpr bool iso_bf16_wide(int DP) { return DP > 256; }
+__host__ inline size_t bw_lj_bytes(int64_t N, int KP) {
+  return (size_t)round_up(cdiv(N, 32), 4) * (size_t)KP * 32 * sizeof(float);
+}
 __host__ __device__ constexpr int bf16_halves(int DP);
 __host__ inline int bf16_blocks_per_group(int DP, int KB);
 
@@ -187,7 +196,12 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
   p.rexact = p.need && p.KB <= ((p.ctile && !lse_in_regs(p.DP)) ? ctile_need_exact_cap(ctile_blocks(p.DP))
                                                                  : need_exact_cap(p.DP));
   p.ndr = p.ctile ? (int)cdiv(p.DP, kDrange) : 1;
-  if (bf16) {
+  p.bfw = bf16 && iso_bf16_wide(p.DP);
+  if (p.bfw) {
+    p.cpg = kBwCB;
+    p.rgroups = 1;
+    p.ndr = (int)cdiv(p.DP, kBwDR);
+  } else if (bf16) {
     p.cpg = bf16_blocks_per_group(p.DP, p.KB);
     p.rgroups = kAccWaves / (p.cpg * bf16_halves(p.DP));
   } else if (p.lj) {
@@ -203,7 +217,13 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
   }
   p.ncg = (int)cdiv(p.KB, p.cpg);
   const int64_t tile_rows = 32 * p.rgroups;
-  if (p.ctile && N > 0 && p.KB > 0) {
+  if (p.bfw && N > 0 && p.KB > 0) {
+    // About two workgroups per compute unit.
+    int64_t want = cdiv((int64_t)2 * current_device_cus(), (int64_t)p.ncg * p.ndr);
+    if (want > cdiv(N, 32)) want = cdiv(N, 32);
+    p.rows_per_slab = round_up(cdiv(N, want), 32);
+    p.nslab = (int)cdiv(N, p.rows_per_slab);
+  } else if (p.ctile && N > 0 && p.KB > 0) {
     // One 4-wave workgroup per (slab, block, dimension range) and compute unit (its
     // X tile takes most of the LDS): about two rounds of workgroups.
     int64_t want = cdiv((int64_t)2 * current_device_cus(), (int64_t)p.KB * p.ndr);
@@ -245,7 +265,8 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
   // with its per-row block maxima and need mask; the default plan keeps the masks only.
   // (The default plan's pass 1 up to D = 128 runs 8 tiles per workgroup.)
   const size_t ntile = (p.lj || p.need) ? (size_t)round_up(cdiv(N, 32), p.need ? 8 : 4) * p.KB : 0;
-  p.off_lj = off;     off = align256(off + (p.lj ? ntile * kLjTile * sizeof(float) : 0));
+  p.off_lj = off;
+  off = align256(off + (p.bfw ? bw_lj_bytes(N, p.KP) : p.lj ? ntile * kLjTile * sizeof(float) : 0));
   p.off_ljmax = off;  off = align256(off + (p.lj ? ntile * 32 * sizeof(float) : 0));
   p.off_ljmask = off; off = align256(off + ntile * sizeof(unsigned));
   p.off_ljcount = off; off = align256(off + ((p.lj || p.need) ? 64 * sizeof(unsigned) : 0));
@@ -3101,10 +3122,378 @@ hipError_t launch_bf16(const IsoPlan& pl, const float* X, int64_t ldx, unsigned 
                        : launch(std::integral_constant<int, 4>{});
 }
 
+// ---------------------------------------------------------------------------
+// bf16 operand contract above D = 256 (any D).  A row's rounded operands no longer
+// fit in registers, so pass 1 (iso_bf16_lse_wide) tiles the contraction over
+// components: per tile of kBwCTB component blocks each wave re-reads its 32 rows
+// (L2) chunk by chunk, rounds them to bf16 and accumulates S^T = mu_b . x_b^T for
+// the tile's blocks, with the tile's operands staged in LDS: an fp32 chain per 256
+// dimensions, added into an fp64 sum; S, ||x_b||^2 (fp64) and the constants are
+// combined in fp64 and the fp32 log-joint is stored, [32-row tile][KP][32 rows].  Pass 2 (iso_bf16_accum_wide) reads r
+// from it: bf16(r)^T bf16(X) per range of kBwDR dimensions on an X tile rounded to
+// bf16 in LDS, Nk = sum r, and sig_acc = sum r ||x_b - mu||^2 with
+// ish ||x_b - mu||^2 = c0' - ll2, c0' = c0 + ish ||mu||^2 (the log-joint's terms
+// regrouped).  Calls whose log-joint exceeds kMaxLjBytes run as row chunks.
+// ---------------------------------------------------------------------------
+constexpr int kBwCTB = 4;    // component blocks per pass-1 tile
+constexpr int kBwQS = 4;     // 16-dimension chunks per pass-1 stage
+constexpr int kBwFlush = 4;  // stages per fp32 chain: its sum then joins an fp64 one
+__host__ __device__ constexpr int bw_stage_ops() { return kBwCTB * kBwQS * 64; }   // bf16x8
+__host__ __device__ constexpr size_t bw_lse_lds_bytes() {
+  return (size_t)2 * (bw_stage_ops() * sizeof(bf16x8) + kBwCTB * 32 * sizeof(f32x4));
+}
+
+__global__ __launch_bounds__(kThreads) void iso_bf16_lse_wide(const float* __restrict__ X, int64_t ldx,
+                                                              int64_t N, int D, int DP,
+                                                              const bf16x8* __restrict__ mu_op,
+                                                              const f32x4* __restrict__ kc, int KB, int KP,
+                                                              float* __restrict__ logZ,
+                                                              float2* __restrict__ rowstat,
+                                                              float* __restrict__ lj) {
+  constexpr int SO = bw_stage_ops();
+  constexpr int LPT = SO / kThreads;
+  static_assert(LPT == kBwCTB && kThreads == kBwQS * 64, "fetch register u holds block u of the tile");
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                               // [2][SO]
+  f32x4* kc_l = reinterpret_cast<f32x4*>(lds_raw + 2 * SO * sizeof(bf16x8));       // [2][CTB * 32]
+
+  const int NQ = DP / 16, nst = NQ / kBwQS;
+  const int ntile = (KB + kBwCTB - 1) / kBwCTB;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t tile = (int64_t)blockIdx.x * kWaves + wave;
+  const int64_t row = tile * 32 + c;
+  const bool valid = row < N;
+  const int64_t nstage = (int64_t)ntile * nst;
+
+  bf16x8 st[LPT];
+  f32x4 kst = {-INFINITY, 0.0f, 0.0f, 0.0f};
+  auto fetch = [&](int64_t s) {
+    const int t = (int)(s / nst), qs = (int)(s % nst);
+    const int kb0 = t * kBwCTB;
+    const int cnt = KB - kb0 < kBwCTB ? KB - kb0 : kBwCTB;
+    const int qq = tid >> 6;
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      if (u < cnt) {
+        st[u] = mu_op[((int64_t)(kb0 + u) * NQ + kBwQS * qs + qq) * 64 + lane];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) st[u][e] = (__bf16)0.0f;
+      }
+    }
+    if (tid < kBwCTB * 32) kst = tid < cnt * 32 ? kc[(int64_t)kb0 * 32 + tid] : f32x4{-INFINITY, 0.0f, 0.0f, 0.0f};
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) mu_l[buf * SO + u * kThreads + tid] = st[u];
+    if (tid < kBwCTB * 32) kc_l[buf * kBwCTB * 32 + tid] = kst;
+  };
+  // This lane's row, dimensions 16q + 8g .. +7 of the stage's chunks.
+  f32x4 raw[2 * kBwQS];
+  auto loadx = [&](int64_t s) {
+    const int qs = (int)(s % nst);
+#pragma unroll
+    for (int qq = 0; qq < kBwQS; ++qq) {
+      const int d0 = 16 * (kBwQS * qs + qq) + 8 * g;
+      raw[2 * qq] = load_row4(X, ldx, row, d0, D, valid);
+      raw[2 * qq + 1] = load_row4(X, ldx, row, d0 + 4, D, valid);
+    }
+  };
+
+  // S of the tile's blocks: an fp32 chain over kBwFlush stages (256 dimensions),
+  // then added to an fp64 sum, so no fp32 chain grows past ~1/4 of S at D ~ 1000.
+  f32x16 acc[kBwCTB];
+  double sacc[kBwCTB][16];
+#pragma unroll
+  for (int u = 0; u < kBwCTB; ++u) {
+    acc[u] = zero16();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sacc[u][i] = 0.0;
+  }
+  // This half's sum of squares (fp64: a sequential fp32 sum over D ~ 1000 terms
+  // of ~4 each would carry ~4e-3), then the row's.
+  double xsq = 0.0, xsqf = 0.0;
+  float mx = -INFINITY, sm = 0.0f;
+  float* ljr = lj + tile * (int64_t)KP * 32 + c;
+
+  if (nstage > 0) {
+    fetch(0);
+    loadx(0);
+    commit(0);
+  }
+  __syncthreads();
+  for (int64_t s = 0; s < nstage; ++s) {
+    const int buf = (int)(s & 1);
+    const bool more = s + 1 < nstage;
+    const int t = (int)(s / nst), qs = (int)(s % nst);
+    const int kb0 = t * kBwCTB;
+    const int cnt = KB - kb0 < kBwCTB ? KB - kb0 : kBwCTB;
+    bf16x8 xb[kBwQS];
+#pragma unroll
+    for (int qq = 0; qq < kBwQS; ++qq) xb[qq] = to_bf16x8(raw[2 * qq], raw[2 * qq + 1]);
+    if (t == 0) {
+#pragma unroll
+      for (int qq = 0; qq < kBwQS; ++qq) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const double v = (double)(float)xb[qq][e];
+          xsq = fma(v, v, xsq);
+        }
+      }
+    }
+    if (more) {
+      fetch(s + 1);
+      loadx(s + 1);
+    }
+    const bf16x8* mp = mu_l + buf * SO + lane;
+#pragma unroll
+    for (int u = 0; u < kBwCTB; ++u) {
+      if (u < cnt) {
+#pragma unroll
+        for (int qq = 0; qq < kBwQS; ++qq) acc[u] = mfma_bf16(mp[(u * kBwQS + qq) * 64], xb[qq], acc[u]);
+      }
+    }
+    if ((qs + 1) % kBwFlush == 0 || qs == nst - 1) {
+#pragma unroll
+      for (int u = 0; u < kBwCTB; ++u) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sacc[u][i] += (double)acc[u][i];
+        acc[u] = zero16();
+      }
+    }
+    if (qs == nst - 1) {   // the tile's blocks are complete: S^T, lane = row, register i = component
+      if (t == 0) xsqf = xsq + __shfl_xor(xsq, 32);
+      const f32x4* kp = kc_l + buf * kBwCTB * 32;
+      float bm = -INFINITY;
+      float ll[kBwCTB][16];
+#pragma unroll
+      for (int u = 0; u < kBwCTB; ++u) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          // c0 - ish ||x_b||^2 + 2 ish S with the terms (each ~4 D log2 units on
+          // clustered data) combined in fp64, rounded once.
+          const f32x4 w = kp[u * 32 + acc_row(i, g)];
+          ll[u][i] = (float)(((double)w.x - (double)w.y * xsqf) + (double)w.z * sacc[u][i]);
+          sacc[u][i] = 0.0;
+          if (u < cnt) {
+            if (valid) ljr[((int64_t)(kb0 + u) * 32 + acc_row(i, g)) * 32] = ll[u][i];
+            bm = fmaxf(bm, ll[u][i]);
+          }
+        }
+      }
+      const float mn = fmaxf(mx, bm);
+      const float ms = (mn == -INFINITY) ? 0.0f : mn;
+      float a = sm * fast_exp2(mx - ms);
+#pragma unroll
+      for (int u = 0; u < kBwCTB; ++u) {
+        if (u < cnt) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) a += fast_exp2(ll[u][i] - ms);
+        }
+      }
+      sm = a;
+      mx = mn;
+    }
+    if (more) commit(buf ^ 1);
+    lds_barrier();
+  }
+  const float mo = __shfl_xor(mx, 32);
+  const float so = __shfl_xor(sm, 32);
+  const float mn = fmaxf(mx, mo);
+  const float ms = (mn == -INFINITY) ? 0.0f : mn;
+  const float lz2 = mn + log2f(sm * fast_exp2(mx - ms) + so * fast_exp2(mo - ms));
+  if (valid && g == 0) {
+    rowstat[row] = make_float2(lz2, (float)xsqf);
+    if (logZ) logZ[row] = lz2 * (float)kLn2;
+  }
+}
+
+// Pass 2: one workgroup per (row slab, group of kBwCB component blocks, range of
+// kBwDR dimensions); wave u owns block cg kBwCB + u and every column of the range (8
+// tiles of 32).  Per 32-row tile the workgroup stages the rows' range of X rounded
+// to bf16 (row-major, stride kBwDR + 16: an odd multiple of 32 bytes, as the
+// transposing reads want) and their {logZ2, ||x_b||^2}; each lane forms r for its
+// component (lane % 32) and the 8 rows of each 16-row step its half-wave supplies,
+// which is the A-operand layout of bf16(r)^T X, so no exchange is needed.  The waves
+// of range 0 also sum Nk and r (c0' - ll2).
+__host__ __device__ constexpr int bw_xr() { return kBwDR + 16; }
+__host__ __device__ constexpr size_t bw_accum_lds_bytes() {
+  return (size_t)2 * 32 * bw_xr() * sizeof(__bf16) + (size_t)2 * 32 * sizeof(float2);
+}
+
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kBwCB, 64 * kBwCB), amdgpu_waves_per_eu(2, 2)))
+void iso_bf16_accum_wide(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int DP,
+                         const f32x4* __restrict__ kc, int KB, int KP, const float2* __restrict__ rowstat,
+                         const float* __restrict__ lj, int nslab, int64_t rows_per_slab, int ncg, int ndr,
+                         float* __restrict__ part_mu, float* __restrict__ part_nk,
+                         float* __restrict__ part_sig, int dense) {
+  constexpr int T = 64 * kBwCB;
+  constexpr int XR = bw_xr();
+  constexpr int NJ = kBwDR / 32;
+  constexpr int LPT = 32 * (kBwDR / 4) / T;   // float4 of the X tile per thread
+  static_assert(LPT * T == 32 * kBwDR / 4, "even split");
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  __bf16* xr = reinterpret_cast<__bf16*>(lds_raw);                      // [2][32][XR]
+  float2* rs = reinterpret_cast<float2*>(xr + 2 * 32 * XR);              // [2][32]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int dr = (int)(blockIdx.x % ndr);
+  const int64_t rest = blockIdx.x / ndr;
+  const int cg = (int)(rest % ncg);
+  const int slab = (int)(rest / ncg);
+  const int kb = cg * kBwCB + wave;
+  const bool active = kb < KB;
+  const bool stats = active && dr == 0;
+  const int col0 = dr * kBwDR;
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
+
+  const int64_t comp = (int64_t)kb * 32 + c;
+  f32x4 w = {-INFINITY, 0.0f, 0.0f, 0.0f};
+  if (active) w = kc[comp];
+  const float c0p = (float)((double)w.x + (double)w.y * (double)w.w);   // c0 + ish ||mu||^2
+
+  f32x4 stage[LPT];
+  float2 rstage = make_float2(INFINITY, 0.0f);
+  auto fetch = [&](int t) {
+    const int64_t row0 = r_begin + (int64_t)t * 32;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * T + tid;
+      const int64_t rw = row0 + idx / (kBwDR / 4);
+      stage[q] = load_row4(X, ldx, rw, col0 + (idx % (kBwDR / 4)) * 4, D, rw < r_end);
+    }
+    if (tid < 32) rstage = row0 + tid < r_end ? rowstat[row0 + tid] : make_float2(INFINITY, 0.0f);
+  };
+  auto commit = [&](int buf) {
+    __bf16* dst = xr + buf * 32 * XR;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int idx = q * T + tid;
+      const f32x4 v = stage[q];
+      typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+      const bf16x4 b = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+      *reinterpret_cast<bf16x4*>(dst + (idx / (kBwDR / 4)) * XR + (idx % (kBwDR / 4)) * 4) = b;
+    }
+    if (tid < 32) rs[buf * 32 + tid] = rstage;
+  };
+
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
+  float nk = 0.0f, sg = 0.0f;
+  if (ntiles > 0) {
+    fetch(0);
+    commit(0);
+  }
+  lds_barrier();
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < ntiles;
+    if (more) fetch(t + 1);
+    if (active) {
+      const int64_t row0 = r_begin + (int64_t)t * 32;
+      const float* lrow = lj + (((row0 >> 5) * KP) + comp) * 32;
+      const float2* rt = rs + buf * 32;
+      bf16x8 a[2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const f32x4 l0 = *reinterpret_cast<const f32x4*>(lrow + 16 * p + 8 * g);
+        const f32x4 l1 = *reinterpret_cast<const f32x4*>(lrow + 16 * p + 8 * g + 4);
+        const float lv[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+        float r8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int rr = 16 * p + 8 * g + e;
+          const bool in = row0 + rr < r_end;   // rows past N hold no log-joint
+          const float l = in ? lv[e] : c0p;
+          const float rv = in ? fast_exp2(l - rt[rr].x) : 0.0f;
+          r8[e] = rv;
+          if (stats) {
+            nk += rv;
+            sg = fmaf(rv, c0p - l, sg);
+          }
+        }
+        a[p] = to_bf16x8(f32x4{r8[0], r8[1], r8[2], r8[3]}, f32x4{r8[4], r8[5], r8[6], r8[7]});
+      }
+      const __bf16* xt = xr + buf * 32 * XR;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        // A step whose 16 rows x 32 components of bf16(r) are all zero adds nothing.
+        if (dense || any_nonzero(a[p])) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) acc[j] = mfma_bf16(a[p], lds_rows_operand(xt, XR, 16 * p, 32 * j, lane), acc[j]);
+        }
+      }
+    }
+    if (more) commit(buf ^ 1);
+    lds_barrier();
+  }
+  if (!active) return;
+  const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int col = col0 + 32 * j + c;
+    if (col < DP) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) part_mu[(kbase + acc_row(i, g)) * DP + col] = acc[j][i];
+    }
+  }
+  if (dr == 0) {
+    nk += __shfl_xor(nk, 32);
+    sg += __shfl_xor(sg, 32);
+    if (g == 0) {
+      part_nk[kbase + c] = nk;
+      part_sig[kbase + c] = w.y > 0.0f ? sg / w.y : 0.0f;
+    }
+  }
+}
+
+hipError_t launch_bf16_wide(const IsoPlan& pl, const float* X, int64_t ldx, unsigned char* ws, float* logZ,
+                            bool run1, bool run2, bool dense, hipStream_t stream) {
+  const bf16x8* mu_op = reinterpret_cast<const bf16x8*>(ws + pl.off_musw);
+  const f32x4* kc = reinterpret_cast<const f32x4*>(ws + pl.off_kcblk);
+  float2* rowstat = reinterpret_cast<float2*>(ws + pl.off_rowstat);
+  float* lj = reinterpret_cast<float*>(ws + pl.off_lj);
+  if (run1) {
+    constexpr size_t lds1 = bw_lse_lds_bytes();
+    static_assert(lds1 <= 65536, "pass-1 stages fit the default LDS allocation");
+    hipLaunchKernelGGL(iso_bf16_lse_wide, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1, stream,
+                       X, ldx, pl.N, (int)pl.D, pl.DP, mu_op, kc, pl.KB, pl.KP, logZ, rowstat, lj);
+  }
+  if (!run2) return hipGetLastError();
+  constexpr size_t lds2 = bw_accum_lds_bytes();
+  static_assert(lds2 <= 65536, "pass-2 tiles fit the default LDS allocation");
+  hipLaunchKernelGGL(iso_bf16_accum_wide, dim3((unsigned)((int64_t)pl.nslab * pl.ncg * pl.ndr)), dim3(64 * kBwCB),
+                     lds2, stream, X, ldx, pl.N, (int)pl.D, pl.DP, kc, pl.KB, pl.KP, rowstat, lj, pl.nslab,
+                     pl.rows_per_slab, pl.ncg, pl.ndr, reinterpret_cast<float*>(ws + pl.off_part_mu),
+                     reinterpret_cast<float*>(ws + pl.off_part_nk), reinterpret_cast<float*>(ws + pl.off_part_sig),
+                     dense ? 1 : 0);
+  return hipGetLastError();
+}
+
 }  // namespace
 }  // namespace fgmm
 
 using namespace fgmm;
+
+namespace {
+// Rows per call of the bf16 contract above D = 256, whose log-joint must fit
+// kMaxLjBytes: a multiple of 128 rows.  Larger calls run in chunks of this many rows.
+int64_t iso_bw_chunk_rows(int64_t K) {
+  const int64_t KP = round_up(K < 1 ? 1 : K, 32);
+  return (int64_t)(kMaxLjBytes / ((size_t)KP * 32 * sizeof(float))) / 4 * 4 * 32;
+}
+bool iso_bw_call(int64_t D, unsigned flags) {
+  return (flags & FGMM_FLAG_BF16) != 0 && iso_bf16_wide(iso_padded_dim(D));
+}
+}  // namespace
 
 extern "C" size_t fgmm_iso_workspace_bytes(int64_t N, int64_t K, int64_t D) {
   if (N < 0 || K < 0 || D < 1) return 0;
@@ -3113,7 +3502,8 @@ extern "C" size_t fgmm_iso_workspace_bytes(int64_t N, int64_t K, int64_t D) {
 
 extern "C" size_t fgmm_iso_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
   if (N < 0 || K < 0 || D < 1) return 0;
-  return make_plan(N, K, D, wants_stored_lj(flags), (flags & FGMM_FLAG_BF16) != 0).total;
+  const int64_t rows = iso_bw_call(D, flags) ? std::min(N, iso_bw_chunk_rows(K)) : N;
+  return make_plan(rows, K, D, wants_stored_lj(flags), (flags & FGMM_FLAG_BF16) != 0).total;
 }
 
 extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -3136,7 +3526,22 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
     return FGMM_ERR_INVALID_ARG;
   if (N > kMaxRows || K > (int64_t)1 << 24) return FGMM_ERR_UNSUPPORTED;
   const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
-  if (bf16 && D > 256) return FGMM_ERR_UNSUPPORTED;
+  if (iso_bw_call(D, flags) && K > 0 && N > iso_bw_chunk_rows(K)) {
+    // The bf16 contract above D = 256 stores the log-joint, at most kMaxLjBytes per
+    // call: larger N runs as consecutive row chunks on one workspace, each chunk after
+    // the first adding its statistics to the outputs.  A phase split cannot span them.
+    if (flags & (FGMM_FLAG_PHASE1 | FGMM_FLAG_PHASE2)) return FGMM_ERR_UNSUPPORTED;
+    const int64_t rows = iso_bw_chunk_rows(K);
+    for (int64_t r0 = 0; r0 < N; r0 += rows) {
+      const int64_t n = std::min(rows, N - r0);
+      const unsigned f = r0 == 0 ? flags : (flags | FGMM_FLAG_ACCUMULATE);
+      const int st = fgmm_iso_estep_f32(X + r0 * ldx, ldx, n, D, mu, ldmu, K, log_sigma_sq, log_pi,
+                                        logZ ? logZ + r0 : nullptr, Nk, mu_acc, sig_acc, workspace,
+                                        workspace_bytes, f, stream_);
+      if (st != FGMM_OK) return st;
+    }
+    return FGMM_OK;
+  }
   // The stored log-joint path streams X with 32-bit buffer offsets (row stride at
   // most kMaxBufLdx floats); wider strides recompute, which needs less workspace.
   const IsoPlan pl = make_plan(N, K, D, wants_stored_lj(flags) && ldx <= kMaxBufLdx, bf16);
@@ -3172,7 +3577,9 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
                   : launch_passes<DP>(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
     };
     hipError_t e = hipSuccess;
-    if (!bf16 && pl.DP > 128) {
+    if (pl.bfw) {
+      e = launch_bf16_wide(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
+    } else if (!bf16 && pl.DP > 128) {
       e = launch_ctile(pl, X, ldx, ws, logZ, run1, run2, dense, stream);
       if (e == hipSuccess && pl.lj && run2) {
         if (pl.DP == 192) e = launch_passes<192>(pl, X, ldx, ws, logZ, false, true, dense, stream);

@@ -124,7 +124,8 @@ def bf16_round(t: Tensor) -> Tensor:
 
 
 def estep_iso_bf16(X: Tensor, mu: Tensor, log_sigma_sq: Tensor, log_pi: Tensor, *,
-                   chunk: int = _DEFAULT_CHUNK) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+                   chunk: int = _DEFAULT_CHUNK,
+                   dtype: torch.dtype = torch.float64) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     """Isotropic E-step with the bf16 operand contract of flash_gmm_h100.py:247-328.
 
     X and mu are rounded to bfloat16 for both contractions (:277-284); x_sq is the
@@ -133,20 +134,23 @@ def estep_iso_bf16(X: Tensor, mu: Tensor, log_sigma_sq: Tensor, log_pi: Tensor, 
     (:137-138); r = 2^(ll2 - logZ2); Nk = sum r, sig_acc = sum r (x_sq - 2 x.mu +
     mu_sq) (:210-224); mu_acc = bf16(r)^T x (:230-231); logZ = logZ2 ln 2 (:326).
     Everything except those roundings is float64 here (the reference accumulates
-    in float32).
+    in float32); ``dtype=torch.float32`` evaluates the same steps in float32 (the
+    constants formed in float64 and rounded once), the reference's own arithmetic,
+    whose distance from the float64 result bounds what a float32 kernel can reach.
     """
     X32, mu32 = _as(X, torch.float32), _as(mu, torch.float32)
-    Xb, mub = bf16_round(X32), bf16_round(mu32)
+    Xb, mub = bf16_round(X32).to(dtype), bf16_round(mu32).to(dtype)
     lss, lpi = _as(log_sigma_sq, torch.float64), _as(log_pi, torch.float64)
     N, D = X32.shape
     K = mu32.shape[0]
     mu_sq = (mu32.double() ** 2).sum(dim=1)
     ish = 0.5 * torch.exp(-lss) * LOG2_E
     c0 = (lpi - 0.5 * D * (LOG_2PI + lss)) * LOG2_E - ish * mu_sq
-    logZ = torch.empty(N, dtype=torch.float64)
-    Nk = torch.zeros(K, dtype=torch.float64)
-    mu_acc = torch.zeros(K, D, dtype=torch.float64)
-    sig_acc = torch.zeros(K, dtype=torch.float64)
+    mu_sq, ish, c0 = mu_sq.to(dtype), ish.to(dtype), c0.to(dtype)
+    logZ = torch.empty(N, dtype=dtype)
+    Nk = torch.zeros(K, dtype=dtype)
+    mu_acc = torch.zeros(K, D, dtype=dtype)
+    sig_acc = torch.zeros(K, dtype=dtype)
     ln2 = math.log(2.0)
     for n0 in range(0, N, chunk):
         xb = Xb[n0:n0 + chunk]
@@ -158,7 +162,7 @@ def estep_iso_bf16(X: Tensor, mu: Tensor, log_sigma_sq: Tensor, log_pi: Tensor, 
         r = torch.exp2(ll2 - lz2[:, None])
         Nk += r.sum(dim=0)
         sig_acc += (r * (x_sq[:, None] - 2.0 * xmu + mu_sq[None, :])).sum(dim=0)
-        mu_acc += bf16_round(r).T @ xb
+        mu_acc += bf16_round(r).to(dtype).T @ xb
     return logZ, Nk, mu_acc, sig_acc
 
 
@@ -231,7 +235,8 @@ def diag_bf16_weights(mu: Tensor, log_sigma_sq: Tensor) -> Tuple[Tensor, Tensor]
 
 
 def estep_diag_bf16(X: Tensor, mu: Tensor, log_sigma_sq: Tensor, log_pi: Tensor, *,
-                    chunk: int = _DEFAULT_CHUNK) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+                    chunk: int = _DEFAULT_CHUNK,
+                    dtype: torch.dtype = torch.float64) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     """Diagonal E-step with the bf16 operand contract of flash_gmm_diag_h100.py.
 
     x and x^2 (squared in float32) are rounded to bfloat16 (:86-88, :238-239), and so
@@ -241,7 +246,8 @@ def estep_diag_bf16(X: Tensor, mu: Tensor, log_sigma_sq: Tensor, log_pi: Tensor,
     bf16(x) and rxsq = bf16(r)^T bf16(x^2) (:251, :255-256); sig_acc = rxsq -
     2 mu mu_acc + mu^2 Nk (:260); logZ = logZ2 ln 2 (:382).  Rows are partitioned (no slab
     overlap, unlike :220-231).  Everything except the roundings is float64 here
-    (the reference accumulates in float32).
+    (the reference accumulates in float32); ``dtype=torch.float32`` evaluates the
+    same steps in float32, as estep_iso_bf16 does.
     """
     X32 = _as(X, torch.float32)
     mu64 = _as(mu, torch.float64)
@@ -251,26 +257,27 @@ def estep_diag_bf16(X: Tensor, mu: Tensor, log_sigma_sq: Tensor, log_pi: Tensor,
     if lss.shape != (K, D):
         raise ValueError(f"log_sigma_sq must be (K, D)=({K}, {D}), got {tuple(lss.shape)}")
     w1, w2 = diag_bf16_weights(mu, log_sigma_sq)
-    w1b, w2b = bf16_round(w1), bf16_round(w2)
+    w1b, w2b = bf16_round(w1).to(dtype), bf16_round(w2).to(dtype)
     c0 = ((lpi - 0.5 * (D * LOG_2PI + lss.sum(dim=1))) * LOG2_E
-          - 0.5 * LOG2_E * (mu64 * mu64 * torch.exp(-lss)).sum(dim=1))
-    logZ = torch.empty(N, dtype=torch.float64)
-    Nk = torch.zeros(K, dtype=torch.float64)
-    mu_acc = torch.zeros(K, D, dtype=torch.float64)
-    rxsq = torch.zeros(K, D, dtype=torch.float64)
+          - 0.5 * LOG2_E * (mu64 * mu64 * torch.exp(-lss)).sum(dim=1)).to(dtype)
+    logZ = torch.empty(N, dtype=dtype)
+    Nk = torch.zeros(K, dtype=dtype)
+    mu_acc = torch.zeros(K, D, dtype=dtype)
+    rxsq = torch.zeros(K, D, dtype=dtype)
     ln2 = math.log(2.0)
     for n0 in range(0, N, chunk):
         x = X32[n0:n0 + chunk]
-        xb, xsqb = bf16_round(x), bf16_round(x * x)
+        xb, xsqb = bf16_round(x).to(dtype), bf16_round(x * x).to(dtype)
         ll2 = c0[None, :] - xsqb @ w1b.T + 2.0 * (xb @ w2b.T)
         lz2 = torch.logsumexp(ll2 * ln2, dim=1) / ln2
         logZ[n0:n0 + chunk] = lz2 * ln2
         r = torch.exp2(ll2 - lz2[:, None])
-        rb = bf16_round(r)
+        rb = bf16_round(r).to(dtype)
         Nk += r.sum(dim=0)
         mu_acc += rb.T @ xb
         rxsq += rb.T @ xsqb
-    sig_acc = rxsq - 2.0 * mu64 * mu_acc + mu64 * mu64 * Nk[:, None]
+    m = mu64.to(dtype)
+    sig_acc = rxsq - 2.0 * m * mu_acc + m * m * Nk[:, None]
     return logZ, Nk, mu_acc, sig_acc
 
 

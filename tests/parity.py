@@ -40,6 +40,19 @@ def logz_atol_fp32(ref32_logZ, ref64_logZ, D):
 # ~ ||x||^2) remains; logZ is checked at 2e-3 (the contract itself is ~1 away from
 # the fp64 result on clustered data), the statistics at REL.
 LOGZ_ATOL_BF16 = 2e-3
+
+
+def logz_atol_bf16(ref32_logZ, ref64_logZ, D):
+    """The bf16-contract logZ bound at width D: 2e-3 up to D = 256; above, the
+    log-joint's float32 terms (c0, ish ||x||^2, 2 ish x.mu, each ~ 4 D log2 units
+    on this data) carry rounding that grows with D, and the bound is max(2e-3, the
+    error of the float32 restatement of the contract on the same rows).  ref32_logZ
+    comes from the contract's oracle evaluated in float32."""
+    if D <= 256:
+        return LOGZ_ATOL_BF16
+    return max(LOGZ_ATOL_BF16, logz_err(ref32_logZ, ref64_logZ))
+
+
 # Under the bf16 contract, mu_acc and the diagonal / full second moments sum products
 # whose factor r (or r x) is rounded to bf16.  The kernel's fp32 r differs from the
 # oracle's float64 r in the last bits, and that moves a product's bf16 rounding by one
@@ -50,6 +63,14 @@ LOGZ_ATOL_BF16 = 2e-3
 # this contract, flash_gmm_h100.py:276); Nk and the isotropic sig_acc, formed from
 # the fp32 r, keep the float32 bounds.
 REL_BF16_STATS = 1e-3
+# Above D = 256 the log-joint's float32 terms carry up to ~2e-3 of rounding (the
+# reference's own arithmetic as much: logz_atol_bf16), so r moves by ~1e-3 relative and
+# bf16(r) rounds one unit (2^-8) apart far more often; a component whose sums come from
+# a dozen rows then moves by ~2^-8 |x| / max|mu_acc_k| per flipped row (measured: one
+# flip, 1.6e-3, at N=4000, K=64, D=960 on N(0, I) data).  There these statistics are
+# held to the reference's stated tolerance for the bf16 path, 5e-3
+# (flash_gmm_h100.py:274-276).
+REL_BF16_STATS_WIDE = 5e-3
 
 
 def _np(t):
@@ -65,7 +86,7 @@ def _per_component_normwise(g, r, rel, what):
     assert (err <= rel * scale).all(), f"{what} per-component norm-wise err {(err / scale).max()}"
 
 
-def assert_close_stats(got, ref, what="", logz_atol=LOGZ_ATOL, bf16_stats=False):
+def assert_close_stats(got, ref, what="", logz_atol=LOGZ_ATOL, bf16_stats=False, bf16_rel=REL_BF16_STATS):
     lz, nk, mu_acc, sig = (_np(t) for t in got)
     rlz, rnk, rmu, rsig = (np.asarray(t, dtype=np.float64) for t in ref)
     if rlz.size:
@@ -74,9 +95,9 @@ def assert_close_stats(got, ref, what="", logz_atol=LOGZ_ATOL, bf16_stats=False)
         assert np.array_equal(np.isfinite(lz), finite), f"{what} logZ finiteness"
         assert err[finite].max(initial=0) <= logz_atol, f"{what} logZ max abs err {err[finite].max()}"
     if bf16_stats:
-        _per_component_normwise(mu_acc, rmu, REL_BF16_STATS, f"{what} mu_acc")
+        _per_component_normwise(mu_acc, rmu, bf16_rel, f"{what} mu_acc")
         if rsig.ndim > 1:
-            _per_component_normwise(sig, rsig, REL_BF16_STATS, f"{what} sig")
+            _per_component_normwise(sig, rsig, bf16_rel, f"{what} sig")
             rsig = rsig[:0]
         rmu = rmu[:0]
     for name, g, r in (("Nk", nk, rnk), ("sig", sig, rsig)):

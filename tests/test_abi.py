@@ -136,7 +136,6 @@ def _call_iso(**kw):
     (dict(mu=None), _lib.FGMM_ERR_INVALID_ARG),
     (dict(ldmu=16), _lib.FGMM_ERR_INVALID_ARG),
     (dict(Nk=None), _lib.FGMM_ERR_INVALID_ARG),
-    (dict(D=300, ldx=300, ldmu=300, flags=_lib.FLAG_BF16), _lib.FGMM_ERR_UNSUPPORTED),
     (dict(N=(1 << 37) + 1), _lib.FGMM_ERR_UNSUPPORTED),  # pass-1 grid limit
     (dict(ws_bytes=16), _lib.FGMM_ERR_WORKSPACE),
     (dict(ws=None), _lib.FGMM_ERR_WORKSPACE),
@@ -162,10 +161,8 @@ def _call_full(D, flags=0):
 @no_gpu
 def test_dimension_limits():
     """Largest supported D per covariance model; one past it is UNSUPPORTED.  The
-    isotropic and diagonal fp32 E-steps take any D, their bf16 contracts stop at 256;
-    the full-covariance E-step stops at 4096, its bf16 contract at 128."""
-    assert _call_iso(D=257, ldx=260, ldmu=257, flags=_lib.FLAG_BF16) == _lib.FGMM_ERR_UNSUPPORTED
-    assert _call_diag(257, flags=_lib.FLAG_BF16) == _lib.FGMM_ERR_UNSUPPORTED
+    isotropic and diagonal E-steps (and their bf16 contracts) take any D; the
+    full-covariance E-step stops at 4096, its bf16 contract at 128."""
     assert _call_full(4097) == _lib.FGMM_ERR_UNSUPPORTED
     assert _call_full(129, flags=_lib.FLAG_BF16) == _lib.FGMM_ERR_UNSUPPORTED
     # workspace queries accept the supported range
@@ -177,6 +174,10 @@ def test_dimension_limits():
         L.fgmm_full_workspace_bytes(100, 10, 256) > L.fgmm_full_workspace_bytes(100, 10, 128) > \
         L.fgmm_full_workspace_bytes(100, 10, 64) > 0
     assert L.fgmm_full_workspace_bytes(100, 10, 4096) > 0 == L.fgmm_full_workspace_bytes(100, 10, 4097)
+    # the bf16 contracts above D = 256 store the N x K log-joint
+    B = _lib.FLAG_BF16
+    for q in (L.fgmm_iso_workspace_bytes_ex, L.fgmm_diag_workspace_bytes_ex):
+        assert q(4096, 64, 960, B) > q(4096, 64, 300, B) >= 4096 * 64 * 4
 
 
 def test_python_layer_rejects_cpu_tensors():

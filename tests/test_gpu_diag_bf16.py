@@ -7,7 +7,7 @@ import torch
 
 from flash_gmm import FlashGMMError, data, diag_estep_into, flash_gmm_estep_diag
 from oracle import gmm_oracle as O
-from parity import LOGZ_ATOL_BF16, assert_close_stats
+from parity import LOGZ_ATOL_BF16, REL_BF16_STATS_WIDE, assert_close_stats, logz_atol_bf16, logz_err
 
 pytestmark = pytest.mark.gpu
 
@@ -118,3 +118,41 @@ def test_bad_precision_string(gpu_device):
     inp = data.diag_clustered(10, 4, 8, seed=11)
     with pytest.raises(FlashGMMError):
         flash_gmm_estep_diag(*[inp[k].to(gpu_device) for k in KEYS], precision="fp16")
+
+
+# Above D = 256 the contract stores the log-joint (pass 1 tiled over components, pass 2
+# from the stored rows per range of 128 dimensions): GloVe-300 and GIST-960 widths, one
+# past the narrow kernels, a partial last range and component tile, K = 1.
+WIDE_SHAPES = [(1000, 40, 257), (3000, 100, 300), (2000, 130, 960), (700, 33, 1100), (65, 1, 640)]
+
+
+@pytest.mark.parametrize("N,K,D", WIDE_SHAPES)
+def test_above_256_against_oracle(N, K, D, gpu_device):
+    print(f"diag bf16 wide N={N} K={K} D={D}", flush=True)
+    inp = data.diag_clustered(N, K, D, seed=N + K + D)
+    got, ref = _into(inp, gpu_device), oracle(inp)
+    atol = logz_atol_bf16(O.estep_diag_bf16(*[inp[k] for k in KEYS], dtype=torch.float32)[0], ref[0], D)
+    print(f"max |logZ - oracle| {logz_err(got[0], ref[0]):.2e}, bound {atol:.2e}", flush=True)
+    assert_close_stats(got, ref, f"diag bf16 N={N} K={K} D={D}", logz_atol=atol, bf16_stats=True,
+                       bf16_rel=REL_BF16_STATS_WIDE)
+
+
+def test_above_256_dense_and_phase_split(gpu_device):
+    """FGMM_FLAG_DENSE and PHASE1-then-PHASE2 give the single call's bits at D = 300."""
+    from flash_gmm import _lib, diag_estep_into
+    N, K, D = 3000, 70, 300
+    inp = data.diag_clustered(N, K, D, seed=31)
+    dev = gpu_device
+    ref = _into(inp, dev)
+    for u, v in zip(_into(inp, dev, dense=True), ref):
+        assert torch.equal(u, v)
+    L = _lib.lib()
+    ws = torch.empty(L.fgmm_diag_workspace_bytes_ex(N, K, D, _lib.FLAG_BF16), dtype=torch.uint8, device=dev)
+    args = [inp[k].to(dev) for k in KEYS]
+    out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, D, device=dev)]
+    diag_estep_into(*args, *out, workspace=ws, phase=1, precision="bf16")
+    diag_estep_into(*args, None, *out[1:], workspace=ws, phase=2, precision="bf16")
+    torch.cuda.synchronize()
+    for u, v in zip(out, ref):
+        assert torch.equal(u, v)

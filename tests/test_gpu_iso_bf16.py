@@ -8,7 +8,7 @@ import torch
 
 from flash_gmm import FlashGMMError, data, flash_gmm_estep, iso_estep_into
 from oracle import gmm_oracle as O
-from parity import LOGZ_ATOL_BF16, assert_close_stats
+from parity import LOGZ_ATOL_BF16, REL_BF16_STATS_WIDE, assert_close_stats, logz_atol_bf16, logz_err
 
 pytestmark = pytest.mark.gpu
 
@@ -97,3 +97,52 @@ def test_bad_precision_string(gpu_device):
     inp = data.iso_plain(10, 4, 8, seed=11)
     with pytest.raises(FlashGMMError):
         flash_gmm_estep(*[inp[k].to(gpu_device) for k in KEYS], precision="fp16")
+
+
+# Above D = 256 the contract stores the log-joint: pass 1 tiles the contraction over
+# components, pass 2 reads r from the stored rows per range of 256 dimensions.
+# GloVe-300 and GIST-960 widths, one past the narrow kernels, several dimension
+# ranges with a partial last one, partial component tiles and K = 1.
+WIDE_SHAPES = [(1000, 40, 257), (3000, 100, 300), (2000, 130, 960), (700, 33, 1100), (65, 1, 640)]
+
+
+@pytest.mark.parametrize("N,K,D", WIDE_SHAPES)
+def test_above_256_against_oracle(N, K, D, gpu_device):
+    print(f"iso bf16 wide N={N} K={K} D={D}", flush=True)
+    inp = data.iso_clustered(N, K, D, seed=N + K + D)
+    got, ref = _into(inp, gpu_device), oracle(inp)
+    atol = logz_atol_bf16(O.estep_iso_bf16(*[inp[k] for k in KEYS], dtype=torch.float32)[0], ref[0], D)
+    print(f"max |logZ - oracle| {logz_err(got[0], ref[0]):.2e}, bound {atol:.2e}", flush=True)
+    # mu_acc sums bf16(r) x: with the log-joint within the float32 restatement's
+    # error of the replay, bf16(r) can round one unit apart (parity.REL_BF16_STATS_WIDE).
+    assert_close_stats(got, ref, f"bf16 N={N} K={K} D={D}", logz_atol=atol, bf16_stats=True,
+                       bf16_rel=REL_BF16_STATS_WIDE)
+
+
+def test_above_256_plain_gaussian_dense_and_phase_split(gpu_device):
+    """The reference's smoke data at D = 960 (every r fractional) against the oracle;
+    FGMM_FLAG_DENSE and PHASE1-then-PHASE2 give the single call's bits."""
+    from flash_gmm import _lib
+    g = torch.Generator().manual_seed(7)
+    N, K, D = 4000, 64, 960
+    inp = {"X": torch.randn(N, D, generator=g), "mu": torch.randn(K, D, generator=g),
+           "log_sigma_sq": torch.zeros(K), "log_pi": torch.full((K,), -math.log(K))}
+    dev = gpu_device
+    ref = _into(inp, dev)
+    r64 = oracle(inp)
+    atol = logz_atol_bf16(O.estep_iso_bf16(*[inp[k] for k in KEYS], dtype=torch.float32)[0], r64[0], D)
+    print(f"max |logZ - oracle| {logz_err(ref[0], r64[0]):.2e}, bound {atol:.2e}", flush=True)
+    assert_close_stats(ref, r64, "bf16 smoke data D=960", logz_atol=atol, bf16_stats=True,
+                       bf16_rel=REL_BF16_STATS_WIDE)
+    for u, v in zip(_into(inp, dev, dense=True), ref):
+        assert torch.equal(u, v)
+    L = _lib.lib()
+    ws = torch.empty(L.fgmm_iso_workspace_bytes_ex(N, K, D, _lib.FLAG_BF16), dtype=torch.uint8, device=dev)
+    args = [inp[k].to(dev) for k in KEYS]
+    out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+           torch.empty(K, device=dev)]
+    iso_estep_into(*args, *out, workspace=ws, phase=1, precision="bf16")
+    iso_estep_into(*args, None, *out[1:], workspace=ws, phase=2, precision="bf16")
+    torch.cuda.synchronize()
+    for u, v in zip(out, ref):
+        assert torch.equal(u, v)

@@ -192,6 +192,26 @@ def test_iso_bf16_brute_force_tiny():
     np.testing.assert_allclose(sig_acc.numpy(), sig_b, rtol=1e-10)
 
 
+def test_bf16_float32_mode_is_the_same_contract_in_float32():
+    """dtype=float32 evaluates the bf16 contracts' steps in float32: at small D it
+    stays within float32 rounding of the float64 evaluation (logZ 1e-4, statistics
+    1e-4), and it is not the float64 evaluation itself (the rounding is visible)."""
+    X, mu, lss, lpi = _iso_inputs(N=400, K=7, D=24, seed=23)
+    a = O.estep_iso_bf16(X, mu, lss, lpi)
+    b = O.estep_iso_bf16(X, mu, lss, lpi, dtype=torch.float32)
+    assert b[0].dtype == torch.float32
+    assert 0 < (a[0] - b[0].double()).abs().max() < 1e-4
+    for u, v in zip(a[1:], b[1:]):
+        np.testing.assert_allclose(v.double().numpy(), u.numpy(), rtol=1e-4, atol=1e-4 * float(u.abs().max()))
+    g = torch.Generator().manual_seed(24)
+    lssd = torch.rand(7, 24, generator=g, dtype=torch.float64) - 0.5
+    a = O.estep_diag_bf16(X, mu, lssd, lpi)
+    b = O.estep_diag_bf16(X, mu, lssd, lpi, dtype=torch.float32)
+    assert 0 < (a[0] - b[0].double()).abs().max() < 1e-4
+    for u, v in zip(a[1:], b[1:]):
+        np.testing.assert_allclose(v.double().numpy(), u.numpy(), rtol=1e-4, atol=1e-4 * float(u.abs().max()))
+
+
 def test_bf16_scalar_rounding_ties_to_even():
     """The brute-force rounding itself: ties go to the even bfloat16 neighbour."""
     one_ulp = 2.0 ** -7                      # bf16 spacing at 1.0
