@@ -7,8 +7,10 @@
  * stream) and never synchronises the device.  Functions return FGMM_OK (0) or
  * a negative status; fgmm_strerror() names it.  Nothing aborts or exits.
  *
- * All device memory is owned by the caller: outputs, and a workspace sized by
- * the matching *_workspace_bytes() query.  The work split (and so the workspace
+ * All device memory of the E-steps is owned by the caller: outputs, and a
+ * workspace sized by the matching *_workspace_bytes() query (fgmm_full_mstep_f32
+ * above D = 128 and the streaming driver allocate their own scratch and release
+ * it: in stream order, and before returning).  The work split (and so the workspace
  * size) follows the compute-unit count of the current device: query with the
  * device current that the call will run on.  The library keeps no allocations
  * between calls, except the fixed scratch array of fgmm_iso_estep_f32_noalloc.
@@ -121,8 +123,9 @@ const char *fgmm_strerror(int status);
 /*   Nk_k    = sum_n r_nk,  r_nk = exp(ll_nk - logZ_n)                        */
 /*   mu_acc  = sum_n r_nk x_n                                                 */
 /*   sig_acc = sum_n r_nk ||x_n - mu_k||^2                                    */
-/* log_sigma_sq and log_pi are contiguous (K).  Any D >= 1 (the bf16         */
-/* contract: D <= 256).                                                       */
+/* log_sigma_sq and log_pi are contiguous (K).  Any D >= 1.  Above D = 256   */
+/* the bf16 contract stores the N x K log-joint (16 GiB at most per call:     */
+/* larger N runs as row chunks, as the full model's bf16 contract does).      */
 /* ------------------------------------------------------------------------ */
 size_t fgmm_iso_workspace_bytes(int64_t N, int64_t K, int64_t D);
 /* Workspace for a call made with `flags` (FGMM_FLAG_STORE_LOGJOINT, RECOMPUTE
@@ -171,7 +174,8 @@ int fgmm_iso_estep_f32_noalloc(const float *X, int64_t ldx, int64_t N, int64_t D
 /*   ll_nk      = log_pi_k - 0.5*(D log(2 pi) + sum_d lss_kd)                 */
 /*                - 0.5 * sum_d (x_nd - mu_kd)^2 exp(-lss_kd)                 */
 /*   sig_acc_kd = sum_n r_nk (x_nd - mu_kd)^2                                 */
-/* Any D >= 1 (the bf16 contract: D <= 256).                                  */
+/* Any D >= 1 (above D = 256 the bf16 contract stores the log-joint, as the  */
+/* isotropic one does).                                                       */
 /* ------------------------------------------------------------------------ */
 size_t fgmm_diag_workspace_bytes(int64_t N, int64_t K, int64_t D);
 size_t fgmm_diag_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags);

@@ -393,9 +393,17 @@ def mstep_diag(Nk: Tensor, mu_acc: Tensor, sig_acc: Tensor, N: int):
 
 def prec_chol_from_cov(cov: Tensor) -> Tensor:
     """Lower-triangular L with L L^T = cov^-1 (the prec_chol parameterisation of
-    flash_gmm_full_h100.py:238,247-248), in float64."""
-    c = cov.double()
-    return torch.linalg.cholesky(torch.linalg.inv(c))
+    flash_gmm_full_h100.py:238,247-248), in float64.  Per component in numpy: batched
+    float64 inverses through torch's CPU backend have come back not positive definite
+    on some hosts (see flash_gmm.data.full_clustered)."""
+    import numpy as np
+    c = cov.double().cpu().numpy()
+    batch = c.reshape(-1, c.shape[-2], c.shape[-1])
+    out = np.empty_like(batch)
+    for k in range(batch.shape[0]):
+        p = np.linalg.inv(batch[k])
+        out[k] = np.linalg.cholesky(0.5 * (p + p.T))
+    return torch.from_numpy(out.reshape(c.shape))
 
 
 def mstep_full(Nk: Tensor, mu_acc: Tensor, sig_outer: Tensor, N: int):
