@@ -56,6 +56,8 @@ struct FullPlan {
   bool need;    // default plan: pass 1 leaves need masks, pass 2 gathers
   bool rexact;  // need masks from the per-(row, component) bounds (else the running max)
   bool wide;    // D > 256: full_lse_wide stores the log-joint, full_accum_wide reads it
+  bool keep_lj; // 128 < D <= 256, default plan: pass 1 also stores the log-joint, and the
+                // gathering pass 2 reads r from it instead of whitening the needed rows
   int nstrip;   // wide pass 2: strips of upper sig_outer blocks (one wave each)
   int ngrp;     // waves per (slab, component) in the gathering pass 2 (groups of sig blocks)
   int grid1;    // pass-1 workgroups with need masks (a persistent grid)
@@ -129,6 +131,10 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.lj = p.wide ? K > 0
                 : (allow_lj || bf16) && K > 0 && p.DP <= 128 && full_lj_bytes(N, p.KP) <= kMaxLjBytes;
   p.need = !bf16 && !p.lj && K > 0;
+  // Above D = 128 the gathering pass 2 runs as 2-4 launches (groups of sig_outer
+  // blocks), each of which would whiten the needed rows again; 4 bytes per (row,
+  // component) of stored log-joint replace those D x D whitenings.
+  p.keep_lj = p.need && p.DP > 128 && !p.wide && full_lj_bytes(N, p.KP) <= kMaxLjBytes;
   p.rexact = p.need && K <= kNeedExactMaxK;
   p.ngrp = gather_sig_groups(p.DP);
   if (bf16) {
@@ -193,7 +199,7 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.off_part_mu = off;  off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
   p.off_part_nk = off;  off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
   p.off_lj = off;
-  if (p.lj) off = align256(off + full_lj_bytes(N, p.KP));
+  if (p.lj || p.keep_lj) off = align256(off + full_lj_bytes(N, p.KP));
   // Need masks: one word per (32-row tile of the pass-1 grid, component).
   p.grid1 = 0;
   p.off_need = off;
@@ -327,14 +333,16 @@ constexpr int kLjmNeed = 2;    // need masks only (the default plan)
 // own writes, read back by the same lanes once logZ2 is final), and writes the need
 // word of each (32-row tile, component): bit r set unless the bound of row r is
 // kLjNeedGap below its logZ2 (need_put_masks).
-template <int DP, int LJM>
+// KEEP (with need masks): also store the log-joint, for a pass 2 that reads r.
+template <int DP, int LJM, bool KEEP = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(full_waves_per_eu(DP), full_waves_per_eu(DP))))
 void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, const bf16x8* __restrict__ l3,
                  const double* __restrict__ esw, const double* __restrict__ ck, int K, int KP,
                  float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj,
                  unsigned* __restrict__ need, unsigned short* __restrict__ bound, int rexact, int dense) {
-  constexpr bool LJ = LJM == kLjmStore;
+  constexpr bool LJ = LJM == kLjmStore || KEEP;
+  static_assert(!KEEP || LJM == kLjmNeed, "KEEP adds the log-joint to the need masks");
   constexpr int NMB = DP / 32, NQ = DP / 16;
   constexpr int SMB = full_x6_smb<DP>();          // coordinate blocks per stage
   constexpr int NST = NMB / SMB;                  // stages per component
@@ -760,7 +768,9 @@ constexpr size_t gather_lds_bytes() {
 __host__ __device__ constexpr int gather_groups(int nslab) { return (nslab + kGatherWaves - 1) / kGatherWaves; }
 __host__ inline int64_t gather_grid(int nslab, int K) { return gather_item_grid(gather_groups(nslab), K); }
 
-template <int DP, int GRP>
+// LJR: r comes from the log-joint pass 1 stored (keep_lj plans) instead of a
+// whitening of the queued rows.
+template <int DP, int GRP, bool LJR = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * kGatherWaves, 64 * kGatherWaves),
                           amdgpu_waves_per_eu(gather_waves_per_eu(DP), gather_waves_per_eu(DP))))
 void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
@@ -768,7 +778,7 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
                        const double* __restrict__ ck, int K, int KP, const double* __restrict__ rowstat,
                        const unsigned* __restrict__ need, int nslab, int64_t rows_per_slab,
                        float* __restrict__ part_sig, float* __restrict__ part_mu, float* __restrict__ part_nk,
-                       int dense) {
+                       int dense, const float* __restrict__ lj) {
   constexpr int NMB = DP / 32, NQ = DP / 16, NSB = NMB * (NMB + 1) / 2;
   constexpr int NGRP = gather_sig_groups(DP);
   constexpr int NSBG = (NSB + NGRP - 1) / NGRP;              // blocks per group
@@ -793,9 +803,10 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   const int c = lane & 31, g = lane >> 5;
   int sg, k;
   if (!gather_item(blockIdx.x, gather_groups(nslab), K, sg, k)) return;   // uniform over the workgroup
-  if constexpr (OPS_LDS)
+  if constexpr (OPS_LDS && !LJR)
     for (int idx = tid; idx < BLK; idx += 64 * kGatherWaves) l_l[idx] = l3[(int64_t)k * BLK + idx];
-  for (int idx = tid; idx <= DP; idx += 64 * kGatherWaves) e_l[idx] = idx < DP ? esw[(int64_t)k * DP + idx] : ck[k];
+  if constexpr (!LJR)
+    for (int idx = tid; idx <= DP; idx += 64 * kGatherWaves) e_l[idx] = idx < DP ? esw[(int64_t)k * DP + idx] : ck[k];
   const bf16x8* lops = OPS_LDS ? l_l : l3 + (int64_t)k * BLK;
   __syncthreads();
   const int slab = sg * kGatherWaves + wave;
@@ -833,6 +844,7 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   // the slab spans under 2 GiB (uniform), else load_row4.
   f32x4 raw[2 * NQ];
   double rst;
+  float lraw = 0.0f;   // LJR: the stored log-joint of the lane's queued row
   const int64_t slab_bytes = (r_end - r_begin) * ldx * (int64_t)sizeof(float);
   const bool xbuf = D == DP && slab_bytes <= ((int64_t)1 << 31) - 256;
   const buf_rsrc xres = make_rsrc(X + r_begin * ldx, xbuf ? (uint32_t)slab_bytes : 0u);
@@ -856,6 +868,10 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
     }
     const double z = buf_load_f64(rres, buf_off(ok ? e * (int)sizeof(double) : kBufOob));
     rst = ok ? z : INFINITY;
+    if constexpr (LJR) {
+      const int64_t rr = r_begin + (ok ? e : 0);   // a row of the slab: no branch
+      lraw = lj[((rr >> 5) * KP + k) * 32 + (rr & 31)];
+    }
   };
 
   f32x16 acc[SB1 - SB0];
@@ -878,14 +894,15 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
     if (!PREFETCH) issue(e);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the previous tile's LDS reads are done
     // Each chunk to the LDS tile, then split three ways (its fp32 registers free after).
-    bf16x8 xb[NQ][3];
+    bf16x8 xb[LJR ? 1 : NQ][3];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       *reinterpret_cast<f32x4*>(xt + c * RS + 16 * q + 8 * g) = raw[2 * q];
       *reinterpret_cast<f32x4*>(xt + c * RS + 16 * q + 8 * g + 4) = raw[2 * q + 1];
-      split3_bf16(raw[2 * q], raw[2 * q + 1], xb[q]);
+      if constexpr (!LJR) split3_bf16(raw[2 * q], raw[2 * q + 1], xb[q]);
     }
     const double lz2 = rst;
+    const float lcur = lraw;
     int en = -1;
     int cnt_next = 0;
     if (PREFETCH) {
@@ -893,22 +910,27 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
       if (cnt_next > 0) issue(en);
     }
 
-    // maha of row c as pass 1 forms it (lane = row, register = coordinate).
-    double maha = 0.0;
+    float rv;
+    if constexpr (LJR) {
+      rv = fast_exp2((float)((double)lcur - lz2));   // r from the stored log-joint
+    } else {
+      // maha of row c as pass 1 forms it (lane = row, register = coordinate).
+      double maha = 0.0;
 #pragma unroll DP <= 64 ? NMB : 1
-    for (int mb = 0; mb < NMB; ++mb) {
-      const f32x16 t = x6c_tile<NQ, 1>([&](int q, int u) { return lops[((mb * NQ + q) * 4 + u) * 64 + lane]; },
-                                       xb, ones);
-      const double* eb = e_l + mb * 32 + g * 16;
+      for (int mb = 0; mb < NMB; ++mb) {
+        const f32x16 t = x6c_tile<NQ, 1>([&](int q, int u) { return lops[((mb * NQ + q) * 4 + u) * 64 + lane]; },
+                                         xb, ones);
+        const double* eb = e_l + mb * 32 + g * 16;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const double v = (double)t[i] + eb[i];
-        maha = fma(v, v, maha);
+        for (int i = 0; i < 16; ++i) {
+          const double v = (double)t[i] + eb[i];
+          maha = fma(v, v, maha);
+        }
       }
+      maha += __shfl_xor(maha, 32);
+      const double ll = e_l[DP] - hl * maha;
+      rv = fast_exp2((float)(ll - lz2));
     }
-    maha += __shfl_xor(maha, 32);
-    const double ll = e_l[DP] - hl * maha;
-    const float rv = fast_exp2((float)(ll - lz2));
     if (g == 0) {
       if constexpr (FIRST) nk += rv;
       rx[c] = rv;
@@ -991,15 +1013,18 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
                          float* logZ, bool run1, bool run2, bool dense, hipStream_t stream) {
   const double* ck = reinterpret_cast<const double*>(ws + pl.off_ck);
   double* rowstat = reinterpret_cast<double*>(ws + pl.off_rowstat);
-  float* lj = pl.lj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
+  float* lj = (pl.lj || pl.keep_lj) ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
   auto set_lds = [](const void* f, size_t bytes) -> hipError_t {
     return bytes > 65536 ? hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes)
                          : hipSuccess;
   };
   if (run1) {
     constexpr size_t lds1 = full_x6_lds_bytes<DP>();
-    // The stored plan runs up to D = 128 only.
-    auto kern = (DP > 128 || pl.need) ? &full_lse_x6<DP, kLjmNeed> : &full_lse_x6<DP, DP <= 128 ? kLjmStore : kLjmNeed>;
+    // The stored plan runs up to D = 128 only; above, the default plan keeps the
+    // log-joint beside the need masks (keep_lj) where it fits.
+    auto kern = (DP > 128 || pl.need)
+                    ? (DP > 128 && pl.keep_lj ? &full_lse_x6<DP, kLjmNeed, (DP > 128)> : &full_lse_x6<DP, kLjmNeed>)
+                    : &full_lse_x6<DP, DP <= 128 ? kLjmStore : kLjmNeed>;
     hipError_t e = set_lds(reinterpret_cast<const void*>(kern), lds1);
     if (e != hipSuccess) return e;
     const unsigned grid1 = pl.need ? (unsigned)pl.grid1 : (unsigned)cdiv(pl.N, 32 * kWaves);
@@ -1021,14 +1046,15 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
       auto launch = [&](auto grp_tag) -> hipError_t {
         constexpr int GRP = decltype(grp_tag)::value;
         if constexpr (GRP < gather_sig_groups(DP)) {
-          hipError_t e = set_lds(reinterpret_cast<const void*>(&full_accum_gather<DP, GRP>), lds2);
+          auto kern2 = (DP > 128 && pl.keep_lj) ? &full_accum_gather<DP, GRP, (DP > 128)> : &full_accum_gather<DP, GRP>;
+          hipError_t e = set_lds(reinterpret_cast<const void*>(kern2), lds2);
           if (e != hipSuccess) return e;
-          hipLaunchKernelGGL((full_accum_gather<DP, GRP>), dim3((unsigned)gather_grid(pl.nslab, (int)pl.K)),
+          hipLaunchKernelGGL(kern2, dim3((unsigned)gather_grid(pl.nslab, (int)pl.K)),
                              dim3(64 * kGatherWaves), lds2, stream, X, ldx, pl.N, (int)pl.D,
                              reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
                              reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, rowstat,
                              reinterpret_cast<const unsigned*>(ws + pl.off_need), pl.nslab, pl.rows_per_slab,
-                             psig, pmu, pnk, dense ? 1 : 0);
+                             psig, pmu, pnk, dense ? 1 : 0, lj);
         }
         return hipSuccess;
       };
