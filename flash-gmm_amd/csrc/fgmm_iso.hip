@@ -139,6 +139,8 @@ struct IsoPlan {
   bool rexact;  // need masks from the block maxima kept in LDS (else the running-max bound)
   int ndr;      // dimension ranges of the component-tiled pass 2 (and of the wide bf16 pass 2)
   bool bfw;     // bf16 contract above D = 256: stored log-joint, iso_bf16_*_wide
+  bool bfneed;  // bf16 contract up to D = 128: need masks from pass 1, iso_bf16_gather in pass 2
+                // (or iso_bf16_accum where most pairs are needed)
   size_t off_musw, off_mu3, off_kcblk, off_kclin, off_kcgat, off_rowstat, off_part_mu, off_part_nk,
       off_part_sig, off_lj, off_ljmax, off_ljmask, off_ljcount, total;
 };
@@ -173,6 +175,9 @@ __host__ inline bool use_stored_lj(int64_t N, int DP, int KB, bool allow) {
 // bf16 pass 2: 4 component blocks per workgroup, or 2 / 1 for K <= 64 / 32 where
 // the taller X tiles fit in LDS (row-major and transposed bf16, double-buffered).
 __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB);
+__host__ __device__ constexpr size_t bf16_lse_lds_base(int DP) {
+  return (size_t)2 * (DP / 16) * 64 * 16 + (size_t)2 * 32 * 16;   // mu blocks (bf16x8) and constants (f32x4)
+}
 // Above D = 256 the bf16 contract stores the log-joint (defined with its kernels).
 constexpr int kBwCB = 8;     // component blocks per wide bf16 pass-2 workgroup (one per wave)
 constexpr int kBwDR = 256;   // dimensions per wide bf16 pass-2 workgroup
@@ -250,6 +255,10 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
     p.nslab = 0;
   }
   p.npart = p.nslab * p.rgroups;
+  // The bf16 contract's need masks: each row's block maxima (bf16, 2 bytes per row and
+  // block for the 4 waves of a pass-1 workgroup) must fit in LDS beside the stages.
+  p.bfneed = bf16 && !p.bfw && p.DP <= 128 && p.KB > 0 &&
+             bf16_lse_lds_base(p.DP) + (size_t)kWaves * 32 * p.KB * 2 <= kMaxLds;
   size_t off = 0;
   // The bf16 contract's operands (the fp32 plans read only the split operands below).
   p.off_musw = off;    off = align256(off + (bf16 ? (size_t)p.KP * p.DP * sizeof(float) : 0));
@@ -264,12 +273,12 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
   // One log-joint tile per pass-1 wave (the grid's 32-row tiles, rounded up to 4),
   // with its per-row block maxima and need mask; the default plan keeps the masks only.
   // (The default plan's pass 1 up to D = 128 runs 8 tiles per workgroup.)
-  const size_t ntile = (p.lj || p.need) ? (size_t)round_up(cdiv(N, 32), p.need ? 8 : 4) * p.KB : 0;
+  const size_t ntile = (p.lj || p.need || p.bfneed) ? (size_t)round_up(cdiv(N, 32), p.need ? 8 : 4) * p.KB : 0;
   p.off_lj = off;
   off = align256(off + (p.bfw ? bw_lj_bytes(N, p.KP) : p.lj ? ntile * kLjTile * sizeof(float) : 0));
   p.off_ljmax = off;  off = align256(off + (p.lj ? ntile * 32 * sizeof(float) : 0));
   p.off_ljmask = off; off = align256(off + ntile * sizeof(unsigned));
-  p.off_ljcount = off; off = align256(off + ((p.lj || p.need) ? 64 * sizeof(unsigned) : 0));
+  p.off_ljcount = off; off = align256(off + ((p.lj || p.need || p.bfneed) ? 64 * sizeof(unsigned) : 0));
   p.total = off;
   return p;
 }
@@ -2720,8 +2729,10 @@ __global__ __launch_bounds__(64) void iso_bf16_prep(const float* __restrict__ mu
                                                     int64_t K, int D, int DP,
                                                     const float* __restrict__ lss,
                                                     const float* __restrict__ lpi,
-                                                    bf16x8* __restrict__ mu_op, f32x4* __restrict__ kc) {
+                                                    bf16x8* __restrict__ mu_op, f32x4* __restrict__ kc,
+                                                    unsigned* __restrict__ ljcount) {
   const int kb = blockIdx.x, lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  if (ljcount && kb == 0) ljcount[lane] = 0u;   // pass 1 counts the needed pairs into these
   const int64_t k = (int64_t)kb * 32 + c;
   const bool valid = k < K;
   const int NC = DP / 16;
@@ -2753,19 +2764,27 @@ __global__ __launch_bounds__(64) void iso_bf16_prep(const float* __restrict__ mu
 
 // Pass 1: grid over 128-row tiles, 4 waves of 32 rows.  X is rounded to bf16 in
 // registers as it is loaded; mu blocks (bf16 operands + constants) stream through an
-// LDS double buffer.  Writes logZ and per-row {logZ2, ||x_b||^2} (fp32).
+// LDS double buffer.  Writes logZ and per-row {logZ2, ||x_b||^2} (fp32).  With NEED
+// each row's block maximum, rounded up to bf16, stays in LDS, and once logZ2 is final
+// the need words (bit r of (tile, block) set unless row r's maximum lies kLjNeedGap
+// below its logZ2, so that every responsibility of a cleared pair is exactly zero in
+// fp32) and the needed-pair count are written, as the fp32 default plan does.
 template <int DP>
 constexpr size_t bf16_lse_lds_bytes() {
-  return (size_t)2 * (DP / 16) * 64 * sizeof(bf16x8) + (size_t)2 * 32 * sizeof(f32x4);
+  static_assert(bf16_lse_lds_base(DP) == (size_t)2 * (DP / 16) * 64 * sizeof(bf16x8) + (size_t)2 * 32 * sizeof(f32x4),
+                "host sizing");
+  return bf16_lse_lds_base(DP);
 }
 
-template <int DP>
+template <int DP, bool NEED = false>
 __global__ __launch_bounds__(kThreads) void iso_bf16_lse(const float* __restrict__ X, int64_t ldx,
                                                          int64_t N, int D,
                                                          const bf16x8* __restrict__ mu_op,
                                                          const f32x4* __restrict__ kc, int KB,
                                                          float* __restrict__ logZ,
-                                                         float2* __restrict__ rowstat) {
+                                                         float2* __restrict__ rowstat,
+                                                         unsigned* __restrict__ ljmask,
+                                                         unsigned* __restrict__ ljcount, int dense) {
   constexpr int NC = DP / 16;
   constexpr int BLK = NC * 64;                 // bf16x8 per 32-component block
   constexpr int LPT = (BLK + kThreads - 1) / kThreads;
@@ -2773,10 +2792,12 @@ __global__ __launch_bounds__(kThreads) void iso_bf16_lse(const float* __restrict
   extern __shared__ __align__(16) unsigned char lds_raw[];
   bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                                // [2][BLK]
   f32x4* kc_l = reinterpret_cast<f32x4*>(lds_raw + 2 * BLK * sizeof(bf16x8));      // [2][32]
+  unsigned short* rmax_l = reinterpret_cast<unsigned short*>(lds_raw + bf16_lse_lds_bytes<DP>());   // [wave][KB][32]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
-  const int64_t row = ((int64_t)blockIdx.x * kWaves + wave) * 32 + c;
+  const int64_t tile = (int64_t)blockIdx.x * kWaves + wave;
+  const int64_t row = tile * 32 + c;
   const bool valid = row < N;
 
   bf16x8 st[LPT];
@@ -2845,6 +2866,7 @@ __global__ __launch_bounds__(kThreads) void iso_bf16_lse(const float* __restrict
       ll[i] = fmaf(w.z, acc[i], fmaf(-w.y, xsq, w.x));
       bm = fmaxf(bm, ll[i]);
     }
+    if constexpr (NEED) rmax_l[(wave * KB + kb) * 32 + c] = bf16_bits_up(lj_row_max(bm));   // both halves: same value
     const float mn = fmaxf(mx, bm);
     const float ms = (mn == -INFINITY) ? 0.0f : mn;
     float a = sm * fast_exp2(mx - ms);
@@ -2863,6 +2885,14 @@ __global__ __launch_bounds__(kThreads) void iso_bf16_lse(const float* __restrict
   if (valid && g == 0) {
     rowstat[row] = make_float2(lz2, xsq);
     if (logZ) logZ[row] = lz2 * (float)kLn2;
+  }
+  if constexpr (NEED) {
+    // Pass 2 forms fl(ll2 - logZ2) with ll2 <= the bound, so a cleared pair gives
+    // 2^x = 0 there (lz2 is a float: need_put_masks' low part is 0).
+    const unsigned short* rm = rmax_l + wave * KB * 32 + c;
+    if (g == 0)
+      need_put_masks([&](int kb) { return bf16_bits_to_float(rm[kb * 32]); }, ljmask + tile * KB,
+                     ljcount + (tile & 63), KB, c, (double)lz2, valid, dense != 0);
   }
 }
 
@@ -2903,7 +2933,8 @@ void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                     const bf16x8* __restrict__ mu_op, const f32x4* __restrict__ kc, int KB, int KP,
                     const float2* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
                     float* __restrict__ part_mu, float* __restrict__ part_nk,
-                    float* __restrict__ part_sig, int dense) {
+                    float* __restrict__ part_sig, int dense, const unsigned* __restrict__ needcount,
+                    int64_t dense_min) {
   constexpr int NC = DP / 16 / NH;             // 16-dimension chunks of the contraction per wave
   constexpr int NJ = DP / 32 / NH;             // 32-column tiles of r^T X per wave
   constexpr int RG = kAccWaves / (CB * NH);    // row groups of waves (32 rows each)
@@ -2915,6 +2946,10 @@ void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   constexpr int LPT = (NV + kAccThreads - 1) / kAccThreads;
   static_assert(kAccWaves % (CB * NH) == 0 && NV % kAccThreads == 0 && (DP / 32) % NH == 0,
                 "even split");
+
+  // With need masks and fewer than dense_min needed pairs iso_bf16_gather runs instead
+  // (uniform exit).
+  if (needcount && need_total(needcount) < dense_min) return;
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   __bf16* xr = reinterpret_cast<__bf16*>(lds_raw);                        // [2][TR][XR]
@@ -3086,18 +3121,236 @@ void iso_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   }
 }
 
+// Pass 2 of the bf16 contract up to D = 128 where few pairs are needed (pass 1's
+// needed-pair count below dense_min; iso_bf16_accum runs otherwise): one wave per
+// (row slab, component block), 4 waves of one block on consecutive slabs per
+// workgroup, the block's bf16 operands in LDS.  Each wave queues the rows whose need
+// bit is set (queue_fill, as the fp32 gathering pass does) and per 32 queued rows:
+//   - loads them (buffer resource over the slab: a lane without a row reads zeros),
+//     rounds them to bf16 in the A-operand layout (lane = row) and writes them
+//     row-major to its LDS tile;
+//   - S = x_b . mu_b in the contraction order of pass 1 (one chain; the per-half sums
+//     do not depend on the operand roles), so the log-joint is pass 1's bit for bit
+//     and a cleared pair would give r = 0 exactly;
+//   - r = 2^(ll2 - logZ2), Nk, sum r ||x_b||^2 and sum r S on the VALU, and
+//     bf16(r)^T x_b on the matrix cores (r as the A operand, the rows read from LDS by
+//     the transposing reads).
+// The rows of the next tile are in flight while a tile is computed.  slab counts the
+// partials of iso_bf16_accum's split (its slabs times its row groups), so either
+// kernel fills the same partial slots.
+__host__ __device__ constexpr int bf16_gather_rs(int DP) { return DP + 16; }   // bf16 row stride (odd x 32 bytes)
+__host__ __device__ constexpr size_t bf16_gather_lds_bytes(int DP) {
+  return (size_t)(DP / 16) * 64 * sizeof(bf16x8)                   // the block's mu operands
+         + (size_t)kGatherWaves * 32 * bf16_gather_rs(DP) * 2       // x_b tile per wave
+         + (size_t)kGatherWaves * 32 * sizeof(float2)               // row state per wave
+         + (size_t)kGatherWaves * 64 * sizeof(int);                 // row queue per wave
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kGatherWaves, 64 * kGatherWaves),
+                          amdgpu_waves_per_eu(gather_waves_per_simd(DP), gather_waves_per_simd(DP))))
+void iso_bf16_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                     const bf16x8* __restrict__ mu_op, const f32x4* __restrict__ kc, int KB, int KP,
+                     const float2* __restrict__ rowstat, const unsigned* __restrict__ need,
+                     const unsigned* __restrict__ needcount, int64_t dense_min, int nslab,
+                     int64_t rows_per_slab, float* __restrict__ part_mu, float* __restrict__ part_nk,
+                     float* __restrict__ part_sig, int dense) {
+  constexpr int NC = DP / 16;
+  constexpr int NJ = DP / 32;
+  constexpr int RS = bf16_gather_rs(DP);
+  constexpr int BLK = NC * 64;   // bf16x8 per component block
+  static_assert(DP <= 128, "one contraction chain");
+  if (need_total(needcount) >= dense_min) return;   // iso_bf16_accum runs instead (uniform exit)
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  unsigned char* lp = lds_raw;
+  bf16x8* mu_l = reinterpret_cast<bf16x8*>(lp);     lp += (size_t)BLK * sizeof(bf16x8);
+  __bf16* xt_all = reinterpret_cast<__bf16*>(lp);   lp += (size_t)kGatherWaves * 32 * RS * 2;
+  float2* rs_all = reinterpret_cast<float2*>(lp);   lp += (size_t)kGatherWaves * 32 * sizeof(float2);
+  int* q_all = reinterpret_cast<int*>(lp);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  int sg, kb;
+  if (!gather_item(blockIdx.x, gather_groups(nslab), KB, sg, kb)) return;   // uniform over the workgroup
+  for (int idx = tid; idx < BLK; idx += 64 * kGatherWaves) mu_l[idx] = mu_op[(int64_t)kb * BLK + idx];
+  __syncthreads();
+  const int slab = sg * kGatherWaves + wave;
+  if (slab >= nslab) return;   // no barrier follows
+
+  __bf16* xt = xt_all + wave * 32 * RS;
+  float2* rs_l = rs_all + wave * 32;
+  int* q_l = q_all + wave * 64;
+  const f32x4 w = kc[(int64_t)kb * 32 + c];   // {c0, ish, 2 ish, ||mu||^2} of component c
+  const float c0 = w.x, ish = w.y, ish2 = w.z, musq = w.w;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int64_t t_begin = r_begin / 32, t_end = r_end > r_begin ? cdiv(r_end, 32) : t_begin;
+
+  auto words = [&](int64_t tb) -> unsigned {
+    const int64_t t = tb + lane;
+    return t < t_end ? need[t * KB + kb] : 0u;
+  };
+  int64_t tb = t_begin;
+  unsigned mword = words(tb), mnext = words(tb + 64);
+  int jn = 0;
+  int qh = 0, qt = 0;
+  auto take = [&](int& e) -> int {
+    queue_fill<(DP > 64)>(words, tb, t_begin, t_end, mword, mnext, jn, qt, qh, lane, c, g, q_l);
+    const int cnt = qt - qh < 32 ? qt - qh : 32;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    e = c < cnt ? q_l[(qh + c) & 63] : -1;
+    qh += cnt;
+    return cnt;
+  };
+
+  f32x4 raw[2 * NC];
+  float2 rst;
+  const bool xbuf = slab_fits(r_end > r_begin ? r_end - r_begin : 0, ldx);
+  const bool xfull = xbuf && D == DP;
+  const buf_rsrc xres = slab_rsrc(X, ldx, r_begin, xbuf && r_end > r_begin ? r_end : r_begin);
+  const buf_rsrc rres = make_rsrc(rowstat + r_begin, (uint32_t)((r_end > r_begin ? r_end - r_begin : 0) * sizeof(float2)));
+  auto issue = [&](int e) __attribute__((always_inline)) {
+    const bool ok = e >= 0;
+    if (xfull) {
+      const int off = buf_off(ok ? (int)((int64_t)e * ldx * (int64_t)sizeof(float)) + 32 * g : kBufOob);
+#pragma unroll
+      for (int q = 0; q < NC; ++q) {
+        raw[2 * q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 64 * q, 0));
+        raw[2 * q + 1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 64 * q + 16, 0));
+      }
+    } else if (xbuf) {
+#pragma unroll
+      for (int q = 0; q < NC; ++q) {
+        raw[2 * q] = slab_row4(xres, ldx, e, 16 * q + 8 * g, D, ok);
+        raw[2 * q + 1] = slab_row4(xres, ldx, e, 16 * q + 8 * g + 4, D, ok);
+      }
+    } else {
+      const int64_t row = r_begin + (ok ? e : 0);
+#pragma unroll
+      for (int q = 0; q < NC; ++q) {
+        raw[2 * q] = load_row4(X, ldx, row, 16 * q + 8 * g, D, ok);
+        raw[2 * q + 1] = load_row4(X, ldx, row, 16 * q + 8 * g + 4, D, ok);
+      }
+    }
+    const float2 v = __builtin_bit_cast(
+        float2, __builtin_amdgcn_raw_buffer_load_b64(rres, buf_off(ok ? e * (int)sizeof(float2) : kBufOob), 0, 0));
+    rst = make_float2(ok ? v.x : INFINITY, v.y);   // a row past the queue: logZ2 = +inf, r = 0
+  };
+
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
+  float nk = 0.0f, srx = 0.0f, srs = 0.0f;
+
+  int e;
+  int cnt = take(e);
+  if (cnt > 0) issue(e);
+  while (cnt > 0) {
+    // This tile's rows: bf16 in the A-operand layout, row-major to LDS, row state to LDS.
+    bf16x8 xa[NC];
+#pragma unroll
+    for (int q = 0; q < NC; ++q) xa[q] = to_bf16x8(raw[2 * q], raw[2 * q + 1]);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the previous tile's LDS reads are done
+#pragma unroll
+    for (int q = 0; q < NC; ++q) *reinterpret_cast<bf16x8*>(xt + c * RS + 16 * q + 8 * g) = xa[q];
+    if (g == 0) rs_l[c] = rst;
+    int en;
+    const int cnt_next = take(en);
+    if (cnt_next > 0) issue(en);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+    // S = x_b mu_b^T: lane = component c, register i = row acc_row(i, g).
+    f32x16 s = zero16();
+#pragma unroll
+    for (int q = 0; q < NC; ++q) s = mfma_bf16(xa[q], mu_l[q * 64 + lane], s);
+    float r[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float2 z = rs_l[acc_row(i, g)];   // {logZ2, ||x_b||^2}
+      const float ll = fmaf(ish2, s[i], fmaf(-ish, z.y, c0));
+      const float rv = fast_exp2(ll - z.x);
+      nk += rv;
+      srx = fmaf(rv, z.y, srx);
+      srs = fmaf(rv, s[i], srs);
+      r[i] = rv;
+    }
+    bf16x8 a[2];
+    acc_to_row_operands(r, a);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      // A step whose 16 rows of bf16(r) are all zero adds nothing.
+      if (dense || any_nonzero(a[p])) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[j] = mfma_bf16(a[p], lds_rows_operand(xt, RS, 16 * p, 32 * j, lane), acc[j]);
+      }
+    }
+    e = en;
+    cnt = cnt_next;
+  }
+
+  nk += __shfl_xor(nk, 32);
+  srx += __shfl_xor(srx, 32);
+  srs += __shfl_xor(srs, 32);
+  const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[j][i];
+  }
+  if (g == 0) {
+    part_nk[kbase + c] = nk;
+    part_sig[kbase + c] = fmaf(musq, nk, fmaf(-2.0f, srs, srx));
+  }
+}
+
 template <int DP>
 hipError_t launch_bf16(const IsoPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
                        float* logZ, bool run1, bool run2, bool dense, hipStream_t stream) {
   const bf16x8* mu_op = reinterpret_cast<const bf16x8*>(ws + pl.off_musw);
   const f32x4* kc = reinterpret_cast<const f32x4*>(ws + pl.off_kcblk);
   float2* rowstat = reinterpret_cast<float2*>(ws + pl.off_rowstat);
+  unsigned* ljmask = reinterpret_cast<unsigned*>(ws + pl.off_ljmask);
+  unsigned* ljcount = reinterpret_cast<unsigned*>(ws + pl.off_ljcount);
   if (run1) {
-    constexpr size_t lds1 = bf16_lse_lds_bytes<DP>();
-    hipLaunchKernelGGL(iso_bf16_lse<DP>, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
-                       stream, X, ldx, pl.N, (int)pl.D, mu_op, kc, pl.KB, logZ, rowstat);
+    if (pl.bfneed) {
+      if constexpr (DP <= 128) {
+        const size_t lds1 = bf16_lse_lds_bytes<DP>() + (size_t)kWaves * 32 * pl.KB * 2;
+        if (lds1 > 65536) {
+          hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_bf16_lse<DP, true>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+          if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL((iso_bf16_lse<DP, true>), dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
+                           stream, X, ldx, pl.N, (int)pl.D, mu_op, kc, pl.KB, logZ, rowstat, ljmask, ljcount,
+                           dense ? 1 : 0);
+      }
+    } else {
+      constexpr size_t lds1 = bf16_lse_lds_bytes<DP>();
+      hipLaunchKernelGGL(iso_bf16_lse<DP>, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
+                         stream, X, ldx, pl.N, (int)pl.D, mu_op, kc, pl.KB, logZ, rowstat, ljmask, ljcount,
+                         dense ? 1 : 0);
+    }
   }
   if (!run2) return hipGetLastError();
+  // With need masks: the gathering pass (one slab per partial of the dense split) when
+  // fewer than 3/4 of the (row, block) pairs are needed, else iso_bf16_accum; both are
+  // launched and the needed-pair count selects one on the device.
+  const int64_t dense_min = cdiv(cdiv(pl.N, 32) * 32 * (int64_t)pl.KB * 3, 4);
+  if (pl.bfneed) {
+    if constexpr (DP <= 128) {
+      constexpr size_t ldsg = bf16_gather_lds_bytes(DP);
+      static_assert(ldsg <= 65536, "gathering tiles fit the default LDS allocation");
+      hipLaunchKernelGGL(iso_bf16_gather<DP>, dim3((unsigned)gather_grid(pl.npart, pl.KB)),
+                         dim3(64 * kGatherWaves), ldsg, stream, X, ldx, pl.N, (int)pl.D, mu_op, kc, pl.KB, pl.KP,
+                         rowstat, ljmask, ljcount, dense_min, pl.npart, (int64_t)round_up(cdiv(pl.N, pl.npart), 32),
+                         reinterpret_cast<float*>(ws + pl.off_part_mu), reinterpret_cast<float*>(ws + pl.off_part_nk),
+                         reinterpret_cast<float*>(ws + pl.off_part_sig), dense ? 1 : 0);
+    }
+  }
   auto launch = [&](auto cb_tag) -> hipError_t {
     constexpr int CB = decltype(cb_tag)::value;
     constexpr size_t lds = bf16_accum_lds_bytes(DP, CB);
@@ -3113,7 +3366,8 @@ hipError_t launch_bf16(const IsoPlan& pl, const float* X, int64_t ldx, unsigned 
                          lds, stream, X, ldx, pl.N, (int)pl.D, mu_op, kc, pl.KB, pl.KP, rowstat,
                          pl.nslab, pl.rows_per_slab, reinterpret_cast<float*>(ws + pl.off_part_mu),
                          reinterpret_cast<float*>(ws + pl.off_part_nk),
-                         reinterpret_cast<float*>(ws + pl.off_part_sig), dense ? 1 : 0);
+                         reinterpret_cast<float*>(ws + pl.off_part_sig), dense ? 1 : 0,
+                         pl.bfneed ? ljcount : nullptr, dense_min);
       return hipGetLastError();
     }
   };
@@ -3562,7 +3816,8 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
   if (run1 && bf16)
     hipLaunchKernelGGL(iso_bf16_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, K, (int)D, pl.DP,
                        log_sigma_sq, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_musw),
-                       reinterpret_cast<f32x4*>(ws + pl.off_kcblk));
+                       reinterpret_cast<f32x4*>(ws + pl.off_kcblk),
+                       pl.bfneed ? reinterpret_cast<unsigned*>(ws + pl.off_ljcount) : nullptr);
   else if (run1)
     hipLaunchKernelGGL(iso_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, K, (int)D, pl.DP,
                        log_sigma_sq, log_pi, reinterpret_cast<double2*>(ws + pl.off_kcblk),
