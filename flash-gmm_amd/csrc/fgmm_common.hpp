@@ -528,6 +528,16 @@ __device__ __forceinline__ void need_put_masks(RM rmax, unsigned* __restrict__ m
   if (count && c == 0 && pairs != 0) atomicAdd(count, pairs);
 }
 
+// Total of the 64 needed-pair counters pass 1 adds to, in 64 bits (needed rows of a
+// call can pass 2^32); one wave, uniform result.
+__device__ __forceinline__ int64_t need_total(const unsigned* __restrict__ count) {
+  uint64_t v = count[threadIdx.x & 63];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return (int64_t)__builtin_amdgcn_readfirstlane((unsigned)(v & 0xffffffffu)) |
+         ((int64_t)__builtin_amdgcn_readfirstlane((unsigned)(v >> 32)) << 32);
+}
+
 // x6c_tile_rows with the rows' splits produced per chunk by loadX(q, xa[3]) (for
 // operands formed from other data, such as the diagonal model's [x^2, x] features):
 // the same products, order and chains, NCH chunks' splits live at a time.

@@ -78,6 +78,9 @@ __host__ __device__ constexpr size_t accum_drange_lds_bytes(int DR) {
          + (size_t)kCtWaves * 64 * sizeof(int);              // row queue per wave
 }
 
+__host__ __device__ constexpr size_t bf16_lse_lds_base(int DP) {
+  return (size_t)2 * (DP / 8) * 64 * 16 + (size_t)2 * 32 * sizeof(float);   // feature blocks and c0
+}
 // bf16 operand contract (defined with its kernels below).  Above D = 256 it stores
 // the log-joint ([32-row tile][KP][32 rows], fp32).
 constexpr int kBwCB = 8;     // component blocks per wide bf16 pass-2 workgroup (one per wave)
@@ -110,6 +113,8 @@ struct DiagPlan {
   bool rexact;      // need masks from block maxima kept in LDS (else the running-max bound)
   int ndr;          // dimension ranges of the range pass 2 (and of the wide bf16 pass 2)
   bool bfw;         // bf16 contract above D = 256: stored log-joint, diag_bf16_*_wide
+  bool bfneed;      // bf16 contract up to D = 128: need masks from pass 1, diag_bf16_gather in pass 2
+                    // (or diag_bf16_accum where most pairs are needed)
   size_t off_musw, off_mu3, off_kcx6, off_kcx6lin, off_kclin, off_rowstat, off_part_mu,
       off_part_sq, off_part_nk, off_lj, off_ljmax, off_ljmask, off_ljcount, total;
 };
@@ -220,12 +225,16 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   // (32-row tile, block), ORed by pass 2.
   p.lj_sparse = p.lj && diag_uses_x6(p.DP);
   const size_t ntile = (p.lj || p.need) ? (size_t)round_up(cdiv(N, 32), 4) * p.KB : 0;
-  const size_t nsp = (p.lj_sparse || p.need) ? ntile : 0;
+  // The bf16 contract's need masks (one word per (tile, block)): each row's block maxima
+  // (bf16, 2 bytes per row and block for the 4 waves of a pass-1 workgroup) in LDS.
+  p.bfneed = bf16 && !p.bfw && p.DP <= 128 && p.KB > 0 &&
+             bf16_lse_lds_base(p.DP) + (size_t)kWaves * 32 * p.KB * 2 <= kMaxLds;
+  const size_t nsp = (p.lj_sparse || p.need || p.bfneed) ? (p.bfneed ? (size_t)round_up(cdiv(N, 32), 4) * p.KB : ntile) : 0;
   p.off_lj = off;
   off = align256(off + (p.bfw ? bw_lj_bytes(N, p.KP) : p.lj ? ntile * kLjTile * sizeof(float) : 0));
   p.off_ljmax = off;   off = align256(off + (p.lj_sparse ? nsp * 64 * sizeof(float) : 0));
   p.off_ljmask = off;  off = align256(off + nsp * sizeof(uint2));
-  p.off_ljcount = off; off = align256(off + (p.lj_sparse ? 64 * sizeof(unsigned) : 0));
+  p.off_ljcount = off; off = align256(off + ((p.lj_sparse || p.bfneed) ? 64 * sizeof(unsigned) : 0));
   p.total = off;
   return p;
 }
@@ -2104,8 +2113,10 @@ __global__ __launch_bounds__(64) void diag_bf16_prep(const float* __restrict__ m
                                                      const float* __restrict__ lss, int64_t ldlss,
                                                      int64_t K, int D, int DP,
                                                      const float* __restrict__ lpi,
-                                                     bf16x8* __restrict__ mu_op, float* __restrict__ kc) {
+                                                     bf16x8* __restrict__ mu_op, float* __restrict__ kc,
+                                                     unsigned* __restrict__ ljcount) {
   const int kb = blockIdx.x, lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  if (ljcount && kb == 0) ljcount[lane] = 0u;   // pass 1 counts the needed pairs into these
   const int64_t k = (int64_t)kb * 32 + c;
   const bool valid = k < K;
   const int NCF = DP / 8;
@@ -2156,18 +2167,25 @@ __device__ __forceinline__ float bf16_diag_ll(float c0, const float (&s)[NCH]) {
 // Pass 1: grid over 128-row tiles, 4 waves of 32 rows.  Each lane rounds its row's
 // x and x^2 to bf16 as it loads them; feature blocks of 32 components (and c0)
 // stream through an LDS double buffer.  Writes logZ and logZ2 per row.
+// With NEED each row's block maximum, rounded up to bf16, stays in LDS, and once
+// logZ2 is final the need words and the needed-pair count are written (as for the
+// isotropic contract).
 template <int DP>
 constexpr size_t bf16_lse_lds_bytes() {
-  return (size_t)2 * (DP / 8) * 64 * sizeof(bf16x8) + (size_t)2 * 32 * sizeof(float);
+  static_assert(bf16_lse_lds_base(DP) == (size_t)2 * (DP / 8) * 64 * sizeof(bf16x8) + (size_t)2 * 32 * sizeof(float),
+                "host sizing");
+  return bf16_lse_lds_base(DP);
 }
 
-template <int DP>
+template <int DP, bool NEED = false>
 __global__ __launch_bounds__(kThreads) void diag_bf16_lse(const float* __restrict__ X, int64_t ldx,
                                                           int64_t N, int D,
                                                           const bf16x8* __restrict__ mu_op,
                                                           const float* __restrict__ kc, int KB,
                                                           float* __restrict__ logZ,
-                                                          float* __restrict__ rowstat) {
+                                                          float* __restrict__ rowstat,
+                                                          unsigned* __restrict__ ljmask,
+                                                          unsigned* __restrict__ ljcount, int dense) {
   constexpr int NCF = DP / 8;                  // 16-feature chunks
   constexpr int NCH = bf16_chains(DP);
   constexpr int CPC = NCF / NCH;               // chunks per chain
@@ -2178,10 +2196,12 @@ __global__ __launch_bounds__(kThreads) void diag_bf16_lse(const float* __restric
   extern __shared__ __align__(16) unsigned char lds_raw[];
   bf16x8* mu_l = reinterpret_cast<bf16x8*>(lds_raw);                               // [2][BLK]
   float* kc_l = reinterpret_cast<float*>(lds_raw + 2 * BLK * sizeof(bf16x8));      // [2][32]
+  unsigned short* rmax_l = reinterpret_cast<unsigned short*>(lds_raw + bf16_lse_lds_bytes<DP>());   // [wave][KB][32]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, g = lane >> 5;
-  const int64_t row = ((int64_t)blockIdx.x * kWaves + wave) * 32 + c;
+  const int64_t tile = (int64_t)blockIdx.x * kWaves + wave;
+  const int64_t row = tile * 32 + c;
   const bool valid = row < N;
 
   bf16x8 st[LPT];
@@ -2240,6 +2260,7 @@ __global__ __launch_bounds__(kThreads) void diag_bf16_lse(const float* __restric
       ll[i] = bf16_diag_ll<NCH>(kp[acc_row(i, g)], s);
       bm = fmaxf(bm, ll[i]);
     }
+    if constexpr (NEED) rmax_l[(wave * KB + kb) * 32 + c] = bf16_bits_up(lj_row_max(bm));   // both halves: same value
     const float mn = fmaxf(mx, bm);
     const float ms = (mn == -INFINITY) ? 0.0f : mn;
     float a = sm * fast_exp2(mx - ms);
@@ -2259,6 +2280,12 @@ __global__ __launch_bounds__(kThreads) void diag_bf16_lse(const float* __restric
     rowstat[row] = lz2;
     if (logZ) logZ[row] = lz2 * (float)kLn2;
   }
+  if constexpr (NEED) {
+    const unsigned short* rm = rmax_l + wave * KB * 32 + c;
+    if (g == 0)
+      need_put_masks([&](int kb) { return bf16_bits_to_float(rm[kb * 32]); }, ljmask + tile * KB,
+                     ljcount + (tile & 63), KB, c, (double)lz2, valid, dense != 0);
+  }
 }
 
 // Pass 2: grid over (row slab x group of CB component blocks); 8 waves = CB blocks x
@@ -2277,7 +2304,8 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                      const bf16x8* __restrict__ mu_op, const float* __restrict__ kc, int KB, int KP,
                      const float* __restrict__ rowstat, int nslab, int64_t rows_per_slab,
                      float* __restrict__ part_mu, float* __restrict__ part_sq,
-                     float* __restrict__ part_nk, int dense) {
+                     float* __restrict__ part_nk, int dense, const unsigned* __restrict__ needcount,
+                     int64_t dense_min) {
   constexpr int F = 2 * DP;                    // features per row
   constexpr int NCF = F / 16;                  // 16-feature chunks
   constexpr int NCH = bf16_chains(DP);
@@ -2298,6 +2326,10 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   static_assert(kAccWaves % (CB * NH) == 0 && NCH % NH == 0 &&
                     (NH == 1 || CPW == 1) && FW % 32 == 0 && DP % 32 == 0,
                 "even split");
+
+  // With need masks and fewer than dense_min needed pairs diag_bf16_gather runs instead
+  // (uniform exit).
+  if (needcount && need_total(needcount) < dense_min) return;
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   __bf16* xr = reinterpret_cast<__bf16*>(lds_raw);                        // [2][TR][XR]
@@ -2514,23 +2546,236 @@ void diag_bf16_accum(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   }
 }
 
+// Pass 2 of the bf16 contract up to D = 128 where few pairs are needed (pass 1's
+// needed-pair count below dense_min; diag_bf16_accum runs otherwise): one wave per
+// (row slab, component block), 4 waves of one block on consecutive slabs per
+// workgroup, the block's feature operands in LDS.  Each wave queues the rows whose
+// need bit is set and per 32 queued rows:
+//   - loads them (buffer resource over the slab), forms bf16(x^2) and bf16(x) in the
+//     A-operand layout (lane = row) and writes them row-major ([x^2 | x]) to its LDS
+//     tile;
+//   - S in pass 1's two chains (x^2, then x) and order, the log-joint as
+//     (c0 + s_x2) + s_x, so a cleared pair would give r = 0 exactly;
+//   - r = 2^(ll2 - logZ2), Nk on the VALU, bf16(r)^T [x^2 | x] on the matrix cores.
+// slab counts the partials of diag_bf16_accum's split, so either kernel fills the
+// same partial slots.
+__host__ __device__ constexpr size_t bf16_gather_lds_bytes(int DP) {
+  return (size_t)(DP / 8) * 64 * sizeof(bf16x8)                    // the block's feature operands
+         + (size_t)kGatherWaves * 32 * bf16_xr_stride(DP) * 2       // [x^2 | x] tile per wave
+         + (size_t)kGatherWaves * 32 * sizeof(float)                // logZ2 per wave
+         + (size_t)kGatherWaves * 64 * sizeof(int);                 // row queue per wave
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kGatherWaves, 64 * kGatherWaves),
+                          amdgpu_waves_per_eu(gather_waves_per_simd(DP), gather_waves_per_simd(DP))))
+void diag_bf16_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
+                      const bf16x8* __restrict__ mu_op, const float* __restrict__ kc, int KB, int KP,
+                      const float* __restrict__ rowstat, const unsigned* __restrict__ need,
+                      const unsigned* __restrict__ needcount, int64_t dense_min, int nslab,
+                      int64_t rows_per_slab, float* __restrict__ part_mu, float* __restrict__ part_sq,
+                      float* __restrict__ part_nk, int dense) {
+  constexpr int NQ = DP / 16;        // 16-dimension chunks (per feature)
+  constexpr int NCF = DP / 8;        // 16-feature chunks
+  constexpr int NJ = DP / 32;        // 32-column tiles per feature
+  constexpr int RS = bf16_xr_stride(DP);
+  constexpr int BLK = NCF * 64;      // bf16x8 per component block
+  static_assert(DP <= 128 && bf16_chains(DP) == 2, "two chains: x^2, then x");
+  if (need_total(needcount) >= dense_min) return;   // diag_bf16_accum runs instead (uniform exit)
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  unsigned char* lp = lds_raw;
+  bf16x8* mu_l = reinterpret_cast<bf16x8*>(lp);     lp += (size_t)BLK * sizeof(bf16x8);
+  __bf16* xt_all = reinterpret_cast<__bf16*>(lp);   lp += (size_t)kGatherWaves * 32 * RS * 2;
+  float* rs_all = reinterpret_cast<float*>(lp);     lp += (size_t)kGatherWaves * 32 * sizeof(float);
+  int* q_all = reinterpret_cast<int*>(lp);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  int sg, kb;
+  if (!gather_item(blockIdx.x, gather_groups(nslab), KB, sg, kb)) return;   // uniform over the workgroup
+  for (int idx = tid; idx < BLK; idx += 64 * kGatherWaves) mu_l[idx] = mu_op[(int64_t)kb * BLK + idx];
+  __syncthreads();
+  const int slab = sg * kGatherWaves + wave;
+  if (slab >= nslab) return;   // no barrier follows
+
+  __bf16* xt = xt_all + wave * 32 * RS;
+  float* rs_l = rs_all + wave * 32;
+  int* q_l = q_all + wave * 64;
+  const float c0 = kc[(int64_t)kb * 32 + c];
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int64_t t_begin = r_begin / 32, t_end = r_end > r_begin ? cdiv(r_end, 32) : t_begin;
+
+  auto words = [&](int64_t tb) -> unsigned {
+    const int64_t t = tb + lane;
+    return t < t_end ? need[t * KB + kb] : 0u;
+  };
+  int64_t tb = t_begin;
+  unsigned mword = words(tb), mnext = words(tb + 64);
+  int jn = 0;
+  int qh = 0, qt = 0;
+  auto take = [&](int& e) -> int {
+    queue_fill<(DP > 32)>(words, tb, t_begin, t_end, mword, mnext, jn, qt, qh, lane, c, g, q_l);
+    const int cnt = qt - qh < 32 ? qt - qh : 32;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    e = c < cnt ? q_l[(qh + c) & 63] : -1;
+    qh += cnt;
+    return cnt;
+  };
+
+  f32x4 raw[2 * NQ];
+  float rst;
+  const int64_t nrows = r_end > r_begin ? r_end - r_begin : 0;
+  const bool xbuf = slab_fits(nrows, ldx);
+  const bool xfull = xbuf && D == DP;
+  const buf_rsrc xres = slab_rsrc(X, ldx, r_begin, xbuf ? r_begin + nrows : r_begin);
+  const buf_rsrc rres = make_rsrc(rowstat + r_begin, (uint32_t)(nrows * sizeof(float)));
+  auto issue = [&](int e) __attribute__((always_inline)) {
+    const bool ok = e >= 0;
+    if (xfull) {
+      const int off = buf_off(ok ? (int)((int64_t)e * ldx * (int64_t)sizeof(float)) + 32 * g : kBufOob);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        raw[2 * q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 64 * q, 0));
+        raw[2 * q + 1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 64 * q + 16, 0));
+      }
+    } else if (xbuf) {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        raw[2 * q] = slab_row4(xres, ldx, e, 16 * q + 8 * g, D, ok);
+        raw[2 * q + 1] = slab_row4(xres, ldx, e, 16 * q + 8 * g + 4, D, ok);
+      }
+    } else {
+      const int64_t row = r_begin + (ok ? e : 0);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        raw[2 * q] = load_row4(X, ldx, row, 16 * q + 8 * g, D, ok);
+        raw[2 * q + 1] = load_row4(X, ldx, row, 16 * q + 8 * g + 4, D, ok);
+      }
+    }
+    const float v = buf_load_f32(rres, buf_off(ok ? e * (int)sizeof(float) : kBufOob));
+    rst = ok ? v : INFINITY;   // a row past the queue: logZ2 = +inf, r = 0
+  };
+
+  f32x16 acc[2][NJ];   // [x^2 | x] columns
+#pragma unroll
+  for (int f = 0; f < 2; ++f)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[f][j] = zero16();
+  float nk = 0.0f;
+
+  int e;
+  int cnt = take(e);
+  if (cnt > 0) issue(e);
+  while (cnt > 0) {
+    bf16x8 x2[NQ], x1[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      x2[q] = to_bf16x8(raw[2 * q] * raw[2 * q], raw[2 * q + 1] * raw[2 * q + 1]);
+      x1[q] = to_bf16x8(raw[2 * q], raw[2 * q + 1]);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the previous tile's LDS reads are done
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      *reinterpret_cast<bf16x8*>(xt + c * RS + 16 * q + 8 * g) = x2[q];
+      *reinterpret_cast<bf16x8*>(xt + c * RS + DP + 16 * q + 8 * g) = x1[q];
+    }
+    if (g == 0) rs_l[c] = rst;
+    int en;
+    const int cnt_next = take(en);
+    if (cnt_next > 0) issue(en);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+    // Chains of S = F W^T: lane = component c, register i = row acc_row(i, g).
+    f32x16 s0 = zero16(), s1 = zero16();
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      s0 = mfma_bf16(x2[q], mu_l[q * 64 + lane], s0);
+      s1 = mfma_bf16(x1[q], mu_l[(NQ + q) * 64 + lane], s1);
+    }
+    float r[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float sv[2] = {s0[i], s1[i]};
+      const float rv = fast_exp2(bf16_diag_ll<2>(c0, sv) - rs_l[acc_row(i, g)]);
+      nk += rv;
+      r[i] = rv;
+    }
+    bf16x8 a[2];
+    acc_to_row_operands(r, a);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      // A step whose 16 rows of bf16(r) are all zero adds nothing.
+      if (dense || any_nonzero(a[p])) {
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+            acc[f][j] = mfma_bf16(a[p], lds_rows_operand(xt, RS, 16 * p, f * DP + 32 * j, lane), acc[f][j]);
+      }
+    }
+    e = en;
+    cnt = cnt_next;
+  }
+
+  nk += __shfl_xor(nk, 32);
+  const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      part_sq[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[0][j][i];
+      part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[1][j][i];
+    }
+  }
+  if (g == 0) part_nk[kbase + c] = nk;
+}
+
 template <int DP>
 hipError_t launch_bf16(const DiagPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
                        float* logZ, bool run1, bool run2, bool dense, hipStream_t stream) {
   const bf16x8* mu_op = reinterpret_cast<const bf16x8*>(ws + pl.off_musw);
   const float* kc = reinterpret_cast<const float*>(ws + pl.off_kclin);
   float* rowstat = reinterpret_cast<float*>(ws + pl.off_rowstat);
+  unsigned* ljmask = reinterpret_cast<unsigned*>(ws + pl.off_ljmask);
+  unsigned* ljcount = reinterpret_cast<unsigned*>(ws + pl.off_ljcount);
   if (run1) {
-    constexpr size_t lds1 = bf16_lse_lds_bytes<DP>();
+    auto kern = pl.bfneed ? &diag_bf16_lse<DP, (DP <= 128)> : &diag_bf16_lse<DP>;
+    const size_t lds1 = bf16_lse_lds_bytes<DP>() + (pl.bfneed ? (size_t)kWaves * 32 * pl.KB * 2 : 0);
     if (lds1 > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_bf16_lse<DP>),
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
       if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(diag_bf16_lse<DP>, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
-                       stream, X, ldx, pl.N, (int)pl.D, mu_op, kc, pl.KB, logZ, rowstat);
+    hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(pl.N, 32 * kWaves)), dim3(kThreads), lds1,
+                       stream, X, ldx, pl.N, (int)pl.D, mu_op, kc, pl.KB, logZ, rowstat, ljmask, ljcount,
+                       dense ? 1 : 0);
   }
   if (!run2) return hipGetLastError();
+  // With need masks: the gathering pass (one slab per partial of the dense split) when
+  // fewer than 3/4 of the (row, block) pairs are needed, else diag_bf16_accum; both are
+  // launched and the needed-pair count selects one on the device.
+  const int64_t dense_min = cdiv(cdiv(pl.N, 32) * 32 * (int64_t)pl.KB * 3, 4);
+  if (pl.bfneed) {
+    if constexpr (DP <= 128) {
+      constexpr size_t ldsg = bf16_gather_lds_bytes(DP);
+      static_assert(ldsg <= kMaxLds, "gathering tiles fit LDS");
+      if (ldsg > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_bf16_gather<DP>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)ldsg);
+        if (e != hipSuccess) return e;
+      }
+      hipLaunchKernelGGL(diag_bf16_gather<DP>, dim3((unsigned)gather_grid(pl.npart, pl.KB)),
+                         dim3(64 * kGatherWaves), ldsg, stream, X, ldx, pl.N, (int)pl.D, mu_op, kc, pl.KB, pl.KP,
+                         rowstat, ljmask, ljcount, dense_min, pl.npart, (int64_t)round_up(cdiv(pl.N, pl.npart), 32),
+                         reinterpret_cast<float*>(ws + pl.off_part_mu), reinterpret_cast<float*>(ws + pl.off_part_sq),
+                         reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
+    }
+  }
   auto launch = [&](auto cb_tag) -> hipError_t {
     constexpr int CB = decltype(cb_tag)::value;
     if constexpr (CB * bf16_parts(DP) > kAccWaves) {
@@ -2550,7 +2795,8 @@ hipError_t launch_bf16(const DiagPlan& pl, const float* X, int64_t ldx, unsigned
                            pl.KP, rowstat, pl.nslab, pl.rows_per_slab,
                            reinterpret_cast<float*>(ws + pl.off_part_mu),
                            reinterpret_cast<float*>(ws + pl.off_part_sq),
-                           reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0);
+                           reinterpret_cast<float*>(ws + pl.off_part_nk), dense ? 1 : 0,
+                           pl.bfneed ? ljcount : nullptr, dense_min);
         return hipGetLastError();
       }
     }
@@ -2984,7 +3230,8 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   if (run1 && bf16)
     hipLaunchKernelGGL(diag_bf16_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
                        (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_musw),
-                       reinterpret_cast<float*>(ws + pl.off_kclin));
+                       reinterpret_cast<float*>(ws + pl.off_kclin),
+                       pl.bfneed ? reinterpret_cast<unsigned*>(ws + pl.off_ljcount) : nullptr);
   else if (run1)
     hipLaunchKernelGGL(diag_x6_prep, dim3(pl.KB), dim3(64), 0, stream, mu, ldmu, log_sigma_sq, ldlss, K,
                        (int)D, pl.DP, log_pi, reinterpret_cast<bf16x8*>(ws + pl.off_mu3),

@@ -1017,14 +1017,6 @@ __device__ __forceinline__ unsigned lj_pair_total(const unsigned* __restrict__ c
   return __builtin_amdgcn_readfirstlane(v);
 }
 
-// The same total in 64 bits (needed rows of the default plan can pass 2^32).
-__device__ __forceinline__ int64_t need_total(const unsigned* __restrict__ count) {
-  uint64_t v = count[threadIdx.x & 63];
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return (int64_t)__builtin_amdgcn_readfirstlane((unsigned)(v & 0xffffffffu)) |
-         ((int64_t)__builtin_amdgcn_readfirstlane((unsigned)(v >> 32)) << 32);
-}
 
 // ---------------------------------------------------------------------------
 // Pass 2 of the default plan (D <= 128): the log-joint is recomputed only for the
