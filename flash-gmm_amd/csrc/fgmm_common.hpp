@@ -687,6 +687,12 @@ constexpr size_t kMaxLjBytes = (size_t)16 << 30;
 __host__ __device__ constexpr bool wants_stored_lj(unsigned flags) {
   return (flags & FGMM_FLAG_STORE_LOGJOINT) != 0 && (flags & FGMM_FLAG_RECOMPUTE) == 0;
 }
+// The device-selected stored branch (FGMM_FLAG_STORE_LOGJOINT_AUTO), unless an
+// explicit plan flag takes precedence.
+__host__ __device__ constexpr bool wants_auto_lj(unsigned flags) {
+  return (flags & FGMM_FLAG_STORE_LOGJOINT_AUTO) != 0 &&
+         (flags & (FGMM_FLAG_STORE_LOGJOINT | FGMM_FLAG_RECOMPUTE | FGMM_FLAG_BF16)) == 0;
+}
 
 // Largest row stride (floats) of X for the buffer-loaded streaming passes: a
 // tile's byte offsets (256 rows x stride x 4) must stay below 2^31.

@@ -133,6 +133,9 @@ struct IsoPlan {
   int64_t rows_per_slab;
   bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16)
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it (FGMM_FLAG_STORE_LOGJOINT)
+  bool autolj;  // the default plan with a stored-log-joint branch that a row-sample probe
+                // selects on the device (FGMM_FLAG_STORE_LOGJOINT_AUTO, D <= 128)
+  int nprobe;   // sampled 32-row tiles of that probe
   int lj_nh;    // column parts per component block in that pass 2 (1 or 2)
   bool need;    // default plan: pass 1 leaves need masks, pass 2 gathers the needed rows
   bool ctile;   // default plan above D = 128: component-tiled pass 1, dimension-range pass 2
@@ -142,7 +145,7 @@ struct IsoPlan {
   bool bfneed;  // bf16 contract up to D = 128: need masks from pass 1, iso_bf16_gather in pass 2
                 // (or iso_bf16_accum where most pairs are needed)
   size_t off_musw, off_mu3, off_kcblk, off_kclin, off_kcgat, off_rowstat, off_part_mu, off_part_nk,
-      off_part_sig, off_lj, off_ljmax, off_ljmask, off_ljcount, total;
+      off_part_sig, off_lj, off_ljmax, off_ljmask, off_ljcount, off_xsplit, off_zpair, off_probe, total;
 };
 
 // Pass 1 with need masks keeps a bf16 bound of each row's block maximum in LDS,
@@ -158,6 +161,9 @@ __host__ __device__ constexpr bool lse_in_regs(int DP) { return DP <= 128 || DP 
 __host__ __device__ constexpr int lse_waves_per_simd(int DP) { return DP <= 128 ? 2 : 1; }
 // The pipelined pass 1 up to D = 128 is one 8-wave workgroup per compute unit
 // (two waves per SIMD) with a third buffer of block constants.
+// The pipelined pass 1 of the stored plan also passes each block's log-joint tile
+// through LDS (one 32 x 36-float tile per wave), so that its stores are whole lines.
+constexpr size_t kPipeStoreLds = (size_t)8 * 32 * 36 * sizeof(float);
 __host__ __device__ constexpr int need_exact_cap(int DP) {
   return DP <= 128 ? (int)((kMaxLds - lse_lds_base(DP) - 32 * 16 - 16) / (8 * 32 * 2))
                    : (int)((kMaxLds / (lse_waves_per_simd(DP) == 2 ? 2 : 1) - lse_lds_base(DP)) / (kWaves * 32 * 2));
@@ -178,6 +184,35 @@ __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB);
 __host__ __device__ constexpr size_t bf16_lse_lds_base(int DP) {
   return (size_t)2 * (DP / 16) * 64 * 16 + (size_t)2 * 32 * 16;   // mu blocks (bf16x8) and constants (f32x4)
 }
+constexpr int kLjtWavesPlan = 8;   // component blocks per stored pass-2 workgroup up to D = 128 (iso_accum_ljt)
+// The stored-log-joint probe (FGMM_FLAG_STORE_LOGJOINT_AUTO): up to kProbeTiles
+// 32-row tiles spread over the rows, one count of needed (row, block) pairs per
+// tile; at least half of the sampled pairs selects the stored branch.  Up to
+// kProbeMaxKB blocks (the probe keeps a tile's block maxima in LDS).
+constexpr int kProbeTiles = 64;
+constexpr int kProbeMaxKB = 512;
+__host__ __device__ constexpr size_t probe_bytes() { return (size_t)kProbeTiles * sizeof(unsigned); }
+// What a kernel needs to evaluate the probe's choice (count == nullptr: no probe).
+struct ProbeSel {
+  const unsigned* count;
+  int n;
+  int64_t min_pairs;
+};
+// The stored branch is selected (uniform; false without a probe).
+__device__ __forceinline__ bool probe_selects(const ProbeSel& p) {
+  if (p.count == nullptr) return false;
+  const int lane = threadIdx.x & 63;
+  unsigned v = lane < p.n ? p.count[lane] : 0u;
+  uint64_t t = v;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o);
+  const uint64_t tot = (uint64_t)__builtin_amdgcn_readfirstlane((unsigned)t) |
+                       ((uint64_t)__builtin_amdgcn_readfirstlane((unsigned)(t >> 32)) << 32);
+  return (int64_t)tot >= p.min_pairs;
+}
+__host__ __device__ constexpr int gather_rs(int DP) { return DP + 16; }   // bf16 row stride of the X tiles
+// The stored plan's bf16 X tiles (hi, lo; 32 rows at that stride) up to D = 128.
+__host__ __device__ constexpr size_t ljt_xsplit_bytes(int DP) { return (size_t)2 * 32 * gather_rs(DP) * 2; }
 // Above D = 256 the bf16 contract stores the log-joint (defined with its kernels).
 constexpr int kBwCB = 8;     // component blocks per wide bf16 pass-2 workgroup (one per wave)
 constexpr int kBwDR = 256;   // dimensions per wide bf16 pass-2 workgroup
@@ -188,7 +223,8 @@ __host__ inline size_t bw_lj_bytes(int64_t N, int KP) {
 __host__ __device__ constexpr int bf16_halves(int DP);
 __host__ inline int bf16_blocks_per_group(int DP, int KB);
 
-IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool bf16 = false) {
+IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool bf16 = false,
+                  bool auto_lj = false) {
   IsoPlan p{};
   p.N = N; p.K = K; p.D = D;
   p.DP = iso_padded_dim(D);
@@ -197,9 +233,14 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
   p.bf16 = bf16;
   p.lj = !bf16 && use_stored_lj(N, p.DP, p.KB, allow_lj);
   p.need = !bf16 && !p.lj;
+  p.autolj = p.need && auto_lj && p.DP <= 128 && N > 0 && p.KB > 0 && p.KB <= kProbeMaxKB &&
+             (size_t)round_up(cdiv(N, 32), 8) * (size_t)p.KB * kLjTile * sizeof(float) <= kMaxLjBytes;
+  p.nprobe = p.autolj ? (int)std::min<int64_t>(kProbeTiles, cdiv(N, 32)) : 0;
   p.ctile = p.need && p.DP > 128;
-  p.rexact = p.need && p.KB <= ((p.ctile && !lse_in_regs(p.DP)) ? ctile_need_exact_cap(ctile_blocks(p.DP))
-                                                                 : need_exact_cap(p.DP));
+  p.rexact = (p.need || (p.lj && p.DP <= 128)) &&
+             p.KB <= ((p.ctile && !lse_in_regs(p.DP)) ? ctile_need_exact_cap(ctile_blocks(p.DP))
+                      : (p.lj || p.autolj) ? need_exact_cap(p.DP) - (int)(kPipeStoreLds / (8 * 32 * 2))
+                                           : need_exact_cap(p.DP));
   p.ndr = p.ctile ? (int)cdiv(p.DP, kDrange) : 1;
   p.bfw = bf16 && iso_bf16_wide(p.DP);
   if (p.bfw) {
@@ -209,6 +250,10 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
   } else if (bf16) {
     p.cpg = bf16_blocks_per_group(p.DP, p.KB);
     p.rgroups = kAccWaves / (p.cpg * bf16_halves(p.DP));
+  } else if (p.lj && p.DP <= 128) {
+    p.cpg = kLjtWavesPlan;   // iso_accum_ljt: one wave per block, 8 blocks per workgroup
+    p.lj_nh = 1;
+    p.rgroups = 1;
   } else if (p.lj) {
     // 8 component blocks per workgroup, or 4 for K <= 224 and for D > 192; with 4
     // blocks above D = 128 two waves share a block (one half of the columns each):
@@ -249,6 +294,7 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
     const int64_t max_slabs = cdiv(N, tile_rows);
     if (want > max_slabs) want = max_slabs;
     p.rows_per_slab = round_up(cdiv(N, want), tile_rows);
+    if (p.lj && p.DP <= 128) p.rows_per_slab = cap_slab_rows(p.rows_per_slab, sizeof(double2));
     p.nslab = (int)cdiv(N, p.rows_per_slab);
   } else {
     p.rows_per_slab = tile_rows;
@@ -273,12 +319,19 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
   // One log-joint tile per pass-1 wave (the grid's 32-row tiles, rounded up to 4),
   // with its per-row block maxima and need mask; the default plan keeps the masks only.
   // (The default plan's pass 1 up to D = 128 runs 8 tiles per workgroup.)
-  const size_t ntile = (p.lj || p.need || p.bfneed) ? (size_t)round_up(cdiv(N, 32), p.need ? 8 : 4) * p.KB : 0;
+  const bool pipe1 = (p.need || p.lj) && p.DP <= 128;   // pass 1 is iso_lse_pipe (8 tiles per workgroup)
+  const size_t ntile = (p.lj || p.need || p.bfneed) ? (size_t)round_up(cdiv(N, 32), pipe1 ? 8 : 4) * p.KB : 0;
   p.off_lj = off;
-  off = align256(off + (p.bfw ? bw_lj_bytes(N, p.KP) : p.lj ? ntile * kLjTile * sizeof(float) : 0));
-  p.off_ljmax = off;  off = align256(off + (p.lj ? ntile * 32 * sizeof(float) : 0));
+  off = align256(off + (p.bfw ? bw_lj_bytes(N, p.KP) : (p.lj || p.autolj) ? ntile * kLjTile * sizeof(float) : 0));
+  p.off_ljmax = off;  off = align256(off + (p.lj && !pipe1 ? ntile * 32 * sizeof(float) : 0));
   p.off_ljmask = off; off = align256(off + ntile * sizeof(unsigned));
   p.off_ljcount = off; off = align256(off + ((p.lj || p.need || p.bfneed) ? 64 * sizeof(unsigned) : 0));
+  // The stored plan up to D = 128: each pass-1 tile's bf16 X parts and logZ2 pairs.
+  const size_t ptiles = ((p.lj || p.autolj) && pipe1) ? (size_t)round_up(cdiv(N, 32), 8) : 0;
+  p.off_xsplit = off; off = align256(off + ptiles * ljt_xsplit_bytes(p.DP));
+  p.off_zpair = off;  off = align256(off + ptiles * 32 * sizeof(float2));
+  // The probe: sampled rows' block maxima, its counters and the selector word.
+  p.off_probe = off;  off = align256(off + (p.autolj ? probe_bytes() : 0));
   p.total = off;
   return p;
 }
@@ -600,7 +653,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kPipeThreads, kPipeThreads
 void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                   const bf16x8* __restrict__ mu3, const double2* __restrict__ kc_blk, int KB,
                   float* __restrict__ logZ, double2* __restrict__ rowstat, unsigned* __restrict__ ljmask,
-                  unsigned* __restrict__ ljcount, int dense) {
+                  unsigned* __restrict__ ljcount, int dense, float* __restrict__ lj,
+                  ProbeSel probe, __bf16* __restrict__ xsplit, float2* __restrict__ zpair) {
   static_assert(DP <= 128, "pipelined pass 1 keeps all of a row's splits in registers");
   constexpr int NQ = DP / 16;
   constexpr int BLK = NQ * 4 * 64;        // bf16x8 per 32-component block
@@ -611,6 +665,9 @@ void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   double2* kc_l = reinterpret_cast<double2*>(lds_raw + 2 * BLK * sizeof(bf16x8));   // [3][32]
   unsigned* simd_l = reinterpret_cast<unsigned*>(kc_l + 3 * 32);                     // [4]
   unsigned short* rmax_l = reinterpret_cast<unsigned short*>(lds_raw + lse_pipe_lds_bytes<DP>());
+  // Stored plan: the wave's log-joint tile on its way to memory (after the bounds).
+  float* tr_l = reinterpret_cast<float*>(lds_raw + lse_pipe_lds_bytes<DP>() +
+                                         (REXACT ? (size_t)kPipeWaves * 32 * KB * 2 : 0));
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -618,6 +675,9 @@ void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   const int64_t tile = (int64_t)blockIdx.x * kPipeWaves + wave;
   const int64_t row = tile * 32 + c;
   const bool valid = row < N;
+  // Whether this call stores the log-joint: never without lj, always without a
+  // probe, else as the probe's counts (written before this kernel) say.
+  const bool store = lj != nullptr && (probe.count == nullptr || probe_selects(probe));
 
   // Block kb's operands into mu buffer kb & 1, its constants into kc buffer kb % 3.
   // A lane whose piece lies past the block (BLK not a multiple of the workgroup's
@@ -654,6 +714,16 @@ void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     }
     split3_bf16(lo, hi, xb[q]);
   }
+  if (store) {
+    // The tile's bf16 (hi, lo) parts of X for the stored plan's pass 2, row-major
+    // with its LDS row stride (ljt_xsplit_bytes per tile).
+    __bf16* xp = xsplit + tile * (2 * 32 * gather_rs(DP)) + c * gather_rs(DP) + 8 * g;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      *reinterpret_cast<bf16x8*>(xp + 16 * q) = xb[q][0];
+      *reinterpret_cast<bf16x8*>(xp + 32 * gather_rs(DP) + 16 * q) = xb[q][1];
+    }
+  }
   xsq += __shfl_xor(xsq, 32);
   const bf16x8 ones = x6c_ones(lane);
   lds_barrier();   // simd_l cleared
@@ -675,7 +745,9 @@ void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   float run_max = -INFINITY;
   unsigned pairs = 0;
   // Log-joint, block max and exp2 sum of block kb (its contraction in xm), as iso_lse
-  // forms them; returns the row's block maximum over both half-waves.
+  // forms them; returns the row's block maximum over both half-waves.  When storing,
+  // the lane's 16 values go to the block's tile (row-major, one 128-byte line per
+  // row).
   auto epilogue = [&](int kb, const f32x16& xm) {
     const double2* kp = kc_l + (kb % 3) * 32 + g * 16;
     // All 16 constant reads in flight before the first is used.
@@ -697,7 +769,26 @@ void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     for (int i = 0; i < 16; ++i) acc += fast_exp2((float)(ll[i] - ms));
     sm = acc;
     mx = mn;
-    return lj_row_max(bm);
+    const float R = lj_row_max(bm);
+    if (store) {
+      // Every row of every block, so that each epilogue issues exactly four store
+      // instructions (the block barrier's wait leaves these in flight); a row past N
+      // lands in the padding of the last tiles.  The tile is transposed through the
+      // wave's LDS tile (row stride 36 floats) so that each store writes 8 whole rows.
+      float* tl = tr_l + wave * 32 * 36;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 v = {(float)ll[4 * j], (float)ll[4 * j + 1], (float)ll[4 * j + 2], (float)ll[4 * j + 3]};
+        *reinterpret_cast<f32x4*>(tl + c * 36 + 8 * j + 4 * g) = v;
+      }
+      float* p = lj + (tile * KB + kb) * kLjTile;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int rr = 8 * q + (lane >> 3), cc = 4 * (lane & 7);
+        *reinterpret_cast<f32x4*>(p + rr * 32 + cc) = *reinterpret_cast<const f32x4*>(tl + rr * 36 + cc);
+      }
+    }
+    return R;
   };
   // The need bound of block kb: kept in LDS (REXACT) or tested against the running
   // max.  Both half-waves store the row's bound (the same value); the mask word goes
@@ -734,7 +825,16 @@ void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     }
     put_need(kb - 1, R);
     xm = xn;
-    dma_barrier();
+    // Block kb + 1's operands have landed once at most this iteration's stores (the
+    // log-joint's four, the mask word's one) are in flight: the stores of a block
+    // complete behind the next block's contraction.
+    if (store) {
+      if constexpr (REXACT) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else {
+      if constexpr (REXACT) dma_barrier();
+      else asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
   }
   put_need(KB - 1, epilogue(KB - 1, xm));
 
@@ -748,6 +848,12 @@ void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   if (valid && g == 0) {
     rowstat[row] = make_double2(xsq, lz2);
     if (logZ) logZ[row] = (float)(lz2 * kLn2);
+  }
+  if (store && g == 0) {
+    // logZ2 as the (hi, lo) float pair the stored plan's pass 2 subtracts.
+    const float zh = (float)lz2;
+    const float zl = (lz2 > -INFINITY && lz2 < INFINITY) ? (float)(lz2 - (double)zh) : 0.0f;
+    zpair[tile * 32 + c] = make_float2(zh, zl);
   }
   if constexpr (REXACT) {
     // Each lane reads back the bounds it wrote itself.
@@ -763,6 +869,105 @@ void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       if (pairs != 0) atomicAdd(ljcount + (tile & 63), pairs);
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// The probe of FGMM_FLAG_STORE_LOGJOINT_AUTO (up to D = 128): one workgroup per
+// sampled 32-row tile; its waves take the component blocks in turn and form each
+// row's block maximum R of the log-joint in LDS.  An estimate suffices here, so
+// the contraction keeps two of pass 1's seven steps per 16-dimension chunk (the
+// centring step and x1 mu1: an error of a fraction of a log2 unit against the
+// kLjNeedGap = 160 margin).  Then, per row, the blocks with R >= M - kLjNeedGap (M
+// the row's largest R) are counted: an estimate of the pairs pass 1 will mark as
+// needed, since logZ2 >= M.  The tile's count is written; no atomics: the kernels
+// that need the choice sum the counts themselves (probe_selects).
+// ---------------------------------------------------------------------------
+constexpr int kProbeWaves = 16;
+template <int DP>
+__global__ __launch_bounds__(64 * kProbeWaves) void iso_store_probe(const float* __restrict__ X, int64_t ldx,
+                                                                    int64_t N, int D,
+                                                                    const bf16x8* __restrict__ mu3,
+                                                                    const double2* __restrict__ kc_blk, int KB,
+                                                                    int ntile, unsigned* __restrict__ count) {
+  constexpr int NQ = DP / 16;
+  constexpr int BLK = NQ * 4 * 64;
+  __shared__ float rmax[kProbeMaxKB * 32];
+  __shared__ unsigned part[kProbeWaves];
+  const int s = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t tile = (int64_t)s * cdiv(N, 32) / ntile;
+  const int64_t row = tile * 32 + c;
+  const bool valid = row < N;
+
+  bf16x8 xh[NQ];
+  double xsq = 0.0;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int d0 = 16 * q + 8 * g;
+    const f32x4 lo = load_row4(X, ldx, row, d0, D, valid), hi = load_row4(X, ldx, row, d0 + 4, D, valid);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xsq = fma((double)lo[e], (double)lo[e], xsq);
+      xsq = fma((double)hi[e], (double)hi[e], xsq);
+    }
+    xh[q] = to_bf16x8(lo, hi);
+  }
+  xsq += __shfl_xor(xsq, 32);
+  const bf16x8 ones = x6c_ones(lane);
+  for (int kb = wave; kb < KB; kb += kProbeWaves) {
+    const bf16x8* mp = mu3 + (int64_t)kb * BLK + lane;
+    bf16x8 a0[NQ], a3[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      a0[q] = mp[(q * 4 + 0) * 64];
+      a3[q] = mp[(q * 4 + 3) * 64];
+    }
+    f32x16 acc[4] = {zero16(), zero16(), zero16(), zero16()};
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      acc[q & 3] = mfma_bf16(a3[q], ones, acc[q & 3]);
+      acc[q & 3] = mfma_bf16(a0[q], xh[q], acc[q & 3]);
+    }
+    const double2* kp = kc_blk + (int64_t)kb * 32 + g * 16;
+    double bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const double2 cb = kp[i];
+      const float xm = (acc[0][i] + acc[1][i]) + (acc[2][i] + acc[3][i]);
+      bm = fmax(bm, fma(-cb.y, fma(-2.0, (double)xm, xsq), cb.x));
+    }
+    const float R = lj_row_max(bm);
+    if (g == 0) rmax[kb * 32 + c] = R;
+  }
+  __syncthreads();
+  // Row c's maximum and needed blocks; the waves split the blocks again.
+  unsigned need = 0;
+  if (g == 0 && valid) {
+    float M = -INFINITY;
+    for (int kb = 0; kb < KB; ++kb) M = fmaxf(M, rmax[kb * 32 + c]);
+    for (int kb = wave; kb < KB; kb += kProbeWaves) need += (rmax[kb * 32 + c] - M >= -kLjNeedGap) ? 1u : 0u;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) need += __shfl_xor(need, o);
+  if (lane == 0) part[wave] = need;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned tot = 0;
+    for (int w = 0; w < kProbeWaves; ++w) tot += part[w];
+    count[s] = tot;
+  }
+}
+
+// The probe's threshold: half of the sampled (row, block) pairs.
+__host__ inline int64_t probe_min_pairs(int64_t N, int ntile, int KB) {
+  int64_t rows = 0;
+  for (int s = 0; s < ntile; ++s) {
+    const int64_t t = (int64_t)s * cdiv(N, 32) / ntile;
+    rows += std::min<int64_t>(32, N - t * 32);
+  }
+  return cdiv(rows * KB, 2);
 }
 
 // ---------------------------------------------------------------------------
@@ -1043,7 +1248,6 @@ __device__ __forceinline__ unsigned lj_pair_total(const unsigned* __restrict__ c
 // once and from that XCD's L2 after.
 // ---------------------------------------------------------------------------
 
-__host__ __device__ constexpr int gather_rs(int DP) { return DP + 16; }   // bf16 row stride of the X tiles
 
 __host__ __device__ constexpr size_t gather_lds_bytes(int DP) {
   return (size_t)(DP / 16) * 4 * 64 * 16                          // mu block (bf16x8 operands)
@@ -1068,13 +1272,15 @@ void iso_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int D
                       const double2* __restrict__ rowstat, const unsigned* __restrict__ need,
                       const unsigned* __restrict__ needcount, int64_t dense_min, int nslab,
                       int64_t rows_per_slab, float* __restrict__ part_mu, float* __restrict__ part_nk,
-                      float* __restrict__ part_sig, int dense) {
+                      float* __restrict__ part_sig, int dense, ProbeSel sel) {
   constexpr int NQ = DP / 16;
   constexpr int NJ = DP / 32;
   constexpr int RS = gather_rs(DP);
   constexpr int BLK = NQ * 4 * 64;   // bf16x8 per component block
   // With at least dense_min needed rows iso_accum_tiles runs instead (uniform exit).
   if (need_total(needcount) >= dense_min) return;
+  // The stored branch of FGMM_FLAG_STORE_LOGJOINT_AUTO runs instead when selected.
+  if (probe_selects(sel)) return;
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   unsigned char* lp = lds_raw;
@@ -1283,7 +1489,7 @@ void iso_accum_tiles(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                      const double2* __restrict__ rowstat, const unsigned* __restrict__ need,
                      const unsigned* __restrict__ needcount, int64_t dense_min, int nslab,
                      int64_t rows_per_slab, float* __restrict__ part_mu, float* __restrict__ part_nk,
-                     float* __restrict__ part_sig, int dense) {
+                     float* __restrict__ part_sig, int dense, ProbeSel sel) {
   constexpr int NQ = DP / 16;
   constexpr int NJ = DP / 32;
   constexpr int RS = gather_rs(DP);
@@ -1293,6 +1499,7 @@ void iso_accum_tiles(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   constexpr int LPT = 32 * V4 / NT;       // float4 per thread per tile
   static_assert((32 * V4) % NT == 0, "tile split");
   if (need_total(needcount) < dense_min) return;   // the gathering kernel runs (uniform exit)
+  if (probe_selects(sel)) return;   // the stored branch runs
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   __bf16* xs = reinterpret_cast<__bf16*>(lds_raw);                                   // [2][3][32][RS]
@@ -1485,7 +1692,7 @@ void iso_accum_tiles2(const float* __restrict__ X, int64_t ldx, int64_t N, int D
                       const double2* __restrict__ rowstat, const unsigned* __restrict__ need,
                       const unsigned* __restrict__ needcount, int64_t dense_min, int nslab,
                       int64_t rows_per_slab, float* __restrict__ part_mu, float* __restrict__ part_nk,
-                      float* __restrict__ part_sig, int dense) {
+                      float* __restrict__ part_sig, int dense, ProbeSel sel) {
   constexpr int NQ = DP / 16;
   constexpr int NQH = NQ / 2;              // chunks of this wave's chain
   constexpr int NJ = DP / 32;
@@ -1497,6 +1704,7 @@ void iso_accum_tiles2(const float* __restrict__ X, int64_t ldx, int64_t N, int D
   constexpr int LPT = (NV + NT - 1) / NT;  // float4 per thread per tile
   static_assert(NQ % 2 == 0 && kIsoChains == 2, "one chain per wave of a pair");
   if (need_total(needcount) < dense_min) return;   // the gathering kernel runs (uniform exit)
+  if (probe_selects(sel)) return;   // the stored branch runs
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   __bf16* xs = reinterpret_cast<__bf16*>(lds_raw);                                   // [3][3][32][RS]
@@ -2216,6 +2424,284 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 }
 
 // ---------------------------------------------------------------------------
+// Pass 2 from the stored log-joint up to D = 128.  Pass 1 (iso_lse_pipe storing)
+// leaves per 32-row tile the log-joint of every block, the bf16 (hi, lo) parts of
+// the tile's X rows (row-major at this kernel's LDS row stride) and the rows' logZ2
+// as (hi, lo) float pairs.  r^T X runs on the bf16 matrix cores in the split form of
+// the gathering pass: r and x each in two bf16 parts and, per 16-row step, the
+// products r2 x1, r1 x2 and r1 x1 added in that order.
+//
+// Grid over (row slab x group of 8 component blocks); wave w owns block 8 cg + w
+// and that block's partial of the slab.  The workgroups of a slab are dealt to one
+// XCD, so that the X parts come from HBM once and from that XCD's L2 for the other
+// groups.  Three LDS stages, each one tile's X parts, the 8 blocks' log-joint tiles
+// and the logZ2 pairs, all filled by buffer-to-LDS loads: at step t the workgroup
+// issues tile t + 2's, computes tile t and waits for tile t + 1's before the barrier.
+// A wave issues the same loads every step (log-joint rows whose need bit is clear
+// read as zeros and get r = 0, as do rows past the slab: no sum changes), so that
+// wait is a fixed count of its own outstanding loads, and no global load of the
+// loop is left for the compiler to wait on.  A wave skips a tile whose need word is
+// zero.  `sel` (when given) is the word pass 1 read: the kernel returns unless set.
+// ---------------------------------------------------------------------------
+constexpr int kLjtWaves = kLjtWavesPlan;
+constexpr int kLjtStages = 3;
+
+template <int DP>
+struct LjtShape {
+  static constexpr int XB = (int)ljt_xsplit_bytes(DP);     // a tile's X parts
+  static constexpr int XP = XB / 16;                        // their 16-byte pieces, a multiple of 64
+  static constexpr int XQ = (XP + 64 * kLjtWaves - 1) / (64 * kLjtWaves);
+  static constexpr int LJB = kLjtWaves * kLjTile * 4;       // the 8 blocks' log-joint tiles
+  static constexpr int OFF_X = LJB, OFF_Z = LJB + XB;
+  static constexpr int STAGE = LJB + XB + 32 * 8;
+  static constexpr size_t lds = (size_t)kLjtStages * STAGE;
+  // X loads of wave w per tile (whole waves of pieces: XP is a multiple of 64).
+  static constexpr int xloads(int w) {
+    int n = 0;
+    for (int q = 0; q < XQ; ++q) n += (q * 64 * kLjtWaves + w * 64 < XP) ? 1 : 0;
+    return n;
+  }
+};
+__host__ inline int64_t ljt_grid(int nslab, int ncg) { return (int64_t)8 * cdiv(nslab, 8) * ncg; }
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N <= 63, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// vm_wait for a wave-uniform count below 16.
+__device__ __forceinline__ void vm_wait_n(int n) {
+  switch (n) {
+    case 0: vm_wait<0>(); break;   case 1: vm_wait<1>(); break;   case 2: vm_wait<2>(); break;
+    case 3: vm_wait<3>(); break;   case 4: vm_wait<4>(); break;   case 5: vm_wait<5>(); break;
+    case 6: vm_wait<6>(); break;   case 7: vm_wait<7>(); break;   case 8: vm_wait<8>(); break;
+    case 9: vm_wait<9>(); break;   case 10: vm_wait<10>(); break; case 11: vm_wait<11>(); break;
+    case 12: vm_wait<12>(); break; case 13: vm_wait<13>(); break; case 14: vm_wait<14>(); break;
+    default: vm_wait<0>(); break;
+  }
+}
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kLjtWaves, 64 * kLjtWaves), amdgpu_waves_per_eu(2, 2)))
+void iso_accum_ljt(const float* __restrict__ lj, const __bf16* __restrict__ xsplit, const float2* __restrict__ zpair,
+                   int64_t N, const unsigned* __restrict__ ljmask, const unsigned* __restrict__ ljcount,
+                   int64_t sparse_max, ProbeSel sel, const double4* __restrict__ kc_lin,
+                   int KB, int KP, int nslab, int64_t rows_per_slab, int ncg, float* __restrict__ part_mu,
+                   float* __restrict__ part_nk, float* __restrict__ part_sig, int dense) {
+  static_assert(DP <= 128 && DP % 32 == 0, "one 32-row tile of X per stage");
+  using SH = LjtShape<DP>;
+  static_assert(SH::XP % 64 == 0, "whole waves of X pieces");
+  constexpr int NJ = DP / 32;
+  constexpr int RS = gather_rs(DP);
+  constexpr int NS = kLjtStages;
+  // iso_accum_sparse takes the call when pass 1 found the masks sparse; with a
+  // selector word, the recomputing kernels take it unless the word is set.
+  if (sparse_max >= 0 && need_total(ljcount) <= sparse_max) return;
+  if (sel.count != nullptr && !probe_selects(sel)) return;
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  // Workgroup -> (slab, component group): the ncg groups of slab s run on XCD s % 8.
+  const int xcd = blockIdx.x & 7, item = blockIdx.x >> 3;
+  const int slab = (item / ncg) * 8 + xcd, cg = item % ncg;
+  if (slab >= nslab) return;   // uniform over the workgroup
+  const int kb = cg * kLjtWaves + wave;
+  const bool active = kb < KB;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
+  const int64_t tile0 = r_begin >> 5;   // rows_per_slab is a multiple of 32
+
+  // C0_k and 1 / b_k, as iso_accum_lj forms them.
+  float c0 = 0.0f, ibk = 0.0f;
+  if (active) {
+    const double4 kc = kc_lin[(int64_t)kb * 32 + c];
+    const double c0d = fma(kc.y, kc.z, kc.x);
+    if (c0d > -INFINITY && c0d < INFINITY) {
+      c0 = (float)c0d;
+      ibk = (float)(1.0 / kc.y);
+    }
+  }
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
+  float nk = 0.0f, sig = 0.0f;
+
+  // The wave's need word of tile t (0 past the slab or the blocks): a scalar load.
+  auto mword = [&](int t) -> unsigned {
+    const bool ok = active && t < ntiles;
+    const unsigned v = ljmask[ok ? (tile0 + t) * KB + kb : 0];
+    return ok ? v : 0u;
+  };
+  // Tile t into stage S: the X parts (whole waves of pieces), the wave's log-joint
+  // tile (piece l of load q is row 8 q + l / 8; out of range where the row's bit is
+  // clear or past the slab) and, by wave 0, the rows' logZ2 pairs.
+  const int nx = SH::xloads(wave);
+  const int nloads = nx + 4 + (wave == 0 ? 1 : 0);
+  auto issue = [&](int t, auto stage_tag, unsigned m) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage_tag)::value;
+    unsigned char* st = lds_raw + (size_t)S * SH::STAGE;
+    const bool in = t < ntiles;
+    const int64_t tg = tile0 + t;
+    const DmaSrc xsrc = dma_src(in ? reinterpret_cast<const unsigned char*>(xsplit) + tg * SH::XB
+                                   : reinterpret_cast<const unsigned char*>(xsplit),
+                                in ? (uint32_t)SH::XB : 0u);
+#pragma unroll
+    for (int q = 0; q < SH::XQ; ++q) {
+      if (q * 64 * kLjtWaves + wave * 64 < SH::XP)
+        lds_dma16(xsrc, st + SH::OFF_X + (q * 64 * kLjtWaves + wave * 64) * 16,
+                  (q * 64 * kLjtWaves + tid) * 16, 0);
+    }
+    const DmaSrc lsrc = dma_src(m ? lj + (tg * KB + kb) * kLjTile : lj, m ? (uint32_t)(kLjTile * 4) : 0u);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = 8 * q + (lane >> 3);
+      lds_dma16(lsrc, st + wave * kLjTile * 4 + q * 1024, ((m >> row) & 1u) ? (q * 64 + lane) * 16 : kBufOob, 0);
+    }
+    if (wave == 0) {
+      const int nrow = in ? (int)(r_end - (r_begin + (int64_t)t * 32) < 32 ? r_end - (r_begin + (int64_t)t * 32) : 32) : 0;
+      const DmaSrc zsrc = dma_src(zpair + tg * 32 * (in ? 1 : 0), (uint32_t)(nrow * sizeof(float2)));
+      if (lane < 16) lds_dma16(zsrc, st + SH::OFF_Z, lane * 16, 0);
+    }
+  };
+  // Tile t in stage S (need word m, not 0): one straight-line block, its LDS reads
+  // issued ahead of their uses, half 1's reads and VALU work issued while half 0's
+  // matrix steps run.  (The stage base goes through a register, so that the reads
+  // keep small offsets.)
+  auto compute = [&](auto stage_tag, unsigned m) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage_tag)::value;
+    int sb = S * SH::STAGE;
+    asm volatile("" : "+s"(sb));
+    const unsigned char* st = lds_raw + sb;
+    const float* lt = reinterpret_cast<const float*>(st + wave * kLjTile * 4) + c;
+    const float2* zt = reinterpret_cast<const float2*>(st + SH::OFF_Z);
+    const __bf16* xt = reinterpret_cast<const __bf16*>(st + SH::OFF_X);
+    const unsigned mg = m >> (4 * g);
+    float lv[16];
+    float2 zv[16];
+    auto rows = [&](int p) __attribute__((always_inline)) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        lv[8 * p + e] = lt[acc_row(8 * p + e, g) * 32];
+        zv[8 * p + e] = zt[acc_row(8 * p + e, g)];
+      }
+    };
+    bf16x8 b1[2][NJ], b2[2][NJ];
+    auto bops = [&](int p) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        b1[p][j] = lds_rows_operand(xt, RS, 16 * p, 32 * j, lane);
+        b2[p][j] = lds_rows_operand(xt + 32 * RS, RS, 16 * p, 32 * j, lane);
+      }
+    };
+    bf16x8 a1[2], a2[2];
+    // Responsibilities of rows 16 p .. 16 p + 15 (registers 8 p .. 8 p + 7 of the
+    // accumulator layout), exponentiated on every lane and selected (no branch): a
+    // row not read has l = 0, whose power is discarded.
+    auto half = [&](int p) __attribute__((always_inline)) {
+      float r[8], res[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = 8 * p + e;
+        const float l = lv[i];
+        const float ex = fast_exp2((l - zv[i].x) - zv[i].y);
+        const float rv = ((mg >> (8 * (i >> 2) + (i & 3))) & 1u) ? ex : 0.0f;
+        r[e] = rv;
+        res[e] = rv - (float)(__bf16)rv;
+        nk += rv;
+        sig = fmaf(rv, c0 - l, sig);
+      }
+      a1[p] = acc_to_row_operand(r);
+      a2[p] = acc_to_row_operand(res);
+    };
+    auto steps = [&](int p) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        acc[j] = mfma_bf16(a2[p], b1[p][j], acc[j]);
+        acc[j] = mfma_bf16(a1[p], b2[p][j], acc[j]);
+        acc[j] = mfma_bf16(a1[p], b1[p][j], acc[j]);
+      }
+    };
+    // All of the tile's LDS reads first, then half 0's responsibilities; half 1's
+    // VALU work is interleaved with half 0's matrix steps (one step, then about an
+    // NJ-th of the work: the wave issues it while the matrix core runs the step).
+    rows(0);
+    bops(0);
+    rows(1);
+    bops(1);
+    half(0);
+    __builtin_amdgcn_sched_barrier(0);
+    steps(0);
+    half(1);
+#pragma unroll
+    for (int k = 0; k < 3 * NJ; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 24 / NJ, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    steps(1);
+  };
+
+  unsigned mk[NS];   // need words of the tiles in the stages
+  unsigned mnext = 0u;
+  // Step t, stage S = t mod 3: issue tile t + 2 (stage (S + 2) mod 3, free since the
+  // last barrier), compute tile t, wait for tile t + 1's stage (the loads issued
+  // after it are tile t + 2's), barrier.
+  auto step = [&](int t, auto stage_tag) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage_tag)::value;
+    constexpr int S2 = (S + 2) % NS;
+    mk[S2] = mnext;
+    issue(t + 2, std::integral_constant<int, S2>{}, mnext);
+    mnext = mword(t + 3);
+    if (mk[S] != 0u) compute(stage_tag, mk[S]);
+    vm_wait_n(nloads);
+    __syncthreads();
+  };
+
+  if (ntiles > 0) {
+    mk[0] = mword(0);
+    mk[1] = mword(1);
+    issue(0, std::integral_constant<int, 0>{}, mk[0]);
+    issue(1, std::integral_constant<int, 1>{}, mk[1]);
+    mnext = mword(2);
+    vm_wait_n(nloads);   // tile 0's stage
+    __syncthreads();
+  }
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  for (int t = 0; t < ntiles; t += NS) {
+    step(t, S0{});
+    if (t + 1 >= ntiles) break;
+    step(t + 1, S1{});
+    if (t + 2 >= ntiles) break;
+    step(t + 2, S2{});
+  }
+  vm_wait<0>();   // no buffer-to-LDS load outlives the workgroup
+
+  if (active) {
+    nk += __shfl_xor(nk, 32);
+    sig += __shfl_xor(sig, 32);
+    sig = ibk != 0.0f ? sig * ibk : 0.0f;
+    const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) part_mu[(kbase + acc_row(i, g)) * DP + 32 * j + c] = acc[j][i];
+    }
+    if (g == 0) {
+      part_nk[kbase + c] = nk;
+      part_sig[kbase + c] = sig;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Pass 2 from the sparse stored log-joint, for data whose need masks are sparse
 // (clustered data: most (row, block) pairs have no nonzero responsibility).  No
 // workgroup-wide staging: each wave owns one (row slab, row group, component
@@ -2257,7 +2743,7 @@ void iso_accum_sparse(const float* __restrict__ X, int64_t ldx, int64_t N, const
   // The batch's tiles with a nonzero mask, in order: (mask, tile offset in the batch).
   __shared__ uint2 work[kSparseWaves][BT];
 
-  if ((int64_t)lj_pair_total(ljcount) > sparse_max) return;
+  if (need_total(ljcount) > sparse_max) return;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 31, g = lane >> 5;
@@ -2576,17 +3062,25 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   float* pmu = reinterpret_cast<float*>(ws + pl.off_part_mu);
   float* pnk = reinterpret_cast<float*>(ws + pl.off_part_nk);
   float* psig = reinterpret_cast<float*>(ws + pl.off_part_sig);
-  float* lj = pl.lj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
-  float* ljmax = pl.lj ? reinterpret_cast<float*>(ws + pl.off_ljmax) : nullptr;
+  float* lj = (pl.lj || pl.autolj) ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
   unsigned* ljmask = reinterpret_cast<unsigned*>(ws + pl.off_ljmask);
   unsigned* ljcount = reinterpret_cast<unsigned*>(ws + pl.off_ljcount);
   if (run1) {
-    const int64_t nblk1 = cdiv(pl.N, 32 * kWaves);
     if constexpr (DP <= 128) {
       hipError_t e = hipSuccess;
-      if (pl.need) {
-        // The default plan: the software-pipelined pass 1.
-        const size_t lds1 = lse_pipe_lds_bytes<DP>() + (pl.rexact ? (size_t)kPipeWaves * 32 * pl.KB * 2 : 0);
+      if (pl.need || pl.lj) {
+        // The software-pipelined pass 1 (the stored plan's also writes the log-joint;
+        // with FGMM_FLAG_STORE_LOGJOINT_AUTO the probe's selector decides first).
+        unsigned* probe = pl.autolj ? reinterpret_cast<unsigned*>(ws + pl.off_probe) : nullptr;
+        if (pl.autolj)
+          hipLaunchKernelGGL((iso_store_probe<DP>), dim3((unsigned)pl.nprobe), dim3(64 * kProbeWaves), 0, stream, X, ldx, pl.N,
+                             (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3), kc_blk, pl.KB, pl.nprobe,
+                             probe);
+        const ProbeSel psel = probe ? ProbeSel{probe, pl.nprobe, probe_min_pairs(pl.N, pl.nprobe, pl.KB)}
+                                    : ProbeSel{nullptr, 0, 0};
+        const bool st = pl.lj || pl.autolj;
+        const size_t lds1 = lse_pipe_lds_bytes<DP>() + (pl.rexact ? (size_t)kPipeWaves * 32 * pl.KB * 2 : 0) +
+                            (st ? kPipeStoreLds : 0);
         auto kern = pl.rexact ? &iso_lse_pipe<DP, 1> : &iso_lse_pipe<DP, 0>;
         if (lds1 > 65536)
           e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -2594,18 +3088,8 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(pl.N, 32 * kPipeWaves)), dim3(kPipeThreads), lds1, stream,
                            X, ldx, pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3), kc_blk,
-                           pl.KB, logZ, rowstat, ljmask, ljcount, dense ? 1 : 0);
-      } else {
-        // The stored plan: iso_lse also writes the log-joint rows.
-        const size_t lds1 = lse_lds_bytes<DP>();
-        auto kern = &iso_lse<DP, kLjmStore>;
-        if (lds1 > 65536)
-          e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)lds1);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(kern, dim3((unsigned)nblk1), dim3(kThreads), lds1, stream, X, ldx, pl.N,
-                           (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3), kc_blk, pl.KB,
-                           logZ, rowstat, lj, ljmax, ljmask, ljcount, dense ? 1 : 0, 0);
+                           pl.KB, logZ, rowstat, ljmask, ljcount, dense ? 1 : 0, lj, psel,
+                           reinterpret_cast<__bf16*>(ws + pl.off_xsplit), reinterpret_cast<float2*>(ws + pl.off_zpair));
       }
     } else {
       return hipErrorInvalidValue;   // launch_ctile runs pass 1 above D = 128
@@ -2619,6 +3103,24 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
       // (measured at N=1M K=1024: at a quarter it takes half the tile kernel's time, with
       // every pair needed 1.1-1.25 times it).
       const int64_t dense_min = cdiv(cdiv(pl.N, 32) * 32 * (int64_t)pl.KB * 3, 4);
+      // FGMM_FLAG_STORE_LOGJOINT_AUTO: the stored branch (iso_accum_ljt over the same
+      // slabs and partials) is launched too; the probe's selector picks one side.
+      const ProbeSel sel = pl.autolj ? ProbeSel{reinterpret_cast<const unsigned*>(ws + pl.off_probe), pl.nprobe,
+                                                probe_min_pairs(pl.N, pl.nprobe, pl.KB)}
+                                     : ProbeSel{nullptr, 0, 0};
+      if (pl.autolj) {
+        constexpr size_t ldsj = LjtShape<DP>::lds;
+        static_assert(ldsj <= kMaxLds, "stored pass-2 stages exceed LDS");
+        hipError_t ej = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_ljt<DP>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)ldsj);
+        if (ej != hipSuccess) return ej;
+        const int ncg = (int)cdiv(pl.KB, kLjtWaves);
+        hipLaunchKernelGGL((iso_accum_ljt<DP>), dim3((unsigned)ljt_grid(pl.nslab, ncg)), dim3(64 * kLjtWaves), ldsj,
+                           stream, lj, reinterpret_cast<const __bf16*>(ws + pl.off_xsplit),
+                           reinterpret_cast<const float2*>(ws + pl.off_zpair), pl.N, ljmask, ljcount, (int64_t)-1,
+                           sel, kc_lin, pl.KB, pl.KP, pl.nslab, pl.rows_per_slab, ncg, pmu, pnk, psig,
+                           dense ? 1 : 0);
+      }
       constexpr size_t lds = gather_lds_bytes(DP);
       static_assert(lds <= kMaxLds, "gathering pass 2 exceeds LDS");
       hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_gather<DP>),
@@ -2629,7 +3131,7 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
                          reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
                          reinterpret_cast<const double4*>(ws + pl.off_kcgat), pl.KB, pl.KP, rowstat,
                          ljmask, ljcount, dense_min, pl.nslab, pl.rows_per_slab, pmu, pnk, psig,
-                         dense ? 1 : 0);
+                         dense ? 1 : 0, sel);
       // The tile pass: one wave per block up to D = 64, a pair of waves (one chain
       // each) at D = 96 and 128.
       auto tiles = [&](auto kern, size_t lds_t, int waves) -> hipError_t {
@@ -2639,7 +3141,7 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
         hipLaunchKernelGGL(kern, dim3((unsigned)(pl.nslab * cdiv(pl.KB, kTileBlocks))), dim3(64 * waves), lds_t,
                            stream, X, ldx, pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
                            reinterpret_cast<const double4*>(ws + pl.off_kcgat), pl.KB, pl.KP, rowstat, ljmask,
-                           ljcount, dense_min, pl.nslab, pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
+                           ljcount, dense_min, pl.nslab, pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0, sel);
         return hipGetLastError();
       };
       if constexpr (DP > 64) {
@@ -2652,21 +3154,35 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
     }
   }
   if (!pl.lj) return hipErrorInvalidValue;   // not a plan of this launcher
-  const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
-  // Sparse masks (on average at most 2 needed row pairs per tile and block) go to
-  // iso_accum_sparse where it applies (D a multiple of 32 up to 128); both kernels
-  // are launched and each returns unless the count selects it.
-  int64_t sparse_max = -1;
-  if constexpr (DP >= 64 && DP <= 128) {
-    if (pl.D == DP) {
-      sparse_max = 2 * cdiv(pl.N, 32) * pl.KB;
-      const int64_t nw = (int64_t)pl.nslab * pl.rgroups * pl.KB;
-      hipLaunchKernelGGL((iso_accum_sparse<DP>), dim3((unsigned)cdiv(nw, kSparseWaves)),
-                         dim3(64 * kSparseWaves), 0, stream, X, ldx, pl.N, lj, ljmask, ljcount,
-                         sparse_max, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rgroups,
-                         pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
+  if constexpr (DP <= 128) {
+    // Sparse masks (on average at most 3 needed rows per tile and block) go to
+    // iso_accum_sparse where it applies (D a multiple of 32, 64 to 128); both kernels
+    // are launched and each returns unless the needed-row count selects it.
+    int64_t sparse_max = -1;
+    if constexpr (DP >= 64) {
+      if (pl.D == DP) {
+        sparse_max = 3 * cdiv(pl.N, 32) * pl.KB;
+        const int64_t nw = (int64_t)pl.nslab * pl.rgroups * pl.KB;
+        hipLaunchKernelGGL((iso_accum_sparse<DP>), dim3((unsigned)cdiv(nw, kSparseWaves)),
+                           dim3(64 * kSparseWaves), 0, stream, X, ldx, pl.N, lj, ljmask, ljcount,
+                           sparse_max, kc_lin, pl.KB, pl.KP, rowstat, pl.nslab, pl.rgroups,
+                           pl.rows_per_slab, pmu, pnk, psig, dense ? 1 : 0);
+      }
     }
+    constexpr size_t lds = LjtShape<DP>::lds;
+    static_assert(lds <= kMaxLds, "stored pass-2 stages exceed LDS");
+    hipError_t el = hipFuncSetAttribute(reinterpret_cast<const void*>(&iso_accum_ljt<DP>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (el != hipSuccess) return el;
+    hipLaunchKernelGGL((iso_accum_ljt<DP>), dim3((unsigned)ljt_grid(pl.nslab, pl.ncg)), dim3(64 * kLjtWaves), lds,
+                       stream, lj, reinterpret_cast<const __bf16*>(ws + pl.off_xsplit),
+                       reinterpret_cast<const float2*>(ws + pl.off_zpair), pl.N, ljmask, ljcount, sparse_max,
+                       ProbeSel{nullptr, 0, 0}, kc_lin, pl.KB, pl.KP, pl.nslab, pl.rows_per_slab, pl.ncg, pmu, pnk,
+                       psig, dense ? 1 : 0);
+    return hipGetLastError();
   }
+  const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
+  const int64_t sparse_max = -1;
   auto launch = [&](auto cb_tag, auto nh_tag) -> hipError_t {
     constexpr int CB = decltype(cb_tag)::value;
     constexpr int NH = decltype(nh_tag)::value;
@@ -2686,13 +3202,11 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
   using I1 = std::integral_constant<int, 1>;
   using I4 = std::integral_constant<int, 4>;
   hipError_t e = hipSuccess;
-  if constexpr (DP >= 64) {
+  if constexpr (DP > 128) {
     if (DP <= 192 && pl.cpg == 8) {
       if constexpr (DP <= 192) e = launch(std::integral_constant<int, 8>{}, I1{});
-    } else if constexpr (DP > 128) {
-      e = launch(I4{}, std::integral_constant<int, 2>{});
     } else {
-      e = launch(I4{}, I1{});
+      e = launch(I4{}, std::integral_constant<int, 2>{});
     }
   }
   if (e != hipSuccess) return e;
@@ -3749,7 +4263,7 @@ extern "C" size_t fgmm_iso_workspace_bytes(int64_t N, int64_t K, int64_t D) {
 extern "C" size_t fgmm_iso_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
   if (N < 0 || K < 0 || D < 1) return 0;
   const int64_t rows = iso_bw_call(D, flags) ? std::min(N, iso_bw_chunk_rows(K)) : N;
-  return make_plan(rows, K, D, wants_stored_lj(flags), (flags & FGMM_FLAG_BF16) != 0).total;
+  return make_plan(rows, K, D, wants_stored_lj(flags), (flags & FGMM_FLAG_BF16) != 0, wants_auto_lj(flags)).total;
 }
 
 extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -3790,7 +4304,7 @@ extern "C" int fgmm_iso_estep_f32(const float* X, int64_t ldx, int64_t N, int64_
   }
   // The stored log-joint path streams X with 32-bit buffer offsets (row stride at
   // most kMaxBufLdx floats); wider strides recompute, which needs less workspace.
-  const IsoPlan pl = make_plan(N, K, D, wants_stored_lj(flags) && ldx <= kMaxBufLdx, bf16);
+  const IsoPlan pl = make_plan(N, K, D, wants_stored_lj(flags) && ldx <= kMaxBufLdx, bf16, wants_auto_lj(flags));
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;
   unsigned char* ws = static_cast<unsigned char*>(workspace);

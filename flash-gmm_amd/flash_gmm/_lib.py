@@ -32,6 +32,7 @@ FLAG_DENSE = 1 << 5
 FLAG_RECOMPUTE = 1 << 6
 FLAG_BF16 = 1 << 7
 FLAG_STORE_LOGJOINT = 1 << 9
+FLAG_STORE_LOGJOINT_AUTO = 1 << 10
 
 
 class FlashGMMError(AssertionError, ValueError):

@@ -127,9 +127,10 @@ def _workspace(ws_fn, N, K, D, flags, dev, workspace):
     try:
         return _empty_workspace(ws_bytes, dev), flags
     except torch.cuda.OutOfMemoryError:
-        if not flags & _lib.FLAG_STORE_LOGJOINT or flags & (_lib.FLAG_PHASE1 | _lib.FLAG_PHASE2):
+        stored = _lib.FLAG_STORE_LOGJOINT | _lib.FLAG_STORE_LOGJOINT_AUTO
+        if not flags & stored or flags & (_lib.FLAG_PHASE1 | _lib.FLAG_PHASE2):
             raise
-        lean = flags & ~_lib.FLAG_STORE_LOGJOINT
+        lean = flags & ~stored
         with torch.cuda.device(dev):
             lean_bytes = int(ws_fn(N, K, D, lean))
         if workspace is not None and workspace.numel() >= lean_bytes:
@@ -138,10 +139,14 @@ def _workspace(ws_fn, N, K, D, flags, dev, workspace):
 
 
 def _plan_flags(flags, dense, recompute, store_log_joint, precision):
+    _require(store_log_joint in (True, False, "auto"),
+             f"store_log_joint must be True, False or 'auto', got {store_log_joint!r}")
     if dense:
         flags |= _lib.FLAG_DENSE
     if recompute:
         flags |= _lib.FLAG_RECOMPUTE
+    elif store_log_joint == "auto":
+        flags |= _lib.FLAG_STORE_LOGJOINT_AUTO
     elif store_log_joint:
         flags |= _lib.FLAG_STORE_LOGJOINT
     if precision == "bf16":
@@ -162,7 +167,7 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
                    accumulate: bool = False, atomic_reduce: bool = False,
                    workspace: torch.Tensor | None = None, phase: int = 0,
                    dense: bool = False, recompute: bool = False,
-                   store_log_joint: bool = False, precision: str = "fp32") -> None:
+                   store_log_joint: bool | str = False, precision: str = "fp32") -> None:
     """Isotropic E-step writing into caller-provided outputs.
 
     ``logZ`` may be None (it is then not written).  With ``accumulate`` the
@@ -176,7 +181,10 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     nonzero responsibility (``recompute=True`` asks for this explicitly).
     ``store_log_joint`` makes pass 1 store the fp32 N x K log-joint in the
     workspace for pass 2 to read (O(N*K) workspace, 4.3 GB at N=1M, K=1024;
-    phase-split calls must agree).
+    phase-split calls must agree).  ``store_log_joint="auto"`` (up to D = 128)
+    reserves that workspace and lets a row-sample probe on the device choose per
+    call: the stored branch where most (row, component block) pairs are needed
+    (dense data), the default plan otherwise.
     ``precision="bf16"`` selects the bf16 operand contract of the reference's H100
     kernels (flash_gmm_h100.py:247-328): X and mu rounded to bfloat16 for the
     contractions, fp32 accumulation and log-sum-exp.
@@ -209,6 +217,23 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
     _lib.check(st, "fgmm_iso_estep_f32")
 
 
+# The drop-in call reserves the stored log-joint's workspace (store_log_joint="auto")
+# while it takes at most this fraction of the device's memory.
+AUTO_STORE_MEMORY_FRACTION = 1.0 / 8
+
+
+def _auto_store(N, K, D, dev, precision):
+    """store_log_joint for the drop-in call: "auto" where its workspace is modest."""
+    if precision != "fp32" or N == 0 or K == 0:
+        return False
+    L = _lib.lib()
+    with torch.cuda.device(dev):
+        extra = int(L.fgmm_iso_workspace_bytes_ex(N, K, D, _lib.FLAG_STORE_LOGJOINT_AUTO)) - \
+            int(L.fgmm_iso_workspace_bytes(N, K, D))
+        total = torch.cuda.get_device_properties(dev).total_memory
+    return "auto" if 0 < extra <= total * AUTO_STORE_MEMORY_FRACTION else False
+
+
 def flash_gmm_estep(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tensor,
                     log_pi: torch.Tensor, BLOCK_N: int = 64, BLOCK_K: int = 16,
                     BLOCK_D: int = 128, *, precision: str = "fp32"):
@@ -218,7 +243,9 @@ def flash_gmm_estep(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tenso
     mu_acc (K, D) = sum_n r_nk x_n, sig_acc (K,) = sum_n r_nk ||x_n - mu_k||^2
     (flash_gmm.py:22-37).  BLOCK_N / BLOCK_K / BLOCK_D are ignored.
     ``precision="bf16"`` follows the bf16 operand contract of the H100 variant
-    (flash_gmm_h100.py:247-328) instead of fp32 arithmetic.
+    (flash_gmm_h100.py:247-328) instead of fp32 arithmetic.  Up to D = 128 the
+    call runs with store_log_joint="auto" (see iso_estep_into) while that
+    workspace takes at most AUTO_STORE_MEMORY_FRACTION of the device's memory.
     """
     _check_common(X, mu, log_pi)
     N, D = X.shape
@@ -228,7 +255,8 @@ def flash_gmm_estep(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tenso
     Nk = torch.empty(K, device=dev, dtype=torch.float32)
     mu_acc = torch.empty(K, D, device=dev, dtype=torch.float32)
     sig_acc = torch.empty(K, device=dev, dtype=torch.float32)
-    iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, precision=precision)
+    iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, precision=precision,
+                   store_log_joint=_auto_store(N, K, D, dev, precision))
     return logZ, Nk, mu_acc, sig_acc
 
 

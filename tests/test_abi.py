@@ -72,23 +72,35 @@ def test_default_workspace_is_lean():
 
 
 def test_iso_workspace_holds_stored_log_joint():
-    """FGMM_FLAG_STORE_LOGJOINT adds the fp32 log-joint tiles (N/32 x K/32 x 4 KiB) where
-    pass 2 reads them, with a per-row block maximum (128 bytes) per tile; the need masks
-    are in both plans (the default plan rounds its tiles to 8 per pass-1 workgroup, the
-    stored plan to 4).  RECOMPUTE overrides it."""
+    """FGMM_FLAG_STORE_LOGJOINT adds, up to D = 128, the fp32 log-joint tiles (N/32 x
+    K/32 x 4 KiB) and per 32-row tile the rows' bf16 X parts (2 x 32 x (D + 16) x 2
+    bytes) and logZ pairs (256 bytes), tiles rounded to 8 per pass-1 workgroup as in
+    the default plan (whose need masks both plans hold).  STORE_LOGJOINT_AUTO adds the
+    same plus the probe's counts; RECOMPUTE overrides both."""
     L = _lib.lib()
-    R, S = _lib.FLAG_RECOMPUTE, _lib.FLAG_STORE_LOGJOINT
+    R, S, A = _lib.FLAG_RECOMPUTE, _lib.FLAG_STORE_LOGJOINT, _lib.FLAG_STORE_LOGJOINT_AUTO
     N, K, D = 1_000_000, 1024, 128
     stored = L.fgmm_iso_workspace_bytes_ex(N, K, D, S)
+    auto = L.fgmm_iso_workspace_bytes_ex(N, K, D, A)
     lean = L.fgmm_iso_workspace_bytes(N, K, D)
     assert L.fgmm_iso_workspace_bytes_ex(N, K, D, S | R) == lean
-    pairs = -(-N // 128) * 4 * (K // 32)
-    tiles = pairs * (4096 + 128)
-    mask_slack = 8 * (K // 32) * 4
-    assert tiles - mask_slack <= stored - lean <= tiles + 4 * 256
+    assert L.fgmm_iso_workspace_bytes_ex(N, K, D, A | R) == lean
+    assert L.fgmm_iso_workspace_bytes_ex(N, K, D, A | S) == stored
+    ptiles = -(-N // 256) * 8
+    extra = ptiles * ((K // 32) * 4096 + 2 * 32 * (D + 16) * 2 + 256)
+    assert extra <= auto - lean <= extra + 4 * 256 + 256
+    # The explicit plan's pass-2 work split differs (partials), within a few MB.
+    assert abs(stored - auto) < 0.01 * extra
+    # AUTO applies up to D = 128 only.
+    assert L.fgmm_iso_workspace_bytes_ex(N, K, 192, A) == L.fgmm_iso_workspace_bytes(N, K, 192)
+    # Not stored: D <= 32, K <= 96, or more than 16 GiB of tiles (AUTO: the last).
+    for n, k, d in [(N, K, 32), (N, 96, 128), (N, 96, 192), (20_000_000, 1024, 128)]:
+        assert L.fgmm_iso_workspace_bytes(n, k, d) == L.fgmm_iso_workspace_bytes_ex(n, k, d, S)
+    assert L.fgmm_iso_workspace_bytes(20_000_000, K, D) == L.fgmm_iso_workspace_bytes_ex(20_000_000, K, D, A)
     # Not stored: D <= 32, K <= 96, or more than 16 GiB of tiles.
     for n, k, d in [(N, K, 32), (N, 96, 128), (N, 96, 192), (20_000_000, 1024, 128)]:
         assert L.fgmm_iso_workspace_bytes(n, k, d) == L.fgmm_iso_workspace_bytes_ex(n, k, d, S)
+    pairs = -(-N // 128) * 4 * (K // 32)
     # Diagonal: stored for K > 96 at every D.
     d_stored = L.fgmm_diag_workspace_bytes_ex(N, K, 96, S)
     d_lean = L.fgmm_diag_workspace_bytes(N, K, 96)
