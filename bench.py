@@ -264,7 +264,8 @@ def make_runner(kind, inp, N, K, D, dev, precision="fp32", store=False, atomic=F
     logZ = torch.empty(N, device=dev)
     Nk = torch.empty(K, device=dev)
     mu_acc = torch.empty(K, D, device=dev)
-    flags = (_lib.FLAG_STORE_LOGJOINT if store else 0) | (_lib.FLAG_BF16 if precision == "bf16" else 0)
+    flags = ((_lib.FLAG_STORE_LOGJOINT_AUTO if store == "auto" else _lib.FLAG_STORE_LOGJOINT if store else 0) |
+             (_lib.FLAG_BF16 if precision == "bf16" else 0))
     ws = torch.empty(max(1, int(getattr(L, f"fgmm_{kind}_workspace_bytes_ex")(N, K, D, flags))),
                      dtype=torch.uint8, device=dev)
     if kind == "iso":
@@ -345,8 +346,12 @@ def time_dropin(kind, inp, steps, warmup, stream):
 KERNELS = {
     # (kind, plan) -> (pass-1 kernel, pass-2 kernel)
     ("iso", "default"): ("iso_lse_pipe (need masks)", "iso_accum_gather / iso_accum_tiles (by the needed-pair count)"),
+    ("iso", "auto"): ("iso_store_probe, iso_lse_pipe (need masks; stores the log-joint where the probe selects it)",
+                      "iso_accum_ljt where the probe selected the stored branch, else iso_accum_gather / "
+                      "iso_accum_tiles2 (by the needed-pair count)"),
     ("iso", "default_wide"): ("iso_lse_ctile (need masks)", "iso_accum_drange"),
-    ("iso", "stored"): ("iso_lse (stores the log-joint)", "iso_accum_sparse / iso_accum_lj"),
+    ("iso", "stored"): ("iso_lse_pipe (stores the log-joint, bf16 X parts, logZ pairs)",
+                        "iso_accum_sparse / iso_accum_ljt (by the needed-pair count)"),
     ("iso", "stored_wide"): ("iso_lse_ctile (stores the log-joint)", "iso_accum_lj"),
     ("diag", "default"): ("diag_lse_x6 (need masks)", "diag_accum_gather"),
     ("diag", "default_wide"): ("diag_lse_ctile (need masks)", "diag_accum_drange"),
@@ -360,6 +365,8 @@ KERNELS = {
 def kernel_names(kind, D, precision, stored):
     if precision == "bf16":
         return f"{kind}_bf16_lse", f"{kind}_bf16_accum"
+    if stored == "auto":
+        return KERNELS[("iso", "auto")] if (kind == "iso" and D <= 128) else kernel_names(kind, D, precision, False)
     wide = kind != "full" and D > 128
     if stored and (D > 256 or (kind == "full" and D > 128)):
         stored = False          # the stored plan's widths; above them the call runs the default plan
@@ -391,7 +398,10 @@ def main_workload(args):
     kind = workload.split("_")[0]
     bf16 = args.precision == "bf16"
     log(f"generating workload {workload} on {torch.cuda.get_device_name(dev)}")
-    inp, outs, r = measure(args, workload, args.precision, args.store_log_joint, dev)
+    # The phases run the plan the drop-in call takes: store_log_joint="auto" for the
+    # isotropic model up to D = 128 (flash_gmm_estep), else the default plan.
+    mode = True if args.store_log_joint else ("auto" if (kind == "iso" and not bf16 and D <= 128) else False)
+    inp, outs, r = measure(args, workload, args.precision, mode, dev)
     split_ms, p1, p2 = r["ms"], r["p1"], r["p2"]
     log(f"timed {args.steps} steps as two phase calls: {split_ms:.3f} ms/step (phase1 {p1:.3f} ms, "
         f"phase2 {p2:.3f} ms)")
@@ -407,7 +417,7 @@ def main_workload(args):
         ms, med = split_ms, None
 
     (flop, f1, f2), alg_bytes = algorithmic(kind, N, K, D)
-    k1, k2 = kernel_names(kind, D, args.precision, args.store_log_joint)
+    k1, k2 = kernel_names(kind, D, args.precision, mode)
     ex1, unit1, peak1 = pass1_executed(kind, N, K, D, args.precision, args.store_log_joint)
     phases = {
         "phase1": {"kernel": k1 + " + prologue", "ms": p1, "fp32_algorithmic_flop": f1,
@@ -427,6 +437,11 @@ def main_workload(args):
         ex2 = pairs / 32.0 * (7 * DP // 16 + 3 * 2 * DP // 32) * 32768.0
         need = {"needed_row_block_pairs": pairs, "fraction": pairs / (N * KB),
                 "basis": "estimated from the inputs and the kernel's logZ (float32)"}
+        if mode == "auto" and pairs >= 0.5 * N * KB:
+            # The stored branch: r^T X only (3 products, 2 row steps, DP / 32 column
+            # tiles) for every (32-row tile, block) with a needed row.
+            ex2 = (-(-N // 32)) * KB * 3 * 2 * (DP // 32) * 32768.0
+            need["branch"] = "stored (iso_accum_ljt)"
         phases["phase2"].update(executed_matrix_flop=ex2, executed_unit="bf16",
                                 executed_tflops=ex2 / (p2 * 1e-3) / 1e12, needed_pairs=need)
     if kind == "iso" and bf16 and not args.store_log_joint:
@@ -488,6 +503,10 @@ def main_workload(args):
                    "generator": f"flash_gmm.data.make({workload!r}), generated on device",
                    "reduce": "deterministic fixed-order tree",
                    "log_joint": "stored by phase 1, read by phase 2 (opt-in)" if args.store_log_joint
+                   else "the default plan with a device-selected stored branch (store_log_joint='auto', "
+                        "the drop-in's mode): a row-sample probe chooses per call; need bits from "
+                        "phase 1 and gathered rows in phase 2 where few pairs are needed, the stored "
+                        "log-joint where most are" if mode == "auto"
                    else "recomputed (default O(N + K*D) plan: need bits from phase 1, gathered rows "
                         "in phase 2)" if (D <= 128 and not bf16)
                    else "recomputed (default O(N + K*D) plan)",
@@ -539,15 +558,23 @@ def main_workload(args):
         # lss = 0, uniform log pi), where every responsibility is nonzero.
         ref_wl = "iso_ref_n1m_k1024_d128"
         torch.cuda.empty_cache()
-        rinp, _, rr = measure(args, ref_wl, "fp32", False, dev)
+        rinp, _, rr = measure(args, ref_wl, "fp32", "auto", dev)
         rms, rmed = time_dropin("iso", rinp, args.steps, args.warmup, stream)
+        del rr["call"]
+        torch.cuda.empty_cache()
+        _, _, rd = measure(args, ref_wl, "fp32", False, dev, inp=rinp)
         out["reference_smoke_workload"] = {
             "workload": ref_wl, "N": N, "K": K, "D": D, "value": N / (rms * 1e-3), "unit": "samples/s",
             "ms_per_step": rms, "median_call_ms": rmed, "phase1_ms": rr["p1"], "phase2_ms": rr["p2"],
+            "plan": "the drop-in call (store_log_joint='auto': the probe selects the stored branch here)",
+            "default_plan": {"ms_per_step": rd["ms"], "phase1_ms": rd["p1"], "phase2_ms": rd["p2"],
+                             "note": "the O(N + K*D) plan on the same data (pass 2 recomputes the "
+                                     "contraction for every pair)"},
             "vs_baseline": (N / (rms * 1e-3)) / A100_SAMPLES_PER_S,
             "data": "X, mu ~ N(0, I), lss = 0, log pi = -log K (flash_gmm.py:228-234), generated on device"}
-        log(f"reference smoke workload: {rms:.3f} ms/step (phase1 {rr['p1']:.3f}, phase2 {rr['p2']:.3f})")
-        del rinp, rr
+        log(f"reference smoke workload: {rms:.3f} ms/step (phase1 {rr['p1']:.3f}, phase2 {rr['p2']:.3f}); "
+            f"default plan {rd['ms']:.3f} ms")
+        del rinp, rr, rd
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline and not bf16:
         log("timing the CPU baseline (bounded sample)")
