@@ -59,11 +59,20 @@ WORKLOADS = {
 # (FETCH_SIZE KiB, WRITE_SIZE KiB); the commands and tables are in profiles/.
 TRAFFIC_KIB = {
     # (workload, plan, precision): {kernel: (fetch KiB, write KiB)}; "phase1" names pass 1's
+    # The drop-in's mode (store_log_joint="auto"): on this clustered data the probe keeps
+    # the default plan, and iso_accum_ljt returns at once.
     ("iso_n1m_k1024_d128", "default", "fp32"): {
         "phase1": "iso_lse_pipe<128, 1>",
-        "iso_prep": (314, 1_104), "iso_lse_pipe<128, 1>": (311_019, 24_415),
-        "iso_accum_gather<128>": (268_553, 33_280), "iso_accum_tiles2<128>": (22, 0),
-        "iso_reduce": (20_873, 662)},
+        "iso_prep": (310, 1_104), "iso_store_probe<128>": (2_679, 2), "iso_lse_pipe<128, 1>": (310_989, 24_415),
+        "iso_accum_ljt<128>": (10, 0), "iso_accum_gather<128>": (268_566, 33_280),
+        "iso_accum_tiles2<128>": (12, 0), "iso_reduce": (20_857, 663)},
+    # The reference's N(0, I) data: the probe selects the stored branch (pass 1 writes the
+    # log-joint, the X parts and the logZ pairs; iso_accum_ljt reads them back).
+    ("iso_ref_n1m_k1024_d128", "default", "fp32"): {
+        "phase1": "iso_lse_pipe<128, 1>",
+        "iso_prep": (310, 1_104), "iso_store_probe<128>": (2_679, 2),
+        "iso_lse_pipe<128, 1>": (316_772, 4_534_764), "iso_accum_ljt<128>": (2_289_322, 33_280),
+        "iso_accum_gather<128>": (22, 0), "iso_accum_tiles2<128>": (13, 0), "iso_reduce": (20_835, 664)},
     ("diag_n1m_k1024_d96", "default", "fp32"): {
         "phase1": "diag_lse_x6<96, 2>",
         "diag_x6_prep": (457, 1_552), "diag_lse_x6<96, 2>": (193_991, 19_532),
