@@ -146,6 +146,33 @@ __device__ __forceinline__ f32x2 bf16_pair_widen(unsigned w) {
   return r;
 }
 
+// acc_to_row_operand of r8 (hi) and of its exact residuals r8 - bf16(r8) (lo): each
+// pair is rounded once, and the residuals come from the widened rounding.
+__device__ __forceinline__ void acc_to_row_operands_split(const float* r8, bf16x8& hi, bf16x8& lo) {
+  unsigned ph[4], pl[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const f32x2 v = {r8[2 * j], r8[2 * j + 1]};
+    ph[j] = bf16_pair(v);
+    const f32x2 w = bf16_pair_widen(ph[j]);
+    const f32x2 d = {v.x - w.x, v.y - w.y};
+    pl[j] = bf16_pair(d);
+  }
+  uint4 wh, wl;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const auto sh = __builtin_amdgcn_permlane32_swap(ph[hh], ph[2 + hh], false, false);
+    const auto sl = __builtin_amdgcn_permlane32_swap(pl[hh], pl[2 + hh], false, false);
+    if (hh == 0) {
+      wh.x = sh[0]; wh.z = sh[1]; wl.x = sl[0]; wl.z = sl[1];
+    } else {
+      wh.y = sh[0]; wh.w = sh[1]; wl.y = sl[0]; wl.w = sl[1];
+    }
+  }
+  hi = __builtin_bit_cast(bf16x8, wh);
+  lo = __builtin_bit_cast(bf16x8, wl);
+}
+
 __device__ __forceinline__ void split3_bf16(const f32x4 lo, const f32x4 hi, bf16x8 (&s)[3]) {
   const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
   uint4 w[3];

@@ -714,16 +714,6 @@ void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     }
     split3_bf16(lo, hi, xb[q]);
   }
-  if (store) {
-    // The tile's bf16 (hi, lo) parts of X for the stored plan's pass 2, row-major
-    // with its LDS row stride (ljt_xsplit_bytes per tile).
-    __bf16* xp = xsplit + tile * (2 * 32 * gather_rs(DP)) + c * gather_rs(DP) + 8 * g;
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      *reinterpret_cast<bf16x8*>(xp + 16 * q) = xb[q][0];
-      *reinterpret_cast<bf16x8*>(xp + 32 * gather_rs(DP) + 16 * q) = xb[q][1];
-    }
-  }
   xsq += __shfl_xor(xsq, 32);
   const bf16x8 ones = x6c_ones(lane);
   lds_barrier();   // simd_l cleared
@@ -849,11 +839,23 @@ void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     rowstat[row] = make_double2(xsq, lz2);
     if (logZ) logZ[row] = (float)(lz2 * kLn2);
   }
-  if (store && g == 0) {
-    // logZ2 as the (hi, lo) float pair the stored plan's pass 2 subtracts.
-    const float zh = (float)lz2;
-    const float zl = (lz2 > -INFINITY && lz2 < INFINITY) ? (float)(lz2 - (double)zh) : 0.0f;
-    zpair[tile * 32 + c] = make_float2(zh, zl);
+  if (store) {
+    // The tile's bf16 (hi, lo) parts of X for the stored plan's pass 2, row-major
+    // with its LDS row stride (ljt_xsplit_bytes per tile).  Written last, so that no
+    // wait of the block loop covers them.
+    __bf16* xp = xsplit + tile * (2 * 32 * gather_rs(DP)) + c * gather_rs(DP) + 8 * g;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      *reinterpret_cast<bf16x8*>(xp + 16 * q) = xb[q][0];
+      *reinterpret_cast<bf16x8*>(xp + 32 * gather_rs(DP) + 16 * q) = xb[q][1];
+    }
+    if (g == 0) {
+      // logZ2 as the (hi, lo) float pair the stored plan's pass 2 subtracts; +inf
+      // for a row past N, whose responsibilities are then exactly 0 there.
+      const float zh = valid ? (float)lz2 : INFINITY;
+      const float zl = (valid && lz2 > -INFINITY && lz2 < INFINITY) ? (float)(lz2 - (double)zh) : 0.0f;
+      zpair[tile * 32 + c] = make_float2(zh, zl);
+    }
   }
   if constexpr (REXACT) {
     // Each lane reads back the bounds it wrote itself.
@@ -2437,11 +2439,14 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 // groups.  Three LDS stages, each one tile's X parts, the 8 blocks' log-joint tiles
 // and the logZ2 pairs, all filled by buffer-to-LDS loads: at step t the workgroup
 // issues tile t + 2's, computes tile t and waits for tile t + 1's before the barrier.
-// A wave issues the same loads every step (log-joint rows whose need bit is clear
-// read as zeros and get r = 0, as do rows past the slab: no sum changes), so that
-// wait is a fixed count of its own outstanding loads, and no global load of the
-// loop is left for the compiler to wait on.  A wave skips a tile whose need word is
-// zero.  `sel` (when given) is the word pass 1 read: the kernel returns unless set.
+// A wave issues the same loads every step, so that wait is a fixed count of its own
+// outstanding loads, and no global load of the loop is left for the compiler to
+// wait on.  A wave skips a tile whose need word is zero (its loads then read out of
+// range); otherwise it loads and exponentiates the whole log-joint tile with no
+// per-row select: a row whose need bit is clear has l < logZ2 - kLjNeedGap in every
+// component of the block, so 2^(l - logZ2) is exactly 0 in fp32, and pass 1 gives a
+// row past N the logZ2 pair (+inf, 0).  `sel` (when given) is the word pass 1 read:
+// the kernel returns unless set.
 // ---------------------------------------------------------------------------
 constexpr int kLjtWaves = kLjtWavesPlan;
 constexpr int kLjtStages = 3;
@@ -2454,13 +2459,14 @@ struct LjtShape {
   static constexpr int LJB = kLjtWaves * kLjTile * 4;       // the 8 blocks' log-joint tiles
   static constexpr int OFF_X = LJB, OFF_Z = LJB + XB;
   static constexpr int STAGE = LJB + XB + 32 * 8;
-  static constexpr size_t lds = (size_t)kLjtStages * STAGE;
-  // X loads of wave w per tile (whole waves of pieces: XP is a multiple of 64).
-  static constexpr int xloads(int w) {
-    int n = 0;
-    for (int q = 0; q < XQ; ++q) n += (q * 64 * kLjtWaves + w * 64 < XP) ? 1 : 0;
-    return n;
-  }
+  // After the stages, one 1 KB line that the loads a wave issues only to keep its
+  // count fixed (out of range: they write zeros) land in.
+  static constexpr int OFF_PAD = kLjtStages * STAGE;
+  static constexpr size_t lds = (size_t)OFF_PAD + 1024;
+  // Loads of every wave per tile: XQ of X parts (the last one out of range on the
+  // waves past XP), 4 of its log-joint tile, 1 of logZ2 pairs (wave 0; an
+  // out-of-range one elsewhere).
+  static constexpr int NLOADS = XQ + 4 + 1;
 };
 __host__ inline int64_t ljt_grid(int nslab, int ncg) { return (int64_t)8 * cdiv(nslab, 8) * ncg; }
 
@@ -2468,17 +2474,6 @@ template <int N>
 __device__ __forceinline__ void vm_wait() {
   static_assert(N >= 0 && N <= 63, "vmcnt field");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-// vm_wait for a wave-uniform count below 16.
-__device__ __forceinline__ void vm_wait_n(int n) {
-  switch (n) {
-    case 0: vm_wait<0>(); break;   case 1: vm_wait<1>(); break;   case 2: vm_wait<2>(); break;
-    case 3: vm_wait<3>(); break;   case 4: vm_wait<4>(); break;   case 5: vm_wait<5>(); break;
-    case 6: vm_wait<6>(); break;   case 7: vm_wait<7>(); break;   case 8: vm_wait<8>(); break;
-    case 9: vm_wait<9>(); break;   case 10: vm_wait<10>(); break; case 11: vm_wait<11>(); break;
-    case 12: vm_wait<12>(); break; case 13: vm_wait<13>(); break; case 14: vm_wait<14>(); break;
-    default: vm_wait<0>(); break;
-  }
 }
 
 template <int DP>
@@ -2539,10 +2534,10 @@ void iso_accum_ljt(const float* __restrict__ lj, const __bf16* __restrict__ xspl
     return ok ? v : 0u;
   };
   // Tile t into stage S: the X parts (whole waves of pieces), the wave's log-joint
-  // tile (piece l of load q is row 8 q + l / 8; out of range where the row's bit is
-  // clear or past the slab) and, by wave 0, the rows' logZ2 pairs.
-  const int nx = SH::xloads(wave);
-  const int nloads = nx + 4 + (wave == 0 ? 1 : 0);
+  // tile (piece l of load q is row 8 q + l / 8; all out of range when the need word
+  // is 0 or the tile is past the slab) and, by wave 0, the rows' logZ2 pairs.
+  constexpr int NL = SH::NLOADS;
+  unsigned char* const pad = lds_raw + SH::OFF_PAD;
   auto issue = [&](int t, auto stage_tag, unsigned m) __attribute__((always_inline)) {
     constexpr int S = decltype(stage_tag)::value;
     unsigned char* st = lds_raw + (size_t)S * SH::STAGE;
@@ -2556,17 +2551,18 @@ void iso_accum_ljt(const float* __restrict__ lj, const __bf16* __restrict__ xspl
       if (q * 64 * kLjtWaves + wave * 64 < SH::XP)
         lds_dma16(xsrc, st + SH::OFF_X + (q * 64 * kLjtWaves + wave * 64) * 16,
                   (q * 64 * kLjtWaves + tid) * 16, 0);
+      else
+        lds_dma16(xsrc, pad, kBufOob, 0);
     }
     const DmaSrc lsrc = dma_src(m ? lj + (tg * KB + kb) * kLjTile : lj, m ? (uint32_t)(kLjTile * 4) : 0u);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int row = 8 * q + (lane >> 3);
-      lds_dma16(lsrc, st + wave * kLjTile * 4 + q * 1024, ((m >> row) & 1u) ? (q * 64 + lane) * 16 : kBufOob, 0);
-    }
+    for (int q = 0; q < 4; ++q) lds_dma16(lsrc, st + wave * kLjTile * 4 + q * 1024, (q * 64 + lane) * 16, 0);
     if (wave == 0) {
-      const int nrow = in ? (int)(r_end - (r_begin + (int64_t)t * 32) < 32 ? r_end - (r_begin + (int64_t)t * 32) : 32) : 0;
-      const DmaSrc zsrc = dma_src(zpair + tg * 32 * (in ? 1 : 0), (uint32_t)(nrow * sizeof(float2)));
+      // All 32 pairs of a tile in range (those of rows past N are (+inf, 0)).
+      const DmaSrc zsrc = dma_src(zpair + tg * 32 * (in ? 1 : 0), in ? (uint32_t)(32 * sizeof(float2)) : 0u);
       if (lane < 16) lds_dma16(zsrc, st + SH::OFF_Z, lane * 16, 0);
+    } else {
+      lds_dma16(lsrc, pad, kBufOob, 0);
     }
   };
   // Tile t in stage S (need word m, not 0): one straight-line block, its LDS reads
@@ -2578,17 +2574,28 @@ void iso_accum_ljt(const float* __restrict__ lj, const __bf16* __restrict__ xspl
     int sb = S * SH::STAGE;
     asm volatile("" : "+s"(sb));
     const unsigned char* st = lds_raw + sb;
-    const float* lt = reinterpret_cast<const float*>(st + wave * kLjTile * 4) + c;
-    const float2* zt = reinterpret_cast<const float2*>(st + SH::OFF_Z);
+    // The lane's column of rows 4g, 4g + 1, ... of the wave's log-joint tile and its
+    // logZ2 pairs, each from one base register and immediate offsets.
+    int lofs = sb + wave * kLjTile * 4 + 4 * c + 4 * 32 * 4 * g;
+    int zofs = sb + SH::OFF_Z + 4 * 8 * g;
+    asm volatile("" : "+v"(lofs), "+v"(zofs));
+    const float* lt = reinterpret_cast<const float*>(lds_raw + lofs);
+    const f32x4* zt = reinterpret_cast<const f32x4*>(lds_raw + zofs);
     const __bf16* xt = reinterpret_cast<const __bf16*>(st + SH::OFF_X);
-    const unsigned mg = m >> (4 * g);
     float lv[16];
     float2 zv[16];
+    // Registers 4j .. 4j + 3 hold rows 8j + 4g .. 8j + 4g + 3 (acc_row).
     auto rows = [&](int p) __attribute__((always_inline)) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        lv[8 * p + e] = lt[acc_row(8 * p + e, g) * 32];
-        zv[8 * p + e] = zt[acc_row(8 * p + e, g)];
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * p + jj;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) lv[4 * j + e] = lt[(8 * j + e) * 32];
+        const f32x4 z01 = zt[4 * j], z23 = zt[4 * j + 1];
+        zv[4 * j] = make_float2(z01[0], z01[1]);
+        zv[4 * j + 1] = make_float2(z01[2], z01[3]);
+        zv[4 * j + 2] = make_float2(z23[0], z23[1]);
+        zv[4 * j + 3] = make_float2(z23[2], z23[3]);
       }
     };
     bf16x8 b1[2][NJ], b2[2][NJ];
@@ -2601,23 +2608,19 @@ void iso_accum_ljt(const float* __restrict__ lj, const __bf16* __restrict__ xspl
     };
     bf16x8 a1[2], a2[2];
     // Responsibilities of rows 16 p .. 16 p + 15 (registers 8 p .. 8 p + 7 of the
-    // accumulator layout), exponentiated on every lane and selected (no branch): a
-    // row not read has l = 0, whose power is discarded.
+    // accumulator layout) and their bf16 (hi, lo) parts, each pair rounded once.
     auto half = [&](int p) __attribute__((always_inline)) {
-      float r[8], res[8];
+      float r[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int i = 8 * p + e;
         const float l = lv[i];
-        const float ex = fast_exp2((l - zv[i].x) - zv[i].y);
-        const float rv = ((mg >> (8 * (i >> 2) + (i & 3))) & 1u) ? ex : 0.0f;
+        const float rv = fast_exp2((l - zv[i].x) - zv[i].y);
         r[e] = rv;
-        res[e] = rv - (float)(__bf16)rv;
         nk += rv;
         sig = fmaf(rv, c0 - l, sig);
       }
-      a1[p] = acc_to_row_operand(r);
-      a2[p] = acc_to_row_operand(res);
+      acc_to_row_operands_split(r, a1[p], a2[p]);
     };
     auto steps = [&](int p) __attribute__((always_inline)) {
 #pragma unroll
@@ -2659,7 +2662,7 @@ void iso_accum_ljt(const float* __restrict__ lj, const __bf16* __restrict__ xspl
     issue(t + 2, std::integral_constant<int, S2>{}, mnext);
     mnext = mword(t + 3);
     if (mk[S] != 0u) compute(stage_tag, mk[S]);
-    vm_wait_n(nloads);
+    vm_wait<NL>();
     __syncthreads();
   };
 
@@ -2669,7 +2672,7 @@ void iso_accum_ljt(const float* __restrict__ lj, const __bf16* __restrict__ xspl
     issue(0, std::integral_constant<int, 0>{}, mk[0]);
     issue(1, std::integral_constant<int, 1>{}, mk[1]);
     mnext = mword(2);
-    vm_wait_n(nloads);   // tile 0's stage
+    vm_wait<NL>();   // tile 0's stage
     __syncthreads();
   }
   using S0 = std::integral_constant<int, 0>;
