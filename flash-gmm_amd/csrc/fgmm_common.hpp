@@ -146,6 +146,18 @@ __device__ __forceinline__ f32x2 bf16_pair_widen(unsigned w) {
   return r;
 }
 
+// acc_to_row_operand of registers already packed in bf16 pairs (w[j] = registers
+// 2j, 2j + 1 of the eight).
+__device__ __forceinline__ bf16x8 pairs_to_row_operand(const unsigned (&w)[4]) {
+  uint4 wv;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(w[hh], w[2 + hh], false, false);
+    if (hh == 0) { wv.x = sw[0]; wv.z = sw[1]; } else { wv.y = sw[0]; wv.w = sw[1]; }
+  }
+  return __builtin_bit_cast(bf16x8, wv);
+}
+
 // acc_to_row_operand of r8 (hi) and of its exact residuals r8 - bf16(r8) (lo): each
 // pair is rounded once, and the residuals come from the widened rounding.
 __device__ __forceinline__ void acc_to_row_operands_split(const float* r8, bf16x8& hi, bf16x8& lo) {
@@ -154,23 +166,27 @@ __device__ __forceinline__ void acc_to_row_operands_split(const float* r8, bf16x
   for (int j = 0; j < 4; ++j) {
     const f32x2 v = {r8[2 * j], r8[2 * j + 1]};
     ph[j] = bf16_pair(v);
-    const f32x2 w = bf16_pair_widen(ph[j]);
-    const f32x2 d = {v.x - w.x, v.y - w.y};
-    pl[j] = bf16_pair(d);
+    pl[j] = bf16_pair(v - bf16_pair_widen(ph[j]));
   }
-  uint4 wh, wl;
+  hi = pairs_to_row_operand(ph);
+  lo = pairs_to_row_operand(pl);
+}
+
+// The same with three parts: r8 = r1 + r2 + r3 exactly before r3's rounding
+// (split3_bf16's parts, in the row-operand layout).
+__device__ __forceinline__ void acc_to_row_operands_split3(const float* r8, bf16x8& a1, bf16x8& a2, bf16x8& a3) {
+  unsigned p1[4], p2[4], p3[4];
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    const auto sh = __builtin_amdgcn_permlane32_swap(ph[hh], ph[2 + hh], false, false);
-    const auto sl = __builtin_amdgcn_permlane32_swap(pl[hh], pl[2 + hh], false, false);
-    if (hh == 0) {
-      wh.x = sh[0]; wh.z = sh[1]; wl.x = sl[0]; wl.z = sl[1];
-    } else {
-      wh.y = sh[0]; wh.w = sh[1]; wl.y = sl[0]; wl.w = sl[1];
-    }
+  for (int j = 0; j < 4; ++j) {
+    const f32x2 v = {r8[2 * j], r8[2 * j + 1]};
+    p1[j] = bf16_pair(v);
+    const f32x2 d1 = v - bf16_pair_widen(p1[j]);
+    p2[j] = bf16_pair(d1);
+    p3[j] = bf16_pair(d1 - bf16_pair_widen(p2[j]));
   }
-  hi = __builtin_bit_cast(bf16x8, wh);
-  lo = __builtin_bit_cast(bf16x8, wl);
+  a1 = pairs_to_row_operand(p1);
+  a2 = pairs_to_row_operand(p2);
+  a3 = pairs_to_row_operand(p3);
 }
 
 __device__ __forceinline__ void split3_bf16(const f32x4 lo, const f32x4 hi, bf16x8 (&s)[3]) {
@@ -666,6 +682,12 @@ __device__ __forceinline__ void lds_dma16(const DmaSrc& r, void* dst, int voff, 
                "s_mov_b32 m0, %0"
                : "=&s"(saved) : "s"(lds), "v"(voff), "s"(r.words), "s"(soff) : "memory");
 }
+// Wait until at most N vector-memory operations of the wave are outstanding.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N <= 63, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 __device__ __forceinline__ void dma_barrier() {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
@@ -734,6 +756,43 @@ constexpr int kWideReduce = 128;
 
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 __host__ __device__ constexpr int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
+
+// The stored-log-joint probe (FGMM_FLAG_STORE_LOGJOINT_AUTO): up to kProbeTiles
+// 32-row tiles spread over the rows, one count of needed (row, block) pairs per
+// tile; at least half of the sampled pairs selects the stored branch.  Up to
+// kProbeMaxKB blocks (a probe keeps a tile's block maxima in LDS).
+constexpr int kProbeTiles = 64;
+constexpr int kProbeMaxKB = 512;
+__host__ __device__ constexpr size_t probe_bytes() { return (size_t)kProbeTiles * sizeof(unsigned); }
+// What a kernel needs to evaluate the probe's choice (count == nullptr: no probe).
+struct ProbeSel {
+  const unsigned* count;
+  int n;
+  int64_t min_pairs;
+};
+// The stored branch is selected (uniform; false without a probe).
+__device__ __forceinline__ bool probe_selects(const ProbeSel& p) {
+  if (p.count == nullptr) return false;
+  const int lane = threadIdx.x & 63;
+  unsigned v = lane < p.n ? p.count[lane] : 0u;
+  uint64_t t = v;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o);
+  const uint64_t tot = (uint64_t)__builtin_amdgcn_readfirstlane((unsigned)t) |
+                       ((uint64_t)__builtin_amdgcn_readfirstlane((unsigned)(t >> 32)) << 32);
+  return (int64_t)tot >= p.min_pairs;
+}
+// The sampled tiles (tile s of ntile is s * tiles / ntile) and the probe's
+// threshold: half of the sampled (row, block) pairs.
+__host__ __device__ inline int64_t probe_tile(int s, int64_t N, int ntile) { return (int64_t)s * cdiv(N, 32) / ntile; }
+__host__ inline int64_t probe_min_pairs(int64_t N, int ntile, int KB) {
+  int64_t rows = 0;
+  for (int s = 0; s < ntile; ++s) {
+    const int64_t t = probe_tile(s, N, ntile);
+    rows += N - t * 32 < 32 ? N - t * 32 : 32;
+  }
+  return cdiv(rows * KB, 2);
+}
 
 __host__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 

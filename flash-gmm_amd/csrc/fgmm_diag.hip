@@ -97,6 +97,18 @@ __host__ __device__ constexpr int bf16_row_partials(int DP, int CB);
 // Pass 1 keeps the rows' split features in registers (diag_lse_x6) up to D = 128.
 __host__ __device__ constexpr bool diag_uses_x6(int DP) { return DP <= 128; }
 
+// The stored branch of FGMM_FLAG_STORE_LOGJOINT_AUTO (default plan, D <= 96): pass 1
+// keeps every log-joint tile (row-major, as the stored plan's), the rows' features
+// [x^2 | x] in three bf16 parts (row stride ljd_rs, chunk q at columns 16q .. 16q + 15
+// in pass 1's order) and logZ2 as (hi, lo) float pairs; diag_accum_ljt streams them.
+__host__ __device__ constexpr int ljd_rs(int DP) { return 2 * DP + 16; }
+__host__ __device__ constexpr size_t ljd_xsplit_bytes(int DP) { return (size_t)3 * 32 * ljd_rs(DP) * 2; }
+__host__ __device__ constexpr bool ljd_applies(int DP) { return DP <= 96; }
+// Piece (16 bytes) swizzle of a 32 x 16 float transposition tile: row r's piece p sits
+// at p ^ ljd_swz(r), so that the column writes and the row reads of a wave fall in
+// distinct banks.
+__device__ __forceinline__ int ljd_swz(int r) { return (((r >> 2) & 1) << 1) | (((r >> 1) ^ (r >> 3)) & 1); }
+
 struct DiagPlan {
   int64_t N, K, D;
   int DP, FP;   // D padded (32 up to 128, then 64); feature count 2*DP
@@ -115,6 +127,10 @@ struct DiagPlan {
   bool bfw;         // bf16 contract above D = 256: stored log-joint, diag_bf16_*_wide
   bool bfneed;      // bf16 contract up to D = 128: need masks from pass 1, diag_bf16_gather in pass 2
                     // (or diag_bf16_accum where most pairs are needed)
+  bool autolj;      // the default plan with a stored branch that a row-sample probe selects on the
+                    // device (FGMM_FLAG_STORE_LOGJOINT_AUTO, D <= 96)
+  int nprobe;       // the probe's sampled tiles
+  size_t off_xsplit, off_zpair, off_probe;
   size_t off_musw, off_mu3, off_kcx6, off_kcx6lin, off_kclin, off_rowstat, off_part_mu,
       off_part_sq, off_part_nk, off_lj, off_ljmax, off_ljmask, off_ljcount, total;
 };
@@ -140,7 +156,8 @@ __host__ inline bool use_stored_lj(int64_t N, int KB, int DP, bool allow) {
          (size_t)round_up(cdiv(N, 32), 4) * (size_t)KB * kLjTile * sizeof(float) <= kMaxLjBytes;
 }
 
-DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool bf16 = false) {
+DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool bf16 = false,
+                   bool auto_lj = false) {
   DiagPlan p{};
   p.N = N; p.K = K; p.D = D;
   p.DP = diag_padded_dim(D);
@@ -150,6 +167,9 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.bf16 = bf16;
   p.lj = !bf16 && use_stored_lj(N, p.KB, p.DP, allow_lj);
   p.need = !bf16 && !p.lj;
+  p.autolj = p.need && auto_lj && ljd_applies(p.DP) && N > 0 && p.KB > 0 && p.KB <= kProbeMaxKB &&
+             (size_t)round_up(cdiv(N, 32), 4) * (size_t)p.KB * kLjTile * sizeof(float) <= kMaxLjBytes;
+  p.nprobe = p.autolj ? (int)std::min<int64_t>(kProbeTiles, cdiv(N, 32)) : 0;
   p.ctile = !bf16 && !diag_uses_x6(p.DP);
   p.rexact = p.need && p.KB <= (p.ctile ? ctile_need_exact_cap(ctile_blocks(p.DP)) : need_exact_cap(p.DP));
   p.ndr = p.ctile ? (int)cdiv(p.DP, kDrange) : 1;
@@ -231,10 +251,16 @@ DiagPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
              bf16_lse_lds_base(p.DP) + (size_t)kWaves * 32 * p.KB * 2 <= kMaxLds;
   const size_t nsp = (p.lj_sparse || p.need || p.bfneed) ? (p.bfneed ? (size_t)round_up(cdiv(N, 32), 4) * p.KB : ntile) : 0;
   p.off_lj = off;
-  off = align256(off + (p.bfw ? bw_lj_bytes(N, p.KP) : p.lj ? ntile * kLjTile * sizeof(float) : 0));
+  off = align256(off + (p.bfw ? bw_lj_bytes(N, p.KP) : (p.lj || p.autolj) ? ntile * kLjTile * sizeof(float) : 0));
   p.off_ljmax = off;   off = align256(off + (p.lj_sparse ? nsp * 64 * sizeof(float) : 0));
   p.off_ljmask = off;  off = align256(off + nsp * sizeof(uint2));
   p.off_ljcount = off; off = align256(off + ((p.lj_sparse || p.bfneed) ? 64 * sizeof(unsigned) : 0));
+  // The stored branch's feature parts and logZ2 pairs (one per pass-1 tile) and the
+  // probe's counts.
+  const size_t ptiles = p.autolj ? (size_t)round_up(cdiv(N, 32), 4) : 0;
+  p.off_xsplit = off;  off = align256(off + ptiles * ljd_xsplit_bytes(p.DP));
+  p.off_zpair = off;   off = align256(off + ptiles * 32 * sizeof(float2));
+  p.off_probe = off;   off = align256(off + (p.autolj ? probe_bytes() : 0));
   p.total = off;
   return p;
 }
@@ -354,13 +380,14 @@ __global__ __launch_bounds__(64) void diag_x6_prep(const float* __restrict__ mu,
 constexpr int kLjmStore = 1;   // the stored log-joint, its half-block maxima and need masks
 constexpr int kLjmNeed = 2;    // need masks only (the default plan)
 
-template <int DP, int LJM>
+template <int DP, int LJM, bool ST = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(kAccThreads, kAccThreads), amdgpu_waves_per_eu(2, 2)))
 void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                  const bf16x8* __restrict__ mu3, const double* __restrict__ kc_x6, int KB,
                  float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj,
                  float* __restrict__ ljmax, unsigned* __restrict__ ljmask, unsigned* __restrict__ ljcount,
-                 int dense, int rexact) {
+                 int dense, int rexact, ProbeSel probe, float* __restrict__ ljd, __bf16* __restrict__ xsplit,
+                 float2* __restrict__ zpair) {
   constexpr bool LJ = LJM == kLjmStore;
   constexpr int NQ = DP / 8;              // chunks of 8 dimensions (16 features)
   constexpr int NQH = NQ / 2;             // per half
@@ -385,6 +412,12 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   const int64_t tile = (int64_t)blockIdx.x * kWaves + rg;   // 32-row tile
   const int64_t row = tile * 32 + c;
   const bool valid = row < N;
+  // The stored branch of FGMM_FLAG_STORE_LOGJOINT_AUTO (default plan) is the ST
+  // instance: it also writes every log-joint tile, the rows' feature parts and logZ2
+  // pairs for diag_accum_ljt.  Both instances are launched; the probe's counts let
+  // one of them run.
+  static_assert(!ST || LJM == kLjmNeed, "the stored branch is the default plan's");
+  if (probe.count != nullptr && probe_selects(probe) != ST) return;
 
   // Blocks go global -> registers -> LDS.  Up to D = 96 through two register
   // stages: block kb + 2 is fetched while block kb is contracted and lands in LDS at
@@ -466,6 +499,26 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       for (int j = 0; j < 8; ++j) acc += fast_exp2((float)(ll[j] - ms));
       sm = acc;
       mx = mn;
+      if constexpr (ST) {
+        // This wave's 16 components of the 32 rows, row-major into the tile's columns
+        // 16H .. 16H + 15, transposed through the exchange slot just read (exr's: its
+        // writer, the other wave, writes it again only after the next barrier).  A
+        // lane holds local columns 4g .. 4g + 3 (ll[0..3]) and 8 + 4g .. (ll[4..7]);
+        // the 16-byte pieces of row r sit at piece p ^ ljd_swz(r).
+        float* tl = ex + ((size_t)(buf * kWaves + rg) * 2 + (1 - H)) * 8 * 64;
+        const int sw = ljd_swz(c);
+        *reinterpret_cast<f32x4*>(tl + c * 16 + 4 * (g ^ sw)) =
+            f32x4{(float)ll[0], (float)ll[1], (float)ll[2], (float)ll[3]};
+        *reinterpret_cast<f32x4*>(tl + c * 16 + 4 * ((2 + g) ^ sw)) =
+            f32x4{(float)ll[4], (float)ll[5], (float)ll[6], (float)ll[7]};
+        float* dst = ljd + (tile * KB + kb) * kLjTile + 16 * H;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int rr = 16 * u + (lane >> 2), pc = lane & 3;
+          *reinterpret_cast<f32x4*>(dst + rr * 32 + 4 * pc) =
+              *reinterpret_cast<const f32x4*>(tl + rr * 16 + 4 * (pc ^ ljd_swz(rr)));
+        }
+      }
       // Sparse stored log-joint (fgmm_common.hpp): this wave's 16 components of each
       // row (register groups 2H, 2H + 1), with their max in its half of the maxima.
       if constexpr (LJ)
@@ -525,6 +578,25 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     rowstat[row] = lz2;
     if (logZ) logZ[row] = (float)(lz2 * kLn2);
   }
+  if constexpr (ST) {
+    // The three bf16 parts of this wave's chunks of the row's features (row-major,
+    // ljd_rs(DP) apart, chunk q at columns 16 q .. 16 q + 15 as pass 1 orders them)
+    // and, from one wave, the row's logZ2 as a (hi, lo) float pair; +inf for a row
+    // past N, whose responsibilities are then exactly 0.
+    constexpr int RS = ljd_rs(DP);
+    __bf16* xp = xsplit + tile * (3 * 32 * RS) + c * RS + 8 * g;
+#pragma unroll
+    for (int qq = 0; qq < NQH; ++qq) {
+#pragma unroll
+      for (int t = 0; t < 3; ++t)
+        *reinterpret_cast<bf16x8*>(xp + t * 32 * RS + 16 * (h * NQH + qq)) = xb[qq][t];
+    }
+    if (h == 0 && g == 0) {
+      const float zh = valid ? (float)lz2 : INFINITY;
+      const float zl = (valid && lz2 > -INFINITY && lz2 < INFINITY) ? (float)(lz2 - (double)zh) : 0.0f;
+      zpair[tile * 32 + c] = make_float2(zh, zl);
+    }
+  }
   // Each wave's need masks from its own maxima; pass 2 ORs the two words.
   if constexpr (LJ) {
     if (g == 0)
@@ -543,6 +615,84 @@ void diag_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
       if (lane == 0 && nanbits != 0)
         for (int kb = 0; kb < KB; ++kb) ljmask[(tile * KB + kb) * 2 + h] |= nanbits;
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The probe of FGMM_FLAG_STORE_LOGJOINT_AUTO: one workgroup per sampled 32-row tile;
+// its waves take the component blocks in turn and form each row's block maximum R
+// of the log-joint in LDS.  An estimate suffices here, so the contraction keeps two
+// of pass 1's seven steps per 16-feature chunk (the centring step and x1 w1), each
+// row's chunks whole in one wave.  Then, per row, the blocks with R >= M -
+// kLjNeedGap (M the row's largest R) are counted: an estimate of the pairs pass 1
+// will mark as needed, since logZ2 >= M.  The tile's count is written; the kernels
+// that need the choice sum the counts themselves (probe_selects).
+// ---------------------------------------------------------------------------
+constexpr int kProbeWaves = 16;
+template <int DP>
+__global__ __launch_bounds__(64 * kProbeWaves) void diag_store_probe(const float* __restrict__ X, int64_t ldx,
+                                                                     int64_t N, int D,
+                                                                     const bf16x8* __restrict__ mu3,
+                                                                     const double* __restrict__ kc_x6, int KB,
+                                                                     int ntile, unsigned* __restrict__ count) {
+  constexpr int NQ = DP / 8;
+  __shared__ float rmax[kProbeMaxKB * 32];
+  __shared__ unsigned part[kProbeWaves];
+  const int s = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t tile = probe_tile(s, N, ntile);
+  const int64_t row = tile * 32 + c;
+  const bool valid = row < N;
+
+  bf16x8 xh[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const f32x4 x = load_row4(X, ldx, row, 8 * q + 4 * g, D, valid);
+    xh[q] = to_bf16x8(x * x, x);
+  }
+  const bf16x8 ones = x6c_ones(lane);
+  for (int kb = wave; kb < KB; kb += kProbeWaves) {
+    const bf16x8* mp = mu3 + (int64_t)kb * NQ * 4 * 64 + lane;
+    bf16x8 a0[NQ], a3[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      a0[q] = mp[(q * 4 + 0) * 64];
+      a3[q] = mp[(q * 4 + 3) * 64];
+    }
+    f32x16 acc[4] = {zero16(), zero16(), zero16(), zero16()};
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      acc[q & 3] = mfma_bf16(a3[q], ones, acc[q & 3]);
+      acc[q & 3] = mfma_bf16(a0[q], xh[q], acc[q & 3]);
+    }
+    const double* kp = kc_x6 + (int64_t)kb * 32 + g * 16;
+    double bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float xm = (acc[0][i] + acc[1][i]) + (acc[2][i] + acc[3][i]);
+      bm = fmax(bm, kp[i] + (double)xm);
+    }
+    const float R = lj_row_max(bm);
+    if (g == 0) rmax[kb * 32 + c] = R;
+  }
+  __syncthreads();
+  // Row c's maximum and needed blocks; the waves split the blocks again.
+  unsigned need = 0;
+  if (g == 0 && valid) {
+    float M = -INFINITY;
+    for (int kb = 0; kb < KB; ++kb) M = fmaxf(M, rmax[kb * 32 + c]);
+    for (int kb = wave; kb < KB; kb += kProbeWaves) need += (rmax[kb * 32 + c] - M >= -kLjNeedGap) ? 1u : 0u;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) need += __shfl_xor(need, o);
+  if (lane == 0) part[wave] = need;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned tot = 0;
+    for (int w = 0; w < kProbeWaves; ++w) tot += part[w];
+    count[s] = tot;
   }
 }
 
@@ -1454,13 +1604,15 @@ void diag_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
                        const bf16x8* __restrict__ mu3, const double* __restrict__ kc_x6lin, int KB, int KP,
                        const double* __restrict__ rowstat, const uint2* __restrict__ need, int nslab,
                        int64_t rows_per_slab, float* __restrict__ part_mu, float* __restrict__ part_sq,
-                       float* __restrict__ part_nk, int dense) {
+                       float* __restrict__ part_nk, int dense, ProbeSel sel) {
   constexpr int NQ = DP / 8;      // chunks of 8 dimensions (16 features)
   constexpr int NQH = NQ / 2;
   constexpr int NJ = DP / 32;
   constexpr int RS = gather_rs(DP);
   constexpr int BLK = NQ * 4 * 64;
   static_assert(NQ % 2 == 0, "two halves of chunks");
+  // The stored branch's diag_accum_ljt takes the call when the probe selects it.
+  if (probe_selects(sel)) return;
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
   unsigned char* lp = lds_raw;
@@ -1630,6 +1782,219 @@ void diag_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
     }
   }
   if (g == 0) part_nk[kbase + c] = nk;
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2 of the stored branch (FGMM_FLAG_STORE_LOGJOINT_AUTO, D <= 96): pass 1 left
+// per 32-row tile every block's log-joint tile, the rows' features [x^2 | x] in three
+// bf16 parts and logZ2 as (hi, lo) float pairs.  Per 16-row step, r is split in three
+// bf16 parts as well and r^T [x^2 | x] is accumulated from the six products of
+// significance at least 2^-16, smallest first (r3 f1, r2 f2, r1 f3, r2 f1, r1 f2,
+// r1 f1), as the gathering pass does: the sig identity in diag_reduce needs an fp32
+// step's accuracy of these moments.
+//
+// Grid over (row slab x group of 8 component blocks); wave w owns block 8 cg + w and
+// its partial of the slab; the workgroups of a slab run on one XCD, so the feature
+// parts come from HBM once.  Stages of one tile each (its feature parts, the 8
+// blocks' log-joint tiles, the logZ2 pairs), all filled by buffer-to-LDS loads,
+// three where they fit in LDS (D <= 32) and two above: at step t the workgroup
+// issues tile t + NS - 1's loads, computes tile t and waits for tile t + 1's.  Every
+// wave issues the same number of loads per tile (loads that only keep the count go
+// out of range into a pad line), so that wait is a fixed count.  A wave skips a
+// tile whose need words are both zero; otherwise it exponentiates the whole tile
+// with no per-row select: a row whose need bits are clear has l < logZ2 - kLjNeedGap
+// in every component of the block (pass 1's bounds are rounded up), so 2^(l - logZ2)
+// is exactly 0 in fp32, and a row past N has the pair (+inf, 0).  `sel` is the
+// probe's selector: the kernel returns unless it selects the stored branch.
+// ---------------------------------------------------------------------------
+constexpr int kLjdWaves = 8;
+
+template <int DP>
+struct LjdShape {
+  static constexpr int RS = ljd_rs(DP);
+  static constexpr int XB = (int)ljd_xsplit_bytes(DP);      // a tile's feature parts
+  static constexpr int XP = XB / 16;                         // their 16-byte pieces
+  static constexpr int XQ = (XP + 64 * kLjdWaves - 1) / (64 * kLjdWaves);
+  static constexpr int LJB = kLjdWaves * kLjTile * 4;        // the 8 blocks' log-joint tiles
+  static constexpr int OFF_X = LJB, OFF_Z = LJB + XB;
+  static constexpr int STAGE = LJB + XB + 32 * 8;
+  static constexpr int NS = (size_t)3 * STAGE + 1024 <= kMaxLds ? 3 : 2;
+  static constexpr int OFF_PAD = NS * STAGE;
+  static constexpr size_t lds = (size_t)OFF_PAD + 1024;
+  // Loads of every wave per tile: XQ of feature parts, 4 of its log-joint tile, 1 of
+  // logZ2 pairs (wave 0's; an out-of-range one elsewhere).
+  static constexpr int NLOADS = XQ + 4 + 1;
+};
+__host__ inline int64_t ljd_grid(int nslab, int ncg) { return (int64_t)8 * cdiv(nslab, 8) * ncg; }
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kLjdWaves, 64 * kLjdWaves), amdgpu_waves_per_eu(2, 2)))
+void diag_accum_ljt(const float* __restrict__ lj, const __bf16* __restrict__ xsplit, const float2* __restrict__ zpair,
+                    int64_t N, const uint2* __restrict__ need, ProbeSel sel, int KB, int KP, int nslab,
+                    int64_t rows_per_slab, int ncg, float* __restrict__ part_mu, float* __restrict__ part_sq,
+                    float* __restrict__ part_nk) {
+  using SH = LjdShape<DP>;
+  static_assert(SH::XP % 64 == 0, "whole waves of feature pieces");
+  static_assert(SH::lds <= kMaxLds, "stages exceed LDS");
+  constexpr int NJ = 2 * DP / 32;   // 32-feature column tiles
+  constexpr int RS = SH::RS;
+  constexpr int NS = SH::NS;
+  constexpr int NL = SH::NLOADS;
+  if (!probe_selects(sel)) return;
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  // Workgroup -> (slab, component group): the ncg groups of slab s run on XCD s % 8.
+  const int xcd = blockIdx.x & 7, item = blockIdx.x >> 3;
+  const int slab = (item / ncg) * 8 + xcd, cg = item % ncg;
+  if (slab >= nslab) return;   // uniform over the workgroup
+  const int kb = cg * kLjdWaves + wave;
+  const bool active = kb < KB;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
+  const int64_t tile0 = r_begin >> 5;   // rows_per_slab is a multiple of 32
+
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = zero16();
+  float nk = 0.0f;
+
+  // The wave's need words of tile t (0 past the slab or the blocks), ORed.
+  auto mword = [&](int t) -> unsigned {
+    const bool ok = active && t < ntiles;
+    const uint2 v = need[ok ? (tile0 + t) * KB + kb : 0];
+    return ok ? (v.x | v.y) : 0u;
+  };
+  unsigned char* const pad = lds_raw + SH::OFF_PAD;
+  auto issue = [&](int t, auto stage_tag, unsigned m) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage_tag)::value;
+    unsigned char* st = lds_raw + (size_t)S * SH::STAGE;
+    const bool in = t < ntiles;
+    const int64_t tg = tile0 + t;
+    const DmaSrc xsrc = dma_src(in ? reinterpret_cast<const unsigned char*>(xsplit) + tg * SH::XB
+                                   : reinterpret_cast<const unsigned char*>(xsplit),
+                                in ? (uint32_t)SH::XB : 0u);
+#pragma unroll
+    for (int q = 0; q < SH::XQ; ++q) {
+      if (q * 64 * kLjdWaves + wave * 64 < SH::XP)
+        lds_dma16(xsrc, st + SH::OFF_X + (q * 64 * kLjdWaves + wave * 64) * 16,
+                  (q * 64 * kLjdWaves + tid) * 16, 0);
+      else
+        lds_dma16(xsrc, pad, kBufOob, 0);
+    }
+    const DmaSrc lsrc = dma_src(m ? lj + (tg * KB + kb) * kLjTile : lj, m ? (uint32_t)(kLjTile * 4) : 0u);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) lds_dma16(lsrc, st + wave * kLjTile * 4 + q * 1024, (q * 64 + lane) * 16, 0);
+    if (wave == 0) {
+      const DmaSrc zsrc = dma_src(zpair + tg * 32 * (in ? 1 : 0), in ? (uint32_t)(32 * sizeof(float2)) : 0u);
+      if (lane < 16) lds_dma16(zsrc, st + SH::OFF_Z, lane * 16, 0);
+    } else {
+      lds_dma16(lsrc, pad, kBufOob, 0);
+    }
+  };
+  // Tile t in stage S: per 16-row half p, r in three parts (registers 8p .. 8p + 7 of
+  // the accumulator layout: lane = component, rows acc_row), then the six products
+  // for each column tile.
+  auto compute = [&](auto stage_tag) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage_tag)::value;
+    int sb = S * SH::STAGE;
+    asm volatile("" : "+s"(sb));
+    int lofs = sb + wave * kLjTile * 4 + 4 * c + 4 * 32 * 4 * g;
+    int zofs = sb + SH::OFF_Z + 4 * 8 * g;
+    asm volatile("" : "+v"(lofs), "+v"(zofs));
+    const float* lt = reinterpret_cast<const float*>(lds_raw + lofs);
+    const f32x4* zt = reinterpret_cast<const f32x4*>(lds_raw + zofs);
+    const __bf16* xt = reinterpret_cast<const __bf16*>(lds_raw + sb + SH::OFF_X);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      float r[8];
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * p + jj;   // registers 4j .. 4j + 3: rows 8j + 4g .. + 3
+        const f32x4 z01 = zt[4 * j], z23 = zt[4 * j + 1];
+        const float zh[4] = {z01[0], z01[2], z23[0], z23[2]}, zl[4] = {z01[1], z01[3], z23[1], z23[3]};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float rv = fast_exp2((lt[(8 * j + e) * 32] - zh[e]) - zl[e]);
+          r[4 * jj + e] = rv;
+          nk += rv;
+        }
+      }
+      bf16x8 a1, a2, a3;
+      acc_to_row_operands_split3(r, a1, a2, a3);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const bf16x8 f1 = lds_rows_operand(xt, RS, 16 * p, 32 * j, lane);
+        const bf16x8 f2 = lds_rows_operand(xt + 32 * RS, RS, 16 * p, 32 * j, lane);
+        const bf16x8 f3 = lds_rows_operand(xt + 64 * RS, RS, 16 * p, 32 * j, lane);
+        acc[j] = mfma_bf16(a3, f1, acc[j]);
+        acc[j] = mfma_bf16(a2, f2, acc[j]);
+        acc[j] = mfma_bf16(a1, f3, acc[j]);
+        acc[j] = mfma_bf16(a2, f1, acc[j]);
+        acc[j] = mfma_bf16(a1, f2, acc[j]);
+        acc[j] = mfma_bf16(a1, f1, acc[j]);
+      }
+    }
+  };
+
+  unsigned mk[NS];
+  unsigned mnext = 0u;
+  // Step t, stage S = t mod NS: issue tile t + NS - 1 (its stage was freed by the last
+  // barrier), compute tile t, wait for tile t + 1's stage (the loads issued after it
+  // are those of tiles t + 2 ..), barrier.
+  auto step = [&](int t, auto stage_tag) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage_tag)::value;
+    constexpr int SI = (S + NS - 1) % NS;
+    mk[SI] = mnext;
+    issue(t + NS - 1, std::integral_constant<int, SI>{}, mnext);
+    mnext = mword(t + NS);
+    if (mk[S] != 0u) compute(stage_tag);
+    vm_wait<(NS - 2) * NL>();
+    __syncthreads();
+  };
+  if (ntiles > 0) {
+#pragma unroll
+    for (int u = 0; u < NS - 1; ++u) mk[u] = mword(u);
+    issue(0, std::integral_constant<int, 0>{}, mk[0]);
+    if constexpr (NS == 3) issue(1, std::integral_constant<int, 1>{}, mk[1]);
+    mnext = mword(NS - 1);
+    vm_wait<(NS - 2) * NL>();   // tile 0's stage
+    __syncthreads();
+  }
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2 % NS>;
+  for (int t = 0; t < ntiles; t += NS) {
+    step(t, S0{});
+    if (t + 1 >= ntiles) break;
+    step(t + 1, S1{});
+    if constexpr (NS == 3) {
+      if (t + 2 >= ntiles) break;
+      step(t + 2, S2{});
+    }
+  }
+  vm_wait<0>();   // no buffer-to-LDS load outlives the workgroup
+
+  if (active) {
+    nk += __shfl_xor(nk, 32);
+    const int64_t kbase = (int64_t)slab * KP + (int64_t)kb * 32;
+    // Column f of the feature parts is x^2 (f % 8 < 4) or x of dimension
+    // 8 (f / 16) + 4 ((f / 8) % 2) + f % 4.
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int f = 32 * j + c;
+      const int dim = 8 * (f >> 4) + 4 * ((f >> 3) & 1) + (f & 3);
+      float* dst = ((f & 7) < 4 ? part_sq : part_mu) + dim;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dst[(kbase + acc_row(i, g)) * DP] = acc[j][i];
+    }
+    if (g == 0) part_nk[kbase + c] = nk;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1966,21 +2331,45 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
   float* pmu = reinterpret_cast<float*>(ws + pl.off_part_mu);
   float* psq = reinterpret_cast<float*>(ws + pl.off_part_sq);
   float* pnk = reinterpret_cast<float*>(ws + pl.off_part_nk);
+  // FGMM_FLAG_STORE_LOGJOINT_AUTO: the probe's counts, which pass 1 and both pass-2
+  // kernels read to select the stored branch.
+  unsigned* probe = pl.autolj ? reinterpret_cast<unsigned*>(ws + pl.off_probe) : nullptr;
+  const ProbeSel psel = probe ? ProbeSel{probe, pl.nprobe, probe_min_pairs(pl.N, pl.nprobe, pl.KB)}
+                              : ProbeSel{nullptr, 0, 0};
   if (run1) {
     const unsigned nblk1 = (unsigned)cdiv(pl.N, 32 * kWaves);
     if constexpr (diag_uses_x6(DP)) {
-      const size_t lds1 = x6_lds_bytes<DP>() + (pl.rexact ? (size_t)kAccWaves * 32 * pl.KB * 2 : 0);
-      auto kern = pl.lj ? &diag_lse_x6<DP, kLjmStore> : &diag_lse_x6<DP, kLjmNeed>;
-      if (lds1 > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
-        if (e != hipSuccess) return e;
+      if constexpr (ljd_applies(DP)) {
+        if (pl.autolj)
+          hipLaunchKernelGGL((diag_store_probe<DP>), dim3((unsigned)pl.nprobe), dim3(64 * kProbeWaves), 0, stream,
+                             X, ldx, pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
+                             reinterpret_cast<const double*>(ws + pl.off_kcx6), pl.KB, pl.nprobe, probe);
       }
+      const size_t lds1 = x6_lds_bytes<DP>() + (pl.rexact ? (size_t)kAccWaves * 32 * pl.KB * 2 : 0);
       uint2* masks = pl.need ? reinterpret_cast<uint2*>(ws + pl.off_ljmask) : ljmask;
-      hipLaunchKernelGGL(kern, dim3(nblk1), dim3(kAccThreads), lds1, stream, X, ldx, pl.N, (int)pl.D,
-                         reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
-                         reinterpret_cast<const double*>(ws + pl.off_kcx6), pl.KB, logZ, rowstat, lj,
-                         ljmax, reinterpret_cast<unsigned*>(masks), ljcount, dense ? 1 : 0, pl.rexact ? 1 : 0);
+      auto launch1 = [&](auto kern) -> hipError_t {
+        if (lds1 > 65536) {
+          hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
+          if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL(kern, dim3(nblk1), dim3(kAccThreads), lds1, stream, X, ldx, pl.N, (int)pl.D,
+                           reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
+                           reinterpret_cast<const double*>(ws + pl.off_kcx6), pl.KB, logZ, rowstat, lj,
+                           ljmax, reinterpret_cast<unsigned*>(masks), ljcount, dense ? 1 : 0, pl.rexact ? 1 : 0,
+                           psel, pl.autolj ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr,
+                           reinterpret_cast<__bf16*>(ws + pl.off_xsplit),
+                           reinterpret_cast<float2*>(ws + pl.off_zpair));
+        return hipSuccess;
+      };
+      hipError_t e1 = launch1(pl.lj ? &diag_lse_x6<DP, kLjmStore> : &diag_lse_x6<DP, kLjmNeed>);
+      if (e1 != hipSuccess) return e1;
+      if constexpr (ljd_applies(DP)) {
+        if (pl.autolj) {
+          e1 = launch1(&diag_lse_x6<DP, kLjmNeed, true>);
+          if (e1 != hipSuccess) return e1;
+        }
+      }
     } else {
       return hipErrorInvalidValue;   // launch_ctile runs pass 1 above D = 128
     }
@@ -1989,6 +2378,23 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
   const dim3 grid2((unsigned)(pl.nslab * pl.ncg));
   if constexpr (diag_uses_x6(DP)) {
     if (pl.need) {
+      // With the stored branch both pass-2 kernels are launched over the same slabs and
+      // partials; the probe's selector lets one of them run.
+      if constexpr (ljd_applies(DP)) {
+        if (pl.autolj) {
+          using SH = LjdShape<DP>;
+          hipError_t ej = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum_ljt<DP>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)SH::lds);
+          if (ej != hipSuccess) return ej;
+          const int ncg = (int)cdiv(pl.KB, kLjdWaves);
+          hipLaunchKernelGGL((diag_accum_ljt<DP>), dim3((unsigned)ljd_grid(pl.nslab, ncg)), dim3(64 * kLjdWaves),
+                             SH::lds, stream, reinterpret_cast<const float*>(ws + pl.off_lj),
+                             reinterpret_cast<const __bf16*>(ws + pl.off_xsplit),
+                             reinterpret_cast<const float2*>(ws + pl.off_zpair), pl.N,
+                             reinterpret_cast<const uint2*>(ws + pl.off_ljmask), psel, pl.KB, pl.KP, pl.nslab,
+                             pl.rows_per_slab, ncg, pmu, psq, pnk);
+        }
+      }
       constexpr size_t lds = gather_lds_bytes(DP);
       static_assert(lds <= kMaxLds, "gathering pass 2 exceeds LDS");
       hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&diag_accum_gather<DP>),
@@ -1999,7 +2405,7 @@ hipError_t launch_passes(const DiagPlan& pl, const float* X, int64_t ldx, unsign
                          reinterpret_cast<const bf16x8*>(ws + pl.off_mu3),
                          reinterpret_cast<const double*>(ws + pl.off_kcx6lin), pl.KB, pl.KP, rowstat,
                          reinterpret_cast<const uint2*>(ws + pl.off_ljmask), pl.nslab, pl.rows_per_slab,
-                         pmu, psq, pnk, dense ? 1 : 0);
+                         pmu, psq, pnk, dense ? 1 : 0, psel);
       return hipGetLastError();
     }
     if (pl.lj_sparse) {
@@ -3173,7 +3579,7 @@ extern "C" size_t fgmm_diag_workspace_bytes(int64_t N, int64_t K, int64_t D) {
 extern "C" size_t fgmm_diag_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, unsigned flags) {
   if (N < 0 || K < 0 || D < 1) return 0;
   const int64_t rows = diag_bw_call(D, flags) ? std::min(N, diag_bw_chunk_rows(K)) : N;
-  return make_plan(rows, K, D, wants_stored_lj(flags), (flags & FGMM_FLAG_BF16) != 0).total;
+  return make_plan(rows, K, D, wants_stored_lj(flags), (flags & FGMM_FLAG_BF16) != 0, wants_auto_lj(flags)).total;
 }
 
 extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -3214,7 +3620,7 @@ extern "C" int fgmm_diag_estep_f32(const float* X, int64_t ldx, int64_t N, int64
   // The stored-log-joint pass 2 addresses X tiles with 32-bit buffer offsets (row
   // stride at most kMaxBufLdx floats); wider strides recompute, which needs less
   // workspace.
-  const DiagPlan pl = make_plan(N, K, D, wants_stored_lj(flags) && ldx <= kMaxBufLdx, bf16);
+  const DiagPlan pl = make_plan(N, K, D, wants_stored_lj(flags) && ldx <= kMaxBufLdx, bf16, wants_auto_lj(flags));
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;
   if (!want_logz) logZ = nullptr;
   unsigned char* ws = static_cast<unsigned char*>(workspace);

@@ -185,31 +185,6 @@ __host__ __device__ constexpr size_t bf16_lse_lds_base(int DP) {
   return (size_t)2 * (DP / 16) * 64 * 16 + (size_t)2 * 32 * 16;   // mu blocks (bf16x8) and constants (f32x4)
 }
 constexpr int kLjtWavesPlan = 8;   // component blocks per stored pass-2 workgroup up to D = 128 (iso_accum_ljt)
-// The stored-log-joint probe (FGMM_FLAG_STORE_LOGJOINT_AUTO): up to kProbeTiles
-// 32-row tiles spread over the rows, one count of needed (row, block) pairs per
-// tile; at least half of the sampled pairs selects the stored branch.  Up to
-// kProbeMaxKB blocks (the probe keeps a tile's block maxima in LDS).
-constexpr int kProbeTiles = 64;
-constexpr int kProbeMaxKB = 512;
-__host__ __device__ constexpr size_t probe_bytes() { return (size_t)kProbeTiles * sizeof(unsigned); }
-// What a kernel needs to evaluate the probe's choice (count == nullptr: no probe).
-struct ProbeSel {
-  const unsigned* count;
-  int n;
-  int64_t min_pairs;
-};
-// The stored branch is selected (uniform; false without a probe).
-__device__ __forceinline__ bool probe_selects(const ProbeSel& p) {
-  if (p.count == nullptr) return false;
-  const int lane = threadIdx.x & 63;
-  unsigned v = lane < p.n ? p.count[lane] : 0u;
-  uint64_t t = v;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o);
-  const uint64_t tot = (uint64_t)__builtin_amdgcn_readfirstlane((unsigned)t) |
-                       ((uint64_t)__builtin_amdgcn_readfirstlane((unsigned)(t >> 32)) << 32);
-  return (int64_t)tot >= p.min_pairs;
-}
 __host__ __device__ constexpr int gather_rs(int DP) { return DP + 16; }   // bf16 row stride of the X tiles
 // The stored plan's bf16 X tiles (hi, lo; 32 rows at that stride) up to D = 128.
 __host__ __device__ constexpr size_t ljt_xsplit_bytes(int DP) { return (size_t)2 * 32 * gather_rs(DP) * 2; }
@@ -899,7 +874,7 @@ __global__ __launch_bounds__(64 * kProbeWaves) void iso_store_probe(const float*
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, g = lane >> 5;
-  const int64_t tile = (int64_t)s * cdiv(N, 32) / ntile;
+  const int64_t tile = probe_tile(s, N, ntile);
   const int64_t row = tile * 32 + c;
   const bool valid = row < N;
 
@@ -962,15 +937,6 @@ __global__ __launch_bounds__(64 * kProbeWaves) void iso_store_probe(const float*
   }
 }
 
-// The probe's threshold: half of the sampled (row, block) pairs.
-__host__ inline int64_t probe_min_pairs(int64_t N, int ntile, int KB) {
-  int64_t rows = 0;
-  for (int s = 0; s < ntile; ++s) {
-    const int64_t t = (int64_t)s * cdiv(N, 32) / ntile;
-    rows += std::min<int64_t>(32, N - t * 32);
-  }
-  return cdiv(rows * KB, 2);
-}
 
 // ---------------------------------------------------------------------------
 // Pass 1 of the default plan above D = 128 (any D).  The split operands of a row
@@ -2470,11 +2436,6 @@ struct LjtShape {
 };
 __host__ inline int64_t ljt_grid(int nslab, int ncg) { return (int64_t)8 * cdiv(nslab, 8) * ncg; }
 
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  static_assert(N >= 0 && N <= 63, "vmcnt field");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 
 template <int DP>
 __global__ __attribute__((amdgpu_flat_work_group_size(64 * kLjtWaves, 64 * kLjtWaves), amdgpu_waves_per_eu(2, 2)))

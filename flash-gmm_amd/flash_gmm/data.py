@@ -149,6 +149,19 @@ def reference_smoke(N: int = 1_000_000, K: int = 1024, D: int = 128, seed: int =
     return dict(X=X, mu=mu, log_sigma_sq=lss, log_pi=lpi)
 
 
+def diag_reference_smoke(N: int = 1_000_000, K: int = 1024, D: int = 96, seed: int = 0,
+                         device="cpu") -> Dict[str, torch.Tensor]:
+    """The reference smoke workload's data (flash_gmm.py:228-234: X, mu ~ N(0, I),
+    uniform weights) for the diagonal model, with per-dimension variances
+    log sigma^2 ~ N(0, 0.2^2): every component is within reach of every row."""
+    g = _gen(device, seed)
+    X = _randn(g, N, D, device=device)
+    mu = _randn(g, K, D, device=device)
+    lss = 0.2 * _randn(g, K, D, device=device)
+    lpi = torch.full((K,), -math.log(K), device=device)
+    return dict(X=X, mu=mu, log_sigma_sq=lss, log_pi=lpi)
+
+
 WORKLOADS = {
     # name: (generator, default sizes, default seed)
     "iso_n10k_k64_d32": (iso_plain, dict(N=10_000, K=64, D=32), 0),
@@ -158,6 +171,8 @@ WORKLOADS = {
     # the reference's own smoke workload (flash_gmm.py:228-234): nearly every
     # responsibility is nonzero, so no accumulation work can be skipped
     "iso_ref_n1m_k1024_d128": (reference_smoke, dict(N=1_000_000, K=1024, D=128), 0),
+    # the same dense regime for the diagonal model at its benchmark shape
+    "diag_ref_n1m_k1024_d96": (diag_reference_smoke, dict(N=1_000_000, K=1024, D=96), 0),
     # wider shapes (split-dimension accumulation paths)
     "diag_n1m_k256_d256": (diag_clustered, dict(N=1_000_000, K=256, D=256), 5),
     "full_n100k_k64_d128": (full_clustered, dict(N=100_000, K=64, D=128), 6),

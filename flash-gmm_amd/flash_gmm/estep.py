@@ -222,14 +222,15 @@ def iso_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
 AUTO_STORE_MEMORY_FRACTION = 1.0 / 8
 
 
-def _auto_store(N, K, D, dev, precision):
+def _auto_store(N, K, D, dev, precision, model="iso"):
     """store_log_joint for the drop-in call: "auto" where its workspace is modest."""
     if precision != "fp32" or N == 0 or K == 0:
         return False
     L = _lib.lib()
+    ws_ex = getattr(L, f"fgmm_{model}_workspace_bytes_ex")
+    ws = getattr(L, f"fgmm_{model}_workspace_bytes")
     with torch.cuda.device(dev):
-        extra = int(L.fgmm_iso_workspace_bytes_ex(N, K, D, _lib.FLAG_STORE_LOGJOINT_AUTO)) - \
-            int(L.fgmm_iso_workspace_bytes(N, K, D))
+        extra = int(ws_ex(N, K, D, _lib.FLAG_STORE_LOGJOINT_AUTO)) - int(ws(N, K, D))
         total = torch.cuda.get_device_properties(dev).total_memory
     return "auto" if 0 < extra <= total * AUTO_STORE_MEMORY_FRACTION else False
 
@@ -263,9 +264,12 @@ def flash_gmm_estep(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.Tenso
 def diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, *,
                     accumulate: bool = False, atomic_reduce: bool = False,
                     workspace: torch.Tensor | None = None, phase: int = 0, dense: bool = False,
-                    recompute: bool = False, store_log_joint: bool = False,
+                    recompute: bool = False, store_log_joint: bool | str = False,
                     precision: str = "fp32") -> None:
     """Diagonal-covariance E-step into caller-provided outputs (sig_acc is (K, D)).
+
+    The plan arguments are iso_estep_into's; ``store_log_joint="auto"`` applies up
+    to D = 96 (above, the call runs the default plan).
 
     ``precision="bf16"`` selects the bf16 operand contract of the reference's
     diagonal H100 kernels (flash_gmm_diag_h100.py:63-130, :159-282): x, x^2 and the
@@ -312,7 +316,9 @@ def flash_gmm_estep_diag(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.
 
     sig_acc[k, d] = sum_n r_nk (x_nd - mu_kd)^2 (flash_gmm_diag_h100.py:258-260).
     ``precision="bf16"`` follows the reference kernels' bf16 operand contract
-    instead of fp32 arithmetic.
+    instead of fp32 arithmetic.  Up to D = 96 the call runs with
+    store_log_joint="auto" (see diag_estep_into) while that workspace takes at most
+    AUTO_STORE_MEMORY_FRACTION of the device's memory.
     """
     _check_common(X, mu, log_pi)
     N, D = X.shape
@@ -324,7 +330,8 @@ def flash_gmm_estep_diag(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.
     Nk = torch.empty(K, device=dev, dtype=torch.float32)
     mu_acc = torch.empty(K, D, device=dev, dtype=torch.float32)
     sig_acc = torch.empty(K, D, device=dev, dtype=torch.float32)
-    diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, precision=precision)
+    diag_estep_into(X, mu, log_sigma_sq, log_pi, logZ, Nk, mu_acc, sig_acc, precision=precision,
+                    store_log_joint=_auto_store(N, K, D, dev, precision, "diag"))
     return logZ, Nk, mu_acc, sig_acc
 
 

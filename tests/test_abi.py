@@ -97,9 +97,6 @@ def test_iso_workspace_holds_stored_log_joint():
     for n, k, d in [(N, K, 32), (N, 96, 128), (N, 96, 192), (20_000_000, 1024, 128)]:
         assert L.fgmm_iso_workspace_bytes(n, k, d) == L.fgmm_iso_workspace_bytes_ex(n, k, d, S)
     assert L.fgmm_iso_workspace_bytes(20_000_000, K, D) == L.fgmm_iso_workspace_bytes_ex(20_000_000, K, D, A)
-    # Not stored: D <= 32, K <= 96, or more than 16 GiB of tiles.
-    for n, k, d in [(N, K, 32), (N, 96, 128), (N, 96, 192), (20_000_000, 1024, 128)]:
-        assert L.fgmm_iso_workspace_bytes(n, k, d) == L.fgmm_iso_workspace_bytes_ex(n, k, d, S)
     pairs = -(-N // 128) * 4 * (K // 32)
     # Diagonal: stored for K > 96 at every D.
     d_stored = L.fgmm_diag_workspace_bytes_ex(N, K, 96, S)
@@ -107,6 +104,16 @@ def test_iso_workspace_holds_stored_log_joint():
     assert d_lean == L.fgmm_diag_workspace_bytes_ex(N, K, 96, R) == L.fgmm_diag_workspace_bytes_ex(N, K, 96, 0)
     assert d_stored - d_lean >= pairs * (4096 + 256)
     assert L.fgmm_diag_workspace_bytes(N, 96, 96) == L.fgmm_diag_workspace_bytes_ex(N, 96, 96, S)
+    # Diagonal STORE_LOGJOINT_AUTO (D <= 96): the log-joint tiles and per 32-row tile
+    # the rows' features [x^2 | x] in three bf16 parts (3 x 32 x (2 D + 16) x 2 bytes)
+    # and logZ pairs, tiles rounded to 4 per pass-1 workgroup, and the probe's counts.
+    d_auto = L.fgmm_diag_workspace_bytes_ex(N, K, 96, A)
+    tiles = -(-N // 128) * 4
+    dextra = tiles * ((K // 32) * 4096 + 3 * 32 * (2 * 96 + 16) * 2 + 256)
+    assert dextra <= d_auto - d_lean <= dextra + 4 * 256
+    assert L.fgmm_diag_workspace_bytes_ex(N, K, 96, A | R) == d_lean
+    assert L.fgmm_diag_workspace_bytes_ex(N, K, 96, A | S) == d_stored
+    assert L.fgmm_diag_workspace_bytes_ex(N, K, 128, A) == L.fgmm_diag_workspace_bytes(N, K, 128)
     # Full: stored whenever it fits, 32 floats per (32-row tile, component).
     q, qx = L.fgmm_full_workspace_bytes, L.fgmm_full_workspace_bytes_ex
     assert q(5000, 64, 64) == qx(5000, 64, 64, 0) == qx(5000, 64, 64, R) > 0

@@ -263,3 +263,92 @@ def test_atomic_reduce_matches_the_tree(gpu_device):
     torch.cuda.synchronize()
     for u, v in zip(acc_out[1:], acc[1:]):
         torch.testing.assert_close(u, 2 * v, rtol=1e-5, atol=1e-5 * float(v.abs().max()))
+
+
+# FGMM_FLAG_STORE_LOGJOINT_AUTO (store_log_joint="auto", D <= 96): the device-selected
+# stored branch (diag_accum_ljt) on dense data, the default plan elsewhere.
+DIAG_AUTO_DENSE_SHAPES = [(20000, 256, 96), (9000, 300, 64), (5000, 130, 61), (3000, 64, 32), (777, 40, 90),
+                          (4099, 520, 80)]
+
+
+@pytest.mark.parametrize("N,K,D", DIAG_AUTO_DENSE_SHAPES)
+def test_auto_store_dense_takes_stored_branch(N, K, D, gpu_device):
+    """On dense data (X, mu ~ N(0, I), per-dimension variances near 1) the probe selects
+    the stored branch: its statistics differ from the default plan's in the last bits
+    (another summation) and agree with the oracle."""
+    inp = data.diag_reference_smoke(N, K, D, seed=N % 97)
+    auto = _into(inp, gpu_device, store_log_joint="auto")
+    base = _into(inp, gpu_device)
+    assert any(not torch.equal(u, v) for u, v in zip(auto[1:], base[1:]))
+    ref = oracle(inp)
+    check_wide(auto, inp, f"diag auto dense N={N} K={K} D={D}", D, ref=ref)
+    check_wide(base, inp, f"diag default dense N={N} K={K} D={D}", D, ref=ref)
+
+
+@pytest.mark.parametrize("N,K,D", [(20000, 1024, 96), (9000, 300, 64), (5000, 512, 90), (3000, 300, 128)])
+def test_auto_store_clustered_is_the_default_plan(N, K, D, gpu_device):
+    """On clustered data with many components the probe keeps the default plan, and
+    above D = 96 the flag does not apply: every output bitwise equal to a call
+    without the flag.  (At D = 32 the axis-aligned clusters overlap enough that most
+    (row, block) pairs are needed, and the stored branch is the probe's choice.)"""
+    inp = data.diag_clustered(N, K, D, seed=K % 13 + D)
+    auto = _into(inp, gpu_device, store_log_joint="auto")
+    base = _into(inp, gpu_device)
+    for u, v in zip(auto, base):
+        assert torch.equal(u, v)
+
+
+@pytest.mark.parametrize("kind", ["dense", "clustered"])
+def test_auto_store_phase_split_and_reuse(kind, gpu_device):
+    """PHASE1 then PHASE2 on one workspace equals the single call bitwise, and calls
+    alternating between dense and clustered data on that workspace each select their
+    own branch."""
+    from flash_gmm import _lib
+    L = _lib.lib()
+    dev = gpu_device
+    dense_inp = data.diag_reference_smoke(6000, 256, 96, seed=4)
+    clus_inp = data.diag_clustered(6000, 256, 96, seed=5)
+    inp = dense_inp if kind == "dense" else clus_inp
+    other = clus_inp if kind == "dense" else dense_inp
+    N, D = inp["X"].shape
+    K = inp["mu"].shape[0]
+    ws = torch.empty(L.fgmm_diag_workspace_bytes_ex(N, K, D, _lib.FLAG_STORE_LOGJOINT_AUTO), dtype=torch.uint8,
+                     device=dev)
+    ref = _into(inp, dev, store_log_joint="auto")
+    ref_other = _into(other, dev, store_log_joint="auto")
+    for _ in range(2):
+        for cur, want in ((inp, ref), (other, ref_other)):
+            out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+                   torch.empty(K, D, device=dev)]
+            args = [cur[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
+            diag_estep_into(*args, *out, workspace=ws, phase=1, store_log_joint="auto")
+            diag_estep_into(*args, None, *out[1:], workspace=ws, phase=2, store_log_joint="auto")
+            torch.cuda.synchronize()
+            for u, v in zip(out, want):
+                assert torch.equal(u, v)
+
+
+def test_auto_store_full_size_dense(gpu_device):
+    """The dense regime at the benchmark shape (N = 1M, K = 1024, D = 96) through the
+    drop-in call, which takes the stored branch: invariants over all rows (sum Nk = N,
+    sum mu_acc = sum X, the sig identity against sum X^2 - ...) and all four outputs
+    against the oracle on a 32,768-row prefix run on its own."""
+    dev = gpu_device
+    inp = data.make("diag_ref_n1m_k1024_d96", device=dev)
+    X = inp["X"]
+    got = flash_gmm_estep_diag(X, inp["mu"], inp["log_sigma_sq"], inp["log_pi"])
+    base = _into({k: v for k, v in inp.items()}, dev)
+    torch.cuda.synchronize()
+    N = X.shape[0]
+    assert abs(got[1].double().sum().item() - N) <= 1e-4 * N
+    torch.testing.assert_close(got[2].double().sum(0), X.double().sum(0), rtol=1e-4, atol=1e-3 * N ** 0.5)
+    # The stored branch and the default plan agree on all rows: logZ (pass 1 of both,
+    # another instance of the kernel) to 1e-5, the statistics to 1e-5 of each
+    # output's largest magnitude.
+    assert float((got[0] - base[0]).abs().max()) <= 1e-5
+    for u, v in zip(got[1:], base[1:]):
+        assert float((u - v).abs().max()) <= 1e-5 * float(v.abs().max())
+    sub = {k: (v[:32768].cpu() if k == "X" else v.cpu()) for k, v in inp.items()}
+    part = flash_gmm_estep_diag(*[sub[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")])
+    torch.cuda.synchronize()
+    check_wide(part, sub, "diag auto N=32768 K=1024 D=96 dense", 96)
