@@ -61,6 +61,11 @@ struct FullPlan {
   int nstrip;   // wide pass 2: strips of upper sig_outer blocks (one wave each)
   int ngrp;     // waves per (slab, component) in the gathering pass 2 (groups of sig blocks)
   int grid1;    // pass-1 workgroups with need masks (a persistent grid)
+  bool autolj;  // default plan with a stored branch that a row-sample probe selects on the device
+                // (FGMM_FLAG_STORE_LOGJOINT_AUTO, D <= 64): pass 1 also keeps the log-joint, and
+                // full_accum_ljt reads r from it over the same slabs and partials
+  int nprobe;   // the probe's sampled tiles
+  size_t off_probe;
   size_t off_lop, off_bsw, off_ck, off_l3, off_esw, off_rowstat, off_part_sig, off_part_mu, off_part_nk,
       off_lj, off_need, off_bound, total;
 };
@@ -70,6 +75,10 @@ struct FullPlan {
 // of its rows' log-joint in the workspace, reused tile after tile; beyond this many
 // components the masks come from the running-max bound instead.
 constexpr int kNeedExactMaxK = 1024;
+
+// The stored branch of FGMM_FLAG_STORE_LOGJOINT_AUTO runs up to D = 64 (sig_outer's
+// accumulators and split operands of one component fit a wave's registers).
+__host__ __device__ constexpr bool flj_applies(int DP) { return DP <= 64; }
 
 
 
@@ -117,7 +126,8 @@ __host__ __device__ constexpr int bf16_comps_per_wg(int NMB);
 __host__ __device__ constexpr int bf16_comp_reps(int NMB);
 __host__ __device__ constexpr int bf16_row_groups(int NMB);
 
-FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool bf16 = false) {
+FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool bf16 = false,
+                   bool auto_lj = false) {
   FullPlan p{};
   p.N = N; p.K = K; p.D = D;
   p.DP = (int)round_up(D < 1 ? 1 : D, 32);
@@ -135,6 +145,9 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   // blocks), each of which would whiten the needed rows again; 4 bytes per (row,
   // component) of stored log-joint replace those D x D whitenings.
   p.keep_lj = p.need && p.DP > 128 && !p.wide && full_lj_bytes(N, p.KP) <= kMaxLjBytes;
+  p.autolj = p.need && auto_lj && flj_applies(p.DP) && N > 0 && K <= kProbeMaxKB &&
+             full_lj_bytes(N, p.KP) <= kMaxLjBytes;
+  p.nprobe = p.autolj ? (int)std::min<int64_t>(kProbeTiles, cdiv(N, 32)) : 0;
   p.rexact = p.need && K <= kNeedExactMaxK;
   p.ngrp = gather_sig_groups(p.DP);
   if (bf16) {
@@ -199,7 +212,7 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.off_part_mu = off;  off = align256(off + (size_t)p.npart * p.KP * p.DP * sizeof(float));
   p.off_part_nk = off;  off = align256(off + (size_t)p.npart * p.KP * sizeof(float));
   p.off_lj = off;
-  if (p.lj || p.keep_lj) off = align256(off + full_lj_bytes(N, p.KP));
+  if (p.lj || p.keep_lj || p.autolj) off = align256(off + full_lj_bytes(N, p.KP));
   // Need masks: one word per (32-row tile of the pass-1 grid, component).
   p.grid1 = 0;
   p.off_need = off;
@@ -209,6 +222,8 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
     p.grid1 = (int)std::min<int64_t>(cdiv(N, 32 * kWaves), (int64_t)full_waves_per_eu(p.DP) * current_device_cus());
     if (p.rexact) off = align256(off + (size_t)p.grid1 * kWaves * 32 * p.KP * sizeof(unsigned short));
   }
+  p.off_probe = off;
+  if (p.autolj) off = align256(off + probe_bytes());
   p.total = off;
   return p;
 }
@@ -340,9 +355,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
 void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, const bf16x8* __restrict__ l3,
                  const double* __restrict__ esw, const double* __restrict__ ck, int K, int KP,
                  float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj,
-                 unsigned* __restrict__ need, unsigned short* __restrict__ bound, int rexact, int dense) {
+                 unsigned* __restrict__ need, unsigned short* __restrict__ bound, int rexact, int dense,
+                 ProbeSel probe) {
   constexpr bool LJ = LJM == kLjmStore || KEEP;
   static_assert(!KEEP || LJM == kLjmNeed, "KEEP adds the log-joint to the need masks");
+  // FGMM_FLAG_STORE_LOGJOINT_AUTO launches both need-mask instances; the probe's
+  // counts let the KEEP one (the stored branch) or the other run.
+  if (probe.count != nullptr && probe_selects(probe) != KEEP) return;
   constexpr int NMB = DP / 32, NQ = DP / 16;
   constexpr int SMB = full_x6_smb<DP>();          // coordinate blocks per stage
   constexpr int NST = NMB / SMB;                  // stages per component
@@ -467,6 +486,81 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
         for (int k = 0; k < K; ++k) need[tile * KP + k] |= nanbits;
     }
   }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The probe of FGMM_FLAG_STORE_LOGJOINT_AUTO (D <= 64, K <= kProbeMaxKB): one
+// workgroup per sampled 32-row tile; its waves take the components in turn and form
+// each row's log-joint in LDS from the whitening's centring step and x1 L1 product
+// only (an error of a few log2 units against the kLjNeedGap = 160 margin).  Then,
+// per row, the components with ll >= M - kLjNeedGap (M the row's largest) are
+// counted: an estimate of the pairs pass 1 marks as needed.  The tile's count is
+// written; the kernels that need the choice sum the counts (probe_selects).
+// ---------------------------------------------------------------------------
+constexpr int kProbeWaves = 16;
+template <int DP>
+__global__ __launch_bounds__(64 * kProbeWaves) void full_store_probe(const float* __restrict__ X, int64_t ldx,
+                                                                     int64_t N, int D,
+                                                                     const bf16x8* __restrict__ l3,
+                                                                     const double* __restrict__ esw,
+                                                                     const double* __restrict__ ck, int K,
+                                                                     int ntile, unsigned* __restrict__ count) {
+  constexpr int NMB = DP / 32, NQ = DP / 16;
+  __shared__ float lmax[kProbeMaxKB * 32];
+  __shared__ unsigned part[kProbeWaves];
+  const int s = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int64_t tile = probe_tile(s, N, ntile);
+  const int64_t row = tile * 32 + c;
+  const bool valid = row < N;
+
+  bf16x8 xh[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int d0 = 16 * q + 8 * g;
+    xh[q] = to_bf16x8(load_row4(X, ldx, row, d0, D, valid), load_row4(X, ldx, row, d0 + 4, D, valid));
+  }
+  const bf16x8 ones = x6c_ones(lane);
+  const double hl = 0.5 * kLog2e;
+  for (int k = wave; k < K; k += kProbeWaves) {
+    double maha = 0.0;
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+      const bf16x8* lp = l3 + ((int64_t)k * NMB + mb) * NQ * 4 * 64 + lane;
+      f32x16 acc[2] = {zero16(), zero16()};
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        acc[q & 1] = mfma_bf16(lp[(q * 4 + 3) * 64], ones, acc[q & 1]);
+        acc[q & 1] = mfma_bf16(lp[(q * 4 + 0) * 64], xh[q], acc[q & 1]);
+      }
+      const double* eb = esw + ((int64_t)k * NMB + mb) * 32 + g * 16;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const double v = (double)(acc[0][i] + acc[1][i]) + eb[i];
+        maha = fma(v, v, maha);
+      }
+    }
+    maha += __shfl_xor(maha, 32);
+    if (g == 0) lmax[k * 32 + c] = (float)(ck[k] - hl * maha);
+  }
+  __syncthreads();
+  unsigned need = 0;
+  if (g == 0 && valid) {
+    float M = -INFINITY;
+    for (int k = 0; k < K; ++k) M = fmaxf(M, lmax[k * 32 + c]);
+    for (int k = wave; k < K; k += kProbeWaves) need += (lmax[k * 32 + c] - M >= -kLjNeedGap) ? 1u : 0u;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) need += __shfl_xor(need, o);
+  if (lane == 0) part[wave] = need;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned tot = 0;
+    for (int w = 0; w < kProbeWaves; ++w) tot += part[w];
+    count[s] = tot;
   }
 }
 
@@ -778,9 +872,10 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
                        const double* __restrict__ ck, int K, int KP, const double* __restrict__ rowstat,
                        const unsigned* __restrict__ need, int nslab, int64_t rows_per_slab,
                        float* __restrict__ part_sig, float* __restrict__ part_mu, float* __restrict__ part_nk,
-                       int dense, const float* __restrict__ lj) {
+                       int dense, const float* __restrict__ lj, ProbeSel sel) {
   constexpr int NMB = DP / 32, NQ = DP / 16, NSB = NMB * (NMB + 1) / 2;
   constexpr int NGRP = gather_sig_groups(DP);
+  if (probe_selects(sel)) return;   // the stored branch's full_accum_ljt takes the call
   constexpr int NSBG = (NSB + NGRP - 1) / NGRP;              // blocks per group
   constexpr int SB0 = GRP * NSBG;                            // this group's blocks SB0 .. SB1 - 1
   constexpr int SB1 = SB0 + NSBG < NSB ? SB0 + NSBG : NSB;
@@ -1008,17 +1103,283 @@ void full_accum_gather(const float* __restrict__ X, int64_t ldx, int64_t N, int 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Pass 2 of the stored branch (FGMM_FLAG_STORE_LOGJOINT_AUTO, D <= 64): r from the
+// log-joint that pass 1 kept beside its need masks, over the default plan's slabs
+// and partials.  One workgroup per (row slab, group of 8 components), one component
+// per wave, so each 32-row X tile serves eight components: its fp32 rows, the eight
+// components' log-joint columns and the rows' logZ2 reach LDS by buffer-to-LDS loads
+// (four stages); every wave issues the same number of loads per tile (loads that
+// only keep the count go out of range into a pad line), so the wait before each
+// barrier is a fixed count.  The waves split the next tile's rows exactly into three
+// bf16 parts (the B operands of sig_outer, read transposed) while computing the
+// current one.  Per 16-row step, a = r x (fp32) is split as well and the six
+// products of significance at least 2^-16 are added smallest first, as the
+// gathering pass does; steps whose 16 rows carry no responsibility are skipped.
+// `sel` is the probe's selector: the kernel returns unless it selects this branch.
+// ---------------------------------------------------------------------------
+constexpr int kFljWaves = 8;
+
+template <int DP>
+struct FljShape {
+  static constexpr int NMB = DP / 32;
+  static constexpr int XRS = DP + 4;                     // fp32 row stride of an X tile
+  static constexpr int XPR = XRS / 4;                    // its 16-byte pieces per row (the last: padding)
+  static constexpr int XPC = (32 * XPR + 63) / 64 * 64;  // pieces of the tile's region (whole waves)
+  static constexpr int XQ = (XPC + 64 * kFljWaves - 1) / (64 * kFljWaves);
+  static constexpr int PRS = DP + 16;                    // bf16 row stride of the split parts
+  static constexpr int XB = XPC * 16;
+  static constexpr int OFF_LJ = XB;                      // the 8 components' log-joint columns
+  static constexpr int OFF_Z = XB + kFljWaves * 32 * 4;  // logZ2 of the 32 rows
+  static constexpr int STAGE = OFF_Z + 32 * 8;
+  static constexpr int NS = 4;
+  static constexpr int PB = 3 * 32 * PRS * 2;            // one tile's split parts
+  static constexpr int OFF_PARTS = NS * STAGE;
+  static constexpr int OFF_R = OFF_PARTS + 2 * PB;       // r of the tile per wave
+  static constexpr int OFF_PAD = OFF_R + kFljWaves * 32 * 4;
+  static constexpr size_t lds = (size_t)OFF_PAD + 1024;
+  // Loads of every wave per tile: XQ of X pieces, then 1 of log-joint columns (wave
+  // 0), of logZ2 (wave 1) or into the pad line.
+  static constexpr int NLOADS = XQ + 1;
+};
+__host__ inline int64_t flj_grid(int nslab, int ncg) { return (int64_t)8 * cdiv(nslab, 8) * ncg; }
+
+template <int DP>
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * kFljWaves, 64 * kFljWaves), amdgpu_waves_per_eu(2, 2)))
+void full_accum_ljt(const float* __restrict__ X, int64_t ldx, int64_t N, int D, int K, int KP,
+                    const double* __restrict__ rowstat, const float* __restrict__ lj, int nslab,
+                    int64_t rows_per_slab, int ncg, float* __restrict__ part_sig, float* __restrict__ part_mu,
+                    float* __restrict__ part_nk, int dense, ProbeSel sel) {
+  using SH = FljShape<DP>;
+  constexpr int NMB = SH::NMB, NSB = NMB * (NMB + 1) / 2;
+  constexpr int XRS = SH::XRS, PRS = SH::PRS, NS = SH::NS, NL = SH::NLOADS;
+  static_assert(SH::lds <= 160 * 1024, "stages exceed LDS");
+  if (!probe_selects(sel)) return;
+
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  // Workgroup -> (slab, component group): the ncg groups of slab s run on XCD s % 8.
+  const int xcd = blockIdx.x & 7, item = blockIdx.x >> 3;
+  const int slab = (item / ncg) * 8 + xcd, cg = item % ncg;
+  if (slab >= nslab) return;   // uniform over the workgroup
+  const int k = cg * kFljWaves + wave;
+  const bool active = k < K;
+
+  const int64_t r_begin = (int64_t)slab * rows_per_slab;
+  int64_t r_end = r_begin + rows_per_slab;
+  if (r_end > N) r_end = N;
+  const int ntiles = r_end > r_begin ? (int)cdiv(r_end - r_begin, 32) : 0;
+  const int64_t tile0 = r_begin >> 5;   // rows_per_slab is a multiple of 32
+  const int ncol = (D + 3) / 4;   // pieces of a row that hold columns below D
+  // This lane's X pieces, offsets into the tile's rows (the host keeps 32 rows of
+  // ldx under 2 GiB): slot q of wave w is LDS piece 64 (8 q + w) + lane of the tile
+  // (row piece / XPR, column piece % XPR); the padding piece of each row, columns
+  // past D and pieces past the tile read zeros.
+  int xoff[SH::XQ];
+#pragma unroll
+  for (int q = 0; q < SH::XQ; ++q) {
+    const int pc = (q * kFljWaves + wave) * 64 + lane;
+    const int rr = pc / SH::XPR, cc = pc % SH::XPR;
+    xoff[q] = (pc < 32 * SH::XPR && cc < ncol) ? (int)((int64_t)rr * ldx * 4 + cc * 16) : kBufOob;
+  }
+  unsigned char* const pad = lds_raw + SH::OFF_PAD;
+
+  auto issue = [&](int t, auto stage_tag) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage_tag)::value;
+    unsigned char* st = lds_raw + (size_t)S * SH::STAGE;
+    const bool in = t < ntiles;
+    const int64_t row0 = r_begin + (int64_t)t * 32;
+    const int64_t nrow = in ? (r_end - row0 < 32 ? r_end - row0 : 32) : 0;
+    const DmaSrc xsrc = dma_src(X + (in ? row0 : r_begin) * ldx, (uint32_t)(nrow * ldx * (int64_t)sizeof(float)));
+#pragma unroll
+    for (int q = 0; q < SH::XQ; ++q) {
+      if ((q * kFljWaves + wave) * 64 < SH::XPC)
+        lds_dma16(xsrc, st + (q * kFljWaves + wave) * 64 * 16, xoff[q], 0);
+      else
+        lds_dma16(xsrc, pad, kBufOob, 0);
+    }
+    const int64_t tg = tile0 + t;
+    if (wave == 0) {
+      // The group's 8 columns (out of range past KP).
+      const int nk = KP - cg * kFljWaves < kFljWaves ? KP - cg * kFljWaves : kFljWaves;
+      const DmaSrc lsrc = dma_src(lj + (in ? (tg * KP + cg * kFljWaves) * 32 : 0), in ? (uint32_t)(nk * 128) : 0u);
+      lds_dma16(lsrc, st + SH::OFF_LJ, lane * 16, 0);
+    } else if (wave == 1) {
+      const DmaSrc zsrc = dma_src(rowstat + (in ? row0 : 0), (uint32_t)(nrow * sizeof(double)));
+      if (lane < 16) lds_dma16(zsrc, st + SH::OFF_Z, lane * 16, 0);
+    } else {
+      lds_dma16(xsrc, pad, kBufOob, 0);
+    }
+  };
+  // The waves split tile t's fp32 rows (stage S) into parts buffer t & 1: lane
+  // (wave, lane) takes pieces wave * 64 + lane + 512 j of the 32 x DP / 4.
+  auto split = [&](int t, auto stage_tag) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage_tag)::value;
+    const float* xs = reinterpret_cast<const float*>(lds_raw + (size_t)S * SH::STAGE);
+    __bf16* pt = reinterpret_cast<__bf16*>(lds_raw + SH::OFF_PARTS + (t & 1) * SH::PB);
+#pragma unroll
+    for (int j = 0; j < (32 * DP / 4 + 64 * kFljWaves - 1) / (64 * kFljWaves); ++j) {
+      const int pc = j * 64 * kFljWaves + tid;
+      if (32 * DP / 4 % (64 * kFljWaves) == 0 || pc < 32 * DP / 4) {
+        const int rr = pc / (DP / 4), cc = 4 * (pc % (DP / 4));
+        const f32x4 v = *reinterpret_cast<const f32x4*>(xs + rr * XRS + cc);
+        uint2 w[3];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const f32x2 a = {v[2 * h], v[2 * h + 1]};
+          const unsigned p1 = bf16_pair(a);
+          const f32x2 d1 = a - bf16_pair_widen(p1);
+          const unsigned p2 = bf16_pair(d1);
+          const unsigned p3 = bf16_pair(d1 - bf16_pair_widen(p2));
+          (h == 0 ? w[0].x : w[0].y) = p1;
+          (h == 0 ? w[1].x : w[1].y) = p2;
+          (h == 0 ? w[2].x : w[2].y) = p3;
+        }
+#pragma unroll
+        for (int u = 0; u < 3; ++u) *reinterpret_cast<uint2*>(pt + (u * 32 + rr) * PRS + cc) = w[u];
+      }
+    }
+  };
+
+  f32x16 acc[NSB];
+#pragma unroll
+  for (int sb = 0; sb < NSB; ++sb) acc[sb] = zero16();
+  float mua[NMB];
+#pragma unroll
+  for (int mb = 0; mb < NMB; ++mb) mua[mb] = 0.0f;
+  float nk = 0.0f;
+  float* rx = reinterpret_cast<float*>(lds_raw + SH::OFF_R) + wave * 32;
+
+  auto compute = [&](int t, auto stage_tag) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage_tag)::value;
+    const unsigned char* st = lds_raw + (size_t)S * SH::STAGE;
+    const float* xt = reinterpret_cast<const float*>(st);
+    const float l = reinterpret_cast<const float*>(st + SH::OFF_LJ)[wave * 32 + c];
+    const double z = reinterpret_cast<const double*>(st + SH::OFF_Z)[c];
+    const __bf16* pt = reinterpret_cast<const __bf16*>(lds_raw + SH::OFF_PARTS + (t & 1) * SH::PB);
+    // r of row c (both half-waves hold it); 0 past the slab.
+    const bool rin = r_begin + (int64_t)t * 32 + c < r_end;
+    const float rv = (active && rin) ? fast_exp2((float)((double)l - z)) : 0.0f;
+    if (g == 0) {
+      nk += rv;
+      rx[c] = rv;
+    }
+    const unsigned nz = (unsigned)__builtin_amdgcn_ballot_w64(rv != 0.0f);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if (!dense && ((nz >> (16 * p)) & 0xffffu) == 0u) continue;
+      const int rb = 16 * p + 8 * g;
+      const f32x4 r0 = *reinterpret_cast<const f32x4*>(rx + rb), r1 = *reinterpret_cast<const f32x4*>(rx + rb + 4);
+      const float rr[8] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+      bf16x8 ba[NMB][3], bx[NMB][3];
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) {
+        float a[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          a[e] = rr[e] * xt[(rb + e) * XRS + 32 * mb + c];
+          mua[mb] += a[e];
+        }
+        split3_bf16(f32x4{a[0], a[1], a[2], a[3]}, f32x4{a[4], a[5], a[6], a[7]}, ba[mb]);
+#pragma unroll
+        for (int u = 0; u < 3; ++u) bx[mb][u] = lds_rows_operand(pt + u * 32 * PRS, PRS, 16 * p, 32 * mb, lane);
+      }
+#pragma unroll
+      for (int m1 = 0; m1 < NMB; ++m1) {
+#pragma unroll
+        for (int m2 = m1; m2 < NMB; ++m2) {
+          f32x16& a = acc[m1 * NMB - m1 * (m1 - 1) / 2 + (m2 - m1)];
+          a = mfma_bf16(ba[m1][2], bx[m2][0], a);
+          a = mfma_bf16(ba[m1][1], bx[m2][1], a);
+          a = mfma_bf16(ba[m1][0], bx[m2][2], a);
+          a = mfma_bf16(ba[m1][1], bx[m2][0], a);
+          a = mfma_bf16(ba[m1][0], bx[m2][1], a);
+          a = mfma_bf16(ba[m1][0], bx[m2][0], a);
+        }
+      }
+    }
+  };
+
+  // Step t, stage S = t mod 4: issue tile t + 3, split tile t + 1 (its stage landed
+  // at the last barrier), compute tile t (split during the previous step), wait for
+  // tile t + 2's stage, barrier.
+  auto step = [&](int t, auto stage_tag) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage_tag)::value;
+    issue(t + 3, std::integral_constant<int, (S + 3) % NS>{});
+    if (t + 1 < ntiles) split(t + 1, std::integral_constant<int, (S + 1) % NS>{});
+    compute(t, stage_tag);
+    vm_wait<NL>();
+    __syncthreads();
+  };
+  if (ntiles > 0) {
+    issue(0, std::integral_constant<int, 0>{});
+    issue(1, std::integral_constant<int, 1>{});
+    issue(2, std::integral_constant<int, 2>{});
+    vm_wait<2 * NL>();   // tile 0
+    __syncthreads();
+    split(0, std::integral_constant<int, 0>{});
+    vm_wait<NL>();       // tile 1
+    __syncthreads();
+  }
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
+  for (int t = 0; t < ntiles; t += NS) {
+    step(t, S0{});
+    if (t + 1 >= ntiles) break;
+    step(t + 1, S1{});
+    if (t + 2 >= ntiles) break;
+    step(t + 2, S2{});
+    if (t + 3 >= ntiles) break;
+    step(t + 3, S3{});
+  }
+  vm_wait<0>();   // no buffer-to-LDS load outlives the workgroup
+
+  if (active) {
+    const int64_t pbase = (int64_t)slab * KP + k;
+    float* ps = part_sig + pbase * NSB * 1024;
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) ps[sb * 1024 + acc_row(i, g) * 32 + c] = acc[sb][i];
+    }
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+      const float v = mua[mb] + __shfl_xor(mua[mb], 32);
+      if (g == 0) part_mu[pbase * DP + 32 * mb + c] = v;
+    }
+    float nks = nk;
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) nks += __shfl_xor(nks, o);
+    if (lane == 0) part_nk[pbase] = nks;
+  }
+}
+
 template <int DP>
 hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsigned char* ws,
                          float* logZ, bool run1, bool run2, bool dense, hipStream_t stream) {
   const double* ck = reinterpret_cast<const double*>(ws + pl.off_ck);
   double* rowstat = reinterpret_cast<double*>(ws + pl.off_rowstat);
-  float* lj = (pl.lj || pl.keep_lj) ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
+  float* lj = (pl.lj || pl.keep_lj || pl.autolj) ? reinterpret_cast<float*>(ws + pl.off_lj) : nullptr;
   auto set_lds = [](const void* f, size_t bytes) -> hipError_t {
     return bytes > 65536 ? hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes)
                          : hipSuccess;
   };
+  // FGMM_FLAG_STORE_LOGJOINT_AUTO: the probe's counts select the branch in both passes.
+  unsigned* probe = pl.autolj ? reinterpret_cast<unsigned*>(ws + pl.off_probe) : nullptr;
+  const ProbeSel psel = probe ? ProbeSel{probe, pl.nprobe, probe_min_pairs(pl.N, pl.nprobe, (int)pl.K)}
+                              : ProbeSel{nullptr, 0, 0};
   if (run1) {
+    if constexpr (flj_applies(DP)) {
+      if (pl.autolj)
+        hipLaunchKernelGGL((full_store_probe<DP>), dim3((unsigned)pl.nprobe), dim3(64 * kProbeWaves), 0, stream, X,
+                           ldx, pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
+                           reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.nprobe, probe);
+    }
     constexpr size_t lds1 = full_x6_lds_bytes<DP>();
     // The stored plan runs up to D = 128 only; above, the default plan keeps the
     // log-joint beside the need masks (keep_lj) where it fits.
@@ -1032,7 +1393,22 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
                        pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
                        reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, logZ,
                        rowstat, lj, reinterpret_cast<unsigned*>(ws + pl.off_need),
-                       reinterpret_cast<unsigned short*>(ws + pl.off_bound), pl.rexact ? 1 : 0, dense ? 1 : 0);
+                       reinterpret_cast<unsigned short*>(ws + pl.off_bound), pl.rexact ? 1 : 0, dense ? 1 : 0,
+                       psel);
+    if constexpr (flj_applies(DP)) {
+      if (pl.autolj) {
+        // The stored branch's instance: the same pass, also keeping the log-joint.
+        auto kst = &full_lse_x6<DP, kLjmNeed, true>;
+        e = set_lds(reinterpret_cast<const void*>(kst), lds1);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(kst, dim3(grid1), dim3(kThreads), lds1, stream, X, ldx, pl.N, (int)pl.D,
+                           reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
+                           reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, logZ, rowstat,
+                           lj, reinterpret_cast<unsigned*>(ws + pl.off_need),
+                           reinterpret_cast<unsigned short*>(ws + pl.off_bound), pl.rexact ? 1 : 0, dense ? 1 : 0,
+                           psel);
+      }
+    }
   }
   if (!run2) return hipGetLastError();
   float* psig = reinterpret_cast<float*>(ws + pl.off_part_sig);
@@ -1054,10 +1430,21 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
                              reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
                              reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, rowstat,
                              reinterpret_cast<const unsigned*>(ws + pl.off_need), pl.nslab, pl.rows_per_slab,
-                             psig, pmu, pnk, dense ? 1 : 0, lj);
+                             psig, pmu, pnk, dense ? 1 : 0, lj, psel);
         }
         return hipSuccess;
       };
+      if constexpr (flj_applies(DP)) {
+        if (pl.autolj) {
+          using SH = FljShape<DP>;
+          hipError_t ej = set_lds(reinterpret_cast<const void*>(&full_accum_ljt<DP>), SH::lds);
+          if (ej != hipSuccess) return ej;
+          const int ncg = (int)cdiv(pl.K, kFljWaves);
+          hipLaunchKernelGGL((full_accum_ljt<DP>), dim3((unsigned)flj_grid(pl.nslab, ncg)), dim3(64 * kFljWaves),
+                             SH::lds, stream, X, ldx, pl.N, (int)pl.D, (int)pl.K, pl.KP, rowstat, lj, pl.nslab,
+                             pl.rows_per_slab, ncg, psig, pmu, pnk, dense ? 1 : 0, psel);
+        }
+      }
       hipError_t e = launch(std::integral_constant<int, 0>{});
       if (e == hipSuccess) e = launch(std::integral_constant<int, 1>{});
       if (e == hipSuccess) e = launch(std::integral_constant<int, 2>{});
@@ -1979,7 +2366,7 @@ extern "C" size_t fgmm_full_workspace_bytes_ex(int64_t N, int64_t K, int64_t D, 
   const bool bf16 = (flags & FGMM_FLAG_BF16) != 0;
   if (D > (bf16 ? 128 : kFullMaxD)) return 0;
   const int64_t rows = full_lj_chunked(D, bf16) ? std::min(N, full_lj_chunk_rows(K)) : N;
-  return make_plan(rows, K, D, wants_stored_lj(flags), bf16).total;
+  return make_plan(rows, K, D, wants_stored_lj(flags), bf16, wants_auto_lj(flags)).total;
 }
 
 extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64_t D, const float* mu,
@@ -2023,7 +2410,7 @@ extern "C" int fgmm_full_estep_f32(const float* X, int64_t ldx, int64_t N, int64
     }
     return FGMM_OK;
   }
-  const FullPlan pl = make_plan(N, K, D, wants_stored_lj(flags), bf16);
+  const FullPlan pl = make_plan(N, K, D, wants_stored_lj(flags), bf16, wants_auto_lj(flags) && ldx <= kMaxBufLdx);
   // The bf16 contract always stores the log-joint: N x K floats within kMaxLjBytes.
   if (bf16 && K > 0 && !pl.lj) return FGMM_ERR_UNSUPPORTED;
   if (workspace_bytes < pl.total || (pl.total > 0 && workspace == nullptr)) return FGMM_ERR_WORKSPACE;

@@ -162,6 +162,25 @@ def diag_reference_smoke(N: int = 1_000_000, K: int = 1024, D: int = 96, seed: i
     return dict(X=X, mu=mu, log_sigma_sq=lss, log_pi=lpi)
 
 
+def full_reference_smoke(N: int = 250_000, K: int = 256, D: int = 64, seed: int = 0,
+                         device="cpu") -> Dict[str, torch.Tensor]:
+    """The reference smoke workload's data (flash_gmm.py:228-234: X, mu ~ N(0, I),
+    uniform weights) for the full model: Sigma_k = I + 0.2 A_k A_k^T / D with
+    A_k ~ N(0, 1), prec_chol_k = cholesky(inv(Sigma_k)) in float64 on the host.
+    Every component is within reach of every row."""
+    g = _gen(device, seed)
+    X = _randn(g, N, D, device=device)
+    mu = _randn(g, K, D, device=device)
+    A64 = torch.randn(K, D, D, generator=g, device=device, dtype=torch.float32).double().cpu().numpy()
+    prec = np.empty((K, D, D))
+    for k in range(K):
+        s = np.eye(D) + 0.2 * (A64[k] @ A64[k].T) / D
+        prec[k] = np.linalg.cholesky(np.linalg.inv(s))
+    prec_chol = torch.from_numpy(prec).float().contiguous().to(device)
+    lpi = torch.full((K,), -math.log(K), device=device)
+    return dict(X=X, mu=mu, prec_chol=prec_chol, log_pi=lpi)
+
+
 WORKLOADS = {
     # name: (generator, default sizes, default seed)
     "iso_n10k_k64_d32": (iso_plain, dict(N=10_000, K=64, D=32), 0),
@@ -173,6 +192,7 @@ WORKLOADS = {
     "iso_ref_n1m_k1024_d128": (reference_smoke, dict(N=1_000_000, K=1024, D=128), 0),
     # the same dense regime for the diagonal model at its benchmark shape
     "diag_ref_n1m_k1024_d96": (diag_reference_smoke, dict(N=1_000_000, K=1024, D=96), 0),
+    "full_ref_n250k_k256_d64": (full_reference_smoke, dict(N=250_000, K=256, D=64), 0),
     # wider shapes (split-dimension accumulation paths)
     "diag_n1m_k256_d256": (diag_clustered, dict(N=1_000_000, K=256, D=256), 5),
     "full_n100k_k64_d128": (full_clustered, dict(N=100_000, K=64, D=128), 6),

@@ -338,9 +338,12 @@ def flash_gmm_estep_diag(X: torch.Tensor, mu: torch.Tensor, log_sigma_sq: torch.
 def full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, *,
                     accumulate: bool = False, atomic_reduce: bool = False,
                     workspace: torch.Tensor | None = None, phase: int = 0, dense: bool = False,
-                    recompute: bool = False, store_log_joint: bool = False,
+                    recompute: bool = False, store_log_joint: bool | str = False,
                     precision: str = "fp32") -> None:
     """Full-covariance E-step into caller-provided outputs (sig_outer is (K, D, D)).
+
+    The plan arguments are iso_estep_into's; ``store_log_joint="auto"`` applies up
+    to D = 64 and K = 512 (elsewhere the call runs the default plan).
 
     ``precision="bf16"`` selects the bf16 operand contract of the reference's full
     H100 kernels (flash_gmm_full_h100.py:71-228): x and L rounded to bfloat16 for the
@@ -390,7 +393,9 @@ def flash_gmm_estep_full(X: torch.Tensor, mu: torch.Tensor, prec_chol: torch.Ten
     prec_chol[k] is lower-triangular with prec_chol[k] @ prec_chol[k].T = Sigma_k^-1;
     sig_outer[k] = sum_n r_nk x_n x_n^T (flash_gmm_full_h100.py:245-260).
     ``precision="bf16"`` follows the reference kernels' bf16 operand contract
-    instead of fp32 arithmetic.
+    instead of fp32 arithmetic.  Up to D = 64 the call runs with
+    store_log_joint="auto" (see full_estep_into) while that workspace takes at most
+    AUTO_STORE_MEMORY_FRACTION of the device's memory.
     """
     _check_common(X, mu, log_pi)
     N, D = X.shape
@@ -402,5 +407,6 @@ def flash_gmm_estep_full(X: torch.Tensor, mu: torch.Tensor, prec_chol: torch.Ten
     Nk = torch.empty(K, device=dev, dtype=torch.float32)
     mu_acc = torch.empty(K, D, device=dev, dtype=torch.float32)
     sig_outer = torch.empty(K, D, D, device=dev, dtype=torch.float32)
-    full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, precision=precision)
+    full_estep_into(X, mu, prec_chol, log_pi, logZ, Nk, mu_acc, sig_outer, precision=precision,
+                    store_log_joint=_auto_store(N, K, D, dev, precision, "full"))
     return logZ, Nk, mu_acc, sig_outer

@@ -116,6 +116,12 @@ def test_iso_workspace_holds_stored_log_joint():
     assert L.fgmm_diag_workspace_bytes_ex(N, K, 128, A) == L.fgmm_diag_workspace_bytes(N, K, 128)
     # Full: stored whenever it fits, 32 floats per (32-row tile, component).
     q, qx = L.fgmm_full_workspace_bytes, L.fgmm_full_workspace_bytes_ex
+    # Full STORE_LOGJOINT_AUTO (D <= 64, K <= 512): the default plan plus the kept
+    # log-joint (tiles rounded to 4 per pass-1 workgroup) and the probe's counts.
+    f_lj = -(-250_000 // 128) * 4 * 256 * 32 * 4
+    assert f_lj <= qx(250_000, 256, 64, A) - q(250_000, 256, 64) <= f_lj + 2 * 256
+    assert qx(250_000, 256, 96, A) == q(250_000, 256, 96)
+    assert qx(250_000, 600, 64, A) == q(250_000, 600, 64)
     assert q(5000, 64, 64) == qx(5000, 64, 64, 0) == qx(5000, 64, 64, R) > 0
     n = 250_000
     lj_bytes = -(-n // 128) * 4 * 256 * 128

@@ -196,3 +196,91 @@ def test_atomic_reduce_matches_the_tree(gpu_device):
     torch.cuda.synchronize()
     for u, v in zip(acc_out[1:], acc[1:]):
         torch.testing.assert_close(u, 2 * v, rtol=1e-5, atol=1e-5 * float(v.abs().max()))
+
+
+# FGMM_FLAG_STORE_LOGJOINT_AUTO (store_log_joint="auto", D <= 64, K <= 512): the
+# device-selected stored branch (pass 1 keeps the log-joint, full_accum_ljt reads r
+# from it) on dense data, the default plan elsewhere.
+FULL_AUTO_DENSE_SHAPES = [(8000, 128, 64), (6000, 64, 64), (3001, 130, 61), (3000, 40, 32), (777, 20, 50),
+                          (4099, 257, 33)]
+
+
+@pytest.mark.parametrize("N,K,D", FULL_AUTO_DENSE_SHAPES)
+def test_auto_store_dense_takes_stored_branch(N, K, D, gpu_device):
+    """On dense data (X, mu ~ N(0, I), covariances near I) the probe selects the
+    stored branch: its statistics differ from the default plan's in the last bits
+    (another summation) and agree with the oracle."""
+    inp = data.full_reference_smoke(N, K, D, seed=N % 97)
+    auto = _into(inp, gpu_device, store_log_joint="auto")
+    base = _into(inp, gpu_device)
+    assert any(not torch.equal(u, v) for u, v in zip(auto[1:], base[1:]))
+    ref = oracle(inp)
+    assert_close_stats(auto, ref, f"full auto dense N={N} K={K} D={D}")
+    assert_close_stats(base, ref, f"full default dense N={N} K={K} D={D}")
+
+
+@pytest.mark.parametrize("N,K,D", [(20000, 256, 64), (5000, 512, 48), (3000, 100, 96), (2000, 600, 32)])
+def test_auto_store_clustered_is_the_default_plan(N, K, D, gpu_device):
+    """On clustered data the probe keeps the default plan, and above D = 64 or
+    K = 512 the flag does not apply: every output bitwise equal to a call without
+    the flag."""
+    inp = data.full_clustered(N, K, D, seed=K % 13 + D)
+    auto = _into(inp, gpu_device, store_log_joint="auto")
+    base = _into(inp, gpu_device)
+    for u, v in zip(auto, base):
+        assert torch.equal(u, v)
+
+
+@pytest.mark.parametrize("kind", ["dense", "clustered"])
+def test_auto_store_phase_split_and_reuse(kind, gpu_device):
+    """PHASE1 then PHASE2 on one workspace equals the single call bitwise, and calls
+    alternating between dense and clustered data on that workspace each select their
+    own branch."""
+    from flash_gmm import _lib
+    L = _lib.lib()
+    dev = gpu_device
+    dense_inp = data.full_reference_smoke(6000, 128, 64, seed=4)
+    clus_inp = data.full_clustered(6000, 128, 64, seed=5)
+    inp = dense_inp if kind == "dense" else clus_inp
+    other = clus_inp if kind == "dense" else dense_inp
+    N, D = inp["X"].shape
+    K = inp["mu"].shape[0]
+    ws = torch.empty(L.fgmm_full_workspace_bytes_ex(N, K, D, _lib.FLAG_STORE_LOGJOINT_AUTO), dtype=torch.uint8,
+                     device=dev)
+    ref = _into(inp, dev, store_log_joint="auto")
+    ref_other = _into(other, dev, store_log_joint="auto")
+    for _ in range(2):
+        for cur, want in ((inp, ref), (other, ref_other)):
+            out = [torch.empty(N, device=dev), torch.empty(K, device=dev), torch.empty(K, D, device=dev),
+                   torch.empty(K, D, D, device=dev)]
+            args = [cur[k].to(dev) for k in KEYS]
+            full_estep_into(*args, *out, workspace=ws, phase=1, store_log_joint="auto")
+            full_estep_into(*args, None, *out[1:], workspace=ws, phase=2, store_log_joint="auto")
+            torch.cuda.synchronize()
+            for u, v in zip(out, want):
+                assert torch.equal(u, v)
+
+
+def test_auto_store_full_size_dense(gpu_device):
+    """The dense regime at the benchmark shape (N = 250K, K = 256, D = 64) through the
+    drop-in call, which takes the stored branch: sum Nk = N, sum mu_acc = sum X,
+    sum sig_outer = X^T X over all rows, agreement with the default plan, and all
+    four outputs against the oracle on an 8,192-row prefix run on its own."""
+    dev = gpu_device
+    inp = data.make("full_ref_n250k_k256_d64", device=dev)
+    got = flash_gmm_estep_full(*[inp[k] for k in KEYS])
+    base = _into(inp, dev)
+    torch.cuda.synchronize()
+    N = inp["X"].shape[0]
+    X = inp["X"].double()
+    assert abs(got[1].double().sum().item() - N) <= 1e-5 * N
+    torch.testing.assert_close(got[2].double().sum(0), X.sum(0), rtol=0,
+                               atol=1e-5 * float(got[2].abs().sum(0).max()))
+    xtx = X.T @ X
+    torch.testing.assert_close(got[3].double().sum(0), xtx, rtol=0, atol=1e-5 * float(xtx.abs().max()))
+    assert float((got[0] - base[0]).abs().max()) <= 1e-5
+    for u, v in zip(got[1:], base[1:]):
+        assert float((u - v).abs().max()) <= 1e-5 * float(v.abs().max())
+    sub = {k: (v[:8192].cpu() if k == "X" else v.cpu()) for k, v in inp.items()}
+    part = run_gpu(sub, dev)
+    assert_close_stats(part, oracle(sub), "full auto N=8192 K=256 D=64 dense")
