@@ -42,6 +42,9 @@ WORKLOADS = {
     "iso_n1m_k1024_d128": (1_000_000, 1024, 128),
     "iso_ref_n1m_k1024_d128": (1_000_000, 1024, 128),
     "diag_n1m_k1024_d96": (1_000_000, 1024, 96),
+    # the reference's dense data (X, mu ~ N(0, I)) for the diagonal and full models
+    "diag_ref_n1m_k1024_d96": (1_000_000, 1024, 96),
+    "full_ref_n250k_k256_d64": (250_000, 256, 64),
     "full_n250k_k256_d64": (250_000, 256, 64),
     "diag_n1m_k256_d256": (1_000_000, 256, 256),
     "full_n100k_k64_d128": (100_000, 64, 128),
@@ -363,19 +366,37 @@ KERNELS = {
                         "iso_accum_sparse / iso_accum_ljt (by the needed-pair count)"),
     ("iso", "stored_wide"): ("iso_lse_ctile (stores the log-joint)", "iso_accum_lj"),
     ("diag", "default"): ("diag_lse_x6 (need masks)", "diag_accum_gather"),
+    ("diag", "auto"): ("diag_store_probe, diag_lse_x6 (need masks; the instance that also stores the "
+                       "log-joint, the rows' feature parts and logZ pairs runs where the probe selects it)",
+                       "diag_accum_ljt where the probe selected the stored branch, else diag_accum_gather"),
     ("diag", "default_wide"): ("diag_lse_ctile (need masks)", "diag_accum_drange"),
     ("diag", "stored"): ("diag_lse_x6 (stores the log-joint)", "diag_accum_sparse / diag_accum_lj2"),
     ("diag", "stored_wide"): ("diag_lse_ctile (stores the log-joint)", "diag_accum_lj"),
     ("full", "default"): ("full_lse_x6 (need masks)", "full_accum_gather"),
+    ("full", "auto"): ("full_store_probe, full_lse_x6 (need masks; the instance that also keeps the "
+                       "log-joint runs where the probe selects it)",
+                       "full_accum_ljt where the probe selected the stored branch, else full_accum_gather"),
     ("full", "stored"): ("full_lse_x6 (stores the log-joint)", "full_accum"),
 }
+
+
+# Widths up to which the drop-in call runs with store_log_joint="auto" (the
+# device-selected stored branch; the full model also needs K <= 512).
+AUTO_MAX_D = {"iso": 128, "diag": 96, "full": 64}
+
+
+def dropin_mode(kind, K, D, precision):
+    """store_log_joint of the drop-in call for this shape."""
+    if precision != "fp32" or D > AUTO_MAX_D[kind] or (kind == "full" and K > 512):
+        return False
+    return "auto"
 
 
 def kernel_names(kind, D, precision, stored):
     if precision == "bf16":
         return f"{kind}_bf16_lse", f"{kind}_bf16_accum"
     if stored == "auto":
-        return KERNELS[("iso", "auto")] if (kind == "iso" and D <= 128) else kernel_names(kind, D, precision, False)
+        return KERNELS[(kind, "auto")] if D <= AUTO_MAX_D[kind] else kernel_names(kind, D, precision, False)
     wide = kind != "full" and D > 128
     if stored and (D > 256 or (kind == "full" and D > 128)):
         stored = False          # the stored plan's widths; above them the call runs the default plan
@@ -407,9 +428,9 @@ def main_workload(args):
     kind = workload.split("_")[0]
     bf16 = args.precision == "bf16"
     log(f"generating workload {workload} on {torch.cuda.get_device_name(dev)}")
-    # The phases run the plan the drop-in call takes: store_log_joint="auto" for the
-    # isotropic model up to D = 128 (flash_gmm_estep), else the default plan.
-    mode = True if args.store_log_joint else ("auto" if (kind == "iso" and not bf16 and D <= 128) else False)
+    # The phases run the plan the drop-in call takes: store_log_joint="auto" (iso up
+    # to D = 128, diag to 96, full to 64), else the default plan.
+    mode = True if args.store_log_joint else dropin_mode(kind, K, D, args.precision)
     inp, outs, r = measure(args, workload, args.precision, mode, dev)
     split_ms, p1, p2 = r["ms"], r["p1"], r["p2"]
     log(f"timed {args.steps} steps as two phase calls: {split_ms:.3f} ms/step (phase1 {p1:.3f} ms, "
@@ -585,6 +606,30 @@ def main_workload(args):
             f"default plan {rd['ms']:.3f} ms")
         del rinp, rr, rd
         torch.cuda.empty_cache()
+        # The same dense regime for the diagonal and full models at their benchmark
+        # shapes: the drop-in call (the probe selects the stored branch) beside the
+        # default plan, whose pass 2 recomputes every pair.
+        dense = {}
+        for dwl in ("diag_ref_n1m_k1024_d96", "full_ref_n250k_k256_d64"):
+            dN, dK, dD = WORKLOADS[dwl]
+            dkind = dwl.split("_")[0]
+            dinp, _, da = measure(args, dwl, "fp32", "auto", dev)
+            dms, dmed = time_dropin(dkind, dinp, args.steps, args.warmup, stream)
+            del da["call"]
+            torch.cuda.empty_cache()
+            _, _, dd = measure(args, dwl, "fp32", False, dev, inp=dinp)
+            del dd["call"]
+            dense[dwl] = {"N": dN, "K": dK, "D": dD, "ms_per_step": dms, "median_call_ms": dmed,
+                          "value": dN / (dms * 1e-3), "unit": "samples/s",
+                          "phase1_ms": da["p1"], "phase2_ms": da["p2"],
+                          "plan": "the drop-in call (store_log_joint='auto': the probe selects the stored "
+                                  "branch here)",
+                          "default_plan": {"ms_per_step": dd["ms"], "phase1_ms": dd["p1"], "phase2_ms": dd["p2"]}}
+            log(f"{dwl}: drop-in {dms:.3f} ms/step (phase1 {da['p1']:.3f}, phase2 {da['p2']:.3f}); "
+                f"default plan {dd['ms']:.3f} ms (phase2 {dd['p2']:.3f})")
+            del dinp, da, dd
+            torch.cuda.empty_cache()
+        out["dense_regime_diag_full"] = dense
     if not args.no_cpu_baseline and not bf16:
         log("timing the CPU baseline (bounded sample)")
         out["cpu_baseline"] = cpu_baseline(inp, kind, K, D, logZ)

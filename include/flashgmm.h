@@ -105,17 +105,19 @@ enum fgmm_flags {
      * *_workspace_bytes_ex(..., flags).  Calls that split the phases must agree
      * on this flag. */
     FGMM_FLAG_STORE_LOGJOINT = 1u << 9,
-    /* Opt-in, isotropic model up to D = 128 (elsewhere it has no effect): the
-     * default plan plus a stored-log-joint branch that the device selects per
-     * call.  A probe samples up to 64 tiles of 32 rows before pass 1; when at
-     * least half of their (row, component block) pairs can carry a nonzero
-     * responsibility (dense data, e.g. the reference's X, mu ~ N(0, I) benchmark),
-     * pass 1 also stores the log-joint, the rows' bf16 X parts and logZ pairs, and
-     * pass 2 reads them instead of recomputing the D-contraction; otherwise the
-     * call runs as the default plan.  No host synchronisation; the workspace is
-     * O(N*K) (about 4.7 GB at N=1M, K=1024, D=128: size it with
-     * fgmm_iso_workspace_bytes_ex) and the branch applies while the log-joint
-     * fits in 16 GiB.  STORE_LOGJOINT and RECOMPUTE take precedence. */
+    /* Opt-in, isotropic model up to D = 128, diagonal up to D = 96, full up to
+     * D = 64 and K = 512 (elsewhere it has no effect): the default plan plus a
+     * stored-log-joint branch that the device selects per call.  A probe samples
+     * up to 64 tiles of 32 rows before pass 1; when at least half of their (row,
+     * component block) pairs (full: (row, component)) can carry a nonzero
+     * responsibility (dense data, e.g. the reference's X, mu ~ N(0, I)
+     * benchmark), pass 1 also stores the log-joint (iso, diag: with the rows'
+     * split features and logZ pairs) and pass 2 reads them instead of recomputing
+     * the contraction; otherwise the call runs as the default plan.  No host
+     * synchronisation; the workspace is O(N*K) (about 4.7 GB at N=1M, K=1024,
+     * D=128 isotropic, 5.4 GB at D=96 diagonal, 0.26 GB at N=250K, K=256
+     * full: size it with *_workspace_bytes_ex) and the branch applies while the
+     * log-joint fits in 16 GiB.  STORE_LOGJOINT and RECOMPUTE take precedence. */
     FGMM_FLAG_STORE_LOGJOINT_AUTO = 1u << 10,
 };
 
