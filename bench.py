@@ -373,7 +373,7 @@ KERNELS = {
     ("diag", "stored"): ("diag_lse_x6 (stores the log-joint)", "diag_accum_sparse / diag_accum_lj2"),
     ("diag", "stored_wide"): ("diag_lse_ctile (stores the log-joint)", "diag_accum_lj"),
     ("full", "default"): ("full_lse_x6 (need masks)", "full_accum_gather"),
-    ("full", "auto"): ("full_store_probe, full_lse_x6 (need masks; the instance that also keeps the "
+    ("full", "auto"): ("full_probe_ll, full_probe_count, full_lse_x6 (need masks; the instance that also keeps the "
                        "log-joint runs where the probe selects it)",
                        "full_accum_ljt where the probe selected the stored branch, else full_accum_gather"),
     ("full", "stored"): ("full_lse_x6 (stores the log-joint)", "full_accum"),

@@ -223,7 +223,7 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
     if (p.rexact) off = align256(off + (size_t)p.grid1 * kWaves * 32 * p.KP * sizeof(unsigned short));
   }
   p.off_probe = off;
-  if (p.autolj) off = align256(off + probe_bytes());
+  if (p.autolj) off = align256(off + probe_bytes() + (size_t)p.nprobe * p.KP * 32 * sizeof(float));
   p.total = off;
   return p;
 }
@@ -490,26 +490,26 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
 }
 
 // ---------------------------------------------------------------------------
-// The probe of FGMM_FLAG_STORE_LOGJOINT_AUTO (D <= 64, K <= kProbeMaxKB): one
-// workgroup per sampled 32-row tile; its waves take the components in turn and form
-// each row's log-joint in LDS from the whitening's centring step and x1 L1 product
-// only (an error of a few log2 units against the kLjNeedGap = 160 margin).  Then,
+// The probe of FGMM_FLAG_STORE_LOGJOINT_AUTO (D <= 64, K <= kProbeMaxKB), in two
+// kernels.  full_probe_ll: kProbeSplit workgroups per sampled 32-row tile, each over
+// a quarter of the components, form the rows' log-joint from the whitening's
+// centring step and x1 L1 product only (an error of a few log2 units against the
+// kLjNeedGap = 160 margin) into `lls` ([tile][KP][32] floats).  full_probe_count:
 // per row, the components with ll >= M - kLjNeedGap (M the row's largest) are
-// counted: an estimate of the pairs pass 1 marks as needed.  The tile's count is
-// written; the kernels that need the choice sum the counts (probe_selects).
+// counted, an estimate of the pairs pass 1 marks as needed; the tile's count is
+// written, and the kernels that need the choice sum the counts (probe_selects).
 // ---------------------------------------------------------------------------
 constexpr int kProbeWaves = 16;
+constexpr int kProbeSplit = 4;
 template <int DP>
-__global__ __launch_bounds__(64 * kProbeWaves) void full_store_probe(const float* __restrict__ X, int64_t ldx,
-                                                                     int64_t N, int D,
-                                                                     const bf16x8* __restrict__ l3,
-                                                                     const double* __restrict__ esw,
-                                                                     const double* __restrict__ ck, int K,
-                                                                     int ntile, unsigned* __restrict__ count) {
+__global__ __launch_bounds__(64 * kProbeWaves) void full_probe_ll(const float* __restrict__ X, int64_t ldx,
+                                                                  int64_t N, int D,
+                                                                  const bf16x8* __restrict__ l3,
+                                                                  const double* __restrict__ esw,
+                                                                  const double* __restrict__ ck, int K, int KP,
+                                                                  int ntile, float* __restrict__ lls) {
   constexpr int NMB = DP / 32, NQ = DP / 16;
-  __shared__ float lmax[kProbeMaxKB * 32];
-  __shared__ unsigned part[kProbeWaves];
-  const int s = blockIdx.x;
+  const int s = blockIdx.x / kProbeSplit, part = blockIdx.x % kProbeSplit;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, g = lane >> 5;
@@ -525,7 +525,7 @@ __global__ __launch_bounds__(64 * kProbeWaves) void full_store_probe(const float
   }
   const bf16x8 ones = x6c_ones(lane);
   const double hl = 0.5 * kLog2e;
-  for (int k = wave; k < K; k += kProbeWaves) {
+  for (int k = part * kProbeWaves + wave; k < K; k += kProbeSplit * kProbeWaves) {
     double maha = 0.0;
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) {
@@ -544,24 +544,36 @@ __global__ __launch_bounds__(64 * kProbeWaves) void full_store_probe(const float
       }
     }
     maha += __shfl_xor(maha, 32);
-    if (g == 0) lmax[k * 32 + c] = (float)(ck[k] - hl * maha);
+    if (g == 0) lls[((int64_t)s * KP + k) * 32 + c] = (float)(ck[k] - hl * maha);
   }
+}
+
+__global__ __launch_bounds__(256) void full_probe_count(int64_t N, int K, int KP, int ntile,
+                                                        const float* __restrict__ lls,
+                                                        unsigned* __restrict__ count) {
+  __shared__ float mrow[8][32];
+  __shared__ unsigned part[4];
+  const int s = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = tid & 31, grp = tid >> 5;   // 8 groups of 32 lanes, each over every 8th component
+  const int64_t tile = probe_tile(s, N, ntile);
+  const bool valid = tile * 32 + c < N;
+  const float* lt = lls + (int64_t)s * KP * 32 + c;
+  float M = -INFINITY;
+  for (int k = grp; k < K; k += 8) M = fmaxf(M, lt[k * 32]);
+  mrow[grp][c] = M;
   __syncthreads();
+  M = mrow[0][c];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) M = fmaxf(M, mrow[j][c]);
   unsigned need = 0;
-  if (g == 0 && valid) {
-    float M = -INFINITY;
-    for (int k = 0; k < K; ++k) M = fmaxf(M, lmax[k * 32 + c]);
-    for (int k = wave; k < K; k += kProbeWaves) need += (lmax[k * 32 + c] - M >= -kLjNeedGap) ? 1u : 0u;
-  }
+  if (valid)
+    for (int k = grp; k < K; k += 8) need += (lt[k * 32] - M >= -kLjNeedGap) ? 1u : 0u;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) need += __shfl_xor(need, o);
   if (lane == 0) part[wave] = need;
   __syncthreads();
-  if (tid == 0) {
-    unsigned tot = 0;
-    for (int w = 0; w < kProbeWaves; ++w) tot += part[w];
-    count[s] = tot;
-  }
+  if (tid == 0) count[s] = part[0] + part[1] + part[2] + part[3];
 }
 
 // ---------------------------------------------------------------------------
@@ -1375,10 +1387,15 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
                               : ProbeSel{nullptr, 0, 0};
   if (run1) {
     if constexpr (flj_applies(DP)) {
-      if (pl.autolj)
-        hipLaunchKernelGGL((full_store_probe<DP>), dim3((unsigned)pl.nprobe), dim3(64 * kProbeWaves), 0, stream, X,
-                           ldx, pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
-                           reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.nprobe, probe);
+      if (pl.autolj) {
+        // The probe's log-joints follow its counts in the workspace.
+        float* lls = reinterpret_cast<float*>(ws + pl.off_probe + probe_bytes());
+        hipLaunchKernelGGL((full_probe_ll<DP>), dim3((unsigned)(pl.nprobe * kProbeSplit)), dim3(64 * kProbeWaves), 0,
+                           stream, X, ldx, pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
+                           reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, pl.nprobe, lls);
+        hipLaunchKernelGGL(full_probe_count, dim3((unsigned)pl.nprobe), dim3(256), 0, stream, pl.N, (int)pl.K, pl.KP,
+                           pl.nprobe, lls, probe);
+      }
     }
     constexpr size_t lds1 = full_x6_lds_bytes<DP>();
     // The stored plan runs up to D = 128 only; above, the default plan keeps the

@@ -117,8 +117,9 @@ def test_iso_workspace_holds_stored_log_joint():
     # Full: stored whenever it fits, 32 floats per (32-row tile, component).
     q, qx = L.fgmm_full_workspace_bytes, L.fgmm_full_workspace_bytes_ex
     # Full STORE_LOGJOINT_AUTO (D <= 64, K <= 512): the default plan plus the kept
-    # log-joint (tiles rounded to 4 per pass-1 workgroup) and the probe's counts.
-    f_lj = -(-250_000 // 128) * 4 * 256 * 32 * 4
+    # log-joint (tiles rounded to 4 per pass-1 workgroup), the probe's counts and its
+    # log-joints of 64 sampled tiles.
+    f_lj = -(-250_000 // 128) * 4 * 256 * 32 * 4 + 64 * 256 * 32 * 4
     assert f_lj <= qx(250_000, 256, 64, A) - q(250_000, 256, 64) <= f_lj + 2 * 256
     assert qx(250_000, 256, 96, A) == q(250_000, 256, 96)
     assert qx(250_000, 600, 64, A) == q(250_000, 600, 64)
