@@ -184,7 +184,7 @@ __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB);
 __host__ __device__ constexpr size_t bf16_lse_lds_base(int DP) {
   return (size_t)2 * (DP / 16) * 64 * 16 + (size_t)2 * 32 * 16;   // mu blocks (bf16x8) and constants (f32x4)
 }
-constexpr int kLjtWavesPlan = 8;   // component blocks per stored pass-2 workgroup up to D = 128 (iso_accum_ljt)
+constexpr int kLjtWavesPlan = 4;   // component blocks per stored pass-2 workgroup up to D = 128 (iso_accum_ljt)
 __host__ __device__ constexpr int gather_rs(int DP) { return DP + 16; }   // bf16 row stride of the X tiles
 // The stored plan's bf16 X tiles (hi, lo; 32 rows at that stride) up to D = 128.
 __host__ __device__ constexpr size_t ljt_xsplit_bytes(int DP) { return (size_t)2 * 32 * gather_rs(DP) * 2; }
@@ -226,7 +226,7 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
     p.cpg = bf16_blocks_per_group(p.DP, p.KB);
     p.rgroups = kAccWaves / (p.cpg * bf16_halves(p.DP));
   } else if (p.lj && p.DP <= 128) {
-    p.cpg = kLjtWavesPlan;   // iso_accum_ljt: one wave per block, 8 blocks per workgroup
+    p.cpg = kLjtWavesPlan;   // iso_accum_ljt: one wave per block, 4 blocks per workgroup
     p.lj_nh = 1;
     p.rgroups = 1;
   } else if (p.lj) {
@@ -263,7 +263,9 @@ IsoPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool b
     p.rows_per_slab = cap_slab_rows(round_up(cdiv(N, want), 32), sizeof(double2));
     p.nslab = (int)cdiv(N, p.rows_per_slab);
   } else if (N > 0 && p.ncg > 0) {
-    int64_t want = (int64_t)current_device_cus() / p.ncg;
+    // One 8-wave workgroup per compute unit; the stored pass 2 up to D = 128 runs two
+    // 4-wave workgroups on each.
+    int64_t want = (int64_t)current_device_cus() * (p.lj && p.DP <= 128 ? 8 / kLjtWavesPlan : 1) / p.ncg;
     if (want >= 8) want = (want / 8) * 8;  // keeps a slab's workgroups on one XCD
     if (want < 1) want = 1;
     const int64_t max_slabs = cdiv(N, tile_rows);
@@ -2399,12 +2401,16 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 // the gathering pass: r and x each in two bf16 parts and, per 16-row step, the
 // products r2 x1, r1 x2 and r1 x1 added in that order.
 //
-// Grid over (row slab x group of 8 component blocks); wave w owns block 8 cg + w
-// and that block's partial of the slab.  The workgroups of a slab are dealt to one
-// XCD, so that the X parts come from HBM once and from that XCD's L2 for the other
-// groups.  Three LDS stages, each one tile's X parts, the 8 blocks' log-joint tiles
-// and the logZ2 pairs, all filled by buffer-to-LDS loads: at step t the workgroup
-// issues tile t + 2's, computes tile t and waits for tile t + 1's before the barrier.
+// Grid over (row slab x group of kLjtWaves = 4 component blocks); wave w owns block
+// 4 cg + w and that block's partial of the slab.  The workgroups of a slab are dealt
+// to one XCD, so that the X parts come from HBM once and from that XCD's L2 for the
+// other groups.  Two LDS stages, each one tile's X parts, the 4 blocks' log-joint
+// tiles and the logZ2 pairs, all filled by buffer-to-LDS loads: at step t the
+// workgroup issues tile t + 1's, computes tile t and waits for tile t + 1's before
+// the barrier.  Two such workgroups share a compute unit (one wave of each per
+// SIMD), so one computes while the other waits at its barrier: with one 8-wave
+// workgroup of three stages the waves spent 37% of their cycles waiting (1.32 ms at
+// N=1M, K=1024, D=128 on N(0, I) data; 1.20 ms this way).
 // A wave issues the same loads every step, so that wait is a fixed count of its own
 // outstanding loads, and no global load of the loop is left for the compiler to
 // wait on.  A wave skips a tile whose need word is zero (its loads then read out of
@@ -2415,14 +2421,14 @@ void iso_accum_lj(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 // the kernel returns unless set.
 // ---------------------------------------------------------------------------
 constexpr int kLjtWaves = kLjtWavesPlan;
-constexpr int kLjtStages = 3;
+constexpr int kLjtStages = 2;
 
 template <int DP>
 struct LjtShape {
   static constexpr int XB = (int)ljt_xsplit_bytes(DP);     // a tile's X parts
   static constexpr int XP = XB / 16;                        // their 16-byte pieces, a multiple of 64
   static constexpr int XQ = (XP + 64 * kLjtWaves - 1) / (64 * kLjtWaves);
-  static constexpr int LJB = kLjtWaves * kLjTile * 4;       // the 8 blocks' log-joint tiles
+  static constexpr int LJB = kLjtWaves * kLjTile * 4;       // the blocks' log-joint tiles
   static constexpr int OFF_X = LJB, OFF_Z = LJB + XB;
   static constexpr int STAGE = LJB + XB + 32 * 8;
   // After the stages, one 1 KB line that the loads a wave issues only to keep its
@@ -2613,38 +2619,40 @@ void iso_accum_ljt(const float* __restrict__ lj, const __bf16* __restrict__ xspl
 
   unsigned mk[NS];   // need words of the tiles in the stages
   unsigned mnext = 0u;
-  // Step t, stage S = t mod 3: issue tile t + 2 (stage (S + 2) mod 3, free since the
+  // Step t, stage S = t mod NS: issue tile t + NS - 1 (its stage was freed by the
   // last barrier), compute tile t, wait for tile t + 1's stage (the loads issued
-  // after it are tile t + 2's), barrier.
+  // after it are those of tiles t + 2 ..), barrier.
   auto step = [&](int t, auto stage_tag) __attribute__((always_inline)) {
     constexpr int S = decltype(stage_tag)::value;
-    constexpr int S2 = (S + 2) % NS;
-    mk[S2] = mnext;
-    issue(t + 2, std::integral_constant<int, S2>{}, mnext);
-    mnext = mword(t + 3);
+    constexpr int SI = (S + NS - 1) % NS;
+    mk[SI] = mnext;
+    issue(t + NS - 1, std::integral_constant<int, SI>{}, mnext);
+    mnext = mword(t + NS);
     if (mk[S] != 0u) compute(stage_tag, mk[S]);
-    vm_wait<NL>();
+    vm_wait<(NS - 2) * NL>();
     __syncthreads();
   };
 
   if (ntiles > 0) {
-    mk[0] = mword(0);
-    mk[1] = mword(1);
+#pragma unroll
+    for (int u = 0; u < NS - 1; ++u) mk[u] = mword(u);
     issue(0, std::integral_constant<int, 0>{}, mk[0]);
-    issue(1, std::integral_constant<int, 1>{}, mk[1]);
-    mnext = mword(2);
-    vm_wait<NL>();   // tile 0's stage
+    if constexpr (NS == 3) issue(1, std::integral_constant<int, 1>{}, mk[1]);
+    mnext = mword(NS - 1);
+    vm_wait<(NS - 2) * NL>();   // tile 0's stage
     __syncthreads();
   }
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
-  using S2 = std::integral_constant<int, 2>;
+  using S2 = std::integral_constant<int, 2 % NS>;
   for (int t = 0; t < ntiles; t += NS) {
     step(t, S0{});
     if (t + 1 >= ntiles) break;
     step(t + 1, S1{});
-    if (t + 2 >= ntiles) break;
-    step(t + 2, S2{});
+    if constexpr (NS == 3) {
+      if (t + 2 >= ntiles) break;
+      step(t + 2, S2{});
+    }
   }
   vm_wait<0>();   // no buffer-to-LDS load outlives the workgroup
 
