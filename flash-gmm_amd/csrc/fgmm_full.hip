@@ -1217,7 +1217,7 @@ void full_accum_ljt(const float* __restrict__ X, int64_t ldx, int64_t N, int D, 
       // The group's 8 columns (out of range past KP).
       const int nk = KP - cg * kFljWaves < kFljWaves ? KP - cg * kFljWaves : kFljWaves;
       const DmaSrc lsrc = dma_src(lj + (in ? (tg * KP + cg * kFljWaves) * 32 : 0), in ? (uint32_t)(nk * 128) : 0u);
-      lds_dma16(lsrc, st + SH::OFF_LJ, lane * 16, 0);
+      if (lane < 8 * kFljWaves) lds_dma16(lsrc, st + SH::OFF_LJ, lane * 16, 0);   // 8 lanes per 128-byte column
     } else if (wave == 1) {
       const DmaSrc zsrc = dma_src(rowstat + (in ? row0 : 0), (uint32_t)(nrow * sizeof(double)));
       if (lane < 16) lds_dma16(zsrc, st + SH::OFF_Z, lane * 16, 0);
