@@ -352,3 +352,20 @@ def test_auto_store_full_size_dense(gpu_device):
     part = flash_gmm_estep_diag(*[sub[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")])
     torch.cuda.synchronize()
     check_wide(part, sub, "diag auto N=32768 K=1024 D=96 dense", 96)
+
+
+def test_auto_store_accumulate_over_chunks(gpu_device):
+    """FGMM_FLAG_ACCUMULATE with the stored branch selected: three row chunks added
+    into the outputs equal one call over all rows (to float32 rounding)."""
+    dev = gpu_device
+    inp = data.diag_reference_smoke(9000, 256, 96, seed=7)
+    args = [inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
+    ref = _into(inp, dev, store_log_joint="auto")
+    K, D = 256, 96
+    nk, ma, sg = torch.zeros(K, device=dev), torch.zeros(K, D, device=dev), torch.zeros(K, D, device=dev)
+    for n0 in range(0, 9000, 3000):
+        diag_estep_into(args[0][n0:n0 + 3000], *args[1:], None, nk, ma, sg, accumulate=True, store_log_joint="auto")
+    torch.cuda.synchronize()
+    torch.testing.assert_close(nk, ref[1], rtol=1e-5, atol=1e-4)
+    torch.testing.assert_close(ma, ref[2], rtol=1e-5, atol=1e-5 * float(ref[2].abs().max()))
+    torch.testing.assert_close(sg, ref[3], rtol=1e-5, atol=1e-5 * float(ref[3].abs().max()))

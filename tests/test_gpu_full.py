@@ -284,3 +284,20 @@ def test_auto_store_full_size_dense(gpu_device):
     sub = {k: (v[:8192].cpu() if k == "X" else v.cpu()) for k, v in inp.items()}
     part = run_gpu(sub, dev)
     assert_close_stats(part, oracle(sub), "full auto N=8192 K=256 D=64 dense")
+
+
+def test_auto_store_accumulate_over_chunks(gpu_device):
+    """FGMM_FLAG_ACCUMULATE with the stored branch selected: three row chunks added
+    into the outputs equal one call over all rows (to float32 rounding)."""
+    dev = gpu_device
+    inp = data.full_reference_smoke(6000, 128, 64, seed=7)
+    args = [inp[k].to(dev) for k in KEYS]
+    ref = _into(inp, dev, store_log_joint="auto")
+    K, D = 128, 64
+    nk, ma, so = torch.zeros(K, device=dev), torch.zeros(K, D, device=dev), torch.zeros(K, D, D, device=dev)
+    for n0 in range(0, 6000, 2000):
+        full_estep_into(args[0][n0:n0 + 2000], *args[1:], None, nk, ma, so, accumulate=True, store_log_joint="auto")
+    torch.cuda.synchronize()
+    torch.testing.assert_close(nk, ref[1], rtol=1e-5, atol=1e-4)
+    torch.testing.assert_close(ma, ref[2], rtol=1e-5, atol=1e-5 * float(ref[2].abs().max()))
+    torch.testing.assert_close(so, ref[3], rtol=1e-5, atol=1e-5 * float(ref[3].abs().max()))

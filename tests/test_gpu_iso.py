@@ -275,6 +275,24 @@ def test_accumulate_over_chunks_equals_one_call(gpu_device):
     torch.testing.assert_close(sig, ref[3], rtol=1e-5, atol=1e-4)
 
 
+def test_auto_store_accumulate_over_chunks(gpu_device):
+    """FGMM_FLAG_ACCUMULATE with the stored branch selected (dense data): three row
+    chunks added into the outputs equal one call over all rows (to float32 rounding)."""
+    inp = data.reference_smoke(9000, 256, 128, seed=10)
+    dev = gpu_device
+    args = [inp[k].to(dev) for k in ("X", "mu", "log_sigma_sq", "log_pi")]
+    ref = _into(inp, dev, store_log_joint="auto")
+    K, D = 256, 128
+    nk, mu_acc, sig = torch.zeros(K, device=dev), torch.zeros(K, D, device=dev), torch.zeros(K, device=dev)
+    for n0 in range(0, 9000, 3000):
+        iso_estep_into(args[0][n0:n0 + 3000], *args[1:], None, nk, mu_acc, sig, accumulate=True,
+                       store_log_joint="auto")
+    torch.cuda.synchronize()
+    torch.testing.assert_close(nk, ref[1], rtol=1e-5, atol=1e-4)
+    torch.testing.assert_close(mu_acc, ref[2], rtol=1e-5, atol=1e-5 * float(ref[2].abs().max()))
+    torch.testing.assert_close(sig, ref[3], rtol=1e-5, atol=1e-5 * float(ref[3].abs().max()))
+
+
 def test_headline_shape_mid_size(gpu_device):
     """K=1024, D=128 clustered data at N=65,536 against the float64 oracle."""
     inp = data.iso_clustered(65536, 1024, 128, seed=1)
