@@ -163,10 +163,13 @@ int fgmm_iso_estep_f32(const float *X, int64_t ldx, int64_t N, int64_t D,
 /* own code object, which HIP loads on a GPU at its first use there: the first */
 /* noalloc call on that GPU reserves it (other entry points never do; with     */
 /* deferred loading off, HIP_ENABLE_DEFERRED_LOADING=0, every code object is   */
-/* loaded with the library), and it is held until the process ends.  Calls     */
-/* whose workspace                                                             */
-/* (fgmm_iso_workspace_bytes_ex with the same flags) exceeds it return         */
-/* FGMM_ERR_SCRATCH: about 1.5M rows at K=1024, D=128 (N=1M fits).             */
+/* loaded with the library), and it is held until the process ends.  A call   */
+/* whose workspace (fgmm_iso_workspace_bytes_ex with the same flags) exceeds   */
+/* it (above about 1.5M rows at K=1024, D=128) runs as consecutive row chunks  */
+/* on the array, each after the first adding its statistics to the outputs:   */
+/* logZ is the one-call result per row, the statistics round once per chunk.   */
+/* Such a call with FGMM_FLAG_PHASE1 or PHASE2, or one where not even 256 rows */
+/* fit, returns FGMM_ERR_SCRATCH.                                              */
 /* FGMM_FLAG_STORE_LOGJOINT is rejected (FGMM_ERR_INVALID_ARG).  Every call on */
 /* a GPU uses that GPU's one array: calls that overlap on one GPU (different   */
 /* streams or host threads without ordering) race, and a PHASE2 call reads     */

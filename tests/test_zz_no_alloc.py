@@ -105,9 +105,30 @@ def test_noalloc_phase_split_and_bf16(gpu_device):
         assert torch.equal(u, v)
 
 
+def test_noalloc_runs_row_chunks_beyond_its_scratch(gpu_device):
+    """Beyond FGMM_NOALLOC_SCRATCH_BYTES of one call's workspace the entry point runs
+    consecutive row chunks on its array: logZ bitwise the workspace entry point's (a
+    row's log-normaliser does not depend on the other rows), the statistics to float32
+    rounding (they are added once per chunk), and against invariants of all rows."""
+    L = _lib.lib()
+    dev = gpu_device
+    N, K, D = 3_000_000, 1024, 128
+    assert L.fgmm_iso_workspace_bytes(N, K, D) > 64 << 20
+    inp = data.iso_clustered(N, K, D, seed=36, device=dev)
+    ref = _run(inp, dev, noalloc=False)
+    got = _run(inp, dev, noalloc=True)
+    assert torch.equal(got[0], ref[0])
+    for u, v in zip(got[1:], ref[1:]):
+        assert float((u - v).abs().max()) <= 1e-5 * float(v.abs().max())
+    assert abs(got[1].double().sum().item() - N) <= 1e-5 * N
+    torch.testing.assert_close(got[2].double().sum(0), inp["X"].double().sum(0), rtol=1e-5,
+                               atol=1e-5 * float(got[2].abs().sum(0).max()))
+
+
 def test_noalloc_rejects_what_does_not_fit(gpu_device):
-    """Beyond FGMM_NOALLOC_SCRATCH_BYTES of workspace: FGMM_ERR_SCRATCH, nothing launched;
-    the stored log-joint: FGMM_ERR_INVALID_ARG."""
+    """A phase-split call beyond FGMM_NOALLOC_SCRATCH_BYTES of workspace (it cannot span
+    row chunks): FGMM_ERR_SCRATCH, nothing launched; the stored log-joint:
+    FGMM_ERR_INVALID_ARG."""
     L = _lib.lib()
     dev = gpu_device
     N, K, D = 4_000_000, 1024, 128
@@ -116,10 +137,14 @@ def test_noalloc_rejects_what_does_not_fit(gpu_device):
     mu = torch.zeros(K, D, device=dev)
     lss, lpi = torch.zeros(K, device=dev), torch.zeros(K, device=dev)
     o = _outputs(N, K, D, dev)
-    st = L.fgmm_iso_estep_f32_noalloc(X.data_ptr(), D, N, D, mu.data_ptr(), D, K, lss.data_ptr(),
-                                      lpi.data_ptr(), *[t.data_ptr() for t in o], 0, _lib.stream_handle(dev))
-    assert st == _lib.FGMM_ERR_SCRATCH
+    for ph in (_lib.FLAG_PHASE1, _lib.FLAG_PHASE2):
+        st = L.fgmm_iso_estep_f32_noalloc(X.data_ptr(), D, N, D, mu.data_ptr(), D, K, lss.data_ptr(),
+                                          lpi.data_ptr(), *[t.data_ptr() for t in o], ph,
+                                          _lib.stream_handle(dev))
+        assert st == _lib.FGMM_ERR_SCRATCH
     assert "scratch" in L.fgmm_strerror(st).decode()
+    torch.cuda.synchronize()
+    assert torch.isnan(o[1]).all()   # nothing was written
     small = data.iso_clustered(100, 40, 32, seed=34)
     Xs, mus, lsss, lpis = _inputs(small, dev)
     os_ = _outputs(100, 40, 32, dev)
