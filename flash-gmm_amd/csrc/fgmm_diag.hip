@@ -2505,11 +2505,21 @@ __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB) {
          (size_t)2 * (256 / (CB * bf16_parts(DP))) * sizeof(float) +
          (bf16_parts(DP) > 1 ? (size_t)kAccWaves * 16 * 64 * sizeof(float) : 0);
 }
+// The next super-tile waits in registers (float4 per thread) while one is processed.
+// The staging each part count leaves room for without spilling to scratch (two parts
+// keep a split r and the exchange's sums besides): 8, 4 and 6 float4.
+__host__ __device__ constexpr int bf16_stage_cap(int DP) {
+  return bf16_parts(DP) == 1 ? 8 : bf16_parts(DP) == 2 ? 4 : 6;
+}
+__host__ __device__ constexpr bool bf16_accum_fits(int DP, int CB) {
+  return bf16_accum_lds_bytes(DP, CB) <= kMaxLds &&
+         (256 / (CB * bf16_parts(DP))) * (DP / 4) / kAccThreads <= bf16_stage_cap(DP);
+}
 // Component blocks per pass-2 workgroup: as many as 8 waves hold (4, or 2 with four
-// parts), fewer when K has fewer blocks so that no wave idles.
+// parts), fewer when K has fewer blocks so that no wave idles, where that shape fits.
 __host__ inline int bf16_blocks_per_group(int DP, int KB) {
   int cb = bf16_parts(DP) == 4 ? 2 : 4;
-  while (cb > 1 && KB <= cb / 2 && bf16_accum_lds_bytes(DP, cb / 2) <= kMaxLds) cb /= 2;
+  while (cb > 1 && KB <= cb / 2 && bf16_accum_fits(DP, cb / 2)) cb /= 2;
   return cb;
 }
 
@@ -3188,7 +3198,7 @@ hipError_t launch_bf16(const DiagPlan& pl, const float* X, int64_t ldx, unsigned
       return hipErrorInvalidValue;   // never chosen by the plan
     } else {
       constexpr size_t lds = bf16_accum_lds_bytes(DP, CB);
-      if constexpr (lds > kMaxLds) {
+      if constexpr (!bf16_accum_fits(DP, CB)) {
         return hipErrorInvalidValue;   // never chosen by the plan
       } else {
         if (lds > 65536) {

@@ -390,21 +390,20 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
   // Both half-waves hold row c's log-joint; both store it (same value, same address).
   float* ljt = LJ ? lj + tile * KP * 32 + c : nullptr;
 
-  // Stage s = k NST + sub holds blocks SMB sub .. of component k: contiguous in
-  // l3 and esw.
-  bf16x8 st[LPT];
-  double est = 0.0;
+  // Stage s = k NST + sub holds blocks SMB sub .. of component k: contiguous in l3
+  // and esw.  Both reach LDS buffer s & 1 by buffer-to-LDS loads (no staging
+  // registers): LPT 16-byte pieces per lane of the operands, and the NE e values from
+  // the first NE / 2 lanes of wave 0.
   auto fetch = [&](int64_t s) {
-    const bf16x8* src = l3 + s * BLK;
+    const DmaSrc r = dma_src(l3 + s * BLK, (uint32_t)(BLK * sizeof(bf16x8)));
+    bf16x8* dst = l_l + (s & 1) * BLK + wave * 64;
 #pragma unroll
-    for (int q = 0; q < LPT; ++q) st[q] = src[q * kThreads + tid];
-    if (tid < NE) est = esw[s * NE + tid];
-    else if (tid == NE) est = ck[s / NST];
-  };
-  auto commit = [&](int buf) {
-#pragma unroll
-    for (int q = 0; q < LPT; ++q) l_l[buf * BLK + q * kThreads + tid] = st[q];
-    if (tid <= NE) e_l[buf * BW + tid] = est;
+    for (int q = 0; q < LPT; ++q)
+      lds_dma16(r, dst + q * kThreads, tid * (int)sizeof(bf16x8), q * kThreads * (int)sizeof(bf16x8));
+    if (wave == 0 && lane < NE / 2) {
+      const DmaSrc re = dma_src(esw + s * NE, (uint32_t)(NE * sizeof(double)));
+      lds_dma16(re, e_l + (s & 1) * BW, lane * 16, 0);
+    }
   };
   fetch(0);
   // This lane's row, dimensions 16q + 8g .. +7, split three ways.
@@ -415,8 +414,7 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
     split3_bf16(load_row4(X, ldx, row, d0, D, valid), load_row4(X, ldx, row, d0 + 4, D, valid), xb[q]);
   }
   const bf16x8 ones = x6c_ones(lane);
-  commit(0);
-  __syncthreads();
+  dma_barrier();
 
   const double hl = 0.5 * kLog2e;
   double mx = -INFINITY;
@@ -426,8 +424,10 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
   double maha = 0.0;
   for (int64_t s = 0; s < nstage; ++s) {
     const int buf = (int)(s & 1);
-    const bool more = s + 1 < nstage;
-    if (more) fetch(s + 1);
+    if (s + 1 < nstage) fetch(s + 1);
+    // Component s / NST completes with this stage: its constant, read early.
+    const bool done = NST == 1 || (int)(s % NST) == NST - 1;
+    const double ckv = done ? ck[s / NST] : 0.0;
     const bf16x8* lc = l_l + buf * BLK + lane;
     const double* ec = e_l + buf * BW;
 #pragma unroll
@@ -443,9 +443,13 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
         maha = fma(v, v, maha);
       }
     }
-    if (NST == 1 || (int)(s % NST) == NST - 1) {   // component s / NST complete
+    // Stage s + 1 has landed and every wave is done with buffer buf, which stage s + 2
+    // fills; what follows reads registers only.  The stores below are in flight behind
+    // the next stage's contraction (this wait also drains them, a stage later).
+    dma_barrier();
+    if (done) {   // component s / NST complete
       maha += __shfl_xor(maha, 32);
-      const double ll = ec[NE] - hl * maha;
+      const double ll = ckv - hl * maha;
       if constexpr (LJ) ljt[(s / NST) * 32] = (float)ll;
       if constexpr (LJM == kLjmNeed) {
         const int64_t k = s / NST;
@@ -466,8 +470,6 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
       mx = mn;
       maha = 0.0;
     }
-    if (more) commit(buf ^ 1);
-    lds_barrier();
   }
   const double lz2 = mx + (double)log2f(sm);
   if (valid && g == 0) {

@@ -3388,6 +3388,11 @@ __global__ __launch_bounds__(kThreads) void iso_bf16_lse(const float* __restrict
 // The row stride (DP + 16 bf16) is an odd multiple of 32 bytes, the stride the
 // transposing reads want.
 __host__ __device__ constexpr int bf16_xr_stride(int DP) { return DP + 16; }   // bf16 per X row
+// The next super-tile waits in registers (float4 per thread) while this one is
+// processed: at most 8 float4 where the halves of D need no exchange, 6 where they do
+// (its buffer and the two halves' sums take the rest); more spills to scratch.
+__host__ __device__ constexpr int bf16_stage_cap(int DP) { return bf16_halves(DP) == 1 ? 8 : 6; }
+__host__ __device__ constexpr int bf16_stage_f4(int TR, int DP) { return TR * (DP / 4) / kAccThreads; }
 // Row groups each wave takes per super-tile: two where the halves of D need no
 // exchange, so every barrier and every tile load covers twice the work.
 __host__ __device__ constexpr int bf16_rows_per_wave(int DP) { return bf16_halves(DP) == 1 ? 2 : 1; }
@@ -3399,9 +3404,16 @@ __host__ __device__ constexpr size_t bf16_accum_lds_bytes(int DP, int CB) {
          (size_t)2 * bf16_tile_rows(DP, CB) * sizeof(float2) +
          (bf16_halves(DP) > 1 ? (size_t)kAccWaves * 16 * 64 * sizeof(float) : 0);
 }
+// Whether iso_bf16_accum<DP, CB> fits: its tiles in LDS, its staging within the cap.
+__host__ __device__ constexpr bool bf16_accum_fits(int DP, int CB) {
+  return bf16_accum_lds_bytes(DP, CB) <= kMaxLds &&
+         bf16_stage_f4(bf16_tile_rows(DP, CB), DP) <= bf16_stage_cap(DP);
+}
+// Component blocks per workgroup: as few as K has (no idle waves), unless that shape
+// does not fit; 4 always does.
 __host__ inline int bf16_blocks_per_group(int DP, int KB) {
-  if (KB <= 1 && bf16_accum_lds_bytes(DP, 1) <= kMaxLds) return 1;
-  if (KB <= 2 && bf16_accum_lds_bytes(DP, 2) <= kMaxLds) return 2;
+  if (KB <= 1 && bf16_accum_fits(DP, 1)) return 1;
+  if (KB <= 2 && bf16_accum_fits(DP, 2)) return 2;
   return 4;
 }
 
@@ -3832,7 +3844,7 @@ hipError_t launch_bf16(const IsoPlan& pl, const float* X, int64_t ldx, unsigned 
   auto launch = [&](auto cb_tag) -> hipError_t {
     constexpr int CB = decltype(cb_tag)::value;
     constexpr size_t lds = bf16_accum_lds_bytes(DP, CB);
-    if constexpr (lds > kMaxLds) {
+    if constexpr (!bf16_accum_fits(DP, CB)) {
       return hipErrorInvalidValue;   // never chosen by the plan
     } else {
       if (lds > 65536) {
