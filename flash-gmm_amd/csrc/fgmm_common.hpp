@@ -265,6 +265,33 @@ __device__ __forceinline__ f32x16 x6c_tile(LA loadA, const bf16x8 (&xb)[NQ][3], 
   return t;
 }
 
+// x6c_tile<NQ, 1> for T tiles of rows at once (xb[u] the B operand of tile u): each
+// A operand read serves all T tiles, and every tile's steps, their order and its one
+// chain are x6c_tile<NQ, 1>'s, so out[u] is the same bits as that call gives.
+template <int NQ, int T, typename LA>
+__device__ __forceinline__ void x6c_tile_multi(LA loadA, const bf16x8 (&xb)[T][NQ][3], const bf16x8 ones,
+                                               f32x16 (&out)[T]) {
+#pragma unroll
+  for (int u = 0; u < T; ++u) out[u] = zero16();
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    bf16x8 a[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) a[t] = loadA(q, t);
+#pragma unroll
+    for (int u = 0; u < T; ++u) {
+#pragma unroll
+      for (int step = 0; step < 7; ++step) {
+        const bf16x8 A = step == 0 ? a[1] : step == 1 ? a[2] : step <= 3 ? a[0]
+                       : step == 4 ? a[1] : step == 5 ? a[3] : a[0];
+        const bf16x8 B = step == 0 ? xb[u][q][1] : step == 1 ? xb[u][q][0] : step == 2 ? xb[u][q][2]
+                       : step == 3 ? xb[u][q][1] : step == 4 ? xb[u][q][0] : step == 5 ? ones : xb[u][q][0];
+        out[u] = mfma_bf16(A, B, out[u]);
+      }
+    }
+  }
+}
+
 // x6c_tile with the operand roles exchanged: A holds the rows' splits (lane m = row,
 // xa[q][s] = split s of dimensions 16q + 8(lane/32) + e) and the ones operand of the
 // offset step, B holds mu's splits and centring offsets (loadB(q, t), lane n =

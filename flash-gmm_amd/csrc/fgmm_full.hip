@@ -54,7 +54,7 @@ struct FullPlan {
   bool lj;      // pass 1 stores the log-joint; pass 2 reads it
   bool bf16;    // bf16 operand contract (FGMM_FLAG_BF16); always stores the log-joint
   bool need;    // default plan: pass 1 leaves need masks, pass 2 gathers
-  bool rexact;  // need masks from the per-(row, component) bounds (else the running max)
+  int needmode; // how pass 1 forms the need masks: kNeedLists, kNeedBounds or kNeedRunMax
   bool wide;    // D > 256: full_lse_wide stores the log-joint, full_accum_wide reads it
   bool keep_lj; // 128 < D <= 256, default plan: pass 1 also stores the log-joint, and the
                 // gathering pass 2 reads r from it instead of whitening the needed rows
@@ -70,24 +70,65 @@ struct FullPlan {
       off_lj, off_need, off_bound, total;
 };
 
-// Need masks of the full model are per (32-row tile, component).  Pass 1 then runs a
-// persistent grid of grid1 workgroups, each wave with a slot of 32 x KP bf16 bounds
-// of its rows' log-joint in the workspace, reused tile after tile; beyond this many
-// components the masks come from the running-max bound instead.
+// One LDS stage holds SMB 32-coordinate blocks of one component: all of them up to
+// D = 64, one above (a whole component's operands, 72 or 128 KiB, would not fit twice).
+__host__ __device__ constexpr int full_x6_smb(int DP) { return DP <= 64 ? DP / 32 : 1; }
+__host__ __device__ constexpr int full_x6_stage(int DP) { return full_x6_smb(DP) * (DP / 16) * 4 * 64; }   // bf16x8
+__host__ __device__ constexpr size_t full_x6_lds_bytes(int DP) {
+  return (size_t)2 * full_x6_stage(DP) * sizeof(bf16x8) + (size_t)2 * (32 * full_x6_smb(DP) + 8) * sizeof(double);
+}
+constexpr size_t kFullLds = 160 * 1024;   // LDS per compute unit
+
+// Need masks of the full model are per (32-row tile, component); pass 1 runs a
+// persistent grid of grid1 workgroups and forms them in one of three ways:
+//   kNeedLists:  each row keeps a list of candidates: the components within
+//                kLjSkipGap of the row's running maximum when they were formed, each
+//                with a bf16 upper bound of its log-joint.  The first
+//                full_list_cands of a row sit in LDS, the rest of its kNeedListCap in
+//                the wave's slot of the workspace, reused tile after tile; a candidate
+//                past those sets its bit at once.  Once logZ2 is final the listed candidates are tested as
+//                need_put_masks tests, into mask words in LDS.  On clustered data a row
+//                has a few tens of candidates, so the workspace sees a few bytes per
+//                row.  Used where the LDS lists and words fit beside the operand
+//                stages.
+//   kNeedBounds: each wave has a slot of 32 x KP bf16 bounds in the workspace, reused
+//                tile after tile (up to kNeedExactMaxK components).
+//   kNeedRunMax: the bit is set when the component is within kLjSkipGap of the running
+//                maximum.
+// The first two give the exact bits (the first unless a row has more than
+// kNeedListCap candidates); otherwise a superset of them.  A pair outside
+// the exact set has responsibility exactly 0, so the outputs are the same bits in every
+// form.
 constexpr int kNeedExactMaxK = 1024;
+constexpr int kNeedRunMax = 0, kNeedBounds = 1, kNeedLists = 2;
+constexpr int kNeedListCap = 64;   // listed candidates per row
+// 32-row tiles per pass-1 wave: two up to D = 64, where the wave's registers hold both
+// tiles' split rows, so that each operand read from LDS serves 64 rows and the
+// operand set streams through the XCD's L2 half as many times.
+__host__ __device__ constexpr int full_x6_tpw(int DP) { return DP <= 64 ? 2 : 1; }
+// Candidates per row in LDS (the rest of a list is in the workspace).
+__host__ __device__ constexpr int full_list_cands(int DP) { return full_x6_tpw(DP) == 2 ? 4 : 16; }
+// Per wave: the LDS candidates of its rows, then a mask word per (tile, component).
+__host__ __device__ constexpr size_t full_list_lds_bytes(int DP, int KP) {
+  return (size_t)kWaves * full_x6_tpw(DP) * ((size_t)full_list_cands(DP) * 32 + (size_t)KP) * sizeof(unsigned);
+}
+// Candidates per row in the workspace.
+__host__ __device__ constexpr int full_list_spill(int DP, int K) {
+  return (K < kNeedListCap ? K : kNeedListCap) > full_list_cands(DP)
+             ? (K < kNeedListCap ? K : kNeedListCap) - full_list_cands(DP)
+             : 0;
+}
 
 // The stored branch of FGMM_FLAG_STORE_LOGJOINT_AUTO runs up to D = 64 (sig_outer's
 // accumulators and split operands of one component fit a wave's registers).
 __host__ __device__ constexpr bool flj_applies(int DP) { return DP <= 64; }
 
-
-
 // Stored log-joint of the full model: per (32-row tile, component) 32 floats, rows
-// contiguous, [tile][KP][32]; one tile per pass-1 wave (the grid's tiles, rounded
-// up to 4).  Pass 2 reads it unless recomputation is requested or it would exceed
+// contiguous, [tile][KP][32]; the tiles of the pass-1 grid (rounded up to 8, a
+// workgroup's tiles with two per wave).  Pass 2 reads it unless recomputation is requested or it would exceed
 // kMaxLjBytes: recomputing costs a D x D whitening per (row, component).
 __host__ inline size_t full_lj_bytes(int64_t N, int KP) {
-  return (size_t)round_up(cdiv(N, 32), 4) * (size_t)KP * 32 * sizeof(float);
+  return (size_t)round_up(cdiv(N, 32), 8) * (size_t)KP * 32 * sizeof(float);
 }
 
 // The gathering pass 2 holds the accumulators of the upper 32x32 blocks of sig_outer
@@ -148,7 +189,10 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.autolj = p.need && auto_lj && flj_applies(p.DP) && N > 0 && K <= kProbeMaxKB &&
              full_lj_bytes(N, p.KP) <= kMaxLjBytes;
   p.nprobe = p.autolj ? (int)std::min<int64_t>(kProbeTiles, cdiv(N, 32)) : 0;
-  p.rexact = p.need && K <= kNeedExactMaxK;
+  p.needmode = !p.need ? kNeedRunMax
+               : full_x6_lds_bytes(p.DP) + full_list_lds_bytes(p.DP, p.KP) <= kFullLds / full_waves_per_eu(p.DP)
+                   ? kNeedLists
+                   : K <= kNeedExactMaxK ? kNeedBounds : kNeedRunMax;
   p.ngrp = gather_sig_groups(p.DP);
   if (bf16) {
     p.ncg = (int)cdiv(K, (int64_t)bf16_comps_per_wg(p.NMB) * bf16_comp_reps(p.NMB));
@@ -216,11 +260,14 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   // Need masks: one word per (32-row tile of the pass-1 grid, component).
   p.grid1 = 0;
   p.off_need = off;
-  if (p.need) off = align256(off + (size_t)round_up(cdiv(N, 32), 4) * p.KP * sizeof(unsigned));
+  if (p.need) off = align256(off + (size_t)round_up(cdiv(N, 32), 8) * p.KP * sizeof(unsigned));
   p.off_bound = off;
   if (p.need && N > 0) {
-    p.grid1 = (int)std::min<int64_t>(cdiv(N, 32 * kWaves), (int64_t)full_waves_per_eu(p.DP) * current_device_cus());
-    if (p.rexact) off = align256(off + (size_t)p.grid1 * kWaves * 32 * p.KP * sizeof(unsigned short));
+    const int tpw = full_x6_tpw(p.DP);
+    p.grid1 = (int)std::min<int64_t>(cdiv(N, 32 * kWaves * tpw), (int64_t)full_waves_per_eu(p.DP) * current_device_cus());
+    const size_t slot_rows = (size_t)p.grid1 * kWaves * 32 * tpw;
+    if (p.needmode == kNeedBounds) off = align256(off + slot_rows * p.KP * sizeof(unsigned short));
+    if (p.needmode == kNeedLists) off = align256(off + slot_rows * full_list_spill(p.DP, (int)K) * sizeof(unsigned));
   }
   p.off_probe = off;
   if (p.autolj) off = align256(off + probe_bytes() + (size_t)p.nprobe * p.KP * 32 * sizeof(float));
@@ -327,48 +374,48 @@ __global__ __launch_bounds__(256) void full_x6_prep(const float* __restrict__ mu
   }
 }
 
-// One LDS stage holds SMB 32-coordinate blocks of one component: all of them up to
-// D = 64, one above (a whole component's operands, 72 or 128 KiB, would not fit twice).
-template <int DP>
-constexpr int full_x6_smb() { return DP <= 64 ? DP / 32 : 1; }
-template <int DP>
-constexpr int full_x6_stage() { return full_x6_smb<DP>() * (DP / 16) * 4 * 64; }   // bf16x8
-template <int DP>
-constexpr size_t full_x6_lds_bytes() {
-  return (size_t)2 * full_x6_stage<DP>() * sizeof(bf16x8) + (size_t)2 * (32 * full_x6_smb<DP>() + 8) * sizeof(double);
-}
 
 // What pass 1 leaves for pass 2 besides logZ2.
 constexpr int kLjmStore = 1;   // the stored log-joint
 constexpr int kLjmNeed = 2;    // need masks only (the default plan)
 
 // With need masks (LJM == kLjmNeed) the grid is persistent: workgroup b takes the
-// 128-row tiles b, b + gridDim.x, ...; wave w of workgroup b keeps the bf16 upper
-// bounds of its rows' log-joint, [component][row], in slot 4 b + w of `bound` (its
-// own writes, read back by the same lanes once logZ2 is final), and writes the need
-// word of each (32-row tile, component): bit r set unless the bound of row r is
-// kLjNeedGap below its logZ2 (need_put_masks).
-// KEEP (with need masks): also store the log-joint, for a pass 2 that reads r.
-template <int DP, int LJM, bool KEEP = false>
+// tile groups b, b + gridDim.x, ... of 32 kWaves TPW rows (TPW = full_x6_tpw 32-row
+// tiles per wave).  Wave w of workgroup b keeps, in its slot 4 b + w of `bound`, the
+// workspace part of its rows' candidate lists (needmode kNeedLists, [row][entry]
+// words, the first entries in LDS) or the bf16 upper bounds of its rows' log-joint
+// (kNeedBounds, [tile][component][row]); each lane reads back its own writes once
+// logZ2 is final.  The wave writes the need word of each (32-row tile, component): bit
+// r set unless the bound of row r is kLjNeedGap below its logZ2 (need_put_masks).
+// KEEP (with need masks): also store the log-joint, for a pass 2 that reads r.  NM is
+// the need-mask form (one body per form keeps the others' registers out of the
+// contraction loop).
+template <int DP, int LJM, bool KEEP = false, int NM = kNeedRunMax>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(full_waves_per_eu(DP), full_waves_per_eu(DP))))
 void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, const bf16x8* __restrict__ l3,
                  const double* __restrict__ esw, const double* __restrict__ ck, int K, int KP,
                  float* __restrict__ logZ, double* __restrict__ rowstat, float* __restrict__ lj,
-                 unsigned* __restrict__ need, unsigned short* __restrict__ bound, int rexact, int dense,
-                 ProbeSel probe) {
+                 unsigned* __restrict__ need, unsigned short* __restrict__ bound, int dense, ProbeSel probe) {
+  constexpr int needmode = NM;
   constexpr bool LJ = LJM == kLjmStore || KEEP;
   static_assert(!KEEP || LJM == kLjmNeed, "KEEP adds the log-joint to the need masks");
+  // The stored branch's instance (D <= 64): its pass 2 (full_accum_ljt) reads r from
+  // the kept log-joint and no need masks, so none are formed.  Above D = 128 the
+  // gathering pass 2 reads both.
+  constexpr bool MASKS = LJM == kLjmNeed && !(KEEP && flj_applies(DP));
   // FGMM_FLAG_STORE_LOGJOINT_AUTO launches both need-mask instances; the probe's
   // counts let the KEEP one (the stored branch) or the other run.
   if (probe.count != nullptr && probe_selects(probe) != KEEP) return;
   constexpr int NMB = DP / 32, NQ = DP / 16;
-  constexpr int SMB = full_x6_smb<DP>();          // coordinate blocks per stage
+  constexpr int SMB = full_x6_smb(DP);            // coordinate blocks per stage
   constexpr int NST = NMB / SMB;                  // stages per component
-  constexpr int BLK = full_x6_stage<DP>();        // bf16x8 per stage
+  constexpr int BLK = full_x6_stage(DP);          // bf16x8 per stage
   constexpr int LPT = BLK / kThreads;
   constexpr int NE = 32 * SMB;                    // e values per stage
   constexpr int BW = NE + 8;                      // doubles per stage (e, then c)
+  constexpr int TPW = full_x6_tpw(DP);            // 32-row tiles per wave
+  constexpr int NC = full_list_cands(DP);         // candidates per row in LDS
   static_assert(BLK % kThreads == 0 && kThreads > NE, "even split");
 
   extern __shared__ __align__(16) unsigned char lds_raw[];
@@ -378,17 +425,31 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, g = lane >> 5;
-  const int64_t ntw = cdiv(N, 32 * kWaves);
+  const bool lists = MASKS && needmode == kNeedLists;
+  // kNeedLists: the wave's LDS candidates [NC][TPW * 32 rows] (component << 16 | bf16
+  // bound), then its mask words [TPW][KP]; the rest of row u's list at spill + u 32 nsp.
+  unsigned* cand_l = reinterpret_cast<unsigned*>(lds_raw + full_x6_lds_bytes(DP)) +
+                     wave * TPW * (NC * 32 + KP);
+  unsigned* word_l = cand_l + NC * 32 * TPW;
+  if (lists)
+    for (int k = lane; k < TPW * KP; k += 64) word_l[k] = 0u;
+  const int nsp = full_list_spill(DP, K);
+  const int64_t slot = (int64_t)blockIdx.x * kWaves + wave;
+  unsigned* spill = lists ? reinterpret_cast<unsigned*>(bound) + (slot * TPW * 32 + c) * nsp : nullptr;
+  unsigned short* bnd = MASKS && needmode == kNeedBounds ? bound + slot * TPW * 32 * KP : nullptr;
+  const int64_t ntw = cdiv(N, 32 * kWaves * TPW);
   const int64_t tw_step = LJM == kLjmNeed ? (int64_t)gridDim.x : ntw;
-  unsigned short* bnd = LJM == kLjmNeed && rexact
-                            ? bound + ((int64_t)blockIdx.x * kWaves + wave) * 32 * KP : nullptr;
 
   for (int64_t tw = blockIdx.x; tw < ntw; tw += tw_step) {
-  const int64_t tile = tw * kWaves + wave;   // 32-row tile
-  const int64_t row = tile * 32 + c;
-  const bool valid = row < N;
-  // Both half-waves hold row c's log-joint; both store it (same value, same address).
-  float* ljt = LJ ? lj + tile * KP * 32 + c : nullptr;
+  int64_t tile[TPW];   // the wave's 32-row tiles
+  bool valid[TPW];     // this lane's row of each
+  int ncand[TPW];      // the row's listed candidates (kNeedLists; lanes of half-wave 0)
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    tile[u] = (tw * kWaves + wave) * TPW + u;
+    valid[u] = tile[u] * 32 + c < N;
+    ncand[u] = 0;
+  }
 
   // Stage s = k NST + sub holds blocks SMB sub .. of component k: contiguous in l3
   // and esw.  Both reach LDS buffer s & 1 by buffer-to-LDS loads (no staging
@@ -406,22 +467,32 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
     }
   };
   fetch(0);
-  // This lane's row, dimensions 16q + 8g .. +7, split three ways.
-  bf16x8 xb[NQ][3];
+  // This lane's rows, dimensions 16q + 8g .. +7, split three ways.
+  bf16x8 xb[TPW][NQ][3];
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) {
-    const int d0 = 16 * q + 8 * g;
-    split3_bf16(load_row4(X, ldx, row, d0, D, valid), load_row4(X, ldx, row, d0 + 4, D, valid), xb[q]);
+  for (int u = 0; u < TPW; ++u) {
+    const int64_t row = tile[u] * 32 + c;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int d0 = 16 * q + 8 * g;
+      split3_bf16(load_row4(X, ldx, row, d0, D, valid[u]), load_row4(X, ldx, row, d0 + 4, D, valid[u]),
+                  xb[u][q]);
+    }
   }
   const bf16x8 ones = x6c_ones(lane);
   dma_barrier();
 
   const double hl = 0.5 * kLog2e;
-  double mx = -INFINITY;
-  float sm = 0.0f;
-  float run_max = -INFINITY;   // need masks from the running max (not rexact)
+  double mx[TPW], maha[TPW];
+  float sm[TPW], run_max[TPW];   // run_max: the running-max need bound (not kNeedBounds)
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    mx[u] = -INFINITY;
+    maha[u] = 0.0;
+    sm[u] = 0.0f;
+    run_max[u] = -INFINITY;
+  }
   const int64_t nstage = (int64_t)K * NST;
-  double maha = 0.0;
   for (int64_t s = 0; s < nstage; ++s) {
     const int buf = (int)(s & 1);
     if (s + 1 < nstage) fetch(s + 1);
@@ -433,14 +504,19 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
 #pragma unroll
     for (int mb = 0; mb < SMB; ++mb) {
       // lane = row, register i = whitened coordinate 32 mb + acc_row(i, g).  One
-      // accumulation chain: no chain sums, and 3.12 ms against 3.56 ms with four at
-      // N=250K, K=256, D=64.
-      const f32x16 t = x6c_tile<NQ, 1>([&](int q, int u) { return lc[((mb * NQ + q) * 4 + u) * 64]; }, xb, ones);
+      // accumulation chain per tile: no chain sums, and 3.12 ms against 3.56 ms with
+      // four at N=250K, K=256, D=64.
+      f32x16 t[TPW];
+      x6c_tile_multi<NQ, TPW>([&](int q, int v) { return lc[((mb * NQ + q) * 4 + v) * 64]; }, xb, ones, t);
       const double* eb = ec + mb * 32 + g * 16;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const double v = (double)t[i] + eb[i];
-        maha = fma(v, v, maha);
+        const double e = eb[i];
+#pragma unroll
+        for (int u = 0; u < TPW; ++u) {
+          const double v = (double)t[u][i] + e;
+          maha[u] = fma(v, v, maha[u]);
+        }
       }
     }
     // Stage s + 1 has landed and every wave is done with buffer buf, which stage s + 2
@@ -448,44 +524,93 @@ void full_lse_x6(const float* __restrict__ X, int64_t ldx, int64_t N, int D, con
     // the next stage's contraction (this wait also drains them, a stage later).
     dma_barrier();
     if (done) {   // component s / NST complete
-      maha += __shfl_xor(maha, 32);
-      const double ll = ckv - hl * maha;
-      if constexpr (LJ) ljt[(s / NST) * 32] = (float)ll;
-      if constexpr (LJM == kLjmNeed) {
-        const int64_t k = s / NST;
-        if (rexact) {
-          if (g == 0) bnd[k * 32 + c] = bf16_bits_up((float)ll);
-        } else {
-          // logZ2 >= the row's final maximum >= run_max (less a rounding), so a
-          // component kLjSkipGap below the running max cannot reach need_put_masks' test.
-          run_max = fmaxf(run_max, (float)ll);
-          const bool nb = valid && (dense != 0 || !((float)ll - run_max < -kLjSkipGap));
-          const unsigned bits = (unsigned)__builtin_amdgcn_ballot_w64(nb);
-          if (lane == 0) need[tile * KP + k] = bits;
+      const int k = (int)(s / NST);
+#pragma unroll
+      for (int u = 0; u < TPW; ++u) {
+        maha[u] += __shfl_xor(maha[u], 32);
+        const double ll = ckv - hl * maha[u];
+        // Both half-waves hold row c's log-joint; both store it (same value, address).
+        if constexpr (LJ) lj[(tile[u] * KP + k) * 32 + c] = (float)ll;
+        if constexpr (MASKS) {
+          if (needmode == kNeedBounds) {
+            if (g == 0) bnd[((int64_t)u * KP + k) * 32 + c] = bf16_bits_up((float)ll);
+          } else {
+            // logZ2 >= the row's final maximum >= run_max (less a rounding), so a
+            // component kLjSkipGap below the running max cannot reach need_put_masks'
+            // test (with |run_max| < 2^24, where those roundings stay far inside the
+            // margin).
+            run_max[u] = fmaxf(run_max[u], (float)ll);
+            const bool near = !(fabsf(run_max[u]) < 0x1p24f && (float)ll - run_max[u] < -kLjSkipGap);
+            if (lists) {
+              // A candidate goes on the row's list (the LDS part, then the workspace
+              // part), or past its end sets its bit now.
+              if (valid[u] && g == 0 && dense == 0 && near) {
+                const unsigned e = ((unsigned)k << 16) | bf16_bits_up((float)ll);
+                const int n = ncand[u];
+                if (n < NC) {
+                  cand_l[n * TPW * 32 + u * 32 + c] = e;
+                  ncand[u] = n + 1;
+                } else if (n < NC + nsp) {
+                  spill[(int64_t)u * 32 * nsp + n - NC] = e;
+                  ncand[u] = n + 1;
+                } else {
+                  atomicOr(word_l + u * KP + k, 1u << c);
+                }
+              }
+            } else {
+              const unsigned bits = (unsigned)__builtin_amdgcn_ballot_w64(valid[u] && (dense != 0 || near));
+              if (lane == 0) need[tile[u] * KP + k] = bits;
+            }
+          }
         }
+        const double mn = fmax(mx[u], ll);
+        const double ms = (mn == -INFINITY) ? 0.0 : mn;
+        sm[u] = sm[u] * fast_exp2((float)(mx[u] - ms)) + fast_exp2((float)(ll - ms));
+        mx[u] = mn;
+        maha[u] = 0.0;
       }
-      const double mn = fmax(mx, ll);
-      const double ms = (mn == -INFINITY) ? 0.0 : mn;
-      sm = sm * fast_exp2((float)(mx - ms)) + fast_exp2((float)(ll - ms));
-      mx = mn;
-      maha = 0.0;
     }
   }
-  const double lz2 = mx + (double)log2f(sm);
-  if (valid && g == 0) {
-    rowstat[row] = lz2;
-    if (logZ) logZ[row] = (float)(lz2 * kLn2);
-  }
-  if constexpr (LJM == kLjmNeed) {
-    if (rexact) {
-      if (g == 0)
-        need_put_masks([&](int k) { return bf16_bits_to_float(bnd[(int64_t)k * 32 + c]); }, need + tile * KP,
-                       nullptr, K, c, lz2, valid, dense != 0);
-    } else {
-      // A row whose logZ2 is NaN gets its bit for every component, as the exact test gives it.
-      const unsigned nanbits = (unsigned)__builtin_amdgcn_ballot_w64(valid && g == 0 && lz2 != lz2);
-      if (lane == 0 && nanbits != 0)
-        for (int k = 0; k < K; ++k) need[tile * KP + k] |= nanbits;
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    const int64_t row = tile[u] * 32 + c;
+    const double lz2 = mx[u] + (double)log2f(sm[u]);
+    if (valid[u] && g == 0) {
+      rowstat[row] = lz2;
+      if (logZ) logZ[row] = (float)(lz2 * kLn2);
+    }
+    if constexpr (MASKS) {
+      if (needmode == kNeedBounds) {
+        const unsigned short* bt = bnd + (int64_t)u * KP * 32 + c;
+        if (g == 0)
+          need_put_masks([&](int k) { return bf16_bits_to_float(bt[(int64_t)k * 32]); }, need + tile[u] * KP,
+                         nullptr, K, c, lz2, valid[u], dense != 0);
+      } else if (lists) {
+        // need_put_masks' test on the row's candidates, then the words out (coalesced)
+        // and cleared for the next tile.  A row whose logZ2 is NaN gets every bit, and
+        // with `dense` every valid row does, as need_put_masks gives them.
+        const float zx = (float)lz2;
+        const float zy = (lz2 > -INFINITY && lz2 < INFINITY) ? (float)(lz2 - (double)zx) : 0.0f;
+        unsigned* wu = word_l + u * KP;
+        for (int i = 0; i < ncand[u]; ++i) {
+          const unsigned e = i < NC ? cand_l[i * TPW * 32 + u * 32 + c] : spill[(int64_t)u * 32 * nsp + i - NC];
+          const float R = bf16_bits_to_float((unsigned short)(e & 0xffffu));
+          if (!(((R - zx) - zy) < -kLjNeedGap)) atomicOr(wu + (e >> 16), 1u << c);
+        }
+        const unsigned vbits = (unsigned)__builtin_amdgcn_ballot_w64(valid[u] && g == 0);
+        const unsigned nanbits = (unsigned)__builtin_amdgcn_ballot_w64(valid[u] && g == 0 && lz2 != lz2);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's ORs before its reads
+        for (int k = lane; k < K; k += 64) {
+          need[tile[u] * KP + k] = dense != 0 ? vbits : (wu[k] | nanbits);
+          wu[k] = 0u;
+        }
+      } else {
+        // A row whose logZ2 is NaN gets its bit for every component, as the exact test
+        // gives it.
+        const unsigned nanbits = (unsigned)__builtin_amdgcn_ballot_w64(valid[u] && g == 0 && lz2 != lz2);
+        if (lane == 0 && nanbits != 0)
+          for (int k = 0; k < K; ++k) need[tile[u] * KP + k] |= nanbits;
+      }
     }
   }
   }
@@ -1399,24 +1524,32 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
                            pl.nprobe, lls, probe);
       }
     }
-    constexpr size_t lds1 = full_x6_lds_bytes<DP>();
+    const size_t lds1 = full_x6_lds_bytes(DP) + (pl.needmode == kNeedLists ? full_list_lds_bytes(DP, pl.KP) : 0);
     // The stored plan runs up to D = 128 only; above, the default plan keeps the
     // log-joint beside the need masks (keep_lj) where it fits.
+    // The need-mask instances, one per form.
+    auto need_kern = [&](auto keep_tag) {
+      constexpr bool KEEP = decltype(keep_tag)::value;
+      return pl.needmode == kNeedLists    ? &full_lse_x6<DP, kLjmNeed, KEEP, kNeedLists>
+             : pl.needmode == kNeedBounds ? &full_lse_x6<DP, kLjmNeed, KEEP, kNeedBounds>
+                                          : &full_lse_x6<DP, kLjmNeed, KEEP, kNeedRunMax>;
+    };
     auto kern = (DP > 128 || pl.need)
-                    ? (DP > 128 && pl.keep_lj ? &full_lse_x6<DP, kLjmNeed, (DP > 128)> : &full_lse_x6<DP, kLjmNeed>)
+                    ? (DP > 128 && pl.keep_lj ? need_kern(std::integral_constant<bool, (DP > 128)>{})
+                                              : need_kern(std::false_type{}))
                     : &full_lse_x6<DP, DP <= 128 ? kLjmStore : kLjmNeed>;
     hipError_t e = set_lds(reinterpret_cast<const void*>(kern), lds1);
     if (e != hipSuccess) return e;
-    const unsigned grid1 = pl.need ? (unsigned)pl.grid1 : (unsigned)cdiv(pl.N, 32 * kWaves);
+    const unsigned grid1 = pl.need ? (unsigned)pl.grid1 : (unsigned)cdiv(pl.N, 32 * kWaves * full_x6_tpw(DP));
     hipLaunchKernelGGL(kern, dim3(grid1), dim3(kThreads), lds1, stream, X, ldx,
                        pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
                        reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, logZ,
                        rowstat, lj, reinterpret_cast<unsigned*>(ws + pl.off_need),
-                       reinterpret_cast<unsigned short*>(ws + pl.off_bound), pl.rexact ? 1 : 0, dense ? 1 : 0,
-                       psel);
+                       reinterpret_cast<unsigned short*>(ws + pl.off_bound), dense ? 1 : 0, psel);
     if constexpr (flj_applies(DP)) {
       if (pl.autolj) {
-        // The stored branch's instance: the same pass, also keeping the log-joint.
+        // The stored branch's instance: the same pass, keeping the log-joint and no need
+        // masks (so no need-mask form).
         auto kst = &full_lse_x6<DP, kLjmNeed, true>;
         e = set_lds(reinterpret_cast<const void*>(kst), lds1);
         if (e != hipSuccess) return e;
@@ -1424,8 +1557,7 @@ hipError_t launch_passes(const FullPlan& pl, const float* X, int64_t ldx, unsign
                            reinterpret_cast<const bf16x8*>(ws + pl.off_l3),
                            reinterpret_cast<const double*>(ws + pl.off_esw), ck, (int)pl.K, pl.KP, logZ, rowstat,
                            lj, reinterpret_cast<unsigned*>(ws + pl.off_need),
-                           reinterpret_cast<unsigned short*>(ws + pl.off_bound), pl.rexact ? 1 : 0, dense ? 1 : 0,
-                           psel);
+                           reinterpret_cast<unsigned short*>(ws + pl.off_bound), dense ? 1 : 0, psel);
       }
     }
   }
@@ -2366,12 +2498,12 @@ using namespace fgmm;
 
 namespace {
 // Rows per call of the plans that always store the log-joint (the bf16 contract and
-// D > 256), whose N/32 tiles of KP x 32 floats must fit kMaxLjBytes: a multiple of
-// 128 rows.  Larger calls run in chunks of this many rows.
+// D > 256), whose N/32 tiles of KP x 32 floats (rounded up to 8) must fit
+// kMaxLjBytes: a multiple of 256 rows.  Larger calls run in chunks of this many rows.
 bool full_lj_chunked(int64_t D, bool bf16) { return bf16 || full_is_wide((int)round_up(D, 32)); }
 int64_t full_lj_chunk_rows(int64_t K) {
   const int64_t KP = round_up(K < 1 ? 1 : K, kCompsPerWG);
-  const int64_t tiles = (int64_t)(kMaxLjBytes / ((size_t)KP * 32 * sizeof(float))) / 4 * 4;
+  const int64_t tiles = (int64_t)(kMaxLjBytes / ((size_t)KP * 32 * sizeof(float))) / 8 * 8;
   return tiles * 32;
 }
 }  // namespace

@@ -97,6 +97,21 @@ def test_zero_step_skip_is_bitwise_dense(N, K, D, seed, stored, gpu_device):
     assert_close_stats(outs[1], oracle(inp), "full dense")
 
 
+@pytest.mark.parametrize("N,K,D", [(8192, 256, 64), (3000, 40, 128), (3000, 1100, 32),
+                                   (2000, 600, 64), (1500, 1100, 64)])
+def test_default_plan_on_dense_data(N, K, D, gpu_device):
+    """The default plan where nearly every pair is needed (the reference's N(0, I) data).
+    Pass 1 forms its need masks from per-row candidate lists where they fit in LDS (the
+    first three shapes: the lists overflow and set bits directly), else from bounds in
+    the workspace (K = 600, D = 64) or the running maximum (K = 1100, D = 64).  Every
+    form must give the oracle's outputs, and agree with dense=True."""
+    inp = data.full_reference_smoke(N, K, D, seed=11)
+    a = _into(inp, gpu_device)
+    b = _into(inp, gpu_device, dense=True)
+    assert_dense_agrees(a, b, bitwise=False)
+    assert_close_stats(a, oracle(inp), f"full default plan dense data N={N} K={K} D={D}")
+
+
 @pytest.mark.parametrize("D", [72, 48])
 @pytest.mark.parametrize("stored", [False, True])
 def test_phase_split_equals_one_call(stored, D, gpu_device):

@@ -133,7 +133,7 @@ def test_log_joint_beyond_16gib_runs_in_row_chunks(gpu_device):
     from flash_gmm import _lib
     dev = gpu_device
     K, D = 1024, 8
-    chunk = (16 << 30) // (K * 32 * 4) // 4 * 4 * 32          # rows per 16 GiB of log-joint
+    chunk = (16 << 30) // (K * 32 * 4) // 8 * 8 * 32          # rows per 16 GiB of log-joint
     N = chunk + 3000
     assert N * K * 4 > 16 << 30
     print(f"full bf16 chunked N={N} K={K} D={D} chunk={chunk}", flush=True)
