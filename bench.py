@@ -56,7 +56,7 @@ WORKLOADS = {
 }
 
 # HBM traffic per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (separate runs)
-# on this bench command (--steps 2 --warmup 1 --no-cpu-baseline --no-extra-runs), each
+# on this bench command (--steps 10 --warmup 2 --no-cpu-baseline --no-extra-runs), each
 # scaled by what the counter reads for a 512 MiB device copy (bench.py
 # --copy-calibration 512: FETCH_SIZE x2.0, WRITE_SIZE x1.0).  Per kernel of one step:
 # (FETCH_SIZE KiB, WRITE_SIZE KiB); the commands and tables are in profiles/.
@@ -80,16 +80,26 @@ TRAFFIC_KIB = {
         "phase1": "diag_lse_x6<96, 2>",
         "diag_x6_prep": (457, 1_552), "diag_lse_x6<96, 2>": (193_991, 19_532),
         "diag_accum_gather<96>": (207_844, 49_408), "diag_reduce": (25_823, 780)},
+    # The drop-in's mode: on this clustered data the probe keeps the default plan, and
+    # the stored branch's pass-1 instance and full_accum_ljt return at once.
     ("full_n250k_k256_d64", "default", "fp32"): {
-        "phase1": "full_lse_x6<64, 2>",
-        "full_x6_prep": (2_130, 8_328), "full_lse_x6<64, 2>": (332_914, 135_805),
-        "full_accum_gather<64, 0>": (68_315, 25_150), "full_reduce_sig": (12_323, 4_096),
-        "full_reduce": (284, 65)},
+        "phase1": "full_lse_x6<64, 2, 0, 2>",
+        "full_x6_prep": (2_134, 8_328), "full_probe_ll<64>": (5_285, 2_048), "full_probe_count": (1_045, 2),
+        "full_lse_x6<64, 2, 0, 2>": (177_976, 67_765), "full_lse_x6<64, 2, 1, 0>": (17, 0),
+        "full_accum_ljt<64>": (23, 0), "full_accum_gather<64, 0, 0>": (68_174, 25_150),
+        "full_reduce_sig": (12_328, 4_096), "full_reduce": (286, 65)},
+    # N(0, I) data: the probe selects the stored branch.
+    ("full_ref_n250k_k256_d64", "default", "fp32"): {
+        "phase1": "full_lse_x6<64, 2, 1, 0>",
+        "full_x6_prep": (2_134, 8_328), "full_probe_ll<64>": (5_285, 2_048), "full_probe_count": (1_045, 2),
+        "full_lse_x6<64, 2, 0, 2>": (23, 0), "full_lse_x6<64, 2, 1, 0>": (152_892, 253_042),
+        "full_accum_ljt<64>": (157_397, 25_096), "full_accum_gather<64, 0, 0>": (15, 0),
+        "full_reduce_sig": (12_328, 4_096), "full_reduce": (286, 65)},
     ("full_n100k_k64_d128", "default", "fp32"): {
-        "phase1": "full_lse_x6<128, 2>",
-        "full_x6_prep": (2_108, 8_258), "full_lse_x6<128, 2>": (138_802, 49_128),
-        "full_accum_gather<128, 0>": (94_638, 82_968), "full_reduce_sig": (40_995, 4_096),
-        "full_reduce": (540, 32)},
+        "phase1": "full_lse_x6<128, 2, 0, 2>",
+        "full_x6_prep": (2_112, 8_258), "full_lse_x6<128, 2, 0, 2>": (135_236, 1_984),
+        "full_accum_gather<128, 0, 0>": (94_705, 82_968), "full_reduce_sig": (41_000, 4_096),
+        "full_reduce": (542, 32)},
 }
 
 
