@@ -1,5 +1,5 @@
 """GPU parity of the full-covariance E-step against the CPU oracle (tolerances in parity.py;
-sig_outer is checked like sig_acc, element-wise with the 1e-6*max floor)."""
+sig_outer element-wise against sqrt(S_ii S_jj) of its component)."""
 
 import os
 import sys
