@@ -91,8 +91,8 @@ constexpr size_t kFullLds = 160 * 1024;   // LDS per compute unit
 //                has a few tens of candidates, so the workspace sees a few bytes per
 //                row.  Used where the LDS lists and words fit beside the operand
 //                stages.
-//   kNeedBounds: each wave has a slot of 32 x KP bf16 bounds in the workspace, reused
-//                tile after tile (up to kNeedExactMaxK components).
+//   kNeedBounds: each wave has a slot of TPW x 32 x KP bf16 bounds in the workspace,
+//                reused tile after tile (up to kNeedExactMaxK components).
 //   kNeedRunMax: the bit is set when the component is within kLjSkipGap of the running
 //                maximum.
 // The first two give the exact bits (the first unless a row has more than
