@@ -189,8 +189,10 @@ FullPlan make_plan(int64_t N, int64_t K, int64_t D, bool allow_lj = false, bool 
   p.autolj = p.need && auto_lj && flj_applies(p.DP) && N > 0 && K <= kProbeMaxKB &&
              full_lj_bytes(N, p.KP) <= kMaxLjBytes;
   p.nprobe = p.autolj ? (int)std::min<int64_t>(kProbeTiles, cdiv(N, 32)) : 0;
+  // A list entry holds the component in 16 bits (the LDS limit keeps K far below that).
   p.needmode = !p.need ? kNeedRunMax
-               : full_x6_lds_bytes(p.DP) + full_list_lds_bytes(p.DP, p.KP) <= kFullLds / full_waves_per_eu(p.DP)
+               : p.KP < 65536 &&
+                         full_x6_lds_bytes(p.DP) + full_list_lds_bytes(p.DP, p.KP) <= kFullLds / full_waves_per_eu(p.DP)
                    ? kNeedLists
                    : K <= kNeedExactMaxK ? kNeedBounds : kNeedRunMax;
   p.ngrp = gather_sig_groups(p.DP);
