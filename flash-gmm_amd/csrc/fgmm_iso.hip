@@ -616,9 +616,35 @@ void iso_lse(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
 // buffer-to-LDS loads (no staging registers), double buffered; the constants are
 // triple buffered, since block kb - 1's are read while block kb + 1's arrive.
 // The eight 32-row tiles share one staging of each mu block.
+//
+// Workgroups below `full` take 8 tiles each (whole rounds of one workgroup per compute
+// unit); the rest take `small` tiles each, so that the tiles left after the last whole
+// round spread over every compute unit instead of a few workgroups of 8.  A wave of
+// such a group without a tile (wave >= small, or past the last tile) is idle: it issues
+// its share of the block loads and meets every barrier, and computes and writes
+// nothing.
 // ---------------------------------------------------------------------------
 constexpr int kPipeWaves = 8;
 constexpr int kPipeThreads = 64 * kPipeWaves;
+
+// iso_lse_pipe's grid: whole rounds of 8-tile workgroups (one per compute unit),
+// then the tiles left in groups of `small`, one group per compute unit.
+struct PipeGrid {
+  int64_t grid, full;
+  int small;
+};
+__host__ inline PipeGrid pipe_grid(int64_t N) {
+  const int64_t T = cdiv(N, 32), G = cdiv(T, kPipeWaves), cus = current_device_cus();
+  PipeGrid pg{G, G, kPipeWaves};
+  const int64_t F = T / (kPipeWaves * cus);
+  const int64_t R = T - F * kPipeWaves * cus;
+  if (F > 0 && R > 0) {
+    pg.small = (int)cdiv(R, cus);
+    pg.full = F * cus;
+    pg.grid = pg.full + cdiv(R, (int64_t)pg.small);
+  }
+  return pg;
+}
 
 template <int DP>
 constexpr size_t lse_pipe_lds_bytes() {
@@ -631,7 +657,8 @@ void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
                   const bf16x8* __restrict__ mu3, const double2* __restrict__ kc_blk, int KB,
                   float* __restrict__ logZ, double2* __restrict__ rowstat, unsigned* __restrict__ ljmask,
                   unsigned* __restrict__ ljcount, int dense, float* __restrict__ lj,
-                  ProbeSel probe, __bf16* __restrict__ xsplit, float2* __restrict__ zpair) {
+                  ProbeSel probe, __bf16* __restrict__ xsplit, float2* __restrict__ zpair, int64_t full,
+                  int small) {
   static_assert(DP <= 128, "pipelined pass 1 keeps all of a row's splits in registers");
   constexpr int NQ = DP / 16;
   constexpr int BLK = NQ * 4 * 64;        // bf16x8 per 32-component block
@@ -649,9 +676,12 @@ void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, g = lane >> 5;
-  const int64_t tile = (int64_t)blockIdx.x * kPipeWaves + wave;
+  const bool tail = (int64_t)blockIdx.x >= full;
+  const int64_t tile = tail ? full * kPipeWaves + ((int64_t)blockIdx.x - full) * small + wave
+                            : (int64_t)blockIdx.x * kPipeWaves + wave;
+  const bool idle = tail && (wave >= small || tile * 32 >= N);
   const int64_t row = tile * 32 + c;
-  const bool valid = row < N;
+  const bool valid = !idle && row < N;
   // Whether this call stores the log-joint: never without lj, always without a
   // probe, else as the probe's counts (written before this kernel) say.
   const bool store = lj != nullptr && (probe.count == nullptr || probe_selects(probe));
@@ -774,6 +804,17 @@ void iso_lse_pipe(const float* __restrict__ X, int64_t ldx, int64_t N, int D,
     }
   };
 
+  if (idle) {
+    // Its share of every block's loads and every barrier (the active waves meet no
+    // barrier after the block loop), nothing else.
+    if (KB > 1) fetch(1);
+    dma_barrier();
+    for (int kb = 1; kb < KB; ++kb) {
+      if (kb + 1 < KB) fetch(kb + 1);
+      dma_barrier();
+    }
+    return;
+  }
   if (KB > 1) fetch(1);
   f32x16 xm = contract(0);
   dma_barrier();
@@ -3058,10 +3099,12 @@ hipError_t launch_passes(const IsoPlan& pl, const float* X, int64_t ldx, unsigne
           e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)lds1);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(pl.N, 32 * kPipeWaves)), dim3(kPipeThreads), lds1, stream,
+        const PipeGrid pg = pipe_grid(pl.N);
+        hipLaunchKernelGGL(kern, dim3((unsigned)pg.grid), dim3(kPipeThreads), lds1, stream,
                            X, ldx, pl.N, (int)pl.D, reinterpret_cast<const bf16x8*>(ws + pl.off_mu3), kc_blk,
                            pl.KB, logZ, rowstat, ljmask, ljcount, dense ? 1 : 0, lj, psel,
-                           reinterpret_cast<__bf16*>(ws + pl.off_xsplit), reinterpret_cast<float2*>(ws + pl.off_zpair));
+                           reinterpret_cast<__bf16*>(ws + pl.off_xsplit), reinterpret_cast<float2*>(ws + pl.off_zpair),
+                           pg.full, pg.small);
       }
     } else {
       return hipErrorInvalidValue;   // launch_ctile runs pass 1 above D = 128
