@@ -66,9 +66,9 @@ TRAFFIC_KIB = {
     # the default plan, and iso_accum_ljt returns at once.
     ("iso_n1m_k1024_d128", "default", "fp32"): {
         "phase1": "iso_lse_pipe<128, 1>",
-        "iso_prep": (310, 1_104), "iso_store_probe<128>": (2_679, 2), "iso_lse_pipe<128, 1>": (310_989, 24_415),
-        "iso_accum_ljt<128>": (10, 0), "iso_accum_gather<128>": (268_566, 33_280),
-        "iso_accum_tiles2<128>": (12, 0), "iso_reduce": (20_857, 663)},
+        "iso_prep": (311, 1_104), "iso_store_probe<128>": (2_680, 2), "iso_lse_pipe<128, 1>": (310_281, 24_414),
+        "iso_accum_ljt<128>": (18, 0), "iso_accum_gather<128>": (268_569, 33_280),
+        "iso_accum_tiles2<128>": (16, 0), "iso_reduce": (20_842, 664)},
     # The reference's N(0, I) data: the probe selects the stored branch (pass 1 writes the
     # log-joint, the X parts and the logZ pairs; iso_accum_ljt reads them back).
     ("iso_ref_n1m_k1024_d128", "default", "fp32"): {
