@@ -77,8 +77,8 @@ TRAFFIC_KIB = {
         "iso_lse_pipe<128, 1>": (316_772, 4_534_764), "iso_accum_ljt<128>": (2_289_322, 33_280),
         "iso_accum_gather<128>": (22, 0), "iso_accum_tiles2<128>": (13, 0), "iso_reduce": (20_835, 664)},
     ("diag_n1m_k1024_d96", "default", "fp32"): {
-        "phase1": "diag_lse_x6<96, 2>",
-        "diag_x6_prep": (457, 1_552), "diag_lse_x6<96, 2>": (193_991, 19_532),
+        "phase1": "diag_lse_x6<96, 2, 0>",
+        "diag_x6_prep": (457, 1_552), "diag_lse_x6<96, 2, 0>": (193_991, 19_532),
         "diag_accum_gather<96>": (207_844, 49_408), "diag_reduce": (25_823, 780)},
     # The drop-in's mode: on this clustered data the probe keeps the default plan, and
     # the stored branch's pass-1 instance and full_accum_ljt return at once.
