@@ -299,6 +299,29 @@ def test_headline_shape_mid_size(gpu_device):
     assert_close_stats(run_gpu(inp, gpu_device), oracle(inp), "K1024 D128 N65536")
 
 
+@pytest.mark.parametrize("kind", ["clustered", "dense"])
+def test_pass1_tail_groups(kind, gpu_device):
+    """Pass 1 (D <= 128) runs whole rounds of 8-tile workgroups, one per compute unit,
+    then the tiles left in smaller groups whose spare waves only load and meet the
+    barriers.  At an N that leaves 531 tiles after one round (groups of 3, the last
+    tile partial): all four outputs against the oracle, the default plan against
+    dense=True, and store_log_joint='auto' (on the dense data the stored branch, which
+    reads the log-joint tiles, X parts and logZ pairs pass 1 wrote)."""
+    cus = torch.cuda.get_device_properties(gpu_device).multi_processor_count
+    N = 8 * cus * 32 + 530 * 32 + 17
+    print(f"tail groups {kind} N={N} CUs={cus}", flush=True)
+    inp = (data.iso_clustered(N, 256, 128, seed=5) if kind == "clustered"
+           else data.reference_smoke(N, 256, 128, seed=5))
+    ref = oracle(inp)
+    base = _into(inp, gpu_device)
+    assert_close_stats(base, ref, f"tail groups {kind} N={N}")
+    auto = _into(inp, gpu_device, store_log_joint="auto")
+    assert torch.equal(auto[0], base[0])
+    assert_close_stats(auto, ref, f"tail groups auto {kind} N={N}")
+    dense = _into(inp, gpu_device, dense=True)
+    assert_dense_agrees(base, dense, bitwise=False)
+
+
 @pytest.mark.parametrize("N,K,D", [(50_000, 48, 64), (30_000, 20, 30), (40_000, 64, 96)])
 def test_small_k_mid_size(N, K, D, gpu_device):
     """Few component blocks: pass 2 runs 1 or 2 blocks per workgroup with more row groups."""
